@@ -1,0 +1,277 @@
+"""Learner throughput of the PPO update on one MI355X.
+
+A step is one complete PPO.update (bootstrap value, GAE, the epoch
+permutations, and every minibatch forward/backward/loss/clip/Adam step) over
+one synthetic rollout already resident in HBM.  The default workload is the
+discrete Anakin configuration: obs [T=128, N=2048, 400] binary, 6 actions,
+shared 2x256 ReLU torso, 4 epochs x 8 minibatches of 32768.
+
+Prints one JSON line: learner samples/s, the roofline of the dominant kernel
+(timed live with HIP events, launch by launch) and the oracle's CPU rate on a
+bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK = {"fp32_mfma": 157.3, "bf16_mfma": 2516.6, "hbm": 8000.0}  # TFLOP/s, TFLOP/s, GB/s
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--launch-reps", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--profile-only", action="store_true", help="warmup + timed updates only")
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def synthetic_rollout(recipe, params, device, seed):
+    """Seeded rollout of the workload's distributions generated on the device,
+    with actions / log-probs / values from the initial network."""
+    import torch
+    from boonta_amd import torch_ref
+    from boonta_amd.types import Timestep, Transition
+
+    T, N, D = recipe.T, recipe.N, recipe.obs_dim
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    shape = (T + 1, N, D)
+    if recipe.name == "discrete-anakin":
+        obs = (torch.rand(shape, device=device, generator=g) < 0.1).float()
+    elif recipe.name == "large-obs-bf16":
+        obs = torch.rand(shape, device=device, generator=g)
+        binary = torch.zeros(D, dtype=torch.bool, device=device)
+        binary[torch.randperm(D, device=device, generator=g)[: (3 * D) // 4]] = True
+        obs[..., binary] = (obs[..., binary] < 0.05).float()
+    else:
+        obs = torch.randn(shape, device=device, generator=g)
+    if recipe.name == "discrete-tiny":
+        reward = torch.ones(T, N, device=device)
+    elif recipe.name == "discrete-anakin":
+        reward = (torch.rand(T, N, device=device, generator=g) < 0.05).float()
+    elif recipe.name == "large-obs-bf16":
+        reward = (torch.rand(T, N, device=device, generator=g) < 0.02).float()
+    else:
+        reward = torch.randn(T, N, device=device, generator=g)
+    terminated = torch.rand(T, N, device=device, generator=g) < recipe.done_p
+    truncated = torch.zeros(T, N, dtype=torch.bool, device=device)
+    plan = recipe.network.plan(D)
+    tparams = _to_torch(params, device)
+    acts, lps, vals = [], [], []
+    flat_obs = obs[:-1].reshape(T * N, D)
+    for s in range(0, T * N, 65536):
+        a, lp, v = torch_ref.sample(tparams, plan, flat_obs[s:s + 65536], g)
+        acts.append(a)
+        lps.append(lp)
+        vals.append(v)
+    action = torch.cat(acts).reshape((T, N) + tuple(acts[0].shape[1:])).contiguous()
+    tr = Transition(
+        first=Timestep(obs=obs[:-1]),
+        second=Timestep(obs=obs[1:], action=action, reward=reward.contiguous(), terminated=terminated,
+                        truncated=truncated),
+        aux={"log_prob": torch.cat(lps).reshape(T, N).contiguous(),
+             "value": torch.cat(vals).reshape(T, N).contiguous()})
+    return tr
+
+
+def _to_torch(tree, device):
+    import torch
+    if isinstance(tree, dict):
+        return {k: _to_torch(v, device) for k, v in tree.items()}
+    return torch.from_numpy(np.asarray(tree, np.float32)).to(device)
+
+
+def launch_work(name, args):
+    """(flops, bytes) of one launch: algorithmic work of the call's shapes."""
+    if name == "ppo_gemm_f32":
+        M, N, K = args[10], args[11], args[12]
+        return 2.0 * M * N * K, 4.0 * (M * K + K * N + M * N)
+    if name == "ppo_gae_f32":
+        T, N = args[10], args[11]
+        return 0.0, 18.0 * T * N + 4.0 * N
+    if name == "ppo_adam_clip_f32":
+        n = args[6]
+        return 0.0, 28.0 * n
+    return 0.0, 0.0
+
+
+def time_launches(ex, reps, per_update_steps):
+    """Times every launch of (bootstrap + GAE + permutations + one minibatch
+    step) with HIP events on the launching stream."""
+    import torch
+    from boonta_amd import _lib
+
+    calls = ex.record(max_steps=1)
+    stream = torch.cuda.current_stream()
+    st = stream.cuda_stream
+    mb_start = next(i for i, (n, _) in enumerate(calls) if n == "ppo_gemm_f32" and i > 0 and
+                    calls[i - 1][0] == "ppo_epoch_permutations")
+    rows = []
+    for i, (name, args) in enumerate(calls):
+        args = (st,) + tuple(args[1:])
+        _lib.call(name, *args)  # warm
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            _lib.call(name, *args)
+        e1.record(stream)
+        e1.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        count = per_update_steps if i >= mb_start else 1
+        flops, nbytes = launch_work(name, args)
+        rows.append({"i": i, "name": name, "ms": ms, "count": count, "flops": flops, "bytes": nbytes,
+                     "shape": [a for a in args[10:13]] if name == "ppo_gemm_f32" else None,
+                     "layout": [args[1], args[2]] if name == "ppo_gemm_f32" else None})
+    return rows
+
+
+def cpu_baseline(recipe, params, tr_dev, budget_s):
+    """The oracle (float64 numpy) on the host: minibatch steps of the same
+    workload until the time budget, extrapolated to one update."""
+    import torch
+    from oracle import gae as ogae
+    from oracle import ppo as oppo
+
+    plan = recipe.network.plan(recipe.obs_dim)
+    T, N = recipe.T, recipe.N
+    B, mb, E, M = recipe.batch, recipe.minibatch, recipe.cfg.update_epochs, recipe.cfg.num_minibatches
+    cfg = {"clip_coefficient": recipe.cfg.clip_coefficient, "clip_value_loss": recipe.cfg.clip_value_loss,
+           "entropy_coefficient": recipe.cfg.entropy_coefficient, "value_coefficient": recipe.cfg.value_coefficient}
+    a = recipe.optimizer.adam
+    opt = {"lr": a.learning_rate, "max_grad_norm": recipe.optimizer.max_grad_norm}
+    rng = np.random.default_rng(0)
+    s = tr_dev.second
+    reward = s.reward.cpu().numpy()
+    term, trunc = s.terminated.cpu().numpy(), s.truncated.cpu().numpy()
+    value = tr_dev.aux["value"].cpu().numpy()
+    t0 = time.perf_counter()
+    adv, ret = ogae.gae(reward, term, trunc, value, value[-1], recipe.cfg.gamma, recipe.cfg.gae_lambda)
+    t_gae = time.perf_counter() - t0
+    p = oppo.tree_map(lambda x: np.asarray(x, np.float64), params)
+    st = oppo.optimizer_init(p)
+    obs_flat = tr_dev.first.obs.reshape(B, -1)
+    act_flat = s.action.reshape((B,) + tuple(s.action.shape[2:]))
+    lp_flat = tr_dev.aux["log_prob"].reshape(B)
+    v_flat = tr_dev.aux["value"].reshape(B)
+    advf, retf = adv.reshape(B), ret.reshape(B)
+    steps, spent = 0, 0.0
+    while spent < budget_s and steps < 64:
+        idx = np.sort(rng.permutation(B)[:mb])
+        it = torch.from_numpy(idx).to(obs_flat.device)
+        x = obs_flat[it].cpu().numpy()
+        act = act_flat[it].cpu().numpy()
+        olp, ov = lp_flat[it].cpu().numpy(), v_flat[it].cpu().numpy()
+        t0 = time.perf_counter()
+        _, _, grads = oppo.loss_and_grad(p, plan, cfg, x, act, olp, ov, advf[idx], retf[idx])
+        p, st, _ = oppo.optimizer_update(grads, st, p, opt)
+        spent += time.perf_counter() - t0
+        steps += 1
+    t_step = spent / steps
+    t_update = E * M * t_step + t_gae
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count()
+    threads = int(os.environ.get("OMP_NUM_THREADS", cores))
+    return {"value": B / t_update, "unit": "samples/s", "cores": min(cores, threads), "kind": "port",
+            "sample": f"oracle float64 numpy: GAE over the full [{T},{N}] rollout plus {steps} minibatch "
+                      f"steps of {mb} rows (forward, backward, clip, Adam; {spent:.1f} s), extrapolated to "
+                      f"{E}x{M} steps per update"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (every GPU box here has one "
+              "GPU; the multi-GPU design is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from boonta_amd import recipes
+    from boonta_amd.algorithms.ppo import PPO
+    from boonta_amd.random import key as make_key
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    recipe = recipes.make(args.config)
+    dev = torch.device("cuda:0")
+    log(f"workload {recipe.name}: T={recipe.T} N={recipe.N} obs={recipe.obs_dim} "
+        f"{recipe.cfg.update_epochs}x{recipe.cfg.num_minibatches} minibatches of {recipe.minibatch}")
+    params = recipe.network.init(recipe.seed, recipe.obs_dim)["params"]
+    alg = PPO(cfg=recipe.cfg, network=recipe.network, optimizer=recipe.optimizer, use_graph=not args.no_graph)
+    state = alg.init_from_params({"params": params}, recipe.obs_dim)
+    tr = synthetic_rollout(recipe, params, dev, recipe.seed)
+    torch.cuda.synchronize()
+    log("rollout ready")
+    for w in range(args.warmup):
+        alg.update(state, make_key(w), tr)
+        torch.cuda.synchronize()
+        log(f"warmup {w + 1}/{args.warmup} done")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        alg.update(state, make_key(100 + k), tr)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    log(f"timed {args.steps} updates in {elapsed:.3f} s")
+    ms = 1000.0 * elapsed / args.steps
+    value = recipe.batch * args.steps / elapsed
+    logs = alg.logs(state, recipe.T, recipe.N, recipe.obs_dim)
+    if not all(np.isfinite(v).all() for v in logs.values()):
+        raise RuntimeError("non-finite learner logs")
+    out = {
+        "metric": "PPO learner samples/sec on 1 MI355X + % of HBM/MFMA roofline per kernel",
+        "value": value, "unit": "samples/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded rollout of the workload's distributions, random-init network)",
+        "config": {"workload": f"config {args.config}: {recipe.name}", "T": recipe.T, "N": recipe.N,
+                   "obs": recipe.obs_dim, "epochs": recipe.cfg.update_epochs,
+                   "minibatches": recipe.cfg.num_minibatches, "minibatch": recipe.minibatch,
+                   "global_batch": recipe.batch, "graph": not args.no_graph},
+    }
+    if not args.profile_only:
+        ex = alg.executor(state, recipe.T, recipe.N, recipe.obs_dim)
+        rows = time_launches(ex, args.launch_reps, recipe.cfg.update_epochs * recipe.cfg.num_minibatches)
+        total = sum(r["ms"] * r["count"] for r in rows)
+        dom = max(rows, key=lambda r: r["ms"] * r["count"])
+        if dom["flops"] > 0:
+            achieved = dom["flops"] / (dom["ms"] * 1e-3) / 1e12
+            roof = {"bound": "mfma", "achieved": achieved, "peak": PEAK["fp32_mfma"], "unit": "TFLOP/s",
+                    "frac": achieved / PEAK["fp32_mfma"], "traffic": None}
+        else:
+            achieved = dom["bytes"] / (dom["ms"] * 1e-3) / 1e9
+            roof = {"bound": "hbm", "achieved": achieved, "peak": PEAK["hbm"], "unit": "GB/s",
+                    "frac": achieved / PEAK["hbm"], "traffic": None}
+        roof["kernel"] = f"{dom['name']} layout={dom['layout']} MNK={dom['shape']}"
+        roof["avg_ms"] = dom["ms"]
+        roof["share_of_update"] = dom["ms"] * dom["count"] / total
+        out["roofline"] = roof
+        out["launches"] = [{k: r[k] for k in ("name", "layout", "shape", "ms", "count")} for r in rows]
+        out["launch_sum_ms"] = total
+        if not args.skip_cpu:
+            log("cpu baseline ...")
+            out["cpu_baseline"] = cpu_baseline(recipe, params, tr, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

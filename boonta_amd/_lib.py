@@ -1,0 +1,100 @@
+"""ctypes binding of libppo_hip.so (the C ABI declared in include/ppo_hip.h).
+
+The library is the only compute path: if it is missing or a call fails, an
+error is raised; nothing falls back to a CPU or PyTorch implementation.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libppo_hip.so")
+CSRC = os.path.join(_HERE, "csrc")
+
+P = ctypes.c_void_p
+I = ctypes.c_int
+I64 = ctypes.c_int64
+F = ctypes.c_float
+D = ctypes.c_double
+SZ = ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/ppo_hip.h
+SIGNATURES = {
+    "ppo_last_error": (ctypes.c_char_p, []),
+    "ppo_clear_error": (None, []),
+    "ppo_abi_version": (I, []),
+    "ppo_device_check": (I, [I]),
+    "ppo_gae_f32": (I, [P, P, P, P, P, P, P, P, P, P, I, I, D, D, I]),
+    "ppo_threefry_split": (I, [P, P, P, I64]),
+    "ppo_permutation_workspace": (SZ, [I64]),
+    "ppo_permutation": (I, [P, P, P, I64, P, SZ]),
+    "ppo_epoch_permutations_workspace": (SZ, [I, I64]),
+    "ppo_epoch_permutations": (I, [P, P, I, I64, P, P, SZ]),
+    "ppo_gemm_f32": (I, [P, I, I, P, I64, P, P, I64, P, I64, I, I, I, I, I64, I, P, I, P, P, I64, P, I]),
+    "ppo_layernorm_act_fwd_f32": (I, [P, P, I64, P, P, P, I64, P, P, I, I, F, I]),
+    "ppo_layernorm_bwd_blocks": (I, [I]),
+    "ppo_layernorm_act_bwd_f32": (I, [P, P, I64, P, I64, P, P, P, P, P, I64, P, I, I, I]),
+    "ppo_act_fwd_f32": (I, [P, P, I64, P, I64, I, I, I]),
+    "ppo_act_bwd_f32": (I, [P, P, I64, P, I64, P, I64, I, I, I]),
+    "ppo_loss_blocks": (I, [I]),
+    "ppo_loss_stat_count": (I, []),
+    "ppo_loss_f32": (I, [P, I, I, P, P, I64, P, I64, I, P, P, P, P, P, P, P, P, P, P, P, F, I, F, F, F]),
+    "ppo_loss_finalize": (I, [P, P, I, I, F, F, P]),
+    "ppo_grad_reduce_segment_bytes": (I, []),
+    "ppo_grad_reduce_chunk_bytes": (I, []),
+    "ppo_grad_reduce_chunk_elems": (I, []),
+    "ppo_grad_reduce": (I, [P, P, P, I, P]),
+    "ppo_adam_clip_f32": (I, [P, P, P, P, P, P, I64, P, I, F, F, F, F, F, P, I]),
+    "ppo_count_advance": (I, [P, P, I]),
+}
+
+ACT = {"none": 0, None: 0, "relu": 1, "tanh": 2, "silu": 3}
+DIST = {"categorical": 0, "gaussian": 1}
+
+_lib = None
+
+
+class KernelError(RuntimeError):
+    pass
+
+
+def build(verbose: bool = False) -> str:
+    """Compiles the HIP sources for gfx950 into boonta_amd/libppo_hip.so."""
+    jobs = str(min(16, os.cpu_count() or 4))
+    out = subprocess.run(["make", "-C", CSRC, "-j", jobs], capture_output=not verbose, text=True)
+    if out.returncode != 0:
+        raise KernelError(f"building libppo_hip.so failed:\n{out.stdout}\n{out.stderr}")
+    return LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    """Loads the library (it must already be built; see build())."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise KernelError(f"{LIB_PATH} is missing: build it with boonta_amd._lib.build() "
+                          "(hipcc --offload-arch=gfx950); there is no fallback path")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def call(name: str, *args) -> int:
+    """Calls an int-returning entry point and raises on a negative status."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.ppo_last_error().decode(errors="replace")
+        raise KernelError(f"{name} failed ({rc}): {msg}")
+    return rc
+
+
+def exported_symbols() -> list[str]:
+    return list(SIGNATURES)

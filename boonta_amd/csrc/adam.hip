@@ -1,0 +1,175 @@
+// Gradient assembly and the optimizer step of the learner:
+//
+//   1. ppo_grad_reduce: every gradient leaf arrives as `nparts` partial
+//      buffers (split-K GEMM slices, per-block LayerNorm / scale partials).
+//      One launch sums them in a fixed order straight into the flat gradient
+//      buffer and leaves one partial sum of squares per block for the norm.
+//   2. ppo_adam_clip_f32: optax.chain(clip_by_global_norm(max_norm), adam(lr))
+//      of optax 0.2.8, as every PPO recipe builds it
+//      (hangar/recipes/ppo_cartpole.py:44-47; applied at
+//      boonta/algorithms/ppo.py:182-191) in one bandwidth-bound pass over the
+//      flat parameter, gradient and moment buffers:
+//        g <- g                      if ||g|| < max_norm
+//             (g / ||g||) * max_norm otherwise
+//        mu = (1-b1) g + b1 mu;  nu = (1-b2) g^2 + b2 nu;  count += 1
+//        p  <- p + (-lr) * ((mu / (1 - b1^count)) / (sqrt(nu / (1 - b2^count)) + eps))
+//      The global norm is re-folded from the per-block partials by every
+//      block, so no extra launch or grid barrier is needed, and the optax
+//      step counter lives in device memory (count_base + step_offset + 1), so
+//      a captured graph replays with the right bias corrections.
+#include "common.h"
+
+#include <algorithm>
+
+namespace {
+
+struct Segment {
+  float* dst;
+  const float* src;
+  int64_t count;
+  int64_t part_stride;
+  int nparts;
+  int pad_;
+};
+
+struct Chunk {
+  int seg;
+  int pad_;
+  int64_t start;
+};
+
+constexpr int REDUCE_THREADS = 256;
+constexpr int CHUNK = 2048;  // elements per block
+
+__global__ void __launch_bounds__(REDUCE_THREADS)
+grad_reduce_kernel(const Segment* __restrict__ segs, const Chunk* __restrict__ chunks, double* __restrict__ sumsq) {
+  __shared__ double red[REDUCE_THREADS / 64];
+  const Chunk ch = chunks[blockIdx.x];
+  const Segment sg = segs[ch.seg];
+  const int64_t end = min(sg.count, ch.start + (int64_t)CHUNK);
+  double sq = 0.0;
+  for (int64_t i = ch.start + threadIdx.x; i < end; i += REDUCE_THREADS) {
+    float acc = 0.f;
+    const float* s = sg.src + i;
+    for (int q = 0; q < sg.nparts; ++q) acc += s[(int64_t)q * sg.part_stride];
+    sg.dst[i] = acc;
+    sq += (double)acc * (double)acc;
+  }
+  sq = ppo::wave_sum_d(sq);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sq;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int w = 0; w < REDUCE_THREADS / 64; ++w) t += red[w];
+    sumsq[blockIdx.x] = t;
+  }
+}
+
+struct AdamParams {
+  float* p;
+  const float* g;
+  float* mu;
+  float* nu;
+  __bf16* p_bf16;  // optional compute copy of the parameters
+  int64_t n;       // multiple of 4
+  const double* sumsq;
+  int nsumsq;
+  float max_norm;  // <= 0: no clipping
+  float lr, b1, b2, eps;
+  const int* count_base;
+  int step_offset;
+};
+
+__global__ void __launch_bounds__(256) adam_kernel(AdamParams a) {
+  __shared__ float s_scale_norm[2];
+  __shared__ float s_bc[2];
+  if (threadIdx.x < 64) {
+    double t = 0.0;
+    for (int i = threadIdx.x; i < a.nsumsq; i += 64) t += a.sumsq[i];
+    t = ppo::wave_sum_d(t);
+    if (threadIdx.x == 0) {
+      const float norm = (float)sqrt(t);
+      s_scale_norm[0] = norm;
+      s_scale_norm[1] = (a.max_norm > 0.f && !(norm < a.max_norm)) ? 1.f : 0.f;
+      const int count = *a.count_base + a.step_offset + 1;
+      s_bc[0] = 1.f - powf(a.b1, (float)count);
+      s_bc[1] = 1.f - powf(a.b2, (float)count);
+    }
+  }
+  __syncthreads();
+  const float norm = s_scale_norm[0];
+  const bool clip = s_scale_norm[1] != 0.f;
+  const float bc1 = s_bc[0], bc2 = s_bc[1];
+  const float omb1 = 1.f - a.b1, omb2 = 1.f - a.b2;
+  const float neg_lr = -a.lr;
+  const int64_t n4 = a.n / 4;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
+    floatx4 g = reinterpret_cast<const floatx4*>(a.g)[i];
+    floatx4 m = reinterpret_cast<floatx4*>(a.mu)[i];
+    floatx4 v = reinterpret_cast<floatx4*>(a.nu)[i];
+    floatx4 p = reinterpret_cast<floatx4*>(a.p)[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float ge = g[e];
+      if (clip) ge = (ge / norm) * a.max_norm;
+      const float me = omb1 * ge + a.b1 * m[e];
+      const float ve = omb2 * (ge * ge) + a.b2 * v[e];
+      m[e] = me;
+      v[e] = ve;
+      const float u = neg_lr * ((me / bc1) / (sqrtf(ve / bc2) + a.eps));
+      p[e] = p[e] + u;
+    }
+    reinterpret_cast<floatx4*>(a.mu)[i] = m;
+    reinterpret_cast<floatx4*>(a.nu)[i] = v;
+    reinterpret_cast<floatx4*>(a.p)[i] = p;
+    if (a.p_bf16) {
+      bf16x4 b;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) b[e] = (__bf16)p[e];
+      reinterpret_cast<bf16x4*>(a.p_bf16)[i] = b;
+    }
+  }
+}
+
+__global__ void count_advance_kernel(int* count_base, int steps) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) *count_base += steps;
+}
+
+}  // namespace
+
+PPO_EXPORT int ppo_grad_reduce_segment_bytes(void) { return (int)sizeof(Segment); }
+PPO_EXPORT int ppo_grad_reduce_chunk_bytes(void) { return (int)sizeof(Chunk); }
+PPO_EXPORT int ppo_grad_reduce_chunk_elems(void) { return CHUNK; }
+
+// segs/chunks: device tables (layout: ppo_grad_reduce_{segment,chunk}_bytes),
+// one block per chunk; sumsq receives nchunks doubles.
+PPO_EXPORT int ppo_grad_reduce(void* stream, const void* segs, const void* chunks, int nchunks, double* sumsq) {
+  if (nchunks < 0 || !segs || !chunks || !sumsq) return ppo::set_error(PPO_ERR_ARG, "ppo_grad_reduce: bad argument");
+  if (nchunks == 0) return PPO_OK;
+  hipLaunchKernelGGL(grad_reduce_kernel, dim3(nchunks), dim3(REDUCE_THREADS), 0, ppo::as_stream(stream),
+                     (const Segment*)segs, (const Chunk*)chunks, sumsq);
+  return ppo::check_launch("ppo_grad_reduce");
+}
+
+PPO_EXPORT int ppo_adam_clip_f32(void* stream, float* params, const float* grads, float* mu, float* nu,
+                                 void* params_bf16, int64_t n, const double* sumsq, int nsumsq, float max_norm,
+                                 float lr, float b1, float b2, float eps, const int* count_base, int step_offset) {
+  if (n < 0 || (n % 4) != 0 || !params || !grads || !mu || !nu || !count_base || (nsumsq > 0 && !sumsq) ||
+      nsumsq < 0)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_adam_clip_f32: bad argument (n=%lld must be a multiple of 4)",
+                          (long long)n);
+  if (((uintptr_t)params | (uintptr_t)grads | (uintptr_t)mu | (uintptr_t)nu) & 15u)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_adam_clip_f32: buffers must be 16-byte aligned");
+  if (n == 0) return PPO_OK;
+  AdamParams a{params, grads, mu, nu, (__bf16*)params_bf16, n, sumsq, nsumsq, max_norm, lr, b1, b2, eps,
+               count_base, step_offset};
+  const int blocks = (int)std::min<int64_t>(ppo::ceil_div64(n / 4, 256), 2048);
+  hipLaunchKernelGGL(adam_kernel, dim3(blocks), dim3(256), 0, ppo::as_stream(stream), a);
+  return ppo::check_launch("ppo_adam_clip_f32");
+}
+
+PPO_EXPORT int ppo_count_advance(void* stream, int* count_base, int steps) {
+  if (!count_base) return ppo::set_error(PPO_ERR_ARG, "ppo_count_advance: null counter");
+  hipLaunchKernelGGL(count_advance_kernel, dim3(1), dim3(64), 0, ppo::as_stream(stream), count_base, steps);
+  return ppo::check_launch("ppo_count_advance");
+}

@@ -1,0 +1,82 @@
+// Shared helpers for the PPO learner kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+
+#ifndef PPO_EXPORT
+#define PPO_EXPORT extern "C" __attribute__((visibility("default")))
+#endif
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+enum PpoStatus {
+  PPO_OK = 0,
+  PPO_ERR_ARG = -1,     // invalid argument (shape, pointer, enum)
+  PPO_ERR_LAUNCH = -2,  // kernel launch failed
+  PPO_ERR_SPACE = -3,   // workspace too small
+};
+
+// Activation codes shared with the host side.
+enum PpoAct { ACT_NONE = 0, ACT_RELU = 1, ACT_TANH = 2, ACT_SILU = 3 };
+
+namespace ppo {
+
+int set_error(int code, const char* fmt, ...);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(PPO_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return PPO_OK;
+}
+
+inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+inline int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float act_fwd(int act, float x) {
+  switch (act) {
+    case ACT_RELU: return x > 0.f ? x : 0.f;
+    case ACT_TANH: return tanhf(x);
+    case ACT_SILU: return x / (1.f + __expf(-x));
+    default: return x;
+  }
+}
+
+// Derivative of the activation, from its input x (silu) or output y (relu, tanh).
+__device__ __forceinline__ float act_grad(int act, float x_or_y) {
+  switch (act) {
+    case ACT_RELU: return x_or_y > 0.f ? 1.f : 0.f;
+    case ACT_TANH: return 1.f - x_or_y * x_or_y;
+    case ACT_SILU: {
+      float s = 1.f / (1.f + __expf(-x_or_y));
+      return s * (1.f + x_or_y * (1.f - s));
+    }
+    default: return 1.f;
+  }
+}
+
+}  // namespace ppo

@@ -1,0 +1,37 @@
+// Error reporting of the C ABI: every entry point returns 0 or a negative
+// PpoStatus and leaves a message for ppo_last_error() on the calling thread.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "common.h"
+
+namespace {
+thread_local char g_last_error[512] = "";
+}
+
+namespace ppo {
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+}  // namespace ppo
+
+PPO_EXPORT const char* ppo_last_error(void) { return g_last_error; }
+
+PPO_EXPORT void ppo_clear_error(void) { g_last_error[0] = '\0'; }
+
+PPO_EXPORT int ppo_abi_version(void) { return 1; }
+
+// Reports whether a HIP device is usable from this process (0 = yes).
+PPO_EXPORT int ppo_device_check(int device) {
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n <= device || device < 0)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_device_check: device %d unavailable (%d devices, %s)", device, n,
+                          hipGetErrorString(e));
+  return PPO_OK;
+}

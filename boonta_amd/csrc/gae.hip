@@ -1,0 +1,126 @@
+// GAE as a reverse scan over the time-major T x N rollout.
+//
+// Follows boonta/algorithms/advantage_estimators.py:8-56: for t = T-1 .. 0,
+//   delta_t = rho_t * (r_t + gamma * (1 - term_t) * V_{t+1} - V_t) * (1 - trunc_t)
+//   A_t     = delta_t + gamma * lambda * c_t * (1 - term_t) * (1 - trunc_t) * A_{t+1}
+// with V_T = bootstrap, A_T = 0, and returns_t = A_t + V_t.
+//
+// Layout: every [T, N] array is time-major, so lane n of a wavefront owns env
+// column n and each time step is one coalesced 256-byte row read per wave.
+// delta_t depends only on data, so the only serial dependence is the affine
+// recurrence A_t = delta_t + k_t A_{t+1}.  When N alone cannot fill the chip,
+// the T axis is cut into `chunks` pieces: each piece first folds its steps into
+// an affine map (P, Q) with A_start = P + Q * A_after, the maps are chained
+// across pieces through LDS, then every piece replays its steps from the true
+// carry.  The arithmetic of each step keeps the reference's operation order and
+// is not contracted into FMAs.
+#include "common.h"
+
+namespace {
+
+struct GaeArgs {
+  const float* reward;
+  const uint8_t* terminated;
+  const uint8_t* truncated;
+  const float* values;
+  const float* bootstrap;
+  const float* rho;  // may be null (1.0)
+  const float* c;    // may be null (1.0)
+  float* adv;
+  float* ret;
+  int T, N;
+  float gamma;     // fp32(gamma)
+  float gl;        // fp32(gamma * lambda), product taken in double like a Python float
+};
+
+struct Step {
+  float delta, k;
+};
+
+__device__ __forceinline__ Step gae_step(const GaeArgs& a, int t, int n, float next_value) {
+  const int64_t i = (int64_t)t * a.N + n;
+  const float r = a.reward[i];
+  const float te = a.terminated[i] ? 1.f : 0.f;
+  const float tr = a.truncated[i] ? 1.f : 0.f;
+  const float v = a.values[i];
+  const float rho = a.rho ? a.rho[i] : 1.f;
+  const float c = a.c ? a.c[i] : 1.f;
+  const float one_te = __fsub_rn(1.f, te);
+  const float one_tr = __fsub_rn(1.f, tr);
+  float d = __fadd_rn(r, __fmul_rn(__fmul_rn(a.gamma, one_te), next_value));
+  d = __fmul_rn(rho, __fsub_rn(d, v));
+  d = __fmul_rn(d, one_tr);
+  float k = __fmul_rn(__fmul_rn(__fmul_rn(a.gl, c), one_te), one_tr);
+  return {d, k};
+}
+
+__device__ __forceinline__ float next_value_at(const GaeArgs& a, int t, int n) {
+  // V_{t+1}, with V_T = bootstrap
+  return (t + 1 < a.T) ? a.values[(int64_t)(t + 1) * a.N + n] : a.bootstrap[n];
+}
+
+// blockDim = (64, chunks): threadIdx.x = column within the wave, threadIdx.y = piece of T.
+__global__ void __launch_bounds__(1024) gae_kernel(GaeArgs a) {
+  __shared__ float sP[16][64];
+  __shared__ float sQ[16][64];
+  const int n = blockIdx.x * 64 + threadIdx.x;
+  const int chunks = blockDim.y;
+  const int j = threadIdx.y;
+  const bool live = n < a.N;
+  const int t_lo = (int)(((int64_t)a.T * j) / chunks);
+  const int t_hi = (int)(((int64_t)a.T * (j + 1)) / chunks);  // exclusive
+
+  float carry = 0.f;
+  if (chunks > 1) {
+    float P = 0.f, Q = 1.f;
+    if (live) {
+      for (int t = t_hi - 1; t >= t_lo; --t) {
+        Step s = gae_step(a, t, n, next_value_at(a, t, n));
+        P = __fadd_rn(s.delta, __fmul_rn(s.k, P));
+        Q = __fmul_rn(s.k, Q);
+      }
+    }
+    sP[j][threadIdx.x] = P;
+    sQ[j][threadIdx.x] = Q;
+    __syncthreads();
+    for (int q = chunks - 1; q > j; --q)
+      carry = __fadd_rn(sP[q][threadIdx.x], __fmul_rn(sQ[q][threadIdx.x], carry));
+  }
+  if (!live) return;
+  float A = carry;
+  for (int t = t_hi - 1; t >= t_lo; --t) {
+    const float nv = next_value_at(a, t, n);
+    Step s = gae_step(a, t, n, nv);
+    A = __fadd_rn(s.delta, __fmul_rn(s.k, A));
+    const int64_t i = (int64_t)t * a.N + n;
+    a.adv[i] = A;
+    a.ret[i] = __fadd_rn(A, a.values[i]);
+  }
+}
+
+}  // namespace
+
+PPO_EXPORT int ppo_gae_f32(void* stream, const float* reward, const uint8_t* terminated,
+                           const uint8_t* truncated, const float* values,
+                           const float* bootstrap, const float* rho, const float* c,
+                           float* advantages, float* returns, int T, int N, double gamma,
+                           double gae_lambda, int chunks) {
+  if (T < 0 || N < 0) return ppo::set_error(PPO_ERR_ARG, "ppo_gae_f32: negative shape T=%d N=%d", T, N);
+  if (T == 0 || N == 0) return PPO_OK;
+  if (!reward || !terminated || !truncated || !values || !bootstrap || !advantages || !returns)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gae_f32: null buffer");
+  if (chunks <= 0) {
+    // enough waves for ~4 per CU, capped by T and the LDS table
+    const int waves = (N + 63) / 64;
+    chunks = 1;
+    while (chunks < 16 && waves * chunks < 1024 && T / (chunks * 2) >= 4) chunks *= 2;
+  }
+  if (chunks > 16) return ppo::set_error(PPO_ERR_ARG, "ppo_gae_f32: chunks %d > 16", chunks);
+  if (chunks > T) chunks = T;
+  GaeArgs a{reward, terminated, truncated, values, bootstrap, rho, c, advantages, returns,
+            T, N, (float)gamma, (float)(gamma * gae_lambda)};
+  dim3 block(64, chunks);
+  dim3 grid((N + 63) / 64);
+  hipLaunchKernelGGL(gae_kernel, grid, block, 0, ppo::as_stream(stream), a);
+  return ppo::check_launch("ppo_gae_f32");
+}

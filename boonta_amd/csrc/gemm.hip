@@ -1,0 +1,331 @@
+// fp32 GEMM on CDNA4 matrix cores (v_mfma_f32_32x32x2_f32), LDS-staged and
+// double-buffered, for the Dense layers of the learner's torso:
+//
+//   forward      Y[M,N]  = act(X[rows(M),K] W[K,N] + b)      (A k-contiguous, B n-contiguous)
+//   backward dX  dX[M,K] = (dY[M,N] W[K,N]^T) * act'(aux)    (A k-contiguous, B k-contiguous)
+//   backward dW  dW[K,N] = X[rows,K]^T dY[rows,N]             (both operands row-major over the
+//                                                             reduction dim; split over rows)
+//
+// One kernel template covers the three: C[m][n] = sum_k A(m,k) B(k,n) where A is
+// stored either [m][k] (A_K) or [k][m], and B either [n][k] (B_K) or [k][n].
+// Each operand keeps its global orientation in LDS, so global loads are 16-byte
+// vectors along the contiguous axis and no transpose happens on the way in.
+//
+// Tiling: 256 threads = 4 wave64s in a 2x2 grid; each wave owns a
+// (BM/2) x (BN/2) sub-tile made of 32x32 MFMA blocks.  BK = 16 per stage.  The
+// reduction index is permuted inside each group of 8 so that lane half h of a
+// wave consumes k = 8g + 4h + s at MFMA step s: a k-contiguous operand then
+// feeds four MFMAs from one ds_read_b128, the other orientation from four
+// conflict-free ds_read_b32 rows.
+//
+// A row gather (minibatch indices) applies to the rows of X in the forward
+// (A_K: row m -> rows[m]) and in dW (reduction row k -> rows[k]), so the
+// minibatch is never materialised.  dW also sums B's columns over each split
+// for the bias gradient (one extra add per MFMA in the waves of the first row
+// tile), and writes one partial per split; partials are reduced in a fixed
+// order later, so results do not depend on scheduling.
+#include "common.h"
+
+#include <algorithm>
+
+namespace {
+
+constexpr int BK = 16;
+constexpr int LDS_PAD = 4;
+
+enum Epilogue { EPI_STORE = 0, EPI_BIAS_ACT = 1, EPI_DACT = 2 };
+
+struct GemmParams {
+  const float* A;
+  int64_t lda;
+  const int32_t* rows;  // gather indices (see header comment) or null
+  const float* B;
+  int64_t ldb;
+  float* C;
+  int64_t ldc;
+  int64_t c_split_stride;  // elements between split-K partial outputs
+  int M, N, K;
+  int k_per_split;  // multiple of BK
+  int epi;
+  const float* bias;  // EPI_BIAS_ACT: [N] or null
+  int act;
+  float* pre;  // EPI_BIAS_ACT: optional pre-activation output (ldc)
+  const float* aux;  // EPI_DACT: activation output (relu, tanh) or input (silu), ld = ldaux
+  int64_t ldaux;
+  float* bias_grad;  // dW: [splits][N] column sums of B, or null
+};
+
+template <bool VEC>
+__device__ __forceinline__ floatx4 load4(const float* __restrict__ p, int i, int lim) {
+  floatx4 v;
+  if (VEC) {
+    if (i < lim) {
+      v = *reinterpret_cast<const floatx4*>(p + i);
+    } else {
+      v = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = (i + e < lim) ? p[i + e] : 0.f;
+  }
+  return v;
+}
+
+template <int BM, int BN, bool A_K, bool B_K, bool VA, bool VB>
+__global__ void __launch_bounds__(256, 2) gemm_f32_kernel(GemmParams p) {
+  constexpr int A_ROWS = A_K ? BM : BK;
+  constexpr int A_COLS = A_K ? BK : BM;
+  constexpr int B_ROWS = B_K ? BN : BK;
+  constexpr int B_COLS = B_K ? BK : BN;
+  constexpr int A_PER = (BM * BK / 4) / 256;  // float4 loads per thread per stage
+  constexpr int B_PER = (BN * BK / 4) / 256;
+  constexpr int MB = BM / 64;  // 32x32 blocks per wave along M
+  constexpr int NB = BN / 64;
+  static_assert(A_PER >= 1 && B_PER >= 1, "tile too small for 256 threads");
+
+  __shared__ __attribute__((aligned(16))) float sA[2][A_ROWS][A_COLS + LDS_PAD];
+  __shared__ __attribute__((aligned(16))) float sB[2][B_ROWS][B_COLS + LDS_PAD];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave & 1;
+  const int wn = wave >> 1;
+  const int h = lane >> 5;
+  const int l32 = lane & 31;
+  const int m0 = blockIdx.y * BM;
+  const int n0 = blockIdx.x * BN;
+  const int split = blockIdx.z;
+  const int kb = split * p.k_per_split;
+  const int ke = min(p.K, kb + p.k_per_split);
+
+  floatx16 acc[MB][NB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  float bsum[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) bsum[j] = 0.f;
+  const bool do_bsum = (p.bias_grad != nullptr) && (blockIdx.y == 0) && (wm == 0);
+
+  floatx4 ra[A_PER], rb[B_PER];
+
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < A_PER; ++j) {
+      const int f = tid + 256 * j;
+      if (A_K) {
+        const int r = f / (BK / 4);
+        const int c = (f % (BK / 4)) * 4;
+        const int gm = m0 + r;
+        if (gm < p.M) {
+          const int64_t row = p.rows ? (int64_t)p.rows[gm] : (int64_t)gm;
+          ra[j] = load4<VA>(p.A + row * p.lda, k0 + c, ke);
+        } else {
+          ra[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+      } else {
+        const int r = f / (BM / 4);
+        const int c = (f % (BM / 4)) * 4;
+        const int k = k0 + r;
+        if (k < ke) {
+          const int64_t row = p.rows ? (int64_t)p.rows[k] : (int64_t)k;
+          ra[j] = load4<VA>(p.A + row * p.lda, m0 + c, p.M);
+        } else {
+          ra[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < B_PER; ++j) {
+      const int f = tid + 256 * j;
+      if (B_K) {
+        const int r = f / (BK / 4);
+        const int c = (f % (BK / 4)) * 4;
+        const int gn = n0 + r;
+        rb[j] = gn < p.N ? load4<VB>(p.B + (int64_t)gn * p.ldb, k0 + c, ke) : floatx4{0.f, 0.f, 0.f, 0.f};
+      } else {
+        const int r = f / (BN / 4);
+        const int c = (f % (BN / 4)) * 4;
+        const int k = k0 + r;
+        rb[j] = k < ke ? load4<VB>(p.B + (int64_t)k * p.ldb, n0 + c, p.N) : floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
+
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < A_PER; ++j) {
+      const int f = tid + 256 * j;
+      const int r = A_K ? f / (BK / 4) : f / (BM / 4);
+      const int c = A_K ? (f % (BK / 4)) * 4 : (f % (BM / 4)) * 4;
+      *reinterpret_cast<floatx4*>(&sA[buf][r][c]) = ra[j];
+    }
+#pragma unroll
+    for (int j = 0; j < B_PER; ++j) {
+      const int f = tid + 256 * j;
+      const int r = B_K ? f / (BK / 4) : f / (BN / 4);
+      const int c = B_K ? (f % (BK / 4)) * 4 : (f % (BN / 4)) * 4;
+      *reinterpret_cast<floatx4*>(&sB[buf][r][c]) = rb[j];
+    }
+  };
+
+  const int nk = (ke > kb) ? (ke - kb + BK - 1) / BK : 0;
+  if (nk > 0) {
+    gload(kb);
+    sstore(0);
+  }
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) gload(kb + (kt + 1) * BK);
+#pragma unroll
+    for (int g = 0; g < BK / 8; ++g) {
+      const int kk = 8 * g + 4 * h;
+      floatx4 a4[MB], b4[NB];
+#pragma unroll
+      for (int bi = 0; bi < MB; ++bi) {
+        const int i = wm * (BM / 2) + bi * 32 + l32;
+        if (A_K) {
+          a4[bi] = *reinterpret_cast<const floatx4*>(&sA[buf][i][kk]);
+        } else {
+#pragma unroll
+          for (int s = 0; s < 4; ++s) a4[bi][s] = sA[buf][kk + s][i];
+        }
+      }
+#pragma unroll
+      for (int bj = 0; bj < NB; ++bj) {
+        const int j = wn * (BN / 2) + bj * 32 + l32;
+        if (B_K) {
+          b4[bj] = *reinterpret_cast<const floatx4*>(&sB[buf][j][kk]);
+        } else {
+#pragma unroll
+          for (int s = 0; s < 4; ++s) b4[bj][s] = sB[buf][kk + s][j];
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int bi = 0; bi < MB; ++bi)
+#pragma unroll
+          for (int bj = 0; bj < NB; ++bj)
+            acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[bi][s], b4[bj][s], acc[bi][bj], 0, 0, 0);
+      if (do_bsum) {
+#pragma unroll
+        for (int bj = 0; bj < NB; ++bj) bsum[bj] += (b4[bj][0] + b4[bj][1]) + (b4[bj][2] + b4[bj][3]);
+      }
+    }
+    if (kt + 1 < nk) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---------------------------------------------------------------- epilogue
+  float* C = p.C + (int64_t)split * p.c_split_stride;
+#pragma unroll
+  for (int bi = 0; bi < MB; ++bi) {
+#pragma unroll
+    for (int bj = 0; bj < NB; ++bj) {
+      const int gn = n0 + wn * (BN / 2) + bj * 32 + l32;
+      const bool n_ok = gn < p.N;
+      float bias = 0.f;
+      if (p.epi == EPI_BIAS_ACT && p.bias && n_ok) bias = p.bias[gn];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int gm = m0 + wm * (BM / 2) + bi * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (!n_ok || gm >= p.M) continue;
+        float v = acc[bi][bj][r];
+        const int64_t o = (int64_t)gm * p.ldc + gn;
+        if (p.epi == EPI_BIAS_ACT) {
+          v += bias;
+          if (p.pre) p.pre[o] = v;
+          v = ppo::act_fwd(p.act, v);
+        } else if (p.epi == EPI_DACT) {
+          v *= ppo::act_grad(p.act, p.aux[(int64_t)gm * p.ldaux + gn]);
+        }
+        C[o] = v;
+      }
+    }
+  }
+  if (do_bsum) {
+#pragma unroll
+    for (int bj = 0; bj < NB; ++bj) {
+      const float t = bsum[bj] + __shfl_xor(bsum[bj], 32, 64);
+      const int gn = n0 + wn * (BN / 2) + bj * 32 + l32;
+      if (h == 0 && gn < p.N) p.bias_grad[(int64_t)split * p.N + gn] = t;
+    }
+  }
+}
+
+template <int BM, int BN, bool A_K, bool B_K>
+int launch_tile(hipStream_t st, const GemmParams& p, int splits, bool va, bool vb) {
+  dim3 grid(ppo::ceil_div(p.N, BN), ppo::ceil_div(p.M, BM), splits);
+  dim3 block(256);
+  if (va && vb) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, A_K, B_K, true, true>), grid, block, 0, st, p);
+  else if (va) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, A_K, B_K, true, false>), grid, block, 0, st, p);
+  else if (vb) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, A_K, B_K, false, true>), grid, block, 0, st, p);
+  else hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, A_K, B_K, false, false>), grid, block, 0, st, p);
+  return ppo::check_launch("ppo_gemm_f32");
+}
+
+template <bool A_K, bool B_K>
+int launch_layout(hipStream_t st, const GemmParams& p, int splits, bool va, bool vb, int tile) {
+  switch (tile) {
+    case 0: return launch_tile<128, 128, A_K, B_K>(st, p, splits, va, vb);
+    case 1: return launch_tile<128, 64, A_K, B_K>(st, p, splits, va, vb);
+    case 2: return launch_tile<64, 128, A_K, B_K>(st, p, splits, va, vb);
+    default: return launch_tile<64, 64, A_K, B_K>(st, p, splits, va, vb);
+  }
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+}  // namespace
+
+// Generic entry: C[m][n] (+ split * c_split_stride) = epilogue(sum_k A(m,k) B(k,n)).
+//   a_layout 0: A[m * lda + k]; 1: A[k * lda + m].   b_layout 0: B[k * ldb + n]; 1: B[n * ldb + k].
+//   rows: gather of A's rows (layout 0: over m; layout 1: over k) or null.
+//   epi 0: store; 1: bias + activation (pre-activation to `pre` if non-null);
+//   2: multiply by act'(aux).  bias_grad (layout a=1, b=0 only): [splits][N] sums of B.
+//   tile: -1 picks a tile; 0: 128x128, 1: 128x64, 2: 64x128, 3: 64x64.
+PPO_EXPORT int ppo_gemm_f32(void* stream, int a_layout, int b_layout, const float* A, int64_t lda,
+                            const int32_t* rows, const float* B, int64_t ldb, float* C, int64_t ldc, int M,
+                            int N, int K, int splits, int64_t c_split_stride, int epi, const float* bias,
+                            int act, float* pre, const float* aux, int64_t ldaux, float* bias_grad, int tile) {
+  if (M < 0 || N < 0 || K < 0 || splits < 1 || a_layout < 0 || a_layout > 1 || b_layout < 0 || b_layout > 1 ||
+      epi < 0 || epi > 2 || act < 0 || act > 3)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32: bad argument (M=%d N=%d K=%d splits=%d)", M, N, K, splits);
+  if (M == 0 || N == 0) return PPO_OK;
+  if (!A || !B || !C) return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32: null operand");
+  if (epi == EPI_DACT && !aux) return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32: EPI_DACT needs aux");
+  if (bias_grad && !(a_layout == 1 && b_layout == 0))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32: bias_grad needs a_layout=1, b_layout=0");
+  if (splits > 1 && c_split_stride < (int64_t)M * ldc)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32: split stride too small");
+  GemmParams p;
+  p.A = A; p.lda = lda; p.rows = rows; p.B = B; p.ldb = ldb; p.C = C; p.ldc = ldc;
+  p.c_split_stride = c_split_stride; p.M = M; p.N = N; p.K = K;
+  const int kps = ((ppo::ceil_div(K > 0 ? K : 1, splits) + BK - 1) / BK) * BK;
+  p.k_per_split = kps;
+  p.epi = epi; p.bias = bias; p.act = act; p.pre = pre; p.aux = aux; p.ldaux = ldaux; p.bias_grad = bias_grad;
+  // vector loads need 16-byte rows along the contiguous axis
+  const int a_contig = a_layout == 0 ? K : M;
+  const int b_contig = b_layout == 1 ? K : N;
+  const bool va = (lda % 4 == 0) && (a_contig % 4 == 0) && aligned16(A);
+  const bool vb = (ldb % 4 == 0) && (b_contig % 4 == 0) && aligned16(B);
+  if (tile < 0) {
+    const int64_t t128 = (int64_t)ppo::ceil_div(M, 128) * ppo::ceil_div(N, 128) * splits;
+    if (t128 >= 512) tile = 0;
+    else if ((int64_t)ppo::ceil_div(M, 128) * ppo::ceil_div(N, 64) * splits >= 512) tile = 1;
+    else if ((int64_t)ppo::ceil_div(M, 64) * ppo::ceil_div(N, 128) * splits >= 512) tile = 2;
+    else tile = 3;
+  }
+  hipStream_t st = ppo::as_stream(stream);
+  if (a_layout == 0 && b_layout == 0) return launch_layout<true, false>(st, p, splits, va, vb, tile);
+  if (a_layout == 0 && b_layout == 1) return launch_layout<true, true>(st, p, splits, va, vb, tile);
+  if (a_layout == 1 && b_layout == 0) return launch_layout<false, false>(st, p, splits, va, vb, tile);
+  return launch_layout<false, true>(st, p, splits, va, vb, tile);
+}

@@ -1,0 +1,502 @@
+"""The compiled PPO learner step for MLP actor-critics.
+
+``Program`` lowers a network plan into the flat parameter layout and a tower
+structure (trunk layers; actor / critic layers; heads).  ``MLPExecutor``
+binds a program to one rollout shape (T, N, minibatches, epochs), owns every
+device buffer the update needs, and issues the update as a fixed sequence of
+C-ABI launches on one stream:
+
+    bootstrap value  (critic path on second.obs[-1])   ppo.py:208-212
+    GAE reverse scan                                    ppo.py:213-219
+    E epoch permutations (threefry + radix sort)        ppo.py:199-201,230-231
+    per minibatch (ppo.py:148-197):
+        forward GEMMs (minibatch rows gathered inside the first GEMM)
+        head GEMM -> fused loss + cotangents -> 8 logged scalars
+        backward GEMMs (dX with the activation derivative fused, dW split
+        over rows with the bias gradient), LayerNorm backward
+        gradient assembly (+ global-norm partials), clip + Adam
+
+Because every pointer is fixed once the executor exists, the whole update can
+be captured into one HIP graph and replayed (the optax step count and the
+PRNG key are read from device memory).
+"""
+from __future__ import annotations
+
+import math
+import struct
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import _lib
+from .flat import FlatLayout, Region, round_up
+
+EPI_STORE, EPI_BIAS_ACT, EPI_DACT = 0, 1, 2
+A_ROW, A_COL = 0, 1          # a_layout: [m][k] / [k][m]
+B_KN, B_NK = 0, 1            # b_layout: [k][n] / [n][k]
+
+
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+def _act(name):
+    return _lib.ACT[name]
+
+
+# ------------------------------------------------------------------- program
+@dataclass
+class DenseSpec:
+    path: tuple
+    fin: int
+    fout: int
+    w: Region
+    b: Region | None
+
+
+@dataclass
+class LayerSpec:
+    dense: DenseSpec
+    ln: dict | None = None        # {"path", "eps", "scale": Region, "bias": Region}
+    act: str | None = None
+
+    @property
+    def fout(self):
+        return self.dense.fout
+
+    @property
+    def ld(self):
+        return self.dense.w.ld
+
+
+def _group(stages):
+    """dense [layernorm] [act] groups; returns (layers, trailing dense or None)."""
+    layers, i = [], 0
+    while i < len(stages):
+        st = stages[i]
+        if st["op"] != "dense":
+            raise NotImplementedError(f"stage {st['op']} must follow a Dense layer")
+        layer = {"dense": st, "ln": None, "act": None}
+        i += 1
+        if i < len(stages) and stages[i]["op"] == "layernorm":
+            layer["ln"] = stages[i]
+            i += 1
+        if i < len(stages) and stages[i]["op"] == "act":
+            layer["act"] = stages[i]["fn"]
+            i += 1
+        layers.append(layer)
+    return layers
+
+
+class Program:
+    """Flat layout + tower structure of an MLP actor-critic plan."""
+
+    def __init__(self, plan: dict):
+        if plan.get("torso") is not None:
+            raise NotImplementedError("recurrent torsos use the recurrent executor")
+        if plan["compute_dtype"] != "float32":
+            raise NotImplementedError("bf16 compute is not compiled yet")
+        self.plan = plan
+        L = FlatLayout()
+        self.layout = L
+
+        def dense(st, ld=None, w_region=None, b_region=None, col=0):
+            fin, fout = st["in"], st["out"]
+            if w_region is None:
+                w_region = L.region(fin, ld or round_up(fout, 4))
+            L.add_leaf(tuple(st["path"]) + ("kernel",), w_region.offset + col, (fin, fout), (w_region.ld, 1))
+            if st.get("bias", True):
+                if b_region is None:
+                    b_region = L.region(1, w_region.ld)
+                L.add_leaf(tuple(st["path"]) + ("bias",), b_region.offset + col, (fout,), (1,))
+            return DenseSpec(tuple(st["path"]), fin, fout, w_region, b_region if st.get("bias", True) else None)
+
+        def layer(g):
+            d = dense(g["dense"])
+            ln = None
+            if g["ln"] is not None:
+                F = g["dense"]["out"]
+                sc, bi = L.region(1, F), L.region(1, F)
+                L.add_leaf(tuple(g["ln"]["path"]) + ("scale",), sc.offset, (F,), (1,))
+                L.add_leaf(tuple(g["ln"]["path"]) + ("bias",), bi.offset, (F,), (1,))
+                ln = {"path": tuple(g["ln"]["path"]), "eps": g["ln"].get("eps", 1e-6), "scale": sc, "bias": bi}
+            return LayerSpec(d, ln, g["act"])
+
+        trunk = _group(plan["trunk"])
+        actor = _group(plan["actor"])
+        critic = _group(plan["critic"])
+        if not actor or actor[-1]["ln"] is not None or actor[-1]["act"] is not None:
+            raise NotImplementedError("the actor must end in a plain Dense")
+        if not critic or critic[-1]["ln"] is not None or critic[-1]["act"] is not None:
+            raise NotImplementedError("the critic must end in a plain Dense")
+        actor_head, critic_head = actor[-1]["dense"], critic[-1]["dense"]
+        actor, critic = actor[:-1], critic[:-1]
+        if trunk and (actor or critic):
+            raise NotImplementedError("a shared trunk followed by separate towers is not compiled")
+        self.trunk = [layer(g) for g in trunk]
+        self.actor_layers = [layer(g) for g in actor]
+        self.critic_layers = [layer(g) for g in critic]
+        self.dist = plan["dist"]
+        self.head_out = actor_head["out"]
+        self.shared_head = not actor and not critic
+        if self.shared_head:
+            F = actor_head["in"]
+            ldh = round_up(self.head_out + 1, 4)
+            w = L.region(F, ldh)
+            b = L.region(1, ldh)
+            self.head_a = dense(actor_head, w_region=w, b_region=b, col=0)
+            self.head_c = dense(critic_head, w_region=w, b_region=b, col=self.head_out)
+        else:
+            self.head_a = dense(actor_head)
+            self.head_c = dense(critic_head)
+        self.scale_region = None
+        if self.dist["kind"] == "gaussian" and self.dist.get("scale") is not None:
+            D = self.dist["dim"]
+            self.scale_region = L.region(1, D)
+            L.add_leaf(tuple(self.dist["scale"]), self.scale_region.offset, (D,), (1,))
+        L.finish()
+
+    @property
+    def action_dim(self) -> int:
+        return self.dist["num"] if self.dist["kind"] == "categorical" else self.dist["dim"]
+
+
+# --------------------------------------------------------------- buffers
+def _splits(rows: int, m: int, n: int) -> int:
+    tiles = max(1, math.ceil(m / 128) * math.ceil(n / 128))
+    return max(1, min(max(1, rows // 256), math.ceil(512 / tiles)))
+
+
+@dataclass
+class LayerBufs:
+    spec: LayerSpec
+    Y: torch.Tensor
+    Z: torch.Tensor | None = None
+    PRE: torch.Tensor | None = None
+    mean: torch.Tensor | None = None
+    rstd: torch.Tensor | None = None
+    dY: torch.Tensor | None = None
+    dZ: torch.Tensor | None = None
+    wpart: torch.Tensor | None = None
+    bpart: torch.Tensor | None = None
+    lnpart: torch.Tensor | None = None
+    splits: int = 1
+    lnblocks: int = 0
+
+
+class FlatState:
+    """Device buffers of the parameters, gradient, Adam moments and count."""
+
+    def __init__(self, program: Program, device):
+        n = program.layout.size
+        self.program = program
+        self.device = device
+        self.P = torch.zeros(n, dtype=torch.float32, device=device)
+        self.G = torch.zeros(n, dtype=torch.float32, device=device)
+        self.MU = torch.zeros(n, dtype=torch.float32, device=device)
+        self.NU = torch.zeros(n, dtype=torch.float32, device=device)
+        self.count = torch.zeros(1, dtype=torch.int32, device=device)
+
+    def view(self, region: Region, col: int = 0) -> int:
+        return self.P.data_ptr() + 4 * (region.offset + col)
+
+
+class MLPExecutor:
+    """One compiled PPO.update for fixed (T, N, obs, minibatches, epochs)."""
+
+    def __init__(self, program: Program, flat: FlatState, cfg, chain, T: int, N: int):
+        self._call = _lib.call
+        self.prog = program
+        self.flat = flat
+        self.cfg = cfg
+        self.chain = chain
+        self.T, self.N = T, N
+        self.B = T * N
+        self.E = int(cfg.update_epochs)
+        self.M = int(cfg.num_minibatches)
+        if self.B % self.M:
+            raise ValueError(f"batch {self.B} is not divisible into {self.M} minibatches")
+        self.mb = self.B // self.M
+        dev = flat.device
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.obs_dim = program.plan["obs_dim"]
+        mb = self.mb
+
+        def layer_bufs(spec: LayerSpec, rows: int, train: bool) -> LayerBufs:
+            ld = spec.ld
+            b = LayerBufs(spec, Y=torch.zeros(rows, ld, **f32))
+            if spec.ln is not None:
+                b.Z = torch.zeros(rows, ld, **f32)
+                b.mean = torch.zeros(rows, **f32)
+                b.rstd = torch.zeros(rows, **f32)
+            elif spec.act == "silu":
+                b.PRE = torch.zeros(rows, ld, **f32)
+            if train:
+                b.dZ = torch.zeros(rows, ld, **f32)
+                if spec.ln is not None:
+                    b.dY = torch.zeros(rows, ld, **f32)
+                    b.lnblocks = _lib.load().ppo_layernorm_bwd_blocks(rows)
+                    b.lnpart = torch.zeros(b.lnblocks, 2 * spec.fout, **f32)
+                b.splits = _splits(rows, spec.dense.fin, ld)
+                b.wpart = torch.zeros(b.splits, spec.dense.fin, ld, **f32)
+                b.bpart = torch.zeros(b.splits, ld, **f32)
+            return b
+
+        self.trunk = [layer_bufs(s, mb, True) for s in program.trunk]
+        self.actor = [layer_bufs(s, mb, True) for s in program.actor_layers]
+        self.critic = [layer_bufs(s, mb, True) for s in program.critic_layers]
+        self.boot_layers = [layer_bufs(s, N, False) for s in
+                            (program.trunk if program.shared_head else program.critic_layers)]
+        ha, hc = program.head_a, program.head_c
+        if program.shared_head:
+            self.HEAD = torch.zeros(mb, ha.w.ld, **f32)
+            self.DHEAD = torch.zeros(mb, ha.w.ld, **f32)
+            self.head_splits = _splits(mb, ha.fin, ha.w.ld)
+            self.HWPART = torch.zeros(self.head_splits, ha.fin, ha.w.ld, **f32)
+            self.HBPART = torch.zeros(self.head_splits, ha.w.ld, **f32)
+            self.HEADB = torch.zeros(N, ha.w.ld, **f32)
+        else:
+            self.HA = torch.zeros(mb, ha.w.ld, **f32)
+            self.DHA = torch.zeros(mb, ha.w.ld, **f32)
+            self.HC = torch.zeros(mb, hc.w.ld, **f32)
+            self.DHC = torch.zeros(mb, hc.w.ld, **f32)
+            self.ha_splits = _splits(mb, ha.fin, ha.w.ld)
+            self.hc_splits = _splits(mb, hc.fin, hc.w.ld)
+            self.HAWPART = torch.zeros(self.ha_splits, ha.fin, ha.w.ld, **f32)
+            self.HABPART = torch.zeros(self.ha_splits, ha.w.ld, **f32)
+            self.HCWPART = torch.zeros(self.hc_splits, hc.fin, hc.w.ld, **f32)
+            self.HCBPART = torch.zeros(self.hc_splits, hc.w.ld, **f32)
+            self.HEADB = torch.zeros(N, hc.w.ld, **f32)
+        lib = _lib.load()
+        self.loss_blocks = lib.ppo_loss_blocks(mb)
+        self.nstat = lib.ppo_loss_stat_count()
+        self.STATS = torch.zeros(self.loss_blocks, self.nstat, dtype=torch.float64, device=dev)
+        self.DSCALE = (torch.zeros(self.loss_blocks, program.dist["dim"], **f32)
+                       if program.scale_region is not None else None)
+        self.LOGS = torch.zeros(self.E * self.M, 9, **f32)
+        self.BOOT = torch.zeros(N, **f32)
+        self.ADV = torch.zeros(self.B, **f32)
+        self.RET = torch.zeros(self.B, **f32)
+        self.PERM = torch.zeros(self.E, self.B, dtype=torch.int32, device=dev)
+        ws = lib.ppo_epoch_permutations_workspace(self.E, self.B)
+        self.PERM_WS = torch.zeros(ws, dtype=torch.uint8, device=dev)
+        self.KEY = torch.zeros(2, dtype=torch.int32, device=dev)
+        self._build_reduce_tables()
+
+    # ------------------------------------------------------ gradient tables
+    def _build_reduce_tables(self):
+        flat = self.flat
+        G = flat.G.data_ptr()
+        segs = []  # (dst, src, count, part_stride, nparts)
+
+        def dense_segs(spec: DenseSpec, wpart, bpart, splits):
+            n = spec.fin * spec.w.ld
+            segs.append((G + 4 * spec.w.offset, wpart.data_ptr(), n, n, splits))
+            if spec.b is not None:
+                segs.append((G + 4 * spec.b.offset, bpart.data_ptr(), spec.w.ld, spec.w.ld, splits))
+
+        for lb in self.trunk + self.actor + self.critic:
+            dense_segs(lb.spec.dense, lb.wpart, lb.bpart, lb.splits)
+            if lb.spec.ln is not None:
+                F = lb.spec.fout
+                segs.append((G + 4 * lb.spec.ln["scale"].offset, lb.lnpart.data_ptr(), F, 2 * F, lb.lnblocks))
+                segs.append((G + 4 * lb.spec.ln["bias"].offset, lb.lnpart.data_ptr() + 4 * F, F, 2 * F,
+                             lb.lnblocks))
+        p = self.prog
+        if p.shared_head:
+            dense_segs(p.head_a, self.HWPART, self.HBPART, self.head_splits)
+        else:
+            dense_segs(p.head_a, self.HAWPART, self.HABPART, self.ha_splits)
+            dense_segs(p.head_c, self.HCWPART, self.HCBPART, self.hc_splits)
+        if p.scale_region is not None:
+            D = p.dist["dim"]
+            segs.append((G + 4 * p.scale_region.offset, self.DSCALE.data_ptr(), D, D, self.loss_blocks))
+        lib = _lib.load()
+        assert lib.ppo_grad_reduce_segment_bytes() == 40 and lib.ppo_grad_reduce_chunk_bytes() == 16
+        chunk = lib.ppo_grad_reduce_chunk_elems()
+        seg_bytes = b"".join(struct.pack("<QQqqii", d, s, c, st, n, 0) for d, s, c, st, n in segs)
+        chunks = []
+        for i, (_, _, c, _, _) in enumerate(segs):
+            for start in range(0, c, chunk):
+                chunks.append(struct.pack("<iiq", i, 0, start))
+        dev = flat.device
+        self.SEGS = torch.tensor(list(seg_bytes), dtype=torch.uint8, device=dev)
+        self.CHUNKS = torch.tensor(list(b"".join(chunks)), dtype=torch.uint8, device=dev)
+        self.nchunks = len(chunks)
+        self.SUMSQ = torch.zeros(self.nchunks, dtype=torch.float64, device=dev)
+        self.segments = segs
+
+    # ------------------------------------------------------------- pieces
+    def _fwd_layers(self, st, layers, x, ldx, rows_idx, nrows):
+        for lb in layers:
+            s = lb.spec
+            d = s.dense
+            W = self.flat.view(d.w)
+            Bb = self.flat.view(d.b) if d.b is not None else None
+            if s.ln is not None:
+                self._call("ppo_gemm_f32", st, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(lb.Z), s.ld, nrows,
+                          s.ld, d.fin, 1, 0, EPI_BIAS_ACT, Bb, 0, None, None, 0, None, -1)
+                self._call("ppo_layernorm_act_fwd_f32", st, _p(lb.Z), s.ld, self.flat.view(s.ln["scale"]),
+                          self.flat.view(s.ln["bias"]), _p(lb.Y), s.ld, _p(lb.mean), _p(lb.rstd), nrows, s.fout,
+                          s.ln["eps"], _act(s.act))
+            else:
+                self._call("ppo_gemm_f32", st, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(lb.Y), s.ld, nrows,
+                          s.ld, d.fin, 1, 0, EPI_BIAS_ACT, Bb, _act(s.act), _p(lb.PRE), None, 0, None, -1)
+            x, ldx, rows_idx = _p(lb.Y), s.ld, None
+        return x, ldx, rows_idx
+
+    def _dx_target(self, lb: LayerBufs):
+        """(dst, epi, act, aux, ldaux) for the cotangent of layer lb's output."""
+        s = lb.spec
+        if s.ln is not None:
+            return _p(lb.dY), EPI_STORE, 0, None, 0
+        if s.act is None:
+            return _p(lb.dZ), EPI_STORE, 0, None, 0
+        aux = lb.PRE if s.act == "silu" else lb.Y
+        return _p(lb.dZ), EPI_DACT, _act(s.act), _p(aux), s.ld
+
+    def _bwd_layers(self, st, layers, x0, ldx0, idx0):
+        """Back-propagates through layers whose last output cotangent is in place."""
+        for i in range(len(layers) - 1, -1, -1):
+            lb = layers[i]
+            s = lb.spec
+            d = s.dense
+            if s.ln is not None:
+                self._call("ppo_layernorm_act_bwd_f32", st, _p(lb.dY), s.ld, _p(lb.Z), s.ld, _p(lb.mean),
+                          _p(lb.rstd), self.flat.view(s.ln["scale"]), self.flat.view(s.ln["bias"]), _p(lb.dZ),
+                          s.ld, _p(lb.lnpart), self.mb, s.fout, _act(s.act))
+            if i > 0:
+                x, ldx, ridx = _p(layers[i - 1].Y), layers[i - 1].spec.ld, None
+            else:
+                x, ldx, ridx = x0, ldx0, idx0
+            self._call("ppo_gemm_f32", st, A_COL, B_KN, x, ldx, ridx, _p(lb.dZ), s.ld, _p(lb.wpart), s.ld, d.fin,
+                      s.ld, self.mb, lb.splits, d.fin * s.ld, EPI_STORE, None, 0, None, None, 0, _p(lb.bpart), -1)
+            if i > 0:
+                dst, epi, act, aux, ldaux = self._dx_target(layers[i - 1])
+                self._call("ppo_gemm_f32", st, A_ROW, B_NK, _p(lb.dZ), s.ld, None, self.flat.view(d.w), d.w.ld,
+                          dst, layers[i - 1].spec.ld, self.mb, d.fin, s.ld, 1, 0, epi, None, act, aux, ldaux,
+                          None, -1)
+
+    def _head_back(self, st, layers, dhead, head: DenseSpec, wpart, bpart, splits, hx, ldhx, hidx):
+        """Head dW and the cotangent of the head input."""
+        self._call("ppo_gemm_f32", st, A_COL, B_KN, hx, ldhx, hidx, _p(dhead), head.w.ld, _p(wpart), head.w.ld,
+                  head.fin, head.w.ld, self.mb, splits, head.fin * head.w.ld, EPI_STORE, None, 0, None, None, 0,
+                  _p(bpart), -1)
+        if layers:
+            dst, epi, act, aux, ldaux = self._dx_target(layers[-1])
+            self._call("ppo_gemm_f32", st, A_ROW, B_NK, _p(dhead), head.w.ld, None, self.flat.view(head.w),
+                      head.w.ld, dst, layers[-1].spec.ld, self.mb, head.fin, head.w.ld, 1, 0, epi, None, act, aux,
+                      ldaux, None, -1)
+
+    # ----------------------------------------------------------- the update
+    def bind(self, inputs: dict):
+        """Pointers of the transition leaves (device tensors, time-major)."""
+        self.inp = inputs
+
+    def issue(self, st: int, max_steps: int | None = None):
+        """Enqueues one whole PPO.update on stream handle ``st``.  ``max_steps``
+        stops after that many minibatch steps (the gradient buffer then holds
+        the last step's gradient): a hook for parity tests."""
+        inp, prog, cfg, chain = self.inp, self.prog, self.cfg, self.chain
+        T, N, B, mb = self.T, self.N, self.B, self.mb
+        obs, ldo = inp["obs"], self.obs_dim
+        # 1. bootstrap value of second.obs[-1] with the current parameters
+        x, ldx, _ = inp["next_obs_last"], ldo, None
+        if prog.shared_head:
+            x, ldx, _ = self._fwd_layers(st, self.boot_layers, x, ldx, None, N)
+            h = prog.head_a
+            self._call("ppo_gemm_f32", st, A_ROW, B_KN, x, ldx, None, self.flat.view(h.w), h.w.ld, _p(self.HEADB),
+                      h.w.ld, N, h.w.ld, h.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(h.b), 0, None, None, 0, None, -1)
+            vcol = prog.head_out
+        else:
+            x, ldx, _ = self._fwd_layers(st, self.boot_layers, x, ldx, None, N)
+            h = prog.head_c
+            self._call("ppo_gemm_f32", st, A_ROW, B_KN, x, ldx, None, self.flat.view(h.w), h.w.ld, _p(self.HEADB),
+                      h.w.ld, N, h.w.ld, h.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(h.b), 0, None, None, 0, None, -1)
+            vcol = 0
+        self._call("ppo_act_fwd_f32", st, _p(self.HEADB) + 4 * vcol, self.HEADB.shape[1], _p(self.BOOT), 1, N, 1, 0)
+        # 2. GAE
+        self._call("ppo_gae_f32", st, inp["reward"], inp["terminated"], inp["truncated"], inp["value"],
+                  _p(self.BOOT), None, None, _p(self.ADV), _p(self.RET), T, N, float(cfg.gamma),
+                  float(cfg.gae_lambda), 0)
+        if cfg.normalize_advantage:
+            raise NotImplementedError("normalize_advantage is not compiled yet")
+        # 3. epoch permutations of the flattened batch
+        self._call("ppo_epoch_permutations", st, _p(self.KEY), self.E, B, _p(self.PERM), _p(self.PERM_WS),
+                  self.PERM_WS.numel())
+        # 4. minibatch steps
+        adam = chain.adam
+        max_norm = chain.max_grad_norm if chain.max_grad_norm is not None else 0.0
+        dist = _lib.DIST[prog.dist["kind"]]
+        A = prog.action_dim
+        for e in range(self.E):
+            for m in range(self.M):
+                step = e * self.M + m
+                if max_steps is not None and step >= max_steps:
+                    return
+                idx = _p(self.PERM) + 4 * (e * B + m * mb)
+                self._minibatch(st, idx, step, obs, ldo, dist, A)
+                self._call("ppo_grad_reduce", st, _p(self.SEGS), _p(self.CHUNKS), self.nchunks, _p(self.SUMSQ))
+                self._call("ppo_adam_clip_f32", st, _p(self.flat.P), _p(self.flat.G), _p(self.flat.MU),
+                          _p(self.flat.NU), None, self.flat.P.numel(), _p(self.SUMSQ), self.nchunks,
+                          float(max_norm), adam.learning_rate, adam.b1, adam.b2, adam.eps, _p(self.flat.count),
+                          step)
+        self._call("ppo_count_advance", st, _p(self.flat.count), self.E * self.M)
+
+    def _minibatch(self, st, idx, step, obs, ldo, dist, A):
+        prog, cfg, inp, mb = self.prog, self.cfg, self.inp, self.mb
+        clip = float(cfg.clip_coefficient)
+        scale_ptr = self.flat.view(prog.scale_region) if prog.scale_region is not None else None
+        act_i = inp["action"] if dist == 0 else None
+        act_f = inp["action"] if dist == 1 else None
+        if prog.shared_head:
+            hx, ldhx, hidx = self._fwd_layers(st, self.trunk, obs, ldo, idx, mb)
+            h = prog.head_a
+            self._call("ppo_gemm_f32", st, A_ROW, B_KN, hx, ldhx, hidx, self.flat.view(h.w), h.w.ld, _p(self.HEAD),
+                      h.w.ld, mb, h.w.ld, h.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(h.b), 0, None, None, 0, None,
+                      -1)
+            vcol = prog.head_out
+            self._call("ppo_loss_f32", st, dist, mb, idx, _p(self.HEAD), h.w.ld, _p(self.HEAD) + 4 * vcol, h.w.ld,
+                      A, scale_ptr, act_i, act_f, inp["log_prob"], inp["value"], _p(self.ADV), _p(self.RET),
+                      _p(self.DHEAD), _p(self.DHEAD) + 4 * vcol, _p(self.DSCALE), _p(self.STATS), clip,
+                      int(cfg.clip_value_loss), float(cfg.entropy_coefficient), float(cfg.value_coefficient), 1.0)
+            self._call("ppo_loss_finalize", st, _p(self.STATS), self.loss_blocks, mb,
+                      float(cfg.entropy_coefficient), float(cfg.value_coefficient), _p(self.LOGS) + 4 * 9 * step)
+            self._head_back(st, self.trunk, self.DHEAD, h, self.HWPART, self.HBPART, self.head_splits, hx, ldhx,
+                            hidx)
+            self._bwd_layers(st, self.trunk, obs, ldo, idx)
+        else:
+            ax, ldax, aidx = self._fwd_layers(st, self.actor, obs, ldo, idx, mb)
+            cx, ldcx, cidx = self._fwd_layers(st, self.critic, obs, ldo, idx, mb)
+            ha, hc = prog.head_a, prog.head_c
+            self._call("ppo_gemm_f32", st, A_ROW, B_KN, ax, ldax, aidx, self.flat.view(ha.w), ha.w.ld, _p(self.HA),
+                      ha.w.ld, mb, ha.w.ld, ha.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(ha.b), 0, None, None, 0,
+                      None, -1)
+            self._call("ppo_gemm_f32", st, A_ROW, B_KN, cx, ldcx, cidx, self.flat.view(hc.w), hc.w.ld, _p(self.HC),
+                      hc.w.ld, mb, hc.w.ld, hc.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(hc.b), 0, None, None, 0,
+                      None, -1)
+            self._call("ppo_loss_f32", st, dist, mb, idx, _p(self.HA), ha.w.ld, _p(self.HC), hc.w.ld, A, scale_ptr,
+                      act_i, act_f, inp["log_prob"], inp["value"], _p(self.ADV), _p(self.RET), _p(self.DHA),
+                      _p(self.DHC), _p(self.DSCALE), _p(self.STATS), clip, int(cfg.clip_value_loss),
+                      float(cfg.entropy_coefficient), float(cfg.value_coefficient), 1.0)
+            self._call("ppo_loss_finalize", st, _p(self.STATS), self.loss_blocks, mb,
+                      float(cfg.entropy_coefficient), float(cfg.value_coefficient), _p(self.LOGS) + 4 * 9 * step)
+            self._head_back(st, self.actor, self.DHA, ha, self.HAWPART, self.HABPART, self.ha_splits, ax, ldax,
+                            aidx)
+            self._head_back(st, self.critic, self.DHC, hc, self.HCWPART, self.HCBPART, self.hc_splits, cx, ldcx,
+                            cidx)
+            self._bwd_layers(st, self.actor, obs, ldo, idx)
+            self._bwd_layers(st, self.critic, obs, ldo, idx)
+
+    # ------------------------------------------------------------ recording
+    def record(self, max_steps: int | None = None) -> list:
+        """The launch sequence of one update as (entry point, args) without
+        running it (used by the benchmark to time single launches)."""
+        calls = []
+        self._call = lambda name, *args: calls.append((name, args))
+        try:
+            self.issue(0, max_steps=max_steps)
+        finally:
+            self._call = _lib.call
+        return calls

@@ -1,0 +1,148 @@
+/*
+ * libppo_hip.so — C ABI of the MI355X (gfx950) PPO learner kernels.
+ *
+ * These are the entry points the XLA FFI custom-call targets of boonta's
+ * learner bind (one handler per target, each forwarding XLA's stream and
+ * buffers to the launcher below).  They take a HIP stream
+ * as `void*`, device pointers and sizes; enqueue work asynchronously; never
+ * synchronise, allocate, or retain pointers across calls; and return 0 or a
+ * negative status, with a message from ppo_last_error() on the calling thread.
+ * Every [T, N] array is time-major (row t, column n), as boonta's rollout
+ * leaves it; every matrix is row-major with an explicit leading dimension.
+ */
+#ifndef PPO_HIP_H_
+#define PPO_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define PPO_OK 0
+#define PPO_ERR_ARG (-1)
+#define PPO_ERR_LAUNCH (-2)
+#define PPO_ERR_SPACE (-3)
+
+/* Activation codes (flax.linen relu / tanh / silu). */
+#define PPO_ACT_NONE 0
+#define PPO_ACT_RELU 1
+#define PPO_ACT_TANH 2
+#define PPO_ACT_SILU 3
+
+/* Distribution codes of the actor head. */
+#define PPO_DIST_CATEGORICAL 0
+#define PPO_DIST_GAUSSIAN 1
+
+/* ---------------------------------------------------------------- errors */
+const char* ppo_last_error(void);
+void ppo_clear_error(void);
+int ppo_abi_version(void);
+int ppo_device_check(int device);
+
+/* ------------------------------------------------------------------- GAE
+ * Replaces boonta/algorithms/advantage_estimators.py:8-56
+ * (generalized_advantage_estimator(transitions, values, bootstrap, gamma,
+ * gae_lambda, rho=1., c=1.) -> (advantages, returns)), called at
+ * boonta/algorithms/ppo.py:213-219 and recurrent_ppo.py:199-205.
+ * reward/values/rho/c/advantages/returns: float [T, N]; terminated/truncated:
+ * bool bytes [T, N]; bootstrap: float [N]; rho, c may be NULL (= 1).
+ * chunks: pieces the T axis is cut into (<= 16); 0 picks one. */
+int ppo_gae_f32(void* stream, const float* reward, const uint8_t* terminated, const uint8_t* truncated,
+                const float* values, const float* bootstrap, const float* rho, const float* c,
+                float* advantages, float* returns, int T, int N, double gamma, double gae_lambda,
+                int chunks);
+
+/* ----------------------------------------------------------- permutation
+ * Replace jax.random.split(key, E) and jax.random.permutation(key, n) at
+ * boonta/algorithms/ppo.py:200,230 and recurrent_ppo.py:272,278 (jax 0.10.2,
+ * threefry2x32, partitionable).  key: device uint32[2] key data. */
+int ppo_threefry_split(void* stream, const uint32_t* key, uint32_t* out, int64_t num);
+size_t ppo_permutation_workspace(int64_t n);
+int ppo_permutation(void* stream, const uint32_t* key, int32_t* out, int64_t n, void* workspace,
+                    size_t workspace_bytes);
+size_t ppo_epoch_permutations_workspace(int epochs, int64_t n);
+/* out[e * n + i] = permutation(split(key, epochs)[e], n)[i] (ppo.py:199-201,230-231). */
+int ppo_epoch_permutations(void* stream, const uint32_t* key, int epochs, int64_t n, int32_t* out,
+                           void* workspace, size_t workspace_bytes);
+
+/* ------------------------------------------------------------------ GEMM
+ * Dense layers of the torso and heads (flax.linen.Dense as composed in
+ * hangar/recipes/*.py; forward at boonta/networks/network.py:38-49, backward
+ * of jax.value_and_grad at boonta/algorithms/ppo.py:155-157), fp32 MFMA.
+ * C[m][n] (+ split * c_split_stride) = epilogue(sum_k A(m,k) B(k,n))
+ *   a_layout 0: A[m*lda + k]   1: A[k*lda + m]
+ *   b_layout 0: B[k*ldb + n]   1: B[n*ldb + k]
+ *   rows: gather of A's rows (layout 0 over m, layout 1 over k), or NULL
+ *   epi 0: store; 1: + bias[n], activation `act` (pre-activation to `pre`);
+ *       2: multiply by act'(aux) (aux: activation output for relu/tanh,
+ *       input for silu)
+ *   splits > 1: split of the reduction; partial s at C + s * c_split_stride
+ *   bias_grad (a_layout 1, b_layout 0): [splits][N] column sums of B
+ *   tile: -1 automatic; 0 128x128, 1 128x64, 2 64x128, 3 64x64. */
+int ppo_gemm_f32(void* stream, int a_layout, int b_layout, const float* A, int64_t lda, const int32_t* rows,
+                 const float* B, int64_t ldb, float* C, int64_t ldc, int M, int N, int K, int splits,
+                 int64_t c_split_stride, int epi, const float* bias, int act, float* pre, const float* aux,
+                 int64_t ldaux, float* bias_grad, int tile);
+
+/* ------------------------------------------------------ LayerNorm / act
+ * flax.linen.LayerNorm (epsilon, fast variance, scale and bias) followed by
+ * an activation, as the Dense -> LayerNorm -> act blocks of the configs.
+ * Forward stores per-row mean/rstd for the backward. */
+int ppo_layernorm_act_fwd_f32(void* stream, const float* z, int64_t ldz, const float* gamma, const float* beta,
+                              float* y, int64_t ldy, float* mean, float* rstd, int rows, int F, float eps,
+                              int act);
+int ppo_layernorm_bwd_blocks(int rows);
+/* dy: cotangent of the activation output; writes dz and partial[blocks][2F]
+ * (scale | bias gradient sums per block). */
+int ppo_layernorm_act_bwd_f32(void* stream, const float* dy, int64_t lddy, const float* z, int64_t ldz,
+                              const float* mean, const float* rstd, const float* gamma, const float* beta,
+                              float* dz, int64_t lddz, float* partial, int rows, int F, int act);
+int ppo_act_fwd_f32(void* stream, const float* x, int64_t ldx, float* y, int64_t ldy, int rows, int F, int act);
+int ppo_act_bwd_f32(void* stream, const float* dy, int64_t lddy, const float* aux, int64_t ldaux, float* dx,
+                    int64_t lddx, int rows, int F, int act);
+
+/* ------------------------------------------------------------------ loss
+ * Replaces loss_fn of boonta/algorithms/ppo.py:77-146 (recurrent_ppo.py:101-184)
+ * with distrax Categorical / MultivariateNormalDiag of
+ * boonta/networks/distributions.py:8-57, and its cotangent w.r.t. the head
+ * outputs.  head: logits [rows, A] or Gaussian mean [rows, A] (+ raw scale at
+ * column A + j when scale_param is NULL); value at value[r * ldv].  Per-sample
+ * inputs are indexed through idx (minibatch row -> sample).  Writes dhead,
+ * dvalue (same layouts), stats_partial[blocks][ppo_loss_stat_count()] and,
+ * for a state-independent scale, dscale_partial[blocks][A]. */
+int ppo_loss_blocks(int rows);
+int ppo_loss_stat_count(void);
+int ppo_loss_f32(void* stream, int dist, int rows, const int32_t* idx, const float* head, int64_t ldh,
+                 const float* value, int64_t ldv, int A, const float* scale_param, const int32_t* action_i,
+                 const float* action_f, const float* old_logp, const float* old_value, const float* adv,
+                 const float* ret, float* dhead, float* dvalue, float* dscale_partial, double* stats_partial,
+                 float clip_eps, int clip_value_loss, float ent_coef, float vf_coef, float temperature);
+/* The logged scalars of ppo.py:170-179 in order, then the total loss: out9[9]. */
+int ppo_loss_finalize(void* stream, const double* stats_partial, int nblocks, int rows, float ent_coef,
+                      float vf_coef, float* out9);
+
+/* ------------------------------------------------------------- optimizer
+ * Replaces optax.chain(optax.clip_by_global_norm(max_norm), optax.adam(lr))
+ * .update + optax.apply_updates at boonta/algorithms/ppo.py:182-191 (chain
+ * built at hangar/recipes/ppo_cartpole.py:44-47), on flat fp32 buffers.
+ * ppo_grad_reduce sums the partials of every gradient leaf into the flat
+ * gradient (device tables of segments and chunks) and leaves one sum of
+ * squares per chunk; ppo_adam_clip_f32 folds them into the global norm.
+ * The optax count is count_base[0] + step_offset + 1 (device int32). */
+int ppo_grad_reduce_segment_bytes(void);
+int ppo_grad_reduce_chunk_bytes(void);
+int ppo_grad_reduce_chunk_elems(void);
+int ppo_grad_reduce(void* stream, const void* segs, const void* chunks, int nchunks, double* sumsq);
+int ppo_adam_clip_f32(void* stream, float* params, const float* grads, float* mu, float* nu, void* params_bf16,
+                      int64_t n, const double* sumsq, int nsumsq, float max_norm, float lr, float b1, float b2,
+                      float eps, const int* count_base, int step_offset);
+int ppo_count_advance(void* stream, int* count_base, int steps);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PPO_HIP_H_ */

@@ -1,0 +1,273 @@
+"""Oracle PPO learner update (test infrastructure only; float64 throughout).
+
+Restates, for the MLP and GRU actor-critics of the learner:
+
+- ``loss_fn`` boonta/algorithms/ppo.py:77-146 and recurrent_ppo.py:101-184:
+  ratio = exp(logp - old), approx KL, clip fraction, clipped surrogate,
+  (clipped) value loss, entropy bonus; and its gradient as jax.value_and_grad
+  takes it (ppo.py:155-157), including jax's tie rule for min/max (an equal
+  pair shares the cotangent half and half) and jnp.clip = min(hi, max(lo, x)).
+- the logged scalars ppo.py:167-180.
+- ``optax.chain(clip_by_global_norm(m), adam(lr))`` of optax 0.2.8 (a
+  third-party dependency, uv.lock:10743-10744; call sites
+  hangar/recipes/ppo_cartpole.py:44-47, ppo.py:182-191): g <- g if
+  ||g|| < m else (g / ||g||) * m; mu = (1-b1) g + b1 mu; nu = (1-b2) g^2 + b2 nu;
+  count += 1; p <- p - lr * (mu / (1 - b1^count)) / (sqrt(nu / (1 - b2^count)) + eps).
+- ``PPO.update`` ppo.py:199-233 and ``RecurrentPPO.update`` recurrent_ppo.py:186-281:
+  bootstrap, GAE, optional normalisation, flatten (index t * N + n), split the
+  key into E epoch keys, permute, reshape into M minibatches, scan.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import gae as _gae
+from . import nets
+from . import prng
+
+F64 = np.float64
+
+
+# ---------------------------------------------------------------- jax tie rule
+def _d_min(x, y):
+    """(d min(x,y)/dx, d min(x,y)/dy) with jax's balanced tie rule."""
+    ans = np.minimum(x, y)
+    ex, ey = (x == ans), (y == ans)
+    dx = ex / np.where(ey, 2.0, 1.0)
+    dy = ey / np.where(ex, 2.0, 1.0)
+    return dx, dy
+
+
+def _d_max(x, y):
+    ans = np.maximum(x, y)
+    ex, ey = (x == ans), (y == ans)
+    dx = ex / np.where(ey, 2.0, 1.0)
+    dy = ey / np.where(ex, 2.0, 1.0)
+    return dx, dy
+
+
+def _clip_and_grad(x, lo, hi):
+    """jnp.clip(x, lo, hi) = minimum(hi, maximum(lo, x)) and d/dx."""
+    m = np.maximum(lo, x)
+    _, dm_dx = _d_max(np.full_like(x, lo), x)
+    out = np.minimum(hi, m)
+    _, dout_dm = _d_min(np.full_like(x, hi), m)
+    return out, dout_dm * dm_dx
+
+
+# ------------------------------------------------------------------- the loss
+def loss_terms(logp, ent, value, old_logp, old_value, adv, ret, cfg):
+    """Scalar loss, logs and the per-row cotangents (g_logp, g_ent, g_value)."""
+    n = logp.shape[0]
+    eps = cfg["clip_coefficient"]
+    ratio = np.exp(logp - old_logp)
+    kl = np.mean(old_logp - logp)
+    clipfrac = np.mean((np.abs(ratio - 1.0) > eps).astype(F64))
+    cr, dcr = _clip_and_grad(ratio, 1.0 - eps, 1.0 + eps)
+    pg1, pg2 = ratio * adv, cr * adv
+    actor = -np.minimum(pg1, pg2).mean()
+    d1, d2 = _d_min(pg1, pg2)
+    d_ratio = -(d1 * adv + d2 * adv * dcr) / n
+    g_logp = d_ratio * ratio
+
+    vl1 = 0.5 * (value - ret) ** 2
+    if cfg["clip_value_loss"]:
+        dv_clip, dcv = _clip_and_grad(value - old_value, -eps, eps)
+        vc = old_value + dv_clip
+        vl2 = 0.5 * (vc - ret) ** 2
+        crit_rows = np.maximum(vl1, vl2)
+        a1, a2 = _d_max(vl1, vl2)
+        g_v_rows = a1 * (value - ret) + a2 * (vc - ret) * dcv
+    else:
+        crit_rows = vl1
+        g_v_rows = value - ret
+    critic = crit_rows.mean()
+    entropy = ent.mean()
+    loss = actor - cfg["entropy_coefficient"] * entropy + cfg["value_coefficient"] * critic
+    g_value = cfg["value_coefficient"] * g_v_rows / n
+    g_ent = np.full(n, -cfg["entropy_coefficient"] / n)
+    resid = ret - value
+    logs = {
+        "actor/loss": actor,
+        "actor/entropy": entropy,
+        "actor/approximate_kl": kl,
+        "actor/clip_fraction": clipfrac,
+        "actor/advantage": adv.mean(),
+        "critic/loss": critic,
+        "critic/explained_variance": 1.0 - resid.var() / (ret.var() + 1e-8),
+        "critic/value": value.mean(),
+    }
+    return loss, logs, (g_logp, g_ent, g_value)
+
+
+def _head_stats(params, plan, head, action):
+    d = plan["dist"]
+    if d["kind"] == "categorical":
+        lp, ent, cache = nets.categorical_stats(head, action)
+        return lp, ent, cache
+    if d["kind"] == "gaussian":
+        if d.get("scale") is not None:
+            raw = np.broadcast_to(np.asarray(nets.get(params, d["scale"]), F64), head.shape)
+            mean = head
+        else:
+            mean, raw = np.split(head, 2, axis=-1)
+        sigma = nets.gaussian_sigma(raw)
+        lp, ent = nets.gaussian_stats(mean, sigma, np.asarray(action, F64))
+        return lp, ent, (mean, raw, sigma)
+    raise ValueError(d["kind"])
+
+
+def _head_grad(plan, cache, action, g_lp, g_ent, grads):
+    d = plan["dist"]
+    if d["kind"] == "categorical":
+        return nets.categorical_grad(cache, action, g_lp, g_ent)
+    mean, raw, sigma = cache
+    dmean, dsig = nets.gaussian_grad(mean, sigma, np.asarray(action, F64), g_lp, g_ent)
+    draw = dsig / (1.0 + np.exp(-raw))       # softplus' = sigmoid
+    if d.get("scale") is not None:
+        nets.add_in(grads, tuple(d["scale"]), draw.sum(0))
+        return dmean
+    return np.concatenate([dmean, draw], axis=-1)
+
+
+def zeros_like_tree(t):
+    if isinstance(t, dict):
+        return {k: zeros_like_tree(v) for k, v in t.items()}
+    return np.zeros(np.shape(t), F64)
+
+
+def loss_and_grad(params, plan, cfg, obs, action, old_logp, old_value, adv, ret):
+    """One minibatch of the MLP learner: loss, logs, grads (float64)."""
+    head, value, cache = nets.forward(params, plan, obs)
+    lp, ent, hcache = _head_stats(params, plan, head, action)
+    loss, logs, (g_lp, g_ent, g_v) = loss_terms(
+        lp, ent, value, np.asarray(old_logp, F64), np.asarray(old_value, F64),
+        np.asarray(adv, F64), np.asarray(ret, F64), cfg)
+    grads = zeros_like_tree(params)
+    dhead = _head_grad(plan, hcache, action, g_lp, g_ent, grads)
+    nets.backward(params, plan, cache, dhead, g_v, grads)
+    return loss, logs, grads
+
+
+def recurrent_loss_and_grad(params, plan, cfg, obs, done, carry, action, old_logp,
+                            old_value, adv, ret):
+    """One env-major sequence minibatch [B, T, ...] of RecurrentPPO."""
+    B, T = done.shape
+    head, value, _, cache = nets.recurrent_forward(params, plan, obs, done, carry)
+    hf = head.reshape(B * T, -1)
+    act = np.asarray(action).reshape((B * T,) + np.shape(action)[2:])
+    lp, ent, hcache = _head_stats(params, plan, hf, act)
+    loss, logs, (g_lp, g_ent, g_v) = loss_terms(
+        lp, ent, value.reshape(-1), np.asarray(old_logp, F64).reshape(-1),
+        np.asarray(old_value, F64).reshape(-1), np.asarray(adv, F64).reshape(-1),
+        np.asarray(ret, F64).reshape(-1), cfg)
+    grads = zeros_like_tree(params)
+    dhead = _head_grad(plan, hcache, act, g_lp, g_ent, grads)
+    nets.recurrent_backward(params, plan, cache, dhead.reshape(B, T, -1),
+                            g_v.reshape(B, T), grads)
+    return loss, logs, grads
+
+
+# ------------------------------------------------------------------ optimizer
+def tree_leaves(t, prefix=()):
+    if isinstance(t, dict):
+        out = []
+        for k in sorted(t):
+            out += tree_leaves(t[k], prefix + (k,))
+        return out
+    return [(prefix, t)]
+
+
+def tree_map(f, *ts):
+    if isinstance(ts[0], dict):
+        return {k: tree_map(f, *(t[k] for t in ts)) for k in ts[0]}
+    return f(*ts)
+
+
+def optimizer_init(params):
+    z = tree_map(lambda p: np.zeros(np.shape(p), F64), params)
+    return {"count": 0, "mu": z, "nu": tree_map(np.copy, z)}
+
+
+def optimizer_update(grads, state, params, opt):
+    """clip_by_global_norm(max_grad_norm) then adam(lr, b1, b2, eps)."""
+    gnorm = np.sqrt(sum(float((np.asarray(g, F64) ** 2).sum()) for _, g in tree_leaves(grads)))
+    if opt.get("max_grad_norm") is not None and not gnorm < opt["max_grad_norm"]:
+        grads = tree_map(lambda g: (g / gnorm) * opt["max_grad_norm"], grads)
+    b1, b2, eps, lr = opt.get("b1", 0.9), opt.get("b2", 0.999), opt.get("eps", 1e-8), opt["lr"]
+    count = state["count"] + 1
+    mu = tree_map(lambda g, m: (1 - b1) * g + b1 * m, grads, state["mu"])
+    nu = tree_map(lambda g, v: (1 - b2) * g * g + b2 * v, grads, state["nu"])
+    c1, c2 = 1 - b1 ** count, 1 - b2 ** count
+    new = tree_map(lambda p, m, v: np.asarray(p, F64) - lr * ((m / c1) / (np.sqrt(v / c2) + eps)),
+                   params, mu, nu)
+    return new, {"count": count, "mu": mu, "nu": nu}, gnorm
+
+
+# ------------------------------------------------------------------- updates
+def ppo_update(params, opt_state, plan, cfg, opt, tr, key, record=None):
+    """PPO.update (ppo.py:76-233) on a transition dict of [T, N, ...] arrays:
+    obs (first.obs), next_obs_last (second.obs[-1]), action, reward,
+    terminated, truncated, log_prob, value.  Returns (params, opt_state, logs)."""
+    T, N = tr["reward"].shape
+    B = T * N
+    _, boot, _ = nets.forward(params, plan, tr["next_obs_last"])
+    adv, ret = _gae.gae(tr["reward"], tr["terminated"], tr["truncated"], tr["value"],
+                        boot, cfg["gamma"], cfg["gae_lambda"])
+    if cfg.get("normalize_advantage"):
+        adv = (adv - adv.mean()) / (adv.std() + 1e-8)
+    flat = lambda a: np.asarray(a).reshape((B,) + np.shape(a)[2:])
+    obs, act = flat(tr["obs"]), flat(tr["action"])
+    olp, ov, fa, fr = flat(tr["log_prob"]), flat(tr["value"]), flat(adv), flat(ret)
+    E, M = cfg["update_epochs"], cfg["num_minibatches"]
+    perms = prng.epoch_permutations(key, E, B)
+    logs = []
+    for e in range(E):
+        for idx in perms[e].reshape(M, -1):
+            loss, lg, grads = loss_and_grad(params, plan, cfg, obs[idx], act[idx],
+                                            olp[idx], ov[idx], fa[idx], fr[idx])
+            params, opt_state, gnorm = optimizer_update(grads, opt_state, params, opt)
+            lg["loss"] = loss
+            lg["grad_norm"] = gnorm
+            logs.append(lg)
+            if record is not None:
+                record(e, idx, grads, params)
+    return params, opt_state, {"advantages": adv, "returns": ret, "bootstrap": boot,
+                               "permutations": perms, "logs": logs}
+
+
+def recurrent_ppo_update(params, opt_state, plan, cfg, opt, tr, key, record=None):
+    """RecurrentPPO.update (recurrent_ppo.py:98-281).  ``tr`` holds time-major
+    [T, N, ...] obs, first_done (first.done), action, reward, terminated,
+    truncated, log_prob, value, carry0 (carry[0], [N, H]), carry_last
+    (carry[-1]), next_obs_last (second.obs[-1]) and next_done_last
+    (second.done[-1])."""
+    T, N = tr["reward"].shape
+    # Transition.tail (utils/transition.py:20-26): a 2-step sequence of
+    # (first[-1], second[-1]) from carry[-1]; the bootstrap is the 2nd value.
+    seq_obs = np.stack([tr["obs"][-1], tr["next_obs_last"]], axis=1)
+    seq_done = np.stack([tr["first_done"][-1], tr["next_done_last"]], axis=1)
+    _, val, _, _ = nets.recurrent_forward(params, plan, seq_obs, seq_done, tr["carry_last"])
+    boot = val[:, -1]
+    adv, ret = _gae.gae(tr["reward"], tr["terminated"], tr["truncated"], tr["value"],
+                        boot, cfg["gamma"], cfg["gae_lambda"])
+    if cfg.get("normalize_advantage"):
+        adv = (adv - adv.mean()) / (adv.std() + 1e-8)
+    E, M = cfg["update_epochs"], cfg["num_minibatches"]
+    perms = prng.epoch_permutations(key, E, N)
+    em = lambda a, idx: np.moveaxis(np.take(np.asarray(a), idx, axis=1), 0, 1)
+    logs = []
+    for e in range(E):
+        for idx in perms[e].reshape(M, -1):
+            loss, lg, grads = recurrent_loss_and_grad(
+                params, plan, cfg, em(tr["obs"], idx), em(tr["first_done"], idx),
+                np.asarray(tr["carry0"])[idx], em(tr["action"], idx),
+                em(tr["log_prob"], idx), em(tr["value"], idx), em(adv, idx), em(ret, idx))
+            params, opt_state, gnorm = optimizer_update(grads, opt_state, params, opt)
+            lg["loss"] = loss
+            lg["grad_norm"] = gnorm
+            logs.append(lg)
+            if record is not None:
+                record(e, idx, grads, params)
+    return params, opt_state, {"advantages": adv, "returns": ret, "bootstrap": boot,
+                               "permutations": perms, "logs": logs}

@@ -1,0 +1,46 @@
+"""The C ABI library loads without a GPU and exports every entry point that
+include/ppo_hip.h declares (no compute call is made here)."""
+import ctypes
+import os
+import re
+
+from boonta_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "ppo_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ppo_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_bound_functions():
+    assert set(declared_functions()) == set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    missing = [name for name in declared_functions() if not hasattr(lib, name)]
+    assert not missing
+
+
+def test_host_only_entry_points_answer_without_a_device():
+    lib = _lib.load()
+    assert lib.ppo_abi_version() == 1
+    assert lib.ppo_loss_stat_count() == 11
+    assert lib.ppo_grad_reduce_segment_bytes() == 40
+    assert lib.ppo_grad_reduce_chunk_bytes() == 16
+    assert lib.ppo_permutation_workspace(1 << 20) > 3 * 4 * (1 << 20)
+
+
+def test_argument_errors_are_reported_not_launched():
+    lib = _lib.load()
+    rc = lib.ppo_gae_f32(None, None, None, None, None, None, None, None, None, None, 4, 4, 0.99, 0.95, 0)
+    assert rc == -1
+    assert b"null buffer" in lib.ppo_last_error()
+    rc = lib.ppo_gemm_f32(None, 0, 0, None, 0, None, None, 0, None, 0, -1, 4, 4, 1, 0, 0, None, 0, None, None,
+                          0, None, -1)
+    assert rc == -1
+    assert lib.ppo_adam_clip_f32(None, None, None, None, None, None, 6, None, 0, 0.5, 1e-3, 0.9, 0.999, 1e-8,
+                                 None, 0) == -1

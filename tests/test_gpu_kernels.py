@@ -1,0 +1,349 @@
+"""Kernel-level parity of the HIP path (through the C ABI) against the oracle
+and float64 numpy: GAE, Threefry split and permutations (bit-exact), the
+fp32 MFMA GEMM in all layouts with gather / epilogues / split-K, LayerNorm,
+the fused loss and clip + Adam."""
+import numpy as np
+import pytest
+import torch
+
+from boonta_amd import _lib
+from oracle import gae as ogae
+from oracle import nets, ppo, prng
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def st():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def dev(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.to(DEV)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+# ------------------------------------------------------------------- GAE
+def run_gae(r, te, tr, v, b, gamma, lam, rho=None, c=None, chunks=0):
+    T, N = r.shape
+    adv = torch.empty(T, N, device=DEV)
+    ret = torch.empty(T, N, device=DEV)
+    R, V, Bt = dev(r.astype(np.float32)), dev(v.astype(np.float32)), dev(b.astype(np.float32))
+    TE, TR = dev(te), dev(tr)
+    RHO = dev(rho.astype(np.float32)) if rho is not None else None
+    C = dev(c.astype(np.float32)) if c is not None else None
+    _lib.call("ppo_gae_f32", st(), R.data_ptr(), TE.data_ptr(), TR.data_ptr(), V.data_ptr(), Bt.data_ptr(),
+              None if RHO is None else RHO.data_ptr(), None if C is None else C.data_ptr(), adv.data_ptr(),
+              ret.data_ptr(), T, N, gamma, lam, chunks)
+    return host(adv), host(ret)
+
+
+@pytest.mark.parametrize("weighted", [False, True], ids=["gae", "vtrace"])
+@pytest.mark.parametrize("chunks", [1, 3])
+def test_gae_on_the_reference_known_answer_case(weighted, chunks):
+    g = np.random.default_rng(0)
+    shape = (6, 3)
+    reward, values = g.normal(size=shape), g.normal(size=shape)
+    bootstrap = g.normal(size=shape[1:])
+    terminated = g.random(shape) < 0.2
+    truncated = (g.random(shape) < 0.2) & ~terminated
+    rho, c = (g.uniform(0.5, 1.5, shape) if weighted else np.ones(shape) for _ in range(2))
+    f = lambda x: x.astype(np.float32).astype(np.float64)
+    exp_a, exp_r = ogae.gae(f(reward), terminated, truncated, f(values), f(bootstrap), 0.9, 0.8,
+                            rho=f(rho), c=f(c))
+    adv, ret = run_gae(reward, terminated, truncated, values, bootstrap, 0.9, 0.8,
+                       rho if weighted else None, c if weighted else None, chunks)
+    # the reference test's tolerance (tests/test_algorithms.py:193-194)
+    np.testing.assert_allclose(adv, exp_a, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(ret, exp_r, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("T, N, chunks", [(128, 2048, 0), (128, 2048, 1), (16, 4096, 0), (64, 1024, 0),
+                                          (64, 1024, 16), (1, 5, 0), (37, 70, 4)])
+def test_gae_at_workload_shapes(T, N, chunks):
+    g = np.random.default_rng(T * 1000 + N)
+    r = g.normal(size=(T, N)).astype(np.float32)
+    v = g.normal(size=(T, N)).astype(np.float32)
+    b = g.normal(size=N).astype(np.float32)
+    te = g.random((T, N)) < 0.01
+    tr = (g.random((T, N)) < 0.005) & ~te
+    exp_a, exp_r = ogae.gae(r, te, tr, v, b, 0.99, 0.95)
+    adv, ret = run_gae(r, te, tr, v, b, 0.99, 0.95, chunks=chunks)
+    np.testing.assert_allclose(adv, exp_a, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(ret, exp_r, rtol=1e-5, atol=1e-5)
+
+
+# ------------------------------------------------------------ permutation
+def test_threefry_split_is_bit_exact():
+    for seed in (0, 1, 42, 2**31 + 5):
+        k = prng.key(seed)
+        K = dev(k.view(np.int32))
+        out = torch.empty(7, 2, dtype=torch.int32, device=DEV)
+        _lib.call("ppo_threefry_split", st(), K.data_ptr(), out.data_ptr(), 7)
+        np.testing.assert_array_equal(host(out).view(np.uint32), prng.split(k, 7))
+
+
+@pytest.mark.parametrize("n", [0, 1, 2, 7, 512, 1024, 1625, 1626, 4095, 4096, 4097, 65536, 262144])
+def test_permutation_is_bit_exact(n):
+    k = prng.key(1000 + n)
+    K = dev(k.view(np.int32))
+    out = torch.zeros(max(n, 1), dtype=torch.int32, device=DEV)
+    ws = torch.zeros(_lib.load().ppo_permutation_workspace(n), dtype=torch.uint8, device=DEV)
+    _lib.call("ppo_permutation", st(), K.data_ptr(), out.data_ptr(), n, ws.data_ptr(), ws.numel())
+    got = host(out)[:n]
+    np.testing.assert_array_equal(got, prng.permutation(k, n))
+
+
+@pytest.mark.parametrize("E, n", [(4, 512), (4, 65536), (4, 262144), (4, 1024)])
+def test_epoch_permutations_are_bit_exact(E, n):
+    k = prng.key(7 * n + E)
+    K = dev(k.view(np.int32))
+    out = torch.zeros(E, n, dtype=torch.int32, device=DEV)
+    ws = torch.zeros(_lib.load().ppo_epoch_permutations_workspace(E, n), dtype=torch.uint8, device=DEV)
+    _lib.call("ppo_epoch_permutations", st(), K.data_ptr(), E, n, out.data_ptr(), ws.data_ptr(), ws.numel())
+    np.testing.assert_array_equal(host(out), prng.epoch_permutations(k, E, n))
+
+
+# ------------------------------------------------------------------- GEMM
+def act_np(name, x):
+    return nets.act_fwd(name, x) if name != "none" else x
+
+
+def gemm_case(a_layout, b_layout, M, N, K, rows_src=None, gather=False, epi=0, act="none", splits=1,
+              with_pre=False, bias_grad=False, seed=0, tile=-1):
+    g = np.random.default_rng(seed)
+    # logical operands A (M x K) and B (K x N), stored per layout
+    if a_layout == 0:
+        src_rows = rows_src or M
+        Astore = g.standard_normal((src_rows, K)).astype(np.float32)
+        idx = g.permutation(src_rows)[:M].astype(np.int32) if gather else None
+        Alog = Astore[idx] if gather else Astore
+    else:
+        src_rows = rows_src or K
+        Astore = g.standard_normal((src_rows, M)).astype(np.float32)
+        idx = g.permutation(src_rows)[:K].astype(np.int32) if gather else None
+        Alog = (Astore[idx] if gather else Astore).T
+    Blog = g.standard_normal((K, N)).astype(np.float32)
+    Bstore = Blog if b_layout == 0 else np.ascontiguousarray(Blog.T)
+    bias = g.standard_normal(N).astype(np.float32)
+    aux = g.standard_normal((M, N)).astype(np.float32)
+    if act in ("relu", "tanh") and epi == 2:
+        aux = act_np(act, aux).astype(np.float32)
+    A_t, B_t = dev(Astore), dev(Bstore)
+    idx_t = dev(idx) if idx is not None else None
+    C = torch.zeros(splits, M, N, device=DEV)
+    PRE = torch.zeros(M, N, device=DEV) if with_pre else None
+    AUX = dev(aux)
+    BIAS = dev(bias)
+    BG = torch.zeros(splits, N, device=DEV) if bias_grad else None
+    lda = Astore.shape[1]
+    ldb = Bstore.shape[1]
+    _lib.call("ppo_gemm_f32", st(), a_layout, b_layout, A_t.data_ptr(), lda,
+              None if idx_t is None else idx_t.data_ptr(), B_t.data_ptr(), ldb, C.data_ptr(), N, M, N, K, splits,
+              M * N, epi, BIAS.data_ptr() if epi == 1 else None, _lib.ACT[act],
+              None if PRE is None else PRE.data_ptr(), AUX.data_ptr() if epi == 2 else None, N,
+              None if BG is None else BG.data_ptr(), tile)
+    ref = Alog.astype(np.float64) @ Blog.astype(np.float64)
+    got = host(C).sum(0)
+    if epi == 1:
+        pre = ref + bias
+        if with_pre:
+            np.testing.assert_allclose(host(PRE), pre, rtol=1e-4, atol=1e-4)
+        ref = act_np(act, pre)
+        got = host(C)[0]
+    elif epi == 2:
+        ref = ref * nets.act_bwd(act, aux, aux, np.ones_like(ref)) if act != "none" else ref
+        got = host(C)[0]
+    scale = np.abs(Alog).astype(np.float64) @ np.abs(Blog).astype(np.float64) + 1.0
+    assert np.all(np.abs(got - ref) <= 1e-5 * scale), np.abs(got - ref).max()
+    if bias_grad:
+        np.testing.assert_allclose(host(BG).sum(0), Blog.astype(np.float64).sum(0), rtol=1e-4, atol=1e-3)
+
+
+@pytest.mark.parametrize("a_layout, b_layout", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M, N, K", [(256, 256, 64), (100, 72, 87), (33, 7, 5), (1, 1, 1), (300, 130, 400)])
+def test_gemm_layouts_match_float64(a_layout, b_layout, M, N, K):
+    gemm_case(a_layout, b_layout, M, N, K, seed=M + N + K)
+
+
+@pytest.mark.parametrize("tile", [0, 1, 2, 3])
+def test_gemm_every_tile(tile):
+    gemm_case(0, 0, 200, 190, 48, tile=tile, seed=tile)
+    gemm_case(1, 0, 130, 70, 500, tile=tile, splits=3, bias_grad=True, seed=tile + 10)
+
+
+def test_gemm_forward_gathers_rows():
+    gemm_case(0, 0, 512, 256, 400, rows_src=4096, gather=True)
+    gemm_case(0, 0, 100, 64, 87, rows_src=1000, gather=True)
+
+
+@pytest.mark.parametrize("act", ["none", "relu", "tanh", "silu"])
+def test_gemm_bias_activation_epilogue(act):
+    gemm_case(0, 0, 300, 256, 64, epi=1, act=act, with_pre=True)
+
+
+@pytest.mark.parametrize("act", ["relu", "tanh", "silu"])
+def test_gemm_activation_derivative_epilogue(act):
+    gemm_case(0, 1, 300, 256, 136, epi=2, act=act)
+
+
+@pytest.mark.parametrize("splits", [1, 4, 64])
+def test_gemm_split_rows_with_bias_gradient(splits):
+    gemm_case(1, 0, 400, 256, 4096, rows_src=8192, gather=True, splits=splits, bias_grad=True)
+    gemm_case(1, 0, 256, 8, 2048, splits=splits, bias_grad=True)
+
+
+# -------------------------------------------------------------- LayerNorm
+@pytest.mark.parametrize("F, act", [(256, "silu"), (512, "relu"), (64, "tanh"), (100, "none")])
+def test_layernorm_forward_and_backward(F, act):
+    g = np.random.default_rng(F)
+    rows = 777
+    z = g.normal(0.3, 2.0, (rows, F)).astype(np.float32)
+    gamma = g.normal(1, 0.2, F).astype(np.float32)
+    beta = g.normal(0, 0.2, F).astype(np.float32)
+    dy = g.standard_normal((rows, F)).astype(np.float32)
+    stages = [{"op": "layernorm", "path": ("ln",), "width": F, "eps": 1e-6}]
+    if act != "none":
+        stages.append({"op": "act", "fn": act})
+    params = {"ln": {"scale": gamma, "bias": beta}}
+    y_ref, caches = nets.stages_forward(params, stages, z.astype(np.float64))
+    grads = {}
+    dz_ref = nets.stages_backward(params, stages, caches, dy.astype(np.float64), grads)
+    Z, G, Bt, DY = dev(z), dev(gamma), dev(beta), dev(dy)
+    Y = torch.zeros(rows, F, device=DEV)
+    mean = torch.zeros(rows, device=DEV)
+    rstd = torch.zeros(rows, device=DEV)
+    _lib.call("ppo_layernorm_act_fwd_f32", st(), Z.data_ptr(), F, G.data_ptr(), Bt.data_ptr(), Y.data_ptr(), F,
+              mean.data_ptr(), rstd.data_ptr(), rows, F, 1e-6, _lib.ACT[act])
+    np.testing.assert_allclose(host(Y), y_ref, rtol=1e-4, atol=1e-5)
+    blocks = _lib.load().ppo_layernorm_bwd_blocks(rows)
+    DZ = torch.zeros(rows, F, device=DEV)
+    part = torch.zeros(blocks, 2 * F, device=DEV)
+    _lib.call("ppo_layernorm_act_bwd_f32", st(), DY.data_ptr(), F, Z.data_ptr(), F, mean.data_ptr(),
+              rstd.data_ptr(), G.data_ptr(), Bt.data_ptr(), DZ.data_ptr(), F, part.data_ptr(), rows, F,
+              _lib.ACT[act])
+    np.testing.assert_allclose(host(DZ), dz_ref, rtol=1e-4, atol=1e-4)
+    p = host(part).sum(0)
+    np.testing.assert_allclose(p[:F], grads["ln"]["scale"], rtol=1e-4, atol=1e-3)
+    np.testing.assert_allclose(p[F:], grads["ln"]["bias"], rtol=1e-4, atol=1e-3)
+
+
+# ------------------------------------------------------------------- loss
+CFG = {"clip_coefficient": 0.2, "clip_value_loss": True, "entropy_coefficient": 0.01, "value_coefficient": 0.5}
+
+
+@pytest.mark.parametrize("dist, A, spread", [("categorical", 6, False), ("categorical", 43, False),
+                                             ("gaussian", 8, True), ("gaussian", 3, False)])
+def test_fused_loss_matches_the_oracle(dist, A, spread):
+    g = np.random.default_rng(A)
+    rows, B = 3000, 5000
+    width = A if (dist == "categorical" or spread) else 2 * A
+    ld = width + 2
+    head = g.normal(0, 1, (rows, ld)).astype(np.float32)
+    value = head[:, width].copy()
+    idx = g.permutation(B)[:rows].astype(np.int32)
+    if dist == "categorical":
+        action = g.integers(0, A, B).astype(np.int32)
+    else:
+        action = g.standard_normal((B, A)).astype(np.float32)
+    scale = g.normal(0, 0.5, A).astype(np.float32) if spread else None
+    old_logp = g.normal(-1.5, 0.3, B).astype(np.float32)
+    old_value = (g.normal(0, 1, B)).astype(np.float32)
+    old_value[idx[:1000]] = value[:1000] + g.normal(0, 0.05, 1000)   # some inside the value clip
+    adv = g.normal(0, 1, B).astype(np.float32)
+    ret = g.normal(0, 1, B).astype(np.float32)
+    # oracle
+    h64 = head[:, :width].astype(np.float64)
+    if dist == "categorical":
+        lp, ent, cache = nets.categorical_stats(h64, action[idx])
+    else:
+        raw = np.broadcast_to(scale.astype(np.float64), (rows, A)) if spread else h64[:, A:]
+        mean = h64[:, :A]
+        sig = nets.gaussian_sigma(raw)
+        lp, ent = nets.gaussian_stats(mean, sig, action[idx].astype(np.float64))
+    old_logp[idx[:500]] = lp[:500].astype(np.float32)   # ratio 1 rows
+    loss, logs, (g_lp, g_ent, g_v) = ppo.loss_terms(lp, ent, value.astype(np.float64),
+                                                    old_logp[idx].astype(np.float64),
+                                                    old_value[idx].astype(np.float64),
+                                                    adv[idx].astype(np.float64), ret[idx].astype(np.float64), CFG)
+    grads = {}
+    if dist == "categorical":
+        dhead_ref = nets.categorical_grad(cache, action[idx], g_lp, g_ent)
+    else:
+        dmean, dsig = nets.gaussian_grad(mean, sig, action[idx].astype(np.float64), g_lp, g_ent)
+        draw = dsig / (1 + np.exp(-raw))
+        dhead_ref = dmean if spread else np.concatenate([dmean, draw], -1)
+        dscale_ref = draw.sum(0)
+    # GPU
+    H = dev(head)
+    DH = torch.zeros(rows, ld, device=DEV)
+    blocks = _lib.load().ppo_loss_blocks(rows)
+    STATS = torch.zeros(blocks, 11, dtype=torch.float64, device=DEV)
+    DS = torch.zeros(blocks, A, device=DEV) if spread else None
+    SC = dev(scale) if spread else None
+    IDX, ACT = dev(idx), dev(action)
+    OLP, OV, ADV, RET = dev(old_logp), dev(old_value), dev(adv), dev(ret)
+    _lib.call("ppo_loss_f32", st(), _lib.DIST[dist], rows, IDX.data_ptr(), H.data_ptr(), ld,
+              H.data_ptr() + 4 * width, ld, A, None if SC is None else SC.data_ptr(),
+              ACT.data_ptr() if dist == "categorical" else None, ACT.data_ptr() if dist == "gaussian" else None,
+              OLP.data_ptr(), OV.data_ptr(), ADV.data_ptr(), RET.data_ptr(), DH.data_ptr(),
+              DH.data_ptr() + 4 * width, None if DS is None else DS.data_ptr(), STATS.data_ptr(), 0.2, 1, 0.01,
+              0.5, 1.0)
+    out = torch.zeros(9, device=DEV)
+    _lib.call("ppo_loss_finalize", st(), STATS.data_ptr(), blocks, rows, 0.01, 0.5, out.data_ptr())
+    dh = host(DH)
+    np.testing.assert_allclose(dh[:, :width], dhead_ref, rtol=1e-4, atol=1e-8)
+    np.testing.assert_allclose(dh[:, width], g_v, rtol=1e-4, atol=1e-9)
+    np.testing.assert_array_equal(dh[:, width + 1:], 0.0)
+    o = host(out)
+    names = ["actor/loss", "actor/entropy", "actor/approximate_kl", "actor/clip_fraction", "actor/advantage",
+             "critic/loss", "critic/explained_variance", "critic/value"]
+    for i, n in enumerate(names):
+        np.testing.assert_allclose(o[i], logs[n], rtol=1e-5, atol=1e-6, err_msg=n)
+    np.testing.assert_allclose(o[8], loss, rtol=1e-5, atol=1e-6)
+    if spread:
+        np.testing.assert_allclose(host(DS).sum(0), dscale_ref, rtol=1e-4, atol=1e-7)
+
+
+# ------------------------------------------------------------------- Adam
+@pytest.mark.parametrize("max_norm, scale", [(0.5, 1.0), (0.5, 1e-3), (0.0, 1.0)])
+def test_grad_reduce_and_adam_match_optax_restatement(max_norm, scale):
+    import struct
+    g = np.random.default_rng(int(scale * 1000) + int(max_norm * 10))
+    n = 4096 + 64
+    nparts = 5
+    parts = (g.standard_normal((nparts, n)) * scale * 0.01).astype(np.float32)
+    p0 = g.standard_normal(n).astype(np.float32)
+    mu0 = (g.standard_normal(n) * 1e-3).astype(np.float32)
+    nu0 = (g.random(n) * 1e-5).astype(np.float32)
+    P, MU, NU = dev(p0), dev(mu0), dev(nu0)
+    Gt = torch.zeros(n, device=DEV)
+    PARTS = dev(parts)
+    segs = struct.pack("<QQqqii", Gt.data_ptr(), PARTS.data_ptr(), n, n, nparts, 0)
+    chunk = _lib.load().ppo_grad_reduce_chunk_elems()
+    chunks = b"".join(struct.pack("<iiq", 0, 0, s) for s in range(0, n, chunk))
+    nch = len(range(0, n, chunk))
+    SEGS = torch.tensor(list(segs), dtype=torch.uint8, device=DEV)
+    CH = torch.tensor(list(chunks), dtype=torch.uint8, device=DEV)
+    SQ = torch.zeros(nch, dtype=torch.float64, device=DEV)
+    _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), CH.data_ptr(), nch, SQ.data_ptr())
+    count = torch.tensor([6], dtype=torch.int32, device=DEV)
+    _lib.call("ppo_adam_clip_f32", st(), P.data_ptr(), Gt.data_ptr(), MU.data_ptr(), NU.data_ptr(), None, n,
+              SQ.data_ptr(), nch, max_norm, 3e-4, 0.9, 0.999, 1e-8, count.data_ptr(), 2)
+    grad = parts.astype(np.float64).sum(0)
+    np.testing.assert_allclose(host(Gt), grad, rtol=1e-5, atol=1e-9)
+    opt = {"lr": 3e-4, "max_grad_norm": max_norm if max_norm > 0 else None}
+    state = {"count": 8, "mu": {"w": mu0.astype(np.float64)}, "nu": {"w": nu0.astype(np.float64)}}
+    new, st2, gn = ppo.optimizer_update({"w": grad}, state, {"w": p0.astype(np.float64)}, opt)
+    np.testing.assert_allclose(np.sqrt(host(SQ).sum()), gn, rtol=1e-6)
+    np.testing.assert_allclose(host(MU), st2["mu"]["w"], rtol=1e-5, atol=1e-10)
+    np.testing.assert_allclose(host(NU), st2["nu"]["w"], rtol=1e-5, atol=1e-14)
+    np.testing.assert_allclose(host(P), new["w"], rtol=1e-6, atol=1e-7)
