@@ -46,7 +46,7 @@ SIGNATURES = {
     "ppo_grad_reduce_chunk_bytes": (I, []),
     "ppo_grad_reduce_chunk_elems": (I, []),
     "ppo_grad_reduce": (I, [P, P, P, I, P]),
-    "ppo_adam_clip_f32": (I, [P, P, P, P, P, P, I64, P, I, F, F, F, F, F, P, I]),
+    "ppo_adam_clip_f32": (I, [P, P, P, P, P, P, I64, P, I, D, D, D, D, D, P, I]),
     "ppo_count_advance": (I, [P, P, I]),
 }
 

@@ -75,7 +75,10 @@ struct AdamParams {
   const double* sumsq;
   int nsumsq;
   float max_norm;  // <= 0: no clipping
-  float lr, b1, b2, eps;
+  float neg_lr;    // fp32(-lr)
+  float b1, b2;    // fp32(b1), fp32(b2): the decay of the old moment and of the bias correction
+  float omb1, omb2;  // fp32(1 - b1), fp32(1 - b2) with the difference taken in double
+  float eps;
   const int* count_base;
   int step_offset;
 };
@@ -100,8 +103,8 @@ __global__ void __launch_bounds__(256) adam_kernel(AdamParams a) {
   const float norm = s_scale_norm[0];
   const bool clip = s_scale_norm[1] != 0.f;
   const float bc1 = s_bc[0], bc2 = s_bc[1];
-  const float omb1 = 1.f - a.b1, omb2 = 1.f - a.b2;
-  const float neg_lr = -a.lr;
+  const float omb1 = a.omb1, omb2 = a.omb2;
+  const float neg_lr = a.neg_lr;
   const int64_t n4 = a.n / 4;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
     floatx4 g = reinterpret_cast<const floatx4*>(a.g)[i];
@@ -151,9 +154,12 @@ PPO_EXPORT int ppo_grad_reduce(void* stream, const void* segs, const void* chunk
   return ppo::check_launch("ppo_grad_reduce");
 }
 
+// Hyper-parameters arrive as double, as optax receives Python floats: 1 - b is
+// formed in double and rounded once to fp32, like optax's (1 - decay) * g.
 PPO_EXPORT int ppo_adam_clip_f32(void* stream, float* params, const float* grads, float* mu, float* nu,
-                                 void* params_bf16, int64_t n, const double* sumsq, int nsumsq, float max_norm,
-                                 float lr, float b1, float b2, float eps, const int* count_base, int step_offset) {
+                                 void* params_bf16, int64_t n, const double* sumsq, int nsumsq, double max_norm,
+                                 double lr, double b1, double b2, double eps, const int* count_base,
+                                 int step_offset) {
   if (n < 0 || (n % 4) != 0 || !params || !grads || !mu || !nu || !count_base || (nsumsq > 0 && !sumsq) ||
       nsumsq < 0)
     return ppo::set_error(PPO_ERR_ARG, "ppo_adam_clip_f32: bad argument (n=%lld must be a multiple of 4)",
@@ -161,8 +167,8 @@ PPO_EXPORT int ppo_adam_clip_f32(void* stream, float* params, const float* grads
   if (((uintptr_t)params | (uintptr_t)grads | (uintptr_t)mu | (uintptr_t)nu) & 15u)
     return ppo::set_error(PPO_ERR_ARG, "ppo_adam_clip_f32: buffers must be 16-byte aligned");
   if (n == 0) return PPO_OK;
-  AdamParams a{params, grads, mu, nu, (__bf16*)params_bf16, n, sumsq, nsumsq, max_norm, lr, b1, b2, eps,
-               count_base, step_offset};
+  AdamParams a{params, grads, mu, nu, (__bf16*)params_bf16, n, sumsq, nsumsq, (float)max_norm, (float)(-lr),
+               (float)b1, (float)b2, (float)(1.0 - b1), (float)(1.0 - b2), (float)eps, count_base, step_offset};
   const int blocks = (int)std::min<int64_t>(ppo::ceil_div64(n / 4, 256), 2048);
   hipLaunchKernelGGL(adam_kernel, dim3(blocks), dim3(256), 0, ppo::as_stream(stream), a);
   return ppo::check_launch("ppo_adam_clip_f32");

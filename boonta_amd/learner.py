@@ -375,7 +375,7 @@ class MLPExecutor:
             if i > 0:
                 dst, epi, act, aux, ldaux = self._dx_target(layers[i - 1])
                 self._call("ppo_gemm_f32", st, A_ROW, B_NK, _p(lb.dZ), s.ld, None, self.flat.view(d.w), d.w.ld,
-                          dst, layers[i - 1].spec.ld, self.mb, d.fin, s.ld, 1, 0, epi, None, act, aux, ldaux,
+                          dst, layers[i - 1].spec.ld, self.mb, d.fin, s.ld, 1, 0, epi, None, act, None, aux, ldaux,
                           None, -1)
 
     def _head_back(self, st, layers, dhead, head: DenseSpec, wpart, bpart, splits, hx, ldhx, hidx):
@@ -386,8 +386,8 @@ class MLPExecutor:
         if layers:
             dst, epi, act, aux, ldaux = self._dx_target(layers[-1])
             self._call("ppo_gemm_f32", st, A_ROW, B_NK, _p(dhead), head.w.ld, None, self.flat.view(head.w),
-                      head.w.ld, dst, layers[-1].spec.ld, self.mb, head.fin, head.w.ld, 1, 0, epi, None, act, aux,
-                      ldaux, None, -1)
+                      head.w.ld, dst, layers[-1].spec.ld, self.mb, head.fin, head.w.ld, 1, 0, epi, None, act, None,
+                      aux, ldaux, None, -1)
 
     # ----------------------------------------------------------- the update
     def bind(self, inputs: dict):

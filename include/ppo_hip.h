@@ -137,8 +137,8 @@ int ppo_grad_reduce_chunk_bytes(void);
 int ppo_grad_reduce_chunk_elems(void);
 int ppo_grad_reduce(void* stream, const void* segs, const void* chunks, int nchunks, double* sumsq);
 int ppo_adam_clip_f32(void* stream, float* params, const float* grads, float* mu, float* nu, void* params_bf16,
-                      int64_t n, const double* sumsq, int nsumsq, float max_norm, float lr, float b1, float b2,
-                      float eps, const int* count_base, int step_offset);
+                      int64_t n, const double* sumsq, int nsumsq, double max_norm, double lr, double b1,
+                      double b2, double eps, const int* count_base, int step_offset);
 int ppo_count_advance(void* stream, int* count_base, int steps);
 
 #ifdef __cplusplus

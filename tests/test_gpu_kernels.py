@@ -339,11 +339,13 @@ def test_grad_reduce_and_adam_match_optax_restatement(max_norm, scale):
     _lib.call("ppo_adam_clip_f32", st(), P.data_ptr(), Gt.data_ptr(), MU.data_ptr(), NU.data_ptr(), None, n,
               SQ.data_ptr(), nch, max_norm, 3e-4, 0.9, 0.999, 1e-8, count.data_ptr(), 2)
     grad = parts.astype(np.float64).sum(0)
-    np.testing.assert_allclose(host(Gt), grad, rtol=1e-5, atol=1e-9)
+    # absolute floors: fp32 rounding of the operands (|parts| <= ~0.05, |b1 mu| ~ 1e-3,
+    # |b2 nu| ~ 1e-5), which exceed the result where terms cancel
+    np.testing.assert_allclose(host(Gt), grad, rtol=1e-5, atol=1e-8 * max(scale, 1e-3))
     opt = {"lr": 3e-4, "max_grad_norm": max_norm if max_norm > 0 else None}
     state = {"count": 8, "mu": {"w": mu0.astype(np.float64)}, "nu": {"w": nu0.astype(np.float64)}}
     new, st2, gn = ppo.optimizer_update({"w": grad}, state, {"w": p0.astype(np.float64)}, opt)
     np.testing.assert_allclose(np.sqrt(host(SQ).sum()), gn, rtol=1e-6)
-    np.testing.assert_allclose(host(MU), st2["mu"]["w"], rtol=1e-5, atol=1e-10)
-    np.testing.assert_allclose(host(NU), st2["nu"]["w"], rtol=1e-5, atol=1e-14)
+    np.testing.assert_allclose(host(MU), st2["mu"]["w"], rtol=1e-5, atol=1e-9)
+    np.testing.assert_allclose(host(NU), st2["nu"]["w"], rtol=1e-5, atol=1e-12)
     np.testing.assert_allclose(host(P), new["w"], rtol=1e-6, atol=1e-7)

@@ -1,0 +1,98 @@
+"""Host logic of the learner without a GPU: each workload's flat layout and its
+full launch sequence, recorded instead of launched and checked against the C
+signatures (arity, required pointers, buffer extents)."""
+import numpy as np
+import pytest
+import torch
+
+from boonta_amd import _lib, recipes
+from boonta_amd.flat import load_tree, tree_from_flat, tree_to_numpy
+from boonta_amd.learner import FlatState, MLPExecutor, Program
+from oracle import ppo as oppo
+
+MLP_CONFIGS = [1, 2, 3]
+
+
+def small(config):
+    r = recipes.make(config)
+    if config == 2:
+        return r.resized(T=16, N=64, num_minibatches=4, update_epochs=2)
+    if config == 3:
+        return r.resized(T=8, N=64, num_minibatches=4, update_epochs=2)
+    return r
+
+
+def fake_inputs(ex):
+    return {k: 4096 * (i + 1) for i, k in enumerate(
+        ["obs", "next_obs_last", "action", "reward", "terminated", "truncated", "log_prob", "value"])}
+
+
+@pytest.mark.parametrize("config", MLP_CONFIGS)
+def test_recorded_launches_match_the_c_signatures(config):
+    r = small(config)
+    prog = Program(r.network.plan(r.obs_dim))
+    flat = FlatState(prog, torch.device("cpu"))
+    ex = MLPExecutor(prog, flat, r.cfg, r.optimizer, r.T, r.N)
+    ex.bind(fake_inputs(ex))
+    calls = ex.record()
+    names = [n for n, _ in calls]
+    steps = r.cfg.update_epochs * r.cfg.num_minibatches
+    assert names.count("ppo_adam_clip_f32") == steps
+    assert names.count("ppo_loss_f32") == steps
+    assert names[-1] == "ppo_count_advance"
+    for name, args in calls:
+        _, argtypes = _lib.SIGNATURES[name]
+        assert len(args) == len(argtypes), (name, len(args), len(argtypes))
+        if name == "ppo_gemm_f32":
+            (_, a_layout, b_layout, A, lda, rows, B, ldb, C, ldc, M, N, K, splits, stride, epi, bias, act, pre,
+             aux, ldaux, bias_grad, tile) = args
+            assert A and B and C and M > 0 and N > 0 and K > 0
+            assert ldc >= N
+            assert lda >= (K if a_layout == 0 else M)
+            assert ldb >= (N if b_layout == 0 else K)
+            if epi == 2:
+                assert aux and ldaux >= N
+            if splits > 1:
+                assert stride >= M * ldc
+
+
+@pytest.mark.parametrize("config", MLP_CONFIGS)
+def test_flat_layout_round_trips_the_parameter_tree(config):
+    r = recipes.make(config)
+    prog = Program(r.network.plan(r.obs_dim))
+    flat = FlatState(prog, torch.device("cpu"))
+    params = r.network.init(3, r.obs_dim)["params"]
+    load_tree(prog.layout, flat.P, params)
+    back = tree_to_numpy(tree_from_flat(prog.layout, flat.P))
+    a, b = dict(oppo.tree_leaves(params)), dict(oppo.tree_leaves(back))
+    assert set(a) == set(b)
+    for k in a:
+        np.testing.assert_array_equal(np.asarray(a[k], np.float32), b[k])
+    # every element outside the leaves is padding and stays zero
+    used = np.zeros(prog.layout.size, bool)
+    for lf in prog.layout.leaves.values():
+        idx = lf.offset + sum(np.indices(lf.shape)[d] * lf.strides[d] for d in range(len(lf.shape)))
+        assert not used[idx].any(), "leaves overlap"
+        used[idx] = True
+    assert np.all(flat.P.numpy()[~used] == 0)
+    assert prog.layout.size % 64 == 0
+
+
+def test_shared_heads_pack_logits_and_value_in_one_matrix():
+    r = recipes.make(2)
+    prog = Program(r.network.plan(r.obs_dim))
+    assert prog.shared_head
+    assert prog.head_a.w is prog.head_c.w
+    assert prog.head_a.w.ld == 8            # 6 logits + 1 value, padded to 4
+    lf_a = prog.layout.leaves[("head", "actor", "kernel")]
+    lf_c = prog.layout.leaves[("head", "critic", "kernel")]
+    assert lf_c.offset == lf_a.offset + 6 and lf_a.strides == (8, 1)
+
+
+def test_unsupported_compositions_raise():
+    from boonta_amd import networks as nn
+    bad = nn.Network(feature_extractor=nn.FeatureExtractor(nn.Sequential([nn.Dense(8), nn.relu])),
+                     head=nn.ActorCritic(actor=nn.Categorical(nn.Sequential([nn.Dense(8), nn.relu, nn.Dense(2)])),
+                                         critic=nn.Dense(1)))
+    with pytest.raises(NotImplementedError):
+        Program(bad.plan(4))
