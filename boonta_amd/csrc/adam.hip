@@ -39,29 +39,46 @@ struct Chunk {
 };
 
 constexpr int REDUCE_THREADS = 256;
-constexpr int CHUNK = 2048;  // elements per block
+constexpr int CHUNK = 256;  // elements per block: one float4 per lane of a wave
 
+// One block per chunk of 256 gradient elements.  Each of the 4 waves sums a
+// contiguous quarter of the partials for the same 64 float4 (two interleaved
+// accumulators to keep loads in flight), then the quarters are added in wave
+// order: a fixed association, so the result never depends on scheduling.
 __global__ void __launch_bounds__(REDUCE_THREADS)
 grad_reduce_kernel(const Segment* __restrict__ segs, const Chunk* __restrict__ chunks, double* __restrict__ sumsq) {
-  __shared__ double red[REDUCE_THREADS / 64];
+  __shared__ floatx4 part[REDUCE_THREADS / 64][64];
   const Chunk ch = chunks[blockIdx.x];
   const Segment sg = segs[ch.seg];
-  const int64_t end = min(sg.count, ch.start + (int64_t)CHUNK);
-  double sq = 0.0;
-  for (int64_t i = ch.start + threadIdx.x; i < end; i += REDUCE_THREADS) {
-    float acc = 0.f;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t i = ch.start + 4 * lane;  // first element of this lane's float4
+  const bool live = i < sg.count;
+  const int q0 = (sg.nparts * wave) / 4, q1 = (sg.nparts * (wave + 1)) / 4;
+  floatx4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+  if (live) {
     const float* s = sg.src + i;
-    for (int q = 0; q < sg.nparts; ++q) acc += s[(int64_t)q * sg.part_stride];
-    sg.dst[i] = acc;
-    sq += (double)acc * (double)acc;
+    int q = q0;
+    for (; q + 1 < q1; q += 2) {
+      a0 += *reinterpret_cast<const floatx4*>(s + (int64_t)q * sg.part_stride);
+      a1 += *reinterpret_cast<const floatx4*>(s + (int64_t)(q + 1) * sg.part_stride);
+    }
+    if (q < q1) a0 += *reinterpret_cast<const floatx4*>(s + (int64_t)q * sg.part_stride);
   }
-  sq = ppo::wave_sum_d(sq);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sq;
+  part[wave][lane] = a0 + a1;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    double t = 0.0;
-    for (int w = 0; w < REDUCE_THREADS / 64; ++w) t += red[w];
-    sumsq[blockIdx.x] = t;
+  if (wave == 0) {
+    double sq = 0.0;
+    if (live) {
+      floatx4 t = part[0][lane];
+#pragma unroll
+      for (int w = 1; w < REDUCE_THREADS / 64; ++w) t += part[w][lane];
+      *reinterpret_cast<floatx4*>(sg.dst + i) = t;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sq += (double)t[e] * (double)t[e];
+    }
+    sq = ppo::wave_sum_d(sq);
+    if (lane == 0) sumsq[blockIdx.x] = sq;
   }
 }
 
@@ -146,6 +163,8 @@ PPO_EXPORT int ppo_grad_reduce_chunk_elems(void) { return CHUNK; }
 
 // segs/chunks: device tables (layout: ppo_grad_reduce_{segment,chunk}_bytes),
 // one block per chunk; sumsq receives nchunks doubles.
+// Every segment's count, part stride and pointers must be multiples of 4
+// floats (16 bytes): the learner's flat layout guarantees it.
 PPO_EXPORT int ppo_grad_reduce(void* stream, const void* segs, const void* chunks, int nchunks, double* sumsq) {
   if (nchunks < 0 || !segs || !chunks || !sumsq) return ppo::set_error(PPO_ERR_ARG, "ppo_grad_reduce: bad argument");
   if (nchunks == 0) return PPO_OK;

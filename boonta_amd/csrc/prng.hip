@@ -107,28 +107,34 @@ radix_hist_kernel(const uint32_t* __restrict__ keys, int64_t n, int shift, uint3
   for (int d = threadIdx.x; d < RADIX; d += SORT_THREADS) hist[(int64_t)d * tiles + blockIdx.x] = cnt[d];
 }
 
-// Exclusive scan of hist[RADIX * tiles] (digit-major) in one workgroup.
-__global__ void __launch_bounds__(1024) radix_scan_kernel(uint32_t* __restrict__ hist, int64_t total) {
-  __shared__ uint32_t part[1024];
-  const int tid = threadIdx.x;
-  const int64_t per = (total + 1023) / 1024;
-  const int64_t lo = tid * per;
-  const int64_t hi = lo + per < total ? lo + per : total;
-  uint32_t s = 0;
-  for (int64_t i = lo; i < hi; ++i) s += hist[i];
-  part[tid] = s;
+// Exclusive scan of hist[RADIX * tiles] (digit-major) in one workgroup:
+// thread d totals digit d over the tiles, one LDS scan turns the 256 totals
+// into digit bases, and each thread then rewrites its row as running offsets.
+__global__ void __launch_bounds__(RADIX) radix_scan_kernel(uint32_t* __restrict__ hist, int tiles) {
+  __shared__ uint32_t base[RADIX];
+  const int d = threadIdx.x;
+  uint32_t* row = hist + (int64_t)d * tiles;
+  uint32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+  int t = 0;
+  for (; t + 3 < tiles; t += 4) {
+    s0 += row[t];
+    s1 += row[t + 1];
+    s2 += row[t + 2];
+    s3 += row[t + 3];
+  }
+  for (; t < tiles; ++t) s0 += row[t];
+  base[d] = (s0 + s1) + (s2 + s3);
   __syncthreads();
-  // Hillis-Steele inclusive scan over the 1024 partial sums
-  for (int off = 1; off < 1024; off <<= 1) {
-    uint32_t v = tid >= off ? part[tid - off] : 0u;
+  for (int off = 1; off < RADIX; off <<= 1) {
+    const uint32_t v = d >= off ? base[d - off] : 0u;
     __syncthreads();
-    part[tid] += v;
+    base[d] += v;
     __syncthreads();
   }
-  uint32_t run = tid ? part[tid - 1] : 0u;
-  for (int64_t i = lo; i < hi; ++i) {
-    uint32_t v = hist[i];
-    hist[i] = run;
+  uint32_t run = d ? base[d - 1] : 0u;
+  for (t = 0; t < tiles; ++t) {
+    const uint32_t v = row[t];
+    row[t] = run;
     run += v;
   }
 }
@@ -249,7 +255,7 @@ int permutation_impl(hipStream_t st, const uint32_t* key, int32_t* out, int64_t 
       const int shift = pass * RADIX_BITS;
       hipLaunchKernelGGL(radix_hist_kernel, dim3(tiles), dim3(SORT_THREADS), 0, st, kin, n, shift,
                          s.hist, tiles);
-      hipLaunchKernelGGL(radix_scan_kernel, dim3(1), dim3(1024), 0, st, s.hist, (int64_t)RADIX * tiles);
+      hipLaunchKernelGGL(radix_scan_kernel, dim3(1), dim3(RADIX), 0, st, s.hist, tiles);
       hipLaunchKernelGGL(radix_scatter_kernel, dim3(tiles), dim3(SORT_THREADS), 0, st, kin, vin, kout,
                          vout, n, shift, s.hist, tiles);
       std::swap(kin, kout);

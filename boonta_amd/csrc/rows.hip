@@ -367,13 +367,18 @@ __global__ void __launch_bounds__(ROW_THREADS) ppo_loss_kernel(LossParams p) {
 // step (ppo.py:170-179 order): actor/loss, actor/entropy, actor/approximate_kl,
 // actor/clip_fraction, actor/advantage, critic/loss, critic/explained_variance,
 // critic/value; then the total loss in slot 8.
-__global__ void loss_finalize_kernel(const double* __restrict__ partial, int nblocks, int rows, float ent_coef,
-                                     float vf_coef, float* __restrict__ out) {
+__global__ void __launch_bounds__(256)
+loss_finalize_kernel(const double* __restrict__ partial, int nblocks, int rows, float ent_coef, float vf_coef,
+                     float* __restrict__ out) {
   __shared__ double s[NSTAT];
-  if (threadIdx.x < NSTAT) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  // wave w folds statistics w, w + 4, w + 8 over the block partials
+  for (int k = wave; k < NSTAT; k += 4) {
     double t = 0.0;
-    for (int b = 0; b < nblocks; ++b) t += partial[(int64_t)b * NSTAT + threadIdx.x];
-    s[threadIdx.x] = t;
+    for (int b = lane; b < nblocks; b += 64) t += partial[(int64_t)b * NSTAT + k];
+    t = ppo::wave_sum_d(t);
+    if (lane == 0) s[k] = t;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -508,7 +513,7 @@ PPO_EXPORT int ppo_loss_finalize(void* stream, const double* stats_partial, int 
                                  float vf_coef, float* out9) {
   if (nblocks <= 0 || rows <= 0 || !stats_partial || !out9)
     return ppo::set_error(PPO_ERR_ARG, "ppo_loss_finalize: bad argument");
-  hipLaunchKernelGGL(loss_finalize_kernel, dim3(1), dim3(64), 0, ppo::as_stream(stream), stats_partial, nblocks,
+  hipLaunchKernelGGL(loss_finalize_kernel, dim3(1), dim3(256), 0, ppo::as_stream(stream), stats_partial, nblocks,
                      rows, ent_coef, vf_coef, out9);
   return ppo::check_launch("ppo_loss_finalize");
 }

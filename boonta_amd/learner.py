@@ -249,7 +249,24 @@ class MLPExecutor:
         self.boot_layers = [layer_bufs(s, N, False) for s in
                             (program.trunk if program.shared_head else program.critic_layers)]
         ha, hc = program.head_a, program.head_c
-        if program.shared_head:
+        lib = _lib.load()
+        self.fused = self._can_fuse(program)
+        if self.fused:
+            hb = lib.ppo_head_loss_blocks(mb)
+            self.head_blocks = hb
+        if self.fused and program.shared_head:
+            self.HWPART = torch.zeros(hb, ha.fin, ha.w.ld, **f32)
+            self.HBPART = torch.zeros(hb, ha.w.ld, **f32)
+            self.head_splits = hb
+            self.HEADB = torch.zeros(N, ha.w.ld, **f32)
+        elif self.fused:
+            self.HAWPART = torch.zeros(hb, ha.fin, ha.w.ld, **f32)
+            self.HABPART = torch.zeros(hb, ha.w.ld, **f32)
+            self.HCWPART = torch.zeros(hb, hc.fin, hc.w.ld, **f32)
+            self.HCBPART = torch.zeros(hb, hc.w.ld, **f32)
+            self.ha_splits = self.hc_splits = hb
+            self.HEADB = torch.zeros(N, hc.w.ld, **f32)
+        elif program.shared_head:
             self.HEAD = torch.zeros(mb, ha.w.ld, **f32)
             self.DHEAD = torch.zeros(mb, ha.w.ld, **f32)
             self.head_splits = _splits(mb, ha.fin, ha.w.ld)
@@ -268,8 +285,7 @@ class MLPExecutor:
             self.HCWPART = torch.zeros(self.hc_splits, hc.fin, hc.w.ld, **f32)
             self.HCBPART = torch.zeros(self.hc_splits, hc.w.ld, **f32)
             self.HEADB = torch.zeros(N, hc.w.ld, **f32)
-        lib = _lib.load()
-        self.loss_blocks = lib.ppo_loss_blocks(mb)
+        self.loss_blocks = self.head_blocks if self.fused else lib.ppo_loss_blocks(mb)
         self.nstat = lib.ppo_loss_stat_count()
         self.STATS = torch.zeros(self.loss_blocks, self.nstat, dtype=torch.float64, device=dev)
         self.DSCALE = (torch.zeros(self.loss_blocks, program.dist["dim"], **f32)
@@ -283,6 +299,23 @@ class MLPExecutor:
         self.PERM_WS = torch.zeros(ws, dtype=torch.uint8, device=dev)
         self.KEY = torch.zeros(2, dtype=torch.int32, device=dev)
         self._build_reduce_tables()
+
+    @staticmethod
+    def _can_fuse(program: Program) -> bool:
+        """The fused head + loss kernel applies when the heads read torso
+        features (not the raw observation) of one width <= 512 and the actor
+        head has at most 16 outputs (plus the value column when shared)."""
+        lib = _lib.load()
+        ha, hc = program.head_a, program.head_c
+        if program.shared_head:
+            if not program.trunk:
+                return False
+            na = program.head_out + 1
+        else:
+            if not program.actor_layers or not program.critic_layers or ha.fin != hc.fin:
+                return False
+            na = program.head_out
+        return na <= lib.ppo_head_loss_max_outputs() and ha.fin <= lib.ppo_head_loss_max_features()
 
     # ------------------------------------------------------ gradient tables
     def _build_reduce_tables(self):
@@ -444,12 +477,56 @@ class MLPExecutor:
                           step)
         self._call("ppo_count_advance", st, _p(self.flat.count), self.E * self.M)
 
+    def _fused_head_loss(self, st, idx, step, dist, A, scale_ptr, act_i, act_f):
+        prog, cfg, inp, mb = self.prog, self.cfg, self.inp, self.mb
+        if prog.shared_head:
+            la, lc = self.trunk[-1], None
+            h = prog.head_a
+            na = prog.head_out + 1
+            wpa, bpa, wpc, bpc = self.HWPART, self.HBPART, None, None
+        else:
+            la, lc = self.actor[-1], self.critic[-1]
+            h = prog.head_a
+            na = prog.head_out
+            wpa, bpa, wpc, bpc = self.HAWPART, self.HABPART, self.HCWPART, self.HCBPART
+        da, epa, acta, auxa, ldauxa = self._dx_target(la)
+        acta = acta if epa == EPI_DACT else 0
+        if lc is not None:
+            hc = prog.head_c
+            dc, epc, actc, auxc, ldauxc = self._dx_target(lc)
+            actc = actc if epc == EPI_DACT else 0
+            c_args = (_p(lc.Y), lc.spec.ld, self.flat.view(hc.w), hc.w.ld, self.flat.view(hc.b))
+            cd_args = (actc, auxc, ldauxc, dc, lc.spec.ld)
+        else:
+            c_args = (None, 0, None, 0, None)
+            cd_args = (0, None, 0, None, 0)
+        self._call("ppo_head_loss_f32", st, dist, mb, idx, _p(la.Y), la.spec.ld, self.flat.view(h.w), h.w.ld,
+                   self.flat.view(h.b), na, *c_args, h.fin, A, scale_ptr, act_i, act_f, inp["log_prob"],
+                   inp["value"], _p(self.ADV), _p(self.RET), acta, auxa, ldauxa, da, la.spec.ld, *cd_args,
+                   _p(wpa), _p(bpa), _p(wpc), _p(bpc), _p(self.DSCALE), _p(self.STATS),
+                   float(cfg.clip_coefficient), int(cfg.clip_value_loss), float(cfg.entropy_coefficient),
+                   float(cfg.value_coefficient), 1.0)
+        self._call("ppo_loss_finalize", st, _p(self.STATS), self.loss_blocks, mb, float(cfg.entropy_coefficient),
+                   float(cfg.value_coefficient), _p(self.LOGS) + 4 * 9 * step)
+
     def _minibatch(self, st, idx, step, obs, ldo, dist, A):
         prog, cfg, inp, mb = self.prog, self.cfg, self.inp, self.mb
         clip = float(cfg.clip_coefficient)
         scale_ptr = self.flat.view(prog.scale_region) if prog.scale_region is not None else None
         act_i = inp["action"] if dist == 0 else None
         act_f = inp["action"] if dist == 1 else None
+        if self.fused:
+            if prog.shared_head:
+                self._fwd_layers(st, self.trunk, obs, ldo, idx, mb)
+                self._fused_head_loss(st, idx, step, dist, A, scale_ptr, act_i, act_f)
+                self._bwd_layers(st, self.trunk, obs, ldo, idx)
+            else:
+                self._fwd_layers(st, self.actor, obs, ldo, idx, mb)
+                self._fwd_layers(st, self.critic, obs, ldo, idx, mb)
+                self._fused_head_loss(st, idx, step, dist, A, scale_ptr, act_i, act_f)
+                self._bwd_layers(st, self.actor, obs, ldo, idx)
+                self._bwd_layers(st, self.critic, obs, ldo, idx)
+            return
         if prog.shared_head:
             hx, ldhx, hidx = self._fwd_layers(st, self.trunk, obs, ldo, idx, mb)
             h = prog.head_a

@@ -124,6 +124,27 @@ int ppo_loss_f32(void* stream, int dist, int rows, const int32_t* idx, const flo
 int ppo_loss_finalize(void* stream, const double* stats_partial, int nblocks, int rows, float ent_coef,
                       float vf_coef, float* out9);
 
+/* Fused heads + loss + head backward: one wavefront per sample row reads the
+ * torso output once.  Group a is the actor head, or both heads packed into one
+ * [F, ldwa] matrix with the value in column na - 1 when hc is NULL; group c is
+ * the critic head of separate towers.  Writes the cotangent of each head input
+ * (times act'(aux) when act != NONE), per-block head weight / bias gradient
+ * partials [blocks][F][ld] / [blocks][ld] (blocks = ppo_head_loss_blocks(rows)),
+ * statistics and Gaussian scale partials as ppo_loss_f32 does.  F <= 512,
+ * na <= 16. */
+int ppo_head_loss_blocks(int rows);
+int ppo_head_loss_max_outputs(void);
+int ppo_head_loss_max_features(void);
+int ppo_head_loss_f32(void* stream, int dist, int rows, const int32_t* idx, const float* ha, int64_t ldha,
+                      const float* wa, int64_t ldwa, const float* ba, int na, const float* hc, int64_t ldhc,
+                      const float* wc, int64_t ldwc, const float* bc, int F, int A, const float* scale_param,
+                      const int32_t* action_i, const float* action_f, const float* old_logp,
+                      const float* old_value, const float* adv, const float* ret, int act_a, const float* aux_a,
+                      int64_t ldaux_a, float* dha, int64_t lddha, int act_c, const float* aux_c,
+                      int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a,
+                      float* wpart_c, float* bpart_c, float* dscale_partial, double* stats_partial,
+                      float clip_eps, int clip_value_loss, float ent_coef, float vf_coef, float temperature);
+
 /* ------------------------------------------------------------- optimizer
  * Replaces optax.chain(optax.clip_by_global_norm(max_norm), optax.adam(lr))
  * .update + optax.apply_updates at boonta/algorithms/ppo.py:182-191 (chain

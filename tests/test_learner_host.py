@@ -38,7 +38,9 @@ def test_recorded_launches_match_the_c_signatures(config):
     names = [n for n, _ in calls]
     steps = r.cfg.update_epochs * r.cfg.num_minibatches
     assert names.count("ppo_adam_clip_f32") == steps
-    assert names.count("ppo_loss_f32") == steps
+    assert names.count("ppo_loss_finalize") == steps
+    # every workload here has torso features in front of its heads: the fused kernel runs
+    assert names.count("ppo_head_loss_f32") == steps and "ppo_loss_f32" not in names
     assert names[-1] == "ppo_count_advance"
     for name, args in calls:
         _, argtypes = _lib.SIGNATURES[name]
@@ -54,6 +56,9 @@ def test_recorded_launches_match_the_c_signatures(config):
                 assert aux and ldaux >= N
             if splits > 1:
                 assert stride >= M * ldc
+        if name == "ppo_head_loss_f32":
+            ha, wa, ba, dha, wpa, bpa, stats = args[4], args[6], args[8], args[27], args[34], args[35], args[39]
+            assert all((ha, wa, ba, dha, wpa, bpa, stats))
 
 
 @pytest.mark.parametrize("config", MLP_CONFIGS)
