@@ -9,11 +9,18 @@
 //   permutation(key, n): x = arange(n); repeat ceil(3 ln n / ln(2^32-1)) times:
 //       key, sub = split(key); x = stable_sort_by_key(bits32(sub)[0:n], x)
 //
-// The stable sort is an LSD radix sort over four 8-bit digits.  Each pass has
-// three kernels: per-tile digit counts, one exclusive scan over the
-// (digit, tile) table, and a scatter that ranks equal digits in input order
-// with wavefront ballots (8 ballots give each lane the mask of lanes holding
-// its digit), so the result is bit-identical to any stable sort.
+// A stable sort by 32-bit keys is the same as a sort by the unique 64-bit
+// pair (key, position).  Each shuffle round therefore runs as an MSD bucket
+// sort, for all epochs at once (grid.y = epoch):
+//   1. bits: the round's sort keys, and per 4096-element tile a histogram of
+//      the top b key bits (b sized for ~512 elements per bucket);
+//   2. scan: bucket bases and per-(bucket, tile) offsets;
+//   3. scatter: every element, with its position, into its bucket (order
+//      inside a bucket does not matter);
+//   4. sort: one workgroup per bucket sorts (key, position) pairs in LDS with a
+//      bitonic network and writes the values in order.
+// A bucket larger than the LDS capacity (not reachable for Threefry keys at
+// these sizes, but handled) is ranked by counting instead, which is exact.
 #include "common.h"
 
 #include <algorithm>
@@ -22,12 +29,11 @@
 
 namespace {
 
-constexpr int RADIX_BITS = 8;
-constexpr int RADIX = 1 << RADIX_BITS;
-constexpr int SORT_THREADS = 256;
-constexpr int SORT_ITEMS = 16;  // items per thread
-constexpr int SORT_TILE = SORT_THREADS * SORT_ITEMS;
-constexpr int SORT_WAVES = SORT_THREADS / 64;
+constexpr int TILE = 4096;          // elements per histogram / scatter block
+constexpr int TILE_THREADS = 256;
+constexpr int BUCKET_CAP = 4096;    // elements a bucket sorts in LDS
+constexpr int SORT_THREADS = 512;
+constexpr int MAX_BUCKET_BITS = 12;
 
 __device__ __forceinline__ uint32_t rotl(uint32_t v, uint32_t r) {
   return (v << r) | (v >> (32u - r));
@@ -63,137 +69,187 @@ __global__ void split_kernel(const uint32_t* __restrict__ key, uint32_t* __restr
   out[2 * i + 1] = x1;
 }
 
-// One shuffle round's sort keys: bits32(subkey) with subkey = split(key, 2)[1],
-// plus the iota values on the first round.
-__global__ void round_bits_kernel(const uint32_t* __restrict__ key_in,
-                                  uint32_t* __restrict__ sort_keys, int32_t* __restrict__ vals,
-                                  int64_t n, int first_round) {
-  const uint32_t k0 = key_in[0], k1 = key_in[1];
-  uint32_t s0 = 0, s1 = 1;  // split(key, 2)[1] = threefry(key, (0, 1))
+// The subkey of shuffle round `round` of epoch e: the epoch key is
+// split(key, E)[e] (or key itself when `split_epochs` is 0); each round takes
+// (key, sub) = split(key).
+__device__ __forceinline__ void round_subkey(const uint32_t* key, int split_epochs, int e, int round, uint32_t& s0,
+                                             uint32_t& s1) {
+  uint32_t k0 = key[0], k1 = key[1];
+  if (split_epochs) {
+    uint32_t x0 = 0, x1 = (uint32_t)e;
+    threefry2x32(k0, k1, x0, x1);
+    k0 = x0;
+    k1 = x1;
+  }
+  for (int r = 0; r < round; ++r) {
+    uint32_t x0 = 0, x1 = 0;
+    threefry2x32(k0, k1, x0, x1);
+    k0 = x0;
+    k1 = x1;
+  }
+  s0 = 0;
+  s1 = 1;
   threefry2x32(k0, k1, s0, s1);
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+}
+
+struct ShuffleArgs {
+  const uint32_t* key;  // device key data [2]
+  int split_epochs;
+  int64_t n;
+  int tiles;
+  int bbits;            // bucket bits (0: one bucket)
+  int nb;               // 1 << bbits
+  int round;
+  int32_t* out;         // [E][n]: values in, values out
+  uint32_t* keys;       // [E][n]
+  uint32_t* hist;       // [E][nb][tiles]
+  uint32_t* bstart;     // [E][nb + 1]
+  uint32_t* tkey;       // [E][n] bucketed keys
+  uint32_t* tpos;       // [E][n] bucketed positions
+  int32_t* tval;        // [E][n] bucketed values
+};
+
+__device__ __forceinline__ uint32_t bucket_of(uint32_t k, int bbits) {
+  return bbits ? (k >> (32 - bbits)) : 0u;
+}
+
+__global__ void __launch_bounds__(TILE_THREADS) shuffle_bits_kernel(ShuffleArgs a) {
+  extern __shared__ uint32_t cnt[];  // [nb]
+  const int e = blockIdx.y;
+  for (int d = threadIdx.x; d < a.nb; d += TILE_THREADS) cnt[d] = 0;
+  __syncthreads();
+  uint32_t s0, s1;
+  round_subkey(a.key, a.split_epochs, e, a.round, s0, s1);
+  const int64_t base = (int64_t)blockIdx.x * TILE;
+  uint32_t* keys = a.keys + (int64_t)e * a.n;
+  int32_t* vals = a.out + (int64_t)e * a.n;
+  for (int it = 0; it < TILE / TILE_THREADS; ++it) {
+    const int64_t i = base + (int64_t)it * TILE_THREADS + threadIdx.x;
+    if (i >= a.n) break;
     uint32_t x0 = (uint32_t)((uint64_t)i >> 32), x1 = (uint32_t)((uint64_t)i & 0xffffffffu);
     threefry2x32(s0, s1, x0, x1);
-    sort_keys[i] = x0 ^ x1;
-    if (first_round) vals[i] = (int32_t)i;
-  }
-}
-
-// Writes split(key, 2)[0] into key_out; launched after round_bits_kernel so an
-// in-place update cannot race with its readers.
-__global__ void advance_key_kernel(const uint32_t* key_in, uint32_t* key_out) {
-  if (threadIdx.x == 0 && blockIdx.x == 0) {
-    uint32_t x0 = 0, x1 = 0;
-    threefry2x32(key_in[0], key_in[1], x0, x1);
-    key_out[0] = x0;
-    key_out[1] = x1;
-  }
-}
-
-__global__ void __launch_bounds__(SORT_THREADS)
-radix_hist_kernel(const uint32_t* __restrict__ keys, int64_t n, int shift, uint32_t* __restrict__ hist,
-                  int tiles) {
-  __shared__ uint32_t cnt[RADIX];
-  for (int d = threadIdx.x; d < RADIX; d += SORT_THREADS) cnt[d] = 0;
-  __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * SORT_TILE;
-#pragma unroll
-  for (int it = 0; it < SORT_ITEMS; ++it) {
-    const int64_t i = base + (int64_t)it * SORT_THREADS + threadIdx.x;
-    if (i < n) atomicAdd(&cnt[(keys[i] >> shift) & (RADIX - 1)], 1u);
+    const uint32_t k = x0 ^ x1;
+    keys[i] = k;
+    if (a.round == 0) vals[i] = (int32_t)i;
+    atomicAdd(&cnt[bucket_of(k, a.bbits)], 1u);
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < RADIX; d += SORT_THREADS) hist[(int64_t)d * tiles + blockIdx.x] = cnt[d];
+  uint32_t* hist = a.hist + (int64_t)e * a.nb * a.tiles;
+  for (int d = threadIdx.x; d < a.nb; d += TILE_THREADS) hist[(int64_t)d * a.tiles + blockIdx.x] = cnt[d];
 }
 
-// Exclusive scan of hist[RADIX * tiles] (digit-major) in one workgroup:
-// thread d totals digit d over the tiles, one LDS scan turns the 256 totals
-// into digit bases, and each thread then rewrites its row as running offsets.
-__global__ void __launch_bounds__(RADIX) radix_scan_kernel(uint32_t* __restrict__ hist, int tiles) {
-  __shared__ uint32_t base[RADIX];
-  const int d = threadIdx.x;
-  uint32_t* row = hist + (int64_t)d * tiles;
-  uint32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0;
-  int t = 0;
-  for (; t + 3 < tiles; t += 4) {
-    s0 += row[t];
-    s1 += row[t + 1];
-    s2 += row[t + 2];
-    s3 += row[t + 3];
-  }
-  for (; t < tiles; ++t) s0 += row[t];
-  base[d] = (s0 + s1) + (s2 + s3);
-  __syncthreads();
-  for (int off = 1; off < RADIX; off <<= 1) {
-    const uint32_t v = d >= off ? base[d - off] : 0u;
-    __syncthreads();
-    base[d] += v;
-    __syncthreads();
-  }
-  uint32_t run = d ? base[d - 1] : 0u;
-  for (t = 0; t < tiles; ++t) {
-    const uint32_t v = row[t];
-    row[t] = run;
-    run += v;
-  }
-}
-
-// Stable scatter of one 8-bit digit.  Wave w of a tile owns the contiguous
-// items [w * 64 * SORT_ITEMS, (w+1) * 64 * SORT_ITEMS) and walks them in order
-// 64 at a time, so counting equal digits in lane order inside each step and
-// accumulating across steps and waves gives the stable rank.
-__global__ void __launch_bounds__(SORT_THREADS)
-radix_scatter_kernel(const uint32_t* __restrict__ keys_in, const int32_t* __restrict__ vals_in,
-                     uint32_t* __restrict__ keys_out, int32_t* __restrict__ vals_out, int64_t n,
-                     int shift, const uint32_t* __restrict__ offsets, int tiles) {
-  __shared__ uint32_t wcount[SORT_WAVES][RADIX];
-  __shared__ uint32_t base_off[RADIX];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  for (int d = threadIdx.x; d < RADIX; d += SORT_THREADS) {
-    base_off[d] = offsets[(int64_t)d * tiles + blockIdx.x];
-#pragma unroll
-    for (int w = 0; w < SORT_WAVES; ++w) wcount[w][d] = 0;
+// One workgroup per epoch: bucket totals, their exclusive scan (bucket
+// starts), and each (bucket, tile) count rewritten as its write offset.
+__global__ void __launch_bounds__(1024) shuffle_scan_kernel(ShuffleArgs a) {
+  extern __shared__ uint32_t tot[];  // [nb]
+  const int e = blockIdx.x;
+  uint32_t* hist = a.hist + (int64_t)e * a.nb * a.tiles;
+  for (int d = threadIdx.x; d < a.nb; d += blockDim.x) {
+    uint32_t s = 0;
+    for (int t = 0; t < a.tiles; ++t) s += hist[(int64_t)d * a.tiles + t];
+    tot[d] = s;
   }
   __syncthreads();
-  const uint64_t lt_mask = lane ? (~0ull >> (64 - lane)) : 0ull;
-  const int64_t wbase = (int64_t)blockIdx.x * SORT_TILE + (int64_t)wave * 64 * SORT_ITEMS;
-  uint32_t key[SORT_ITEMS];
-  int32_t val[SORT_ITEMS];
-  uint32_t rank[SORT_ITEMS];
-#pragma unroll
-  for (int it = 0; it < SORT_ITEMS; ++it) {
-    const int64_t i = wbase + (int64_t)it * 64 + lane;
-    const bool ok = i < n;
-    key[it] = ok ? keys_in[i] : 0u;
-    val[it] = ok ? vals_in[i] : 0;
-    const uint32_t d = (key[it] >> shift) & (RADIX - 1);
-    uint64_t match = __ballot(ok);
-#pragma unroll
-    for (int b = 0; b < RADIX_BITS; ++b) {
-      const uint64_t bal = __ballot((d >> b) & 1u);
-      match &= ((d >> b) & 1u) ? bal : ~bal;
+  if (threadIdx.x == 0) {
+    // nb <= 4096: a serial scan here is a few microseconds
+    uint32_t run = 0;
+    for (int d = 0; d < a.nb; ++d) {
+      const uint32_t v = tot[d];
+      tot[d] = run;
+      run += v;
     }
-    const uint32_t before = ok ? wcount[wave][d] : 0u;
-    const uint32_t within = (uint32_t)__popcll(match & lt_mask);
-    // every lane has read the running count before the group leader bumps it
-    __builtin_amdgcn_wave_barrier();
-    if (ok && within == 0) wcount[wave][d] = before + (uint32_t)__popcll(match);
-    __builtin_amdgcn_wave_barrier();
-    rank[it] = before + within;
   }
   __syncthreads();
-#pragma unroll
-  for (int it = 0; it < SORT_ITEMS; ++it) {
-    const int64_t i = wbase + (int64_t)it * 64 + lane;
-    if (i >= n) continue;
-    const uint32_t d = (key[it] >> shift) & (RADIX - 1);
-    uint32_t off = base_off[d];
-    for (int w = 0; w < wave; ++w) off += wcount[w][d];
-    off += rank[it];
-    keys_out[off] = key[it];
-    vals_out[off] = val[it];
+  uint32_t* bstart = a.bstart + (int64_t)e * (a.nb + 1);
+  for (int d = threadIdx.x; d < a.nb; d += blockDim.x) {
+    bstart[d] = tot[d];
+    uint32_t run = tot[d];
+    for (int t = 0; t < a.tiles; ++t) {
+      const uint32_t v = hist[(int64_t)d * a.tiles + t];
+      hist[(int64_t)d * a.tiles + t] = run;
+      run += v;
+    }
+  }
+  if (threadIdx.x == 0) bstart[a.nb] = (uint32_t)a.n;
+}
+
+__global__ void __launch_bounds__(TILE_THREADS) shuffle_scatter_kernel(ShuffleArgs a) {
+  extern __shared__ uint32_t slot[];  // [nb]
+  const int e = blockIdx.y;
+  const uint32_t* hist = a.hist + (int64_t)e * a.nb * a.tiles;
+  for (int d = threadIdx.x; d < a.nb; d += TILE_THREADS) slot[d] = hist[(int64_t)d * a.tiles + blockIdx.x];
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * TILE;
+  const uint32_t* keys = a.keys + (int64_t)e * a.n;
+  const int32_t* vals = a.out + (int64_t)e * a.n;
+  const int64_t eo = (int64_t)e * a.n;
+  for (int it = 0; it < TILE / TILE_THREADS; ++it) {
+    const int64_t i = base + (int64_t)it * TILE_THREADS + threadIdx.x;
+    if (i >= a.n) break;
+    const uint32_t k = keys[i];
+    const uint32_t pos = atomicAdd(&slot[bucket_of(k, a.bbits)], 1u);
+    a.tkey[eo + pos] = k;
+    a.tpos[eo + pos] = (uint32_t)i;
+    a.tval[eo + pos] = vals[i];
+  }
+}
+
+__global__ void __launch_bounds__(SORT_THREADS) shuffle_sort_kernel(ShuffleArgs a) {
+  __shared__ uint64_t sk[BUCKET_CAP];
+  __shared__ int32_t sv[BUCKET_CAP];
+  const int e = blockIdx.y;
+  const int b = blockIdx.x;
+  const uint32_t* bstart = a.bstart + (int64_t)e * (a.nb + 1);
+  const int64_t s = bstart[b], t = bstart[b + 1];
+  const int m = (int)(t - s);
+  const int64_t eo = (int64_t)e * a.n;
+  int32_t* out = a.out + eo;
+  if (m <= 0) return;
+  if (m <= BUCKET_CAP) {
+    int p2 = 1;
+    while (p2 < m) p2 <<= 1;
+    for (int i = threadIdx.x; i < p2; i += SORT_THREADS) {
+      if (i < m) {
+        sk[i] = ((uint64_t)a.tkey[eo + s + i] << 32) | (uint64_t)a.tpos[eo + s + i];
+        sv[i] = a.tval[eo + s + i];
+      } else {
+        sk[i] = ~0ull;
+        sv[i] = 0;
+      }
+    }
+    __syncthreads();
+    // bitonic sort of p2 unique-or-sentinel keys, ascending
+    for (int k = 2; k <= p2; k <<= 1) {
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        for (int i = threadIdx.x; i < p2; i += SORT_THREADS) {
+          const int l = i ^ j;
+          if (l > i) {
+            const bool up = (i & k) == 0;
+            const uint64_t x = sk[i], y = sk[l];
+            if ((x > y) == up) {
+              sk[i] = y;
+              sk[l] = x;
+              const int32_t tv = sv[i];
+              sv[i] = sv[l];
+              sv[l] = tv;
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+    for (int i = threadIdx.x; i < m; i += SORT_THREADS) out[s + i] = sv[i];
+  } else {
+    // rank by counting: exact for any size, quadratic
+    for (int i = threadIdx.x; i < m; i += SORT_THREADS) {
+      const uint64_t ki = ((uint64_t)a.tkey[eo + s + i] << 32) | (uint64_t)a.tpos[eo + s + i];
+      int rank = 0;
+      for (int j = 0; j < m; ++j) {
+        const uint64_t kj = ((uint64_t)a.tkey[eo + s + j] << 32) | (uint64_t)a.tpos[eo + s + j];
+        rank += kj < ki ? 1 : 0;
+      }
+      out[s + rank] = a.tval[eo + s + i];
+    }
   }
 }
 
@@ -202,73 +258,84 @@ int shuffle_rounds(int64_t n) {
   return (int)ceil(3.0 * log(m) / log(4294967295.0));
 }
 
-struct SortSpace {
-  uint32_t* keys_a;
-  uint32_t* keys_b;
-  int32_t* vals_b;
-  uint32_t* hist;
-  uint32_t* key;  // running round key [2]
-};
+int bucket_bits(int64_t n) {
+  if (n <= BUCKET_CAP) return 0;
+  int b = 0;
+  while (b < MAX_BUCKET_BITS && (n >> b) > 512) ++b;
+  return b;
+}
 
 size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
 
-size_t sort_space_bytes(int64_t n) {
-  const int64_t tiles = ppo::ceil_div64(n > 0 ? n : 1, SORT_TILE);
-  return 2 * align256(sizeof(uint32_t) * n) + align256(sizeof(int32_t) * n) +
-         align256(sizeof(uint32_t) * RADIX * tiles) + 256;
+struct Space {
+  uint32_t *keys, *hist, *bstart, *tkey, *tpos;
+  int32_t* tval;
+};
+
+size_t space_bytes(int epochs, int64_t n) {
+  const int64_t E = epochs > 0 ? epochs : 1;
+  const int64_t nn = n > 0 ? n : 1;
+  const int64_t tiles = ppo::ceil_div64(nn, TILE);
+  const int64_t nb = int64_t(1) << bucket_bits(nn);
+  return 4 * align256(sizeof(uint32_t) * E * nn) + align256(sizeof(uint32_t) * E * nb * tiles) +
+         align256(sizeof(uint32_t) * E * (nb + 1));
 }
 
-SortSpace carve(void* ws, int64_t n) {
-  const int64_t tiles = ppo::ceil_div64(n > 0 ? n : 1, SORT_TILE);
+Space carve(void* ws, int epochs, int64_t n) {
+  const int64_t E = epochs > 0 ? epochs : 1;
+  const int64_t tiles = ppo::ceil_div64(n, TILE);
+  const int64_t nb = int64_t(1) << bucket_bits(n);
   char* p = (char*)ws;
-  SortSpace s;
-  s.keys_a = (uint32_t*)p; p += align256(sizeof(uint32_t) * n);
-  s.keys_b = (uint32_t*)p; p += align256(sizeof(uint32_t) * n);
-  s.vals_b = (int32_t*)p; p += align256(sizeof(int32_t) * n);
-  s.hist = (uint32_t*)p; p += align256(sizeof(uint32_t) * RADIX * tiles);
-  s.key = (uint32_t*)p;
+  Space s;
+  s.keys = (uint32_t*)p; p += align256(sizeof(uint32_t) * E * n);
+  s.tkey = (uint32_t*)p; p += align256(sizeof(uint32_t) * E * n);
+  s.tpos = (uint32_t*)p; p += align256(sizeof(uint32_t) * E * n);
+  s.tval = (int32_t*)p; p += align256(sizeof(uint32_t) * E * n);
+  s.hist = (uint32_t*)p; p += align256(sizeof(uint32_t) * E * nb * tiles);
+  s.bstart = (uint32_t*)p;
   return s;
 }
 
-// permutation(key, n) into out (device); key is a device pointer to 2 words.
-int permutation_impl(hipStream_t st, const uint32_t* key, int32_t* out, int64_t n, void* ws) {
-  if (n <= 0) return PPO_OK;
-  SortSpace s = carve(ws, n);
-  const int tiles = (int)ppo::ceil_div64(n, SORT_TILE);
+// out[e * n + i] = i for every epoch row
+__global__ void iota_kernel(int32_t* out, int64_t n, int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < total) out[i] = (int32_t)(i % n);
+}
+
+// permutation(split(key, epochs)[e], n) for every e (split_epochs = 1), or of
+// key itself (split_epochs = 0, epochs = 1), into out[e * n + i].
+int shuffle_impl(hipStream_t st, const uint32_t* key, int split_epochs, int epochs, int64_t n, int32_t* out,
+                 void* ws) {
+  if (n <= 0 || epochs <= 0) return PPO_OK;
   const int rounds = shuffle_rounds(n);
   if (rounds == 0) {
-    // n <= 1: the identity
-    hipLaunchKernelGGL(round_bits_kernel, dim3(1), dim3(64), 0, st, key, s.keys_a, out, n, 1);
+    // n == 1: the identity
+    hipLaunchKernelGGL(iota_kernel, dim3((unsigned)ppo::ceil_div64(n * epochs, 256)), dim3(256), 0, st, out, n,
+                       n * epochs);
     return ppo::check_launch("ppo_permutation");
   }
-  const int bits_blocks = (int)std::min<int64_t>(ppo::ceil_div64(n, 256), 4096);
+  Space sp = carve(ws, epochs, n);
+  ShuffleArgs a;
+  a.key = key; a.split_epochs = split_epochs; a.n = n;
+  a.tiles = (int)ppo::ceil_div64(n, TILE);
+  a.bbits = bucket_bits(n);
+  a.nb = 1 << a.bbits;
+  a.out = out; a.keys = sp.keys; a.hist = sp.hist; a.bstart = sp.bstart;
+  a.tkey = sp.tkey; a.tpos = sp.tpos; a.tval = sp.tval;
+  const size_t shm = sizeof(uint32_t) * a.nb;
   for (int r = 0; r < rounds; ++r) {
-    const uint32_t* kr = r == 0 ? key : s.key;
-    hipLaunchKernelGGL(round_bits_kernel, dim3(bits_blocks), dim3(256), 0, st, kr, s.keys_a, out, n,
-                       r == 0 ? 1 : 0);
-    if (r + 1 < rounds) hipLaunchKernelGGL(advance_key_kernel, dim3(1), dim3(64), 0, st, kr, s.key);
-    uint32_t* kin = s.keys_a;
-    int32_t* vin = out;
-    uint32_t* kout = s.keys_b;
-    int32_t* vout = s.vals_b;
-    for (int pass = 0; pass < 32 / RADIX_BITS; ++pass) {
-      const int shift = pass * RADIX_BITS;
-      hipLaunchKernelGGL(radix_hist_kernel, dim3(tiles), dim3(SORT_THREADS), 0, st, kin, n, shift,
-                         s.hist, tiles);
-      hipLaunchKernelGGL(radix_scan_kernel, dim3(1), dim3(RADIX), 0, st, s.hist, tiles);
-      hipLaunchKernelGGL(radix_scatter_kernel, dim3(tiles), dim3(SORT_THREADS), 0, st, kin, vin, kout,
-                         vout, n, shift, s.hist, tiles);
-      std::swap(kin, kout);
-      std::swap(vin, vout);
-    }
-    // an even number of passes leaves the values back in `out`
+    a.round = r;
+    hipLaunchKernelGGL(shuffle_bits_kernel, dim3(a.tiles, epochs), dim3(TILE_THREADS), shm, st, a);
+    hipLaunchKernelGGL(shuffle_scan_kernel, dim3(epochs), dim3(1024), shm, st, a);
+    hipLaunchKernelGGL(shuffle_scatter_kernel, dim3(a.tiles, epochs), dim3(TILE_THREADS), shm, st, a);
+    hipLaunchKernelGGL(shuffle_sort_kernel, dim3(a.nb, epochs), dim3(SORT_THREADS), 0, st, a);
   }
   return ppo::check_launch("ppo_permutation");
 }
 
 }  // namespace
 
-PPO_EXPORT size_t ppo_permutation_workspace(int64_t n) { return sort_space_bytes(n); }
+PPO_EXPORT size_t ppo_permutation_workspace(int64_t n) { return space_bytes(1, n); }
 
 PPO_EXPORT int ppo_threefry_split(void* stream, const uint32_t* key, uint32_t* out, int64_t num) {
   if (num < 0 || !key || !out) return ppo::set_error(PPO_ERR_ARG, "ppo_threefry_split: bad argument");
@@ -282,32 +349,20 @@ PPO_EXPORT int ppo_permutation(void* stream, const uint32_t* key, int32_t* out, 
                                size_t workspace_bytes) {
   if (n < 0 || n > INT32_MAX || !key || (n > 0 && !out))
     return ppo::set_error(PPO_ERR_ARG, "ppo_permutation: bad argument (n=%lld)", (long long)n);
-  if (workspace_bytes < sort_space_bytes(n) || (n > 0 && !workspace))
+  if (workspace_bytes < space_bytes(1, n) || (n > 0 && !workspace))
     return ppo::set_error(PPO_ERR_SPACE, "ppo_permutation: workspace %zu < %zu bytes", workspace_bytes,
-                          sort_space_bytes(n));
-  return permutation_impl(ppo::as_stream(stream), key, out, n, workspace);
+                          space_bytes(1, n));
+  return shuffle_impl(ppo::as_stream(stream), key, 0, 1, n, out, workspace);
 }
 
-// out[e * n + i] = permutation(split(key, epochs)[e], n)[i]; epoch keys are
-// written to the first 2 * epochs words after the sort space in `workspace`.
-PPO_EXPORT size_t ppo_epoch_permutations_workspace(int epochs, int64_t n) {
-  return sort_space_bytes(n) + align256(sizeof(uint32_t) * 2 * (epochs > 0 ? epochs : 1));
-}
+PPO_EXPORT size_t ppo_epoch_permutations_workspace(int epochs, int64_t n) { return space_bytes(epochs, n); }
 
+// out[e * n + i] = permutation(split(key, epochs)[e], n)[i], all epochs in the same launches.
 PPO_EXPORT int ppo_epoch_permutations(void* stream, const uint32_t* key, int epochs, int64_t n, int32_t* out,
                                       void* workspace, size_t workspace_bytes) {
-  if (epochs < 0 || n < 0 || n > INT32_MAX || !key || (epochs > 0 && n > 0 && !out))
+  if (epochs < 0 || epochs > 65535 || n < 0 || n > INT32_MAX || !key || (epochs > 0 && n > 0 && !out))
     return ppo::set_error(PPO_ERR_ARG, "ppo_epoch_permutations: bad argument");
-  if (workspace_bytes < ppo_epoch_permutations_workspace(epochs, n) || !workspace)
+  if (workspace_bytes < space_bytes(epochs, n) || !workspace)
     return ppo::set_error(PPO_ERR_SPACE, "ppo_epoch_permutations: workspace too small");
-  if (epochs == 0) return PPO_OK;
-  hipStream_t st = ppo::as_stream(stream);
-  uint32_t* keys = (uint32_t*)((char*)workspace + sort_space_bytes(n));
-  hipLaunchKernelGGL(split_kernel, dim3((unsigned)ppo::ceil_div64(epochs, 64)), dim3(64), 0, st, key, keys,
-                     (int64_t)epochs);
-  for (int e = 0; e < epochs; ++e) {
-    int rc = permutation_impl(st, keys + 2 * e, out + (int64_t)e * n, n, workspace);
-    if (rc) return rc;
-  }
-  return ppo::check_launch("ppo_epoch_permutations");
+  return shuffle_impl(ppo::as_stream(stream), key, 1, epochs, n, out, workspace);
 }

@@ -102,7 +102,7 @@ def test_permutation_is_bit_exact(n):
     np.testing.assert_array_equal(got, prng.permutation(k, n))
 
 
-@pytest.mark.parametrize("E, n", [(4, 512), (4, 65536), (4, 262144), (4, 1024)])
+@pytest.mark.parametrize("E, n", [(4, 512), (4, 65536), (4, 262144), (4, 1024), (3, 1), (2, 5000), (1, 2000000)])
 def test_epoch_permutations_are_bit_exact(E, n):
     k = prng.key(7 * n + E)
     K = dev(k.view(np.int32))
