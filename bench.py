@@ -37,7 +37,22 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--profile-only", action="store_true", help="warmup + timed updates only")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run 5 plain device copies of MIB MiB (calibrates rocprofv3 FETCH/WRITE_SIZE)")
     return ap.parse_args()
+
+
+def copy_probe(mib):
+    """Five torch device-to-device copies of a known size: the reference
+    dispatch against which the FETCH_SIZE / WRITE_SIZE counters are scaled."""
+    import torch
+    n = mib * (1 << 20) // 4
+    x = torch.ones(n, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(5):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": 4 * n}), flush=True)
 
 
 def log(msg):
@@ -98,6 +113,20 @@ def _to_torch(tree, device):
     if isinstance(tree, dict):
         return {k: _to_torch(v, device) for k, v in tree.items()}
     return torch.from_numpy(np.asarray(tree, np.float32)).to(device)
+
+
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 --pmc
+    summary (profiles/traffic.json), or None when that shape was not measured."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(workload, {}).get(kernel)
+    except (OSError, ValueError):
+        return None
+    if not rec:
+        return None
+    return 1024.0 * (rec["fetch_kib"] * rec["fetch_scale"] + rec["write_kib"] * rec["write_scale"])
 
 
 def launch_work(name, args):
@@ -212,6 +241,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
     recipe = recipes.make(args.config)
     dev = torch.device("cuda:0")
     log(f"workload {recipe.name}: T={recipe.T} N={recipe.N} obs={recipe.obs_dim} "
@@ -262,6 +294,7 @@ def main():
             roof = {"bound": "hbm", "achieved": achieved, "peak": PEAK["hbm"], "unit": "GB/s",
                     "frac": achieved / PEAK["hbm"], "traffic": None}
         roof["kernel"] = f"{dom['name']} layout={dom['layout']} MNK={dom['shape']}"
+        roof["traffic"] = measured_traffic(out["config"]["workload"], roof["kernel"])
         roof["avg_ms"] = dom["ms"]
         roof["share_of_update"] = dom["ms"] * dom["count"] / total
         out["roofline"] = roof
