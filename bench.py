@@ -91,6 +91,18 @@ def synthetic_rollout(recipe, params, device, seed):
     truncated = torch.zeros(T, N, dtype=torch.bool, device=device)
     plan = recipe.network.plan(D)
     tparams = _to_torch(params, device)
+    if plan["torso"] is not None:
+        # first.done[t] = second.done[t-1] (same-step auto-reset); first.done[0] drawn
+        first_term = torch.cat([torch.rand(1, N, device=device, generator=g) < recipe.done_p, terminated[:-1]])
+        first_trunc = torch.zeros_like(first_term)
+        H = plan["torso"]["features"]
+        carry0 = torch.tanh(torch.randn(N, H, device=device, generator=g))
+        action, logp, value, carry = torch_ref.recurrent_sample(tparams, plan, obs[:-1], first_term, carry0, g)
+        return Transition(
+            first=Timestep(obs=obs[:-1], terminated=first_term.contiguous(), truncated=first_trunc),
+            second=Timestep(obs=obs[1:], action=action.contiguous(), reward=reward.contiguous(),
+                            terminated=terminated, truncated=truncated),
+            aux={"log_prob": logp.contiguous(), "value": value.contiguous()}, carry=carry.contiguous())
     acts, lps, vals = [], [], []
     flat_obs = obs[:-1].reshape(T * N, D)
     for s in range(0, T * N, 65536):
@@ -130,7 +142,9 @@ def measured_traffic(workload, kernel):
 
 
 def launch_work(name, args):
-    """(flops, bytes) of one launch: algorithmic work of the call's shapes."""
+    """(flops, bytes) of one launch: algorithmic work of the call's shapes
+    (GEMM: 2MNK FLOP; bandwidth-bound kernels: the bytes the computation must
+    read and write once)."""
     if name == "ppo_gemm_f32":
         M, N, K = args[10], args[11], args[12]
         return 2.0 * M * N * K, 4.0 * (M * K + K * N + M * N)
@@ -140,22 +154,57 @@ def launch_work(name, args):
     if name == "ppo_adam_clip_f32":
         n = args[6]
         return 0.0, 28.0 * n
+    if name == "ppo_head_loss_f32":
+        rows, F, A = args[2], args[15], args[16]
+        groups = 2 if args[10] else 1
+        acts = (1 if args[26] else 0) + (1 if args[31] else 0)
+        per_row = 4.0 * F * (2 * groups + acts) + 4.0 * 6 + (4.0 * A if args[1] == 1 else 0.0)
+        return 0.0, rows * per_row
+    if name in ("ppo_gru_fwd_step_f32",):
+        Bm, H = args[-2], args[-1]
+        return 2.0 * Bm * H * 3 * H, 4.0 * Bm * (3 * H + 2 * H + 6 * H) + 4.0 * H * 3 * H
+    if name in ("ppo_gru_bwd_step_f32",):
+        Bm, H = args[-2], args[-1]
+        flops = 2.0 * Bm * 3 * H * H if args[1] else 0.0
+        return flops, 4.0 * Bm * (3 * H + 2 * H + 7 * H) + (4.0 * H * 3 * H if args[1] else 0.0)
+    if name == "ppo_layernorm_act_fwd_f32":
+        rows, F = args[9], args[10]
+        return 0.0, 4.0 * rows * (2 * F + 2)
+    if name == "ppo_layernorm_act_bwd_f32":
+        rows, F = args[13], args[14]
+        return 0.0, 4.0 * rows * (3 * F + 2)
     return 0.0, 0.0
 
 
+def launch_key(name, args):
+    """Launches with the same entry point and shape do the same work."""
+    if name == "ppo_gemm_f32":
+        return (name, args[1], args[2]) + tuple(args[10:16])
+    if name in ("ppo_gru_fwd_step_f32", "ppo_gru_bwd_step_f32"):
+        return (name, args[-2], args[-1], bool(args[1]))
+    return (name, id(args))
+
+
 def time_launches(ex, reps, per_update_steps):
-    """Times every launch of (bootstrap + GAE + permutations + one minibatch
-    step) with HIP events on the launching stream."""
+    """Times the launches of (bootstrap + GAE + permutations + one minibatch
+    step) with HIP events on the launching stream: each distinct launch shape
+    once, `reps` back-to-back repetitions, counted as many times as it occurs
+    per update."""
     import torch
     from boonta_amd import _lib
 
     calls = ex.record(max_steps=1)
     stream = torch.cuda.current_stream()
     st = stream.cuda_stream
-    mb_start = next(i for i, (n, _) in enumerate(calls) if n == "ppo_gemm_f32" and i > 0 and
-                    calls[i - 1][0] == "ppo_epoch_permutations")
-    rows = []
+    first_mb = max(i for i, (n, _) in enumerate(calls)
+                   if n in ("ppo_epoch_permutations", "ppo_sequence_rows")) + 1
+    rows, seen = [], {}
     for i, (name, args) in enumerate(calls):
+        count = per_update_steps if i >= first_mb else 1
+        key = launch_key(name, args)
+        if key in seen:
+            seen[key]["count"] += count
+            continue
         args = (st,) + tuple(args[1:])
         _lib.call(name, *args)  # warm
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -165,11 +214,14 @@ def time_launches(ex, reps, per_update_steps):
         e1.record(stream)
         e1.synchronize()
         ms = e0.elapsed_time(e1) / reps
-        count = per_update_steps if i >= mb_start else 1
         flops, nbytes = launch_work(name, args)
-        rows.append({"i": i, "name": name, "ms": ms, "count": count, "flops": flops, "bytes": nbytes,
-                     "shape": [a for a in args[10:13]] if name == "ppo_gemm_f32" else None,
-                     "layout": [args[1], args[2]] if name == "ppo_gemm_f32" else None})
+        row = {"i": i, "name": name, "ms": ms, "count": count, "flops": flops, "bytes": nbytes,
+               "shape": [a for a in args[10:13]] if name == "ppo_gemm_f32" else None,
+               "layout": [args[1], args[2]] if name == "ppo_gemm_f32" else None}
+        if name.startswith("ppo_gru"):
+            row["shape"] = [args[-2], args[-1]]
+        rows.append(row)
+        seen[key] = row
     return rows
 
 
@@ -197,23 +249,45 @@ def cpu_baseline(recipe, params, tr_dev, budget_s):
     t_gae = time.perf_counter() - t0
     p = oppo.tree_map(lambda x: np.asarray(x, np.float64), params)
     st = oppo.optimizer_init(p)
-    obs_flat = tr_dev.first.obs.reshape(B, -1)
-    act_flat = s.action.reshape((B,) + tuple(s.action.shape[2:]))
-    lp_flat = tr_dev.aux["log_prob"].reshape(B)
-    v_flat = tr_dev.aux["value"].reshape(B)
-    advf, retf = adv.reshape(B), ret.reshape(B)
     steps, spent = 0, 0.0
-    while spent < budget_s and steps < 64:
-        idx = np.sort(rng.permutation(B)[:mb])
-        it = torch.from_numpy(idx).to(obs_flat.device)
-        x = obs_flat[it].cpu().numpy()
-        act = act_flat[it].cpu().numpy()
-        olp, ov = lp_flat[it].cpu().numpy(), v_flat[it].cpu().numpy()
-        t0 = time.perf_counter()
-        _, _, grads = oppo.loss_and_grad(p, plan, cfg, x, act, olp, ov, advf[idx], retf[idx])
-        p, st, _ = oppo.optimizer_update(grads, st, p, opt)
-        spent += time.perf_counter() - t0
-        steps += 1
+    if recipe.recurrent:
+        # sequence minibatches of N / M whole envs x T steps (recurrent_ppo.py:214-223)
+        f = tr_dev.first
+        em = lambda a, envs: np.moveaxis(a[:, envs], 0, 1)
+        obs_h = f.obs.cpu().numpy()
+        done_h = (f.terminated | f.truncated).cpu().numpy()
+        act_h = s.action.cpu().numpy()
+        lp_h, v_h = tr_dev.aux["log_prob"].cpu().numpy(), value
+        carry0 = tr_dev.carry[0].cpu().numpy()
+        nb = N // M
+        while spent < budget_s and steps < 64:
+            envs = np.sort(rng.permutation(N)[:nb])
+            args = (em(obs_h, envs), em(done_h, envs), carry0[envs], em(act_h, envs), em(lp_h, envs),
+                    em(v_h, envs), em(adv, envs), em(ret, envs))
+            t0 = time.perf_counter()
+            _, _, grads = oppo.recurrent_loss_and_grad(p, plan, cfg, *args)
+            p, st, _ = oppo.optimizer_update(grads, st, p, opt)
+            spent += time.perf_counter() - t0
+            steps += 1
+        mb = f"{nb} envs x {T} steps"
+    else:
+        obs_flat = tr_dev.first.obs.reshape(B, -1)
+        act_flat = s.action.reshape((B,) + tuple(s.action.shape[2:]))
+        lp_flat = tr_dev.aux["log_prob"].reshape(B)
+        v_flat = tr_dev.aux["value"].reshape(B)
+        advf, retf = adv.reshape(B), ret.reshape(B)
+        while spent < budget_s and steps < 64:
+            idx = np.sort(rng.permutation(B)[:mb])
+            it = torch.from_numpy(idx).to(obs_flat.device)
+            x = obs_flat[it].cpu().numpy()
+            act = act_flat[it].cpu().numpy()
+            olp, ov = lp_flat[it].cpu().numpy(), v_flat[it].cpu().numpy()
+            t0 = time.perf_counter()
+            _, _, grads = oppo.loss_and_grad(p, plan, cfg, x, act, olp, ov, advf[idx], retf[idx])
+            p, st, _ = oppo.optimizer_update(grads, st, p, opt)
+            spent += time.perf_counter() - t0
+            steps += 1
+        mb = f"{mb} rows"
     t_step = spent / steps
     t_update = E * M * t_step + t_gae
     try:
@@ -223,7 +297,7 @@ def cpu_baseline(recipe, params, tr_dev, budget_s):
     threads = int(os.environ.get("OMP_NUM_THREADS", cores))
     return {"value": B / t_update, "unit": "samples/s", "cores": min(cores, threads), "kind": "port",
             "sample": f"oracle float64 numpy: GAE over the full [{T},{N}] rollout plus {steps} minibatch "
-                      f"steps of {mb} rows (forward, backward, clip, Adam; {spent:.1f} s), extrapolated to "
+                      f"steps of {mb} (forward, backward, clip, Adam; {spent:.1f} s), extrapolated to "
                       f"{E}x{M} steps per update"}
 
 
@@ -236,6 +310,7 @@ def main():
     import torch
     from boonta_amd import recipes
     from boonta_amd.algorithms.ppo import PPO
+    from boonta_amd.algorithms.recurrent_ppo import RecurrentPPO
     from boonta_amd.random import key as make_key
 
     if not torch.cuda.is_available():
@@ -249,7 +324,8 @@ def main():
     log(f"workload {recipe.name}: T={recipe.T} N={recipe.N} obs={recipe.obs_dim} "
         f"{recipe.cfg.update_epochs}x{recipe.cfg.num_minibatches} minibatches of {recipe.minibatch}")
     params = recipe.network.init(recipe.seed, recipe.obs_dim)["params"]
-    alg = PPO(cfg=recipe.cfg, network=recipe.network, optimizer=recipe.optimizer, use_graph=not args.no_graph)
+    cls = RecurrentPPO if recipe.recurrent else PPO
+    alg = cls(cfg=recipe.cfg, network=recipe.network, optimizer=recipe.optimizer, use_graph=not args.no_graph)
     state = alg.init_from_params({"params": params}, recipe.obs_dim)
     tr = synthetic_rollout(recipe, params, dev, recipe.seed)
     torch.cuda.synchronize()

@@ -27,6 +27,8 @@ SIGNATURES = {
     "ppo_abi_version": (I, []),
     "ppo_device_check": (I, [I]),
     "ppo_gae_f32": (I, [P, P, P, P, P, P, P, P, P, P, I, I, D, D, I]),
+    "ppo_normalize_workspace": (SZ, [I64]),
+    "ppo_normalize_advantages_f32": (I, [P, P, I64, P, SZ]),
     "ppo_threefry_split": (I, [P, P, P, I64]),
     "ppo_permutation_workspace": (SZ, [I64]),
     "ppo_permutation": (I, [P, P, P, I64, P, SZ]),
@@ -47,6 +49,10 @@ SIGNATURES = {
     "ppo_head_loss_max_features": (I, []),
     "ppo_head_loss_f32": (I, [P, I, I, P, P, I64, P, I64, P, I, P, I64, P, I64, P, I, I, P, P, P, P, P, P, P,
                               I, P, I64, P, I64, I, P, I64, P, I64, P, P, P, P, P, P, F, I, F, F, F]),
+    "ppo_gru_fwd_step_f32": (I, [P, P, I64, P, I64, P, P, P, P, P, I64, P, P, I64, P, I64, P, I64, I, I]),
+    "ppo_gru_bwd_step_f32": (I, [P, P, I64, P, I64, P, I64, P, I64, P, P, P, P, I64, P, I64, P, I64, P, I64, P,
+                                 I64, I, I]),
+    "ppo_sequence_rows": (I, [P, P, I, I, I, I, P]),
     "ppo_grad_reduce_segment_bytes": (I, []),
     "ppo_grad_reduce_chunk_bytes": (I, []),
     "ppo_grad_reduce_chunk_elems": (I, []),

@@ -124,16 +124,18 @@ class PPO:
         raise NotImplementedError("the rollout-side PPO.step is not compiled yet")
 
     # ---------------------------------------------------------------- update
+    @staticmethod
+    def _need(t, dtype, name, shape=None):
+        if not isinstance(t, torch.Tensor) or t.dtype != dtype or not t.is_contiguous() or not t.is_cuda:
+            raise TypeError(f"{name} must be a contiguous {dtype} device tensor")
+        if shape is not None and tuple(t.shape) != tuple(shape):
+            raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+        return t.data_ptr()
+
     def _inputs(self, transitions, obs_dim: int) -> tuple[dict, tuple]:
         f, s, aux = transitions.first, transitions.second, transitions.aux
         T, N = s.reward.shape[:2]
-
-        def need(t, dtype, name, shape=None):
-            if not isinstance(t, torch.Tensor) or t.dtype != dtype or not t.is_contiguous() or not t.is_cuda:
-                raise TypeError(f"{name} must be a contiguous {dtype} device tensor")
-            if shape is not None and tuple(t.shape) != tuple(shape):
-                raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
-            return t.data_ptr()
+        need = self._need
 
         prog = self.program(obs_dim)
         if prog.dist["kind"] == "categorical":
@@ -155,11 +157,13 @@ class PPO:
         }
         return inp, tuple(sorted(inp.items()))
 
+    executor_class = MLPExecutor
+
     def executor(self, state, T: int, N: int, obs_dim: int) -> MLPExecutor:
         flat = flat_state_of(state)
         k = (id(flat), T, N, obs_dim)
         if k not in self._executors:
-            self._executors[k] = MLPExecutor(self.program(obs_dim), flat, self.cfg, self.chain, T, N)
+            self._executors[k] = self.executor_class(self.program(obs_dim), flat, self.cfg, self.chain, T, N)
         return self._executors[k]
 
     def update(self, state: PPOState, key, transitions) -> PPOState:

@@ -124,3 +124,100 @@ PPO_EXPORT int ppo_gae_f32(void* stream, const float* reward, const uint8_t* ter
   hipLaunchKernelGGL(gae_kernel, grid, block, 0, ppo::as_stream(stream), a);
   return ppo::check_launch("ppo_gae_f32");
 }
+
+// ------------------------------------------------- advantage normalisation
+// (A - mean(A)) / (std(A) + 1e-8) over all T * N advantages, population
+// std, as boonta/algorithms/ppo.py:220-221 (recurrent_ppo.py:206-207).  Three
+// launches without a grid barrier: per-block sums; every block folds the sums
+// into the mean and writes per-block sums of squared deviations; every block
+// folds those into the std and normalises its elements.  Partial sums are
+// fp64 and folded in a fixed order.
+namespace {
+
+constexpr int NORM_THREADS = 256;
+constexpr int NORM_PER_THREAD = 16;
+constexpr int NORM_PER_BLOCK = NORM_THREADS * NORM_PER_THREAD;
+
+__device__ double block_sum_d(double v) {
+  __shared__ double s[NORM_THREADS / 64];
+  v = ppo::wave_sum_d(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0) s[w] = v;
+  __syncthreads();
+  double t = 0.0;
+  for (int i = 0; i < NORM_THREADS / 64; ++i) t += s[i];
+  __syncthreads();
+  return t;
+}
+
+__device__ double fold(const double* part, int nblocks) {
+  // every thread folds the same partials in the same order
+  double t = 0.0;
+  for (int i = 0; i < nblocks; ++i) t += part[i];
+  return t;
+}
+
+__global__ void __launch_bounds__(NORM_THREADS) norm_sum_kernel(const float* a, int64_t n, double* part) {
+  const int64_t base = (int64_t)blockIdx.x * NORM_PER_BLOCK;
+  double v = 0.0;
+  for (int j = 0; j < NORM_PER_THREAD; ++j) {
+    const int64_t i = base + (int64_t)j * NORM_THREADS + threadIdx.x;
+    if (i < n) v += (double)a[i];
+  }
+  v = block_sum_d(v);
+  if (threadIdx.x == 0) part[blockIdx.x] = v;
+}
+
+__global__ void __launch_bounds__(NORM_THREADS) norm_dev_kernel(const float* a, int64_t n, const double* sums,
+                                                                double* part, int nblocks) {
+  const double mean = fold(sums, nblocks) / (double)n;
+  const int64_t base = (int64_t)blockIdx.x * NORM_PER_BLOCK;
+  double v = 0.0;
+  for (int j = 0; j < NORM_PER_THREAD; ++j) {
+    const int64_t i = base + (int64_t)j * NORM_THREADS + threadIdx.x;
+    if (i < n) {
+      const double d = (double)a[i] - mean;
+      v += d * d;
+    }
+  }
+  v = block_sum_d(v);
+  if (threadIdx.x == 0) part[blockIdx.x] = v;
+}
+
+__global__ void __launch_bounds__(NORM_THREADS) norm_apply_kernel(float* a, int64_t n, const double* sums,
+                                                                  const double* devs, int nblocks) {
+  const float mean = (float)(fold(sums, nblocks) / (double)n);
+  const float stdv = (float)sqrt(fold(devs, nblocks) / (double)n);
+  const float den = stdv + 1e-8f;
+  const int64_t base = (int64_t)blockIdx.x * NORM_PER_BLOCK;
+  for (int j = 0; j < NORM_PER_THREAD; ++j) {
+    const int64_t i = base + (int64_t)j * NORM_THREADS + threadIdx.x;
+    if (i < n) a[i] = (a[i] - mean) / den;
+  }
+}
+
+}  // namespace
+
+PPO_EXPORT size_t ppo_normalize_workspace(int64_t n) {
+  if (n <= 0) return 0;
+  return 2 * sizeof(double) * (size_t)ppo::ceil_div64(n, NORM_PER_BLOCK);
+}
+
+PPO_EXPORT int ppo_normalize_advantages_f32(void* stream, float* adv, int64_t n, void* workspace,
+                                            size_t workspace_bytes) {
+  if (n < 0) return ppo::set_error(PPO_ERR_ARG, "ppo_normalize_advantages_f32: negative size");
+  if (n == 0) return PPO_OK;
+  if (!adv || !workspace) return ppo::set_error(PPO_ERR_ARG, "ppo_normalize_advantages_f32: null buffer");
+  if (workspace_bytes < ppo_normalize_workspace(n))
+    return ppo::set_error(PPO_ERR_SPACE, "ppo_normalize_advantages_f32: workspace %zu < %zu bytes",
+                          workspace_bytes, ppo_normalize_workspace(n));
+  const int64_t nb = ppo::ceil_div64(n, NORM_PER_BLOCK);
+  if (nb > (1 << 20)) return ppo::set_error(PPO_ERR_ARG, "ppo_normalize_advantages_f32: n too large");
+  double* sums = static_cast<double*>(workspace);
+  double* devs = sums + nb;
+  hipStream_t s = ppo::as_stream(stream);
+  hipLaunchKernelGGL(norm_sum_kernel, dim3((unsigned)nb), dim3(NORM_THREADS), 0, s, adv, n, sums);
+  hipLaunchKernelGGL(norm_dev_kernel, dim3((unsigned)nb), dim3(NORM_THREADS), 0, s, adv, n, sums, devs, (int)nb);
+  hipLaunchKernelGGL(norm_apply_kernel, dim3((unsigned)nb), dim3(NORM_THREADS), 0, s, adv, n, sums, devs, (int)nb);
+  return ppo::check_launch("ppo_normalize_advantages_f32");
+}

@@ -93,8 +93,6 @@ class Program:
     """Flat layout + tower structure of an MLP actor-critic plan."""
 
     def __init__(self, plan: dict):
-        if plan.get("torso") is not None:
-            raise NotImplementedError("recurrent torsos use the recurrent executor")
         if plan["compute_dtype"] != "float32":
             raise NotImplementedError("bf16 compute is not compiled yet")
         self.plan = plan
@@ -135,6 +133,11 @@ class Program:
         if trunk and (actor or critic):
             raise NotImplementedError("a shared trunk followed by separate towers is not compiled")
         self.trunk = [layer(g) for g in trunk]
+        self.gru = None
+        if plan.get("torso") is not None:
+            if actor or critic:
+                raise NotImplementedError("a recurrent torso must feed plain Dense heads")
+            self.gru = self._gru(L, plan["torso"])
         self.actor_layers = [layer(g) for g in actor]
         self.critic_layers = [layer(g) for g in critic]
         self.dist = plan["dist"]
@@ -157,9 +160,39 @@ class Program:
             L.add_leaf(tuple(self.dist["scale"]), self.scale_region.offset, (D,), (1,))
         L.finish()
 
+    @staticmethod
+    def _gru(L: FlatLayout, t: dict) -> "GRUSpec":
+        """flax GRUCell parameters as two side-by-side matrices: the input
+        kernels [in, 3H] in column order (in, ir, iz) with their biases, and
+        the recurrent kernels [H, 3H] in order (hr, hz, hn), plus hn's bias."""
+        H, I = t["features"], t["in"]
+        if H % 64:
+            raise NotImplementedError("the GRU width must be a multiple of 64")
+        base = tuple(t["path"])
+        wi, bi = L.region(I, 3 * H), L.region(1, 3 * H)
+        wh, bhn = L.region(H, 3 * H), L.region(1, H)
+        for g, col in (("in", 0), ("ir", H), ("iz", 2 * H)):
+            L.add_leaf(base + (g, "kernel"), wi.offset + col, (I, H), (3 * H, 1))
+            L.add_leaf(base + (g, "bias"), bi.offset + col, (H,), (1,))
+        for g, col in (("hr", 0), ("hz", H), ("hn", 2 * H)):
+            L.add_leaf(base + (g, "kernel"), wh.offset + col, (H, H), (3 * H, 1))
+        L.add_leaf(base + ("hn", "bias"), bhn.offset, (H,), (1,))
+        return GRUSpec(base, I, H, wi, bi, wh, bhn)
+
     @property
     def action_dim(self) -> int:
         return self.dist["num"] if self.dist["kind"] == "categorical" else self.dist["dim"]
+
+
+@dataclass
+class GRUSpec:
+    path: tuple
+    fin: int
+    H: int
+    wi: Region
+    bi: Region
+    wh: Region
+    bhn: Region
 
 
 # --------------------------------------------------------------- buffers
@@ -206,6 +239,8 @@ class MLPExecutor:
     """One compiled PPO.update for fixed (T, N, obs, minibatches, epochs)."""
 
     def __init__(self, program: Program, flat: FlatState, cfg, chain, T: int, N: int):
+        if program.gru is not None and type(self) is MLPExecutor:
+            raise TypeError("a recurrent program runs on RecurrentExecutor")
         self._call = _lib.call
         self.prog = program
         self.flat = flat
@@ -215,8 +250,9 @@ class MLPExecutor:
         self.B = T * N
         self.E = int(cfg.update_epochs)
         self.M = int(cfg.num_minibatches)
-        if self.B % self.M:
-            raise ValueError(f"batch {self.B} is not divisible into {self.M} minibatches")
+        self.perm_n = self._perm_size()
+        if self.perm_n % self.M:
+            raise ValueError(f"{self.perm_n} permuted items are not divisible into {self.M} minibatches")
         self.mb = self.B // self.M
         dev = flat.device
         f32 = dict(dtype=torch.float32, device=dev)
@@ -246,7 +282,7 @@ class MLPExecutor:
         self.trunk = [layer_bufs(s, mb, True) for s in program.trunk]
         self.actor = [layer_bufs(s, mb, True) for s in program.actor_layers]
         self.critic = [layer_bufs(s, mb, True) for s in program.critic_layers]
-        self.boot_layers = [layer_bufs(s, N, False) for s in
+        self.boot_layers = [layer_bufs(s, self._boot_rows(), False) for s in
                             (program.trunk if program.shared_head else program.critic_layers)]
         ha, hc = program.head_a, program.head_c
         lib = _lib.load()
@@ -294,11 +330,20 @@ class MLPExecutor:
         self.BOOT = torch.zeros(N, **f32)
         self.ADV = torch.zeros(self.B, **f32)
         self.RET = torch.zeros(self.B, **f32)
-        self.PERM = torch.zeros(self.E, self.B, dtype=torch.int32, device=dev)
-        ws = lib.ppo_epoch_permutations_workspace(self.E, self.B)
+        self.PERM = torch.zeros(self.E, self.perm_n, dtype=torch.int32, device=dev)
+        ws = lib.ppo_epoch_permutations_workspace(self.E, self.perm_n)
         self.PERM_WS = torch.zeros(ws, dtype=torch.uint8, device=dev)
         self.KEY = torch.zeros(2, dtype=torch.int32, device=dev)
+        self.NORM_WS = torch.zeros(max(1, lib.ppo_normalize_workspace(self.B)), dtype=torch.uint8, device=dev)
+        self._alloc_extra()
         self._build_reduce_tables()
+
+    def _alloc_extra(self):
+        """Buffers a subclass adds before the gradient tables are built."""
+
+    def _extra_segments(self, G: int) -> list:
+        """Gradient segments (dst, src, count, part_stride, nparts) a subclass adds."""
+        return []
 
     @staticmethod
     def _can_fuse(program: Program) -> bool:
@@ -308,7 +353,7 @@ class MLPExecutor:
         lib = _lib.load()
         ha, hc = program.head_a, program.head_c
         if program.shared_head:
-            if not program.trunk:
+            if not program.trunk and program.gru is None:
                 return False
             na = program.head_out + 1
         else:
@@ -345,6 +390,7 @@ class MLPExecutor:
         if p.scale_region is not None:
             D = p.dist["dim"]
             segs.append((G + 4 * p.scale_region.offset, self.DSCALE.data_ptr(), D, D, self.loss_blocks))
+        segs += self._extra_segments(G)
         lib = _lib.load()
         assert lib.ppo_grad_reduce_segment_bytes() == 40 and lib.ppo_grad_reduce_chunk_bytes() == 16
         chunk = lib.ppo_grad_reduce_chunk_elems()
@@ -361,22 +407,40 @@ class MLPExecutor:
         self.segments = segs
 
     # ------------------------------------------------------------- pieces
-    def _fwd_layers(self, st, layers, x, ldx, rows_idx, nrows):
+    def _normalize(self, st):
+        """Advantage normalisation over the whole rollout (ppo.py:220-221)."""
+        if self.cfg.normalize_advantage:
+            self._call("ppo_normalize_advantages_f32", st, _p(self.ADV), self.B, _p(self.NORM_WS),
+                       self.NORM_WS.numel())
+
+    def _perm_size(self) -> int:
+        """Items one epoch permutes: every sample (ppo.py:200)."""
+        return self.B
+
+    def _boot_rows(self) -> int:
+        """Rows of the bootstrap forward: second.obs[-1] (ppo.py:208-212)."""
+        return self.N
+
+    def _fwd_layers(self, st, layers, x, ldx, rows_idx, nrows, row0=0):
+        """Forward of Dense[+LayerNorm][+act] layers on nrows rows, writing
+        each layer's buffers from row ``row0`` on."""
         for lb in layers:
             s = lb.spec
             d = s.dense
             W = self.flat.view(d.w)
             Bb = self.flat.view(d.b) if d.b is not None else None
+            o = 4 * row0 * s.ld
             if s.ln is not None:
-                self._call("ppo_gemm_f32", st, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(lb.Z), s.ld, nrows,
+                self._call("ppo_gemm_f32", st, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(lb.Z) + o, s.ld, nrows,
                           s.ld, d.fin, 1, 0, EPI_BIAS_ACT, Bb, 0, None, None, 0, None, -1)
-                self._call("ppo_layernorm_act_fwd_f32", st, _p(lb.Z), s.ld, self.flat.view(s.ln["scale"]),
-                          self.flat.view(s.ln["bias"]), _p(lb.Y), s.ld, _p(lb.mean), _p(lb.rstd), nrows, s.fout,
-                          s.ln["eps"], _act(s.act))
+                self._call("ppo_layernorm_act_fwd_f32", st, _p(lb.Z) + o, s.ld, self.flat.view(s.ln["scale"]),
+                          self.flat.view(s.ln["bias"]), _p(lb.Y) + o, s.ld, _p(lb.mean) + 4 * row0,
+                          _p(lb.rstd) + 4 * row0, nrows, s.fout, s.ln["eps"], _act(s.act))
             else:
-                self._call("ppo_gemm_f32", st, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(lb.Y), s.ld, nrows,
-                          s.ld, d.fin, 1, 0, EPI_BIAS_ACT, Bb, _act(s.act), _p(lb.PRE), None, 0, None, -1)
-            x, ldx, rows_idx = _p(lb.Y), s.ld, None
+                pre = _p(lb.PRE) + o if lb.PRE is not None else None
+                self._call("ppo_gemm_f32", st, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(lb.Y) + o, s.ld, nrows,
+                          s.ld, d.fin, 1, 0, EPI_BIAS_ACT, Bb, _act(s.act), pre, None, 0, None, -1)
+            x, ldx, rows_idx = _p(lb.Y) + o, s.ld, None
         return x, ldx, rows_idx
 
     def _dx_target(self, lb: LayerBufs):
@@ -453,8 +517,7 @@ class MLPExecutor:
         self._call("ppo_gae_f32", st, inp["reward"], inp["terminated"], inp["truncated"], inp["value"],
                   _p(self.BOOT), None, None, _p(self.ADV), _p(self.RET), T, N, float(cfg.gamma),
                   float(cfg.gae_lambda), 0)
-        if cfg.normalize_advantage:
-            raise NotImplementedError("normalize_advantage is not compiled yet")
+        self._normalize(st)
         # 3. epoch permutations of the flattened batch
         self._call("ppo_epoch_permutations", st, _p(self.KEY), self.E, B, _p(self.PERM), _p(self.PERM_WS),
                   self.PERM_WS.numel())
@@ -477,10 +540,16 @@ class MLPExecutor:
                           step)
         self._call("ppo_count_advance", st, _p(self.flat.count), self.E * self.M)
 
+    def _head_a_io(self, la: LayerBufs):
+        """(input, ld, cotangent destination, act, aux, ldaux) of head group a:
+        the last layer's output, and where its cotangent goes."""
+        da, epa, acta, auxa, ldauxa = self._dx_target(la)
+        return _p(la.Y), la.spec.ld, da, (acta if epa == EPI_DACT else 0), auxa, ldauxa
+
     def _fused_head_loss(self, st, idx, step, dist, A, scale_ptr, act_i, act_f):
         prog, cfg, inp, mb = self.prog, self.cfg, self.inp, self.mb
         if prog.shared_head:
-            la, lc = self.trunk[-1], None
+            la, lc = (self.trunk[-1] if self.trunk else None), None
             h = prog.head_a
             na = prog.head_out + 1
             wpa, bpa, wpc, bpc = self.HWPART, self.HBPART, None, None
@@ -489,8 +558,7 @@ class MLPExecutor:
             h = prog.head_a
             na = prog.head_out
             wpa, bpa, wpc, bpc = self.HAWPART, self.HABPART, self.HCWPART, self.HCBPART
-        da, epa, acta, auxa, ldauxa = self._dx_target(la)
-        acta = acta if epa == EPI_DACT else 0
+        ya, ldya, da, acta, auxa, ldauxa = self._head_a_io(la)
         if lc is not None:
             hc = prog.head_c
             dc, epc, actc, auxc, ldauxc = self._dx_target(lc)
@@ -500,9 +568,9 @@ class MLPExecutor:
         else:
             c_args = (None, 0, None, 0, None)
             cd_args = (0, None, 0, None, 0)
-        self._call("ppo_head_loss_f32", st, dist, mb, idx, _p(la.Y), la.spec.ld, self.flat.view(h.w), h.w.ld,
+        self._call("ppo_head_loss_f32", st, dist, mb, idx, ya, ldya, self.flat.view(h.w), h.w.ld,
                    self.flat.view(h.b), na, *c_args, h.fin, A, scale_ptr, act_i, act_f, inp["log_prob"],
-                   inp["value"], _p(self.ADV), _p(self.RET), acta, auxa, ldauxa, da, la.spec.ld, *cd_args,
+                   inp["value"], _p(self.ADV), _p(self.RET), acta, auxa, ldauxa, da, ldya, *cd_args,
                    _p(wpa), _p(bpa), _p(wpc), _p(bpc), _p(self.DSCALE), _p(self.STATS),
                    float(cfg.clip_coefficient), int(cfg.clip_value_loss), float(cfg.entropy_coefficient),
                    float(cfg.value_coefficient), 1.0)

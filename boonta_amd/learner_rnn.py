@@ -1,0 +1,210 @@
+"""The compiled learner step of RecurrentPPO (boonta/algorithms/recurrent_ppo.py:98-281).
+
+``RecurrentExecutor`` extends the MLP executor with the GRU torso of
+``Network(feature_extractor=<MLP>, torso=RNN(GRUCell(H)), head=ActorCritic(Dense, Dense))``.
+One update is this fixed launch sequence on one stream:
+
+    bootstrap (Transition.tail, transition.py:20-26; recurrent_ppo.py:188-198):
+        trunk on first.obs[-1] and second.obs[-1], input projections, two GRU
+        steps from carry[-1] with the resets first.done[-1] / second.done[-1],
+        value head
+    GAE                                              recurrent_ppo.py:199-205
+    E permutations of the N envs                     recurrent_ppo.py:269-279
+    sample rows of every sequence minibatch          (t * N + env, time-major)
+    per minibatch of B = N / M envs x T steps (recurrent_ppo.py:214-267):
+        trunk forward (rows gathered in the first GEMM), input projections of
+        all T * B rows in one GEMM, T GRU forward steps from carry[0][envs]
+        with the resets first.done, fused heads + loss + head backward, T GRU
+        backward steps, dWh / dWi / dX GEMMs, trunk backward, gradient
+        assembly, clip + Adam
+
+The minibatch keeps its rows time-major (row = t * B + b), so step t of the
+recurrence reads and writes one contiguous block; the loss is a mean over all
+rows, so the row order does not change it.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .learner import A_COL, A_ROW, B_KN, B_NK, EPI_BIAS_ACT, EPI_STORE, FlatState, MLPExecutor, Program, _p, _splits
+
+
+class RecurrentExecutor(MLPExecutor):
+    """One compiled RecurrentPPO.update for fixed (T, N, obs, minibatches, epochs)."""
+
+    def __init__(self, program: Program, flat: FlatState, cfg, chain, T: int, N: int):
+        if program.gru is None:
+            raise TypeError("RecurrentExecutor needs a program with a GRU torso")
+        if not program.shared_head:
+            raise NotImplementedError("the recurrent learner compiles plain Dense actor and critic heads")
+        super().__init__(program, flat, cfg, chain, T, N)
+        if not self.fused:
+            raise NotImplementedError("the recurrent learner needs the fused head + loss kernel "
+                                      "(head width <= 512, at most 15 actions)")
+
+    def _perm_size(self) -> int:
+        """RecurrentPPO permutes envs, not samples (recurrent_ppo.py:272)."""
+        return self.N
+
+    def _boot_rows(self) -> int:
+        """The tail sequence has two steps per env (transition.py:20-26)."""
+        return 2 * self.N
+
+    def _alloc_extra(self):
+        g = self.prog.gru
+        H, I = g.H, g.fin
+        dev = self.flat.device
+        f32 = dict(dtype=torch.float32, device=dev)
+        rows = self.mb
+        self.Bm = self.N // self.M
+        self.ROWS = torch.zeros(self.E * self.M, rows, dtype=torch.int32, device=dev)
+        self.XI = torch.zeros(rows, 3 * H, **f32)
+        self.HOUT = torch.zeros(rows, H, **f32)
+        self.HP = torch.zeros(rows, H, **f32)
+        self.GATES = torch.zeros(rows, 4 * H, **f32)
+        self.DHOUT = torch.zeros(rows, H, **f32)
+        self.DHS = torch.zeros(rows, H, **f32)
+        self.DGATE = torch.zeros(rows, 4 * H, **f32)
+        self.wh_splits = _splits(rows, H, 3 * H)
+        self.wi_splits = _splits(rows, I, 3 * H)
+        self.WHPART = torch.zeros(self.wh_splits, H, 3 * H, **f32)
+        self.WHBPART = torch.zeros(self.wh_splits, 3 * H, **f32)
+        self.WIPART = torch.zeros(self.wi_splits, I, 3 * H, **f32)
+        self.WIBPART = torch.zeros(self.wi_splits, 3 * H, **f32)
+        n2 = 2 * self.N
+        self.XIB = torch.zeros(n2, 3 * H, **f32)
+        self.HB = torch.zeros(n2, H, **f32)
+
+    def _extra_segments(self, G: int) -> list:
+        g = self.prog.gru
+        H, I = g.H, g.fin
+        return [
+            (G + 4 * g.wi.offset, _p(self.WIPART), I * 3 * H, I * 3 * H, self.wi_splits),
+            (G + 4 * g.bi.offset, _p(self.WIBPART), 3 * H, 3 * H, self.wi_splits),
+            (G + 4 * g.wh.offset, _p(self.WHPART), H * 3 * H, H * 3 * H, self.wh_splits),
+            # hn's bias gradient is the column sum of dhn, the last H columns
+            (G + 4 * g.bhn.offset, _p(self.WHBPART) + 4 * 2 * H, H, 3 * H, self.wh_splits),
+        ]
+
+    def _head_a_io(self, la):
+        """The heads read the GRU output directly (no activation between)."""
+        H = self.prog.gru.H
+        return _p(self.HOUT), H, _p(self.DHOUT), 0, None, 0
+
+    # ------------------------------------------------------------------ pieces
+    def _trunk_out(self):
+        """(pointer, ld) of the trunk's output rows (the GRU input)."""
+        if self.trunk:
+            lb = self.trunk[-1]
+            return _p(lb.Y), lb.spec.ld
+        return None, 0
+
+    def _gru_fwd(self, st, xi, hprev, hprev_rows, term, trunc, flag_rows, h_out, hp_out, gates, B):
+        g = self.prog.gru
+        H = g.H
+        self._call("ppo_gru_fwd_step_f32", st, xi, 3 * H, hprev, H, hprev_rows, term, trunc, flag_rows,
+                   self.flat.view(g.wh), 3 * H, self.flat.view(g.bhn), h_out, H, hp_out, H, gates, 4 * H, B, H)
+
+    def issue(self, st: int, max_steps: int | None = None):
+        inp, prog, cfg, chain = self.inp, self.prog, self.cfg, self.chain
+        g = prog.gru
+        H, I = g.H, g.fin
+        T, N, B, mb, Bm = self.T, self.N, self.B, self.mb, self.Bm
+        ldo = self.obs_dim
+        if not self.trunk:
+            raise NotImplementedError("the recurrent learner needs an MLP feature extractor before the GRU")
+        # 1. bootstrap: the two-step tail sequence from carry[-1]
+        last = 4 * (T - 1) * N
+        self._fwd_layers(st, self.boot_layers, inp["obs"] + last * ldo, ldo, None, N, row0=0)
+        self._fwd_layers(st, self.boot_layers, inp["next_obs_last"], ldo, None, N, row0=N)
+        eb = self.boot_layers[-1]
+        self._call("ppo_gemm_f32", st, A_ROW, B_KN, _p(eb.Y), eb.spec.ld, None, self.flat.view(g.wi), 3 * H,
+                   _p(self.XIB), 3 * H, 2 * N, 3 * H, I, 1, 0, EPI_BIAS_ACT, self.flat.view(g.bi), 0, None, None, 0,
+                   None, -1)
+        self._gru_fwd(st, _p(self.XIB), inp["carry_last"], None, inp["first_terminated"] + (T - 1) * N,
+                      inp["first_truncated"] + (T - 1) * N, None, _p(self.HB), None, None, N)
+        self._gru_fwd(st, _p(self.XIB) + 4 * N * 3 * H, _p(self.HB), None, inp["terminated"] + (T - 1) * N,
+                      inp["truncated"] + (T - 1) * N, None, _p(self.HB) + 4 * N * H, None, None, N)
+        h = prog.head_a
+        self._call("ppo_gemm_f32", st, A_ROW, B_KN, _p(self.HB) + 4 * N * H, H, None, self.flat.view(h.w), h.w.ld,
+                   _p(self.HEADB), h.w.ld, N, h.w.ld, h.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(h.b), 0, None, None,
+                   0, None, -1)
+        self._call("ppo_act_fwd_f32", st, _p(self.HEADB) + 4 * prog.head_out, self.HEADB.shape[1], _p(self.BOOT),
+                   1, N, 1, 0)
+        # 2. GAE
+        self._call("ppo_gae_f32", st, inp["reward"], inp["terminated"], inp["truncated"], inp["value"],
+                   _p(self.BOOT), None, None, _p(self.ADV), _p(self.RET), T, N, float(cfg.gamma),
+                   float(cfg.gae_lambda), 0)
+        self._normalize(st)
+        # 3. env permutations, and the sample rows of every minibatch
+        self._call("ppo_epoch_permutations", st, _p(self.KEY), self.E, N, _p(self.PERM), _p(self.PERM_WS),
+                   self.PERM_WS.numel())
+        self._call("ppo_sequence_rows", st, _p(self.PERM), self.E * self.M, T, N, Bm, _p(self.ROWS))
+        # 4. minibatch steps
+        adam = chain.adam
+        max_norm = chain.max_grad_norm if chain.max_grad_norm is not None else 0.0
+        for e in range(self.E):
+            for m in range(self.M):
+                step = e * self.M + m
+                if max_steps is not None and step >= max_steps:
+                    return
+                rows = _p(self.ROWS) + 4 * step * mb
+                envs = _p(self.PERM) + 4 * (e * N + m * Bm)
+                self._sequence_minibatch(st, rows, envs, step)
+                self._call("ppo_grad_reduce", st, _p(self.SEGS), _p(self.CHUNKS), self.nchunks, _p(self.SUMSQ))
+                self._call("ppo_adam_clip_f32", st, _p(self.flat.P), _p(self.flat.G), _p(self.flat.MU),
+                           _p(self.flat.NU), None, self.flat.P.numel(), _p(self.SUMSQ), self.nchunks,
+                           float(max_norm), adam.learning_rate, adam.b1, adam.b2, adam.eps, _p(self.flat.count),
+                           step)
+        self._call("ppo_count_advance", st, _p(self.flat.count), self.E * self.M)
+
+    def _sequence_minibatch(self, st, rows, envs, step):
+        inp, prog, cfg = self.inp, self.prog, self.cfg
+        g = prog.gru
+        H, I = g.H, g.fin
+        T, mb, Bm = self.T, self.mb, self.Bm
+        ldo = self.obs_dim
+        fterm, ftrunc = inp["first_terminated"], inp["first_truncated"]
+        # forward: trunk on the gathered rows, input projections of every step
+        self._fwd_layers(st, self.trunk, inp["obs"], ldo, rows, mb)
+        e_ptr, lde = self._trunk_out()
+        self._call("ppo_gemm_f32", st, A_ROW, B_KN, e_ptr, lde, None, self.flat.view(g.wi), 3 * H, _p(self.XI),
+                   3 * H, mb, 3 * H, I, 1, 0, EPI_BIAS_ACT, self.flat.view(g.bi), 0, None, None, 0, None, -1)
+        blk = Bm * H
+        for t in range(T):
+            if t == 0:
+                hprev, hrows = inp["carry0"], envs
+            else:
+                hprev, hrows = _p(self.HOUT) + 4 * (t - 1) * blk, None
+            self._gru_fwd(st, _p(self.XI) + 4 * t * Bm * 3 * H, hprev, hrows, fterm, ftrunc, rows + 4 * t * Bm,
+                          _p(self.HOUT) + 4 * t * blk, _p(self.HP) + 4 * t * blk,
+                          _p(self.GATES) + 4 * t * Bm * 4 * H, Bm)
+        # loss and the cotangent of every GRU output
+        dist = _lib.DIST[prog.dist["kind"]]
+        self._fused_head_loss(st, rows, step, dist, prog.action_dim, None, inp["action"], None)
+        # backward through time
+        wh = self.flat.view(g.wh)
+        G4 = 4 * H
+        s = T - 1
+        self._call("ppo_gru_bwd_step_f32", st, None, 0, None, 0, None, 0, None, 0, None, None, None,
+                   _p(self.DHOUT) + 4 * s * blk, H, _p(self.GATES) + 4 * s * Bm * G4, G4, _p(self.HP) + 4 * s * blk,
+                   H, _p(self.DHS) + 4 * s * blk, H, _p(self.DGATE) + 4 * s * Bm * G4, G4, Bm, H)
+        for t in range(T - 1, 0, -1):
+            s = t - 1
+            self._call("ppo_gru_bwd_step_f32", st, _p(self.DGATE) + 4 * (t * Bm * G4 + H), G4, wh, 3 * H,
+                       _p(self.DHS) + 4 * t * blk, H, _p(self.GATES) + 4 * (t * Bm * G4 + 2 * H), G4, fterm, ftrunc,
+                       rows + 4 * t * Bm, _p(self.DHOUT) + 4 * s * blk, H, _p(self.GATES) + 4 * s * Bm * G4, G4,
+                       _p(self.HP) + 4 * s * blk, H, _p(self.DHS) + 4 * s * blk, H,
+                       _p(self.DGATE) + 4 * s * Bm * G4, G4, Bm, H)
+        # recurrent and input kernels: dWh = HP^T [dar|daz|dhn], dWi = E^T [dan|dar|daz]
+        self._call("ppo_gemm_f32", st, A_COL, B_KN, _p(self.HP), H, None, _p(self.DGATE) + 4 * H, G4,
+                   _p(self.WHPART), 3 * H, H, 3 * H, mb, self.wh_splits, H * 3 * H, EPI_STORE, None, 0, None, None, 0,
+                   _p(self.WHBPART), -1)
+        self._call("ppo_gemm_f32", st, A_COL, B_KN, e_ptr, lde, None, _p(self.DGATE), G4, _p(self.WIPART), 3 * H,
+                   I, 3 * H, mb, self.wi_splits, I * 3 * H, EPI_STORE, None, 0, None, None, 0, _p(self.WIBPART), -1)
+        # cotangent of the trunk output: [dan|dar|daz] Wi^T, times the trunk's activation derivative
+        dst, epi, act, aux, ldaux = self._dx_target(self.trunk[-1])
+        self._call("ppo_gemm_f32", st, A_ROW, B_NK, _p(self.DGATE), G4, None, self.flat.view(g.wi), 3 * H, dst,
+                   self.trunk[-1].spec.ld, mb, I, 3 * H, 1, 0, epi, None, act, None, aux, ldaux, None, -1)
+        self._bwd_layers(st, self.trunk, inp["obs"], ldo, rows)

@@ -55,6 +55,12 @@ int ppo_gae_f32(void* stream, const float* reward, const uint8_t* terminated, co
                 float* advantages, float* returns, int T, int N, double gamma, double gae_lambda,
                 int chunks);
 
+/* Advantage normalisation (A - mean) / (std + 1e-8), population std over
+ * all n advantages, in place: boonta/algorithms/ppo.py:220-221 and
+ * recurrent_ppo.py:206-207 (PPOConfig.normalize_advantage). */
+size_t ppo_normalize_workspace(int64_t n);
+int ppo_normalize_advantages_f32(void* stream, float* adv, int64_t n, void* workspace, size_t workspace_bytes);
+
 /* ----------------------------------------------------------- permutation
  * Replace jax.random.split(key, E) and jax.random.permutation(key, n) at
  * boonta/algorithms/ppo.py:200,230 and recurrent_ppo.py:272,278 (jax 0.10.2,
@@ -144,6 +150,35 @@ int ppo_head_loss_f32(void* stream, int dist, int rows, const int32_t* idx, cons
                       int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a,
                       float* wpart_c, float* bpart_c, float* dscale_partial, double* stats_partial,
                       float clip_eps, int clip_value_loss, float ent_coef, float vf_coef, float temperature);
+
+/* ------------------------------------------------------------------- GRU
+ * One time step of flax.linen.GRUCell inside boonta's RNN block
+ * (boonta/networks/blocks/rnn.py:34-54, reset_carry :11-16), forward and
+ * backward, for a time-major batch of Bm sequences; replaces the nn.scan
+ * forward and its BPTT under jax.value_and_grad in
+ * boonta/algorithms/recurrent_ppo.py:101-184.  H must be a multiple of 64.
+ *   xi     [Bm, 3H] input projections x Wi + bi, columns (n | r | z)
+ *   wh     [H, 3H]  recurrent kernels, columns (r | z | n); bhn [H]
+ *   gates  [Bm, 4H] saved (n | r | z | hn); dgate [Bm, 4H] (dan | dar | daz | dhn)
+ * Forward: h_prev row b is hprev[(hprev_rows ? hprev_rows[b] : b) * ldh]; it
+ * is replaced by zeros where terminated[i] | truncated[i], i = flag_rows ?
+ * flag_rows[b] : b (flags may be NULL: no reset).  Writes h_out, and when
+ * non-NULL hp_out (the reset previous carry) and gates.
+ * Backward at step t (dg = dgate_t + H, or NULL for the first call at the
+ * last step): dh_s = dout_s + (reset_t ? 0 : dg Wh^T + dh_t * z_t), then the
+ * gate cotangents of step s = t - 1 into dgate_s. */
+int ppo_gru_fwd_step_f32(void* stream, const float* xi, int64_t ldxi, const float* hprev, int64_t ldh,
+                         const int32_t* hprev_rows, const uint8_t* terminated, const uint8_t* truncated,
+                         const int32_t* flag_rows, const float* wh, int64_t ldwh, const float* bhn, float* h_out,
+                         int64_t ldo, float* hp_out, int64_t ldhp, float* gates, int64_t ldg, int Bm, int H);
+int ppo_gru_bwd_step_f32(void* stream, const float* dg, int64_t lddg, const float* wh, int64_t ldwh,
+                         const float* dh_t, int64_t lddht, const float* z_t, int64_t ldz, const uint8_t* terminated,
+                         const uint8_t* truncated, const int32_t* flag_rows, const float* dout, int64_t lddo,
+                         const float* gates_s, int64_t ldg, const float* hp_s, int64_t ldhp, float* dh_s,
+                         int64_t lddhs, float* dgate_s, int64_t lddgs, int Bm, int H);
+/* Sample rows of S env-major sequence minibatches (recurrent_ppo.py:217-223):
+ * out[s * T * Bm + t * Bm + b] = t * N + envs[s * Bm + b]. */
+int ppo_sequence_rows(void* stream, const int32_t* envs, int S, int T, int N, int Bm, int32_t* out);
 
 /* ------------------------------------------------------------- optimizer
  * Replaces optax.chain(optax.clip_by_global_norm(max_norm), optax.adam(lr))

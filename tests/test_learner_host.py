@@ -8,9 +8,11 @@ import torch
 from boonta_amd import _lib, recipes
 from boonta_amd.flat import load_tree, tree_from_flat, tree_to_numpy
 from boonta_amd.learner import FlatState, MLPExecutor, Program
+from boonta_amd.learner_rnn import RecurrentExecutor
 from oracle import ppo as oppo
 
 MLP_CONFIGS = [1, 2, 3]
+FP32_CONFIGS = [1, 2, 3, 4]
 
 
 def small(config):
@@ -19,24 +21,37 @@ def small(config):
         return r.resized(T=16, N=64, num_minibatches=4, update_epochs=2)
     if config == 3:
         return r.resized(T=8, N=64, num_minibatches=4, update_epochs=2)
+    if config == 4:
+        return r.resized(T=8, N=64, num_minibatches=4, update_epochs=2)
     return r
+
+
+def executor(r, prog, flat):
+    cls = RecurrentExecutor if prog.gru is not None else MLPExecutor
+    return cls(prog, flat, r.cfg, r.optimizer, r.T, r.N)
 
 
 def fake_inputs(ex):
     return {k: 4096 * (i + 1) for i, k in enumerate(
-        ["obs", "next_obs_last", "action", "reward", "terminated", "truncated", "log_prob", "value"])}
+        ["obs", "next_obs_last", "action", "reward", "terminated", "truncated", "log_prob", "value",
+         "first_terminated", "first_truncated", "carry0", "carry_last"])}
 
 
-@pytest.mark.parametrize("config", MLP_CONFIGS)
+@pytest.mark.parametrize("config", FP32_CONFIGS)
 def test_recorded_launches_match_the_c_signatures(config):
     r = small(config)
     prog = Program(r.network.plan(r.obs_dim))
     flat = FlatState(prog, torch.device("cpu"))
-    ex = MLPExecutor(prog, flat, r.cfg, r.optimizer, r.T, r.N)
+    ex = executor(r, prog, flat)
     ex.bind(fake_inputs(ex))
     calls = ex.record()
     names = [n for n, _ in calls]
     steps = r.cfg.update_epochs * r.cfg.num_minibatches
+    if prog.gru is not None:
+        # two bootstrap steps, then T forward and T backward steps per minibatch
+        assert names.count("ppo_gru_fwd_step_f32") == 2 + steps * r.T
+        assert names.count("ppo_gru_bwd_step_f32") == steps * r.T
+        assert names.count("ppo_sequence_rows") == 1
     assert names.count("ppo_adam_clip_f32") == steps
     assert names.count("ppo_loss_finalize") == steps
     # every workload here has torso features in front of its heads: the fused kernel runs
@@ -61,7 +76,7 @@ def test_recorded_launches_match_the_c_signatures(config):
             assert all((ha, wa, ba, dha, wpa, bpa, stats))
 
 
-@pytest.mark.parametrize("config", MLP_CONFIGS)
+@pytest.mark.parametrize("config", FP32_CONFIGS)
 def test_flat_layout_round_trips_the_parameter_tree(config):
     r = recipes.make(config)
     prog = Program(r.network.plan(r.obs_dim))
