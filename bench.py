@@ -145,7 +145,7 @@ def launch_work(name, args):
     """(flops, bytes) of one launch: algorithmic work of the call's shapes
     (GEMM: 2MNK FLOP; bandwidth-bound kernels: the bytes the computation must
     read and write once)."""
-    if name == "ppo_gemm_f32":
+    if name in ("ppo_gemm_f32", "ppo_gemm_bf16"):
         M, N, K = args[10], args[11], args[12]
         return 2.0 * M * N * K, 4.0 * (M * K + K * N + M * N)
     if name == "ppo_gae_f32":
@@ -178,7 +178,7 @@ def launch_work(name, args):
 
 def launch_key(name, args):
     """Launches with the same entry point and shape do the same work."""
-    if name == "ppo_gemm_f32":
+    if name in ("ppo_gemm_f32", "ppo_gemm_bf16"):
         return (name, args[1], args[2]) + tuple(args[10:16])
     if name in ("ppo_gru_fwd_step_f32", "ppo_gru_bwd_step_f32"):
         return (name, args[-2], args[-1], bool(args[1]))
@@ -216,8 +216,8 @@ def time_launches(ex, reps, per_update_steps):
         ms = e0.elapsed_time(e1) / reps
         flops, nbytes = launch_work(name, args)
         row = {"i": i, "name": name, "ms": ms, "count": count, "flops": flops, "bytes": nbytes,
-               "shape": [a for a in args[10:13]] if name == "ppo_gemm_f32" else None,
-               "layout": [args[1], args[2]] if name == "ppo_gemm_f32" else None}
+               "shape": [a for a in args[10:13]] if name.startswith("ppo_gemm") else None,
+               "layout": [args[1], args[2]] if name.startswith("ppo_gemm") else None}
         if name.startswith("ppo_gru"):
             row["shape"] = [args[-2], args[-1]]
         rows.append(row)
@@ -349,7 +349,8 @@ def main():
     out = {
         "metric": "PPO learner samples/sec on 1 MI355X + % of HBM/MFMA roofline per kernel",
         "value": value, "unit": "samples/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16" if recipe.network.plan(recipe.obs_dim)["compute_dtype"] == "bfloat16" else "f32",
         "data": "synthetic (seeded rollout of the workload's distributions, random-init network)",
         "config": {"workload": f"config {args.config}: {recipe.name}", "T": recipe.T, "N": recipe.N,
                    "obs": recipe.obs_dim, "epochs": recipe.cfg.update_epochs,
@@ -363,8 +364,9 @@ def main():
         dom = max(rows, key=lambda r: r["ms"] * r["count"])
         if dom["flops"] > 0:
             achieved = dom["flops"] / (dom["ms"] * 1e-3) / 1e12
-            roof = {"bound": "mfma", "achieved": achieved, "peak": PEAK["fp32_mfma"], "unit": "TFLOP/s",
-                    "frac": achieved / PEAK["fp32_mfma"], "traffic": None}
+            peak = PEAK["bf16_mfma"] if dom["name"] == "ppo_gemm_bf16" else PEAK["fp32_mfma"]
+            roof = {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
+                    "frac": achieved / peak, "traffic": None}
         else:
             achieved = dom["bytes"] / (dom["ms"] * 1e-3) / 1e9
             roof = {"bound": "hbm", "achieved": achieved, "peak": PEAK["hbm"], "unit": "GB/s",

@@ -29,8 +29,10 @@ struct Segment {
   int64_t count;
   int64_t part_stride;
   int nparts;
-  int pad_;
+  int flags;  // SEG_ROUND_BF16: the summed gradient is rounded to bf16
 };
+
+constexpr int SEG_ROUND_BF16 = 1;
 
 struct Chunk {
   int seg;
@@ -73,6 +75,11 @@ grad_reduce_kernel(const Segment* __restrict__ segs, const Chunk* __restrict__ c
       floatx4 t = part[0][lane];
 #pragma unroll
       for (int w = 1; w < REDUCE_THREADS / 64; ++w) t += part[w][lane];
+      if (sg.flags & SEG_ROUND_BF16) {
+        // the gradient of a parameter cast to bf16 arrives as a bf16 cotangent
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] = ppo::bf16_round(t[e]);
+      }
       *reinterpret_cast<floatx4*>(sg.dst + i) = t;
 #pragma unroll
       for (int e = 0; e < 4; ++e) sq += (double)t[e] * (double)t[e];

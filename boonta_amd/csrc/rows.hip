@@ -26,7 +26,7 @@ template <int VPL>
 __global__ void __launch_bounds__(ROW_THREADS)
 ln_act_fwd_kernel(const float* __restrict__ z, int64_t ldz, const float* __restrict__ gamma,
                   const float* __restrict__ beta, float* __restrict__ y, int64_t ldy, float* __restrict__ mean_out,
-                  float* __restrict__ rstd_out, int rows, int F, float eps, int act) {
+                  float* __restrict__ rstd_out, int rows, int F, float eps, int act, int round) {
   const int lane = threadIdx.x & 63;
   const int wpb = ROW_THREADS / 64;
   for (int64_t r = (int64_t)blockIdx.x * wpb + (threadIdx.x >> 6); r < rows; r += (int64_t)gridDim.x * wpb) {
@@ -53,7 +53,18 @@ ln_act_fwd_kernel(const float* __restrict__ z, int64_t ldz, const float* __restr
 #pragma unroll
     for (int e = 0; e < VPL; ++e) {
       const int f = lane + 64 * e;
-      if (f < F) yr[f] = ppo::act_fwd(act, (v[e] - mean) * (rstd * gamma[f]) + beta[f]);
+      if (f < F) {
+        float o = (v[e] - mean) * (rstd * gamma[f]) + beta[f];
+        if (round) {
+          // flax casts the fp32 LayerNorm result back to the bf16 compute dtype
+          o = ppo::bf16_round(o);
+          o = ppo::act_fwd(act, o);
+          if (act != ACT_RELU && act != ACT_NONE) o = ppo::bf16_round(o);
+        } else {
+          o = ppo::act_fwd(act, o);
+        }
+        yr[f] = o;
+      }
     }
   }
 }
@@ -67,7 +78,7 @@ __global__ void __launch_bounds__(ROW_THREADS)
 ln_act_bwd_kernel(const float* __restrict__ dy, int64_t lddy, const float* __restrict__ z, int64_t ldz,
                   const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
                   const float* __restrict__ gamma, const float* __restrict__ beta, float* __restrict__ dz,
-                  int64_t lddz, float* __restrict__ partial, int rows, int F, int act) {
+                  int64_t lddz, float* __restrict__ partial, int rows, int F, int act, int round) {
   __shared__ float red[ROW_THREADS / 64][2][VPL * 64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -85,7 +96,8 @@ ln_act_bwd_kernel(const float* __restrict__ dy, int64_t lddy, const float* __res
       const int f = lane + 64 * e;
       if (f < F) {
         xh[e] = (z[r * ldz + f] - mean) * rstd;
-        const float yl = xh[e] * gamma[f] + beta[f];
+        float yl = xh[e] * gamma[f] + beta[f];
+        if (round) yl = ppo::bf16_round(yl);
         const float a = (act == ACT_RELU || act == ACT_TANH) ? ppo::act_fwd(act, yl) : yl;
         const float dyl = dy[r * lddy + f] * ppo::act_grad(act, a);
         acc_g[e] += dyl * xh[e];
@@ -103,7 +115,10 @@ ln_act_bwd_kernel(const float* __restrict__ dy, int64_t lddy, const float* __res
 #pragma unroll
     for (int e = 0; e < VPL; ++e) {
       const int f = lane + 64 * e;
-      if (f < F) dz[r * lddz + f] = rstd * (g[e] - sg - xh[e] * sgx);
+      if (f < F) {
+        const float d = rstd * (g[e] - sg - xh[e] * sgx);
+        dz[r * lddz + f] = round ? ppo::bf16_round(d) : d;
+      }
     }
   }
 #pragma unroll
@@ -401,37 +416,52 @@ loss_finalize_kernel(const double* __restrict__ partial, int nblocks, int rows, 
 
 template <int VPL>
 int launch_ln_fwd(hipStream_t st, int blocks, const float* z, int64_t ldz, const float* gamma, const float* beta,
-                  float* y, int64_t ldy, float* mean, float* rstd, int rows, int F, float eps, int act) {
+                  float* y, int64_t ldy, float* mean, float* rstd, int rows, int F, float eps, int act, int round) {
   hipLaunchKernelGGL((ln_act_fwd_kernel<VPL>), dim3(blocks), dim3(ROW_THREADS), 0, st, z, ldz, gamma, beta, y, ldy,
-                     mean, rstd, rows, F, eps, act);
+                     mean, rstd, rows, F, eps, act, round);
   return ppo::check_launch("ppo_layernorm_act_fwd_f32");
 }
 
 template <int VPL>
 int launch_ln_bwd(hipStream_t st, int blocks, const float* dy, int64_t lddy, const float* z, int64_t ldz,
                   const float* mean, const float* rstd, const float* gamma, const float* beta, float* dz,
-                  int64_t lddz, float* partial, int rows, int F, int act) {
+                  int64_t lddz, float* partial, int rows, int F, int act, int round) {
   hipLaunchKernelGGL((ln_act_bwd_kernel<VPL>), dim3(blocks), dim3(ROW_THREADS), 0, st, dy, lddy, z, ldz, mean, rstd,
-                     gamma, beta, dz, lddz, partial, rows, F, act);
+                     gamma, beta, dz, lddz, partial, rows, F, act, round);
   return ppo::check_launch("ppo_layernorm_act_bwd_f32");
 }
 
 }  // namespace
 
-PPO_EXPORT int ppo_layernorm_act_fwd_f32(void* stream, const float* z, int64_t ldz, const float* gamma,
-                                         const float* beta, float* y, int64_t ldy, float* mean, float* rstd,
-                                         int rows, int F, float eps, int act) {
+static int layernorm_fwd(const char* name, void* stream, const float* z, int64_t ldz, const float* gamma,
+                         const float* beta, float* y, int64_t ldy, float* mean, float* rstd, int rows, int F,
+                         float eps, int act, int round) {
   if (rows < 0 || F <= 0 || F > 64 * MAX_VPL || act < 0 || act > 3 || !z || !gamma || !beta || !y)
-    return ppo::set_error(PPO_ERR_ARG, "ppo_layernorm_act_fwd_f32: bad argument (rows=%d F=%d)", rows, F);
+    return ppo::set_error(PPO_ERR_ARG, "%s: bad argument (rows=%d F=%d)", name, rows, F);
   if (rows == 0) return PPO_OK;
   const int blocks = std::min(ppo::ceil_div(rows, ROW_THREADS / 64), 4096);
   hipStream_t st = ppo::as_stream(stream);
   const int vpl = ppo::ceil_div(F, 64);
-  if (vpl <= 1) return launch_ln_fwd<1>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act);
-  if (vpl <= 2) return launch_ln_fwd<2>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act);
-  if (vpl <= 4) return launch_ln_fwd<4>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act);
-  if (vpl <= 8) return launch_ln_fwd<8>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act);
-  return launch_ln_fwd<16>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act);
+  if (vpl <= 1) return launch_ln_fwd<1>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act, round);
+  if (vpl <= 2) return launch_ln_fwd<2>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act, round);
+  if (vpl <= 4) return launch_ln_fwd<4>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act, round);
+  if (vpl <= 8) return launch_ln_fwd<8>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act, round);
+  return launch_ln_fwd<16>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act, round);
+}
+
+PPO_EXPORT int ppo_layernorm_act_fwd_f32(void* stream, const float* z, int64_t ldz, const float* gamma,
+                                         const float* beta, float* y, int64_t ldy, float* mean, float* rstd,
+                                         int rows, int F, float eps, int act) {
+  return layernorm_fwd("ppo_layernorm_act_fwd_f32", stream, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps,
+                       act, 0);
+}
+
+// bf16 compute: statistics and normalisation in fp32, the result rounded to bf16.
+PPO_EXPORT int ppo_layernorm_act_fwd_bf16(void* stream, const float* z, int64_t ldz, const float* gamma,
+                                          const float* beta, float* y, int64_t ldy, float* mean, float* rstd,
+                                          int rows, int F, float eps, int act) {
+  return layernorm_fwd("ppo_layernorm_act_fwd_bf16", stream, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps,
+                       act, 1);
 }
 
 // Partials: [blocks][2F]; blocks = ppo_layernorm_bwd_blocks(rows).
@@ -439,21 +469,38 @@ PPO_EXPORT int ppo_layernorm_bwd_blocks(int rows) {
   return std::max(1, std::min(ppo::ceil_div(rows, 4 * (ROW_THREADS / 64)), 512));
 }
 
+static int layernorm_bwd(const char* name, void* stream, const float* dy, int64_t lddy, const float* z,
+                         int64_t ldz, const float* mean, const float* rstd, const float* gamma, const float* beta,
+                         float* dz, int64_t lddz, float* partial, int rows, int F, int act, int round) {
+  if (rows < 0 || F <= 0 || F > 64 * MAX_VPL || act < 0 || act > 3 || !dy || !z || !mean || !rstd || !gamma ||
+      !beta || !dz || !partial)
+    return ppo::set_error(PPO_ERR_ARG, "%s: bad argument (rows=%d F=%d)", name, rows, F);
+  const int blocks = ppo_layernorm_bwd_blocks(rows);
+  hipStream_t st = ppo::as_stream(stream);
+  const int vpl = ppo::ceil_div(F, 64);
+  if (vpl <= 1) return launch_ln_bwd<1>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round);
+  if (vpl <= 2) return launch_ln_bwd<2>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round);
+  if (vpl <= 4) return launch_ln_bwd<4>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round);
+  if (vpl <= 8) return launch_ln_bwd<8>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round);
+  return launch_ln_bwd<16>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round);
+}
+
 PPO_EXPORT int ppo_layernorm_act_bwd_f32(void* stream, const float* dy, int64_t lddy, const float* z, int64_t ldz,
                                          const float* mean, const float* rstd, const float* gamma,
                                          const float* beta, float* dz, int64_t lddz, float* partial, int rows,
                                          int F, int act) {
-  if (rows < 0 || F <= 0 || F > 64 * MAX_VPL || act < 0 || act > 3 || !dy || !z || !mean || !rstd || !gamma ||
-      !beta || !dz || !partial)
-    return ppo::set_error(PPO_ERR_ARG, "ppo_layernorm_act_bwd_f32: bad argument (rows=%d F=%d)", rows, F);
-  const int blocks = ppo_layernorm_bwd_blocks(rows);
-  hipStream_t st = ppo::as_stream(stream);
-  const int vpl = ppo::ceil_div(F, 64);
-  if (vpl <= 1) return launch_ln_bwd<1>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act);
-  if (vpl <= 2) return launch_ln_bwd<2>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act);
-  if (vpl <= 4) return launch_ln_bwd<4>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act);
-  if (vpl <= 8) return launch_ln_bwd<8>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act);
-  return launch_ln_bwd<16>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act);
+  return layernorm_bwd("ppo_layernorm_act_bwd_f32", stream, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz,
+                       partial, rows, F, act, 0);
+}
+
+// bf16 compute: the LayerNorm output was rounded to bf16 before the activation,
+// and the input cotangent is rounded to bf16 (the cast's transpose).
+PPO_EXPORT int ppo_layernorm_act_bwd_bf16(void* stream, const float* dy, int64_t lddy, const float* z, int64_t ldz,
+                                          const float* mean, const float* rstd, const float* gamma,
+                                          const float* beta, float* dz, int64_t lddz, float* partial, int rows,
+                                          int F, int act) {
+  return layernorm_bwd("ppo_layernorm_act_bwd_bf16", stream, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz,
+                       partial, rows, F, act, 1);
 }
 
 PPO_EXPORT int ppo_act_fwd_f32(void* stream, const float* x, int64_t ldx, float* y, int64_t ldy, int rows, int F,

@@ -93,8 +93,11 @@ class Program:
     """Flat layout + tower structure of an MLP actor-critic plan."""
 
     def __init__(self, plan: dict):
-        if plan["compute_dtype"] != "float32":
-            raise NotImplementedError("bf16 compute is not compiled yet")
+        if plan["compute_dtype"] not in ("float32", "bfloat16"):
+            raise NotImplementedError(f"compute dtype {plan['compute_dtype']} is not compiled")
+        self.bf16 = plan["compute_dtype"] == "bfloat16"
+        if self.bf16 and plan.get("torso") is not None:
+            raise NotImplementedError("a bf16 recurrent torso is not compiled")
         self.plan = plan
         L = FlatLayout()
         self.layout = L
@@ -243,6 +246,9 @@ class MLPExecutor:
             raise TypeError("a recurrent program runs on RecurrentExecutor")
         self._call = _lib.call
         self.prog = program
+        self.bf16 = program.bf16
+        self._ln_fwd = "ppo_layernorm_act_fwd_bf16" if self.bf16 else "ppo_layernorm_act_fwd_f32"
+        self._ln_bwd = "ppo_layernorm_act_bwd_bf16" if self.bf16 else "ppo_layernorm_act_bwd_f32"
         self.flat = flat
         self.cfg = cfg
         self.chain = chain
@@ -342,7 +348,7 @@ class MLPExecutor:
         """Buffers a subclass adds before the gradient tables are built."""
 
     def _extra_segments(self, G: int) -> list:
-        """Gradient segments (dst, src, count, part_stride, nparts) a subclass adds."""
+        """Gradient segments (dst, src, count, part_stride, nparts, flags) a subclass adds."""
         return []
 
     @staticmethod
@@ -352,6 +358,8 @@ class MLPExecutor:
         head has at most 16 outputs (plus the value column when shared)."""
         lib = _lib.load()
         ha, hc = program.head_a, program.head_c
+        if program.bf16:
+            return False
         if program.shared_head:
             if not program.trunk and program.gru is None:
                 return False
@@ -368,19 +376,21 @@ class MLPExecutor:
         G = flat.G.data_ptr()
         segs = []  # (dst, src, count, part_stride, nparts)
 
+        rb = 1 if self.bf16 else 0   # a bf16 Dense's kernel and bias gradients are bf16 values
+
         def dense_segs(spec: DenseSpec, wpart, bpart, splits):
             n = spec.fin * spec.w.ld
-            segs.append((G + 4 * spec.w.offset, wpart.data_ptr(), n, n, splits))
+            segs.append((G + 4 * spec.w.offset, wpart.data_ptr(), n, n, splits, rb))
             if spec.b is not None:
-                segs.append((G + 4 * spec.b.offset, bpart.data_ptr(), spec.w.ld, spec.w.ld, splits))
+                segs.append((G + 4 * spec.b.offset, bpart.data_ptr(), spec.w.ld, spec.w.ld, splits, rb))
 
         for lb in self.trunk + self.actor + self.critic:
             dense_segs(lb.spec.dense, lb.wpart, lb.bpart, lb.splits)
             if lb.spec.ln is not None:
                 F = lb.spec.fout
-                segs.append((G + 4 * lb.spec.ln["scale"].offset, lb.lnpart.data_ptr(), F, 2 * F, lb.lnblocks))
+                segs.append((G + 4 * lb.spec.ln["scale"].offset, lb.lnpart.data_ptr(), F, 2 * F, lb.lnblocks, 0))
                 segs.append((G + 4 * lb.spec.ln["bias"].offset, lb.lnpart.data_ptr() + 4 * F, F, 2 * F,
-                             lb.lnblocks))
+                             lb.lnblocks, 0))
         p = self.prog
         if p.shared_head:
             dense_segs(p.head_a, self.HWPART, self.HBPART, self.head_splits)
@@ -389,14 +399,14 @@ class MLPExecutor:
             dense_segs(p.head_c, self.HCWPART, self.HCBPART, self.hc_splits)
         if p.scale_region is not None:
             D = p.dist["dim"]
-            segs.append((G + 4 * p.scale_region.offset, self.DSCALE.data_ptr(), D, D, self.loss_blocks))
+            segs.append((G + 4 * p.scale_region.offset, self.DSCALE.data_ptr(), D, D, self.loss_blocks, 0))
         segs += self._extra_segments(G)
         lib = _lib.load()
         assert lib.ppo_grad_reduce_segment_bytes() == 40 and lib.ppo_grad_reduce_chunk_bytes() == 16
         chunk = lib.ppo_grad_reduce_chunk_elems()
-        seg_bytes = b"".join(struct.pack("<QQqqii", d, s, c, st, n, 0) for d, s, c, st, n in segs)
+        seg_bytes = b"".join(struct.pack("<QQqqii", d, s, c, st, n, f) for d, s, c, st, n, f in segs)
         chunks = []
-        for i, (_, _, c, _, _) in enumerate(segs):
+        for i, (_, _, c, _, _, _) in enumerate(segs):
             for start in range(0, c, chunk):
                 chunks.append(struct.pack("<iiq", i, 0, start))
         dev = flat.device
@@ -407,6 +417,22 @@ class MLPExecutor:
         self.segments = segs
 
     # ------------------------------------------------------------- pieces
+    def _gemm(self, st, a_layout, b_layout, A, lda, rows, B, ldb, C, ldc, M, N, K, splits, stride, epi, bias, act,
+              pre, aux, ldaux, bias_grad, tile):
+        """One Dense contraction: fp32 MFMA, or for a bf16-compute network the
+        bf16 MFMA GEMM with flax's casts (operands rounded to bf16 as read; the
+        forward and input-cotangent results rounded to bf16; dW partials kept
+        fp32 and rounded after their sum)."""
+        if not self.bf16:
+            self._call("ppo_gemm_f32", st, a_layout, b_layout, A, lda, rows, B, ldb, C, ldc, M, N, K, splits, stride,
+                       epi, bias, act, pre, aux, ldaux, bias_grad, tile)
+            return
+        if pre is not None:
+            raise NotImplementedError("a bf16 Dense with a SiLU activation and no LayerNorm is not compiled")
+        round_out = 0 if a_layout == A_COL else 1
+        self._call("ppo_gemm_bf16", st, a_layout, b_layout, A, lda, rows, B, ldb, C, ldc, M, N, K, splits, stride, epi,
+                   bias, act, round_out, aux, ldaux, bias_grad, tile)
+
     def _normalize(self, st):
         """Advantage normalisation over the whole rollout (ppo.py:220-221)."""
         if self.cfg.normalize_advantage:
@@ -431,14 +457,14 @@ class MLPExecutor:
             Bb = self.flat.view(d.b) if d.b is not None else None
             o = 4 * row0 * s.ld
             if s.ln is not None:
-                self._call("ppo_gemm_f32", st, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(lb.Z) + o, s.ld, nrows,
+                self._gemm(st, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(lb.Z) + o, s.ld, nrows,
                           s.ld, d.fin, 1, 0, EPI_BIAS_ACT, Bb, 0, None, None, 0, None, -1)
-                self._call("ppo_layernorm_act_fwd_f32", st, _p(lb.Z) + o, s.ld, self.flat.view(s.ln["scale"]),
+                self._call(self._ln_fwd, st, _p(lb.Z) + o, s.ld, self.flat.view(s.ln["scale"]),
                           self.flat.view(s.ln["bias"]), _p(lb.Y) + o, s.ld, _p(lb.mean) + 4 * row0,
                           _p(lb.rstd) + 4 * row0, nrows, s.fout, s.ln["eps"], _act(s.act))
             else:
                 pre = _p(lb.PRE) + o if lb.PRE is not None else None
-                self._call("ppo_gemm_f32", st, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(lb.Y) + o, s.ld, nrows,
+                self._gemm(st, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(lb.Y) + o, s.ld, nrows,
                           s.ld, d.fin, 1, 0, EPI_BIAS_ACT, Bb, _act(s.act), pre, None, 0, None, -1)
             x, ldx, rows_idx = _p(lb.Y) + o, s.ld, None
         return x, ldx, rows_idx
@@ -460,29 +486,29 @@ class MLPExecutor:
             s = lb.spec
             d = s.dense
             if s.ln is not None:
-                self._call("ppo_layernorm_act_bwd_f32", st, _p(lb.dY), s.ld, _p(lb.Z), s.ld, _p(lb.mean),
+                self._call(self._ln_bwd, st, _p(lb.dY), s.ld, _p(lb.Z), s.ld, _p(lb.mean),
                           _p(lb.rstd), self.flat.view(s.ln["scale"]), self.flat.view(s.ln["bias"]), _p(lb.dZ),
                           s.ld, _p(lb.lnpart), self.mb, s.fout, _act(s.act))
             if i > 0:
                 x, ldx, ridx = _p(layers[i - 1].Y), layers[i - 1].spec.ld, None
             else:
                 x, ldx, ridx = x0, ldx0, idx0
-            self._call("ppo_gemm_f32", st, A_COL, B_KN, x, ldx, ridx, _p(lb.dZ), s.ld, _p(lb.wpart), s.ld, d.fin,
+            self._gemm(st, A_COL, B_KN, x, ldx, ridx, _p(lb.dZ), s.ld, _p(lb.wpart), s.ld, d.fin,
                       s.ld, self.mb, lb.splits, d.fin * s.ld, EPI_STORE, None, 0, None, None, 0, _p(lb.bpart), -1)
             if i > 0:
                 dst, epi, act, aux, ldaux = self._dx_target(layers[i - 1])
-                self._call("ppo_gemm_f32", st, A_ROW, B_NK, _p(lb.dZ), s.ld, None, self.flat.view(d.w), d.w.ld,
+                self._gemm(st, A_ROW, B_NK, _p(lb.dZ), s.ld, None, self.flat.view(d.w), d.w.ld,
                           dst, layers[i - 1].spec.ld, self.mb, d.fin, s.ld, 1, 0, epi, None, act, None, aux, ldaux,
                           None, -1)
 
     def _head_back(self, st, layers, dhead, head: DenseSpec, wpart, bpart, splits, hx, ldhx, hidx):
         """Head dW and the cotangent of the head input."""
-        self._call("ppo_gemm_f32", st, A_COL, B_KN, hx, ldhx, hidx, _p(dhead), head.w.ld, _p(wpart), head.w.ld,
+        self._gemm(st, A_COL, B_KN, hx, ldhx, hidx, _p(dhead), head.w.ld, _p(wpart), head.w.ld,
                   head.fin, head.w.ld, self.mb, splits, head.fin * head.w.ld, EPI_STORE, None, 0, None, None, 0,
                   _p(bpart), -1)
         if layers:
             dst, epi, act, aux, ldaux = self._dx_target(layers[-1])
-            self._call("ppo_gemm_f32", st, A_ROW, B_NK, _p(dhead), head.w.ld, None, self.flat.view(head.w),
+            self._gemm(st, A_ROW, B_NK, _p(dhead), head.w.ld, None, self.flat.view(head.w),
                       head.w.ld, dst, layers[-1].spec.ld, self.mb, head.fin, head.w.ld, 1, 0, epi, None, act, None,
                       aux, ldaux, None, -1)
 
@@ -503,13 +529,13 @@ class MLPExecutor:
         if prog.shared_head:
             x, ldx, _ = self._fwd_layers(st, self.boot_layers, x, ldx, None, N)
             h = prog.head_a
-            self._call("ppo_gemm_f32", st, A_ROW, B_KN, x, ldx, None, self.flat.view(h.w), h.w.ld, _p(self.HEADB),
+            self._gemm(st, A_ROW, B_KN, x, ldx, None, self.flat.view(h.w), h.w.ld, _p(self.HEADB),
                       h.w.ld, N, h.w.ld, h.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(h.b), 0, None, None, 0, None, -1)
             vcol = prog.head_out
         else:
             x, ldx, _ = self._fwd_layers(st, self.boot_layers, x, ldx, None, N)
             h = prog.head_c
-            self._call("ppo_gemm_f32", st, A_ROW, B_KN, x, ldx, None, self.flat.view(h.w), h.w.ld, _p(self.HEADB),
+            self._gemm(st, A_ROW, B_KN, x, ldx, None, self.flat.view(h.w), h.w.ld, _p(self.HEADB),
                       h.w.ld, N, h.w.ld, h.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(h.b), 0, None, None, 0, None, -1)
             vcol = 0
         self._call("ppo_act_fwd_f32", st, _p(self.HEADB) + 4 * vcol, self.HEADB.shape[1], _p(self.BOOT), 1, N, 1, 0)
@@ -598,7 +624,7 @@ class MLPExecutor:
         if prog.shared_head:
             hx, ldhx, hidx = self._fwd_layers(st, self.trunk, obs, ldo, idx, mb)
             h = prog.head_a
-            self._call("ppo_gemm_f32", st, A_ROW, B_KN, hx, ldhx, hidx, self.flat.view(h.w), h.w.ld, _p(self.HEAD),
+            self._gemm(st, A_ROW, B_KN, hx, ldhx, hidx, self.flat.view(h.w), h.w.ld, _p(self.HEAD),
                       h.w.ld, mb, h.w.ld, h.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(h.b), 0, None, None, 0, None,
                       -1)
             vcol = prog.head_out
@@ -615,10 +641,10 @@ class MLPExecutor:
             ax, ldax, aidx = self._fwd_layers(st, self.actor, obs, ldo, idx, mb)
             cx, ldcx, cidx = self._fwd_layers(st, self.critic, obs, ldo, idx, mb)
             ha, hc = prog.head_a, prog.head_c
-            self._call("ppo_gemm_f32", st, A_ROW, B_KN, ax, ldax, aidx, self.flat.view(ha.w), ha.w.ld, _p(self.HA),
+            self._gemm(st, A_ROW, B_KN, ax, ldax, aidx, self.flat.view(ha.w), ha.w.ld, _p(self.HA),
                       ha.w.ld, mb, ha.w.ld, ha.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(ha.b), 0, None, None, 0,
                       None, -1)
-            self._call("ppo_gemm_f32", st, A_ROW, B_KN, cx, ldcx, cidx, self.flat.view(hc.w), hc.w.ld, _p(self.HC),
+            self._gemm(st, A_ROW, B_KN, cx, ldcx, cidx, self.flat.view(hc.w), hc.w.ld, _p(self.HC),
                       hc.w.ld, mb, hc.w.ld, hc.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(hc.b), 0, None, None, 0,
                       None, -1)
             self._call("ppo_loss_f32", st, dist, mb, idx, _p(self.HA), ha.w.ld, _p(self.HC), hc.w.ld, A, scale_ptr,

@@ -80,11 +80,11 @@ class RecurrentExecutor(MLPExecutor):
         g = self.prog.gru
         H, I = g.H, g.fin
         return [
-            (G + 4 * g.wi.offset, _p(self.WIPART), I * 3 * H, I * 3 * H, self.wi_splits),
-            (G + 4 * g.bi.offset, _p(self.WIBPART), 3 * H, 3 * H, self.wi_splits),
-            (G + 4 * g.wh.offset, _p(self.WHPART), H * 3 * H, H * 3 * H, self.wh_splits),
+            (G + 4 * g.wi.offset, _p(self.WIPART), I * 3 * H, I * 3 * H, self.wi_splits, 0),
+            (G + 4 * g.bi.offset, _p(self.WIBPART), 3 * H, 3 * H, self.wi_splits, 0),
+            (G + 4 * g.wh.offset, _p(self.WHPART), H * 3 * H, H * 3 * H, self.wh_splits, 0),
             # hn's bias gradient is the column sum of dhn, the last H columns
-            (G + 4 * g.bhn.offset, _p(self.WHBPART) + 4 * 2 * H, H, 3 * H, self.wh_splits),
+            (G + 4 * g.bhn.offset, _p(self.WHBPART) + 4 * 2 * H, H, 3 * H, self.wh_splits, 0),
         ]
 
     def _head_a_io(self, la):
@@ -119,7 +119,7 @@ class RecurrentExecutor(MLPExecutor):
         self._fwd_layers(st, self.boot_layers, inp["obs"] + last * ldo, ldo, None, N, row0=0)
         self._fwd_layers(st, self.boot_layers, inp["next_obs_last"], ldo, None, N, row0=N)
         eb = self.boot_layers[-1]
-        self._call("ppo_gemm_f32", st, A_ROW, B_KN, _p(eb.Y), eb.spec.ld, None, self.flat.view(g.wi), 3 * H,
+        self._gemm(st, A_ROW, B_KN, _p(eb.Y), eb.spec.ld, None, self.flat.view(g.wi), 3 * H,
                    _p(self.XIB), 3 * H, 2 * N, 3 * H, I, 1, 0, EPI_BIAS_ACT, self.flat.view(g.bi), 0, None, None, 0,
                    None, -1)
         self._gru_fwd(st, _p(self.XIB), inp["carry_last"], None, inp["first_terminated"] + (T - 1) * N,
@@ -127,7 +127,7 @@ class RecurrentExecutor(MLPExecutor):
         self._gru_fwd(st, _p(self.XIB) + 4 * N * 3 * H, _p(self.HB), None, inp["terminated"] + (T - 1) * N,
                       inp["truncated"] + (T - 1) * N, None, _p(self.HB) + 4 * N * H, None, None, N)
         h = prog.head_a
-        self._call("ppo_gemm_f32", st, A_ROW, B_KN, _p(self.HB) + 4 * N * H, H, None, self.flat.view(h.w), h.w.ld,
+        self._gemm(st, A_ROW, B_KN, _p(self.HB) + 4 * N * H, H, None, self.flat.view(h.w), h.w.ld,
                    _p(self.HEADB), h.w.ld, N, h.w.ld, h.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(h.b), 0, None, None,
                    0, None, -1)
         self._call("ppo_act_fwd_f32", st, _p(self.HEADB) + 4 * prog.head_out, self.HEADB.shape[1], _p(self.BOOT),
@@ -169,7 +169,7 @@ class RecurrentExecutor(MLPExecutor):
         # forward: trunk on the gathered rows, input projections of every step
         self._fwd_layers(st, self.trunk, inp["obs"], ldo, rows, mb)
         e_ptr, lde = self._trunk_out()
-        self._call("ppo_gemm_f32", st, A_ROW, B_KN, e_ptr, lde, None, self.flat.view(g.wi), 3 * H, _p(self.XI),
+        self._gemm(st, A_ROW, B_KN, e_ptr, lde, None, self.flat.view(g.wi), 3 * H, _p(self.XI),
                    3 * H, mb, 3 * H, I, 1, 0, EPI_BIAS_ACT, self.flat.view(g.bi), 0, None, None, 0, None, -1)
         blk = Bm * H
         for t in range(T):
@@ -198,13 +198,13 @@ class RecurrentExecutor(MLPExecutor):
                        _p(self.HP) + 4 * s * blk, H, _p(self.DHS) + 4 * s * blk, H,
                        _p(self.DGATE) + 4 * s * Bm * G4, G4, Bm, H)
         # recurrent and input kernels: dWh = HP^T [dar|daz|dhn], dWi = E^T [dan|dar|daz]
-        self._call("ppo_gemm_f32", st, A_COL, B_KN, _p(self.HP), H, None, _p(self.DGATE) + 4 * H, G4,
+        self._gemm(st, A_COL, B_KN, _p(self.HP), H, None, _p(self.DGATE) + 4 * H, G4,
                    _p(self.WHPART), 3 * H, H, 3 * H, mb, self.wh_splits, H * 3 * H, EPI_STORE, None, 0, None, None, 0,
                    _p(self.WHBPART), -1)
-        self._call("ppo_gemm_f32", st, A_COL, B_KN, e_ptr, lde, None, _p(self.DGATE), G4, _p(self.WIPART), 3 * H,
+        self._gemm(st, A_COL, B_KN, e_ptr, lde, None, _p(self.DGATE), G4, _p(self.WIPART), 3 * H,
                    I, 3 * H, mb, self.wi_splits, I * 3 * H, EPI_STORE, None, 0, None, None, 0, _p(self.WIBPART), -1)
         # cotangent of the trunk output: [dan|dar|daz] Wi^T, times the trunk's activation derivative
         dst, epi, act, aux, ldaux = self._dx_target(self.trunk[-1])
-        self._call("ppo_gemm_f32", st, A_ROW, B_NK, _p(self.DGATE), G4, None, self.flat.view(g.wi), 3 * H, dst,
+        self._gemm(st, A_ROW, B_NK, _p(self.DGATE), G4, None, self.flat.view(g.wi), 3 * H, dst,
                    self.trunk[-1].spec.ld, mb, I, 3 * H, 1, 0, epi, None, act, None, aux, ldaux, None, -1)
         self._bwd_layers(st, self.trunk, inp["obs"], ldo, rows)

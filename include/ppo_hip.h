@@ -93,6 +93,22 @@ int ppo_gemm_f32(void* stream, int a_layout, int b_layout, const float* A, int64
                  int64_t c_split_stride, int epi, const float* bias, int act, float* pre, const float* aux,
                  int64_t ldaux, float* bias_grad, int tile);
 
+/* bf16 compute (flax Dense with dtype=bfloat16, param_dtype=float32; the
+ * mixed precision of boonta/networks/README.md:73-77): the same contraction
+ * and layouts as ppo_gemm_f32 on v_mfma_f32_32x32x16_bf16 with fp32
+ * accumulation.  Operands stay fp32 in memory and are rounded to bf16 (round
+ * to nearest even) as they are read: the casts of the input, the kernel and
+ * any fp32 cotangent.  round_out != 0 rounds the result to bf16 (and with
+ * epi 1 adds the bf16-rounded bias and rounds again, then the activation);
+ * round_out = 0 keeps fp32 (dW partials, rounded after their sum by
+ * ppo_grad_reduce). */
+int ppo_gemm_bf16(void* stream, int a_layout, int b_layout, const float* A, int64_t lda, const int32_t* rows,
+                  const float* B, int64_t ldb, float* C, int64_t ldc, int M, int N, int K, int splits,
+                  int64_t c_split_stride, int epi, const float* bias, int act, int round_out, const float* aux,
+                  int64_t ldaux, float* bias_grad, int tile);
+/* x[i] <- bf16(x[i]) in place (the fp32 value of the nearest-even bf16). */
+int ppo_round_bf16(void* stream, float* x, int64_t n);
+
 /* ------------------------------------------------------ LayerNorm / act
  * flax.linen.LayerNorm (epsilon, fast variance, scale and bias) followed by
  * an activation, as the Dense -> LayerNorm -> act blocks of the configs.
@@ -106,6 +122,15 @@ int ppo_layernorm_bwd_blocks(int rows);
 int ppo_layernorm_act_bwd_f32(void* stream, const float* dy, int64_t lddy, const float* z, int64_t ldz,
                               const float* mean, const float* rstd, const float* gamma, const float* beta,
                               float* dz, int64_t lddz, float* partial, int rows, int F, int act);
+/* bf16 compute: flax's LayerNorm with dtype=bfloat16 computes statistics and
+ * the normalisation in fp32 and casts the result to bf16 before the
+ * activation; the backward rounds the input cotangent to bf16. */
+int ppo_layernorm_act_fwd_bf16(void* stream, const float* z, int64_t ldz, const float* gamma, const float* beta,
+                               float* y, int64_t ldy, float* mean, float* rstd, int rows, int F, float eps,
+                               int act);
+int ppo_layernorm_act_bwd_bf16(void* stream, const float* dy, int64_t lddy, const float* z, int64_t ldz,
+                               const float* mean, const float* rstd, const float* gamma, const float* beta,
+                               float* dz, int64_t lddz, float* partial, int rows, int F, int act);
 int ppo_act_fwd_f32(void* stream, const float* x, int64_t ldx, float* y, int64_t ldy, int rows, int F, int act);
 int ppo_act_bwd_f32(void* stream, const float* dy, int64_t lddy, const float* aux, int64_t ldaux, float* dx,
                     int64_t lddx, int rows, int F, int act);
@@ -187,6 +212,11 @@ int ppo_sequence_rows(void* stream, const int32_t* envs, int S, int T, int N, in
  * ppo_grad_reduce sums the partials of every gradient leaf into the flat
  * gradient (device tables of segments and chunks) and leaves one sum of
  * squares per chunk; ppo_adam_clip_f32 folds them into the global norm.
+ * A segment is {float* dst; const float* src; int64 count; int64
+ * part_stride; int32 nparts; int32 flags} (flags bit 0: round the summed
+ * gradient to bf16, for parameters a bf16-compute layer casts); a chunk is
+ * {int32 segment; int32 pad; int64 start} covering
+ * ppo_grad_reduce_chunk_elems() elements.
  * The optax count is count_base[0] + step_offset + 1 (device int32). */
 int ppo_grad_reduce_segment_bytes(void);
 int ppo_grad_reduce_chunk_bytes(void);

@@ -80,18 +80,39 @@ def act_bwd(fn, x, y, dy):
     raise ValueError(fn)
 
 
+# ----------------------------------------------------------------- bf16 casts
+def bf16(x):
+    """Round to the nearest-even bfloat16 value, via float32 (XLA rounds its
+    fp32 results to bf16), returned as float64."""
+    a = np.ascontiguousarray(np.asarray(x, F64).astype(np.float32))
+    u = a.view(np.uint32).astype(np.uint64)
+    u = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return (u & 0xFFFFFFFF).astype(np.uint32).view(np.float32).astype(F64)
+
+
+def _cast(x, dtype):
+    return bf16(x) if dtype == "bfloat16" else x
+
+
 # ---------------------------------------------------------------- stage lists
-def stages_forward(params, stages, x):
-    """Runs a stage list on x [rows, features]; returns (y, caches)."""
+def stages_forward(params, stages, x, dtype="float32"):
+    """Runs a stage list on x [rows, features]; returns (y, caches).
+
+    With dtype "bfloat16" the flax mixed-precision casts are applied
+    (boonta/networks/README.md:73-77): a Dense casts its input, kernel and bias
+    to bf16, its dot returns bf16 (fp32 accumulation) and the bias add is a
+    bf16 add; LayerNorm computes in fp32 and returns bf16; activations run on
+    bf16 values."""
     caches = []
     for st in stages:
         op = st["op"]
         if op == "dense":
             p = get(params, st["path"])
-            w = np.asarray(p["kernel"], F64)
-            y = x @ w
+            x = _cast(x, dtype)
+            w = _cast(np.asarray(p["kernel"], F64), dtype)
+            y = _cast(x @ w, dtype)
             if st.get("bias", True):
-                y = y + np.asarray(p["bias"], F64)
+                y = _cast(y + _cast(np.asarray(p["bias"], F64), dtype), dtype)
             caches.append(x)
             x = y
         elif op == "layernorm":
@@ -101,9 +122,11 @@ def stages_forward(params, stages, x):
             rstd = 1.0 / np.sqrt(var + st.get("eps", 1e-6))
             xhat = (x - mean) * rstd
             caches.append((xhat, rstd))
-            x = xhat * np.asarray(p["scale"], F64) + np.asarray(p["bias"], F64)
+            x = _cast(xhat * np.asarray(p["scale"], F64) + np.asarray(p["bias"], F64), dtype)
         elif op == "act":
             y = act_fwd(st["fn"], x)
+            if st["fn"] != "relu":
+                y = _cast(y, dtype)
             caches.append((x, y))
             x = y
         else:
@@ -111,32 +134,40 @@ def stages_forward(params, stages, x):
     return x, caches
 
 
-def stages_backward(params, stages, caches, dy, grads, need_dx=True):
+def stages_backward(params, stages, caches, dy, grads, need_dx=True, dtype="float32"):
     """Back-propagates dy through a stage list, adding parameter gradients
-    into ``grads`` (same nesting as params).  Returns dx (or None)."""
+    into ``grads`` (same nesting as params).  Returns dx (or None).
+
+    With dtype "bfloat16", every cotangent of a bf16 value is bf16 (the
+    transposes of jax's casts): a Dense's input cotangent and its kernel and
+    bias gradients are bf16 results converted to fp32, and LayerNorm's input
+    cotangent is rounded to bf16."""
+    dy = _cast(dy, dtype)
     for i in range(len(stages) - 1, -1, -1):
         st, cache = stages[i], caches[i]
         op = st["op"]
         if op == "dense":
             p = get(params, st["path"])
             x = cache
-            add_in(grads, tuple(st["path"]) + ("kernel",), x.T @ dy)
+            add_in(grads, tuple(st["path"]) + ("kernel",), _cast(x.T @ dy, dtype))
             if st.get("bias", True):
-                add_in(grads, tuple(st["path"]) + ("bias",), dy.sum(0))
+                add_in(grads, tuple(st["path"]) + ("bias",), _cast(dy.sum(0), dtype))
             if i == 0 and not need_dx:
                 return None
-            dy = dy @ np.asarray(p["kernel"], F64).T
+            dy = _cast(dy @ _cast(np.asarray(p["kernel"], F64), dtype).T, dtype)
         elif op == "layernorm":
             p = get(params, st["path"])
             xhat, rstd = cache
             add_in(grads, tuple(st["path"]) + ("scale",), (dy * xhat).sum(0))
             add_in(grads, tuple(st["path"]) + ("bias",), dy.sum(0))
             g = dy * np.asarray(p["scale"], F64)
-            dy = rstd * (g - g.mean(-1, keepdims=True)
-                         - xhat * (g * xhat).mean(-1, keepdims=True))
+            dy = _cast(rstd * (g - g.mean(-1, keepdims=True)
+                               - xhat * (g * xhat).mean(-1, keepdims=True)), dtype)
         elif op == "act":
             x, y = cache
             dy = act_bwd(st["fn"], x, y, dy)
+            if st["fn"] != "relu":
+                dy = _cast(dy, dtype)
     return dy
 
 
@@ -271,21 +302,25 @@ def gaussian_grad(mean, sigma, action, g_lp, g_ent):
 # -------------------------------------------------------------- whole network
 def forward(params, plan, obs):
     """MLP network forward on obs [rows, obs_dim].  Returns (head, value, cache),
-    head being logits [rows, A] or mean [rows, D]."""
+    head being logits [rows, A] or mean [rows, D] (the heads' outputs are cast
+    to fp32 before the distribution: distributions.py:35, actor_critic.py:14)."""
+    dt = plan.get("compute_dtype", "float32")
     x = np.asarray(obs, F64)
-    h, c_trunk = stages_forward(params, plan["trunk"], x)
-    head, c_actor = stages_forward(params, plan["actor"], h)
-    val, c_critic = stages_forward(params, plan["critic"], h)
+    h, c_trunk = stages_forward(params, plan["trunk"], x, dt)
+    head, c_actor = stages_forward(params, plan["actor"], h, dt)
+    val, c_critic = stages_forward(params, plan["critic"], h, dt)
     return head, val[:, 0], (c_trunk, c_actor, c_critic)
 
 
 def backward(params, plan, cache, dhead, dvalue, grads):
+    dt = plan.get("compute_dtype", "float32")
     c_trunk, c_actor, c_critic = cache
     need = len(plan["trunk"]) > 0
-    dh = stages_backward(params, plan["actor"], c_actor, dhead, grads, need_dx=need)
-    dh2 = stages_backward(params, plan["critic"], c_critic, dvalue[:, None], grads, need_dx=need)
+    dh = stages_backward(params, plan["actor"], c_actor, dhead, grads, need_dx=need, dtype=dt)
+    dh2 = stages_backward(params, plan["critic"], c_critic, dvalue[:, None], grads, need_dx=need, dtype=dt)
     if need:
-        stages_backward(params, plan["trunk"], c_trunk, dh + dh2, grads, need_dx=False)
+        # two bf16 cotangents of the shared features add in bf16
+        stages_backward(params, plan["trunk"], c_trunk, _cast(dh + dh2, dt), grads, need_dx=False, dtype=dt)
 
 
 def recurrent_forward(params, plan, obs, done, carry):

@@ -1,0 +1,278 @@
+"""Parity of the bf16-compute path (flax Dense / LayerNorm with
+dtype=bfloat16; boonta/networks/README.md:73-77) on the GPU, through the C ABI,
+against the oracle's bf16 emulation:
+
+- ppo_gemm_bf16 in every layout, with the row gather, split-K with the bias
+  gradient, and the bias + activation epilogue with flax's roundings;
+- the bf16 LayerNorm + ReLU forward and backward;
+- the whole PPO.update of the large-observation network (obs 8268, shared
+  3x512 LayerNorm + ReLU, 43 actions) at a size the oracle finishes in seconds.
+
+Tolerances: a bf16-rounded result may differ from the float64 emulation by one
+bf16 unit where the fp32 accumulation order flips a rounding (2^-7 relative),
+and most elements must agree exactly; unrounded fp32 partials 1e-5 relative;
+gradients, parameters, advantages and losses 2e-2 relative (the north-star
+bar for bf16 configs); permutations bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+from boonta_amd import _lib
+from boonta_amd.algorithms.ppo import flat_state_of
+from boonta_amd.flat import tree_from_flat, tree_to_numpy
+from boonta_amd.random import key as make_key
+from oracle import nets, ppo
+from ppo_cases import device_transition, gpu_algorithm, make_case, oracle_cfg, oracle_opt, rel_l2, to64
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+ULP = 2.0 ** -7
+
+
+def st():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def within_one_bf16_ulp(got, exp, exact_frac=0.97, atol=1e-30, inner=None):
+    """|got - exp| <= one bf16 unit of exp (plus one unit of an inner rounded
+    value ``inner`` that a later bias add can cancel, plus atol for values
+    that cancel to near zero, where fp32 accumulation error dominates)."""
+    got = np.asarray(got, np.float64)
+    exp = np.asarray(exp, np.float64)
+    tol = np.abs(exp) * ULP + atol
+    if inner is not None:
+        tol = tol + np.abs(inner) * ULP
+    assert np.all(np.abs(got - exp) <= tol), float(np.max(np.abs(got - exp) / (np.abs(exp) + 1e-30)))
+    assert np.mean(got == exp) >= exact_frac, np.mean(got == exp)
+
+
+def gemm_case(a_layout, b_layout, M, N, K, rows_src=None, gather=False, epi=0, act=0, splits=1, round_out=1,
+              bias_grad=False, seed=0, tile=-1):
+    g = np.random.default_rng(seed)
+    if a_layout == 0:
+        src = rows_src or M
+        Astore = g.standard_normal((src, K)).astype(np.float32)
+        idx = g.permutation(src)[:M].astype(np.int32) if gather else None
+        Alog = Astore[idx] if gather else Astore
+    else:
+        src = rows_src or K
+        Astore = g.standard_normal((src, M)).astype(np.float32)
+        idx = g.permutation(src)[:K].astype(np.int32) if gather else None
+        Alog = (Astore[idx] if gather else Astore).T
+    Blog = g.standard_normal((K, N)).astype(np.float32)
+    Bstore = Blog if b_layout == 0 else np.ascontiguousarray(Blog.T)
+    bias = g.standard_normal(N).astype(np.float32)
+    C = torch.zeros(splits, M, N, device=DEV)
+    BG = torch.zeros(splits, N, device=DEV) if bias_grad else None
+    A_t, B_t, BIAS = dev(Astore), dev(Bstore), dev(bias)
+    idx_t = dev(idx) if idx is not None else None
+    _lib.call("ppo_gemm_bf16", st(), a_layout, b_layout, A_t.data_ptr(), Astore.shape[1],
+              None if idx_t is None else idx_t.data_ptr(), B_t.data_ptr(), Bstore.shape[1], C.data_ptr(), N, M, N, K,
+              splits, M * N, epi, BIAS.data_ptr() if epi == 1 else None, act, round_out, None, 0,
+              None if BG is None else BG.data_ptr(), tile)
+    torch.cuda.synchronize()
+    Ab, Bb = nets.bf16(Alog), nets.bf16(Blog)
+    exact = Ab @ Bb
+    got = C.cpu().numpy().astype(np.float64).sum(0)
+    if round_out:
+        exp = nets.bf16(exact)
+        inner = None
+        if epi == 1:
+            # bf16(bf16(dot) + bf16(bias)): a one-unit flip of the rounded dot
+            # survives the bias add
+            inner = exp
+            exp = nets.bf16(exp + nets.bf16(bias))
+            if act == 1:
+                exp = np.maximum(exp, 0.0)
+        within_one_bf16_ulp(got, exp, atol=1e-5 * np.sqrt(K), inner=inner)
+    else:
+        np.testing.assert_allclose(got, exact, rtol=1e-5, atol=1e-4 * np.sqrt(K))
+    if bias_grad:
+        np.testing.assert_allclose(BG.cpu().numpy().astype(np.float64).sum(0), Bb.sum(0), rtol=1e-5,
+                                   atol=1e-5 * np.sqrt(K))
+
+
+@pytest.mark.parametrize("a_layout, b_layout", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M, N, K", [(256, 512, 512), (77, 44, 8268), (130, 70, 33)])
+def test_gemm_bf16_layouts(a_layout, b_layout, M, N, K):
+    gemm_case(a_layout, b_layout, M, N, K, seed=M + N + K + 7 * a_layout + b_layout)
+
+
+@pytest.mark.parametrize("tile", [0, 1, 2, 3])
+def test_gemm_bf16_every_tile(tile):
+    gemm_case(0, 0, 200, 190, 48, tile=tile, seed=tile)
+    gemm_case(1, 0, 130, 70, 500, tile=tile, splits=3, round_out=0, bias_grad=True, seed=tile + 10)
+
+
+def test_gemm_bf16_forward_gathers_rows_with_bias_relu():
+    gemm_case(0, 0, 512, 512, 8268, rows_src=4096, gather=True, epi=1, act=1)
+    gemm_case(0, 0, 100, 44, 512, rows_src=1000, gather=True, epi=1, act=0)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 16])
+def test_gemm_bf16_dw_over_gathered_rows(splits):
+    gemm_case(1, 0, 8268, 512, 1024, rows_src=4096, gather=True, splits=splits, round_out=0, bias_grad=True)
+
+
+def test_round_bf16():
+    x = np.random.default_rng(4).standard_normal(100003).astype(np.float32) * 100
+    X = dev(x)
+    _lib.call("ppo_round_bf16", st(), X.data_ptr(), x.size)
+    np.testing.assert_array_equal(X.cpu().numpy().astype(np.float64), nets.bf16(x))
+
+
+def test_layernorm_relu_bf16_forward_and_backward():
+    g = np.random.default_rng(5)
+    rows, F = 333, 512
+    z = nets.bf16(g.normal(0.2, 1.5, (rows, F)))
+    gamma = g.normal(1, 0.2, F).astype(np.float32)
+    beta = g.normal(0, 0.2, F).astype(np.float32)
+    dy = nets.bf16(g.standard_normal((rows, F)))
+    stages = [{"op": "layernorm", "path": ("ln",), "width": F, "eps": 1e-6}, {"op": "act", "fn": "relu"}]
+    params = {"ln": {"scale": gamma.astype(np.float64), "bias": beta.astype(np.float64)}}
+    y_ref, caches = nets.stages_forward(params, stages, z, "bfloat16")
+    grads = {}
+    dz_ref = nets.stages_backward(params, stages, caches, dy, grads, dtype="bfloat16")
+    Z, G, Bt, DY = dev(z.astype(np.float32)), dev(gamma), dev(beta), dev(dy.astype(np.float32))
+    Y = torch.zeros(rows, F, device=DEV)
+    MEAN = torch.zeros(rows, device=DEV)
+    RSTD = torch.zeros(rows, device=DEV)
+    _lib.call("ppo_layernorm_act_fwd_bf16", st(), Z.data_ptr(), F, G.data_ptr(), Bt.data_ptr(), Y.data_ptr(), F,
+              MEAN.data_ptr(), RSTD.data_ptr(), rows, F, 1e-6, 1)
+    nb = _lib.load().ppo_layernorm_bwd_blocks(rows)
+    DZ = torch.zeros(rows, F, device=DEV)
+    PART = torch.zeros(nb, 2 * F, device=DEV)
+    _lib.call("ppo_layernorm_act_bwd_bf16", st(), DY.data_ptr(), F, Z.data_ptr(), F, MEAN.data_ptr(), RSTD.data_ptr(),
+              G.data_ptr(), Bt.data_ptr(), DZ.data_ptr(), F, PART.data_ptr(), rows, F, 1)
+    torch.cuda.synchronize()
+    within_one_bf16_ulp(Y.cpu().numpy(), y_ref, exact_frac=0.99, atol=1e-6)
+    within_one_bf16_ulp(DZ.cpu().numpy(), dz_ref, exact_frac=0.95, atol=1e-5)
+    part = PART.cpu().numpy().astype(np.float64).sum(0)
+    np.testing.assert_allclose(part[:F], grads["ln"]["scale"], rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(part[F:], grads["ln"]["bias"], rtol=1e-4, atol=1e-4)
+
+
+# ------------------------------------------------------------------ whole update
+CASE = dict(config=5, T=8, N=32, M=2, E=2)
+TOL = 2e-2
+
+
+def run_both(max_steps=None, key_seed=5):
+    r, plan, params, tr, roll = make_case(**CASE)
+    assert plan["compute_dtype"] == "bfloat16"
+    key = make_key(key_seed)
+    records = []
+    p_or, _, info = ppo.ppo_update(to64(params), ppo.optimizer_init(to64(params)), plan, oracle_cfg(r.cfg),
+                                   oracle_opt(r.optimizer), tr, key,
+                                   record=lambda e, idx, g, p: records.append((idx.copy(), g)))
+    alg = gpu_algorithm(r, use_graph=False)
+    state = alg.init_from_params({"params": params}, r.obs_dim)
+    trans = device_transition(tr, roll)
+    if max_steps is None:
+        alg.update(state, key, trans)
+    else:
+        ex = alg.executor(state, r.T, r.N, r.obs_dim)
+        ex.KEY.copy_(torch.from_numpy(key.view(np.int32).copy()))
+        ex.bind(alg._inputs(trans, r.obs_dim)[0])
+        ex.issue(torch.cuda.current_stream().cuda_stream, max_steps=max_steps)
+    torch.cuda.synchronize()
+    return r, alg, state, (p_or, info, records)
+
+
+def leaves(tree):
+    return dict(ppo.tree_leaves(tree))
+
+
+def test_bf16_update_bootstrap_advantages_and_permutations():
+    r, alg, state, (_, info, _) = run_both()
+    ex = alg.executor(state, r.T, r.N, r.obs_dim)
+    np.testing.assert_array_equal(ex.PERM.cpu().numpy(), info["permutations"])
+    assert rel_l2(ex.BOOT.cpu().numpy(), info["bootstrap"]) <= TOL
+    assert rel_l2(ex.ADV.cpu().numpy(), info["advantages"].reshape(-1)) <= TOL
+    assert rel_l2(ex.RET.cpu().numpy(), info["returns"].reshape(-1)) <= TOL
+
+
+def flat_tree(flat, buf):
+    return leaves(tree_to_numpy(tree_from_flat(flat.program.layout, buf)))
+
+
+def test_bf16_every_step_teacher_forced():
+    """Each optimizer step against the oracle at the GPU's own parameters.
+
+    Adam moves every parameter by about lr per step whatever the gradient's
+    size, so an element whose bf16 gradient is within rounding of zero can
+    step the other way, and two bf16 trajectories drift apart step by step
+    (as two XLA builds with different fusion would).  So every step k is
+    checked on its own: the GPU's gradient at step k against the oracle's
+    gradient at the GPU's parameters before step k, on the same minibatch
+    (bit-exact permutation) with the GPU's advantages and returns (2e-2); the
+    GPU's logs of step k against the oracle's at those parameters (2e-2); and
+    the GPU's clip + Adam step against optax's restatement applied to the
+    GPU's gradient and moments (1e-5 relative, 1e-8 absolute: lr is 3e-4)."""
+    r, plan, params, tr, roll = make_case(**CASE)
+    key = make_key(5)
+    cfg, opt = oracle_cfg(r.cfg), oracle_opt(r.optimizer)
+    B = r.T * r.N
+    flat_obs = tr["obs"].reshape(B, -1)
+    act, olp, ov = tr["action"].reshape(B), tr["log_prob"].reshape(B), tr["value"].reshape(B)
+    steps = r.cfg.update_epochs * r.cfg.num_minibatches
+    prev = None
+    for k in range(1, steps + 1):
+        alg = gpu_algorithm(r, use_graph=False)
+        state = alg.init_from_params({"params": params}, r.obs_dim)
+        trans = device_transition(tr, roll)
+        ex = alg.executor(state, r.T, r.N, r.obs_dim)
+        ex.KEY.copy_(torch.from_numpy(key.view(np.int32).copy()))
+        ex.bind(alg._inputs(trans, r.obs_dim)[0])
+        ex.issue(torch.cuda.current_stream().cuda_stream, max_steps=k)
+        torch.cuda.synchronize()
+        flat = flat_state_of(state)
+        cur = {"P": flat_tree(flat, flat.P), "G": flat_tree(flat, flat.G), "MU": flat_tree(flat, flat.MU),
+               "NU": flat_tree(flat, flat.NU)}
+        if prev is None:
+            prev = {"P": leaves(to64(params)), "MU": {p: np.zeros_like(v) for p, v in cur["P"].items()},
+                    "NU": {p: np.zeros_like(v) for p, v in cur["P"].items()}}
+        perm = ex.PERM.cpu().numpy()
+        mb = B // r.cfg.num_minibatches
+        e, m = divmod(k - 1, r.cfg.num_minibatches)
+        idx = perm[e, m * mb:(m + 1) * mb]
+        adv, ret = ex.ADV.cpu().numpy()[idx], ex.RET.cpu().numpy()[idx]
+        p_prev = tree_of(prev["P"])
+        loss, lg, g_or = ppo.loss_and_grad(p_prev, plan, cfg, flat_obs[idx], act[idx], olp[idx], ov[idx], adv, ret)
+        for path, g in leaves(g_or).items():
+            assert rel_l2(cur["G"][path], g) <= TOL, (k, path, rel_l2(cur["G"][path], g))
+        logs = alg.logs(state, r.T, r.N, r.obs_dim)
+        np.testing.assert_allclose(logs["loss"][k - 1], loss, rtol=TOL, atol=1e-3)
+        np.testing.assert_allclose(logs["critic/value"][k - 1], lg["critic/value"], rtol=TOL, atol=1e-3)
+        # clip + Adam on the GPU's own gradient and moments
+        new, _, _ = ppo.optimizer_update(tree_of(cur["G"]), {"count": k - 1, "mu": tree_of(prev["MU"]),
+                                                             "nu": tree_of(prev["NU"])}, p_prev, opt)
+        for path, pv in leaves(new).items():
+            # fp32 Adam (its bias corrections 1 - b^count cancel in fp32, as optax's do) against float64
+            np.testing.assert_allclose(cur["P"][path], pv, rtol=1e-5, atol=1e-8, err_msg=f"step {k} {path}")
+        prev = cur
+
+
+def tree_of(flat_leaves):
+    out = {}
+    for path, v in flat_leaves.items():
+        node = out
+        for key in path[:-1]:
+            node = node.setdefault(key, {})
+        node[path[-1]] = np.asarray(v, np.float64)
+    return out
+
+
+def test_bf16_whole_update_is_finite_and_counts_steps():
+    r, alg, state, (p_or, info, _) = run_both()
+    assert int(flat_state_of(state).count.item()) == r.cfg.update_epochs * r.cfg.num_minibatches
+    p_gpu = leaves(tree_to_numpy(state.params["params"]))
+    assert all(np.isfinite(v).all() for v in p_gpu.values())
+    logs = alg.logs(state, r.T, r.N, r.obs_dim)
+    assert all(np.isfinite(v).all() for v in logs.values())
+    # the first step runs at the initial parameters on both sides
+    np.testing.assert_allclose(logs["loss"][0], info["logs"][0]["loss"], rtol=TOL, atol=1e-3)

@@ -13,6 +13,7 @@ from oracle import ppo as oppo
 
 MLP_CONFIGS = [1, 2, 3]
 FP32_CONFIGS = [1, 2, 3, 4]
+ALL_CONFIGS = [1, 2, 3, 4, 5]
 
 
 def small(config):
@@ -23,6 +24,8 @@ def small(config):
         return r.resized(T=8, N=64, num_minibatches=4, update_epochs=2)
     if config == 4:
         return r.resized(T=8, N=64, num_minibatches=4, update_epochs=2)
+    if config == 5:
+        return r.resized(T=8, N=32, num_minibatches=2, update_epochs=2)
     return r
 
 
@@ -37,7 +40,7 @@ def fake_inputs(ex):
          "first_terminated", "first_truncated", "carry0", "carry_last"])}
 
 
-@pytest.mark.parametrize("config", FP32_CONFIGS)
+@pytest.mark.parametrize("config", ALL_CONFIGS)
 def test_recorded_launches_match_the_c_signatures(config):
     r = small(config)
     prog = Program(r.network.plan(r.obs_dim))
@@ -54,13 +57,18 @@ def test_recorded_launches_match_the_c_signatures(config):
         assert names.count("ppo_sequence_rows") == 1
     assert names.count("ppo_adam_clip_f32") == steps
     assert names.count("ppo_loss_finalize") == steps
-    # every workload here has torso features in front of its heads: the fused kernel runs
-    assert names.count("ppo_head_loss_f32") == steps and "ppo_loss_f32" not in names
+    if prog.bf16:
+        # 43 actions: the unfused head GEMM + loss + head backward, every GEMM on bf16 MFMA
+        assert names.count("ppo_loss_f32") == steps and "ppo_gemm_f32" not in names
+        assert all(n != "ppo_layernorm_act_fwd_f32" for n in names)
+    else:
+        # every fp32 workload has torso features in front of its heads: the fused kernel runs
+        assert names.count("ppo_head_loss_f32") == steps and "ppo_loss_f32" not in names
     assert names[-1] == "ppo_count_advance"
     for name, args in calls:
         _, argtypes = _lib.SIGNATURES[name]
         assert len(args) == len(argtypes), (name, len(args), len(argtypes))
-        if name == "ppo_gemm_f32":
+        if name in ("ppo_gemm_f32", "ppo_gemm_bf16"):
             (_, a_layout, b_layout, A, lda, rows, B, ldb, C, ldc, M, N, K, splits, stride, epi, bias, act, pre,
              aux, ldaux, bias_grad, tile) = args
             assert A and B and C and M > 0 and N > 0 and K > 0
@@ -76,7 +84,7 @@ def test_recorded_launches_match_the_c_signatures(config):
             assert all((ha, wa, ba, dha, wpa, bpa, stats))
 
 
-@pytest.mark.parametrize("config", FP32_CONFIGS)
+@pytest.mark.parametrize("config", ALL_CONFIGS)
 def test_flat_layout_round_trips_the_parameter_tree(config):
     r = recipes.make(config)
     prog = Program(r.network.plan(r.obs_dim))
