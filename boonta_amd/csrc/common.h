@@ -39,6 +39,30 @@ inline int check_launch(const char* what) {
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 inline int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Tile coordinates for a GEMM grid (gridDim.x = N tiles, .y = M tiles, .z =
+// reduction splits) on a part with 8 XCDs, each with its own L2: the hardware
+// hands workgroup w to XCD w % 8, so the linear id is remapped to give XCD x a
+// contiguous range of logical tiles, ordered N fastest, then M, then split.
+// Tiles that read the same A rows (and, in a split-K launch, the same
+// reduction slice) then run together on one XCD and share its L2.
+struct TileCoord {
+  int n, m, z;
+};
+
+__device__ __forceinline__ TileCoord xcd_tile() {
+  const int gx = gridDim.x, gy = gridDim.y;
+  const int total = gx * gy * gridDim.z;
+  const int w = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  const int x = w & 7, j = w >> 3;
+  const int q = total >> 3, r = total & 7;
+  const int t = x * q + (x < r ? x : r) + j;
+  TileCoord c;
+  c.n = t % gx;
+  c.m = (t / gx) % gy;
+  c.z = t / (gx * gy);
+  return c;
+}
+
 // Round to nearest even bf16 (NaN stays NaN), returned as the fp32 value
 // of that bf16 (bits() gives the 16-bit pattern).
 __device__ __forceinline__ uint32_t bf16_bits(float x) {

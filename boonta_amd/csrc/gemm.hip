@@ -30,7 +30,7 @@
 
 namespace {
 
-constexpr int BK = 16;
+constexpr int BK_MIN = 16;  // reduction granule: k_per_split is a multiple of it
 constexpr int LDS_PAD = 4;
 
 enum Epilogue { EPI_STORE = 0, EPI_BIAS_ACT = 1, EPI_DACT = 2 };
@@ -71,7 +71,7 @@ __device__ __forceinline__ floatx4 load4(const float* __restrict__ p, int i, int
   return v;
 }
 
-template <int BM, int BN, bool A_K, bool B_K, bool VA, bool VB>
+template <int BM, int BN, int BK, bool A_K, bool B_K, bool VA, bool VB>
 __global__ void __launch_bounds__(256, 2) gemm_f32_kernel(GemmParams p) {
   constexpr int A_ROWS = A_K ? BM : BK;
   constexpr int A_COLS = A_K ? BK : BM;
@@ -93,9 +93,10 @@ __global__ void __launch_bounds__(256, 2) gemm_f32_kernel(GemmParams p) {
   const int wn = wave >> 1;
   const int h = lane >> 5;
   const int l32 = lane & 31;
-  const int m0 = blockIdx.y * BM;
-  const int n0 = blockIdx.x * BN;
-  const int split = blockIdx.z;
+  const ppo::TileCoord tc = ppo::xcd_tile();
+  const int m0 = tc.m * BM;
+  const int n0 = tc.n * BN;
+  const int split = tc.z;
   const int kb = split * p.k_per_split;
   const int ke = min(p.K, kb + p.k_per_split);
 
@@ -109,7 +110,7 @@ __global__ void __launch_bounds__(256, 2) gemm_f32_kernel(GemmParams p) {
   float bsum[NB];
 #pragma unroll
   for (int j = 0; j < NB; ++j) bsum[j] = 0.f;
-  const bool do_bsum = (p.bias_grad != nullptr) && (blockIdx.y == 0) && (wm == 0);
+  const bool do_bsum = (p.bias_grad != nullptr) && (tc.m == 0) && (wm == 0);
 
   floatx4 ra[A_PER], rb[B_PER];
 
@@ -260,24 +261,28 @@ __global__ void __launch_bounds__(256, 2) gemm_f32_kernel(GemmParams p) {
   }
 }
 
-template <int BM, int BN, bool A_K, bool B_K>
+template <int BM, int BN, int BK, bool A_K, bool B_K>
 int launch_tile(hipStream_t st, const GemmParams& p, int splits, bool va, bool vb) {
   dim3 grid(ppo::ceil_div(p.N, BN), ppo::ceil_div(p.M, BM), splits);
   dim3 block(256);
-  if (va && vb) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, A_K, B_K, true, true>), grid, block, 0, st, p);
-  else if (va) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, A_K, B_K, true, false>), grid, block, 0, st, p);
-  else if (vb) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, A_K, B_K, false, true>), grid, block, 0, st, p);
-  else hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, A_K, B_K, false, false>), grid, block, 0, st, p);
+  if (va && vb) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, A_K, B_K, true, true>), grid, block, 0, st, p);
+  else if (va) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, A_K, B_K, true, false>), grid, block, 0, st, p);
+  else if (vb) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, A_K, B_K, false, true>), grid, block, 0, st, p);
+  else hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, A_K, B_K, false, false>), grid, block, 0, st, p);
   return ppo::check_launch("ppo_gemm_f32");
 }
 
 template <bool A_K, bool B_K>
 int launch_layout(hipStream_t st, const GemmParams& p, int splits, bool va, bool vb, int tile) {
   switch (tile) {
-    case 0: return launch_tile<128, 128, A_K, B_K>(st, p, splits, va, vb);
-    case 1: return launch_tile<128, 64, A_K, B_K>(st, p, splits, va, vb);
-    case 2: return launch_tile<64, 128, A_K, B_K>(st, p, splits, va, vb);
-    default: return launch_tile<64, 64, A_K, B_K>(st, p, splits, va, vb);
+    case 0: return launch_tile<128, 128, 16, A_K, B_K>(st, p, splits, va, vb);
+    case 1: return launch_tile<128, 64, 16, A_K, B_K>(st, p, splits, va, vb);
+    case 2: return launch_tile<64, 128, 16, A_K, B_K>(st, p, splits, va, vb);
+    case 3: return launch_tile<64, 64, 16, A_K, B_K>(st, p, splits, va, vb);
+    case 4: return launch_tile<128, 128, 32, A_K, B_K>(st, p, splits, va, vb);
+    case 5: return launch_tile<128, 64, 32, A_K, B_K>(st, p, splits, va, vb);
+    case 6: return launch_tile<64, 128, 32, A_K, B_K>(st, p, splits, va, vb);
+    default: return launch_tile<64, 64, 32, A_K, B_K>(st, p, splits, va, vb);
   }
 }
 
@@ -290,13 +295,14 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 //   rows: gather of A's rows (layout 0: over m; layout 1: over k) or null.
 //   epi 0: store; 1: bias + activation (pre-activation to `pre` if non-null);
 //   2: multiply by act'(aux).  bias_grad (layout a=1, b=0 only): [splits][N] sums of B.
-//   tile: -1 picks a tile; 0: 128x128, 1: 128x64, 2: 64x128, 3: 64x64.
+//   tile: -1 picks a tile; 0: 128x128, 1: 128x64, 2: 64x128, 3: 64x64 with 16 reduction
+//   elements per LDS stage; 4-7 the same tiles with 32 per stage.
 PPO_EXPORT int ppo_gemm_f32(void* stream, int a_layout, int b_layout, const float* A, int64_t lda,
                             const int32_t* rows, const float* B, int64_t ldb, float* C, int64_t ldc, int M,
                             int N, int K, int splits, int64_t c_split_stride, int epi, const float* bias,
                             int act, float* pre, const float* aux, int64_t ldaux, float* bias_grad, int tile) {
   if (M < 0 || N < 0 || K < 0 || splits < 1 || a_layout < 0 || a_layout > 1 || b_layout < 0 || b_layout > 1 ||
-      epi < 0 || epi > 2 || act < 0 || act > 3)
+      epi < 0 || epi > 2 || act < 0 || act > 3 || tile > 7)
     return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32: bad argument (M=%d N=%d K=%d splits=%d)", M, N, K, splits);
   if (M == 0 || N == 0) return PPO_OK;
   if (!A || !B || !C) return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32: null operand");
@@ -308,7 +314,7 @@ PPO_EXPORT int ppo_gemm_f32(void* stream, int a_layout, int b_layout, const floa
   GemmParams p;
   p.A = A; p.lda = lda; p.rows = rows; p.B = B; p.ldb = ldb; p.C = C; p.ldc = ldc;
   p.c_split_stride = c_split_stride; p.M = M; p.N = N; p.K = K;
-  const int kps = ((ppo::ceil_div(K > 0 ? K : 1, splits) + BK - 1) / BK) * BK;
+  const int kps = ((ppo::ceil_div(K > 0 ? K : 1, splits) + BK_MIN - 1) / BK_MIN) * BK_MIN;
   p.k_per_split = kps;
   p.epi = epi; p.bias = bias; p.act = act; p.pre = pre; p.aux = aux; p.ldaux = ldaux; p.bias_grad = bias_grad;
   // vector loads need 16-byte rows along the contiguous axis
@@ -316,13 +322,10 @@ PPO_EXPORT int ppo_gemm_f32(void* stream, int a_layout, int b_layout, const floa
   const int b_contig = b_layout == 1 ? K : N;
   const bool va = (lda % 4 == 0) && (a_contig % 4 == 0) && aligned16(A);
   const bool vb = (ldb % 4 == 0) && (b_contig % 4 == 0) && aligned16(B);
-  if (tile < 0) {
-    const int64_t t128 = (int64_t)ppo::ceil_div(M, 128) * ppo::ceil_div(N, 128) * splits;
-    if (t128 >= 512) tile = 0;
-    else if ((int64_t)ppo::ceil_div(M, 128) * ppo::ceil_div(N, 64) * splits >= 512) tile = 1;
-    else if ((int64_t)ppo::ceil_div(M, 64) * ppo::ceil_div(N, 128) * splits >= 512) tile = 2;
-    else tile = 3;
-  }
+  // 64 x 64 tiles measure fastest on every learner shape on MI355X (more
+  // resident workgroups per CU hide the global-load latency better than the
+  // larger tiles' register reuse gains).
+  if (tile < 0) tile = 3;
   hipStream_t st = ppo::as_stream(stream);
   if (a_layout == 0 && b_layout == 0) return launch_layout<true, false>(st, p, splits, va, vb, tile);
   if (a_layout == 0 && b_layout == 1) return launch_layout<true, true>(st, p, splits, va, vb, tile);

@@ -163,9 +163,10 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_kernel(GemmParams p) {
   const int wn = wave >> 1;
   const int h = lane >> 5;
   const int l32 = lane & 31;
-  const int m0 = blockIdx.y * BM;
-  const int n0 = blockIdx.x * BN;
-  const int split = blockIdx.z;
+  const ppo::TileCoord tc = ppo::xcd_tile();
+  const int m0 = tc.m * BM;
+  const int n0 = tc.n * BN;
+  const int split = tc.z;
   const int kb = split * p.k_per_split;
   const int ke = min(p.K, kb + p.k_per_split);
 
@@ -179,7 +180,7 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_kernel(GemmParams p) {
   float bsum[NB];
 #pragma unroll
   for (int j = 0; j < NB; ++j) bsum[j] = 0.f;
-  const bool do_bsum = (p.bias_grad != nullptr) && (blockIdx.y == 0) && (wm == 0);
+  const bool do_bsum = (p.bias_grad != nullptr) && (tc.m == 0) && (wm == 0);
 
   Stage<BM, A_K, VA> sa;
   Stage<BN, B_K, VB> sb;
@@ -326,12 +327,9 @@ PPO_EXPORT int ppo_gemm_bf16(void* stream, int a_layout, int b_layout, const flo
   const int b_contig = b_layout == 1 ? K : N;
   const bool va = (lda % 4 == 0) && (a_contig % 4 == 0) && aligned16(A);
   const bool vb = (ldb % 4 == 0) && (b_contig % 4 == 0) && aligned16(B);
-  if (tile < 0) {
-    if ((int64_t)ppo::ceil_div(M, 128) * ppo::ceil_div(N, 128) * splits >= 512) tile = 0;
-    else if ((int64_t)ppo::ceil_div(M, 128) * ppo::ceil_div(N, 64) * splits >= 512) tile = 1;
-    else if ((int64_t)ppo::ceil_div(M, 64) * ppo::ceil_div(N, 128) * splits >= 512) tile = 2;
-    else tile = 3;
-  }
+  // 64 x 128 for long reductions (the first layer's 8268 features), 64 x 64
+  // otherwise: the measured best on the learner shapes.
+  if (tile < 0) tile = (K >= 2048 && (int64_t)ppo::ceil_div(M, 64) * ppo::ceil_div(N, 128) * splits >= 256) ? 2 : 3;
   hipStream_t st = ppo::as_stream(stream);
   if (a_layout == 0 && b_layout == 0) return launch_layout<true, false>(st, p, splits, va, vb, tile);
   if (a_layout == 0 && b_layout == 1) return launch_layout<true, true>(st, p, splits, va, vb, tile);

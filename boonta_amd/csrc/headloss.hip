@@ -1,27 +1,26 @@
-// Fused policy/value heads + PPO loss + head backward, one pass over the torso
-// output of a minibatch.
+// Fused policy/value heads + PPO loss + head backward over one minibatch.
 //
 // Follows loss_fn of boonta/algorithms/ppo.py:77-146 (recurrent_ppo.py:101-184)
 // with the heads of boonta/networks/heads.py:9-45 (a Dense layer each, or one
 // Dense feeding both when actor and critic share the torso) and the
 // distributions of boonta/networks/distributions.py:8-57.
 //
-// Work split: each wavefront owns a run of <= 64 consecutive rows; lane l
-// holds features f = l + 64 e (e < VPL) and the matching head-weight rows in
-// registers for the whole block.
-//   A. one row at a time: the NA head outputs are VPL * NA FMAs per lane and a
-//      butterfly reduce-scatter (NA/2 + NA/4 + ... exchanges instead of NA
-//      full wave reductions); they go to LDS;
+// One workgroup of 4 wave64s owns a tile of 64 minibatch rows and does the
+// head algebra on matrix cores (v_mfma_f32_16x16x4f32), with every operand
+// loaded in one pass so the global-load latency is paid a few times per tile
+// rather than once per row:
+//   A. head outputs OUT[64, 16] = H[64, F] Wa[F, 16] (each wave 16 rows; the
+//      value of separate towers is one more column from Hc wc) -> LDS;
 //   B. one lane per row: the loss, its statistics and the cotangents of the
-//      head outputs, computed once per row instead of redundantly per lane;
-//   C. one row at a time again: the cotangent of the torso output,
-//      sum_j dout_j W[f][j] times the derivative of the torso's last
-//      activation, is written, and H[f] * dout_j accumulates the head weight
-//      gradient in registers.
-// Rows are prefetched two ahead in A and C.
-// Per-block partials (head weights and biases, Gaussian scale, statistics)
-// are folded across the block's waves in a fixed order; the gradient reduce
-// kernel sums the blocks.
+//      head outputs (jax's tie rules for min / max / clip) -> LDS, with the
+//      block's statistic, bias and Gaussian-scale partials;
+//   C1. the cotangent of each head input, dH[64, F] = dOUT[64, 16] Wa^T times
+//      the derivative of the torso's last activation (each wave 16 rows);
+//   C2. the head weight gradient partial H^T dOUT [F, 16] (each wave a quarter
+//      of F).
+// Per-block partials are summed in a fixed order by the gradient reduce, so
+// results do not depend on scheduling.  F must be a multiple of 16 (<= 512)
+// and the heads have at most 16 outputs.
 #include "common.h"
 
 #include <algorithm>
@@ -29,7 +28,6 @@
 namespace {
 
 constexpr int HL_THREADS = 256;
-constexpr int HL_WAVES = HL_THREADS / 64;
 
 enum Dist { DIST_CATEGORICAL = 0, DIST_GAUSSIAN = 1 };
 enum Stat {
@@ -56,34 +54,6 @@ struct HeadLossParams {
   float clip_eps; int clip_value_loss; float ent_coef, vf_coef, inv_n, temperature;
 };
 
-template <int NA>
-__device__ __forceinline__ float reduce_scatter(float (&v)[NA], int lane) {
-  float buf[NA];
-#pragma unroll
-  for (int k = 0; k < NA; ++k) buf[k] = v[k];
-  int off = 32;
-#pragma unroll
-  for (int size = NA; size > 1; size >>= 1) {
-    const int half = size >> 1;
-    const bool hi = (lane & off) != 0;
-#pragma unroll
-    for (int k = 0; k < half; ++k) {
-      const float send = hi ? buf[k] : buf[k + half];
-      const float recv = __shfl_xor(send, off, 64);
-      buf[k] = (hi ? buf[k + half] : buf[k]) + recv;
-    }
-    off >>= 1;
-  }
-#pragma unroll
-  for (; off >= 1; off >>= 1) buf[0] += __shfl_xor(buf[0], off, 64);
-  return buf[0];
-}
-
-template <int NA>
-constexpr int log2_of() {
-  return NA <= 1 ? 0 : 1 + log2_of<NA / 2>();
-}
-
 __device__ __forceinline__ float tie_first(float x, float y, float ans) {
   return (x == ans ? 1.f : 0.f) / (y == ans ? 2.f : 1.f);
 }
@@ -97,395 +67,312 @@ __device__ __forceinline__ float softplusf(float x) { return fmaxf(x, 0.f) + log
 
 constexpr float LOG_2PI = 1.8378770664093453f;
 
-template <int VPL, int NA, bool SEP>
-__global__ void __launch_bounds__(HL_THREADS) head_loss_kernel(HeadLossParams p) {
-  extern __shared__ float smem[];  // fold buffer [F][NA + 1]
-  constexpr int NO = NA + 1;       // head outputs + the critic's value (separate towers)
-  __shared__ float s_out[HL_WAVES][64][NO];
-  __shared__ float s_dout[HL_WAVES][64][NO];
-  __shared__ double s_stats[HL_WAVES][NSTAT];
-  __shared__ float s_vec[HL_WAVES][3][NA];  // db_a, db_c (col 0), dscale
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  constexpr int P = log2_of<NA>();
-  const int F = p.F;
+constexpr int TR = 64;   // rows per workgroup
+constexpr int LDO = 20;  // LDS row pitch: 16 head outputs + the separate critic's value, 16-byte rows
+
+// The loss and output cotangents of one row (phase B).  out[0..15]: head
+// outputs with bias; v: the value.  Writes dout[0..15], dvalue and adds to
+// the statistics / Gaussian-scale accumulators.
+__device__ __forceinline__ void row_loss(const HeadLossParams& p, bool sep, int64_t s, const float (&out)[16],
+                                         float v, float (&dout)[16], float& dvalue, double (&st)[NSTAT],
+                                         float (&dsc)[16]) {
   const int A = p.A;
-
-  // Each wave owns a contiguous run of at most 64 rows (the launch sizes the
-  // grid for it): lane k of the wave is the run's k-th row in phase B.
-  const int total_waves = gridDim.x * HL_WAVES;
-  const int per_wave = (p.rows + total_waves - 1) / total_waves;
-  const int gw = blockIdx.x * HL_WAVES + wave;
-  const int r_begin = __builtin_amdgcn_readfirstlane(min(p.rows, gw * per_wave));
-  const int r_end = __builtin_amdgcn_readfirstlane(min(p.rows, r_begin + per_wave));
-  const int R = r_end - r_begin;
-
-  // head weights of this lane's features, in registers for phases A and C
-  float wa[VPL][NA];
-  float wc[VPL];
+  const float olp = p.old_logp[s], Av = p.adv[s], Rt = p.ret[s], vold = p.old_value[s];
+  const float eps = p.clip_eps;
+  const float inv_t = 1.f / p.temperature;
+  float lp = 0.f, ent = 0.f, lse = 0.f;
+  int a = 0;
 #pragma unroll
-  for (int e = 0; e < VPL; ++e) {
-    const int f = lane + 64 * e;
+  for (int j = 0; j < 16; ++j) dout[j] = 0.f;
+  if (p.dist == DIST_CATEGORICAL) {
+    float mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < NA; ++j) wa[e][j] = (f < F && j < p.na) ? p.wa[(int64_t)f * p.ldwa + j] : 0.f;
-    wc[e] = (SEP && f < F) ? p.wc[(int64_t)f * p.ldwc] : 0.f;
-  }
-
-  // ---------------- phase A: head outputs of every row, one wavefront per row
-  {
-    float hb[2][VPL], hcb[2][VPL];
-    auto fetch = [&](int row, float (&h)[VPL], float (&hc)[VPL]) {
+    for (int j = 0; j < 16; ++j) if (j < A) mx = fmaxf(mx, out[j] * inv_t);
+    float se = 0.f;
 #pragma unroll
-      for (int e = 0; e < VPL; ++e) {
-        const int f = lane + 64 * e;
-        const bool ok = row < r_end && f < F;
-        h[e] = ok ? p.ha[(int64_t)row * p.ldha + f] : 0.f;
-        hc[e] = (SEP && ok) ? p.hc[(int64_t)row * p.ldhc + f] : 0.f;
+    for (int j = 0; j < 16; ++j) if (j < A) se += __expf(out[j] * inv_t - mx);
+    lse = mx + __logf(se);
+    a = p.action_i[s];
+    float za = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) za = (j == a) ? out[j] * inv_t : za;
+    lp = (a >= 0 && a < A) ? za - lse : -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (j < A) {
+        const float lq = out[j] * inv_t - lse;
+        ent -= __expf(lq) * lq;
       }
-    };
-    auto step = [&](int k, float (&h)[VPL], float (&hc)[VPL]) {
-      float part[NA];
+  } else {
 #pragma unroll
-      for (int j = 0; j < NA; ++j) part[j] = 0.f;
-      float pc = 0.f;
+    for (int j = 0; j < 16; ++j)
+      if (j < A) {
+        float raw = 0.f;
+        if (p.scale_param) {
+          raw = p.scale_param[j];
+        } else {
 #pragma unroll
-      for (int e = 0; e < VPL; ++e) {
-#pragma unroll
-        for (int j = 0; j < NA; ++j) part[j] += h[e] * wa[e][j];
-        pc += hc[e] * wc[e];
+          for (int q = 0; q < 16; ++q) raw = (q == A + j) ? out[q] : raw;
+        }
+        const float sig = p.temperature * (softplusf(raw) + 1e-3f);
+        const float zz = (p.action_f[s * A + j] - out[j]) / sig;
+        const float ls = __logf(sig);
+        lp += -0.5f * zz * zz - ls - 0.5f * LOG_2PI;
+        ent += 0.5f + 0.5f * LOG_2PI + ls;
       }
-      fetch(r_begin + k + 2, h, hc);
-      const float mine = reduce_scatter<NA>(part, lane);
-      if ((lane & ((64 >> P) - 1)) == 0) s_out[wave][k][lane >> (6 - P)] = mine;
-      if (SEP) {
-        const float v = ppo::wave_sum(pc);
-        if (lane == 0) s_out[wave][k][NA] = v;
+  }
+  const float ratio = __expf(lp - olp);
+  float cr, dcr;
+  clip_grad(ratio, 1.f - eps, 1.f + eps, cr, dcr);
+  const float pg1 = ratio * Av, pg2 = cr * Av;
+  const float pmin = fminf(pg1, pg2);
+  const float g_lp = -(tie_first(pg1, pg2, pmin) * Av + tie_first(pg2, pg1, pmin) * Av * dcr) * p.inv_n * ratio;
+  const float g_ent = -p.ent_coef * p.inv_n;
+  const float vl1 = 0.5f * (v - Rt) * (v - Rt);
+  float crow, gv;
+  if (p.clip_value_loss) {
+    float dv, ddv;
+    clip_grad(v - vold, -eps, eps, dv, ddv);
+    const float vc = vold + dv;
+    const float vl2 = 0.5f * (vc - Rt) * (vc - Rt);
+    crow = fmaxf(vl1, vl2);
+    gv = tie_first(vl1, vl2, crow) * (v - Rt) + tie_first(vl2, vl1, crow) * (vc - Rt) * ddv;
+  } else {
+    crow = vl1;
+    gv = v - Rt;
+  }
+  dvalue = p.vf_coef * gv * p.inv_n;
+  if (p.dist == DIST_CATEGORICAL) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (j < A) {
+        const float lq = out[j] * inv_t - lse;
+        const float q = __expf(lq);
+        dout[j] = (g_lp * ((j == a ? 1.f : 0.f) - q) - g_ent * q * (lq + ent)) * inv_t;
       }
-    };
-    fetch(r_begin, hb[0], hcb[0]);
-    fetch(r_begin + 1, hb[1], hcb[1]);
-    for (int k = 0; k < R; k += 2) {
-      step(k, hb[0], hcb[0]);
-      if (k + 1 < R) step(k + 1, hb[1], hcb[1]);
-    }
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-  // ---------------- phase B: loss and output cotangents, one lane per row
-  double st[NSTAT];
+  } else {
 #pragma unroll
-  for (int i = 0; i < NSTAT; ++i) st[i] = 0.0;
-  float db_a[NA], dsc[NA];
+    for (int j = 0; j < 16; ++j)
+      if (j < A) {
+        float raw = 0.f;
+        if (p.scale_param) {
+          raw = p.scale_param[j];
+        } else {
 #pragma unroll
-  for (int j = 0; j < NA; ++j) db_a[j] = dsc[j] = 0.f;
-  float db_c = 0.f;
-  if (lane < R) {
-    const int r = r_begin + lane;
-    const int64_t s = p.idx ? (int64_t)p.idx[r] : (int64_t)r;
-    const float olp = p.old_logp[s], Av = p.adv[s], Rt = p.ret[s], vold = p.old_value[s];
-    const float eps = p.clip_eps;
-    const float inv_t = 1.f / p.temperature;
-    float out[NA];
-#pragma unroll
-    for (int j = 0; j < NA; ++j) out[j] = s_out[wave][lane][j] + (j < p.na ? p.ba[j] : 0.f);
-    const float v = SEP ? s_out[wave][lane][NA] + p.bc[0] : out[p.na - 1];
-
-    float lp = 0.f, ent = 0.f;
-    float dout[NA];
-#pragma unroll
-    for (int j = 0; j < NA; ++j) dout[j] = 0.f;
-    float lse = 0.f;
-    int a = 0;
-    if (p.dist == DIST_CATEGORICAL) {
-      float mx = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < NA; ++j) if (j < A) mx = fmaxf(mx, out[j] * inv_t);
-      float se = 0.f;
-#pragma unroll
-      for (int j = 0; j < NA; ++j) if (j < A) se += __expf(out[j] * inv_t - mx);
-      lse = mx + __logf(se);
-      a = p.action_i[s];
-      float za = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < NA; ++j) za = (j == a) ? out[j] * inv_t : za;
-      lp = (a >= 0 && a < A) ? za - lse : -INFINITY;
-#pragma unroll
-      for (int j = 0; j < NA; ++j)
-        if (j < A) {
-          const float lq = out[j] * inv_t - lse;
-          ent -= __expf(lq) * lq;
+          for (int q = 0; q < 16; ++q) raw = (q == A + j) ? out[q] : raw;
         }
-    } else {
+        const float sig = p.temperature * (softplusf(raw) + 1e-3f);
+        const float d = p.action_f[s * A + j] - out[j];
+        dout[j] = g_lp * d / (sig * sig);
+        const float dsig = g_lp * (d * d / (sig * sig * sig) - 1.f / sig) + g_ent / sig;
+        const float draw = dsig * p.temperature / (1.f + __expf(-raw));
+        if (p.scale_param) {
+          dsc[j] += draw;
+        } else {
 #pragma unroll
-      for (int j = 0; j < NA; ++j)
-        if (j < A) {
-          float raw = 0.f;
-          if (p.scale_param) {
-            raw = p.scale_param[j];
-          } else {
-#pragma unroll
-            for (int q = 0; q < NA; ++q) raw = (q == A + j) ? out[q] : raw;
-          }
-          const float sig = p.temperature * (softplusf(raw) + 1e-3f);
-          const float zz = (p.action_f[s * A + j] - out[j]) / sig;
-          const float ls = __logf(sig);
-          lp += -0.5f * zz * zz - ls - 0.5f * LOG_2PI;
-          ent += 0.5f + 0.5f * LOG_2PI + ls;
-        }
-    }
-
-    // loss terms and cotangents (jax tie rules for min / max / clip)
-    const float ratio = __expf(lp - olp);
-    float cr, dcr;
-    clip_grad(ratio, 1.f - eps, 1.f + eps, cr, dcr);
-    const float pg1 = ratio * Av, pg2 = cr * Av;
-    const float pmin = fminf(pg1, pg2);
-    const float g_lp = -(tie_first(pg1, pg2, pmin) * Av + tie_first(pg2, pg1, pmin) * Av * dcr) * p.inv_n * ratio;
-    const float g_ent = -p.ent_coef * p.inv_n;
-    const float vl1 = 0.5f * (v - Rt) * (v - Rt);
-    float crow, gv;
-    if (p.clip_value_loss) {
-      float dv, ddv;
-      clip_grad(v - vold, -eps, eps, dv, ddv);
-      const float vc = vold + dv;
-      const float vl2 = 0.5f * (vc - Rt) * (vc - Rt);
-      crow = fmaxf(vl1, vl2);
-      gv = tie_first(vl1, vl2, crow) * (v - Rt) + tie_first(vl2, vl1, crow) * (vc - Rt) * ddv;
-    } else {
-      crow = vl1;
-      gv = v - Rt;
-    }
-    const float dvalue = p.vf_coef * gv * p.inv_n;
-
-    if (p.dist == DIST_CATEGORICAL) {
-#pragma unroll
-      for (int j = 0; j < NA; ++j)
-        if (j < A) {
-          const float lq = out[j] * inv_t - lse;
-          const float q = __expf(lq);
-          dout[j] = (g_lp * ((j == a ? 1.f : 0.f) - q) - g_ent * q * (lq + ent)) * inv_t;
-        }
-    } else {
-#pragma unroll
-      for (int j = 0; j < NA; ++j)
-        if (j < A) {
-          float raw = 0.f;
-          if (p.scale_param) {
-            raw = p.scale_param[j];
-          } else {
-#pragma unroll
-            for (int q = 0; q < NA; ++q) raw = (q == A + j) ? out[q] : raw;
-          }
-          const float sig = p.temperature * (softplusf(raw) + 1e-3f);
-          const float d = p.action_f[s * A + j] - out[j];
-          dout[j] = g_lp * d / (sig * sig);
-          const float dsig = g_lp * (d * d / (sig * sig * sig) - 1.f / sig) + g_ent / sig;
-          const float draw = dsig * p.temperature / (1.f + __expf(-raw));
-          if (p.scale_param) {
-            dsc[j] += draw;
-          } else {
-#pragma unroll
-            for (int q = 0; q < NA; ++q) dout[q] = (q == A + j) ? draw : dout[q];
-          }
-        }
-    }
-    if (!SEP) {
-#pragma unroll
-      for (int j = 0; j < NA; ++j) dout[j] = (j == p.na - 1) ? dvalue : dout[j];
-    }
-#pragma unroll
-    for (int j = 0; j < NA; ++j) {
-      s_dout[wave][lane][j] = dout[j];
-      db_a[j] += dout[j];
-    }
-    s_dout[wave][lane][NA] = dvalue;
-    db_c += dvalue;
-
-    st[ST_ACTOR] += (double)(-pmin);
-    st[ST_ENTROPY] += (double)ent;
-    st[ST_KL] += (double)(olp - lp);
-    st[ST_CLIPFRAC] += (fabsf(ratio - 1.f) > eps) ? 1.0 : 0.0;
-    st[ST_ADV] += (double)Av;
-    st[ST_CRITIC] += (double)crow;
-    const double res = (double)Rt - (double)v;
-    st[ST_RESID] += res;
-    st[ST_RESID2] += res * res;
-    st[ST_RET] += (double)Rt;
-    st[ST_RET2] += (double)Rt * (double)Rt;
-    st[ST_VALUE] += (double)v;
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-  // ---------------- phase C: head backward, one wavefront per row
-  // The activation derivative reads the layer output itself for relu / tanh
-  // (aux == h) and the pre-activation for silu.
-  const bool load_xa = p.act_a != ACT_NONE && !(p.aux_a == p.ha && p.ldaux_a == p.ldha);
-  const bool load_xc = SEP && p.act_c != ACT_NONE && !(p.aux_c == p.hc && p.ldaux_c == p.ldhc);
-  float acc_a[VPL][NA];
-  float acc_c[VPL];
-#pragma unroll
-  for (int e = 0; e < VPL; ++e) {
-    acc_c[e] = 0.f;
-#pragma unroll
-    for (int j = 0; j < NA; ++j) acc_a[e][j] = 0.f;
-  }
-  {
-    float hb[2][VPL], hcb[2][VPL], xab[2][VPL], xcb[2][VPL];
-    auto fetch = [&](int row, float (&h)[VPL], float (&hc)[VPL], float (&xa)[VPL], float (&xc)[VPL]) {
-#pragma unroll
-      for (int e = 0; e < VPL; ++e) {
-        const int f = lane + 64 * e;
-        const bool ok = row < r_end && f < F;
-        h[e] = ok ? p.ha[(int64_t)row * p.ldha + f] : 0.f;
-        xa[e] = (ok && load_xa) ? p.aux_a[(int64_t)row * p.ldaux_a + f] : h[e];
-        hc[e] = (SEP && ok) ? p.hc[(int64_t)row * p.ldhc + f] : 0.f;
-        xc[e] = (ok && load_xc) ? p.aux_c[(int64_t)row * p.ldaux_c + f] : hc[e];
-      }
-    };
-    auto step = [&](int k, float (&h)[VPL], float (&hc)[VPL], float (&xa)[VPL], float (&xc)[VPL]) {
-      const int r = r_begin + k;
-      float dout[NA];
-#pragma unroll
-      for (int j = 0; j < NA; ++j) dout[j] = s_dout[wave][k][j];
-      const float dvalue = s_dout[wave][k][NA];
-#pragma unroll
-      for (int e = 0; e < VPL; ++e) {
-        const int f = lane + 64 * e;
-        float g = 0.f;
-#pragma unroll
-        for (int j = 0; j < NA; ++j) {
-          g += dout[j] * wa[e][j];
-          acc_a[e][j] += h[e] * dout[j];
-        }
-        if (f < F) {
-          if (p.act_a != ACT_NONE) g *= ppo::act_grad(p.act_a, xa[e]);
-          p.dha[(int64_t)r * p.lddha + f] = g;
-        }
-        if (SEP) {
-          float gc = dvalue * wc[e];
-          acc_c[e] += hc[e] * dvalue;
-          if (f < F) {
-            if (p.act_c != ACT_NONE) gc *= ppo::act_grad(p.act_c, xc[e]);
-            p.dhc[(int64_t)r * p.lddhc + f] = gc;
-          }
+          for (int q = 0; q < 16; ++q) dout[q] = (q == A + j) ? draw : dout[q];
         }
       }
-      fetch(r + 2, h, hc, xa, xc);
-    };
-    fetch(r_begin, hb[0], hcb[0], xab[0], xcb[0]);
-    fetch(r_begin + 1, hb[1], hcb[1], xab[1], xcb[1]);
-    for (int k = 0; k < R; k += 2) {
-      step(k, hb[0], hcb[0], xab[0], xcb[0]);
-      if (k + 1 < R) step(k + 1, hb[1], hcb[1], xab[1], xcb[1]);
-    }
   }
-
-  // ---- fold lanes, then the block's waves, in a fixed order
+  if (!sep) {
 #pragma unroll
-  for (int i = 0; i < NSTAT; ++i) st[i] = ppo::wave_sum_d(st[i]);
-#pragma unroll
-  for (int j = 0; j < NA; ++j) {
-    db_a[j] = ppo::wave_sum(db_a[j]);
-    dsc[j] = ppo::wave_sum(dsc[j]);
+    for (int j = 0; j < 16; ++j) dout[j] = (j == p.na - 1) ? dvalue : dout[j];
   }
-  db_c = ppo::wave_sum(db_c);
-  if (lane == 0) {
-#pragma unroll
-    for (int i = 0; i < NSTAT; ++i) s_stats[wave][i] = st[i];
-#pragma unroll
-    for (int j = 0; j < NA; ++j) {
-      s_vec[wave][0][j] = db_a[j];
-      s_vec[wave][2][j] = dsc[j];
-    }
-    s_vec[wave][1][0] = db_c;
-  }
-  float* fold = smem;  // [F][NA + 1]
-  const int ldf = NA + 1;
-  for (int w = 0; w < HL_WAVES; ++w) {
-    if (wave == w) {
-#pragma unroll
-      for (int e = 0; e < VPL; ++e) {
-        const int f = lane + 64 * e;
-        if (f < F) {
-#pragma unroll
-          for (int j = 0; j < NA; ++j) fold[f * ldf + j] = (w ? fold[f * ldf + j] : 0.f) + acc_a[e][j];
-          fold[f * ldf + NA] = (w ? fold[f * ldf + NA] : 0.f) + acc_c[e];
-        }
-      }
-    }
-    __syncthreads();
-  }
-  const int64_t blk = blockIdx.x;
-  for (int i = threadIdx.x; i < F * (int)p.ldwa; i += HL_THREADS) {
-    const int f = i / (int)p.ldwa, j = i % (int)p.ldwa;
-    p.wpart_a[blk * F * p.ldwa + i] = j < NA ? fold[f * ldf + j] : 0.f;
-  }
-  if (SEP) {
-    for (int i = threadIdx.x; i < F * (int)p.ldwc; i += HL_THREADS) {
-      const int f = i / (int)p.ldwc, j = i % (int)p.ldwc;
-      p.wpart_c[blk * F * p.ldwc + i] = j == 0 ? fold[f * ldf + NA] : 0.f;
-    }
-  }
-  if (threadIdx.x < (int)p.ldwa) {
-    float t = 0.f;
-    for (int w = 0; w < HL_WAVES; ++w) t += threadIdx.x < NA ? s_vec[w][0][threadIdx.x] : 0.f;
-    p.bpart_a[blk * p.ldwa + threadIdx.x] = t;
-  }
-  if (SEP && threadIdx.x < (int)p.ldwc) {
-    float t = 0.f;
-    for (int w = 0; w < HL_WAVES; ++w) t += threadIdx.x == 0 ? s_vec[w][1][0] : 0.f;
-    p.bpart_c[blk * p.ldwc + threadIdx.x] = t;
-  }
-  if (p.scale_param && threadIdx.x < A) {
-    float t = 0.f;
-    for (int w = 0; w < HL_WAVES; ++w) t += s_vec[w][2][threadIdx.x];
-    p.dscale_partial[blk * A + threadIdx.x] = t;
-  }
-  if (threadIdx.x < NSTAT) {
-    double t = 0.0;
-    for (int w = 0; w < HL_WAVES; ++w) t += s_stats[w][threadIdx.x];
-    p.stats_partial[blk * NSTAT + threadIdx.x] = t;
-  }
+  st[ST_ACTOR] += (double)(-pmin);
+  st[ST_ENTROPY] += (double)ent;
+  st[ST_KL] += (double)(olp - lp);
+  st[ST_CLIPFRAC] += (fabsf(ratio - 1.f) > eps) ? 1.0 : 0.0;
+  st[ST_ADV] += (double)Av;
+  st[ST_CRITIC] += (double)crow;
+  const double res = (double)Rt - (double)v;
+  st[ST_RESID] += res;
+  st[ST_RESID2] += res * res;
+  st[ST_RET] += (double)Rt;
+  st[ST_RET2] += (double)Rt * (double)Rt;
+  st[ST_VALUE] += (double)v;
 }
 
-template <int VPL, int NA, bool SEP>
-int launch(hipStream_t st, const HeadLossParams& p, int blocks) {
-  const size_t shm = sizeof(float) * (size_t)p.F * (NA + 1);
-  hipLaunchKernelGGL((head_loss_kernel<VPL, NA, SEP>), dim3(blocks), dim3(HL_THREADS), shm, st, p);
-  return ppo::check_launch("ppo_head_loss_f32");
-}
-
-template <int VPL, bool SEP>
-int launch_na(hipStream_t st, const HeadLossParams& p, int blocks) {
-  if (p.na <= 4) return launch<VPL, 4, SEP>(st, p, blocks);
-  if (p.na <= 8) return launch<VPL, 8, SEP>(st, p, blocks);
-  return launch<VPL, 16, SEP>(st, p, blocks);
+__device__ __forceinline__ floatx4 mfma4(floatx4 a, const float (&b)[4], floatx4 acc) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], acc, 0, 0, 0);
+  return acc;
 }
 
 template <bool SEP>
-int launch_vpl(hipStream_t st, const HeadLossParams& p, int blocks) {
-  const int vpl = ppo::ceil_div(p.F, 64);
-  if (vpl <= 1) return launch_na<1, SEP>(st, p, blocks);
-  if (vpl <= 2) return launch_na<2, SEP>(st, p, blocks);
-  if (vpl <= 4) return launch_na<4, SEP>(st, p, blocks);
-  return launch_na<8, SEP>(st, p, blocks);
+__global__ void __launch_bounds__(HL_THREADS) head_loss_kernel(HeadLossParams p) {
+  __shared__ __attribute__((aligned(16))) float s_out[TR][LDO];
+  __shared__ __attribute__((aligned(16))) float s_dout[TR][LDO];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 15;   // MFMA row (A) / column (B, D)
+  const int kq = lane >> 4;   // MFMA k group; D rows 4 * kq + v
+  const int F = p.F;
+  const int r0 = blockIdx.x * TR;
+  const int64_t blk = blockIdx.x;
+
+  // ---------------- A. head outputs of the wave's 16 rows
+  {
+    const int row = r0 + 16 * wave + li;
+    const bool live = row < p.rows;
+    const float* hrow = p.ha + (int64_t)(live ? row : 0) * p.ldha;
+    const float* crow = SEP ? p.hc + (int64_t)(live ? row : 0) * p.ldhc : nullptr;
+    const bool jv = li < p.na;
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f}, accc = {0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < F; kb += 16) {
+      const int k = kb + 4 * kq;
+      const floatx4 av = live ? *reinterpret_cast<const floatx4*>(hrow + k) : floatx4{0.f, 0.f, 0.f, 0.f};
+      float bv[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) bv[s] = jv ? p.wa[(int64_t)(k + s) * p.ldwa + li] : 0.f;
+      acc = mfma4(av, bv, acc);
+      if (SEP) {
+        const floatx4 cv = live ? *reinterpret_cast<const floatx4*>(crow + k) : floatx4{0.f, 0.f, 0.f, 0.f};
+        float wv[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) wv[s] = li == 0 ? p.wc[(int64_t)(k + s) * p.ldwc] : 0.f;
+        accc = mfma4(cv, wv, accc);
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      s_out[16 * wave + 4 * kq + v][li] = acc[v];
+      if (SEP && li == 0) s_out[16 * wave + 4 * kq + v][16] = accc[v];
+    }
+  }
+  __syncthreads();
+
+  // ---------------- B. loss and output cotangents, one lane of wave 0 per row
+  if (wave == 0) {
+    double st[NSTAT];
+#pragma unroll
+    for (int i = 0; i < NSTAT; ++i) st[i] = 0.0;
+    float db[16], dsc[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) db[j] = dsc[j] = 0.f;
+    float dbc = 0.f;
+    const int r = r0 + lane;
+    float dout[16];
+    float dvalue = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) dout[j] = 0.f;
+    if (r < p.rows) {
+      const int64_t s = p.idx ? (int64_t)p.idx[r] : (int64_t)r;
+      float out[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) out[j] = s_out[lane][j] + (j < p.na ? p.ba[j] : 0.f);
+      const float v = SEP ? s_out[lane][16] + p.bc[0] : out[p.na - 1];
+      row_loss(p, SEP, s, out, v, dout, dvalue, st, dsc);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) db[j] = dout[j];
+      dbc = dvalue;
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s_dout[lane][j] = dout[j];
+    s_dout[lane][16] = dvalue;
+    // block partials: statistics, head biases, Gaussian scale (fixed-order wave sums)
+#pragma unroll
+    for (int i = 0; i < NSTAT; ++i) st[i] = ppo::wave_sum_d(st[i]);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      db[j] = ppo::wave_sum(db[j]);
+      dsc[j] = ppo::wave_sum(dsc[j]);
+    }
+    dbc = ppo::wave_sum(dbc);
+    if (lane < NSTAT) {
+      double t = 0.0;
+#pragma unroll
+      for (int i = 0; i < NSTAT; ++i) t = (i == lane) ? st[i] : t;
+      p.stats_partial[blk * NSTAT + lane] = t;
+    }
+    if (lane < (int)p.ldwa) {
+      float t = 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) t = (j == lane) ? db[j] : t;
+      p.bpart_a[blk * p.ldwa + lane] = t;
+    }
+    if (SEP && lane < (int)p.ldwc) p.bpart_c[blk * p.ldwc + lane] = lane == 0 ? dbc : 0.f;
+    if (p.scale_param && lane < p.A) {
+      float t = 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) t = (j == lane) ? dsc[j] : t;
+      p.dscale_partial[blk * p.A + lane] = t;
+    }
+  }
+  __syncthreads();
+
+  // ---------------- C1. cotangent of the head inputs (the wave's 16 rows)
+  {
+    const floatx4 dv4 = *reinterpret_cast<const floatx4*>(&s_dout[16 * wave + li][4 * kq]);
+    const bool live_a = r0 + 16 * wave + li < p.rows;
+    for (int fb = 0; fb < F; fb += 16) {
+      const int f = fb + li;  // B column = output feature
+      float bv[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int j = 4 * kq + s;
+        bv[s] = j < p.na ? p.wa[(int64_t)f * p.ldwa + j] : 0.f;
+      }
+      const floatx4 g = mfma4(live_a ? dv4 : floatx4{0.f, 0.f, 0.f, 0.f}, bv, floatx4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int rr = 16 * wave + 4 * kq + v;
+        const int row = r0 + rr;
+        if (row >= p.rows) continue;
+        float d = g[v];
+        if (p.act_a != ACT_NONE) d *= ppo::act_grad(p.act_a, p.aux_a[(int64_t)row * p.ldaux_a + f]);
+        p.dha[(int64_t)row * p.lddha + f] = d;
+        if (SEP) {
+          float dc = s_dout[rr][16] * p.wc[(int64_t)f * p.ldwc];
+          if (p.act_c != ACT_NONE) dc *= ppo::act_grad(p.act_c, p.aux_c[(int64_t)row * p.ldaux_c + f]);
+          p.dhc[(int64_t)row * p.lddhc + f] = dc;
+        }
+      }
+    }
+  }
+
+  // ---------------- C2. head weight gradient partial H^T dOUT (16-feature blocks dealt to the waves)
+  {
+    for (int fb = 16 * wave; fb < F; fb += 64) {
+      const int f = fb + li;  // A row = feature
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f}, accc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int cc = 0; cc < TR / 16; ++cc) {
+        floatx4 av, cv = {0.f, 0.f, 0.f, 0.f};
+        float bv[4], wv[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int rr = 16 * cc + 4 * kq + s;
+          const int row = r0 + rr;
+          const bool ok = row < p.rows;
+          av[s] = ok ? p.ha[(int64_t)row * p.ldha + f] : 0.f;
+          bv[s] = s_dout[rr][li];
+          if (SEP) {
+            cv[s] = ok ? p.hc[(int64_t)row * p.ldhc + f] : 0.f;
+            wv[s] = li == 0 ? s_dout[rr][16] : 0.f;
+          }
+        }
+        acc = mfma4(av, bv, acc);
+        if (SEP) accc = mfma4(cv, wv, accc);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int ff = fb + 4 * kq + v;
+        if (li < (int)p.ldwa) p.wpart_a[(blk * F + ff) * p.ldwa + li] = acc[v];
+        if (SEP && li < (int)p.ldwc) p.wpart_c[(blk * F + ff) * p.ldwc + li] = li == 0 ? accc[v] : 0.f;
+      }
+    }
+  }
 }
 
 }  // namespace
 
-// Blocks the fused kernel launches for `rows` (the partial buffers' leading extent).
-// At least enough waves that each owns <= 64 rows; up to 512 blocks otherwise.
-PPO_EXPORT int ppo_head_loss_blocks(int rows) {
-  const int need = ppo::ceil_div(rows, HL_WAVES * 64);
-  return std::max(std::max(1, need), std::min(ppo::ceil_div(rows, HL_WAVES * 16), 512));
-}
+// Blocks the fused kernel launches for `rows` (the partial buffers' leading
+// extent): one per 64-row tile.
+PPO_EXPORT int ppo_head_loss_blocks(int rows) { return std::max(1, ppo::ceil_div(rows, TR)); }
 
-// Largest head width (outputs of group a) and feature width the fused kernel takes.
+// Largest head width (outputs of group a) and feature width the fused kernel
+// takes; the feature width must also be a multiple of 16.
 PPO_EXPORT int ppo_head_loss_max_outputs(void) { return 16; }
 PPO_EXPORT int ppo_head_loss_max_features(void) { return 512; }
 
@@ -499,7 +386,8 @@ PPO_EXPORT int ppo_head_loss_f32(
     float* dscale_partial, double* stats_partial, float clip_eps, int clip_value_loss, float ent_coef,
     float vf_coef, float temperature) {
   const bool sep = hc != nullptr;
-  if (rows < 0 || F <= 0 || F > 512 || na <= 0 || na > 16 || ldwa < na || A <= 0 || A > 16 ||
+  if (rows < 0 || F <= 0 || F > 512 || F % 16 != 0 || na <= 0 || na > 16 || ldwa < na || ldwa > 16 || A <= 0 ||
+      A > 16 ||
       (dist != DIST_CATEGORICAL && dist != DIST_GAUSSIAN) || !ha || !wa || !ba || !old_logp || !old_value ||
       !adv || !ret || !dha || !wpart_a || !bpart_a || !stats_partial || temperature <= 0.f)
     return ppo::set_error(PPO_ERR_ARG, "ppo_head_loss_f32: bad argument (rows=%d F=%d na=%d A=%d)", rows, F, na, A);
@@ -510,6 +398,9 @@ PPO_EXPORT int ppo_head_loss_f32(
   if (scale_param && !dscale_partial) return ppo::set_error(PPO_ERR_ARG, "ppo_head_loss_f32: missing dscale buffer");
   if ((act_a != ACT_NONE && !aux_a) || (sep && act_c != ACT_NONE && !aux_c))
     return ppo::set_error(PPO_ERR_ARG, "ppo_head_loss_f32: activation derivative needs aux");
+  if (sep && ldwc > 16) return ppo::set_error(PPO_ERR_ARG, "ppo_head_loss_f32: ldwc > 16");
+  if ((reinterpret_cast<uintptr_t>(ha) & 15) || ldha % 4 || (sep && ((reinterpret_cast<uintptr_t>(hc) & 15) || ldhc % 4)))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_head_loss_f32: head inputs need 16-byte aligned rows");
   if (rows == 0) return PPO_OK;
   HeadLossParams p;
   p.dist = dist; p.rows = rows; p.idx = idx;
@@ -525,5 +416,7 @@ PPO_EXPORT int ppo_head_loss_f32(
   p.inv_n = 1.f / (float)rows; p.temperature = temperature;
   const int blocks = ppo_head_loss_blocks(rows);
   hipStream_t st = ppo::as_stream(stream);
-  return sep ? launch_vpl<true>(st, p, blocks) : launch_vpl<false>(st, p, blocks);
+  if (sep) hipLaunchKernelGGL(head_loss_kernel<true>, dim3(blocks), dim3(HL_THREADS), 0, st, p);
+  else hipLaunchKernelGGL(head_loss_kernel<false>, dim3(blocks), dim3(HL_THREADS), 0, st, p);
+  return ppo::check_launch("ppo_head_loss_f32");
 }

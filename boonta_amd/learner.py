@@ -368,7 +368,8 @@ class MLPExecutor:
             if not program.actor_layers or not program.critic_layers or ha.fin != hc.fin:
                 return False
             na = program.head_out
-        return na <= lib.ppo_head_loss_max_outputs() and ha.fin <= lib.ppo_head_loss_max_features()
+        return (na <= lib.ppo_head_loss_max_outputs() and ha.fin <= lib.ppo_head_loss_max_features()
+                and ha.fin % 16 == 0)
 
     # ------------------------------------------------------ gradient tables
     def _build_reduce_tables(self):

@@ -349,3 +349,117 @@ def test_grad_reduce_and_adam_match_optax_restatement(max_norm, scale):
     np.testing.assert_allclose(host(MU), st2["mu"]["w"], rtol=1e-5, atol=1e-9)
     np.testing.assert_allclose(host(NU), st2["nu"]["w"], rtol=1e-5, atol=1e-12)
     np.testing.assert_allclose(host(P), new["w"], rtol=1e-6, atol=1e-7)
+
+
+# ------------------------------------------------------- fused heads + loss
+@pytest.mark.parametrize("sep, dist, A, F, rows, act", [
+    (False, "categorical", 15, 128, 100, "relu"),     # packed heads, 15 logits + value = 16 outputs
+    (True, "gaussian", 4, 64, 197, "tanh"),           # separate towers, state-dependent scale
+    (True, "gaussian", 8, 256, 64, "silu"),           # separate towers, state-independent scale
+    (True, "categorical", 2, 64, 1, "tanh"),          # a single row
+    (False, "categorical", 6, 256, 4099, "none"),     # ragged last tile
+])
+def test_fused_heads_loss_and_head_backward(sep, dist, A, F, rows, act):
+    g = np.random.default_rng(F + rows + A)
+    B = rows + 37
+    spread = dist == "gaussian" and F == 256
+    width = A if (dist == "categorical" or spread) else 2 * A
+    na = width if sep else width + 1
+    ldw = (na + 3) // 4 * 4
+    z = g.normal(0, 1, (rows, F)).astype(np.float32)          # the torso's last pre-activations
+    zc = g.normal(0, 1, (rows, F)).astype(np.float32)
+    ha = act_np(act, z).astype(np.float32)
+    hc = act_np(act, zc).astype(np.float32) if sep else None
+    wa = np.zeros((F, ldw), np.float32)
+    wa[:, :na] = g.normal(0, 1 / np.sqrt(F), (F, na))
+    ba = np.zeros(ldw, np.float32)
+    ba[:na] = g.normal(0, 0.1, na)
+    wc = g.normal(0, 1 / np.sqrt(F), (F, 4)).astype(np.float32)
+    wc[:, 1:] = 0
+    bc = np.array([0.3, 0, 0, 0], np.float32)
+    idx = g.permutation(B)[:rows].astype(np.int32)
+    action = (g.integers(0, A, B).astype(np.int32) if dist == "categorical"
+              else g.standard_normal((B, A)).astype(np.float32))
+    scale = g.normal(0, 0.5, A).astype(np.float32) if spread else None
+    old_logp = g.normal(-1.5, 0.3, B).astype(np.float32)
+    old_value = g.normal(0, 1, B).astype(np.float32)
+    adv = g.normal(0, 1, B).astype(np.float32)
+    ret = g.normal(0, 1, B).astype(np.float32)
+    # oracle: heads in float64, the loss, its cotangents, then the head backward
+    ha64, wa64 = ha.astype(np.float64), wa[:, :na].astype(np.float64)
+    out = ha64 @ wa64 + ba[:na]
+    value = (hc.astype(np.float64) @ wc[:, 0] + bc[0]) if sep else out[:, na - 1]
+    if dist == "categorical":
+        lp, ent, cache = nets.categorical_stats(out[:, :A], action[idx])
+    else:
+        raw = np.broadcast_to(scale.astype(np.float64), (rows, A)) if spread else out[:, A:2 * A]
+        mean = out[:, :A]
+        sig = nets.gaussian_sigma(raw)
+        lp, ent = nets.gaussian_stats(mean, sig, action[idx].astype(np.float64))
+    loss, logs, (g_lp, g_ent, g_v) = ppo.loss_terms(lp, ent, value, old_logp[idx].astype(np.float64),
+                                                    old_value[idx].astype(np.float64),
+                                                    adv[idx].astype(np.float64), ret[idx].astype(np.float64), CFG)
+    dout = np.zeros((rows, na))
+    if dist == "categorical":
+        dout[:, :A] = nets.categorical_grad(cache, action[idx], g_lp, g_ent)
+    else:
+        dmean, dsig = nets.gaussian_grad(mean, sig, action[idx].astype(np.float64), g_lp, g_ent)
+        draw = dsig / (1 + np.exp(-raw))
+        dout[:, :A] = dmean
+        if not spread:
+            dout[:, A:2 * A] = draw
+    if not sep:
+        dout[:, na - 1] = g_v
+    def dact(pre, post):
+        if act == "none":
+            return np.ones_like(pre, np.float64)
+        return nets.act_bwd(act, pre.astype(np.float64), post.astype(np.float64), np.ones_like(pre, np.float64))
+    # the kernel reads the activation output for relu / tanh and its input for silu
+    aux_a, aux_c = (z, zc) if act == "silu" else (ha, hc)
+    dha_ref = (dout @ wa64.T) * dact(z, ha)
+    dwa_ref = ha64.T @ dout
+    # GPU
+    HA, WA, BA, WC, BC = dev(ha), dev(wa), dev(ba), dev(wc), dev(bc)
+    HC = dev(hc) if sep else None
+    XA = dev(aux_a)
+    XC = dev(aux_c) if sep else None
+    blocks = _lib.load().ppo_head_loss_blocks(rows)
+    DHA = torch.zeros(rows, F, device=DEV)
+    DHC = torch.zeros(rows, F, device=DEV) if sep else None
+    WPA = torch.full((blocks, F, ldw), float("nan"), device=DEV)
+    BPA = torch.full((blocks, ldw), float("nan"), device=DEV)
+    WPC = torch.full((blocks, F, 4), float("nan"), device=DEV) if sep else None
+    BPC = torch.full((blocks, 4), float("nan"), device=DEV) if sep else None
+    DS = torch.zeros(blocks, A, device=DEV) if spread else None
+    STATS = torch.zeros(blocks, 11, dtype=torch.float64, device=DEV)
+    IDX, ACT = dev(idx), dev(action)
+    OLP, OV, ADV, RET = dev(old_logp), dev(old_value), dev(adv), dev(ret)
+    SC = dev(scale) if spread else None
+    a_code = _lib.ACT[act]
+    p = lambda t: None if t is None else t.data_ptr()
+    _lib.call("ppo_head_loss_f32", st(), _lib.DIST[dist], rows, IDX.data_ptr(), HA.data_ptr(), F, WA.data_ptr(), ldw,
+              BA.data_ptr(), na, p(HC), F, p(WC) if sep else None, 4, p(BC) if sep else None, F, A, p(SC),
+              ACT.data_ptr() if dist == "categorical" else None, ACT.data_ptr() if dist == "gaussian" else None,
+              OLP.data_ptr(), OV.data_ptr(), ADV.data_ptr(), RET.data_ptr(), a_code, XA.data_ptr(), F,
+              DHA.data_ptr(), F, a_code if sep else 0, p(XC), F, p(DHC), F, WPA.data_ptr(),
+              BPA.data_ptr(), p(WPC), p(BPC), p(DS), STATS.data_ptr(), 0.2, 1, 0.01, 0.5, 1.0)
+    outv = torch.zeros(9, device=DEV)
+    _lib.call("ppo_loss_finalize", st(), STATS.data_ptr(), blocks, rows, 0.01, 0.5, outv.data_ptr())
+    np.testing.assert_allclose(host(DHA), dha_ref, rtol=1e-4, atol=1e-7)
+    wpa = host(WPA).astype(np.float64).sum(0)
+    np.testing.assert_allclose(wpa[:, :na], dwa_ref, rtol=1e-4, atol=1e-7)
+    np.testing.assert_array_equal(wpa[:, na:], 0.0)
+    bpa = host(BPA).astype(np.float64).sum(0)
+    np.testing.assert_allclose(bpa[:na], dout.sum(0), rtol=1e-4, atol=1e-7)
+    if sep:
+        dhc_ref = np.outer(g_v, wc[:, 0]) * dact(zc, hc)
+        np.testing.assert_allclose(host(DHC), dhc_ref, rtol=1e-4, atol=1e-8)
+        wpc = host(WPC).astype(np.float64).sum(0)
+        np.testing.assert_allclose(wpc[:, 0], hc.astype(np.float64).T @ g_v, rtol=1e-4, atol=1e-8)
+        np.testing.assert_array_equal(wpc[:, 1:], 0.0)
+        np.testing.assert_allclose(host(BPC).astype(np.float64).sum(0)[0], g_v.sum(), rtol=1e-4, atol=1e-8)
+    if spread:
+        np.testing.assert_allclose(host(DS).astype(np.float64).sum(0), draw.sum(0), rtol=1e-4, atol=1e-7)
+    o = host(outv)
+    np.testing.assert_allclose(o[8], loss, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(o[1], logs["actor/entropy"], rtol=1e-5, atol=1e-6)
