@@ -16,8 +16,10 @@
 //      block's statistic, bias and Gaussian-scale partials;
 //   C1. the cotangent of each head input, dH[64, F] = dOUT[64, 16] Wa^T times
 //      the derivative of the torso's last activation (each wave 16 rows);
-//   C2. the head weight gradient partial H^T dOUT [F, 16] (each wave a quarter
-//      of F).
+//   C2. the head weight gradient partial H^T dOUT [F, 16] (16-feature blocks
+//      dealt round-robin to the waves).
+// Every loop issues the loads of four 16-wide steps before their MFMAs, so
+// four global round trips overlap.
 // Per-block partials are summed in a fixed order by the gradient reduce, so
 // results do not depend on scheduling.  F must be a multiple of 16 (<= 512)
 // and the heads have at most 16 outputs.
@@ -219,19 +221,26 @@ __global__ void __launch_bounds__(HL_THREADS) head_loss_kernel(HeadLossParams p)
     const float* crow = SEP ? p.hc + (int64_t)(live ? row : 0) * p.ldhc : nullptr;
     const bool jv = li < p.na;
     floatx4 acc = {0.f, 0.f, 0.f, 0.f}, accc = {0.f, 0.f, 0.f, 0.f};
-    for (int kb = 0; kb < F; kb += 16) {
-      const int k = kb + 4 * kq;
-      const floatx4 av = live ? *reinterpret_cast<const floatx4*>(hrow + k) : floatx4{0.f, 0.f, 0.f, 0.f};
-      float bv[4];
+    for (int k0 = 0; k0 < F; k0 += 64) {
+      floatx4 av[4], cv[4];
+      float bv[4][4], wv[4][4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) bv[s] = jv ? p.wa[(int64_t)(k + s) * p.ldwa + li] : 0.f;
-      acc = mfma4(av, bv, acc);
-      if (SEP) {
-        const floatx4 cv = live ? *reinterpret_cast<const floatx4*>(crow + k) : floatx4{0.f, 0.f, 0.f, 0.f};
-        float wv[4];
+      for (int u = 0; u < 4; ++u) {
+        const int k = k0 + 16 * u + 4 * kq;
+        const bool in = live && k0 + 16 * u < F;
+        av[u] = in ? *reinterpret_cast<const floatx4*>(hrow + k) : floatx4{0.f, 0.f, 0.f, 0.f};
+        if (SEP) cv[u] = in ? *reinterpret_cast<const floatx4*>(crow + k) : floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < 4; ++s) wv[s] = li == 0 ? p.wc[(int64_t)(k + s) * p.ldwc] : 0.f;
-        accc = mfma4(cv, wv, accc);
+        for (int s = 0; s < 4; ++s) {
+          const bool kin = k0 + 16 * u < F;
+          bv[u][s] = (jv && kin) ? p.wa[(int64_t)(k + s) * p.ldwa + li] : 0.f;
+          if (SEP) wv[u][s] = (li == 0 && kin) ? p.wc[(int64_t)(k + s) * p.ldwc] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        acc = mfma4(av[u], bv[u], acc);
+        if (SEP) accc = mfma4(cv[u], wv[u], accc);
       }
     }
 #pragma unroll
@@ -305,27 +314,42 @@ __global__ void __launch_bounds__(HL_THREADS) head_loss_kernel(HeadLossParams p)
   {
     const floatx4 dv4 = *reinterpret_cast<const floatx4*>(&s_dout[16 * wave + li][4 * kq]);
     const bool live_a = r0 + 16 * wave + li < p.rows;
-    for (int fb = 0; fb < F; fb += 16) {
-      const int f = fb + li;  // B column = output feature
-      float bv[4];
+    const floatx4 a_in = live_a ? dv4 : floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int f0 = 0; f0 < F; f0 += 64) {
+      float bv[4][4], xa[4][4], xc[4][4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int j = 4 * kq + s;
-        bv[s] = j < p.na ? p.wa[(int64_t)f * p.ldwa + j] : 0.f;
+      for (int u = 0; u < 4; ++u) {
+        const int f = f0 + 16 * u + li;  // B column = output feature
+        const bool fin = f0 + 16 * u < F;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int j = 4 * kq + s;
+          bv[u][s] = (fin && j < p.na) ? p.wa[(int64_t)f * p.ldwa + j] : 0.f;
+          const int row = r0 + 16 * wave + 4 * kq + s;
+          const bool ok = fin && row < p.rows;
+          xa[u][s] = (ok && p.act_a != ACT_NONE) ? p.aux_a[(int64_t)row * p.ldaux_a + f] : 0.f;
+          if (SEP) xc[u][s] = (ok && p.act_c != ACT_NONE) ? p.aux_c[(int64_t)row * p.ldaux_c + f] : 0.f;
+        }
       }
-      const floatx4 g = mfma4(live_a ? dv4 : floatx4{0.f, 0.f, 0.f, 0.f}, bv, floatx4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int rr = 16 * wave + 4 * kq + v;
-        const int row = r0 + rr;
-        if (row >= p.rows) continue;
-        float d = g[v];
-        if (p.act_a != ACT_NONE) d *= ppo::act_grad(p.act_a, p.aux_a[(int64_t)row * p.ldaux_a + f]);
-        p.dha[(int64_t)row * p.lddha + f] = d;
-        if (SEP) {
-          float dc = s_dout[rr][16] * p.wc[(int64_t)f * p.ldwc];
-          if (p.act_c != ACT_NONE) dc *= ppo::act_grad(p.act_c, p.aux_c[(int64_t)row * p.ldaux_c + f]);
-          p.dhc[(int64_t)row * p.lddhc + f] = dc;
+      for (int u = 0; u < 4; ++u) {
+        const int f = f0 + 16 * u + li;
+        if (f0 + 16 * u >= F) break;
+        const floatx4 g = mfma4(a_in, bv[u], floatx4{0.f, 0.f, 0.f, 0.f});
+        const float wcf = SEP ? p.wc[(int64_t)f * p.ldwc] : 0.f;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int rr = 16 * wave + 4 * kq + v;
+          const int row = r0 + rr;
+          if (row >= p.rows) continue;
+          float d = g[v];
+          if (p.act_a != ACT_NONE) d *= ppo::act_grad(p.act_a, xa[u][v]);
+          p.dha[(int64_t)row * p.lddha + f] = d;
+          if (SEP) {
+            float dc = s_dout[rr][16] * wcf;
+            if (p.act_c != ACT_NONE) dc *= ppo::act_grad(p.act_c, xc[u][v]);
+            p.dhc[(int64_t)row * p.lddhc + f] = dc;
+          }
         }
       }
     }
@@ -336,24 +360,28 @@ __global__ void __launch_bounds__(HL_THREADS) head_loss_kernel(HeadLossParams p)
     for (int fb = 16 * wave; fb < F; fb += 64) {
       const int f = fb + li;  // A row = feature
       floatx4 acc = {0.f, 0.f, 0.f, 0.f}, accc = {0.f, 0.f, 0.f, 0.f};
+      floatx4 av[TR / 16], cv[TR / 16];
 #pragma unroll
       for (int cc = 0; cc < TR / 16; ++cc) {
-        floatx4 av, cv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int row = r0 + 16 * cc + 4 * kq + s;
+          const bool ok = row < p.rows;
+          av[cc][s] = ok ? p.ha[(int64_t)row * p.ldha + f] : 0.f;
+          cv[cc][s] = (SEP && ok) ? p.hc[(int64_t)row * p.ldhc + f] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int cc = 0; cc < TR / 16; ++cc) {
         float bv[4], wv[4];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           const int rr = 16 * cc + 4 * kq + s;
-          const int row = r0 + rr;
-          const bool ok = row < p.rows;
-          av[s] = ok ? p.ha[(int64_t)row * p.ldha + f] : 0.f;
           bv[s] = s_dout[rr][li];
-          if (SEP) {
-            cv[s] = ok ? p.hc[(int64_t)row * p.ldhc + f] : 0.f;
-            wv[s] = li == 0 ? s_dout[rr][16] : 0.f;
-          }
+          wv[s] = (SEP && li == 0) ? s_dout[rr][16] : 0.f;
         }
-        acc = mfma4(av, bv, acc);
-        if (SEP) accc = mfma4(cv, wv, accc);
+        acc = mfma4(av[cc], bv, acc);
+        if (SEP) accc = mfma4(cv[cc], wv, accc);
       }
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
