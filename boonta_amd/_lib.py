@@ -37,6 +37,8 @@ SIGNATURES = {
     "ppo_gemm_f32": (I, [P, I, I, P, I64, P, P, I64, P, I64, I, I, I, I, I64, I, P, I, P, P, I64, P, I]),
     "ppo_gemm_bf16": (I, [P, I, I, P, I64, P, P, I64, P, I64, I, I, I, I, I64, I, P, I, I, P, I64, P, I]),
     "ppo_round_bf16": (I, [P, P, I64]),
+    "ppo_gemm_bf16s": (I, [P, I, I, I, I, P, I64, P, P, I64, P, I64, I, I, I, I, I64, I, P, I, I, P, I64, P, I]),
+    "ppo_cast_bf16": (I, [P, P, P, I64]),
     "ppo_layernorm_act_fwd_f32": (I, [P, P, I64, P, P, P, I64, P, P, I, I, F, I]),
     "ppo_layernorm_act_fwd_bf16": (I, [P, P, I64, P, P, P, I64, P, P, I, I, F, I]),
     "ppo_layernorm_act_bwd_bf16": (I, [P, P, I64, P, I64, P, P, P, P, P, I64, P, I, I, I]),

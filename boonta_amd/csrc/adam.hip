@@ -94,7 +94,7 @@ struct AdamParams {
   const float* g;
   float* mu;
   float* nu;
-  __bf16* p_bf16;  // optional compute copy of the parameters
+  void* p_bf16;    // optional bf16 image of the parameters (16-bit patterns)
   int64_t n;       // multiple of 4
   const double* sumsq;
   int nsumsq;
@@ -150,10 +150,11 @@ __global__ void __launch_bounds__(256) adam_kernel(AdamParams a) {
     reinterpret_cast<floatx4*>(a.nu)[i] = v;
     reinterpret_cast<floatx4*>(a.p)[i] = p;
     if (a.p_bf16) {
-      bf16x4 b;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) b[e] = (__bf16)p[e];
-      reinterpret_cast<bf16x4*>(a.p_bf16)[i] = b;
+      // the bf16 image a bf16-compute layer multiplies with (round to nearest even)
+      uint2 b;
+      b.x = ppo::bf16_bits(p[0]) | (ppo::bf16_bits(p[1]) << 16);
+      b.y = ppo::bf16_bits(p[2]) | (ppo::bf16_bits(p[3]) << 16);
+      reinterpret_cast<uint2*>(a.p_bf16)[i] = b;
     }
   }
 }
@@ -193,7 +194,7 @@ PPO_EXPORT int ppo_adam_clip_f32(void* stream, float* params, const float* grads
   if (((uintptr_t)params | (uintptr_t)grads | (uintptr_t)mu | (uintptr_t)nu) & 15u)
     return ppo::set_error(PPO_ERR_ARG, "ppo_adam_clip_f32: buffers must be 16-byte aligned");
   if (n == 0) return PPO_OK;
-  AdamParams a{params, grads, mu, nu, (__bf16*)params_bf16, n, sumsq, nsumsq, (float)max_norm, (float)(-lr),
+  AdamParams a{params, grads, mu, nu, params_bf16, n, sumsq, nsumsq, (float)max_norm, (float)(-lr),
                (float)b1, (float)b2, (float)(1.0 - b1), (float)(1.0 - b2), (float)eps, count_base, step_offset};
   const int blocks = (int)std::min<int64_t>(ppo::ceil_div64(n / 4, 256), 2048);
   hipLaunchKernelGGL(adam_kernel, dim3(blocks), dim3(256), 0, ppo::as_stream(stream), a);

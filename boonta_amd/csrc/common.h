@@ -63,6 +63,20 @@ __device__ __forceinline__ TileCoord xcd_tile() {
   return c;
 }
 
+// Loads that never branch: an out-of-range element reads a clamped, valid
+// address and the value is then replaced by zero.  A load under a divergent
+// branch makes the compiler wait for it at the branch join; these keep every
+// load of a stage in flight together.
+__device__ __forceinline__ floatx4 load4_or_zero(const float* p, int64_t i, bool ok) {
+  const floatx4 v = *reinterpret_cast<const floatx4*>(p + (ok ? i : 0));
+  return ok ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+}
+
+__device__ __forceinline__ float load_or_zero(const float* p, int64_t i, bool ok) {
+  const float v = p[ok ? i : 0];
+  return ok ? v : 0.f;
+}
+
 // Round to nearest even bf16 (NaN stays NaN), returned as the fp32 value
 // of that bf16 (bits() gives the 16-bit pattern).
 __device__ __forceinline__ uint32_t bf16_bits(float x) {

@@ -55,19 +55,32 @@ struct GemmParams {
   float* bias_grad;  // dW: [splits][N] column sums of B, or null
 };
 
+// Four consecutive elements of a (valid) row at i.  Out-of-range elements
+// read a clamped valid address and are flagged in `bits` (bit e set: element
+// e valid); the zeroing happens when the stage is written to LDS, after the
+// MFMAs of the current stage, so the loads stay in flight behind them.
 template <bool VEC>
-__device__ __forceinline__ floatx4 load4(const float* __restrict__ p, int i, int lim) {
+__device__ __forceinline__ floatx4 load4(const float* __restrict__ p, int i, int lim, bool ok, uint32_t& bits) {
   floatx4 v;
   if (VEC) {
-    if (i < lim) {
-      v = *reinterpret_cast<const floatx4*>(p + i);
-    } else {
-      v = floatx4{0.f, 0.f, 0.f, 0.f};
-    }
+    const bool in = ok && i < lim;
+    v = *reinterpret_cast<const floatx4*>(p + (in ? i : 0));
+    bits = in ? 0xfu : 0u;
   } else {
+    bits = 0u;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = (i + e < lim) ? p[i + e] : 0.f;
+    for (int e = 0; e < 4; ++e) {
+      const bool in = ok && i + e < lim;
+      v[e] = p[in ? i + e : 0];
+      bits |= in ? (1u << e) : 0u;
+    }
   }
+  return v;
+}
+
+__device__ __forceinline__ floatx4 masked(floatx4 v, uint32_t bits) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = ((bits >> e) & 1u) ? v[e] : 0.f;
   return v;
 }
 
@@ -113,31 +126,37 @@ __global__ void __launch_bounds__(256, 2) gemm_f32_kernel(GemmParams p) {
   const bool do_bsum = (p.bias_grad != nullptr) && (tc.m == 0) && (wm == 0);
 
   floatx4 ra[A_PER], rb[B_PER];
+  uint32_t ma[A_PER], mb[B_PER];
+  // A_K: each thread's A rows (gathered or not) are the same at every stage
+  const float* arow[A_K ? A_PER : 1];
+  bool arow_ok[A_K ? A_PER : 1];
+  if (A_K) {
+#pragma unroll
+    for (int j = 0; j < A_PER; ++j) {
+      const int gm = m0 + (tid + 256 * j) / (BK / 4);
+      const bool ok = gm < p.M;
+      const int gmc = ok ? gm : 0;
+      const int64_t row = p.rows ? (int64_t)p.rows[gmc] : (int64_t)gmc;
+      arow[j] = p.A + row * p.lda;
+      arow_ok[j] = ok;
+    }
+  }
 
   auto gload = [&](int k0) {
 #pragma unroll
     for (int j = 0; j < A_PER; ++j) {
       const int f = tid + 256 * j;
       if (A_K) {
-        const int r = f / (BK / 4);
         const int c = (f % (BK / 4)) * 4;
-        const int gm = m0 + r;
-        if (gm < p.M) {
-          const int64_t row = p.rows ? (int64_t)p.rows[gm] : (int64_t)gm;
-          ra[j] = load4<VA>(p.A + row * p.lda, k0 + c, ke);
-        } else {
-          ra[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-        }
+        ra[j] = load4<VA>(arow[j], k0 + c, ke, arow_ok[j], ma[j]);
       } else {
         const int r = f / (BM / 4);
         const int c = (f % (BM / 4)) * 4;
         const int k = k0 + r;
-        if (k < ke) {
-          const int64_t row = p.rows ? (int64_t)p.rows[k] : (int64_t)k;
-          ra[j] = load4<VA>(p.A + row * p.lda, m0 + c, p.M);
-        } else {
-          ra[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-        }
+        const bool ok = k < ke;
+        const int kc = ok ? k : 0;
+        const int64_t row = p.rows ? (int64_t)p.rows[kc] : (int64_t)kc;
+        ra[j] = load4<VA>(p.A + row * p.lda, m0 + c, p.M, ok, ma[j]);
       }
     }
 #pragma unroll
@@ -147,12 +166,14 @@ __global__ void __launch_bounds__(256, 2) gemm_f32_kernel(GemmParams p) {
         const int r = f / (BK / 4);
         const int c = (f % (BK / 4)) * 4;
         const int gn = n0 + r;
-        rb[j] = gn < p.N ? load4<VB>(p.B + (int64_t)gn * p.ldb, k0 + c, ke) : floatx4{0.f, 0.f, 0.f, 0.f};
+        const bool ok = gn < p.N;
+        rb[j] = load4<VB>(p.B + (int64_t)(ok ? gn : 0) * p.ldb, k0 + c, ke, ok, mb[j]);
       } else {
         const int r = f / (BN / 4);
         const int c = (f % (BN / 4)) * 4;
         const int k = k0 + r;
-        rb[j] = k < ke ? load4<VB>(p.B + (int64_t)k * p.ldb, n0 + c, p.N) : floatx4{0.f, 0.f, 0.f, 0.f};
+        const bool ok = k < ke;
+        rb[j] = load4<VB>(p.B + (int64_t)(ok ? k : 0) * p.ldb, n0 + c, p.N, ok, mb[j]);
       }
     }
   };
@@ -163,14 +184,14 @@ __global__ void __launch_bounds__(256, 2) gemm_f32_kernel(GemmParams p) {
       const int f = tid + 256 * j;
       const int r = A_K ? f / (BK / 4) : f / (BM / 4);
       const int c = A_K ? (f % (BK / 4)) * 4 : (f % (BM / 4)) * 4;
-      *reinterpret_cast<floatx4*>(&sA[buf][r][c]) = ra[j];
+      *reinterpret_cast<floatx4*>(&sA[buf][r][c]) = masked(ra[j], ma[j]);
     }
 #pragma unroll
     for (int j = 0; j < B_PER; ++j) {
       const int f = tid + 256 * j;
       const int r = B_K ? f / (BK / 4) : f / (BN / 4);
       const int c = B_K ? (f % (BK / 4)) * 4 : (f % (BN / 4)) * 4;
-      *reinterpret_cast<floatx4*>(&sB[buf][r][c]) = rb[j];
+      *reinterpret_cast<floatx4*>(&sB[buf][r][c]) = masked(rb[j], mb[j]);
     }
   };
 

@@ -61,15 +61,32 @@ using ppo::bf16_round;
 
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) { return bf16_bits(lo) | (bf16_bits(hi) << 16); }
 
+// Four consecutive elements of a (valid) row at i; out-of-range elements read a
+// clamped valid address and are flagged in `bits` (bit e set: element e valid).
+// They are zeroed when the stage is written to LDS, after the current stage's
+// MFMAs, so the loads stay in flight behind them.
 template <bool VEC>
-__device__ __forceinline__ floatx4 load4(const float* __restrict__ p, int i, int lim) {
+__device__ __forceinline__ floatx4 load4(const float* __restrict__ p, int i, int lim, bool ok, uint32_t& bits) {
   floatx4 v;
   if (VEC) {
-    v = (i < lim) ? *reinterpret_cast<const floatx4*>(p + i) : floatx4{0.f, 0.f, 0.f, 0.f};
+    const bool in = ok && i < lim;
+    v = *reinterpret_cast<const floatx4*>(p + (in ? i : 0));
+    bits = in ? 0xfu : 0u;
   } else {
+    bits = 0u;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = (i + e < lim) ? p[i + e] : 0.f;
+    for (int e = 0; e < 4; ++e) {
+      const bool in = ok && i + e < lim;
+      v[e] = p[in ? i + e : 0];
+      bits |= in ? (1u << e) : 0u;
+    }
   }
+  return v;
+}
+
+__device__ __forceinline__ floatx4 masked(floatx4 v, uint32_t bits) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = ((bits >> e) & 1u) ? v[e] : 0.f;
   return v;
 }
 
@@ -81,39 +98,46 @@ struct Stage {
   static constexpr int PER = UNITS / 256;
   static_assert(PER >= 1 && UNITS % 256 == 0, "tile too small for 256 threads");
   floatx4 r[PER][2];
+  uint32_t bits[PER][2];
+  const float* rowp[KC ? PER : 1];  // KC: this thread's rows, fixed for every stage
+  bool row_ok[KC ? PER : 1];
 
-  // base: operand pointer; ld: its leading dimension; r0: first row (m or n)
-  // of the tile; lim_row: rows available; k0, ke: k range of this stage and
-  // of the split; rows_idx: gather over the row index (KC) or over k (!KC).
+  // KC only: resolve (and gather) the thread's rows once.
+  __device__ __forceinline__ void init(const float* __restrict__ base, int64_t ld, int r0, int lim_row,
+                                       const int32_t* rows_idx, int tid) {
+    if (!KC) return;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int g = r0 + (tid + 256 * j) / (BK / 8);
+      const bool ok = g < lim_row;
+      const int gc = ok ? g : 0;
+      const int64_t row = rows_idx ? (int64_t)rows_idx[gc] : (int64_t)gc;
+      rowp[j] = base + row * ld;
+      row_ok[j] = ok;
+    }
+  }
+
+  // k0, ke: k range of this stage and of the split; !KC: base/ld/r0/lim_row
+  // address [k][row] memory and rows_idx gathers over k.
   __device__ __forceinline__ void load(const float* __restrict__ base, int64_t ld, int r0, int lim_row, int k0,
                                        int ke, const int32_t* rows_idx, int tid) {
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int f = tid + 256 * j;
       if (KC) {
-        const int rr = f / (BK / 8);
         const int c = (f % (BK / 8)) * 8;
-        const int g = r0 + rr;
-        if (g < lim_row) {
-          const int64_t row = rows_idx ? (int64_t)rows_idx[g] : (int64_t)g;
-          const float* p = base + row * ld;
-          r[j][0] = load4<V>(p, k0 + c, ke);
-          r[j][1] = load4<V>(p, k0 + c + 4, ke);
-        } else {
-          r[j][0] = r[j][1] = floatx4{0.f, 0.f, 0.f, 0.f};
-        }
+        r[j][0] = load4<V>(rowp[j], k0 + c, ke, row_ok[j], bits[j][0]);
+        r[j][1] = load4<V>(rowp[j], k0 + c + 4, ke, row_ok[j], bits[j][1]);
       } else {
         const int kp = f / (ROWS / 4);        // k pair within the stage
         const int c = (f % (ROWS / 4)) * 4;   // 4 consecutive rows
         const int k = k0 + 2 * kp;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
-          if (k + q < ke) {
-            const int64_t row = rows_idx ? (int64_t)rows_idx[k + q] : (int64_t)(k + q);
-            r[j][q] = load4<V>(base + row * ld, r0 + c, lim_row);
-          } else {
-            r[j][q] = floatx4{0.f, 0.f, 0.f, 0.f};
-          }
+          const bool ok = k + q < ke;
+          const int kc = ok ? k + q : 0;
+          const int64_t row = rows_idx ? (int64_t)rows_idx[kc] : (int64_t)kc;
+          r[j][q] = load4<V>(base + row * ld, r0 + c, lim_row, ok, bits[j][q]);
         }
       }
     }
@@ -123,21 +147,23 @@ struct Stage {
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int f = tid + 256 * j;
+      const floatx4 a = masked(r[j][0], bits[j][0]);
+      const floatx4 b = masked(r[j][1], bits[j][1]);
       if (KC) {
         const int rr = f / (BK / 8);
         const int c = (f % (BK / 8)) * 8;
         uint4 v;
-        v.x = pack2(r[j][0][0], r[j][0][1]);
-        v.y = pack2(r[j][0][2], r[j][0][3]);
-        v.z = pack2(r[j][1][0], r[j][1][1]);
-        v.w = pack2(r[j][1][2], r[j][1][3]);
+        v.x = pack2(a[0], a[1]);
+        v.y = pack2(a[2], a[3]);
+        v.z = pack2(b[0], b[1]);
+        v.w = pack2(b[2], b[3]);
         *reinterpret_cast<uint4*>(&s[rr][c]) = v;
       } else {
         const int kp = f / (ROWS / 4);
         const int c = (f % (ROWS / 4)) * 4;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          *reinterpret_cast<uint32_t*>(&s[c + e][2 * kp]) = pack2(r[j][0][e], r[j][1][e]);
+          *reinterpret_cast<uint32_t*>(&s[c + e][2 * kp]) = pack2(a[e], b[e]);
       }
     }
   }
@@ -184,6 +210,8 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_kernel(GemmParams p) {
 
   Stage<BM, A_K, VA> sa;
   Stage<BN, B_K, VB> sb;
+  sa.init(p.A, p.lda, m0, p.M, p.rows, tid);
+  sb.init(p.B, p.ldb, n0, p.N, nullptr, tid);
   // A rows are m (A_K) or the gathered reduction rows (!A_K); B never gathers.
   auto gload = [&](int k0) {
     sa.load(p.A, p.lda, m0, p.M, k0, ke, p.rows, tid);

@@ -108,6 +108,19 @@ int ppo_gemm_bf16(void* stream, int a_layout, int b_layout, const float* A, int6
                   int64_t ldaux, float* bias_grad, int tile);
 /* x[i] <- bf16(x[i]) in place (the fp32 value of the nearest-even bf16). */
 int ppo_round_bf16(void* stream, float* x, int64_t n);
+/* The same contraction for long reductions (the first layer of a bf16 network
+ * over thousands of observation features), pipelined for bf16 MFMA rates
+ * (256 x 128 tiles, 8 waves, BK 64, loads two stages ahead).  a_bf16 / b_bf16:
+ * the operand is stored as bf16 bit patterns (the observation copy, the bf16
+ * image of the parameters) instead of fp32.  Rows must be 16-byte aligned; a
+ * bf16 operand's row pitch is at least its contiguous extent rounded up to 8.
+ * tile: -1 picks; 0: 256 x 128; 1: 128 x 128. */
+int ppo_gemm_bf16s(void* stream, int a_layout, int b_layout, int a_bf16, int b_bf16, const void* A, int64_t lda,
+                   const int32_t* rows, const void* B, int64_t ldb, float* C, int64_t ldc, int M, int N, int K,
+                   int splits, int64_t c_split_stride, int epi, const float* bias, int act, int round_out,
+                   const float* aux, int64_t ldaux, float* bias_grad, int tile);
+/* y[i] = bf16(x[i]) as 16-bit patterns (the bf16 observation copy); 16-byte aligned. */
+int ppo_cast_bf16(void* stream, const float* x, void* y, int64_t n);
 
 /* ------------------------------------------------------ LayerNorm / act
  * flax.linen.LayerNorm (epsilon, fast variance, scale and bias) followed by
@@ -222,6 +235,7 @@ int ppo_grad_reduce_segment_bytes(void);
 int ppo_grad_reduce_chunk_bytes(void);
 int ppo_grad_reduce_chunk_elems(void);
 int ppo_grad_reduce(void* stream, const void* segs, const void* chunks, int nchunks, double* sumsq);
+/* params_bf16 (may be NULL): receives the bf16 image of the updated parameters. */
 int ppo_adam_clip_f32(void* stream, float* params, const float* grads, float* mu, float* nu, void* params_bf16,
                       int64_t n, const double* sumsq, int nsumsq, double max_norm, double lr, double b1,
                       double b2, double eps, const int* count_base, int step_offset);

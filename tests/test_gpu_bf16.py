@@ -276,3 +276,90 @@ def test_bf16_whole_update_is_finite_and_counts_steps():
     assert all(np.isfinite(v).all() for v in logs.values())
     # the first step runs at the initial parameters on both sides
     np.testing.assert_allclose(logs["loss"][0], info["logs"][0]["loss"], rtol=TOL, atol=1e-3)
+
+
+# --------------------------------------------- pipelined GEMM for long reductions
+def to_bf16_bits(x):
+    """bf16 bit patterns (uint16) of the nearest-even bf16 of x."""
+    return (nets.bf16(x).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def gemm_s_case(a_layout, b_layout, a_bf16, b_bf16, M, N, K, rows_src=None, gather=False, epi=0, act=0, splits=1,
+                round_out=1, bias_grad=False, seed=0, tile=-1):
+    g = np.random.default_rng(seed)
+    if a_layout == 0:
+        src = rows_src or M
+        Alog_src = g.standard_normal((src, K)).astype(np.float32)
+        idx = g.permutation(src)[:M].astype(np.int32) if gather else None
+        Alog = Alog_src[idx] if gather else Alog_src
+        contig = K
+    else:
+        src = rows_src or K
+        Alog_src = g.standard_normal((src, M)).astype(np.float32)
+        idx = g.permutation(src)[:K].astype(np.int32) if gather else None
+        Alog = (Alog_src[idx] if gather else Alog_src).T
+        contig = M
+    Blog = g.standard_normal((K, N)).astype(np.float32)
+    Bstore = Blog if b_layout == 0 else np.ascontiguousarray(Blog.T)
+
+    def stored(x, as_bf16):
+        if not as_bf16:
+            return dev(x), x.shape[1]
+        ld = (x.shape[1] + 7) // 8 * 8 + 8          # a padded pitch, padding filled with junk bits
+        buf = np.full((x.shape[0], ld), 0x7FC0, np.uint16)
+        buf[:, :x.shape[1]] = to_bf16_bits(x)
+        return dev(buf.view(np.int16)), ld
+
+    A_t, lda = stored(Alog_src, a_bf16)
+    B_t, ldb = stored(Bstore, b_bf16)
+    bias = g.standard_normal(N).astype(np.float32)
+    C = torch.zeros(splits, M, N, device=DEV)
+    BG = torch.zeros(splits, N, device=DEV) if bias_grad else None
+    BIAS = dev(bias)
+    idx_t = dev(idx) if idx is not None else None
+    _lib.call("ppo_gemm_bf16s", st(), a_layout, b_layout, a_bf16, b_bf16, A_t.data_ptr(), lda,
+              None if idx_t is None else idx_t.data_ptr(), B_t.data_ptr(), ldb, C.data_ptr(), N, M, N, K, splits,
+              M * N, epi, BIAS.data_ptr() if epi == 1 else None, act, round_out, None, 0,
+              None if BG is None else BG.data_ptr(), tile)
+    torch.cuda.synchronize()
+    Ab, Bb = nets.bf16(Alog), nets.bf16(Blog)
+    exact = Ab @ Bb
+    got = C.cpu().numpy().astype(np.float64).sum(0)
+    if round_out:
+        exp = nets.bf16(exact)
+        inner = None
+        if epi == 1:
+            inner = exp
+            exp = nets.bf16(exp + nets.bf16(bias))
+            if act == 1:
+                exp = np.maximum(exp, 0.0)
+        within_one_bf16_ulp(got, exp, atol=1e-5 * np.sqrt(K), inner=inner)
+    else:
+        np.testing.assert_allclose(got, exact, rtol=1e-5, atol=1e-4 * np.sqrt(K))
+    if bias_grad:
+        np.testing.assert_allclose(BG.cpu().numpy().astype(np.float64).sum(0), Bb.sum(0), rtol=1e-5,
+                                   atol=1e-5 * np.sqrt(K))
+
+
+@pytest.mark.parametrize("a_layout, b_layout", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("a_bf16, b_bf16", [(1, 1), (1, 0), (0, 1), (0, 0)])
+def test_gemm_bf16s_layouts_and_storage(a_layout, b_layout, a_bf16, b_bf16):
+    gemm_s_case(a_layout, b_layout, a_bf16, b_bf16, 300, 136, 700, seed=a_layout * 8 + b_layout * 4 + 2 * a_bf16 + b_bf16)
+
+
+@pytest.mark.parametrize("tile", [0, 1])
+def test_gemm_bf16s_first_layer_shapes(tile):
+    # forward: gathered bf16 observation rows (8268 features, a ragged last stage) x bf16 weights
+    gemm_s_case(0, 0, 1, 1, 1024, 512, 8268, rows_src=3000, gather=True, epi=1, act=1, tile=tile)
+    # dW over gathered rows, fp32 cotangent, split-K with the bias gradient
+    gemm_s_case(1, 0, 1, 0, 8268, 512, 1024, rows_src=3000, gather=True, splits=2, round_out=0, bias_grad=True,
+                tile=tile)
+
+
+def test_cast_bf16():
+    x = np.random.default_rng(9).standard_normal(100005).astype(np.float32) * 10
+    X = dev(x)
+    Y = torch.zeros(100005 + 3, dtype=torch.int16, device=DEV)
+    _lib.call("ppo_cast_bf16", st(), X.data_ptr(), Y.data_ptr(), x.size)
+    got = Y.cpu().numpy()[:x.size].view(np.uint16)
+    np.testing.assert_array_equal(got, to_bf16_bits(x))
