@@ -39,9 +39,12 @@ SIGNATURES = {
     "ppo_round_bf16": (I, [P, P, I64]),
     "ppo_gemm_bf16s": (I, [P, I, I, I, I, P, I64, P, P, I64, P, I64, I, I, I, I, I64, I, P, I, I, P, I64, P, I]),
     "ppo_cast_bf16": (I, [P, P, P, I64]),
+    "ppo_cast_bf16_2d": (I, [P, P, I64, P, I64, I, I]),
+    "ppo_splits_bias_act_bf16": (I, [P, P, I64, I64, I, P, I, P, I64, I, I]),
     "ppo_layernorm_act_fwd_f32": (I, [P, P, I64, P, P, P, I64, P, P, I, I, F, I]),
     "ppo_layernorm_act_fwd_bf16": (I, [P, P, I64, P, P, P, I64, P, P, I, I, F, I]),
     "ppo_layernorm_act_bwd_bf16": (I, [P, P, I64, P, I64, P, P, P, P, P, I64, P, I, I, I]),
+    "ppo_layernorm_act_bwd_bf16_out16": (I, [P, P, I64, P, I64, P, P, P, P, P, I64, P, I, I, I]),
     "ppo_layernorm_bwd_blocks": (I, [I]),
     "ppo_layernorm_act_bwd_f32": (I, [P, P, I64, P, I64, P, P, P, P, P, I64, P, I, I, I]),
     "ppo_act_fwd_f32": (I, [P, P, I64, P, I64, I, I, I]),

@@ -1,0 +1,25 @@
+// Pipelined bf16 GEMM with both operands stored as bf16: the DMA-fed kernel
+// (gemm_bf16d.h), or the register-staged one when a gathered k-outer A
+// operand's split holds more reduction rows than the kernel caches.
+#include "gemm_bf16d.h"
+
+namespace ppo_bf16s {
+
+template <bool A_K, bool B_K>
+int launch_tt(hipStream_t st, const Params& p, int splits, int tile) {
+  const bool dma = A_K || p.rows == nullptr || p.k_per_split <= KIDX_MAX;
+  if (!dma) return launch_tile<A_K, B_K, uint16_t, uint16_t>(st, p, splits, tile);
+  if (tile == 1) return launch_d<128, 128, 2, 2, A_K, B_K>(st, p, splits);
+  return launch_d<256, 128, 4, 2, A_K, B_K>(st, p, splits);
+}
+
+template <>
+int launch_layouts<uint16_t, uint16_t>(hipStream_t st, const Params& p, int splits, int tile, int a_layout,
+                                       int b_layout) {
+  if (a_layout == 0 && b_layout == 0) return launch_tt<true, false>(st, p, splits, tile);
+  if (a_layout == 0 && b_layout == 1) return launch_tt<true, true>(st, p, splits, tile);
+  if (a_layout == 1 && b_layout == 0) return launch_tt<false, false>(st, p, splits, tile);
+  return launch_tt<false, true>(st, p, splits, tile);
+}
+
+}  // namespace ppo_bf16s

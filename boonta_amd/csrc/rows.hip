@@ -77,8 +77,8 @@ template <int VPL>
 __global__ void __launch_bounds__(ROW_THREADS)
 ln_act_bwd_kernel(const float* __restrict__ dy, int64_t lddy, const float* __restrict__ z, int64_t ldz,
                   const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
-                  const float* __restrict__ gamma, const float* __restrict__ beta, float* __restrict__ dz,
-                  int64_t lddz, float* __restrict__ partial, int rows, int F, int act, int round) {
+                  const float* __restrict__ gamma, const float* __restrict__ beta, void* __restrict__ dz,
+                  int64_t lddz, float* __restrict__ partial, int rows, int F, int act, int round, int out16) {
   __shared__ float red[ROW_THREADS / 64][2][VPL * 64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -117,7 +117,10 @@ ln_act_bwd_kernel(const float* __restrict__ dy, int64_t lddy, const float* __res
       const int f = lane + 64 * e;
       if (f < F) {
         const float d = rstd * (g[e] - sg - xh[e] * sgx);
-        dz[r * lddz + f] = round ? ppo::bf16_round(d) : d;
+        if (out16)
+          static_cast<uint16_t*>(dz)[r * lddz + f] = (uint16_t)ppo::bf16_bits(d);
+        else
+          static_cast<float*>(dz)[r * lddz + f] = round ? ppo::bf16_round(d) : d;
       }
     }
   }
@@ -424,10 +427,10 @@ int launch_ln_fwd(hipStream_t st, int blocks, const float* z, int64_t ldz, const
 
 template <int VPL>
 int launch_ln_bwd(hipStream_t st, int blocks, const float* dy, int64_t lddy, const float* z, int64_t ldz,
-                  const float* mean, const float* rstd, const float* gamma, const float* beta, float* dz,
-                  int64_t lddz, float* partial, int rows, int F, int act, int round) {
+                  const float* mean, const float* rstd, const float* gamma, const float* beta, void* dz,
+                  int64_t lddz, float* partial, int rows, int F, int act, int round, int out16) {
   hipLaunchKernelGGL((ln_act_bwd_kernel<VPL>), dim3(blocks), dim3(ROW_THREADS), 0, st, dy, lddy, z, ldz, mean, rstd,
-                     gamma, beta, dz, lddz, partial, rows, F, act, round);
+                     gamma, beta, dz, lddz, partial, rows, F, act, round, out16);
   return ppo::check_launch("ppo_layernorm_act_bwd_f32");
 }
 
@@ -471,18 +474,19 @@ PPO_EXPORT int ppo_layernorm_bwd_blocks(int rows) {
 
 static int layernorm_bwd(const char* name, void* stream, const float* dy, int64_t lddy, const float* z,
                          int64_t ldz, const float* mean, const float* rstd, const float* gamma, const float* beta,
-                         float* dz, int64_t lddz, float* partial, int rows, int F, int act, int round) {
+                         void* dz, int64_t lddz, float* partial, int rows, int F, int act, int round,
+                         int out16 = 0) {
   if (rows < 0 || F <= 0 || F > 64 * MAX_VPL || act < 0 || act > 3 || !dy || !z || !mean || !rstd || !gamma ||
       !beta || !dz || !partial)
     return ppo::set_error(PPO_ERR_ARG, "%s: bad argument (rows=%d F=%d)", name, rows, F);
   const int blocks = ppo_layernorm_bwd_blocks(rows);
   hipStream_t st = ppo::as_stream(stream);
   const int vpl = ppo::ceil_div(F, 64);
-  if (vpl <= 1) return launch_ln_bwd<1>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round);
-  if (vpl <= 2) return launch_ln_bwd<2>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round);
-  if (vpl <= 4) return launch_ln_bwd<4>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round);
-  if (vpl <= 8) return launch_ln_bwd<8>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round);
-  return launch_ln_bwd<16>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round);
+  if (vpl <= 1) return launch_ln_bwd<1>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round, out16);
+  if (vpl <= 2) return launch_ln_bwd<2>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round, out16);
+  if (vpl <= 4) return launch_ln_bwd<4>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round, out16);
+  if (vpl <= 8) return launch_ln_bwd<8>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round, out16);
+  return launch_ln_bwd<16>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round, out16);
 }
 
 PPO_EXPORT int ppo_layernorm_act_bwd_f32(void* stream, const float* dy, int64_t lddy, const float* z, int64_t ldz,
@@ -501,6 +505,16 @@ PPO_EXPORT int ppo_layernorm_act_bwd_bf16(void* stream, const float* dy, int64_t
                                           int F, int act) {
   return layernorm_bwd("ppo_layernorm_act_bwd_bf16", stream, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz,
                        partial, rows, F, act, 1);
+}
+
+// The same with the input cotangent stored as bf16 bit patterns (dz16, row
+// pitch lddz16 elements): the bf16 operand of the first layer's dW GEMM.
+PPO_EXPORT int ppo_layernorm_act_bwd_bf16_out16(void* stream, const float* dy, int64_t lddy, const float* z,
+                                                int64_t ldz, const float* mean, const float* rstd,
+                                                const float* gamma, const float* beta, void* dz16, int64_t lddz16,
+                                                float* partial, int rows, int F, int act) {
+  return layernorm_bwd("ppo_layernorm_act_bwd_bf16_out16", stream, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz16,
+                       lddz16, partial, rows, F, act, 1, 1);
 }
 
 PPO_EXPORT int ppo_act_fwd_f32(void* stream, const float* x, int64_t ldx, float* y, int64_t ldy, int rows, int F,

@@ -219,6 +219,8 @@ class LayerBufs:
     lnpart: torch.Tensor | None = None
     splits: int = 1
     lnblocks: int = 0
+    fpart: torch.Tensor | None = None
+    dZ16: torch.Tensor | None = None
 
 
 class FlatState:
@@ -240,6 +242,9 @@ class FlatState:
 
 class MLPExecutor:
     """One compiled PPO.update for fixed (T, N, obs, minibatches, epochs)."""
+
+    FWD16_SPLITS = 2  # K splits of the bf16 first-layer forward (256 tiles of 256 x 128 at 8192 x 512)
+    DW16_SPLITS = 4   # row splits of the bf16 first-layer dW
 
     def __init__(self, program: Program, flat: FlatState, cfg, chain, T: int, N: int):
         if program.gru is not None and type(self) is MLPExecutor:
@@ -288,6 +293,25 @@ class MLPExecutor:
         self.trunk = [layer_bufs(s, mb, True) for s in program.trunk]
         self.actor = [layer_bufs(s, mb, True) for s in program.actor_layers]
         self.critic = [layer_bufs(s, mb, True) for s in program.critic_layers]
+        # bf16 network: the first Dense of each torso group contracts the bf16
+        # observation copy with the bf16 image of the parameters on the
+        # pipelined GEMM (forward split over K, dW over rows)
+        firsts = [g[0] for g in (self.trunk, self.actor, self.critic) if g]
+        self.obs16 = (self.bf16 and program.gru is None and self.obs_dim % 4 == 0 and bool(firsts)
+                      and all(lb.spec.ld % 8 == 0 and lb.spec.dense.w.ld % 8 == 0 for lb in firsts))
+        if self.obs16:
+            i16 = dict(dtype=torch.int16, device=dev)
+            self.ldo16 = (self.obs_dim + 7) // 8 * 8
+            self.OBS16 = torch.zeros(self.B, self.ldo16, **i16)
+            self.P16 = torch.zeros(flat.P.numel(), **i16)
+            for lb in firsts:
+                d = lb.spec.dense
+                lb.splits = self.DW16_SPLITS
+                lb.wpart = torch.zeros(lb.splits, d.fin, lb.spec.ld, **f32)
+                lb.bpart = torch.zeros(lb.splits, lb.spec.ld, **f32)
+                lb.fpart = torch.zeros(self.FWD16_SPLITS, mb, lb.spec.ld, **f32)
+                if lb.spec.ln is not None:
+                    lb.dZ16 = torch.zeros(mb, lb.spec.ld, **i16)
         self.boot_layers = [layer_bufs(s, self._boot_rows(), False) for s in
                             (program.trunk if program.shared_head else program.critic_layers)]
         ha, hc = program.head_a, program.head_c
@@ -448,16 +472,36 @@ class MLPExecutor:
         """Rows of the bootstrap forward: second.obs[-1] (ppo.py:208-212)."""
         return self.N
 
+    def _reads_obs16(self, x, rows_idx, row0) -> bool:
+        """True for the first layer of a minibatch pass over the observation
+        (gathered rows of inputs["obs"]), which then reads the bf16 copy."""
+        return self.obs16 and rows_idx is not None and row0 == 0 and x == self.inp["obs"]
+
+    def _view16(self, region: Region) -> int:
+        """Address of a parameter region in the bf16 parameter image."""
+        return _p(self.P16) + 2 * region.offset
+
     def _fwd_layers(self, st, layers, x, ldx, rows_idx, nrows, row0=0):
         """Forward of Dense[+LayerNorm][+act] layers on nrows rows, writing
         each layer's buffers from row ``row0`` on."""
-        for lb in layers:
+        for li, lb in enumerate(layers):
             s = lb.spec
             d = s.dense
             W = self.flat.view(d.w)
             Bb = self.flat.view(d.b) if d.b is not None else None
             o = 4 * row0 * s.ld
-            if s.ln is not None:
+            if li == 0 and self._reads_obs16(x, rows_idx, row0):
+                dst = lb.Z if s.ln is not None else lb.Y
+                self._call("ppo_gemm_bf16s", st, A_ROW, B_KN, 1, 1, _p(self.OBS16), self.ldo16, rows_idx,
+                           self._view16(d.w), d.w.ld, _p(lb.fpart), s.ld, nrows, s.ld, d.fin, self.FWD16_SPLITS,
+                           nrows * s.ld, EPI_STORE, None, 0, 0, None, 0, None, -1)
+                self._call("ppo_splits_bias_act_bf16", st, _p(lb.fpart), s.ld, nrows * s.ld, self.FWD16_SPLITS, Bb,
+                           _act(s.act) if s.ln is None else 0, _p(dst), s.ld, nrows, s.ld)
+                if s.ln is not None:
+                    self._call(self._ln_fwd, st, _p(lb.Z), s.ld, self.flat.view(s.ln["scale"]),
+                               self.flat.view(s.ln["bias"]), _p(lb.Y), s.ld, _p(lb.mean), _p(lb.rstd), nrows,
+                               s.fout, s.ln["eps"], _act(s.act))
+            elif s.ln is not None:
                 self._gemm(st, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(lb.Z) + o, s.ld, nrows,
                           s.ld, d.fin, 1, 0, EPI_BIAS_ACT, Bb, 0, None, None, 0, None, -1)
                 self._call(self._ln_fwd, st, _p(lb.Z) + o, s.ld, self.flat.view(s.ln["scale"]),
@@ -486,16 +530,25 @@ class MLPExecutor:
             lb = layers[i]
             s = lb.spec
             d = s.dense
-            if s.ln is not None:
-                self._call(self._ln_bwd, st, _p(lb.dY), s.ld, _p(lb.Z), s.ld, _p(lb.mean),
-                          _p(lb.rstd), self.flat.view(s.ln["scale"]), self.flat.view(s.ln["bias"]), _p(lb.dZ),
-                          s.ld, _p(lb.lnpart), self.mb, s.fout, _act(s.act))
             if i > 0:
                 x, ldx, ridx = _p(layers[i - 1].Y), layers[i - 1].spec.ld, None
             else:
                 x, ldx, ridx = x0, ldx0, idx0
-            self._gemm(st, A_COL, B_KN, x, ldx, ridx, _p(lb.dZ), s.ld, _p(lb.wpart), s.ld, d.fin,
-                      s.ld, self.mb, lb.splits, d.fin * s.ld, EPI_STORE, None, 0, None, None, 0, _p(lb.bpart), -1)
+            obs16 = i == 0 and self._reads_obs16(x, ridx, 0)
+            dz16 = obs16 and s.ln is not None  # the first layer's cotangent feeds only its dW: keep it bf16
+            if s.ln is not None:
+                self._call("ppo_layernorm_act_bwd_bf16_out16" if dz16 else self._ln_bwd, st, _p(lb.dY), s.ld,
+                           _p(lb.Z), s.ld, _p(lb.mean), _p(lb.rstd), self.flat.view(s.ln["scale"]),
+                           self.flat.view(s.ln["bias"]), _p(lb.dZ16) if dz16 else _p(lb.dZ), s.ld, _p(lb.lnpart),
+                           self.mb, s.fout, _act(s.act))
+            if obs16:
+                self._call("ppo_gemm_bf16s", st, A_COL, B_KN, 1, 1 if dz16 else 0, _p(self.OBS16), self.ldo16, ridx,
+                           _p(lb.dZ16) if dz16 else _p(lb.dZ), s.ld, _p(lb.wpart), s.ld, d.fin, s.ld, self.mb,
+                           lb.splits, d.fin * s.ld, EPI_STORE, None, 0, 0, None, 0, _p(lb.bpart), -1)
+            else:
+                self._gemm(st, A_COL, B_KN, x, ldx, ridx, _p(lb.dZ), s.ld, _p(lb.wpart), s.ld, d.fin,
+                          s.ld, self.mb, lb.splits, d.fin * s.ld, EPI_STORE, None, 0, None, None, 0, _p(lb.bpart),
+                          -1)
             if i > 0:
                 dst, epi, act, aux, ldaux = self._dx_target(layers[i - 1])
                 self._gemm(st, A_ROW, B_NK, _p(lb.dZ), s.ld, None, self.flat.view(d.w), d.w.ld,
@@ -525,6 +578,11 @@ class MLPExecutor:
         inp, prog, cfg, chain = self.inp, self.prog, self.cfg, self.chain
         T, N, B, mb = self.T, self.N, self.B, self.mb
         obs, ldo = inp["obs"], self.obs_dim
+        if self.obs16:
+            # bf16 copies the first-layer GEMMs read: the rollout's observations
+            # (once per update) and the parameters (Adam refreshes the image)
+            self._call("ppo_cast_bf16_2d", st, obs, ldo, _p(self.OBS16), self.ldo16, B, ldo)
+            self._call("ppo_cast_bf16", st, _p(self.flat.P), _p(self.P16), self.flat.P.numel())
         # 1. bootstrap value of second.obs[-1] with the current parameters
         x, ldx, _ = inp["next_obs_last"], ldo, None
         if prog.shared_head:
@@ -562,7 +620,8 @@ class MLPExecutor:
                 self._minibatch(st, idx, step, obs, ldo, dist, A)
                 self._call("ppo_grad_reduce", st, _p(self.SEGS), _p(self.CHUNKS), self.nchunks, _p(self.SUMSQ))
                 self._call("ppo_adam_clip_f32", st, _p(self.flat.P), _p(self.flat.G), _p(self.flat.MU),
-                          _p(self.flat.NU), None, self.flat.P.numel(), _p(self.SUMSQ), self.nchunks,
+                          _p(self.flat.NU), _p(self.P16) if self.obs16 else None, self.flat.P.numel(),
+                          _p(self.SUMSQ), self.nchunks,
                           float(max_norm), adam.learning_rate, adam.b1, adam.b2, adam.eps, _p(self.flat.count),
                           step)
         self._call("ppo_count_advance", st, _p(self.flat.count), self.E * self.M)

@@ -114,13 +114,24 @@ int ppo_round_bf16(void* stream, float* x, int64_t n);
  * the operand is stored as bf16 bit patterns (the observation copy, the bf16
  * image of the parameters) instead of fp32.  Rows must be 16-byte aligned; a
  * bf16 operand's row pitch is at least its contiguous extent rounded up to 8.
- * tile: -1 picks; 0: 256 x 128; 1: 128 x 128. */
+ * With both operands stored as bf16, stages are copied straight from global
+ * memory into LDS (no register staging), three stages in flight.
+ * tile: -1 picks; 0: 256 x 128 (8 waves), 1: 128 x 128 (4 waves). */
 int ppo_gemm_bf16s(void* stream, int a_layout, int b_layout, int a_bf16, int b_bf16, const void* A, int64_t lda,
                    const int32_t* rows, const void* B, int64_t ldb, float* C, int64_t ldc, int M, int N, int K,
                    int splits, int64_t c_split_stride, int epi, const float* bias, int act, int round_out,
                    const float* aux, int64_t ldaux, float* bias_grad, int tile);
-/* y[i] = bf16(x[i]) as 16-bit patterns (the bf16 observation copy); 16-byte aligned. */
+/* y[i] = bf16(x[i]) as 16-bit patterns (the bf16 parameter image); 16-byte aligned. */
 int ppo_cast_bf16(void* stream, const float* x, void* y, int64_t n);
+/* Row-pitched bf16 copy (the per-update observation copy): y[r][c] = bf16(x[r][c])
+ * for c < cols, 0 for cols <= c < ldy; ldy a multiple of 8, ldx of 4, both
+ * buffers 16-byte aligned. */
+int ppo_cast_bf16_2d(void* stream, const float* x, int64_t ldx, void* y, int64_t ldy, int rows, int cols);
+/* out[r][j] = act(bf16(bf16(sum_s partials[s][r][j]) + bf16(bias[j]))), each step
+ * rounded to bf16 (flax's Dense in bf16 after a split-K contraction; bias may
+ * be NULL, act 0 = none).  Partials are added in split order. */
+int ppo_splits_bias_act_bf16(void* stream, const float* partials, int64_t ldp, int64_t split_stride, int nsplit,
+                             const float* bias, int act, float* out, int64_t ldc, int rows, int cols);
 
 /* ------------------------------------------------------ LayerNorm / act
  * flax.linen.LayerNorm (epsilon, fast variance, scale and bias) followed by
@@ -144,6 +155,11 @@ int ppo_layernorm_act_fwd_bf16(void* stream, const float* z, int64_t ldz, const 
 int ppo_layernorm_act_bwd_bf16(void* stream, const float* dy, int64_t lddy, const float* z, int64_t ldz,
                                const float* mean, const float* rstd, const float* gamma, const float* beta,
                                float* dz, int64_t lddz, float* partial, int rows, int F, int act);
+/* ppo_layernorm_act_bwd_bf16 with dz stored as bf16 bit patterns (row pitch
+ * lddz16 elements): the operand of a bf16 dW contraction. */
+int ppo_layernorm_act_bwd_bf16_out16(void* stream, const float* dy, int64_t lddy, const float* z, int64_t ldz,
+                                     const float* mean, const float* rstd, const float* gamma, const float* beta,
+                                     void* dz16, int64_t lddz16, float* partial, int rows, int F, int act);
 int ppo_act_fwd_f32(void* stream, const float* x, int64_t ldx, float* y, int64_t ldy, int rows, int F, int act);
 int ppo_act_bwd_f32(void* stream, const float* dy, int64_t lddy, const float* aux, int64_t ldaux, float* dx,
                     int64_t lddx, int rows, int F, int act);

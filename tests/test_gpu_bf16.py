@@ -151,6 +151,14 @@ def test_layernorm_relu_bf16_forward_and_backward():
     torch.cuda.synchronize()
     within_one_bf16_ulp(Y.cpu().numpy(), y_ref, exact_frac=0.99, atol=1e-6)
     within_one_bf16_ulp(DZ.cpu().numpy(), dz_ref, exact_frac=0.95, atol=1e-5)
+    # the bf16-stored cotangent holds exactly the bits of the rounded fp32 one
+    DZ16 = torch.zeros(rows, F + 8, dtype=torch.int16, device=DEV)
+    PART16 = torch.zeros(nb, 2 * F, device=DEV)
+    _lib.call("ppo_layernorm_act_bwd_bf16_out16", st(), DY.data_ptr(), F, Z.data_ptr(), F, MEAN.data_ptr(),
+              RSTD.data_ptr(), G.data_ptr(), Bt.data_ptr(), DZ16.data_ptr(), F + 8, PART16.data_ptr(), rows, F, 1)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(DZ16.cpu().numpy()[:, :F].view(np.uint16), to_bf16_bits(DZ.cpu().numpy()))
+    np.testing.assert_array_equal(PART16.cpu().numpy(), PART.cpu().numpy())
     part = PART.cpu().numpy().astype(np.float64).sum(0)
     np.testing.assert_allclose(part[:F], grads["ln"]["scale"], rtol=1e-4, atol=1e-4)
     np.testing.assert_allclose(part[F:], grads["ln"]["bias"], rtol=1e-4, atol=1e-4)
@@ -344,7 +352,8 @@ def gemm_s_case(a_layout, b_layout, a_bf16, b_bf16, M, N, K, rows_src=None, gath
 @pytest.mark.parametrize("a_layout, b_layout", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("a_bf16, b_bf16", [(1, 1), (1, 0), (0, 1), (0, 0)])
 def test_gemm_bf16s_layouts_and_storage(a_layout, b_layout, a_bf16, b_bf16):
-    gemm_s_case(a_layout, b_layout, a_bf16, b_bf16, 300, 136, 700, seed=a_layout * 8 + b_layout * 4 + 2 * a_bf16 + b_bf16)
+    seed = a_layout * 8 + b_layout * 4 + 2 * a_bf16 + b_bf16
+    gemm_s_case(a_layout, b_layout, a_bf16, b_bf16, 300, 136, 700, seed=seed, tile=seed % 2)
 
 
 @pytest.mark.parametrize("tile", [0, 1])
@@ -354,6 +363,17 @@ def test_gemm_bf16s_first_layer_shapes(tile):
     # dW over gathered rows, fp32 cotangent, split-K with the bias gradient
     gemm_s_case(1, 0, 1, 0, 8268, 512, 1024, rows_src=3000, gather=True, splits=2, round_out=0, bias_grad=True,
                 tile=tile)
+    # the same with a bf16 cotangent: both operands bf16, copied straight to LDS
+    gemm_s_case(1, 0, 1, 1, 8268, 512, 1024, rows_src=3000, gather=True, splits=4, round_out=0, bias_grad=True,
+                tile=tile)
+
+
+def test_gemm_bf16s_gathered_reduction_beyond_index_cache():
+    """A split over more than 2048 gathered reduction rows (k-outer A) runs on
+    the register-staged pipeline; 2048 and fewer on the direct copies."""
+    for splits in (1, 3):  # 4200 rows per split, then 1408
+        gemm_s_case(1, 0, 1, 1, 300, 136, 4200, rows_src=5000, gather=True, splits=splits, round_out=0,
+                    bias_grad=True, seed=splits)
 
 
 def test_cast_bf16():
@@ -363,3 +383,52 @@ def test_cast_bf16():
     _lib.call("ppo_cast_bf16", st(), X.data_ptr(), Y.data_ptr(), x.size)
     got = Y.cpu().numpy()[:x.size].view(np.uint16)
     np.testing.assert_array_equal(got, to_bf16_bits(x))
+
+
+def test_cast_bf16_rows_pads_with_zeros():
+    rows, cols, ldy = 37, 8268, 8280
+    x = (np.random.default_rng(10).standard_normal((rows, cols)) * 3).astype(np.float32)
+    X = dev(x)
+    Y = torch.full((rows, ldy), 0x7FC0, dtype=torch.int16, device=DEV)
+    _lib.call("ppo_cast_bf16_2d", st(), X.data_ptr(), cols, Y.data_ptr(), ldy, rows, cols)
+    got = Y.cpu().numpy().view(np.uint16)
+    np.testing.assert_array_equal(got[:, :cols], to_bf16_bits(x))
+    assert (got[:, cols:] == 0).all()
+
+
+@pytest.mark.parametrize("act", [0, 1])
+def test_splits_bias_act_bf16_matches_single_pass_epilogue(act):
+    """The split-K epilogue equals ppo_gemm_bf16s's own epilogue on one split."""
+    rows, cols, ns, K = 300, 136, 3, 700
+    g = np.random.default_rng(11 + act)
+    A = g.standard_normal((rows, K)).astype(np.float32)
+    Bm = g.standard_normal((K, cols)).astype(np.float32)
+    bias = dev(g.standard_normal(cols).astype(np.float32))
+    At, Bt = dev(A), dev(Bm)
+    one = torch.zeros(rows, cols, device=DEV)
+    part = torch.zeros(ns, rows, cols, device=DEV)
+    out = torch.zeros(rows, cols, device=DEV)
+    _lib.call("ppo_gemm_bf16s", st(), 0, 0, 0, 0, At.data_ptr(), K, None, Bt.data_ptr(), cols, one.data_ptr(), cols,
+              rows, cols, K, 1, 0, 1, bias.data_ptr(), act, 1, None, 0, None, -1)
+    _lib.call("ppo_gemm_bf16s", st(), 0, 0, 0, 0, At.data_ptr(), K, None, Bt.data_ptr(), cols, part.data_ptr(), cols,
+              rows, cols, K, ns, rows * cols, 0, None, 0, 0, None, 0, None, -1)
+    _lib.call("ppo_splits_bias_act_bf16", st(), part.data_ptr(), cols, rows * cols, ns, bias.data_ptr(), act,
+              out.data_ptr(), cols, rows, cols)
+    torch.cuda.synchronize()
+    # fp32 sums of the same products in another order: equal up to one bf16 unit of the rounded dot
+    exact = nets.bf16(A) @ nets.bf16(Bm)
+    b = bias.cpu().numpy()
+    exp = nets.bf16(nets.bf16(exact) + nets.bf16(b))
+    if act == 1:
+        exp = np.maximum(exp, 0.0)
+    within_one_bf16_ulp(out.cpu().numpy(), exp, atol=1e-5 * np.sqrt(K), inner=nets.bf16(exact))
+    within_one_bf16_ulp(one.cpu().numpy(), exp, atol=1e-5 * np.sqrt(K), inner=nets.bf16(exact))
+    s = part.cpu().numpy().astype(np.float32)
+    total = s[0]
+    for i in range(1, ns):
+        total = total + s[i]
+    v = nets.bf16(nets.bf16(total) + nets.bf16(b))
+    if act == 1:
+        v = np.maximum(v, 0.0)
+    # bit-exact against the same partials added in split order
+    np.testing.assert_array_equal(out.cpu().numpy(), v.astype(np.float32))
