@@ -148,6 +148,16 @@ def launch_work(name, args):
     if name in ("ppo_gemm_f32", "ppo_gemm_bf16"):
         M, N, K = args[10], args[11], args[12]
         return 2.0 * M * N * K, 4.0 * (M * K + K * N + M * N)
+    if name == "ppo_gemm_bf16s":
+        M, N, K = args[12], args[13], args[14]
+        ea, eb = (2.0 if args[3] else 4.0), (2.0 if args[4] else 4.0)
+        return 2.0 * M * N * K, ea * M * K + eb * K * N + 4.0 * M * N * args[15]
+    if name == "ppo_cast_bf16_2d":
+        rows, cols, ldy = args[5], args[6], args[4]
+        return 0.0, 4.0 * rows * cols + 2.0 * rows * ldy
+    if name == "ppo_splits_bias_act_bf16":
+        nsplit, rows, cols = args[4], args[9], args[10]
+        return 0.0, 4.0 * rows * cols * (nsplit + 1)
     if name == "ppo_gae_f32":
         T, N = args[10], args[11]
         return 0.0, 18.0 * T * N + 4.0 * N
@@ -167,12 +177,15 @@ def launch_work(name, args):
         Bm, H = args[-2], args[-1]
         flops = 2.0 * Bm * 3 * H * H if args[1] else 0.0
         return flops, 4.0 * Bm * (3 * H + 2 * H + 7 * H) + (4.0 * H * 3 * H if args[1] else 0.0)
-    if name == "ppo_layernorm_act_fwd_f32":
+    if name in ("ppo_layernorm_act_fwd_f32", "ppo_layernorm_act_fwd_bf16"):
         rows, F = args[9], args[10]
         return 0.0, 4.0 * rows * (2 * F + 2)
-    if name == "ppo_layernorm_act_bwd_f32":
-        rows, F = args[13], args[14]
+    if name in ("ppo_layernorm_act_bwd_f32", "ppo_layernorm_act_bwd_bf16"):
+        rows, F = args[12], args[13]
         return 0.0, 4.0 * rows * (3 * F + 2)
+    if name == "ppo_layernorm_act_bwd_bf16_out16":
+        rows, F = args[12], args[13]
+        return 0.0, rows * (4.0 * 2 * F + 2.0 * F + 8.0)
     return 0.0, 0.0
 
 
@@ -180,6 +193,8 @@ def launch_key(name, args):
     """Launches with the same entry point and shape do the same work."""
     if name in ("ppo_gemm_f32", "ppo_gemm_bf16"):
         return (name, args[1], args[2]) + tuple(args[10:16])
+    if name == "ppo_gemm_bf16s":
+        return (name,) + tuple(args[1:5]) + tuple(args[12:16])
     if name in ("ppo_gru_fwd_step_f32", "ppo_gru_bwd_step_f32"):
         return (name, args[-2], args[-1], bool(args[1]))
     return (name, id(args))
@@ -218,6 +233,8 @@ def time_launches(ex, reps, per_update_steps):
         row = {"i": i, "name": name, "ms": ms, "count": count, "flops": flops, "bytes": nbytes,
                "shape": [a for a in args[10:13]] if name.startswith("ppo_gemm") else None,
                "layout": [args[1], args[2]] if name.startswith("ppo_gemm") else None}
+        if name == "ppo_gemm_bf16s":
+            row["shape"] = [a for a in args[12:15]]
         if name.startswith("ppo_gru"):
             row["shape"] = [args[-2], args[-1]]
         rows.append(row)
@@ -364,7 +381,7 @@ def main():
         dom = max(rows, key=lambda r: r["ms"] * r["count"])
         if dom["flops"] > 0:
             achieved = dom["flops"] / (dom["ms"] * 1e-3) / 1e12
-            peak = PEAK["bf16_mfma"] if dom["name"] == "ppo_gemm_bf16" else PEAK["fp32_mfma"]
+            peak = PEAK["bf16_mfma"] if dom["name"] in ("ppo_gemm_bf16", "ppo_gemm_bf16s") else PEAK["fp32_mfma"]
             roof = {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
                     "frac": achieved / peak, "traffic": None}
         else:

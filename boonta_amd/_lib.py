@@ -43,6 +43,7 @@ SIGNATURES = {
     "ppo_splits_bias_act_bf16": (I, [P, P, I64, I64, I, P, I, P, I64, I, I]),
     "ppo_layernorm_act_fwd_f32": (I, [P, P, I64, P, P, P, I64, P, P, I, I, F, I]),
     "ppo_layernorm_act_fwd_bf16": (I, [P, P, I64, P, P, P, I64, P, P, I, I, F, I]),
+    "ppo_layernorm_act_fwd_bf16_out16": (I, [P, P, I64, P, P, P, I64, P, I64, P, P, I, I, F, I]),
     "ppo_layernorm_act_bwd_bf16": (I, [P, P, I64, P, I64, P, P, P, P, P, I64, P, I, I, I]),
     "ppo_layernorm_act_bwd_bf16_out16": (I, [P, P, I64, P, I64, P, P, P, P, P, I64, P, I, I, I]),
     "ppo_layernorm_bwd_blocks": (I, [I]),
@@ -66,6 +67,7 @@ SIGNATURES = {
     "ppo_grad_reduce_chunk_bytes": (I, []),
     "ppo_grad_reduce_chunk_elems": (I, []),
     "ppo_grad_reduce": (I, [P, P, P, I, P]),
+    "ppo_sumsq_total": (I, [P, P, I, P]),
     "ppo_adam_clip_f32": (I, [P, P, P, P, P, P, I64, P, I, D, D, D, D, D, P, I]),
     "ppo_count_advance": (I, [P, P, I]),
 }

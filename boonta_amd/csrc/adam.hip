@@ -159,6 +159,25 @@ __global__ void __launch_bounds__(256) adam_kernel(AdamParams a) {
   }
 }
 
+// Sum of the per-chunk squares in a fixed order: thread t adds chunks
+// t, t + 1024, ... in turn, then the block's 1024 partials are added as a
+// fixed tree (wave sums, then the 16 wave totals in wave order).
+constexpr int NORM_THREADS = 1024;
+__global__ void __launch_bounds__(NORM_THREADS) sumsq_total_kernel(const double* __restrict__ sumsq, int n,
+                                                                   double* __restrict__ total) {
+  __shared__ double w[NORM_THREADS / 64];
+  double t = 0.0;
+  for (int i = threadIdx.x; i < n; i += NORM_THREADS) t += sumsq[i];
+  t = ppo::wave_sum_d(t);
+  if ((threadIdx.x & 63) == 0) w[threadIdx.x >> 6] = t;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double s = 0.0;
+    for (int i = 0; i < NORM_THREADS / 64; ++i) s += w[i];
+    total[0] = s;
+  }
+}
+
 __global__ void count_advance_kernel(int* count_base, int steps) {
   if (threadIdx.x == 0 && blockIdx.x == 0) *count_base += steps;
 }
@@ -199,6 +218,14 @@ PPO_EXPORT int ppo_adam_clip_f32(void* stream, float* params, const float* grads
   const int blocks = (int)std::min<int64_t>(ppo::ceil_div64(n / 4, 256), 2048);
   hipLaunchKernelGGL(adam_kernel, dim3(blocks), dim3(256), 0, ppo::as_stream(stream), a);
   return ppo::check_launch("ppo_adam_clip_f32");
+}
+
+// total[0] = sum of sumsq[0..n) in a fixed order (one block): hands the
+// optimizer one squared norm instead of every block re-adding n partials.
+PPO_EXPORT int ppo_sumsq_total(void* stream, const double* sumsq, int n, double* total) {
+  if (n < 0 || !total || (n > 0 && !sumsq)) return ppo::set_error(PPO_ERR_ARG, "ppo_sumsq_total: bad argument");
+  hipLaunchKernelGGL(sumsq_total_kernel, dim3(1), dim3(NORM_THREADS), 0, ppo::as_stream(stream), sumsq, n, total);
+  return ppo::check_launch("ppo_sumsq_total");
 }
 
 PPO_EXPORT int ppo_count_advance(void* stream, int* count_base, int steps) {

@@ -26,7 +26,8 @@ template <int VPL>
 __global__ void __launch_bounds__(ROW_THREADS)
 ln_act_fwd_kernel(const float* __restrict__ z, int64_t ldz, const float* __restrict__ gamma,
                   const float* __restrict__ beta, float* __restrict__ y, int64_t ldy, float* __restrict__ mean_out,
-                  float* __restrict__ rstd_out, int rows, int F, float eps, int act, int round) {
+                  float* __restrict__ rstd_out, int rows, int F, float eps, int act, int round,
+                  uint16_t* __restrict__ y16, int64_t ldy16) {
   const int lane = threadIdx.x & 63;
   const int wpb = ROW_THREADS / 64;
   for (int64_t r = (int64_t)blockIdx.x * wpb + (threadIdx.x >> 6); r < rows; r += (int64_t)gridDim.x * wpb) {
@@ -64,6 +65,7 @@ ln_act_fwd_kernel(const float* __restrict__ z, int64_t ldz, const float* __restr
           o = ppo::act_fwd(act, o);
         }
         yr[f] = o;
+        if (y16) y16[r * ldy16 + f] = (uint16_t)ppo::bf16_bits(o);
       }
     }
   }
@@ -419,9 +421,10 @@ loss_finalize_kernel(const double* __restrict__ partial, int nblocks, int rows, 
 
 template <int VPL>
 int launch_ln_fwd(hipStream_t st, int blocks, const float* z, int64_t ldz, const float* gamma, const float* beta,
-                  float* y, int64_t ldy, float* mean, float* rstd, int rows, int F, float eps, int act, int round) {
+                  float* y, int64_t ldy, float* mean, float* rstd, int rows, int F, float eps, int act, int round,
+                  uint16_t* y16, int64_t ldy16) {
   hipLaunchKernelGGL((ln_act_fwd_kernel<VPL>), dim3(blocks), dim3(ROW_THREADS), 0, st, z, ldz, gamma, beta, y, ldy,
-                     mean, rstd, rows, F, eps, act, round);
+                     mean, rstd, rows, F, eps, act, round, y16, ldy16);
   return ppo::check_launch("ppo_layernorm_act_fwd_f32");
 }
 
@@ -438,18 +441,18 @@ int launch_ln_bwd(hipStream_t st, int blocks, const float* dy, int64_t lddy, con
 
 static int layernorm_fwd(const char* name, void* stream, const float* z, int64_t ldz, const float* gamma,
                          const float* beta, float* y, int64_t ldy, float* mean, float* rstd, int rows, int F,
-                         float eps, int act, int round) {
+                         float eps, int act, int round, uint16_t* y16 = nullptr, int64_t ldy16 = 0) {
   if (rows < 0 || F <= 0 || F > 64 * MAX_VPL || act < 0 || act > 3 || !z || !gamma || !beta || !y)
     return ppo::set_error(PPO_ERR_ARG, "%s: bad argument (rows=%d F=%d)", name, rows, F);
   if (rows == 0) return PPO_OK;
   const int blocks = std::min(ppo::ceil_div(rows, ROW_THREADS / 64), 4096);
   hipStream_t st = ppo::as_stream(stream);
   const int vpl = ppo::ceil_div(F, 64);
-  if (vpl <= 1) return launch_ln_fwd<1>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act, round);
-  if (vpl <= 2) return launch_ln_fwd<2>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act, round);
-  if (vpl <= 4) return launch_ln_fwd<4>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act, round);
-  if (vpl <= 8) return launch_ln_fwd<8>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act, round);
-  return launch_ln_fwd<16>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act, round);
+  if (vpl <= 1) return launch_ln_fwd<1>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act, round, y16, ldy16);
+  if (vpl <= 2) return launch_ln_fwd<2>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act, round, y16, ldy16);
+  if (vpl <= 4) return launch_ln_fwd<4>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act, round, y16, ldy16);
+  if (vpl <= 8) return launch_ln_fwd<8>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act, round, y16, ldy16);
+  return launch_ln_fwd<16>(st, blocks, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps, act, round, y16, ldy16);
 }
 
 PPO_EXPORT int ppo_layernorm_act_fwd_f32(void* stream, const float* z, int64_t ldz, const float* gamma,
@@ -465,6 +468,16 @@ PPO_EXPORT int ppo_layernorm_act_fwd_bf16(void* stream, const float* z, int64_t 
                                           int rows, int F, float eps, int act) {
   return layernorm_fwd("ppo_layernorm_act_fwd_bf16", stream, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F, eps,
                        act, 1);
+}
+
+// The same, also storing the output as bf16 bit patterns (y16, row pitch
+// ldy16 elements): the bf16 operand of the next layer's GEMMs.
+PPO_EXPORT int ppo_layernorm_act_fwd_bf16_out16(void* stream, const float* z, int64_t ldz, const float* gamma,
+                                                const float* beta, float* y, int64_t ldy, void* y16, int64_t ldy16,
+                                                float* mean, float* rstd, int rows, int F, float eps, int act) {
+  if (!y16 || ldy16 < F) return ppo::set_error(PPO_ERR_ARG, "ppo_layernorm_act_fwd_bf16_out16: bad bf16 output");
+  return layernorm_fwd("ppo_layernorm_act_fwd_bf16_out16", stream, z, ldz, gamma, beta, y, ldy, mean, rstd, rows, F,
+                       eps, act, 1, static_cast<uint16_t*>(y16), ldy16);
 }
 
 // Partials: [blocks][2F]; blocks = ppo_layernorm_bwd_blocks(rows).

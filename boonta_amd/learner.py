@@ -221,6 +221,7 @@ class LayerBufs:
     lnblocks: int = 0
     fpart: torch.Tensor | None = None
     dZ16: torch.Tensor | None = None
+    Y16: torch.Tensor | None = None
 
 
 class FlatState:
@@ -245,6 +246,7 @@ class MLPExecutor:
 
     FWD16_SPLITS = 2  # K splits of the bf16 first-layer forward (256 tiles of 256 x 128 at 8192 x 512)
     DW16_SPLITS = 4   # row splits of the bf16 first-layer dW
+    DW16_SPLITS_INNER = 16  # row splits of a bf16 dW between two LayerNorm layers
 
     def __init__(self, program: Program, flat: FlatState, cfg, chain, T: int, N: int):
         if program.gru is not None and type(self) is MLPExecutor:
@@ -312,6 +314,20 @@ class MLPExecutor:
                 lb.fpart = torch.zeros(self.FWD16_SPLITS, mb, lb.spec.ld, **f32)
                 if lb.spec.ln is not None:
                     lb.dZ16 = torch.zeros(mb, lb.spec.ld, **i16)
+            # the LayerNorm layers also keep their output and take their
+            # cotangent as bf16, so every torso contraction has bf16 operands
+            for group in (self.trunk, self.actor, self.critic):
+                for li, lb in enumerate(group):
+                    if lb.spec.ln is None:
+                        continue
+                    lb.Y16 = torch.zeros(mb, lb.spec.ld, **i16)
+                    if lb.dZ16 is None:
+                        lb.dZ16 = torch.zeros(mb, lb.spec.ld, **i16)
+                    if li > 0 and group[li - 1].spec.ln is not None:
+                        d = lb.spec.dense
+                        lb.splits = self.DW16_SPLITS_INNER
+                        lb.wpart = torch.zeros(lb.splits, d.fin, lb.spec.ld, **f32)
+                        lb.bpart = torch.zeros(lb.splits, lb.spec.ld, **f32)
         self.boot_layers = [layer_bufs(s, self._boot_rows(), False) for s in
                             (program.trunk if program.shared_head else program.critic_layers)]
         ha, hc = program.head_a, program.head_c
@@ -439,6 +455,7 @@ class MLPExecutor:
         self.CHUNKS = torch.tensor(list(b"".join(chunks)), dtype=torch.uint8, device=dev)
         self.nchunks = len(chunks)
         self.SUMSQ = torch.zeros(self.nchunks, dtype=torch.float64, device=dev)
+        self.SUMSQ1 = torch.zeros(1, dtype=torch.float64, device=dev)
         self.segments = segs
 
     # ------------------------------------------------------------- pieces
@@ -477,6 +494,22 @@ class MLPExecutor:
         (gathered rows of inputs["obs"]), which then reads the bf16 copy."""
         return self.obs16 and rows_idx is not None and row0 == 0 and x == self.inp["obs"]
 
+    def _y16_input(self, layers, li, nrows, row0) -> bool:
+        """True when layer li of a training group reads the bf16 output of
+        layer li - 1 (minibatch passes of a bf16 network)."""
+        return (li > 0 and row0 == 0 and nrows == self.mb and layers[li - 1].Y16 is not None
+                and layers[li].spec.dense.w.ld % 8 == 0)
+
+    def _ln_forward(self, st, lb, o, row0, nrows):
+        s = lb.spec
+        scale, bias = self.flat.view(s.ln["scale"]), self.flat.view(s.ln["bias"])
+        if lb.Y16 is not None and row0 == 0 and nrows == self.mb:
+            self._call("ppo_layernorm_act_fwd_bf16_out16", st, _p(lb.Z), s.ld, scale, bias, _p(lb.Y), s.ld,
+                       _p(lb.Y16), s.ld, _p(lb.mean), _p(lb.rstd), nrows, s.fout, s.ln["eps"], _act(s.act))
+        else:
+            self._call(self._ln_fwd, st, _p(lb.Z) + o, s.ld, scale, bias, _p(lb.Y) + o, s.ld, _p(lb.mean) + 4 * row0,
+                       _p(lb.rstd) + 4 * row0, nrows, s.fout, s.ln["eps"], _act(s.act))
+
     def _view16(self, region: Region) -> int:
         """Address of a parameter region in the bf16 parameter image."""
         return _p(self.P16) + 2 * region.offset
@@ -498,15 +531,19 @@ class MLPExecutor:
                 self._call("ppo_splits_bias_act_bf16", st, _p(lb.fpart), s.ld, nrows * s.ld, self.FWD16_SPLITS, Bb,
                            _act(s.act) if s.ln is None else 0, _p(dst), s.ld, nrows, s.ld)
                 if s.ln is not None:
-                    self._call(self._ln_fwd, st, _p(lb.Z), s.ld, self.flat.view(s.ln["scale"]),
-                               self.flat.view(s.ln["bias"]), _p(lb.Y), s.ld, _p(lb.mean), _p(lb.rstd), nrows,
-                               s.fout, s.ln["eps"], _act(s.act))
+                    self._ln_forward(st, lb, o, row0, nrows)
+            elif self._y16_input(layers, li, nrows, row0):
+                prev = layers[li - 1]
+                dst = lb.Z if s.ln is not None else lb.Y
+                self._call("ppo_gemm_bf16s", st, A_ROW, B_KN, 1, 1, _p(prev.Y16), prev.spec.ld, None,
+                           self._view16(d.w), d.w.ld, _p(dst), s.ld, nrows, s.ld, d.fin, 1, 0, EPI_BIAS_ACT, Bb,
+                           _act(s.act) if s.ln is None else 0, 1, None, 0, None, -1)
+                if s.ln is not None:
+                    self._ln_forward(st, lb, o, row0, nrows)
             elif s.ln is not None:
                 self._gemm(st, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(lb.Z) + o, s.ld, nrows,
                           s.ld, d.fin, 1, 0, EPI_BIAS_ACT, Bb, 0, None, None, 0, None, -1)
-                self._call(self._ln_fwd, st, _p(lb.Z) + o, s.ld, self.flat.view(s.ln["scale"]),
-                          self.flat.view(s.ln["bias"]), _p(lb.Y) + o, s.ld, _p(lb.mean) + 4 * row0,
-                          _p(lb.rstd) + 4 * row0, nrows, s.fout, s.ln["eps"], _act(s.act))
+                self._ln_forward(st, lb, o, row0, nrows)
             else:
                 pre = _p(lb.PRE) + o if lb.PRE is not None else None
                 self._gemm(st, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(lb.Y) + o, s.ld, nrows,
@@ -535,25 +572,38 @@ class MLPExecutor:
             else:
                 x, ldx, ridx = x0, ldx0, idx0
             obs16 = i == 0 and self._reads_obs16(x, ridx, 0)
-            dz16 = obs16 and s.ln is not None  # the first layer's cotangent feeds only its dW: keep it bf16
+            y16 = i > 0 and layers[i - 1].Y16 is not None
+            # bf16 cotangent of a LayerNorm layer: read by its dW and dX contractions
+            dz16 = s.ln is not None and lb.dZ16 is not None and (obs16 or i > 0)
             if s.ln is not None:
                 self._call("ppo_layernorm_act_bwd_bf16_out16" if dz16 else self._ln_bwd, st, _p(lb.dY), s.ld,
                            _p(lb.Z), s.ld, _p(lb.mean), _p(lb.rstd), self.flat.view(s.ln["scale"]),
                            self.flat.view(s.ln["bias"]), _p(lb.dZ16) if dz16 else _p(lb.dZ), s.ld, _p(lb.lnpart),
                            self.mb, s.fout, _act(s.act))
+            dz = _p(lb.dZ16) if dz16 else _p(lb.dZ)
             if obs16:
-                self._call("ppo_gemm_bf16s", st, A_COL, B_KN, 1, 1 if dz16 else 0, _p(self.OBS16), self.ldo16, ridx,
-                           _p(lb.dZ16) if dz16 else _p(lb.dZ), s.ld, _p(lb.wpart), s.ld, d.fin, s.ld, self.mb,
-                           lb.splits, d.fin * s.ld, EPI_STORE, None, 0, 0, None, 0, _p(lb.bpart), -1)
+                self._call("ppo_gemm_bf16s", st, A_COL, B_KN, 1, int(dz16), _p(self.OBS16), self.ldo16, ridx, dz,
+                           s.ld, _p(lb.wpart), s.ld, d.fin, s.ld, self.mb, lb.splits, d.fin * s.ld, EPI_STORE, None,
+                           0, 0, None, 0, _p(lb.bpart), -1)
+            elif y16 or dz16:
+                a = _p(layers[i - 1].Y16) if y16 else x
+                self._call("ppo_gemm_bf16s", st, A_COL, B_KN, int(y16), int(dz16), a, ldx, None, dz, s.ld,
+                           _p(lb.wpart), s.ld, d.fin, s.ld, self.mb, lb.splits, d.fin * s.ld, EPI_STORE, None, 0, 0,
+                           None, 0, _p(lb.bpart), -1)
             else:
                 self._gemm(st, A_COL, B_KN, x, ldx, ridx, _p(lb.dZ), s.ld, _p(lb.wpart), s.ld, d.fin,
                           s.ld, self.mb, lb.splits, d.fin * s.ld, EPI_STORE, None, 0, None, None, 0, _p(lb.bpart),
                           -1)
             if i > 0:
                 dst, epi, act, aux, ldaux = self._dx_target(layers[i - 1])
-                self._gemm(st, A_ROW, B_NK, _p(lb.dZ), s.ld, None, self.flat.view(d.w), d.w.ld,
-                          dst, layers[i - 1].spec.ld, self.mb, d.fin, s.ld, 1, 0, epi, None, act, None, aux, ldaux,
-                          None, -1)
+                if dz16:
+                    self._call("ppo_gemm_bf16s", st, A_ROW, B_NK, 1, 1, dz, s.ld, None, self._view16(d.w), d.w.ld,
+                               dst, layers[i - 1].spec.ld, self.mb, d.fin, s.ld, 1, 0, epi, None, act, 1, aux,
+                               ldaux, None, -1)
+                else:
+                    self._gemm(st, A_ROW, B_NK, _p(lb.dZ), s.ld, None, self.flat.view(d.w), d.w.ld,
+                              dst, layers[i - 1].spec.ld, self.mb, d.fin, s.ld, 1, 0, epi, None, act, None, aux,
+                              ldaux, None, -1)
 
     def _head_back(self, st, layers, dhead, head: DenseSpec, wpart, bpart, splits, hx, ldhx, hidx):
         """Head dW and the cotangent of the head input."""
@@ -619,9 +669,10 @@ class MLPExecutor:
                 idx = _p(self.PERM) + 4 * (e * B + m * mb)
                 self._minibatch(st, idx, step, obs, ldo, dist, A)
                 self._call("ppo_grad_reduce", st, _p(self.SEGS), _p(self.CHUNKS), self.nchunks, _p(self.SUMSQ))
+                self._call("ppo_sumsq_total", st, _p(self.SUMSQ), self.nchunks, _p(self.SUMSQ1))
                 self._call("ppo_adam_clip_f32", st, _p(self.flat.P), _p(self.flat.G), _p(self.flat.MU),
                           _p(self.flat.NU), _p(self.P16) if self.obs16 else None, self.flat.P.numel(),
-                          _p(self.SUMSQ), self.nchunks,
+                          _p(self.SUMSQ1), 1,
                           float(max_norm), adam.learning_rate, adam.b1, adam.b2, adam.eps, _p(self.flat.count),
                           step)
         self._call("ppo_count_advance", st, _p(self.flat.count), self.E * self.M)

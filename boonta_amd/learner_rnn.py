@@ -153,8 +153,9 @@ class RecurrentExecutor(MLPExecutor):
                 envs = _p(self.PERM) + 4 * (e * N + m * Bm)
                 self._sequence_minibatch(st, rows, envs, step)
                 self._call("ppo_grad_reduce", st, _p(self.SEGS), _p(self.CHUNKS), self.nchunks, _p(self.SUMSQ))
+                self._call("ppo_sumsq_total", st, _p(self.SUMSQ), self.nchunks, _p(self.SUMSQ1))
                 self._call("ppo_adam_clip_f32", st, _p(self.flat.P), _p(self.flat.G), _p(self.flat.MU),
-                           _p(self.flat.NU), None, self.flat.P.numel(), _p(self.SUMSQ), self.nchunks,
+                           _p(self.flat.NU), None, self.flat.P.numel(), _p(self.SUMSQ1), 1,
                            float(max_norm), adam.learning_rate, adam.b1, adam.b2, adam.eps, _p(self.flat.count),
                            step)
         self._call("ppo_count_advance", st, _p(self.flat.count), self.E * self.M)

@@ -152,6 +152,11 @@ int ppo_layernorm_act_bwd_f32(void* stream, const float* dy, int64_t lddy, const
 int ppo_layernorm_act_fwd_bf16(void* stream, const float* z, int64_t ldz, const float* gamma, const float* beta,
                                float* y, int64_t ldy, float* mean, float* rstd, int rows, int F, float eps,
                                int act);
+/* ppo_layernorm_act_fwd_bf16 that also stores y as bf16 bit patterns (y16,
+ * row pitch ldy16 elements): the operand of the next bf16 contraction. */
+int ppo_layernorm_act_fwd_bf16_out16(void* stream, const float* z, int64_t ldz, const float* gamma, const float* beta,
+                                     float* y, int64_t ldy, void* y16, int64_t ldy16, float* mean, float* rstd,
+                                     int rows, int F, float eps, int act);
 int ppo_layernorm_act_bwd_bf16(void* stream, const float* dy, int64_t lddy, const float* z, int64_t ldz,
                                const float* mean, const float* rstd, const float* gamma, const float* beta,
                                float* dz, int64_t lddz, float* partial, int rows, int F, int act);
@@ -255,6 +260,9 @@ int ppo_grad_reduce(void* stream, const void* segs, const void* chunks, int nchu
 int ppo_adam_clip_f32(void* stream, float* params, const float* grads, float* mu, float* nu, void* params_bf16,
                       int64_t n, const double* sumsq, int nsumsq, double max_norm, double lr, double b1,
                       double b2, double eps, const int* count_base, int step_offset);
+/* total[0] = sum of sumsq[0..n) in a fixed order (one block of 1024 threads):
+ * the squared global norm, handed to ppo_adam_clip_f32 as one partial. */
+int ppo_sumsq_total(void* stream, const double* sumsq, int n, double* total);
 int ppo_count_advance(void* stream, int* count_base, int steps);
 
 #ifdef __cplusplus

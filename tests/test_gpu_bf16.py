@@ -151,7 +151,14 @@ def test_layernorm_relu_bf16_forward_and_backward():
     torch.cuda.synchronize()
     within_one_bf16_ulp(Y.cpu().numpy(), y_ref, exact_frac=0.99, atol=1e-6)
     within_one_bf16_ulp(DZ.cpu().numpy(), dz_ref, exact_frac=0.95, atol=1e-5)
-    # the bf16-stored cotangent holds exactly the bits of the rounded fp32 one
+    # the bf16-stored output and cotangent hold exactly the bits of the rounded fp32 ones
+    Y2 = torch.zeros(rows, F, device=DEV)
+    Y16 = torch.zeros(rows, F + 8, dtype=torch.int16, device=DEV)
+    _lib.call("ppo_layernorm_act_fwd_bf16_out16", st(), Z.data_ptr(), F, G.data_ptr(), Bt.data_ptr(), Y2.data_ptr(),
+              F, Y16.data_ptr(), F + 8, MEAN.data_ptr(), RSTD.data_ptr(), rows, F, 1e-6, 1)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(Y2.cpu().numpy(), Y.cpu().numpy())
+    np.testing.assert_array_equal(Y16.cpu().numpy()[:, :F].view(np.uint16), to_bf16_bits(Y.cpu().numpy()))
     DZ16 = torch.zeros(rows, F + 8, dtype=torch.int16, device=DEV)
     PART16 = torch.zeros(nb, 2 * F, device=DEV)
     _lib.call("ppo_layernorm_act_bwd_bf16_out16", st(), DY.data_ptr(), F, Z.data_ptr(), F, MEAN.data_ptr(),

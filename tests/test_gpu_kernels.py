@@ -349,6 +349,27 @@ def test_grad_reduce_and_adam_match_optax_restatement(max_norm, scale):
     np.testing.assert_allclose(host(MU), st2["mu"]["w"], rtol=1e-5, atol=1e-9)
     np.testing.assert_allclose(host(NU), st2["nu"]["w"], rtol=1e-5, atol=1e-12)
     np.testing.assert_allclose(host(P), new["w"], rtol=1e-6, atol=1e-7)
+    # the same step from the squared norm folded once (the learner's path)
+    SQ1 = torch.zeros(1, dtype=torch.float64, device=DEV)
+    _lib.call("ppo_sumsq_total", st(), SQ.data_ptr(), nch, SQ1.data_ptr())
+    P2, MU2, NU2 = dev(p0), dev(mu0), dev(nu0)
+    _lib.call("ppo_adam_clip_f32", st(), P2.data_ptr(), Gt.data_ptr(), MU2.data_ptr(), NU2.data_ptr(), None, n,
+              SQ1.data_ptr(), 1, max_norm, 3e-4, 0.9, 0.999, 1e-8, count.data_ptr(), 2)
+    np.testing.assert_allclose(host(SQ1)[0], host(SQ).sum(), rtol=1e-14)
+    np.testing.assert_allclose(host(P2), new["w"], rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("n", [0, 1, 1023, 1024, 18700])
+def test_sumsq_total_fixed_order(n):
+    v = np.random.default_rng(n).random(n)
+    V = torch.tensor(v, dtype=torch.float64, device=DEV) if n else torch.zeros(1, dtype=torch.float64, device=DEV)
+    T1 = torch.full((1,), 7.0, dtype=torch.float64, device=DEV)
+    T2 = torch.full((1,), 7.0, dtype=torch.float64, device=DEV)
+    _lib.call("ppo_sumsq_total", st(), V.data_ptr(), n, T1.data_ptr())
+    _lib.call("ppo_sumsq_total", st(), V.data_ptr(), n, T2.data_ptr())
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(host(T1)[0], v.sum(), rtol=1e-13, atol=0)
+    assert host(T1)[0] == host(T2)[0]
 
 
 # ------------------------------------------------------- fused heads + loss
