@@ -88,6 +88,33 @@ __device__ __forceinline__ uint32_t bf16_bits(float x) {
 
 __device__ __forceinline__ float bf16_round(float x) { return __uint_as_float(bf16_bits(x) << 16); }
 
+// ---- direct global -> LDS copies (global_load_lds_dwordx4) ----
+// One 1 KB copy: lane l's 16 bytes at src go to LDS lds_wave_base + 16 l.
+// Issued as inline assembly so that the compiler's wait insertion does not
+// treat every later LDS read as dependent on it (it cannot tell the slots of
+// a ring buffer apart and would wait for all copies); stage_barrier waits
+// for the copies explicitly.
+__device__ __forceinline__ void lds_copy16(const void* src, void* lds_wave_base) {
+  typedef __attribute__((address_space(3))) void lds_void_t;
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)(lds_wave_base));
+  asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(m0v) : "memory");
+}
+
+// Ring-buffer stage barrier: this wave's copies older than the newest N are
+// complete and its LDS accesses are done, then every wave of the block meets.
+template <int N>
+__device__ __forceinline__ void stage_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
+}
+
+// XOR applied to the 16-byte chunk index (0..7) of row r of a 128-byte-row
+// LDS tile: neither 16-byte copies / stores (8 lanes per row) nor reads of
+// one chunk over 32 consecutive rows put two lanes of a bank phase on a bank.
+__device__ __forceinline__ int kc_swizzle(int r) {
+  return (r & 3) ^ ((r & 4) ? 5 : 0) ^ ((r & 8) ? 3 : 0) ^ ((r & 16) ? 4 : 0);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

@@ -24,36 +24,16 @@
 // for the bias gradient (one extra add per MFMA in the waves of the first row
 // tile), and writes one partial per split; partials are reduced in a fixed
 // order later, so results do not depend on scheduling.
-#include "common.h"
+#include "gemm_f32.h"
 
 #include <algorithm>
 
 namespace {
 
+using namespace ppo_f32;
+
 constexpr int BK_MIN = 16;  // reduction granule: k_per_split is a multiple of it
 constexpr int LDS_PAD = 4;
-
-enum Epilogue { EPI_STORE = 0, EPI_BIAS_ACT = 1, EPI_DACT = 2 };
-
-struct GemmParams {
-  const float* A;
-  int64_t lda;
-  const int32_t* rows;  // gather indices (see header comment) or null
-  const float* B;
-  int64_t ldb;
-  float* C;
-  int64_t ldc;
-  int64_t c_split_stride;  // elements between split-K partial outputs
-  int M, N, K;
-  int k_per_split;  // multiple of BK
-  int epi;
-  const float* bias;  // EPI_BIAS_ACT: [N] or null
-  int act;
-  float* pre;  // EPI_BIAS_ACT: optional pre-activation output (ldc)
-  const float* aux;  // EPI_DACT: activation output (relu, tanh) or input (silu), ld = ldaux
-  int64_t ldaux;
-  float* bias_grad;  // dW: [splits][N] column sums of B, or null
-};
 
 // Four consecutive elements of a (valid) row at i.  Out-of-range elements
 // read a clamped valid address and are flagged in `bits` (bit e set: element
@@ -245,41 +225,7 @@ __global__ void __launch_bounds__(256, 2) gemm_f32_kernel(GemmParams p) {
     __syncthreads();
   }
 
-  // ---------------------------------------------------------------- epilogue
-  float* C = p.C + (int64_t)split * p.c_split_stride;
-#pragma unroll
-  for (int bi = 0; bi < MB; ++bi) {
-#pragma unroll
-    for (int bj = 0; bj < NB; ++bj) {
-      const int gn = n0 + wn * (BN / 2) + bj * 32 + l32;
-      const bool n_ok = gn < p.N;
-      float bias = 0.f;
-      if (p.epi == EPI_BIAS_ACT && p.bias && n_ok) bias = p.bias[gn];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int gm = m0 + wm * (BM / 2) + bi * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (!n_ok || gm >= p.M) continue;
-        float v = acc[bi][bj][r];
-        const int64_t o = (int64_t)gm * p.ldc + gn;
-        if (p.epi == EPI_BIAS_ACT) {
-          v += bias;
-          if (p.pre) p.pre[o] = v;
-          v = ppo::act_fwd(p.act, v);
-        } else if (p.epi == EPI_DACT) {
-          v *= ppo::act_grad(p.act, p.aux[(int64_t)gm * p.ldaux + gn]);
-        }
-        C[o] = v;
-      }
-    }
-  }
-  if (do_bsum) {
-#pragma unroll
-    for (int bj = 0; bj < NB; ++bj) {
-      const float t = bsum[bj] + __shfl_xor(bsum[bj], 32, 64);
-      const int gn = n0 + wn * (BN / 2) + bj * 32 + l32;
-      if (h == 0 && gn < p.N) p.bias_grad[(int64_t)split * p.N + gn] = t;
-    }
-  }
+  epilogue_f32<MB, NB>(p, acc, bsum, do_bsum, m0 + wm * (BM / 2), n0 + wn * (BN / 2), split, lane);
 }
 
 template <int BM, int BN, int BK, bool A_K, bool B_K>
@@ -316,8 +262,9 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 //   rows: gather of A's rows (layout 0: over m; layout 1: over k) or null.
 //   epi 0: store; 1: bias + activation (pre-activation to `pre` if non-null);
 //   2: multiply by act'(aux).  bias_grad (layout a=1, b=0 only): [splits][N] sums of B.
-//   tile: -1 picks a tile; 0: 128x128, 1: 128x64, 2: 64x128, 3: 64x64 with 16 reduction
-//   elements per LDS stage; 4-7 the same tiles with 32 per stage.
+//   tile: -1 picks a tile; 0: 128x128, 1: 128x64, 2: 64x128, 3: 64x64 (copy-fed, 32 reduction
+//   elements per stage, when the operands allow; else register-staged with 16); 4-7 the same
+//   tiles register-staged with 32 per stage.
 PPO_EXPORT int ppo_gemm_f32(void* stream, int a_layout, int b_layout, const float* A, int64_t lda,
                             const int32_t* rows, const float* B, int64_t ldb, float* C, int64_t ldc, int M,
                             int N, int K, int splits, int64_t c_split_stride, int epi, const float* bias,
@@ -348,6 +295,14 @@ PPO_EXPORT int ppo_gemm_f32(void* stream, int a_layout, int b_layout, const floa
   // larger tiles' register reuse gains).
   if (tile < 0) tile = 3;
   hipStream_t st = ppo::as_stream(stream);
+  // Tiles 0-3 run on the copy-fed pipeline (gemm_f32d.hip) whenever every
+  // operand row is 16-byte vectorisable and a gathered k-outer A fits its
+  // index cache; tiles 4-7 (and the rest) on the register-staged one here.
+  const int kps_d = ((ppo::ceil_div(K > 0 ? K : 1, splits) + F32D_BK - 1) / F32D_BK) * F32D_BK;
+  if (tile <= 3 && va && vb && !(a_layout == 1 && rows && kps_d > F32D_KIDX_MAX)) {
+    p.k_per_split = kps_d;
+    return launch_dma(st, p, splits, tile, a_layout, b_layout);
+  }
   if (a_layout == 0 && b_layout == 0) return launch_layout<true, false>(st, p, splits, va, vb, tile);
   if (a_layout == 0 && b_layout == 1) return launch_layout<true, true>(st, p, splits, va, vb, tile);
   if (a_layout == 1 && b_layout == 0) return launch_layout<false, false>(st, p, splits, va, vb, tile);

@@ -27,32 +27,13 @@ namespace ppo_bf16s {
 constexpr int NBUF = 3;
 constexpr int KIDX_MAX = 2048;  // reduction rows per split when the k-outer A operand is gathered
 
-__device__ __forceinline__ int kc_swizzle(int r) {
-  return (r & 3) ^ ((r & 4) ? 5 : 0) ^ ((r & 8) ? 3 : 0) ^ ((r & 16) ? 4 : 0);
-}
+using ppo::kc_swizzle;
 __device__ __forceinline__ int ko_swizzle(int k) { return ((k & 1) ? 4 : 0) ^ ((k & 2) ? 10 : 0); }
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void global_void_t;
-
-// One 1 KB copy: lane l's 16 bytes at src go to LDS wave_base + 16 l.  Issued
-// as inline assembly so that the compiler's wait insertion does not treat
-// every later LDS read as dependent on it (it cannot tell the ring slots
-// apart and would wait for all copies); the stage barrier below waits for
-// the copies explicitly.
 __device__ __forceinline__ void copy16_to_lds(const uint16_t* src, uint16_t* lds_wave_base) {
-  const uint32_t m0v =
-      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)(lds_wave_base));
-  asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(m0v) : "memory");
+  ppo::lds_copy16(src, lds_wave_base);
 }
-
-// Stage barrier: this wave's copies older than the newest N are complete
-// and its LDS accesses are done, then every wave meets.
-template <int N>
-__device__ __forceinline__ void stage_barrier() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
-}
+using ppo::stage_barrier;
 
 // One operand's copies: ROWS x BK per stage in 1 KB copies (64 lanes x 16 B),
 // PERW copies per wave.  For copy i of a wave, lane l fills LDS unit

@@ -1,0 +1,83 @@
+// Shared pieces of the fp32 GEMM (gemm.hip: register-staged pipeline;
+// gemm_f32d.hip: pipeline fed by direct global -> LDS copies): parameters
+// and the epilogue.
+#pragma once
+#include "common.h"
+
+namespace ppo_f32 {
+
+enum Epilogue { EPI_STORE = 0, EPI_BIAS_ACT = 1, EPI_DACT = 2 };
+
+struct GemmParams {
+  const float* A;
+  int64_t lda;
+  const int32_t* rows;  // gather indices (A's rows for a_layout 0, reduction rows for 1) or null
+  const float* B;
+  int64_t ldb;
+  float* C;
+  int64_t ldc;
+  int64_t c_split_stride;  // elements between split-K partial outputs
+  int M, N, K;
+  int k_per_split;  // multiple of the kernel's stage depth
+  int epi;
+  const float* bias;  // EPI_BIAS_ACT: [N] or null
+  int act;
+  float* pre;  // EPI_BIAS_ACT: optional pre-activation output (ldc)
+  const float* aux;  // EPI_DACT: activation output (relu, tanh) or input (silu), ld = ldaux
+  int64_t ldaux;
+  float* bias_grad;  // dW: [splits][N] column sums of B, or null
+};
+
+// Stores a wave's MB x NB blocks of 32 x 32 (v_mfma_f32_32x32x*: lane l holds
+// rows 8 (r / 4) + 4 (l / 32) + r % 4 of column l % 32) from row wm0 and column
+// wn0 through the epilogue, and the bias-gradient column sums of B.
+template <int MB, int NB>
+__device__ __forceinline__ void epilogue_f32(const GemmParams& p, floatx16 (&acc)[MB][NB], const float (&bsum)[NB],
+                                             bool do_bsum, int wm0, int wn0, int split, int lane) {
+  const int h = lane >> 5;
+  const int l32 = lane & 31;
+  float* C = p.C + (int64_t)split * p.c_split_stride;
+#pragma unroll
+  for (int bi = 0; bi < MB; ++bi) {
+#pragma unroll
+    for (int bj = 0; bj < NB; ++bj) {
+      const int gn = wn0 + bj * 32 + l32;
+      const bool n_ok = gn < p.N;
+      float bias = 0.f;
+      if (p.epi == EPI_BIAS_ACT && p.bias && n_ok) bias = p.bias[gn];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int gm = wm0 + bi * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (!n_ok || gm >= p.M) continue;
+        float v = acc[bi][bj][r];
+        const int64_t o = (int64_t)gm * p.ldc + gn;
+        if (p.epi == EPI_BIAS_ACT) {
+          v += bias;
+          if (p.pre) p.pre[o] = v;
+          v = ppo::act_fwd(p.act, v);
+        } else if (p.epi == EPI_DACT) {
+          v *= ppo::act_grad(p.act, p.aux[(int64_t)gm * p.ldaux + gn]);
+        }
+        C[o] = v;
+      }
+    }
+  }
+  if (do_bsum) {
+#pragma unroll
+    for (int bj = 0; bj < NB; ++bj) {
+      const float t = bsum[bj] + __shfl_xor(bsum[bj], 32, 64);
+      const int gn = wn0 + bj * 32 + l32;
+      if (h == 0 && gn < p.N) p.bias_grad[(int64_t)split * p.N + gn] = t;
+    }
+  }
+}
+
+// The copy-fed pipeline (gemm_f32d.hip): 16-byte rows along every operand's
+// contiguous axis, stage depth F32D_BK; false when the shape needs the
+// register-staged one (a gathered k-outer A with more reduction rows per
+// split than the kernel caches).
+constexpr int F32D_BK = 32;
+constexpr int F32D_KIDX_MAX = 2048;
+int launch_dma(hipStream_t st, const GemmParams& p, int splits, int tile, int a_layout, int b_layout);
+
+}  // namespace ppo_f32

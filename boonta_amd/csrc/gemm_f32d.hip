@@ -1,0 +1,261 @@
+// fp32 GEMM fed by direct global -> LDS copies (global_load_lds_dwordx4: each
+// lane's 16 bytes land at the wave's LDS base + 16 * lane), for operands with
+// 16-byte rows along their contiguous axis.  Same contraction, layouts, row
+// gather, split-K and epilogues as the register-staged kernel in gemm.hip;
+// no registers hold staged data and no LDS store instructions run, so three
+// stages of copies stay in flight behind the MFMAs.
+//
+// Tiles: 4 wave64s in 2 x 2, each (BM/2) x (BN/2) of 32 x 32 blocks of
+// v_mfma_f32_32x32x2_f32; 32 reduction elements per stage.  Inside each group
+// of 8 reduction elements, lane half h consumes k = 8g + 4h + s at MFMA step
+// s (both operands use the same order, so the sum is unchanged).
+// LDS layouts (fp32, 16-byte chunks XOR-swizzled on the copy side):
+//   k-contiguous [ROWS][32]: chunk c of row r at c ^ kc_swizzle(r); an operand
+//     read (4 consecutive k of one row) is one 16-byte read;
+//   k-outer [32][ROWS]: chunk c of k row k at c ^ (8 * bit 2 of k), so the two
+//     lane halves (k and k + 4) read different bank halves.
+// Ragged edges: rows beyond M / N are read from a clamped in-range row or
+// column (only outputs that are not stored see them); a final stage cut short
+// by K goes through registers with the elements past K zeroed.
+#include "gemm_f32.h"
+
+namespace ppo_f32 {
+namespace {
+
+constexpr int BK = F32D_BK;
+constexpr int NBUF = 3;
+constexpr int NW = 4;
+
+__device__ __forceinline__ int ko_swizzle32(int k) { return ((k >> 2) & 1) << 3; }
+
+// One operand's copies: ROWS x BK fp32 per stage in 1 KB copies (64 lanes x
+// 16 B), PERW per wave; copy i of a wave fills LDS units 64 (wave PERW + i) + l.
+template <int ROWS, bool KC>
+struct Operand {
+  static constexpr int ELEMS = ROWS * BK;
+  static constexpr int COPIES = ELEMS / 256;
+  static constexpr int PERW = COPIES / NW;
+  static_assert(PERW >= 1 && COPIES % NW == 0, "tile too small for four waves");
+  static_assert(KC || ROWS >= 64, "k-outer swizzle needs 16 chunks per k row");
+  const float* src[PERW];  // KC: the (gathered) row; k-outer: the operand base
+  int col[PERW];           // KC: the unit's k offset in the stage; k-outer: its first element (clamped)
+  int krow[PERW];          // k-outer: the unit's k row in the stage
+  bool ok[PERW];           // KC: row in range
+
+  __device__ __forceinline__ void init(const float* base, int64_t ld, int r0, int lim, const int32_t* rows_idx,
+                                       int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < PERW; ++i) {
+      const int u = 64 * (wave * PERW + i) + lane;
+      if (KC) {
+        const int r = u / (BK / 4);
+        const int g = r0 + r;
+        ok[i] = g < lim;
+        const int gc = ok[i] ? g : 0;
+        const int64_t row = rows_idx ? (int64_t)rows_idx[gc] : (int64_t)gc;
+        src[i] = base + row * ld;
+        col[i] = 4 * ((u % (BK / 4)) ^ ppo::kc_swizzle(r));
+        krow[i] = 0;
+      } else {
+        const int k = u / (ROWS / 4);
+        const int c = (u % (ROWS / 4)) ^ ko_swizzle32(k);
+        const int last = ((lim - 1) / 4) * 4;
+        src[i] = base;
+        col[i] = min(r0 + 4 * c, last);
+        krow[i] = k;
+        ok[i] = true;
+      }
+    }
+  }
+
+  __device__ __forceinline__ int64_t row_of(int k, int kb, const int32_t* kidx) const {
+    return kidx ? (int64_t)kidx[k - kb] : (int64_t)k;
+  }
+
+  __device__ __forceinline__ void copy(float* lds_stage, int64_t ld, int k0, int kb, const int32_t* kidx,
+                                       int wave) const {
+#pragma unroll
+    for (int i = 0; i < PERW; ++i) {
+      float* dst = lds_stage + 256 * (wave * PERW + i);
+      if (KC)
+        ppo::lds_copy16(src[i] + k0 + col[i], dst);
+      else
+        ppo::lds_copy16(src[i] + row_of(k0 + krow[i], kb, kidx) * ld + col[i], dst);
+    }
+  }
+
+  // Registers, elements at k >= ke (k-outer: also columns >= lim) zeroed.
+  __device__ __forceinline__ void copy_masked(float* lds_stage, int64_t ld, int k0, int ke, int lim, int kb,
+                                              const int32_t* kidx, int wave, int lane) const {
+    floatx4 v[PERW];
+#pragma unroll
+    for (int i = 0; i < PERW; ++i) {
+      if (KC) {
+        const int k = k0 + col[i];
+        const bool in = ok[i] && k < ke;
+        v[i] = *reinterpret_cast<const floatx4*>(src[i] + (in ? k : 0));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[i][e] = (in && k + e < ke) ? v[i][e] : 0.f;
+      } else {
+        const int k = k0 + krow[i];
+        const bool in = k < ke;
+        v[i] = *reinterpret_cast<const floatx4*>(src[i] + row_of(in ? k : k0, kb, kidx) * ld + col[i]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[i][e] = (in && col[i] + e < lim) ? v[i][e] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < PERW; ++i)
+      *reinterpret_cast<floatx4*>(lds_stage + 256 * (wave * PERW + i) + 4 * lane) = v[i];
+  }
+};
+
+// Operand values of 32 rows from rbase for reduction group g: element s is
+// the value at k = 8g + 4h + s of row rbase + l32.
+template <int ROWS, bool KC>
+__device__ __forceinline__ floatx4 operand(const float* lds, int rbase, int g, int lane) {
+  const int h = lane >> 5;
+  const int r = rbase + (lane & 31);
+  if (KC) {
+    const int c = 2 * g + h;
+    return *reinterpret_cast<const floatx4*>(lds + r * BK + ((c ^ ppo::kc_swizzle(r)) << 2));
+  } else {
+    floatx4 v;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int k = 8 * g + 4 * h + s;
+      v[s] = lds[k * ROWS + ((((r >> 2) ^ ko_swizzle32(k))) << 2) + (r & 3)];
+    }
+    return v;
+  }
+}
+
+template <int BM, int BN, bool A_K, bool B_K>
+__global__ void __launch_bounds__(NW * 64) gemm_f32d_kernel(GemmParams p) {
+  constexpr int MB = BM / 64, NB = BN / 64;
+  using OpA = Operand<BM, A_K>;
+  using OpB = Operand<BN, B_K>;
+  __shared__ __attribute__((aligned(1024))) float sA[NBUF][OpA::ELEMS];
+  __shared__ __attribute__((aligned(1024))) float sB[NBUF][OpB::ELEMS];
+  __shared__ int32_t sIdx[A_K ? 1 : F32D_KIDX_MAX];  // gather indices of the split (k-outer A)
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave & 1;
+  const int wn = wave >> 1;
+  const ppo::TileCoord tc = ppo::xcd_tile();
+  const int m0 = tc.m * BM;
+  const int n0 = tc.n * BN;
+  const int split = tc.z;
+  const int kb = split * p.k_per_split;
+  const int ke = min(p.K, kb + p.k_per_split);
+
+  floatx16 acc[MB][NB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  float bsum[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) bsum[j] = 0.f;
+  const bool do_bsum = (p.bias_grad != nullptr) && (tc.m == 0) && (wm == 0);
+
+  OpA oa;
+  OpB ob;
+  oa.init(p.A, p.lda, m0, p.M, A_K ? p.rows : nullptr, wave, lane);
+  ob.init(p.B, p.ldb, n0, p.N, nullptr, wave, lane);
+  const int32_t* kidx = nullptr;
+  if (!A_K && p.rows) {
+    for (int i = threadIdx.x; i < ke - kb; i += NW * 64) sIdx[i] = p.rows[kb + i];
+    kidx = sIdx;
+    __syncthreads();
+  }
+
+  const int nk = (ke > kb) ? (ke - kb + BK - 1) / BK : 0;
+  const int nfull = (ke - kb) / BK;
+  constexpr int PER_STAGE = OpA::PERW + OpB::PERW;
+
+  auto issue = [&](int s) {
+    float* la = sA[s % NBUF];
+    float* lb = sB[s % NBUF];
+    const int k0 = kb + s * BK;
+    if (s < nfull) {
+      oa.copy(la, p.lda, k0, kb, kidx, wave);
+      ob.copy(lb, p.ldb, k0, kb, nullptr, wave);
+    } else {
+      oa.copy_masked(la, p.lda, k0, ke, p.M, kb, kidx, wave, lane);
+      ob.copy_masked(lb, p.ldb, k0, ke, p.N, kb, nullptr, wave, lane);
+    }
+  };
+
+#pragma unroll
+  for (int s = 0; s < NBUF - 1; ++s)
+    if (s < nk) issue(s);
+
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 1 < nk)
+      ppo::stage_barrier<PER_STAGE * (NBUF - 2)>();
+    else
+      ppo::stage_barrier<0>();
+    if (kt + NBUF - 1 < nk) issue(kt + NBUF - 1);
+    const float* la = sA[kt % NBUF];
+    const float* lb = sB[kt % NBUF];
+    floatx4 a4[2][MB], b4[2][NB];
+    auto read_ops = [&](int set, int g) {
+#pragma unroll
+      for (int bi = 0; bi < MB; ++bi) a4[set][bi] = operand<BM, A_K>(la, wm * (BM / 2) + bi * 32, g, lane);
+#pragma unroll
+      for (int bj = 0; bj < NB; ++bj) b4[set][bj] = operand<BN, B_K>(lb, wn * (BN / 2) + bj * 32, g, lane);
+    };
+    read_ops(0, 0);
+#pragma unroll
+    for (int g = 0; g < BK / 8; ++g) {
+      const int cur = g & 1;
+      if (g + 1 < BK / 8) read_ops(cur ^ 1, g + 1);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int bi = 0; bi < MB; ++bi)
+#pragma unroll
+          for (int bj = 0; bj < NB; ++bj)
+            acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[cur][bi][s], b4[cur][bj][s], acc[bi][bj], 0, 0, 0);
+      if (do_bsum) {
+#pragma unroll
+        for (int bj = 0; bj < NB; ++bj)
+          bsum[bj] += (b4[cur][bj][0] + b4[cur][bj][1]) + (b4[cur][bj][2] + b4[cur][bj][3]);
+      }
+    }
+  }
+
+  epilogue_f32<MB, NB>(p, acc, bsum, do_bsum, m0 + wm * (BM / 2), n0 + wn * (BN / 2), split, lane);
+}
+
+template <int BM, int BN, bool A_K, bool B_K>
+int launch(hipStream_t st, const GemmParams& p, int splits) {
+  dim3 grid(ppo::ceil_div(p.N, BN), ppo::ceil_div(p.M, BM), splits);
+  hipLaunchKernelGGL((gemm_f32d_kernel<BM, BN, A_K, B_K>), grid, dim3(NW * 64), 0, st, p);
+  return ppo::check_launch("ppo_gemm_f32");
+}
+
+template <bool A_K, bool B_K>
+int launch_tile(hipStream_t st, const GemmParams& p, int splits, int tile) {
+  switch (tile) {
+    case 0: return launch<128, 128, A_K, B_K>(st, p, splits);
+    case 1: return launch<128, 64, A_K, B_K>(st, p, splits);
+    case 2: return launch<64, 128, A_K, B_K>(st, p, splits);
+    default: return launch<64, 64, A_K, B_K>(st, p, splits);
+  }
+}
+
+}  // namespace
+
+int launch_dma(hipStream_t st, const GemmParams& p, int splits, int tile, int a_layout, int b_layout) {
+  if (a_layout == 0 && b_layout == 0) return launch_tile<true, false>(st, p, splits, tile);
+  if (a_layout == 0 && b_layout == 1) return launch_tile<true, true>(st, p, splits, tile);
+  if (a_layout == 1 && b_layout == 0) return launch_tile<false, false>(st, p, splits, tile);
+  return launch_tile<false, true>(st, p, splits, tile);
+}
+
+}  // namespace ppo_f32

@@ -169,12 +169,13 @@ def gemm_case(a_layout, b_layout, M, N, K, rows_src=None, gather=False, epi=0, a
 
 
 @pytest.mark.parametrize("a_layout, b_layout", [(0, 0), (0, 1), (1, 0), (1, 1)])
-@pytest.mark.parametrize("M, N, K", [(256, 256, 64), (100, 72, 87), (33, 7, 5), (1, 1, 1), (300, 130, 400)])
+@pytest.mark.parametrize("M, N, K", [(256, 256, 64), (100, 72, 87), (33, 7, 5), (1, 1, 1), (300, 130, 400),
+                                     (300, 132, 404), (68, 36, 1000)])
 def test_gemm_layouts_match_float64(a_layout, b_layout, M, N, K):
     gemm_case(a_layout, b_layout, M, N, K, seed=M + N + K)
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7])
 def test_gemm_every_tile(tile):
     gemm_case(0, 0, 200, 190, 48, tile=tile, seed=tile)
     gemm_case(1, 0, 130, 70, 500, tile=tile, splits=3, bias_grad=True, seed=tile + 10)
