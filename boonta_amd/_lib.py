@@ -26,6 +26,9 @@ SIGNATURES = {
     "ppo_clear_error": (None, []),
     "ppo_abi_version": (I, []),
     "ppo_device_check": (I, [I]),
+    "ppo_event_create": (I, [ctypes.POINTER(ctypes.c_void_p)]),
+    "ppo_event_destroy": (I, [P]),
+    "ppo_stream_wait": (I, [P, P, P]),
     "ppo_gae_f32": (I, [P, P, P, P, P, P, P, P, P, P, I, I, D, D, I]),
     "ppo_normalize_workspace": (SZ, [I64]),
     "ppo_normalize_advantages_f32": (I, [P, P, I64, P, SZ]),

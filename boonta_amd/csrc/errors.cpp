@@ -35,3 +35,32 @@ PPO_EXPORT int ppo_device_check(int device) {
                           hipGetErrorString(e));
   return PPO_OK;
 }
+
+// ---- stream ordering for the learner's two-tower fork / join ----
+// An event without timing, for ppo_stream_wait.
+PPO_EXPORT int ppo_event_create(void** event) {
+  if (!event) return ppo::set_error(PPO_ERR_ARG, "ppo_event_create: null output");
+  hipEvent_t e = nullptr;
+  const hipError_t r = hipEventCreateWithFlags(&e, hipEventDisableTiming);
+  if (r != hipSuccess) return ppo::set_error(PPO_ERR_LAUNCH, "ppo_event_create: %s", hipGetErrorString(r));
+  *event = e;
+  return PPO_OK;
+}
+
+PPO_EXPORT int ppo_event_destroy(void* event) {
+  if (event) (void)hipEventDestroy(static_cast<hipEvent_t>(event));
+  return PPO_OK;
+}
+
+// Work issued on `waiter` after this call starts after everything issued on
+// `signaller` before it (the event is recorded on signaller, then waited on
+// by waiter).  Inside a stream capture this forks / joins the captured graph.
+// Stream handles are hipStream_t values (0: the null stream).
+PPO_EXPORT int ppo_stream_wait(void* waiter, void* signaller, void* event) {
+  if (!event) return ppo::set_error(PPO_ERR_ARG, "ppo_stream_wait: null event");
+  hipEvent_t e = static_cast<hipEvent_t>(event);
+  hipError_t r = hipEventRecord(e, ppo::as_stream(signaller));
+  if (r == hipSuccess) r = hipStreamWaitEvent(ppo::as_stream(waiter), e, 0);
+  if (r != hipSuccess) return ppo::set_error(PPO_ERR_LAUNCH, "ppo_stream_wait: %s", hipGetErrorString(r));
+  return PPO_OK;
+}

@@ -22,6 +22,7 @@ PRNG key are read from device memory).
 """
 from __future__ import annotations
 
+import ctypes
 import math
 import struct
 from dataclasses import dataclass, field
@@ -383,6 +384,17 @@ class MLPExecutor:
         self.NORM_WS = torch.zeros(max(1, lib.ppo_normalize_workspace(self.B)), dtype=torch.uint8, device=dev)
         self._alloc_extra()
         self._build_reduce_tables()
+        # separate actor and critic towers run their chains on two streams
+        self.side = torch.cuda.Stream(device=dev) if torch.device(dev).type == "cuda" else None
+        self._recording = False
+        self._ev_fork = self._ev_join = None
+        if self.side is not None:
+            evs = []
+            for _ in range(2):
+                h = ctypes.c_void_p()
+                self._call("ppo_event_create", ctypes.byref(h))
+                evs.append(h.value)
+            self._ev_fork, self._ev_join = evs
 
     def _alloc_extra(self):
         """Buffers a subclass adds before the gradient tables are built."""
@@ -726,11 +738,15 @@ class MLPExecutor:
                 self._fused_head_loss(st, idx, step, dist, A, scale_ptr, act_i, act_f)
                 self._bwd_layers(st, self.trunk, obs, ldo, idx)
             else:
+                s2 = self._fork(st)
                 self._fwd_layers(st, self.actor, obs, ldo, idx, mb)
-                self._fwd_layers(st, self.critic, obs, ldo, idx, mb)
+                self._fwd_layers(s2, self.critic, obs, ldo, idx, mb)
+                self._join(st, s2)
                 self._fused_head_loss(st, idx, step, dist, A, scale_ptr, act_i, act_f)
+                s2 = self._fork(st)
                 self._bwd_layers(st, self.actor, obs, ldo, idx)
-                self._bwd_layers(st, self.critic, obs, ldo, idx)
+                self._bwd_layers(s2, self.critic, obs, ldo, idx)
+                self._join(st, s2)
             return
         if prog.shared_head:
             hx, ldhx, hidx = self._fwd_layers(st, self.trunk, obs, ldo, idx, mb)
@@ -749,27 +765,31 @@ class MLPExecutor:
                             hidx)
             self._bwd_layers(st, self.trunk, obs, ldo, idx)
         else:
-            ax, ldax, aidx = self._fwd_layers(st, self.actor, obs, ldo, idx, mb)
-            cx, ldcx, cidx = self._fwd_layers(st, self.critic, obs, ldo, idx, mb)
             ha, hc = prog.head_a, prog.head_c
+            s2 = self._fork(st)
+            ax, ldax, aidx = self._fwd_layers(st, self.actor, obs, ldo, idx, mb)
+            cx, ldcx, cidx = self._fwd_layers(s2, self.critic, obs, ldo, idx, mb)
             self._gemm(st, A_ROW, B_KN, ax, ldax, aidx, self.flat.view(ha.w), ha.w.ld, _p(self.HA),
                       ha.w.ld, mb, ha.w.ld, ha.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(ha.b), 0, None, None, 0,
                       None, -1)
-            self._gemm(st, A_ROW, B_KN, cx, ldcx, cidx, self.flat.view(hc.w), hc.w.ld, _p(self.HC),
+            self._gemm(s2, A_ROW, B_KN, cx, ldcx, cidx, self.flat.view(hc.w), hc.w.ld, _p(self.HC),
                       hc.w.ld, mb, hc.w.ld, hc.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(hc.b), 0, None, None, 0,
                       None, -1)
+            self._join(st, s2)
             self._call("ppo_loss_f32", st, dist, mb, idx, _p(self.HA), ha.w.ld, _p(self.HC), hc.w.ld, A, scale_ptr,
                       act_i, act_f, inp["log_prob"], inp["value"], _p(self.ADV), _p(self.RET), _p(self.DHA),
                       _p(self.DHC), _p(self.DSCALE), _p(self.STATS), clip, int(cfg.clip_value_loss),
                       float(cfg.entropy_coefficient), float(cfg.value_coefficient), 1.0)
             self._call("ppo_loss_finalize", st, _p(self.STATS), self.loss_blocks, mb,
                       float(cfg.entropy_coefficient), float(cfg.value_coefficient), _p(self.LOGS) + 4 * 9 * step)
+            s2 = self._fork(st)
             self._head_back(st, self.actor, self.DHA, ha, self.HAWPART, self.HABPART, self.ha_splits, ax, ldax,
                             aidx)
-            self._head_back(st, self.critic, self.DHC, hc, self.HCWPART, self.HCBPART, self.hc_splits, cx, ldcx,
+            self._head_back(s2, self.critic, self.DHC, hc, self.HCWPART, self.HCBPART, self.hc_splits, cx, ldcx,
                             cidx)
             self._bwd_layers(st, self.actor, obs, ldo, idx)
-            self._bwd_layers(st, self.critic, obs, ldo, idx)
+            self._bwd_layers(s2, self.critic, obs, ldo, idx)
+            self._join(st, s2)
 
     # ------------------------------------------------------------ recording
     def record(self, max_steps: int | None = None) -> list:
@@ -777,8 +797,31 @@ class MLPExecutor:
         running it (used by the benchmark to time single launches)."""
         calls = []
         self._call = lambda name, *args: calls.append((name, args))
+        self._recording = True
         try:
             self.issue(0, max_steps=max_steps)
         finally:
             self._call = _lib.call
+            self._recording = False
         return calls
+
+    # ------------------------------------------------------ two towers at once
+    def _fork(self, st: int) -> int:
+        """Handle of the side stream, ordered after everything issued on st so
+        far (inside a graph capture this forks the captured graph)."""
+        if self._recording or self.side is None:
+            return st
+        side = self.side.cuda_stream
+        self._call("ppo_stream_wait", side, st, self._ev_fork)
+        return side
+
+    def _join(self, st: int, st2: int):
+        """Orders st after everything issued on the side stream st2."""
+        if st2 == st:
+            return
+        self._call("ppo_stream_wait", st, st2, self._ev_join)
+
+    def __del__(self):
+        for ev in (getattr(self, "_ev_fork", None), getattr(self, "_ev_join", None)):
+            if ev:
+                _lib.load().ppo_event_destroy(ev)

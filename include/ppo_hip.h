@@ -41,6 +41,14 @@ const char* ppo_last_error(void);
 void ppo_clear_error(void);
 int ppo_abi_version(void);
 int ppo_device_check(int device);
+/* Stream ordering for running independent chains (the actor and critic
+ * towers) on two streams: ppo_stream_wait makes work issued on `waiter`
+ * after the call start after everything issued on `signaller` before it
+ * (event recorded on signaller, waited on by waiter; inside a stream capture
+ * this forks / joins the graph).  Streams are hipStream_t handles. */
+int ppo_event_create(void** event);
+int ppo_event_destroy(void* event);
+int ppo_stream_wait(void* waiter, void* signaller, void* event);
 
 /* ------------------------------------------------------------------- GAE
  * Replaces boonta/algorithms/advantage_estimators.py:8-56

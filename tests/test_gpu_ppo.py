@@ -92,8 +92,11 @@ def test_parameters_and_logs_after_the_update(name):
     print(f"{name}: worst parameter rel-L2 {worst:.2e}")
 
 
-def test_graph_replay_equals_eager_and_is_deterministic():
-    case = CASES["c2-small"]
+@pytest.mark.parametrize("name", ["c2-small", "c3-small"])
+def test_graph_replay_equals_eager_and_is_deterministic(name):
+    """Shared trunk, and separate actor/critic towers (whose chains run on two
+    streams, forked and joined inside the captured graph)."""
+    case = CASES[name]
     results = []
     for use_graph in (False, True, True):
         r, plan, params, tr, roll = make_case(**case)
