@@ -5,9 +5,9 @@
 // registers hold staged data and no LDS store instructions run.  Contraction,
 // layouts, row gather, split-K and epilogue are those of gemm_bf16s_kernel.
 //
-// LDS holds NBUF stages in a ring; stage kt + NBUF - 1 is issued right after
-// the barrier that opens stage kt, so NBUF - 1 stages of loads are in flight
-// behind the MFMAs.  Layouts (bf16, no padding, 16-byte chunks XOR-swizzled
+// LDS holds NBUF stages in a ring (3 for 256 x 128 tiles, 4 for 128 x 128);
+// stage kt + NBUF - 1 is issued right after the barrier that opens stage kt,
+// so NBUF - 1 stages of loads are in flight behind the MFMAs.  Layouts (bf16, no padding, 16-byte chunks XOR-swizzled
 // by the row so that transpose reads, 16-byte operand reads and the copies
 // all spread over the LDS banks):
 //   k-contiguous operand [ROWS][BK]: chunk c of row r at c ^ kc_swizzle(r);
@@ -24,7 +24,6 @@
 
 namespace ppo_bf16s {
 
-constexpr int NBUF = 3;
 constexpr int KIDX_MAX = 2048;  // reduction rows per split when the k-outer A operand is gathered
 
 using ppo::kc_swizzle;
@@ -141,7 +140,21 @@ __device__ __forceinline__ bf16x8 doperand(const uint16_t* lds, int r0, int kk, 
   }
 }
 
-template <int BM, int BN, int WM, int WN, bool A_K, bool B_K>
+// Stage barrier that lets the copies of the `younger` (<= Y) stages issued
+// after the awaited one stay in flight.
+template <int PER_STAGE, int Y>
+__device__ __forceinline__ void ring_barrier(int younger) {
+  if constexpr (Y == 0) {
+    stage_barrier<0>();
+  } else {
+    if (younger >= Y)
+      stage_barrier<PER_STAGE * Y>();
+    else
+      ring_barrier<PER_STAGE, Y - 1>(younger);
+  }
+}
+
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF>
 __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_bf16d_kernel(Params p) {
   constexpr int NW = WM * WN;
   constexpr int BI = BM / WM / 32, BJ = BN / WN / 32;
@@ -244,11 +257,7 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_bf16d_kernel(Params p) {
   for (int kt = 0; kt < nk; ++kt) {
     // this wave's copies of stage kt are done once at most the younger
     // stages' copies are outstanding; the barrier then covers every wave's
-    if (kt + 1 < nk && NBUF > 2) {
-      stage_barrier<PER_STAGE * (NBUF - 2)>();
-    } else {
-      stage_barrier<0>();
-    }
+    ring_barrier<PER_STAGE, NBUF - 2>(min(NBUF - 2, nk - 1 - kt));
     if (kt + NBUF - 1 < nk) issue(kt + NBUF - 1);  // the slot stage kt - 1 used
     mma_stage(sA[kt % NBUF], sB[kt % NBUF]);
   }
@@ -256,10 +265,10 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_bf16d_kernel(Params p) {
   epilogue<BI, BJ>(p, acc, bsum, do_bsum, m0 + wm * (BI * 32), n0 + wn * (BJ * 32), split, lane);
 }
 
-template <int BM, int BN, int WM, int WN, bool A_K, bool B_K>
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF>
 int launch_d(hipStream_t st, const Params& p, int splits) {
   dim3 grid(ppo::ceil_div(p.N, BN), ppo::ceil_div(p.M, BM), splits);
-  hipLaunchKernelGGL((gemm_bf16d_kernel<BM, BN, WM, WN, A_K, B_K>), grid, dim3(WM * WN * 64), 0, st, p);
+  hipLaunchKernelGGL((gemm_bf16d_kernel<BM, BN, WM, WN, A_K, B_K, NBUF>), grid, dim3(WM * WN * 64), 0, st, p);
   return ppo::check_launch("ppo_gemm_bf16s");
 }
 

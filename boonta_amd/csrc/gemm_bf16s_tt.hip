@@ -3,14 +3,18 @@
 // operand's split holds more reduction rows than the kernel caches.
 #include "gemm_bf16d.h"
 
+#ifndef PPO_BF16D_NBUF128
+#define PPO_BF16D_NBUF128 4  // ring depth of the 128 x 128 tiles (4 x 32 KB of LDS)
+#endif
+
 namespace ppo_bf16s {
 
 template <bool A_K, bool B_K>
 int launch_tt(hipStream_t st, const Params& p, int splits, int tile) {
   const bool dma = A_K || p.rows == nullptr || p.k_per_split <= KIDX_MAX;
   if (!dma) return launch_tile<A_K, B_K, uint16_t, uint16_t>(st, p, splits, tile);
-  if (tile == 1) return launch_d<128, 128, 2, 2, A_K, B_K>(st, p, splits);
-  return launch_d<256, 128, 4, 2, A_K, B_K>(st, p, splits);
+  if (tile == 1) return launch_d<128, 128, 2, 2, A_K, B_K, PPO_BF16D_NBUF128>(st, p, splits);
+  return launch_d<256, 128, 4, 2, A_K, B_K, 3>(st, p, splits);
 }
 
 template <>

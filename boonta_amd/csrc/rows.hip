@@ -85,44 +85,73 @@ ln_act_bwd_kernel(const float* __restrict__ dy, int64_t lddy, const float* __res
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wpb = ROW_THREADS / 64;
-  float acc_g[VPL], acc_b[VPL];
+  float acc_g[VPL], acc_b[VPL], gam[VPL], bet[VPL];
 #pragma unroll
-  for (int e = 0; e < VPL; ++e) acc_g[e] = acc_b[e] = 0.f;
-  for (int64_t r = (int64_t)blockIdx.x * wpb + wave; r < rows; r += (int64_t)gridDim.x * wpb) {
-    const float mean = mean_in[r];
-    const float rstd = rstd_in[r];
-    float xh[VPL], g[VPL];
-    float sg = 0.f, sgx = 0.f;
+  for (int e = 0; e < VPL; ++e) {
+    acc_g[e] = acc_b[e] = 0.f;
+    const int f = lane + 64 * e;
+    gam[e] = f < F ? gamma[f] : 0.f;
+    bet[e] = f < F ? beta[f] : 0.f;
+  }
+  // A wave takes rows r0, r0 + stride, ... and loads RB of them before
+  // computing any, so their global-load latencies overlap.
+  constexpr int RB = VPL <= 8 ? 4 : 2;
+  const int64_t stride = (int64_t)gridDim.x * wpb;
+  for (int64_t r0 = (int64_t)blockIdx.x * wpb + wave; r0 < rows; r0 += RB * stride) {
+    float zv[RB][VPL], dv[RB][VPL], mu[RB], rs[RB];
 #pragma unroll
-    for (int e = 0; e < VPL; ++e) {
-      const int f = lane + 64 * e;
-      if (f < F) {
-        xh[e] = (z[r * ldz + f] - mean) * rstd;
-        float yl = xh[e] * gamma[f] + beta[f];
-        if (round) yl = ppo::bf16_round(yl);
-        const float a = (act == ACT_RELU || act == ACT_TANH) ? ppo::act_fwd(act, yl) : yl;
-        const float dyl = dy[r * lddy + f] * ppo::act_grad(act, a);
-        acc_g[e] += dyl * xh[e];
-        acc_b[e] += dyl;
-        g[e] = dyl * gamma[f];
-      } else {
-        xh[e] = 0.f;
-        g[e] = 0.f;
+    for (int j = 0; j < RB; ++j) {
+      const int64_t r = r0 + j * stride;
+      const int64_t rr = r < rows ? r : r0;
+      mu[j] = mean_in[rr];
+      rs[j] = rstd_in[rr];
+#pragma unroll
+      for (int e = 0; e < VPL; ++e) {
+        const int f = lane + 64 * e;
+        const int fc = f < F ? f : 0;
+        zv[j][e] = z[rr * ldz + fc];
+        dv[j][e] = dy[rr * lddy + fc];
       }
-      sg += g[e];
-      sgx += g[e] * xh[e];
     }
-    sg = ppo::wave_sum(sg) / (float)F;
-    sgx = ppo::wave_sum(sgx) / (float)F;
 #pragma unroll
-    for (int e = 0; e < VPL; ++e) {
-      const int f = lane + 64 * e;
-      if (f < F) {
-        const float d = rstd * (g[e] - sg - xh[e] * sgx);
-        if (out16)
-          static_cast<uint16_t*>(dz)[r * lddz + f] = (uint16_t)ppo::bf16_bits(d);
-        else
-          static_cast<float*>(dz)[r * lddz + f] = round ? ppo::bf16_round(d) : d;
+    for (int j = 0; j < RB; ++j) {
+      const int64_t r = r0 + j * stride;
+      if (r >= rows) break;
+      const float mean = mu[j];
+      const float rstd = rs[j];
+      float xh[VPL], g[VPL];
+      float sg = 0.f, sgx = 0.f;
+#pragma unroll
+      for (int e = 0; e < VPL; ++e) {
+        const int f = lane + 64 * e;
+        if (f < F) {
+          xh[e] = (zv[j][e] - mean) * rstd;
+          float yl = xh[e] * gam[e] + bet[e];
+          if (round) yl = ppo::bf16_round(yl);
+          const float a = (act == ACT_RELU || act == ACT_TANH) ? ppo::act_fwd(act, yl) : yl;
+          const float dyl = dv[j][e] * ppo::act_grad(act, a);
+          acc_g[e] += dyl * xh[e];
+          acc_b[e] += dyl;
+          g[e] = dyl * gam[e];
+        } else {
+          xh[e] = 0.f;
+          g[e] = 0.f;
+        }
+        sg += g[e];
+        sgx += g[e] * xh[e];
+      }
+      sg = ppo::wave_sum(sg) / (float)F;
+      sgx = ppo::wave_sum(sgx) / (float)F;
+#pragma unroll
+      for (int e = 0; e < VPL; ++e) {
+        const int f = lane + 64 * e;
+        if (f < F) {
+          const float d = rstd * (g[e] - sg - xh[e] * sgx);
+          if (out16)
+            static_cast<uint16_t*>(dz)[r * lddz + f] = (uint16_t)ppo::bf16_bits(d);
+          else
+            static_cast<float*>(dz)[r * lddz + f] = round ? ppo::bf16_round(d) : d;
+        }
       }
     }
   }
@@ -482,7 +511,8 @@ PPO_EXPORT int ppo_layernorm_act_fwd_bf16_out16(void* stream, const float* z, in
 
 // Partials: [blocks][2F]; blocks = ppo_layernorm_bwd_blocks(rows).
 PPO_EXPORT int ppo_layernorm_bwd_blocks(int rows) {
-  return std::max(1, std::min(ppo::ceil_div(rows, 4 * (ROW_THREADS / 64)), 512));
+  // two rows per wave until the grid holds 512 blocks (more rows per wave beyond)
+  return std::max(1, std::min(ppo::ceil_div(rows, 2 * (ROW_THREADS / 64)), 512));
 }
 
 static int layernorm_bwd(const char* name, void* stream, const float* dy, int64_t lddy, const float* z,
