@@ -36,12 +36,20 @@ constexpr int WAVES = 4;
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
 
+// Branches only on which flag arrays exist (uniform), never on loaded data,
+// so the flag loads stay in flight with the others.
 __device__ __forceinline__ bool done_at(const uint8_t* term, const uint8_t* trunc, const int32_t* rows,
                                         int b) {
   if (!term && !trunc) return false;
   const int64_t i = rows ? (int64_t)rows[b] : (int64_t)b;
-  return (term && term[i]) || (trunc && trunc[i]);
+  const uint32_t t1 = term ? term[i] : 0u;
+  const uint32_t t2 = trunc ? trunc[i] : 0u;
+  return (t1 | t2) != 0u;
 }
+
+// Scheduling barrier: the batch of independent loads above it is issued
+// before the first MFMA below it consumes one of them.
+__device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0); }
 
 struct FwdArgs {
   const float* xi; int64_t ldxi;
@@ -55,52 +63,84 @@ struct FwdArgs {
   int Bm, H;
 };
 
-// grid (ceil(Bm / 16), H / 16), block 256
+// grid (ceil(Bm / 16), H / 16), block 256.  NIT: 16-wide k steps per wave
+// (H / 64) when known at compile time (all of a wave's loads then issue
+// before its first MFMA); 0: a runtime loop.  The epilogue's operands are
+// loaded at entry, so their latency overlaps the contraction's.
+template <int NIT>
 __global__ void __launch_bounds__(256) gru_fwd_step_kernel(FwdArgs a) {
   __shared__ float red[WAVES][3][TILE][TILE + 1];
-  __shared__ uint8_t reset[TILE];
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int b0 = blockIdx.x * TILE;
   const int u0 = blockIdx.y * TILE;
   const int H = a.H;
-  if (tid < TILE) {
-    const int b = b0 + tid;
-    reset[tid] = (b < a.Bm) ? (uint8_t)done_at(a.term, a.trunc, a.flag_rows, b) : (uint8_t)1;
-  }
-  __syncthreads();
 
   // A operand: row i = lane % 16 of the tile, k = base + 4 * (lane / 16) + s.
   const int i = lane & 15;
   const int kq = lane >> 4;
   const int b = b0 + i;
-  const bool live = !reset[i];
-  const float* hrow = nullptr;
-  if (live) {
-    const int64_t r = a.hprev_rows ? (int64_t)a.hprev_rows[b] : (int64_t)b;
-    hrow = a.hprev + r * a.ldh;
-  }
+  const bool b_ok = b < a.Bm;
+  const int bc = b_ok ? b : b0;
+  const int64_t ra = a.hprev_rows ? (int64_t)a.hprev_rows[bc] : (int64_t)bc;
+  const float* hrow = a.hprev + ra * a.ldh;
   const int kspan = H / WAVES;
   const int kbeg = wave * kspan;
-  floatx4 acc[3];
-#pragma unroll
-  for (int g = 0; g < 3; ++g) acc[g] = floatx4{0.f, 0.f, 0.f, 0.f};
   const float* wcol = a.wh + u0 + i;  // B operand: column u0 + i of each gate block
-  for (int base = kbeg; base < kbeg + kspan; base += 16) {
+  auto load = [&](int base, floatx4& av, float (&bv)[3][4]) {
     const int k = base + 4 * kq;
-    floatx4 av = live ? *reinterpret_cast<const floatx4*>(hrow + k) : floatx4{0.f, 0.f, 0.f, 0.f};
-    float bv[3][4];
+    av = *reinterpret_cast<const floatx4*>(hrow + k);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const float* wr = wcol + (int64_t)(k + s) * a.ldwh;
 #pragma unroll
       for (int g = 0; g < 3; ++g) bv[g][s] = wr[g * H];
     }
+  };
+  floatx4 av[NIT > 0 ? NIT : 1];
+  float bv[NIT > 0 ? NIT : 1][3][4];
+  if (NIT > 0) {
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) load(kbeg + 16 * it, av[it], bv[it]);
+  }
+  const bool live = b_ok && !done_at(a.term, a.trunc, a.flag_rows, b);
+
+  // epilogue operands of this thread's (sequence, unit)
+  const int ti = tid >> 4;   // sequence within the tile
+  const int tj = tid & 15;   // unit within the tile
+  const int bb = b0 + ti;
+  const int u = u0 + tj;
+  const bool bb_ok = bb < a.Bm;
+  const int bbc = bb_ok ? bb : b0;
+  const float* x = a.xi + (int64_t)bbc * a.ldxi;
+  const float xn = x[u], xr = x[H + u], xz = x[2 * H + u];
+  const float bhn = a.bhn[u];
+  const bool reset_e = bb_ok ? done_at(a.term, a.trunc, a.flag_rows, bb) : true;
+  const int64_t re = a.hprev_rows ? (int64_t)a.hprev_rows[bbc] : (int64_t)bbc;
+  const float hp_raw = a.hprev[re * a.ldh + u];
+  issue_fence();
+
+  floatx4 acc[3];
+#pragma unroll
+  for (int g = 0; g < 3; ++g) acc[g] = floatx4{0.f, 0.f, 0.f, 0.f};
+  auto mma = [&](floatx4 avv, const float (&bvv)[3][4]) {
+    if (!live) avv = floatx4{0.f, 0.f, 0.f, 0.f};  // a reset sequence starts from h = 0
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
 #pragma unroll
-      for (int g = 0; g < 3; ++g) acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bv[g][s], acc[g], 0, 0, 0);
+      for (int g = 0; g < 3; ++g) acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(avv[s], bvv[g][s], acc[g], 0, 0, 0);
+    }
+  };
+  if (NIT > 0) {
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) mma(av[it], bv[it]);
+  } else {
+    for (int base = kbeg; base < kbeg + kspan; base += 16) {
+      floatx4 a1;
+      float b1[3][4];
+      load(base, a1, b1);
+      mma(a1, b1);
     }
   }
   // D layout: lane holds rows 4 * (lane / 16) + v, column lane % 16.
@@ -110,11 +150,7 @@ __global__ void __launch_bounds__(256) gru_fwd_step_kernel(FwdArgs a) {
     for (int v = 0; v < 4; ++v) red[wave][g][4 * kq + v][i] = acc[g][v];
   __syncthreads();
 
-  const int ti = tid >> 4;   // sequence within the tile
-  const int tj = tid & 15;   // unit within the tile
-  const int bb = b0 + ti;
-  if (bb >= a.Bm) return;
-  const int u = u0 + tj;
+  if (!bb_ok) return;
   float ar = 0.f, az = 0.f, an = 0.f;
 #pragma unroll
   for (int w = 0; w < WAVES; ++w) {
@@ -122,16 +158,11 @@ __global__ void __launch_bounds__(256) gru_fwd_step_kernel(FwdArgs a) {
     az += red[w][1][ti][tj];
     an += red[w][2][ti][tj];
   }
-  float hp = 0.f;
-  if (!reset[ti]) {
-    const int64_t r = a.hprev_rows ? (int64_t)a.hprev_rows[bb] : (int64_t)bb;
-    hp = a.hprev[r * a.ldh + u];
-  }
-  const float* x = a.xi + (int64_t)bb * a.ldxi;
-  const float r = sigmoidf_(x[H + u] + ar);
-  const float z = sigmoidf_(x[2 * H + u] + az);
-  const float hn = an + a.bhn[u];
-  const float n = tanhf(x[u] + r * hn);
+  const float hp = reset_e ? 0.f : hp_raw;
+  const float r = sigmoidf_(xr + ar);
+  const float z = sigmoidf_(xz + az);
+  const float hn = an + bhn;
+  const float n = tanhf(xn + r * hn);
   const float h = (1.f - z) * n + z * hp;
   a.h_out[(int64_t)bb * a.ldo + u] = h;
   if (a.hp_out) a.hp_out[(int64_t)bb * a.ldhp + u] = hp;
@@ -160,7 +191,10 @@ struct BwdArgs {
   int Bm, H;
 };
 
-// grid (ceil(Bm / 16), H / 16), block 256
+// grid (ceil(Bm / 16), H / 16), block 256.  NIT: 16-wide k steps per wave
+// (3H / 64) when known at compile time; 0: a runtime loop.  The epilogue's
+// operands are loaded at entry.
+template <int NIT>
 __global__ void __launch_bounds__(256) gru_bwd_step_kernel(BwdArgs a) {
   __shared__ float red[WAVES][TILE][TILE + 1];
   const int tid = threadIdx.x;
@@ -173,41 +207,65 @@ __global__ void __launch_bounds__(256) gru_bwd_step_kernel(BwdArgs a) {
   const int tj = tid & 15;
   const int bb = b0 + ti;
   const int u = u0 + tj;
+  const bool bb_ok = bb < a.Bm;
+  const int bbc = bb_ok ? bb : b0;
+
+  // contraction operands: dhp[b][u] = sum_c dgate_t[b][H + c] * Wh[u][c], c < 3H
+  const int i = lane & 15;
+  const int kq = lane >> 4;
+  const bool live = b0 + i < a.Bm;
+  const float* arow = a.dg ? a.dg + (int64_t)(live ? b0 + i : b0) * a.lddg : nullptr;
+  const float* brow = a.wh ? a.wh + (int64_t)(u0 + i) * a.ldwh : nullptr;
+  const int kspan = 3 * H / WAVES;
+  const int kbeg = wave * kspan;
+  floatx4 av[NIT > 0 ? NIT : 1], bv[NIT > 0 ? NIT : 1];
+  if (NIT > 0 && a.dg) {
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int k = kbeg + 16 * it + 4 * kq;
+      av[it] = *reinterpret_cast<const floatx4*>(arow + k);
+      bv[it] = *reinterpret_cast<const floatx4*>(brow + k);
+    }
+  }
+  // epilogue operands
+  float dh = a.dout[(int64_t)bbc * a.lddo + u];
+  const float* gs = a.gates_s + (int64_t)bbc * a.ldg;
+  const float n = gs[u], r = gs[H + u], z = gs[2 * H + u], hn = gs[3 * H + u];
+  const float hp = a.hp_s[(int64_t)bbc * a.ldhp + u];
+  float direct = 0.f;
+  bool reset_t = false;
+  if (a.dg) {
+    direct = a.dh_t[(int64_t)bbc * a.lddht + u] * a.z_t[(int64_t)bbc * a.ldz + u];
+    reset_t = done_at(a.term, a.trunc, a.flag_rows, bbc);
+  }
+  issue_fence();
 
   if (a.dg) {
-    // dhp[b][u] = sum_c dgate_t[b][H + c] * Wh[u][c], c < 3H
-    const int i = lane & 15;
-    const int kq = lane >> 4;
-    const int b = b0 + i;
-    const bool live = b < a.Bm;
-    const float* arow = a.dg + (int64_t)(live ? b : 0) * a.lddg;
-    const float* brow = a.wh + (int64_t)(u0 + i) * a.ldwh;
-    const int K = 3 * H;
-    const int kspan = K / WAVES;
-    const int kbeg = wave * kspan;
     floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int base = kbeg; base < kbeg + kspan; base += 16) {
-      const int k = base + 4 * kq;
-      const floatx4 av = live ? *reinterpret_cast<const floatx4*>(arow + k) : floatx4{0.f, 0.f, 0.f, 0.f};
-      const floatx4 bv = *reinterpret_cast<const floatx4*>(brow + k);
+    auto mma = [&](floatx4 x, floatx4 y) {
+      if (!live) x = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bv[s], acc, 0, 0, 0);
+      for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[s], y[s], acc, 0, 0, 0);
+    };
+    if (NIT > 0) {
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) mma(av[it], bv[it]);
+    } else {
+      for (int base = kbeg; base < kbeg + kspan; base += 16) {
+        const int k = base + 4 * kq;
+        mma(*reinterpret_cast<const floatx4*>(arow + k), *reinterpret_cast<const floatx4*>(brow + k));
+      }
     }
 #pragma unroll
     for (int v = 0; v < 4; ++v) red[wave][4 * kq + v][i] = acc[v];
     __syncthreads();
   }
-  if (bb >= a.Bm) return;
+  if (!bb_ok) return;
 
-  float dh = a.dout[(int64_t)bb * a.lddo + u];
   if (a.dg) {
-    float dhp = red[0][ti][tj] + red[1][ti][tj] + red[2][ti][tj] + red[3][ti][tj];
-    dhp += a.dh_t[(int64_t)bb * a.lddht + u] * a.z_t[(int64_t)bb * a.ldz + u];
-    if (!done_at(a.term, a.trunc, a.flag_rows, bb)) dh += dhp;
+    const float dhp = red[0][ti][tj] + red[1][ti][tj] + red[2][ti][tj] + red[3][ti][tj] + direct;
+    if (!reset_t) dh += dhp;
   }
-  const float* g = a.gates_s + (int64_t)bb * a.ldg;
-  const float n = g[u], r = g[H + u], z = g[2 * H + u], hn = g[3 * H + u];
-  const float hp = a.hp_s[(int64_t)bb * a.ldhp + u];
   const float dn = dh * (1.f - z);
   const float dz = dh * (hp - n);
   const float dan = dn * (1.f - n * n);
@@ -259,7 +317,14 @@ PPO_EXPORT int ppo_gru_fwd_step_f32(void* stream, const float* xi, int64_t ldxi,
   FwdArgs a{xi, ldxi, hprev, ldh, hprev_rows, terminated, truncated, flag_rows, wh, ldwh, bhn,
             h_out, ldo, hp_out, ldhp, gates, ldg, Bm, H};
   dim3 grid(ppo::ceil_div(Bm, TILE), H / TILE);
-  hipLaunchKernelGGL(gru_fwd_step_kernel, grid, dim3(256), 0, ppo::as_stream(stream), a);
+  hipStream_t st = ppo::as_stream(stream);
+  switch (H / 64) {  // 16-wide k steps per wave
+    case 1: hipLaunchKernelGGL(gru_fwd_step_kernel<1>, grid, dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL(gru_fwd_step_kernel<2>, grid, dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL(gru_fwd_step_kernel<4>, grid, dim3(256), 0, st, a); break;
+    case 8: hipLaunchKernelGGL(gru_fwd_step_kernel<8>, grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL(gru_fwd_step_kernel<0>, grid, dim3(256), 0, st, a); break;
+  }
   return ppo::check_launch("ppo_gru_fwd_step_f32");
 }
 
@@ -285,7 +350,13 @@ PPO_EXPORT int ppo_gru_bwd_step_f32(void* stream, const float* dg, int64_t lddg,
   BwdArgs a{dg, lddg, wh, ldwh, dh_t, lddht, z_t, ldz, terminated, truncated, flag_rows,
             dout, lddo, gates_s, ldg, hp_s, ldhp, dh_s, lddhs, dgate_s, lddgs, Bm, H};
   dim3 grid(ppo::ceil_div(Bm, TILE), H / TILE);
-  hipLaunchKernelGGL(gru_bwd_step_kernel, grid, dim3(256), 0, ppo::as_stream(stream), a);
+  hipStream_t st = ppo::as_stream(stream);
+  switch (3 * H / 64) {  // 16-wide k steps per wave
+    case 3: hipLaunchKernelGGL(gru_bwd_step_kernel<3>, grid, dim3(256), 0, st, a); break;
+    case 6: hipLaunchKernelGGL(gru_bwd_step_kernel<6>, grid, dim3(256), 0, st, a); break;
+    case 12: hipLaunchKernelGGL(gru_bwd_step_kernel<12>, grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL(gru_bwd_step_kernel<0>, grid, dim3(256), 0, st, a); break;
+  }
   return ppo::check_launch("ppo_gru_bwd_step_f32");
 }
 
