@@ -249,7 +249,8 @@ int launch_layout(hipStream_t st, const GemmParams& p, int splits, bool va, bool
     case 4: return launch_tile<128, 128, 32, A_K, B_K>(st, p, splits, va, vb);
     case 5: return launch_tile<128, 64, 32, A_K, B_K>(st, p, splits, va, vb);
     case 6: return launch_tile<64, 128, 32, A_K, B_K>(st, p, splits, va, vb);
-    default: return launch_tile<64, 64, 32, A_K, B_K>(st, p, splits, va, vb);
+    case 7: return launch_tile<64, 64, 32, A_K, B_K>(st, p, splits, va, vb);
+    default: return launch_tile<128, 128, 16, A_K, B_K>(st, p, splits, va, vb);  // 8, 9 without copies
   }
 }
 
@@ -264,13 +265,13 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 //   2: multiply by act'(aux).  bias_grad (layout a=1, b=0 only): [splits][N] sums of B.
 //   tile: -1 picks a tile; 0: 128x128, 1: 128x64, 2: 64x128, 3: 64x64 (copy-fed, 32 reduction
 //   elements per stage, when the operands allow; else register-staged with 16); 4-7 the same
-//   tiles register-staged with 32 per stage.
+//   tiles register-staged with 32 per stage; 8: 128x256 and 9: 256x128 on 8 waves (copy-fed).
 PPO_EXPORT int ppo_gemm_f32(void* stream, int a_layout, int b_layout, const float* A, int64_t lda,
                             const int32_t* rows, const float* B, int64_t ldb, float* C, int64_t ldc, int M,
                             int N, int K, int splits, int64_t c_split_stride, int epi, const float* bias,
                             int act, float* pre, const float* aux, int64_t ldaux, float* bias_grad, int tile) {
   if (M < 0 || N < 0 || K < 0 || splits < 1 || a_layout < 0 || a_layout > 1 || b_layout < 0 || b_layout > 1 ||
-      epi < 0 || epi > 2 || act < 0 || act > 3 || tile > 7)
+      epi < 0 || epi > 2 || act < 0 || act > 3 || tile > 9)
     return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32: bad argument (M=%d N=%d K=%d splits=%d)", M, N, K, splits);
   if (M == 0 || N == 0) return PPO_OK;
   if (!A || !B || !C) return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32: null operand");
@@ -290,16 +291,18 @@ PPO_EXPORT int ppo_gemm_f32(void* stream, int a_layout, int b_layout, const floa
   const int b_contig = b_layout == 1 ? K : N;
   const bool va = (lda % 4 == 0) && (a_contig % 4 == 0) && aligned16(A);
   const bool vb = (ldb % 4 == 0) && (b_contig % 4 == 0) && aligned16(B);
-  // 64 x 64 tiles measure fastest on every learner shape on MI355X (more
-  // resident workgroups per CU hide the global-load latency better than the
-  // larger tiles' register reuse gains).
+  // Default 64 x 64: three resident workgroups per CU hide latency best over
+  // the learner's shapes as a whole inside the update graph (the 8-wave tiles
+  // win some isolated launches by 5-10% and lose others by up to 35%).
   if (tile < 0) tile = 3;
   hipStream_t st = ppo::as_stream(stream);
-  // Tiles 0-3 run on the copy-fed pipeline (gemm_f32d.hip) whenever every
-  // operand row is 16-byte vectorisable and a gathered k-outer A fits its
-  // index cache; tiles 4-7 (and the rest) on the register-staged one here.
+  // Tiles 0-3 and 8-9 run on the copy-fed pipeline (gemm_f32d.hip) whenever
+  // every operand row is 16-byte vectorisable and a gathered k-outer A fits
+  // its index cache; tiles 4-7 (and the rest) on the register-staged one here
+  // (8 and 9 then fall back to 128 x 128).
   const int kps_d = ((ppo::ceil_div(K > 0 ? K : 1, splits) + F32D_BK - 1) / F32D_BK) * F32D_BK;
-  if (tile <= 3 && va && vb && !(a_layout == 1 && rows && kps_d > F32D_KIDX_MAX)) {
+  const bool dma_tile = tile <= 3 || tile >= 8;
+  if (dma_tile && va && vb && !(a_layout == 1 && rows && kps_d > F32D_KIDX_MAX)) {
     p.k_per_split = kps_d;
     return launch_dma(st, p, splits, tile, a_layout, b_layout);
   }

@@ -5,10 +5,13 @@
 // no registers hold staged data and no LDS store instructions run, so three
 // stages of copies stay in flight behind the MFMAs.
 //
-// Tiles: 4 wave64s in 2 x 2, each (BM/2) x (BN/2) of 32 x 32 blocks of
-// v_mfma_f32_32x32x2_f32; 32 reduction elements per stage.  Inside each group
-// of 8 reduction elements, lane half h consumes k = 8g + 4h + s at MFMA step
-// s (both operands use the same order, so the sum is unchanged).
+// Tiles: 4 wave64s in 2 x 2 (64 / 128 x 64 / 128 tiles) or 8 in 2 x 4 / 4 x 2
+// (128 x 256, 256 x 128), each wave (BM/WM) x (BN/WN) of 32 x 32 blocks of
+// v_mfma_f32_32x32x2_f32; 32 reduction elements per stage.  The 8-wave tiles
+// read 2-4x fewer operand bytes per FLOP from L2 (a 64 x 64 tile at full fp32
+// MFMA rate needs more L2 bandwidth than the chip has).  Inside each group of
+// 8 reduction elements, lane half h consumes k = 8g + 4h + s at MFMA step s
+// (both operands use the same order, so the sum is unchanged).
 // LDS layouts (fp32, 16-byte chunks XOR-swizzled on the copy side):
 //   k-contiguous [ROWS][32]: chunk c of row r at c ^ kc_swizzle(r); an operand
 //     read (4 consecutive k of one row) is one 16-byte read;
@@ -24,18 +27,18 @@ namespace {
 
 constexpr int BK = F32D_BK;
 constexpr int NBUF = 3;
-constexpr int NW = 4;
 
 __device__ __forceinline__ int ko_swizzle32(int k) { return ((k >> 2) & 1) << 3; }
 
 // One operand's copies: ROWS x BK fp32 per stage in 1 KB copies (64 lanes x
-// 16 B), PERW per wave; copy i of a wave fills LDS units 64 (wave PERW + i) + l.
-template <int ROWS, bool KC>
+// 16 B), PERW per wave (NW waves); copy i of a wave fills LDS units
+// 64 (wave PERW + i) + l.
+template <int ROWS, bool KC, int NW>
 struct Operand {
   static constexpr int ELEMS = ROWS * BK;
   static constexpr int COPIES = ELEMS / 256;
   static constexpr int PERW = COPIES / NW;
-  static_assert(PERW >= 1 && COPIES % NW == 0, "tile too small for four waves");
+  static_assert(PERW >= 1 && COPIES % NW == 0, "tile too small for the wave count");
   static_assert(KC || ROWS >= 64, "k-outer swizzle needs 16 chunks per k row");
   const float* src[PERW];  // KC: the (gathered) row; k-outer: the operand base
   int col[PERW];           // KC: the unit's k offset in the stage; k-outer: its first element (clamped)
@@ -130,19 +133,21 @@ __device__ __forceinline__ floatx4 operand(const float* lds, int rbase, int g, i
   }
 }
 
-template <int BM, int BN, bool A_K, bool B_K>
-__global__ void __launch_bounds__(NW * 64) gemm_f32d_kernel(GemmParams p) {
-  constexpr int MB = BM / 64, NB = BN / 64;
-  using OpA = Operand<BM, A_K>;
-  using OpB = Operand<BN, B_K>;
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K>
+__global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_kernel(GemmParams p) {
+  constexpr int NW = WM * WN;
+  constexpr int MB = BM / WM / 32, NB = BN / WN / 32;  // 32 x 32 blocks per wave
+  static_assert(MB * WM * 32 == BM && NB * WN * 32 == BN, "tile must split into 32 x 32 blocks");
+  using OpA = Operand<BM, A_K, NW>;
+  using OpB = Operand<BN, B_K, NW>;
   __shared__ __attribute__((aligned(1024))) float sA[NBUF][OpA::ELEMS];
   __shared__ __attribute__((aligned(1024))) float sB[NBUF][OpB::ELEMS];
   __shared__ int32_t sIdx[A_K ? 1 : F32D_KIDX_MAX];  // gather indices of the split (k-outer A)
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave & 1;
-  const int wn = wave >> 1;
+  const int wm = wave % WM;
+  const int wn = wave / WM;
   const ppo::TileCoord tc = ppo::xcd_tile();
   const int m0 = tc.m * BM;
   const int n0 = tc.n * BN;
@@ -205,9 +210,9 @@ __global__ void __launch_bounds__(NW * 64) gemm_f32d_kernel(GemmParams p) {
     floatx4 a4[2][MB], b4[2][NB];
     auto read_ops = [&](int set, int g) {
 #pragma unroll
-      for (int bi = 0; bi < MB; ++bi) a4[set][bi] = operand<BM, A_K>(la, wm * (BM / 2) + bi * 32, g, lane);
+      for (int bi = 0; bi < MB; ++bi) a4[set][bi] = operand<BM, A_K>(la, wm * (BM / WM) + bi * 32, g, lane);
 #pragma unroll
-      for (int bj = 0; bj < NB; ++bj) b4[set][bj] = operand<BN, B_K>(lb, wn * (BN / 2) + bj * 32, g, lane);
+      for (int bj = 0; bj < NB; ++bj) b4[set][bj] = operand<BN, B_K>(lb, wn * (BN / WN) + bj * 32, g, lane);
     };
     read_ops(0, 0);
 #pragma unroll
@@ -229,23 +234,25 @@ __global__ void __launch_bounds__(NW * 64) gemm_f32d_kernel(GemmParams p) {
     }
   }
 
-  epilogue_f32<MB, NB>(p, acc, bsum, do_bsum, m0 + wm * (BM / 2), n0 + wn * (BN / 2), split, lane);
+  epilogue_f32<MB, NB>(p, acc, bsum, do_bsum, m0 + wm * (BM / WM), n0 + wn * (BN / WN), split, lane);
 }
 
-template <int BM, int BN, bool A_K, bool B_K>
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K>
 int launch(hipStream_t st, const GemmParams& p, int splits) {
   dim3 grid(ppo::ceil_div(p.N, BN), ppo::ceil_div(p.M, BM), splits);
-  hipLaunchKernelGGL((gemm_f32d_kernel<BM, BN, A_K, B_K>), grid, dim3(NW * 64), 0, st, p);
+  hipLaunchKernelGGL((gemm_f32d_kernel<BM, BN, WM, WN, A_K, B_K>), grid, dim3(WM * WN * 64), 0, st, p);
   return ppo::check_launch("ppo_gemm_f32");
 }
 
 template <bool A_K, bool B_K>
 int launch_tile(hipStream_t st, const GemmParams& p, int splits, int tile) {
   switch (tile) {
-    case 0: return launch<128, 128, A_K, B_K>(st, p, splits);
-    case 1: return launch<128, 64, A_K, B_K>(st, p, splits);
-    case 2: return launch<64, 128, A_K, B_K>(st, p, splits);
-    default: return launch<64, 64, A_K, B_K>(st, p, splits);
+    case 0: return launch<128, 128, 2, 2, A_K, B_K>(st, p, splits);
+    case 1: return launch<128, 64, 2, 2, A_K, B_K>(st, p, splits);
+    case 2: return launch<64, 128, 2, 2, A_K, B_K>(st, p, splits);
+    case 8: return launch<128, 256, 2, 4, A_K, B_K>(st, p, splits);
+    case 9: return launch<256, 128, 4, 2, A_K, B_K>(st, p, splits);
+    default: return launch<64, 64, 2, 2, A_K, B_K>(st, p, splits);
   }
 }
 

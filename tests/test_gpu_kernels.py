@@ -175,7 +175,7 @@ def test_gemm_layouts_match_float64(a_layout, b_layout, M, N, K):
     gemm_case(a_layout, b_layout, M, N, K, seed=M + N + K)
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 8, 9])
 def test_gemm_every_tile(tile):
     gemm_case(0, 0, 200, 190, 48, tile=tile, seed=tile)
     gemm_case(1, 0, 130, 70, 500, tile=tile, splits=3, bias_grad=True, seed=tile + 10)
