@@ -26,6 +26,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace {
 
@@ -73,126 +74,211 @@ constexpr float LOG_2PI = 1.8378770664093453f;
 constexpr int TR = 64;   // rows per workgroup
 constexpr int LDO = 20;  // LDS row pitch: 16 head outputs + the separate critic's value, 16-byte rows
 
-// The loss and output cotangents of one row (phase B).  out[0..15]: head
-// outputs with bias; v: the value.  Writes dout[0..15], dvalue and adds to
-// the statistics / Gaussian-scale accumulators.
-__device__ __forceinline__ void row_loss(const HeadLossParams& p, bool sep, int64_t s, const float (&out)[16],
-                                         float v, float (&dout)[16], float& dvalue, double (&st)[NSTAT],
-                                         float (&dsc)[16]) {
+// Phase B runs element-parallel: thread t owns output column j = t % 16 of
+// local rows t / 16 + 16 g (g < ROWS / 16).  The 16 lanes of a row reduce
+// over the head outputs with xor butterflies (every lane ends with the same
+// bits: floating-point addition and max are commutative), compute the row's
+// scalar loss terms redundantly, and write the row's output cotangents to
+// LDS.  Block partials are column sums over the rows in LDS, in row order.
+
+// Rollout inputs seen by one (row, column) thread of phase B; loaded at the
+// start of the kernel so their latency hides behind phase A.
+struct LaneIn {
+  float olp, adv, ret, vold;
+  float actf;  // Gaussian action component j
+  int a;       // categorical action
+  bool live;   // the row exists
+};
+
+__device__ __forceinline__ LaneIn load_lane(const HeadLossParams& p, int r, int j) {
+  LaneIn in;
+  in.live = r < p.rows;
+  const int rc = in.live ? r : p.rows - 1;
+  const int64_t s = p.idx ? (int64_t)p.idx[rc] : (int64_t)rc;
+  in.olp = p.old_logp[s];
+  in.adv = p.adv[s];
+  in.ret = p.ret[s];
+  in.vold = p.old_value[s];
+  in.a = 0;
+  in.actf = 0.f;
+  if (p.dist == DIST_CATEGORICAL) in.a = p.action_i[s];
+  else in.actf = p.action_f[s * p.A + min(j, p.A - 1)];
+  return in;
+}
+
+// Per-thread constants of phase B (column j): the head bias and, for a
+// state-independent Gaussian scale, sigma_j, log sigma_j and the softplus
+// derivative at the raw scale.
+struct ColConst {
+  float bias, bias_c;
+  float sig, lsig, dsp;
+};
+
+__device__ __forceinline__ ColConst load_cols(const HeadLossParams& p, bool sep, int j) {
+  ColConst c;
+  const float b = p.ba[min(j, p.na - 1)];
+  c.bias = j < p.na ? b : 0.f;
+  c.bias_c = sep ? p.bc[0] : 0.f;
+  c.sig = c.lsig = c.dsp = 0.f;
+  if (p.scale_param) {
+    const float raw = p.scale_param[min(j, p.A - 1)];
+    c.sig = p.temperature * (softplusf(raw) + 1e-3f);
+    c.lsig = __logf(c.sig);
+    c.dsp = p.temperature / (1.f + __expf(-raw));
+  }
+  return c;
+}
+
+__device__ __forceinline__ float row16_sum(float v) {
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 16);
+  return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 16));
+  return v;
+}
+
+// Phase B over ROWS rows whose head outputs (no bias) are the sum of NPART
+// LDS partials src[w][row][0..16] (column 16: the separate critic's value).
+// Writes dout[row][0..16] (rows past the minibatch: zeros), the statistics
+// and Gaussian-scale terms of each row to st / dsc, then (after a barrier)
+// the block partials.  Ends with a barrier, so dout is ready for phase C.
+template <int ROWS, int NPART, bool SEP>
+__device__ __forceinline__ void phase_b(const HeadLossParams& p, int64_t blk, const float (*src)[ROWS][LDO],
+                                        float (*dout)[LDO], double (*st)[NSTAT], float (*dsc)[16],
+                                        const LaneIn (&in)[ROWS / 16], const ColConst& cc) {
+  const int t = threadIdx.x;
+  const int j = t & 15;
   const int A = p.A;
-  const float olp = p.old_logp[s], Av = p.adv[s], Rt = p.ret[s], vold = p.old_value[s];
-  const float eps = p.clip_eps;
   const float inv_t = 1.f / p.temperature;
-  float lp = 0.f, ent = 0.f, lse = 0.f;
-  int a = 0;
+  const float eps = p.clip_eps;
+  const bool jin = j < A;
+  const bool gauss = p.dist != DIST_CATEGORICAL;
+  const bool spread = p.scale_param != nullptr;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) dout[j] = 0.f;
-  if (p.dist == DIST_CATEGORICAL) {
-    float mx = -INFINITY;
+  for (int g = 0; g < ROWS / 16; ++g) {
+    const int rr = (t >> 4) + 16 * g;
+    const LaneIn& x = in[g];
+    float o = src[0][rr][j];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) if (j < A) mx = fmaxf(mx, out[j] * inv_t);
-    float se = 0.f;
+    for (int w = 1; w < NPART; ++w) o += src[w][rr][j];
+    o += cc.bias;
+    float v;
+    if (SEP) {
+      float c = src[0][rr][16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) if (j < A) se += __expf(out[j] * inv_t - mx);
-    lse = mx + __logf(se);
-    a = p.action_i[s];
-    float za = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) za = (j == a) ? out[j] * inv_t : za;
-    lp = (a >= 0 && a < A) ? za - lse : -INFINITY;
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-      if (j < A) {
-        const float lq = out[j] * inv_t - lse;
-        ent -= __expf(lq) * lq;
+      for (int w = 1; w < NPART; ++w) c += src[w][rr][16];
+      v = c + cc.bias_c;
+    } else {
+      v = __shfl(o, p.na - 1, 16);
+    }
+    float lp, ent, val, draw = 0.f, pmin_r, clip_r;
+    if (!gauss) {
+      const float z = o * inv_t;
+      const float mx = row16_max(jin ? z : -INFINITY);
+      const float se = row16_sum(jin ? __expf(z - mx) : 0.f);
+      const float lse = mx + __logf(se);
+      const float za = row16_sum(j == x.a ? z : 0.f);
+      lp = (x.a >= 0 && x.a < A) ? za - lse : -INFINITY;
+      const float lq = z - lse;
+      const float q = __expf(lq);
+      ent = -row16_sum(jin ? q * lq : 0.f);
+      // per-row terms below need lp and ent; the cotangent follows them
+      val = 0.f;
+      const float ratio = __expf(lp - x.olp);
+      float cr, dcr;
+      clip_grad(ratio, 1.f - eps, 1.f + eps, cr, dcr);
+      const float pg1 = ratio * x.adv, pg2 = cr * x.adv;
+      const float pmin = fminf(pg1, pg2);
+      const float g_lp =
+          -(tie_first(pg1, pg2, pmin) * x.adv + tie_first(pg2, pg1, pmin) * x.adv * dcr) * p.inv_n * ratio;
+      const float g_ent = -p.ent_coef * p.inv_n;
+      val = jin ? (g_lp * ((j == x.a ? 1.f : 0.f) - q) - g_ent * q * (lq + ent)) * inv_t : 0.f;
+      pmin_r = pmin;
+      clip_r = (fabsf(ratio - 1.f) > eps) ? 1.f : 0.f;
+    } else {
+      const float raw = spread ? 0.f : __shfl(o, min(A + j, 15), 16);
+      const float sig = spread ? cc.sig : p.temperature * (softplusf(raw) + 1e-3f);
+      const float ls = spread ? cc.lsig : __logf(sig);
+      const float d = x.actf - o;
+      const float zz = d / sig;
+      lp = row16_sum(jin ? -0.5f * zz * zz - ls - 0.5f * LOG_2PI : 0.f);
+      ent = row16_sum(jin ? 0.5f + 0.5f * LOG_2PI + ls : 0.f);
+      const float ratio = __expf(lp - x.olp);
+      float cr, dcr;
+      clip_grad(ratio, 1.f - eps, 1.f + eps, cr, dcr);
+      const float pg1 = ratio * x.adv, pg2 = cr * x.adv;
+      const float pmin = fminf(pg1, pg2);
+      const float g_lp =
+          -(tie_first(pg1, pg2, pmin) * x.adv + tie_first(pg2, pg1, pmin) * x.adv * dcr) * p.inv_n * ratio;
+      const float g_ent = -p.ent_coef * p.inv_n;
+      val = jin ? g_lp * d / (sig * sig) : 0.f;
+      const float dsig = g_lp * (d * d / (sig * sig * sig) - 1.f / sig) + g_ent / sig;
+      draw = dsig * (spread ? cc.dsp : p.temperature / (1.f + __expf(-raw)));
+      if (!spread) {
+        const float dr = __shfl(draw, max(j - A, 0), 16);
+        if (j >= A && j < 2 * A) val = dr;
       }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-      if (j < A) {
-        float raw = 0.f;
-        if (p.scale_param) {
-          raw = p.scale_param[j];
-        } else {
-#pragma unroll
-          for (int q = 0; q < 16; ++q) raw = (q == A + j) ? out[q] : raw;
-        }
-        const float sig = p.temperature * (softplusf(raw) + 1e-3f);
-        const float zz = (p.action_f[s * A + j] - out[j]) / sig;
-        const float ls = __logf(sig);
-        lp += -0.5f * zz * zz - ls - 0.5f * LOG_2PI;
-        ent += 0.5f + 0.5f * LOG_2PI + ls;
-      }
+      pmin_r = pmin;
+      clip_r = (fabsf(ratio - 1.f) > eps) ? 1.f : 0.f;
+    }
+    // value loss (the same in every lane of the row)
+    const float vl1 = 0.5f * (v - x.ret) * (v - x.ret);
+    float crow, gv;
+    if (p.clip_value_loss) {
+      float dv, ddv;
+      clip_grad(v - x.vold, -eps, eps, dv, ddv);
+      const float vc = x.vold + dv;
+      const float vl2 = 0.5f * (vc - x.ret) * (vc - x.ret);
+      crow = fmaxf(vl1, vl2);
+      gv = tie_first(vl1, vl2, crow) * (v - x.ret) + tie_first(vl2, vl1, crow) * (vc - x.ret) * ddv;
+    } else {
+      crow = vl1;
+      gv = v - x.ret;
+    }
+    const float dvalue = p.vf_coef * gv * p.inv_n;
+    if (!SEP && j == p.na - 1) val = dvalue;
+    dout[rr][j] = x.live ? val : 0.f;
+    if (spread) dsc[rr][j] = (x.live && jin) ? draw : 0.f;
+    if (j == 0) {
+      dout[rr][16] = x.live ? dvalue : 0.f;
+      const double res = (double)x.ret - (double)v;
+      const bool l = x.live;
+      st[rr][ST_ACTOR] = l ? (double)(-pmin_r) : 0.0;
+      st[rr][ST_ENTROPY] = l ? (double)ent : 0.0;
+      st[rr][ST_KL] = l ? (double)(x.olp - lp) : 0.0;
+      st[rr][ST_CLIPFRAC] = l ? (double)clip_r : 0.0;
+      st[rr][ST_ADV] = l ? (double)x.adv : 0.0;
+      st[rr][ST_CRITIC] = l ? (double)crow : 0.0;
+      st[rr][ST_RESID] = l ? res : 0.0;
+      st[rr][ST_RESID2] = l ? res * res : 0.0;
+      st[rr][ST_RET] = l ? (double)x.ret : 0.0;
+      st[rr][ST_RET2] = l ? (double)x.ret * (double)x.ret : 0.0;
+      st[rr][ST_VALUE] = l ? (double)v : 0.0;
+    }
   }
-  const float ratio = __expf(lp - olp);
-  float cr, dcr;
-  clip_grad(ratio, 1.f - eps, 1.f + eps, cr, dcr);
-  const float pg1 = ratio * Av, pg2 = cr * Av;
-  const float pmin = fminf(pg1, pg2);
-  const float g_lp = -(tie_first(pg1, pg2, pmin) * Av + tie_first(pg2, pg1, pmin) * Av * dcr) * p.inv_n * ratio;
-  const float g_ent = -p.ent_coef * p.inv_n;
-  const float vl1 = 0.5f * (v - Rt) * (v - Rt);
-  float crow, gv;
-  if (p.clip_value_loss) {
-    float dv, ddv;
-    clip_grad(v - vold, -eps, eps, dv, ddv);
-    const float vc = vold + dv;
-    const float vl2 = 0.5f * (vc - Rt) * (vc - Rt);
-    crow = fmaxf(vl1, vl2);
-    gv = tie_first(vl1, vl2, crow) * (v - Rt) + tie_first(vl2, vl1, crow) * (vc - Rt) * ddv;
-  } else {
-    crow = vl1;
-    gv = v - Rt;
+  __syncthreads();
+  // block partials: column sums over the rows in row order (wave 0)
+  if (t < NSTAT) {
+    double a = 0.0;
+    for (int r = 0; r < ROWS; ++r) a += st[r][t];
+    p.stats_partial[blk * NSTAT + t] = a;
+  } else if (t >= 16 && t < 16 + (int)p.ldwa) {
+    float a = 0.f;
+    for (int r = 0; r < ROWS; ++r) a += dout[r][t - 16];
+    p.bpart_a[blk * p.ldwa + (t - 16)] = a;
+  } else if (SEP && t >= 32 && t < 32 + (int)p.ldwc) {
+    float a = 0.f;
+    if (t == 32)
+      for (int r = 0; r < ROWS; ++r) a += dout[r][16];
+    p.bpart_c[blk * p.ldwc + (t - 32)] = a;
+  } else if (spread && t >= 48 && t < 48 + A) {
+    float a = 0.f;
+    for (int r = 0; r < ROWS; ++r) a += dsc[r][t - 48];
+    p.dscale_partial[blk * A + (t - 48)] = a;
   }
-  dvalue = p.vf_coef * gv * p.inv_n;
-  if (p.dist == DIST_CATEGORICAL) {
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-      if (j < A) {
-        const float lq = out[j] * inv_t - lse;
-        const float q = __expf(lq);
-        dout[j] = (g_lp * ((j == a ? 1.f : 0.f) - q) - g_ent * q * (lq + ent)) * inv_t;
-      }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-      if (j < A) {
-        float raw = 0.f;
-        if (p.scale_param) {
-          raw = p.scale_param[j];
-        } else {
-#pragma unroll
-          for (int q = 0; q < 16; ++q) raw = (q == A + j) ? out[q] : raw;
-        }
-        const float sig = p.temperature * (softplusf(raw) + 1e-3f);
-        const float d = p.action_f[s * A + j] - out[j];
-        dout[j] = g_lp * d / (sig * sig);
-        const float dsig = g_lp * (d * d / (sig * sig * sig) - 1.f / sig) + g_ent / sig;
-        const float draw = dsig * p.temperature / (1.f + __expf(-raw));
-        if (p.scale_param) {
-          dsc[j] += draw;
-        } else {
-#pragma unroll
-          for (int q = 0; q < 16; ++q) dout[q] = (q == A + j) ? draw : dout[q];
-        }
-      }
-  }
-  if (!sep) {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) dout[j] = (j == p.na - 1) ? dvalue : dout[j];
-  }
-  st[ST_ACTOR] += (double)(-pmin);
-  st[ST_ENTROPY] += (double)ent;
-  st[ST_KL] += (double)(olp - lp);
-  st[ST_CLIPFRAC] += (fabsf(ratio - 1.f) > eps) ? 1.0 : 0.0;
-  st[ST_ADV] += (double)Av;
-  st[ST_CRITIC] += (double)crow;
-  const double res = (double)Rt - (double)v;
-  st[ST_RESID] += res;
-  st[ST_RESID2] += res * res;
-  st[ST_RET] += (double)Rt;
-  st[ST_RET2] += (double)Rt * (double)Rt;
-  st[ST_VALUE] += (double)v;
 }
 
 __device__ __forceinline__ floatx4 mfma4(floatx4 a, const float (&b)[4], floatx4 acc) {
@@ -203,8 +289,10 @@ __device__ __forceinline__ floatx4 mfma4(floatx4 a, const float (&b)[4], floatx4
 
 template <bool SEP>
 __global__ void __launch_bounds__(HL_THREADS) head_loss_kernel(HeadLossParams p) {
-  __shared__ __attribute__((aligned(16))) float s_out[TR][LDO];
+  __shared__ __attribute__((aligned(16))) float s_out[1][TR][LDO];
   __shared__ __attribute__((aligned(16))) float s_dout[TR][LDO];
+  __shared__ double s_st[TR][NSTAT];
+  __shared__ float s_dsc[TR][16];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int li = lane & 15;   // MFMA row (A) / column (B, D)
@@ -212,6 +300,12 @@ __global__ void __launch_bounds__(HL_THREADS) head_loss_kernel(HeadLossParams p)
   const int F = p.F;
   const int r0 = blockIdx.x * TR;
   const int64_t blk = blockIdx.x;
+
+  // phase B's inputs, loaded first
+  LaneIn lin[TR / 16];
+#pragma unroll
+  for (int g = 0; g < TR / 16; ++g) lin[g] = load_lane(p, r0 + (threadIdx.x >> 4) + 16 * g, threadIdx.x & 15);
+  const ColConst cc = load_cols(p, SEP, threadIdx.x & 15);
 
   // ---------------- A. head outputs of the wave's 16 rows
   {
@@ -245,70 +339,14 @@ __global__ void __launch_bounds__(HL_THREADS) head_loss_kernel(HeadLossParams p)
     }
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      s_out[16 * wave + 4 * kq + v][li] = acc[v];
-      if (SEP && li == 0) s_out[16 * wave + 4 * kq + v][16] = accc[v];
+      s_out[0][16 * wave + 4 * kq + v][li] = acc[v];
+      if (SEP && li == 0) s_out[0][16 * wave + 4 * kq + v][16] = accc[v];
     }
   }
   __syncthreads();
 
-  // ---------------- B. loss and output cotangents, one lane of wave 0 per row
-  if (wave == 0) {
-    double st[NSTAT];
-#pragma unroll
-    for (int i = 0; i < NSTAT; ++i) st[i] = 0.0;
-    float db[16], dsc[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) db[j] = dsc[j] = 0.f;
-    float dbc = 0.f;
-    const int r = r0 + lane;
-    float dout[16];
-    float dvalue = 0.f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) dout[j] = 0.f;
-    if (r < p.rows) {
-      const int64_t s = p.idx ? (int64_t)p.idx[r] : (int64_t)r;
-      float out[16];
-#pragma unroll
-      for (int j = 0; j < 16; ++j) out[j] = s_out[lane][j] + (j < p.na ? p.ba[j] : 0.f);
-      const float v = SEP ? s_out[lane][16] + p.bc[0] : out[p.na - 1];
-      row_loss(p, SEP, s, out, v, dout, dvalue, st, dsc);
-#pragma unroll
-      for (int j = 0; j < 16; ++j) db[j] = dout[j];
-      dbc = dvalue;
-    }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) s_dout[lane][j] = dout[j];
-    s_dout[lane][16] = dvalue;
-    // block partials: statistics, head biases, Gaussian scale (fixed-order wave sums)
-#pragma unroll
-    for (int i = 0; i < NSTAT; ++i) st[i] = ppo::wave_sum_d(st[i]);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      db[j] = ppo::wave_sum(db[j]);
-      dsc[j] = ppo::wave_sum(dsc[j]);
-    }
-    dbc = ppo::wave_sum(dbc);
-    if (lane < NSTAT) {
-      double t = 0.0;
-#pragma unroll
-      for (int i = 0; i < NSTAT; ++i) t = (i == lane) ? st[i] : t;
-      p.stats_partial[blk * NSTAT + lane] = t;
-    }
-    if (lane < (int)p.ldwa) {
-      float t = 0.f;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) t = (j == lane) ? db[j] : t;
-      p.bpart_a[blk * p.ldwa + lane] = t;
-    }
-    if (SEP && lane < (int)p.ldwc) p.bpart_c[blk * p.ldwc + lane] = lane == 0 ? dbc : 0.f;
-    if (p.scale_param && lane < p.A) {
-      float t = 0.f;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) t = (j == lane) ? dsc[j] : t;
-      p.dscale_partial[blk * p.A + lane] = t;
-    }
-  }
-  __syncthreads();
+  // ---------------- B. loss and output cotangents (element-parallel)
+  phase_b<TR, 1, SEP>(p, blk, s_out, s_dout, s_st, s_dsc, lin, cc);
 
   // ---------------- C1. cotangent of the head inputs (the wave's 16 rows)
   {
@@ -393,11 +431,158 @@ __global__ void __launch_bounds__(HL_THREADS) head_loss_kernel(HeadLossParams p)
   }
 }
 
+// The same computation for small minibatches: a workgroup owns TS = 16 rows
+// and its four waves split the features instead of the rows (16-feature
+// blocks fb = 16 (wave + 4 i), i < NB), so a minibatch of a few thousand
+// rows still spreads over hundreds of workgroups.  Every operand of phases
+// A, C1 and C2 (none depends on the loss) and the rows' rollout inputs are
+// loaded before the first MFMA: one global round trip per phase chain.
+// Phase A's four per-wave partial head outputs are summed in wave order.
+constexpr int TS = 16;
+
+template <bool SEP, int NB>
+__global__ void __launch_bounds__(HL_THREADS) head_loss_fs_kernel(HeadLossParams p) {
+  __shared__ __attribute__((aligned(16))) float s_part[4][TS][LDO];
+  __shared__ __attribute__((aligned(16))) float s_dout[TS][LDO];
+  __shared__ double s_st[TS][NSTAT];
+  __shared__ float s_dsc[TS][16];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 15;
+  const int kq = lane >> 4;
+  const int F = p.F;
+  const int r0 = blockIdx.x * TS;  // < rows: the grid has ceil(rows / TS) blocks
+  const int64_t blk = blockIdx.x;
+  const int last = p.rows - 1;
+
+  // phase B's inputs (thread: row threadIdx.x / 16, column threadIdx.x % 16)
+  LaneIn lin[1];
+  lin[0] = load_lane(p, r0 + (threadIdx.x >> 4), threadIdx.x & 15);
+  const ColConst cc = load_cols(p, SEP, threadIdx.x & 15);
+
+  // ---- loads of phases A, C1, C2 (clamped in-range addresses, zeroed after)
+  // A: lane (row li, k group kq); C1 / C2: lane (feature li, rows 4 kq + s)
+  const bool liveA = r0 + li < p.rows;
+  const int64_t rowA = min(r0 + li, last);
+  int64_t rowq[4];
+  bool liveq[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    liveq[q] = r0 + 4 * kq + q < p.rows;
+    rowq[q] = min(r0 + 4 * kq + q, last);
+  }
+  const int ja = min(li, (int)p.ldwa - 1);  // head output column of A's B operand
+  floatx4 hA[NB], cA[NB];
+  float wA[NB][4], wC[NB][4], bT[NB][4], xa[NB][4], xc[NB][4], h2[NB][4], c2[NB][4], wcf[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int fb = 16 * (wave + 4 * i);
+    const int fbc = fb < F ? fb : 0;
+    hA[i] = *reinterpret_cast<const floatx4*>(p.ha + rowA * p.ldha + fbc + 4 * kq);
+    if (SEP) cA[i] = *reinterpret_cast<const floatx4*>(p.hc + rowA * p.ldhc + fbc + 4 * kq);
+    const int f = fbc + li;
+    if (SEP) wcf[i] = p.wc[(int64_t)f * p.ldwc];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      wA[i][q] = p.wa[(int64_t)(fbc + 4 * kq + q) * p.ldwa + ja];
+      if (SEP) wC[i][q] = p.wc[(int64_t)(fbc + 4 * kq + q) * p.ldwc];
+      bT[i][q] = p.wa[(int64_t)f * p.ldwa + min(4 * kq + q, (int)p.ldwa - 1)];
+      if (p.act_a != ACT_NONE) xa[i][q] = p.aux_a[rowq[q] * p.ldaux_a + f];
+      if (SEP && p.act_c != ACT_NONE) xc[i][q] = p.aux_c[rowq[q] * p.ldaux_c + f];
+      h2[i][q] = p.ha[rowq[q] * p.ldha + f];
+      if (SEP) c2[i][q] = p.hc[rowq[q] * p.ldhc + f];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const bool fin = 16 * (wave + 4 * i) < F;
+    const floatx4 z4 = {0.f, 0.f, 0.f, 0.f};
+    hA[i] = (fin && liveA) ? hA[i] : z4;
+    if (SEP) cA[i] = (fin && liveA) ? cA[i] : z4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      wA[i][q] = (fin && li < p.na) ? wA[i][q] : 0.f;
+      if (SEP) wC[i][q] = (fin && li == 0) ? wC[i][q] : 0.f;
+      bT[i][q] = (fin && 4 * kq + q < p.na) ? bT[i][q] : 0.f;
+      h2[i][q] = (fin && liveq[q]) ? h2[i][q] : 0.f;
+      if (SEP) c2[i][q] = (fin && liveq[q]) ? c2[i][q] : 0.f;
+    }
+  }
+
+  // ---------------- A. per-wave partial head outputs of the 16 rows
+  {
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f}, accc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      acc = mfma4(hA[i], wA[i], acc);
+      if (SEP) accc = mfma4(cA[i], wC[i], accc);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      s_part[wave][4 * kq + v][li] = acc[v];
+      if (SEP && li == 0) s_part[wave][4 * kq + v][16] = accc[v];
+    }
+  }
+  __syncthreads();
+
+  // ---------------- B. loss and output cotangents (element-parallel)
+  phase_b<TS, 4, SEP>(p, blk, s_part, s_dout, s_st, s_dsc, lin, cc);
+
+  // ---------------- C1. cotangent of the head inputs; C2. head weight gradient partial
+  const floatx4 dv4 = *reinterpret_cast<const floatx4*>(&s_dout[li][4 * kq]);
+  const floatx4 a_in = liveA ? dv4 : floatx4{0.f, 0.f, 0.f, 0.f};
+  float dq[4], dvq[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    dq[q] = s_dout[4 * kq + q][li];
+    dvq[q] = s_dout[4 * kq + q][16];
+  }
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int fb = 16 * (wave + 4 * i);
+    if (fb >= F) break;
+    const int f = fb + li;
+    const floatx4 g = mfma4(a_in, bT[i], floatx4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      if (!liveq[v]) continue;
+      const int64_t row = rowq[v];
+      float d = g[v];
+      if (p.act_a != ACT_NONE) d *= ppo::act_grad(p.act_a, xa[i][v]);
+      p.dha[row * p.lddha + f] = d;
+      if (SEP) {
+        float dc = dvq[v] * wcf[i];
+        if (p.act_c != ACT_NONE) dc *= ppo::act_grad(p.act_c, xc[i][v]);
+        p.dhc[row * p.lddhc + f] = dc;
+      }
+    }
+    float wv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) wv[q] = li == 0 ? dvq[q] : 0.f;
+    const floatx4 gw = mfma4(floatx4{h2[i][0], h2[i][1], h2[i][2], h2[i][3]}, dq, floatx4{0.f, 0.f, 0.f, 0.f});
+    floatx4 gc = {0.f, 0.f, 0.f, 0.f};
+    if (SEP) gc = mfma4(floatx4{c2[i][0], c2[i][1], c2[i][2], c2[i][3]}, wv, gc);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int ff = fb + 4 * kq + v;
+      if (li < (int)p.ldwa) p.wpart_a[(blk * F + ff) * p.ldwa + li] = gw[v];
+      if (SEP && li < (int)p.ldwc) p.wpart_c[(blk * F + ff) * p.ldwc + li] = li == 0 ? gc[v] : 0.f;
+    }
+  }
+}
+
 }  // namespace
 
+#ifndef PPO_HL_SMALL_ROWS
+#define PPO_HL_SMALL_ROWS 16384  // minibatches up to this many rows take the feature-split kernel
+#endif
+
 // Blocks the fused kernel launches for `rows` (the partial buffers' leading
-// extent): one per 64-row tile.
-PPO_EXPORT int ppo_head_loss_blocks(int rows) { return std::max(1, ppo::ceil_div(rows, TR)); }
+// extent): one per 16-row tile up to PPO_HL_SMALL_ROWS rows, else one per
+// 64-row tile.
+PPO_EXPORT int ppo_head_loss_blocks(int rows) {
+  return std::max(1, ppo::ceil_div(rows, rows <= PPO_HL_SMALL_ROWS ? TS : TR));
+}
 
 // Largest head width (outputs of group a) and feature width the fused kernel
 // takes; the feature width must also be a multiple of 16.
@@ -444,7 +629,21 @@ PPO_EXPORT int ppo_head_loss_f32(
   p.inv_n = 1.f / (float)rows; p.temperature = temperature;
   const int blocks = ppo_head_loss_blocks(rows);
   hipStream_t st = ppo::as_stream(stream);
-  if (sep) hipLaunchKernelGGL(head_loss_kernel<true>, dim3(blocks), dim3(HL_THREADS), 0, st, p);
-  else hipLaunchKernelGGL(head_loss_kernel<false>, dim3(blocks), dim3(HL_THREADS), 0, st, p);
+  if (rows <= PPO_HL_SMALL_ROWS) {
+    const int nb = ppo::ceil_div(F, 64);  // 16-feature blocks per wave
+    auto fs = [&](auto sep_c) {
+      constexpr bool S = decltype(sep_c)::value;
+      if (nb <= 1) hipLaunchKernelGGL((head_loss_fs_kernel<S, 1>), dim3(blocks), dim3(HL_THREADS), 0, st, p);
+      else if (nb <= 2) hipLaunchKernelGGL((head_loss_fs_kernel<S, 2>), dim3(blocks), dim3(HL_THREADS), 0, st, p);
+      else if (nb <= 4) hipLaunchKernelGGL((head_loss_fs_kernel<S, 4>), dim3(blocks), dim3(HL_THREADS), 0, st, p);
+      else hipLaunchKernelGGL((head_loss_fs_kernel<S, 8>), dim3(blocks), dim3(HL_THREADS), 0, st, p);
+    };
+    if (sep) fs(std::true_type{});
+    else fs(std::false_type{});
+  } else if (sep) {
+    hipLaunchKernelGGL(head_loss_kernel<true>, dim3(blocks), dim3(HL_THREADS), 0, st, p);
+  } else {
+    hipLaunchKernelGGL(head_loss_kernel<false>, dim3(blocks), dim3(HL_THREADS), 0, st, p);
+  }
   return ppo::check_launch("ppo_head_loss_f32");
 }
