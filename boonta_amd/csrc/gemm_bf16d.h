@@ -5,7 +5,8 @@
 // registers hold staged data and no LDS store instructions run.  Contraction,
 // layouts, row gather, split-K and epilogue are those of gemm_bf16s_kernel.
 //
-// LDS holds NBUF stages in a ring (3 for 256 x 128 tiles, 4 for 128 x 128);
+// LDS holds NBUF stages in a ring (3 for 256 x 128 tiles, 4 for 128 x 128,
+// 2 for 256 x 256);
 // stage kt + NBUF - 1 is issued right after the barrier that opens stage kt,
 // so NBUF - 1 stages of loads are in flight behind the MFMAs.  Layouts (bf16, no padding, 16-byte chunks XOR-swizzled
 // by the row so that transpose reads, 16-byte operand reads and the copies
@@ -25,6 +26,7 @@
 namespace ppo_bf16s {
 
 constexpr int KIDX_MAX = 2048;  // reduction rows per split when the k-outer A operand is gathered
+constexpr int KIDX_256 = 4096;  // the same for the 256 x 256 tile (its ring holds two stages)
 
 using ppo::kc_swizzle;
 __device__ __forceinline__ int ko_swizzle(int k) { return ((k & 1) ? 4 : 0) ^ ((k & 2) ? 10 : 0); }
@@ -154,7 +156,7 @@ __device__ __forceinline__ void ring_barrier(int younger) {
   }
 }
 
-template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF>
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF, int KIDX = KIDX_MAX>
 __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_bf16d_kernel(Params p) {
   constexpr int NW = WM * WN;
   constexpr int BI = BM / WM / 32, BJ = BN / WN / 32;
@@ -164,7 +166,7 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_bf16d_kernel(Params p) {
   __shared__ __attribute__((aligned(1024))) uint16_t sA[NBUF][OpA::ELEMS];
   __shared__ __attribute__((aligned(1024))) uint16_t sB[NBUF][OpB::ELEMS];
   // gather indices of the split's reduction rows (A k-outer and gathered)
-  __shared__ int32_t sIdx[A_K ? 1 : KIDX_MAX];
+  __shared__ int32_t sIdx[A_K ? 1 : KIDX];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -265,10 +267,11 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_bf16d_kernel(Params p) {
   epilogue<BI, BJ>(p, acc, bsum, do_bsum, m0 + wm * (BI * 32), n0 + wn * (BJ * 32), split, lane);
 }
 
-template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF>
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF, int KIDX = KIDX_MAX>
 int launch_d(hipStream_t st, const Params& p, int splits) {
   dim3 grid(ppo::ceil_div(p.N, BN), ppo::ceil_div(p.M, BM), splits);
-  hipLaunchKernelGGL((gemm_bf16d_kernel<BM, BN, WM, WN, A_K, B_K, NBUF>), grid, dim3(WM * WN * 64), 0, st, p);
+  hipLaunchKernelGGL((gemm_bf16d_kernel<BM, BN, WM, WN, A_K, B_K, NBUF, KIDX>), grid, dim3(WM * WN * 64), 0, st,
+                     p);
   return ppo::check_launch("ppo_gemm_bf16s");
 }
 

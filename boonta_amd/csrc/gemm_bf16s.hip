@@ -80,13 +80,13 @@ __global__ void splits_bias_act_bf16_kernel(const float* __restrict__ p, int64_t
 // a_bf16 / b_bf16: the operand is stored as bf16 (uint16 bit patterns) rather
 // than fp32.
 // tile: -1 picks; 0: 256 x 128 (8 waves of 64 x 64), 1: 128 x 128 (4 waves of
-// 64 x 64).
+// 64 x 64), 2: 256 x 256 (8 waves of 128 x 64; both operands bf16, else 0).
 PPO_EXPORT int ppo_gemm_bf16s(void* stream, int a_layout, int b_layout, int a_bf16, int b_bf16, const void* A,
                               int64_t lda, const int32_t* rows, const void* B, int64_t ldb, float* C, int64_t ldc,
                               int M, int N, int K, int splits, int64_t c_split_stride, int epi, const float* bias,
                               int act, int round_out, const float* aux, int64_t ldaux, float* bias_grad, int tile) {
   if (M < 0 || N < 0 || K < 0 || splits < 1 || a_layout < 0 || a_layout > 1 || b_layout < 0 || b_layout > 1 ||
-      epi < 0 || epi > 2 || act < 0 || act > 3 || tile > 1)
+      epi < 0 || epi > 2 || act < 0 || act > 3 || tile > 2)
     return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_bf16s: bad argument (M=%d N=%d K=%d splits=%d)", M, N, K, splits);
   if (M == 0 || N == 0) return PPO_OK;
   if (!A || !B || !C) return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_bf16s: null operand");

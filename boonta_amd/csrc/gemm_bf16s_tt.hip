@@ -11,8 +11,10 @@ namespace ppo_bf16s {
 
 template <bool A_K, bool B_K>
 int launch_tt(hipStream_t st, const Params& p, int splits, int tile) {
-  const bool dma = A_K || p.rows == nullptr || p.k_per_split <= KIDX_MAX;
-  if (!dma) return launch_tile<A_K, B_K, uint16_t, uint16_t>(st, p, splits, tile);
+  const bool gathered_k = !A_K && p.rows != nullptr;  // the split's gather indices are cached in LDS
+  if (tile == 2 && (!gathered_k || p.k_per_split <= KIDX_256))
+    return launch_d<256, 256, 2, 4, A_K, B_K, 2, KIDX_256>(st, p, splits);
+  if (gathered_k && p.k_per_split > KIDX_MAX) return launch_tile<A_K, B_K, uint16_t, uint16_t>(st, p, splits, tile);
   if (tile == 1) return launch_d<128, 128, 2, 2, A_K, B_K, PPO_BF16D_NBUF128>(st, p, splits);
   return launch_d<256, 128, 4, 2, A_K, B_K, 3>(st, p, splits);
 }

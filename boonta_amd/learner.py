@@ -246,7 +246,8 @@ class MLPExecutor:
     """One compiled PPO.update for fixed (T, N, obs, minibatches, epochs)."""
 
     FWD16_SPLITS = 2  # K splits of the bf16 first-layer forward (256 tiles of 256 x 128 at 8192 x 512)
-    DW16_SPLITS = 4   # row splits of the bf16 first-layer dW
+    DW16_SPLITS = 3   # row splits of the bf16 first-layer dW (with 256 x 256 tiles: 198 workgroups at 8268 x 512)
+    DW16_TILE = 2     # 256 x 256 tiles for the bf16 first-layer dW
     DW16_SPLITS_INNER = 16  # row splits of a bf16 dW between two LayerNorm layers
 
     def __init__(self, program: Program, flat: FlatState, cfg, chain, T: int, N: int):
@@ -596,7 +597,7 @@ class MLPExecutor:
             if obs16:
                 self._call("ppo_gemm_bf16s", st, A_COL, B_KN, 1, int(dz16), _p(self.OBS16), self.ldo16, ridx, dz,
                            s.ld, _p(lb.wpart), s.ld, d.fin, s.ld, self.mb, lb.splits, d.fin * s.ld, EPI_STORE, None,
-                           0, 0, None, 0, _p(lb.bpart), -1)
+                           0, 0, None, 0, _p(lb.bpart), self.DW16_TILE)
             elif y16 or dz16:
                 a = _p(layers[i - 1].Y16) if y16 else x
                 self._call("ppo_gemm_bf16s", st, A_COL, B_KN, int(y16), int(dz16), a, ldx, None, dz, s.ld,

@@ -95,7 +95,10 @@ int ppo_epoch_permutations(void* stream, const uint32_t* key, int epochs, int64_
  *       input for silu)
  *   splits > 1: split of the reduction; partial s at C + s * c_split_stride
  *   bias_grad (a_layout 1, b_layout 0): [splits][N] column sums of B
- *   tile: -1 automatic; 0 128x128, 1 128x64, 2 64x128, 3 64x64. */
+ *   tile: -1 automatic (64x64); 0 128x128, 1 128x64, 2 64x128, 3 64x64
+ *   (operands copied straight into LDS, 32 reduction steps per stage); 4-7
+ *   the same tiles staged through registers; 8 128x256, 9 256x128 (8 waves,
+ *   copied straight into LDS). */
 int ppo_gemm_f32(void* stream, int a_layout, int b_layout, const float* A, int64_t lda, const int32_t* rows,
                  const float* B, int64_t ldb, float* C, int64_t ldc, int M, int N, int K, int splits,
                  int64_t c_split_stride, int epi, const float* bias, int act, float* pre, const float* aux,
@@ -124,7 +127,8 @@ int ppo_round_bf16(void* stream, float* x, int64_t n);
  * bf16 operand's row pitch is at least its contiguous extent rounded up to 8.
  * With both operands stored as bf16, stages are copied straight from global
  * memory into LDS (no register staging), three stages in flight.
- * tile: -1 picks; 0: 256 x 128 (8 waves), 1: 128 x 128 (4 waves). */
+ * tile: -1 picks; 0: 256 x 128 (8 waves), 1: 128 x 128 (4 waves), 2: 256 x 256
+ * (8 waves, two stages; both operands bf16, otherwise tile 0). */
 int ppo_gemm_bf16s(void* stream, int a_layout, int b_layout, int a_bf16, int b_bf16, const void* A, int64_t lda,
                    const int32_t* rows, const void* B, int64_t ldb, float* C, int64_t ldc, int M, int N, int K,
                    int splits, int64_t c_split_stride, int epi, const float* bias, int act, int round_out,

@@ -354,6 +354,7 @@ def gemm_s_case(a_layout, b_layout, a_bf16, b_bf16, M, N, K, rows_src=None, gath
     if bias_grad:
         np.testing.assert_allclose(BG.cpu().numpy().astype(np.float64).sum(0), Bb.sum(0), rtol=1e-5,
                                    atol=1e-5 * np.sqrt(K))
+    return C
 
 
 @pytest.mark.parametrize("a_layout, b_layout", [(0, 0), (0, 1), (1, 0), (1, 1)])
@@ -363,7 +364,33 @@ def test_gemm_bf16s_layouts_and_storage(a_layout, b_layout, a_bf16, b_bf16):
     gemm_s_case(a_layout, b_layout, a_bf16, b_bf16, 300, 136, 700, seed=seed, tile=seed % 2)
 
 
-@pytest.mark.parametrize("tile", [0, 1])
+@pytest.mark.parametrize("a_layout, b_layout", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_bf16s_256x256_tile(a_layout, b_layout):
+    """Tile 2 (256 x 256, two stages): ragged M, N and K, a gathered operand,
+    split-K, and the bit-identical result of tile 0 at the same splits (both
+    accumulate each output along k in the same order)."""
+    seed = 20 + 2 * a_layout + b_layout
+    bg = a_layout == 1 and b_layout == 0
+    c2 = gemm_s_case(a_layout, b_layout, 1, 1, 300, 270, 650, rows_src=900, gather=True, splits=2, round_out=0,
+                     bias_grad=bg, seed=seed, tile=2)
+    c0 = gemm_s_case(a_layout, b_layout, 1, 1, 300, 270, 650, rows_src=900, gather=True, splits=2, round_out=0,
+                     bias_grad=bg, seed=seed, tile=0)
+    assert torch.equal(c2, c0)
+    gemm_s_case(a_layout, b_layout, 1, 1, 520, 300, 200, epi=1, act=1, seed=seed + 10, tile=2)
+
+
+def test_gemm_bf16s_256x256_gathered_reduction():
+    """Tile 2 caches up to 4096 gathered reduction rows per split (k-outer A);
+    more run on the register-staged pipeline."""
+    for splits in (2, 1):  # 2112 rows per split (beyond the 2048 of the other tiles), then 4224
+        gemm_s_case(1, 0, 1, 1, 300, 136, 4200, rows_src=5000, gather=True, splits=splits, round_out=0,
+                    bias_grad=True, seed=30 + splits, tile=2)
+    # exactly 4096 rows: a full index cache
+    gemm_s_case(1, 0, 1, 1, 300, 136, 4096, rows_src=5000, gather=True, splits=1, round_out=0, bias_grad=True,
+                seed=33, tile=2)
+
+
+@pytest.mark.parametrize("tile", [0, 1, 2])
 def test_gemm_bf16s_first_layer_shapes(tile):
     # forward: gathered bf16 observation rows (8268 features, a ragged last stage) x bf16 weights
     gemm_s_case(0, 0, 1, 1, 1024, 512, 8268, rows_src=3000, gather=True, epi=1, act=1, tile=tile)
