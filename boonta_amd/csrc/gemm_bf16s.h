@@ -20,6 +20,7 @@
 //     16 lanes, lane i receives element i % 4 of the 8-byte rows addressed by
 //     lanes 4e + i / 4, e = 0..3).
 #pragma once
+#include <utility>
 #include "common.h"
 
 #include <algorithm>
@@ -229,46 +230,53 @@ __device__ __forceinline__ bf16x8 operand(const uint16_t* lds, int r0, int kk, i
   }
 }
 
-// Stores a wave's BI x BJ blocks of 32 x 32 (rows from wm0, columns from
-// wn0) with the epilogue, and the bias-gradient column sums of B.
+// One 32 x 32 block (rows wm0b.., columns wn0b..) of the epilogue.
+__device__ __forceinline__ void epilogue_block(const Params& p, float* C, const floatx16& a, int wm0b, int wn0b,
+                                               int h, int l32) {
+  const bool rnd = p.round_out != 0;
+  const int gn = wn0b + l32;
+  const bool n_ok = gn < p.N;
+  float bias = 0.f;
+  if (p.epi == EPI_BIAS_ACT && p.bias && n_ok) bias = rnd ? bf16_round(p.bias[gn]) : p.bias[gn];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int gm = wm0b + 8 * (r >> 2) + 4 * h + (r & 3);
+    if (!n_ok || gm >= p.M) continue;
+    float v = a[r];
+    if (rnd) v = bf16_round(v);
+    if (p.epi == EPI_BIAS_ACT) {
+      if (p.bias) {
+        v += bias;
+        if (rnd) v = bf16_round(v);
+      }
+      if (p.act != ACT_NONE) {
+        v = ppo::act_fwd(p.act, v);
+        if (rnd) v = bf16_round(v);
+      }
+    } else if (p.epi == EPI_DACT) {
+      v *= ppo::act_grad(p.act, p.aux[(int64_t)gm * p.ldaux + gn]);
+      if (rnd) v = bf16_round(v);
+    }
+    C[(int64_t)gm * p.ldc + gn] = v;
+  }
+}
+
+template <int BI, int BJ, int... I>
+__device__ __forceinline__ void epilogue_blocks(const Params& p, float* C, floatx16 (&acc)[BI][BJ], int wm0, int wn0,
+                                                int h, int l32, std::integer_sequence<int, I...>) {
+  // compile-time block indices: the accumulators stay in registers
+  (epilogue_block(p, C, acc[I / BJ][I % BJ], wm0 + (I / BJ) * 32, wn0 + (I % BJ) * 32, h, l32), ...);
+}
+
+// The wave's BI x BJ accumulator blocks (rows from wm0, columns from wn0)
+// with the epilogue, and the bias-gradient column sums of B.
 template <int BI, int BJ>
 __device__ __forceinline__ void epilogue(const Params& p, floatx16 (&acc)[BI][BJ], const float (&bsum)[BJ],
                                          bool do_bsum, int wm0, int wn0, int split, int lane) {
   const int h = lane >> 5;
   const int l32 = lane & 31;
-  const bool rnd = p.round_out != 0;
   float* C = p.C + (int64_t)split * p.c_split_stride;
-#pragma unroll
-  for (int bi = 0; bi < BI; ++bi) {
-#pragma unroll
-    for (int bj = 0; bj < BJ; ++bj) {
-      const int gn = wn0 + bj * 32 + l32;
-      const bool n_ok = gn < p.N;
-      float bias = 0.f;
-      if (p.epi == EPI_BIAS_ACT && p.bias && n_ok) bias = rnd ? bf16_round(p.bias[gn]) : p.bias[gn];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int gm = wm0 + bi * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (!n_ok || gm >= p.M) continue;
-        float v = acc[bi][bj][r];
-        if (rnd) v = bf16_round(v);
-        if (p.epi == EPI_BIAS_ACT) {
-          if (p.bias) {
-            v += bias;
-            if (rnd) v = bf16_round(v);
-          }
-          if (p.act != ACT_NONE) {
-            v = ppo::act_fwd(p.act, v);
-            if (rnd) v = bf16_round(v);
-          }
-        } else if (p.epi == EPI_DACT) {
-          v *= ppo::act_grad(p.act, p.aux[(int64_t)gm * p.ldaux + gn]);
-          if (rnd) v = bf16_round(v);
-        }
-        C[(int64_t)gm * p.ldc + gn] = v;
-      }
-    }
-  }
+  epilogue_blocks<BI, BJ>(p, C, acc, wm0, wn0, h, l32, std::make_integer_sequence<int, BI * BJ>{});
   if (do_bsum) {
 #pragma unroll
     for (int bj = 0; bj < BJ; ++bj) {
