@@ -44,9 +44,11 @@ constexpr int REDUCE_THREADS = 256;
 constexpr int CHUNK = 256;  // elements per block: one float4 per lane of a wave
 
 // One block per chunk of 256 gradient elements.  Each of the 4 waves sums a
-// contiguous quarter of the partials for the same 64 float4 (two interleaved
-// accumulators to keep loads in flight), then the quarters are added in wave
-// order: a fixed association, so the result never depends on scheduling.
+// contiguous quarter of the partials for the same 64 float4, eight partials
+// per step (eight loads in flight per lane, added as a fixed tree; the last
+// step's missing partials read a clamped partial and count as zero), then
+// the quarters are added in wave order: a fixed association, so the result
+// never depends on scheduling.
 __global__ void __launch_bounds__(REDUCE_THREADS)
 grad_reduce_kernel(const Segment* __restrict__ segs, const Chunk* __restrict__ chunks, double* __restrict__ sumsq) {
   __shared__ floatx4 part[REDUCE_THREADS / 64][64];
@@ -57,17 +59,23 @@ grad_reduce_kernel(const Segment* __restrict__ segs, const Chunk* __restrict__ c
   const int64_t i = ch.start + 4 * lane;  // first element of this lane's float4
   const bool live = i < sg.count;
   const int q0 = (sg.nparts * wave) / 4, q1 = (sg.nparts * (wave + 1)) / 4;
-  floatx4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
-  if (live) {
+  constexpr int U = 8;
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (live && q1 > q0) {
     const float* s = sg.src + i;
-    int q = q0;
-    for (; q + 1 < q1; q += 2) {
-      a0 += *reinterpret_cast<const floatx4*>(s + (int64_t)q * sg.part_stride);
-      a1 += *reinterpret_cast<const floatx4*>(s + (int64_t)(q + 1) * sg.part_stride);
+    for (int q = q0; q < q1; q += U) {
+      floatx4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int qq = min(q + u, q1 - 1);
+        v[u] = *reinterpret_cast<const floatx4*>(s + (int64_t)qq * sg.part_stride);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = q + u < q1 ? v[u] : floatx4{0.f, 0.f, 0.f, 0.f};
+      acc += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
     }
-    if (q < q1) a0 += *reinterpret_cast<const floatx4*>(s + (int64_t)q * sg.part_stride);
   }
-  part[wave][lane] = a0 + a1;
+  part[wave][lane] = acc;
   __syncthreads();
   if (wave == 0) {
     double sq = 0.0;

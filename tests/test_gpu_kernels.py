@@ -315,6 +315,39 @@ def test_fused_loss_matches_the_oracle(dist, A, spread):
 
 
 # ------------------------------------------------------------------- Adam
+@pytest.mark.parametrize("nparts", [1, 3, 37, 64])
+def test_grad_reduce_partials(nparts):
+    """Partial sums of two segments (ragged counts, padded part strides):
+    the reduced gradient and its per-chunk squared norms."""
+    import struct
+    g = np.random.default_rng(nparts)
+    chunk = _lib.load().ppo_grad_reduce_chunk_elems()
+    specs = [(1000, 1008), (300, 304)]  # (count, part stride)
+    segs, chunks, outs, refs = b"", b"", [], []
+    keep = []
+    for k, (n, stride) in enumerate(specs):
+        parts = (g.standard_normal((nparts, stride)) * 0.1).astype(np.float32)
+        P = dev(parts)
+        D = torch.full((n,), float("nan"), device=DEV)
+        keep += [P, D]
+        segs += struct.pack("<QQqqii", D.data_ptr(), P.data_ptr(), n, stride, nparts, 0)
+        chunks += b"".join(struct.pack("<iiq", k, 0, s) for s in range(0, n, chunk))
+        outs.append(D)
+        refs.append(parts[:, :n].astype(np.float64).sum(0))
+    nch = len(chunks) // 16
+    SEGS = torch.tensor(list(segs), dtype=torch.uint8, device=DEV)
+    CH = torch.tensor(list(chunks), dtype=torch.uint8, device=DEV)
+    SQ = torch.zeros(nch, dtype=torch.float64, device=DEV)
+    _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), CH.data_ptr(), nch, SQ.data_ptr())
+    torch.cuda.synchronize()
+    tot = 0.0
+    for D, ref in zip(outs, refs):
+        got = host(D).astype(np.float64)
+        np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6 * np.sqrt(nparts))
+        tot += float((got * got).sum())
+    np.testing.assert_allclose(host(SQ).sum(), tot, rtol=1e-12)
+
+
 @pytest.mark.parametrize("max_norm, scale", [(0.5, 1.0), (0.5, 1e-3), (0.0, 1.0)])
 def test_grad_reduce_and_adam_match_optax_restatement(max_norm, scale):
     import struct
