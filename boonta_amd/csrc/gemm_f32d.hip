@@ -2,8 +2,12 @@
 // lane's 16 bytes land at the wave's LDS base + 16 * lane), for operands with
 // 16-byte rows along their contiguous axis.  Same contraction, layouts, row
 // gather, split-K and epilogues as the register-staged kernel in gemm.hip;
-// no registers hold staged data and no LDS store instructions run, so three
-// stages of copies stay in flight behind the MFMAs.
+// no registers hold staged data and no LDS store instructions run.  The
+// 4-wave tiles keep a ring of two stages (the copies of the next stage in
+// flight behind the MFMAs of this one): the smaller LDS footprint keeps more
+// workgroups resident per CU, which hides the L2 latency better than a third
+// stage does (LDS allows five 64 x 64 workgroups per CU instead of three, two
+// 128 x 128 instead of one).  The 8-wave tiles keep three.
 //
 // Tiles: 4 wave64s in 2 x 2 (64 / 128 x 64 / 128 tiles) or 8 in 2 x 4 / 4 x 2
 // (128 x 256, 256 x 128), each wave (BM/WM) x (BN/WN) of 32 x 32 blocks of
@@ -26,7 +30,6 @@ namespace ppo_f32 {
 namespace {
 
 constexpr int BK = F32D_BK;
-constexpr int NBUF = 3;
 
 __device__ __forceinline__ int ko_swizzle32(int k) { return ((k >> 2) & 1) << 3; }
 
@@ -133,7 +136,7 @@ __device__ __forceinline__ floatx4 operand(const float* lds, int rbase, int g, i
   }
 }
 
-template <int BM, int BN, int WM, int WN, bool A_K, bool B_K>
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF>
 __global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_kernel(GemmParams p) {
   constexpr int NW = WM * WN;
   constexpr int MB = BM / WM / 32, NB = BN / WN / 32;  // 32 x 32 blocks per wave
@@ -239,8 +242,9 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_kernel(GemmParams p) {
 
 template <int BM, int BN, int WM, int WN, bool A_K, bool B_K>
 int launch(hipStream_t st, const GemmParams& p, int splits) {
+  constexpr int NBUF = WM * WN == 4 ? 2 : 3;
   dim3 grid(ppo::ceil_div(p.N, BN), ppo::ceil_div(p.M, BM), splits);
-  hipLaunchKernelGGL((gemm_f32d_kernel<BM, BN, WM, WN, A_K, B_K>), grid, dim3(WM * WN * 64), 0, st, p);
+  hipLaunchKernelGGL((gemm_f32d_kernel<BM, BN, WM, WN, A_K, B_K, NBUF>), grid, dim3(WM * WN * 64), 0, st, p);
   return ppo::check_launch("ppo_gemm_f32");
 }
 
