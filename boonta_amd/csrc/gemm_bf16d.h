@@ -5,7 +5,7 @@
 // registers hold staged data and no LDS store instructions run.  Contraction,
 // layouts, row gather, split-K and epilogue are those of gemm_bf16s_kernel.
 //
-// LDS holds NBUF stages in a ring (3 for 256 x 128 tiles, 4 for 128 x 128,
+// LDS holds NBUF stages in a ring (3 for 256 x 128 tiles, 2 for 128 x 128,
 // 2 for 256 x 256);
 // stage kt + NBUF - 1 is issued right after the barrier that opens stage kt,
 // so NBUF - 1 stages of loads are in flight behind the MFMAs.  Layouts (bf16, no padding, 16-byte chunks XOR-swizzled

@@ -4,7 +4,7 @@
 #include "gemm_bf16d.h"
 
 #ifndef PPO_BF16D_NBUF128
-#define PPO_BF16D_NBUF128 4  // ring depth of the 128 x 128 tiles (4 x 32 KB of LDS)
+#define PPO_BF16D_NBUF128 2  // ring depth of the 128 x 128 tiles (2 x 32 KB of LDS)
 #endif
 
 namespace ppo_bf16s {

@@ -245,7 +245,8 @@ class FlatState:
 class MLPExecutor:
     """One compiled PPO.update for fixed (T, N, obs, minibatches, epochs)."""
 
-    FWD16_SPLITS = 2  # K splits of the bf16 first-layer forward (256 tiles of 256 x 128 at 8192 x 512)
+    FWD16_SPLITS = 2  # K splits of the bf16 first-layer forward (512 workgroups of 128 x 128 at 8192 x 512)
+    FWD16_TILE = 1    # 128 x 128 tiles (two resident per CU) for the bf16 first-layer forward
     DW16_SPLITS = 3   # row splits of the bf16 first-layer dW (with 256 x 256 tiles: 198 workgroups at 8268 x 512)
     DW16_TILE = 2     # 256 x 256 tiles for the bf16 first-layer dW
     DW16_SPLITS_INNER = 16  # row splits of a bf16 dW between two LayerNorm layers
@@ -540,7 +541,7 @@ class MLPExecutor:
                 dst = lb.Z if s.ln is not None else lb.Y
                 self._call("ppo_gemm_bf16s", st, A_ROW, B_KN, 1, 1, _p(self.OBS16), self.ldo16, rows_idx,
                            self._view16(d.w), d.w.ld, _p(lb.fpart), s.ld, nrows, s.ld, d.fin, self.FWD16_SPLITS,
-                           nrows * s.ld, EPI_STORE, None, 0, 0, None, 0, None, -1)
+                           nrows * s.ld, EPI_STORE, None, 0, 0, None, 0, None, self.FWD16_TILE)
                 self._call("ppo_splits_bias_act_bf16", st, _p(lb.fpart), s.ld, nrows * s.ld, self.FWD16_SPLITS, Bb,
                            _act(s.act) if s.ln is None else 0, _p(dst), s.ld, nrows, s.ld)
                 if s.ln is not None:
