@@ -108,6 +108,21 @@ __device__ __forceinline__ void stage_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
 }
 
+// Stage barrier of a ring whose stages each issue PER_STAGE copies per wave:
+// the awaited stage's copies are complete while those of the `younger`
+// (<= Y) stages issued after it stay in flight.
+template <int PER_STAGE, int Y>
+__device__ __forceinline__ void ring_barrier(int younger) {
+  if constexpr (Y == 0) {
+    stage_barrier<0>();
+  } else {
+    if (younger >= Y)
+      stage_barrier<PER_STAGE * Y>();
+    else
+      ring_barrier<PER_STAGE, Y - 1>(younger);
+  }
+}
+
 // XOR applied to the 16-byte chunk index (0..7) of row r of a 128-byte-row
 // LDS tile: neither 16-byte copies / stores (8 lanes per row) nor reads of
 // one chunk over 32 consecutive rows put two lanes of a bank phase on a bank.

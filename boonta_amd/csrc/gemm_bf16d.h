@@ -142,19 +142,7 @@ __device__ __forceinline__ bf16x8 doperand(const uint16_t* lds, int r0, int kk, 
   }
 }
 
-// Stage barrier that lets the copies of the `younger` (<= Y) stages issued
-// after the awaited one stay in flight.
-template <int PER_STAGE, int Y>
-__device__ __forceinline__ void ring_barrier(int younger) {
-  if constexpr (Y == 0) {
-    stage_barrier<0>();
-  } else {
-    if (younger >= Y)
-      stage_barrier<PER_STAGE * Y>();
-    else
-      ring_barrier<PER_STAGE, Y - 1>(younger);
-  }
-}
+using ppo::ring_barrier;
 
 template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF, int KIDX = KIDX_MAX>
 __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_bf16d_kernel(Params p) {
