@@ -32,6 +32,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--path", choices=("update", "step"), default="update",
+                    help="update: the learner update (default); step: the rollout-side PPO.step "
+                         "(forward + action sampling) for one rollout of T steps over N envs")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--launch-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -158,6 +161,12 @@ def launch_work(name, args):
     if name == "ppo_splits_bias_act_bf16":
         nsplit, rows, cols = args[4], args[9], args[10]
         return 0.0, 4.0 * rows * cols * (nsplit + 1)
+    if name == "ppo_sample_categorical_f32":
+        rows, A = args[3], args[4]
+        return 0.0, 4.0 * rows * (A + 4)
+    if name == "ppo_sample_gaussian_f32":
+        rows, D = args[5], args[6]
+        return 0.0, 4.0 * rows * (3 * D + 3)
     if name == "ppo_gae_f32":
         T, N = args[10], args[11]
         return 0.0, 18.0 * T * N + 4.0 * N
@@ -318,6 +327,158 @@ def cpu_baseline(recipe, params, tr_dev, budget_s):
                       f"{E}x{M} steps per update"}
 
 
+def roofline_of(dom, total, workload):
+    if dom["flops"] > 0:
+        achieved = dom["flops"] / (dom["ms"] * 1e-3) / 1e12
+        peak = PEAK["bf16_mfma"] if dom["name"] in ("ppo_gemm_bf16", "ppo_gemm_bf16s") else PEAK["fp32_mfma"]
+        roof = {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
+                "frac": achieved / peak, "traffic": None}
+    else:
+        achieved = dom["bytes"] / (dom["ms"] * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": achieved, "peak": PEAK["hbm"], "unit": "GB/s",
+                "frac": achieved / PEAK["hbm"], "traffic": None}
+    roof["kernel"] = f"{dom['name']} layout={dom['layout']} MNK={dom['shape']}"
+    roof["traffic"] = measured_traffic(workload, roof["kernel"])
+    roof["avg_ms"] = dom["ms"]
+    roof["share_of_update"] = dom["ms"] * dom["count"] / total
+    return roof
+
+
+def time_calls(calls, reps, count):
+    """Each distinct launch of ``calls`` timed alone with HIP events on the
+    launching stream (``reps`` back-to-back repetitions), counted ``count``
+    times per measured unit."""
+    import torch
+    from boonta_amd import _lib
+
+    stream = torch.cuda.current_stream()
+    st = stream.cuda_stream
+    rows = []
+    for i, (name, args) in enumerate(calls):
+        args = (st,) + tuple(args[1:])
+        _lib.call(name, *args)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            _lib.call(name, *args)
+        e1.record(stream)
+        e1.synchronize()
+        flops, nbytes = launch_work(name, args)
+        row = {"i": i, "name": name, "ms": e0.elapsed_time(e1) / reps, "count": count, "flops": flops,
+               "bytes": nbytes,
+               "shape": [a for a in args[10:13]] if name.startswith("ppo_gemm") else None,
+               "layout": [args[1], args[2]] if name.startswith("ppo_gemm") else None}
+        if name == "ppo_gemm_bf16s":
+            row["shape"] = [a for a in args[12:15]]
+        rows.append(row)
+    return rows
+
+
+def step_main(args, recipe, alg, state, params, dev):
+    """Rollout-side PPO.step: one measured unit is the action selection of a
+    whole rollout, T steps over N envs (forward + sample_and_log_prob per
+    step, each step with its own key), captured once into a HIP graph and
+    replayed with the observations resident in HBM."""
+    import torch
+    from boonta_amd import synthetic
+    from boonta_amd.random import key as make_key
+
+    T, N, D = recipe.T, recipe.N, recipe.obs_dim
+    obs_np = synthetic.rollout(recipe, T, N)["obs"]
+    obs = torch.from_numpy(obs_np).to(dev)
+    ex = alg.step_executor(state, N, D)
+    dist = ex.prog.dist
+    if dist["kind"] == "categorical":
+        act = torch.zeros(T, N, dtype=torch.int32, device=dev)
+    else:
+        act = torch.zeros(T, N, dist["dim"], dtype=torch.float32, device=dev)
+    lp = torch.zeros(T, N, dtype=torch.float32, device=dev)
+    val = torch.zeros(T, N, dtype=torch.float32, device=dev)
+    keys = torch.from_numpy(np.stack([make_key(5000 + t) for t in range(T)]).view(np.int32)).to(dev)
+
+    def issue_rollout():
+        st = torch.cuda.current_stream().cuda_stream
+        for t in range(T):
+            ex.issue(st, obs[t].data_ptr(), D, 1.0, act[t].data_ptr(), lp[t].data_ptr(), val[t].data_ptr(),
+                     keys[t].data_ptr())
+
+    issue_rollout()
+    torch.cuda.synchronize()
+    g = None
+    if not args.no_graph:
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(g, stream=side):
+                issue_rollout()
+        torch.cuda.current_stream().wait_stream(side)
+    run = g.replay if g is not None else issue_rollout
+    for w in range(args.warmup):
+        run()
+        torch.cuda.synchronize()
+        log(f"warmup {w + 1}/{args.warmup} done")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    log(f"timed {args.steps} rollouts of action selection in {elapsed:.3f} s")
+    if not torch.isfinite(lp).all() or not torch.isfinite(val).all():
+        raise RuntimeError("non-finite step outputs")
+    out = {
+        "metric": "PPO.step action-selection samples/sec on 1 MI355X (rollout forward + sampling)",
+        "value": T * N * args.steps / elapsed, "unit": "samples/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": 1000.0 * elapsed / args.steps, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16" if ex.bf16 else "f32",
+        "data": "synthetic (seeded observations of the workload's distribution, random-init network)",
+        "config": {"workload": f"config {args.config}: {recipe.name} (PPO.step)", "T": T, "N": N, "obs": D,
+                   "graph": not args.no_graph},
+    }
+    if not args.profile_only:
+        calls = ex.record(obs[0].data_ptr(), D, 1.0, act[0].data_ptr(), lp[0].data_ptr(), val[0].data_ptr(),
+                          keys[0].data_ptr())
+        rows = time_calls(calls, args.launch_reps, T)
+        total = sum(r["ms"] * r["count"] for r in rows)
+        dom = max(rows, key=lambda r: r["ms"] * r["count"])
+        out["roofline"] = roofline_of(dom, total, out["config"]["workload"])
+        out["launches"] = [{k: r[k] for k in ("name", "layout", "shape", "ms", "count")} for r in rows]
+        out["launch_sum_ms"] = total
+        if not args.skip_cpu:
+            log("cpu baseline ...")
+            from oracle import nets as onets
+            from oracle import sample as osample
+
+            plan = recipe.network.plan(D)
+            p64 = params
+            spent, steps = 0.0, 0
+            while spent < args.cpu_seconds and steps < T:
+                x = obs_np[steps]
+                t1 = time.perf_counter()
+                head, value, _ = onets.forward(p64, plan, x)
+                k = make_key(5000 + steps)
+                if dist["kind"] == "categorical":
+                    osample.categorical_sample(head, k, 1.0)
+                elif dist.get("scale") is not None:
+                    osample.gaussian_sample(head, np.asarray(onets.get(p64, dist["scale"])), k, 1.0)
+                else:
+                    Dm = dist["dim"]
+                    osample.gaussian_sample(head[:, :Dm], head[:, Dm:], k, 1.0)
+                spent += time.perf_counter() - t1
+                steps += 1
+            try:
+                cores = len(os.sched_getaffinity(0))
+            except AttributeError:
+                cores = os.cpu_count()
+            threads = int(os.environ.get("OMP_NUM_THREADS", cores))
+            out["cpu_baseline"] = {"value": N * steps / spent, "unit": "samples/s", "cores": min(cores, threads),
+                                   "kind": "port",
+                                   "sample": f"oracle float64 numpy: {steps} steps of forward + sampling over "
+                                             f"{N} envs ({spent:.1f} s)"}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -344,6 +505,12 @@ def main():
     cls = RecurrentPPO if recipe.recurrent else PPO
     alg = cls(cfg=recipe.cfg, network=recipe.network, optimizer=recipe.optimizer, use_graph=not args.no_graph)
     state = alg.init_from_params({"params": params}, recipe.obs_dim)
+    if args.path == "step":
+        if recipe.recurrent:
+            print("bench.py --path step covers the MLP workloads (1, 2, 3, 5)", file=sys.stderr)
+            sys.exit(2)
+        step_main(args, recipe, alg, state, params, dev)
+        return
     tr = synthetic_rollout(recipe, params, dev, recipe.seed)
     torch.cuda.synchronize()
     log("rollout ready")
@@ -379,20 +546,7 @@ def main():
         rows = time_launches(ex, args.launch_reps, recipe.cfg.update_epochs * recipe.cfg.num_minibatches)
         total = sum(r["ms"] * r["count"] for r in rows)
         dom = max(rows, key=lambda r: r["ms"] * r["count"])
-        if dom["flops"] > 0:
-            achieved = dom["flops"] / (dom["ms"] * 1e-3) / 1e12
-            peak = PEAK["bf16_mfma"] if dom["name"] in ("ppo_gemm_bf16", "ppo_gemm_bf16s") else PEAK["fp32_mfma"]
-            roof = {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
-                    "frac": achieved / peak, "traffic": None}
-        else:
-            achieved = dom["bytes"] / (dom["ms"] * 1e-3) / 1e9
-            roof = {"bound": "hbm", "achieved": achieved, "peak": PEAK["hbm"], "unit": "GB/s",
-                    "frac": achieved / PEAK["hbm"], "traffic": None}
-        roof["kernel"] = f"{dom['name']} layout={dom['layout']} MNK={dom['shape']}"
-        roof["traffic"] = measured_traffic(out["config"]["workload"], roof["kernel"])
-        roof["avg_ms"] = dom["ms"]
-        roof["share_of_update"] = dom["ms"] * dom["count"] / total
-        out["roofline"] = roof
+        out["roofline"] = roofline_of(dom, total, out["config"]["workload"])
         out["launches"] = [{k: r[k] for k in ("name", "layout", "shape", "ms", "count")} for r in rows]
         out["launch_sum_ms"] = total
         if not args.skip_cpu:

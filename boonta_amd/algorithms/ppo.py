@@ -5,6 +5,9 @@ Mirrors boonta/algorithms/ppo.py:17-233: ``PPOConfig`` (:17-27), ``PPOState``
 advantage_estimator=generalized_advantage_estimator)`` with ``init`` (:45-55),
 ``step`` (:57-74) and ``update(state, key, transitions) -> state`` (:76-233).
 
+``step`` runs the network forward and the head's sample_and_log_prob as HIP
+kernels (see ``rollout.StepExecutor``).
+
 ``update`` runs bootstrap, GAE, the epoch permutations and every minibatch
 forward/backward/clip/Adam step as HIP kernels (see ``learner.MLPExecutor``);
 by default the whole update is captured once into a HIP graph per input
@@ -25,6 +28,7 @@ from ..flat import load_tree, tree_from_flat
 from ..learner import FlatState, MLPExecutor, Program
 from ..optim import EmptyState, ScaleByAdamState, as_chain
 from ..random import key_data
+from ..rollout import StepExecutor
 from .advantage_estimators import generalized_advantage_estimator
 
 
@@ -89,6 +93,7 @@ class PPO:
         self._programs: dict = {}
         self._executors: dict = {}
         self._graphs: dict = {}
+        self._steppers: dict = {}
 
     # ------------------------------------------------------------------ init
     def program(self, obs_dim: int) -> Program:
@@ -120,8 +125,42 @@ class PPO:
                         params={"params": tree_from_flat(lay, flat.P)}, optimizer_state=opt_state)
 
     # ------------------------------------------------------------------ step
+    def step_executor(self, state, rows: int, obs_dim: int) -> StepExecutor:
+        flat = flat_state_of(state)
+        k = (id(flat), rows, obs_dim)
+        if k not in self._steppers:
+            self._steppers[k] = StepExecutor(self.program(obs_dim), flat, rows)
+        return self._steppers[k]
+
     def step(self, state, carry, key, timestep, temperature: float = 1.0):
-        raise NotImplementedError("the rollout-side PPO.step is not compiled yet")
+        """Acts on ``timestep.obs`` [N, obs] (ppo.py:57-74): the network forward
+        with the current parameters, then ``dist.sample_and_log_prob(seed=key)``.
+        Returns (state, carry, action, {"log_prob": [N], "value": [N]}); action
+        is int32 [N] (categorical) or float32 [N, D] (Gaussian).  ``key`` is
+        key data (host or device) used as given, like the reference's seed."""
+        obs = timestep.obs
+        if (not isinstance(obs, torch.Tensor) or obs.dtype != torch.float32 or obs.dim() != 2
+                or not obs.is_contiguous() or not obs.is_cuda):
+            raise TypeError("timestep.obs must be a contiguous float32 [N, obs] device tensor")
+        N, obs_dim = (int(d) for d in obs.shape)
+        ex = self.step_executor(state, N, obs_dim)
+        if isinstance(key, torch.Tensor) and key.is_cuda:
+            if key.numel() != 2 or key.element_size() != 4:
+                raise ValueError("a device key must hold two 32-bit words")
+            ex.KEY.copy_(key.reshape(2).view(torch.int32))
+        else:
+            ex.KEY.copy_(torch.from_numpy(key_data(key).view(np.int32).copy()))
+        dev = ex.KEY.device
+        dist = ex.prog.dist
+        if dist["kind"] == "categorical":
+            action = torch.empty(N, dtype=torch.int32, device=dev)
+        else:
+            action = torch.empty(N, dist["dim"], dtype=torch.float32, device=dev)
+        log_prob = torch.empty(N, dtype=torch.float32, device=dev)
+        value = torch.empty(N, dtype=torch.float32, device=dev)
+        ex.issue(torch.cuda.current_stream().cuda_stream, obs.data_ptr(), obs_dim, float(temperature),
+                 action.data_ptr(), log_prob.data_ptr(), value.data_ptr())
+        return state, carry, action, {"log_prob": log_prob, "value": value}
 
     # ---------------------------------------------------------------- update
     @staticmethod

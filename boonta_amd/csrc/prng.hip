@@ -22,6 +22,7 @@
 // A bucket larger than the LDS capacity (not reachable for Threefry keys at
 // these sizes, but handled) is ranked by counting instead, which is exact.
 #include "common.h"
+#include "threefry.h"
 
 #include <algorithm>
 #include <math.h>
@@ -29,35 +30,13 @@
 
 namespace {
 
+using ppo::threefry2x32;
+
 constexpr int TILE = 4096;          // elements per histogram / scatter block
 constexpr int TILE_THREADS = 256;
 constexpr int BUCKET_CAP = 4096;    // elements a bucket sorts in LDS
 constexpr int SORT_THREADS = 512;
 constexpr int MAX_BUCKET_BITS = 12;
-
-__device__ __forceinline__ uint32_t rotl(uint32_t v, uint32_t r) {
-  return (v << r) | (v >> (32u - r));
-}
-
-__device__ __forceinline__ void threefry2x32(uint32_t k0, uint32_t k1, uint32_t& x0, uint32_t& x1) {
-  const uint32_t ks2 = k0 ^ k1 ^ 0x1BD11BDAu;
-  const uint32_t ks[3] = {k0, k1, ks2};
-  x0 += k0;
-  x1 += k1;
-#pragma unroll
-  for (uint32_t s = 1; s <= 5; ++s) {
-    const uint32_t r0 = (s & 1) ? 13u : 17u;
-    const uint32_t r1 = (s & 1) ? 15u : 29u;
-    const uint32_t r2 = (s & 1) ? 26u : 16u;
-    const uint32_t r3 = (s & 1) ? 6u : 24u;
-    x0 += x1; x1 = rotl(x1, r0); x1 ^= x0;
-    x0 += x1; x1 = rotl(x1, r1); x1 ^= x0;
-    x0 += x1; x1 = rotl(x1, r2); x1 ^= x0;
-    x0 += x1; x1 = rotl(x1, r3); x1 ^= x0;
-    x0 += ks[s % 3];
-    x1 += ks[(s + 1) % 3] + s;
-  }
-}
 
 // keys[2*i..2*i+1] = split(key, num)[i]
 __global__ void split_kernel(const uint32_t* __restrict__ key, uint32_t* __restrict__ out, int64_t num) {

@@ -242,7 +242,150 @@ class FlatState:
         return self.P.data_ptr() + 4 * (region.offset + col)
 
 
-class MLPExecutor:
+def forward_bufs(spec: LayerSpec, rows: int, device) -> LayerBufs:
+    """Forward-only buffers of one layer on ``rows`` rows: its output, and what
+    the forward keeps (pre-LayerNorm values and statistics, pre-SiLU values)."""
+    f32 = dict(dtype=torch.float32, device=device)
+    b = LayerBufs(spec, Y=torch.zeros(rows, spec.ld, **f32))
+    if spec.ln is not None:
+        b.Z = torch.zeros(rows, spec.ld, **f32)
+        b.mean = torch.zeros(rows, **f32)
+        b.rstd = torch.zeros(rows, **f32)
+    elif spec.act == "silu":
+        b.PRE = torch.zeros(rows, spec.ld, **f32)
+    return b
+
+
+SPLIT_FWD_MIN_K = 1024  # a bf16 Dense reading an fp32 input this wide runs split-K
+
+
+def split_forward_bufs(lb: LayerBufs, rows: int, device, bf16: bool) -> None:
+    """Gives a group's first layer the fp32 partials of a split-K forward when
+    it is a bf16 Dense with a long reduction over an fp32 input (the
+    large-observation bootstrap and rollout step: few row tiles, so the
+    reduction is what fills the chip)."""
+    d = lb.spec.dense
+    if not bf16 or d.fin < SPLIT_FWD_MIN_K or d.fin % 4 or lb.spec.ld % 4:
+        return
+    tiles = math.ceil(rows / 128) * math.ceil(lb.spec.ld / 128)
+    S = max(1, min(math.ceil(256 / tiles), d.fin // 512, 16))
+    # every split must own part of the reduction (64-element stages)
+    while S > 1 and (S - 1) * (math.ceil(math.ceil(d.fin / S) / 64) * 64) >= d.fin:
+        S -= 1
+    if S > 1:
+        lb.fpart = torch.zeros(S, rows, lb.spec.ld, dtype=torch.float32, device=device)
+
+
+class ForwardChain:
+    """Issues the forward of Dense[+LayerNorm][+act] layer groups through the
+    C ABI (fp32 MFMA, or the bf16 GEMMs with flax's casts for a bf16 network).
+    The learner's executors and the rollout step share it."""
+
+    def __init__(self, program: "Program", flat: "FlatState"):
+        self._call = _lib.call
+        self.prog = program
+        self.bf16 = program.bf16
+        self._ln_fwd = "ppo_layernorm_act_fwd_bf16" if self.bf16 else "ppo_layernorm_act_fwd_f32"
+        self._ln_bwd = "ppo_layernorm_act_bwd_bf16" if self.bf16 else "ppo_layernorm_act_bwd_f32"
+        self.flat = flat
+        self.obs16 = False
+        self.mb = -1
+        self.inp: dict = {}
+
+    def _gemm(self, st, a_layout, b_layout, A, lda, rows, B, ldb, C, ldc, M, N, K, splits, stride, epi, bias, act,
+              pre, aux, ldaux, bias_grad, tile):
+        """One Dense contraction: fp32 MFMA, or for a bf16-compute network the
+        bf16 MFMA GEMM with flax's casts (operands rounded to bf16 as read; the
+        forward and input-cotangent results rounded to bf16; dW partials kept
+        fp32 and rounded after their sum)."""
+        if not self.bf16:
+            self._call("ppo_gemm_f32", st, a_layout, b_layout, A, lda, rows, B, ldb, C, ldc, M, N, K, splits, stride,
+                       epi, bias, act, pre, aux, ldaux, bias_grad, tile)
+            return
+        if pre is not None:
+            raise NotImplementedError("a bf16 Dense with a SiLU activation and no LayerNorm is not compiled")
+        round_out = 0 if a_layout == A_COL else 1
+        self._call("ppo_gemm_bf16", st, a_layout, b_layout, A, lda, rows, B, ldb, C, ldc, M, N, K, splits, stride, epi,
+                   bias, act, round_out, aux, ldaux, bias_grad, tile)
+
+    def _reads_obs16(self, x, rows_idx, row0) -> bool:
+        """True for the first layer of a minibatch pass over the observation
+        (gathered rows of inputs["obs"]), which then reads the bf16 copy."""
+        return self.obs16 and rows_idx is not None and row0 == 0 and x == self.inp["obs"]
+
+    def _y16_input(self, layers, li, nrows, row0) -> bool:
+        """True when layer li of a training group reads the bf16 output of
+        layer li - 1 (minibatch passes of a bf16 network)."""
+        return (li > 0 and row0 == 0 and nrows == self.mb and layers[li - 1].Y16 is not None
+                and layers[li].spec.dense.w.ld % 8 == 0)
+
+    def _ln_forward(self, st, lb, o, row0, nrows):
+        s = lb.spec
+        scale, bias = self.flat.view(s.ln["scale"]), self.flat.view(s.ln["bias"])
+        if lb.Y16 is not None and row0 == 0 and nrows == self.mb:
+            self._call("ppo_layernorm_act_fwd_bf16_out16", st, _p(lb.Z), s.ld, scale, bias, _p(lb.Y), s.ld,
+                       _p(lb.Y16), s.ld, _p(lb.mean), _p(lb.rstd), nrows, s.fout, s.ln["eps"], _act(s.act))
+        else:
+            self._call(self._ln_fwd, st, _p(lb.Z) + o, s.ld, scale, bias, _p(lb.Y) + o, s.ld, _p(lb.mean) + 4 * row0,
+                       _p(lb.rstd) + 4 * row0, nrows, s.fout, s.ln["eps"], _act(s.act))
+
+    def _view16(self, region: Region) -> int:
+        """Address of a parameter region in the bf16 parameter image."""
+        return _p(self.P16) + 2 * region.offset
+
+    def _fwd_layers(self, st, layers, x, ldx, rows_idx, nrows, row0=0):
+        """Forward of Dense[+LayerNorm][+act] layers on nrows rows, writing
+        each layer's buffers from row ``row0`` on."""
+        for li, lb in enumerate(layers):
+            s = lb.spec
+            d = s.dense
+            W = self.flat.view(d.w)
+            Bb = self.flat.view(d.b) if d.b is not None else None
+            o = 4 * row0 * s.ld
+            if li == 0 and self._reads_obs16(x, rows_idx, row0):
+                dst = lb.Z if s.ln is not None else lb.Y
+                self._call("ppo_gemm_bf16s", st, A_ROW, B_KN, 1, 1, _p(self.OBS16), self.ldo16, rows_idx,
+                           self._view16(d.w), d.w.ld, _p(lb.fpart), s.ld, nrows, s.ld, d.fin, self.FWD16_SPLITS,
+                           nrows * s.ld, EPI_STORE, None, 0, 0, None, 0, None, self.FWD16_TILE)
+                self._call("ppo_splits_bias_act_bf16", st, _p(lb.fpart), s.ld, nrows * s.ld, self.FWD16_SPLITS, Bb,
+                           _act(s.act) if s.ln is None else 0, _p(dst), s.ld, nrows, s.ld)
+                if s.ln is not None:
+                    self._ln_forward(st, lb, o, row0, nrows)
+            elif (li == 0 and lb.fpart is not None and rows_idx is None and row0 == 0 and self.bf16
+                  and x % 16 == 0 and ldx % 4 == 0 and nrows <= lb.fpart.shape[1]):
+                # bf16 Dense on an fp32 input: split-K partials on the pipelined
+                # GEMM (operands rounded to bf16 as staged), summed in split
+                # order with flax's bf16 bias add and activation
+                S = lb.fpart.shape[0]
+                dst = lb.Z if s.ln is not None else lb.Y
+                self._call("ppo_gemm_bf16s", st, A_ROW, B_KN, 0, 0, x, ldx, None, W, d.w.ld, _p(lb.fpart), s.ld,
+                           nrows, s.ld, d.fin, S, lb.fpart.shape[1] * s.ld, EPI_STORE, None, 0, 0, None, 0, None,
+                           -1)
+                self._call("ppo_splits_bias_act_bf16", st, _p(lb.fpart), s.ld, lb.fpart.shape[1] * s.ld, S, Bb,
+                           _act(s.act) if s.ln is None else 0, _p(dst), s.ld, nrows, s.ld)
+                if s.ln is not None:
+                    self._ln_forward(st, lb, o, row0, nrows)
+            elif self._y16_input(layers, li, nrows, row0):
+                prev = layers[li - 1]
+                dst = lb.Z if s.ln is not None else lb.Y
+                self._call("ppo_gemm_bf16s", st, A_ROW, B_KN, 1, 1, _p(prev.Y16), prev.spec.ld, None,
+                           self._view16(d.w), d.w.ld, _p(dst), s.ld, nrows, s.ld, d.fin, 1, 0, EPI_BIAS_ACT, Bb,
+                           _act(s.act) if s.ln is None else 0, 1, None, 0, None, -1)
+                if s.ln is not None:
+                    self._ln_forward(st, lb, o, row0, nrows)
+            elif s.ln is not None:
+                self._gemm(st, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(lb.Z) + o, s.ld, nrows,
+                          s.ld, d.fin, 1, 0, EPI_BIAS_ACT, Bb, 0, None, None, 0, None, -1)
+                self._ln_forward(st, lb, o, row0, nrows)
+            else:
+                pre = _p(lb.PRE) + o if lb.PRE is not None else None
+                self._gemm(st, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(lb.Y) + o, s.ld, nrows,
+                          s.ld, d.fin, 1, 0, EPI_BIAS_ACT, Bb, _act(s.act), pre, None, 0, None, -1)
+            x, ldx, rows_idx = _p(lb.Y) + o, s.ld, None
+        return x, ldx, rows_idx
+
+
+class MLPExecutor(ForwardChain):
     """One compiled PPO.update for fixed (T, N, obs, minibatches, epochs)."""
 
     FWD16_SPLITS = 2  # K splits of the bf16 first-layer forward (512 workgroups of 128 x 128 at 8192 x 512)
@@ -254,12 +397,7 @@ class MLPExecutor:
     def __init__(self, program: Program, flat: FlatState, cfg, chain, T: int, N: int):
         if program.gru is not None and type(self) is MLPExecutor:
             raise TypeError("a recurrent program runs on RecurrentExecutor")
-        self._call = _lib.call
-        self.prog = program
-        self.bf16 = program.bf16
-        self._ln_fwd = "ppo_layernorm_act_fwd_bf16" if self.bf16 else "ppo_layernorm_act_fwd_f32"
-        self._ln_bwd = "ppo_layernorm_act_bwd_bf16" if self.bf16 else "ppo_layernorm_act_bwd_f32"
-        self.flat = flat
+        ForwardChain.__init__(self, program, flat)
         self.cfg = cfg
         self.chain = chain
         self.T, self.N = T, N
@@ -277,13 +415,7 @@ class MLPExecutor:
 
         def layer_bufs(spec: LayerSpec, rows: int, train: bool) -> LayerBufs:
             ld = spec.ld
-            b = LayerBufs(spec, Y=torch.zeros(rows, ld, **f32))
-            if spec.ln is not None:
-                b.Z = torch.zeros(rows, ld, **f32)
-                b.mean = torch.zeros(rows, **f32)
-                b.rstd = torch.zeros(rows, **f32)
-            elif spec.act == "silu":
-                b.PRE = torch.zeros(rows, ld, **f32)
+            b = forward_bufs(spec, rows, dev)
             if train:
                 b.dZ = torch.zeros(rows, ld, **f32)
                 if spec.ln is not None:
@@ -333,6 +465,8 @@ class MLPExecutor:
                         lb.bpart = torch.zeros(lb.splits, lb.spec.ld, **f32)
         self.boot_layers = [layer_bufs(s, self._boot_rows(), False) for s in
                             (program.trunk if program.shared_head else program.critic_layers)]
+        if self.boot_layers and program.gru is None:
+            split_forward_bufs(self.boot_layers[0], self._boot_rows(), dev, self.bf16)
         ha, hc = program.head_a, program.head_c
         lib = _lib.load()
         self.fused = self._can_fuse(program)
@@ -473,22 +607,6 @@ class MLPExecutor:
         self.segments = segs
 
     # ------------------------------------------------------------- pieces
-    def _gemm(self, st, a_layout, b_layout, A, lda, rows, B, ldb, C, ldc, M, N, K, splits, stride, epi, bias, act,
-              pre, aux, ldaux, bias_grad, tile):
-        """One Dense contraction: fp32 MFMA, or for a bf16-compute network the
-        bf16 MFMA GEMM with flax's casts (operands rounded to bf16 as read; the
-        forward and input-cotangent results rounded to bf16; dW partials kept
-        fp32 and rounded after their sum)."""
-        if not self.bf16:
-            self._call("ppo_gemm_f32", st, a_layout, b_layout, A, lda, rows, B, ldb, C, ldc, M, N, K, splits, stride,
-                       epi, bias, act, pre, aux, ldaux, bias_grad, tile)
-            return
-        if pre is not None:
-            raise NotImplementedError("a bf16 Dense with a SiLU activation and no LayerNorm is not compiled")
-        round_out = 0 if a_layout == A_COL else 1
-        self._call("ppo_gemm_bf16", st, a_layout, b_layout, A, lda, rows, B, ldb, C, ldc, M, N, K, splits, stride, epi,
-                   bias, act, round_out, aux, ldaux, bias_grad, tile)
-
     def _normalize(self, st):
         """Advantage normalisation over the whole rollout (ppo.py:220-221)."""
         if self.cfg.normalize_advantage:
@@ -502,68 +620,6 @@ class MLPExecutor:
     def _boot_rows(self) -> int:
         """Rows of the bootstrap forward: second.obs[-1] (ppo.py:208-212)."""
         return self.N
-
-    def _reads_obs16(self, x, rows_idx, row0) -> bool:
-        """True for the first layer of a minibatch pass over the observation
-        (gathered rows of inputs["obs"]), which then reads the bf16 copy."""
-        return self.obs16 and rows_idx is not None and row0 == 0 and x == self.inp["obs"]
-
-    def _y16_input(self, layers, li, nrows, row0) -> bool:
-        """True when layer li of a training group reads the bf16 output of
-        layer li - 1 (minibatch passes of a bf16 network)."""
-        return (li > 0 and row0 == 0 and nrows == self.mb and layers[li - 1].Y16 is not None
-                and layers[li].spec.dense.w.ld % 8 == 0)
-
-    def _ln_forward(self, st, lb, o, row0, nrows):
-        s = lb.spec
-        scale, bias = self.flat.view(s.ln["scale"]), self.flat.view(s.ln["bias"])
-        if lb.Y16 is not None and row0 == 0 and nrows == self.mb:
-            self._call("ppo_layernorm_act_fwd_bf16_out16", st, _p(lb.Z), s.ld, scale, bias, _p(lb.Y), s.ld,
-                       _p(lb.Y16), s.ld, _p(lb.mean), _p(lb.rstd), nrows, s.fout, s.ln["eps"], _act(s.act))
-        else:
-            self._call(self._ln_fwd, st, _p(lb.Z) + o, s.ld, scale, bias, _p(lb.Y) + o, s.ld, _p(lb.mean) + 4 * row0,
-                       _p(lb.rstd) + 4 * row0, nrows, s.fout, s.ln["eps"], _act(s.act))
-
-    def _view16(self, region: Region) -> int:
-        """Address of a parameter region in the bf16 parameter image."""
-        return _p(self.P16) + 2 * region.offset
-
-    def _fwd_layers(self, st, layers, x, ldx, rows_idx, nrows, row0=0):
-        """Forward of Dense[+LayerNorm][+act] layers on nrows rows, writing
-        each layer's buffers from row ``row0`` on."""
-        for li, lb in enumerate(layers):
-            s = lb.spec
-            d = s.dense
-            W = self.flat.view(d.w)
-            Bb = self.flat.view(d.b) if d.b is not None else None
-            o = 4 * row0 * s.ld
-            if li == 0 and self._reads_obs16(x, rows_idx, row0):
-                dst = lb.Z if s.ln is not None else lb.Y
-                self._call("ppo_gemm_bf16s", st, A_ROW, B_KN, 1, 1, _p(self.OBS16), self.ldo16, rows_idx,
-                           self._view16(d.w), d.w.ld, _p(lb.fpart), s.ld, nrows, s.ld, d.fin, self.FWD16_SPLITS,
-                           nrows * s.ld, EPI_STORE, None, 0, 0, None, 0, None, self.FWD16_TILE)
-                self._call("ppo_splits_bias_act_bf16", st, _p(lb.fpart), s.ld, nrows * s.ld, self.FWD16_SPLITS, Bb,
-                           _act(s.act) if s.ln is None else 0, _p(dst), s.ld, nrows, s.ld)
-                if s.ln is not None:
-                    self._ln_forward(st, lb, o, row0, nrows)
-            elif self._y16_input(layers, li, nrows, row0):
-                prev = layers[li - 1]
-                dst = lb.Z if s.ln is not None else lb.Y
-                self._call("ppo_gemm_bf16s", st, A_ROW, B_KN, 1, 1, _p(prev.Y16), prev.spec.ld, None,
-                           self._view16(d.w), d.w.ld, _p(dst), s.ld, nrows, s.ld, d.fin, 1, 0, EPI_BIAS_ACT, Bb,
-                           _act(s.act) if s.ln is None else 0, 1, None, 0, None, -1)
-                if s.ln is not None:
-                    self._ln_forward(st, lb, o, row0, nrows)
-            elif s.ln is not None:
-                self._gemm(st, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(lb.Z) + o, s.ld, nrows,
-                          s.ld, d.fin, 1, 0, EPI_BIAS_ACT, Bb, 0, None, None, 0, None, -1)
-                self._ln_forward(st, lb, o, row0, nrows)
-            else:
-                pre = _p(lb.PRE) + o if lb.PRE is not None else None
-                self._gemm(st, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(lb.Y) + o, s.ld, nrows,
-                          s.ld, d.fin, 1, 0, EPI_BIAS_ACT, Bb, _act(s.act), pre, None, 0, None, -1)
-            x, ldx, rows_idx = _p(lb.Y) + o, s.ld, None
-        return x, ldx, rows_idx
 
     def _dx_target(self, lb: LayerBufs):
         """(dst, epi, act, aux, ldaux) for the cotangent of layer lb's output."""

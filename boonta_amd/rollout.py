@@ -1,0 +1,101 @@
+"""The rollout-side ``PPO.step`` on MI355X kernels (boonta/algorithms/ppo.py:57-74).
+
+``StepExecutor`` binds an MLP program to a number of environments and issues,
+on one stream:
+
+    network forward on timestep.obs [rows, obs]     network.py:18-49 (shared
+        trunk or separate actor / critic towers, as in the learner)
+    head GEMMs -> logits or mean, and the value column
+    sample_and_log_prob(seed=key)                   distributions.py:8-57
+        (``ppo_sample_categorical_f32`` / ``ppo_sample_gaussian_f32``)
+
+The forward reuses the learner's kernels (``ForwardChain``) and reads the
+same flat parameter buffer, so a step issued after an update sees the updated
+parameters without a copy.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .learner import (A_ROW, B_KN, EPI_BIAS_ACT, DenseSpec, FlatState, ForwardChain, Program, _p, forward_bufs,
+                      split_forward_bufs)
+
+
+class StepExecutor(ForwardChain):
+    """PPO.step for a fixed number of environments (rows)."""
+
+    def __init__(self, program: Program, flat: FlatState, rows: int):
+        if program.gru is not None:
+            raise TypeError("a recurrent program steps through RecurrentPPO")
+        super().__init__(program, flat)
+        lib = _lib.load()
+        if program.action_dim > lib.ppo_sample_max_outputs():
+            raise NotImplementedError(f"an action dimension above {lib.ppo_sample_max_outputs()} is not compiled")
+        dev = flat.device
+        self.rows = rows
+        self.trunk = [forward_bufs(s, rows, dev) for s in program.trunk]
+        self.actor = [forward_bufs(s, rows, dev) for s in program.actor_layers]
+        self.critic = [forward_bufs(s, rows, dev) for s in program.critic_layers]
+        for group in (self.trunk, self.actor, self.critic):
+            if group:
+                split_forward_bufs(group[0], rows, dev, self.bf16)
+        f32 = dict(dtype=torch.float32, device=dev)
+        ha, hc = program.head_a, program.head_c
+        if program.shared_head:
+            self.HEAD = torch.zeros(rows, ha.w.ld, **f32)
+        else:
+            self.HA = torch.zeros(rows, ha.w.ld, **f32)
+            self.HC = torch.zeros(rows, hc.w.ld, **f32)
+        self.KEY = torch.zeros(2, dtype=torch.int32, device=dev)
+
+    def _head(self, st, x, ldx, h: DenseSpec, out: torch.Tensor):
+        """Head Dense on the last features (bias added, no activation)."""
+        self._gemm(st, A_ROW, B_KN, x, ldx, None, self.flat.view(h.w), h.w.ld, _p(out), h.w.ld, self.rows,
+                   h.w.ld, h.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(h.b) if h.b is not None else None, 0, None,
+                   None, 0, None, -1)
+
+    def issue(self, st: int, obs: int, ldo: int, temperature: float, action: int, log_prob: int, value: int,
+              key: int | None = None):
+        """Enqueues one step on stream handle ``st``: obs is a device pointer
+        to [rows, ldo] float32; action [rows] int32 (categorical) or [rows, D]
+        float32 (Gaussian), log_prob and value [rows] float32; key a device
+        pointer to uint32[2] key data (default: this executor's KEY buffer)."""
+        key = _p(self.KEY) if key is None else key
+        prog = self.prog
+        rows = self.rows
+        if prog.shared_head:
+            x, ldx, _ = self._fwd_layers(st, self.trunk, obs, ldo, None, rows)
+            self._head(st, x, ldx, prog.head_a, self.HEAD)
+            head, ldh = self.HEAD, self.HEAD.shape[1]
+            vsrc, ldv = _p(self.HEAD) + 4 * prog.head_out, ldh
+        else:
+            xa, lda, _ = self._fwd_layers(st, self.actor, obs, ldo, None, rows)
+            self._head(st, xa, lda, prog.head_a, self.HA)
+            xc, ldc, _ = self._fwd_layers(st, self.critic, obs, ldo, None, rows)
+            self._head(st, xc, ldc, prog.head_c, self.HC)
+            head, ldh = self.HA, self.HA.shape[1]
+            vsrc, ldv = _p(self.HC), self.HC.shape[1]
+        dist = prog.dist
+        if dist["kind"] == "categorical":
+            self._call("ppo_sample_categorical_f32", st, _p(head), ldh, rows, dist["num"], vsrc, ldv, key,
+                       float(temperature), action, log_prob, value)
+        else:
+            D = dist["dim"]
+            if prog.scale_region is not None:
+                scale, lds = self.flat.view(prog.scale_region), 0
+            else:
+                scale, lds = _p(head) + 4 * D, ldh
+            self._call("ppo_sample_gaussian_f32", st, _p(head), ldh, scale, lds, rows, D, vsrc, ldv, key,
+                       float(temperature), action, D, log_prob, value)
+
+    def record(self, *issue_args) -> list:
+        """The launch sequence of one step as (entry point, args) without
+        running it (used by the benchmark to time single launches)."""
+        calls = []
+        self._call = lambda name, *args: calls.append((name, args))
+        try:
+            self.issue(0, *issue_args)
+        finally:
+            self._call = _lib.call
+        return calls

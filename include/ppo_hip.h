@@ -82,6 +82,28 @@ size_t ppo_epoch_permutations_workspace(int epochs, int64_t n);
 int ppo_epoch_permutations(void* stream, const uint32_t* key, int epochs, int64_t n, int32_t* out,
                            void* workspace, size_t workspace_bytes);
 
+/* -------------------------------------------------------------- sampling
+ * Replace dist.sample_and_log_prob(seed=key) in the rollout-side PPO.step
+ * (boonta/algorithms/ppo.py:57-74) for boonta's categorical head
+ * (networks/distributions.py:8-23: log_softmax of preferences / temperature,
+ * Gumbel-max draw of jax.random.gumbel(key, (1, rows, A)), greedy one-hot at
+ * temperature <= 0) and diagonal Gaussian head (distributions.py:42-57:
+ * sigma = temperature * (softplus(s) + 1e-3), eps = jax.random.normal(key,
+ * (1, rows, D)), action = sigma * eps + mean).  key: device uint32[2] key data,
+ * used as given (no split).  value (may be NULL) receives value_src[r * ldv],
+ * the critic column (remove_feature_axis, utils/axis.py:11-12).  A and D are at
+ * most ppo_sample_max_outputs(). */
+int ppo_sample_max_outputs(void);
+int ppo_sample_categorical_f32(void* stream, const float* pref, int64_t ldp, int rows, int A,
+                               const float* value_src, int64_t ldv, const uint32_t* key, float temperature,
+                               int32_t* action, float* log_prob, float* value);
+/* scale_raw: the raw scale s, [rows, lds] per row (state-dependent head: the
+ * second half of the head outputs), or one [D] vector when lds == 0
+ * (state-independent SpreadScale parameter). */
+int ppo_sample_gaussian_f32(void* stream, const float* mean, int64_t ldm, const float* scale_raw, int64_t lds,
+                            int rows, int D, const float* value_src, int64_t ldv, const uint32_t* key,
+                            float temperature, float* action, int64_t lda, float* log_prob, float* value);
+
 /* ------------------------------------------------------------------ GEMM
  * Dense layers of the torso and heads (flax.linen.Dense as composed in
  * hangar/recipes/*.py; forward at boonta/networks/network.py:38-49, backward

@@ -44,3 +44,12 @@ def test_argument_errors_are_reported_not_launched():
     assert rc == -1
     assert lib.ppo_adam_clip_f32(None, None, None, None, None, None, 6, None, 0, 0.5, 1e-3, 0.9, 0.999, 1e-8,
                                  None, 0) == -1
+
+
+def test_sampling_rejects_unsupported_sizes_without_launching():
+    lib = _lib.load()
+    big = lib.ppo_sample_max_outputs() + 1
+    assert lib.ppo_sample_categorical_f32(None, 1, big, 4, big, None, 0, 1, 1.0, 1, 1, None) == -1
+    assert b"ppo_sample_categorical_f32" in lib.ppo_last_error()
+    assert lib.ppo_sample_gaussian_f32(None, 1, big, 1, 0, 4, big, None, 0, 1, 1.0, 1, big, 1, None) == -1
+    assert lib.ppo_sample_categorical_f32(None, 1, 6, 4, 6, None, 0, None, 1.0, 1, 1, None) == -1

@@ -1,0 +1,200 @@
+"""Parity of the rollout-side PPO.step (boonta/algorithms/ppo.py:57-74) and
+its sampling kernels against the oracle (oracle/sample.py, oracle/nets.py) on
+the same seeded inputs, and the replay invariant of the reference's
+tests/test_algorithms.py:343-366: an update whose optimizer does not move the
+parameters recomputes exactly the log-probabilities its rollout acted on.
+
+Tolerances (written here):
+- sampled categorical actions bit-exact wherever the oracle's two largest
+  perturbed logits differ by more than 1e-4 (fp32; 2e-2, about two bf16
+  rounding steps of a unit logit, for the bf16 network), and at least 90 % of
+  rows must qualify;
+- log-probabilities and values 1e-5 relative (atol 1e-5) in fp32, 2e-2 for
+  the bf16 network;
+- Gaussian actions 1e-5 relative to |sigma eps| + |mean| (atol 1e-6): the
+  float32 erfinv (Giles' polynomial) against scipy's float64 erfinv;
+- replay: |approximate KL| <= 1e-6 and clip fraction 0 in every step.
+"""
+import numpy as np
+import pytest
+import torch
+
+from boonta_amd import _lib, optim, recipes, synthetic
+from boonta_amd.algorithms.ppo import PPO, flat_state_of
+from boonta_amd.random import key as make_key
+from boonta_amd.types import Timestep, Transition
+from oracle import nets, sample
+from ppo_cases import gpu_algorithm
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def key_dev(k):
+    return dev(np.asarray(k, np.uint32).view(np.int32))
+
+
+def log_softmax64(x):
+    x = np.asarray(x, np.float64)
+    s = x - x.max(-1, keepdims=True)
+    return s - np.log(np.exp(s).sum(-1, keepdims=True))
+
+
+def check_categorical(act, lp, pref, key, temperature, margin_tol, rtol):
+    a_or, _, margin = sample.categorical_sample(pref, key, temperature)
+    ok = margin > margin_tol
+    assert ok.mean() > 0.9
+    np.testing.assert_array_equal(act[ok], a_or[ok])
+    assert act.min() >= 0 and act.max() < pref.shape[1]
+    rows = np.arange(len(act))
+    if temperature > 0:
+        want = log_softmax64(np.asarray(pref, np.float64) / temperature)[rows, act]
+    else:
+        want = np.where(act == np.argmax(pref, -1), 0.0, -np.inf)
+    np.testing.assert_allclose(lp, want, rtol=rtol, atol=rtol)
+
+
+@pytest.mark.parametrize("A", [1, 2, 6, 43, 128])
+@pytest.mark.parametrize("temperature", [1.0, 0.5, 0.0])
+def test_categorical_kernel_matches_the_oracle(A, temperature):
+    rng = np.random.default_rng(A)
+    rows, ld = 1000, A + 3
+    buf = rng.standard_normal((rows, ld)).astype(np.float32) * 2
+    pref = buf[:, :A]
+    key = make_key(31 + A)
+    d = dev(buf)
+    act = torch.empty(rows, dtype=torch.int32, device="cuda")
+    lp = torch.empty(rows, dtype=torch.float32, device="cuda")
+    val = torch.empty(rows, dtype=torch.float32, device="cuda")
+    _lib.call("ppo_sample_categorical_f32", stream(), d.data_ptr(), ld, rows, A, d.data_ptr() + 4 * A, ld,
+              key_dev(key).data_ptr(), temperature, act.data_ptr(), lp.data_ptr(), val.data_ptr())
+    torch.cuda.synchronize()
+    check_categorical(act.cpu().numpy(), lp.cpu().numpy(), pref, key, temperature, 1e-4, 1e-5)
+    np.testing.assert_array_equal(val.cpu().numpy(), buf[:, A])
+
+
+@pytest.mark.parametrize("D", [1, 8, 17])
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("temperature", [1.0, 0.5])
+def test_gaussian_kernel_matches_the_oracle(D, per_row, temperature):
+    rng = np.random.default_rng(100 + D)
+    rows, ld = 3000, 2 * D + 1
+    buf = rng.standard_normal((rows, ld)).astype(np.float32)
+    vec = rng.standard_normal(D).astype(np.float32)
+    mean = buf[:, :D]
+    raw = buf[:, D:2 * D] if per_row else vec
+    key = make_key(7 * D + int(per_row))
+    d, v = dev(buf), dev(vec)
+    act = torch.empty(rows, D, dtype=torch.float32, device="cuda")
+    lp = torch.empty(rows, dtype=torch.float32, device="cuda")
+    val = torch.empty(rows, dtype=torch.float32, device="cuda")
+    scale, lds = (d.data_ptr() + 4 * D, ld) if per_row else (v.data_ptr(), 0)
+    _lib.call("ppo_sample_gaussian_f32", stream(), d.data_ptr(), ld, scale, lds, rows, D, d.data_ptr() + 8 * D,
+              ld, key_dev(key).data_ptr(), temperature, act.data_ptr(), D, lp.data_ptr(), val.data_ptr())
+    torch.cuda.synchronize()
+    a_or, lp_or, eps = sample.gaussian_sample(mean, raw, key, temperature)
+    sig = temperature * (sample.softplus(np.broadcast_to(raw, mean.shape)) + 1e-3)
+    a = act.cpu().numpy()
+    np.testing.assert_array_less(np.abs(a - a_or), 1e-5 * (np.abs(sig * eps) + np.abs(mean)) + 1e-6)
+    np.testing.assert_allclose(lp.cpu().numpy(), lp_or, rtol=1e-5, atol=1e-5)
+    np.testing.assert_array_equal(val.cpu().numpy(), buf[:, 2 * D])
+
+
+STEP_CASES = {
+    "c1-tiny": dict(config=1, N=64),
+    "c2-anakin": dict(config=2, N=512),
+    "c3-gaussian": dict(config=3, N=512),
+    "c5-bf16": dict(config=5, N=512),
+}
+
+
+@pytest.mark.parametrize("name", list(STEP_CASES))
+@pytest.mark.parametrize("temperature", [1.0, 0.5])
+def test_step_matches_the_oracle(name, temperature):
+    case = STEP_CASES[name]
+    r = recipes.make(case["config"]).resized(N=case["N"])
+    N, D = r.N, r.obs_dim
+    plan = r.network.plan(D)
+    params = r.network.init(0, D)["params"]
+    obs = synthetic.rollout(r, T=1, N=N)["obs"][0]
+    head, value, _ = nets.forward(params, plan, obs)
+    alg = gpu_algorithm(r, use_graph=False)
+    state = alg.init_from_params({"params": params}, D)
+    key = make_key(2024)
+    _, carry, action, aux = alg.step(state, None, key, Timestep(obs=dev(obs)), temperature=temperature)
+    torch.cuda.synchronize()
+    assert carry is None
+    bf16 = plan.get("compute_dtype") == "bfloat16"
+    rtol = 2e-2 if bf16 else 1e-5
+    np.testing.assert_allclose(aux["value"].cpu().numpy(), value, rtol=rtol, atol=rtol)
+    dist = plan["dist"]
+    if dist["kind"] == "categorical":
+        check_categorical(action.cpu().numpy(), aux["log_prob"].cpu().numpy(), head, key, temperature,
+                          2e-2 if bf16 else 1e-4, rtol)
+    else:
+        Dm = dist["dim"]
+        if dist.get("scale") is not None:
+            mean, raw = head, np.asarray(nets.get(params, dist["scale"]), np.float64)
+        else:
+            mean, raw = head[:, :Dm], head[:, Dm:]
+        a_or, lp_or, eps = sample.gaussian_sample(mean, raw, key, temperature)
+        sig = temperature * (sample.softplus(np.broadcast_to(raw, mean.shape)) + 1e-3)
+        a = action.cpu().numpy()
+        assert a.shape == (N, Dm)
+        np.testing.assert_array_less(np.abs(a - a_or), 1e-5 * (np.abs(sig * eps) + np.abs(mean)) + 1e-5)
+        np.testing.assert_allclose(aux["log_prob"].cpu().numpy(), lp_or, rtol=rtol, atol=rtol)
+
+
+def test_step_takes_a_device_key_and_follows_the_updated_parameters():
+    r = recipes.make(2).resized(N=256)
+    D = r.obs_dim
+    params = r.network.init(3, D)["params"]
+    obs = synthetic.rollout(r, T=1, N=r.N)["obs"][0]
+    alg = gpu_algorithm(r, use_graph=False)
+    state = alg.init_from_params({"params": params}, D)
+    key = make_key(9)
+    o = dev(obs)
+    _, _, a1, x1 = alg.step(state, None, key, Timestep(obs=o))
+    _, _, a2, x2 = alg.step(state, None, key_dev(key), Timestep(obs=o))
+    torch.cuda.synchronize()
+    assert torch.equal(a1, a2) and torch.equal(x1["log_prob"], x2["log_prob"])
+    # parameters changed in place are seen by the next step (one flat buffer)
+    flat_state_of(state).P.add_(0.01)
+    _, _, a3, x3 = alg.step(state, None, key, Timestep(obs=o))
+    torch.cuda.synchronize()
+    assert not torch.equal(x1["value"], x3["value"])
+
+
+@pytest.mark.parametrize("config", [1, 2, 3])
+def test_update_replays_what_step_acted_on(config):
+    """tests/test_algorithms.py:343-366: with an optimizer that leaves the
+    parameters where they are, every minibatch's recomputed log-probabilities
+    equal the rollout's (KL 0, nothing clipped)."""
+    r = recipes.make(config).resized(T=8, N=64, num_minibatches=4, update_epochs=2)
+    T, N, D = r.T, r.N, r.obs_dim
+    roll = synthetic.rollout(r, T, N)
+    alg = PPO(cfg=r.cfg, network=r.network, optimizer=optim.chain(optim.clip_by_global_norm(0.5), optim.adam(0.0)))
+    obs = dev(roll["obs"])
+    state, _ = alg.init(make_key(0), Timestep(obs=obs[0]))
+    actions, lps, values = [], [], []
+    for t in range(T):
+        _, _, a, aux = alg.step(state, None, make_key(100 + t), Timestep(obs=obs[t].contiguous()))
+        actions.append(a)
+        lps.append(aux["log_prob"])
+        values.append(aux["value"])
+    second = Timestep(obs=obs[1:], action=torch.stack(actions), reward=dev(roll["reward"]),
+                      terminated=dev(roll["terminated"]), truncated=dev(roll["truncated"]))
+    trans = Transition(first=Timestep(obs=obs[:-1]), second=second,
+                       aux={"log_prob": torch.stack(lps), "value": torch.stack(values)})
+    alg.update(state, make_key(5), trans)
+    torch.cuda.synchronize()
+    logs = alg.logs(state, T, N, D)
+    assert np.all(np.abs(logs["actor/approximate_kl"]) <= 1e-6), logs["actor/approximate_kl"]
+    np.testing.assert_array_equal(logs["actor/clip_fraction"], 0.0)
