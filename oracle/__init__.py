@@ -19,6 +19,10 @@ Parity status of each part (what pins it):
   (within tolerance only).
 - ``ppo.loss_terms``: closed forms (ratio 1 at replay, clip fraction, KL 0) and
   finite differences of the scalar loss.
+- ``sample``: the rollout-side Gumbel-max / Gaussian draws pinned by uniform
+  endpoints on hand-computed words, chi-square of Gumbel-max frequencies,
+  normal moments and a Kolmogorov-Smirnov test, and scipy's log-densities
+  (parity with a live jax.random bit stream: unpinned).
 - ``ppo.optimizer_update``: closed form of Adam's first step
   (|update| = lr for |g| >> eps) and clip invariants; optax itself: unpinned.
 """
