@@ -384,9 +384,18 @@ def step_main(args, recipe, alg, state, params, dev):
     from boonta_amd.random import key as make_key
 
     T, N, D = recipe.T, recipe.N, recipe.obs_dim
-    obs_np = synthetic.rollout(recipe, T, N)["obs"]
+    roll = synthetic.rollout(recipe, T, N)
+    obs_np = roll["obs"]
     obs = torch.from_numpy(obs_np).to(dev)
     ex = alg.step_executor(state, N, D)
+    rec = recipe.recurrent
+    if rec:
+        # the carry entering every step, and each step's reset flags first.done[t]
+        H = ex.prog.gru.H
+        carries = torch.zeros(T + 1, N, H, dtype=torch.float32, device=dev)
+        ft_np = np.concatenate([roll["first_done"][:1], roll["terminated"][:-1]], axis=0)
+        ftr_np = np.concatenate([np.zeros((1, N), bool), roll["truncated"][:-1]], axis=0)
+        ft, ftr = torch.from_numpy(ft_np).to(dev), torch.from_numpy(ftr_np).to(dev)
     dist = ex.prog.dist
     if dist["kind"] == "categorical":
         act = torch.zeros(T, N, dtype=torch.int32, device=dev)
@@ -396,11 +405,18 @@ def step_main(args, recipe, alg, state, params, dev):
     val = torch.zeros(T, N, dtype=torch.float32, device=dev)
     keys = torch.from_numpy(np.stack([make_key(5000 + t) for t in range(T)]).view(np.int32)).to(dev)
 
+    def step_args(t):
+        if rec:
+            return (obs[t].data_ptr(), D, carries[t].data_ptr(), ft[t].data_ptr(), ftr[t].data_ptr(), 1.0,
+                    carries[t + 1].data_ptr(), act[t].data_ptr(), lp[t].data_ptr(), val[t].data_ptr(),
+                    keys[t].data_ptr())
+        return (obs[t].data_ptr(), D, 1.0, act[t].data_ptr(), lp[t].data_ptr(), val[t].data_ptr(),
+                keys[t].data_ptr())
+
     def issue_rollout():
         st = torch.cuda.current_stream().cuda_stream
         for t in range(T):
-            ex.issue(st, obs[t].data_ptr(), D, 1.0, act[t].data_ptr(), lp[t].data_ptr(), val[t].data_ptr(),
-                     keys[t].data_ptr())
+            ex.issue(st, *step_args(t))
 
     issue_rollout()
     torch.cuda.synchronize()
@@ -437,8 +453,7 @@ def step_main(args, recipe, alg, state, params, dev):
                    "graph": not args.no_graph},
     }
     if not args.profile_only:
-        calls = ex.record(obs[0].data_ptr(), D, 1.0, act[0].data_ptr(), lp[0].data_ptr(), val[0].data_ptr(),
-                          keys[0].data_ptr())
+        calls = ex.record(*step_args(0))
         rows = time_calls(calls, args.launch_reps, T)
         total = sum(r["ms"] * r["count"] for r in rows)
         dom = max(rows, key=lambda r: r["ms"] * r["count"])
@@ -453,10 +468,16 @@ def step_main(args, recipe, alg, state, params, dev):
             plan = recipe.network.plan(D)
             p64 = params
             spent, steps = 0.0, 0
+            h = np.zeros((N, ex.prog.gru.H)) if rec else None
             while spent < args.cpu_seconds and steps < T:
                 x = obs_np[steps]
                 t1 = time.perf_counter()
-                head, value, _ = onets.forward(p64, plan, x)
+                if rec:
+                    done = (ft_np[steps] | ftr_np[steps])[:, None]
+                    head, value, h, _ = onets.recurrent_forward(p64, plan, x[:, None, :], done, h)
+                    head = head[:, 0]
+                else:
+                    head, value, _ = onets.forward(p64, plan, x)
                 k = make_key(5000 + steps)
                 if dist["kind"] == "categorical":
                     osample.categorical_sample(head, k, 1.0)
@@ -506,9 +527,6 @@ def main():
     alg = cls(cfg=recipe.cfg, network=recipe.network, optimizer=recipe.optimizer, use_graph=not args.no_graph)
     state = alg.init_from_params({"params": params}, recipe.obs_dim)
     if args.path == "step":
-        if recipe.recurrent:
-            print("bench.py --path step covers the MLP workloads (1, 2, 3, 5)", file=sys.stderr)
-            sys.exit(2)
         step_main(args, recipe, alg, state, params, dev)
         return
     tr = synthetic_rollout(recipe, params, dev, recipe.seed)

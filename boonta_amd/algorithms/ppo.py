@@ -125,12 +125,23 @@ class PPO:
                         params={"params": tree_from_flat(lay, flat.P)}, optimizer_state=opt_state)
 
     # ------------------------------------------------------------------ step
-    def step_executor(self, state, rows: int, obs_dim: int) -> StepExecutor:
+    step_class = StepExecutor
+
+    def step_executor(self, state, rows: int, obs_dim: int):
         flat = flat_state_of(state)
         k = (id(flat), rows, obs_dim)
         if k not in self._steppers:
-            self._steppers[k] = StepExecutor(self.program(obs_dim), flat, rows)
+            self._steppers[k] = self.step_class(self.program(obs_dim), flat, rows)
         return self._steppers[k]
+
+    @staticmethod
+    def _set_key(ex, key):
+        if isinstance(key, torch.Tensor) and key.is_cuda:
+            if key.numel() != 2 or key.element_size() != 4:
+                raise ValueError("a device key must hold two 32-bit words")
+            ex.KEY.copy_(key.reshape(2).view(torch.int32))
+        else:
+            ex.KEY.copy_(torch.from_numpy(key_data(key).view(np.int32).copy()))
 
     def step(self, state, carry, key, timestep, temperature: float = 1.0):
         """Acts on ``timestep.obs`` [N, obs] (ppo.py:57-74): the network forward
@@ -144,12 +155,7 @@ class PPO:
             raise TypeError("timestep.obs must be a contiguous float32 [N, obs] device tensor")
         N, obs_dim = (int(d) for d in obs.shape)
         ex = self.step_executor(state, N, obs_dim)
-        if isinstance(key, torch.Tensor) and key.is_cuda:
-            if key.numel() != 2 or key.element_size() != 4:
-                raise ValueError("a device key must hold two 32-bit words")
-            ex.KEY.copy_(key.reshape(2).view(torch.int32))
-        else:
-            ex.KEY.copy_(torch.from_numpy(key_data(key).view(np.int32).copy()))
+        self._set_key(ex, key)
         dev = ex.KEY.device
         dist = ex.prog.dist
         if dist["kind"] == "categorical":

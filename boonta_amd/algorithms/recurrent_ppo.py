@@ -3,7 +3,8 @@
 Mirrors boonta/algorithms/recurrent_ppo.py:19-281: ``RecurrentPPOConfig``
 (:19-28), ``RecurrentPPOState`` (:31-35) and ``RecurrentPPO(cfg, network,
 optimizer, auxiliary_losses=(), advantage_estimator=...)`` with ``init``
-(:45-69) and ``update(state, key, transitions) -> state`` (:98-281).
+(:45-69), ``step`` (:71-96) and ``update(state, key, transitions) -> state``
+(:98-281).  ``step`` runs on ``RecurrentStepExecutor`` (boonta_amd/rollout.py).
 
 ``transitions`` is a ``Transition`` of time-major [T, N, ...] device tensors
 whose ``first`` timestep carries ``terminated``/``truncated`` (its ``done`` is
@@ -21,6 +22,7 @@ import torch
 
 from ..learner_rnn import RecurrentExecutor
 from ..random import key_data
+from ..rollout import RecurrentStepExecutor
 from .ppo import PPO, PPOConfig, PPOState
 
 
@@ -35,6 +37,7 @@ RecurrentPPOState = PPOState
 @dataclass
 class RecurrentPPO(PPO):
     executor_class = RecurrentExecutor
+    step_class = RecurrentStepExecutor
 
     def init(self, key, timestep) -> tuple[PPOState, torch.Tensor]:
         """(state, carry): the zero initial carry [N, H] of the GRU
@@ -44,6 +47,37 @@ class RecurrentPPO(PPO):
         n = int(timestep.obs.shape[0])
         carry = torch.zeros(n, plan["torso"]["features"], dtype=torch.float32, device=torch.device(self.device))
         return state, carry
+
+    def step(self, state, carry, key, timestep, temperature: float = 1.0):
+        """One time step for N envs (recurrent_ppo.py:71-96): the carry is reset
+        to zeros where ``timestep`` is done (terminated | truncated; None flags
+        reset nothing), the GRU advances one step and the head's action is
+        sampled.  Returns (state, new carry [N, H], action int32 [N],
+        {"log_prob": [N], "value": [N]}); ``carry`` None is the zero carry."""
+        obs = timestep.obs
+        if (not isinstance(obs, torch.Tensor) or obs.dtype != torch.float32 or obs.dim() != 2
+                or not obs.is_contiguous() or not obs.is_cuda):
+            raise TypeError("timestep.obs must be a contiguous float32 [N, obs] device tensor")
+        N, obs_dim = (int(d) for d in obs.shape)
+        ex = self.step_executor(state, N, obs_dim)
+        H = ex.prog.gru.H
+        dev = ex.KEY.device
+        if carry is None:
+            carry = torch.zeros(N, H, dtype=torch.float32, device=dev)
+        self._need(carry, torch.float32, "carry", (N, H))
+        flags = []
+        for name in ("terminated", "truncated"):
+            f = getattr(timestep, name)
+            flags.append(None if f is None else self._need(f, torch.bool, f"timestep.{name}", (N,)))
+        self._set_key(ex, key)
+        new_carry = torch.empty(N, H, dtype=torch.float32, device=dev)
+        action = torch.empty(N, dtype=torch.int32, device=dev)
+        log_prob = torch.empty(N, dtype=torch.float32, device=dev)
+        value = torch.empty(N, dtype=torch.float32, device=dev)
+        ex.issue(torch.cuda.current_stream().cuda_stream, obs.data_ptr(), obs_dim, carry.data_ptr(), flags[0],
+                 flags[1], float(temperature), new_carry.data_ptr(), action.data_ptr(), log_prob.data_ptr(),
+                 value.data_ptr())
+        return state, new_carry, action, {"log_prob": log_prob, "value": value}
 
     def _inputs(self, transitions, obs_dim: int) -> tuple[dict, tuple]:
         inp, _ = super()._inputs(transitions, obs_dim)

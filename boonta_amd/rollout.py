@@ -9,6 +9,12 @@ on one stream:
     sample_and_log_prob(seed=key)                   distributions.py:8-57
         (``ppo_sample_categorical_f32`` / ``ppo_sample_gaussian_f32``)
 
+``RecurrentStepExecutor`` is the same for ``RecurrentPPO.step``
+(recurrent_ppo.py:71-96): trunk forward, the GRU input projection, one GRU
+step from the given carry with the carry reset to zeros where the timestep is
+done (reset_carry, networks/blocks/rnn.py:11-16,43-46), the heads on the new
+carry, and the sampling launch.
+
 The forward reuses the learner's kernels (``ForwardChain``) and reads the
 same flat parameter buffer, so a step issued after an update sees the updated
 parameters without a copy.
@@ -18,7 +24,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .learner import (A_ROW, B_KN, EPI_BIAS_ACT, DenseSpec, FlatState, ForwardChain, Program, _p, forward_bufs,
+from .learner import (A_ROW, B_KN, EPI_BIAS_ACT, LayerBufs, DenseSpec, FlatState, ForwardChain, Program, _p, forward_bufs,
                       split_forward_bufs)
 
 
@@ -92,6 +98,65 @@ class StepExecutor(ForwardChain):
     def record(self, *issue_args) -> list:
         """The launch sequence of one step as (entry point, args) without
         running it (used by the benchmark to time single launches)."""
+        calls = []
+        self._call = lambda name, *args: calls.append((name, args))
+        try:
+            self.issue(0, *issue_args)
+        finally:
+            self._call = _lib.call
+        return calls
+
+
+class RecurrentStepExecutor(ForwardChain):
+    """RecurrentPPO.step for a fixed number of environments (rows): the
+    network of ``Network(feature_extractor=<MLP>, torso=RNN(GRUCell(H)),
+    head=ActorCritic(Dense, Dense))`` one time step at a time."""
+
+    def __init__(self, program: Program, flat: FlatState, rows: int):
+        if program.gru is None:
+            raise TypeError("RecurrentStepExecutor needs a program with a GRU torso")
+        if not program.shared_head or not program.trunk:
+            raise NotImplementedError("the recurrent step compiles an MLP feature extractor, the GRU and plain "
+                                      "Dense heads")
+        if program.dist["kind"] != "categorical":
+            raise NotImplementedError("the recurrent step compiles a categorical head")
+        super().__init__(program, flat)
+        lib = _lib.load()
+        if program.action_dim > lib.ppo_sample_max_outputs():
+            raise NotImplementedError(f"an action dimension above {lib.ppo_sample_max_outputs()} is not compiled")
+        dev = flat.device
+        H = program.gru.H
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.rows = rows
+        self.trunk: list[LayerBufs] = [forward_bufs(s, rows, dev) for s in program.trunk]
+        self.XI = torch.zeros(rows, 3 * H, **f32)
+        self.HEAD = torch.zeros(rows, program.head_a.w.ld, **f32)
+        self.KEY = torch.zeros(2, dtype=torch.int32, device=dev)
+
+    def issue(self, st: int, obs: int, ldo: int, carry: int, terminated: int | None, truncated: int | None,
+              temperature: float, carry_out: int, action: int, log_prob: int, value: int, key: int | None = None):
+        """Enqueues one step: obs [rows, ldo] and carry [rows, H] float32 in,
+        terminated / truncated [rows] bool (or None: no reset); the new carry
+        [rows, H], action [rows] int32, log_prob and value [rows] out."""
+        key = _p(self.KEY) if key is None else key
+        prog = self.prog
+        g = prog.gru
+        H, I = g.H, g.fin
+        rows = self.rows
+        x, ldx, _ = self._fwd_layers(st, self.trunk, obs, ldo, None, rows)
+        self._gemm(st, A_ROW, B_KN, x, ldx, None, self.flat.view(g.wi), 3 * H, _p(self.XI), 3 * H, rows, 3 * H, I,
+                   1, 0, EPI_BIAS_ACT, self.flat.view(g.bi), 0, None, None, 0, None, -1)
+        self._call("ppo_gru_fwd_step_f32", st, _p(self.XI), 3 * H, carry, H, None, terminated, truncated, None,
+                   self.flat.view(g.wh), 3 * H, self.flat.view(g.bhn), carry_out, H, None, H, None, 4 * H, rows, H)
+        h = prog.head_a
+        self._gemm(st, A_ROW, B_KN, carry_out, H, None, self.flat.view(h.w), h.w.ld, _p(self.HEAD), h.w.ld, rows,
+                   h.w.ld, h.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(h.b) if h.b is not None else None, 0, None,
+                   None, 0, None, -1)
+        ldh = self.HEAD.shape[1]
+        self._call("ppo_sample_categorical_f32", st, _p(self.HEAD), ldh, rows, prog.dist["num"],
+                   _p(self.HEAD) + 4 * prog.head_out, ldh, key, float(temperature), action, log_prob, value)
+
+    def record(self, *issue_args) -> list:
         calls = []
         self._call = lambda name, *args: calls.append((name, args))
         try:

@@ -24,7 +24,8 @@ from boonta_amd.algorithms.ppo import PPO, flat_state_of
 from boonta_amd.random import key as make_key
 from boonta_amd.types import Timestep, Transition
 from oracle import nets, sample
-from ppo_cases import gpu_algorithm
+from boonta_amd.algorithms.recurrent_ppo import RecurrentPPO
+from ppo_cases import gpu_algorithm, gpu_recurrent_algorithm
 
 pytestmark = pytest.mark.gpu
 
@@ -193,6 +194,73 @@ def test_update_replays_what_step_acted_on(config):
                       terminated=dev(roll["terminated"]), truncated=dev(roll["truncated"]))
     trans = Transition(first=Timestep(obs=obs[:-1]), second=second,
                        aux={"log_prob": torch.stack(lps), "value": torch.stack(values)})
+    alg.update(state, make_key(5), trans)
+    torch.cuda.synchronize()
+    logs = alg.logs(state, T, N, D)
+    assert np.all(np.abs(logs["actor/approximate_kl"]) <= 1e-6), logs["actor/approximate_kl"]
+    np.testing.assert_array_equal(logs["actor/clip_fraction"], 0.0)
+
+
+def test_recurrent_step_matches_the_oracle():
+    """RecurrentPPO.step (recurrent_ppo.py:71-96): reset where done, one GRU
+    step, heads on the new carry, then the categorical draw."""
+    r = recipes.make(4).resized(N=256)
+    N, D = r.N, r.obs_dim
+    plan = r.network.plan(D)
+    H = plan["torso"]["features"]
+    params = r.network.init(0, D)["params"]
+    rng = np.random.default_rng(4)
+    obs = synthetic.rollout(r, T=1, N=N)["obs"][0]
+    carry = np.tanh(rng.standard_normal((N, H))).astype(np.float32)
+    term = rng.random(N) < 0.2
+    trunc = (rng.random(N) < 0.1) & ~term
+    head, value, final, _ = nets.recurrent_forward(params, plan, obs[:, None, :], (term | trunc)[:, None], carry)
+    alg = gpu_recurrent_algorithm(r, use_graph=False)
+    state = alg.init_from_params({"params": params}, D)
+    key = make_key(44)
+    _, c2, action, aux = alg.step(state, dev(carry), key, Timestep(obs=dev(obs), terminated=dev(term),
+                                                                    truncated=dev(trunc)))
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(c2.cpu().numpy(), final, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(aux["value"].cpu().numpy(), value[:, 0], rtol=1e-5, atol=1e-5)
+    check_categorical(action.cpu().numpy(), aux["log_prob"].cpu().numpy(), head[:, 0], key, 1.0, 1e-4, 1e-5)
+    # no carry is the zero carry; with every env done the given carry is forgotten
+    _, c0, a0, x0 = alg.step(state, None, key, Timestep(obs=dev(obs)))
+    done = torch.ones(N, dtype=torch.bool, device="cuda")
+    _, c1, a1, x1 = alg.step(state, dev(carry), key, Timestep(obs=dev(obs), terminated=done,
+                                                                truncated=torch.zeros_like(done)))
+    torch.cuda.synchronize()
+    assert torch.equal(c0, c1) and torch.equal(a0, a1) and torch.equal(x0["log_prob"], x1["log_prob"])
+
+
+def test_recurrent_update_replays_what_step_acted_on():
+    """tests/test_algorithms.py:368-380 (every torso replays what it acted
+    on): the update's sequence minibatches recompute the step-by-step GRU from
+    carry[0] with the resets first.done."""
+    r = recipes.make(4).resized(T=8, N=64, num_minibatches=4, update_epochs=2)
+    T, N, D = r.T, r.N, r.obs_dim
+    roll = synthetic.rollout(r, T, N)
+    first_term = np.concatenate([roll["first_done"][:1], roll["terminated"][:-1]], axis=0)
+    first_trunc = np.concatenate([np.zeros((1, N), bool), roll["truncated"][:-1]], axis=0)
+    alg = RecurrentPPO(cfg=r.cfg, network=r.network,
+                       optimizer=optim.chain(optim.clip_by_global_norm(0.5), optim.adam(0.0)))
+    obs = dev(roll["obs"])
+    state, carry = alg.init(make_key(0), Timestep(obs=obs[0]))
+    carry = torch.tanh(torch.randn(carry.shape, generator=torch.Generator().manual_seed(3))).cuda()
+    ft, ftr = dev(first_term), dev(first_trunc)
+    carries, actions, lps, values = [], [], [], []
+    for t in range(T):
+        carries.append(carry)
+        _, carry, a, aux = alg.step(state, carry, make_key(200 + t),
+                                    Timestep(obs=obs[t].contiguous(), terminated=ft[t], truncated=ftr[t]))
+        actions.append(a)
+        lps.append(aux["log_prob"])
+        values.append(aux["value"])
+    second = Timestep(obs=obs[1:], action=torch.stack(actions), reward=dev(roll["reward"]),
+                      terminated=dev(roll["terminated"]), truncated=dev(roll["truncated"]))
+    trans = Transition(first=Timestep(obs=obs[:-1], terminated=ft, truncated=ftr), second=second,
+                       aux={"log_prob": torch.stack(lps), "value": torch.stack(values)},
+                       carry=torch.stack(carries))
     alg.update(state, make_key(5), trans)
     torch.cuda.synchronize()
     logs = alg.logs(state, T, N, D)
