@@ -32,9 +32,12 @@ def parse():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", type=int, default=2)
-    ap.add_argument("--path", choices=("update", "step"), default="update",
+    ap.add_argument("--path", choices=("update", "step", "scan"), default="update",
                     help="update: the learner update (default); step: the rollout-side PPO.step "
-                         "(forward + action sampling) for one rollout of T steps over N envs")
+                         "(forward + action sampling) for one rollout of T steps over N envs; scan: the "
+                         "linear-recurrence scan forward + backward of an SSM torso")
+    ap.add_argument("--scan-shape", default="1024,64,256", help="batch,steps,features of --path scan")
+    ap.add_argument("--scan-dtype", choices=("f32", "bf16"), default="f32")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--launch-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -500,6 +503,79 @@ def step_main(args, recipe, alg, state, params, dev):
     print(json.dumps(out), flush=True)
 
 
+def scan_main(args):
+    """Linear-recurrence scan (the SSM / MinGRU torso kernel): one step is a
+    forward and a backward over [batch, steps, features] resident in HBM.
+    Algorithmic bytes: forward reads a, b and writes h; backward reads a, h
+    and the cotangent and writes da and db (init / dinit rows are extra)."""
+    import torch
+    from boonta_amd import _lib
+
+    n, t, f = (int(x) for x in args.scan_shape.split(","))
+    dt = torch.float32 if args.scan_dtype == "f32" else torch.bfloat16
+    code = 0 if dt == torch.float32 else 1
+    es = 4 if dt == torch.float32 else 2
+    g = torch.Generator(device="cuda").manual_seed(0)
+    a = (torch.rand((n, t, f), generator=g, device="cuda") * 0.9 + 0.05).to(dt)
+    b = torch.rand((n, t, f), generator=g, device="cuda").to(dt)
+    init = torch.randn((n, f), generator=g, device="cuda").to(dt)
+    cot = torch.randn((n, t, f), generator=g, device="cuda").to(dt)
+    h, da, db, dinit = torch.empty_like(a), torch.empty_like(a), torch.empty_like(a), torch.empty_like(init)
+    st = torch.cuda.current_stream()
+    fwd = ("ppo_linear_scan_fwd", (st.cuda_stream, code, a.data_ptr(), b.data_ptr(), init.data_ptr(),
+                                   h.data_ptr(), n, t, f))
+    bwd = ("ppo_linear_scan_bwd", (st.cuda_stream, code, a.data_ptr(), h.data_ptr(), init.data_ptr(),
+                                   cot.data_ptr(), da.data_ptr(), db.data_ptr(), dinit.data_ptr(), n, t, f))
+
+    def one():
+        _lib.call(fwd[0], *fwd[1])
+        _lib.call(bwd[0], *bwd[1])
+
+    for _ in range(args.warmup):
+        one()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        one()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    per = {}
+    for name, cargs in (fwd, bwd):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(args.launch_reps):
+            _lib.call(name, *cargs)
+        e1.record(st)
+        e1.synchronize()
+        per[name] = e0.elapsed_time(e1) / args.launch_reps
+    elems = n * t * f
+    nbytes = {"ppo_linear_scan_fwd": 3 * es * elems + es * n * f, "ppo_linear_scan_bwd": 5 * es * elems + 2 * es * n * f}
+    dom = max(per, key=per.get)
+    achieved = nbytes[dom] / (per[dom] * 1e-3) / 1e9
+    out = {
+        "metric": "linear-recurrence scan forward+backward elements/sec on 1 MI355X",
+        "value": elems * args.steps / elapsed, "unit": "elements/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": 1000.0 * elapsed / args.steps, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": args.scan_dtype, "data": "synthetic (uniform a, b)",
+        "config": {"workload": f"linear scan [{n}, {t}, {f}] {args.scan_dtype}"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK["hbm"], "unit": "GB/s",
+                     "frac": achieved / PEAK["hbm"], "traffic": None, "kernel": dom, "avg_ms": per[dom]},
+        "launches": [{"name": k, "ms": v, "GB/s": nbytes[k] / (v * 1e-3) / 1e9} for k, v in per.items()],
+    }
+    if not args.skip_cpu:
+        from oracle import scan as oscan
+        k = max(1, min(n, 64))
+        an, bn, inn, cn = (x[:k].float().cpu().numpy() for x in (a, b, init, cot))
+        t1 = time.perf_counter()
+        hh = oscan.forward(an, bn, inn)
+        oscan.vjp(an, hh, inn, cn)
+        spent = time.perf_counter() - t1
+        out["cpu_baseline"] = {"value": k * t * f / spent, "unit": "elements/s", "cores": 1, "kind": "port",
+                               "sample": f"oracle float64 numpy forward + VJP on {k} of the {n} sequences "
+                                         f"({spent:.2f} s)"}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -517,6 +593,9 @@ def main():
         sys.exit(1)
     if args.copy_probe:
         copy_probe(args.copy_probe)
+        return
+    if args.path == "scan":
+        scan_main(args)
         return
     recipe = recipes.make(args.config)
     dev = torch.device("cuda:0")

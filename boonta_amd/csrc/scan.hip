@@ -1,0 +1,295 @@
+// Linear-recurrence scan h_t = a_t * h_{t-1} + b_t over [batch, steps, features]
+// and its vector-Jacobian product, the kernels behind boonta's SSM / MinGRU
+// torsos (boonta/networks/kernels/scan.py:13-88: `scan` with its custom VJP;
+// the SSM block calls it at networks/blocks/ssm.py:31-55).
+//
+// Forward:  h_t = a_t h_{t-1} + b_t, h_{-1} = init, accumulated in float32 and
+//           stored in the operands' type (float32 or bf16 storage).
+// Backward (cotangent g of h):
+//           db_t = g_t + a_{t+1} db_{t+1}   (db_{steps-1} = g_{steps-1})
+//           da_t = db_t h_{t-1}             (h_{-1} = init)
+//           dinit = db_0 a_0
+//           with db accumulated in float32 and stored in the operands' type;
+//           for bf16 storage da and dinit multiply the stored (rounded) db and
+//           are rounded again, as the reference's bf16 array arithmetic does.
+//
+// Layout and parallelism: element (n, t, f) at (n * steps + t) * features + f.
+// Each lane owns VW consecutive features of one sequence (16-byte loads for
+// float32 with VW = 4), so every step reads one coalesced row.  When the
+// batch x feature lanes alone cannot fill the chip, the time axis is cut into
+// C <= 16 chunks, one wave each, in one workgroup: every wave first folds its
+// chunk into the affine map (A, B) of h_end = A h_start + B, the waves
+// exchange the maps through LDS, and each wave composes the maps before it (in
+// time order for the forward, in reverse for the backward) to start its own
+// chunk from the exact carry, then re-reads the chunk and writes its outputs.
+#include "common.h"
+
+#include <algorithm>
+
+namespace {
+
+constexpr int MAX_CHUNKS = 16;
+constexpr int MAX_VW = 4;
+
+enum ScanDtype { SCAN_F32 = 0, SCAN_BF16 = 1 };
+
+__device__ __forceinline__ void load_vec(const float* p, int64_t i, float (&v)[1]) { v[0] = p[i]; }
+__device__ __forceinline__ void load_vec(const float* p, int64_t i, float (&v)[4]) {
+  const floatx4 x = *reinterpret_cast<const floatx4*>(p + i);
+  v[0] = x[0]; v[1] = x[1]; v[2] = x[2]; v[3] = x[3];
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t u) { return __uint_as_float((uint32_t)u << 16); }
+__device__ __forceinline__ void load_vec(const uint16_t* p, int64_t i, float (&v)[1]) { v[0] = bf16_to_f32(p[i]); }
+__device__ __forceinline__ void load_vec(const uint16_t* p, int64_t i, float (&v)[4]) {
+  const uint2 x = *reinterpret_cast<const uint2*>(p + i);
+  v[0] = __uint_as_float(x.x << 16); v[1] = __uint_as_float(x.x & 0xffff0000u);
+  v[2] = __uint_as_float(x.y << 16); v[3] = __uint_as_float(x.y & 0xffff0000u);
+}
+
+__device__ __forceinline__ void store_vec(float* p, int64_t i, const float (&v)[1]) { p[i] = v[0]; }
+__device__ __forceinline__ void store_vec(float* p, int64_t i, const float (&v)[4]) {
+  floatx4 x;
+  x[0] = v[0]; x[1] = v[1]; x[2] = v[2]; x[3] = v[3];
+  *reinterpret_cast<floatx4*>(p + i) = x;
+}
+__device__ __forceinline__ void store_vec(uint16_t* p, int64_t i, const float (&v)[1]) {
+  p[i] = (uint16_t)ppo::bf16_bits(v[0]);
+}
+__device__ __forceinline__ void store_vec(uint16_t* p, int64_t i, const float (&v)[4]) {
+  uint2 x;
+  x.x = ppo::bf16_bits(v[0]) | (ppo::bf16_bits(v[1]) << 16);
+  x.y = ppo::bf16_bits(v[2]) | (ppo::bf16_bits(v[3]) << 16);
+  *reinterpret_cast<uint2*>(p + i) = x;
+}
+
+// The value a stored element of type S holds (identity for float32).
+__device__ __forceinline__ float stored(float x, const float*) { return x; }
+__device__ __forceinline__ float stored(float x, const uint16_t*) { return ppo::bf16_round(x); }
+
+struct ScanArgs {
+  const void* a;
+  const void* b;     // forward: b; backward: the cotangent of h
+  const void* h;     // backward: the forward's output
+  const void* init;
+  void* out;         // forward: h; backward: db
+  void* da;
+  void* dinit;
+  int steps, F, chunk;
+};
+
+template <typename S, int VW>
+__global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_fwd_kernel(ScanArgs p) {
+  __shared__ float sA[MAX_CHUNKS][64 * MAX_VW];
+  __shared__ float sB[MAX_CHUNKS][64 * MAX_VW];
+  const S* a = static_cast<const S*>(p.a);
+  const S* b = static_cast<const S*>(p.b);
+  const S* init = static_cast<const S*>(p.init);
+  S* out = static_cast<S*>(p.out);
+  const int lane = threadIdx.x & 63, c = threadIdx.x >> 6, C = blockDim.x >> 6;
+  const int f0 = (blockIdx.x * 64 + lane) * VW;
+  const bool ok = f0 < p.F;
+  const int64_t n = blockIdx.y;
+  const int t0 = c * p.chunk, t1 = min(p.steps, t0 + p.chunk);
+  const int64_t base = n * (int64_t)p.steps * p.F + f0;
+  float h[VW];
+  if (ok) {
+    load_vec(init, n * (int64_t)p.F + f0, h);
+  } else {
+#pragma unroll
+    for (int k = 0; k < VW; ++k) h[k] = 0.f;
+  }
+  if (C > 1) {
+    float A[VW], B[VW];
+#pragma unroll
+    for (int k = 0; k < VW; ++k) { A[k] = 1.f; B[k] = 0.f; }
+    if (ok) {
+#pragma unroll 4
+      for (int t = t0; t < t1; ++t) {
+        float av[VW], bv[VW];
+        load_vec(a, base + (int64_t)t * p.F, av);
+        load_vec(b, base + (int64_t)t * p.F, bv);
+#pragma unroll
+        for (int k = 0; k < VW; ++k) {
+          A[k] = av[k] * A[k];
+          B[k] = av[k] * B[k] + bv[k];
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+      sA[c][lane * VW + k] = A[k];
+      sB[c][lane * VW + k] = B[k];
+    }
+    __syncthreads();
+    for (int cc = 0; cc < c; ++cc) {
+#pragma unroll
+      for (int k = 0; k < VW; ++k) h[k] = sA[cc][lane * VW + k] * h[k] + sB[cc][lane * VW + k];
+    }
+  }
+  if (!ok) return;
+#pragma unroll 4
+  for (int t = t0; t < t1; ++t) {
+    float av[VW], bv[VW];
+    load_vec(a, base + (int64_t)t * p.F, av);
+    load_vec(b, base + (int64_t)t * p.F, bv);
+#pragma unroll
+    for (int k = 0; k < VW; ++k) h[k] = av[k] * h[k] + bv[k];
+    store_vec(out, base + (int64_t)t * p.F, h);
+  }
+}
+
+template <typename S, int VW>
+__global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_bwd_kernel(ScanArgs p) {
+  __shared__ float sA[MAX_CHUNKS][64 * MAX_VW];
+  __shared__ float sB[MAX_CHUNKS][64 * MAX_VW];
+  const S* a = static_cast<const S*>(p.a);
+  const S* g = static_cast<const S*>(p.b);
+  const S* hs = static_cast<const S*>(p.h);
+  const S* init = static_cast<const S*>(p.init);
+  S* db = static_cast<S*>(p.out);
+  S* da = static_cast<S*>(p.da);
+  S* dinit = static_cast<S*>(p.dinit);
+  const int lane = threadIdx.x & 63, c = threadIdx.x >> 6, C = blockDim.x >> 6;
+  const int f0 = (blockIdx.x * 64 + lane) * VW;
+  const bool ok = f0 < p.F;
+  const int64_t n = blockIdx.y;
+  const int t0 = c * p.chunk, t1 = min(p.steps, t0 + p.chunk);
+  const int64_t base = n * (int64_t)p.steps * p.F + f0;
+  // reverse recurrence d_t = g_t + alpha_t d_{t+1}, alpha_t = a_{t+1}
+  // (0 past the last step); d entering this chunk from the chunks after it
+  float d[VW];
+#pragma unroll
+  for (int k = 0; k < VW; ++k) d[k] = 0.f;
+  if (C > 1) {
+    float P[VW], Q[VW];
+#pragma unroll
+    for (int k = 0; k < VW; ++k) { P[k] = 1.f; Q[k] = 0.f; }
+    if (ok) {
+#pragma unroll 4
+      for (int t = t1 - 1; t >= t0; --t) {
+        float al[VW], gv[VW];
+        if (t + 1 < p.steps) {
+          load_vec(a, base + (int64_t)(t + 1) * p.F, al);
+        } else {
+#pragma unroll
+          for (int k = 0; k < VW; ++k) al[k] = 0.f;
+        }
+        load_vec(g, base + (int64_t)t * p.F, gv);
+#pragma unroll
+        for (int k = 0; k < VW; ++k) {
+          P[k] = al[k] * P[k];
+          Q[k] = al[k] * Q[k] + gv[k];
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+      sA[c][lane * VW + k] = P[k];
+      sB[c][lane * VW + k] = Q[k];
+    }
+    __syncthreads();
+    for (int cc = C - 1; cc > c; --cc) {
+#pragma unroll
+      for (int k = 0; k < VW; ++k) d[k] = sA[cc][lane * VW + k] * d[k] + sB[cc][lane * VW + k];
+    }
+  }
+  if (!ok) return;
+#pragma unroll 4
+  for (int t = t1 - 1; t >= t0; --t) {
+    float al[VW], gv[VW], hp[VW];
+    if (t + 1 < p.steps) {
+      load_vec(a, base + (int64_t)(t + 1) * p.F, al);
+    } else {
+#pragma unroll
+      for (int k = 0; k < VW; ++k) al[k] = 0.f;
+    }
+    load_vec(g, base + (int64_t)t * p.F, gv);
+    if (t > 0) {
+      load_vec(hs, base + (int64_t)(t - 1) * p.F, hp);
+    } else {
+      load_vec(init, n * (int64_t)p.F + f0, hp);
+    }
+    float dv[VW], dav[VW];
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+      d[k] = al[k] * d[k] + gv[k];
+      dv[k] = stored(d[k], db);
+      dav[k] = dv[k] * hp[k];
+    }
+    store_vec(db, base + (int64_t)t * p.F, d);
+    store_vec(da, base + (int64_t)t * p.F, dav);
+    if (t == 0) {
+      float a0[VW], di[VW];
+      load_vec(a, base, a0);
+#pragma unroll
+      for (int k = 0; k < VW; ++k) di[k] = dv[k] * a0[k];
+      store_vec(dinit, n * (int64_t)p.F + f0, di);
+    }
+  }
+}
+
+bool aligned(const void* ptr, int bytes) { return (reinterpret_cast<uintptr_t>(ptr) % bytes) == 0; }
+
+template <typename S, int VW, bool BWD>
+int launch(hipStream_t st, const ScanArgs& p, int batch) {
+  const int lanes = ppo::ceil_div(p.F, VW);
+  const int groups = ppo::ceil_div(lanes, 64);
+  const int C = ppo::ceil_div(p.steps, p.chunk);
+  dim3 grid(groups, batch), block(64 * C);
+  if (BWD) {
+    hipLaunchKernelGGL((scan_bwd_kernel<S, VW>), grid, block, 0, st, p);
+  } else {
+    hipLaunchKernelGGL((scan_fwd_kernel<S, VW>), grid, block, 0, st, p);
+  }
+  return PPO_OK;
+}
+
+template <bool BWD>
+int dispatch(hipStream_t st, int dtype, ScanArgs p, int batch, const char* what) {
+  // chunks: enough waves to fill the chip (about 8 per CU), at most 16, and
+  // at least 8 steps per chunk
+  const int esize = dtype == SCAN_F32 ? 4 : 2;
+  const void* ptrs[7] = {p.a, p.b, p.h, p.init, p.out, p.da, p.dinit};
+  bool vec = p.F % 4 == 0;
+  for (const void* q : ptrs)
+    if (q && !aligned(q, 4 * esize)) vec = false;
+  const int VW = vec ? 4 : 1;
+  const int64_t waves = (int64_t)batch * ppo::ceil_div(ppo::ceil_div(p.F, VW), 64);
+  int C = (int)std::min<int64_t>(MAX_CHUNKS, std::max<int64_t>(1, ppo::ceil_div64(2048, waves)));
+  C = std::max(1, std::min(C, p.steps / 8));
+  p.chunk = ppo::ceil_div(p.steps, C);
+  if (dtype == SCAN_F32) {
+    if (vec) launch<float, 4, BWD>(st, p, batch); else launch<float, 1, BWD>(st, p, batch);
+  } else {
+    if (vec) launch<uint16_t, 4, BWD>(st, p, batch); else launch<uint16_t, 1, BWD>(st, p, batch);
+  }
+  return ppo::check_launch(what);
+}
+
+}  // namespace
+
+PPO_EXPORT int ppo_linear_scan_fwd(void* stream, int dtype, const void* a, const void* b, const void* init, void* out,
+                                   int batch, int steps, int features) {
+  if (batch < 0 || steps < 0 || features < 0 || (dtype != SCAN_F32 && dtype != SCAN_BF16))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_linear_scan_fwd: bad argument (batch %d steps %d features %d dtype %d)",
+                          batch, steps, features, dtype);
+  if (batch == 0 || steps == 0 || features == 0) return PPO_OK;
+  if (!a || !b || !init || !out) return ppo::set_error(PPO_ERR_ARG, "ppo_linear_scan_fwd: null buffer");
+  if (batch > 65535) return ppo::set_error(PPO_ERR_ARG, "ppo_linear_scan_fwd: batch above 65535");
+  ScanArgs p{a, b, nullptr, init, out, nullptr, nullptr, steps, features, 0};
+  return dispatch<false>(ppo::as_stream(stream), dtype, p, batch, "ppo_linear_scan_fwd");
+}
+
+PPO_EXPORT int ppo_linear_scan_bwd(void* stream, int dtype, const void* a, const void* h, const void* init,
+                                   const void* cot, void* da, void* db, void* dinit, int batch, int steps,
+                                   int features) {
+  if (batch < 0 || steps < 0 || features < 0 || (dtype != SCAN_F32 && dtype != SCAN_BF16))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_linear_scan_bwd: bad argument (batch %d steps %d features %d dtype %d)",
+                          batch, steps, features, dtype);
+  if (batch == 0 || steps == 0 || features == 0) return PPO_OK;
+  if (!a || !h || !init || !cot || !da || !db || !dinit)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_linear_scan_bwd: null buffer");
+  if (batch > 65535) return ppo::set_error(PPO_ERR_ARG, "ppo_linear_scan_bwd: batch above 65535");
+  ScanArgs p{a, cot, h, init, db, da, dinit, steps, features, 0};
+  return dispatch<true>(ppo::as_stream(stream), dtype, p, batch, "ppo_linear_scan_bwd");
+}

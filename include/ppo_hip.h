@@ -104,6 +104,21 @@ int ppo_sample_gaussian_f32(void* stream, const float* mean, int64_t ldm, const 
                             int rows, int D, const float* value_src, int64_t ldv, const uint32_t* key,
                             float temperature, float* action, int64_t lda, float* log_prob, float* value);
 
+/* ------------------------------------------------------- linear scan
+ * Replace boonta's linear-recurrence scan and its custom VJP
+ * (boonta/networks/kernels/scan.py:13-88: scan / _scan_fwd / _scan_bwd),
+ * called by the SSM block (networks/blocks/ssm.py:31-55) behind the MinGRU
+ * and other SSM torsos.  a, b, h, cotangent, da, db: [batch, steps, features]
+ * row-major; init, dinit: [batch, features]; dtype 0 = float32 storage,
+ * 1 = bf16 storage (float32 accumulation in both).
+ *   forward:  h_t = a_t h_{t-1} + b_t, h_{-1} = init
+ *   backward: db_t = cot_t + a_{t+1} db_{t+1}; da_t = db_t h_{t-1};
+ *             dinit = db_0 a_0 */
+int ppo_linear_scan_fwd(void* stream, int dtype, const void* a, const void* b, const void* init, void* out,
+                        int batch, int steps, int features);
+int ppo_linear_scan_bwd(void* stream, int dtype, const void* a, const void* h, const void* init, const void* cot,
+                        void* da, void* db, void* dinit, int batch, int steps, int features);
+
 /* ------------------------------------------------------------------ GEMM
  * Dense layers of the torso and heads (flax.linen.Dense as composed in
  * hangar/recipes/*.py; forward at boonta/networks/network.py:38-49, backward

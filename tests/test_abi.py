@@ -53,3 +53,11 @@ def test_sampling_rejects_unsupported_sizes_without_launching():
     assert b"ppo_sample_categorical_f32" in lib.ppo_last_error()
     assert lib.ppo_sample_gaussian_f32(None, 1, big, 1, 0, 4, big, None, 0, 1, 1.0, 1, big, 1, None) == -1
     assert lib.ppo_sample_categorical_f32(None, 1, 6, 4, 6, None, 0, None, 1.0, 1, 1, None) == -1
+
+
+def test_scan_rejects_bad_arguments_without_launching():
+    lib = _lib.load()
+    assert lib.ppo_linear_scan_fwd(None, 7, 1, 1, 1, 1, 2, 2, 2) == -1
+    assert lib.ppo_linear_scan_fwd(None, 0, None, 1, 1, 1, 2, 2, 2) == -1
+    assert lib.ppo_linear_scan_bwd(None, 0, 1, 1, 1, 1, None, 1, 1, 2, 2, 2) == -1
+    assert lib.ppo_linear_scan_fwd(None, 0, None, None, None, None, 0, 5, 5) == 0
