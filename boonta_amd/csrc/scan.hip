@@ -14,8 +14,9 @@
 //           are rounded again, as the reference's bf16 array arithmetic does.
 //
 // Layout and parallelism: element (n, t, f) at (n * steps + t) * features + f.
-// Each lane owns VW consecutive features of one sequence (16-byte loads for
-// float32 with VW = 4), so every step reads one coalesced row.  When the
+// Each lane owns VW = 4 consecutive features of one sequence where the rows
+// allow (one 16-byte float32 or 8-byte bf16 access), so every step reads one
+// coalesced row.  When the
 // batch x feature lanes alone cannot fill the chip, the time axis is cut into
 // C <= 16 chunks, one wave each, in one workgroup: every wave first folds its
 // chunk into the affine map (A, B) of h_end = A h_start + B, the waves
@@ -29,7 +30,6 @@
 namespace {
 
 constexpr int MAX_CHUNKS = 16;
-constexpr int MAX_VW = 4;
 
 enum ScanDtype { SCAN_F32 = 0, SCAN_BF16 = 1 };
 
@@ -61,7 +61,6 @@ __device__ __forceinline__ void store_vec(uint16_t* p, int64_t i, const float (&
   x.y = ppo::bf16_bits(v[2]) | (ppo::bf16_bits(v[3]) << 16);
   *reinterpret_cast<uint2*>(p + i) = x;
 }
-
 // The value a stored element of type S holds (identity for float32).
 __device__ __forceinline__ float stored(float x, const float*) { return x; }
 __device__ __forceinline__ float stored(float x, const uint16_t*) { return ppo::bf16_round(x); }
@@ -79,8 +78,10 @@ struct ScanArgs {
 
 template <typename S, int VW>
 __global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_fwd_kernel(ScanArgs p) {
-  __shared__ float sA[MAX_CHUNKS][64 * MAX_VW];
-  __shared__ float sB[MAX_CHUNKS][64 * MAX_VW];
+  // per chunk: the (A, B) maps of its 64 x VW lanes (dynamic: none when C = 1)
+  extern __shared__ float smem[];
+  float* sA = smem;
+  float* sB = smem + (blockDim.x >> 6) * 64 * VW;
   const S* a = static_cast<const S*>(p.a);
   const S* b = static_cast<const S*>(p.b);
   const S* init = static_cast<const S*>(p.init);
@@ -117,17 +118,17 @@ __global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_fwd_kernel(ScanArgs p) {
     }
 #pragma unroll
     for (int k = 0; k < VW; ++k) {
-      sA[c][lane * VW + k] = A[k];
-      sB[c][lane * VW + k] = B[k];
+      sA[(c * 64 + lane) * VW + k] = A[k];
+      sB[(c * 64 + lane) * VW + k] = B[k];
     }
     __syncthreads();
     for (int cc = 0; cc < c; ++cc) {
 #pragma unroll
-      for (int k = 0; k < VW; ++k) h[k] = sA[cc][lane * VW + k] * h[k] + sB[cc][lane * VW + k];
+      for (int k = 0; k < VW; ++k) h[k] = sA[(cc * 64 + lane) * VW + k] * h[k] + sB[(cc * 64 + lane) * VW + k];
     }
   }
   if (!ok) return;
-#pragma unroll 4
+#pragma unroll 8
   for (int t = t0; t < t1; ++t) {
     float av[VW], bv[VW];
     load_vec(a, base + (int64_t)t * p.F, av);
@@ -140,8 +141,9 @@ __global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_fwd_kernel(ScanArgs p) {
 
 template <typename S, int VW>
 __global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_bwd_kernel(ScanArgs p) {
-  __shared__ float sA[MAX_CHUNKS][64 * MAX_VW];
-  __shared__ float sB[MAX_CHUNKS][64 * MAX_VW];
+  extern __shared__ float smem[];
+  float* sA = smem;
+  float* sB = smem + (blockDim.x >> 6) * 64 * VW;
   const S* a = static_cast<const S*>(p.a);
   const S* g = static_cast<const S*>(p.b);
   const S* hs = static_cast<const S*>(p.h);
@@ -184,30 +186,31 @@ __global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_bwd_kernel(ScanArgs p) {
     }
 #pragma unroll
     for (int k = 0; k < VW; ++k) {
-      sA[c][lane * VW + k] = P[k];
-      sB[c][lane * VW + k] = Q[k];
+      sA[(c * 64 + lane) * VW + k] = P[k];
+      sB[(c * 64 + lane) * VW + k] = Q[k];
     }
     __syncthreads();
     for (int cc = C - 1; cc > c; --cc) {
 #pragma unroll
-      for (int k = 0; k < VW; ++k) d[k] = sA[cc][lane * VW + k] * d[k] + sB[cc][lane * VW + k];
+      for (int k = 0; k < VW; ++k) d[k] = sA[(cc * 64 + lane) * VW + k] * d[k] + sB[(cc * 64 + lane) * VW + k];
     }
   }
   if (!ok) return;
-#pragma unroll 4
-  for (int t = t1 - 1; t >= t0; --t) {
+  // one step of the reverse recurrence; has_next: a_{t+1} exists; first: t = 0
+  // (h_{t-1} is init, and dinit is written)
+  auto step = [&](int t, bool has_next, bool first) {
     float al[VW], gv[VW], hp[VW];
-    if (t + 1 < p.steps) {
+    if (has_next) {
       load_vec(a, base + (int64_t)(t + 1) * p.F, al);
     } else {
 #pragma unroll
       for (int k = 0; k < VW; ++k) al[k] = 0.f;
     }
     load_vec(g, base + (int64_t)t * p.F, gv);
-    if (t > 0) {
-      load_vec(hs, base + (int64_t)(t - 1) * p.F, hp);
-    } else {
+    if (first) {
       load_vec(init, n * (int64_t)p.F + f0, hp);
+    } else {
+      load_vec(hs, base + (int64_t)(t - 1) * p.F, hp);
     }
     float dv[VW], dav[VW];
 #pragma unroll
@@ -218,14 +221,25 @@ __global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_bwd_kernel(ScanArgs p) {
     }
     store_vec(db, base + (int64_t)t * p.F, d);
     store_vec(da, base + (int64_t)t * p.F, dav);
-    if (t == 0) {
+    if (first) {
       float a0[VW], di[VW];
       load_vec(a, base, a0);
 #pragma unroll
       for (int k = 0; k < VW; ++k) di[k] = dv[k] * a0[k];
       store_vec(dinit, n * (int64_t)p.F + f0, di);
     }
+  };
+  // the last and the first step peeled, so the main loop is branch-free and
+  // its loads can run ahead of the dependent multiply-adds
+  int t = t1 - 1;
+  if (t == p.steps - 1) {
+    step(t, false, t == 0);
+    --t;
   }
+  const int lo = max(t0, 1);
+#pragma unroll 8
+  for (; t >= lo; --t) step(t, true, false);
+  if (t == 0 && t >= t0) step(0, true, true);
 }
 
 bool aligned(const void* ptr, int bytes) { return (reinterpret_cast<uintptr_t>(ptr) % bytes) == 0; }
@@ -236,18 +250,22 @@ int launch(hipStream_t st, const ScanArgs& p, int batch) {
   const int groups = ppo::ceil_div(lanes, 64);
   const int C = ppo::ceil_div(p.steps, p.chunk);
   dim3 grid(groups, batch), block(64 * C);
+  const size_t lds = C > 1 ? 2 * sizeof(float) * (size_t)C * 64 * VW : 0;
   if (BWD) {
-    hipLaunchKernelGGL((scan_bwd_kernel<S, VW>), grid, block, 0, st, p);
+    hipLaunchKernelGGL((scan_bwd_kernel<S, VW>), grid, block, lds, st, p);
   } else {
-    hipLaunchKernelGGL((scan_fwd_kernel<S, VW>), grid, block, 0, st, p);
+    hipLaunchKernelGGL((scan_fwd_kernel<S, VW>), grid, block, lds, st, p);
   }
   return PPO_OK;
 }
 
 template <bool BWD>
 int dispatch(hipStream_t st, int dtype, ScanArgs p, int batch, const char* what) {
-  // chunks: enough waves to fill the chip (about 8 per CU), at most 16, and
-  // at least 8 steps per chunk
+  // 4 features per lane where the rows allow (16-byte float32 or 8-byte bf16
+  // accesses; for bf16, 8 per lane would halve the waves in flight).
+  // Time chunks re-read their operands, so they are used only when the lanes
+  // give too few waves: then enough chunks for twice that, at most 16, each
+  // at least 8 steps long.
   const int esize = dtype == SCAN_F32 ? 4 : 2;
   const void* ptrs[7] = {p.a, p.b, p.h, p.init, p.out, p.da, p.dinit};
   bool vec = p.F % 4 == 0;
@@ -255,7 +273,12 @@ int dispatch(hipStream_t st, int dtype, ScanArgs p, int batch, const char* what)
     if (q && !aligned(q, 4 * esize)) vec = false;
   const int VW = vec ? 4 : 1;
   const int64_t waves = (int64_t)batch * ppo::ceil_div(ppo::ceil_div(p.F, VW), 64);
-  int C = (int)std::min<int64_t>(MAX_CHUNKS, std::max<int64_t>(1, ppo::ceil_div64(2048, waves)));
+  // bf16 rows carry half the bytes per load, so bf16 wants more waves in
+  // flight before the re-read of a second pass stops paying (measured on
+  // [1024, 64, 256]: float32 forward 49 -> 33 us without chunks, bf16 forward
+  // 44 -> 34 us with two)
+  const int64_t enough = dtype == SCAN_F32 ? 512 : 2048;
+  int C = waves >= enough ? 1 : (int)std::min<int64_t>(MAX_CHUNKS, ppo::ceil_div64(2 * enough, waves));
   C = std::max(1, std::min(C, p.steps / 8));
   p.chunk = ppo::ceil_div(p.steps, C);
   if (dtype == SCAN_F32) {
