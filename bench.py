@@ -227,7 +227,8 @@ def time_launches(ex, reps, per_update_steps):
                    if n in ("ppo_epoch_permutations", "ppo_sequence_rows")) + 1
     rows, seen = [], {}
     for i, (name, args) in enumerate(calls):
-        count = per_update_steps if i >= first_mb else 1
+        # the logs of every step are finalized once, after the last step
+        count = per_update_steps if i >= first_mb and name != "ppo_loss_finalize_steps" else 1
         key = launch_key(name, args)
         if key in seen:
             seen[key]["count"] += count

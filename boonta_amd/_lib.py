@@ -62,6 +62,7 @@ SIGNATURES = {
     "ppo_loss_stat_count": (I, []),
     "ppo_loss_f32": (I, [P, I, I, P, P, I64, P, I64, I, P, P, P, P, P, P, P, P, P, P, P, F, I, F, F, F]),
     "ppo_loss_finalize": (I, [P, P, I, I, F, F, P]),
+    "ppo_loss_finalize_steps": (I, [P, P, I, I, I, F, F, P]),
     "ppo_head_loss_blocks": (I, [I]),
     "ppo_head_loss_max_outputs": (I, []),
     "ppo_head_loss_max_features": (I, []),

@@ -422,6 +422,9 @@ loss_finalize_kernel(const double* __restrict__ partial, int nblocks, int rows, 
   __shared__ double s[NSTAT];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  // block i finalizes step i: partials [steps][nblocks][NSTAT], out [steps][9]
+  partial += (int64_t)blockIdx.x * nblocks * NSTAT;
+  out += (int64_t)blockIdx.x * 9;
   // wave w folds statistics w, w + 4, w + 8 over the block partials
   for (int k = wave; k < NSTAT; k += 4) {
     double t = 0.0;
@@ -611,6 +614,16 @@ PPO_EXPORT int ppo_loss_f32(void* stream, int dist, int rows, const int32_t* idx
   p.temperature = temperature;
   hipLaunchKernelGGL(ppo_loss_kernel, dim3(ppo_loss_blocks(rows)), dim3(ROW_THREADS), 0, ppo::as_stream(stream), p);
   return ppo::check_launch("ppo_loss_f32");
+}
+
+PPO_EXPORT int ppo_loss_finalize_steps(void* stream, const double* stats_partial, int nblocks, int rows, int steps,
+                                       float ent_coef, float vf_coef, float* out) {
+  if (nblocks <= 0 || rows <= 0 || steps < 0 || (steps > 0 && (!stats_partial || !out)))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_loss_finalize_steps: bad argument");
+  if (steps == 0) return PPO_OK;
+  hipLaunchKernelGGL(loss_finalize_kernel, dim3(steps), dim3(256), 0, ppo::as_stream(stream), stats_partial, nblocks,
+                     rows, ent_coef, vf_coef, out);
+  return ppo::check_launch("ppo_loss_finalize_steps");
 }
 
 PPO_EXPORT int ppo_loss_finalize(void* stream, const double* stats_partial, int nblocks, int rows, float ent_coef,

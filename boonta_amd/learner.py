@@ -506,7 +506,8 @@ class MLPExecutor(ForwardChain):
             self.HEADB = torch.zeros(N, hc.w.ld, **f32)
         self.loss_blocks = self.head_blocks if self.fused else lib.ppo_loss_blocks(mb)
         self.nstat = lib.ppo_loss_stat_count()
-        self.STATS = torch.zeros(self.loss_blocks, self.nstat, dtype=torch.float64, device=dev)
+        # loss statistics of every step, finalized into LOGS once per update
+        self.STATS = torch.zeros(self.E * self.M, self.loss_blocks, self.nstat, dtype=torch.float64, device=dev)
         self.DSCALE = (torch.zeros(self.loss_blocks, program.dist["dim"], **f32)
                        if program.scale_region is not None else None)
         self.LOGS = torch.zeros(self.E * self.M, 9, **f32)
@@ -727,25 +728,50 @@ class MLPExecutor(ForwardChain):
         self._call("ppo_epoch_permutations", st, _p(self.KEY), self.E, B, _p(self.PERM), _p(self.PERM_WS),
                   self.PERM_WS.numel())
         # 4. minibatch steps
-        adam = chain.adam
-        max_norm = chain.max_grad_norm if chain.max_grad_norm is not None else 0.0
         dist = _lib.DIST[prog.dist["kind"]]
         A = prog.action_dim
         for e in range(self.E):
             for m in range(self.M):
                 step = e * self.M + m
                 if max_steps is not None and step >= max_steps:
+                    self._finish_logs(st, step)
                     return
                 idx = _p(self.PERM) + 4 * (e * B + m * mb)
                 self._minibatch(st, idx, step, obs, ldo, dist, A)
-                self._call("ppo_grad_reduce", st, _p(self.SEGS), _p(self.CHUNKS), self.nchunks, _p(self.SUMSQ))
-                self._call("ppo_sumsq_total", st, _p(self.SUMSQ), self.nchunks, _p(self.SUMSQ1))
-                self._call("ppo_adam_clip_f32", st, _p(self.flat.P), _p(self.flat.G), _p(self.flat.MU),
-                          _p(self.flat.NU), _p(self.P16) if self.obs16 else None, self.flat.P.numel(),
-                          _p(self.SUMSQ1), 1,
-                          float(max_norm), adam.learning_rate, adam.b1, adam.b2, adam.eps, _p(self.flat.count),
-                          step)
+                self._optimizer_step(st, step)
+        self._finish_logs(st, self.E * self.M)
         self._call("ppo_count_advance", st, _p(self.flat.count), self.E * self.M)
+
+    # Up to this many norm partials every Adam block folds itself; above it one
+    # block folds them first (a launch of its own).
+    FOLD_NORM_MAX = 1024
+
+    def _optimizer_step(self, st, step):
+        """Gradient assembly (fixed-order sum of the split partials, with the
+        squared-norm partials), then global-norm clip + Adam (ppo.py:182-191)."""
+        chain = self.chain
+        adam = chain.adam
+        max_norm = chain.max_grad_norm if chain.max_grad_norm is not None else 0.0
+        self._call("ppo_grad_reduce", st, _p(self.SEGS), _p(self.CHUNKS), self.nchunks, _p(self.SUMSQ))
+        if self.nchunks <= self.FOLD_NORM_MAX:
+            norm, nnorm = _p(self.SUMSQ), self.nchunks
+        else:
+            self._call("ppo_sumsq_total", st, _p(self.SUMSQ), self.nchunks, _p(self.SUMSQ1))
+            norm, nnorm = _p(self.SUMSQ1), 1
+        self._call("ppo_adam_clip_f32", st, _p(self.flat.P), _p(self.flat.G), _p(self.flat.MU), _p(self.flat.NU),
+                   _p(self.P16) if self.obs16 else None, self.flat.P.numel(), norm, nnorm, float(max_norm),
+                   adam.learning_rate, adam.b1, adam.b2, adam.eps, _p(self.flat.count), step)
+
+    def _stats(self, step: int) -> int:
+        """Loss-statistics partials of optimizer step ``step``."""
+        return _p(self.STATS) + 8 * step * self.loss_blocks * self.nstat
+
+    def _finish_logs(self, st, steps: int):
+        """The logged scalars of the first ``steps`` optimizer steps (ppo.py:170-180)
+        from their loss statistics, in one launch after the last step."""
+        cfg = self.cfg
+        self._call("ppo_loss_finalize_steps", st, _p(self.STATS), self.loss_blocks, self.mb, steps,
+                   float(cfg.entropy_coefficient), float(cfg.value_coefficient), _p(self.LOGS))
 
     def _head_a_io(self, la: LayerBufs):
         """(input, ld, cotangent destination, act, aux, ldaux) of head group a:
@@ -778,11 +804,9 @@ class MLPExecutor(ForwardChain):
         self._call("ppo_head_loss_f32", st, dist, mb, idx, ya, ldya, self.flat.view(h.w), h.w.ld,
                    self.flat.view(h.b), na, *c_args, h.fin, A, scale_ptr, act_i, act_f, inp["log_prob"],
                    inp["value"], _p(self.ADV), _p(self.RET), acta, auxa, ldauxa, da, ldya, *cd_args,
-                   _p(wpa), _p(bpa), _p(wpc), _p(bpc), _p(self.DSCALE), _p(self.STATS),
+                   _p(wpa), _p(bpa), _p(wpc), _p(bpc), _p(self.DSCALE), self._stats(step),
                    float(cfg.clip_coefficient), int(cfg.clip_value_loss), float(cfg.entropy_coefficient),
                    float(cfg.value_coefficient), 1.0)
-        self._call("ppo_loss_finalize", st, _p(self.STATS), self.loss_blocks, mb, float(cfg.entropy_coefficient),
-                   float(cfg.value_coefficient), _p(self.LOGS) + 4 * 9 * step)
 
     def _minibatch(self, st, idx, step, obs, ldo, dist, A):
         prog, cfg, inp, mb = self.prog, self.cfg, self.inp, self.mb
@@ -815,10 +839,8 @@ class MLPExecutor(ForwardChain):
             vcol = prog.head_out
             self._call("ppo_loss_f32", st, dist, mb, idx, _p(self.HEAD), h.w.ld, _p(self.HEAD) + 4 * vcol, h.w.ld,
                       A, scale_ptr, act_i, act_f, inp["log_prob"], inp["value"], _p(self.ADV), _p(self.RET),
-                      _p(self.DHEAD), _p(self.DHEAD) + 4 * vcol, _p(self.DSCALE), _p(self.STATS), clip,
+                      _p(self.DHEAD), _p(self.DHEAD) + 4 * vcol, _p(self.DSCALE), self._stats(step), clip,
                       int(cfg.clip_value_loss), float(cfg.entropy_coefficient), float(cfg.value_coefficient), 1.0)
-            self._call("ppo_loss_finalize", st, _p(self.STATS), self.loss_blocks, mb,
-                      float(cfg.entropy_coefficient), float(cfg.value_coefficient), _p(self.LOGS) + 4 * 9 * step)
             self._head_back(st, self.trunk, self.DHEAD, h, self.HWPART, self.HBPART, self.head_splits, hx, ldhx,
                             hidx)
             self._bwd_layers(st, self.trunk, obs, ldo, idx)
@@ -836,10 +858,8 @@ class MLPExecutor(ForwardChain):
             self._join(st, s2)
             self._call("ppo_loss_f32", st, dist, mb, idx, _p(self.HA), ha.w.ld, _p(self.HC), hc.w.ld, A, scale_ptr,
                       act_i, act_f, inp["log_prob"], inp["value"], _p(self.ADV), _p(self.RET), _p(self.DHA),
-                      _p(self.DHC), _p(self.DSCALE), _p(self.STATS), clip, int(cfg.clip_value_loss),
+                      _p(self.DHC), _p(self.DSCALE), self._stats(step), clip, int(cfg.clip_value_loss),
                       float(cfg.entropy_coefficient), float(cfg.value_coefficient), 1.0)
-            self._call("ppo_loss_finalize", st, _p(self.STATS), self.loss_blocks, mb,
-                      float(cfg.entropy_coefficient), float(cfg.value_coefficient), _p(self.LOGS) + 4 * 9 * step)
             s2 = self._fork(st)
             self._head_back(st, self.actor, self.DHA, ha, self.HAWPART, self.HABPART, self.ha_splits, ax, ldax,
                             aidx)

@@ -142,22 +142,17 @@ class RecurrentExecutor(MLPExecutor):
                    self.PERM_WS.numel())
         self._call("ppo_sequence_rows", st, _p(self.PERM), self.E * self.M, T, N, Bm, _p(self.ROWS))
         # 4. minibatch steps
-        adam = chain.adam
-        max_norm = chain.max_grad_norm if chain.max_grad_norm is not None else 0.0
         for e in range(self.E):
             for m in range(self.M):
                 step = e * self.M + m
                 if max_steps is not None and step >= max_steps:
+                    self._finish_logs(st, step)
                     return
                 rows = _p(self.ROWS) + 4 * step * mb
                 envs = _p(self.PERM) + 4 * (e * N + m * Bm)
                 self._sequence_minibatch(st, rows, envs, step)
-                self._call("ppo_grad_reduce", st, _p(self.SEGS), _p(self.CHUNKS), self.nchunks, _p(self.SUMSQ))
-                self._call("ppo_sumsq_total", st, _p(self.SUMSQ), self.nchunks, _p(self.SUMSQ1))
-                self._call("ppo_adam_clip_f32", st, _p(self.flat.P), _p(self.flat.G), _p(self.flat.MU),
-                           _p(self.flat.NU), None, self.flat.P.numel(), _p(self.SUMSQ1), 1,
-                           float(max_norm), adam.learning_rate, adam.b1, adam.b2, adam.eps, _p(self.flat.count),
-                           step)
+                self._optimizer_step(st, step)
+        self._finish_logs(st, self.E * self.M)
         self._call("ppo_count_advance", st, _p(self.flat.count), self.E * self.M)
 
     def _sequence_minibatch(self, st, rows, envs, step):

@@ -237,6 +237,12 @@ int ppo_loss_f32(void* stream, int dist, int rows, const int32_t* idx, const flo
 /* The logged scalars of ppo.py:170-179 in order, then the total loss: out9[9]. */
 int ppo_loss_finalize(void* stream, const double* stats_partial, int nblocks, int rows, float ent_coef,
                       float vf_coef, float* out9);
+/* The same for `steps` optimizer steps at once, off the minibatch chain:
+ * stats_partial [steps][nblocks][11] -> out [steps][9] (one launch per update
+ * instead of one per step; the logs of ppo.py:170-180 are not an input of any
+ * later step). */
+int ppo_loss_finalize_steps(void* stream, const double* stats_partial, int nblocks, int rows, int steps,
+                            float ent_coef, float vf_coef, float* out);
 
 /* Fused heads + loss + head backward: one wavefront per sample row reads the
  * torso output once.  Group a is the actor head, or both heads packed into one

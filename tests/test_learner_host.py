@@ -56,7 +56,8 @@ def test_recorded_launches_match_the_c_signatures(config):
         assert names.count("ppo_gru_bwd_step_f32") == steps * r.T
         assert names.count("ppo_sequence_rows") == 1
     assert names.count("ppo_adam_clip_f32") == steps
-    assert names.count("ppo_loss_finalize") == steps
+    assert names.count("ppo_loss_finalize_steps") == 1 and "ppo_loss_finalize" not in names
+    assert names.count("ppo_sumsq_total") == (0 if ex.nchunks <= ex.FOLD_NORM_MAX else steps)
     if prog.bf16:
         # 43 actions: the unfused head GEMM + loss + head backward, every GEMM on bf16 MFMA
         assert names.count("ppo_loss_f32") == steps and "ppo_gemm_f32" not in names
