@@ -262,51 +262,98 @@ __device__ __forceinline__ float softplusf(float x) {
 
 constexpr float LOG_2PI = 1.8378770664093453f;
 
-__global__ void __launch_bounds__(ROW_THREADS) ppo_loss_kernel(LossParams p) {
-  __shared__ double sred[ROW_THREADS / 64][NSTAT];
-  __shared__ float sscale[ROW_THREADS / 64][64];
+// One 16-lane group per row: lane j0 of the group owns head outputs j0,
+// j0 + 16, ... (A <= 64); the row's log-softmax or log-density and entropy are
+// 16-lane butterflies, the scalar clip and value terms are evaluated by every
+// lane of the group alike, and lane 0 of the group adds the row to the block's
+// statistics.  Rows are walked in block-sized strides; a group whose row is
+// past the end idles through the iteration (its butterflies stay inside it).
+constexpr int LOSS_THREADS = 256;
+constexpr int LOSS_GROUP = 16;
+constexpr int LOSS_ROWS = LOSS_THREADS / LOSS_GROUP;
+constexpr int LOSS_K = 4;  // head outputs per lane
+
+__device__ __forceinline__ float group16_sum(float v) {
+#pragma unroll
+  for (int o = LOSS_GROUP / 2; o; o >>= 1) v += __shfl_xor(v, o, LOSS_GROUP);
+  return v;
+}
+__device__ __forceinline__ float group16_max(float v) {
+#pragma unroll
+  for (int o = LOSS_GROUP / 2; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, LOSS_GROUP));
+  return v;
+}
+
+__global__ void __launch_bounds__(LOSS_THREADS) ppo_loss_kernel(LossParams p) {
+  __shared__ double sred[LOSS_THREADS / 64][NSTAT];
+  __shared__ float sscale[LOSS_THREADS / 64][LOSS_GROUP];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int j0 = threadIdx.x % LOSS_GROUP;
+  const int grow = threadIdx.x / LOSS_GROUP;
   double st[NSTAT];
 #pragma unroll
   for (int i = 0; i < NSTAT; ++i) st[i] = 0.0;
-  float dscale_acc[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) dscale_acc[j] = 0.f;
+  float dscale_acc = 0.f;  // state-independent scale: output j0 (D <= 16)
   const float eps = p.clip_eps;
+  const float inv_t = 1.f / p.temperature;
 
-  for (int r = blockIdx.x * ROW_THREADS + threadIdx.x; r < p.rows; r += gridDim.x * ROW_THREADS) {
+  for (int r0 = blockIdx.x * LOSS_ROWS; r0 < p.rows; r0 += gridDim.x * LOSS_ROWS) {
+    const int r = r0 + grow;
+    if (r >= p.rows) continue;
     const int64_t s = p.idx ? (int64_t)p.idx[r] : (int64_t)r;
     const float* hr = p.head + (int64_t)r * p.ldh;
     float* dr = p.dhead + (int64_t)r * p.ldh;
     float lp, ent;
+    float c[LOSS_K];
+    float lse = 0.f;
+    int a = -1;
     if (p.dist == DIST_CATEGORICAL) {
-      const float inv_t = 1.f / p.temperature;
       float mx = -INFINITY;
-      for (int j = 0; j < p.A; ++j) mx = fmaxf(mx, hr[j] * inv_t);
+#pragma unroll
+      for (int k = 0; k < LOSS_K; ++k) {
+        const int j = j0 + LOSS_GROUP * k;
+        c[k] = j < p.A ? hr[j] * inv_t : -INFINITY;
+        mx = fmaxf(mx, c[k]);
+      }
+      mx = group16_max(mx);
       float se = 0.f;
-      for (int j = 0; j < p.A; ++j) se += __expf(hr[j] * inv_t - mx);
-      const float lse = mx + __logf(se);
-      const int a = p.action_i[s];
-      // distrax: log_prob of a value outside [0, A) is -inf (never read past the row)
-      lp = (a >= 0 && a < p.A) ? hr[a] * inv_t - lse : -INFINITY;
-      ent = 0.f;
-      for (int j = 0; j < p.A; ++j) {
-        const float lq = hr[j] * inv_t - lse;
-        ent -= __expf(lq) * lq;
+#pragma unroll
+      for (int k = 0; k < LOSS_K; ++k)
+        if (j0 + LOSS_GROUP * k < p.A) se += __expf(c[k] - mx);
+      lse = mx + __logf(group16_sum(se));
+      a = p.action_i[s];
+      float lpa = 0.f, en = 0.f;
+#pragma unroll
+      for (int k = 0; k < LOSS_K; ++k) {
+        const int j = j0 + LOSS_GROUP * k;
+        if (j < p.A) {
+          const float lq = c[k] - lse;
+          if (j == a) lpa = lq;
+          en -= __expf(lq) * lq;
+        }
       }
+      // distrax: log_prob of a value outside [0, A) is -inf
+      const float lpsum = group16_sum(lpa);
+      lp = (a >= 0 && a < p.A) ? lpsum : -INFINITY;
+      ent = group16_sum(en);
     } else {
-      lp = 0.f;
-      ent = 0.f;
+      float l = 0.f, e = 0.f;
       const float* act = p.action_f + s * p.A;
-      for (int j = 0; j < p.A; ++j) {
-        const float raw = p.scale_param ? p.scale_param[j] : hr[p.A + j];
-        const float sig = p.temperature * (softplusf(raw) + 1e-3f);
-        const float zz = (act[j] - hr[j]) / sig;
-        const float ls = __logf(sig);
-        lp += -0.5f * zz * zz - ls - 0.5f * LOG_2PI;
-        ent += 0.5f + 0.5f * LOG_2PI + ls;
+#pragma unroll
+      for (int k = 0; k < LOSS_K; ++k) {
+        const int j = j0 + LOSS_GROUP * k;
+        if (j < p.A) {
+          const float raw = p.scale_param ? p.scale_param[j] : hr[p.A + j];
+          const float sig = p.temperature * (softplusf(raw) + 1e-3f);
+          const float zz = (act[j] - hr[j]) / sig;
+          const float ls = __logf(sig);
+          l += -0.5f * zz * zz - ls - 0.5f * LOG_2PI;
+          e += 0.5f + 0.5f * LOG_2PI + ls;
+        }
       }
+      lp = group16_sum(l);
+      ent = group16_sum(e);
     }
     const float olp = p.old_logp[s];
     const float A = p.adv[s];
@@ -338,53 +385,56 @@ __global__ void __launch_bounds__(ROW_THREADS) ppo_loss_kernel(LossParams p) {
       crow = vl1;
       gv = v - R;
     }
-    p.dvalue[(int64_t)r * p.ldv] = p.vf_coef * gv * p.inv_n;
+    if (j0 == 0) p.dvalue[(int64_t)r * p.ldv] = p.vf_coef * gv * p.inv_n;
 
     // cotangents of the head outputs
     if (p.dist == DIST_CATEGORICAL) {
-      const float inv_t = 1.f / p.temperature;
-      float mx = -INFINITY;
-      for (int j = 0; j < p.A; ++j) mx = fmaxf(mx, hr[j] * inv_t);
-      float se = 0.f;
-      for (int j = 0; j < p.A; ++j) se += __expf(hr[j] * inv_t - mx);
-      const float lse = mx + __logf(se);
-      const int a = p.action_i[s];
-      for (int j = 0; j < p.A; ++j) {
-        const float lq = hr[j] * inv_t - lse;
-        const float q = __expf(lq);
-        const float d = g_lp * ((j == a ? 1.f : 0.f) - q) - g_ent * q * (lq + ent);
-        dr[j] = d * inv_t;
+#pragma unroll
+      for (int k = 0; k < LOSS_K; ++k) {
+        const int j = j0 + LOSS_GROUP * k;
+        if (j < p.A) {
+          const float lq = c[k] - lse;
+          const float q = __expf(lq);
+          const float d = g_lp * ((j == a ? 1.f : 0.f) - q) - g_ent * q * (lq + ent);
+          dr[j] = d * inv_t;
+        }
       }
     } else {
       const float* act = p.action_f + s * p.A;
-      for (int j = 0; j < p.A; ++j) {
-        const float raw = p.scale_param ? p.scale_param[j] : hr[p.A + j];
-        const float sp = softplusf(raw);
-        const float sig = p.temperature * (sp + 1e-3f);
-        const float d = act[j] - hr[j];
-        dr[j] = g_lp * d / (sig * sig);
-        const float dsig = g_lp * (d * d / (sig * sig * sig) - 1.f / sig) + g_ent / sig;
-        const float draw = dsig * p.temperature / (1.f + __expf(-raw));
-        if (p.scale_param) {
-          if (j < 16) dscale_acc[j] += draw;
-        } else {
-          dr[p.A + j] = draw;
+#pragma unroll
+      for (int k = 0; k < LOSS_K; ++k) {
+        const int j = j0 + LOSS_GROUP * k;
+        if (j < p.A) {
+          const float raw = p.scale_param ? p.scale_param[j] : hr[p.A + j];
+          const float sp = softplusf(raw);
+          const float sig = p.temperature * (sp + 1e-3f);
+          const float d = act[j] - hr[j];
+          dr[j] = g_lp * d / (sig * sig);
+          const float dsig = g_lp * (d * d / (sig * sig * sig) - 1.f / sig) + g_ent / sig;
+          const float draw = dsig * p.temperature / (1.f + __expf(-raw));
+          if (p.scale_param) {
+            dscale_acc += draw;  // k = 0: D <= 16
+          } else {
+            dr[p.A + j] = draw;
+          }
         }
       }
     }
 
-    st[ST_ACTOR] += (double)(-pmin);
-    st[ST_ENTROPY] += (double)ent;
-    st[ST_KL] += (double)(olp - lp);
-    st[ST_CLIPFRAC] += (fabsf(ratio - 1.f) > eps) ? 1.0 : 0.0;
-    st[ST_ADV] += (double)A;
-    st[ST_CRITIC] += (double)crow;
-    const double res = (double)R - (double)v;
-    st[ST_RESID] += res;
-    st[ST_RESID2] += res * res;
-    st[ST_RET] += (double)R;
-    st[ST_RET2] += (double)R * (double)R;
-    st[ST_VALUE] += (double)v;
+    if (j0 == 0) {
+      st[ST_ACTOR] += (double)(-pmin);
+      st[ST_ENTROPY] += (double)ent;
+      st[ST_KL] += (double)(olp - lp);
+      st[ST_CLIPFRAC] += (fabsf(ratio - 1.f) > eps) ? 1.0 : 0.0;
+      st[ST_ADV] += (double)A;
+      st[ST_CRITIC] += (double)crow;
+      const double res = (double)R - (double)v;
+      st[ST_RESID] += res;
+      st[ST_RESID2] += res * res;
+      st[ST_RET] += (double)R;
+      st[ST_RET2] += (double)R * (double)R;
+      st[ST_VALUE] += (double)v;
+    }
   }
 
 #pragma unroll
@@ -393,21 +443,21 @@ __global__ void __launch_bounds__(ROW_THREADS) ppo_loss_kernel(LossParams p) {
     if (lane == 0) sred[wave][i] = t;
   }
   if (p.scale_param) {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const float t = ppo::wave_sum(dscale_acc[j]);
-      if (lane == 0) sscale[wave][j] = t;
-    }
+    // the wave's four groups hold the same outputs: fold them, lanes 0-15 keep the sums
+    float v = dscale_acc;
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    if (lane < LOSS_GROUP) sscale[wave][lane] = v;
   }
   __syncthreads();
   if (threadIdx.x < NSTAT) {
     double t = 0.0;
-    for (int w = 0; w < ROW_THREADS / 64; ++w) t += sred[w][threadIdx.x];
+    for (int w = 0; w < LOSS_THREADS / 64; ++w) t += sred[w][threadIdx.x];
     p.stats_partial[(int64_t)blockIdx.x * NSTAT + threadIdx.x] = t;
   }
   if (p.scale_param && threadIdx.x < p.A) {
     float t = 0.f;
-    for (int w = 0; w < ROW_THREADS / 64; ++w) t += sscale[w][threadIdx.x];
+    for (int w = 0; w < LOSS_THREADS / 64; ++w) t += sscale[w][threadIdx.x];
     p.dscale_partial[(int64_t)blockIdx.x * p.A + threadIdx.x] = t;
   }
 }
@@ -585,7 +635,7 @@ PPO_EXPORT int ppo_act_bwd_f32(void* stream, const float* dy, int64_t lddy, cons
 }
 
 PPO_EXPORT int ppo_loss_blocks(int rows) {
-  return std::max(1, std::min(ppo::ceil_div(rows, ROW_THREADS), 1024));
+  return std::max(1, std::min(ppo::ceil_div(rows, LOSS_ROWS), 1024));
 }
 
 PPO_EXPORT int ppo_loss_stat_count(void) { return NSTAT; }
@@ -612,7 +662,7 @@ PPO_EXPORT int ppo_loss_f32(void* stream, int dist, int rows, const int32_t* idx
   p.dscale_partial = dscale_partial; p.stats_partial = stats_partial; p.clip_eps = clip_eps;
   p.clip_value_loss = clip_value_loss; p.ent_coef = ent_coef; p.vf_coef = vf_coef; p.inv_n = 1.f / (float)rows;
   p.temperature = temperature;
-  hipLaunchKernelGGL(ppo_loss_kernel, dim3(ppo_loss_blocks(rows)), dim3(ROW_THREADS), 0, ppo::as_stream(stream), p);
+  hipLaunchKernelGGL(ppo_loss_kernel, dim3(ppo_loss_blocks(rows)), dim3(LOSS_THREADS), 0, ppo::as_stream(stream), p);
   return ppo::check_launch("ppo_loss_f32");
 }
 
