@@ -242,6 +242,170 @@ __global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_bwd_kernel(ScanArgs p) {
   if (t == 0 && t >= t0) step(0, true, true);
 }
 
+// Register-resident chunks: each wave loads its chunk of at most RL steps once
+// (all loads issued before the first multiply-add), folds it into its affine
+// map, exchanges the maps through LDS, and writes its outputs from the same
+// registers, so chunking costs no second read of the operands.  Steps past
+// the chunk's end hold the identity map (a = 1, b = 0 forward; alpha = 1,
+// g = 0 backward).
+constexpr int RL = 8;
+
+template <typename S, int VW>
+__global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_fwd_reg_kernel(ScanArgs p) {
+  extern __shared__ float smem[];
+  float* sA = smem;
+  float* sB = smem + (blockDim.x >> 6) * 64 * VW;
+  const S* a = static_cast<const S*>(p.a);
+  const S* b = static_cast<const S*>(p.b);
+  const S* init = static_cast<const S*>(p.init);
+  S* out = static_cast<S*>(p.out);
+  const int lane = threadIdx.x & 63, c = threadIdx.x >> 6, C = blockDim.x >> 6;
+  const int f0 = (blockIdx.x * 64 + lane) * VW;
+  const bool ok = f0 < p.F;
+  const int64_t n = blockIdx.y;
+  const int t0 = c * RL, t1 = min(p.steps, t0 + RL);
+  const int64_t base = n * (int64_t)p.steps * p.F + f0;
+  float av[RL][VW], bv[RL][VW], h[VW];
+#pragma unroll
+  for (int i = 0; i < RL; ++i) {
+    if (ok && t0 + i < t1) {
+      load_vec(a, base + (int64_t)(t0 + i) * p.F, av[i]);
+      load_vec(b, base + (int64_t)(t0 + i) * p.F, bv[i]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < VW; ++k) { av[i][k] = 1.f; bv[i][k] = 0.f; }
+    }
+  }
+  if (ok) {
+    load_vec(init, n * (int64_t)p.F + f0, h);
+  } else {
+#pragma unroll
+    for (int k = 0; k < VW; ++k) h[k] = 0.f;
+  }
+  if (C > 1) {
+    float A[VW], B[VW];
+#pragma unroll
+    for (int k = 0; k < VW; ++k) { A[k] = 1.f; B[k] = 0.f; }
+#pragma unroll
+    for (int i = 0; i < RL; ++i) {
+#pragma unroll
+      for (int k = 0; k < VW; ++k) {
+        A[k] = av[i][k] * A[k];
+        B[k] = av[i][k] * B[k] + bv[i][k];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+      sA[(c * 64 + lane) * VW + k] = A[k];
+      sB[(c * 64 + lane) * VW + k] = B[k];
+    }
+    __syncthreads();
+    for (int cc = 0; cc < c; ++cc) {
+#pragma unroll
+      for (int k = 0; k < VW; ++k) h[k] = sA[(cc * 64 + lane) * VW + k] * h[k] + sB[(cc * 64 + lane) * VW + k];
+    }
+  }
+  if (!ok) return;
+#pragma unroll
+  for (int i = 0; i < RL; ++i) {
+#pragma unroll
+    for (int k = 0; k < VW; ++k) h[k] = av[i][k] * h[k] + bv[i][k];
+    if (t0 + i < t1) store_vec(out, base + (int64_t)(t0 + i) * p.F, h);
+  }
+}
+
+template <typename S, int VW>
+__global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_bwd_reg_kernel(ScanArgs p) {
+  extern __shared__ float smem[];
+  float* sA = smem;
+  float* sB = smem + (blockDim.x >> 6) * 64 * VW;
+  const S* a = static_cast<const S*>(p.a);
+  const S* g = static_cast<const S*>(p.b);
+  const S* hs = static_cast<const S*>(p.h);
+  const S* init = static_cast<const S*>(p.init);
+  S* db = static_cast<S*>(p.out);
+  S* da = static_cast<S*>(p.da);
+  S* dinit = static_cast<S*>(p.dinit);
+  const int lane = threadIdx.x & 63, c = threadIdx.x >> 6, C = blockDim.x >> 6;
+  const int f0 = (blockIdx.x * 64 + lane) * VW;
+  const bool ok = f0 < p.F;
+  const int64_t n = blockIdx.y;
+  const int t0 = c * RL, t1 = min(p.steps, t0 + RL);
+  const int64_t base = n * (int64_t)p.steps * p.F + f0;
+  // al[i] = a_{t+1} (0 past the last step), gv[i] = g_t, hp[i] = h_{t-1} (init at t = 0)
+  float al[RL][VW], gv[RL][VW], hp[RL][VW];
+#pragma unroll
+  for (int i = 0; i < RL; ++i) {
+    const int t = t0 + i;
+    if (ok && t < t1) {
+      if (t + 1 < p.steps) {
+        load_vec(a, base + (int64_t)(t + 1) * p.F, al[i]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < VW; ++k) al[i][k] = 0.f;
+      }
+      load_vec(g, base + (int64_t)t * p.F, gv[i]);
+      if (t > 0) {
+        load_vec(hs, base + (int64_t)(t - 1) * p.F, hp[i]);
+      } else {
+        load_vec(init, n * (int64_t)p.F + f0, hp[i]);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < VW; ++k) { al[i][k] = 1.f; gv[i][k] = 0.f; hp[i][k] = 0.f; }
+    }
+  }
+  float d[VW];
+#pragma unroll
+  for (int k = 0; k < VW; ++k) d[k] = 0.f;
+  if (C > 1) {
+    float P[VW], Q[VW];
+#pragma unroll
+    for (int k = 0; k < VW; ++k) { P[k] = 1.f; Q[k] = 0.f; }
+#pragma unroll
+    for (int i = RL - 1; i >= 0; --i) {
+#pragma unroll
+      for (int k = 0; k < VW; ++k) {
+        P[k] = al[i][k] * P[k];
+        Q[k] = al[i][k] * Q[k] + gv[i][k];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+      sA[(c * 64 + lane) * VW + k] = P[k];
+      sB[(c * 64 + lane) * VW + k] = Q[k];
+    }
+    __syncthreads();
+    for (int cc = C - 1; cc > c; --cc) {
+#pragma unroll
+      for (int k = 0; k < VW; ++k) d[k] = sA[(cc * 64 + lane) * VW + k] * d[k] + sB[(cc * 64 + lane) * VW + k];
+    }
+  }
+  if (!ok) return;
+#pragma unroll
+  for (int i = RL - 1; i >= 0; --i) {
+    const int t = t0 + i;
+    float dv[VW], dav[VW];
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+      d[k] = al[i][k] * d[k] + gv[i][k];
+      dv[k] = stored(d[k], db);
+      dav[k] = dv[k] * hp[i][k];
+    }
+    if (t < t1) {
+      store_vec(db, base + (int64_t)t * p.F, d);
+      store_vec(da, base + (int64_t)t * p.F, dav);
+      if (t == 0) {
+        float a0[VW], di[VW];
+        load_vec(a, base, a0);
+#pragma unroll
+        for (int k = 0; k < VW; ++k) di[k] = dv[k] * a0[k];
+        store_vec(dinit, n * (int64_t)p.F + f0, di);
+      }
+    }
+  }
+}
+
 bool aligned(const void* ptr, int bytes) { return (reinterpret_cast<uintptr_t>(ptr) % bytes) == 0; }
 
 template <typename S, int VW, bool BWD>
@@ -255,6 +419,20 @@ int launch(hipStream_t st, const ScanArgs& p, int batch) {
     hipLaunchKernelGGL((scan_bwd_kernel<S, VW>), grid, block, lds, st, p);
   } else {
     hipLaunchKernelGGL((scan_fwd_kernel<S, VW>), grid, block, lds, st, p);
+  }
+  return PPO_OK;
+}
+
+template <typename S, int VW, bool BWD>
+int launch_reg(hipStream_t st, const ScanArgs& p, int batch) {
+  const int groups = ppo::ceil_div(ppo::ceil_div(p.F, VW), 64);
+  const int C = ppo::ceil_div(p.steps, RL);
+  dim3 grid(groups, batch), block(64 * C);
+  const size_t lds = C > 1 ? 2 * sizeof(float) * (size_t)C * 64 * VW : 0;
+  if (BWD) {
+    hipLaunchKernelGGL((scan_bwd_reg_kernel<S, VW>), grid, block, lds, st, p);
+  } else {
+    hipLaunchKernelGGL((scan_fwd_reg_kernel<S, VW>), grid, block, lds, st, p);
   }
   return PPO_OK;
 }
@@ -273,6 +451,16 @@ int dispatch(hipStream_t st, int dtype, ScanArgs p, int batch, const char* what)
     if (q && !aligned(q, 4 * esize)) vec = false;
   const int VW = vec ? 4 : 1;
   const int64_t waves = (int64_t)batch * ppo::ceil_div(ppo::ceil_div(p.F, VW), 64);
+  if (p.steps > RL && p.steps <= RL * MAX_CHUNKS) {
+    // register-resident chunks of RL steps: no re-read, every load in flight at once
+    p.chunk = RL;
+    if (dtype == SCAN_F32) {
+      if (vec) launch_reg<float, 4, BWD>(st, p, batch); else launch_reg<float, 1, BWD>(st, p, batch);
+    } else {
+      if (vec) launch_reg<uint16_t, 4, BWD>(st, p, batch); else launch_reg<uint16_t, 1, BWD>(st, p, batch);
+    }
+    return ppo::check_launch(what);
+  }
   // bf16 rows carry half the bytes per load, so bf16 wants more waves in
   // flight before the re-read of a second pass stops paying (measured on
   // [1024, 64, 256]: float32 forward 49 -> 33 us without chunks, bf16 forward
