@@ -42,6 +42,8 @@ SIGNATURES = {
     "ppo_sample_gaussian_f32": (I, [P, P, I64, P, I64, I, I, P, I64, P, F, P, I64, P, P]),
     "ppo_linear_scan_fwd": (I, [P, I, P, P, P, P, I, I, I]),
     "ppo_linear_scan_bwd": (I, [P, I, P, P, P, P, P, P, P, I, I, I]),
+    "ppo_ssm_scan_fwd": (I, [P, I, P, P, P, P, P, P, I, I, I]),
+    "ppo_ssm_scan_bwd": (I, [P, I, P, P, P, P, P, P, P, P, P, I, I, I]),
     "ppo_gemm_f32": (I, [P, I, I, P, I64, P, P, I64, P, I64, I, I, I, I, I64, I, P, I, P, P, I64, P, I]),
     "ppo_gemm_bf16": (I, [P, I, I, P, I64, P, P, I64, P, I64, I, I, I, I, I64, I, P, I, I, P, I64, P, I]),
     "ppo_round_bf16": (I, [P, P, I64]),

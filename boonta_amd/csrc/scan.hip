@@ -13,6 +13,12 @@
 //           for bf16 storage da and dinit multiply the stored (rounded) db and
 //           are rounded again, as the reference's bf16 array arithmetic does.
 //
+// The SSM block's episode resets (networks/blocks/ssm.py:45-48) can be folded
+// into the same launches (ppo_ssm_scan_*): where done[n, t], the step's decay
+// becomes 0 and its input b + a r (r the carry a reset restarts from, zeros
+// by default), and the backward carries the reset's own chain rule (da = r db
+// there, and no decay into the step).
+//
 // Layout and parallelism: element (n, t, f) at (n * steps + t) * features + f.
 // Each lane owns VW = 4 consecutive features of one sequence where the rows
 // allow (one 16-byte float32 or 8-byte bf16 access), so every step reads one
@@ -74,7 +80,67 @@ struct ScanArgs {
   void* da;
   void* dinit;
   int steps, F, chunk;
+  const uint8_t* done;  // [batch, steps] episode starts of the SSM block, or null
+  const void* reset;    // [batch, features] carry a done step restarts from, or null (zeros)
 };
+
+// The SSM block's reset (networks/blocks/ssm.py:45-48) applied to step t's
+// operands: where done, b' = b + a * r and a' = 0, in the storage type's
+// arithmetic (each product and sum rounded for bf16).
+__device__ __forceinline__ bool is_done(const ScanArgs& p, int64_t n, int t) {
+  return p.done && p.done[n * p.steps + t];
+}
+
+template <typename S, int VW>
+__device__ __forceinline__ void load_reset(const ScanArgs& p, int64_t n, int f0, float (&rv)[VW]) {
+  if (p.reset) {
+    load_vec(static_cast<const S*>(p.reset), n * (int64_t)p.F + f0, rv);
+  } else {
+#pragma unroll
+    for (int k = 0; k < VW; ++k) rv[k] = 0.f;
+  }
+}
+
+template <typename S, int VW>
+__device__ __forceinline__ void load_ab(const ScanArgs& p, const S* a, const S* b, int64_t base, int64_t n, int t,
+                                        int f0, float (&av)[VW], float (&bv)[VW]) {
+  load_vec(a, base + (int64_t)t * p.F, av);
+  load_vec(b, base + (int64_t)t * p.F, bv);
+  if (is_done(p, n, t)) {
+    float rv[VW];
+    load_reset<S, VW>(p, n, f0, rv);
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+      bv[k] = stored(bv[k] + stored(av[k] * rv[k], a), a);
+      av[k] = 0.f;
+    }
+  }
+}
+
+// alpha_t = a'_{t+1}, the (reset) decay of the next step; 0 past the last step
+template <typename S, int VW>
+__device__ __forceinline__ void load_alpha(const ScanArgs& p, const S* a, int64_t base, int64_t n, int t,
+                                           float (&al)[VW]) {
+  if (t + 1 < p.steps && !is_done(p, n, t + 1)) {
+    load_vec(a, base + (int64_t)(t + 1) * p.F, al);
+  } else {
+#pragma unroll
+    for (int k = 0; k < VW; ++k) al[k] = 0.f;
+  }
+}
+
+// da_t: db'_t h_{t-1} where step t was not reset; r db'_t where it was (the
+// cotangent of a through b' = b + a r; a' = 0 passes none)
+template <typename S, int VW>
+__device__ __forceinline__ void reset_da(const ScanArgs& p, const S* a, int64_t n, int t, int f0,
+                                         const float (&dv)[VW], float (&dav)[VW]) {
+  if (is_done(p, n, t)) {
+    float rv[VW];
+    load_reset<S, VW>(p, n, f0, rv);
+#pragma unroll
+    for (int k = 0; k < VW; ++k) dav[k] = stored(rv[k] * dv[k], a);
+  }
+}
 
 template <typename S, int VW>
 __global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_fwd_kernel(ScanArgs p) {
@@ -107,8 +173,7 @@ __global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_fwd_kernel(ScanArgs p) {
 #pragma unroll 4
       for (int t = t0; t < t1; ++t) {
         float av[VW], bv[VW];
-        load_vec(a, base + (int64_t)t * p.F, av);
-        load_vec(b, base + (int64_t)t * p.F, bv);
+        load_ab<S, VW>(p, a, b, base, n, t, f0, av, bv);
 #pragma unroll
         for (int k = 0; k < VW; ++k) {
           A[k] = av[k] * A[k];
@@ -131,8 +196,7 @@ __global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_fwd_kernel(ScanArgs p) {
 #pragma unroll 8
   for (int t = t0; t < t1; ++t) {
     float av[VW], bv[VW];
-    load_vec(a, base + (int64_t)t * p.F, av);
-    load_vec(b, base + (int64_t)t * p.F, bv);
+    load_ab<S, VW>(p, a, b, base, n, t, f0, av, bv);
 #pragma unroll
     for (int k = 0; k < VW; ++k) h[k] = av[k] * h[k] + bv[k];
     store_vec(out, base + (int64_t)t * p.F, h);
@@ -170,12 +234,7 @@ __global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_bwd_kernel(ScanArgs p) {
 #pragma unroll 4
       for (int t = t1 - 1; t >= t0; --t) {
         float al[VW], gv[VW];
-        if (t + 1 < p.steps) {
-          load_vec(a, base + (int64_t)(t + 1) * p.F, al);
-        } else {
-#pragma unroll
-          for (int k = 0; k < VW; ++k) al[k] = 0.f;
-        }
+        load_alpha<S, VW>(p, a, base, n, t, al);
         load_vec(g, base + (int64_t)t * p.F, gv);
 #pragma unroll
         for (int k = 0; k < VW; ++k) {
@@ -201,7 +260,7 @@ __global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_bwd_kernel(ScanArgs p) {
   auto step = [&](int t, bool has_next, bool first) {
     float al[VW], gv[VW], hp[VW];
     if (has_next) {
-      load_vec(a, base + (int64_t)(t + 1) * p.F, al);
+      load_alpha<S, VW>(p, a, base, n, t, al);
     } else {
 #pragma unroll
       for (int k = 0; k < VW; ++k) al[k] = 0.f;
@@ -219,11 +278,16 @@ __global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_bwd_kernel(ScanArgs p) {
       dv[k] = stored(d[k], db);
       dav[k] = dv[k] * hp[k];
     }
+    reset_da<S, VW>(p, a, n, t, f0, dv, dav);
     store_vec(db, base + (int64_t)t * p.F, d);
     store_vec(da, base + (int64_t)t * p.F, dav);
     if (first) {
       float a0[VW], di[VW];
       load_vec(a, base, a0);
+      if (is_done(p, n, 0)) {
+#pragma unroll
+        for (int k = 0; k < VW; ++k) a0[k] = 0.f;
+      }
 #pragma unroll
       for (int k = 0; k < VW; ++k) di[k] = dv[k] * a0[k];
       store_vec(dinit, n * (int64_t)p.F + f0, di);
@@ -269,8 +333,7 @@ __global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_fwd_reg_kernel(ScanArgs 
 #pragma unroll
   for (int i = 0; i < RL; ++i) {
     if (ok && t0 + i < t1) {
-      load_vec(a, base + (int64_t)(t0 + i) * p.F, av[i]);
-      load_vec(b, base + (int64_t)(t0 + i) * p.F, bv[i]);
+      load_ab<S, VW>(p, a, b, base, n, t0 + i, f0, av[i], bv[i]);
     } else {
 #pragma unroll
       for (int k = 0; k < VW; ++k) { av[i][k] = 1.f; bv[i][k] = 0.f; }
@@ -338,12 +401,7 @@ __global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_bwd_reg_kernel(ScanArgs 
   for (int i = 0; i < RL; ++i) {
     const int t = t0 + i;
     if (ok && t < t1) {
-      if (t + 1 < p.steps) {
-        load_vec(a, base + (int64_t)(t + 1) * p.F, al[i]);
-      } else {
-#pragma unroll
-        for (int k = 0; k < VW; ++k) al[i][k] = 0.f;
-      }
+      load_alpha<S, VW>(p, a, base, n, t, al[i]);
       load_vec(g, base + (int64_t)t * p.F, gv[i]);
       if (t > 0) {
         load_vec(hs, base + (int64_t)(t - 1) * p.F, hp[i]);
@@ -393,11 +451,16 @@ __global__ void __launch_bounds__(64 * MAX_CHUNKS) scan_bwd_reg_kernel(ScanArgs 
       dav[k] = dv[k] * hp[i][k];
     }
     if (t < t1) {
+      reset_da<S, VW>(p, a, n, t, f0, dv, dav);
       store_vec(db, base + (int64_t)t * p.F, d);
       store_vec(da, base + (int64_t)t * p.F, dav);
       if (t == 0) {
         float a0[VW], di[VW];
         load_vec(a, base, a0);
+        if (is_done(p, n, 0)) {
+#pragma unroll
+          for (int k = 0; k < VW; ++k) a0[k] = 0.f;
+        }
 #pragma unroll
         for (int k = 0; k < VW; ++k) di[k] = dv[k] * a0[k];
         store_vec(dinit, n * (int64_t)p.F + f0, di);
@@ -445,7 +508,7 @@ int dispatch(hipStream_t st, int dtype, ScanArgs p, int batch, const char* what)
   // give too few waves: then enough chunks for twice that, at most 16, each
   // at least 8 steps long.
   const int esize = dtype == SCAN_F32 ? 4 : 2;
-  const void* ptrs[7] = {p.a, p.b, p.h, p.init, p.out, p.da, p.dinit};
+  const void* ptrs[8] = {p.a, p.b, p.h, p.init, p.out, p.da, p.dinit, p.reset};
   bool vec = p.F % 4 == 0;
   for (const void* q : ptrs)
     if (q && !aligned(q, 4 * esize)) vec = false;
@@ -487,8 +550,20 @@ PPO_EXPORT int ppo_linear_scan_fwd(void* stream, int dtype, const void* a, const
   if (batch == 0 || steps == 0 || features == 0) return PPO_OK;
   if (!a || !b || !init || !out) return ppo::set_error(PPO_ERR_ARG, "ppo_linear_scan_fwd: null buffer");
   if (batch > 65535) return ppo::set_error(PPO_ERR_ARG, "ppo_linear_scan_fwd: batch above 65535");
-  ScanArgs p{a, b, nullptr, init, out, nullptr, nullptr, steps, features, 0};
+  ScanArgs p{a, b, nullptr, init, out, nullptr, nullptr, steps, features, 0, nullptr, nullptr};
   return dispatch<false>(ppo::as_stream(stream), dtype, p, batch, "ppo_linear_scan_fwd");
+}
+
+PPO_EXPORT int ppo_ssm_scan_fwd(void* stream, int dtype, const void* a, const void* b, const uint8_t* done,
+                                const void* reset, const void* carry, void* out, int batch, int steps, int features) {
+  if (batch < 0 || steps < 0 || features < 0 || (dtype != SCAN_F32 && dtype != SCAN_BF16))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_ssm_scan_fwd: bad argument (batch %d steps %d features %d dtype %d)",
+                          batch, steps, features, dtype);
+  if (batch == 0 || steps == 0 || features == 0) return PPO_OK;
+  if (!a || !b || !done || !carry || !out) return ppo::set_error(PPO_ERR_ARG, "ppo_ssm_scan_fwd: null buffer");
+  if (batch > 65535) return ppo::set_error(PPO_ERR_ARG, "ppo_ssm_scan_fwd: batch above 65535");
+  ScanArgs p{a, b, nullptr, carry, out, nullptr, nullptr, steps, features, 0, done, reset};
+  return dispatch<false>(ppo::as_stream(stream), dtype, p, batch, "ppo_ssm_scan_fwd");
 }
 
 PPO_EXPORT int ppo_linear_scan_bwd(void* stream, int dtype, const void* a, const void* h, const void* init,
@@ -501,6 +576,20 @@ PPO_EXPORT int ppo_linear_scan_bwd(void* stream, int dtype, const void* a, const
   if (!a || !h || !init || !cot || !da || !db || !dinit)
     return ppo::set_error(PPO_ERR_ARG, "ppo_linear_scan_bwd: null buffer");
   if (batch > 65535) return ppo::set_error(PPO_ERR_ARG, "ppo_linear_scan_bwd: batch above 65535");
-  ScanArgs p{a, cot, h, init, db, da, dinit, steps, features, 0};
+  ScanArgs p{a, cot, h, init, db, da, dinit, steps, features, 0, nullptr, nullptr};
   return dispatch<true>(ppo::as_stream(stream), dtype, p, batch, "ppo_linear_scan_bwd");
+}
+
+PPO_EXPORT int ppo_ssm_scan_bwd(void* stream, int dtype, const void* a, const void* h, const uint8_t* done,
+                                const void* reset, const void* carry, const void* cot, void* da, void* db,
+                                void* dcarry, int batch, int steps, int features) {
+  if (batch < 0 || steps < 0 || features < 0 || (dtype != SCAN_F32 && dtype != SCAN_BF16))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_ssm_scan_bwd: bad argument (batch %d steps %d features %d dtype %d)",
+                          batch, steps, features, dtype);
+  if (batch == 0 || steps == 0 || features == 0) return PPO_OK;
+  if (!a || !h || !done || !carry || !cot || !da || !db || !dcarry)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_ssm_scan_bwd: null buffer");
+  if (batch > 65535) return ppo::set_error(PPO_ERR_ARG, "ppo_ssm_scan_bwd: batch above 65535");
+  ScanArgs p{a, cot, h, carry, db, da, dcarry, steps, features, 0, done, reset};
+  return dispatch<true>(ppo::as_stream(stream), dtype, p, batch, "ppo_ssm_scan_bwd");
 }

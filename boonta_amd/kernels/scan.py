@@ -9,7 +9,9 @@ vector-Jacobian product, mirroring boonta/networks/kernels/scan.py:
   extra axes between steps and features, [batch, steps, *extra, features],
   folded into the batch;
 - ``get_scan_implementation(name)``: the lookup the SSM block uses
-  (networks/blocks/ssm.py:49).
+  (networks/blocks/ssm.py:49);
+- ``ssm(a, b, done, carry, reset)`` / ``ssm_scan``: the SSM block's episode
+  reset folded into the same launches (ssm.py:40-55).
 
 There is no CPU path: the kernels run on the device the tensors live on.
 """
@@ -76,6 +78,54 @@ def hip(a: torch.Tensor, b: torch.Tensor, init: torch.Tensor) -> torch.Tensor:
 
     out = scan(fold(a), fold(b), init.reshape(-1, features))
     return torch.movedim(out.reshape(batch, *extra, steps, features), -2, 1)
+
+
+class _SSMScan(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, a, b, done, carry, reset):
+        a, b, carry = a.contiguous(), b.contiguous(), carry.contiguous()
+        done = done.contiguous()
+        reset = None if reset is None else reset.contiguous()
+        out = torch.empty_like(a)
+        n, t, f = a.shape
+        _lib.call("ppo_ssm_scan_fwd", _stream(), _DTYPES[a.dtype], a.data_ptr(), b.data_ptr(), done.data_ptr(),
+                  None if reset is None else reset.data_ptr(), carry.data_ptr(), out.data_ptr(), n, t, f)
+        ctx.save_for_backward(a, out, done, carry, reset)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        a, h, done, carry, reset = ctx.saved_tensors
+        g = g.to(a.dtype).contiguous()
+        da, db, dcarry = torch.empty_like(a), torch.empty_like(a), torch.empty_like(carry)
+        n, t, f = a.shape
+        _lib.call("ppo_ssm_scan_bwd", _stream(), _DTYPES[a.dtype], a.data_ptr(), h.data_ptr(), done.data_ptr(),
+                  None if reset is None else reset.data_ptr(), carry.data_ptr(), g.data_ptr(), da.data_ptr(),
+                  db.data_ptr(), dcarry.data_ptr(), n, t, f)
+        return da, db, None, dcarry, None
+
+
+def ssm_scan(a: torch.Tensor, b: torch.Tensor, done: torch.Tensor, carry: torch.Tensor,
+             reset: torch.Tensor | None = None) -> torch.Tensor:
+    """The carries of boonta's SSM block (networks/blocks/ssm.py:40-51): where
+    ``done`` [batch, steps] (bool), the step restarts from ``reset`` (the cell's
+    initial carry; None: zeros) — b' = b + a reset, a' = 0 — then the scan from
+    ``carry``; one launch forward, one backward (``reset`` gets no gradient,
+    like the cell's constant initial carry)."""
+    _check(a, b, carry)
+    if done.dtype != torch.bool or tuple(done.shape) != tuple(a.shape[:2]) or not done.is_cuda:
+        raise ValueError("done must be a bool [batch, steps] device tensor")
+    if reset is not None and (reset.dtype != a.dtype or reset.shape != carry.shape):
+        raise ValueError("reset must match carry's shape and the operands' dtype")
+    return _SSMScan.apply(a, b, done, carry, reset)
+
+
+def ssm(a: torch.Tensor, b: torch.Tensor, done: torch.Tensor, carry: torch.Tensor,
+        reset: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(final carry [batch, features], carries [batch, steps, features]), as
+    SSM.__call__ returns them before the cell's output map (ssm.py:51-55)."""
+    carries = ssm_scan(a, b, done, carry, reset)
+    return carries[:, -1], carries
 
 
 _IMPLEMENTATIONS = {"hip": hip}

@@ -118,6 +118,16 @@ int ppo_linear_scan_fwd(void* stream, int dtype, const void* a, const void* b, c
                         int batch, int steps, int features);
 int ppo_linear_scan_bwd(void* stream, int dtype, const void* a, const void* h, const void* init, const void* cot,
                         void* da, void* db, void* dinit, int batch, int steps, int features);
+/* The SSM block around the scan (networks/blocks/ssm.py:31-55): where
+ * done[n, t] (uint8 [batch, steps]) the step restarts from `reset` ([batch,
+ * features], NULL for the zero initial carry of the MinGRU / SSM cells):
+ * b' = b + a reset, a' = 0, then the scan from `carry`.  The backward returns
+ * the cotangents of a, b and carry through the reset as well. */
+int ppo_ssm_scan_fwd(void* stream, int dtype, const void* a, const void* b, const uint8_t* done, const void* reset,
+                     const void* carry, void* out, int batch, int steps, int features);
+int ppo_ssm_scan_bwd(void* stream, int dtype, const void* a, const void* h, const uint8_t* done, const void* reset,
+                     const void* carry, const void* cot, void* da, void* db, void* dcarry, int batch, int steps,
+                     int features);
 
 /* ------------------------------------------------------------------ GEMM
  * Dense layers of the torso and heads (flax.linen.Dense as composed in

@@ -61,3 +61,9 @@ def test_scan_rejects_bad_arguments_without_launching():
     assert lib.ppo_linear_scan_fwd(None, 0, None, 1, 1, 1, 2, 2, 2) == -1
     assert lib.ppo_linear_scan_bwd(None, 0, 1, 1, 1, 1, None, 1, 1, 2, 2, 2) == -1
     assert lib.ppo_linear_scan_fwd(None, 0, None, None, None, None, 0, 5, 5) == 0
+
+
+def test_ssm_scan_rejects_missing_done_flags():
+    lib = _lib.load()
+    assert lib.ppo_ssm_scan_fwd(None, 0, 1, 1, None, None, 1, 1, 2, 2, 2) == -1
+    assert lib.ppo_ssm_scan_bwd(None, 0, 1, 1, None, None, 1, 1, 1, 1, 1, 2, 2, 2) == -1

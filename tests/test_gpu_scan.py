@@ -6,13 +6,16 @@ Tolerances (written here): float32 storage — forward atol 1e-5 (rtol 1e-5),
 gradients atol 1e-4 (the reference's own bounds); bf16 storage — forward
 within 1e-2 of the exact float32 result of the bf16 inputs, and on the
 64-step problem a relative error at most bf16's machine epsilon and below
-that of a scan that accumulates in bf16; bf16 gradients 2e-2 relative."""
+that of a scan that accumulates in bf16; bf16 gradients 2e-2 relative.
+The SSM block's reset (networks/blocks/ssm.py:40-55) folded into the same
+launches: float32 1e-5 (gradients atol 1e-4), bf16 2e-2, against the oracle's
+masking + scan; with no dones it is bit-identical to the plain scan."""
 import numpy as np
 import pytest
 import torch
 
 from boonta_amd import _lib
-from boonta_amd.kernels import get_scan_implementation, hip, scan
+from boonta_amd.kernels import get_scan_implementation, hip, scan, ssm, ssm_scan
 from oracle import scan as oscan
 
 pytestmark = pytest.mark.gpu
@@ -130,3 +133,43 @@ def test_large_scan_is_linear_and_matches_a_chunk_of_the_oracle():
     torch.testing.assert_close(h12, h1 + h2, rtol=1e-5, atol=1e-5)
     want = oscan.forward(np64(a[:8]), np64(b[:8]), np64(init[:8]))
     np.testing.assert_allclose(np64(h1[:8]), want, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("steps", [1, 9, 16, 64, 200])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("with_reset", [False, True])
+def test_ssm_reset_matches_the_oracle(steps, dtype, with_reset):
+    """networks/blocks/ssm.py:40-55: episode starts restart the recurrence
+    from the cell's initial carry, folded into the scan launches."""
+    batch, features = 6, 128
+    a, b, carry = problem(steps + 17, (batch, steps, features), dtype)
+    g = torch.Generator().manual_seed(steps)
+    done = (torch.rand((batch, steps), generator=g) < 0.2)
+    done[0, 0] = True
+    done = done.cuda()
+    reset = torch.randn((batch, features), generator=g).to(dtype).cuda() if with_reset else None
+    for x in (a, b, carry):
+        x.requires_grad_(True)
+    final, carries = ssm(a, b, done, carry, reset)
+    assert carries.dtype == dtype and final.shape == carry.shape
+    dn = done.cpu().numpy()
+    rn = None if reset is None else np64(reset)
+    want = oscan.ssm_forward(np64(a), np64(b), dn, np64(carry), rn)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    np.testing.assert_allclose(np64(carries), want, rtol=tol, atol=tol)
+    np.testing.assert_array_equal(np64(final), np64(carries)[:, -1])
+    w = torch.randn(a.shape, generator=g).cuda().to(dtype)
+    (carries.float() * w.float()).sum().backward()
+    da, db, dc = oscan.ssm_vjp(np64(a), np64(carries), dn, np64(carry), np64(w), rn)
+    for got, exp in ((a.grad, da), (b.grad, db), (carry.grad, dc)):
+        if dtype == torch.float32:
+            np.testing.assert_allclose(np64(got), exp, rtol=1e-5, atol=1e-4)
+        else:
+            err = np.linalg.norm(np64(got) - exp) / max(np.linalg.norm(exp), 1e-12)
+            assert err < 2e-2, err
+
+
+def test_ssm_without_dones_is_the_plain_scan():
+    a, b, carry = problem(21, (4, 64, 256))
+    done = torch.zeros((4, 64), dtype=torch.bool, device="cuda")
+    torch.testing.assert_close(ssm_scan(a, b, done, carry), scan(a, b, carry), rtol=0, atol=0)

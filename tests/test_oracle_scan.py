@@ -60,3 +60,38 @@ def test_vjp_matches_finite_differences():
             args[which][idx] -= 2 * eps
             num[idx] = (up - f(*args)) / (2 * eps)
         np.testing.assert_allclose(grad, num, rtol=1e-6, atol=1e-8)
+
+
+def test_ssm_reset_forgets_the_past_and_reduces_to_the_scan():
+    a, b, init = problem(6, (3, 9, 4))
+    done = np.zeros((3, 9), bool)
+    np.testing.assert_array_equal(scan.ssm_forward(a, b, done, init), scan.forward(a, b, init))
+    done[:, 4] = True
+    h = scan.ssm_forward(a, b, done, init)
+    a2, b2, init2 = problem(7, (3, 9, 4))
+    a2[:, 4:], b2[:, 4:] = a[:, 4:], b[:, 4:]
+    h2 = scan.ssm_forward(a2, b2, done, init2)
+    np.testing.assert_allclose(h[:, 4:], h2[:, 4:], rtol=1e-12)  # nothing before the reset matters
+    reset = np.random.default_rng(8).standard_normal((3, 4))
+    h3 = scan.ssm_forward(a, b, done, init, reset)
+    np.testing.assert_allclose(h3[:, 4], a[:, 4] * reset + b[:, 4], rtol=1e-12)  # restarts from the reset carry
+
+
+def test_ssm_vjp_matches_finite_differences():
+    a, b, init = problem(9, (2, 6, 3))
+    done = np.zeros((2, 6), bool)
+    done[0, 0] = done[0, 3] = done[1, 5] = True
+    reset = np.random.default_rng(10).standard_normal((2, 3))
+    w = np.random.default_rng(11).standard_normal(a.shape)
+    f = lambda a_, b_, i_: float(np.sum(w * scan.ssm_forward(a_, b_, done, i_, reset)))
+    da, db, dinit = scan.ssm_vjp(a, scan.ssm_forward(a, b, done, init, reset), done, init, w, reset)
+    eps = 1e-6
+    for arr, grad, which in ((a, da, 0), (b, db, 1), (init, dinit, 2)):
+        num = np.zeros_like(arr)
+        for idx in np.ndindex(arr.shape):
+            args = [a.copy(), b.copy(), init.copy()]
+            args[which][idx] += eps
+            up = f(*args)
+            args[which][idx] -= 2 * eps
+            num[idx] = (up - f(*args)) / (2 * eps)
+        np.testing.assert_allclose(grad, num, rtol=1e-6, atol=1e-8)
