@@ -348,6 +348,25 @@ def roofline_of(dom, total, workload):
     return roof
 
 
+def launch_rows(rows):
+    """Every timed launch with its own roofline: achieved TFLOP/s against the
+    MFMA peak for contractions, achieved GB/s of algorithmic bytes against
+    HBM for the rest (frac is null where no algorithmic work is modelled)."""
+    out = []
+    for r in rows:
+        e = {k: r[k] for k in ("name", "layout", "shape", "ms", "count")}
+        sec = r["ms"] * 1e-3
+        if r["flops"] > 0:
+            peak = PEAK["bf16_mfma"] if r["name"] in ("ppo_gemm_bf16", "ppo_gemm_bf16s") else PEAK["fp32_mfma"]
+            e.update(bound="mfma", achieved=r["flops"] / sec / 1e12, frac=r["flops"] / sec / 1e12 / peak)
+        elif r["bytes"] > 0:
+            e.update(bound="hbm", achieved=r["bytes"] / sec / 1e9, frac=r["bytes"] / sec / 1e9 / PEAK["hbm"])
+        else:
+            e.update(bound=None, achieved=None, frac=None)
+        out.append(e)
+    return out
+
+
 def time_calls(calls, reps, count):
     """Each distinct launch of ``calls`` timed alone with HIP events on the
     launching stream (``reps`` back-to-back repetitions), counted ``count``
@@ -462,7 +481,7 @@ def step_main(args, recipe, alg, state, params, dev):
         total = sum(r["ms"] * r["count"] for r in rows)
         dom = max(rows, key=lambda r: r["ms"] * r["count"])
         out["roofline"] = roofline_of(dom, total, out["config"]["workload"])
-        out["launches"] = [{k: r[k] for k in ("name", "layout", "shape", "ms", "count")} for r in rows]
+        out["launches"] = launch_rows(rows)
         out["launch_sum_ms"] = total
         if not args.skip_cpu:
             log("cpu baseline ...")
@@ -645,7 +664,7 @@ def main():
         total = sum(r["ms"] * r["count"] for r in rows)
         dom = max(rows, key=lambda r: r["ms"] * r["count"])
         out["roofline"] = roofline_of(dom, total, out["config"]["workload"])
-        out["launches"] = [{k: r[k] for k in ("name", "layout", "shape", "ms", "count")} for r in rows]
+        out["launches"] = launch_rows(rows)
         out["launch_sum_ms"] = total
         if not args.skip_cpu:
             log("cpu baseline ...")

@@ -14,10 +14,10 @@
 //   B. one lane per row: the loss, its statistics and the cotangents of the
 //      head outputs (jax's tie rules for min / max / clip) -> LDS, with the
 //      block's statistic, bias and Gaussian-scale partials;
-//   C1. the cotangent of each head input, dH[64, F] = dOUT[64, 16] Wa^T times
-//      the derivative of the torso's last activation (each wave 16 rows);
-//   C2. the head weight gradient partial H^T dOUT [F, 16] (16-feature blocks
-//      dealt round-robin to the waves).
+//   C. per 16-feature block (dealt round-robin to the waves) over the tile's
+//      64 rows: C1, the cotangent of each head input, dH = dOUT Wa^T times the
+//      derivative of the torso's last activation, and C2, the head weight
+//      gradient partial H^T dOUT, sharing one load of the H block.
 // Every loop issues the loads of four 16-wide steps before their MFMAs, so
 // four global round trips overlap.
 // Per-block partials are summed in a fixed order by the gradient reduce, so
@@ -348,56 +348,18 @@ __global__ void __launch_bounds__(HL_THREADS) head_loss_kernel(HeadLossParams p)
   // ---------------- B. loss and output cotangents (element-parallel)
   phase_b<TR, 1, SEP>(p, blk, s_out, s_dout, s_st, s_dsc, lin, cc);
 
-  // ---------------- C1. cotangent of the head inputs (the wave's 16 rows)
+  // ---------------- C. per 16-feature block (blocks dealt round-robin to the
+  // waves), over all the tile's rows: C2, the head weight gradient partial
+  // H^T dOUT, and C1, the cotangent of the head inputs dOUT W^T times the
+  // torso activation's derivative.  One load of H[rows, block] serves both:
+  // C2's operand, and C1's activation input when that is the head input
+  // itself (relu / tanh outputs), so H is read twice per launch, not three
+  // times.
   {
-    const floatx4 dv4 = *reinterpret_cast<const floatx4*>(&s_dout[16 * wave + li][4 * kq]);
-    const bool live_a = r0 + 16 * wave + li < p.rows;
-    const floatx4 a_in = live_a ? dv4 : floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int f0 = 0; f0 < F; f0 += 64) {
-      float bv[4][4], xa[4][4], xc[4][4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int f = f0 + 16 * u + li;  // B column = output feature
-        const bool fin = f0 + 16 * u < F;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int j = 4 * kq + s;
-          bv[u][s] = (fin && j < p.na) ? p.wa[(int64_t)f * p.ldwa + j] : 0.f;
-          const int row = r0 + 16 * wave + 4 * kq + s;
-          const bool ok = fin && row < p.rows;
-          xa[u][s] = (ok && p.act_a != ACT_NONE) ? p.aux_a[(int64_t)row * p.ldaux_a + f] : 0.f;
-          if (SEP) xc[u][s] = (ok && p.act_c != ACT_NONE) ? p.aux_c[(int64_t)row * p.ldaux_c + f] : 0.f;
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int f = f0 + 16 * u + li;
-        if (f0 + 16 * u >= F) break;
-        const floatx4 g = mfma4(a_in, bv[u], floatx4{0.f, 0.f, 0.f, 0.f});
-        const float wcf = SEP ? p.wc[(int64_t)f * p.ldwc] : 0.f;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int rr = 16 * wave + 4 * kq + v;
-          const int row = r0 + rr;
-          if (row >= p.rows) continue;
-          float d = g[v];
-          if (p.act_a != ACT_NONE) d *= ppo::act_grad(p.act_a, xa[u][v]);
-          p.dha[(int64_t)row * p.lddha + f] = d;
-          if (SEP) {
-            float dc = s_dout[rr][16] * wcf;
-            if (p.act_c != ACT_NONE) dc *= ppo::act_grad(p.act_c, xc[u][v]);
-            p.dhc[(int64_t)row * p.lddhc + f] = dc;
-          }
-        }
-      }
-    }
-  }
-
-  // ---------------- C2. head weight gradient partial H^T dOUT (16-feature blocks dealt to the waves)
-  {
+    const bool a_is_h = p.aux_a == p.ha && p.ldaux_a == p.ldha;
+    const bool c_is_h = SEP && p.aux_c == p.hc && p.ldaux_c == p.ldhc;
     for (int fb = 16 * wave; fb < F; fb += 64) {
-      const int f = fb + li;  // A row = feature
-      floatx4 acc = {0.f, 0.f, 0.f, 0.f}, accc = {0.f, 0.f, 0.f, 0.f};
+      const int f = fb + li;  // C2: A row = feature; C1: B / D column = feature
       floatx4 av[TR / 16], cv[TR / 16];
 #pragma unroll
       for (int cc = 0; cc < TR / 16; ++cc) {
@@ -409,6 +371,14 @@ __global__ void __launch_bounds__(HL_THREADS) head_loss_kernel(HeadLossParams p)
           cv[cc][s] = (SEP && ok) ? p.hc[(int64_t)row * p.ldhc + f] : 0.f;
         }
       }
+      float wb[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int j = 4 * kq + s;
+        wb[s] = j < p.na ? p.wa[(int64_t)f * p.ldwa + j] : 0.f;
+      }
+      const float wcf = SEP ? p.wc[(int64_t)f * p.ldwc] : 0.f;
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f}, accc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int cc = 0; cc < TR / 16; ++cc) {
         float bv[4], wv[4];
@@ -420,6 +390,27 @@ __global__ void __launch_bounds__(HL_THREADS) head_loss_kernel(HeadLossParams p)
         }
         acc = mfma4(av[cc], bv, acc);
         if (SEP) accc = mfma4(cv[cc], wv, accc);
+        // C1 for rows 16 cc + 4 kq + v of this feature block
+        const bool live = r0 + 16 * cc + li < p.rows;
+        const floatx4 dv4 = *reinterpret_cast<const floatx4*>(&s_dout[16 * cc + li][4 * kq]);
+        const floatx4 a_in = live ? dv4 : floatx4{0.f, 0.f, 0.f, 0.f};
+        const floatx4 g = mfma4(a_in, wb, floatx4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int rr = 16 * cc + 4 * kq + v;
+          const int row = r0 + rr;
+          if (row >= p.rows) continue;
+          float d = g[v];
+          if (p.act_a != ACT_NONE)
+            d *= ppo::act_grad(p.act_a, a_is_h ? av[cc][v] : p.aux_a[(int64_t)row * p.ldaux_a + f]);
+          p.dha[(int64_t)row * p.lddha + f] = d;
+          if (SEP) {
+            float dc = s_dout[rr][16] * wcf;
+            if (p.act_c != ACT_NONE)
+              dc *= ppo::act_grad(p.act_c, c_is_h ? cv[cc][v] : p.aux_c[(int64_t)row * p.ldaux_c + f]);
+            p.dhc[(int64_t)row * p.lddhc + f] = dc;
+          }
+        }
       }
 #pragma unroll
       for (int v = 0; v < 4; ++v) {

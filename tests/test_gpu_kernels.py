@@ -416,6 +416,7 @@ def test_sumsq_total_fixed_order(n):
     (True, "gaussian", 8, 512, 300, "silu"),          # widest features, 8 blocks per wave
     (False, "categorical", 6, 256, 20000, "relu"),    # above 16384 rows: the 64-row tile kernel
     (True, "gaussian", 4, 128, 16390, "tanh"),        # ragged 64-row tiles, separate towers
+    (True, "gaussian", 8, 256, 17000, "silu"),        # 64-row tiles, activation input read separately
 ])
 def test_fused_heads_loss_and_head_backward(sep, dist, A, F, rows, act):
     g = np.random.default_rng(F + rows + A)
