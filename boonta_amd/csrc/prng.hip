@@ -118,35 +118,58 @@ __global__ void __launch_bounds__(TILE_THREADS) shuffle_bits_kernel(ShuffleArgs 
 }
 
 // One workgroup per epoch: bucket totals, their exclusive scan (bucket
-// starts), and each (bucket, tile) count rewritten as its write offset.
-__global__ void __launch_bounds__(1024) shuffle_scan_kernel(ShuffleArgs a) {
+// starts), and each (bucket, tile) count rewritten as its write offset.  The
+// scan over the nb <= 4096 totals is a block scan: thread t owns buckets
+// 4t .. 4t + 3, wave-level inclusive scans of the per-thread sums, then the
+// 16 wave totals.
+constexpr int SCAN_THREADS = 1024;
+
+__global__ void __launch_bounds__(SCAN_THREADS) shuffle_scan_kernel(ShuffleArgs a) {
   extern __shared__ uint32_t tot[];  // [nb]
+  __shared__ uint32_t wsum[SCAN_THREADS / 64];
   const int e = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   uint32_t* hist = a.hist + (int64_t)e * a.nb * a.tiles;
-  for (int d = threadIdx.x; d < a.nb; d += blockDim.x) {
+  for (int d = threadIdx.x; d < a.nb; d += SCAN_THREADS) {
     uint32_t s = 0;
     for (int t = 0; t < a.tiles; ++t) s += hist[(int64_t)d * a.tiles + t];
     tot[d] = s;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    // nb <= 4096: a serial scan here is a few microseconds
-    uint32_t run = 0;
-    for (int d = 0; d < a.nb; ++d) {
-      const uint32_t v = tot[d];
-      tot[d] = run;
-      run += v;
-    }
+  // exclusive scan of tot[0 .. nb)
+  const int d0 = 4 * threadIdx.x;
+  uint32_t v[4], local = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[i] = d0 + i < a.nb ? tot[d0 + i] : 0u;
+    local += v[i];
+  }
+  uint32_t inc = local;  // inclusive scan of the per-thread sums across the wave
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += y;
+  }
+  if (lane == 63) wsum[wave] = inc;
+  __syncthreads();
+  uint32_t before = 0;
+  for (int w = 0; w < wave; ++w) before += wsum[w];
+  uint32_t run = before + inc - local;  // exclusive prefix of this thread's first bucket
+  __syncthreads();  // every tot[] read above happens before the writes below
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (d0 + i < a.nb) tot[d0 + i] = run;
+    run += v[i];
   }
   __syncthreads();
   uint32_t* bstart = a.bstart + (int64_t)e * (a.nb + 1);
-  for (int d = threadIdx.x; d < a.nb; d += blockDim.x) {
+  for (int d = threadIdx.x; d < a.nb; d += SCAN_THREADS) {
     bstart[d] = tot[d];
-    uint32_t run = tot[d];
+    uint32_t r = tot[d];
     for (int t = 0; t < a.tiles; ++t) {
-      const uint32_t v = hist[(int64_t)d * a.tiles + t];
-      hist[(int64_t)d * a.tiles + t] = run;
-      run += v;
+      const uint32_t c = hist[(int64_t)d * a.tiles + t];
+      hist[(int64_t)d * a.tiles + t] = r;
+      r += c;
     }
   }
   if (threadIdx.x == 0) bstart[a.nb] = (uint32_t)a.n;
@@ -305,7 +328,7 @@ int shuffle_impl(hipStream_t st, const uint32_t* key, int split_epochs, int epoc
   for (int r = 0; r < rounds; ++r) {
     a.round = r;
     hipLaunchKernelGGL(shuffle_bits_kernel, dim3(a.tiles, epochs), dim3(TILE_THREADS), shm, st, a);
-    hipLaunchKernelGGL(shuffle_scan_kernel, dim3(epochs), dim3(1024), shm, st, a);
+    hipLaunchKernelGGL(shuffle_scan_kernel, dim3(epochs), dim3(SCAN_THREADS), shm, st, a);
     hipLaunchKernelGGL(shuffle_scatter_kernel, dim3(a.tiles, epochs), dim3(TILE_THREADS), shm, st, a);
     hipLaunchKernelGGL(shuffle_sort_kernel, dim3(a.nb, epochs), dim3(SORT_THREADS), 0, st, a);
   }
