@@ -377,6 +377,12 @@ class ForwardChain:
                            _act(s.act) if s.ln is None else 0, 1, None, 0, None, -1)
                 if s.ln is not None:
                     self._ln_forward(st, lb, o, row0, nrows)
+            elif s.ln is not None and not self.bf16 and s.fout == 256 and s.ld == 256:
+                # Dense -> LayerNorm -> activation in one launch (16 rows x 256 columns per workgroup)
+                self._call("ppo_gemm_ln_act_fwd_f32", st, x, ldx, rows_idx, W, d.w.ld, Bb,
+                           self.flat.view(s.ln["scale"]), self.flat.view(s.ln["bias"]), _p(lb.Z) + o, s.ld,
+                           _p(lb.Y) + o, s.ld, _p(lb.mean) + 4 * row0, _p(lb.rstd) + 4 * row0, nrows, d.fin, s.fout,
+                           s.ln["eps"], _act(s.act))
             elif s.ln is not None:
                 self._gemm(st, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(lb.Z) + o, s.ld, nrows,
                           s.ld, d.fin, 1, 0, EPI_BIAS_ACT, Bb, 0, None, None, 0, None, -1)

@@ -104,6 +104,19 @@ int ppo_sample_gaussian_f32(void* stream, const float* mean, int64_t ldm, const 
                             int rows, int D, const float* value_src, int64_t ldv, const uint32_t* key,
                             float temperature, float* action, int64_t lda, float* log_prob, float* value);
 
+/* ------------------------------------------------ Dense + LayerNorm + act
+ * One torso layer of flax Dense -> LayerNorm -> activation (the Gaussian
+ * workload's towers, hangar recipes' 4 x 256 SiLU MLPs) in a single launch:
+ * Z = X W + b (row r of X is X[rows_idx[r]] when rows_idx is non-NULL), the
+ * row statistics of Z (fast variance, as flax's LayerNorm) and
+ * Y = act((Z - mean) rstd gamma + beta).  Writes Z, mean, rstd and Y, the same
+ * values ppo_gemm_f32 (epi 1, no activation) followed by
+ * ppo_layernorm_act_fwd_f32 leave.  F must be 256. */
+int ppo_gemm_ln_act_fwd_f32(void* stream, const float* X, int64_t ldx, const int32_t* rows_idx, const float* W,
+                            int64_t ldw, const float* bias, const float* gamma, const float* beta, float* Z,
+                            int64_t ldz, float* Y, int64_t ldy, float* mean, float* rstd, int M, int K, int F,
+                            float eps, int act);
+
 /* ------------------------------------------------------- linear scan
  * Replace boonta's linear-recurrence scan and its custom VJP
  * (boonta/networks/kernels/scan.py:13-88: scan / _scan_fwd / _scan_bwd),

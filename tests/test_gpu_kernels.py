@@ -237,6 +237,51 @@ def test_layernorm_forward_and_backward(F, act):
     np.testing.assert_allclose(p[F:], grads["ln"]["bias"], rtol=1e-4, atol=1e-3)
 
 
+@pytest.mark.parametrize("rows, K, gather, act", [(2048, 256, False, "silu"), (777, 87, True, "silu"),
+                                                   (1, 256, False, "relu"), (33, 64, True, "tanh"),
+                                                   (4096, 300, False, "none")])
+def test_fused_dense_layernorm_act_forward(rows, K, gather, act):
+    """ppo_gemm_ln_act_fwd_f32 against float64 (Dense + LayerNorm + act, the
+    oracle's stages) and against the two-launch path it replaces."""
+    F = 256
+    g = np.random.default_rng(rows + K)
+    src_rows = rows + 50 if gather else rows
+    x = g.standard_normal((src_rows, K)).astype(np.float32)
+    idx = g.permutation(src_rows)[:rows].astype(np.int32) if gather else None
+    w = (g.standard_normal((K, F)) / np.sqrt(K)).astype(np.float32)
+    b = g.normal(0, 0.1, F).astype(np.float32)
+    gamma = g.normal(1, 0.2, F).astype(np.float32)
+    beta = g.normal(0, 0.2, F).astype(np.float32)
+    stages = [{"op": "dense", "path": ("d",), "in": K, "out": F},
+              {"op": "layernorm", "path": ("ln",), "width": F, "eps": 1e-6}]
+    if act != "none":
+        stages.append({"op": "act", "fn": act})
+    params = {"d": {"kernel": w, "bias": b}, "ln": {"scale": gamma, "bias": beta}}
+    xs = x[idx] if gather else x
+    y_ref, _ = nets.stages_forward(params, stages, xs.astype(np.float64))
+    z_ref = xs.astype(np.float64) @ w + b
+    X, W, B, G, Bt = dev(x), dev(w), dev(b), dev(gamma), dev(beta)
+    I = dev(idx) if gather else None
+    Z, Y = torch.zeros(rows, F, device=DEV), torch.zeros(rows, F, device=DEV)
+    mean, rstd = torch.zeros(rows, device=DEV), torch.zeros(rows, device=DEV)
+    _lib.call("ppo_gemm_ln_act_fwd_f32", st(), X.data_ptr(), K, None if I is None else I.data_ptr(), W.data_ptr(), F,
+              B.data_ptr(), G.data_ptr(), Bt.data_ptr(), Z.data_ptr(), F, Y.data_ptr(), F, mean.data_ptr(),
+              rstd.data_ptr(), rows, K, F, 1e-6, _lib.ACT[act])
+    np.testing.assert_allclose(host(Z), z_ref, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(host(Y), y_ref, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(host(mean), z_ref.mean(1), rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(host(rstd), 1 / np.sqrt(z_ref.var(1) + 1e-6), rtol=1e-4)
+    # the two launches it replaces leave the same values
+    Z2, Y2 = torch.zeros(rows, F, device=DEV), torch.zeros(rows, F, device=DEV)
+    m2, r2 = torch.zeros(rows, device=DEV), torch.zeros(rows, device=DEV)
+    _lib.call("ppo_gemm_f32", st(), 0, 0, X.data_ptr(), K, None if I is None else I.data_ptr(), W.data_ptr(), F,
+              Z2.data_ptr(), F, rows, F, K, 1, 0, 1, B.data_ptr(), 0, None, None, 0, None, -1)
+    _lib.call("ppo_layernorm_act_fwd_f32", st(), Z2.data_ptr(), F, G.data_ptr(), Bt.data_ptr(), Y2.data_ptr(), F,
+              m2.data_ptr(), r2.data_ptr(), rows, F, 1e-6, _lib.ACT[act])
+    np.testing.assert_allclose(host(Z), host(Z2), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(host(Y), host(Y2), rtol=1e-4, atol=1e-5)
+
+
 # ------------------------------------------------------------------- loss
 CFG = {"clip_coefficient": 0.2, "clip_value_loss": True, "entropy_coefficient": 0.01, "value_coefficient": 0.5}
 
