@@ -164,6 +164,9 @@ def launch_work(name, args):
     if name == "ppo_splits_bias_act_bf16":
         nsplit, rows, cols = args[4], args[9], args[10]
         return 0.0, 4.0 * rows * cols * (nsplit + 1)
+    if name == "ppo_gemm_ln_act_fwd_f32":
+        M, K, Fo = args[15], args[16], args[17]
+        return 2.0 * M * Fo * K, 4.0 * (M * K + K * Fo + 2 * M * Fo)
     if name == "ppo_sample_categorical_f32":
         rows, A = args[3], args[4]
         return 0.0, 4.0 * rows * (A + 4)
