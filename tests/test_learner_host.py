@@ -125,3 +125,47 @@ def test_unsupported_compositions_raise():
                                          critic=nn.Dense(1)))
     with pytest.raises(NotImplementedError):
         Program(bad.plan(4))
+
+
+@pytest.mark.parametrize("config", ALL_CONFIGS)
+def test_rollout_step_launches_match_the_c_signatures(config):
+    """PPO.step / RecurrentPPO.step (ppo.py:57-74, recurrent_ppo.py:71-96):
+    the recorded launch sequence of one env step ends in the sampling launch
+    and every call matches its C signature."""
+    from boonta_amd.rollout import RecurrentStepExecutor, StepExecutor
+    r = small(config)
+    prog = Program(r.network.plan(r.obs_dim))
+    flat = FlatState(prog, torch.device("cpu"))
+    N = r.N
+    if prog.gru is not None:
+        ex = RecurrentStepExecutor(prog, flat, N)
+        calls = ex.record(4096, r.obs_dim, 8192, 12288, 16384, 1.0, 20480, 24576, 28672, 32768)
+        assert [n for n, _ in calls].count("ppo_gru_fwd_step_f32") == 1
+    else:
+        ex = StepExecutor(prog, flat, N)
+        calls = ex.record(4096, r.obs_dim, 1.0, 8192, 12288, 16384)
+    names = [n for n, _ in calls]
+    want = "ppo_sample_categorical_f32" if prog.dist["kind"] == "categorical" else "ppo_sample_gaussian_f32"
+    assert names[-1] == want and names.count(want) == 1
+    for name, args in calls:
+        _, argtypes = _lib.SIGNATURES[name]
+        assert len(args) == len(argtypes), (name, len(args), len(argtypes))
+    sample_args = calls[-1][1]
+    assert sample_args[3 if want.endswith("categorical_f32") else 5] == N     # rows
+    if config == 3:
+        # 256-wide fp32 LayerNorm layers: Dense + LayerNorm + SiLU in one launch each
+        assert names.count("ppo_gemm_ln_act_fwd_f32") == 8 and "ppo_layernorm_act_fwd_f32" not in names
+
+
+def test_gaussian_update_fuses_dense_and_layernorm_forward():
+    r = small(3)
+    prog = Program(r.network.plan(r.obs_dim))
+    flat = FlatState(prog, torch.device("cpu"))
+    ex = executor(r, prog, flat)
+    ex.bind(fake_inputs(ex))
+    names = [n for n, _ in ex.record()]
+    steps = r.cfg.update_epochs * r.cfg.num_minibatches
+    # 4 layers x 2 towers per minibatch step, plus the critic's bootstrap forward
+    assert names.count("ppo_gemm_ln_act_fwd_f32") == 8 * steps + 4
+    assert "ppo_layernorm_act_fwd_f32" not in names
+    assert names.count("ppo_layernorm_act_bwd_f32") == 8 * steps
