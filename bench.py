@@ -204,6 +204,25 @@ def launch_work(name, args):
     return 0.0, 0.0
 
 
+def launch_shape(name, args):
+    """[M, N, K] of a contraction launch (None for the others)."""
+    if name in ("ppo_gemm_f32", "ppo_gemm_bf16"):
+        return list(args[10:13])
+    if name == "ppo_gemm_bf16s":
+        return list(args[12:15])
+    if name == "ppo_gemm_ln_act_fwd_f32":
+        return [args[15], args[17], args[16]]
+    if name.startswith("ppo_gru"):
+        return [args[-2], args[-1]]
+    return None
+
+
+def launch_layout(name, args):
+    if name in ("ppo_gemm_f32", "ppo_gemm_bf16", "ppo_gemm_bf16s"):
+        return [args[1], args[2]]
+    return None
+
+
 def launch_key(name, args):
     """Launches with the same entry point and shape do the same work."""
     if name in ("ppo_gemm_f32", "ppo_gemm_bf16"):
@@ -247,12 +266,7 @@ def time_launches(ex, reps, per_update_steps):
         ms = e0.elapsed_time(e1) / reps
         flops, nbytes = launch_work(name, args)
         row = {"i": i, "name": name, "ms": ms, "count": count, "flops": flops, "bytes": nbytes,
-               "shape": [a for a in args[10:13]] if name.startswith("ppo_gemm") else None,
-               "layout": [args[1], args[2]] if name.startswith("ppo_gemm") else None}
-        if name == "ppo_gemm_bf16s":
-            row["shape"] = [a for a in args[12:15]]
-        if name.startswith("ppo_gru"):
-            row["shape"] = [args[-2], args[-1]]
+               "shape": launch_shape(name, args), "layout": launch_layout(name, args)}
         rows.append(row)
         seen[key] = row
     return rows
@@ -391,11 +405,7 @@ def time_calls(calls, reps, count):
         e1.synchronize()
         flops, nbytes = launch_work(name, args)
         row = {"i": i, "name": name, "ms": e0.elapsed_time(e1) / reps, "count": count, "flops": flops,
-               "bytes": nbytes,
-               "shape": [a for a in args[10:13]] if name.startswith("ppo_gemm") else None,
-               "layout": [args[1], args[2]] if name.startswith("ppo_gemm") else None}
-        if name == "ppo_gemm_bf16s":
-            row["shape"] = [a for a in args[12:15]]
+               "bytes": nbytes, "shape": launch_shape(name, args), "layout": launch_layout(name, args)}
         rows.append(row)
     return rows
 
