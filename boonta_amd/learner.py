@@ -227,6 +227,8 @@ class LayerBufs:
     fpart: torch.Tensor | None = None
     dZ16: torch.Tensor | None = None
     Y16: torch.Tensor | None = None
+    X16: torch.Tensor | None = None  # bf16 copy of a split-K first layer's input rows
+    W16: torch.Tensor | None = None  # and of its kernel
 
 
 class FlatState:
@@ -278,6 +280,11 @@ def split_forward_bufs(lb: LayerBufs, rows: int, device, bf16: bool) -> None:
         S -= 1
     if S > 1:
         lb.fpart = torch.zeros(S, rows, lb.spec.ld, dtype=torch.float32, device=device)
+        if lb.spec.ld % 8 == 0:
+            # bf16 copies of the input rows and of the kernel, so the GEMM takes
+            # its direct global -> LDS copies (flax casts both to bf16 anyway)
+            lb.X16 = torch.zeros(rows, (d.fin + 7) // 8 * 8, dtype=torch.int16, device=device)
+            lb.W16 = torch.zeros(d.fin, d.w.ld, dtype=torch.int16, device=device)
 
 
 class ForwardChain:
@@ -362,9 +369,17 @@ class ForwardChain:
                 # order with flax's bf16 bias add and activation
                 S = lb.fpart.shape[0]
                 dst = lb.Z if s.ln is not None else lb.Y
-                self._call("ppo_gemm_bf16s", st, A_ROW, B_KN, 0, 0, x, ldx, None, W, d.w.ld, _p(lb.fpart), s.ld,
-                           nrows, s.ld, d.fin, S, lb.fpart.shape[1] * s.ld, EPI_STORE, None, 0, 0, None, 0, None,
-                           -1)
+                if lb.X16 is not None and nrows <= lb.X16.shape[0]:
+                    ld16 = lb.X16.shape[1]
+                    self._call("ppo_cast_bf16_2d", st, x, ldx, _p(lb.X16), ld16, nrows, d.fin)
+                    self._call("ppo_cast_bf16", st, W, _p(lb.W16), d.fin * d.w.ld)
+                    self._call("ppo_gemm_bf16s", st, A_ROW, B_KN, 1, 1, _p(lb.X16), ld16, None, _p(lb.W16), d.w.ld,
+                               _p(lb.fpart), s.ld, nrows, s.ld, d.fin, S, lb.fpart.shape[1] * s.ld, EPI_STORE, None,
+                               0, 0, None, 0, None, 1)
+                else:
+                    self._call("ppo_gemm_bf16s", st, A_ROW, B_KN, 0, 0, x, ldx, None, W, d.w.ld, _p(lb.fpart),
+                               s.ld, nrows, s.ld, d.fin, S, lb.fpart.shape[1] * s.ld, EPI_STORE, None, 0, 0, None,
+                               0, None, -1)
                 self._call("ppo_splits_bias_act_bf16", st, _p(lb.fpart), s.ld, lb.fpart.shape[1] * s.ld, S, Bb,
                            _act(s.act) if s.ln is None else 0, _p(dst), s.ld, nrows, s.ld)
                 if s.ln is not None:
