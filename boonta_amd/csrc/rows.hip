@@ -50,7 +50,7 @@ ln_act_fwd_kernel(const float* __restrict__ z, int64_t ldz, const float* __restr
       if (mean_out) mean_out[r] = mean;
       if (rstd_out) rstd_out[r] = rstd;
     }
-    float* yr = y + r * ldy;
+    float* yr = y ? y + r * ldy : nullptr;
 #pragma unroll
     for (int e = 0; e < VPL; ++e) {
       const int f = lane + 64 * e;
@@ -64,7 +64,7 @@ ln_act_fwd_kernel(const float* __restrict__ z, int64_t ldz, const float* __restr
         } else {
           o = ppo::act_fwd(act, o);
         }
-        yr[f] = o;
+        if (yr) yr[f] = o;
         if (y16) y16[r * ldy16 + f] = (uint16_t)ppo::bf16_bits(o);
       }
     }
@@ -524,7 +524,8 @@ int launch_ln_bwd(hipStream_t st, int blocks, const float* dy, int64_t lddy, con
 static int layernorm_fwd(const char* name, void* stream, const float* z, int64_t ldz, const float* gamma,
                          const float* beta, float* y, int64_t ldy, float* mean, float* rstd, int rows, int F,
                          float eps, int act, int round, uint16_t* y16 = nullptr, int64_t ldy16 = 0) {
-  if (rows < 0 || F <= 0 || F > 64 * MAX_VPL || act < 0 || act > 3 || !z || !gamma || !beta || !y)
+  // y may be NULL only when the bf16 copy y16 is written (the fp32 output unused)
+  if (rows < 0 || F <= 0 || F > 64 * MAX_VPL || act < 0 || act > 3 || !z || !gamma || !beta || (!y && !y16))
     return ppo::set_error(PPO_ERR_ARG, "%s: bad argument (rows=%d F=%d)", name, rows, F);
   if (rows == 0) return PPO_OK;
   const int blocks = std::min(ppo::ceil_div(rows, ROW_THREADS / 64), 4096);

@@ -227,6 +227,7 @@ class LayerBufs:
     fpart: torch.Tensor | None = None
     dZ16: torch.Tensor | None = None
     Y16: torch.Tensor | None = None
+    y32_unused: bool = False  # only the bf16 copy Y16 of this layer's output is read
     X16: torch.Tensor | None = None  # bf16 copy of a split-K first layer's input rows
     W16: torch.Tensor | None = None  # and of its kernel
 
@@ -334,7 +335,8 @@ class ForwardChain:
         s = lb.spec
         scale, bias = self.flat.view(s.ln["scale"]), self.flat.view(s.ln["bias"])
         if lb.Y16 is not None and row0 == 0 and nrows == self.mb:
-            self._call("ppo_layernorm_act_fwd_bf16_out16", st, _p(lb.Z), s.ld, scale, bias, _p(lb.Y), s.ld,
+            self._call("ppo_layernorm_act_fwd_bf16_out16", st, _p(lb.Z), s.ld, scale, bias,
+                       None if lb.y32_unused else _p(lb.Y), s.ld,
                        _p(lb.Y16), s.ld, _p(lb.mean), _p(lb.rstd), nrows, s.fout, s.ln["eps"], _act(s.act))
         else:
             self._call(self._ln_fwd, st, _p(lb.Z) + o, s.ld, scale, bias, _p(lb.Y) + o, s.ld, _p(lb.mean) + 4 * row0,
@@ -483,6 +485,8 @@ class MLPExecutor(ForwardChain):
                     lb.Y16 = torch.zeros(mb, lb.spec.ld, **i16)
                     if lb.dZ16 is None:
                         lb.dZ16 = torch.zeros(mb, lb.spec.ld, **i16)
+                    # the next Dense reads (forward and dW) only the bf16 copy
+                    lb.y32_unused = li + 1 < len(group) and group[li + 1].spec.dense.w.ld % 8 == 0
                     if li > 0 and group[li - 1].spec.ln is not None:
                         d = lb.spec.dense
                         lb.splits = self.DW16_SPLITS_INNER

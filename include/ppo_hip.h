@@ -225,7 +225,8 @@ int ppo_layernorm_act_fwd_bf16(void* stream, const float* z, int64_t ldz, const 
                                float* y, int64_t ldy, float* mean, float* rstd, int rows, int F, float eps,
                                int act);
 /* ppo_layernorm_act_fwd_bf16 that also stores y as bf16 bit patterns (y16,
- * row pitch ldy16 elements): the operand of the next bf16 contraction. */
+ * row pitch ldy16 elements): the operand of the next bf16 contraction.  y
+ * may be NULL when only the bf16 copy is read afterwards. */
 int ppo_layernorm_act_fwd_bf16_out16(void* stream, const float* z, int64_t ldz, const float* gamma, const float* beta,
                                      float* y, int64_t ldy, void* y16, int64_t ldy16, float* mean, float* rstd,
                                      int rows, int F, float eps, int act);

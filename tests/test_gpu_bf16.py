@@ -159,6 +159,12 @@ def test_layernorm_relu_bf16_forward_and_backward():
     torch.cuda.synchronize()
     np.testing.assert_array_equal(Y2.cpu().numpy(), Y.cpu().numpy())
     np.testing.assert_array_equal(Y16.cpu().numpy()[:, :F].view(np.uint16), to_bf16_bits(Y.cpu().numpy()))
+    # without the fp32 output (inner layers: the next Dense reads only the bf16 copy)
+    Y16b = torch.zeros(rows, F + 8, dtype=torch.int16, device=DEV)
+    _lib.call("ppo_layernorm_act_fwd_bf16_out16", st(), Z.data_ptr(), F, G.data_ptr(), Bt.data_ptr(), None,
+              F, Y16b.data_ptr(), F + 8, MEAN.data_ptr(), RSTD.data_ptr(), rows, F, 1e-6, 1)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(Y16b.cpu().numpy(), Y16.cpu().numpy())
     DZ16 = torch.zeros(rows, F + 8, dtype=torch.int16, device=DEV)
     PART16 = torch.zeros(nb, 2 * F, device=DEV)
     _lib.call("ppo_layernorm_act_bwd_bf16_out16", st(), DY.data_ptr(), F, Z.data_ptr(), F, MEAN.data_ptr(),
