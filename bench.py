@@ -167,6 +167,10 @@ def launch_work(name, args):
     if name == "ppo_gemm_ln_act_fwd_f32":
         M, K, Fo = args[15], args[16], args[17]
         return 2.0 * M * Fo * K, 4.0 * (M * K + K * Fo + 2 * M * Fo)
+    if name == "ppo_step_mlp_categorical_f32":
+        rows, K0, L, ldwh = args[3], args[4], args[5], args[11]
+        weights = K0 * 256 + (L - 1) * 256 * 256 + 256 * ldwh
+        return 2.0 * rows * weights, 4.0 * (rows * K0 + weights + 3 * rows)
     if name == "ppo_sample_categorical_f32":
         rows, A = args[3], args[4]
         return 0.0, 4.0 * rows * (A + 4)
@@ -205,13 +209,16 @@ def launch_work(name, args):
 
 
 def launch_shape(name, args):
-    """[M, N, K] of a contraction launch (None for the others)."""
+    """[M, N, K] of a contraction launch (the one-launch step: [rows, 256,
+    observation features, trunk layers]; None for the others)."""
     if name in ("ppo_gemm_f32", "ppo_gemm_bf16"):
         return list(args[10:13])
     if name == "ppo_gemm_bf16s":
         return list(args[12:15])
     if name == "ppo_gemm_ln_act_fwd_f32":
         return [args[15], args[17], args[16]]
+    if name == "ppo_step_mlp_categorical_f32":
+        return [args[3], 256, args[4], args[5]]
     if name.startswith("ppo_gru"):
         return [args[-2], args[-1]]
     return None

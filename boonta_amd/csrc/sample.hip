@@ -29,6 +29,7 @@
 // ...; row statistics (max, sum, argmax, log-prob sum) are 16-lane butterflies.
 #include "common.h"
 #include "threefry.h"
+#include "categorical.h"
 
 #include <math.h>
 
@@ -40,32 +41,10 @@ constexpr int ROWS_PER_BLOCK = THREADS / GROUP;
 constexpr int MAX_K = 8;  // columns per lane: A, D <= 128
 constexpr float HALF_LOG_2PI = 0.91893853320467274f;
 
-__device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-  for (int o = GROUP / 2; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, GROUP));
-  return v;
-}
-
 __device__ __forceinline__ float group_sum(float v) {
 #pragma unroll
   for (int o = GROUP / 2; o; o >>= 1) v += __shfl_xor(v, o, GROUP);
   return v;
-}
-
-// (value, index) argmax across the group: larger value wins, the smaller
-// index on equal values; `extra` travels with the winner.
-__device__ __forceinline__ void group_argmax(float& v, int& i, float& extra) {
-#pragma unroll
-  for (int o = GROUP / 2; o; o >>= 1) {
-    const float ov = __shfl_xor(v, o, GROUP);
-    const int oi = __shfl_xor(i, o, GROUP);
-    const float oe = __shfl_xor(extra, o, GROUP);
-    if (ov > v || (ov == v && oi < i)) {
-      v = ov;
-      i = oi;
-      extra = oe;
-    }
-  }
 }
 
 __device__ __forceinline__ float softplus_acc(float x) {
@@ -120,67 +99,13 @@ __global__ void __launch_bounds__(THREADS) sample_categorical_kernel(CatArgs a) 
   const int j0 = threadIdx.x % GROUP;
   const bool row_ok = r < a.rows;
   const uint32_t k0 = a.key[0], k1 = a.key[1];
-  const bool greedy = !(a.temperature > 0.f);
-  const float div = greedy ? 1.f : a.temperature;
   const float* pr = a.pref + (int64_t)(row_ok ? r : 0) * a.ldp;
-
-  float c[MAX_K];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int k = 0; k < MAX_K; ++k) {
-    const int j = j0 + GROUP * k;
-    c[k] = (row_ok && j < a.A) ? pr[j] / div : -INFINITY;
-    mx = fmaxf(mx, c[k]);
-  }
-  mx = group_max(mx);
-  float se = 0.f;
-#pragma unroll
-  for (int k = 0; k < MAX_K; ++k) se += expf(c[k] - mx);  // exp(-inf) = 0 past A
-  float lse = logf(group_sum(se));
-  if (greedy) {
-    // logits = 0 at argmax(log_softmax(preferences)), -inf elsewhere; their
-    // log_softmax is the same vector
-    float bv = -INFINITY, dummy = 0.f;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int k = 0; k < MAX_K; ++k) {
-      const int j = j0 + GROUP * k;
-      const float ls = (c[k] - mx) - lse;
-      if (j < a.A && (ls > bv || bi == 0x7fffffff)) {
-        bv = ls;
-        bi = j;
-      }
-    }
-    group_argmax(bv, bi, dummy);
-#pragma unroll
-    for (int k = 0; k < MAX_K; ++k) c[k] = (j0 + GROUP * k == bi) ? 0.f : -INFINITY;
-    mx = 0.f;
-    lse = 0.f;
-  }
-  float best = -INFINITY, best_lp = -INFINITY;
-  int best_i = 0x7fffffff;
-  const uint64_t base = (uint64_t)(row_ok ? r : 0) * (uint64_t)a.A;
-#pragma unroll
-  for (int k = 0; k < MAX_K; ++k) {
-    const int j = j0 + GROUP * k;
-    if (j < a.A) {
-      const float lsm = (c[k] - mx) - lse;
-      const float f = ppo::unit_float(ppo::random_word(k0, k1, base + (uint64_t)j));
-      // uniform(minval = tiny, maxval = 1): f * (1 - tiny) + tiny, floored at tiny
-      const float tiny = 1.17549435e-38f;
-      const float u = fmaxf(tiny, f * (1.0f - tiny) + tiny);
-      const float z = lsm + -logf(-logf(u));
-      if (z > best || best_i == 0x7fffffff) {
-        best = z;
-        best_i = j;
-        best_lp = lsm;
-      }
-    }
-  }
-  group_argmax(best, best_i, best_lp);
+  int act_i;
+  float lp;
+  ppo::cat::draw(pr, a.A, row_ok, r, k0, k1, a.temperature, j0, act_i, lp);
   if (row_ok && j0 == 0) {
-    a.action[r] = best_i;
-    a.log_prob[r] = best_lp;
+    a.action[r] = act_i;
+    a.log_prob[r] = lp;
     if (a.value) a.value[r] = a.vsrc[(int64_t)r * a.ldv];
   }
 }

@@ -21,17 +21,25 @@ parameters without a copy.
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
-from .learner import (A_ROW, B_KN, EPI_BIAS_ACT, LayerBufs, DenseSpec, FlatState, ForwardChain, Program, _p, forward_bufs,
+from .learner import (A_ROW, B_KN, EPI_BIAS_ACT, LayerBufs, DenseSpec, FlatState, ForwardChain, Program, _act, _p,
+                      forward_bufs,
                       split_forward_bufs)
 
 
 class StepExecutor(ForwardChain):
-    """PPO.step for a fixed number of environments (rows)."""
+    """PPO.step for a fixed number of environments (rows).
 
-    def __init__(self, program: Program, flat: FlatState, rows: int):
+    A float32 shared-trunk MLP of 256-wide Dense layers with one activation
+    and a categorical head of at most 15 logits (the discrete Anakin network)
+    steps in one launch, ``ppo_step_mlp_categorical_f32``; ``fused=False``
+    issues the layer-by-layer GEMMs and the sampling launch instead."""
+
+    def __init__(self, program: Program, flat: FlatState, rows: int, fused: bool = True):
         if program.gru is not None:
             raise TypeError("a recurrent program steps through RecurrentPPO")
         super().__init__(program, flat)
@@ -54,6 +62,21 @@ class StepExecutor(ForwardChain):
             self.HA = torch.zeros(rows, ha.w.ld, **f32)
             self.HC = torch.zeros(rows, hc.w.ld, **f32)
         self.KEY = torch.zeros(2, dtype=torch.int32, device=dev)
+        self.fused = fused and self._fusable(lib)
+
+    def _fusable(self, lib) -> bool:
+        """Whether the one-launch step kernel covers this program."""
+        prog = self.prog
+        trunk = prog.trunk
+        if (self.bf16 or not prog.shared_head or prog.dist["kind"] != "categorical" or not trunk
+                or len(trunk) > lib.ppo_step_mlp_max_layers()):
+            return False
+        if len({s.act for s in trunk}) != 1 or any(s.ln is not None for s in trunk):
+            return False
+        if any(s.fout != 256 or s.ld != 256 or (i > 0 and s.dense.fin != 256) for i, s in enumerate(trunk)):
+            return False
+        h = prog.head_a
+        return h.fin == 256 and h.w.ld <= 16 and prog.head_out == prog.dist["num"] and prog.head_out + 1 <= h.w.ld
 
     def _head(self, st, x, ldx, h: DenseSpec, out: torch.Tensor):
         """Head Dense on the last features (bias added, no activation)."""
@@ -70,6 +93,17 @@ class StepExecutor(ForwardChain):
         key = _p(self.KEY) if key is None else key
         prog = self.prog
         rows = self.rows
+        if self.fused:
+            h, n = prog.head_a, len(prog.trunk)
+            # host arrays of the trunk's kernel / bias pointers (read at launch)
+            ws = (ctypes.c_void_p * n)(*[self.flat.view(s.dense.w) for s in prog.trunk])
+            lds = (ctypes.c_int64 * n)(*[s.ld for s in prog.trunk])
+            bs = (ctypes.c_void_p * n)(*[self.flat.view(s.dense.b) if s.dense.b is not None else None
+                                         for s in prog.trunk])
+            self._call("ppo_step_mlp_categorical_f32", st, obs, ldo, rows, prog.trunk[0].dense.fin, n, ws, lds, bs, _act(prog.trunk[0].act), self.flat.view(h.w), h.w.ld,
+                       self.flat.view(h.b) if h.b is not None else None, prog.dist["num"], key, float(temperature),
+                       action, log_prob, value)
+            return
         if prog.shared_head:
             x, ldx, _ = self._fwd_layers(st, self.trunk, obs, ldo, None, rows)
             self._head(st, x, ldx, prog.head_a, self.HEAD)

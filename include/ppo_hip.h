@@ -104,6 +104,21 @@ int ppo_sample_gaussian_f32(void* stream, const float* mean, int64_t ldm, const 
                             int rows, int D, const float* value_src, int64_t ldv, const uint32_t* key,
                             float temperature, float* action, int64_t lda, float* log_prob, float* value);
 
+/* The whole PPO.step (boonta/algorithms/ppo.py:57-74) of a shared-trunk MLP
+ * with a categorical head in one launch: `layers` trunk Dense layers of 256
+ * features with one activation (network.py:18-49, MLP torso,
+ * networks/blocks/mlp.py), the shared head Dense [256, ldwh] whose columns
+ * 0..A-1 are the logits and column A the value (ActorCritic head), and the
+ * categorical draw of ppo_sample_categorical_f32.  weights / ldw / biases are
+ * HOST arrays of `layers` entries (device pointers to 16-byte aligned
+ * [K_l, 256] kernels, ldw[l] == 256; K_0 = obs_dim, K_l = 256 after); ldwh <= 16.
+ * Same outputs as the trunk GEMMs, the head GEMM and the sampling launch. */
+int ppo_step_mlp_max_layers(void);
+int ppo_step_mlp_categorical_f32(void* stream, const float* obs, int64_t ldo, int rows, int obs_dim, int layers,
+                                 const float* const* weights, const int64_t* ldw, const float* const* biases, int act,
+                                 const float* head_w, int64_t ldwh, const float* head_b, int A, const uint32_t* key,
+                                 float temperature, int32_t* action, float* log_prob, float* value);
+
 /* ------------------------------------------------ Dense + LayerNorm + act
  * One torso layer of flax Dense -> LayerNorm -> activation (the Gaussian
  * workload's towers, hangar recipes' 4 x 256 SiLU MLPs) in a single launch:

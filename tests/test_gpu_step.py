@@ -153,6 +153,43 @@ def test_step_matches_the_oracle(name, temperature):
         np.testing.assert_allclose(aux["log_prob"].cpu().numpy(), lp_or, rtol=rtol, atol=rtol)
 
 
+@pytest.mark.parametrize("rows,pad,temperature", [(1000, 1, 1.0), (2048, 0, 0.7), (37, 3, 0.0)])
+def test_one_launch_step_matches_the_oracle_and_the_chained_launches(rows, pad, temperature):
+    """The discrete Anakin network's whole step in one launch
+    (ppo_step_mlp_categorical_f32): ragged row counts, observation rows with
+    and without 16-byte pitch (pad extra floats per row), greedy draws; against
+    the oracle and the layer-by-layer launches on the same inputs."""
+    from boonta_amd.rollout import StepExecutor
+    r = recipes.make(2).resized(N=rows)
+    D = r.obs_dim
+    params = r.network.init(5, D)["params"]
+    obs = synthetic.rollout(r, T=1, N=rows)["obs"][0]
+    head, value, _ = nets.forward(params, r.network.plan(D), obs)
+    alg = gpu_algorithm(r, use_graph=False)
+    state = alg.init_from_params({"params": params}, D)
+    prog = alg.program(D)
+    o = torch.zeros(rows, D + pad, device="cuda")
+    o[:, :D] = dev(obs)
+    key = make_key(77)
+    out = {}
+    for fused in (True, False):
+        ex = StepExecutor(prog, flat_state_of(state), rows, fused=fused)
+        assert ex.fused == fused
+        ex.KEY.copy_(key_dev(key))
+        act = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
+        lp = torch.full((rows,), float("nan"), device="cuda")
+        v = torch.full((rows,), float("nan"), device="cuda")
+        ex.issue(stream(), o.data_ptr(), D + pad, temperature, act.data_ptr(), lp.data_ptr(), v.data_ptr())
+        torch.cuda.synchronize()
+        out[fused] = (act.cpu().numpy(), lp.cpu().numpy(), v.cpu().numpy())
+    act, lp, v = out[True]
+    np.testing.assert_allclose(v, value, rtol=1e-5, atol=1e-5)
+    check_categorical(act, lp, head, key, temperature, 1e-4, 1e-5)
+    np.testing.assert_allclose(v, out[False][2], rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(lp, out[False][1], rtol=1e-5, atol=1e-5)
+    assert (act == out[False][0]).mean() > 0.99
+
+
 def test_step_takes_a_device_key_and_follows_the_updated_parameters():
     r = recipes.make(2).resized(N=256)
     D = r.obs_dim

@@ -142,7 +142,13 @@ def test_rollout_step_launches_match_the_c_signatures(config):
         calls = ex.record(4096, r.obs_dim, 8192, 12288, 16384, 1.0, 20480, 24576, 28672, 32768)
         assert [n for n, _ in calls].count("ppo_gru_fwd_step_f32") == 1
     else:
-        ex = StepExecutor(prog, flat, N)
+        fused = StepExecutor(prog, flat, N)
+        if fused.fused:
+            # shared 256-wide fp32 trunk, categorical head: the whole step in one launch
+            (name, args), = fused.record(4096, r.obs_dim, 1.0, 8192, 12288, 16384)
+            assert name == "ppo_step_mlp_categorical_f32" and args[3] == N
+            assert len(args) == len(_lib.SIGNATURES[name][1]) and args[5] == len(prog.trunk)
+        ex = StepExecutor(prog, flat, N, fused=False)
         calls = ex.record(4096, r.obs_dim, 1.0, 8192, 12288, 16384)
     names = [n for n, _ in calls]
     want = "ppo_sample_categorical_f32" if prog.dist["kind"] == "categorical" else "ppo_sample_gaussian_f32"
@@ -155,6 +161,8 @@ def test_rollout_step_launches_match_the_c_signatures(config):
     if config == 3:
         # 256-wide fp32 LayerNorm layers: Dense + LayerNorm + SiLU in one launch each
         assert names.count("ppo_gemm_ln_act_fwd_f32") == 8 and "ppo_layernorm_act_fwd_f32" not in names
+    if prog.gru is None:
+        assert fused.fused == (config == 2), "only the discrete Anakin network fits the one-launch step"
 
 
 def test_gaussian_update_fuses_dense_and_layernorm_forward():
