@@ -119,6 +119,22 @@ int ppo_step_mlp_categorical_f32(void* stream, const float* obs, int64_t ldo, in
                                  const float* head_w, int64_t ldwh, const float* head_b, int A, const uint32_t* key,
                                  float temperature, int32_t* action, float* log_prob, float* value);
 
+/* --------------------------------------------- prioritised env selection
+ * Replaces the minibatch selection of RecurrentPuPO.update
+ * (boonta/algorithms/recurrent_pupo.py:226-236): priority[n] =
+ * (sum_t |advantages[t, n]|) ** priority_exponent, probabilities[n] =
+ * (priority[n] + 1e-6) / (sum priority + 1e-6), indices =
+ * jax.random.choice(key, N, (width,), replace=True, p=probabilities) (inverse
+ * CDF on the key's uniform stream), weights[i] = (N * probabilities[indices[i]])
+ * ** -beta.  advantages: float [T, N] with row pitch lda (the V-trace output of
+ * ppo_gae_f32 with rho = min(ratio, advantage_clip), c = min(ratio,
+ * trace_clip)); indices int32 [width]; weights float [width]; probabilities
+ * float [N] (required).  N <= ppo_priority_choice_max_envs(). */
+int ppo_priority_choice_max_envs(void);
+int ppo_priority_choice_f32(void* stream, const float* advantages, int64_t lda, int T, int N, float priority_exponent,
+                            float beta, const uint32_t* key, int width, int32_t* indices, float* weights,
+                            float* probabilities);
+
 /* ------------------------------------------------ Dense + LayerNorm + act
  * One torso layer of flax Dense -> LayerNorm -> activation (the Gaussian
  * workload's towers, hangar recipes' 4 x 256 SiLU MLPs) in a single launch:

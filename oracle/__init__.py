@@ -23,6 +23,10 @@ Parity status of each part (what pins it):
   endpoints on hand-computed words, chi-square of Gumbel-max frequencies,
   normal moments and a Kolmogorov-Smirnov test, and scipy's log-densities
   (parity with a live jax.random bit stream: unpinned).
+- ``priority``: RecurrentPuPO's prioritised env selection, pinned by the
+  closed form of equal priorities, a single-env distribution, a chi-square
+  test of draw frequencies and the weights' closed form (parity with a live
+  ``jax.random.choice`` stream: unpinned).
 - ``ppo.optimizer_update``: closed form of Adam's first step
   (|update| = lr for |g| >> eps) and clip invariants; optax itself: unpinned.
 """

@@ -67,3 +67,23 @@ def test_ssm_scan_rejects_missing_done_flags():
     lib = _lib.load()
     assert lib.ppo_ssm_scan_fwd(None, 0, 1, 1, None, None, 1, 1, 2, 2, 2) == -1
     assert lib.ppo_ssm_scan_bwd(None, 0, 1, 1, None, None, 1, 1, 1, 1, 1, 2, 2, 2) == -1
+
+
+def test_priority_choice_rejects_bad_arguments_without_launching():
+    lib = _lib.load()
+    big = lib.ppo_priority_choice_max_envs() + 1
+    assert lib.ppo_priority_choice_f32(None, 1, big, 4, big, 0.6, 0.4, 1, 4, 1, 1, 1) == -1
+    assert b"ppo_priority_choice_f32" in lib.ppo_last_error()
+    # the probabilities buffer is required (the weights are read from it)
+    assert lib.ppo_priority_choice_f32(None, 1, 8, 4, 8, 0.6, 0.4, 1, 4, 1, 1, None) == -1
+
+
+def test_one_launch_step_rejects_unsupported_networks_without_launching():
+    lib = _lib.load()
+    deep = lib.ppo_step_mlp_max_layers() + 1
+    assert lib.ppo_step_mlp_categorical_f32(None, 1, 400, 16, 400, deep, None, None, None, 1, 1, 8, None, 6, 1, 1.0,
+                                           1, 1, 1) == -1
+    assert b"ppo_step_mlp_categorical_f32" in lib.ppo_last_error()
+    # head wider than 16 outputs
+    assert lib.ppo_step_mlp_categorical_f32(None, 1, 400, 16, 400, 2, None, None, None, 1, 1, 20, None, 6, 1, 1.0,
+                                           1, 1, 1) == -1

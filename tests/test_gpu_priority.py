@@ -1,0 +1,73 @@
+"""Parity of RecurrentPuPO's prioritised env selection
+(boonta/algorithms/recurrent_pupo.py:226-236; ``ppo_priority_choice_f32``)
+against the oracle (oracle/priority.py) on the same seeded V-trace-shaped
+advantages.
+
+Tolerances (written here): probabilities 1e-5 relative (float32 priority
+sums against the oracle's float64); indices bit-exact against the oracle's
+draw on the kernel's own probabilities wherever the draw lies more than
+1e-12 of the total from a cumulative boundary (at least 99.9 % of draws),
+weights 2e-6 relative to (N p[idx]) ** -beta on those probabilities; against
+the oracle's float64 probabilities, at least 95 % of indices equal and the
+rest neighbours, weights 1e-4 relative where the indices agree.
+"""
+import numpy as np
+import pytest
+import torch
+
+from boonta_amd.algorithms.pupo import prioritized_choice
+from boonta_amd.random import key as make_key
+from oracle import priority
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # (T, N, width, exponent, beta): the recurrent workload's 64 x 1024 envs
+    # drawing 256-env minibatches; ragged, one-env, maximum and wide draws
+    (64, 1024, 256, 0.6, 0.4),
+    (7, 1000, 1000, 1.0, 1.0),
+    (3, 1, 5, 0.6, 0.4),
+    (2, 16384, 4096, 0.5, 0.7),
+    (16, 3000, 20000, 0.8, 0.0),
+]
+
+
+@pytest.mark.parametrize("T,N,width,exponent,beta", CASES)
+def test_priority_choice_matches_the_oracle(T, N, width, exponent, beta):
+    rng = np.random.default_rng(T * 7919 + N)
+    adv = (rng.standard_normal((T, N)) * rng.uniform(0.1, 3.0, N)).astype(np.float32)
+    k = make_key(1000 + N)
+    idx, w, prob = prioritized_choice(torch.from_numpy(adv).cuda(), k, width, exponent, beta)
+    torch.cuda.synchronize()
+    idx, w, prob = idx.cpu().numpy(), w.cpu().numpy(), prob.cpu().numpy()
+    i_or, w_or, p_or, _ = priority.priority_choice(adv, k, width, exponent, beta)
+    np.testing.assert_allclose(prob, p_or, rtol=1e-5, atol=1e-9)
+    assert idx.min() >= 0 and idx.max() < N
+    # the draw on the kernel's own float32 probabilities: exact but for draws
+    # within float64 rounding of a boundary
+    i_own, margin = priority.choice(k, prob.astype(np.float64), width)
+    ok = margin > 1e-12
+    assert ok.mean() >= 0.999
+    np.testing.assert_array_equal(idx[ok], i_own[ok])
+    np.testing.assert_allclose(w, (N * prob[idx].astype(np.float64)) ** -beta, rtol=2e-6)
+    # against the oracle's float64 probabilities: neighbours at worst
+    same = idx == i_or
+    assert same.mean() >= 0.95
+    assert np.abs(idx - i_or).max() <= 1
+    np.testing.assert_allclose(w[same], w_or[same], rtol=1e-4)
+
+def test_all_zero_advantages_draw_uniformly_and_a_device_key_matches_a_host_key():
+    T, N, width = 4, 512, 2048
+    adv = torch.zeros(T, N, device="cuda")
+    k = make_key(3)
+    idx, w, prob = prioritized_choice(adv, k, width, 0.6, 0.4)
+    kd = torch.from_numpy(np.asarray(k, np.uint32).view(np.int32).copy()).cuda()
+    idx2, w2, prob2 = prioritized_choice(adv, kd, width, 0.6, 0.4)
+    torch.cuda.synchronize()
+    assert torch.equal(idx, idx2) and torch.equal(w, w2)
+    # (0 + 1e-6) / (0 + 1e-6) = 1 for every env: equal weights on a total of N
+    np.testing.assert_allclose(prob.cpu().numpy(), 1.0, rtol=1e-6)
+    i_or, _, _, margin = priority.priority_choice(np.zeros((T, N)), k, width, 0.6, 0.4)
+    ok = margin > 1e-12
+    np.testing.assert_array_equal(idx.cpu().numpy()[ok], i_or[ok])
+
