@@ -30,6 +30,7 @@ SIGNATURES = {
     "ppo_event_destroy": (I, [P]),
     "ppo_stream_wait": (I, [P, P, P]),
     "ppo_gae_f32": (I, [P, P, P, P, P, P, P, P, P, P, I, I, D, D, I]),
+    "ppo_vtrace_f32": (I, [P, P, P, P, P, P, P, I64, F, F, P, P, I, I, D, D, I]),
     "ppo_normalize_workspace": (SZ, [I64]),
     "ppo_normalize_advantages_f32": (I, [P, P, I64, P, SZ]),
     "ppo_threefry_split": (I, [P, P, P, I64]),

@@ -6,10 +6,12 @@ returns what ``minibatch_fn`` computes from the V-trace advantages before it
 gathers the minibatch: the env indices ``jax.random.choice(key, num_envs,
 (width,), replace=True, p=probabilities)``, the importance weights
 ``(num_envs * probabilities[indices]) ** -beta`` and the probabilities
-themselves, in one launch of ``ppo_priority_choice_f32``.  The V-trace
-advantages come from ``generalized_advantage_estimator`` with per-element
-``rho = min(ratio, advantage_clip)`` and ``c = min(ratio, trace_clip)``
-(recurrent_pupo.py:210-220), which ``ppo_gae_f32`` takes as arrays.
+themselves, in one launch of ``ppo_priority_choice_f32``.
+
+``vtrace(...)`` is the ``vtrace`` closure of recurrent_pupo.py:210-220: the
+advantage estimator with ``rho = min(ratio, advantage_clip)`` and
+``c = min(ratio, trace_clip)`` on the env-major ratio, in one launch of
+``ppo_vtrace_f32`` (the GAE scan forming the clipped weights as it reads them).
 """
 from __future__ import annotations
 
@@ -45,3 +47,29 @@ def prioritized_choice(advantages: torch.Tensor, key, width: int, priority_expon
               float(priority_exponent), float(beta), kd.data_ptr(), width, indices.data_ptr(), weights.data_ptr(),
               probabilities.data_ptr())
     return indices, weights, probabilities
+
+
+def _u8(x):
+    return x.to(torch.uint8).contiguous()
+
+
+def vtrace(reward: torch.Tensor, terminated: torch.Tensor, truncated: torch.Tensor, values: torch.Tensor,
+           bootstrap: torch.Tensor, ratio: torch.Tensor, gamma: float, gae_lambda: float, advantage_clip: float,
+           trace_clip: float, chunks: int = 0):
+    """reward / values float32 [T, N], terminated / truncated bool [T, N],
+    bootstrap [N], ratio float32 [N, T] (env-major, unit column stride), all
+    on the device.  Returns (advantages, returns) float32 [T, N]."""
+    T, N = reward.shape
+    if ratio.dim() != 2 or ratio.shape[0] != N or ratio.shape[1] != T or ratio.stride(1) != 1:
+        raise ValueError("ratio must be [N, T] with unit column stride")
+    f32 = [x.to(torch.float32).contiguous() for x in (reward, values, bootstrap)]
+    if ratio.dtype != torch.float32:
+        raise TypeError("ratio must be float32")
+    te, tr = _u8(terminated), _u8(truncated)
+    adv = torch.empty(T, N, dtype=torch.float32, device=reward.device)
+    ret = torch.empty_like(adv)
+    st = torch.cuda.current_stream(reward.device).cuda_stream
+    _lib.call("ppo_vtrace_f32", st, f32[0].data_ptr(), te.data_ptr(), tr.data_ptr(), f32[1].data_ptr(),
+              f32[2].data_ptr(), ratio.data_ptr(), ratio.stride(0), float(advantage_clip), float(trace_clip),
+              adv.data_ptr(), ret.data_ptr(), T, N, float(gamma), float(gae_lambda), chunks)
+    return adv, ret

@@ -26,6 +26,9 @@ struct GaeArgs {
   const float* bootstrap;
   const float* rho;  // may be null (1.0)
   const float* c;    // may be null (1.0)
+  const float* ratio;  // V-trace: [N, T] importance ratios (row pitch ldr), or null
+  int64_t ldr;
+  float rho_clip, c_clip;
   float* adv;
   float* ret;
   int T, N;
@@ -43,8 +46,13 @@ __device__ __forceinline__ Step gae_step(const GaeArgs& a, int t, int n, float n
   const float te = a.terminated[i] ? 1.f : 0.f;
   const float tr = a.truncated[i] ? 1.f : 0.f;
   const float v = a.values[i];
-  const float rho = a.rho ? a.rho[i] : 1.f;
-  const float c = a.c ? a.c[i] : 1.f;
+  float rho = a.rho ? a.rho[i] : 1.f;
+  float c = a.c ? a.c[i] : 1.f;
+  if (a.ratio) {  // rho = min(ratio, advantage_clip), c = min(ratio, trace_clip)
+    const float q = a.ratio[(int64_t)n * a.ldr + t];
+    rho = fminf(q, a.rho_clip);
+    c = fminf(q, a.c_clip);
+  }
   const float one_te = __fsub_rn(1.f, te);
   const float one_tr = __fsub_rn(1.f, tr);
   float d = __fadd_rn(r, __fmul_rn(__fmul_rn(a.gamma, one_te), next_value));
@@ -100,29 +108,57 @@ __global__ void __launch_bounds__(1024) gae_kernel(GaeArgs a) {
 
 }  // namespace
 
-PPO_EXPORT int ppo_gae_f32(void* stream, const float* reward, const uint8_t* terminated,
-                           const uint8_t* truncated, const float* values,
-                           const float* bootstrap, const float* rho, const float* c,
-                           float* advantages, float* returns, int T, int N, double gamma,
-                           double gae_lambda, int chunks) {
-  if (T < 0 || N < 0) return ppo::set_error(PPO_ERR_ARG, "ppo_gae_f32: negative shape T=%d N=%d", T, N);
+namespace {
+
+int launch_gae(void* stream, GaeArgs a, double gamma, double gae_lambda, int chunks, const char* name) {
+  const int T = a.T, N = a.N;
+  if (T < 0 || N < 0) return ppo::set_error(PPO_ERR_ARG, "%s: negative shape T=%d N=%d", name, T, N);
   if (T == 0 || N == 0) return PPO_OK;
-  if (!reward || !terminated || !truncated || !values || !bootstrap || !advantages || !returns)
-    return ppo::set_error(PPO_ERR_ARG, "ppo_gae_f32: null buffer");
+  if (!a.reward || !a.terminated || !a.truncated || !a.values || !a.bootstrap || !a.adv || !a.ret)
+    return ppo::set_error(PPO_ERR_ARG, "%s: null buffer", name);
   if (chunks <= 0) {
     // enough waves for ~4 per CU, capped by T and the LDS table
     const int waves = (N + 63) / 64;
     chunks = 1;
     while (chunks < 16 && waves * chunks < 1024 && T / (chunks * 2) >= 4) chunks *= 2;
   }
-  if (chunks > 16) return ppo::set_error(PPO_ERR_ARG, "ppo_gae_f32: chunks %d > 16", chunks);
+  if (chunks > 16) return ppo::set_error(PPO_ERR_ARG, "%s: chunks %d > 16", name, chunks);
   if (chunks > T) chunks = T;
-  GaeArgs a{reward, terminated, truncated, values, bootstrap, rho, c, advantages, returns,
-            T, N, (float)gamma, (float)(gamma * gae_lambda)};
+  a.gamma = (float)gamma;
+  a.gl = (float)(gamma * gae_lambda);
   dim3 block(64, chunks);
   dim3 grid((N + 63) / 64);
   hipLaunchKernelGGL(gae_kernel, grid, block, 0, ppo::as_stream(stream), a);
-  return ppo::check_launch("ppo_gae_f32");
+  return ppo::check_launch(name);
+}
+
+}  // namespace
+
+PPO_EXPORT int ppo_gae_f32(void* stream, const float* reward, const uint8_t* terminated,
+                           const uint8_t* truncated, const float* values,
+                           const float* bootstrap, const float* rho, const float* c,
+                           float* advantages, float* returns, int T, int N, double gamma,
+                           double gae_lambda, int chunks) {
+  GaeArgs a{reward, terminated, truncated, values, bootstrap, rho, c, nullptr, 0, 0.f, 0.f, advantages, returns,
+            T, N, 0.f, 0.f};
+  return launch_gae(stream, a, gamma, gae_lambda, chunks, "ppo_gae_f32");
+}
+
+// V-trace as RecurrentPuPO.update calls the estimator
+// (boonta/algorithms/recurrent_pupo.py:210-220): ratio is [N, T] (env-major,
+// row pitch ldr) and rho = min(ratio, advantage_clip), c = min(ratio,
+// trace_clip) are formed as the scan reads them.
+PPO_EXPORT int ppo_vtrace_f32(void* stream, const float* reward, const uint8_t* terminated,
+                              const uint8_t* truncated, const float* values, const float* bootstrap,
+                              const float* ratio, int64_t ldr, float advantage_clip, float trace_clip,
+                              float* advantages, float* returns, int T, int N, double gamma, double gae_lambda,
+                              int chunks) {
+  if (!ratio || ldr < T)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_vtrace_f32: ratio [N, T] needs a row pitch >= T (%lld < %d)",
+                          (long long)ldr, T);
+  GaeArgs a{reward, terminated, truncated, values, bootstrap, nullptr, nullptr, ratio, ldr, advantage_clip,
+            trace_clip, advantages, returns, T, N, 0.f, 0.f};
+  return launch_gae(stream, a, gamma, gae_lambda, chunks, "ppo_vtrace_f32");
 }
 
 // ------------------------------------------------- advantage normalisation

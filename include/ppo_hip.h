@@ -63,6 +63,15 @@ int ppo_gae_f32(void* stream, const float* reward, const uint8_t* terminated, co
                 float* advantages, float* returns, int T, int N, double gamma, double gae_lambda,
                 int chunks);
 
+/* V-trace (boonta/algorithms/recurrent_pupo.py:210-220: the estimator above
+ * with rho = min(ratio, advantage_clip), c = min(ratio, trace_clip)); ratio
+ * is float [N, T] env-major with row pitch ldr >= T, moved to time-major as
+ * the reference's jnp.moveaxis does, by indexing. */
+int ppo_vtrace_f32(void* stream, const float* reward, const uint8_t* terminated, const uint8_t* truncated,
+                   const float* values, const float* bootstrap, const float* ratio, int64_t ldr, float advantage_clip,
+                   float trace_clip, float* advantages, float* returns, int T, int N, double gamma, double gae_lambda,
+                   int chunks);
+
 /* Advantage normalisation (A - mean) / (std + 1e-8), population std over
  * all n advantages, in place: boonta/algorithms/ppo.py:220-221 and
  * recurrent_ppo.py:206-207 (PPOConfig.normalize_advantage). */

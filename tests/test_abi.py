@@ -87,3 +87,9 @@ def test_one_launch_step_rejects_unsupported_networks_without_launching():
     # head wider than 16 outputs
     assert lib.ppo_step_mlp_categorical_f32(None, 1, 400, 16, 400, 2, None, None, None, 1, 1, 20, None, 6, 1, 1.0,
                                            1, 1, 1) == -1
+
+
+def test_vtrace_rejects_a_short_ratio_pitch_without_launching():
+    lib = _lib.load()
+    assert lib.ppo_vtrace_f32(None, 1, 1, 1, 1, 1, 1, 3, 1.0, 1.0, 1, 1, 4, 8, 0.99, 0.95, 0) == -1
+    assert b"ppo_vtrace_f32" in lib.ppo_last_error()

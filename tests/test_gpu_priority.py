@@ -1,4 +1,6 @@
-"""Parity of RecurrentPuPO's prioritised env selection
+"""Parity of RecurrentPuPO's V-trace advantages
+(boonta/algorithms/recurrent_pupo.py:210-220; ``ppo_vtrace_f32``) and its
+prioritised env selection
 (boonta/algorithms/recurrent_pupo.py:226-236; ``ppo_priority_choice_f32``)
 against the oracle (oracle/priority.py) on the same seeded V-trace-shaped
 advantages.
@@ -15,7 +17,9 @@ import numpy as np
 import pytest
 import torch
 
-from boonta_amd.algorithms.pupo import prioritized_choice
+from boonta_amd import _lib
+from boonta_amd.algorithms.pupo import prioritized_choice, vtrace
+from oracle import gae as ogae
 from boonta_amd.random import key as make_key
 from oracle import priority
 
@@ -71,3 +75,36 @@ def test_all_zero_advantages_draw_uniformly_and_a_device_key_matches_a_host_key(
     ok = margin > 1e-12
     np.testing.assert_array_equal(idx.cpu().numpy()[ok], i_or[ok])
 
+
+
+@pytest.mark.parametrize("T,N,chunks", [(64, 1024, 0), (64, 1024, 1), (7, 100, 3), (1, 5, 0)])
+def test_vtrace_matches_the_oracle_and_explicit_clipped_weights(T, N, chunks):
+    """rho = min(ratio, advantage_clip), c = min(ratio, trace_clip) on the
+    env-major ratio (recurrent_pupo.py:210-220): against the oracle's GAE
+    with those weights (1e-5, the reference GAE test's tolerance), and
+    bit-identical to ppo_gae_f32 given the same weights as arrays."""
+    g = np.random.default_rng(T * 31 + N)
+    r = g.normal(size=(T, N)).astype(np.float32)
+    v = g.normal(size=(T, N)).astype(np.float32)
+    b = g.normal(size=N).astype(np.float32)
+    te = g.random((T, N)) < 0.02
+    tr = (g.random((T, N)) < 0.01) & ~te
+    ratio = g.uniform(0.3, 2.0, (N, T)).astype(np.float32)
+    ratio[:, : max(T // 4, 1)] = 1.0    # the first minibatch's ratios are ones
+    aclip, cclip = 1.0, 0.9
+    d = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    adv, ret = vtrace(d(r), d(te), d(tr), d(v), d(b), d(ratio), 0.99, 0.95, aclip, cclip, chunks)
+    rho = np.minimum(ratio.T, np.float32(aclip))
+    c = np.minimum(ratio.T, np.float32(cclip))
+    exp_a, exp_r = ogae.gae(r, te, tr, v, b, 0.99, 0.95, rho=rho.astype(np.float64), c=c.astype(np.float64))
+    np.testing.assert_allclose(adv.cpu().numpy(), exp_a, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(ret.cpu().numpy(), exp_r, rtol=1e-5, atol=1e-5)
+    a2 = torch.empty(T, N, device="cuda")
+    r2 = torch.empty(T, N, device="cuda")
+    u8 = lambda x: d(x.astype(np.uint8))
+    st = torch.cuda.current_stream().cuda_stream
+    R, TE, TR, V, B, RHO, C = d(r), u8(te), u8(tr), d(v), d(b), d(rho), d(c)
+    _lib.call("ppo_gae_f32", st, R.data_ptr(), TE.data_ptr(), TR.data_ptr(), V.data_ptr(), B.data_ptr(),
+              RHO.data_ptr(), C.data_ptr(), a2.data_ptr(), r2.data_ptr(), T, N, 0.99, 0.95, chunks)
+    torch.cuda.synchronize()
+    assert torch.equal(adv, a2) and torch.equal(ret, r2)
