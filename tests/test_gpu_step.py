@@ -190,6 +190,45 @@ def test_one_launch_step_matches_the_oracle_and_the_chained_launches(rows, pad, 
     assert (act == out[False][0]).mean() > 0.99
 
 
+def test_one_launch_step_replays_from_a_graph():
+    """The rollout bench captures env steps into a HIP graph: every replay,
+    with eager work and synchronisations between replays, equals the eager
+    step bit for bit."""
+    from boonta_amd.rollout import StepExecutor
+    rows = 2048
+    r = recipes.make(2).resized(N=rows)
+    D = r.obs_dim
+    params = r.network.init(8, D)["params"]
+    obs = dev(synthetic.rollout(r, T=1, N=rows)["obs"][0])
+    alg = gpu_algorithm(r, use_graph=False)
+    state = alg.init_from_params({"params": params}, D)
+    ex = StepExecutor(alg.program(D), flat_state_of(state), rows)
+    assert ex.fused
+    ex.KEY.copy_(key_dev(make_key(31)))
+    act = torch.zeros(rows, dtype=torch.int32, device="cuda")
+    lp = torch.zeros(rows, device="cuda")
+    v = torch.zeros(rows, device="cuda")
+    args = (obs.data_ptr(), D, 1.0, act.data_ptr(), lp.data_ptr(), v.data_ptr())
+    ex.issue(stream(), *args)
+    torch.cuda.synchronize()
+    want = (act.clone(), lp.clone(), v.clone())
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            ex.issue(side.cuda_stream, *args)
+    torch.cuda.current_stream().wait_stream(side)
+    for _ in range(3):
+        act.fill_(-1)
+        lp.zero_()
+        v.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(act, want[0]) and torch.equal(lp, want[1]) and torch.equal(v, want[2])
+
+
 def test_step_takes_a_device_key_and_follows_the_updated_parameters():
     r = recipes.make(2).resized(N=256)
     D = r.obs_dim
