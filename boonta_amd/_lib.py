@@ -42,6 +42,7 @@ SIGNATURES = {
     "ppo_sample_categorical_f32": (I, [P, P, I64, I, I, P, I64, P, F, P, P, P]),
     "ppo_sample_gaussian_f32": (I, [P, P, I64, P, I64, I, I, P, I64, P, F, P, I64, P, P]),
     "ppo_step_mlp_max_layers": (I, []),
+    "ppo_step_mlp_max_obs": (I, []),
     "ppo_step_mlp_categorical_f32": (I, [P, P, I64, I, I, I, P, P, P, I, P, I64, P, I, P, F, P, P, P]),
     "ppo_priority_choice_max_envs": (I, []),
     "ppo_priority_choice_f32": (I, [P, P, I64, I, I, F, F, P, I, P, P, P]),

@@ -9,7 +9,8 @@
 // gemm_ln.hip: lane li of quarter q holds columns 64 q + 4 li .. + 3), each
 // quarter's contraction split over two waves by alternate 32-deep k chunks,
 // whose partials meet in LDS.  A layer's input is the observation rows (first
-// layer) or the previous layer's activations in LDS; its kernel is read as
+// layer, staged in LDS by one burst of loads at the start) or the previous
+// layer's activations in LDS; its kernel is read as
 // 16-byte rows from global memory (L2: every workgroup reads the same
 // kernels).  Two waves per SIMD hide each other's load latency.  The head
 // (<= 16 outputs) splits its 256-deep contraction over the eight waves; then
@@ -29,6 +30,9 @@ constexpr int SM_MAX_LAYERS = 4;
 constexpr int SM_HEAD = 16;  // head outputs: logits and the value column
 constexpr int SM_U = 2;      // 16-deep k steps per chunk
 constexpr int SM_CH = 16 * SM_U;  // chunk depth
+constexpr int SM_MAX_OBS = 1024;  // observation features staged in LDS
+constexpr int SM_XP = SM_MAX_OBS + 4;  // their LDS row pitch
+constexpr int SM_STAGE = SM_ROWS * SM_MAX_OBS / 4 / SM_THREADS;  // staged vectors per thread
 
 struct StepMlpArgs {
   const float* obs;
@@ -56,49 +60,32 @@ __device__ __forceinline__ floatx4 mfma4(const float (&a)[4], const float (&b)[4
   return acc;
 }
 
-// acc[j] += A[16 rows, K] W[K, c4 + j] for this lane's four columns.  A is
-// the observation rows (FROM_H false; xrow is row 0 for a dead row, whose
-// values are zeroed) or the previous layer's activations in h (K = 256).
+// acc[j] += A[16 rows, K] W[K, c4 + j] for this lane's four columns, A in
+// LDS (row pitch PITCH floats, zero from K up to the next multiple of 64): the
+// staged observation rows (first layer) or the previous layer's activations.
 // The k range is cut into pairs of SM_CH-deep chunks; the wave of k half
 // `khalf` takes chunk `khalf` of every pair (the two k halves of a column
 // quarter are two waves).  Double-buffered: the loads of the next chunk are in
-// flight while the current chunk's MFMAs run.  Every load is unconditional
-// (addresses clamped in bounds, values past K zeroed by selects, the prefetch
-// past the last chunk repeating it) so that the compiler's wait before a
-// chunk's MFMAs leaves the next chunk's loads outstanding.
-template <bool FROM_H, bool VA>
-__device__ __forceinline__ void layer_acc(floatx4 (&acc)[4], const float (*h)[SM_F + 4], const float* xrow,
-                                          bool a_live, int K, int khalf, const float* W, int li, int kq, int c4) {
+// flight while the current chunk's MFMAs run.  Every kernel load is
+// unconditional (rows clamped in bounds, values past K zeroed by selects, the
+// prefetch past the last chunk repeating it) so that the compiler's wait
+// before a chunk's MFMAs leaves the next chunk's loads outstanding.
+template <int PITCH>
+__device__ __forceinline__ void layer_acc(floatx4 (&acc)[4], const float* as, int K, int khalf, const float* W,
+                                          int li, int kq, int c4) {
   const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
   auto load = [&](int k0, float (&a)[SM_U][4], floatx4 (&w)[SM_U][4]) {
 #pragma unroll
     for (int u = 0; u < SM_U; ++u) {
       const int kb = k0 + 16 * u + 4 * kq;
-      if (FROM_H) {
-        const floatx4 x4 = *reinterpret_cast<const floatx4*>(&h[li][kb]);
+      const floatx4 x4 = *reinterpret_cast<const floatx4*>(as + li * PITCH + kb);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) a[u][s] = x4[s];
-      } else if (VA) {
-        const floatx4 x4 = *reinterpret_cast<const floatx4*>(xrow + (unsigned)min(kb, K - 4));
-        const bool ok = a_live && kb < K;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) a[u][s] = ok ? x4[s] : 0.f;
-      } else {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const float x = xrow[(unsigned)min(kb + s, K - 1)];
-          a[u][s] = (a_live && kb + s < K) ? x : 0.f;
-        }
-      }
+      for (int s = 0; s < 4; ++s) a[u][s] = x4[s];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const int k = kb + s;
-        if (FROM_H) {  // K = 256
-          w[u][s] = *reinterpret_cast<const floatx4*>(W + ((unsigned)k * SM_F + (unsigned)c4));
-        } else {
-          const floatx4 v = *reinterpret_cast<const floatx4*>(W + ((unsigned)min(k, K - 1) * SM_F + (unsigned)c4));
-          w[u][s] = k < K ? v : zero;
-        }
+        const floatx4 v = *reinterpret_cast<const floatx4*>(W + ((unsigned)min(k, K - 1) * SM_F + (unsigned)c4));
+        w[u][s] = k < K ? v : zero;
       }
     }
   };
@@ -128,6 +115,7 @@ __device__ __forceinline__ void layer_acc(floatx4 (&acc)[4], const float (*h)[SM
 
 template <bool VA>
 __global__ void __launch_bounds__(SM_THREADS) step_mlp_kernel(StepMlpArgs p) {
+  __shared__ __attribute__((aligned(16))) float xs[SM_ROWS][SM_XP];
   __shared__ __attribute__((aligned(16))) float h[SM_ROWS][SM_F + 4];
   __shared__ __attribute__((aligned(16))) float red[SM_ROWS][SM_F + 4];
   __shared__ float s_head[8][SM_ROWS][SM_HEAD + 1];
@@ -139,19 +127,44 @@ __global__ void __launch_bounds__(SM_THREADS) step_mlp_kernel(StepMlpArgs p) {
   const int li = lane & 15;
   const int kq = lane >> 4;
   const int r0 = blockIdx.x * SM_ROWS;
-  const int ra = r0 + li;
-  const bool a_live = ra < p.rows;
-  const float* xrow = p.obs + (a_live ? (int64_t)ra * p.ldo : 0);
   const int c4 = 64 * quarter + 4 * li;
+
+  // stage the 16 observation rows in LDS, zero past K0 (to a multiple of 64)
+  // and for rows past the end: all of the workgroup's loads are issued
+  // before the first is waited on
+  const int KP = (p.K0 + 63) / 64 * 64;
+  if (VA) {
+    const int q = KP / 4;  // 16-byte vectors per staged row
+    floatx4 xv[SM_STAGE];
+#pragma unroll
+    for (int j = 0; j < SM_STAGE; ++j) {
+      const int v = threadIdx.x + SM_THREADS * j;
+      const int rr = min(v / q, SM_ROWS - 1), c = v - (v / q) * q;
+      const int r = min(r0 + rr, p.rows - 1);
+      const floatx4 x = *reinterpret_cast<const floatx4*>(p.obs + (int64_t)r * p.ldo + min(4 * c, p.K0 - 4));
+      xv[j] = (v < SM_ROWS * q && r0 + rr < p.rows && 4 * c < p.K0) ? x : floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int j = 0; j < SM_STAGE; ++j) {
+      const int v = threadIdx.x + SM_THREADS * j;
+      if (v < SM_ROWS * q) *reinterpret_cast<floatx4*>(&xs[v / q][4 * (v % q)]) = xv[j];
+    }
+  } else {
+    for (int v = threadIdx.x; v < SM_ROWS * KP; v += SM_THREADS) {
+      const int rr = v / KP, c = v - rr * KP;
+      xs[rr][c] = (r0 + rr < p.rows && c < p.K0) ? p.obs[(int64_t)(r0 + rr) * p.ldo + c] : 0.f;
+    }
+  }
+  __syncthreads();
 
   for (int l = 0; l < p.L; ++l) {
     floatx4 acc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
     if (l == 0) {
-      layer_acc<false, VA>(acc, h, xrow, a_live, p.K0, khalf, p.W[0], li, kq, c4);
+      layer_acc<SM_XP>(acc, &xs[0][0], p.K0, khalf, p.W[0], li, kq, c4);
     } else {
-      layer_acc<true, VA>(acc, h, xrow, a_live, SM_F, khalf, p.W[l], li, kq, c4);
+      layer_acc<SM_F + 4>(acc, &h[0][0], SM_F, khalf, p.W[l], li, kq, c4);
     }
     __syncthreads();  // every wave has read this layer's input from h
     if (khalf == 1) {
@@ -222,13 +235,14 @@ bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 
 }  // namespace
 
 PPO_EXPORT int ppo_step_mlp_max_layers() { return SM_MAX_LAYERS; }
+PPO_EXPORT int ppo_step_mlp_max_obs() { return SM_MAX_OBS; }
 
 PPO_EXPORT int ppo_step_mlp_categorical_f32(void* stream, const float* obs, int64_t ldo, int rows, int obs_dim,
                                            int layers, const float* const* weights, const int64_t* ldw,
                                            const float* const* biases, int act, const float* head_w,
                                            int64_t ldwh, const float* head_b, int A, const uint32_t* key,
                                            float temperature, int32_t* action, float* log_prob, float* value) {
-  if (rows < 0 || obs_dim < 1 || ldo < obs_dim || layers < 1 || layers > SM_MAX_LAYERS || act < 0 || act > 3 ||
+  if (rows < 0 || obs_dim < 1 || obs_dim > SM_MAX_OBS || ldo < obs_dim || layers < 1 || layers > SM_MAX_LAYERS || act < 0 || act > 3 ||
       A < 1 || A + 1 > ldwh || ldwh > SM_HEAD || !weights || !ldw || !biases)
     return ppo::set_error(PPO_ERR_ARG, "ppo_step_mlp_categorical_f32: bad argument (rows %d obs %d layers %d A %d "
                           "ldwh %lld)", rows, obs_dim, layers, A, (long long)ldwh);

@@ -69,7 +69,7 @@ class StepExecutor(ForwardChain):
         prog = self.prog
         trunk = prog.trunk
         if (self.bf16 or not prog.shared_head or prog.dist["kind"] != "categorical" or not trunk
-                or len(trunk) > lib.ppo_step_mlp_max_layers()):
+                or len(trunk) > lib.ppo_step_mlp_max_layers() or trunk[0].dense.fin > lib.ppo_step_mlp_max_obs()):
             return False
         if len({s.act for s in trunk}) != 1 or any(s.ln is not None for s in trunk):
             return False

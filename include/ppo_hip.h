@@ -123,6 +123,7 @@ int ppo_sample_gaussian_f32(void* stream, const float* mean, int64_t ldm, const 
  * [K_l, 256] kernels, ldw[l] == 256; K_0 = obs_dim, K_l = 256 after); ldwh <= 16.
  * Same outputs as the trunk GEMMs, the head GEMM and the sampling launch. */
 int ppo_step_mlp_max_layers(void);
+int ppo_step_mlp_max_obs(void); /* obs_dim limit (the rows are staged in LDS) */
 int ppo_step_mlp_categorical_f32(void* stream, const float* obs, int64_t ldo, int rows, int obs_dim, int layers,
                                  const float* const* weights, const int64_t* ldw, const float* const* biases, int act,
                                  const float* head_w, int64_t ldwh, const float* head_b, int A, const uint32_t* key,

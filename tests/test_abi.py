@@ -84,6 +84,9 @@ def test_one_launch_step_rejects_unsupported_networks_without_launching():
     assert lib.ppo_step_mlp_categorical_f32(None, 1, 400, 16, 400, deep, None, None, None, 1, 1, 8, None, 6, 1, 1.0,
                                            1, 1, 1) == -1
     assert b"ppo_step_mlp_categorical_f32" in lib.ppo_last_error()
+    wide = lib.ppo_step_mlp_max_obs() + 4
+    assert lib.ppo_step_mlp_categorical_f32(None, 1, wide, 16, wide, 2, None, None, None, 1, 1, 8, None, 6, 1, 1.0,
+                                           1, 1, 1) == -1
     # head wider than 16 outputs
     assert lib.ppo_step_mlp_categorical_f32(None, 1, 400, 16, 400, 2, None, None, None, 1, 1, 20, None, 6, 1, 1.0,
                                            1, 1, 1) == -1
