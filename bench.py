@@ -619,8 +619,8 @@ def scan_main(args):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (every GPU box here has one "
-              "GPU; the multi-GPU design is described in DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the learner update runs on a "
+              "single GPU; sharding it over several is a design, not built)", file=sys.stderr)
         sys.exit(2)
     import torch
     from boonta_amd import recipes
