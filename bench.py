@@ -22,6 +22,9 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
+# the seeded synthetic rollouts (and the torch forward that fills their
+# actions) are shared with the tests and live beside them
+sys.path.insert(1, os.path.join(ROOT, "tests"))
 
 PEAK = {"fp32_mfma": 157.3, "bf16_mfma": 2516.6, "hbm": 8000.0}  # TFLOP/s, TFLOP/s, GB/s
 
@@ -63,74 +66,6 @@ def copy_probe(mib):
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
-
-
-def synthetic_rollout(recipe, params, device, seed):
-    """Seeded rollout of the workload's distributions generated on the device,
-    with actions / log-probs / values from the initial network."""
-    import torch
-    from boonta_amd import torch_ref
-    from boonta_amd.types import Timestep, Transition
-
-    T, N, D = recipe.T, recipe.N, recipe.obs_dim
-    g = torch.Generator(device=device)
-    g.manual_seed(seed)
-    shape = (T + 1, N, D)
-    if recipe.name == "discrete-anakin":
-        obs = (torch.rand(shape, device=device, generator=g) < 0.1).float()
-    elif recipe.name == "large-obs-bf16":
-        obs = torch.rand(shape, device=device, generator=g)
-        binary = torch.zeros(D, dtype=torch.bool, device=device)
-        binary[torch.randperm(D, device=device, generator=g)[: (3 * D) // 4]] = True
-        obs[..., binary] = (obs[..., binary] < 0.05).float()
-    else:
-        obs = torch.randn(shape, device=device, generator=g)
-    if recipe.name == "discrete-tiny":
-        reward = torch.ones(T, N, device=device)
-    elif recipe.name == "discrete-anakin":
-        reward = (torch.rand(T, N, device=device, generator=g) < 0.05).float()
-    elif recipe.name == "large-obs-bf16":
-        reward = (torch.rand(T, N, device=device, generator=g) < 0.02).float()
-    else:
-        reward = torch.randn(T, N, device=device, generator=g)
-    terminated = torch.rand(T, N, device=device, generator=g) < recipe.done_p
-    truncated = torch.zeros(T, N, dtype=torch.bool, device=device)
-    plan = recipe.network.plan(D)
-    tparams = _to_torch(params, device)
-    if plan["torso"] is not None:
-        # first.done[t] = second.done[t-1] (same-step auto-reset); first.done[0] drawn
-        first_term = torch.cat([torch.rand(1, N, device=device, generator=g) < recipe.done_p, terminated[:-1]])
-        first_trunc = torch.zeros_like(first_term)
-        H = plan["torso"]["features"]
-        carry0 = torch.tanh(torch.randn(N, H, device=device, generator=g))
-        action, logp, value, carry = torch_ref.recurrent_sample(tparams, plan, obs[:-1], first_term, carry0, g)
-        return Transition(
-            first=Timestep(obs=obs[:-1], terminated=first_term.contiguous(), truncated=first_trunc),
-            second=Timestep(obs=obs[1:], action=action.contiguous(), reward=reward.contiguous(),
-                            terminated=terminated, truncated=truncated),
-            aux={"log_prob": logp.contiguous(), "value": value.contiguous()}, carry=carry.contiguous())
-    acts, lps, vals = [], [], []
-    flat_obs = obs[:-1].reshape(T * N, D)
-    for s in range(0, T * N, 65536):
-        a, lp, v = torch_ref.sample(tparams, plan, flat_obs[s:s + 65536], g)
-        acts.append(a)
-        lps.append(lp)
-        vals.append(v)
-    action = torch.cat(acts).reshape((T, N) + tuple(acts[0].shape[1:])).contiguous()
-    tr = Transition(
-        first=Timestep(obs=obs[:-1]),
-        second=Timestep(obs=obs[1:], action=action, reward=reward.contiguous(), terminated=terminated,
-                        truncated=truncated),
-        aux={"log_prob": torch.cat(lps).reshape(T, N).contiguous(),
-             "value": torch.cat(vals).reshape(T, N).contiguous()})
-    return tr
-
-
-def _to_torch(tree, device):
-    import torch
-    if isinstance(tree, dict):
-        return {k: _to_torch(v, device) for k, v in tree.items()}
-    return torch.from_numpy(np.asarray(tree, np.float32)).to(device)
 
 
 def measured_traffic(workload, kernel):
@@ -423,7 +358,7 @@ def step_main(args, recipe, alg, state, params, dev):
     step, each step with its own key), captured once into a HIP graph and
     replayed with the observations resident in HBM."""
     import torch
-    from boonta_amd import synthetic
+    import synthetic
     from boonta_amd.random import key as make_key
 
     T, N, D = recipe.T, recipe.N, recipe.obs_dim
@@ -648,7 +583,7 @@ def main():
     if args.path == "step":
         step_main(args, recipe, alg, state, params, dev)
         return
-    tr = synthetic_rollout(recipe, params, dev, recipe.seed)
+    tr = synthetic.device_rollout(recipe, params, dev, recipe.seed)
     torch.cuda.synchronize()
     log("rollout ready")
     for w in range(args.warmup):

@@ -49,9 +49,10 @@ __device__ __forceinline__ Step gae_step(const GaeArgs& a, int t, int n, float n
   float rho = a.rho ? a.rho[i] : 1.f;
   float c = a.c ? a.c[i] : 1.f;
   if (a.ratio) {  // rho = min(ratio, advantage_clip), c = min(ratio, trace_clip)
+    // jnp.minimum propagates a NaN ratio (fminf would return the clip value)
     const float q = a.ratio[(int64_t)n * a.ldr + t];
-    rho = fminf(q, a.rho_clip);
-    c = fminf(q, a.c_clip);
+    rho = (q < a.rho_clip || q != q) ? q : a.rho_clip;
+    c = (q < a.c_clip || q != q) ? q : a.c_clip;
   }
   const float one_te = __fsub_rn(1.f, te);
   const float one_tr = __fsub_rn(1.f, tr);

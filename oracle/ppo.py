@@ -205,10 +205,12 @@ def optimizer_update(grads, state, params, opt):
 
 
 # ------------------------------------------------------------------- updates
-def ppo_update(params, opt_state, plan, cfg, opt, tr, key, record=None):
+def ppo_update(params, opt_state, plan, cfg, opt, tr, key, record=None, max_steps=None):
     """PPO.update (ppo.py:76-233) on a transition dict of [T, N, ...] arrays:
     obs (first.obs), next_obs_last (second.obs[-1]), action, reward,
-    terminated, truncated, log_prob, value.  Returns (params, opt_state, logs)."""
+    terminated, truncated, log_prob, value.  Returns (params, opt_state, logs).
+    ``max_steps`` stops after that many minibatch steps (bootstrap, GAE and
+    the permutations are whole)."""
     T, N = tr["reward"].shape
     B = T * N
     _, boot, _ = nets.forward(params, plan, tr["next_obs_last"])
@@ -222,21 +224,23 @@ def ppo_update(params, opt_state, plan, cfg, opt, tr, key, record=None):
     E, M = cfg["update_epochs"], cfg["num_minibatches"]
     perms = prng.epoch_permutations(key, E, B)
     logs = []
-    for e in range(E):
-        for idx in perms[e].reshape(M, -1):
-            loss, lg, grads = loss_and_grad(params, plan, cfg, obs[idx], act[idx],
-                                            olp[idx], ov[idx], fa[idx], fr[idx])
-            params, opt_state, gnorm = optimizer_update(grads, opt_state, params, opt)
-            lg["loss"] = loss
-            lg["grad_norm"] = gnorm
-            logs.append(lg)
-            if record is not None:
-                record(e, idx, grads, params)
+    steps = E * M if max_steps is None else min(max_steps, E * M)
+    for step in range(steps):
+        e, m = divmod(step, M)
+        idx = perms[e].reshape(M, -1)[m]
+        loss, lg, grads = loss_and_grad(params, plan, cfg, obs[idx], act[idx],
+                                        olp[idx], ov[idx], fa[idx], fr[idx])
+        params, opt_state, gnorm = optimizer_update(grads, opt_state, params, opt)
+        lg["loss"] = loss
+        lg["grad_norm"] = gnorm
+        logs.append(lg)
+        if record is not None:
+            record(e, idx, grads, params)
     return params, opt_state, {"advantages": adv, "returns": ret, "bootstrap": boot,
                                "permutations": perms, "logs": logs}
 
 
-def recurrent_ppo_update(params, opt_state, plan, cfg, opt, tr, key, record=None):
+def recurrent_ppo_update(params, opt_state, plan, cfg, opt, tr, key, record=None, max_steps=None):
     """RecurrentPPO.update (recurrent_ppo.py:98-281).  ``tr`` holds time-major
     [T, N, ...] obs, first_done (first.done), action, reward, terminated,
     truncated, log_prob, value, carry0 (carry[0], [N, H]), carry_last
@@ -257,17 +261,19 @@ def recurrent_ppo_update(params, opt_state, plan, cfg, opt, tr, key, record=None
     perms = prng.epoch_permutations(key, E, N)
     em = lambda a, idx: np.moveaxis(np.take(np.asarray(a), idx, axis=1), 0, 1)
     logs = []
-    for e in range(E):
-        for idx in perms[e].reshape(M, -1):
-            loss, lg, grads = recurrent_loss_and_grad(
-                params, plan, cfg, em(tr["obs"], idx), em(tr["first_done"], idx),
-                np.asarray(tr["carry0"])[idx], em(tr["action"], idx),
-                em(tr["log_prob"], idx), em(tr["value"], idx), em(adv, idx), em(ret, idx))
-            params, opt_state, gnorm = optimizer_update(grads, opt_state, params, opt)
-            lg["loss"] = loss
-            lg["grad_norm"] = gnorm
-            logs.append(lg)
-            if record is not None:
-                record(e, idx, grads, params)
+    steps = E * M if max_steps is None else min(max_steps, E * M)
+    for step in range(steps):
+        e, m = divmod(step, M)
+        idx = perms[e].reshape(M, -1)[m]
+        loss, lg, grads = recurrent_loss_and_grad(
+            params, plan, cfg, em(tr["obs"], idx), em(tr["first_done"], idx),
+            np.asarray(tr["carry0"])[idx], em(tr["action"], idx),
+            em(tr["log_prob"], idx), em(tr["value"], idx), em(adv, idx), em(ret, idx))
+        params, opt_state, gnorm = optimizer_update(grads, opt_state, params, opt)
+        lg["loss"] = loss
+        lg["grad_norm"] = gnorm
+        logs.append(lg)
+        if record is not None:
+            record(e, idx, grads, params)
     return params, opt_state, {"advantages": adv, "returns": ret, "bootstrap": boot,
                                "permutations": perms, "logs": logs}

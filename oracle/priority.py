@@ -64,3 +64,18 @@ def priority_choice(advantages, key, width: int, exponent: float, beta: float):
     idx, margin = choice(key, prob, width)
     weights = (N * prob[idx]) ** (-float(beta))
     return idx, weights, prob, margin
+
+
+def choice_f32(key, p, width: int) -> np.ndarray:
+    """jax.random.choice's inverse CDF taken the way jax types it: the
+    cumulative sum of the float32 probabilities in float32 (here sequential,
+    n in order; XLA may associate it otherwise) and r = c[-1] * (1 - u) in
+    float32, then searchsorted (side 'left').  The product path draws on a
+    float64 running sum instead; the two differ only for draws that fall
+    between a float32 and a float64 cumulative boundary."""
+    p = np.asarray(p, np.float32)
+    c = np.cumsum(p, dtype=np.float32)
+    u = sample.uniform(key, width, 0.0, 1.0).astype(np.float32)
+    r = np.float32(c[-1]) * (np.float32(1.0) - u)
+    idx = np.minimum(np.searchsorted(c, r, side="left"), len(p) - 1)
+    return idx.astype(np.int64)

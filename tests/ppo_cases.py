@@ -6,7 +6,8 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-from boonta_amd import recipes, synthetic
+import synthetic
+from boonta_amd import recipes
 from boonta_amd.algorithms.ppo import PPO
 from boonta_amd.types import Timestep, Transition
 from oracle import nets, ppo

@@ -59,6 +59,11 @@ def test_priority_choice_matches_the_oracle(T, N, width, exponent, beta):
     assert same.mean() >= 0.95
     assert np.abs(idx - i_or).max() <= 1
     np.testing.assert_allclose(w[same], w_or[same], rtol=1e-4)
+    # against jax's float32 typing of the cumsum and r (sequential order):
+    # at most 0.6 % of draws differ, each by one env
+    i_f32 = priority.choice_f32(k, prob, width)
+    assert (idx != i_f32).mean() <= 0.006
+    assert np.abs(idx - i_f32).max() <= 1
 
 def test_all_zero_advantages_draw_uniformly_and_a_device_key_matches_a_host_key():
     T, N, width = 4, 512, 2048
@@ -108,3 +113,31 @@ def test_vtrace_matches_the_oracle_and_explicit_clipped_weights(T, N, chunks):
               RHO.data_ptr(), C.data_ptr(), a2.data_ptr(), r2.data_ptr(), T, N, 0.99, 0.95, chunks)
     torch.cuda.synchronize()
     assert torch.equal(adv, a2) and torch.equal(ret, r2)
+
+
+def test_vtrace_propagates_a_nan_ratio():
+    """jnp.minimum(NaN, clip) is NaN: a diverged ratio must show up as NaN
+    advantages in its env column (at its step and every earlier one), not as
+    a silently clipped weight; the other columns stay finite and exact."""
+    T, N = 12, 70
+    g = np.random.default_rng(5)
+    r = g.normal(size=(T, N)).astype(np.float32)
+    v = g.normal(size=(T, N)).astype(np.float32)
+    b = g.normal(size=N).astype(np.float32)
+    te = np.zeros((T, N), bool)
+    tr = np.zeros((T, N), bool)
+    ratio = g.uniform(0.3, 2.0, (N, T)).astype(np.float32)
+    ratio[3, 7] = np.nan
+    ratio[65, 0] = np.nan
+    d = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    adv, ret = vtrace(d(r), d(te), d(tr), d(v), d(b), d(ratio), 0.99, 0.95, 1.0, 0.9, 0)
+    torch.cuda.synchronize()
+    rho = np.minimum(ratio.T, np.float32(1.0)).astype(np.float64)
+    c = np.minimum(ratio.T, np.float32(0.9)).astype(np.float64)
+    exp_a, exp_r = ogae.gae(r, te, tr, v, b, 0.99, 0.95, rho=rho, c=c)
+    got = adv.cpu().numpy()
+    assert np.isnan(got[:8, 3]).all() and np.isfinite(got[8:, 3]).all()
+    assert np.isnan(got[0, 65]) and np.isfinite(got[1:, 65]).all()
+    assert np.isfinite(np.delete(got, [3, 65], axis=1)).all()
+    np.testing.assert_allclose(got, exp_a, rtol=1e-5, atol=1e-5, equal_nan=True)
+    np.testing.assert_allclose(ret.cpu().numpy(), exp_r, rtol=1e-5, atol=1e-5, equal_nan=True)

@@ -19,7 +19,8 @@ import numpy as np
 import pytest
 import torch
 
-from boonta_amd import _lib, optim, recipes, synthetic
+import synthetic
+from boonta_amd import _lib, optim, recipes
 from boonta_amd.algorithms.ppo import PPO, flat_state_of
 from boonta_amd.random import key as make_key
 from boonta_amd.types import Timestep, Transition
@@ -188,6 +189,64 @@ def test_one_launch_step_matches_the_oracle_and_the_chained_launches(rows, pad, 
     np.testing.assert_allclose(v, out[False][2], rtol=1e-5, atol=1e-5)
     np.testing.assert_allclose(lp, out[False][1], rtol=1e-5, atol=1e-5)
     assert (act == out[False][0]).mean() > 0.99
+
+
+FUSED_NETS = [
+    # (trunk layers, activation, actions, observation features, row padding)
+    (1, "tanh", 2, 3, 1),        # narrowest observation, one layer
+    (3, "silu", 15, 60, 0),      # widest head (16-column kernel), obs width not a multiple of 16
+    (4, None, 15, 1023, 1),      # deepest trunk, no activation, 1023 features on 16-byte rows
+    (4, "tanh", 2, 1024, 0),     # the widest observation the LDS stage holds
+    (3, None, 2, 1024, 0),
+    (1, "silu", 15, 1023, 0),    # 1023 features on rows without 16-byte pitch
+    (2, "tanh", 7, 64, 3),
+]
+
+
+@pytest.mark.parametrize("layers,act,A,D,pad", FUSED_NETS)
+def test_one_launch_step_on_every_network_it_accepts(layers, act, A, D, pad):
+    """Every shared-trunk float32 network the one-launch step takes (1-4
+    layers of 256 features with one activation or none, at most 15 actions,
+    at most ppo_step_mlp_max_obs() observation features): the fused step
+    against the oracle's forward and categorical draw, and against the
+    layer-by-layer launches, on 300 rows (ragged against the 16-row tiles)."""
+    from boonta_amd import networks as nn
+    from boonta_amd.rollout import StepExecutor
+    rows = 300
+    trunk = []
+    for _ in range(layers):
+        trunk.append(nn.Dense(256))
+        if act is not None:
+            trunk.append({"tanh": nn.tanh, "silu": nn.silu}[act])
+    net = nn.Network(feature_extractor=nn.FeatureExtractor(nn.Sequential(trunk)),
+                     head=nn.ActorCritic(actor=nn.Categorical(nn.Dense(A)), critic=nn.Dense(1)))
+    params = net.init(layers * 100 + A, D)["params"]
+    rng = np.random.default_rng(D + A)
+    obs = rng.standard_normal((rows, D)).astype(np.float32)
+    head, value, _ = nets.forward(params, net.plan(D), obs)
+    alg = PPO(cfg=recipes.make(2).cfg, network=net, optimizer=recipes.make(2).optimizer, use_graph=False)
+    state = alg.init_from_params({"params": params}, D)
+    prog = alg.program(D)
+    o = torch.zeros(rows, D + pad, device="cuda")
+    o[:, :D] = dev(obs)
+    key = make_key(layers + 10 * A)
+    out = {}
+    for fused in (True, False):
+        ex = StepExecutor(prog, flat_state_of(state), rows, fused=fused)
+        assert ex.fused == fused
+        ex.KEY.copy_(key_dev(key))
+        a_ = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
+        lp = torch.full((rows,), float("nan"), device="cuda")
+        v = torch.full((rows,), float("nan"), device="cuda")
+        ex.issue(stream(), o.data_ptr(), D + pad, 1.0, a_.data_ptr(), lp.data_ptr(), v.data_ptr())
+        torch.cuda.synchronize()
+        out[fused] = (a_.cpu().numpy(), lp.cpu().numpy(), v.cpu().numpy())
+    a_, lp, v = out[True]
+    np.testing.assert_allclose(v, value, rtol=1e-5, atol=1e-5)
+    check_categorical(a_, lp, head, key, 1.0, 1e-4, 1e-5)
+    np.testing.assert_allclose(v, out[False][2], rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(lp, out[False][1], rtol=1e-5, atol=1e-5)
+    assert (a_ == out[False][0]).mean() > 0.99
 
 
 def test_one_launch_step_replays_from_a_graph():

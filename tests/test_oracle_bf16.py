@@ -46,9 +46,9 @@ def test_bf16_layernorm_relu_rounds_once_after_the_normalisation():
     params = {"ln": {"scale": 1.0 + 0.1 * rng.standard_normal(512), "bias": 0.1 * rng.standard_normal(512)}}
     stages = [{"op": "layernorm", "path": ("ln",), "eps": 1e-6}, {"op": "act", "fn": "relu"}]
     y, _ = nets.stages_forward(params, stages, x, "bfloat16")
-    mean = x.mean(-1, keepdims=True)
-    var = (x * x).mean(-1, keepdims=True) - mean ** 2
-    ln = (x - mean) / np.sqrt(var + 1e-6) * params["ln"]["scale"] + params["ln"]["bias"]
+    # float64 LayerNorm from torch, rounded once to bf16, then ReLU
+    ln = torch.nn.functional.layer_norm(torch.from_numpy(x), (512,), torch.from_numpy(params["ln"]["scale"]),
+                                        torch.from_numpy(params["ln"]["bias"]), eps=1e-6).numpy()
     np.testing.assert_array_equal(y, np.maximum(torch_bf16(ln), 0.0))
 
 

@@ -229,3 +229,122 @@ def test_gru_recipe_parameter_count():
     r = recipes.make(4)
     params = r.network.init(0, r.obs_dim)["params"]
     assert sum(np.size(v) for _, v in ppo.tree_leaves(params)) == 429577
+
+
+# ----------------------------------------------- pins against library routines
+def _torch_gru_cell(params, H, I):
+    """torch.nn.GRUCell in float64 holding flax GRUCell's parameters
+    (boonta/networks/blocks/rnn.py:47-54): torch's gates are
+    r = s(W_ir x + b_ir + W_hr h + b_hr), z = s(W_iz x + b_iz + W_hz h + b_hz),
+    n = tanh(W_in x + b_in + r * (W_hn h + b_hn)), h' = (1 - z) n + z h; flax's
+    recurrent r and z projections have no bias, so b_hr = b_hz = 0."""
+    import torch
+    cell = torch.nn.GRUCell(I, H).double()
+    k = lambda n: torch.from_numpy(np.asarray(params[n]["kernel"], np.float64))
+    b = lambda n: torch.from_numpy(np.asarray(params[n]["bias"], np.float64))
+    with torch.no_grad():
+        cell.weight_ih.copy_(torch.cat([k("ir"), k("iz"), k("in")], 1).T)
+        cell.bias_ih.copy_(torch.cat([b("ir"), b("iz"), b("in")]))
+        cell.weight_hh.copy_(torch.cat([k("hr"), k("hz"), k("hn")], 1).T)
+        cell.bias_hh.copy_(torch.cat([torch.zeros(2 * H, dtype=torch.float64), b("hn")]))
+    return cell
+
+
+def test_gru_forward_matches_torch_grucell_with_resets():
+    """The oracle's GRU recurrence against torch.nn.GRUCell stepped by hand
+    over 12 steps, the carry zeroed before step t wherever done[b, t]
+    (reset_carry, boonta/networks/blocks/rnn.py:11-16,42-45).  Every gate
+    bias is moved off zero so that a swapped r / z pair or b_hn outside the
+    reset gate changes the result."""
+    import torch
+    rng = np.random.default_rng(12)
+    B, T, I, H = 5, 12, 7, 6
+    net = nn.Network(torso=nn.RNN(nn.GRUCell(H)),
+                     head=nn.ActorCritic(actor=nn.Categorical(nn.Dense(2)), critic=nn.Dense(1)))
+    plan = net.plan(I)
+    params = perturb(net.init(5, I)["params"], rng)
+    torso = plan["torso"]
+    gp = nets.get(params, torso["path"])
+    for g in ("ir", "iz", "in", "hn"):
+        gp[g]["bias"] = gp[g]["bias"] + rng.normal(0, 0.5, H)
+    x = rng.standard_normal((B, T, I))
+    done = rng.random((B, T)) < 0.2
+    done[0, 4] = True
+    carry = np.tanh(rng.standard_normal((B, H)))
+    out, final, _ = nets.gru_forward(params, torso, x, done, carry)
+    cell = _torch_gru_cell(gp, H, I)
+    h = torch.from_numpy(carry)
+    want = np.zeros((B, T, H))
+    with torch.no_grad():
+        for t in range(T):
+            h = torch.where(torch.from_numpy(done[:, t:t + 1]), torch.zeros_like(h), h)
+            h = cell(torch.from_numpy(x[:, t]), h)
+            want[:, t] = h.numpy()
+    np.testing.assert_allclose(out, want, rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(final, want[:, -1], rtol=1e-12, atol=1e-13)
+
+
+@pytest.mark.parametrize("scale", [1.0, 1e-3])
+def test_layernorm_forward_matches_torch_layer_norm(scale):
+    """flax LayerNorm (epsilon 1e-6, scale and bias) against
+    torch.nn.functional.layer_norm in float64.  At scale 1e-3 the row
+    variance is about 1e-6, the size of epsilon, so a wrong epsilon, or
+    epsilon applied outside the square root, is far outside the tolerance."""
+    import torch
+    rng = np.random.default_rng(13)
+    F = 48
+    x = scale * (rng.standard_normal((9, F)) + rng.normal(0, 3, (9, 1)))
+    p = {"ln": {"scale": 1.0 + 0.2 * rng.standard_normal(F), "bias": 0.3 * rng.standard_normal(F)}}
+    y, _ = nets.stages_forward(p, [{"op": "layernorm", "path": ("ln",), "eps": 1e-6}], x)
+    want = torch.nn.functional.layer_norm(torch.from_numpy(x), (F,), torch.from_numpy(p["ln"]["scale"]),
+                                          torch.from_numpy(p["ln"]["bias"]), eps=1e-6).numpy()
+    np.testing.assert_allclose(y, want, rtol=1e-9, atol=1e-9)
+
+
+def test_adam_constant_gradient_moves_every_weight_by_lr_at_every_step():
+    """With a constant gradient g the bias-corrected moments are exactly g and
+    g^2 at every count t (mu_t = (1 - b1^t) g, nu_t = (1 - b2^t) g^2), so each
+    step moves each weight by lr * |g| / (|g| + eps).  A bias correction taken
+    at count - 1, or the decays swapped, breaks this from step 2 on."""
+    rng = np.random.default_rng(14)
+    p0 = {"w": rng.normal(size=40), "b": {"c": rng.normal(size=3)}}
+    g = {"w": rng.normal(size=40) * 10.0 ** rng.integers(-3, 3, 40), "b": {"c": np.array([1e-2, -3.0, 0.5])}}
+    opt = {"lr": 1e-3, "max_grad_norm": None}
+    st = ppo.optimizer_init(p0)
+    p = p0
+    for t in range(1, 6):
+        new, st, _ = ppo.optimizer_update(g, st, p, opt)
+        assert st["count"] == t
+        for path, gl in ppo.tree_leaves(g):
+            step = nets.get(new, path[:-1])[path[-1]] - nets.get(p, path[:-1])[path[-1]]
+            np.testing.assert_allclose(step, -1e-3 * gl / (np.abs(gl) + 1e-8), rtol=1e-9, atol=1e-18)
+        p = new
+
+
+def test_adam_two_steps_hand_computed():
+    """Two Adam steps (b1 0.9, b2 0.999, eps 1e-8, lr 0.1) on one weight with
+    gradients 1 then -2, worked by hand in exact rationals:
+      step 1: mu = 0.1, nu = 0.001, m^ = 1, v^ = 1 -> p1 = p0 - 0.1 / (1 + 1e-8)
+      step 2: mu = 0.9 * 0.1 - 0.2 = -0.11, nu = 0.999 * 0.001 + 0.001 * 4 = 0.004999,
+              m^ = -0.11 / 0.19 = -11/19, v^ = 0.004999 / 0.001999 = 4999/1999,
+              p2 = p1 + 0.1 * (11/19) / (sqrt(4999/1999) + 1e-8)
+    and with the global-norm clip at 0.5 the same gradients enter as 0.5 and -0.5:
+      step 2: mu = 0.045 - 0.05 = -0.005, nu = 0.999 * 0.00025 + 0.00025 = 0.00049975,
+              m^ = -0.005 / 0.19 = -1/38, v^ = 0.00049975 / 0.001999 = 0.25
+              (exactly 1999/7996), p2 = p1 + 0.1 * (1/38) / (0.5 + 1e-8)."""
+    p0 = {"w": np.array([0.3])}
+    opt = {"lr": 0.1, "max_grad_norm": None}
+    p1, st, _ = ppo.optimizer_update({"w": np.array([1.0])}, ppo.optimizer_init(p0), p0, opt)
+    np.testing.assert_allclose(p1["w"], 0.3 - 0.1 / (1 + 1e-8), rtol=1e-14)
+    p2, st, _ = ppo.optimizer_update({"w": np.array([-2.0])}, st, p1, opt)
+    np.testing.assert_allclose(st["mu"]["w"], -0.11, rtol=1e-13)
+    np.testing.assert_allclose(st["nu"]["w"], 0.004999, rtol=1e-13)
+    np.testing.assert_allclose(p2["w"], p1["w"] + 0.1 * (11 / 19) / (np.sqrt(4999 / 1999) + 1e-8), rtol=1e-14)
+    # the same two gradients through clip_by_global_norm(0.5)
+    opt = {"lr": 0.1, "max_grad_norm": 0.5}
+    q1, st, n1 = ppo.optimizer_update({"w": np.array([1.0])}, ppo.optimizer_init(p0), p0, opt)
+    q2, st, n2 = ppo.optimizer_update({"w": np.array([-2.0])}, st, q1, opt)
+    assert (n1, n2) == (1.0, 2.0)
+    np.testing.assert_allclose(st["mu"]["w"], -0.005, rtol=1e-13)
+    np.testing.assert_allclose(st["nu"]["w"], 0.00049975, rtol=1e-13)
+    np.testing.assert_allclose(q2["w"], q1["w"] + 0.1 * (1 / 38) / (0.5 + 1e-8), rtol=1e-14)
