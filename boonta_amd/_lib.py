@@ -38,6 +38,7 @@ SIGNATURES = {
     "ppo_permutation": (I, [P, P, P, I64, P, SZ]),
     "ppo_epoch_permutations_workspace": (SZ, [I, I64]),
     "ppo_epoch_permutations": (I, [P, P, I, I64, P, P, SZ]),
+    "ppo_epoch_permutations_noalloc": (I, [P, P, I, I64, P]),
     "ppo_sample_max_outputs": (I, []),
     "ppo_sample_categorical_f32": (I, [P, P, I64, I, I, P, I64, P, F, P, P, P]),
     "ppo_sample_gaussian_f32": (I, [P, P, I64, P, I64, I, I, P, I64, P, F, P, I64, P, P]),

@@ -26,6 +26,7 @@
 
 #include <algorithm>
 #include <math.h>
+#include <mutex>
 #include <utility>
 
 namespace {
@@ -337,6 +338,40 @@ int shuffle_impl(hipStream_t st, const uint32_t* key, int split_epochs, int epoc
 
 }  // namespace
 
+// Scratch of ppo_epoch_permutations_noalloc: the bucket sort's keys,
+// positions, values, histograms and bucket starts (every byte is rewritten by
+// each call before it is read, so nothing is cleared).  Each GPU the library
+// runs on holds its own copy until the process ends.  Host code never passes
+// the symbol itself to a kernel: the device address is resolved per device
+// with hipGetSymbolAddress and kept in `g_scratch`.
+static constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(24) << 20;  // 4 epochs x 262144 items need 16.5 MB
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+static constexpr int MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch[MAX_DEVICES] = {};
+
+// Device address of `scratch` on the current device (resolved on the first
+// call per device, with that device current).
+static int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
+    return ppo::set_error(PPO_ERR_LAUNCH, "ppo_epoch_permutations_noalloc: no current device (%s)",
+                          hipGetErrorString(e));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return ppo::set_error(PPO_ERR_LAUNCH, "ppo_epoch_permutations_noalloc: scratch address on device %d: %s", dev,
+                            hipGetErrorString(e));
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return PPO_OK;
+}
+
 PPO_EXPORT size_t ppo_permutation_workspace(int64_t n) { return space_bytes(1, n); }
 
 PPO_EXPORT int ppo_threefry_split(void* stream, const uint32_t* key, uint32_t* out, int64_t num) {
@@ -367,4 +402,27 @@ PPO_EXPORT int ppo_epoch_permutations(void* stream, const uint32_t* key, int epo
   if (workspace_bytes < space_bytes(epochs, n) || !workspace)
     return ppo::set_error(PPO_ERR_SPACE, "ppo_epoch_permutations: workspace too small");
   return shuffle_impl(ppo::as_stream(stream), key, 1, epochs, n, out, workspace);
+}
+
+// ppo_epoch_permutations with its workspace in the library's own device
+// scratch: no allocation, for callers that cannot allocate.  Rejects sizes
+// whose workspace exceeds the scratch.  Calls that overlap on one GPU share
+// the scratch and race.
+PPO_EXPORT int ppo_epoch_permutations_noalloc(void* stream, const uint32_t* key, int epochs, int64_t n,
+                                              int32_t* out) {
+  if (epochs < 0 || epochs > 65535 || n < 0 || n > INT32_MAX || !key || (epochs > 0 && n > 0 && !out))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_epoch_permutations_noalloc: bad argument");
+  if (space_bytes(epochs, n) > NOALLOC_SCRATCH_BYTES)
+    return ppo::set_error(PPO_ERR_SPACE, "ppo_epoch_permutations_noalloc: %d epochs of %lld items need %zu bytes "
+                          "of scratch, more than its %zu", epochs, (long long)n, space_bytes(epochs, n),
+                          NOALLOC_SCRATCH_BYTES);
+  hipStream_t st = ppo::as_stream(stream);
+  int cur = -1, sdev = -1;
+  if (hipGetDevice(&cur) != hipSuccess || hipStreamGetDevice(st, &sdev) != hipSuccess || cur != sdev)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_epoch_permutations_noalloc: the stream's device (%d) is not the "
+                          "current device (%d)", sdev, cur);
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != PPO_OK) return rc;
+  return shuffle_impl(st, key, 1, epochs, n, out, ws);
 }
