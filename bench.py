@@ -43,7 +43,11 @@ def parse():
     ap.add_argument("--scan-dtype", choices=("f32", "bf16"), default="f32")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--launch-reps", type=int, default=20)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget of the headline workload")
+    ap.add_argument("--cpu-seconds-also", type=float, default=8.0, help="CPU baseline budget of each --also workload")
+    ap.add_argument("--also", default="auto",
+                    help="other workloads measured in the same run, into the line's 'configs' list: "
+                         "'auto' (3,4,5 beside the default headline 2), 'none', or a comma list")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--profile-only", action="store_true", help="warmup + timed updates only")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -215,12 +219,19 @@ def time_launches(ex, reps, per_update_steps):
 
 
 def cpu_baseline(recipe, params, tr_dev, budget_s):
-    """The oracle (float64 numpy) on the host: minibatch steps of the same
-    workload until the time budget, extrapolated to one update."""
-    import torch
+    """The oracle's update restatement in float32 numpy on the host
+    (oracle.working_precision): the bootstrap forward, GAE over the whole
+    rollout and the epoch permutations, then minibatch steps (gather of the
+    minibatch rows from the host copy of the rollout, forward, backward,
+    clip, Adam) until the time budget, extrapolated to E * M steps."""
+    import oracle
+    from boonta_amd.random import key as make_key
     from oracle import gae as ogae
+    from oracle import nets as onets
     from oracle import ppo as oppo
+    from oracle import prng as oprng
 
+    f32 = np.float32
     plan = recipe.network.plan(recipe.obs_dim)
     T, N = recipe.T, recipe.N
     B, mb, E, M = recipe.batch, recipe.minibatch, recipe.cfg.update_epochs, recipe.cfg.num_minibatches
@@ -228,66 +239,60 @@ def cpu_baseline(recipe, params, tr_dev, budget_s):
            "entropy_coefficient": recipe.cfg.entropy_coefficient, "value_coefficient": recipe.cfg.value_coefficient}
     a = recipe.optimizer.adam
     opt = {"lr": a.learning_rate, "max_grad_norm": recipe.optimizer.max_grad_norm}
-    rng = np.random.default_rng(0)
-    s = tr_dev.second
-    reward = s.reward.cpu().numpy()
-    term, trunc = s.terminated.cpu().numpy(), s.truncated.cpu().numpy()
-    value = tr_dev.aux["value"].cpu().numpy()
-    t0 = time.perf_counter()
-    adv, ret = ogae.gae(reward, term, trunc, value, value[-1], recipe.cfg.gamma, recipe.cfg.gae_lambda)
-    t_gae = time.perf_counter() - t0
-    p = oppo.tree_map(lambda x: np.asarray(x, np.float64), params)
-    st = oppo.optimizer_init(p)
-    steps, spent = 0, 0.0
+    # the rollout resident in host memory (copied before the clock starts)
+    f, s = tr_dev.first, tr_dev.second
+    host = lambda t: t.detach().cpu().numpy()
+    obs, act, reward = host(f.obs), host(s.action), host(s.reward)
+    term, trunc = host(s.terminated), host(s.truncated)
+    logp, value, next_last = host(tr_dev.aux["log_prob"]), host(tr_dev.aux["value"]), host(s.obs[-1])
     if recipe.recurrent:
-        # sequence minibatches of N / M whole envs x T steps (recurrent_ppo.py:214-223)
-        f = tr_dev.first
-        em = lambda a, envs: np.moveaxis(a[:, envs], 0, 1)
-        obs_h = f.obs.cpu().numpy()
-        done_h = (f.terminated | f.truncated).cpu().numpy()
-        act_h = s.action.cpu().numpy()
-        lp_h, v_h = tr_dev.aux["log_prob"].cpu().numpy(), value
-        carry0 = tr_dev.carry[0].cpu().numpy()
-        nb = N // M
-        while spent < budget_s and steps < 64:
-            envs = np.sort(rng.permutation(N)[:nb])
-            args = (em(obs_h, envs), em(done_h, envs), carry0[envs], em(act_h, envs), em(lp_h, envs),
-                    em(v_h, envs), em(adv, envs), em(ret, envs))
+        first_done = host(f.terminated) | host(f.truncated)
+        carry0, carry_last = host(tr_dev.carry[0]), host(tr_dev.carry[-1])
+    key = make_key(recipe.seed)
+    with oracle.working_precision(f32):
+        p = oppo.tree_map(lambda x: np.asarray(x, f32), params)
+        st = oppo.optimizer_init(p)
+        t0 = time.perf_counter()
+        if recipe.recurrent:
+            seq_obs = np.stack([obs[-1], next_last], axis=1)
+            seq_done = np.stack([first_done[-1], term[-1] | trunc[-1]], axis=1)
+            boot = onets.recurrent_forward(p, plan, seq_obs, seq_done, carry_last)[1][:, -1]
+        else:
+            boot = onets.forward(p, plan, next_last)[1]
+        adv, ret = ogae.gae(reward, term, trunc, value, boot, recipe.cfg.gamma, recipe.cfg.gae_lambda,
+                            dtype=f32)
+        perms = oprng.epoch_permutations(key, E, N if recipe.recurrent else B)
+        t_pre = time.perf_counter() - t0
+        steps, spent = 0, 0.0
+        while spent < budget_s and steps < E * M:
+            e, m = divmod(steps, M)
             t0 = time.perf_counter()
-            _, _, grads = oppo.recurrent_loss_and_grad(p, plan, cfg, *args)
+            if recipe.recurrent:
+                # env-major sequence minibatches of N / M whole envs (recurrent_ppo.py:214-223)
+                envs = perms[e].reshape(M, -1)[m]
+                em = lambda x: np.moveaxis(np.take(x, envs, axis=1), 0, 1)
+                _, _, grads = oppo.recurrent_loss_and_grad(p, plan, cfg, em(obs), em(first_done), carry0[envs],
+                                                           em(act), em(logp), em(value), em(adv), em(ret))
+            else:
+                idx = perms[e].reshape(M, -1)[m]
+                flat = lambda x: x.reshape((B,) + x.shape[2:])[idx]
+                _, _, grads = oppo.loss_and_grad(p, plan, cfg, flat(obs), flat(act), flat(logp), flat(value),
+                                                 flat(adv), flat(ret))
             p, st, _ = oppo.optimizer_update(grads, st, p, opt)
             spent += time.perf_counter() - t0
             steps += 1
-        mb = f"{nb} envs x {T} steps"
-    else:
-        obs_flat = tr_dev.first.obs.reshape(B, -1)
-        act_flat = s.action.reshape((B,) + tuple(s.action.shape[2:]))
-        lp_flat = tr_dev.aux["log_prob"].reshape(B)
-        v_flat = tr_dev.aux["value"].reshape(B)
-        advf, retf = adv.reshape(B), ret.reshape(B)
-        while spent < budget_s and steps < 64:
-            idx = np.sort(rng.permutation(B)[:mb])
-            it = torch.from_numpy(idx).to(obs_flat.device)
-            x = obs_flat[it].cpu().numpy()
-            act = act_flat[it].cpu().numpy()
-            olp, ov = lp_flat[it].cpu().numpy(), v_flat[it].cpu().numpy()
-            t0 = time.perf_counter()
-            _, _, grads = oppo.loss_and_grad(p, plan, cfg, x, act, olp, ov, advf[idx], retf[idx])
-            p, st, _ = oppo.optimizer_update(grads, st, p, opt)
-            spent += time.perf_counter() - t0
-            steps += 1
-        mb = f"{mb} rows"
-    t_step = spent / steps
-    t_update = E * M * t_step + t_gae
+    t_update = t_pre + E * M * spent / steps
+    unit = f"{N // M} envs x {T} steps" if recipe.recurrent else f"{mb} rows"
     try:
         cores = len(os.sched_getaffinity(0))
     except AttributeError:
         cores = os.cpu_count()
     threads = int(os.environ.get("OMP_NUM_THREADS", cores))
     return {"value": B / t_update, "unit": "samples/s", "cores": min(cores, threads), "kind": "port",
-            "sample": f"oracle float64 numpy: GAE over the full [{T},{N}] rollout plus {steps} minibatch "
-                      f"steps of {mb} (forward, backward, clip, Adam; {spent:.1f} s), extrapolated to "
-                      f"{E}x{M} steps per update"}
+            "sample": f"oracle restatement in float32 numpy: bootstrap forward, GAE over the full [{T},{N}] "
+                      f"rollout and the {E} epoch permutations ({t_pre:.2f} s), plus {steps} of the {E * M} "
+                      f"minibatch steps of {unit} (gather, forward, backward, clip, Adam; {spent:.1f} s), "
+                      f"extrapolated to one update"}
 
 
 def roofline_of(dom, total, workload):
@@ -561,7 +566,6 @@ def main():
     from boonta_amd import recipes
     from boonta_amd.algorithms.ppo import PPO
     from boonta_amd.algorithms.recurrent_ppo import RecurrentPPO
-    from boonta_amd.random import key as make_key
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
@@ -572,17 +576,56 @@ def main():
     if args.path == "scan":
         scan_main(args)
         return
-    recipe = recipes.make(args.config)
     dev = torch.device("cuda:0")
+    if args.path == "step":
+        recipe = recipes.make(args.config)
+        params = recipe.network.init(recipe.seed, recipe.obs_dim)["params"]
+        cls = RecurrentPPO if recipe.recurrent else PPO
+        alg = cls(cfg=recipe.cfg, network=recipe.network, optimizer=recipe.optimizer,
+                  use_graph=not args.no_graph)
+        state = alg.init_from_params({"params": params}, recipe.obs_dim)
+        step_main(args, recipe, alg, state, params, dev)
+        return
+    out = {"metric": "PPO learner samples/sec on 1 MI355X + % of HBM/MFMA roofline per kernel",
+           **measure_update(args, args.config, dev, headline=True)}
+    extra = also_configs(args)
+    if extra:
+        out["configs"] = []
+        for c in extra:
+            out["configs"].append(measure_update(args, c, dev, headline=False))
+    print(json.dumps(out), flush=True)
+
+
+def also_configs(args) -> list:
+    """The other workloads measured in the same run (their lines go into
+    ``configs``): by default the Gaussian, GRU and bf16 workloads beside the
+    discrete Anakin headline, none for another headline or --profile-only."""
+    if args.profile_only or args.also == "none":
+        return []
+    if args.also == "auto":
+        return [3, 4, 5] if args.config == 2 else []
+    return [int(c) for c in args.also.split(",") if c and int(c) != args.config]
+
+
+def measure_update(args, config: int, dev, headline: bool) -> dict:
+    """One workload: seeded rollout resident in HBM, W untimed updates, K timed
+    updates replayed from the HIP graph; then (unless --profile-only) each
+    launch of one update timed alone for the per-kernel rooflines, and the
+    CPU baseline."""
+    import synthetic
+    import torch
+    from boonta_amd import recipes
+    from boonta_amd.algorithms.ppo import PPO
+    from boonta_amd.algorithms.recurrent_ppo import RecurrentPPO
+    from boonta_amd.random import key as make_key
+
+    recipe = recipes.make(config)
     log(f"workload {recipe.name}: T={recipe.T} N={recipe.N} obs={recipe.obs_dim} "
         f"{recipe.cfg.update_epochs}x{recipe.cfg.num_minibatches} minibatches of {recipe.minibatch}")
     params = recipe.network.init(recipe.seed, recipe.obs_dim)["params"]
     cls = RecurrentPPO if recipe.recurrent else PPO
     alg = cls(cfg=recipe.cfg, network=recipe.network, optimizer=recipe.optimizer, use_graph=not args.no_graph)
     state = alg.init_from_params({"params": params}, recipe.obs_dim)
-    if args.path == "step":
-        step_main(args, recipe, alg, state, params, dev)
-        return
     tr = synthetic.device_rollout(recipe, params, dev, recipe.seed)
     torch.cuda.synchronize()
     log("rollout ready")
@@ -597,18 +640,16 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     log(f"timed {args.steps} updates in {elapsed:.3f} s")
-    ms = 1000.0 * elapsed / args.steps
-    value = recipe.batch * args.steps / elapsed
     logs = alg.logs(state, recipe.T, recipe.N, recipe.obs_dim)
     if not all(np.isfinite(v).all() for v in logs.values()):
         raise RuntimeError("non-finite learner logs")
     out = {
-        "metric": "PPO learner samples/sec on 1 MI355X + % of HBM/MFMA roofline per kernel",
-        "value": value, "unit": "samples/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "value": recipe.batch * args.steps / elapsed, "unit": "samples/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": 1000.0 * elapsed / args.steps, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16" if recipe.network.plan(recipe.obs_dim)["compute_dtype"] == "bfloat16" else "f32",
         "data": "synthetic (seeded rollout of the workload's distributions, random-init network)",
-        "config": {"workload": f"config {args.config}: {recipe.name}", "T": recipe.T, "N": recipe.N,
+        "config": {"workload": f"config {config}: {recipe.name}", "T": recipe.T, "N": recipe.N,
                    "obs": recipe.obs_dim, "epochs": recipe.cfg.update_epochs,
                    "minibatches": recipe.cfg.num_minibatches, "minibatch": recipe.minibatch,
                    "global_batch": recipe.batch, "graph": not args.no_graph},
@@ -623,8 +664,12 @@ def main():
         out["launch_sum_ms"] = total
         if not args.skip_cpu:
             log("cpu baseline ...")
-            out["cpu_baseline"] = cpu_baseline(recipe, params, tr, args.cpu_seconds)
-    print(json.dumps(out), flush=True)
+            budget = args.cpu_seconds if headline else args.cpu_seconds_also
+            out["cpu_baseline"] = cpu_baseline(recipe, params, tr, budget)
+    del tr, alg, state
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
 
 
 if __name__ == "__main__":

@@ -30,7 +30,9 @@ import math
 
 import numpy as np
 
-F64 = np.float64
+# working precision: float64 for every check; bench.py's CPU baseline times
+# the same code in float32 (oracle.working_precision)
+FT = np.float64
 
 
 def get(params, path):
@@ -83,11 +85,11 @@ def act_bwd(fn, x, y, dy):
 # ----------------------------------------------------------------- bf16 casts
 def bf16(x):
     """Round to the nearest-even bfloat16 value, via float32 (XLA rounds its
-    fp32 results to bf16), returned as float64."""
-    a = np.ascontiguousarray(np.asarray(x, F64).astype(np.float32))
+    fp32 results to bf16), returned in the working precision."""
+    a = np.ascontiguousarray(np.asarray(x, FT).astype(np.float32))
     u = a.view(np.uint32).astype(np.uint64)
     u = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
-    return (u & 0xFFFFFFFF).astype(np.uint32).view(np.float32).astype(F64)
+    return (u & 0xFFFFFFFF).astype(np.uint32).view(np.float32).astype(FT)
 
 
 def _cast(x, dtype):
@@ -109,10 +111,10 @@ def stages_forward(params, stages, x, dtype="float32"):
         if op == "dense":
             p = get(params, st["path"])
             x = _cast(x, dtype)
-            w = _cast(np.asarray(p["kernel"], F64), dtype)
+            w = _cast(np.asarray(p["kernel"], FT), dtype)
             y = _cast(x @ w, dtype)
             if st.get("bias", True):
-                y = _cast(y + _cast(np.asarray(p["bias"], F64), dtype), dtype)
+                y = _cast(y + _cast(np.asarray(p["bias"], FT), dtype), dtype)
             caches.append(x)
             x = y
         elif op == "layernorm":
@@ -122,7 +124,7 @@ def stages_forward(params, stages, x, dtype="float32"):
             rstd = 1.0 / np.sqrt(var + st.get("eps", 1e-6))
             xhat = (x - mean) * rstd
             caches.append((xhat, rstd))
-            x = _cast(xhat * np.asarray(p["scale"], F64) + np.asarray(p["bias"], F64), dtype)
+            x = _cast(xhat * np.asarray(p["scale"], FT) + np.asarray(p["bias"], FT), dtype)
         elif op == "act":
             y = act_fwd(st["fn"], x)
             if st["fn"] != "relu":
@@ -154,13 +156,13 @@ def stages_backward(params, stages, caches, dy, grads, need_dx=True, dtype="floa
                 add_in(grads, tuple(st["path"]) + ("bias",), _cast(dy.sum(0), dtype))
             if i == 0 and not need_dx:
                 return None
-            dy = _cast(dy @ _cast(np.asarray(p["kernel"], F64), dtype).T, dtype)
+            dy = _cast(dy @ _cast(np.asarray(p["kernel"], FT), dtype).T, dtype)
         elif op == "layernorm":
             p = get(params, st["path"])
             xhat, rstd = cache
             add_in(grads, tuple(st["path"]) + ("scale",), (dy * xhat).sum(0))
             add_in(grads, tuple(st["path"]) + ("bias",), dy.sum(0))
-            g = dy * np.asarray(p["scale"], F64)
+            g = dy * np.asarray(p["scale"], FT)
             dy = _cast(rstd * (g - g.mean(-1, keepdims=True)
                                - xhat * (g * xhat).mean(-1, keepdims=True)), dtype)
         elif op == "act":
@@ -182,15 +184,15 @@ def gru_forward(params, torso, x, done, carry):
     Before step t the carry is reset to zeros where done[:, t]
     (boonta/networks/blocks/rnn.py:42-45)."""
     p = get(params, torso["path"])
-    k = lambda n: np.asarray(p[n]["kernel"], F64)
-    b = lambda n: np.asarray(p[n]["bias"], F64)
+    k = lambda n: np.asarray(p[n]["kernel"], FT)
+    b = lambda n: np.asarray(p[n]["bias"], FT)
     B, T, _ = x.shape
     H = torso["features"]
     xr = x @ k("ir") + b("ir")
     xz = x @ k("iz") + b("iz")
     xn = x @ k("in") + b("in")
-    h = np.asarray(carry, F64)
-    out = np.zeros((B, T, H))
+    h = np.asarray(carry, FT)
+    out = np.zeros((B, T, H), FT)
     cache = []
     for t in range(T):
         hp = np.where(done[:, t:t + 1], 0.0, h)
@@ -209,18 +211,18 @@ def gru_backward(params, torso, cache, dout, grads):
     gradient (it is data in RecurrentPPO.update)."""
     path = tuple(torso["path"])
     p = get(params, path)
-    k = lambda n: np.asarray(p[n]["kernel"], F64)
+    k = lambda n: np.asarray(p[n]["kernel"], FT)
     x, done, steps = cache
     B, T, _ = x.shape
     H = torso["features"]
-    dh = np.zeros((B, H))
-    dxr = np.zeros((B, T, H))
-    dxz = np.zeros((B, T, H))
-    dxn = np.zeros((B, T, H))
-    dWhr = np.zeros((H, H))
-    dWhz = np.zeros((H, H))
-    dWhn = np.zeros((H, H))
-    dbhn = np.zeros(H)
+    dh = np.zeros((B, H), FT)
+    dxr = np.zeros((B, T, H), FT)
+    dxz = np.zeros((B, T, H), FT)
+    dxn = np.zeros((B, T, H), FT)
+    dWhr = np.zeros((H, H), FT)
+    dWhz = np.zeros((H, H), FT)
+    dWhn = np.zeros((H, H), FT)
+    dbhn = np.zeros(H, FT)
     for t in range(T - 1, -1, -1):
         hp, r, z, hn, n = steps[t]
         dh = dh + dout[:, t]
@@ -305,7 +307,7 @@ def forward(params, plan, obs):
     head being logits [rows, A] or mean [rows, D] (the heads' outputs are cast
     to fp32 before the distribution: distributions.py:35, actor_critic.py:14)."""
     dt = plan.get("compute_dtype", "float32")
-    x = np.asarray(obs, F64)
+    x = np.asarray(obs, FT)
     h, c_trunk = stages_forward(params, plan["trunk"], x, dt)
     head, c_actor = stages_forward(params, plan["actor"], h, dt)
     val, c_critic = stages_forward(params, plan["critic"], h, dt)
@@ -327,7 +329,7 @@ def recurrent_forward(params, plan, obs, done, carry):
     """Recurrent network on obs [B, T, obs_dim], done [B, T]; returns
     (head [B, T, ...], value [B, T], final carry, cache)."""
     B, T, D = obs.shape
-    x = np.asarray(obs, F64).reshape(B * T, D)
+    x = np.asarray(obs, FT).reshape(B * T, D)
     e, c_trunk = stages_forward(params, plan["trunk"], x)
     seq, final, c_gru = gru_forward(params, plan["torso"], e.reshape(B, T, -1), done, carry)
     h = seq.reshape(B * T, -1)

@@ -19,13 +19,15 @@ Restates, for the MLP and GRU actor-critics of the learner:
 """
 from __future__ import annotations
 
+import math
+
 import numpy as np
 
 from . import gae as _gae
 from . import nets
 from . import prng
 
-F64 = np.float64
+FT = np.float64  # working precision (see nets.FT)
 
 
 # ---------------------------------------------------------------- jax tie rule
@@ -33,16 +35,16 @@ def _d_min(x, y):
     """(d min(x,y)/dx, d min(x,y)/dy) with jax's balanced tie rule."""
     ans = np.minimum(x, y)
     ex, ey = (x == ans), (y == ans)
-    dx = ex / np.where(ey, 2.0, 1.0)
-    dy = ey / np.where(ex, 2.0, 1.0)
+    dx = ex / np.where(ey, FT(2), FT(1))
+    dy = ey / np.where(ex, FT(2), FT(1))
     return dx, dy
 
 
 def _d_max(x, y):
     ans = np.maximum(x, y)
     ex, ey = (x == ans), (y == ans)
-    dx = ex / np.where(ey, 2.0, 1.0)
-    dy = ey / np.where(ex, 2.0, 1.0)
+    dx = ex / np.where(ey, FT(2), FT(1))
+    dy = ey / np.where(ex, FT(2), FT(1))
     return dx, dy
 
 
@@ -62,7 +64,7 @@ def loss_terms(logp, ent, value, old_logp, old_value, adv, ret, cfg):
     eps = cfg["clip_coefficient"]
     ratio = np.exp(logp - old_logp)
     kl = np.mean(old_logp - logp)
-    clipfrac = np.mean((np.abs(ratio - 1.0) > eps).astype(F64))
+    clipfrac = np.mean((np.abs(ratio - 1.0) > eps).astype(FT))
     cr, dcr = _clip_and_grad(ratio, 1.0 - eps, 1.0 + eps)
     pg1, pg2 = ratio * adv, cr * adv
     actor = -np.minimum(pg1, pg2).mean()
@@ -85,7 +87,7 @@ def loss_terms(logp, ent, value, old_logp, old_value, adv, ret, cfg):
     entropy = ent.mean()
     loss = actor - cfg["entropy_coefficient"] * entropy + cfg["value_coefficient"] * critic
     g_value = cfg["value_coefficient"] * g_v_rows / n
-    g_ent = np.full(n, -cfg["entropy_coefficient"] / n)
+    g_ent = np.full(n, -cfg["entropy_coefficient"] / n, FT)
     resid = ret - value
     logs = {
         "actor/loss": actor,
@@ -107,12 +109,12 @@ def _head_stats(params, plan, head, action):
         return lp, ent, cache
     if d["kind"] == "gaussian":
         if d.get("scale") is not None:
-            raw = np.broadcast_to(np.asarray(nets.get(params, d["scale"]), F64), head.shape)
+            raw = np.broadcast_to(np.asarray(nets.get(params, d["scale"]), FT), head.shape)
             mean = head
         else:
             mean, raw = np.split(head, 2, axis=-1)
         sigma = nets.gaussian_sigma(raw)
-        lp, ent = nets.gaussian_stats(mean, sigma, np.asarray(action, F64))
+        lp, ent = nets.gaussian_stats(mean, sigma, np.asarray(action, FT))
         return lp, ent, (mean, raw, sigma)
     raise ValueError(d["kind"])
 
@@ -122,7 +124,7 @@ def _head_grad(plan, cache, action, g_lp, g_ent, grads):
     if d["kind"] == "categorical":
         return nets.categorical_grad(cache, action, g_lp, g_ent)
     mean, raw, sigma = cache
-    dmean, dsig = nets.gaussian_grad(mean, sigma, np.asarray(action, F64), g_lp, g_ent)
+    dmean, dsig = nets.gaussian_grad(mean, sigma, np.asarray(action, FT), g_lp, g_ent)
     draw = dsig / (1.0 + np.exp(-raw))       # softplus' = sigmoid
     if d.get("scale") is not None:
         nets.add_in(grads, tuple(d["scale"]), draw.sum(0))
@@ -133,7 +135,7 @@ def _head_grad(plan, cache, action, g_lp, g_ent, grads):
 def zeros_like_tree(t):
     if isinstance(t, dict):
         return {k: zeros_like_tree(v) for k, v in t.items()}
-    return np.zeros(np.shape(t), F64)
+    return np.zeros(np.shape(t), FT)
 
 
 def loss_and_grad(params, plan, cfg, obs, action, old_logp, old_value, adv, ret):
@@ -141,8 +143,8 @@ def loss_and_grad(params, plan, cfg, obs, action, old_logp, old_value, adv, ret)
     head, value, cache = nets.forward(params, plan, obs)
     lp, ent, hcache = _head_stats(params, plan, head, action)
     loss, logs, (g_lp, g_ent, g_v) = loss_terms(
-        lp, ent, value, np.asarray(old_logp, F64), np.asarray(old_value, F64),
-        np.asarray(adv, F64), np.asarray(ret, F64), cfg)
+        lp, ent, value, np.asarray(old_logp, FT), np.asarray(old_value, FT),
+        np.asarray(adv, FT), np.asarray(ret, FT), cfg)
     grads = zeros_like_tree(params)
     dhead = _head_grad(plan, hcache, action, g_lp, g_ent, grads)
     nets.backward(params, plan, cache, dhead, g_v, grads)
@@ -158,9 +160,9 @@ def recurrent_loss_and_grad(params, plan, cfg, obs, done, carry, action, old_log
     act = np.asarray(action).reshape((B * T,) + np.shape(action)[2:])
     lp, ent, hcache = _head_stats(params, plan, hf, act)
     loss, logs, (g_lp, g_ent, g_v) = loss_terms(
-        lp, ent, value.reshape(-1), np.asarray(old_logp, F64).reshape(-1),
-        np.asarray(old_value, F64).reshape(-1), np.asarray(adv, F64).reshape(-1),
-        np.asarray(ret, F64).reshape(-1), cfg)
+        lp, ent, value.reshape(-1), np.asarray(old_logp, FT).reshape(-1),
+        np.asarray(old_value, FT).reshape(-1), np.asarray(adv, FT).reshape(-1),
+        np.asarray(ret, FT).reshape(-1), cfg)
     grads = zeros_like_tree(params)
     dhead = _head_grad(plan, hcache, act, g_lp, g_ent, grads)
     nets.recurrent_backward(params, plan, cache, dhead.reshape(B, T, -1),
@@ -185,13 +187,13 @@ def tree_map(f, *ts):
 
 
 def optimizer_init(params):
-    z = tree_map(lambda p: np.zeros(np.shape(p), F64), params)
+    z = tree_map(lambda p: np.zeros(np.shape(p), FT), params)
     return {"count": 0, "mu": z, "nu": tree_map(np.copy, z)}
 
 
 def optimizer_update(grads, state, params, opt):
     """clip_by_global_norm(max_grad_norm) then adam(lr, b1, b2, eps)."""
-    gnorm = np.sqrt(sum(float((np.asarray(g, F64) ** 2).sum()) for _, g in tree_leaves(grads)))
+    gnorm = math.sqrt(sum(float((np.asarray(g, FT) ** 2).sum()) for _, g in tree_leaves(grads)))
     if opt.get("max_grad_norm") is not None and not gnorm < opt["max_grad_norm"]:
         grads = tree_map(lambda g: (g / gnorm) * opt["max_grad_norm"], grads)
     b1, b2, eps, lr = opt.get("b1", 0.9), opt.get("b2", 0.999), opt.get("eps", 1e-8), opt["lr"]
@@ -199,7 +201,7 @@ def optimizer_update(grads, state, params, opt):
     mu = tree_map(lambda g, m: (1 - b1) * g + b1 * m, grads, state["mu"])
     nu = tree_map(lambda g, v: (1 - b2) * g * g + b2 * v, grads, state["nu"])
     c1, c2 = 1 - b1 ** count, 1 - b2 ** count
-    new = tree_map(lambda p, m, v: np.asarray(p, F64) - lr * ((m / c1) / (np.sqrt(v / c2) + eps)),
+    new = tree_map(lambda p, m, v: np.asarray(p, FT) - lr * ((m / c1) / (np.sqrt(v / c2) + eps)),
                    params, mu, nu)
     return new, {"count": count, "mu": mu, "nu": nu}, gnorm
 
