@@ -47,7 +47,7 @@ def parse():
     ap.add_argument("--cpu-seconds-also", type=float, default=8.0, help="CPU baseline budget of each --also workload")
     ap.add_argument("--also", default="auto",
                     help="other workloads measured in the same run, into the line's 'configs' list: "
-                         "'auto' (3,4,5 beside the default headline 2), 'none', or a comma list")
+                         "'auto' (3,4,5,6 beside the default headline 2), 'none', or a comma list")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--profile-only", action="store_true", help="warmup + timed updates only")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -191,8 +191,9 @@ def time_launches(ex, reps, per_update_steps):
     calls = ex.record(max_steps=1)
     stream = torch.cuda.current_stream()
     st = stream.cuda_stream
-    first_mb = max(i for i, (n, _) in enumerate(calls)
-                   if n in ("ppo_epoch_permutations", "ppo_sequence_rows")) + 1
+    # launches before the first minibatch step: those of an update stopped
+    # before it, less its log finalize
+    first_mb = len(ex.record(max_steps=0)) - 1
     rows, seen = [], {}
     for i, (name, args) in enumerate(calls):
         # the logs of every step are finalized once, after the last step
@@ -249,6 +250,11 @@ def cpu_baseline(recipe, params, tr_dev, budget_s):
         first_done = host(f.terminated) | host(f.truncated)
         carry0, carry_last = host(tr_dev.carry[0]), host(tr_dev.carry[-1])
     key = make_key(recipe.seed)
+    if recipe.algorithm == "pupo":
+        return _cpu_baseline_pupo(recipe, params, plan, cfg, opt, key, budget_s, dict(
+            obs=obs, first_done=first_done, action=act, reward=reward, terminated=term, truncated=trunc,
+            log_prob=logp, value=value, carry0=carry0, carry_last=carry_last, next_obs_last=next_last,
+            next_done_last=term[-1] | trunc[-1]))
     with oracle.working_precision(f32):
         p = oppo.tree_map(lambda x: np.asarray(x, f32), params)
         st = oppo.optimizer_init(p)
@@ -283,16 +289,52 @@ def cpu_baseline(recipe, params, tr_dev, budget_s):
             steps += 1
     t_update = t_pre + E * M * spent / steps
     unit = f"{N // M} envs x {T} steps" if recipe.recurrent else f"{mb} rows"
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        cores = os.cpu_count()
-    threads = int(os.environ.get("OMP_NUM_THREADS", cores))
-    return {"value": B / t_update, "unit": "samples/s", "cores": min(cores, threads), "kind": "port",
+    return {"value": B / t_update, "unit": "samples/s", "cores": _cores(), "kind": "port",
             "sample": f"oracle restatement in float32 numpy: bootstrap forward, GAE over the full [{T},{N}] "
                       f"rollout and the {E} epoch permutations ({t_pre:.2f} s), plus {steps} of the {E * M} "
                       f"minibatch steps of {unit} (gather, forward, backward, clip, Adam; {spent:.1f} s), "
                       f"extrapolated to one update"}
+
+
+def _cores() -> int:
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count()
+    return min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
+
+
+def _cpu_baseline_pupo(recipe, params, plan, cfg, opt, key, budget_s, tr):
+    """RecurrentPuPO's update restated by the oracle in float32: one step
+    (bootstrap + first minibatch step, after one untimed warm-up run), then as
+    many steps as the budget allows, the per-step time extrapolated to E * M
+    steps."""
+    import oracle
+    from oracle import ppo as oppo
+
+    E, M = recipe.cfg.update_epochs, recipe.cfg.num_minibatches
+    c = recipe.cfg
+    cfg = dict(cfg, gamma=c.gamma, gae_lambda=c.gae_lambda, update_epochs=E, num_minibatches=M,
+               advantage_clip=c.advantage_clip, trace_clip=c.trace_clip, priority_exponent=c.priority_exponent,
+               normalize_advantage=c.normalize_advantage)
+    with oracle.working_precision(np.float32):
+        p = oppo.tree_map(lambda x: np.asarray(x, np.float32), params)
+
+        def run(k):
+            t0 = time.perf_counter()
+            oppo.recurrent_pupo_update(p, oppo.optimizer_init(p), plan, cfg, opt, tr, key, 0.2, max_steps=k)
+            return time.perf_counter() - t0
+
+        run(1)  # warm-up
+        t1 = run(1)
+        k = max(1, min(E * M, int(budget_s / max(t1, 1e-9))))
+        per = (run(k) - t1) / (k - 1) if k > 1 else t1
+    t_update = t1 + (E * M - 1) * per
+    return {"value": recipe.batch / t_update, "unit": "samples/s", "cores": _cores(), "kind": "port",
+            "sample": f"oracle restatement of RecurrentPuPO.update in float32 numpy: bootstrap and the first "
+                      f"minibatch step ({t1:.2f} s), then {k} steps (each a V-trace over the full "
+                      f"[{recipe.T},{recipe.N}] rollout, the env draw, gather, forward, backward, clip, Adam; "
+                      f"{per:.2f} s per step), extrapolated to {E * M} steps"}
 
 
 def roofline_of(dom, total, workload):
@@ -564,8 +606,6 @@ def main():
         sys.exit(2)
     import torch
     from boonta_amd import recipes
-    from boonta_amd.algorithms.ppo import PPO
-    from boonta_amd.algorithms.recurrent_ppo import RecurrentPPO
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
@@ -580,9 +620,7 @@ def main():
     if args.path == "step":
         recipe = recipes.make(args.config)
         params = recipe.network.init(recipe.seed, recipe.obs_dim)["params"]
-        cls = RecurrentPPO if recipe.recurrent else PPO
-        alg = cls(cfg=recipe.cfg, network=recipe.network, optimizer=recipe.optimizer,
-                  use_graph=not args.no_graph)
+        alg = algorithm_of(recipe, not args.no_graph)
         state = alg.init_from_params({"params": params}, recipe.obs_dim)
         step_main(args, recipe, alg, state, params, dev)
         return
@@ -596,14 +634,21 @@ def main():
     print(json.dumps(out), flush=True)
 
 
+def algorithm_of(recipe, use_graph: bool):
+    from boonta_amd.algorithms import PPO, RecurrentPPO, RecurrentPuPO
+    cls = RecurrentPuPO if recipe.algorithm == "pupo" else RecurrentPPO if recipe.recurrent else PPO
+    return cls(cfg=recipe.cfg, network=recipe.network, optimizer=recipe.optimizer, use_graph=use_graph)
+
+
 def also_configs(args) -> list:
     """The other workloads measured in the same run (their lines go into
-    ``configs``): by default the Gaussian, GRU and bf16 workloads beside the
-    discrete Anakin headline, none for another headline or --profile-only."""
+    ``configs``): by default the Gaussian, GRU, bf16 and RecurrentPuPO
+    workloads beside the discrete Anakin headline, none for another headline or
+    --profile-only."""
     if args.profile_only or args.also == "none":
         return []
     if args.also == "auto":
-        return [3, 4, 5] if args.config == 2 else []
+        return [3, 4, 5, 6] if args.config == 2 else []
     return [int(c) for c in args.also.split(",") if c and int(c) != args.config]
 
 
@@ -615,16 +660,13 @@ def measure_update(args, config: int, dev, headline: bool) -> dict:
     import synthetic
     import torch
     from boonta_amd import recipes
-    from boonta_amd.algorithms.ppo import PPO
-    from boonta_amd.algorithms.recurrent_ppo import RecurrentPPO
     from boonta_amd.random import key as make_key
 
     recipe = recipes.make(config)
     log(f"workload {recipe.name}: T={recipe.T} N={recipe.N} obs={recipe.obs_dim} "
         f"{recipe.cfg.update_epochs}x{recipe.cfg.num_minibatches} minibatches of {recipe.minibatch}")
     params = recipe.network.init(recipe.seed, recipe.obs_dim)["params"]
-    cls = RecurrentPPO if recipe.recurrent else PPO
-    alg = cls(cfg=recipe.cfg, network=recipe.network, optimizer=recipe.optimizer, use_graph=not args.no_graph)
+    alg = algorithm_of(recipe, not args.no_graph)
     state = alg.init_from_params({"params": params}, recipe.obs_dim)
     tr = synthetic.device_rollout(recipe, params, dev, recipe.seed)
     torch.cuda.synchronize()

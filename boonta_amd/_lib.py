@@ -33,6 +33,8 @@ SIGNATURES = {
     "ppo_vtrace_f32": (I, [P, P, P, P, P, P, P, I64, F, F, P, P, I, I, D, D, I]),
     "ppo_normalize_workspace": (SZ, [I64]),
     "ppo_normalize_advantages_f32": (I, [P, P, I64, P, SZ]),
+    "ppo_pupo_advantages_f32": (I, [P, P, P, I, P, I, I, P]),
+    "ppo_fill_f32": (I, [P, P, I64, F]),
     "ppo_threefry_split": (I, [P, P, P, I64]),
     "ppo_permutation_workspace": (SZ, [I64]),
     "ppo_permutation": (I, [P, P, P, I64, P, SZ]),
@@ -78,6 +80,9 @@ SIGNATURES = {
     "ppo_head_loss_max_features": (I, []),
     "ppo_head_loss_f32": (I, [P, I, I, P, P, I64, P, I64, P, I, P, I64, P, I64, P, I, I, P, P, P, P, P, P, P,
                               I, P, I64, P, I64, I, P, I64, P, I64, P, P, P, P, P, P, F, I, F, F, F]),
+    "ppo_head_loss_ratio_f32": (I, [P, I, I, P, P, I64, P, I64, P, I, P, I64, P, I64, P, I, I, P, P, P, P, P, P, P,
+                                    I, P, I64, P, I64, I, P, I64, P, I64, P, P, P, P, P, P, F, I, F, F, F, P, I,
+                                    I]),
     "ppo_gru_fwd_step_f32": (I, [P, P, I64, P, I64, P, P, P, P, P, I64, P, P, I64, P, I64, P, I64, I, I]),
     "ppo_gru_bwd_step_f32": (I, [P, P, I64, P, I64, P, I64, P, I64, P, P, P, P, I64, P, I64, P, I64, P, I64, P,
                                  I64, I, I]),

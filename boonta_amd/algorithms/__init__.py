@@ -1,6 +1,7 @@
 from .advantage_estimators import generalized_advantage_estimator
 from .ppo import PPO, PPOConfig, PPOState
 from .recurrent_ppo import RecurrentPPO, RecurrentPPOConfig, RecurrentPPOState
+from .recurrent_pupo import RecurrentPuPO, RecurrentPuPOConfig, RecurrentPuPOState
 
 __all__ = ["PPO", "PPOConfig", "PPOState", "RecurrentPPO", "RecurrentPPOConfig", "RecurrentPPOState",
-           "generalized_advantage_estimator"]
+           "RecurrentPuPO", "RecurrentPuPOConfig", "RecurrentPuPOState", "generalized_advantage_estimator"]

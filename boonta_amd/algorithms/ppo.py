@@ -223,7 +223,7 @@ class PPO:
         if not self.use_graph:
             ex.issue(torch.cuda.current_stream().cuda_stream)
             return state
-        gk = (id(ex), sig)
+        gk = self._graph_key(ex, sig)
         g = self._graphs.get(gk)
         if g is None:
             flat = ex.flat
@@ -244,6 +244,10 @@ class PPO:
             self._graphs[gk] = g
         g.replay()
         return state
+
+    def _graph_key(self, ex, sig) -> tuple:
+        """What a captured update depends on beyond the executor's buffers."""
+        return (id(ex), sig)
 
     def logs(self, state, T: int, N: int, obs_dim: int) -> dict:
         """The logged scalars of every minibatch step of the last update

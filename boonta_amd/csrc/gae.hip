@@ -175,14 +175,16 @@ constexpr int NORM_THREADS = 256;
 constexpr int NORM_PER_THREAD = 16;
 constexpr int NORM_PER_BLOCK = NORM_THREADS * NORM_PER_THREAD;
 
+// sum over a workgroup of THREADS threads; every thread gets the total
+template <int THREADS = NORM_THREADS>
 __device__ double block_sum_d(double v) {
-  __shared__ double s[NORM_THREADS / 64];
+  __shared__ double s[THREADS / 64];
   v = ppo::wave_sum_d(v);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   if (lane == 0) s[w] = v;
   __syncthreads();
   double t = 0.0;
-  for (int i = 0; i < NORM_THREADS / 64; ++i) t += s[i];
+  for (int i = 0; i < THREADS / 64; ++i) t += s[i];
   __syncthreads();
   return t;
 }
@@ -233,7 +235,66 @@ __global__ void __launch_bounds__(NORM_THREADS) norm_apply_kernel(float* a, int6
   }
 }
 
+// RecurrentPuPO's minibatch advantages (boonta/algorithms/recurrent_pupo.py
+// :244-250), one workgroup: the V-trace advantages of the minibatch's samples
+// rows[i] (t * N + env, listed time-major: row t * width + b), normalised over
+// the minibatch when `normalize` ((A - mean) / (std + 1e-8), population std,
+// sums in float64), times the importance weight of the row's sequence b:
+//   out[rows[i]] = weights[i % width] * A'[i].
+// A sequence drawn twice (choice with replacement) writes the same value
+// twice: its samples, weight and the minibatch statistics are the same.
+constexpr int PUPO_THREADS = 1024;
+
+__global__ void __launch_bounds__(PUPO_THREADS) pupo_advantages_kernel(const float* adv, const int32_t* rows,
+                                                                       int count, const float* weights, int width,
+                                                                       int normalize, float* out) {
+  float mean = 0.f, den = 1.f;
+  if (normalize) {
+    double v = 0.0;
+    for (int i = threadIdx.x; i < count; i += PUPO_THREADS) v += (double)adv[rows[i]];
+    const double m = block_sum_d<PUPO_THREADS>(v) / (double)count;
+    double d2 = 0.0;
+    for (int i = threadIdx.x; i < count; i += PUPO_THREADS) {
+      const double d = (double)adv[rows[i]] - m;
+      d2 += d * d;
+    }
+    const double var = block_sum_d<PUPO_THREADS>(d2) / (double)count;
+    mean = (float)m;
+    den = (float)sqrt(var) + 1e-8f;
+  }
+  for (int i = threadIdx.x; i < count; i += PUPO_THREADS) {
+    const int32_t r = rows[i];
+    const float a = normalize ? (adv[r] - mean) / den : adv[r];
+    out[r] = weights[i % width] * a;
+  }
+}
+
+__global__ void fill_kernel(float* a, int64_t n, float v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) a[i] = v;
+}
+
 }  // namespace
+
+PPO_EXPORT int ppo_pupo_advantages_f32(void* stream, const float* adv, const int32_t* rows, int count,
+                                       const float* weights, int width, int normalize, float* out) {
+  if (count < 0 || width < 1 || (count > 0 && count % width))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_pupo_advantages_f32: %d rows are not whole steps of %d sequences",
+                          count, width);
+  if (count == 0) return PPO_OK;
+  if (!adv || !rows || !weights || !out) return ppo::set_error(PPO_ERR_ARG, "ppo_pupo_advantages_f32: null buffer");
+  hipLaunchKernelGGL(pupo_advantages_kernel, dim3(1), dim3(PUPO_THREADS), 0, ppo::as_stream(stream), adv, rows, count,
+                     weights, width, normalize, out);
+  return ppo::check_launch("ppo_pupo_advantages_f32");
+}
+
+PPO_EXPORT int ppo_fill_f32(void* stream, float* a, int64_t n, float value) {
+  if (n < 0 || (n > 0 && !a)) return ppo::set_error(PPO_ERR_ARG, "ppo_fill_f32: bad argument");
+  if (n == 0) return PPO_OK;
+  hipLaunchKernelGGL(fill_kernel, dim3((unsigned)ppo::ceil_div64(n, 256)), dim3(256), 0, ppo::as_stream(stream), a, n,
+                     value);
+  return ppo::check_launch("ppo_fill_f32");
+}
 
 PPO_EXPORT size_t ppo_normalize_workspace(int64_t n) {
   if (n <= 0) return 0;

@@ -55,6 +55,9 @@ struct HeadLossParams {
   float* wpart_a; float* bpart_a; float* wpart_c; float* bpart_c;
   float* dscale_partial; double* stats_partial;
   float clip_eps; int clip_value_loss; float ent_coef, vf_coef, inv_n, temperature;
+  // optional: each row's ratio exp(logp - old_logp) written env-major,
+  // ratio_out[(s % ratio_envs) * ratio_steps + s / ratio_envs] for sample s = t * N + env
+  float* ratio_out; int ratio_envs, ratio_steps;
 };
 
 __device__ __forceinline__ float tie_first(float x, float y, float ans) {
@@ -88,6 +91,7 @@ struct LaneIn {
   float actf;  // Gaussian action component j
   int a;       // categorical action
   bool live;   // the row exists
+  int64_t s;   // its sample index
 };
 
 __device__ __forceinline__ LaneIn load_lane(const HeadLossParams& p, int r, int j) {
@@ -95,6 +99,7 @@ __device__ __forceinline__ LaneIn load_lane(const HeadLossParams& p, int r, int 
   in.live = r < p.rows;
   const int rc = in.live ? r : p.rows - 1;
   const int64_t s = p.idx ? (int64_t)p.idx[rc] : (int64_t)rc;
+  in.s = s;
   in.olp = p.old_logp[s];
   in.adv = p.adv[s];
   in.ret = p.ret[s];
@@ -174,7 +179,7 @@ __device__ __forceinline__ void phase_b(const HeadLossParams& p, int64_t blk, co
     } else {
       v = __shfl(o, p.na - 1, 16);
     }
-    float lp, ent, val, draw = 0.f, pmin_r, clip_r;
+    float lp, ent, val, draw = 0.f, pmin_r, clip_r, ratio_r;
     if (!gauss) {
       const float z = o * inv_t;
       const float mx = row16_max(jin ? z : -INFINITY);
@@ -198,6 +203,7 @@ __device__ __forceinline__ void phase_b(const HeadLossParams& p, int64_t blk, co
       val = jin ? (g_lp * ((j == x.a ? 1.f : 0.f) - q) - g_ent * q * (lq + ent)) * inv_t : 0.f;
       pmin_r = pmin;
       clip_r = (fabsf(ratio - 1.f) > eps) ? 1.f : 0.f;
+      ratio_r = ratio;
     } else {
       const float raw = spread ? 0.f : __shfl(o, min(A + j, 15), 16);
       const float sig = spread ? cc.sig : p.temperature * (softplusf(raw) + 1e-3f);
@@ -223,6 +229,7 @@ __device__ __forceinline__ void phase_b(const HeadLossParams& p, int64_t blk, co
       }
       pmin_r = pmin;
       clip_r = (fabsf(ratio - 1.f) > eps) ? 1.f : 0.f;
+      ratio_r = ratio;
     }
     // value loss (the same in every lane of the row)
     const float vl1 = 0.5f * (v - x.ret) * (v - x.ret);
@@ -257,6 +264,7 @@ __device__ __forceinline__ void phase_b(const HeadLossParams& p, int64_t blk, co
       st[rr][ST_RET] = l ? (double)x.ret : 0.0;
       st[rr][ST_RET2] = l ? (double)x.ret * (double)x.ret : 0.0;
       st[rr][ST_VALUE] = l ? (double)v : 0.0;
+      if (p.ratio_out && l) p.ratio_out[(x.s % p.ratio_envs) * p.ratio_steps + x.s / p.ratio_envs] = ratio_r;
     }
   }
   __syncthreads();
@@ -580,7 +588,7 @@ PPO_EXPORT int ppo_head_loss_blocks(int rows) {
 PPO_EXPORT int ppo_head_loss_max_outputs(void) { return 16; }
 PPO_EXPORT int ppo_head_loss_max_features(void) { return 512; }
 
-PPO_EXPORT int ppo_head_loss_f32(
+static int head_loss_impl(
     void* stream, int dist, int rows, const int32_t* idx, const float* ha, int64_t ldha, const float* wa,
     int64_t ldwa, const float* ba, int na, const float* hc, int64_t ldhc, const float* wc, int64_t ldwc,
     const float* bc, int F, int A, const float* scale_param, const int32_t* action_i, const float* action_f,
@@ -588,7 +596,7 @@ PPO_EXPORT int ppo_head_loss_f32(
     const float* aux_a, int64_t ldaux_a, float* dha, int64_t lddha, int act_c, const float* aux_c,
     int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a, float* wpart_c, float* bpart_c,
     float* dscale_partial, double* stats_partial, float clip_eps, int clip_value_loss, float ent_coef,
-    float vf_coef, float temperature) {
+    float vf_coef, float temperature, float* ratio_out, int ratio_envs, int ratio_steps) {
   const bool sep = hc != nullptr;
   if (rows < 0 || F <= 0 || F > 512 || F % 16 != 0 || na <= 0 || na > 16 || ldwa < na || ldwa > 16 || A <= 0 ||
       A > 16 ||
@@ -618,6 +626,7 @@ PPO_EXPORT int ppo_head_loss_f32(
   p.dscale_partial = dscale_partial; p.stats_partial = stats_partial;
   p.clip_eps = clip_eps; p.clip_value_loss = clip_value_loss; p.ent_coef = ent_coef; p.vf_coef = vf_coef;
   p.inv_n = 1.f / (float)rows; p.temperature = temperature;
+  p.ratio_out = ratio_out; p.ratio_envs = ratio_envs; p.ratio_steps = ratio_steps;
   const int blocks = ppo_head_loss_blocks(rows);
   hipStream_t st = ppo::as_stream(stream);
   if (rows <= PPO_HL_SMALL_ROWS) {
@@ -637,4 +646,41 @@ PPO_EXPORT int ppo_head_loss_f32(
     hipLaunchKernelGGL(head_loss_kernel<false>, dim3(blocks), dim3(HL_THREADS), 0, st, p);
   }
   return ppo::check_launch("ppo_head_loss_f32");
+}
+
+PPO_EXPORT int ppo_head_loss_f32(
+    void* stream, int dist, int rows, const int32_t* idx, const float* ha, int64_t ldha, const float* wa,
+    int64_t ldwa, const float* ba, int na, const float* hc, int64_t ldhc, const float* wc, int64_t ldwc,
+    const float* bc, int F, int A, const float* scale_param, const int32_t* action_i, const float* action_f,
+    const float* old_logp, const float* old_value, const float* adv, const float* ret, int act_a,
+    const float* aux_a, int64_t ldaux_a, float* dha, int64_t lddha, int act_c, const float* aux_c,
+    int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a, float* wpart_c, float* bpart_c,
+    float* dscale_partial, double* stats_partial, float clip_eps, int clip_value_loss, float ent_coef,
+    float vf_coef, float temperature) {
+  return head_loss_impl(stream, dist, rows, idx, ha, ldha, wa, ldwa, ba, na, hc, ldhc, wc, ldwc, bc, F, A,
+                        scale_param, action_i, action_f, old_logp, old_value, adv, ret, act_a, aux_a, ldaux_a, dha,
+                        lddha, act_c, aux_c, ldaux_c, dhc, lddhc, wpart_a, bpart_a, wpart_c, bpart_c, dscale_partial,
+                        stats_partial, clip_eps, clip_value_loss, ent_coef, vf_coef, temperature, nullptr, 1, 1);
+}
+
+// ppo_head_loss_f32 that also writes each row's ratio exp(logp - old_logp)
+// into ratio_out[(s % envs) * steps + s / envs], s = idx[row] = t * envs + env
+// (RecurrentPuPO keeps the last ratio of every env and step).  Every sample
+// index must be below envs * steps.
+PPO_EXPORT int ppo_head_loss_ratio_f32(
+    void* stream, int dist, int rows, const int32_t* idx, const float* ha, int64_t ldha, const float* wa,
+    int64_t ldwa, const float* ba, int na, const float* hc, int64_t ldhc, const float* wc, int64_t ldwc,
+    const float* bc, int F, int A, const float* scale_param, const int32_t* action_i, const float* action_f,
+    const float* old_logp, const float* old_value, const float* adv, const float* ret, int act_a,
+    const float* aux_a, int64_t ldaux_a, float* dha, int64_t lddha, int act_c, const float* aux_c,
+    int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a, float* wpart_c, float* bpart_c,
+    float* dscale_partial, double* stats_partial, float clip_eps, int clip_value_loss, float ent_coef,
+    float vf_coef, float temperature, float* ratio_out, int envs, int steps) {
+  if (!ratio_out || envs < 1 || steps < 1 || (int64_t)envs * steps > INT32_MAX)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_head_loss_ratio_f32: bad ratio buffer (envs %d, steps %d)", envs, steps);
+  return head_loss_impl(stream, dist, rows, idx, ha, ldha, wa, ldwa, ba, na, hc, ldhc, wc, ldwc, bc, F, A,
+                        scale_param, action_i, action_f, old_logp, old_value, adv, ret, act_a, aux_a, ldaux_a, dha,
+                        lddha, act_c, aux_c, ldaux_c, dhc, lddhc, wpart_a, bpart_a, wpart_c, bpart_c, dscale_partial,
+                        stats_partial, clip_eps, clip_value_loss, ent_coef, vf_coef, temperature, ratio_out, envs,
+                        steps);
 }

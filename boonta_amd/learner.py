@@ -811,6 +811,14 @@ class MLPExecutor(ForwardChain):
         self._call("ppo_loss_finalize_steps", st, _p(self.STATS), self.loss_blocks, self.mb, steps,
                    float(cfg.entropy_coefficient), float(cfg.value_coefficient), _p(self.LOGS))
 
+    def _loss_adv(self) -> int:
+        """Advantages the loss reads at the minibatch's sample indices."""
+        return _p(self.ADV)
+
+    def _ratio_out(self):
+        """(pointer, envs, steps) where the fused loss keeps each row's ratio, or None."""
+        return None
+
     def _head_a_io(self, la: LayerBufs):
         """(input, ld, cotangent destination, act, aux, ldaux) of head group a:
         the last layer's output, and where its cotangent goes."""
@@ -839,12 +847,16 @@ class MLPExecutor(ForwardChain):
         else:
             c_args = (None, 0, None, 0, None)
             cd_args = (0, None, 0, None, 0)
-        self._call("ppo_head_loss_f32", st, dist, mb, idx, ya, ldya, self.flat.view(h.w), h.w.ld,
-                   self.flat.view(h.b), na, *c_args, h.fin, A, scale_ptr, act_i, act_f, inp["log_prob"],
-                   inp["value"], _p(self.ADV), _p(self.RET), acta, auxa, ldauxa, da, ldya, *cd_args,
-                   _p(wpa), _p(bpa), _p(wpc), _p(bpc), _p(self.DSCALE), self._stats(step),
-                   float(cfg.clip_coefficient), int(cfg.clip_value_loss), float(cfg.entropy_coefficient),
-                   float(cfg.value_coefficient), 1.0)
+        args = (dist, mb, idx, ya, ldya, self.flat.view(h.w), h.w.ld, self.flat.view(h.b), na, *c_args, h.fin, A,
+                scale_ptr, act_i, act_f, inp["log_prob"], inp["value"], self._loss_adv(), _p(self.RET), acta, auxa,
+                ldauxa, da, ldya, *cd_args, _p(wpa), _p(bpa), _p(wpc), _p(bpc), _p(self.DSCALE), self._stats(step),
+                float(cfg.clip_coefficient), int(cfg.clip_value_loss), float(cfg.entropy_coefficient),
+                float(cfg.value_coefficient), 1.0)
+        ratio = self._ratio_out()
+        if ratio is None:
+            self._call("ppo_head_loss_f32", st, *args)
+        else:
+            self._call("ppo_head_loss_ratio_f32", st, *args, *ratio)
 
     def _minibatch(self, st, idx, step, obs, ldo, dist, A):
         prog, cfg, inp, mb = self.prog, self.cfg, self.inp, self.mb

@@ -107,31 +107,12 @@ class RecurrentExecutor(MLPExecutor):
                    self.flat.view(g.wh), 3 * H, self.flat.view(g.bhn), h_out, H, hp_out, H, gates, 4 * H, B, H)
 
     def issue(self, st: int, max_steps: int | None = None):
-        inp, prog, cfg, chain = self.inp, self.prog, self.cfg, self.chain
-        g = prog.gru
-        H, I = g.H, g.fin
-        T, N, B, mb, Bm = self.T, self.N, self.B, self.mb, self.Bm
-        ldo = self.obs_dim
+        inp, cfg = self.inp, self.cfg
+        T, N, mb, Bm = self.T, self.N, self.mb, self.Bm
         if not self.trunk:
             raise NotImplementedError("the recurrent learner needs an MLP feature extractor before the GRU")
         # 1. bootstrap: the two-step tail sequence from carry[-1]
-        last = 4 * (T - 1) * N
-        self._fwd_layers(st, self.boot_layers, inp["obs"] + last * ldo, ldo, None, N, row0=0)
-        self._fwd_layers(st, self.boot_layers, inp["next_obs_last"], ldo, None, N, row0=N)
-        eb = self.boot_layers[-1]
-        self._gemm(st, A_ROW, B_KN, _p(eb.Y), eb.spec.ld, None, self.flat.view(g.wi), 3 * H,
-                   _p(self.XIB), 3 * H, 2 * N, 3 * H, I, 1, 0, EPI_BIAS_ACT, self.flat.view(g.bi), 0, None, None, 0,
-                   None, -1)
-        self._gru_fwd(st, _p(self.XIB), inp["carry_last"], None, inp["first_terminated"] + (T - 1) * N,
-                      inp["first_truncated"] + (T - 1) * N, None, _p(self.HB), None, None, N)
-        self._gru_fwd(st, _p(self.XIB) + 4 * N * 3 * H, _p(self.HB), None, inp["terminated"] + (T - 1) * N,
-                      inp["truncated"] + (T - 1) * N, None, _p(self.HB) + 4 * N * H, None, None, N)
-        h = prog.head_a
-        self._gemm(st, A_ROW, B_KN, _p(self.HB) + 4 * N * H, H, None, self.flat.view(h.w), h.w.ld,
-                   _p(self.HEADB), h.w.ld, N, h.w.ld, h.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(h.b), 0, None, None,
-                   0, None, -1)
-        self._call("ppo_act_fwd_f32", st, _p(self.HEADB) + 4 * prog.head_out, self.HEADB.shape[1], _p(self.BOOT),
-                   1, N, 1, 0)
+        self._bootstrap(st)
         # 2. GAE
         self._call("ppo_gae_f32", st, inp["reward"], inp["terminated"], inp["truncated"], inp["value"],
                    _p(self.BOOT), None, None, _p(self.ADV), _p(self.RET), T, N, float(cfg.gamma),
@@ -154,6 +135,33 @@ class RecurrentExecutor(MLPExecutor):
                 self._optimizer_step(st, step)
         self._finish_logs(st, self.E * self.M)
         self._call("ppo_count_advance", st, _p(self.flat.count), self.E * self.M)
+
+    def _bootstrap(self, st):
+        """Value of second.obs[-1]: the two-step tail sequence (first[-1],
+        second[-1]) from carry[-1] with the resets first.done[-1] /
+        second.done[-1] (transition.py:20-26, recurrent_ppo.py:188-198)."""
+        inp, prog = self.inp, self.prog
+        g = prog.gru
+        H, I = g.H, g.fin
+        T, N = self.T, self.N
+        ldo = self.obs_dim
+        last = 4 * (T - 1) * N
+        self._fwd_layers(st, self.boot_layers, inp["obs"] + last * ldo, ldo, None, N, row0=0)
+        self._fwd_layers(st, self.boot_layers, inp["next_obs_last"], ldo, None, N, row0=N)
+        eb = self.boot_layers[-1]
+        self._gemm(st, A_ROW, B_KN, _p(eb.Y), eb.spec.ld, None, self.flat.view(g.wi), 3 * H,
+                   _p(self.XIB), 3 * H, 2 * N, 3 * H, I, 1, 0, EPI_BIAS_ACT, self.flat.view(g.bi), 0, None, None, 0,
+                   None, -1)
+        self._gru_fwd(st, _p(self.XIB), inp["carry_last"], None, inp["first_terminated"] + (T - 1) * N,
+                      inp["first_truncated"] + (T - 1) * N, None, _p(self.HB), None, None, N)
+        self._gru_fwd(st, _p(self.XIB) + 4 * N * 3 * H, _p(self.HB), None, inp["terminated"] + (T - 1) * N,
+                      inp["truncated"] + (T - 1) * N, None, _p(self.HB) + 4 * N * H, None, None, N)
+        h = prog.head_a
+        self._gemm(st, A_ROW, B_KN, _p(self.HB) + 4 * N * H, H, None, self.flat.view(h.w), h.w.ld,
+                   _p(self.HEADB), h.w.ld, N, h.w.ld, h.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(h.b), 0, None, None,
+                   0, None, -1)
+        self._call("ppo_act_fwd_f32", st, _p(self.HEADB) + 4 * prog.head_out, self.HEADB.shape[1], _p(self.BOOT),
+                   1, N, 1, 0)
 
     def _sequence_minibatch(self, st, rows, envs, step):
         inp, prog, cfg = self.inp, self.prog, self.cfg

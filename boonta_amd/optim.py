@@ -80,3 +80,16 @@ def as_chain(opt) -> Chain:
     if isinstance(opt, Adam):
         return Chain((opt,))
     raise NotImplementedError(f"optimizer {opt!r} is not compiled")
+
+
+@dataclass(frozen=True)
+class ConstantSchedule:
+    """optax.constant_schedule(value): the same value at every step."""
+    value: float
+
+    def __call__(self, step) -> float:
+        return self.value
+
+
+def constant_schedule(value: float) -> ConstantSchedule:
+    return ConstantSchedule(float(value))

@@ -9,6 +9,10 @@ hangar/config/algorithm/{ppo,recurrent_ppo}.yaml and the optimizer chain
   3  Gaussian:         obs [16, 4096, 87];     D = 8, state-independent scale; separate 4x256 LN+SiLU
   4  recurrent GRU:    obs [64, 1024, 128];    8 actions; Dense256+ReLU -> GRU(256)
   5  large obs, bf16:  obs [64, 1024, 8268];   43 actions; shared 3x512 LN+ReLU
+  6  RecurrentPuPO:    workload 4's rollout and network under RecurrentPuPO
+                       (hangar/config/algorithm/recurrent_pupo.yaml: advantage and trace
+                       clip 1, priority exponent 0.8, minibatch advantages normalised,
+                       importance exponent 0.2), 4 epochs x 4 draws of 256 envs
 """
 from __future__ import annotations
 
@@ -19,6 +23,7 @@ import numpy as np
 from . import networks as nn
 from . import optim
 from .algorithms.ppo import PPOConfig
+from .algorithms.recurrent_pupo import RecurrentPuPOConfig
 
 
 @dataclass(frozen=True)
@@ -33,6 +38,7 @@ class Recipe:
     seed: int
     done_p: float
     recurrent: bool = False
+    algorithm: str = "ppo"   # "ppo" (PPO / RecurrentPPO) or "pupo" (RecurrentPuPO)
 
     @property
     def batch(self) -> int:
@@ -123,7 +129,17 @@ def config5() -> Recipe:
                   done_p=0.002)
 
 
-CONFIGS = {1: config1, 2: config2, 3: config3, 4: config4, 5: config5}
+def config6() -> Recipe:
+    r = config4()
+    c = r.cfg
+    cfg = RecurrentPuPOConfig(num_minibatches=c.num_minibatches, update_epochs=c.update_epochs,
+                              clip_coefficient=c.clip_coefficient, clip_value_loss=c.clip_value_loss,
+                              entropy_coefficient=c.entropy_coefficient, value_coefficient=c.value_coefficient,
+                              gamma=c.gamma, gae_lambda=c.gae_lambda)
+    return replace(r, name="recurrent-pupo", cfg=cfg, seed=1006, algorithm="pupo")
+
+
+CONFIGS = {1: config1, 2: config2, 3: config3, 4: config4, 5: config5, 6: config6}
 
 
 def make(config: int) -> Recipe:

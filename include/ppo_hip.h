@@ -78,6 +78,18 @@ int ppo_vtrace_f32(void* stream, const float* reward, const uint8_t* terminated,
 size_t ppo_normalize_workspace(int64_t n);
 int ppo_normalize_advantages_f32(void* stream, float* adv, int64_t n, void* workspace, size_t workspace_bytes);
 
+/* RecurrentPuPO's minibatch advantages (boonta/algorithms/recurrent_pupo.py:
+ * 244-250): out[rows[i]] = weights[i % width] * A'[i] where A' is advantages
+ * [rows[i]] normalised over the count = T * width minibatch samples when
+ * normalize ((A - mean) / (std + 1e-8), population std), rows[i] = t * N + env
+ * listed time-major (ppo_sequence_rows), weights [width] the importance weight
+ * of each drawn sequence (ppo_priority_choice_f32). */
+int ppo_pupo_advantages_f32(void* stream, const float* advantages, const int32_t* rows, int count,
+                            const float* weights, int width, int normalize, float* out);
+/* a[i] = value for i < n (a fill that a captured graph can hold; RecurrentPuPO
+ * starts every update from ratio = ones, recurrent_pupo.py:306). */
+int ppo_fill_f32(void* stream, float* a, int64_t n, float value);
+
 /* ----------------------------------------------------------- permutation
  * Replace jax.random.split(key, E) and jax.random.permutation(key, n) at
  * boonta/algorithms/ppo.py:200,230 and recurrent_ppo.py:272,278 (jax 0.10.2,
@@ -342,6 +354,20 @@ int ppo_head_loss_f32(void* stream, int dist, int rows, const int32_t* idx, cons
                       int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a,
                       float* wpart_c, float* bpart_c, float* dscale_partial, double* stats_partial,
                       float clip_eps, int clip_value_loss, float ent_coef, float vf_coef, float temperature);
+/* ppo_head_loss_f32 that also keeps each row's ratio exp(logp - old_logp),
+ * env-major: ratio_out[(s % envs) * steps + s / envs] for the row's sample
+ * s = idx[row] = t * envs + env (the new ratio RecurrentPuPO scatters back
+ * with stop_gradient, recurrent_pupo.py:123,297). */
+int ppo_head_loss_ratio_f32(void* stream, int dist, int rows, const int32_t* idx, const float* ha, int64_t ldha,
+                            const float* wa, int64_t ldwa, const float* ba, int na, const float* hc, int64_t ldhc,
+                            const float* wc, int64_t ldwc, const float* bc, int F, int A, const float* scale_param,
+                            const int32_t* action_i, const float* action_f, const float* old_logp,
+                            const float* old_value, const float* adv, const float* ret, int act_a,
+                            const float* aux_a, int64_t ldaux_a, float* dha, int64_t lddha, int act_c,
+                            const float* aux_c, int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a,
+                            float* bpart_a, float* wpart_c, float* bpart_c, float* dscale_partial,
+                            double* stats_partial, float clip_eps, int clip_value_loss, float ent_coef,
+                            float vf_coef, float temperature, float* ratio_out, int envs, int steps);
 
 /* ------------------------------------------------------------------- GRU
  * One time step of flax.linen.GRUCell inside boonta's RNN block

@@ -16,6 +16,12 @@ Restates, for the MLP and GRU actor-critics of the learner:
 - ``PPO.update`` ppo.py:199-233 and ``RecurrentPPO.update`` recurrent_ppo.py:186-281:
   bootstrap, GAE, optional normalisation, flatten (index t * N + n), split the
   key into E epoch keys, permute, reshape into M minibatches, scan.
+- ``RecurrentPuPO.update`` recurrent_pupo.py:190-308: the same bootstrap; a
+  ratio [N, T] of ones carried through E * M minibatch steps on the keys
+  split(key, E * M); each step V-trace with rho = min(ratio, advantage_clip),
+  c = min(ratio, trace_clip), prioritised env selection with replacement
+  (oracle/priority.py), the minibatch advantages normalised and weighted per
+  env, the recurrent loss, clip + Adam, and the step's ratios scattered back.
 """
 from __future__ import annotations
 
@@ -25,6 +31,7 @@ import numpy as np
 
 from . import gae as _gae
 from . import nets
+from . import priority as _priority
 from . import prng
 
 FT = np.float64  # working precision (see nets.FT)
@@ -152,8 +159,10 @@ def loss_and_grad(params, plan, cfg, obs, action, old_logp, old_value, adv, ret)
 
 
 def recurrent_loss_and_grad(params, plan, cfg, obs, done, carry, action, old_logp,
-                            old_value, adv, ret):
-    """One env-major sequence minibatch [B, T, ...] of RecurrentPPO."""
+                            old_value, adv, ret, return_ratio=False):
+    """One env-major sequence minibatch [B, T, ...] of RecurrentPPO.  With
+    ``return_ratio`` also each sample's ratio exp(logp - old_logp) [B, T]
+    (RecurrentPuPO's loss_fn returns it, recurrent_pupo.py:123,187)."""
     B, T = done.shape
     head, value, _, cache = nets.recurrent_forward(params, plan, obs, done, carry)
     hf = head.reshape(B * T, -1)
@@ -167,6 +176,8 @@ def recurrent_loss_and_grad(params, plan, cfg, obs, done, carry, action, old_log
     dhead = _head_grad(plan, hcache, act, g_lp, g_ent, grads)
     nets.recurrent_backward(params, plan, cache, dhead.reshape(B, T, -1),
                             g_v.reshape(B, T), grads)
+    if return_ratio:
+        return loss, logs, grads, np.exp(lp - np.asarray(old_logp, FT).reshape(-1)).reshape(B, T)
     return loss, logs, grads
 
 
@@ -279,3 +290,62 @@ def recurrent_ppo_update(params, opt_state, plan, cfg, opt, tr, key, record=None
             record(e, idx, grads, params)
     return params, opt_state, {"advantages": adv, "returns": ret, "bootstrap": boot,
                                "permutations": perms, "logs": logs}
+
+
+def recurrent_pupo_update(params, opt_state, plan, cfg, opt, tr, key, beta, record=None, max_steps=None,
+                          indices=None):
+    """RecurrentPuPO.update (recurrent_pupo.py:100-308) on the transition dict
+    of ``recurrent_ppo_update``.  ``cfg`` adds advantage_clip, trace_clip,
+    priority_exponent and normalize_advantage; ``beta`` is
+    importance_exponent(state.step) (:208).  ``indices`` (a list of [width]
+    arrays, one per step) replaces the oracle's own env draw at each step, so
+    that a run whose advantages differ within rounding can be followed step by
+    step; the oracle's own draws and their distances from a cumulative boundary
+    are returned beside them."""
+    T, N = tr["reward"].shape
+    E, M = cfg["update_epochs"], cfg["num_minibatches"]
+    width = N // M
+    # bootstrap from the tail sequence (:193-203), as RecurrentPPO.update
+    seq_obs = np.stack([tr["obs"][-1], tr["next_obs_last"]], axis=1)
+    seq_done = np.stack([tr["first_done"][-1], tr["next_done_last"]], axis=1)
+    _, val, _, _ = nets.recurrent_forward(params, plan, seq_obs, seq_done, tr["carry_last"])
+    boot = val[:, -1]
+    keys = prng.split(key, E * M)                      # :303-305
+    ratio = np.ones((N, T), FT)                        # :306
+    em = lambda a, idx: np.moveaxis(np.take(np.asarray(a), idx, axis=1), 0, 1)
+    steps = E * M if max_steps is None else min(max_steps, E * M)
+    info = {"bootstrap": boot, "indices": [], "weights": [], "own_indices": [], "margins": [],
+            "probabilities": [], "logs": []}
+    for step in range(steps):
+        # V-trace on the carried ratio (:210-220, :226)
+        rt = ratio.T
+        adv, ret = _gae.gae(tr["reward"], tr["terminated"], tr["truncated"], tr["value"], boot,
+                            cfg["gamma"], cfg["gae_lambda"], rho=np.minimum(rt, cfg["advantage_clip"]),
+                            c=np.minimum(rt, cfg["trace_clip"]), dtype=FT)
+        # prioritised selection with replacement (:228-236)
+        own, _, prob, margin = _priority.priority_choice(adv, keys[step], width, cfg["priority_exponent"], beta)
+        idx = own if indices is None else np.asarray(indices[step], np.int64)
+        weight = (N * prob[idx]) ** (-float(beta))
+        # env-major minibatch, normalised then weighted advantages (:238-253)
+        scaled = em(adv, idx)
+        if cfg.get("normalize_advantage", True):
+            scaled = (scaled - scaled.mean()) / (scaled.std() + 1e-8)
+        scaled = weight[:, None] * scaled
+        loss, lg, grads, new_ratio = recurrent_loss_and_grad(
+            params, plan, cfg, em(tr["obs"], idx), em(tr["first_done"], idx),
+            np.asarray(tr["carry0"])[idx], em(tr["action"], idx), em(tr["log_prob"], idx),
+            em(tr["value"], idx), scaled, em(ret, idx), return_ratio=True)
+        params, opt_state, gnorm = optimizer_update(grads, opt_state, params, opt)
+        lg["loss"] = loss
+        lg["grad_norm"] = gnorm
+        lg["actor/priority_weight"] = weight.mean()
+        lg["actor/priority_beta"] = float(beta)
+        info["logs"].append(lg)
+        ratio[idx] = new_ratio                         # :297, stop_gradient
+        for k, v in (("indices", idx), ("weights", weight), ("own_indices", own), ("margins", margin),
+                     ("probabilities", prob)):
+            info[k].append(v)
+        if record is not None:
+            record(step, idx, grads, params)
+    info["advantages"], info["returns"], info["ratio"] = (adv, ret, ratio) if steps else (None, None, ratio)
+    return params, opt_state, info
