@@ -668,7 +668,10 @@ def measure_update(args, config: int, dev, headline: bool) -> dict:
     params = recipe.network.init(recipe.seed, recipe.obs_dim)["params"]
     alg = algorithm_of(recipe, not args.no_graph)
     state = alg.init_from_params({"params": params}, recipe.obs_dim)
-    tr = synthetic.device_rollout(recipe, params, dev, recipe.seed)
+    # the rollout is written once into the learner's own input buffers (as an
+    # Anakin rollout would be), so the timed updates read it in place
+    tr = alg.rollout_buffers(state, recipe.T, recipe.N, recipe.obs_dim,
+                             fill_from=synthetic.device_rollout(recipe, params, dev, recipe.seed))
     torch.cuda.synchronize()
     log("rollout ready")
     for w in range(args.warmup):

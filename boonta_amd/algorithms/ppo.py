@@ -56,16 +56,17 @@ class PPOState:
         return dataclasses.replace(self, **kw)
 
 
-# flat device storage behind each state's parameter tree, keyed by buffer address
-_FLAT: dict[int, FlatState] = {}
-
-
 def flat_state_of(state) -> FlatState:
+    """The flat device storage behind a state's parameter tree: every leaf is
+    a view of the flat parameter buffer, which carries its FlatState (so the
+    storage, its compiled updates and their graphs live as long as the state's
+    parameters do)."""
     leaf = _first_leaf(state.params)
-    key = leaf.untyped_storage().data_ptr()
-    if key not in _FLAT:
+    base = leaf._base if isinstance(leaf, torch.Tensor) and leaf._base is not None else leaf
+    flat = getattr(base, "_flat_state", None)
+    if flat is None:
         raise ValueError("this state was not created by PPO.init of this package")
-    return _FLAT[key]
+    return flat
 
 
 def _first_leaf(tree):
@@ -91,9 +92,6 @@ class PPO:
             raise NotImplementedError("only the built-in GAE estimator is compiled into the learner")
         self.chain = as_chain(self.optimizer)
         self._programs: dict = {}
-        self._executors: dict = {}
-        self._graphs: dict = {}
-        self._steppers: dict = {}
 
     # ------------------------------------------------------------------ init
     def program(self, obs_dim: int) -> Program:
@@ -117,7 +115,7 @@ class PPO:
         return self._state(flat)
 
     def _state(self, flat: FlatState) -> PPOState:
-        _FLAT[flat.P.untyped_storage().data_ptr()] = flat
+        flat.P._flat_state = flat
         lay = flat.program.layout
         opt_state = (EmptyState(), (ScaleByAdamState(count=flat.count[0], mu=tree_from_flat(lay, flat.MU),
                                                      nu=tree_from_flat(lay, flat.NU)), EmptyState()))
@@ -129,10 +127,10 @@ class PPO:
 
     def step_executor(self, state, rows: int, obs_dim: int):
         flat = flat_state_of(state)
-        k = (id(flat), rows, obs_dim)
-        if k not in self._steppers:
-            self._steppers[k] = self.step_class(self.program(obs_dim), flat, rows)
-        return self._steppers[k]
+        k = (self.step_class, rows, obs_dim)
+        if k not in flat.steppers:
+            flat.steppers[k] = self.step_class(self.program(obs_dim), flat, rows)
+        return flat.steppers[k]
 
     @staticmethod
     def _set_key(ex, key):
@@ -202,29 +200,71 @@ class PPO:
         }
         return inp, tuple(sorted(inp.items()))
 
+    def _stage(self, transitions, own: dict) -> list:
+        """(source, destination) pairs that copy a transition into an
+        executor's own input buffers."""
+        f, s, aux = transitions.first, transitions.second, transitions.aux
+        T = s.reward.shape[0]
+        return [(f.obs, own["obs"][:T]), (s.obs[-1], own["obs"][T]), (s.action, own["action"]),
+                (s.reward, own["reward"]), (s.terminated, own["terminated"]), (s.truncated, own["truncated"]),
+                (aux["log_prob"], own["log_prob"]), (aux["value"], own["value"])]
+
+    def _transition_of(self, own: dict):
+        """A Transition whose leaves are views of an executor's input buffers."""
+        from ..types import Timestep, Transition
+        obs = own["obs"]
+        return Transition(first=Timestep(obs=obs[:-1]),
+                          second=Timestep(obs=obs[1:], action=own["action"], reward=own["reward"],
+                                          terminated=own["terminated"], truncated=own["truncated"]),
+                          aux={"log_prob": own["log_prob"], "value": own["value"]})
+
+    def rollout_buffers(self, state, T: int, N: int, obs_dim: int, fill_from=None):
+        """The input buffers the captured update reads, as a Transition of
+        [T, N, ...] device tensors (first.obs and second.obs are views of one
+        [T + 1, N, obs] buffer).  A rollout written into them is updated with
+        no copy; any other transition is copied into them first.  ``fill_from``
+        (a transition of the same shapes) is copied in now."""
+        own = self.executor(state, T, N, obs_dim).input_buffers()
+        if fill_from is not None:
+            self._inputs(fill_from, obs_dim)
+            for src, dst in self._stage(fill_from, own):
+                dst.copy_(src)
+        return self._transition_of(own)
+
     executor_class = MLPExecutor
 
     def executor(self, state, T: int, N: int, obs_dim: int) -> MLPExecutor:
         flat = flat_state_of(state)
-        k = (id(flat), T, N, obs_dim)
-        if k not in self._executors:
-            self._executors[k] = self.executor_class(self.program(obs_dim), flat, self.cfg, self.chain, T, N)
-        return self._executors[k]
+        k = (self.executor_class, self.cfg, self.chain, T, N, obs_dim)
+        if k not in flat.executors:
+            flat.executors[k] = self.executor_class(self.program(obs_dim), flat, self.cfg, self.chain, T, N)
+        return flat.executors[k]
+
+    # Captured graphs kept per executor (one unless a launch argument such as
+    # RecurrentPuPO's importance exponent varies between updates).
+    MAX_GRAPHS = 4
 
     def update(self, state: PPOState, key, transitions) -> PPOState:
         s = transitions.second
         T, N = s.reward.shape[:2]
         obs_dim = int(transitions.first.obs.shape[-1])
-        inp, sig = self._inputs(transitions, obs_dim)
+        inp, _ = self._inputs(transitions, obs_dim)
         ex = self.executor(state, T, N, obs_dim)
         kd = torch.from_numpy(key_data(key).view(np.int32).copy())
         ex.KEY.copy_(kd, non_blocking=False)
-        ex.bind(inp)
         if not self.use_graph:
+            ex.bind(inp)
             ex.issue(torch.cuda.current_stream().cuda_stream)
             return state
-        gk = self._graph_key(ex, sig)
-        g = self._graphs.get(gk)
+        # The graph reads the executor's own input buffers: a transition held
+        # elsewhere is copied into them (leaves that already are them are not).
+        own = ex.input_buffers()
+        for src, dst in self._stage(transitions, own):
+            if src.data_ptr() != dst.data_ptr():
+                dst.copy_(src)
+        ex.bind(self._inputs(self._transition_of(own), obs_dim)[0])
+        gk = self._graph_key(ex)
+        g = ex.graphs.get(gk)
         if g is None:
             flat = ex.flat
             # An eager pass first loads every kernel; the state is then put back
@@ -241,13 +281,16 @@ class PPO:
                 with torch.cuda.graph(g, stream=side):
                     ex.issue(torch.cuda.current_stream().cuda_stream)
             torch.cuda.current_stream().wait_stream(side)
-            self._graphs[gk] = g
+            while len(ex.graphs) >= self.MAX_GRAPHS:
+                ex.graphs.pop(next(iter(ex.graphs)))
+            ex.graphs[gk] = g
         g.replay()
         return state
 
-    def _graph_key(self, ex, sig) -> tuple:
-        """What a captured update depends on beyond the executor's buffers."""
-        return (id(ex), sig)
+    def _graph_key(self, ex) -> tuple:
+        """Launch arguments a captured update depends on beyond the executor's
+        buffers (none for PPO)."""
+        return ()
 
     def logs(self, state, T: int, N: int, obs_dim: int) -> dict:
         """The logged scalars of every minibatch step of the last update

@@ -79,6 +79,17 @@ class RecurrentPPO(PPO):
                  value.data_ptr())
         return state, new_carry, action, {"log_prob": log_prob, "value": value}
 
+    def _stage(self, transitions, own: dict) -> list:
+        f, carry = transitions.first, transitions.carry
+        return super()._stage(transitions, own) + [
+            (f.terminated, own["first_terminated"]), (f.truncated, own["first_truncated"]),
+            (carry[0], own["carry"][0]), (carry[-1], own["carry"][-1])]
+
+    def _transition_of(self, own: dict):
+        tr = super()._transition_of(own)
+        first = tr.first.replace(terminated=own["first_terminated"], truncated=own["first_truncated"])
+        return tr.replace(first=first, carry=own["carry"])
+
     def _inputs(self, transitions, obs_dim: int) -> tuple[dict, tuple]:
         inp, _ = super()._inputs(transitions, obs_dim)
         f, s = transitions.first, transitions.second

@@ -63,9 +63,9 @@ class RecurrentPuPO(RecurrentPPO):
         ex.beta = self._beta(state)
         return super().update(state, key, transitions)
 
-    def _graph_key(self, ex, sig) -> tuple:
+    def _graph_key(self, ex) -> tuple:
         # beta is a launch argument of every captured env draw
-        return (id(ex), sig, ex.beta)
+        return (ex.beta,)
 
     def logs(self, state, T: int, N: int, obs_dim: int) -> dict:
         """RecurrentPPO's logged scalars plus actor/priority_weight (the mean

@@ -250,6 +250,10 @@ class FlatState:
         self.MU = torch.zeros(n, dtype=torch.float32, device=device)
         self.NU = torch.zeros(n, dtype=torch.float32, device=device)
         self.count = torch.zeros(1, dtype=torch.int32, device=device)
+        # the compiled updates and rollout steps of this state (they live and
+        # die with it)
+        self.executors: dict = {}
+        self.steppers: dict = {}
 
     def view(self, region: Region, col: int = 0) -> int:
         return self.P.data_ptr() + 4 * (region.offset + col)
@@ -729,6 +733,30 @@ class MLPExecutor(ForwardChain):
     def bind(self, inputs: dict):
         """Pointers of the transition leaves (device tensors, time-major)."""
         self.inp = inputs
+
+    def input_buffers(self) -> dict:
+        """The executor's own rollout buffers (allocated on first use), which
+        its captured update graphs read: obs [T + 1, N, obs] (first.obs =
+        obs[:-1], second.obs = obs[1:]), action, reward, terminated,
+        truncated, log_prob and value [T, N, ...]."""
+        if getattr(self, "_own", None) is None:
+            T, N, dev = self.T, self.N, self.flat.device
+            f32 = dict(dtype=torch.float32, device=dev)
+            b8 = dict(dtype=torch.bool, device=dev)
+            dist = self.prog.dist
+            own = {"obs": torch.zeros(T + 1, N, self.obs_dim, **f32),
+                   "action": (torch.zeros(T, N, dtype=torch.int32, device=dev) if dist["kind"] == "categorical"
+                              else torch.zeros(T, N, dist["dim"], **f32)),
+                   "reward": torch.zeros(T, N, **f32), "terminated": torch.zeros(T, N, **b8),
+                   "truncated": torch.zeros(T, N, **b8), "log_prob": torch.zeros(T, N, **f32),
+                   "value": torch.zeros(T, N, **f32)}
+            own.update(self._extra_input_buffers())
+            self._own = own
+            self.graphs: dict = {}
+        return self._own
+
+    def _extra_input_buffers(self) -> dict:
+        return {}
 
     def issue(self, st: int, max_steps: int | None = None):
         """Enqueues one whole PPO.update on stream handle ``st``.  ``max_steps``

@@ -76,6 +76,14 @@ class RecurrentExecutor(MLPExecutor):
         self.XIB = torch.zeros(n2, 3 * H, **f32)
         self.HB = torch.zeros(n2, H, **f32)
 
+    def _extra_input_buffers(self) -> dict:
+        """first.terminated / first.truncated [T, N] and the carry sequence
+        [T, N, H] (only carry[0] and carry[-1] are read)."""
+        T, N, dev = self.T, self.N, self.flat.device
+        return {"first_terminated": torch.zeros(T, N, dtype=torch.bool, device=dev),
+                "first_truncated": torch.zeros(T, N, dtype=torch.bool, device=dev),
+                "carry": torch.zeros(T, N, self.prog.gru.H, dtype=torch.float32, device=dev)}
+
     def _extra_segments(self, G: int) -> list:
         g = self.prog.gru
         H, I = g.H, g.fin

@@ -109,3 +109,35 @@ def test_graph_replay_equals_eager_and_is_deterministic(name):
         results.append(flat_state_of(state).P.cpu().numpy().copy())
     np.testing.assert_array_equal(results[0], results[1])
     np.testing.assert_array_equal(results[1], results[2])
+
+
+@pytest.mark.parametrize("recurrent", [False, True])
+def test_fresh_rollout_buffers_reuse_one_graph_and_equal_eager(recurrent):
+    """A caller that hands in a different rollout buffer every update (two
+    buffers alternating, then one written into rollout_buffers): the graph
+    path copies each into the executor's own buffers and replays the one
+    graph it captured, bit-identical to the eager path on the same sequence."""
+    from ppo_cases import device_recurrent_transition, gpu_recurrent_algorithm, make_recurrent_case
+    if recurrent:
+        cases = [make_recurrent_case(4, T=8, N=64, M=4, E=2, seed=s) for s in (0, 1)]
+        r, params = cases[0][0], cases[0][2]
+        rollouts = [device_recurrent_transition(c[3], c[4], c[5]) for c in cases]
+        make_alg = lambda g: gpu_recurrent_algorithm(r, use_graph=g)
+    else:
+        cases = [make_case(config=2, T=16, N=64, M=4, E=2, seed=s) for s in (0, 1)]
+        r, params = cases[0][0], cases[0][2]
+        rollouts = [device_transition(c[3], c[4]) for c in cases]
+        make_alg = lambda g: gpu_algorithm(r, use_graph=g)
+    results = []
+    for use_graph in (False, True):
+        alg = make_alg(use_graph)
+        state = alg.init_from_params({"params": params}, r.obs_dim)
+        for k, tr in enumerate([rollouts[0], rollouts[1], rollouts[0], rollouts[1]]):
+            alg.update(state, make_key(10 + k), tr)
+        own = alg.rollout_buffers(state, r.T, r.N, r.obs_dim, fill_from=rollouts[0])
+        alg.update(state, make_key(20), own)
+        torch.cuda.synchronize()
+        results.append(flat_state_of(state).P.cpu().numpy().copy())
+        if use_graph:
+            assert len(alg.executor(state, r.T, r.N, r.obs_dim).graphs) == 1
+    np.testing.assert_array_equal(results[0], results[1])
