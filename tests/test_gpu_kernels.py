@@ -460,6 +460,10 @@ def test_sumsq_total_fixed_order(n):
     (False, "categorical", 6, 256, 4099, "none"),     # ragged last tile
     (True, "gaussian", 8, 512, 300, "silu"),          # widest features, 8 blocks per wave
     (False, "categorical", 6, 256, 20000, "relu"),    # above 16384 rows: the 64-row tile kernel
+    (False, "categorical", 6, 256, 32768, "tanh"),    # the discrete Anakin minibatch
+    (False, "categorical", 15, 256, 16400, "silu"),   # 16 outputs, activation input read separately
+    (False, "gaussian", 8, 256, 18000, "relu"),       # shared Gaussian head with a state-independent scale
+    (False, "categorical", 6, 128, 16500, "relu"),    # 64-row tiles on 128 features
     (True, "gaussian", 4, 128, 16390, "tanh"),        # ragged 64-row tiles, separate towers
     (True, "gaussian", 8, 256, 17000, "silu"),        # 64-row tiles, activation input read separately
 ])
