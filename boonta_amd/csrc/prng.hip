@@ -17,10 +17,11 @@
 //   2. scan: bucket bases and per-(bucket, tile) offsets;
 //   3. scatter: every element, with its position, into its bucket (order
 //      inside a bucket does not matter);
-//   4. sort: one workgroup per bucket sorts (key, position) pairs in LDS with a
-//      bitonic network and writes the values in order.
+//   4. sort: one workgroup per bucket splits its unique (key, position) pairs
+//      in LDS by the next 8 key bits, ranks each pair within its sub-bucket by
+//      counting the smaller ones, and writes each value at its rank.
 // A bucket larger than the LDS capacity (not reachable for Threefry keys at
-// these sizes, but handled) is ranked by counting instead, which is exact.
+// these sizes, but handled) is ranked from global memory instead.
 #include "common.h"
 #include "threefry.h"
 
@@ -34,8 +35,8 @@ namespace {
 using ppo::threefry2x32;
 
 constexpr int TILE = 4096;          // elements per histogram / scatter block
-constexpr int TILE_THREADS = 256;
-constexpr int BUCKET_CAP = 4096;    // elements a bucket sorts in LDS
+constexpr int TILE_THREADS = 1024;
+constexpr int SORT_CAP = 2048;      // elements a bucket sorts in LDS
 constexpr int SORT_THREADS = 512;
 constexpr int MAX_BUCKET_BITS = 12;
 
@@ -82,11 +83,9 @@ struct ShuffleArgs {
   int round;
   int32_t* out;         // [E][n]: values in, values out
   uint32_t* keys;       // [E][n]
-  uint32_t* hist;       // [E][nb][tiles]
+  uint32_t* hist;       // [E][tiles][nb]
   uint32_t* bstart;     // [E][nb + 1]
-  uint32_t* tkey;       // [E][n] bucketed keys
-  uint32_t* tpos;       // [E][n] bucketed positions
-  int32_t* tval;        // [E][n] bucketed values
+  uint4* trec;          // [E][n] bucketed records: key, position, value (one 16-byte store each)
 };
 
 __device__ __forceinline__ uint32_t bucket_of(uint32_t k, int bbits) {
@@ -115,15 +114,18 @@ __global__ void __launch_bounds__(TILE_THREADS) shuffle_bits_kernel(ShuffleArgs 
   }
   __syncthreads();
   uint32_t* hist = a.hist + (int64_t)e * a.nb * a.tiles;
-  for (int d = threadIdx.x; d < a.nb; d += TILE_THREADS) hist[(int64_t)d * a.tiles + blockIdx.x] = cnt[d];
+  for (int d = threadIdx.x; d < a.nb; d += TILE_THREADS) hist[(int64_t)blockIdx.x * a.nb + d] = cnt[d];
 }
 
 // One workgroup per epoch: bucket totals, their exclusive scan (bucket
-// starts), and each (bucket, tile) count rewritten as its write offset.  The
-// scan over the nb <= 4096 totals is a block scan: thread t owns buckets
-// 4t .. 4t + 3, wave-level inclusive scans of the per-thread sums, then the
-// 16 wave totals.
+// starts), and each (tile, bucket) count rewritten as its write offset.  The
+// counts are stored tile-major ([tiles][nb]), so the threads of a wave, one
+// bucket each, read consecutive words at every tile, eight tiles' loads in
+// flight at a time.  The scan over the nb <= 4096 totals is a block scan:
+// thread t owns buckets 4t .. 4t + 3, wave-level inclusive scans of the
+// per-thread sums, then the 16 wave totals.
 constexpr int SCAN_THREADS = 1024;
+constexpr int SCAN_BATCH = 8;
 
 __global__ void __launch_bounds__(SCAN_THREADS) shuffle_scan_kernel(ShuffleArgs a) {
   extern __shared__ uint32_t tot[];  // [nb]
@@ -131,9 +133,18 @@ __global__ void __launch_bounds__(SCAN_THREADS) shuffle_scan_kernel(ShuffleArgs 
   const int e = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   uint32_t* hist = a.hist + (int64_t)e * a.nb * a.tiles;
+  const int64_t nb = a.nb;
   for (int d = threadIdx.x; d < a.nb; d += SCAN_THREADS) {
     uint32_t s = 0;
-    for (int t = 0; t < a.tiles; ++t) s += hist[(int64_t)d * a.tiles + t];
+    int t = 0;
+    for (; t + SCAN_BATCH <= a.tiles; t += SCAN_BATCH) {
+      uint32_t c[SCAN_BATCH];
+#pragma unroll
+      for (int i = 0; i < SCAN_BATCH; ++i) c[i] = hist[(t + i) * nb + d];
+#pragma unroll
+      for (int i = 0; i < SCAN_BATCH; ++i) s += c[i];
+    }
+    for (; t < a.tiles; ++t) s += hist[t * nb + d];
     tot[d] = s;
   }
   __syncthreads();
@@ -167,9 +178,20 @@ __global__ void __launch_bounds__(SCAN_THREADS) shuffle_scan_kernel(ShuffleArgs 
   for (int d = threadIdx.x; d < a.nb; d += SCAN_THREADS) {
     bstart[d] = tot[d];
     uint32_t r = tot[d];
-    for (int t = 0; t < a.tiles; ++t) {
-      const uint32_t c = hist[(int64_t)d * a.tiles + t];
-      hist[(int64_t)d * a.tiles + t] = r;
+    int t = 0;
+    for (; t + SCAN_BATCH <= a.tiles; t += SCAN_BATCH) {
+      uint32_t c[SCAN_BATCH];
+#pragma unroll
+      for (int i = 0; i < SCAN_BATCH; ++i) c[i] = hist[(t + i) * nb + d];
+#pragma unroll
+      for (int i = 0; i < SCAN_BATCH; ++i) {
+        hist[(t + i) * nb + d] = r;
+        r += c[i];
+      }
+    }
+    for (; t < a.tiles; ++t) {
+      const uint32_t c = hist[t * nb + d];
+      hist[t * nb + d] = r;
       r += c;
     }
   }
@@ -180,26 +202,47 @@ __global__ void __launch_bounds__(TILE_THREADS) shuffle_scatter_kernel(ShuffleAr
   extern __shared__ uint32_t slot[];  // [nb]
   const int e = blockIdx.y;
   const uint32_t* hist = a.hist + (int64_t)e * a.nb * a.tiles;
-  for (int d = threadIdx.x; d < a.nb; d += TILE_THREADS) slot[d] = hist[(int64_t)d * a.tiles + blockIdx.x];
+  for (int d = threadIdx.x; d < a.nb; d += TILE_THREADS) slot[d] = hist[(int64_t)blockIdx.x * a.nb + d];
   __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * TILE;
   const uint32_t* keys = a.keys + (int64_t)e * a.n;
   const int32_t* vals = a.out + (int64_t)e * a.n;
   const int64_t eo = (int64_t)e * a.n;
-  for (int it = 0; it < TILE / TILE_THREADS; ++it) {
+  // every load of the thread's elements first, then the slots and stores
+  constexpr int PER = TILE / TILE_THREADS;
+  uint32_t k[PER];
+  int32_t v[PER];
+#pragma unroll
+  for (int it = 0; it < PER; ++it) {
+    const int64_t i = base + (int64_t)it * TILE_THREADS + threadIdx.x;
+    k[it] = i < a.n ? keys[i] : 0u;
+    v[it] = i < a.n ? vals[i] : 0;
+  }
+#pragma unroll
+  for (int it = 0; it < PER; ++it) {
     const int64_t i = base + (int64_t)it * TILE_THREADS + threadIdx.x;
     if (i >= a.n) break;
-    const uint32_t k = keys[i];
-    const uint32_t pos = atomicAdd(&slot[bucket_of(k, a.bbits)], 1u);
-    a.tkey[eo + pos] = k;
-    a.tpos[eo + pos] = (uint32_t)i;
-    a.tval[eo + pos] = vals[i];
+    const uint32_t pos = atomicAdd(&slot[bucket_of(k[it], a.bbits)], 1u);
+    a.trec[eo + pos] = make_uint4(k[it], (uint32_t)i, (uint32_t)v[it], 0u);
   }
 }
 
+// One workgroup per bucket.  Its (key, position) pairs are split in LDS by
+// the 8 key bits below the bucket's (an LDS histogram, its scan, and a
+// scatter into per-sub-bucket ranges whose order inside a range is
+// arbitrary); the pairs are unique, so each one's slot is its sub-bucket's
+// start plus the number of smaller pairs in that sub-bucket (about
+// m / 256 compares, not m).
+constexpr int SUB_BITS = 8;
+constexpr int SUB = 1 << SUB_BITS;
+constexpr int SORT_PER = SORT_CAP / SORT_THREADS;
+
 __global__ void __launch_bounds__(SORT_THREADS) shuffle_sort_kernel(ShuffleArgs a) {
-  __shared__ uint64_t sk[BUCKET_CAP];
-  __shared__ int32_t sv[BUCKET_CAP];
+  __shared__ uint64_t sk[SORT_CAP];
+  __shared__ int32_t sv[SORT_CAP];
+  __shared__ uint32_t cnt[SUB];
+  __shared__ uint32_t start[SUB + 1];
+  const int tid = threadIdx.x;
   const int e = blockIdx.y;
   const int b = blockIdx.x;
   const uint32_t* bstart = a.bstart + (int64_t)e * (a.nb + 1);
@@ -208,50 +251,79 @@ __global__ void __launch_bounds__(SORT_THREADS) shuffle_sort_kernel(ShuffleArgs 
   const int64_t eo = (int64_t)e * a.n;
   int32_t* out = a.out + eo;
   if (m <= 0) return;
-  if (m <= BUCKET_CAP) {
-    int p2 = 1;
-    while (p2 < m) p2 <<= 1;
-    for (int i = threadIdx.x; i < p2; i += SORT_THREADS) {
-      if (i < m) {
-        sk[i] = ((uint64_t)a.tkey[eo + s + i] << 32) | (uint64_t)a.tpos[eo + s + i];
-        sv[i] = a.tval[eo + s + i];
-      } else {
-        sk[i] = ~0ull;
-        sv[i] = 0;
+  if (m <= SORT_CAP) {
+    const int shift = 32 - a.bbits - SUB_BITS;
+    for (int d = tid; d < SUB; d += SORT_THREADS) cnt[d] = 0;
+    __syncthreads();
+    uint64_t kk[SORT_PER];
+    int32_t vv[SORT_PER];
+#pragma unroll
+    for (int q = 0; q < SORT_PER; ++q) {
+      const int i = tid + q * SORT_THREADS;
+      const int ic = i < m ? i : m - 1;
+      const uint4 rec = a.trec[eo + s + ic];
+      kk[q] = ((uint64_t)rec.x << 32) | (uint64_t)rec.y;
+      vv[q] = (int32_t)rec.z;
+    }
+#pragma unroll
+    for (int q = 0; q < SORT_PER; ++q)
+      if (tid + q * SORT_THREADS < m) atomicAdd(&cnt[(uint32_t)(kk[q] >> (32 + shift)) & (SUB - 1)], 1u);
+    __syncthreads();
+    // exclusive scan of the SUB counts by the first wave (SUB / 64 per lane)
+    if (tid < 64) {
+      constexpr int PL = SUB / 64;
+      uint32_t c[PL], local = 0;
+#pragma unroll
+      for (int i = 0; i < PL; ++i) {
+        c[i] = cnt[PL * tid + i];
+        local += c[i];
+      }
+      uint32_t inc = local;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(inc, o, 64);
+        if (tid >= o) inc += y;
+      }
+      uint32_t run = inc - local;
+#pragma unroll
+      for (int i = 0; i < PL; ++i) {
+        start[PL * tid + i] = run;
+        run += c[i];
+      }
+      if (tid == 63) start[SUB] = inc;
+    }
+    __syncthreads();
+    for (int d = tid; d < SUB; d += SORT_THREADS) cnt[d] = start[d];  // cursors
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < SORT_PER; ++q) {
+      if (tid + q * SORT_THREADS < m) {
+        const uint32_t p = atomicAdd(&cnt[(uint32_t)(kk[q] >> (32 + shift)) & (SUB - 1)], 1u);
+        sk[p] = kk[q];
+        sv[p] = vv[q];
       }
     }
     __syncthreads();
-    // bitonic sort of p2 unique-or-sentinel keys, ascending
-    for (int k = 2; k <= p2; k <<= 1) {
-      for (int j = k >> 1; j > 0; j >>= 1) {
-        for (int i = threadIdx.x; i < p2; i += SORT_THREADS) {
-          const int l = i ^ j;
-          if (l > i) {
-            const bool up = (i & k) == 0;
-            const uint64_t x = sk[i], y = sk[l];
-            if ((x > y) == up) {
-              sk[i] = y;
-              sk[l] = x;
-              const int32_t tv = sv[i];
-              sv[i] = sv[l];
-              sv[l] = tv;
-            }
-          }
-        }
-        __syncthreads();
-      }
+    for (int i = tid; i < m; i += SORT_THREADS) {
+      const uint64_t ki = sk[i];
+      const uint32_t d = (uint32_t)(ki >> (32 + shift)) & (SUB - 1);
+      const int j1 = (int)start[d + 1];
+      int rank = (int)start[d];
+      for (int j = (int)start[d]; j < j1; ++j) rank += sk[j] < ki;
+      out[s + rank] = sv[i];
     }
-    for (int i = threadIdx.x; i < m; i += SORT_THREADS) out[s + i] = sv[i];
   } else {
-    // rank by counting: exact for any size, quadratic
-    for (int i = threadIdx.x; i < m; i += SORT_THREADS) {
-      const uint64_t ki = ((uint64_t)a.tkey[eo + s + i] << 32) | (uint64_t)a.tpos[eo + s + i];
+    // rank by counting from global memory: exact for any size
+    for (int i = tid; i < m; i += SORT_THREADS) {
+      const uint4 ri = a.trec[eo + s + i];
+      const uint64_t ki = ((uint64_t)ri.x << 32) | (uint64_t)ri.y;
       int rank = 0;
       for (int j = 0; j < m; ++j) {
-        const uint64_t kj = ((uint64_t)a.tkey[eo + s + j] << 32) | (uint64_t)a.tpos[eo + s + j];
+        const uint4 rj = a.trec[eo + s + j];
+        const uint64_t kj = ((uint64_t)rj.x << 32) | (uint64_t)rj.y;
         rank += kj < ki ? 1 : 0;
       }
-      out[s + rank] = a.tval[eo + s + i];
+      out[s + rank] = (int32_t)ri.z;
     }
   }
 }
@@ -262,7 +334,7 @@ int shuffle_rounds(int64_t n) {
 }
 
 int bucket_bits(int64_t n) {
-  if (n <= BUCKET_CAP) return 0;
+  if (n <= SORT_CAP) return 0;
   int b = 0;
   while (b < MAX_BUCKET_BITS && (n >> b) > 512) ++b;
   return b;
@@ -271,8 +343,8 @@ int bucket_bits(int64_t n) {
 size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
 
 struct Space {
-  uint32_t *keys, *hist, *bstart, *tkey, *tpos;
-  int32_t* tval;
+  uint32_t *keys, *hist, *bstart;
+  uint4* trec;
 };
 
 size_t space_bytes(int epochs, int64_t n) {
@@ -280,8 +352,8 @@ size_t space_bytes(int epochs, int64_t n) {
   const int64_t nn = n > 0 ? n : 1;
   const int64_t tiles = ppo::ceil_div64(nn, TILE);
   const int64_t nb = int64_t(1) << bucket_bits(nn);
-  return 4 * align256(sizeof(uint32_t) * E * nn) + align256(sizeof(uint32_t) * E * nb * tiles) +
-         align256(sizeof(uint32_t) * E * (nb + 1));
+  return align256(sizeof(uint32_t) * E * nn) + align256(sizeof(uint4) * E * nn) +
+         align256(sizeof(uint32_t) * E * nb * tiles) + align256(sizeof(uint32_t) * E * (nb + 1));
 }
 
 Space carve(void* ws, int epochs, int64_t n) {
@@ -291,9 +363,7 @@ Space carve(void* ws, int epochs, int64_t n) {
   char* p = (char*)ws;
   Space s;
   s.keys = (uint32_t*)p; p += align256(sizeof(uint32_t) * E * n);
-  s.tkey = (uint32_t*)p; p += align256(sizeof(uint32_t) * E * n);
-  s.tpos = (uint32_t*)p; p += align256(sizeof(uint32_t) * E * n);
-  s.tval = (int32_t*)p; p += align256(sizeof(uint32_t) * E * n);
+  s.trec = (uint4*)p; p += align256(sizeof(uint4) * E * n);
   s.hist = (uint32_t*)p; p += align256(sizeof(uint32_t) * E * nb * tiles);
   s.bstart = (uint32_t*)p;
   return s;
@@ -324,7 +394,7 @@ int shuffle_impl(hipStream_t st, const uint32_t* key, int split_epochs, int epoc
   a.bbits = bucket_bits(n);
   a.nb = 1 << a.bbits;
   a.out = out; a.keys = sp.keys; a.hist = sp.hist; a.bstart = sp.bstart;
-  a.tkey = sp.tkey; a.tpos = sp.tpos; a.tval = sp.tval;
+  a.trec = sp.trec;
   const size_t shm = sizeof(uint32_t) * a.nb;
   for (int r = 0; r < rounds; ++r) {
     a.round = r;
@@ -344,7 +414,7 @@ int shuffle_impl(hipStream_t st, const uint32_t* key, int split_epochs, int epoc
 // runs on holds its own copy until the process ends.  Host code never passes
 // the symbol itself to a kernel: the device address is resolved per device
 // with hipGetSymbolAddress and kept in `g_scratch`.
-static constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(24) << 20;  // 4 epochs x 262144 items need 16.5 MB
+static constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(24) << 20;  // 4 epochs x 262144 items need 20.5 MiB
 static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
 
 static constexpr int MAX_DEVICES = 64;

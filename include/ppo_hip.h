@@ -107,7 +107,7 @@ int ppo_epoch_permutations(void* stream, const uint32_t* key, int epochs, int64_
  * forbid hipMalloc): the same results, with the workspace in the library's own
  * 24 MiB device scratch (one per GPU, held until the process ends) instead of
  * an argument.  Returns PPO_ERR_SPACE when ppo_epoch_permutations_workspace
- * (epochs, n) exceeds 24 MiB (4 epochs of 262144 items need 16.5 MB), and
+ * (epochs, n) exceeds 24 MiB (4 epochs of 262144 items need 20.5 MiB), and
  * PPO_ERR_ARG when the stream's device is not the current device.  Calls that
  * overlap on one GPU share the scratch and race: order them on one stream. */
 int ppo_epoch_permutations_noalloc(void* stream, const uint32_t* key, int epochs, int64_t n, int32_t* out);
