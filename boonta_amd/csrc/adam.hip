@@ -118,10 +118,19 @@ struct AdamParams {
 __global__ void __launch_bounds__(256) adam_kernel(AdamParams a) {
   __shared__ float s_scale_norm[2];
   __shared__ float s_bc[2];
-  if (threadIdx.x < 64) {
+  __shared__ double s_w[4];
+  // the squared norm from its partials, in a fixed order every block repeats:
+  // thread t adds partials t, t + 256, ..., then wave sums, then the four
+  // wave totals in wave order
+  {
     double t = 0.0;
-    for (int i = threadIdx.x; i < a.nsumsq; i += 64) t += a.sumsq[i];
+    for (int i = threadIdx.x; i < a.nsumsq; i += 256) t += a.sumsq[i];
     t = ppo::wave_sum_d(t);
+    if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = t;
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const double t = (s_w[0] + s_w[1]) + (s_w[2] + s_w[3]);
     if (threadIdx.x == 0) {
       const float norm = (float)sqrt(t);
       s_scale_norm[0] = norm;

@@ -808,9 +808,10 @@ class MLPExecutor(ForwardChain):
         self._finish_logs(st, self.E * self.M)
         self._call("ppo_count_advance", st, _p(self.flat.count), self.E * self.M)
 
-    # Up to this many norm partials every Adam block folds itself; above it one
-    # block folds them first (a launch of its own).
-    FOLD_NORM_MAX = 1024
+    # Up to this many norm partials every Adam block folds itself (all 256
+    # threads, about 16 loads each at most); above it one block folds them
+    # first (a launch of its own).
+    FOLD_NORM_MAX = 4096
 
     def _optimizer_step(self, st, step):
         """Gradient assembly (fixed-order sum of the split partials, with the
