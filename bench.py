@@ -86,10 +86,27 @@ def measured_traffic(workload, kernel):
     return 1024.0 * (rec["fetch_kib"] * rec["fetch_scale"] + rec["write_kib"] * rec["write_scale"])
 
 
+def untower(name, args):
+    """(entry point, arguments, towers) of a tower-batched launch as its
+    single-tower entry point's call, and the number of towers it runs."""
+    if not name.endswith("_towers"):
+        return name, args, 1
+    from boonta_amd import _lib
+    base = name[: -len("_towers")]
+    n = len(_lib.SIGNATURES[base][1])
+    return base, (args[0],) + tuple(args[2:n + 1]), int(args[1])
+
+
 def launch_work(name, args):
     """(flops, bytes) of one launch: algorithmic work of the call's shapes
     (GEMM: 2MNK FLOP; bandwidth-bound kernels: the bytes the computation must
-    read and write once)."""
+    read and write once); a tower-batched launch does its towers' work."""
+    name, args, towers = untower(name, args)
+    flops, nbytes = _single_launch_work(name, args)
+    return towers * flops, towers * nbytes
+
+
+def _single_launch_work(name, args):
     if name in ("ppo_gemm_f32", "ppo_gemm_bf16"):
         M, N, K = args[10], args[11], args[12]
         return 2.0 * M * N * K, 4.0 * (M * K + K * N + M * N)
@@ -149,7 +166,14 @@ def launch_work(name, args):
 
 def launch_shape(name, args):
     """[M, N, K] of a contraction launch (the one-launch step: [rows, 256,
-    observation features, trunk layers]; None for the others)."""
+    observation features, trunk layers]; None for the others), with the
+    tower count appended for a tower-batched launch."""
+    base, bargs, towers = untower(name, args)
+    shape = _single_launch_shape(base, bargs)
+    return shape + [towers] if shape is not None and towers > 1 else shape
+
+
+def _single_launch_shape(name, args):
     if name in ("ppo_gemm_f32", "ppo_gemm_bf16"):
         return list(args[10:13])
     if name == "ppo_gemm_bf16s":
@@ -164,6 +188,7 @@ def launch_shape(name, args):
 
 
 def launch_layout(name, args):
+    name, args, _ = untower(name, args)
     if name in ("ppo_gemm_f32", "ppo_gemm_bf16", "ppo_gemm_bf16s"):
         return [args[1], args[2]]
     return None
@@ -171,6 +196,9 @@ def launch_layout(name, args):
 
 def launch_key(name, args):
     """Launches with the same entry point and shape do the same work."""
+    base, bargs, towers = untower(name, args)
+    if towers > 1 and base == "ppo_gemm_f32":
+        return (towers,) + launch_key(base, bargs)
     if name in ("ppo_gemm_f32", "ppo_gemm_bf16"):
         return (name, args[1], args[2]) + tuple(args[10:16])
     if name == "ppo_gemm_bf16s":

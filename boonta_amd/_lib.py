@@ -50,11 +50,15 @@ SIGNATURES = {
     "ppo_priority_choice_max_envs": (I, []),
     "ppo_priority_choice_f32": (I, [P, P, I64, I, I, F, F, P, I, P, P, P]),
     "ppo_gemm_ln_act_fwd_f32": (I, [P, P, I64, P, P, I64, P, P, P, P, I64, P, I64, P, P, I, I, I, F, I]),
+    "ppo_gemm_ln_act_fwd_f32_towers": (I, [P, I, P, I64, P, P, I64, P, P, P, P, I64, P, I64, P, P, I, I, I, F, I,
+                                           I64, I64, I64, I64]),
     "ppo_linear_scan_fwd": (I, [P, I, P, P, P, P, I, I, I]),
     "ppo_linear_scan_bwd": (I, [P, I, P, P, P, P, P, P, P, I, I, I]),
     "ppo_ssm_scan_fwd": (I, [P, I, P, P, P, P, P, P, I, I, I]),
     "ppo_ssm_scan_bwd": (I, [P, I, P, P, P, P, P, P, P, P, P, I, I, I]),
     "ppo_gemm_f32": (I, [P, I, I, P, I64, P, P, I64, P, I64, I, I, I, I, I64, I, P, I, P, P, I64, P, I]),
+    "ppo_gemm_f32_towers": (I, [P, I, I, I, P, I64, P, P, I64, P, I64, I, I, I, I, I64, I, P, I, P, P, I64, P, I,
+                                I64, I64, I64, I64, I64, I64, I64]),
     "ppo_gemm_bf16": (I, [P, I, I, P, I64, P, P, I64, P, I64, I, I, I, I, I64, I, P, I, I, P, I64, P, I]),
     "ppo_round_bf16": (I, [P, P, I64]),
     "ppo_gemm_bf16s": (I, [P, I, I, I, I, P, I64, P, P, I64, P, I64, I, I, I, I, I64, I, P, I, I, P, I64, P, I]),
@@ -68,6 +72,8 @@ SIGNATURES = {
     "ppo_layernorm_act_bwd_bf16_out16": (I, [P, P, I64, P, I64, P, P, P, P, P, I64, P, I, I, I]),
     "ppo_layernorm_bwd_blocks": (I, [I]),
     "ppo_layernorm_act_bwd_f32": (I, [P, P, I64, P, I64, P, P, P, P, P, I64, P, I, I, I]),
+    "ppo_layernorm_act_bwd_f32_towers": (I, [P, I, P, I64, P, I64, P, P, P, P, P, I64, P, I, I, I, I64, I64, I64,
+                                             I64]),
     "ppo_act_fwd_f32": (I, [P, P, I64, P, I64, I, I, I]),
     "ppo_act_bwd_f32": (I, [P, P, I64, P, I64, P, I64, I, I, I]),
     "ppo_loss_blocks": (I, [I]),

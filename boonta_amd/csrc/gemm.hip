@@ -65,7 +65,7 @@ __device__ __forceinline__ floatx4 masked(floatx4 v, uint32_t bits) {
 }
 
 template <int BM, int BN, int BK, bool A_K, bool B_K, bool VA, bool VB>
-__global__ void __launch_bounds__(256, 2) gemm_f32_kernel(GemmParams p) {
+__global__ void __launch_bounds__(256, 2) gemm_f32_kernel(GemmParams p0) {
   constexpr int A_ROWS = A_K ? BM : BK;
   constexpr int A_COLS = A_K ? BK : BM;
   constexpr int B_ROWS = B_K ? BN : BK;
@@ -87,9 +87,11 @@ __global__ void __launch_bounds__(256, 2) gemm_f32_kernel(GemmParams p) {
   const int h = lane >> 5;
   const int l32 = lane & 31;
   const ppo::TileCoord tc = ppo::xcd_tile();
+  const int tower = tc.z / p0.splits;
+  const int split = tc.z - tower * p0.splits;
+  const GemmParams p = tower_params(p0, tower);
   const int m0 = tc.m * BM;
   const int n0 = tc.n * BN;
-  const int split = tc.z;
   const int kb = split * p.k_per_split;
   const int ke = min(p.K, kb + p.k_per_split);
 
@@ -230,7 +232,7 @@ __global__ void __launch_bounds__(256, 2) gemm_f32_kernel(GemmParams p) {
 
 template <int BM, int BN, int BK, bool A_K, bool B_K>
 int launch_tile(hipStream_t st, const GemmParams& p, int splits, bool va, bool vb) {
-  dim3 grid(ppo::ceil_div(p.N, BN), ppo::ceil_div(p.M, BM), splits);
+  dim3 grid(ppo::ceil_div(p.N, BN), ppo::ceil_div(p.M, BM), splits * p.towers);
   dim3 block(256);
   if (va && vb) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, A_K, B_K, true, true>), grid, block, 0, st, p);
   else if (va) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, A_K, B_K, true, false>), grid, block, 0, st, p);
@@ -266,13 +268,16 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 //   tile: -1 picks a tile; 0: 128x128, 1: 128x64, 2: 64x128, 3: 64x64 (copy-fed, 32 reduction
 //   elements per stage, when the operands allow; else register-staged with 16); 4-7 the same
 //   tiles register-staged with 32 per stage; 8: 128x256 and 9: 256x128 on 8 waves (copy-fed).
-PPO_EXPORT int ppo_gemm_f32(void* stream, int a_layout, int b_layout, const float* A, int64_t lda,
-                            const int32_t* rows, const float* B, int64_t ldb, float* C, int64_t ldc, int M,
-                            int N, int K, int splits, int64_t c_split_stride, int epi, const float* bias,
-                            int act, float* pre, const float* aux, int64_t ldaux, float* bias_grad, int tile) {
+static int gemm_f32_impl(void* stream, int a_layout, int b_layout, const float* A, int64_t lda,
+                         const int32_t* rows, const float* B, int64_t ldb, float* C, int64_t ldc, int M, int N,
+                         int K, int splits, int64_t c_split_stride, int epi, const float* bias, int act, float* pre,
+                         const float* aux, int64_t ldaux, float* bias_grad, int tile, int towers,
+                         const int64_t* tstride) {
   if (M < 0 || N < 0 || K < 0 || splits < 1 || a_layout < 0 || a_layout > 1 || b_layout < 0 || b_layout > 1 ||
-      epi < 0 || epi > 2 || act < 0 || act > 3 || tile > 9)
-    return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32: bad argument (M=%d N=%d K=%d splits=%d)", M, N, K, splits);
+      epi < 0 || epi > 2 || act < 0 || act > 3 || tile > 9 || towers < 1 || towers > 8 ||
+      (int64_t)splits * towers > 65535)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32: bad argument (M=%d N=%d K=%d splits=%d towers=%d)", M, N, K,
+                          splits, towers);
   if (M == 0 || N == 0) return PPO_OK;
   if (!A || !B || !C) return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32: null operand");
   if (epi == EPI_DACT && !aux) return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32: EPI_DACT needs aux");
@@ -286,6 +291,13 @@ PPO_EXPORT int ppo_gemm_f32(void* stream, int a_layout, int b_layout, const floa
   const int kps = ((ppo::ceil_div(K > 0 ? K : 1, splits) + BK_MIN - 1) / BK_MIN) * BK_MIN;
   p.k_per_split = kps;
   p.epi = epi; p.bias = bias; p.act = act; p.pre = pre; p.aux = aux; p.ldaux = ldaux; p.bias_grad = bias_grad;
+  p.splits = splits; p.towers = towers;
+  p.tA = tstride[0]; p.tB = tstride[1]; p.tC = tstride[2]; p.tBias = tstride[3]; p.tPre = tstride[4];
+  p.tAux = tstride[5]; p.tBiasGrad = tstride[6];
+  // a tower's strides keep its 16-byte rows aligned
+  for (int i = 0; i < 7; ++i)
+    if (towers > 1 && tstride[i] % 4 != 0)
+      return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32_towers: tower strides must be multiples of 4 elements");
   // vector loads need 16-byte rows along the contiguous axis
   const int a_contig = a_layout == 0 ? K : M;
   const int b_contig = b_layout == 1 ? K : N;
@@ -310,4 +322,29 @@ PPO_EXPORT int ppo_gemm_f32(void* stream, int a_layout, int b_layout, const floa
   if (a_layout == 0 && b_layout == 1) return launch_layout<true, true>(st, p, splits, va, vb, tile);
   if (a_layout == 1 && b_layout == 0) return launch_layout<false, false>(st, p, splits, va, vb, tile);
   return launch_layout<false, true>(st, p, splits, va, vb, tile);
+}
+
+PPO_EXPORT int ppo_gemm_f32(void* stream, int a_layout, int b_layout, const float* A, int64_t lda,
+                            const int32_t* rows, const float* B, int64_t ldb, float* C, int64_t ldc, int M,
+                            int N, int K, int splits, int64_t c_split_stride, int epi, const float* bias,
+                            int act, float* pre, const float* aux, int64_t ldaux, float* bias_grad, int tile) {
+  const int64_t none[7] = {0, 0, 0, 0, 0, 0, 0};
+  return gemm_f32_impl(stream, a_layout, b_layout, A, lda, rows, B, ldb, C, ldc, M, N, K, splits, c_split_stride,
+                       epi, bias, act, pre, aux, ldaux, bias_grad, tile, 1, none);
+}
+
+// ppo_gemm_f32 over `towers` problems of one shape in one grid: problem t's
+// A, B, C, bias, pre, aux and bias_grad are the given pointers plus t times
+// their stride (elements, multiples of 4; 0 shares the operand, as the
+// observation rows both towers of an actor-critic read).
+PPO_EXPORT int ppo_gemm_f32_towers(void* stream, int towers, int a_layout, int b_layout, const float* A,
+                                   int64_t lda, const int32_t* rows, const float* B, int64_t ldb, float* C,
+                                   int64_t ldc, int M, int N, int K, int splits, int64_t c_split_stride, int epi,
+                                   const float* bias, int act, float* pre, const float* aux, int64_t ldaux,
+                                   float* bias_grad, int tile, int64_t stride_a, int64_t stride_b,
+                                   int64_t stride_c, int64_t stride_bias, int64_t stride_pre, int64_t stride_aux,
+                                   int64_t stride_bias_grad) {
+  const int64_t t[7] = {stride_a, stride_b, stride_c, stride_bias, stride_pre, stride_aux, stride_bias_grad};
+  return gemm_f32_impl(stream, a_layout, b_layout, A, lda, rows, B, ldb, C, ldc, M, N, K, splits, c_split_stride,
+                       epi, bias, act, pre, aux, ldaux, bias_grad, tile, towers, t);
 }

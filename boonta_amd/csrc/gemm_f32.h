@@ -26,7 +26,27 @@ struct GemmParams {
   const float* aux;  // EPI_DACT: activation output (relu, tanh) or input (silu), ld = ldaux
   int64_t ldaux;
   float* bias_grad;  // dW: [splits][N] column sums of B, or null
+  // Tower-batched launches (the actor's and critic's same-depth layers in one
+  // grid): blockIdx z = tower * splits + split, and tower t's operands sit
+  // t * stride elements after tower 0's (rows, the gather, is shared).
+  int splits, towers;
+  int64_t tA, tB, tC, tBias, tPre, tAux, tBiasGrad;
 };
+
+// The operands of tower t of a tower-batched launch.
+__device__ __forceinline__ GemmParams tower_params(const GemmParams& p, int t) {
+  GemmParams q = p;
+  if (t) {
+    q.A += t * p.tA;
+    q.B += t * p.tB;
+    q.C += t * p.tC;
+    if (q.bias) q.bias += t * p.tBias;
+    if (q.pre) q.pre += t * p.tPre;
+    if (q.aux) q.aux += t * p.tAux;
+    if (q.bias_grad) q.bias_grad += t * p.tBiasGrad;
+  }
+  return q;
+}
 
 // Stores a wave's MB x NB blocks of 32 x 32 (v_mfma_f32_32x32x*: lane l holds
 // rows 8 (r / 4) + 4 (l / 32) + r % 4 of column l % 32) from row wm0 and column

@@ -137,7 +137,7 @@ __device__ __forceinline__ floatx4 operand(const float* lds, int rbase, int g, i
 }
 
 template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF>
-__global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_kernel(GemmParams p) {
+__global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_kernel(GemmParams p0) {
   constexpr int NW = WM * WN;
   constexpr int MB = BM / WM / 32, NB = BN / WN / 32;  // 32 x 32 blocks per wave
   static_assert(MB * WM * 32 == BM && NB * WN * 32 == BN, "tile must split into 32 x 32 blocks");
@@ -152,9 +152,11 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_kernel(GemmParams p) {
   const int wm = wave % WM;
   const int wn = wave / WM;
   const ppo::TileCoord tc = ppo::xcd_tile();
+  const int tower = tc.z / p0.splits;
+  const int split = tc.z - tower * p0.splits;
+  const GemmParams p = tower_params(p0, tower);
   const int m0 = tc.m * BM;
   const int n0 = tc.n * BN;
-  const int split = tc.z;
   const int kb = split * p.k_per_split;
   const int ke = min(p.K, kb + p.k_per_split);
 
@@ -243,7 +245,7 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_kernel(GemmParams p) {
 template <int BM, int BN, int WM, int WN, bool A_K, bool B_K>
 int launch(hipStream_t st, const GemmParams& p, int splits) {
   constexpr int NBUF = WM * WN == 4 ? 2 : 3;
-  dim3 grid(ppo::ceil_div(p.N, BN), ppo::ceil_div(p.M, BM), splits);
+  dim3 grid(ppo::ceil_div(p.N, BN), ppo::ceil_div(p.M, BM), splits * p.towers);
   hipLaunchKernelGGL((gemm_f32d_kernel<BM, BN, WM, WN, A_K, B_K, NBUF>), grid, dim3(WM * WN * 64), 0, st, p);
   return ppo::check_launch("ppo_gemm_f32");
 }

@@ -49,13 +49,34 @@ struct GemmLnArgs {
   int M, K;
   float eps;
   int act;
+  // tower-batched launches (blockIdx.y = tower): tower t's X, its parameters
+  // (W, bias, gamma, beta), its Z / Y rows and its mean / rstd sit t times
+  // these strides (elements) after tower 0's
+  int64_t tX, tP, tZY, tMR;
 };
+
+__device__ __forceinline__ GemmLnArgs tower_args(const GemmLnArgs& a, int t) {
+  GemmLnArgs q = a;
+  if (t) {
+    q.X += t * a.tX;
+    q.W += t * a.tP;
+    if (q.bias) q.bias += t * a.tP;
+    q.gamma += t * a.tP;
+    q.beta += t * a.tP;
+    q.Z += t * a.tZY;
+    q.Y += t * a.tZY;
+    q.mean += t * a.tMR;
+    q.rstd += t * a.tMR;
+  }
+  return q;
+}
 
 // Column map: block j's MFMA column li of wave w is feature 64 w + 4 li + j,
 // so each lane's four columns are adjacent and every W, bias, gamma, beta, Z
 // and Y access is one 16-byte vector.
 template <bool VA>
-__global__ void __launch_bounds__(GL_THREADS) gemm_ln_fwd_kernel(GemmLnArgs p) {
+__global__ void __launch_bounds__(GL_THREADS) gemm_ln_fwd_kernel(GemmLnArgs p0) {
+  const GemmLnArgs p = tower_args(p0, blockIdx.y);
   __shared__ float s_sum[4][GL_ROWS];
   __shared__ float s_sq[4][GL_ROWS];
   const int lane = threadIdx.x & 63;
@@ -175,11 +196,12 @@ bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 
 
 }  // namespace
 
-PPO_EXPORT int ppo_gemm_ln_act_fwd_f32(void* stream, const float* X, int64_t ldx, const int32_t* rows_idx,
-                                      const float* W, int64_t ldw, const float* bias, const float* gamma,
-                                      const float* beta, float* Z, int64_t ldz, float* Y, int64_t ldy, float* mean,
-                                      float* rstd, int M, int K, int F, float eps, int act) {
-  if (M < 0 || K < 1 || F != GL_F || act < 0 || act > 3 || ldx < K || ldw < F || ldz < F || ldy < F)
+static int gemm_ln_impl(void* stream, const float* X, int64_t ldx, const int32_t* rows_idx, const float* W,
+                        int64_t ldw, const float* bias, const float* gamma, const float* beta, float* Z, int64_t ldz,
+                        float* Y, int64_t ldy, float* mean, float* rstd, int M, int K, int F, float eps, int act,
+                        int towers, int64_t tX, int64_t tP, int64_t tZY, int64_t tMR) {
+  if (M < 0 || K < 1 || F != GL_F || act < 0 || act > 3 || ldx < K || ldw < F || ldz < F || ldy < F ||
+      towers < 1 || towers > 8 || (towers > 1 && (tX % 4 || tP % 4 || tZY % 4)))
     return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_ln_act_fwd_f32: bad argument (M=%d K=%d F=%d, F must be %d)", M, K,
                           F, GL_F);
   if (M == 0) return PPO_OK;
@@ -189,13 +211,36 @@ PPO_EXPORT int ppo_gemm_ln_act_fwd_f32(void* stream, const float* X, int64_t ldx
   if (!aligned16(W) || ldw % 4 || (bias && !aligned16(bias)) || !aligned16(gamma) || !aligned16(beta) ||
       !aligned16(Z) || ldz % 4 || !aligned16(Y) || ldy % 4)
     return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_ln_act_fwd_f32: W, bias, gamma, beta, Z, Y need 16-byte rows");
-  GemmLnArgs a{X, ldx, rows_idx, W, ldw, bias, gamma, beta, Z, ldz, Y, ldy, mean, rstd, M, K, eps, act};
+  GemmLnArgs a{X, ldx, rows_idx, W, ldw, bias, gamma, beta, Z, ldz, Y, ldy, mean, rstd, M, K, eps, act,
+               tX, tP, tZY, tMR};
   const bool va = aligned16(X) && ldx % 4 == 0 && K % 4 == 0;
-  const dim3 grid(ppo::ceil_div(M, GL_ROWS)), block(GL_THREADS);
+  const dim3 grid(ppo::ceil_div(M, GL_ROWS), towers), block(GL_THREADS);
   if (va) {
     hipLaunchKernelGGL(gemm_ln_fwd_kernel<true>, grid, block, 0, ppo::as_stream(stream), a);
   } else {
     hipLaunchKernelGGL(gemm_ln_fwd_kernel<false>, grid, block, 0, ppo::as_stream(stream), a);
   }
   return ppo::check_launch("ppo_gemm_ln_act_fwd_f32");
+}
+
+PPO_EXPORT int ppo_gemm_ln_act_fwd_f32(void* stream, const float* X, int64_t ldx, const int32_t* rows_idx,
+                                      const float* W, int64_t ldw, const float* bias, const float* gamma,
+                                      const float* beta, float* Z, int64_t ldz, float* Y, int64_t ldy, float* mean,
+                                      float* rstd, int M, int K, int F, float eps, int act) {
+  return gemm_ln_impl(stream, X, ldx, rows_idx, W, ldw, bias, gamma, beta, Z, ldz, Y, ldy, mean, rstd, M, K, F, eps,
+                      act, 1, 0, 0, 0, 0);
+}
+
+// ppo_gemm_ln_act_fwd_f32 over `towers` layers of one shape in one grid:
+// tower t reads X + t stride_x (0: both towers read the same rows), its
+// parameters at + t stride_params, and writes Z / Y at + t stride_rows and
+// mean / rstd at + t stride_stats (elements; all but the last multiples of 4).
+PPO_EXPORT int ppo_gemm_ln_act_fwd_f32_towers(void* stream, int towers, const float* X, int64_t ldx,
+                                             const int32_t* rows_idx, const float* W, int64_t ldw, const float* bias,
+                                             const float* gamma, const float* beta, float* Z, int64_t ldz, float* Y,
+                                             int64_t ldy, float* mean, float* rstd, int M, int K, int F, float eps,
+                                             int act, int64_t stride_x, int64_t stride_params, int64_t stride_rows,
+                                             int64_t stride_stats) {
+  return gemm_ln_impl(stream, X, ldx, rows_idx, W, ldw, bias, gamma, beta, Z, ldz, Y, ldy, mean, rstd, M, K, F, eps,
+                      act, towers, stride_x, stride_params, stride_rows, stride_stats);
 }

@@ -72,6 +72,12 @@ ln_act_fwd_kernel(const float* __restrict__ z, int64_t ldz, const float* __restr
 }
 
 // ------------------------------------------------------------ LayerNorm bwd
+// Element strides of tower t's buffers in a tower-batched launch (blockIdx.y
+// = tower): dy / z / dz rows, mean / rstd, gamma / beta, and the partials.
+struct LnTowers {
+  int64_t rows, stats, params, part;
+};
+
 // dy = dL/d(act output) [rows, F]; recomputes the LN output from z, mean,
 // rstd; writes dz [rows, F] and per-block partials [gridDim.x][2F] holding
 // (sum over the block's rows of dyl * xhat | sum of dyl) for scale and bias.
@@ -80,7 +86,19 @@ __global__ void __launch_bounds__(ROW_THREADS)
 ln_act_bwd_kernel(const float* __restrict__ dy, int64_t lddy, const float* __restrict__ z, int64_t ldz,
                   const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
                   const float* __restrict__ gamma, const float* __restrict__ beta, void* __restrict__ dz,
-                  int64_t lddz, float* __restrict__ partial, int rows, int F, int act, int round, int out16) {
+                  int64_t lddz, float* __restrict__ partial, int rows, int F, int act, int round, int out16,
+                  LnTowers tw) {
+  if (blockIdx.y) {  // tower t of a tower-batched launch
+    const int64_t t = blockIdx.y;
+    dy += t * tw.rows;
+    z += t * tw.rows;
+    dz = static_cast<float*>(dz) + t * tw.rows;
+    mean_in += t * tw.stats;
+    rstd_in += t * tw.stats;
+    gamma += t * tw.params;
+    beta += t * tw.params;
+    partial += t * tw.part;
+  }
   __shared__ float red[ROW_THREADS / 64][2][VPL * 64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -513,9 +531,10 @@ int launch_ln_fwd(hipStream_t st, int blocks, const float* z, int64_t ldz, const
 template <int VPL>
 int launch_ln_bwd(hipStream_t st, int blocks, const float* dy, int64_t lddy, const float* z, int64_t ldz,
                   const float* mean, const float* rstd, const float* gamma, const float* beta, void* dz,
-                  int64_t lddz, float* partial, int rows, int F, int act, int round, int out16) {
-  hipLaunchKernelGGL((ln_act_bwd_kernel<VPL>), dim3(blocks), dim3(ROW_THREADS), 0, st, dy, lddy, z, ldz, mean, rstd,
-                     gamma, beta, dz, lddz, partial, rows, F, act, round, out16);
+                  int64_t lddz, float* partial, int rows, int F, int act, int round, int out16, int towers,
+                  LnTowers tw) {
+  hipLaunchKernelGGL((ln_act_bwd_kernel<VPL>), dim3(blocks, towers), dim3(ROW_THREADS), 0, st, dy, lddy, z, ldz, mean,
+                     rstd, gamma, beta, dz, lddz, partial, rows, F, act, round, out16, tw);
   return ppo::check_launch("ppo_layernorm_act_bwd_f32");
 }
 
@@ -572,18 +591,23 @@ PPO_EXPORT int ppo_layernorm_bwd_blocks(int rows) {
 static int layernorm_bwd(const char* name, void* stream, const float* dy, int64_t lddy, const float* z,
                          int64_t ldz, const float* mean, const float* rstd, const float* gamma, const float* beta,
                          void* dz, int64_t lddz, float* partial, int rows, int F, int act, int round,
-                         int out16 = 0) {
+                         int out16 = 0, int towers = 1, LnTowers tw = LnTowers{0, 0, 0, 0}) {
   if (rows < 0 || F <= 0 || F > 64 * MAX_VPL || act < 0 || act > 3 || !dy || !z || !mean || !rstd || !gamma ||
-      !beta || !dz || !partial)
+      !beta || !dz || !partial || towers < 1 || towers > 8 || (towers > 1 && out16))
     return ppo::set_error(PPO_ERR_ARG, "%s: bad argument (rows=%d F=%d)", name, rows, F);
   const int blocks = ppo_layernorm_bwd_blocks(rows);
   hipStream_t st = ppo::as_stream(stream);
   const int vpl = ppo::ceil_div(F, 64);
-  if (vpl <= 1) return launch_ln_bwd<1>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round, out16);
-  if (vpl <= 2) return launch_ln_bwd<2>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round, out16);
-  if (vpl <= 4) return launch_ln_bwd<4>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round, out16);
-  if (vpl <= 8) return launch_ln_bwd<8>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round, out16);
-  return launch_ln_bwd<16>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round, out16);
+  if (vpl <= 1) return launch_ln_bwd<1>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round, out16,
+                                            towers, tw);
+  if (vpl <= 2) return launch_ln_bwd<2>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round, out16,
+                                            towers, tw);
+  if (vpl <= 4) return launch_ln_bwd<4>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round, out16,
+                                            towers, tw);
+  if (vpl <= 8) return launch_ln_bwd<8>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round, out16,
+                                            towers, tw);
+  return launch_ln_bwd<16>(st, blocks, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round, out16,
+                                            towers, tw);
 }
 
 PPO_EXPORT int ppo_layernorm_act_bwd_f32(void* stream, const float* dy, int64_t lddy, const float* z, int64_t ldz,
@@ -592,6 +616,19 @@ PPO_EXPORT int ppo_layernorm_act_bwd_f32(void* stream, const float* dy, int64_t 
                                          int F, int act) {
   return layernorm_bwd("ppo_layernorm_act_bwd_f32", stream, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz, lddz,
                        partial, rows, F, act, 0);
+}
+
+// ppo_layernorm_act_bwd_f32 over `towers` layers of one shape in one grid:
+// tower t's dy / z / dz rows, mean / rstd, gamma / beta and partials sit t
+// times the given element strides after tower 0's.
+PPO_EXPORT int ppo_layernorm_act_bwd_f32_towers(void* stream, int towers, const float* dy, int64_t lddy,
+                                                const float* z, int64_t ldz, const float* mean, const float* rstd,
+                                                const float* gamma, const float* beta, float* dz, int64_t lddz,
+                                                float* partial, int rows, int F, int act, int64_t stride_rows,
+                                                int64_t stride_stats, int64_t stride_params, int64_t stride_part) {
+  return layernorm_bwd("ppo_layernorm_act_bwd_f32_towers", stream, dy, lddy, z, ldz, mean, rstd, gamma, beta, dz,
+                       lddz, partial, rows, F, act, 0, 0, towers,
+                       LnTowers{stride_rows, stride_stats, stride_params, stride_part});
 }
 
 // bf16 compute: the LayerNorm output was rounded to bf16 before the activation,

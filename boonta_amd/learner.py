@@ -298,6 +298,44 @@ def split_forward_bufs(lb: LayerBufs, rows: int, device, bf16: bool) -> None:
             lb.W16 = torch.zeros(d.fin, d.w.ld, dtype=torch.int16, device=device)
 
 
+def paired_train_bufs(sa: LayerSpec, sc: LayerSpec, rows: int, device) -> tuple:
+    """Training buffers of two layers of one shape (an actor and a critic
+    tower at one depth) as the two halves of [2, ...] tensors: each of the
+    critic's buffers sits one fixed stride after the actor's, which is what a
+    tower-batched launch addresses."""
+    f32 = dict(dtype=torch.float32, device=device)
+    ld, fin = sa.ld, sa.dense.fin
+
+    def two(*shape):
+        t = torch.zeros(2, *shape, **f32)
+        return t[0], t[1]
+
+    a, c = LayerBufs(sa, Y=None), LayerBufs(sc, Y=None)
+    a.Y, c.Y = two(rows, ld)
+    a.dZ, c.dZ = two(rows, ld)
+    if sa.ln is not None:
+        a.Z, c.Z = two(rows, ld)
+        a.mean, c.mean = two(rows)
+        a.rstd, c.rstd = two(rows)
+        a.dY, c.dY = two(rows, ld)
+        a.lnblocks = c.lnblocks = _lib.load().ppo_layernorm_bwd_blocks(rows)
+        a.lnpart, c.lnpart = two(a.lnblocks, 2 * sa.fout)
+    elif sa.act == "silu":
+        a.PRE, c.PRE = two(rows, ld)
+    a.splits = c.splits = _splits(rows, fin, ld)
+    a.wpart, c.wpart = two(a.splits, fin, ld)
+    a.bpart, c.bpart = two(a.splits, ld)
+    return a, c
+
+
+def _tstride(a, c) -> int:
+    """Element stride from tower 0's buffer (or pointer) to tower 1's."""
+    pa = a if isinstance(a, int) else a.data_ptr()
+    pc = c if isinstance(c, int) else c.data_ptr()
+    assert (pc - pa) % 4 == 0
+    return (pc - pa) // 4
+
+
 class ForwardChain:
     """Issues the forward of Dense[+LayerNorm][+act] layer groups through the
     C ABI (fp32 MFMA, or the bf16 GEMMs with flax's casts for a bf16 network).
@@ -465,8 +503,17 @@ class MLPExecutor(ForwardChain):
             return b
 
         self.trunk = [layer_bufs(s, mb, True) for s in program.trunk]
-        self.actor = [layer_bufs(s, mb, True) for s in program.actor_layers]
-        self.critic = [layer_bufs(s, mb, True) for s in program.critic_layers]
+        # an actor and a critic tower of one shape (flax's ActorCritic with
+        # separate torsos) run each depth's forward, LayerNorm backward, dW
+        # and input-cotangent contraction for both towers in one launch
+        self.pair = self._pair_stride(program)
+        if self.pair:
+            pairs = [paired_train_bufs(a, c, mb, dev) for a, c in zip(program.actor_layers, program.critic_layers)]
+            self.actor = [a for a, _ in pairs]
+            self.critic = [c for _, c in pairs]
+        else:
+            self.actor = [layer_bufs(s, mb, True) for s in program.actor_layers]
+            self.critic = [layer_bufs(s, mb, True) for s in program.critic_layers]
         # bf16 network: the first Dense of each torso group contracts the bf16
         # observation copy with the bf16 image of the parameters on the
         # pipelined GEMM (forward split over K, dW over rows)
@@ -602,6 +649,34 @@ class MLPExecutor(ForwardChain):
         return (na <= lib.ppo_head_loss_max_outputs() and ha.fin <= lib.ppo_head_loss_max_features()
                 and ha.fin % 16 == 0)
 
+    def _pair_stride(self, program: Program) -> int:
+        """Element offset from every parameter region of the actor tower to the
+        same region of the critic tower when the two towers have one shape
+        (fp32, fused head loss) and can share launches; else 0."""
+        A, C = program.actor_layers, program.critic_layers
+        if (self.bf16 or program.gru is not None or program.shared_head or not A or len(A) != len(C)
+                or not self._can_fuse(program)):
+            return 0
+        D = None
+        for a, c in zip(A, C):
+            shape = lambda s: (s.dense.fin, s.fout, s.ld, s.act, s.dense.b is None, s.ln is None,
+                               s.ln["eps"] if s.ln is not None else None)
+            if shape(a) != shape(c):
+                return 0
+            if a.ln is not None and (a.fout != 256 or a.ld != 256):
+                return 0   # LayerNorm layers run the fused 256-wide Dense + LayerNorm forward
+            regions = [(a.dense.w, c.dense.w)]
+            if a.dense.b is not None:
+                regions.append((a.dense.b, c.dense.b))
+            if a.ln is not None:
+                regions += [(a.ln["scale"], c.ln["scale"]), (a.ln["bias"], c.ln["bias"])]
+            for ra, rc in regions:
+                d = rc.offset - ra.offset
+                D = d if D is None else D
+                if d != D:
+                    return 0
+        return D if D > 0 and D % 4 == 0 else 0
+
     # ------------------------------------------------------ gradient tables
     def _build_reduce_tables(self):
         flat = self.flat
@@ -717,6 +792,57 @@ class MLPExecutor(ForwardChain):
                     self._gemm(st, A_ROW, B_NK, _p(lb.dZ), s.ld, None, self.flat.view(d.w), d.w.ld,
                               dst, layers[i - 1].spec.ld, self.mb, d.fin, s.ld, 1, 0, epi, None, act, None, aux,
                               ldaux, None, -1)
+
+    def _fwd_pair(self, st, x, ldx, rows_idx, nrows):
+        """Forward of the actor (tower 0) and critic (tower 1) towers, one
+        launch per depth; both first layers read the same input rows."""
+        D, sx = self.pair, 0
+        for la, lc in zip(self.actor, self.critic):
+            s = la.spec
+            d = s.dense
+            W = self.flat.view(d.w)
+            Bb = self.flat.view(d.b) if d.b is not None else None
+            if s.ln is not None:
+                self._call("ppo_gemm_ln_act_fwd_f32_towers", st, 2, x, ldx, rows_idx, W, d.w.ld, Bb,
+                           self.flat.view(s.ln["scale"]), self.flat.view(s.ln["bias"]), _p(la.Z), s.ld, _p(la.Y),
+                           s.ld, _p(la.mean), _p(la.rstd), nrows, d.fin, s.fout, s.ln["eps"], _act(s.act), sx, D,
+                           _tstride(la.Y, lc.Y), _tstride(la.mean, lc.mean))
+            else:
+                pre = _p(la.PRE) if la.PRE is not None else None
+                self._call("ppo_gemm_f32_towers", st, 2, A_ROW, B_KN, x, ldx, rows_idx, W, d.w.ld, _p(la.Y), s.ld,
+                           nrows, s.ld, d.fin, 1, 0, EPI_BIAS_ACT, Bb, _act(s.act), pre, None, 0, None, -1, sx, D,
+                           _tstride(la.Y, lc.Y), D, _tstride(la.PRE, lc.PRE) if pre else 0, 0, 0)
+            x, ldx, rows_idx, sx = _p(la.Y), s.ld, None, _tstride(la.Y, lc.Y)
+
+    def _bwd_pair(self, st, x0, ldx0, idx0):
+        """Backward of the actor and critic towers, one launch per depth and
+        contraction, once both last-layer output cotangents are in place."""
+        D, A, C = self.pair, self.actor, self.critic
+        for i in range(len(A) - 1, -1, -1):
+            la, lc = A[i], C[i]
+            s = la.spec
+            d = s.dense
+            if i > 0:
+                x, ldx, ridx, sx = _p(A[i - 1].Y), A[i - 1].spec.ld, None, _tstride(A[i - 1].Y, C[i - 1].Y)
+            else:
+                x, ldx, ridx, sx = x0, ldx0, idx0, 0
+            rs = _tstride(la.dZ, lc.dZ)
+            if s.ln is not None:
+                self._call("ppo_layernorm_act_bwd_f32_towers", st, 2, _p(la.dY), s.ld, _p(la.Z), s.ld, _p(la.mean),
+                           _p(la.rstd), self.flat.view(s.ln["scale"]), self.flat.view(s.ln["bias"]), _p(la.dZ),
+                           s.ld, _p(la.lnpart), self.mb, s.fout, _act(s.act), rs, _tstride(la.mean, lc.mean), D,
+                           _tstride(la.lnpart, lc.lnpart))
+            self._call("ppo_gemm_f32_towers", st, 2, A_COL, B_KN, x, ldx, ridx, _p(la.dZ), s.ld, _p(la.wpart), s.ld,
+                       d.fin, s.ld, self.mb, la.splits, d.fin * s.ld, EPI_STORE, None, 0, None, None, 0,
+                       _p(la.bpart), -1, sx, rs, _tstride(la.wpart, lc.wpart), 0, 0, 0,
+                       _tstride(la.bpart, lc.bpart))
+            if i > 0:
+                dst, epi, act, aux, ldaux = self._dx_target(A[i - 1])
+                dst_c, _, _, aux_c, _ = self._dx_target(C[i - 1])
+                self._call("ppo_gemm_f32_towers", st, 2, A_ROW, B_NK, _p(la.dZ), s.ld, None, self.flat.view(d.w),
+                           d.w.ld, dst, A[i - 1].spec.ld, self.mb, d.fin, s.ld, 1, 0, epi, None, act, None, aux,
+                           ldaux, None, -1, rs, D, _tstride(dst, dst_c), 0, 0,
+                           _tstride(aux, aux_c) if aux is not None else 0, 0)
 
     def _head_back(self, st, layers, dhead, head: DenseSpec, wpart, bpart, splits, hx, ldhx, hidx):
         """Head dW and the cotangent of the head input."""
@@ -898,6 +1024,10 @@ class MLPExecutor(ForwardChain):
                 self._fwd_layers(st, self.trunk, obs, ldo, idx, mb)
                 self._fused_head_loss(st, idx, step, dist, A, scale_ptr, act_i, act_f)
                 self._bwd_layers(st, self.trunk, obs, ldo, idx)
+            elif self.pair:
+                self._fwd_pair(st, obs, ldo, idx, mb)
+                self._fused_head_loss(st, idx, step, dist, A, scale_ptr, act_i, act_f)
+                self._bwd_pair(st, obs, ldo, idx)
             else:
                 s2 = self._fork(st)
                 self._fwd_layers(st, self.actor, obs, ldo, idx, mb)

@@ -182,6 +182,18 @@ int ppo_gemm_ln_act_fwd_f32(void* stream, const float* X, int64_t ldx, const int
                             int64_t ldw, const float* bias, const float* gamma, const float* beta, float* Z,
                             int64_t ldz, float* Y, int64_t ldy, float* mean, float* rstd, int M, int K, int F,
                             float eps, int act);
+/* The same layer for `towers` (<= 8) towers of one shape in one grid (the
+ * actor and critic towers of flax's ActorCritic with separate torsos, one
+ * launch per depth instead of two): tower t reads X + t stride_x (0 when the
+ * towers read the same rows), its W / bias / gamma / beta at
+ * + t stride_params, and writes Z and Y at + t stride_rows and mean / rstd at
+ * + t stride_stats (elements; stride_x, stride_params and stride_rows
+ * multiples of 4).  Bit-identical to one ppo_gemm_ln_act_fwd_f32 per tower. */
+int ppo_gemm_ln_act_fwd_f32_towers(void* stream, int towers, const float* X, int64_t ldx, const int32_t* rows_idx,
+                                   const float* W, int64_t ldw, const float* bias, const float* gamma,
+                                   const float* beta, float* Z, int64_t ldz, float* Y, int64_t ldy, float* mean,
+                                   float* rstd, int M, int K, int F, float eps, int act, int64_t stride_x,
+                                   int64_t stride_params, int64_t stride_rows, int64_t stride_stats);
 
 /* ------------------------------------------------------- linear scan
  * Replace boonta's linear-recurrence scan and its custom VJP
@@ -229,6 +241,18 @@ int ppo_gemm_f32(void* stream, int a_layout, int b_layout, const float* A, int64
                  const float* B, int64_t ldb, float* C, int64_t ldc, int M, int N, int K, int splits,
                  int64_t c_split_stride, int epi, const float* bias, int act, float* pre, const float* aux,
                  int64_t ldaux, float* bias_grad, int tile);
+/* ppo_gemm_f32 for `towers` (<= 8) contractions of one shape in one grid
+ * (the actor and critic towers' forward, dW and input-cotangent products):
+ * contraction t reads A, B, bias and aux and writes C, pre and bias_grad at
+ * t times the given element strides after contraction 0's (a stride of 0
+ * shares the operand; the row gather `rows` is shared).  Bit-identical to
+ * one ppo_gemm_f32 per tower. */
+int ppo_gemm_f32_towers(void* stream, int towers, int a_layout, int b_layout, const float* A, int64_t lda,
+                        const int32_t* rows, const float* B, int64_t ldb, float* C, int64_t ldc, int M, int N, int K,
+                        int splits, int64_t c_split_stride, int epi, const float* bias, int act, float* pre,
+                        const float* aux, int64_t ldaux, float* bias_grad, int tile, int64_t stride_a,
+                        int64_t stride_b, int64_t stride_c, int64_t stride_bias, int64_t stride_pre,
+                        int64_t stride_aux, int64_t stride_bias_grad);
 
 /* bf16 compute (flax Dense with dtype=bfloat16, param_dtype=float32; the
  * mixed precision of boonta/networks/README.md:73-77): the same contraction
@@ -284,6 +308,15 @@ int ppo_layernorm_bwd_blocks(int rows);
 int ppo_layernorm_act_bwd_f32(void* stream, const float* dy, int64_t lddy, const float* z, int64_t ldz,
                               const float* mean, const float* rstd, const float* gamma, const float* beta,
                               float* dz, int64_t lddz, float* partial, int rows, int F, int act);
+/* The same backward for `towers` (<= 8) layers of one shape in one grid:
+ * tower t's dy / z / dz rows, mean / rstd, gamma / beta and partials sit
+ * t times the given element strides after tower 0's.  Bit-identical to one
+ * ppo_layernorm_act_bwd_f32 per tower. */
+int ppo_layernorm_act_bwd_f32_towers(void* stream, int towers, const float* dy, int64_t lddy, const float* z,
+                                     int64_t ldz, const float* mean, const float* rstd, const float* gamma,
+                                     const float* beta, float* dz, int64_t lddz, float* partial, int rows, int F,
+                                     int act, int64_t stride_rows, int64_t stride_stats, int64_t stride_params,
+                                     int64_t stride_part);
 /* bf16 compute: flax's LayerNorm with dtype=bfloat16 computes statistics and
  * the normalisation in fp32 and casts the result to bf16 before the
  * activation; the backward rounds the input cotangent to bf16. */

@@ -1,0 +1,199 @@
+"""Tower-batched launches: the actor and critic towers of an actor-critic
+with separate torsos (flax ActorCritic over two Sequential towers, as in
+hangar's continuous-control recipes; forward at
+boonta/networks/network.py:38-49, backward of jax.value_and_grad at
+boonta/algorithms/ppo.py:155-157) run each depth's Dense + LayerNorm
+forward, LayerNorm backward, dW and input-cotangent contraction for both
+towers in one launch.
+
+Bar: bit-identical to one single-tower launch per tower (each tower's
+values come from the same tile code and the same reduction order), and the
+whole update with paired towers bit-identical to the update that runs the
+towers as separate launches on two streams; the whole update's parity
+against the oracle is the Gaussian cases of the learner tests."""
+import numpy as np
+import pytest
+import torch
+
+from boonta_amd import _lib
+from boonta_amd.algorithms.ppo import PPO, flat_state_of
+from boonta_amd.learner import MLPExecutor
+from boonta_amd.random import key as make_key
+from ppo_cases import device_transition, make_case
+
+pytestmark = pytest.mark.gpu
+
+A_ROW, A_COL, B_KN, B_NK = 0, 1, 0, 1
+
+
+def st():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def rnd(g, *shape, scale=1.0):
+    return torch.from_numpy((g.standard_normal(shape) * scale).astype(np.float32)).cuda()
+
+
+def p(t):
+    return 0 if t is None else t.data_ptr()
+
+
+@pytest.mark.parametrize("rows,K,gather,shared", [(2048, 87, True, True), (300, 256, False, False),
+                                                  (17, 64, True, False)])
+def test_dense_layernorm_forward_towers_equal_single_launches(rows, K, gather, shared):
+    g = np.random.default_rng(rows + K)
+    F, src = 256, rows + 40
+    X = rnd(g, 2, src, K)
+    # each tower's parameters in one block (W | bias | gamma | beta), the
+    # critic's one block after the actor's: one stride for all of them
+    P = rnd(g, 2, K * F + 3 * F, scale=0.1)
+    W = P[:, :K * F].view(2, K, F)
+    bias, gamma, beta = P[:, K * F:K * F + F], P[:, K * F + F:K * F + 2 * F], P[:, K * F + 2 * F:]
+    gamma += 1.0
+    I = torch.from_numpy(g.permutation(src)[:rows].astype(np.int32)).cuda() if gather else None
+    Z, Y = torch.zeros(2, rows, F, device="cuda"), torch.zeros(2, rows, F, device="cuda")
+    mean, rstd = torch.zeros(2, rows, device="cuda"), torch.zeros(2, rows, device="cuda")
+    Zs, Ys, ms, rs = (torch.full_like(t, 7.0) for t in (Z, Y, mean, rstd))
+    x_stride = 0 if shared else src * K
+    for t in range(2):
+        xt = X[0] if shared else X[t]
+        _lib.call("ppo_gemm_ln_act_fwd_f32", st(), p(xt), K, p(I), p(W[t]), F, p(bias[t]), p(gamma[t]), p(beta[t]),
+                  p(Zs[t]), F, p(Ys[t]), F, p(ms[t]), p(rs[t]), rows, K, F, 1e-6, 3)
+    _lib.call("ppo_gemm_ln_act_fwd_f32_towers", st(), 2, p(X[0]), K, p(I), p(W[0]), F, p(bias[0]), p(gamma[0]),
+              p(beta[0]), p(Z[0]), F, p(Y[0]), F, p(mean[0]), p(rstd[0]), rows, K, F, 1e-6, 3, x_stride,
+              P.shape[1], rows * F, rows)
+    torch.cuda.synchronize()
+    for a, b in ((Z, Zs), (Y, Ys), (mean, ms), (rstd, rs)):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("rows,F,act", [(2048, 256, 3), (333, 256, 1), (64, 100, 0)])
+def test_layernorm_backward_towers_equal_single_launches(rows, F, act):
+    g = np.random.default_rng(rows * 3 + F)
+    lib = _lib.load()
+    blocks = lib.ppo_layernorm_bwd_blocks(rows)
+    dy, z = rnd(g, 2, rows, F), rnd(g, 2, rows, F, scale=2.0)
+    zz = z.double()
+    mean = zz.mean(-1).float().contiguous()
+    rstd = (1.0 / (zz.var(-1, unbiased=False) + 1e-6).sqrt()).float().contiguous()
+    gb = rnd(g, 2, 2 * F, scale=0.1)   # each tower's gamma | beta, one stride for both
+    gamma, beta = gb[:, :F], gb[:, F:]
+    gamma += 1.0
+    dz, part = torch.zeros(2, rows, F, device="cuda"), torch.zeros(2, blocks, 2 * F, device="cuda")
+    dzs, parts = torch.full_like(dz, 5.0), torch.full_like(part, 5.0)
+    for t in range(2):
+        _lib.call("ppo_layernorm_act_bwd_f32", st(), p(dy[t]), F, p(z[t]), F, p(mean[t]), p(rstd[t]), p(gamma[t]),
+                  p(beta[t]), p(dzs[t]), F, p(parts[t]), rows, F, act)
+    _lib.call("ppo_layernorm_act_bwd_f32_towers", st(), 2, p(dy[0]), F, p(z[0]), F, p(mean[0]), p(rstd[0]),
+              p(gamma[0]), p(beta[0]), p(dz[0]), F, p(part[0]), rows, F, act, rows * F, rows, 2 * F,
+              blocks * 2 * F)
+    torch.cuda.synchronize()
+    assert torch.equal(dz, dzs) and torch.equal(part, parts)
+
+
+GEMM_CASES = [
+    # (name, a_layout, b_layout, M, N, K, splits, epi, act, gather, shared_a, tile)
+    ("forward-silu-pre", A_ROW, B_KN, 2048, 256, 87, 1, 1, 3, True, True, -1),
+    ("forward-relu-ragged", A_ROW, B_KN, 301, 130, 77, 1, 1, 1, False, False, 5),
+    ("dw-first-layer", A_COL, B_KN, 87, 256, 2048, 16, 0, 0, True, True, -1),
+    ("dw-inner", A_COL, B_KN, 256, 256, 2048, 16, 0, 0, False, False, -1),
+    ("dw-registers", A_COL, B_KN, 64, 96, 1000, 3, 0, 0, False, False, 7),
+    ("dx-dact-silu", A_ROW, B_NK, 2048, 256, 256, 1, 2, 3, False, False, -1),
+    ("dx-dact-tanh-128", A_ROW, B_NK, 512, 256, 256, 1, 2, 2, False, False, 0),
+    ("dx-store-8wave", A_ROW, B_NK, 1024, 256, 256, 1, 0, 0, False, False, 8),
+]
+
+
+def two(g, shape, fill=None, scale=1.0):
+    """Two towers' copies of an operand in one buffer, tower 1 starting at a
+    multiple of 4 elements after tower 0: (tower views, element stride)."""
+    n = int(np.prod(shape))
+    stride = (n + 3) // 4 * 4
+    if fill is None:
+        flat = torch.from_numpy((g.standard_normal(2 * stride) * scale).astype(np.float32)).cuda()
+    else:
+        flat = torch.full((2 * stride,), float(fill), device="cuda")
+    return [flat[t * stride:t * stride + n].view(*shape) for t in range(2)], stride
+
+
+@pytest.mark.parametrize("case", GEMM_CASES, ids=[c[0] for c in GEMM_CASES])
+def test_gemm_towers_equal_single_launches(case):
+    _, al, bl, M, N, K, splits, epi, act, gather, shared, tile = case
+    g = np.random.default_rng(M * 7 + N * 3 + K)
+    # A: [M, K] (layout 0) or [K, M] (layout 1), its gathered axis over `src` rows
+    gl = M if al == A_ROW else K
+    src = gl + 50 if gather else gl
+    a_shape = (src, K) if al == A_ROW else (src, M)
+    A, sa = two(g, a_shape)
+    if shared:
+        A, sa = [A[0], A[0]], 0
+    I = torch.from_numpy(g.permutation(src)[:gl].astype(np.int32)).cuda() if gather else None
+    b_shape = (K, N) if bl == B_KN else (N, K)
+    B, sb = two(g, b_shape, scale=K ** -0.5)
+    C, sc = two(g, (splits, M, N), fill=0)
+    Cs, _ = two(g, (splits, M, N), fill=3)
+    bias, sbias = two(g, (N,), scale=0.1) if epi == 1 else ([None, None], 0)
+    pre, spre = two(g, (M, N), fill=0) if epi == 1 and act == 3 else ([None, None], 0)
+    pres, _ = two(g, (M, N), fill=3) if pre[0] is not None else ([None, None], 0)
+    aux, saux = two(g, (M, N)) if epi == 2 else ([None, None], 0)
+    bg, sbg = two(g, (splits, N), fill=0) if al == A_COL else ([None, None], 0)
+    bgs, _ = two(g, (splits, N), fill=3) if bg[0] is not None else ([None, None], 0)
+    q = lambda t: None if t is None else t.data_ptr()
+    for t in range(2):
+        _lib.call("ppo_gemm_f32", st(), al, bl, q(A[t]), a_shape[1], q(I), q(B[t]), b_shape[1], q(Cs[t]), N, M, N, K,
+                  splits, M * N, epi, q(bias[t]), act, q(pres[t]), q(aux[t]), N, q(bgs[t]), tile)
+    _lib.call("ppo_gemm_f32_towers", st(), 2, al, bl, q(A[0]), a_shape[1], q(I), q(B[0]), b_shape[1], q(C[0]), N, M, N,
+              K, splits, M * N, epi, q(bias[0]), act, q(pre[0]), q(aux[0]), N, q(bg[0]), tile, sa, sb, sc, sbias,
+              spre, saux, sbg)
+    torch.cuda.synchronize()
+    for t in range(2):
+        assert torch.equal(C[t], Cs[t]), t
+        if pre[0] is not None:
+            assert torch.equal(pre[t], pres[t]), t
+        if bg[0] is not None:
+            assert torch.equal(bg[t], bgs[t]), t
+
+
+def test_tower_strides_must_keep_rows_aligned():
+    """A stride that is not a multiple of 4 elements is an argument error
+    (reported before anything is launched)."""
+    X = torch.zeros(2, 64, 64, device="cuda")
+    W = torch.zeros(2, 64, 256, device="cuda")
+    Z = torch.zeros(2, 64, 256, device="cuda")
+    m = torch.zeros(2, 64, device="cuda")
+    with pytest.raises(_lib.KernelError, match="bad argument"):
+        _lib.call("ppo_gemm_ln_act_fwd_f32_towers", st(), 2, p(X), 64, None, p(W), 256, None, p(W), p(W), p(Z), 256,
+                  p(Z), 256, p(m), p(m), 64, 64, 256, 1e-6, 0, 64 * 64, 64 * 256 + 2, 64 * 256, 64)
+    with pytest.raises(_lib.KernelError, match="multiples of 4"):
+        _lib.call("ppo_gemm_f32_towers", st(), 2, A_ROW, B_KN, p(X), 64, None, p(W), 256, p(Z), 256, 64, 256, 64, 1,
+                  0, 0, None, 0, None, None, 0, None, -1, 6, 0, 64 * 256, 0, 0, 0, 0)
+
+
+class _TwoStreams(MLPExecutor):
+    """The executor with tower pairing switched off: each tower's layers run
+    as launches of their own, the towers on two streams."""
+
+    def _pair_stride(self, program):
+        return 0
+
+
+class _TwoStreamsPPO(PPO):
+    executor_class = _TwoStreams
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_paired_towers_update_equals_two_stream_update(use_graph):
+    r, plan, params, tr, roll = make_case(config=3, T=8, N=128, M=4, E=2)
+    results = []
+    for cls in (PPO, _TwoStreamsPPO):
+        alg = cls(cfg=r.cfg, network=r.network, optimizer=r.optimizer, use_graph=use_graph)
+        state = alg.init_from_params({"params": params}, r.obs_dim)
+        ex = alg.executor(state, r.T, r.N, r.obs_dim)
+        assert bool(ex.pair) == (cls is PPO)
+        trans = device_transition(tr, roll)
+        for k in (1, 2):
+            alg.update(state, make_key(k), trans)
+        torch.cuda.synchronize()
+        results.append((flat_state_of(state).P.cpu().numpy().copy(), ex.LOGS.cpu().numpy().copy()))
+    np.testing.assert_array_equal(results[0][0], results[1][0])
+    np.testing.assert_array_equal(results[0][1], results[1][1])

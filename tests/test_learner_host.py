@@ -171,9 +171,66 @@ def test_gaussian_update_fuses_dense_and_layernorm_forward():
     flat = FlatState(prog, torch.device("cpu"))
     ex = executor(r, prog, flat)
     ex.bind(fake_inputs(ex))
-    names = [n for n, _ in ex.record()]
+    calls = ex.record()
+    names = [n for n, _ in calls]
     steps = r.cfg.update_epochs * r.cfg.num_minibatches
-    # 4 layers x 2 towers per minibatch step, plus the critic's bootstrap forward
-    assert names.count("ppo_gemm_ln_act_fwd_f32") == 8 * steps + 4
-    assert "ppo_layernorm_act_fwd_f32" not in names
-    assert names.count("ppo_layernorm_act_bwd_f32") == 8 * steps
+    # the actor and critic towers share every launch of a minibatch step: 4
+    # Dense + LayerNorm + SiLU forwards, 4 LayerNorm backwards, 4 dW and 3
+    # input-cotangent contractions; the critic's bootstrap forward runs alone
+    assert ex.pair == prog.critic_layers[0].dense.w.offset - prog.actor_layers[0].dense.w.offset
+    assert names.count("ppo_gemm_ln_act_fwd_f32_towers") == 4 * steps
+    assert names.count("ppo_gemm_ln_act_fwd_f32") == 4
+    assert names.count("ppo_layernorm_act_bwd_f32_towers") == 4 * steps
+    assert names.count("ppo_gemm_f32_towers") == 7 * steps
+    assert names.count("ppo_gemm_f32") == 1   # the bootstrap value head
+    assert "ppo_layernorm_act_fwd_f32" not in names and "ppo_layernorm_act_bwd_f32" not in names
+    assert "ppo_stream_wait" not in names
+
+    # every tower-1 operand is tower 0's pointer plus its stride, and lands on
+    # the critic's own buffer or parameter region of the same depth
+    def ranges(layers):
+        out = []
+        for lb in layers:
+            for t in (lb.Y, lb.Z, lb.PRE, lb.mean, lb.rstd, lb.dY, lb.dZ, lb.wpart, lb.bpart, lb.lnpart):
+                if t is not None:
+                    out.append((t.data_ptr(), t.data_ptr() + 4 * t.numel()))
+        return out
+
+    def regions(layers):
+        out = set()
+        for s in layers:
+            out.add(flat.view(s.dense.w))
+            if s.dense.b is not None:
+                out.add(flat.view(s.dense.b))
+            if s.ln is not None:
+                out |= {flat.view(s.ln["scale"]), flat.view(s.ln["bias"])}
+        return out
+
+    actor_bufs, critic_bufs = ranges(ex.actor), ranges(ex.critic)
+    actor_params, critic_params = regions(prog.actor_layers), regions(prog.critic_layers)
+    inside = lambda x, rs: any(a <= x < b for a, b in rs)
+    checked = 0
+    for name, args in calls:
+        if name == "ppo_gemm_ln_act_fwd_f32_towers":
+            sx, sp, sr, ss = args[-4:]
+            params = [(args[5], sp), (args[7], sp), (args[8], sp), (args[9], sp)]
+            bufs = [(args[10], sr), (args[12], sr), (args[14], ss), (args[15], ss)] + ([(args[2], sx)] if sx else [])
+        elif name == "ppo_layernorm_act_bwd_f32_towers":
+            sr, ss, sp, spart = args[-4:]
+            params = [(args[8], sp), (args[9], sp)]
+            bufs = [(args[2], sr), (args[4], sr), (args[6], ss), (args[7], ss), (args[10], sr), (args[12], spart)]
+        elif name == "ppo_gemm_f32_towers":
+            sa, sb, sc, sbias, spre, saux, sbg = args[-7:]
+            a_layout, b_layout, A, B, C, pre, aux, bg = args[2], args[3], args[4], args[7], args[9], args[19], \
+                args[20], args[22]
+            params = [(B, sb)] if b_layout == 1 else []   # input cotangent: dZ W^T
+            bufs = ([] if b_layout == 1 else [(B, sb)]) + [(C, sc)] + ([(A, sa)] if sa else [])
+            bufs += [(x, s) for x, s in ((pre, spre), (aux, saux), (bg, sbg)) if x]
+        else:
+            continue
+        for ptr, stride in params:
+            assert stride == ex.pair and ptr in actor_params and ptr + 4 * stride in critic_params, name
+        for ptr, stride in bufs:
+            assert inside(ptr, actor_bufs) and inside(ptr + 4 * stride, critic_bufs), name
+            checked += 1
+    assert checked > 0
