@@ -1,0 +1,456 @@
+// Whole torso chains of Dense -> LayerNorm -> activation layers (all 256
+// wide, fp32) in one launch each, for the actor and critic towers of flax's
+// ActorCritic with separate torsos (the Gaussian workload's 4 x 256 SiLU
+// towers; forward at boonta/networks/network.py:38-49, backward of
+// jax.value_and_grad at boonta/algorithms/ppo.py:155-157).
+//
+// Every row of a minibatch goes through the torso independently, so a
+// workgroup that owns 16 rows can run all layers back to back: the forward
+// keeps each layer's output in LDS as the next layer's input, and the
+// backward keeps each input cotangent in registers for the next LayerNorm
+// backward.  Only what the weight gradients and the next launches need goes
+// to HBM (Z, Y, mean, rstd forward; dZ and the LayerNorm parameter
+// partials backward), and the per-layer launch, prologue and epilogue
+// latencies are paid once per torso instead of once per layer.
+//
+// Tiling (both directions): 16 rows x 256 features per workgroup, four
+// waves of 64 features as four 16 x 16 blocks on v_mfma_f32_16x16x4f32;
+// block j's column li of wave w is feature 64 w + 4 li + j, so a lane holds
+// rows 4 kq + v (v < 4) of four adjacent features and every row access is
+// one 16-byte vector.  The forward's contraction and epilogue are those of
+// ppo_gemm_ln_act_fwd_f32 (same k order, same statistics), so a chain is
+// bit-identical to one fused launch per layer.  The backward's dX = dZ W^T
+// reads the layer's kernel transposed (an image refreshed from the
+// parameters before each step, ppo_transpose_f32_batched), which gives its
+// B operand the forward's coalesced row reads.
+#include "common.h"
+
+namespace {
+
+constexpr int MC_THREADS = 256;
+constexpr int MC_ROWS = 16;
+constexpr int MC_F = 256;
+constexpr int MC_MAXL = 8;
+constexpr int SX_PITCH = MC_F + 4;  // LDS row pitch of the 16-row activation tile
+
+__device__ __forceinline__ floatx4 mfma4(const float (&a)[4], const float (&b)[4], floatx4 acc) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], acc, 0, 0, 0);
+  return acc;
+}
+
+struct FwdArgs {
+  const float* X;  // layer 0 input rows (row r is X[idx[r]] when idx is non-null)
+  int64_t ldx;
+  const int32_t* idx;
+  int M, K0, L, act;
+  float eps;
+  int64_t ldw0;  // row pitch of layer 0's kernel [K0][256]; later layers' kernels are [256][ldw]
+  int64_t ldw, ld;  // ld: row pitch of Z and Y
+  const float* W[MC_MAXL];
+  const float* bias[MC_MAXL];
+  const float* gamma[MC_MAXL];
+  const float* beta[MC_MAXL];
+  float* Z[MC_MAXL];
+  float* Y[MC_MAXL];
+  float* mean[MC_MAXL];
+  float* rstd[MC_MAXL];
+  // tower t's input, parameters, rows (Z, Y) and statistics sit t times
+  // these element strides after tower 0's
+  int64_t tX, tP, tR, tS;
+};
+
+// One layer's 16 x 256 contraction: acc[j] += A[rows][k] W[k][c4 + j] in the
+// k order of the fused per-layer forward (64-deep chunks, each k step of 16
+// as four dependent MFMAs).  A comes from global rows (layer 0) or from the
+// LDS tile.
+template <int SRC, bool VA>
+__device__ __forceinline__ void contract(floatx4 (&acc)[4], const float* xrow, bool a_live, const float* lds_row,
+                                         const float* W, int64_t ldw, int K, int kq, int c4) {
+  auto load = [&](int k0, float (&a)[4][4], floatx4 (&w)[4][4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int kb = k0 + 16 * u + 4 * kq;
+      if (SRC == 1) {
+        const floatx4 x4 = kb < K ? *reinterpret_cast<const floatx4*>(lds_row + kb) : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) a[u][s] = x4[s];
+      } else if (VA) {
+        const floatx4 x4 = (a_live && kb < K) ? *reinterpret_cast<const floatx4*>(xrow + kb)
+                                                : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) a[u][s] = x4[s];
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) a[u][s] = (a_live && kb + s < K) ? xrow[kb + s] : 0.f;
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int k = kb + s;
+        w[u][s] = k < K ? *reinterpret_cast<const floatx4*>(W + (int64_t)k * ldw + c4) : floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
+  auto compute = [&](const float (&a)[4][4], const floatx4 (&w)[4][4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float b[4] = {w[u][0][j], w[u][1][j], w[u][2][j], w[u][3][j]};
+        acc[j] = mfma4(a[u], b, acc[j]);
+      }
+    }
+  };
+  float a0[4][4], a1[4][4];
+  floatx4 w0[4][4], w1[4][4];
+  load(0, a0, w0);
+  for (int k0 = 0; k0 < K; k0 += 128) {
+    if (k0 + 64 < K) load(k0 + 64, a1, w1);
+    compute(a0, w0);
+    if (k0 + 64 >= K) break;
+    if (k0 + 128 < K) load(k0 + 128, a0, w0);
+    compute(a1, w1);
+  }
+}
+
+template <bool VA>
+__global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p) {
+  __shared__ float sX[MC_ROWS][SX_PITCH];
+  __shared__ float s_sum[4][MC_ROWS];
+  __shared__ float s_sq[4][MC_ROWS];
+  const int64_t t = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 15;
+  const int kq = lane >> 4;
+  const int r0 = blockIdx.x * MC_ROWS;
+  const int ra = r0 + li;
+  const bool a_live = ra < p.M;
+  const float* X = p.X + t * p.tX;
+  const float* xrow = X + (a_live ? (int64_t)(p.idx ? p.idx[ra] : ra) * p.ldx : 0);
+  const int c4 = 64 * wave + 4 * li;
+
+  for (int l = 0; l < p.L; ++l) {
+    const float* W = p.W[l] + t * p.tP;
+    floatx4 acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (l == 0)
+      contract<0, VA>(acc, xrow, a_live, nullptr, W, p.ldw0, p.K0, kq, c4);
+    else
+      contract<1, true>(acc, nullptr, true, &sX[li][0], W, p.ldw, MC_F, kq, c4);
+
+    const float* bias = p.bias[l] ? p.bias[l] + t * p.tP : nullptr;
+    const floatx4 bias4 = bias ? *reinterpret_cast<const floatx4*>(bias + c4) : floatx4{0.f, 0.f, 0.f, 0.f};
+    float z[4][4];
+    float ps[4], pq[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      ps[v] = 0.f;
+      pq[v] = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        z[v][j] = acc[j][v] + bias4[j];
+        ps[v] += z[v][j];
+        pq[v] += z[v][j] * z[v][j];
+      }
+#pragma unroll
+      for (int o = 8; o; o >>= 1) {
+        ps[v] += __shfl_xor(ps[v], o, 16);
+        pq[v] += __shfl_xor(pq[v], o, 16);
+      }
+    }
+    if (li == 0) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        s_sum[wave][4 * kq + v] = ps[v];
+        s_sq[wave][4 * kq + v] = pq[v];
+      }
+    }
+    // every wave is past its contraction (its reads of sX) once here
+    __syncthreads();
+    const floatx4 g4 = *reinterpret_cast<const floatx4*>(p.gamma[l] + t * p.tP + c4);
+    const floatx4 be4 = *reinterpret_cast<const floatx4*>(p.beta[l] + t * p.tP + c4);
+    float* Zl = p.Z[l] + t * p.tR;
+    float* Yl = p.Y[l] + t * p.tR;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int rr = 4 * kq + v;
+      const int row = r0 + rr;
+      const float s = (s_sum[0][rr] + s_sum[1][rr]) + (s_sum[2][rr] + s_sum[3][rr]);
+      const float s2 = (s_sq[0][rr] + s_sq[1][rr]) + (s_sq[2][rr] + s_sq[3][rr]);
+      const float mean = s / (float)MC_F;
+      const float var = fmaxf(s2 / (float)MC_F - mean * mean, 0.f);
+      const float rstd = rsqrtf(var + p.eps);
+      floatx4 zo, yo;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        zo[j] = z[v][j];
+        yo[j] = ppo::act_fwd(p.act, (z[v][j] - mean) * (rstd * g4[j]) + be4[j]);
+      }
+      if (l + 1 < p.L) *reinterpret_cast<floatx4*>(&sX[rr][c4]) = yo;
+      if (row >= p.M) continue;
+      if (wave == 0 && li == 0) {
+        p.mean[l][t * p.tS + row] = mean;
+        p.rstd[l][t * p.tS + row] = rstd;
+      }
+      *reinterpret_cast<floatx4*>(Zl + (int64_t)row * p.ld + c4) = zo;
+      *reinterpret_cast<floatx4*>(Yl + (int64_t)row * p.ld + c4) = yo;
+    }
+    // the next layer's contraction reads the tile (and s_sum is rewritten)
+    __syncthreads();
+  }
+}
+
+struct BwdArgs {
+  const float* dY;  // cotangent of the last layer's output
+  int64_t lddy;
+  int M, L, act;
+  int64_t ld;       // row pitch of Z and dZ
+  int64_t ldwt;     // row pitch of the transposed kernels
+  const float* Z[MC_MAXL];
+  const float* mean[MC_MAXL];
+  const float* rstd[MC_MAXL];
+  const float* gamma[MC_MAXL];
+  const float* beta[MC_MAXL];
+  const float* WT[MC_MAXL];  // layer l >= 1: its kernel transposed, WT[out][in]
+  float* dZ[MC_MAXL];
+  float* part[MC_MAXL];      // [blocks][2 F]: scale | bias gradient sums of the block's rows
+  int64_t tR, tS, tP, tWT, tPart;
+};
+
+__global__ void __launch_bounds__(MC_THREADS) mlp_ln_bwd_kernel(BwdArgs p) {
+  __shared__ float sX[MC_ROWS][SX_PITCH];
+  __shared__ float s_sum[4][MC_ROWS];
+  __shared__ float s_sq[4][MC_ROWS];
+  const int64_t t = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 15;
+  const int kq = lane >> 4;
+  const int r0 = blockIdx.x * MC_ROWS;
+  const int c4 = 64 * wave + 4 * li;
+
+  // the cotangent of the current layer's output: rows 4 kq + v, features c4 + j
+  float dy[4][4];
+  {
+    const float* dY = p.dY + t * p.tR;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = r0 + 4 * kq + v;
+      const floatx4 d = row < p.M ? *reinterpret_cast<const floatx4*>(dY + (int64_t)row * p.lddy + c4)
+                                  : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dy[v][j] = d[j];
+    }
+  }
+
+  for (int l = p.L - 1; l >= 0; --l) {
+    const float* Zl = p.Z[l] + t * p.tR;
+    const floatx4 g4 = *reinterpret_cast<const floatx4*>(p.gamma[l] + t * p.tP + c4);
+    const floatx4 be4 = *reinterpret_cast<const floatx4*>(p.beta[l] + t * p.tP + c4);
+    float xh[4][4], g[4][4], mu[4], rs[4];
+    float sg[4], sgx[4];
+    float pg[4] = {0.f, 0.f, 0.f, 0.f}, pb[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = r0 + 4 * kq + v;
+      const bool live = row < p.M;
+      const int rr = live ? row : r0;
+      const floatx4 zz = *reinterpret_cast<const floatx4*>(Zl + (int64_t)rr * p.ld + c4);
+      mu[v] = p.mean[l][t * p.tS + rr];
+      rs[v] = p.rstd[l][t * p.tS + rr];
+      sg[v] = 0.f;
+      sgx[v] = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xh[v][j] = live ? (zz[j] - mu[v]) * rs[v] : 0.f;
+        const float yl = xh[v][j] * g4[j] + be4[j];
+        const float a = (p.act == ACT_RELU || p.act == ACT_TANH) ? ppo::act_fwd(p.act, yl) : yl;
+        const float dyl = live ? dy[v][j] * ppo::act_grad(p.act, a) : 0.f;
+        pg[j] += dyl * xh[v][j];
+        pb[j] += dyl;
+        g[v][j] = dyl * g4[j];
+        sg[v] += g[v][j];
+        sgx[v] += g[v][j] * xh[v][j];
+      }
+#pragma unroll
+      for (int o = 8; o; o >>= 1) {
+        sg[v] += __shfl_xor(sg[v], o, 16);
+        sgx[v] += __shfl_xor(sgx[v], o, 16);
+      }
+    }
+    if (li == 0) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        s_sum[wave][4 * kq + v] = sg[v];
+        s_sq[wave][4 * kq + v] = sgx[v];
+      }
+    }
+    // LayerNorm parameter partials: this block's rows, summed in a fixed
+    // order (the lane's four rows, then the four row groups)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      pg[j] += __shfl_xor(pg[j], 16);
+      pb[j] += __shfl_xor(pb[j], 16);
+      pg[j] += __shfl_xor(pg[j], 32);
+      pb[j] += __shfl_xor(pb[j], 32);
+    }
+    if (kq == 0) {
+      float* part = p.part[l] + t * p.tPart + (int64_t)blockIdx.x * 2 * MC_F;
+      *reinterpret_cast<floatx4*>(part + c4) = floatx4{pg[0], pg[1], pg[2], pg[3]};
+      *reinterpret_cast<floatx4*>(part + MC_F + c4) = floatx4{pb[0], pb[1], pb[2], pb[3]};
+    }
+    // every wave is past the previous dX contraction (its reads of sX) here
+    __syncthreads();
+    float* dZl = p.dZ[l] + t * p.tR;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int rr = 4 * kq + v;
+      const int row = r0 + rr;
+      const float s = ((s_sum[0][rr] + s_sum[1][rr]) + (s_sum[2][rr] + s_sum[3][rr])) / (float)MC_F;
+      const float s2 = ((s_sq[0][rr] + s_sq[1][rr]) + (s_sq[2][rr] + s_sq[3][rr])) / (float)MC_F;
+      floatx4 d;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) d[j] = row < p.M ? rs[v] * (g[v][j] - s - xh[v][j] * s2) : 0.f;
+      if (l > 0) *reinterpret_cast<floatx4*>(&sX[rr][c4]) = d;
+      if (row < p.M) *reinterpret_cast<floatx4*>(dZl + (int64_t)row * p.ld + c4) = d;
+    }
+    if (l == 0) break;
+    __syncthreads();
+    // dY of layer l - 1 = dZ_l W_l^T, from the transposed kernel WT_l[out][in]
+    floatx4 acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    contract<1, true>(acc, nullptr, true, &sX[li][0], p.WT[l] + t * p.tWT, p.ldwt, MC_F, kq, c4);
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dy[v][j] = acc[j][v];
+  }
+}
+
+// dst[b][c][r] = src[b][r][c] for a batch of row-major matrices, through 32 x 32
+// LDS tiles (coalesced reads and writes).
+struct TransposeArgs {
+  const float* src[2 * MC_MAXL];
+  float* dst[2 * MC_MAXL];
+  int rows, cols;
+  int64_t lds, ldd;
+};
+
+__global__ void __launch_bounds__(256) transpose_kernel(TransposeArgs a) {
+  __shared__ float tile[32][33];
+  const float* src = a.src[blockIdx.z];
+  float* dst = a.dst[blockIdx.z];
+  const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+#pragma unroll
+  for (int i = 0; i < 32; i += 8) {
+    const int r = r0 + ty + i, c = c0 + tx;
+    if (r < a.rows && c < a.cols) tile[ty + i][tx] = src[(int64_t)r * a.lds + c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 32; i += 8) {
+    const int c = c0 + ty + i, r = r0 + tx;
+    if (r < a.rows && c < a.cols) dst[(int64_t)c * a.ldd + r] = tile[tx][ty + i];
+  }
+}
+
+bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
+
+}  // namespace
+
+PPO_EXPORT int ppo_mlp_chain_max_layers() { return MC_MAXL; }
+
+// Forward of L Dense(256) -> LayerNorm -> activation layers for `towers`
+// towers in one launch (see the top of this file); arrays hold tower 0's
+// per-layer pointers.
+PPO_EXPORT int ppo_mlp_ln_fwd_f32(void* stream, int towers, int L, const float* X, int64_t ldx,
+                                 const int32_t* rows_idx, int M, int K0, const float* const* W, int64_t ldw0,
+                                 int64_t ldw, const float* const* bias, const float* const* gamma,
+                                 const float* const* beta, float* const* Z, float* const* Y, int64_t ld,
+                                 float* const* mean, float* const* rstd, float eps, int act, int64_t stride_x,
+                                 int64_t stride_params, int64_t stride_rows, int64_t stride_stats) {
+  if (towers < 1 || towers > 8 || L < 1 || L > MC_MAXL || M < 0 || K0 < 1 || act < 0 || act > 3 || ldx < K0 ||
+      ldw0 < MC_F || ldw < MC_F || ld < MC_F || !W || !bias || !gamma || !beta || !Z || !Y || !mean || !rstd ||
+      ldw0 % 4 || ldw % 4 || ld % 4 || (towers > 1 && (stride_x % 4 || stride_params % 4 || stride_rows % 4)))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_mlp_ln_fwd_f32: bad argument (towers=%d L=%d M=%d K0=%d)", towers, L,
+                          M, K0);
+  if (M == 0) return PPO_OK;
+  FwdArgs a{};
+  a.X = X; a.ldx = ldx; a.idx = rows_idx; a.M = M; a.K0 = K0; a.L = L; a.act = act; a.eps = eps;
+  a.ldw0 = ldw0; a.ldw = ldw; a.ld = ld;
+  a.tX = stride_x; a.tP = stride_params; a.tR = stride_rows; a.tS = stride_stats;
+  if (!X) return ppo::set_error(PPO_ERR_ARG, "ppo_mlp_ln_fwd_f32: null input");
+  for (int l = 0; l < L; ++l) {
+    if (!W[l] || !gamma[l] || !beta[l] || !Z[l] || !Y[l] || !mean[l] || !rstd[l] || !aligned16(W[l]) ||
+        (bias[l] && !aligned16(bias[l])) || !aligned16(gamma[l]) || !aligned16(beta[l]) || !aligned16(Z[l]) ||
+        !aligned16(Y[l]))
+      return ppo::set_error(PPO_ERR_ARG, "ppo_mlp_ln_fwd_f32: layer %d needs 16-byte aligned buffers", l);
+    a.W[l] = W[l]; a.bias[l] = bias[l]; a.gamma[l] = gamma[l]; a.beta[l] = beta[l];
+    a.Z[l] = Z[l]; a.Y[l] = Y[l]; a.mean[l] = mean[l]; a.rstd[l] = rstd[l];
+  }
+  const bool va = aligned16(X) && ldx % 4 == 0 && K0 % 4 == 0 && (towers == 1 || stride_x % 4 == 0);
+  const dim3 grid(ppo::ceil_div(M, MC_ROWS), towers), block(MC_THREADS);
+  if (va)
+    hipLaunchKernelGGL(mlp_ln_fwd_kernel<true>, grid, block, 0, ppo::as_stream(stream), a);
+  else
+    hipLaunchKernelGGL(mlp_ln_fwd_kernel<false>, grid, block, 0, ppo::as_stream(stream), a);
+  return ppo::check_launch("ppo_mlp_ln_fwd_f32");
+}
+
+PPO_EXPORT int ppo_mlp_ln_bwd_blocks(int rows) { return rows > 0 ? ppo::ceil_div(rows, MC_ROWS) : 0; }
+
+// Backward of the same chain: from the last layer's output cotangent dY,
+// each layer's LayerNorm + activation backward (dZ, and the scale | bias
+// gradient partials of each 16-row block) and, below the top, the input
+// cotangent dZ W^T through the transposed kernels WT[l] (l >= 1).
+PPO_EXPORT int ppo_mlp_ln_bwd_f32(void* stream, int towers, int L, const float* dY, int64_t lddy, int M,
+                                 const float* const* Z, const float* const* mean, const float* const* rstd,
+                                 const float* const* gamma, const float* const* beta, const float* const* WT,
+                                 int64_t ldwt, float* const* dZ, int64_t ld, float* const* partial, int act,
+                                 int64_t stride_rows, int64_t stride_stats, int64_t stride_params,
+                                 int64_t stride_wt, int64_t stride_part) {
+  if (towers < 1 || towers > 8 || L < 1 || L > MC_MAXL || M < 0 || act < 0 || act > 3 || lddy < MC_F ||
+      ld < MC_F || ldwt < MC_F || !dY || !Z || !mean || !rstd || !gamma || !beta || !WT || !dZ || !partial ||
+      lddy % 4 || ld % 4 || ldwt % 4 ||
+      (towers > 1 && (stride_rows % 4 || stride_params % 4 || stride_wt % 4 || stride_part % 4)))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_mlp_ln_bwd_f32: bad argument (towers=%d L=%d M=%d)", towers, L, M);
+  if (M == 0) return PPO_OK;
+  BwdArgs a{};
+  a.dY = dY; a.lddy = lddy; a.M = M; a.L = L; a.act = act; a.ld = ld; a.ldwt = ldwt;
+  a.tR = stride_rows; a.tS = stride_stats; a.tP = stride_params; a.tWT = stride_wt; a.tPart = stride_part;
+  if (!aligned16(dY)) return ppo::set_error(PPO_ERR_ARG, "ppo_mlp_ln_bwd_f32: dY needs 16-byte rows");
+  for (int l = 0; l < L; ++l) {
+    if (!Z[l] || !mean[l] || !rstd[l] || !gamma[l] || !beta[l] || !dZ[l] || !partial[l] || (l > 0 && !WT[l]) ||
+        !aligned16(Z[l]) || !aligned16(gamma[l]) || !aligned16(beta[l]) || !aligned16(dZ[l]) ||
+        !aligned16(partial[l]) || (l > 0 && !aligned16(WT[l])))
+      return ppo::set_error(PPO_ERR_ARG, "ppo_mlp_ln_bwd_f32: layer %d needs 16-byte aligned buffers", l);
+    a.Z[l] = Z[l]; a.mean[l] = mean[l]; a.rstd[l] = rstd[l]; a.gamma[l] = gamma[l]; a.beta[l] = beta[l];
+    a.WT[l] = l > 0 ? WT[l] : nullptr; a.dZ[l] = dZ[l]; a.part[l] = partial[l];
+  }
+  const dim3 grid(ppo::ceil_div(M, MC_ROWS), towers), block(MC_THREADS);
+  hipLaunchKernelGGL(mlp_ln_bwd_kernel, grid, block, 0, ppo::as_stream(stream), a);
+  return ppo::check_launch("ppo_mlp_ln_bwd_f32");
+}
+
+// dst[b] = src[b]^T for n <= 16 row-major [rows][cols] matrices (pitches lds, ldd).
+PPO_EXPORT int ppo_transpose_f32_batched(void* stream, int n, const float* const* src, float* const* dst, int rows,
+                                        int cols, int64_t lds, int64_t ldd) {
+  if (n < 0 || n > 2 * MC_MAXL || rows < 0 || cols < 0 || lds < cols || ldd < rows || (n > 0 && (!src || !dst)))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_transpose_f32_batched: bad argument (n=%d rows=%d cols=%d)", n, rows,
+                          cols);
+  if (n == 0 || rows == 0 || cols == 0) return PPO_OK;
+  TransposeArgs a{};
+  a.rows = rows; a.cols = cols; a.lds = lds; a.ldd = ldd;
+  for (int b = 0; b < n; ++b) {
+    if (!src[b] || !dst[b]) return ppo::set_error(PPO_ERR_ARG, "ppo_transpose_f32_batched: null matrix %d", b);
+    a.src[b] = src[b];
+    a.dst[b] = dst[b];
+  }
+  const dim3 grid(ppo::ceil_div(cols, 32), ppo::ceil_div(rows, 32), n);
+  hipLaunchKernelGGL(transpose_kernel, grid, dim3(256), 0, ppo::as_stream(stream), a);
+  return ppo::check_launch("ppo_transpose_f32_batched");
+}

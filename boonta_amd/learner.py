@@ -298,11 +298,12 @@ def split_forward_bufs(lb: LayerBufs, rows: int, device, bf16: bool) -> None:
             lb.W16 = torch.zeros(d.fin, d.w.ld, dtype=torch.int16, device=device)
 
 
-def paired_train_bufs(sa: LayerSpec, sc: LayerSpec, rows: int, device) -> tuple:
+def paired_train_bufs(sa: LayerSpec, sc: LayerSpec, rows: int, device, ln_blocks: int | None = None) -> tuple:
     """Training buffers of two layers of one shape (an actor and a critic
     tower at one depth) as the two halves of [2, ...] tensors: each of the
     critic's buffers sits one fixed stride after the actor's, which is what a
-    tower-batched launch addresses."""
+    tower-batched launch addresses.  ``ln_blocks``: LayerNorm partial blocks
+    of the backward that writes them (default: the row kernel's)."""
     f32 = dict(dtype=torch.float32, device=device)
     ld, fin = sa.ld, sa.dense.fin
 
@@ -318,7 +319,7 @@ def paired_train_bufs(sa: LayerSpec, sc: LayerSpec, rows: int, device) -> tuple:
         a.mean, c.mean = two(rows)
         a.rstd, c.rstd = two(rows)
         a.dY, c.dY = two(rows, ld)
-        a.lnblocks = c.lnblocks = _lib.load().ppo_layernorm_bwd_blocks(rows)
+        a.lnblocks = c.lnblocks = ln_blocks if ln_blocks else _lib.load().ppo_layernorm_bwd_blocks(rows)
         a.lnpart, c.lnpart = two(a.lnblocks, 2 * sa.fout)
     elif sa.act == "silu":
         a.PRE, c.PRE = two(rows, ld)
@@ -507,8 +508,13 @@ class MLPExecutor(ForwardChain):
         # separate torsos) run each depth's forward, LayerNorm backward, dW
         # and input-cotangent contraction for both towers in one launch
         self.pair = self._pair_stride(program)
+        # towers of 256-wide LayerNorm layers (one activation, one epsilon)
+        # run each direction of the whole torso chain in one launch
+        self.chain_ln = bool(self.pair) and self.CHAIN and self._chainable(program.actor_layers)
         if self.pair:
-            pairs = [paired_train_bufs(a, c, mb, dev) for a, c in zip(program.actor_layers, program.critic_layers)]
+            lnb = _lib.load().ppo_mlp_ln_bwd_blocks(mb) if self.chain_ln else None
+            pairs = [paired_train_bufs(a, c, mb, dev, lnb)
+                     for a, c in zip(program.actor_layers, program.critic_layers)]
             self.actor = [a for a, _ in pairs]
             self.critic = [c for _, c in pairs]
         else:
@@ -553,6 +559,10 @@ class MLPExecutor(ForwardChain):
                             (program.trunk if program.shared_head else program.critic_layers)]
         if self.boot_layers and program.gru is None:
             split_forward_bufs(self.boot_layers[0], self._boot_rows(), dev, self.bf16)
+        if self.chain_ln:
+            L = len(self.actor)
+            self.WT = torch.zeros(max(L - 1, 1), 2, 256, 256, **f32)
+            self._chain_tables()
         ha, hc = program.head_a, program.head_c
         lib = _lib.load()
         self.fused = self._can_fuse(program)
@@ -648,6 +658,68 @@ class MLPExecutor(ForwardChain):
             na = program.head_out
         return (na <= lib.ppo_head_loss_max_outputs() and ha.fin <= lib.ppo_head_loss_max_features()
                 and ha.fin % 16 == 0)
+
+    CHAIN = True  # paired LayerNorm towers run whole-chain launches
+
+    @staticmethod
+    def _chainable(layers) -> bool:
+        """Layers the whole-chain launches take: 1 to ppo_mlp_chain_max_layers()
+        Dense(256) -> LayerNorm -> activation layers of one activation and
+        epsilon, 256-element rows."""
+        if not layers or len(layers) > _lib.load().ppo_mlp_chain_max_layers():
+            return False
+        s0 = layers[0]
+        return all(s.ln is not None and s.fout == 256 and s.ld == 256 and s.act == s0.act
+                   and s.ln["eps"] == s0.ln["eps"] and s.dense.w.ld == 256 for s in layers)
+
+    def _chain_tables(self):
+        """Per-layer pointer tables of the chain launches (ctypes arrays kept
+        alive on the executor; the pointers are fixed for its lifetime)."""
+        view = self.flat.view
+        A, C = self.actor, self.critic
+        specs = [lb.spec for lb in A]
+        L = len(A)
+        arr = lambda xs: (ctypes.c_void_p * len(xs))(*xs)
+        T = {}
+        T["W"] = arr([view(s.dense.w) for s in specs])
+        T["b"] = arr([view(s.dense.b) if s.dense.b is not None else None for s in specs])
+        T["g"] = arr([view(s.ln["scale"]) for s in specs])
+        T["be"] = arr([view(s.ln["bias"]) for s in specs])
+        T["Z"] = arr([_p(lb.Z) for lb in A])
+        T["Y"] = arr([_p(lb.Y) for lb in A])
+        T["mean"] = arr([_p(lb.mean) for lb in A])
+        T["rstd"] = arr([_p(lb.rstd) for lb in A])
+        T["dZ"] = arr([_p(lb.dZ) for lb in A])
+        T["part"] = arr([_p(lb.lnpart) for lb in A])
+        T["WT"] = arr([None] + [_p(self.WT[l - 1, 0]) for l in range(1, L)])
+        # the transposes: layer l >= 1 of each tower into WT[l - 1, tower]
+        src, dst = [], []
+        for l in range(1, L):
+            for t in range(2):
+                src.append(view(specs[l].dense.w) + 4 * t * self.pair)
+                dst.append(_p(self.WT[l - 1, t]))
+        T["tsrc"], T["tdst"], T["nT"] = arr(src), arr(dst), len(src)
+        boot = self.boot_layers
+        cspecs = [lb.spec for lb in boot]
+        T["bW"] = arr([view(s.dense.w) for s in cspecs])
+        T["bb"] = arr([view(s.dense.b) if s.dense.b is not None else None for s in cspecs])
+        T["bg"] = arr([view(s.ln["scale"]) for s in cspecs])
+        T["bbe"] = arr([view(s.ln["bias"]) for s in cspecs])
+        T["bZ"] = arr([_p(lb.Z) for lb in boot])
+        T["bY"] = arr([_p(lb.Y) for lb in boot])
+        T["bmean"] = arr([_p(lb.mean) for lb in boot])
+        T["brstd"] = arr([_p(lb.rstd) for lb in boot])
+        addr = lambda a: ctypes.cast(a, ctypes.c_void_p).value
+        self._chain_keep = T
+        self._chain = {k: (addr(v) if isinstance(v, ctypes.Array) else v) for k, v in T.items()}
+        s0 = specs[0]
+        self._chain_act, self._chain_eps = _act(s0.act), float(s0.ln["eps"])
+        self._chain_rs = _tstride(A[0].Y, C[0].Y)
+        self._chain_ss = _tstride(A[0].mean, C[0].mean)
+        self._chain_ps = _tstride(A[0].lnpart, C[0].lnpart)
+        assert all(_tstride(a.Z, c.Z) == self._chain_rs == _tstride(a.dZ, c.dZ) == _tstride(a.Y, c.Y)
+                   and _tstride(a.mean, c.mean) == self._chain_ss == _tstride(a.rstd, c.rstd)
+                   and _tstride(a.lnpart, c.lnpart) == self._chain_ps for a, c in zip(A, C))
 
     def _pair_stride(self, program: Program) -> int:
         """Element offset from every parameter region of the actor tower to the
@@ -793,10 +865,27 @@ class MLPExecutor(ForwardChain):
                               dst, layers[i - 1].spec.ld, self.mb, d.fin, s.ld, 1, 0, epi, None, act, None, aux,
                               ldaux, None, -1)
 
+    def _fwd_boot_chain(self, st, x, ldx, nrows):
+        """The critic tower's forward for the bootstrap rows in one launch."""
+        c, boot = self._chain, self.boot_layers
+        s0 = boot[0].spec
+        self._call("ppo_mlp_ln_fwd_f32", st, 1, len(boot), x, ldx, None, nrows, s0.dense.fin, c["bW"],
+                   s0.dense.w.ld, 256, c["bb"], c["bg"], c["bbe"], c["bZ"], c["bY"], s0.ld, c["bmean"], c["brstd"],
+                   self._chain_eps, self._chain_act, 0, 0, 0, 0)
+        return _p(boot[-1].Y), boot[-1].spec.ld
+
     def _fwd_pair(self, st, x, ldx, rows_idx, nrows):
         """Forward of the actor (tower 0) and critic (tower 1) towers, one
         launch per depth; both first layers read the same input rows."""
         D, sx = self.pair, 0
+        if self.chain_ln:
+            c, s0 = self._chain, self.actor[0].spec
+            # the kernels' transposed images for this step's backward
+            self._call("ppo_transpose_f32_batched", st, c["nT"], c["tsrc"], c["tdst"], 256, 256, 256, 256)
+            self._call("ppo_mlp_ln_fwd_f32", st, 2, len(self.actor), x, ldx, rows_idx, nrows, s0.dense.fin, c["W"],
+                       s0.dense.w.ld, 256, c["b"], c["g"], c["be"], c["Z"], c["Y"], s0.ld, c["mean"], c["rstd"],
+                       self._chain_eps, self._chain_act, 0, D, self._chain_rs, self._chain_ss)
+            return
         for la, lc in zip(self.actor, self.critic):
             s = la.spec
             d = s.dense
@@ -818,6 +907,11 @@ class MLPExecutor(ForwardChain):
         """Backward of the actor and critic towers, one launch per depth and
         contraction, once both last-layer output cotangents are in place."""
         D, A, C = self.pair, self.actor, self.critic
+        if self.chain_ln:
+            c = self._chain
+            self._call("ppo_mlp_ln_bwd_f32", st, 2, len(A), _p(A[-1].dY), A[-1].spec.ld, self.mb, c["Z"], c["mean"],
+                       c["rstd"], c["g"], c["be"], c["WT"], 256, c["dZ"], A[0].spec.ld, c["part"], self._chain_act,
+                       self._chain_rs, self._chain_ss, D, 256 * 256, self._chain_ps)
         for i in range(len(A) - 1, -1, -1):
             la, lc = A[i], C[i]
             s = la.spec
@@ -827,7 +921,7 @@ class MLPExecutor(ForwardChain):
             else:
                 x, ldx, ridx, sx = x0, ldx0, idx0, 0
             rs = _tstride(la.dZ, lc.dZ)
-            if s.ln is not None:
+            if s.ln is not None and not self.chain_ln:
                 self._call("ppo_layernorm_act_bwd_f32_towers", st, 2, _p(la.dY), s.ld, _p(la.Z), s.ld, _p(la.mean),
                            _p(la.rstd), self.flat.view(s.ln["scale"]), self.flat.view(s.ln["bias"]), _p(la.dZ),
                            s.ld, _p(la.lnpart), self.mb, s.fout, _act(s.act), rs, _tstride(la.mean, lc.mean), D,
@@ -836,7 +930,7 @@ class MLPExecutor(ForwardChain):
                        d.fin, s.ld, self.mb, la.splits, d.fin * s.ld, EPI_STORE, None, 0, None, None, 0,
                        _p(la.bpart), -1, sx, rs, _tstride(la.wpart, lc.wpart), 0, 0, 0,
                        _tstride(la.bpart, lc.bpart))
-            if i > 0:
+            if i > 0 and not self.chain_ln:
                 dst, epi, act, aux, ldaux = self._dx_target(A[i - 1])
                 dst_c, _, _, aux_c, _ = self._dx_target(C[i - 1])
                 self._call("ppo_gemm_f32_towers", st, 2, A_ROW, B_NK, _p(la.dZ), s.ld, None, self.flat.view(d.w),
@@ -905,7 +999,10 @@ class MLPExecutor(ForwardChain):
                       h.w.ld, N, h.w.ld, h.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(h.b), 0, None, None, 0, None, -1)
             vcol = prog.head_out
         else:
-            x, ldx, _ = self._fwd_layers(st, self.boot_layers, x, ldx, None, N)
+            if self.chain_ln:
+                x, ldx = self._fwd_boot_chain(st, x, ldx, N)
+            else:
+                x, ldx, _ = self._fwd_layers(st, self.boot_layers, x, ldx, None, N)
             h = prog.head_c
             self._gemm(st, A_ROW, B_KN, x, ldx, None, self.flat.view(h.w), h.w.ld, _p(self.HEADB),
                       h.w.ld, N, h.w.ld, h.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(h.b), 0, None, None, 0, None, -1)

@@ -177,19 +177,28 @@ class _TwoStreams(MLPExecutor):
         return 0
 
 
+class _PerLayer(MLPExecutor):
+    """Paired towers issued layer by layer (the whole-chain launches off)."""
+    CHAIN = False
+
+
 class _TwoStreamsPPO(PPO):
     executor_class = _TwoStreams
+
+
+class _PerLayerPPO(PPO):
+    executor_class = _PerLayer
 
 
 @pytest.mark.parametrize("use_graph", [False, True])
 def test_paired_towers_update_equals_two_stream_update(use_graph):
     r, plan, params, tr, roll = make_case(config=3, T=8, N=128, M=4, E=2)
     results = []
-    for cls in (PPO, _TwoStreamsPPO):
+    for cls in (_PerLayerPPO, _TwoStreamsPPO):
         alg = cls(cfg=r.cfg, network=r.network, optimizer=r.optimizer, use_graph=use_graph)
         state = alg.init_from_params({"params": params}, r.obs_dim)
         ex = alg.executor(state, r.T, r.N, r.obs_dim)
-        assert bool(ex.pair) == (cls is PPO)
+        assert bool(ex.pair) == (cls is _PerLayerPPO) and not ex.chain_ln
         trans = device_transition(tr, roll)
         for k in (1, 2):
             alg.update(state, make_key(k), trans)
@@ -197,3 +206,176 @@ def test_paired_towers_update_equals_two_stream_update(use_graph):
         results.append((flat_state_of(state).P.cpu().numpy().copy(), ex.LOGS.cpu().numpy().copy()))
     np.testing.assert_array_equal(results[0][0], results[1][0])
     np.testing.assert_array_equal(results[0][1], results[1][1])
+
+
+# ------------------------------------------------------ whole torso chains
+def chain_case(g, towers, L, M, K0, gather):
+    """Random parameters of `towers` towers of L Dense(256) + LayerNorm layers,
+    each tower's parameters in one block (W0 | b0 | gamma0 | beta0 | W1 | ...),
+    tower t one block after tower 0."""
+    F = 256
+    sizes = [(K0 if l == 0 else F) * F + 3 * F for l in range(L)]
+    block = sum(sizes)
+    P = torch.from_numpy((g.standard_normal((towers, block)) * 0.05).astype(np.float32)).cuda()
+    offs, o = [], 0
+    for l in range(L):
+        K = K0 if l == 0 else F
+        offs.append(dict(W=o, b=o + K * F, g=o + K * F + F, be=o + K * F + 2 * F, K=K))
+        o += sizes[l]
+    for t in range(towers):
+        for d in offs:
+            P[t, d["g"]:d["g"] + F] += 1.0
+    src = M + 30
+    X = torch.from_numpy(g.standard_normal((src, K0)).astype(np.float32)).cuda()
+    I = torch.from_numpy(g.permutation(src)[:M].astype(np.int32)).cuda() if gather else None
+    return P, offs, X, I, block
+
+
+def ptrs(xs):
+    import ctypes
+    a = (ctypes.c_void_p * len(xs))(*xs)
+    return a, ctypes.cast(a, ctypes.c_void_p).value
+
+
+@pytest.mark.parametrize("towers,L,M,K0,gather,act", [(2, 4, 2048, 87, True, 3), (1, 4, 4096, 87, False, 3),
+                                                      (2, 3, 300, 256, False, 1), (2, 1, 17, 64, True, 2),
+                                                      (2, 2, 33, 100, False, 0)])
+def test_forward_chain_equals_one_fused_launch_per_layer(towers, L, M, K0, gather, act):
+    g = np.random.default_rng(M + 7 * L + K0)
+    F = 256
+    P, offs, X, I, block = chain_case(g, towers, L, M, K0, gather)
+    Z = torch.full((L, towers, M, F), 9.0, device="cuda")
+    Y, mean, rstd = torch.full_like(Z, 9.0), torch.full((L, towers, M), 9.0, device="cuda"), \
+        torch.full((L, towers, M), 9.0, device="cuda")
+    Zs, Ys, ms, rs = (torch.full_like(t, 7.0) for t in (Z, Y, mean, rstd))
+    base = P.data_ptr()
+    at = lambda key: [base + 4 * d[key] for d in offs]
+    keep = [ptrs(at("W")), ptrs(at("b")), ptrs(at("g")), ptrs(at("be")), ptrs([Z[l, 0].data_ptr() for l in range(L)]),
+            ptrs([Y[l, 0].data_ptr() for l in range(L)]), ptrs([mean[l, 0].data_ptr() for l in range(L)]),
+            ptrs([rstd[l, 0].data_ptr() for l in range(L)])]
+    a = [k[1] for k in keep]
+    _lib.call("ppo_mlp_ln_fwd_f32", st(), towers, L, X.data_ptr(), K0, p(I), M, K0, a[0], F, F, a[1], a[2], a[3],
+              a[4], a[5], F, a[6], a[7], 1e-6, act, 0, block, M * F, M)
+    for t in range(towers):
+        x, ldx, idx = X.data_ptr(), K0, p(I)
+        for l, d in enumerate(offs):
+            o = base + 4 * t * block
+            _lib.call("ppo_gemm_ln_act_fwd_f32", st(), x, ldx, idx, o + 4 * d["W"], F, o + 4 * d["b"],
+                      o + 4 * d["g"], o + 4 * d["be"], Zs[l, t].data_ptr(), F, Ys[l, t].data_ptr(), F,
+                      ms[l, t].data_ptr(), rs[l, t].data_ptr(), M, d["K"], F, 1e-6, act)
+            x, ldx, idx = Ys[l, t].data_ptr(), F, 0
+    torch.cuda.synchronize()
+    for a_, b_ in ((Z, Zs), (Y, Ys), (mean, ms), (rstd, rs)):
+        assert torch.equal(a_, b_)
+
+
+def torch_tower(P, offs, X, I, t, block, act, eps=1e-6):
+    """float64 torch forward of tower t with every Z kept for its gradient."""
+    F = 256
+    Pd = P[t].double()
+    x = (X[I.long()] if I is not None else X).double()
+    acts = {0: lambda u: u, 1: torch.relu, 2: torch.tanh, 3: torch.nn.functional.silu}
+    Zs, params = [], []
+    for d in offs:
+        W = Pd[d["W"]:d["W"] + d["K"] * F].view(d["K"], F).clone().requires_grad_(True)
+        b = Pd[d["b"]:d["b"] + F]
+        gam = Pd[d["g"]:d["g"] + F].clone().requires_grad_(True)
+        bet = Pd[d["be"]:d["be"] + F].clone().requires_grad_(True)
+        z = x @ W + b
+        z.retain_grad()
+        mu = z.mean(-1, keepdim=True)
+        var = (z * z).mean(-1, keepdim=True) - mu * mu
+        x = acts[act]((z - mu) * torch.rsqrt(var.clamp_min(0) + eps) * gam + bet)
+        Zs.append(z)
+        params.append((W, gam, bet))
+    return x, Zs, params
+
+
+@pytest.mark.parametrize("towers,L,M,act", [(2, 4, 2048, 3), (2, 3, 300, 1), (1, 2, 50, 2), (2, 1, 16, 0)])
+def test_backward_chain_matches_float64_autograd(towers, L, M, act):
+    """dZ of every layer and the LayerNorm scale / bias gradients (sum of the
+    16-row block partials) against torch float64 autograd through the same
+    tower, from the same float32 forward buffers; 1e-5 relative (L2)."""
+    g = np.random.default_rng(M * 3 + L)
+    F, K0 = 256, 87
+    P, offs, X, I, block = chain_case(g, towers, L, M, K0, True)
+    lib = _lib.load()
+    Z = torch.zeros(L, towers, M, F, device="cuda")
+    Y, mean, rstd = torch.zeros_like(Z), torch.zeros(L, towers, M, device="cuda"), \
+        torch.zeros(L, towers, M, device="cuda")
+    base = P.data_ptr()
+    at = lambda key: [base + 4 * d[key] for d in offs]
+    lay = lambda T_: [T_[l, 0].data_ptr() for l in range(L)]
+    keep = [ptrs(at(k)) for k in ("W", "b", "g", "be")] + [ptrs(lay(T_)) for T_ in (Z, Y, mean, rstd)]
+    a = [k[1] for k in keep]
+    _lib.call("ppo_mlp_ln_fwd_f32", st(), towers, L, X.data_ptr(), K0, p(I), M, K0, a[0], F, F, a[1], a[2], a[3],
+              a[4], a[5], F, a[6], a[7], 1e-6, act, 0, block, M * F, M)
+    # transposed kernels of layers 1..L-1
+    WT = torch.zeros(max(L - 1, 1), towers, F, F, device="cuda")
+    src = [base + 4 * (t * block + offs[l]["W"]) for l in range(1, L) for t in range(towers)]
+    dst = [WT[l - 1, t].data_ptr() for l in range(1, L) for t in range(towers)]
+    ks, kd = ptrs(src or [0]), ptrs(dst or [0])
+    _lib.call("ppo_transpose_f32_batched", st(), len(src), ks[1], kd[1], F, F, F, F)
+    dY = torch.from_numpy(g.standard_normal((towers, M, F)).astype(np.float32)).cuda()
+    dZ = torch.full((L, towers, M, F), 5.0, device="cuda")
+    blocks = lib.ppo_mlp_ln_bwd_blocks(M)
+    part = torch.full((L, towers, blocks, 2 * F), 5.0, device="cuda")
+    kb = [ptrs(lay(T_)) for T_ in (Z, mean, rstd)] + [ptrs(at("g")), ptrs(at("be")),
+                                                      ptrs([0] + [WT[l - 1, 0].data_ptr() for l in range(1, L)]),
+                                                      ptrs(lay(dZ)), ptrs(lay(part))]
+    b = [k[1] for k in kb]
+    _lib.call("ppo_mlp_ln_bwd_f32", st(), towers, L, dY.data_ptr(), F, M, b[0], b[1], b[2], b[3], b[4], b[5], F,
+              b[6], F, b[7], act, M * F, M, block, F * F, blocks * 2 * F)
+    torch.cuda.synchronize()
+    for t in range(towers):
+        out, Zs, params = torch_tower(P, offs, X, I, t, block, act)
+        # the chain's forward matches the float64 one; the backward starts
+        # from the same cotangent
+        assert float((Y[L - 1, t].double() - out).norm() / out.norm()) < 1e-5
+        out.backward(dY[t].double())
+        for l in range(L):
+            ref = Zs[l].grad
+            got = dZ[l, t].double()
+            assert float((got - ref).norm() / ref.norm()) < 1e-5, (t, l)
+            _, gam, bet = params[l]
+            tot = part[l, t].double().sum(0)
+            assert float((tot[:F] - gam.grad).norm() / gam.grad.norm()) < 1e-5, (t, l, "scale")
+            assert float((tot[F:] - bet.grad).norm() / bet.grad.norm()) < 1e-5, (t, l, "bias")
+
+
+def test_batched_transpose_is_exact():
+    g = np.random.default_rng(3)
+    mats = [torch.from_numpy(g.standard_normal((r, c)).astype(np.float32)).cuda() for r, c in ((256, 256),) * 3]
+    outs = [torch.zeros(256, 256, device="cuda") for _ in mats]
+    ks, kd = ptrs([m.data_ptr() for m in mats]), ptrs([o.data_ptr() for o in outs])
+    _lib.call("ppo_transpose_f32_batched", st(), 3, ks[1], kd[1], 256, 256, 256, 256)
+    A = torch.from_numpy(g.standard_normal((70, 45)).astype(np.float32)).cuda()
+    B = torch.zeros(45, 72, device="cuda")
+    ka, kb = ptrs([A.data_ptr()]), ptrs([B.data_ptr()])
+    _lib.call("ppo_transpose_f32_batched", st(), 1, ka[1], kb[1], 70, 45, 45, 72)
+    torch.cuda.synchronize()
+    for m, o in zip(mats, outs):
+        assert torch.equal(o, m.t())
+    assert torch.equal(B[:, :70], A.t())
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_chain_update_matches_the_per_layer_update(use_graph):
+    """The whole update with the chain launches against the same update issued
+    layer by layer (equal but for float32 summation order in the backward):
+    parameters after two updates 1e-5 relative (L2), the logged losses 1e-4."""
+    r, plan, params, tr, roll = make_case(config=3, T=8, N=128, M=4, E=2)
+    results = []
+    for cls in (PPO, _PerLayerPPO):
+        alg = cls(cfg=r.cfg, network=r.network, optimizer=r.optimizer, use_graph=use_graph)
+        state = alg.init_from_params({"params": params}, r.obs_dim)
+        ex = alg.executor(state, r.T, r.N, r.obs_dim)
+        assert ex.chain_ln == (cls is PPO)
+        trans = device_transition(tr, roll)
+        for k in (1, 2):
+            alg.update(state, make_key(k), trans)
+        torch.cuda.synchronize()
+        results.append((flat_state_of(state).P.cpu().double(), ex.LOGS.cpu().double()))
+    (pa, la), (pb, lb) = results
+    assert float((pa - pb).norm() / pb.norm()) < 1e-5
+    np.testing.assert_allclose(la.numpy(), lb.numpy(), rtol=1e-4, atol=1e-6)

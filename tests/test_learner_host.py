@@ -165,12 +165,67 @@ def test_rollout_step_launches_match_the_c_signatures(config):
         assert fused.fused == (config == 2), "only the discrete Anakin network fits the one-launch step"
 
 
-def test_gaussian_update_fuses_dense_and_layernorm_forward():
+class PerLayerExecutor(MLPExecutor):
+    """Paired towers issued layer by layer (the whole-chain launches off)."""
+    CHAIN = False
+
+
+def test_gaussian_update_runs_each_torso_chain_in_one_launch():
     r = small(3)
     prog = Program(r.network.plan(r.obs_dim))
     flat = FlatState(prog, torch.device("cpu"))
     ex = executor(r, prog, flat)
     ex.bind(fake_inputs(ex))
+    assert ex.chain_ln
+    names = [n for n, _ in ex.record()]
+    steps = r.cfg.update_epochs * r.cfg.num_minibatches
+    # per minibatch step: the transposed kernel images, the forward chain of
+    # both towers, the fused heads + loss, the backward chain and the four
+    # tower-batched dW contractions; the critic's bootstrap chain once
+    assert names.count("ppo_transpose_f32_batched") == steps
+    assert names.count("ppo_mlp_ln_fwd_f32") == steps + 1
+    assert names.count("ppo_mlp_ln_bwd_f32") == steps
+    assert names.count("ppo_gemm_f32_towers") == 4 * steps
+    assert names.count("ppo_gemm_f32") == 1   # the bootstrap value head
+    for gone in ("ppo_gemm_ln_act_fwd_f32", "ppo_gemm_ln_act_fwd_f32_towers", "ppo_layernorm_act_fwd_f32",
+                 "ppo_layernorm_act_bwd_f32", "ppo_layernorm_act_bwd_f32_towers", "ppo_stream_wait"):
+        assert gone not in names, gone
+    # every table entry is the actor's pointer, and it plus the tower stride
+    # is the critic's pointer of the same layer
+    T = ex._chain_keep
+    D = ex.pair
+    for l, (a, c) in enumerate(zip(ex.actor, ex.critic)):
+        s = a.spec
+        assert T["W"][l] == flat.view(s.dense.w) and T["W"][l] + 4 * D == flat.view(c.spec.dense.w)
+        assert T["g"][l] + 4 * D == flat.view(c.spec.ln["scale"])
+        assert T["be"][l] + 4 * D == flat.view(c.spec.ln["bias"])
+        assert T["b"][l] + 4 * D == flat.view(c.spec.dense.b)
+        for key, attr, stride in (("Z", "Z", ex._chain_rs), ("Y", "Y", ex._chain_rs), ("dZ", "dZ", ex._chain_rs),
+                                  ("mean", "mean", ex._chain_ss), ("rstd", "rstd", ex._chain_ss),
+                                  ("part", "lnpart", ex._chain_ps)):
+            assert T[key][l] == getattr(a, attr).data_ptr(), key
+            assert T[key][l] + 4 * stride == getattr(c, attr).data_ptr(), key
+        assert a.lnpart.shape[0] == _lib.load().ppo_mlp_ln_bwd_blocks(ex.mb)
+    # the transposes read each tower's kernel of layers 1.. into WT[layer - 1, tower]
+    assert T["nT"] == 2 * (len(ex.actor) - 1)
+    k = 0
+    for l in range(1, len(ex.actor)):
+        for t, lb in enumerate((ex.actor[l], ex.critic[l])):
+            assert T["tsrc"][k] == flat.view(lb.spec.dense.w) and T["tdst"][k] == ex.WT[l - 1, t].data_ptr()
+            k += 1
+        assert T["WT"][l] == ex.WT[l - 1, 0].data_ptr()
+    # the bootstrap chain runs the critic's own layers
+    for l, lb in enumerate(ex.boot_layers):
+        assert T["bW"][l] == flat.view(ex.critic[l].spec.dense.w) and T["bY"][l] == lb.Y.data_ptr()
+
+
+def test_gaussian_update_pairs_its_towers_layer_by_layer():
+    r = small(3)
+    prog = Program(r.network.plan(r.obs_dim))
+    flat = FlatState(prog, torch.device("cpu"))
+    ex = PerLayerExecutor(prog, flat, r.cfg, r.optimizer, r.T, r.N)
+    ex.bind(fake_inputs(ex))
+    assert not ex.chain_ln
     calls = ex.record()
     names = [n for n, _ in calls]
     steps = r.cfg.update_epochs * r.cfg.num_minibatches
