@@ -148,6 +148,24 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// LayerNorm arithmetic of the 256-wide fused kernels (Dense + LayerNorm
+// forward, the torso chains forward and backward), with every rounding
+// step explicit so that kernels compiled apart produce the same bits:
+// a row's partial sums (z, then z * z by one fma), its statistics from the
+// sums (fast variance, as flax) and the normalised, scaled value.
+__device__ __forceinline__ void ln_accum(float z, float& s, float& s2) {
+  s += z;
+  s2 = __fmaf_rn(z, z, s2);
+}
+__device__ __forceinline__ void ln_stats256(float s, float s2, float eps, float& mean, float& rstd) {
+  mean = s * (1.f / 256.f);
+  const float var = fmaxf(__fmaf_rn(-mean, mean, s2 * (1.f / 256.f)), 0.f);
+  rstd = rsqrtf(var + eps);
+}
+__device__ __forceinline__ float ln_apply(float z, float mean, float rstd, float gamma, float beta) {
+  return __fmaf_rn(z - mean, rstd * gamma, beta);
+}
+
 __device__ __forceinline__ float act_fwd(int act, float x) {
   switch (act) {
     case ACT_RELU: return x > 0.f ? x : 0.f;

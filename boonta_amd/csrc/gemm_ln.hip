@@ -148,8 +148,7 @@ __global__ void __launch_bounds__(GL_THREADS) gemm_ln_fwd_kernel(GemmLnArgs p0) 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       z[v][j] = acc[j][v] + bias4[j];
-      ps[v] += z[v][j];
-      pq[v] += z[v][j] * z[v][j];
+      ppo::ln_accum(z[v][j], ps[v], pq[v]);
     }
 #pragma unroll
     for (int o = 8; o; o >>= 1) {
@@ -173,9 +172,8 @@ __global__ void __launch_bounds__(GL_THREADS) gemm_ln_fwd_kernel(GemmLnArgs p0) 
     const int row = r0 + rr;
     const float s = (s_sum[0][rr] + s_sum[1][rr]) + (s_sum[2][rr] + s_sum[3][rr]);
     const float s2 = (s_sq[0][rr] + s_sq[1][rr]) + (s_sq[2][rr] + s_sq[3][rr]);
-    const float mean = s / (float)GL_F;
-    const float var = fmaxf(s2 / (float)GL_F - mean * mean, 0.f);
-    const float rstd = rsqrtf(var + p.eps);
+    float mean, rstd;
+    ppo::ln_stats256(s, s2, p.eps, mean, rstd);
     if (row >= p.M) continue;
     if (wave == 0 && li == 0) {
       p.mean[row] = mean;
@@ -185,7 +183,7 @@ __global__ void __launch_bounds__(GL_THREADS) gemm_ln_fwd_kernel(GemmLnArgs p0) 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       zo[j] = z[v][j];
-      yo[j] = ppo::act_fwd(p.act, (z[v][j] - mean) * (rstd * g4[j]) + be4[j]);
+      yo[j] = ppo::act_fwd(p.act, ppo::ln_apply(z[v][j], mean, rstd, g4[j], be4[j]));
     }
     *reinterpret_cast<floatx4*>(p.Z + (int64_t)row * p.ldz + c4) = zo;
     *reinterpret_cast<floatx4*>(p.Y + (int64_t)row * p.ldy + c4) = yo;

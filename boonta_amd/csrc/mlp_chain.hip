@@ -151,8 +151,7 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         z[v][j] = acc[j][v] + bias4[j];
-        ps[v] += z[v][j];
-        pq[v] += z[v][j] * z[v][j];
+        ppo::ln_accum(z[v][j], ps[v], pq[v]);
       }
 #pragma unroll
       for (int o = 8; o; o >>= 1) {
@@ -179,14 +178,13 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p) {
       const int row = r0 + rr;
       const float s = (s_sum[0][rr] + s_sum[1][rr]) + (s_sum[2][rr] + s_sum[3][rr]);
       const float s2 = (s_sq[0][rr] + s_sq[1][rr]) + (s_sq[2][rr] + s_sq[3][rr]);
-      const float mean = s / (float)MC_F;
-      const float var = fmaxf(s2 / (float)MC_F - mean * mean, 0.f);
-      const float rstd = rsqrtf(var + p.eps);
+      float mean, rstd;
+      ppo::ln_stats256(s, s2, p.eps, mean, rstd);
       floatx4 zo, yo;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         zo[j] = z[v][j];
-        yo[j] = ppo::act_fwd(p.act, (z[v][j] - mean) * (rstd * g4[j]) + be4[j]);
+        yo[j] = ppo::act_fwd(p.act, ppo::ln_apply(z[v][j], mean, rstd, g4[j], be4[j]));
       }
       if (l + 1 < p.L) *reinterpret_cast<floatx4*>(&sX[rr][c4]) = yo;
       if (row >= p.M) continue;
@@ -265,7 +263,8 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_bwd_kernel(BwdArgs p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         xh[v][j] = live ? (zz[j] - mu[v]) * rs[v] : 0.f;
-        const float yl = xh[v][j] * g4[j] + be4[j];
+        // the forward's normalised value, rounded as the forward rounded it
+        const float yl = ppo::ln_apply(zz[j], mu[v], rs[v], g4[j], be4[j]);
         const float a = (p.act == ACT_RELU || p.act == ACT_TANH) ? ppo::act_fwd(p.act, yl) : yl;
         const float dyl = live ? dy[v][j] * ppo::act_grad(p.act, a) : 0.f;
         pg[j] += dyl * xh[v][j];
