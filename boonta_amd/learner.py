@@ -298,35 +298,53 @@ def split_forward_bufs(lb: LayerBufs, rows: int, device, bf16: bool) -> None:
             lb.W16 = torch.zeros(d.fin, d.w.ld, dtype=torch.int16, device=device)
 
 
-def paired_train_bufs(sa: LayerSpec, sc: LayerSpec, rows: int, device, ln_blocks: int | None = None) -> tuple:
-    """Training buffers of two layers of one shape (an actor and a critic
-    tower at one depth) as the two halves of [2, ...] tensors: each of the
-    critic's buffers sits one fixed stride after the actor's, which is what a
-    tower-batched launch addresses.  ``ln_blocks``: LayerNorm partial blocks
+def paired_tower_bufs(specs_a, specs_c, rows: int, device, ln_blocks: int | None = None) -> tuple:
+    """Training buffers of two towers of one shape (actor and critic, layer by
+    layer): each kind of buffer of consecutive layers of one shape is one
+    [layers, 2, ...] tensor, so the critic's buffer sits one fixed stride
+    after the actor's at every depth (what a tower-batched launch addresses)
+    and same-shape layers follow each other at that stride too (what a launch
+    batched over depth addresses).  ``ln_blocks``: LayerNorm partial blocks
     of the backward that writes them (default: the row kernel's)."""
     f32 = dict(dtype=torch.float32, device=device)
-    ld, fin = sa.ld, sa.dense.fin
+    L = len(specs_a)
+    A = [LayerBufs(sa, Y=None) for sa in specs_a]
+    C = [LayerBufs(sc, Y=None) for sc in specs_c]
 
-    def two(*shape):
-        t = torch.zeros(2, *shape, **f32)
-        return t[0], t[1]
+    def alloc(attr, shapes):
+        """Per-layer (actor, critic) views; runs of equal shapes share a tensor."""
+        i = 0
+        while i < L:
+            if shapes[i] is None:
+                i += 1
+                continue
+            j = i
+            while j + 1 < L and shapes[j + 1] == shapes[i]:
+                j += 1
+            t = torch.zeros(j - i + 1, 2, *shapes[i], **f32)
+            for k in range(i, j + 1):
+                setattr(A[k], attr, t[k - i, 0])
+                setattr(C[k], attr, t[k - i, 1])
+            i = j + 1
 
-    a, c = LayerBufs(sa, Y=None), LayerBufs(sc, Y=None)
-    a.Y, c.Y = two(rows, ld)
-    a.dZ, c.dZ = two(rows, ld)
-    if sa.ln is not None:
-        a.Z, c.Z = two(rows, ld)
-        a.mean, c.mean = two(rows)
-        a.rstd, c.rstd = two(rows)
-        a.dY, c.dY = two(rows, ld)
-        a.lnblocks = c.lnblocks = ln_blocks if ln_blocks else _lib.load().ppo_layernorm_bwd_blocks(rows)
-        a.lnpart, c.lnpart = two(a.lnblocks, 2 * sa.fout)
-    elif sa.act == "silu":
-        a.PRE, c.PRE = two(rows, ld)
-    a.splits = c.splits = _splits(rows, fin, ld)
-    a.wpart, c.wpart = two(a.splits, fin, ld)
-    a.bpart, c.bpart = two(a.splits, ld)
-    return a, c
+    lib = _lib.load()
+    ln = [s.ln is not None for s in specs_a]
+    alloc("Y", [(rows, s.ld) for s in specs_a])
+    alloc("dZ", [(rows, s.ld) for s in specs_a])
+    alloc("Z", [(rows, s.ld) if ln[i] else None for i, s in enumerate(specs_a)])
+    alloc("dY", [(rows, s.ld) if ln[i] else None for i, s in enumerate(specs_a)])
+    alloc("mean", [(rows,) if ln[i] else None for i in range(L)])
+    alloc("rstd", [(rows,) if ln[i] else None for i in range(L)])
+    blocks = ln_blocks if ln_blocks else lib.ppo_layernorm_bwd_blocks(rows)
+    alloc("lnpart", [(blocks, 2 * s.fout) if ln[i] else None for i, s in enumerate(specs_a)])
+    alloc("PRE", [(rows, s.ld) if not ln[i] and s.act == "silu" else None for i, s in enumerate(specs_a)])
+    for i, s in enumerate(specs_a):
+        A[i].splits = C[i].splits = _splits(rows, s.dense.fin, s.ld)
+        if ln[i]:
+            A[i].lnblocks = C[i].lnblocks = blocks
+    alloc("wpart", [(a.splits, s.dense.fin, s.ld) for a, s in zip(A, specs_a)])
+    alloc("bpart", [(a.splits, s.ld) for a, s in zip(A, specs_a)])
+    return A, C
 
 
 def _tstride(a, c) -> int:
@@ -513,10 +531,7 @@ class MLPExecutor(ForwardChain):
         self.chain_ln = bool(self.pair) and self.CHAIN and self._chainable(program.actor_layers)
         if self.pair:
             lnb = _lib.load().ppo_mlp_ln_bwd_blocks(mb) if self.chain_ln else None
-            pairs = [paired_train_bufs(a, c, mb, dev, lnb)
-                     for a, c in zip(program.actor_layers, program.critic_layers)]
-            self.actor = [a for a, _ in pairs]
-            self.critic = [c for _, c in pairs]
+            self.actor, self.critic = paired_tower_bufs(program.actor_layers, program.critic_layers, mb, dev, lnb)
         else:
             self.actor = [layer_bufs(s, mb, True) for s in program.actor_layers]
             self.critic = [layer_bufs(s, mb, True) for s in program.critic_layers]
@@ -714,12 +729,36 @@ class MLPExecutor(ForwardChain):
         self._chain = {k: (addr(v) if isinstance(v, ctypes.Array) else v) for k, v in T.items()}
         s0 = specs[0]
         self._chain_act, self._chain_eps = _act(s0.act), float(s0.ln["eps"])
+        self._dw_groups = self._plan_dw_groups()
         self._chain_rs = _tstride(A[0].Y, C[0].Y)
         self._chain_ss = _tstride(A[0].mean, C[0].mean)
         self._chain_ps = _tstride(A[0].lnpart, C[0].lnpart)
         assert all(_tstride(a.Z, c.Z) == self._chain_rs == _tstride(a.dZ, c.dZ) == _tstride(a.Y, c.Y)
                    and _tstride(a.mean, c.mean) == self._chain_ss == _tstride(a.rstd, c.rstd)
                    and _tstride(a.lnpart, c.lnpart) == self._chain_ps for a, c in zip(A, C))
+
+    def _plan_dw_groups(self) -> list:
+        """The weight-gradient contractions of the paired towers as batched
+        launches: layer 0 of both towers (the gathered observation rows
+        shared), then every later layer of both towers in one launch when
+        their operands sit at one stride from problem to problem
+        (layer-major, tower-minor), else layer by layer.  Entries:
+        (first layer, problems, input stride)."""
+        A, C = self.actor, self.critic
+        L = len(A)
+        groups = [(0, 2, 0)]
+        probs = [(i, t) for i in range(1, L) for t in range(2)]
+        if len(probs) >= 2 and len(probs) <= 8:
+            lbs = lambda i, t: (A if t == 0 else C)[i]
+            shapes = {(lbs(i, t).spec.dense.fin, lbs(i, t).spec.ld, lbs(i, t).splits) for i, t in probs}
+            ptrs = [(_p(lbs(i - 1, t).Y), _p(lbs(i, t).dZ), _p(lbs(i, t).wpart), _p(lbs(i, t).bpart))
+                    for i, t in probs]
+            steps = {tuple(b - a for a, b in zip(ptrs[k], ptrs[k + 1])) for k in range(len(ptrs) - 1)}
+            if len(shapes) == 1 and len(steps) == 1:
+                groups.append((1, len(probs), (ptrs[1][0] - ptrs[0][0]) // 4))
+                return groups
+        groups += [(i, 2, _tstride(A[i - 1].Y, C[i - 1].Y)) for i in range(1, L)]
+        return groups
 
     def _pair_stride(self, program: Program) -> int:
         """Element offset from every parameter region of the actor tower to the
@@ -912,6 +951,17 @@ class MLPExecutor(ForwardChain):
             self._call("ppo_mlp_ln_bwd_f32", st, 2, len(A), _p(A[-1].dY), A[-1].spec.ld, self.mb, c["Z"], c["mean"],
                        c["rstd"], c["g"], c["be"], c["WT"], 256, c["dZ"], A[0].spec.ld, c["part"], self._chain_act,
                        self._chain_rs, self._chain_ss, D, 256 * 256, self._chain_ps)
+            for i, n, sx in self._dw_groups:
+                la, lc = A[i], C[i]
+                s = la.spec
+                d = s.dense
+                x, ldx, ridx = (x0, ldx0, idx0) if i == 0 else (_p(A[i - 1].Y), A[i - 1].spec.ld, None)
+                # problem k + 1 sits one (actor -> critic, or critic -> next actor) step after problem k
+                self._call("ppo_gemm_f32_towers", st, n, A_COL, B_KN, x, ldx, ridx, _p(la.dZ), s.ld, _p(la.wpart),
+                           s.ld, d.fin, s.ld, self.mb, la.splits, d.fin * s.ld, EPI_STORE, None, 0, None, None, 0,
+                           _p(la.bpart), -1, sx, _tstride(la.dZ, lc.dZ), _tstride(la.wpart, lc.wpart), 0, 0, 0,
+                           _tstride(la.bpart, lc.bpart))
+            return
         for i in range(len(A) - 1, -1, -1):
             la, lc = A[i], C[i]
             s = la.spec

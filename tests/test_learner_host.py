@@ -180,12 +180,31 @@ def test_gaussian_update_runs_each_torso_chain_in_one_launch():
     names = [n for n, _ in ex.record()]
     steps = r.cfg.update_epochs * r.cfg.num_minibatches
     # per minibatch step: the transposed kernel images, the forward chain of
-    # both towers, the fused heads + loss, the backward chain and the four
-    # tower-batched dW contractions; the critic's bootstrap chain once
+    # both towers, the fused heads + loss, the backward chain and the dW
+    # contractions (layer 0 of both towers, then layers 1-3 of both towers in
+    # one launch); the critic's bootstrap chain once
+    calls = ex.record(max_steps=1)
     assert names.count("ppo_transpose_f32_batched") == steps
     assert names.count("ppo_mlp_ln_fwd_f32") == steps + 1
     assert names.count("ppo_mlp_ln_bwd_f32") == steps
-    assert names.count("ppo_gemm_f32_towers") == 4 * steps
+    assert names.count("ppo_gemm_f32_towers") == 2 * steps
+    dw = [a for n, a in calls if n == "ppo_gemm_f32_towers"]
+    assert [a[1] for a in dw] == [2, 6]
+    L = len(ex.actor)
+    for a, first in zip(dw, (0, 1)):
+        n, A_, B_, C_, bg = a[1], a[4], a[7], a[9], a[22]
+        sa, sb, sc, sbg = a[24], a[25], a[26], a[30]
+        for k in range(n):
+            i, t = first + k // 2, k % 2
+            lb = (ex.actor, ex.critic)[t][i]
+            if i > 0:
+                assert A_ + 4 * k * sa == (ex.actor, ex.critic)[t][i - 1].Y.data_ptr()
+            else:
+                assert sa == 0 and A_ == 4096   # both towers read the observation rows
+            assert B_ + 4 * k * sb == lb.dZ.data_ptr()
+            assert C_ + 4 * k * sc == lb.wpart.data_ptr()
+            assert bg + 4 * k * sbg == lb.bpart.data_ptr()
+            assert a[11] == lb.spec.dense.fin and a[13] == ex.mb and a[14] == lb.splits
     assert names.count("ppo_gemm_f32") == 1   # the bootstrap value head
     for gone in ("ppo_gemm_ln_act_fwd_f32", "ppo_gemm_ln_act_fwd_f32_towers", "ppo_layernorm_act_fwd_f32",
                  "ppo_layernorm_act_bwd_f32", "ppo_layernorm_act_bwd_f32_towers", "ppo_stream_wait"):
