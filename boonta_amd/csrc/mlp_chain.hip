@@ -64,9 +64,12 @@ struct FwdArgs {
 // k order of the fused per-layer forward (64-deep chunks, each k step of 16
 // as four dependent MFMAs).  A comes from global rows (layer 0) or from the
 // LDS tile.
-template <int SRC, bool VA>
+template <int SRC, bool VA, int KC = 0>
 __device__ __forceinline__ void contract(floatx4 (&acc)[4], const float* xrow, bool a_live, const float* lds_row,
-                                         const float* W, int64_t ldw, int K, int kq, int c4) {
+                                         const float* W, int64_t ldw, int K_, int kq, int c4) {
+  // KC > 0: the reduction length is that compile-time constant (the 256-wide
+  // layers), so no load is conditional and the prefetches stay in flight
+  const int K = KC > 0 ? KC : K_;
   auto load = [&](int k0, float (&a)[4][4], floatx4 (&w)[4][4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -103,13 +106,24 @@ __device__ __forceinline__ void contract(floatx4 (&acc)[4], const float* xrow, b
   };
   float a0[4][4], a1[4][4];
   floatx4 w0[4][4], w1[4][4];
+  // (on the 256-deep contractions, scheduling barriers keep each chunk's
+  // loads issued ahead of the previous chunk's MFMAs; left alone the
+  // compiler sinks every load next to its MFMA and only two or three stay
+  // in flight)
+  auto fence = [] {
+    if constexpr (KC > 0) __builtin_amdgcn_sched_barrier(0);
+  };
   load(0, a0, w0);
   for (int k0 = 0; k0 < K; k0 += 128) {
     if (k0 + 64 < K) load(k0 + 64, a1, w1);
+    fence();
     compute(a0, w0);
+    fence();
     if (k0 + 64 >= K) break;
     if (k0 + 128 < K) load(k0 + 128, a0, w0);
+    fence();
     compute(a1, w1);
+    fence();
   }
 }
 
@@ -138,7 +152,7 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p) {
     if (l == 0)
       contract<0, VA>(acc, xrow, a_live, nullptr, W, p.ldw0, p.K0, kq, c4);
     else
-      contract<1, true>(acc, nullptr, true, &sX[li][0], W, p.ldw, MC_F, kq, c4);
+      contract<1, true, MC_F>(acc, nullptr, true, &sX[li][0], W, p.ldw, MC_F, kq, c4);
 
     const float* bias = p.bias[l] ? p.bias[l] + t * p.tP : nullptr;
     const floatx4 bias4 = bias ? *reinterpret_cast<const floatx4*>(bias + c4) : floatx4{0.f, 0.f, 0.f, 0.f};
@@ -321,7 +335,7 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_bwd_kernel(BwdArgs p) {
     floatx4 acc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-    contract<1, true>(acc, nullptr, true, &sX[li][0], p.WT[l] + t * p.tWT, p.ldwt, MC_F, kq, c4);
+    contract<1, true, MC_F>(acc, nullptr, true, &sX[li][0], p.WT[l] + t * p.tWT, p.ldwt, MC_F, kq, c4);
 #pragma unroll
     for (int v = 0; v < 4; ++v)
 #pragma unroll
