@@ -98,6 +98,12 @@ SIGNATURES = {
     "ppo_gru_fwd_step_f32": (I, [P, P, I64, P, I64, P, P, P, P, P, I64, P, P, I64, P, I64, P, I64, I, I]),
     "ppo_gru_bwd_step_f32": (I, [P, P, I64, P, I64, P, I64, P, I64, P, P, P, P, I64, P, I64, P, I64, P, I64, P,
                                  I64, I, I]),
+    "ppo_gru_seq_max_workgroups": (I, []),
+    "ppo_gru_seq_sync_ints": (I, [I]),
+    "ppo_gru_fwd_seq_f32": (I, [P, P, I64, I64, P, I64, P, P, P, P, I64, P, I64, P, P, I64, I64, P, I64, I64, P,
+                                I64, I64, I, I, I, P, P, I]),
+    "ppo_gru_bwd_seq_f32": (I, [P, P, I64, P, P, P, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P,
+                                I64, I64, I, I, I, P, P, I]),
     "ppo_sequence_rows": (I, [P, P, I, I, I, I, P]),
     "ppo_grad_reduce_segment_bytes": (I, []),
     "ppo_grad_reduce_chunk_bytes": (I, []),

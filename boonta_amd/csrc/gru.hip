@@ -29,12 +29,38 @@
 // one launch per step in both directions, no inter-workgroup synchronisation.
 #include "common.h"
 
+// No multiply-add contraction in this file: the step and sequence kernels
+// round every operation alike, whatever their scheduling.
+#pragma clang fp contract(off)
+
 namespace {
 
 constexpr int TILE = 16;
 constexpr int WAVES = 4;
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+
+// The cell arithmetic of one (sequence, unit), forward and backward, with
+// every rounding step explicit so that the step and sequence kernels
+// (compiled apart) produce the same bits.
+__device__ __forceinline__ float gru_cell_fwd(float xr, float ar, float xz, float az, float xn, float an, float bhn,
+                                              float hp, float& r, float& z, float& hn, float& n) {
+  r = sigmoidf_(xr + ar);
+  z = sigmoidf_(xz + az);
+  hn = an + bhn;
+  n = tanhf(__fmaf_rn(r, hn, xn));                       // xn + r hn
+  return __fmaf_rn(z, hp, __fmul_rn(1.f - z, n));        // (1 - z) n + z hp
+}
+__device__ __forceinline__ void gru_cell_bwd(float dh, float n, float r, float z, float hn, float hp, float& dan,
+                                             float& dar, float& daz, float& dhn) {
+  const float dn = __fmul_rn(dh, 1.f - z);
+  const float dz = __fmul_rn(dh, hp - n);
+  dan = __fmul_rn(dn, __fmaf_rn(-n, n, 1.f));            // dn (1 - n^2)
+  const float dr = __fmul_rn(dan, hn);
+  dhn = __fmul_rn(dan, r);
+  daz = __fmul_rn(__fmul_rn(dz, z), 1.f - z);
+  dar = __fmul_rn(__fmul_rn(dr, r), 1.f - r);
+}
 
 // Branches only on which flag arrays exist (uniform), never on loaded data,
 // so the flag loads stay in flight with the others.
@@ -159,11 +185,8 @@ __global__ void __launch_bounds__(256) gru_fwd_step_kernel(FwdArgs a) {
     an += red[w][2][ti][tj];
   }
   const float hp = reset_e ? 0.f : hp_raw;
-  const float r = sigmoidf_(xr + ar);
-  const float z = sigmoidf_(xz + az);
-  const float hn = an + bhn;
-  const float n = tanhf(xn + r * hn);
-  const float h = (1.f - z) * n + z * hp;
+  float r, z, hn, n;
+  const float h = gru_cell_fwd(xr, ar, xz, az, xn, an, bhn, hp, r, z, hn, n);
   a.h_out[(int64_t)bb * a.ldo + u] = h;
   if (a.hp_out) a.hp_out[(int64_t)bb * a.ldhp + u] = hp;
   if (a.gates) {
@@ -235,7 +258,7 @@ __global__ void __launch_bounds__(256) gru_bwd_step_kernel(BwdArgs a) {
   float direct = 0.f;
   bool reset_t = false;
   if (a.dg) {
-    direct = a.dh_t[(int64_t)bbc * a.lddht + u] * a.z_t[(int64_t)bbc * a.ldz + u];
+    direct = __fmul_rn(a.dh_t[(int64_t)bbc * a.lddht + u], a.z_t[(int64_t)bbc * a.ldz + u]);
     reset_t = done_at(a.term, a.trunc, a.flag_rows, bbc);
   }
   issue_fence();
@@ -266,13 +289,8 @@ __global__ void __launch_bounds__(256) gru_bwd_step_kernel(BwdArgs a) {
     const float dhp = red[0][ti][tj] + red[1][ti][tj] + red[2][ti][tj] + red[3][ti][tj] + direct;
     if (!reset_t) dh += dhp;
   }
-  const float dn = dh * (1.f - z);
-  const float dz = dh * (hp - n);
-  const float dan = dn * (1.f - n * n);
-  const float dr = dan * hn;
-  const float dhn = dan * r;
-  const float daz = dz * z * (1.f - z);
-  const float dar = dr * r * (1.f - r);
+  float dan, dar, daz, dhn;
+  gru_cell_bwd(dh, n, r, z, hn, hp, dan, dar, daz, dhn);
   a.dh_s[(int64_t)bb * a.lddhs + u] = dh;
   float* o = a.dgate_s + (int64_t)bb * a.lddgs;
   o[u] = dan;
@@ -296,6 +314,294 @@ __global__ void sequence_rows_kernel(const int32_t* envs, int S, int T, int N, i
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// ------------------------------------------------- persistent recurrence
+// The whole sequence in one launch per direction.  Workgroup (x, y) owns
+// sequences 16 x .. 16 x + 15 and units 16 y .. 16 y + 15 for every step, with
+// its slice of the recurrent kernel in LDS for the whole launch.  Step t of a
+// sequence block needs only the previous step of the same block, produced by
+// the gridDim.y workgroups that share x: each of them adds one to the block's
+// counter after a step (its stores made visible at device scope first), and
+// each waits, before the next step's contraction, until the counter reaches
+// gridDim.y times the steps done.  A wait polls at most spin_limit times
+// (0: not at all, which tests the error path from the host): when it gives
+// up it sets *error and the workgroup returns, so every workgroup ends.  The
+// contraction and epilogue of a step are those of the one-step kernels, so
+// the results are the same bits.
+
+struct SeqSync {
+  int* counter;  // [gridDim.x] steps completed, times gridDim.y (zero at launch)
+  int* error;    // set to 1 when a wait gave up
+  int spin_limit;
+};
+
+// Every thread returns whether the block's counter reached target.
+__device__ __forceinline__ bool group_wait(const SeqSync& s, int target, int* s_flag) {
+  if (threadIdx.x == 0) {
+    int ok = 0;
+    const int* c = s.counter + blockIdx.x;
+    for (int it = 0; it < s.spin_limit; ++it) {
+      if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) {
+        ok = 1;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (!ok) __hip_atomic_fetch_or(s.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = ok;
+  }
+  __syncthreads();
+  // every wave sees the other workgroups' stores of the completed steps
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  return *s_flag != 0;
+}
+
+// This workgroup's stores of the step are visible device-wide, then it counts.
+__device__ __forceinline__ void group_signal(const SeqSync& s) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(s.counter + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ void zero_ints_kernel(int* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+struct FwdSeqArgs {
+  const float* xi; int64_t ldxi, xi_step;
+  const float* h0; int64_t ldh0; const int32_t* h0_rows;
+  const uint8_t* term; const uint8_t* trunc; const int32_t* flag_rows; int64_t flag_step;
+  const float* wh; int64_t ldwh;
+  const float* bhn;
+  float* h_out; int64_t ldo, h_step;
+  float* hp_out; int64_t ldhp, hp_step;
+  float* gates; int64_t ldg, g_step;
+  int Bm, H, T;
+  SeqSync sync;
+};
+
+// dynamic LDS: [3 gates][16 units][H + 4] (the B operand rows, k contiguous)
+template <int NIT>
+__global__ void __launch_bounds__(256) gru_fwd_seq_kernel(FwdSeqArgs a) {
+  extern __shared__ float sW[];
+  __shared__ float red[WAVES][3][TILE][TILE + 1];
+  __shared__ int s_flag;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int b0 = blockIdx.x * TILE;
+  const int u0 = blockIdx.y * TILE;
+  const int H = a.H;
+  const int P = H + 4;
+  for (int e = tid; e < 3 * H * TILE; e += 256) {
+    const int i = e % TILE, k = (e / TILE) % H, g = e / (TILE * H);
+    sW[(g * TILE + i) * P + k] = a.wh[(int64_t)k * a.ldwh + g * H + u0 + i];
+  }
+  __syncthreads();
+
+  const int i = lane & 15;
+  const int kq = lane >> 4;
+  const int b = b0 + i;
+  const bool b_ok = b < a.Bm;
+  const int bc = b_ok ? b : b0;
+  const int kbeg = wave * (H / WAVES);
+  const int ti = tid >> 4;
+  const int tj = tid & 15;
+  const int bb = b0 + ti;
+  const int u = u0 + tj;
+  const bool bb_ok = bb < a.Bm;
+  const int bbc = bb_ok ? bb : b0;
+  const float bhn = a.bhn[u];
+
+  for (int t = 0; t < a.T; ++t) {
+    const int32_t* frows = a.flag_rows ? a.flag_rows + t * a.flag_step : nullptr;
+    // this step's own operands first (no other workgroup writes them)
+    const float* x = a.xi + t * a.xi_step + (int64_t)bbc * a.ldxi;
+    const float xn = x[u], xr = x[H + u], xz = x[2 * H + u];
+    const bool reset_e = bb_ok ? done_at(a.term, a.trunc, frows, bb) : true;
+    const bool live = b_ok && !done_at(a.term, a.trunc, frows, b);
+    const float* hbase = a.h0;
+    int64_t ldh = a.ldh0;
+    const int32_t* hrows = a.h0_rows;
+    if (t > 0) {
+      if (!group_wait(a.sync, (int)gridDim.y * t, &s_flag)) return;
+      hbase = a.h_out + (t - 1) * a.h_step;
+      ldh = a.ldo;
+      hrows = nullptr;
+    }
+    const int64_t ra = hrows ? (int64_t)hrows[bc] : (int64_t)bc;
+    const float* hrow = hbase + ra * ldh;
+    floatx4 av[NIT];
+    float bv[NIT][3][4];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int k = kbeg + 16 * it + 4 * kq;
+      av[it] = *reinterpret_cast<const floatx4*>(hrow + k);
+#pragma unroll
+      for (int g = 0; g < 3; ++g) {
+        const floatx4 w = *reinterpret_cast<const floatx4*>(&sW[(g * TILE + i) * P + k]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bv[it][g][q] = w[q];
+      }
+    }
+    const int64_t re = hrows ? (int64_t)hrows[bbc] : (int64_t)bbc;
+    const float hp_raw = hbase[re * ldh + u];
+    issue_fence();
+
+    floatx4 acc[3];
+#pragma unroll
+    for (int g = 0; g < 3; ++g) acc[g] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      floatx4 avv = av[it];
+      if (!live) avv = floatx4{0.f, 0.f, 0.f, 0.f};  // a reset sequence starts from h = 0
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int g = 0; g < 3; ++g)
+          acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(avv[q], bv[it][g][q], acc[g], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < 3; ++g)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[wave][g][4 * kq + v][i] = acc[g][v];
+    __syncthreads();
+
+    if (bb_ok) {
+      float ar = 0.f, az = 0.f, an = 0.f;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) {
+        ar += red[w][0][ti][tj];
+        az += red[w][1][ti][tj];
+        an += red[w][2][ti][tj];
+      }
+      const float hp = reset_e ? 0.f : hp_raw;
+      float r, z, hn, n;
+      const float h = gru_cell_fwd(xr, ar, xz, az, xn, an, bhn, hp, r, z, hn, n);
+      a.h_out[t * a.h_step + (int64_t)bb * a.ldo + u] = h;
+      if (a.hp_out) a.hp_out[t * a.hp_step + (int64_t)bb * a.ldhp + u] = hp;
+      if (a.gates) {
+        float* g = a.gates + t * a.g_step + (int64_t)bb * a.ldg;
+        g[u] = n;
+        g[H + u] = r;
+        g[2 * H + u] = z;
+        g[3 * H + u] = hn;
+      }
+    }
+    // (the signal's barrier also keeps red from being rewritten while read)
+    group_signal(a.sync);
+  }
+}
+
+struct BwdSeqArgs {
+  const float* wh; int64_t ldwh;
+  const uint8_t* term; const uint8_t* trunc; const int32_t* flag_rows; int64_t flag_step;
+  const float* dout; int64_t lddo, dout_step;
+  const float* gates; int64_t ldg, g_step;
+  const float* hp; int64_t ldhp, hp_step;
+  float* dh; int64_t lddh, dh_step;
+  float* dgate; int64_t lddg, dg_step;
+  int Bm, H, T;
+  SeqSync sync;
+};
+
+// dynamic LDS: [16 units][3H + 4] (rows u0 .. u0 + 15 of the recurrent kernel)
+template <int NIT>
+__global__ void __launch_bounds__(256) gru_bwd_seq_kernel(BwdSeqArgs a) {
+  extern __shared__ float sW[];
+  __shared__ float red[WAVES][TILE][TILE + 1];
+  __shared__ int s_flag;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int b0 = blockIdx.x * TILE;
+  const int u0 = blockIdx.y * TILE;
+  const int H = a.H;
+  const int H3 = 3 * H;
+  const int P = H3 + 4;
+  for (int e = tid; e < TILE * H3; e += 256) {
+    const int i = e / H3, c = e - i * H3;
+    sW[i * P + c] = a.wh[(int64_t)(u0 + i) * a.ldwh + c];
+  }
+  __syncthreads();
+
+  const int ti = tid >> 4;
+  const int tj = tid & 15;
+  const int bb = b0 + ti;
+  const int u = u0 + tj;
+  const bool bb_ok = bb < a.Bm;
+  const int bbc = bb_ok ? bb : b0;
+  const int i = lane & 15;
+  const int kq = lane >> 4;
+  const bool live = b0 + i < a.Bm;
+  const int kbeg = wave * (H3 / WAVES);
+
+  for (int s = a.T - 1; s >= 0; --s) {
+    const int t = s + 1;
+    // step s's own operands
+    float dh = a.dout[s * a.dout_step + (int64_t)bbc * a.lddo + u];
+    const float* gs = a.gates + s * a.g_step + (int64_t)bbc * a.ldg;
+    const float n = gs[u], r = gs[H + u], z = gs[2 * H + u], hn = gs[3 * H + u];
+    const float hp = a.hp[s * a.hp_step + (int64_t)bbc * a.ldhp + u];
+    if (t < a.T) {
+      // this thread's own dh_t and step t's update gate and resets
+      const float direct = __fmul_rn(a.dh[t * a.dh_step + (int64_t)bbc * a.lddh + u],
+                                     a.gates[t * a.g_step + (int64_t)bbc * a.ldg + 2 * H + u]);
+      const bool reset_t = done_at(a.term, a.trunc, a.flag_rows ? a.flag_rows + t * a.flag_step : nullptr, bbc);
+      if (!group_wait(a.sync, (int)gridDim.y * (a.T - t), &s_flag)) return;
+      // dhp[b][u] = sum_c dgate_t[b][H + c] Wh[u][c], c < 3H
+      const float* arow = a.dgate + t * a.dg_step + (int64_t)(live ? b0 + i : b0) * a.lddg + H;
+      floatx4 av[NIT], bv[NIT];
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        const int k = kbeg + 16 * it + 4 * kq;
+        av[it] = *reinterpret_cast<const floatx4*>(arow + k);
+        bv[it] = *reinterpret_cast<const floatx4*>(&sW[i * P + k]);
+      }
+      issue_fence();
+      floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        floatx4 x = av[it];
+        if (!live) x = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[q], bv[it][q], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[wave][4 * kq + v][i] = acc[v];
+      __syncthreads();
+      if (bb_ok) {
+        const float dhp = red[0][ti][tj] + red[1][ti][tj] + red[2][ti][tj] + red[3][ti][tj] + direct;
+        if (!reset_t) dh += dhp;
+      }
+    }
+    if (bb_ok) {
+      float dan, dar, daz, dhn;
+      gru_cell_bwd(dh, n, r, z, hn, hp, dan, dar, daz, dhn);
+      a.dh[s * a.dh_step + (int64_t)bb * a.lddh + u] = dh;
+      float* o = a.dgate + s * a.dg_step + (int64_t)bb * a.lddg;
+      o[u] = dan;
+      o[H + u] = dar;
+      o[2 * H + u] = daz;
+      o[3 * H + u] = dhn;
+    }
+    group_signal(a.sync);
+  }
+}
+
+int cu_count() {
+  static int counts[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (counts[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    counts[dev] = n;
+  }
+  return counts[dev];
+}
 
 }  // namespace
 
@@ -370,4 +676,100 @@ PPO_EXPORT int ppo_sequence_rows(void* stream, const int32_t* envs, int S, int T
   hipLaunchKernelGGL(sequence_rows_kernel, dim3((unsigned)ppo::ceil_div64(n, 256)), dim3(256), 0,
                      ppo::as_stream(stream), envs, S, T, N, Bm, out);
   return ppo::check_launch("ppo_sequence_rows");
+}
+
+// Workgroups a sequence launch runs at once (one per compute unit): the
+// sequence entry points need ceil(Bm / 16) * (H / 16) of them at most.
+PPO_EXPORT int ppo_gru_seq_max_workgroups() { return cu_count(); }
+
+// Counters a sequence launch needs in `sync` (it zeroes them itself).
+PPO_EXPORT int ppo_gru_seq_sync_ints(int Bm) { return Bm > 0 ? ppo::ceil_div(Bm, TILE) : 0; }
+
+static int seq_check(const char* name, int Bm, int H, int T, const int* sync, const int* error) {
+  if (Bm < 0 || T < 0 || H <= 0 || H % 64 != 0 || H > 256)
+    return ppo::set_error(PPO_ERR_ARG, "%s: need Bm, T >= 0 and H in {64, 128, 192, 256} (Bm=%d H=%d T=%d)", name, Bm,
+                          H, T);
+  if (!sync || !error) return ppo::set_error(PPO_ERR_ARG, "%s: null sync or error word", name);
+  const int64_t wgs = (int64_t)ppo::ceil_div(Bm, TILE) * (H / TILE);
+  const int cus = cu_count();
+  if (wgs > cus)
+    return ppo::set_error(PPO_ERR_ARG, "%s: %lld workgroups exceed the %d compute units that keep them all resident",
+                          name, (long long)wgs, cus);
+  return PPO_OK;
+}
+
+// Forward of the recurrence over T steps in one launch (see the persistent
+// recurrence notes above): step t reads xi + t xi_step and the resets at
+// flag_rows + t flag_step, the carry entering step 0 from h0 (rows h0_rows),
+// and writes h_out, hp_out and gates at + t times their steps, the values of
+// T ppo_gru_fwd_step_f32 launches.  sync: ppo_gru_seq_sync_ints(Bm) ints;
+// error: set to 1 if a wait gave up after spin_limit polls.
+PPO_EXPORT int ppo_gru_fwd_seq_f32(void* stream, const float* xi, int64_t ldxi, int64_t xi_step, const float* h0,
+                                   int64_t ldh0, const int32_t* h0_rows, const uint8_t* terminated,
+                                   const uint8_t* truncated, const int32_t* flag_rows, int64_t flag_step,
+                                   const float* wh, int64_t ldwh, const float* bhn, float* h_out, int64_t ldo,
+                                   int64_t h_step, float* hp_out, int64_t ldhp, int64_t hp_step, float* gates,
+                                   int64_t ldg, int64_t g_step, int Bm, int H, int T, int* sync, int* error,
+                                   int spin_limit) {
+  const int rc = seq_check("ppo_gru_fwd_seq_f32", Bm, H, T, sync, error);
+  if (rc != PPO_OK) return rc;
+  if (Bm == 0 || T == 0) return PPO_OK;
+  if (!xi || !h0 || !wh || !bhn || !h_out)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gru_fwd_seq_f32: null buffer");
+  if (ldxi < 3 * H || ldh0 < H || ldwh < 3 * H || ldo < H || (hp_out && ldhp < H) || (gates && ldg < 4 * H))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gru_fwd_seq_f32: leading dimension too small");
+  if (!aligned16(h0) || ldh0 % 4 || !aligned16(h_out) || ldo % 4 || h_step % 4)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gru_fwd_seq_f32: h0 and h_out rows must be 16-byte aligned");
+  FwdSeqArgs a{xi, ldxi, xi_step, h0, ldh0, h0_rows, terminated, truncated, flag_rows, flag_step, wh, ldwh, bhn,
+               h_out, ldo, h_step, hp_out, ldhp, hp_step, gates, ldg, g_step, Bm, H, T,
+               SeqSync{sync, error, spin_limit}};
+  hipStream_t st = ppo::as_stream(stream);
+  const int groups = ppo::ceil_div(Bm, TILE);
+  hipLaunchKernelGGL(zero_ints_kernel, dim3(ppo::ceil_div(groups, 256)), dim3(256), 0, st, sync, groups);
+  const dim3 grid(groups, H / TILE);
+  const size_t lds = sizeof(float) * 3 * TILE * (H + 4);
+  switch (H / 64) {
+    case 1: hipLaunchKernelGGL(gru_fwd_seq_kernel<1>, grid, dim3(256), lds, st, a); break;
+    case 2: hipLaunchKernelGGL(gru_fwd_seq_kernel<2>, grid, dim3(256), lds, st, a); break;
+    case 3: hipLaunchKernelGGL(gru_fwd_seq_kernel<3>, grid, dim3(256), lds, st, a); break;
+    default: hipLaunchKernelGGL(gru_fwd_seq_kernel<4>, grid, dim3(256), lds, st, a); break;
+  }
+  return ppo::check_launch("ppo_gru_fwd_seq_f32");
+}
+
+// Backward through time over T steps in one launch: step s (T - 1 down to 0)
+// takes the head cotangent dout + s dout_step, gates and hp of step s, and
+// for s < T - 1 the contraction of dgate_{s+1}[:, H:4H] with Wh^T, dh_{s+1},
+// the update gate and the resets of step s + 1; it writes dh and dgate at
+// + s times their steps, the values of T ppo_gru_bwd_step_f32 launches.
+PPO_EXPORT int ppo_gru_bwd_seq_f32(void* stream, const float* wh, int64_t ldwh, const uint8_t* terminated,
+                                   const uint8_t* truncated, const int32_t* flag_rows, int64_t flag_step,
+                                   const float* dout, int64_t lddo, int64_t dout_step, const float* gates,
+                                   int64_t ldg, int64_t g_step, const float* hp, int64_t ldhp, int64_t hp_step,
+                                   float* dh, int64_t lddh, int64_t dh_step, float* dgate, int64_t lddg,
+                                   int64_t dg_step, int Bm, int H, int T, int* sync, int* error, int spin_limit) {
+  const int rc = seq_check("ppo_gru_bwd_seq_f32", Bm, H, T, sync, error);
+  if (rc != PPO_OK) return rc;
+  if (Bm == 0 || T == 0) return PPO_OK;
+  if (!wh || !dout || !gates || !hp || !dh || !dgate)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gru_bwd_seq_f32: null buffer");
+  if (ldwh < 3 * H || lddo < H || ldg < 4 * H || ldhp < H || lddh < H || lddg < 4 * H)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gru_bwd_seq_f32: leading dimension too small");
+  if (!aligned16(dgate) || lddg % 4 || dg_step % 4)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gru_bwd_seq_f32: dgate rows must be 16-byte aligned");
+  BwdSeqArgs a{wh, ldwh, terminated, truncated, flag_rows, flag_step, dout, lddo, dout_step, gates, ldg, g_step,
+               hp, ldhp, hp_step, dh, lddh, dh_step, dgate, lddg, dg_step, Bm, H, T,
+               SeqSync{sync, error, spin_limit}};
+  hipStream_t st = ppo::as_stream(stream);
+  const int groups = ppo::ceil_div(Bm, TILE);
+  hipLaunchKernelGGL(zero_ints_kernel, dim3(ppo::ceil_div(groups, 256)), dim3(256), 0, st, sync, groups);
+  const dim3 grid(groups, H / TILE);
+  const size_t lds = sizeof(float) * TILE * (3 * H + 4);
+  switch (3 * H / 64) {
+    case 3: hipLaunchKernelGGL(gru_bwd_seq_kernel<3>, grid, dim3(256), lds, st, a); break;
+    case 6: hipLaunchKernelGGL(gru_bwd_seq_kernel<6>, grid, dim3(256), lds, st, a); break;
+    case 9: hipLaunchKernelGGL(gru_bwd_seq_kernel<9>, grid, dim3(256), lds, st, a); break;
+    default: hipLaunchKernelGGL(gru_bwd_seq_kernel<12>, grid, dim3(256), lds, st, a); break;
+  }
+  return ppo::check_launch("ppo_gru_bwd_seq_f32");
 }

@@ -1,0 +1,132 @@
+"""The GRU recurrence of a sequence minibatch in one launch per direction
+(ppo_gru_fwd_seq_f32 / ppo_gru_bwd_seq_f32; the loop of
+boonta/networks/blocks/rnn.py:34-54 and its backward through time) against
+the per-step launches it replaces, whose parity with the oracle is
+test_gpu_rnn.py's: bit-identical h, carries, gates, dh and gate cotangents,
+gathered initial carries and resets included.  The error path of the
+bounded waits is forced from the host (spin limit 0) and must end the launch
+with the error word set."""
+import numpy as np
+import pytest
+import torch
+
+from boonta_amd import _lib
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+SPIN = 1 << 18
+
+
+def st():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def case(B, H, T, seed, reset_p=0.05):
+    rng = np.random.default_rng(seed)
+    c = dict(B=B, H=H, T=T)
+    c["XI"] = dev(rng.standard_normal((T * B, 3 * H)).astype(np.float32))
+    c["WH"] = dev((rng.standard_normal((H, 3 * H)) / np.sqrt(H)).astype(np.float32))
+    c["BHN"] = dev((0.1 * rng.standard_normal(H)).astype(np.float32))
+    c["POOL"] = dev(np.tanh(rng.standard_normal((B + 11, H))).astype(np.float32))
+    c["ENVS"] = dev(rng.permutation(B + 11)[:B].astype(np.int32))
+    c["TERM"] = dev((rng.random(T * B) < reset_p).astype(np.uint8))
+    c["TRUNC"] = dev((rng.random(T * B) < reset_p / 2).astype(np.uint8))
+    c["ROWS"] = dev(rng.permutation(T * B).astype(np.int32))   # flags read through the row table
+    c["DOUT"] = dev(rng.standard_normal((T * B, H)).astype(np.float32))
+    return c
+
+
+def out_bufs(B, H, T):
+    z = lambda *s: torch.full(s, 7.0, device=DEV)
+    return dict(HOUT=z(T * B, H), HP=z(T * B, H), GATES=z(T * B, 4 * H), DHS=z(T * B, H), DG=z(T * B, 4 * H))
+
+
+def run_steps(c, o):
+    B, H, T = c["B"], c["H"], c["T"]
+    blk, g4 = B * H, 4 * H
+    P = lambda k: c[k].data_ptr()
+    Q = lambda k: o[k].data_ptr()
+    for t in range(T):
+        hprev, hrows = (P("POOL"), P("ENVS")) if t == 0 else (Q("HOUT") + 4 * (t - 1) * blk, None)
+        _lib.call("ppo_gru_fwd_step_f32", st(), P("XI") + 4 * t * B * 3 * H, 3 * H, hprev, H, hrows, P("TERM"),
+                  P("TRUNC"), P("ROWS") + 4 * t * B, P("WH"), 3 * H, P("BHN"), Q("HOUT") + 4 * t * blk, H,
+                  Q("HP") + 4 * t * blk, H, Q("GATES") + 4 * t * B * g4, g4, B, H)
+    s = T - 1
+    _lib.call("ppo_gru_bwd_step_f32", st(), None, 0, None, 0, None, 0, None, 0, None, None, None,
+              P("DOUT") + 4 * s * blk, H, Q("GATES") + 4 * s * B * g4, g4, Q("HP") + 4 * s * blk, H,
+              Q("DHS") + 4 * s * blk, H, Q("DG") + 4 * s * B * g4, g4, B, H)
+    for t in range(T - 1, 0, -1):
+        s = t - 1
+        _lib.call("ppo_gru_bwd_step_f32", st(), Q("DG") + 4 * (t * B * g4 + H), g4, P("WH"), 3 * H,
+                  Q("DHS") + 4 * t * blk, H, Q("GATES") + 4 * (t * B * g4 + 2 * H), g4, P("TERM"), P("TRUNC"),
+                  P("ROWS") + 4 * t * B, P("DOUT") + 4 * s * blk, H, Q("GATES") + 4 * s * B * g4, g4,
+                  Q("HP") + 4 * s * blk, H, Q("DHS") + 4 * s * blk, H, Q("DG") + 4 * s * B * g4, g4, B, H)
+
+
+def run_seq(c, o, sync, err, spin=SPIN, backward=True):
+    B, H, T = c["B"], c["H"], c["T"]
+    blk, g4 = B * H, 4 * H
+    P = lambda k: c[k].data_ptr()
+    Q = lambda k: o[k].data_ptr()
+    _lib.call("ppo_gru_fwd_seq_f32", st(), P("XI"), 3 * H, B * 3 * H, P("POOL"), H, P("ENVS"), P("TERM"), P("TRUNC"),
+              P("ROWS"), B, P("WH"), 3 * H, P("BHN"), Q("HOUT"), H, blk, Q("HP"), H, blk, Q("GATES"), g4, B * g4,
+              B, H, T, sync.data_ptr(), err.data_ptr(), spin)
+    if backward:
+        _lib.call("ppo_gru_bwd_seq_f32", st(), P("WH"), 3 * H, P("TERM"), P("TRUNC"), P("ROWS"), B, P("DOUT"), H, blk,
+                  Q("GATES"), g4, B * g4, Q("HP"), H, blk, Q("DHS"), H, blk, Q("DG"), g4, B * g4, B, H, T,
+                  sync.data_ptr(), err.data_ptr(), spin)
+
+
+def sync_bufs(B):
+    n = _lib.load().ppo_gru_seq_sync_ints(B)
+    return torch.full((n,), 123, dtype=torch.int32, device=DEV), torch.zeros(1, dtype=torch.int32, device=DEV)
+
+
+@pytest.mark.parametrize("B,H,T", [(256, 256, 64), (48, 64, 5), (37, 128, 9), (16, 192, 3), (1, 256, 2),
+                                   (256, 256, 1)])
+def test_sequence_launches_equal_the_step_launches(B, H, T):
+    assert (B + 15) // 16 * (H // 16) <= _lib.load().ppo_gru_seq_max_workgroups()
+    c = case(B, H, T, seed=B * 31 + H + T)
+    ref, got = out_bufs(B, H, T), out_bufs(B, H, T)
+    run_steps(c, ref)
+    sync, err = sync_bufs(B)
+    for rep in range(2):   # twice: the launch zeroes its own counters
+        run_seq(c, got, sync, err)
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0
+        for k in ("HOUT", "HP", "GATES", "DHS", "DG"):
+            assert torch.equal(got[k], ref[k]), (rep, k)
+
+
+def test_a_wait_that_gives_up_sets_the_error_word_and_the_launch_ends():
+    """Spin limit 0: every wait past the first step gives up at once.  The
+    launch completes; the error word is set; step 0 (no wait) is done."""
+    B, H, T = 64, 128, 4
+    c = case(B, H, T, seed=5)
+    ref, got = out_bufs(B, H, T), out_bufs(B, H, T)
+    run_steps(c, ref)
+    sync, err = sync_bufs(B)
+    run_seq(c, got, sync, err, spin=0, backward=False)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 1
+    assert torch.equal(got["HOUT"][:B], ref["HOUT"][:B])
+    assert torch.equal(got["GATES"][:B], ref["GATES"][:B])
+    # later steps were not computed
+    assert bool((got["HOUT"][B:] == 7.0).all())
+
+
+def test_grids_larger_than_the_resident_workgroups_are_rejected():
+    lib = _lib.load()
+    cus = lib.ppo_gru_seq_max_workgroups()
+    B = 16 * (cus // 4 + 1)   # (B / 16) * (64 / 16) workgroups > cus
+    sync = torch.zeros(lib.ppo_gru_seq_sync_ints(B), dtype=torch.int32, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    buf = torch.zeros(16, device=DEV)
+    with pytest.raises(_lib.KernelError, match="exceed"):
+        _lib.call("ppo_gru_fwd_seq_f32", st(), buf.data_ptr(), 192, 0, buf.data_ptr(), 64, None, None, None, None, 0,
+                  buf.data_ptr(), 192, buf.data_ptr(), buf.data_ptr(), 64, 0, None, 64, 0, None, 256, 0, B, 64, 2,
+                  sync.data_ptr(), err.data_ptr(), SPIN)
