@@ -99,7 +99,7 @@ SIGNATURES = {
     "ppo_gru_bwd_step_f32": (I, [P, P, I64, P, I64, P, I64, P, I64, P, P, P, P, I64, P, I64, P, I64, P, I64, P,
                                  I64, I, I]),
     "ppo_gru_seq_max_workgroups": (I, []),
-    "ppo_gru_seq_sync_ints": (I, [I]),
+    "ppo_gru_seq_exchange_bytes": (I64, [I, I]),
     "ppo_gru_fwd_seq_f32": (I, [P, P, I64, I64, P, I64, P, P, P, P, I64, P, I64, P, P, I64, I64, P, I64, I64, P,
                                 I64, I64, I, I, I, P, P, I]),
     "ppo_gru_bwd_seq_f32": (I, [P, P, I64, P, P, P, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P,

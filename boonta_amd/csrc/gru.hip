@@ -320,52 +320,97 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 // sequences 16 x .. 16 x + 15 and units 16 y .. 16 y + 15 for every step, with
 // its slice of the recurrent kernel in LDS for the whole launch.  Step t of a
 // sequence block needs only the previous step of the same block, produced by
-// the gridDim.y workgroups that share x: each of them adds one to the block's
-// counter after a step (its stores made visible at device scope first), and
-// each waits, before the next step's contraction, until the counter reaches
-// gridDim.y times the steps done.  A wait polls at most spin_limit times
-// (0: not at all, which tests the error path from the host): when it gives
-// up it sets *error and the workgroup returns, so every workgroup ends.  The
-// contraction and epilogue of a step are those of the one-step kernels, so
-// the results are the same bits.
+// the gridDim.y workgroups that share x.  They hand it over through an
+// exchange ring of two slots, each [Bm][K] 64-bit pairs {value bits, tag}
+// (K = H forward, 3H backward), zeroed at launch: a producer stores each value
+// with the tag of its step (device-coherent 64-bit stores, which land whole),
+// and a consumer loads the K columns of its 16 rows (coalesced,
+// device-coherent 64-bit loads), reloading the pairs whose tag is not yet the
+// step's, then stages the values in LDS for the contraction.  No counter, no
+// fence: a value is read only once its own tag says it is there.  A slot is
+// written again two steps later, only after its producer has consumed the
+// step in between, which every consumer of the slot produced after reading
+// it.  A wait polls at most spin_limit times (0: not at all, which tests the
+// error path from the host): when one gives up it sets *error and the
+// workgroup returns, so every workgroup ends.  The contraction and epilogue
+// of a step are those of the one-step kernels, so the results are the same
+// bits.
+
+typedef unsigned long long u64;
 
 struct SeqSync {
-  int* counter;  // [gridDim.x] steps completed, times gridDim.y (zero at launch)
+  u64* ring;     // [2][Bm][K] pairs, zero at launch
   int* error;    // set to 1 when a wait gave up
   int spin_limit;
 };
 
-// Every thread returns whether the block's counter reached target.
-__device__ __forceinline__ bool group_wait(const SeqSync& s, int target, int* s_flag) {
-  if (threadIdx.x == 0) {
-    int ok = 0;
-    const int* c = s.counter + blockIdx.x;
-    for (int it = 0; it < s.spin_limit; ++it) {
-      if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) {
-        ok = 1;
-        break;
+__device__ __forceinline__ void put_pair(u64* p, float v, unsigned tag) {
+  __hip_atomic_store(p, ((u64)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Stages rows b0 .. b0 + 15 of a ring slot ([Bm][K] pairs) into sA[16][K + 4]
+// once each of their pairs carries `tag`; rows from Bm on (never written) are
+// zeros.  Returns, in every thread, false when a wait gave up.
+template <int K>
+__device__ bool stage_exchange(const u64* slot, int Bm, int b0, unsigned tag, float* sA, const SeqSync& s) {
+  constexpr int NL = TILE * K / 256;
+  static_assert(TILE * K % 256 == 0, "rows of K pairs over 256 threads");
+  const int tid = threadIdx.x;
+  u64 v[NL];
+#pragma unroll
+  for (int q = 0; q < NL; ++q) v[q] = b0 + (tid + 256 * q) / K < Bm ? 0ull : (u64)tag << 32;
+  bool ok = false;
+  for (int it = 0; it < s.spin_limit; ++it) {
+#pragma unroll
+    for (int q = 0; q < NL; ++q) {
+      if ((unsigned)(v[q] >> 32) != tag) {
+        const int e = tid + 256 * q, r = e / K;
+        v[q] = __hip_atomic_load(slot + (int64_t)(b0 + r) * K + (e - r * K), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
       }
-      __builtin_amdgcn_s_sleep(1);
     }
-    if (!ok) __hip_atomic_fetch_or(s.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_flag = ok;
+    bool all = true;
+#pragma unroll
+    for (int q = 0; q < NL; ++q) all = all && (unsigned)(v[q] >> 32) == tag;
+    if (all) {
+      ok = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+#pragma unroll
+  for (int q = 0; q < NL; ++q) {
+    const int e = tid + 256 * q, r = e / K;
+    sA[r * (K + 4) + (e - r * K)] = __uint_as_float((uint32_t)v[q]);
+  }
+  if (!ok) __hip_atomic_fetch_or(s.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __syncthreads_or(!ok) == 0;
+}
+
+// The reset flags of the block's 16 rows for FLAG_CHUNK steps, read once per
+// chunk (their row-table lookups are chains of dependent loads, kept off each
+// step's path): done[j][r] = whether row b0 + r is done at step step0 + dir j
+// (1 for rows from Bm on and steps outside [0, T)).  Barriers on both sides,
+// so no thread still reads the previous chunk.
+constexpr int FLAG_CHUNK = 64;
+
+__device__ __forceinline__ void load_flag_chunk(uint8_t (*done)[TILE], const uint8_t* term, const uint8_t* trunc,
+                                                const int32_t* flag_rows, int64_t flag_step, int Bm, int T, int b0,
+                                                int step0, int dir) {
+  __syncthreads();
+  for (int e = threadIdx.x; e < FLAG_CHUNK * TILE; e += blockDim.x) {
+    const int j = e / TILE, r = e - j * TILE;
+    const int t = step0 + dir * j, b = b0 + r;
+    uint8_t d = 1;
+    if (t >= 0 && t < T && b < Bm) d = done_at(term, trunc, flag_rows ? flag_rows + t * flag_step : nullptr, b);
+    done[j][r] = d;
   }
   __syncthreads();
-  // every wave sees the other workgroups' stores of the completed steps
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  return *s_flag != 0;
 }
 
-// This workgroup's stores of the step are visible device-wide, then it counts.
-__device__ __forceinline__ void group_signal(const SeqSync& s) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_fetch_add(s.counter + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__global__ void zero_ints_kernel(int* p, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0;
+__global__ void zero_u64_kernel(u64* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0ull;
 }
 
 struct FwdSeqArgs {
@@ -381,30 +426,28 @@ struct FwdSeqArgs {
   SeqSync sync;
 };
 
-// dynamic LDS: [3 gates][16 units][H + 4] (the B operand rows, k contiguous)
+// dynamic LDS: [3 gates][16 units][H + 4] (the B operand rows, k contiguous),
+// then [16 sequences][H + 4] (the previous step's h of the block's rows)
 template <int NIT>
 __global__ void __launch_bounds__(256) gru_fwd_seq_kernel(FwdSeqArgs a) {
+  constexpr int H = 64 * NIT;
+  constexpr int P = H + 4;
   extern __shared__ float sW[];
+  float* sA = sW + 3 * TILE * P;
   __shared__ float red[WAVES][3][TILE][TILE + 1];
-  __shared__ int s_flag;
+  __shared__ uint8_t done[FLAG_CHUNK][TILE];
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int b0 = blockIdx.x * TILE;
   const int u0 = blockIdx.y * TILE;
-  const int H = a.H;
-  const int P = H + 4;
   for (int e = tid; e < 3 * H * TILE; e += 256) {
     const int i = e % TILE, k = (e / TILE) % H, g = e / (TILE * H);
     sW[(g * TILE + i) * P + k] = a.wh[(int64_t)k * a.ldwh + g * H + u0 + i];
   }
-  __syncthreads();
 
   const int i = lane & 15;
   const int kq = lane >> 4;
-  const int b = b0 + i;
-  const bool b_ok = b < a.Bm;
-  const int bc = b_ok ? b : b0;
   const int kbeg = wave * (H / WAVES);
   const int ti = tid >> 4;
   const int tj = tid & 15;
@@ -413,31 +456,36 @@ __global__ void __launch_bounds__(256) gru_fwd_seq_kernel(FwdSeqArgs a) {
   const bool bb_ok = bb < a.Bm;
   const int bbc = bb_ok ? bb : b0;
   const float bhn = a.bhn[u];
+  const int64_t slot_size = (int64_t)a.Bm * H;
+  // this thread's input projections, loaded a step ahead (no other
+  // workgroup writes them)
+  const float* x = a.xi + (int64_t)bbc * a.ldxi;
+  float xn = x[u], xr = x[H + u], xz = x[2 * H + u];
 
   for (int t = 0; t < a.T; ++t) {
-    const int32_t* frows = a.flag_rows ? a.flag_rows + t * a.flag_step : nullptr;
-    // this step's own operands first (no other workgroup writes them)
-    const float* x = a.xi + t * a.xi_step + (int64_t)bbc * a.ldxi;
-    const float xn = x[u], xr = x[H + u], xz = x[2 * H + u];
-    const bool reset_e = bb_ok ? done_at(a.term, a.trunc, frows, bb) : true;
-    const bool live = b_ok && !done_at(a.term, a.trunc, frows, b);
-    const float* hbase = a.h0;
-    int64_t ldh = a.ldh0;
-    const int32_t* hrows = a.h0_rows;
-    if (t > 0) {
-      if (!group_wait(a.sync, (int)gridDim.y * t, &s_flag)) return;
-      hbase = a.h_out + (t - 1) * a.h_step;
-      ldh = a.ldo;
-      hrows = nullptr;
+    const int j = t % FLAG_CHUNK;
+    if (j == 0) load_flag_chunk(done, a.term, a.trunc, a.flag_rows, a.flag_step, a.Bm, a.T, b0, t, 1);
+    const bool reset_e = done[j][ti] != 0;
+    const bool live = done[j][i] == 0;
+    if (t == 0) {
+      // the carries entering the sequence, gathered through h0_rows
+      for (int e = tid; e < TILE * H; e += 256) {
+        const int r = e / H, c = e - r * H;
+        const int b = b0 + r;
+        float v = 0.f;
+        if (b < a.Bm) v = a.h0[(a.h0_rows ? (int64_t)a.h0_rows[b] : (int64_t)b) * a.ldh0 + c];
+        sA[r * P + c] = v;
+      }
+      __syncthreads();
+    } else if (!stage_exchange<H>(a.sync.ring + ((t - 1) & 1) * slot_size, a.Bm, b0, (unsigned)t, sA, a.sync)) {
+      return;
     }
-    const int64_t ra = hrows ? (int64_t)hrows[bc] : (int64_t)bc;
-    const float* hrow = hbase + ra * ldh;
     floatx4 av[NIT];
     float bv[NIT][3][4];
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
       const int k = kbeg + 16 * it + 4 * kq;
-      av[it] = *reinterpret_cast<const floatx4*>(hrow + k);
+      av[it] = *reinterpret_cast<const floatx4*>(&sA[i * P + k]);
 #pragma unroll
       for (int g = 0; g < 3; ++g) {
         const floatx4 w = *reinterpret_cast<const floatx4*>(&sW[(g * TILE + i) * P + k]);
@@ -445,9 +493,14 @@ __global__ void __launch_bounds__(256) gru_fwd_seq_kernel(FwdSeqArgs a) {
         for (int q = 0; q < 4; ++q) bv[it][g][q] = w[q];
       }
     }
-    const int64_t re = hrows ? (int64_t)hrows[bbc] : (int64_t)bbc;
-    const float hp_raw = hbase[re * ldh + u];
-    issue_fence();
+    const float hp_raw = sA[ti * P + u];
+    float xn_next = 0.f, xr_next = 0.f, xz_next = 0.f;
+    if (t + 1 < a.T) {
+      const float* xt = x + (t + 1) * a.xi_step;
+      xn_next = xt[u];
+      xr_next = xt[H + u];
+      xz_next = xt[2 * H + u];
+    }
 
     floatx4 acc[3];
 #pragma unroll
@@ -467,6 +520,8 @@ __global__ void __launch_bounds__(256) gru_fwd_seq_kernel(FwdSeqArgs a) {
     for (int g = 0; g < 3; ++g)
 #pragma unroll
       for (int v = 0; v < 4; ++v) red[wave][g][4 * kq + v][i] = acc[g][v];
+    // (after this barrier no thread reads sA or red of this step until the
+    // next step's staging barrier, so the next staging may overwrite sA)
     __syncthreads();
 
     if (bb_ok) {
@@ -480,6 +535,7 @@ __global__ void __launch_bounds__(256) gru_fwd_seq_kernel(FwdSeqArgs a) {
       const float hp = reset_e ? 0.f : hp_raw;
       float r, z, hn, n;
       const float h = gru_cell_fwd(xr, ar, xz, az, xn, an, bhn, hp, r, z, hn, n);
+      if (t + 1 < a.T) put_pair(a.sync.ring + (t & 1) * slot_size + (int64_t)bb * H + u, h, (unsigned)(t + 1));
       a.h_out[t * a.h_step + (int64_t)bb * a.ldo + u] = h;
       if (a.hp_out) a.hp_out[t * a.hp_step + (int64_t)bb * a.ldhp + u] = hp;
       if (a.gates) {
@@ -490,8 +546,9 @@ __global__ void __launch_bounds__(256) gru_fwd_seq_kernel(FwdSeqArgs a) {
         g[3 * H + u] = hn;
       }
     }
-    // (the signal's barrier also keeps red from being rewritten while read)
-    group_signal(a.sync);
+    xn = xn_next;
+    xr = xr_next;
+    xz = xz_next;
   }
 }
 
@@ -507,20 +564,22 @@ struct BwdSeqArgs {
   SeqSync sync;
 };
 
-// dynamic LDS: [16 units][3H + 4] (rows u0 .. u0 + 15 of the recurrent kernel)
+// dynamic LDS: [16 units][3H + 4] (rows u0 .. u0 + 15 of the recurrent kernel),
+// then [16 sequences][3H + 4] (the block's dgate_{s+1}[:, H:4H])
 template <int NIT>
 __global__ void __launch_bounds__(256) gru_bwd_seq_kernel(BwdSeqArgs a) {
+  constexpr int H3 = 64 * NIT;
+  constexpr int H = H3 / 3;
+  constexpr int P = H3 + 4;
   extern __shared__ float sW[];
+  float* sA = sW + TILE * P;
   __shared__ float red[WAVES][TILE][TILE + 1];
-  __shared__ int s_flag;
+  __shared__ uint8_t done[FLAG_CHUNK][TILE];
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int b0 = blockIdx.x * TILE;
   const int u0 = blockIdx.y * TILE;
-  const int H = a.H;
-  const int H3 = 3 * H;
-  const int P = H3 + 4;
   for (int e = tid; e < TILE * H3; e += 256) {
     const int i = e / H3, c = e - i * H3;
     sW[i * P + c] = a.wh[(int64_t)(u0 + i) * a.ldwh + c];
@@ -537,30 +596,44 @@ __global__ void __launch_bounds__(256) gru_bwd_seq_kernel(BwdSeqArgs a) {
   const int kq = lane >> 4;
   const bool live = b0 + i < a.Bm;
   const int kbeg = wave * (H3 / WAVES);
+  const int64_t slot_size = (int64_t)a.Bm * H3;
+  // step s's own operands, loaded a step ahead (no other workgroup writes
+  // them); dh and z of step s + 1 stay in registers from that step
+  auto own = [&](int s, float& dout, float& n, float& r, float& z, float& hn, float& hp) {
+    dout = a.dout[s * a.dout_step + (int64_t)bbc * a.lddo + u];
+    const float* gs = a.gates + s * a.g_step + (int64_t)bbc * a.ldg;
+    n = gs[u];
+    r = gs[H + u];
+    z = gs[2 * H + u];
+    hn = gs[3 * H + u];
+    hp = a.hp[s * a.hp_step + (int64_t)bbc * a.ldhp + u];
+  };
+  float dout, n, r, z, hn, hp;
+  own(a.T - 1, dout, n, r, z, hn, hp);
+  float dh_t = 0.f, z_t = 0.f;
 
   for (int s = a.T - 1; s >= 0; --s) {
     const int t = s + 1;
-    // step s's own operands
-    float dh = a.dout[s * a.dout_step + (int64_t)bbc * a.lddo + u];
-    const float* gs = a.gates + s * a.g_step + (int64_t)bbc * a.ldg;
-    const float n = gs[u], r = gs[H + u], z = gs[2 * H + u], hn = gs[3 * H + u];
-    const float hp = a.hp[s * a.hp_step + (int64_t)bbc * a.ldhp + u];
+    float dh = dout;
+    float dout_n = 0.f, n_n = 0.f, r_n = 0.f, z_n = 0.f, hn_n = 0.f, hp_n = 0.f;
+    const int j = (a.T - 1 - s) % FLAG_CHUNK;   // resets of step t = T - (T - 1 - s)
+    if (j == 0) load_flag_chunk(done, a.term, a.trunc, a.flag_rows, a.flag_step, a.Bm, a.T, b0, t, -1);
     if (t < a.T) {
       // this thread's own dh_t and step t's update gate and resets
-      const float direct = __fmul_rn(a.dh[t * a.dh_step + (int64_t)bbc * a.lddh + u],
-                                     a.gates[t * a.g_step + (int64_t)bbc * a.ldg + 2 * H + u]);
-      const bool reset_t = done_at(a.term, a.trunc, a.flag_rows ? a.flag_rows + t * a.flag_step : nullptr, bbc);
-      if (!group_wait(a.sync, (int)gridDim.y * (a.T - t), &s_flag)) return;
+      const float direct = __fmul_rn(dh_t, z_t);
+      const bool reset_t = done[j][ti] != 0;
+      if (!stage_exchange<H3>(a.sync.ring + (t & 1) * slot_size, a.Bm, b0, (unsigned)(a.T - t), sA, a.sync))
+        return;
+      // (issued after the wait, so that they do not hold it up)
+      if (s > 0) own(s - 1, dout_n, n_n, r_n, z_n, hn_n, hp_n);
       // dhp[b][u] = sum_c dgate_t[b][H + c] Wh[u][c], c < 3H
-      const float* arow = a.dgate + t * a.dg_step + (int64_t)(live ? b0 + i : b0) * a.lddg + H;
       floatx4 av[NIT], bv[NIT];
 #pragma unroll
       for (int it = 0; it < NIT; ++it) {
         const int k = kbeg + 16 * it + 4 * kq;
-        av[it] = *reinterpret_cast<const floatx4*>(arow + k);
+        av[it] = *reinterpret_cast<const floatx4*>(&sA[i * P + k]);
         bv[it] = *reinterpret_cast<const floatx4*>(&sW[i * P + k]);
       }
-      issue_fence();
       floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int it = 0; it < NIT; ++it) {
@@ -571,23 +644,41 @@ __global__ void __launch_bounds__(256) gru_bwd_seq_kernel(BwdSeqArgs a) {
       }
 #pragma unroll
       for (int v = 0; v < 4; ++v) red[wave][4 * kq + v][i] = acc[v];
+      // (after this barrier no thread reads sA or red of this step until the
+      // next step's staging barrier)
       __syncthreads();
       if (bb_ok) {
         const float dhp = red[0][ti][tj] + red[1][ti][tj] + red[2][ti][tj] + red[3][ti][tj] + direct;
         if (!reset_t) dh += dhp;
       }
+    } else if (s > 0) {
+      own(s - 1, dout_n, n_n, r_n, z_n, hn_n, hp_n);
     }
     if (bb_ok) {
       float dan, dar, daz, dhn;
       gru_cell_bwd(dh, n, r, z, hn, hp, dan, dar, daz, dhn);
       a.dh[s * a.dh_step + (int64_t)bb * a.lddh + u] = dh;
+      if (s > 0) {
+        u64* o = a.sync.ring + (s & 1) * slot_size + (int64_t)bb * H3;
+        const unsigned tag = (unsigned)(a.T - s);
+        put_pair(o + u, dar, tag);
+        put_pair(o + H + u, daz, tag);
+        put_pair(o + 2 * H + u, dhn, tag);
+      }
       float* o = a.dgate + s * a.dg_step + (int64_t)bb * a.lddg;
       o[u] = dan;
       o[H + u] = dar;
       o[2 * H + u] = daz;
       o[3 * H + u] = dhn;
     }
-    group_signal(a.sync);
+    dh_t = dh;
+    z_t = z;
+    dout = dout_n;
+    n = n_n;
+    r = r_n;
+    z = z_n;
+    hn = hn_n;
+    hp = hp_n;
   }
 }
 
@@ -682,14 +773,31 @@ PPO_EXPORT int ppo_sequence_rows(void* stream, const int32_t* envs, int S, int T
 // sequence entry points need ceil(Bm / 16) * (H / 16) of them at most.
 PPO_EXPORT int ppo_gru_seq_max_workgroups() { return cu_count(); }
 
-// Counters a sequence launch needs in `sync` (it zeroes them itself).
-PPO_EXPORT int ppo_gru_seq_sync_ints(int Bm) { return Bm > 0 ? ppo::ceil_div(Bm, TILE) : 0; }
+// Bytes of the exchange ring a sequence launch of either direction needs
+// (two slots of [Bm][3H] 64-bit pairs; the launch zeroes what it uses).
+PPO_EXPORT int64_t ppo_gru_seq_exchange_bytes(int Bm, int H) {
+  return Bm > 0 && H > 0 ? 2 * (int64_t)Bm * 3 * H * (int64_t)sizeof(u64) : 0;
+}
 
-static int seq_check(const char* name, int Bm, int H, int T, const int* sync, const int* error) {
+// Launches a persistent kernel with `lds` bytes of dynamic LDS (beyond the
+// 64 KiB a launch gets without asking).
+template <typename Kernel, typename Args>
+static void launch_seq(Kernel k, dim3 grid, size_t lds, hipStream_t st, const Args& a) {
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  hipLaunchKernelGGL(k, grid, dim3(256), lds, st, a);
+}
+
+static void zero_ring(hipStream_t st, void* ring, int64_t n) {
+  const int blocks = (int)std::min<int64_t>(1024, ppo::ceil_div64(n, 256));
+  hipLaunchKernelGGL(zero_u64_kernel, dim3(blocks), dim3(256), 0, st, static_cast<u64*>(ring), n);
+}
+
+static int seq_check(const char* name, int Bm, int H, int T, const void* exchange, const int* error) {
   if (Bm < 0 || T < 0 || H <= 0 || H % 64 != 0 || H > 256)
     return ppo::set_error(PPO_ERR_ARG, "%s: need Bm, T >= 0 and H in {64, 128, 192, 256} (Bm=%d H=%d T=%d)", name, Bm,
                           H, T);
-  if (!sync || !error) return ppo::set_error(PPO_ERR_ARG, "%s: null sync or error word", name);
+  if (!exchange || !error) return ppo::set_error(PPO_ERR_ARG, "%s: null exchange ring or error word", name);
+  if (!aligned16(exchange)) return ppo::set_error(PPO_ERR_ARG, "%s: exchange ring must be 16-byte aligned", name);
   const int64_t wgs = (int64_t)ppo::ceil_div(Bm, TILE) * (H / TILE);
   const int cus = cu_count();
   if (wgs > cus)
@@ -702,16 +810,16 @@ static int seq_check(const char* name, int Bm, int H, int T, const int* sync, co
 // recurrence notes above): step t reads xi + t xi_step and the resets at
 // flag_rows + t flag_step, the carry entering step 0 from h0 (rows h0_rows),
 // and writes h_out, hp_out and gates at + t times their steps, the values of
-// T ppo_gru_fwd_step_f32 launches.  sync: ppo_gru_seq_sync_ints(Bm) ints;
-// error: set to 1 if a wait gave up after spin_limit polls.
+// T ppo_gru_fwd_step_f32 launches.  exchange: ppo_gru_seq_exchange_bytes(Bm,
+// H) bytes; error: set to 1 if a wait gave up after spin_limit polls.
 PPO_EXPORT int ppo_gru_fwd_seq_f32(void* stream, const float* xi, int64_t ldxi, int64_t xi_step, const float* h0,
                                    int64_t ldh0, const int32_t* h0_rows, const uint8_t* terminated,
                                    const uint8_t* truncated, const int32_t* flag_rows, int64_t flag_step,
                                    const float* wh, int64_t ldwh, const float* bhn, float* h_out, int64_t ldo,
                                    int64_t h_step, float* hp_out, int64_t ldhp, int64_t hp_step, float* gates,
-                                   int64_t ldg, int64_t g_step, int Bm, int H, int T, int* sync, int* error,
+                                   int64_t ldg, int64_t g_step, int Bm, int H, int T, void* exchange, int* error,
                                    int spin_limit) {
-  const int rc = seq_check("ppo_gru_fwd_seq_f32", Bm, H, T, sync, error);
+  const int rc = seq_check("ppo_gru_fwd_seq_f32", Bm, H, T, exchange, error);
   if (rc != PPO_OK) return rc;
   if (Bm == 0 || T == 0) return PPO_OK;
   if (!xi || !h0 || !wh || !bhn || !h_out)
@@ -722,17 +830,16 @@ PPO_EXPORT int ppo_gru_fwd_seq_f32(void* stream, const float* xi, int64_t ldxi, 
     return ppo::set_error(PPO_ERR_ARG, "ppo_gru_fwd_seq_f32: h0 and h_out rows must be 16-byte aligned");
   FwdSeqArgs a{xi, ldxi, xi_step, h0, ldh0, h0_rows, terminated, truncated, flag_rows, flag_step, wh, ldwh, bhn,
                h_out, ldo, h_step, hp_out, ldhp, hp_step, gates, ldg, g_step, Bm, H, T,
-               SeqSync{sync, error, spin_limit}};
+               SeqSync{static_cast<u64*>(exchange), error, spin_limit}};
   hipStream_t st = ppo::as_stream(stream);
-  const int groups = ppo::ceil_div(Bm, TILE);
-  hipLaunchKernelGGL(zero_ints_kernel, dim3(ppo::ceil_div(groups, 256)), dim3(256), 0, st, sync, groups);
-  const dim3 grid(groups, H / TILE);
-  const size_t lds = sizeof(float) * 3 * TILE * (H + 4);
+  if (T > 1) zero_ring(st, exchange, 2 * (int64_t)Bm * H);
+  const dim3 grid(ppo::ceil_div(Bm, TILE), H / TILE);
+  const size_t lds = sizeof(float) * 4 * TILE * (H + 4);
   switch (H / 64) {
-    case 1: hipLaunchKernelGGL(gru_fwd_seq_kernel<1>, grid, dim3(256), lds, st, a); break;
-    case 2: hipLaunchKernelGGL(gru_fwd_seq_kernel<2>, grid, dim3(256), lds, st, a); break;
-    case 3: hipLaunchKernelGGL(gru_fwd_seq_kernel<3>, grid, dim3(256), lds, st, a); break;
-    default: hipLaunchKernelGGL(gru_fwd_seq_kernel<4>, grid, dim3(256), lds, st, a); break;
+    case 1: launch_seq(gru_fwd_seq_kernel<1>, grid, lds, st, a); break;
+    case 2: launch_seq(gru_fwd_seq_kernel<2>, grid, lds, st, a); break;
+    case 3: launch_seq(gru_fwd_seq_kernel<3>, grid, lds, st, a); break;
+    default: launch_seq(gru_fwd_seq_kernel<4>, grid, lds, st, a); break;
   }
   return ppo::check_launch("ppo_gru_fwd_seq_f32");
 }
@@ -747,8 +854,9 @@ PPO_EXPORT int ppo_gru_bwd_seq_f32(void* stream, const float* wh, int64_t ldwh, 
                                    const float* dout, int64_t lddo, int64_t dout_step, const float* gates,
                                    int64_t ldg, int64_t g_step, const float* hp, int64_t ldhp, int64_t hp_step,
                                    float* dh, int64_t lddh, int64_t dh_step, float* dgate, int64_t lddg,
-                                   int64_t dg_step, int Bm, int H, int T, int* sync, int* error, int spin_limit) {
-  const int rc = seq_check("ppo_gru_bwd_seq_f32", Bm, H, T, sync, error);
+                                   int64_t dg_step, int Bm, int H, int T, void* exchange, int* error,
+                                   int spin_limit) {
+  const int rc = seq_check("ppo_gru_bwd_seq_f32", Bm, H, T, exchange, error);
   if (rc != PPO_OK) return rc;
   if (Bm == 0 || T == 0) return PPO_OK;
   if (!wh || !dout || !gates || !hp || !dh || !dgate)
@@ -759,17 +867,16 @@ PPO_EXPORT int ppo_gru_bwd_seq_f32(void* stream, const float* wh, int64_t ldwh, 
     return ppo::set_error(PPO_ERR_ARG, "ppo_gru_bwd_seq_f32: dgate rows must be 16-byte aligned");
   BwdSeqArgs a{wh, ldwh, terminated, truncated, flag_rows, flag_step, dout, lddo, dout_step, gates, ldg, g_step,
                hp, ldhp, hp_step, dh, lddh, dh_step, dgate, lddg, dg_step, Bm, H, T,
-               SeqSync{sync, error, spin_limit}};
+               SeqSync{static_cast<u64*>(exchange), error, spin_limit}};
   hipStream_t st = ppo::as_stream(stream);
-  const int groups = ppo::ceil_div(Bm, TILE);
-  hipLaunchKernelGGL(zero_ints_kernel, dim3(ppo::ceil_div(groups, 256)), dim3(256), 0, st, sync, groups);
-  const dim3 grid(groups, H / TILE);
-  const size_t lds = sizeof(float) * TILE * (3 * H + 4);
+  if (T > 1) zero_ring(st, exchange, 2 * (int64_t)Bm * 3 * H);
+  const dim3 grid(ppo::ceil_div(Bm, TILE), H / TILE);
+  const size_t lds = sizeof(float) * 2 * TILE * (3 * H + 4);
   switch (3 * H / 64) {
-    case 3: hipLaunchKernelGGL(gru_bwd_seq_kernel<3>, grid, dim3(256), lds, st, a); break;
-    case 6: hipLaunchKernelGGL(gru_bwd_seq_kernel<6>, grid, dim3(256), lds, st, a); break;
-    case 9: hipLaunchKernelGGL(gru_bwd_seq_kernel<9>, grid, dim3(256), lds, st, a); break;
-    default: hipLaunchKernelGGL(gru_bwd_seq_kernel<12>, grid, dim3(256), lds, st, a); break;
+    case 3: launch_seq(gru_bwd_seq_kernel<3>, grid, lds, st, a); break;
+    case 6: launch_seq(gru_bwd_seq_kernel<6>, grid, lds, st, a); break;
+    case 9: launch_seq(gru_bwd_seq_kernel<9>, grid, lds, st, a); break;
+    default: launch_seq(gru_bwd_seq_kernel<12>, grid, lds, st, a); break;
   }
   return ppo::check_launch("ppo_gru_bwd_seq_f32");
 }

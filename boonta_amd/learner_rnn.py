@@ -75,6 +75,30 @@ class RecurrentExecutor(MLPExecutor):
         n2 = 2 * self.N
         self.XIB = torch.zeros(n2, 3 * H, **f32)
         self.HB = torch.zeros(n2, H, **f32)
+        # the recurrence of a minibatch in one launch per direction when all
+        # its workgroups fit the device at once (else one launch per step)
+        self.seq = self.SEQ and self._seq_fits(self.Bm, H)
+        if self.seq:
+            lib = _lib.load()
+            self.SEQX = torch.zeros(max(1, lib.ppo_gru_seq_exchange_bytes(self.Bm, H) // 8), dtype=torch.int64,
+                                    device=dev)
+            self.SEQERR = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    SEQ = True               # sequence launches where they fit
+    SEQ_SPIN = 1 << 18       # polls of a step wait before it gives up (about a second)
+
+    @staticmethod
+    def _seq_fits(Bm: int, H: int) -> bool:
+        """Whether the one-launch recurrence takes this minibatch: H a multiple
+        of 64 up to 256 and every workgroup resident at once."""
+        if H % 64 or H > 256 or Bm <= 0:
+            return False
+        return (Bm + 15) // 16 * (H // 16) <= _lib.load().ppo_gru_seq_max_workgroups()
+
+    def recurrence_error(self) -> bool:
+        """True when a wait of a one-launch recurrence gave up (the update's
+        results are then not to be used); reading it synchronizes."""
+        return bool(self.seq and int(self.SEQERR.item()) != 0)
 
     def _extra_input_buffers(self) -> dict:
         """first.terminated / first.truncated [T, N] and the carry sequence
@@ -184,7 +208,12 @@ class RecurrentExecutor(MLPExecutor):
         self._gemm(st, A_ROW, B_KN, e_ptr, lde, None, self.flat.view(g.wi), 3 * H, _p(self.XI),
                    3 * H, mb, 3 * H, I, 1, 0, EPI_BIAS_ACT, self.flat.view(g.bi), 0, None, None, 0, None, -1)
         blk = Bm * H
-        for t in range(T):
+        if self.seq:
+            self._call("ppo_gru_fwd_seq_f32", st, _p(self.XI), 3 * H, Bm * 3 * H, inp["carry0"], H, envs, fterm,
+                       ftrunc, rows, Bm, self.flat.view(g.wh), 3 * H, self.flat.view(g.bhn), _p(self.HOUT), H, blk,
+                       _p(self.HP), H, blk, _p(self.GATES), 4 * H, Bm * 4 * H, Bm, H, T, _p(self.SEQX),
+                       _p(self.SEQERR), self.SEQ_SPIN)
+        for t in range(T if not self.seq else 0):
             if t == 0:
                 hprev, hrows = inp["carry0"], envs
             else:
@@ -198,11 +227,17 @@ class RecurrentExecutor(MLPExecutor):
         # backward through time
         wh = self.flat.view(g.wh)
         G4 = 4 * H
-        s = T - 1
-        self._call("ppo_gru_bwd_step_f32", st, None, 0, None, 0, None, 0, None, 0, None, None, None,
-                   _p(self.DHOUT) + 4 * s * blk, H, _p(self.GATES) + 4 * s * Bm * G4, G4, _p(self.HP) + 4 * s * blk,
-                   H, _p(self.DHS) + 4 * s * blk, H, _p(self.DGATE) + 4 * s * Bm * G4, G4, Bm, H)
-        for t in range(T - 1, 0, -1):
+        if self.seq:
+            self._call("ppo_gru_bwd_seq_f32", st, wh, 3 * H, fterm, ftrunc, rows, Bm, _p(self.DHOUT), H, blk,
+                       _p(self.GATES), G4, Bm * G4, _p(self.HP), H, blk, _p(self.DHS), H, blk, _p(self.DGATE), G4,
+                       Bm * G4, Bm, H, T, _p(self.SEQX), _p(self.SEQERR), self.SEQ_SPIN)
+        else:
+            s = T - 1
+            self._call("ppo_gru_bwd_step_f32", st, None, 0, None, 0, None, 0, None, 0, None, None, None,
+                       _p(self.DHOUT) + 4 * s * blk, H, _p(self.GATES) + 4 * s * Bm * G4, G4,
+                       _p(self.HP) + 4 * s * blk, H, _p(self.DHS) + 4 * s * blk, H,
+                       _p(self.DGATE) + 4 * s * Bm * G4, G4, Bm, H)
+        for t in range(T - 1, 0, -1) if not self.seq else ():
             s = t - 1
             self._call("ppo_gru_bwd_step_f32", st, _p(self.DGATE) + 4 * (t * Bm * G4 + H), G4, wh, 3 * H,
                        _p(self.DHS) + 4 * t * blk, H, _p(self.GATES) + 4 * (t * Bm * G4 + 2 * H), G4, fterm, ftrunc,

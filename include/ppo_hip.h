@@ -470,10 +470,12 @@ int ppo_gru_bwd_step_f32(void* stream, const float* dg, int64_t lddg, const floa
 /* The whole recurrence of a sequence minibatch in one launch per direction
  * (the loop of boonta/networks/blocks/rnn.py:34-54 over T steps, and its
  * backward through time): workgroup (x, y) keeps sequences 16x..16x+15 and
- * units 16y..16y+15 for every step with its slice of Wh in LDS; step t of a
- * sequence block waits, on a counter in `sync` (ppo_gru_seq_sync_ints(Bm)
- * ints, zeroed by the call), for the previous step of the same block.  Each
- * wait polls at most spin_limit times (0: none, to exercise the error path);
+ * units 16y..16y+15 for every step with its slice of Wh in LDS; the
+ * workgroups of a sequence block hand each step to the next through
+ * `exchange` (ppo_gru_seq_exchange_bytes(Bm, H) bytes, 16-byte aligned,
+ * zeroed by the call), as {value, step tag} pairs that a consumer polls until
+ * the tag is the step's.  Each wait polls at most spin_limit times (0: none,
+ * to exercise the error path);
  * a wait that gives up sets *error to 1 and its workgroup ends, so the launch
  * always completes.  Needs ceil(Bm / 16) * H / 16 <=
  * ppo_gru_seq_max_workgroups() (all workgroups resident) and H <= 256.
@@ -481,19 +483,19 @@ int ppo_gru_bwd_step_f32(void* stream, const float* dg, int64_t lddg, const floa
  * launches, bit for bit.  Step t's operands sit at the base pointers plus t
  * times the *_step strides (elements; flag_rows + t * flag_step). */
 int ppo_gru_seq_max_workgroups(void);
-int ppo_gru_seq_sync_ints(int Bm);
+int64_t ppo_gru_seq_exchange_bytes(int Bm, int H);
 int ppo_gru_fwd_seq_f32(void* stream, const float* xi, int64_t ldxi, int64_t xi_step, const float* h0, int64_t ldh0,
                         const int32_t* h0_rows, const uint8_t* terminated, const uint8_t* truncated,
                         const int32_t* flag_rows, int64_t flag_step, const float* wh, int64_t ldwh, const float* bhn,
                         float* h_out, int64_t ldo, int64_t h_step, float* hp_out, int64_t ldhp, int64_t hp_step,
-                        float* gates, int64_t ldg, int64_t g_step, int Bm, int H, int T, int* sync, int* error,
-                        int spin_limit);
+                        float* gates, int64_t ldg, int64_t g_step, int Bm, int H, int T, void* exchange,
+                        int* error, int spin_limit);
 int ppo_gru_bwd_seq_f32(void* stream, const float* wh, int64_t ldwh, const uint8_t* terminated,
                         const uint8_t* truncated, const int32_t* flag_rows, int64_t flag_step, const float* dout,
                         int64_t lddo, int64_t dout_step, const float* gates, int64_t ldg, int64_t g_step,
                         const float* hp, int64_t ldhp, int64_t hp_step, float* dh, int64_t lddh, int64_t dh_step,
-                        float* dgate, int64_t lddg, int64_t dg_step, int Bm, int H, int T, int* sync, int* error,
-                        int spin_limit);
+                        float* dgate, int64_t lddg, int64_t dg_step, int Bm, int H, int T, void* exchange,
+                        int* error, int spin_limit);
 /* Sample rows of S env-major sequence minibatches (recurrent_ppo.py:217-223):
  * out[s * T * Bm + t * Bm + b] = t * N + envs[s * Bm + b]. */
 int ppo_sequence_rows(void* stream, const int32_t* envs, int S, int T, int N, int Bm, int32_t* out);

@@ -81,9 +81,10 @@ def run_seq(c, o, sync, err, spin=SPIN, backward=True):
                   sync.data_ptr(), err.data_ptr(), spin)
 
 
-def sync_bufs(B):
-    n = _lib.load().ppo_gru_seq_sync_ints(B)
-    return torch.full((n,), 123, dtype=torch.int32, device=DEV), torch.zeros(1, dtype=torch.int32, device=DEV)
+def sync_bufs(B, H):
+    n = _lib.load().ppo_gru_seq_exchange_bytes(B, H) // 8
+    # garbage tags: the launch must zero the ring it uses
+    return torch.full((n,), 123 << 32, dtype=torch.int64, device=DEV), torch.zeros(1, dtype=torch.int32, device=DEV)
 
 
 @pytest.mark.parametrize("B,H,T", [(256, 256, 64), (48, 64, 5), (37, 128, 9), (16, 192, 3), (1, 256, 2),
@@ -93,8 +94,8 @@ def test_sequence_launches_equal_the_step_launches(B, H, T):
     c = case(B, H, T, seed=B * 31 + H + T)
     ref, got = out_bufs(B, H, T), out_bufs(B, H, T)
     run_steps(c, ref)
-    sync, err = sync_bufs(B)
-    for rep in range(2):   # twice: the launch zeroes its own counters
+    sync, err = sync_bufs(B, H)
+    for rep in range(2):   # twice: the second launch finds the first one's tags in the ring
         run_seq(c, got, sync, err)
         torch.cuda.synchronize()
         assert int(err.item()) == 0
@@ -109,7 +110,7 @@ def test_a_wait_that_gives_up_sets_the_error_word_and_the_launch_ends():
     c = case(B, H, T, seed=5)
     ref, got = out_bufs(B, H, T), out_bufs(B, H, T)
     run_steps(c, ref)
-    sync, err = sync_bufs(B)
+    sync, err = sync_bufs(B, H)
     run_seq(c, got, sync, err, spin=0, backward=False)
     torch.cuda.synchronize()
     assert int(err.item()) == 1
@@ -123,10 +124,44 @@ def test_grids_larger_than_the_resident_workgroups_are_rejected():
     lib = _lib.load()
     cus = lib.ppo_gru_seq_max_workgroups()
     B = 16 * (cus // 4 + 1)   # (B / 16) * (64 / 16) workgroups > cus
-    sync = torch.zeros(lib.ppo_gru_seq_sync_ints(B), dtype=torch.int32, device=DEV)
+    sync = torch.zeros(lib.ppo_gru_seq_exchange_bytes(B, 64) // 8, dtype=torch.int64, device=DEV)
     err = torch.zeros(1, dtype=torch.int32, device=DEV)
     buf = torch.zeros(16, device=DEV)
     with pytest.raises(_lib.KernelError, match="exceed"):
         _lib.call("ppo_gru_fwd_seq_f32", st(), buf.data_ptr(), 192, 0, buf.data_ptr(), 64, None, None, None, None, 0,
                   buf.data_ptr(), 192, buf.data_ptr(), buf.data_ptr(), 64, 0, None, 64, 0, None, 256, 0, B, 64, 2,
                   sync.data_ptr(), err.data_ptr(), SPIN)
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_recurrent_update_with_sequence_launches_equals_the_step_launches(use_graph):
+    """RecurrentPPO.update with each direction of the recurrence in one launch
+    against the same update issued step by step: parameters and logs bit for
+    bit after two updates, and no wait gave up."""
+    from boonta_amd.algorithms.ppo import flat_state_of
+    from boonta_amd.algorithms.recurrent_ppo import RecurrentPPO
+    from boonta_amd.learner_rnn import RecurrentExecutor
+    from boonta_amd.random import key as make_key
+    from ppo_cases import device_recurrent_transition, make_recurrent_case
+
+    class StepExecutor(RecurrentExecutor):
+        SEQ = False
+
+    class StepPPO(RecurrentPPO):
+        executor_class = StepExecutor
+
+    r, plan, params, tr, roll, extra = make_recurrent_case(4, T=16, N=256, M=4, E=2, seed=3)
+    results = []
+    for cls in (RecurrentPPO, StepPPO):
+        alg = cls(cfg=r.cfg, network=r.network, optimizer=r.optimizer, use_graph=use_graph)
+        state = alg.init_from_params({"params": params}, r.obs_dim)
+        ex = alg.executor(state, r.T, r.N, r.obs_dim)
+        assert ex.seq == (cls is RecurrentPPO)
+        trans = device_recurrent_transition(tr, roll, extra)
+        for k in (1, 2):
+            alg.update(state, make_key(k), trans)
+        torch.cuda.synchronize()
+        assert not ex.recurrence_error()
+        results.append((flat_state_of(state).P.cpu().clone(), ex.LOGS.cpu().clone()))
+    assert torch.equal(results[0][0], results[1][0])
+    assert torch.equal(results[0][1], results[1][1])

@@ -308,3 +308,36 @@ def test_gaussian_update_pairs_its_towers_layer_by_layer():
             assert inside(ptr, actor_bufs) and inside(ptr + 4 * stride, critic_bufs), name
             checked += 1
     assert checked > 0
+
+
+class SeqRecurrentExecutor(RecurrentExecutor):
+    """The recurrent executor with the one-launch recurrence taken whatever
+    the device (its launch sequence only is recorded here)."""
+
+    @staticmethod
+    def _seq_fits(Bm, H):
+        return True
+
+
+def test_recurrent_update_runs_each_direction_of_the_recurrence_in_one_launch():
+    r = small(4)
+    prog = Program(r.network.plan(r.obs_dim))
+    flat = FlatState(prog, torch.device("cpu"))
+    ex = SeqRecurrentExecutor(prog, flat, r.cfg, r.optimizer, r.T, r.N)
+    ex.bind(fake_inputs(ex))
+    assert ex.seq
+    calls = ex.record()
+    names = [n for n, _ in calls]
+    steps = r.cfg.update_epochs * r.cfg.num_minibatches
+    assert names.count("ppo_gru_fwd_seq_f32") == steps and names.count("ppo_gru_bwd_seq_f32") == steps
+    assert names.count("ppo_gru_fwd_step_f32") == 2          # the bootstrap's two-step tail
+    assert "ppo_gru_bwd_step_f32" not in names
+    H, Bm, T = prog.gru.H, ex.Bm, r.T
+    for name, args in calls:
+        _, argtypes = _lib.SIGNATURES[name]
+        assert len(args) == len(argtypes), name
+        if name == "ppo_gru_fwd_seq_f32":
+            assert args[3] == Bm * 3 * H and args[10] == Bm and args[-6:-3] == (Bm, H, T)
+            assert args[-3] == ex.SEQX.data_ptr() and args[-2] == ex.SEQERR.data_ptr()
+        if name == "ppo_gru_bwd_seq_f32":
+            assert args[6] == Bm and args[9] == Bm * H and args[-6:-3] == (Bm, H, T)
