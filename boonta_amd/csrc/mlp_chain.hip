@@ -64,13 +64,45 @@ struct FwdArgs {
 // k order of the fused per-layer forward (64-deep chunks, each k step of 16
 // as four dependent MFMAs).  A comes from global rows (layer 0) or from the
 // LDS tile.
-template <int SRC, bool VA, int KC = 0>
+// The kernel operands of one 64-deep chunk: w[u][s] = W[k0 + 16 u + 4 kq +
+// s][c4 .. c4 + 3].  KC > 0: the kernel's row pitch is MC_F, so the loads
+// take one 32-bit lane offset and immediate row offsets from a uniform base
+// (with a run-time pitch the compiler keeps sixteen 64-bit lane addresses
+// per chunk, which it spills).
+template <int KC>
+__device__ __forceinline__ void load_w(int k0, floatx4 (&w)[4][4], const float* W, int64_t ldw, int K, int kq,
+                                       int c4) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    if (KC > 0) {
+      const float* Wu = W + (k0 + 16 * u) * MC_F;
+      const uint32_t lane = (uint32_t)(4 * kq * MC_F + c4);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) w[u][s] = *reinterpret_cast<const floatx4*>(Wu + lane + s * MC_F);
+    } else {
+      const int kb = k0 + 16 * u + 4 * kq;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int k = kb + s;
+        w[u][s] = k < K ? *reinterpret_cast<const floatx4*>(W + (int64_t)k * ldw + c4) : floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  }
+}
+
+// One layer's 16 x 256 contraction: acc[j] += A[rows][k] W[k][c4 + j] in the
+// k order of the fused per-layer forward (64-deep chunks, each k step of 16
+// as four dependent MFMAs).  A comes from global rows (layer 0) or from the
+// LDS tile.  w0: the first chunk's kernel operands, loaded here unless PRE
+// (the caller issued them earlier, ahead of its own stores: a wait for a
+// load also waits for every store issued before it).
+template <int SRC, bool VA, int KC = 0, bool PRE = false>
 __device__ __forceinline__ void contract(floatx4 (&acc)[4], const float* xrow, bool a_live, const float* lds_row,
-                                         const float* W, int64_t ldw, int K_, int kq, int c4) {
+                                         const float* W, int64_t ldw, int K_, int kq, int c4, floatx4 (&w0)[4][4]) {
   // KC > 0: the reduction length is that compile-time constant (the 256-wide
   // layers), so no load is conditional and the prefetches stay in flight
   const int K = KC > 0 ? KC : K_;
-  auto load = [&](int k0, float (&a)[4][4], floatx4 (&w)[4][4]) {
+  auto load_a = [&](int k0, float (&a)[4][4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int kb = k0 + 16 * u + 4 * kq;
@@ -87,11 +119,6 @@ __device__ __forceinline__ void contract(floatx4 (&acc)[4], const float* xrow, b
 #pragma unroll
         for (int s = 0; s < 4; ++s) a[u][s] = (a_live && kb + s < K) ? xrow[kb + s] : 0.f;
       }
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int k = kb + s;
-        w[u][s] = k < K ? *reinterpret_cast<const floatx4*>(W + (int64_t)k * ldw + c4) : floatx4{0.f, 0.f, 0.f, 0.f};
-      }
     }
   };
   auto compute = [&](const float (&a)[4][4], const floatx4 (&w)[4][4]) {
@@ -105,7 +132,7 @@ __device__ __forceinline__ void contract(floatx4 (&acc)[4], const float* xrow, b
     }
   };
   float a0[4][4], a1[4][4];
-  floatx4 w0[4][4], w1[4][4];
+  floatx4 w1[4][4];
   // (on the 256-deep contractions, scheduling barriers keep each chunk's
   // loads issued ahead of the previous chunk's MFMAs; left alone the
   // compiler sinks every load next to its MFMA and only two or three stay
@@ -113,21 +140,32 @@ __device__ __forceinline__ void contract(floatx4 (&acc)[4], const float* xrow, b
   auto fence = [] {
     if constexpr (KC > 0) __builtin_amdgcn_sched_barrier(0);
   };
-  load(0, a0, w0);
+  load_a(0, a0);
+  if (!PRE) load_w<KC>(0, w0, W, ldw, K, kq, c4);
   for (int k0 = 0; k0 < K; k0 += 128) {
-    if (k0 + 64 < K) load(k0 + 64, a1, w1);
+    if (k0 + 64 < K) {
+      load_a(k0 + 64, a1);
+      load_w<KC>(k0 + 64, w1, W, ldw, K, kq, c4);
+    }
     fence();
     compute(a0, w0);
     fence();
     if (k0 + 64 >= K) break;
-    if (k0 + 128 < K) load(k0 + 128, a0, w0);
+    if (k0 + 128 < K) {
+      load_a(k0 + 128, a0);
+      load_w<KC>(k0 + 128, w0, W, ldw, K, kq, c4);
+    }
     fence();
     compute(a1, w1);
     fence();
   }
 }
 
-template <bool VA>
+// ACT: the activation as a compile-time constant, so that the epilogue holds
+// only its code (a run-time switch per element interleaves every case's code,
+// tanhf's included, through the loop and the taken path thrashes the
+// instruction cache)
+template <bool VA, int ACT>
 __global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p) {
   __shared__ float sX[MC_ROWS][SX_PITCH];
   __shared__ float s_sum[4][MC_ROWS];
@@ -144,18 +182,29 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p) {
   const float* xrow = X + (a_live ? (int64_t)(p.idx ? p.idx[ra] : ra) * p.ldx : 0);
   const int c4 = 64 * wave + 4 * li;
 
+  // layer l's bias, scale and offset for this lane's features, and (l >= 1)
+  // the first chunk of its kernel: issued during layer l - 1, ahead of its
+  // stores
+  auto params = [&](int l, floatx4& bias4, floatx4& g4, floatx4& be4) {
+    const float* bias = p.bias[l] ? p.bias[l] + t * p.tP : nullptr;
+    bias4 = bias ? *reinterpret_cast<const floatx4*>(bias + c4) : floatx4{0.f, 0.f, 0.f, 0.f};
+    g4 = *reinterpret_cast<const floatx4*>(p.gamma[l] + t * p.tP + c4);
+    be4 = *reinterpret_cast<const floatx4*>(p.beta[l] + t * p.tP + c4);
+  };
+  floatx4 bias4, g4, be4;
+  params(0, bias4, g4, be4);
+  floatx4 w0[4][4];
+
   for (int l = 0; l < p.L; ++l) {
     const float* W = p.W[l] + t * p.tP;
     floatx4 acc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
     if (l == 0)
-      contract<0, VA>(acc, xrow, a_live, nullptr, W, p.ldw0, p.K0, kq, c4);
+      contract<0, VA>(acc, xrow, a_live, nullptr, W, p.ldw0, p.K0, kq, c4, w0);
     else
-      contract<1, true, MC_F>(acc, nullptr, true, &sX[li][0], W, p.ldw, MC_F, kq, c4);
+      contract<1, true, MC_F, true>(acc, nullptr, true, &sX[li][0], W, MC_F, MC_F, kq, c4, w0);
 
-    const float* bias = p.bias[l] ? p.bias[l] + t * p.tP : nullptr;
-    const floatx4 bias4 = bias ? *reinterpret_cast<const floatx4*>(bias + c4) : floatx4{0.f, 0.f, 0.f, 0.f};
     float z[4][4];
     float ps[4], pq[4];
 #pragma unroll
@@ -180,10 +229,13 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p) {
         s_sq[wave][4 * kq + v] = pq[v];
       }
     }
+    const floatx4 gl = g4, bel = be4;
+    if (l + 1 < p.L) {
+      load_w<MC_F>(0, w0, p.W[l + 1] + t * p.tP, MC_F, MC_F, kq, c4);
+      params(l + 1, bias4, g4, be4);
+    }
     // every wave is past its contraction (its reads of sX) once here
     __syncthreads();
-    const floatx4 g4 = *reinterpret_cast<const floatx4*>(p.gamma[l] + t * p.tP + c4);
-    const floatx4 be4 = *reinterpret_cast<const floatx4*>(p.beta[l] + t * p.tP + c4);
     float* Zl = p.Z[l] + t * p.tR;
     float* Yl = p.Y[l] + t * p.tR;
 #pragma unroll
@@ -198,7 +250,7 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         zo[j] = z[v][j];
-        yo[j] = ppo::act_fwd(p.act, ppo::ln_apply(z[v][j], mean, rstd, g4[j], be4[j]));
+        yo[j] = ppo::act_fwd(ACT, ppo::ln_apply(z[v][j], mean, rstd, gl[j], bel[j]));
       }
       if (l + 1 < p.L) *reinterpret_cast<floatx4*>(&sX[rr][c4]) = yo;
       if (row >= p.M) continue;
@@ -231,6 +283,7 @@ struct BwdArgs {
   int64_t tR, tS, tP, tWT, tPart;
 };
 
+template <int ACT>
 __global__ void __launch_bounds__(MC_THREADS) mlp_ln_bwd_kernel(BwdArgs p) {
   __shared__ float sX[MC_ROWS][SX_PITCH];
   __shared__ float s_sum[4][MC_ROWS];
@@ -257,30 +310,46 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_bwd_kernel(BwdArgs p) {
     }
   }
 
-  for (int l = p.L - 1; l >= 0; --l) {
+  // layer l's LayerNorm operands for this lane (Z at rows 4 kq + v, their
+  // statistics, scale and offset): issued during layer l + 1 before its dX
+  // contraction, and the first chunk of that contraction's kernel ahead of
+  // layer l + 1's stores
+  floatx4 zz[4], g4, be4;
+  float mu[4], rs[4];
+  auto ln_ops = [&](int l) {
     const float* Zl = p.Z[l] + t * p.tR;
-    const floatx4 g4 = *reinterpret_cast<const floatx4*>(p.gamma[l] + t * p.tP + c4);
-    const floatx4 be4 = *reinterpret_cast<const floatx4*>(p.beta[l] + t * p.tP + c4);
-    float xh[4][4], g[4][4], mu[4], rs[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = r0 + 4 * kq + v;
+      const int rr = row < p.M ? row : r0;
+      zz[v] = *reinterpret_cast<const floatx4*>(Zl + (int64_t)rr * p.ld + c4);
+      mu[v] = p.mean[l][t * p.tS + rr];
+      rs[v] = p.rstd[l][t * p.tS + rr];
+    }
+    g4 = *reinterpret_cast<const floatx4*>(p.gamma[l] + t * p.tP + c4);
+    be4 = *reinterpret_cast<const floatx4*>(p.beta[l] + t * p.tP + c4);
+  };
+  ln_ops(p.L - 1);
+  floatx4 w0[4][4];
+
+  for (int l = p.L - 1; l >= 0; --l) {
+    float xh[4][4], g[4][4], rsl[4];
     float sg[4], sgx[4];
     float pg[4] = {0.f, 0.f, 0.f, 0.f}, pb[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int row = r0 + 4 * kq + v;
       const bool live = row < p.M;
-      const int rr = live ? row : r0;
-      const floatx4 zz = *reinterpret_cast<const floatx4*>(Zl + (int64_t)rr * p.ld + c4);
-      mu[v] = p.mean[l][t * p.tS + rr];
-      rs[v] = p.rstd[l][t * p.tS + rr];
+      rsl[v] = rs[v];
       sg[v] = 0.f;
       sgx[v] = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        xh[v][j] = live ? (zz[j] - mu[v]) * rs[v] : 0.f;
+        xh[v][j] = live ? (zz[v][j] - mu[v]) * rs[v] : 0.f;
         // the forward's normalised value, rounded as the forward rounded it
-        const float yl = ppo::ln_apply(zz[j], mu[v], rs[v], g4[j], be4[j]);
-        const float a = (p.act == ACT_RELU || p.act == ACT_TANH) ? ppo::act_fwd(p.act, yl) : yl;
-        const float dyl = live ? dy[v][j] * ppo::act_grad(p.act, a) : 0.f;
+        const float yl = ppo::ln_apply(zz[v][j], mu[v], rs[v], g4[j], be4[j]);
+        const float a = (ACT == ACT_RELU || ACT == ACT_TANH) ? ppo::act_fwd(ACT, yl) : yl;
+        const float dyl = live ? dy[v][j] * ppo::act_grad(ACT, a) : 0.f;
         pg[j] += dyl * xh[v][j];
         pb[j] += dyl;
         g[v][j] = dyl * g4[j];
@@ -309,6 +378,7 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_bwd_kernel(BwdArgs p) {
       pg[j] += __shfl_xor(pg[j], 32);
       pb[j] += __shfl_xor(pb[j], 32);
     }
+    if (l > 0) load_w<MC_F>(0, w0, p.WT[l] + t * p.tWT, MC_F, MC_F, kq, c4);
     if (kq == 0) {
       float* part = p.part[l] + t * p.tPart + (int64_t)blockIdx.x * 2 * MC_F;
       *reinterpret_cast<floatx4*>(part + c4) = floatx4{pg[0], pg[1], pg[2], pg[3]};
@@ -325,17 +395,18 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_bwd_kernel(BwdArgs p) {
       const float s2 = ((s_sq[0][rr] + s_sq[1][rr]) + (s_sq[2][rr] + s_sq[3][rr])) / (float)MC_F;
       floatx4 d;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) d[j] = row < p.M ? rs[v] * (g[v][j] - s - xh[v][j] * s2) : 0.f;
+      for (int j = 0; j < 4; ++j) d[j] = row < p.M ? rsl[v] * (g[v][j] - s - xh[v][j] * s2) : 0.f;
       if (l > 0) *reinterpret_cast<floatx4*>(&sX[rr][c4]) = d;
       if (row < p.M) *reinterpret_cast<floatx4*>(dZl + (int64_t)row * p.ld + c4) = d;
     }
     if (l == 0) break;
     __syncthreads();
+    ln_ops(l - 1);
     // dY of layer l - 1 = dZ_l W_l^T, from the transposed kernel WT_l[out][in]
     floatx4 acc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-    contract<1, true, MC_F>(acc, nullptr, true, &sX[li][0], p.WT[l] + t * p.tWT, p.ldwt, MC_F, kq, c4);
+    contract<1, true, MC_F, true>(acc, nullptr, true, &sX[li][0], p.WT[l] + t * p.tWT, MC_F, MC_F, kq, c4, w0);
 #pragma unroll
     for (int v = 0; v < 4; ++v)
 #pragma unroll
@@ -387,7 +458,7 @@ PPO_EXPORT int ppo_mlp_ln_fwd_f32(void* stream, int towers, int L, const float* 
                                  float* const* mean, float* const* rstd, float eps, int act, int64_t stride_x,
                                  int64_t stride_params, int64_t stride_rows, int64_t stride_stats) {
   if (towers < 1 || towers > 8 || L < 1 || L > MC_MAXL || M < 0 || K0 < 1 || act < 0 || act > 3 || ldx < K0 ||
-      ldw0 < MC_F || ldw < MC_F || ld < MC_F || !W || !bias || !gamma || !beta || !Z || !Y || !mean || !rstd ||
+      ldw0 < MC_F || ldw != MC_F || ld < MC_F || !W || !bias || !gamma || !beta || !Z || !Y || !mean || !rstd ||
       ldw0 % 4 || ldw % 4 || ld % 4 || (towers > 1 && (stride_x % 4 || stride_params % 4 || stride_rows % 4)))
     return ppo::set_error(PPO_ERR_ARG, "ppo_mlp_ln_fwd_f32: bad argument (towers=%d L=%d M=%d K0=%d)", towers, L,
                           M, K0);
@@ -407,10 +478,17 @@ PPO_EXPORT int ppo_mlp_ln_fwd_f32(void* stream, int towers, int L, const float* 
   }
   const bool va = aligned16(X) && ldx % 4 == 0 && K0 % 4 == 0 && (towers == 1 || stride_x % 4 == 0);
   const dim3 grid(ppo::ceil_div(M, MC_ROWS), towers), block(MC_THREADS);
-  if (va)
-    hipLaunchKernelGGL(mlp_ln_fwd_kernel<true>, grid, block, 0, ppo::as_stream(stream), a);
-  else
-    hipLaunchKernelGGL(mlp_ln_fwd_kernel<false>, grid, block, 0, ppo::as_stream(stream), a);
+  hipStream_t st = ppo::as_stream(stream);
+#define PPO_CHAIN_FWD(ACTV)                                                   \
+  if (va) hipLaunchKernelGGL((mlp_ln_fwd_kernel<true, ACTV>), grid, block, 0, st, a); \
+  else hipLaunchKernelGGL((mlp_ln_fwd_kernel<false, ACTV>), grid, block, 0, st, a);
+  switch (act) {
+    case ACT_RELU: PPO_CHAIN_FWD(ACT_RELU) break;
+    case ACT_TANH: PPO_CHAIN_FWD(ACT_TANH) break;
+    case ACT_SILU: PPO_CHAIN_FWD(ACT_SILU) break;
+    default: PPO_CHAIN_FWD(ACT_NONE) break;
+  }
+#undef PPO_CHAIN_FWD
   return ppo::check_launch("ppo_mlp_ln_fwd_f32");
 }
 
@@ -427,7 +505,7 @@ PPO_EXPORT int ppo_mlp_ln_bwd_f32(void* stream, int towers, int L, const float* 
                                  int64_t stride_rows, int64_t stride_stats, int64_t stride_params,
                                  int64_t stride_wt, int64_t stride_part) {
   if (towers < 1 || towers > 8 || L < 1 || L > MC_MAXL || M < 0 || act < 0 || act > 3 || lddy < MC_F ||
-      ld < MC_F || ldwt < MC_F || !dY || !Z || !mean || !rstd || !gamma || !beta || !WT || !dZ || !partial ||
+      ld < MC_F || ldwt != MC_F || !dY || !Z || !mean || !rstd || !gamma || !beta || !WT || !dZ || !partial ||
       lddy % 4 || ld % 4 || ldwt % 4 ||
       (towers > 1 && (stride_rows % 4 || stride_params % 4 || stride_wt % 4 || stride_part % 4)))
     return ppo::set_error(PPO_ERR_ARG, "ppo_mlp_ln_bwd_f32: bad argument (towers=%d L=%d M=%d)", towers, L, M);
@@ -445,7 +523,12 @@ PPO_EXPORT int ppo_mlp_ln_bwd_f32(void* stream, int towers, int L, const float* 
     a.WT[l] = l > 0 ? WT[l] : nullptr; a.dZ[l] = dZ[l]; a.part[l] = partial[l];
   }
   const dim3 grid(ppo::ceil_div(M, MC_ROWS), towers), block(MC_THREADS);
-  hipLaunchKernelGGL(mlp_ln_bwd_kernel, grid, block, 0, ppo::as_stream(stream), a);
+  switch (act) {
+    case ACT_RELU: hipLaunchKernelGGL(mlp_ln_bwd_kernel<ACT_RELU>, grid, block, 0, ppo::as_stream(stream), a); break;
+    case ACT_TANH: hipLaunchKernelGGL(mlp_ln_bwd_kernel<ACT_TANH>, grid, block, 0, ppo::as_stream(stream), a); break;
+    case ACT_SILU: hipLaunchKernelGGL(mlp_ln_bwd_kernel<ACT_SILU>, grid, block, 0, ppo::as_stream(stream), a); break;
+    default: hipLaunchKernelGGL(mlp_ln_bwd_kernel<ACT_NONE>, grid, block, 0, ppo::as_stream(stream), a); break;
+  }
   return ppo::check_launch("ppo_mlp_ln_bwd_f32");
 }
 

@@ -208,7 +208,7 @@ int ppo_gemm_ln_act_fwd_f32_towers(void* stream, int towers, const float* X, int
  *
  * Forward: layer 0 reads X (row r = X[rows_idx[r]] when rows_idx is
  * non-NULL; K0 features, kernel [K0][ldw0]), layer l > 0 the previous
- * output (kernel [256][ldw]); each layer writes Z = x W + b, its row mean /
+ * output (kernel [256][ldw], ldw == 256); each layer writes Z = x W + b, its row mean /
  * rstd (fast variance) and Y = act(LayerNorm(Z)).  Bit-identical to one
  * ppo_gemm_ln_act_fwd_f32 per layer. */
 int ppo_mlp_chain_max_layers(void);
@@ -221,7 +221,7 @@ int ppo_mlp_ln_fwd_f32(void* stream, int towers, int L, const float* X, int64_t 
  * activation + LayerNorm backward (writes dZ and partial[blocks][2 * 256],
  * the scale | bias gradient sums of each 16-row block, blocks =
  * ppo_mlp_ln_bwd_blocks(M)) and for l > 0 the input cotangent dZ W_l^T read
- * through WT[l] = W_l transposed ([256 out][ldwt], e.g. from
+ * through WT[l] = W_l transposed ([256 out][ldwt], ldwt == 256, e.g. from
  * ppo_transpose_f32_batched).  The values of ppo_layernorm_act_bwd_f32 and
  * ppo_gemm_f32 (dZ W^T) per layer, up to float32 summation order. */
 int ppo_mlp_ln_bwd_blocks(int rows);

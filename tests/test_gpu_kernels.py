@@ -196,6 +196,40 @@ def test_gemm_activation_derivative_epilogue(act):
     gemm_case(0, 1, 300, 256, 136, epi=2, act=act)
 
 
+def test_silu_and_its_derivative_on_special_and_extreme_arguments():
+    """SiLU x / (1 + exp(-x)) and its derivative s (1 + x (1 - s)) take the
+    quotient from the hardware reciprocal with one residual correction: the
+    elementwise entry points against float64 over ordinary and extreme
+    arguments, and the IEEE results of the division where the exponential
+    overflows, the argument is infinite, NaN or a signed zero."""
+    rng = np.random.default_rng(11)
+    special = np.array([np.inf, -np.inf, np.nan, 0.0, -0.0, 1e-40, -1e-40, 88.0, -88.0, -103.0, -200.0, 200.0,
+                        1.0, -1.0, 1e-20, -1e-20], dtype=np.float32)
+    x = np.concatenate([special, (rng.standard_normal(4080) * 6).astype(np.float32),
+                        rng.uniform(-90, 90, 4096).astype(np.float32)]).reshape(-1, 64)
+    dy = rng.standard_normal(x.shape).astype(np.float32)
+    X, DY = dev(x), dev(dy)
+    Y, DX = torch.empty_like(X), torch.empty_like(X)
+    rows, F = x.shape
+    _lib.call("ppo_act_fwd_f32", st(), X.data_ptr(), F, Y.data_ptr(), F, rows, F, _lib.ACT["silu"])
+    _lib.call("ppo_act_bwd_f32", st(), DY.data_ptr(), F, X.data_ptr(), F, DX.data_ptr(), F, rows, F, _lib.ACT["silu"])
+    y, dx = host(Y).ravel(), host(DX).ravel()
+    xs = x.ravel().astype(np.float64)
+    with np.errstate(over="ignore", invalid="ignore"):
+        s = 1.0 / (1.0 + np.exp(-xs))
+        y_ref = xs * s
+        g_ref = s * (1.0 + xs * (1.0 - s))
+    fin = np.isfinite(xs)
+    # float32 exp of arguments near 88 carries ~1e-5 relative error from its range reduction, and
+    # overflows below -88.7, where SiLU (|y| < 1e-35) comes out as -0
+    np.testing.assert_allclose(y[fin], y_ref[fin], rtol=2e-5, atol=1e-35)
+    np.testing.assert_allclose(dx[fin], (dy.ravel() * g_ref)[fin], rtol=2e-5, atol=1e-30)
+    assert y[0] == np.inf and np.isnan(y[1]) and np.isnan(y[2])
+    assert y[3] == 0 and not np.signbit(y[3]) and y[4] == 0 and np.signbit(y[4])
+    assert y[10] == 0 and np.signbit(y[10]) and y[11] == 200.0   # exp(200) overflows: -200 / inf = -0
+    assert np.isfinite(dx[fin]).all()
+
+
 @pytest.mark.parametrize("splits", [1, 4, 64])
 def test_gemm_split_rows_with_bias_gradient(splits):
     gemm_case(1, 0, 400, 256, 4096, rows_src=8192, gather=True, splits=splits, bias_grad=True)
