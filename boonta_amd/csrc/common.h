@@ -183,10 +183,16 @@ __device__ __forceinline__ float div_ge1(float x, float d) {
   return (res == 0.f || !__builtin_isfinite(q1)) ? q : q1;
 }
 
+// tanhf out of line: its expansion is long, and kernels that take the
+// activation at run time switch on it per element inside unrolled epilogues,
+// where every inlined copy (taken or not) would sit between the taken
+// case's instructions.
+static __device__ __attribute__((noinline)) float tanh_call(float x) { return tanhf(x); }
+
 __device__ __forceinline__ float act_fwd(int act, float x) {
   switch (act) {
     case ACT_RELU: return x > 0.f ? x : 0.f;
-    case ACT_TANH: return tanhf(x);
+    case ACT_TANH: return tanh_call(x);
     case ACT_SILU: return div_ge1(x, 1.f + __expf(-x));
     default: return x;
   }
