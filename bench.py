@@ -145,6 +145,20 @@ def _single_launch_work(name, args):
         acts = (1 if args[26] else 0) + (1 if args[31] else 0)
         per_row = 4.0 * F * (2 * groups + acts) + 4.0 * 6 + (4.0 * A if args[1] == 1 else 0.0)
         return 0.0, rows * per_row
+    if name == "ppo_mlp_ln_fwd_f32":
+        towers, L, M, K0 = args[1], args[2], args[6], args[7]
+        weights = 256 * (K0 + 256 * (L - 1)) + 3 * 256 * L
+        return towers * 2.0 * M * 256 * (K0 + 256 * (L - 1)), towers * 4.0 * (M * K0 + weights + M * L * (2 * 256 + 2))
+    if name == "ppo_mlp_ln_bwd_f32":
+        towers, L, M = args[1], args[2], args[5]
+        weights = 256 * 256 * (L - 1) + 2 * 256 * L
+        return towers * 2.0 * M * 256 * 256 * (L - 1), towers * 4.0 * (M * 256 + weights + M * L * (2 * 256 + 2))
+    if name == "ppo_gru_fwd_seq_f32":
+        Bm, H, T = args[-6], args[-5], args[-4]
+        return 2.0 * Bm * H * 3 * H * T, 4.0 * T * Bm * (3 * H + H + H + 4 * H) + 4.0 * H * 3 * H
+    if name == "ppo_gru_bwd_seq_f32":
+        Bm, H, T = args[-6], args[-5], args[-4]
+        return 2.0 * Bm * 3 * H * H * max(T - 1, 0), 4.0 * T * Bm * (H + 4 * H + H + H + 4 * H) + 4.0 * H * 3 * H
     if name in ("ppo_gru_fwd_step_f32",):
         Bm, H = args[-2], args[-1]
         return 2.0 * Bm * H * 3 * H, 4.0 * Bm * (3 * H + 2 * H + 6 * H) + 4.0 * H * 3 * H
@@ -166,8 +180,10 @@ def _single_launch_work(name, args):
 
 def launch_shape(name, args):
     """[M, N, K] of a contraction launch (the one-launch step: [rows, 256,
-    observation features, trunk layers]; None for the others), with the
-    tower count appended for a tower-batched launch."""
+    observation features, trunk layers]; a torso chain: [rows, 256, first
+    layer's inputs, layers, towers]; a GRU sequence launch: [sequences,
+    units, steps]; None for the others), with the tower count appended for a
+    tower-batched launch."""
     base, bargs, towers = untower(name, args)
     shape = _single_launch_shape(base, bargs)
     return shape + [towers] if shape is not None and towers > 1 else shape
@@ -182,6 +198,12 @@ def _single_launch_shape(name, args):
         return [args[15], args[17], args[16]]
     if name == "ppo_step_mlp_categorical_f32":
         return [args[3], 256, args[4], args[5]]
+    if name == "ppo_mlp_ln_fwd_f32":
+        return [args[6], 256, args[7], args[2], args[1]]
+    if name == "ppo_mlp_ln_bwd_f32":
+        return [args[5], 256, 256, args[2], args[1]]
+    if name in ("ppo_gru_fwd_seq_f32", "ppo_gru_bwd_seq_f32"):
+        return [args[-6], args[-5], args[-4]]
     if name.startswith("ppo_gru"):
         return [args[-2], args[-1]]
     return None
@@ -205,6 +227,8 @@ def launch_key(name, args):
         return (name,) + tuple(args[1:5]) + tuple(args[12:16])
     if name in ("ppo_gru_fwd_step_f32", "ppo_gru_bwd_step_f32"):
         return (name, args[-2], args[-1], bool(args[1]))
+    if name in ("ppo_gru_fwd_seq_f32", "ppo_gru_bwd_seq_f32"):
+        return (name, args[-6], args[-5], args[-4])
     return (name, id(args))
 
 
