@@ -52,10 +52,9 @@ SIGNATURES = {
     "ppo_gemm_ln_act_fwd_f32": (I, [P, P, I64, P, P, I64, P, P, P, P, I64, P, I64, P, P, I, I, I, F, I]),
     "ppo_mlp_chain_max_layers": (I, []),
     "ppo_mlp_ln_fwd_f32": (I, [P, I, I, P, I64, P, I, I, P, I64, I64, P, P, P, P, P, I64, P, P, F, I, I64, I64, I64,
-                               I64]),
+                               I64, P, I64]),
     "ppo_mlp_ln_bwd_blocks": (I, [I]),
     "ppo_mlp_ln_bwd_f32": (I, [P, I, I, P, I64, I, P, P, P, P, P, P, I64, P, I64, P, I, I64, I64, I64, I64, I64]),
-    "ppo_transpose_f32_batched": (I, [P, I, P, P, I, I, I64, I64]),
     "ppo_gemm_ln_act_fwd_f32_towers": (I, [P, I, P, I64, P, P, I64, P, P, P, P, I64, P, I64, P, P, I, I, I, F, I,
                                            I64, I64, I64, I64]),
     "ppo_linear_scan_fwd": (I, [P, I, P, P, P, P, I, I, I]),

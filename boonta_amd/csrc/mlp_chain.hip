@@ -20,9 +20,9 @@
 // one 16-byte vector.  The forward's contraction and epilogue are those of
 // ppo_gemm_ln_act_fwd_f32 (same k order, same statistics), so a chain is
 // bit-identical to one fused launch per layer.  The backward's dX = dZ W^T
-// reads the layer's kernel transposed (an image refreshed from the
-// parameters before each step, ppo_transpose_f32_batched), which gives its
-// B operand the forward's coalesced row reads.
+// reads the layer's kernel transposed (an image the forward writes from the
+// parameters it is given, each workgroup a share of its rows), which gives
+// its B operand the forward's coalesced row reads.
 #include "common.h"
 
 namespace {
@@ -55,9 +55,10 @@ struct FwdArgs {
   float* Y[MC_MAXL];
   float* mean[MC_MAXL];
   float* rstd[MC_MAXL];
-  // tower t's input, parameters, rows (Z, Y) and statistics sit t times
-  // these element strides after tower 0's
-  int64_t tX, tP, tR, tS;
+  float* WT[MC_MAXL];  // layer l >= 1: its kernel transposed [256 out][256 in] (written), or all null
+  // tower t's input, parameters, rows (Z, Y), statistics and transposed
+  // kernels sit t times these element strides after tower 0's
+  int64_t tX, tP, tR, tS, tWT;
 };
 
 // One layer's 16 x 256 contraction: acc[j] += A[rows][k] W[k][c4 + j] in the
@@ -195,6 +196,58 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p) {
   params(0, bias4, g4, be4);
   floatx4 w0[4][4];
 
+  // this workgroup's share of the transposed kernels of layers 1.. (the
+  // backward's dX reads them): 32 x 32 tiles of WT_l[o][k] = W_l[k][o],
+  // tiles blockIdx.x + i gridDim.x of the (L - 1) x 64 of a tower.  Up to
+  // WT_EARLY tiles per workgroup: each thread loads one 16-byte run of a
+  // tile row here, puts it in an LDS tile after the first layer's
+  // contraction and writes a 16-byte run of the transposed tile after that
+  // layer's statistics barrier (loads and stores coalesced, off the chain's
+  // path); more tiles go through a loop at the end of the kernel.
+  constexpr int WT_EARLY = 2;
+  __shared__ float s_tile[WT_EARLY][32][33];
+  const int nwg = gridDim.x;
+  const int wt_tiles = p.WT[1] != nullptr ? (p.L - 1) * 64 : 0;
+  const int wt_mine = wt_tiles > (int)blockIdx.x ? (wt_tiles - 1 - (int)blockIdx.x) / nwg + 1 : 0;
+  const bool wt_early = wt_mine <= WT_EARLY;
+  const int tr_row = threadIdx.x >> 3, tr_q = threadIdx.x & 7;   // tile row / 16-byte run of it
+  // W_l or WT_l of layer ll (read through compile-time indices: a run-time
+  // index into the argument arrays would put them in scratch)
+  auto wl = [&](int ll) {
+    const float* r = nullptr;
+#pragma unroll
+    for (int q = 1; q < MC_MAXL; ++q)
+      if (q == ll) r = p.W[q];
+    return r + t * p.tP;
+  };
+  auto wtl = [&](int ll) {
+    float* r = nullptr;
+#pragma unroll
+    for (int q = 1; q < MC_MAXL; ++q)
+      if (q == ll) r = p.WT[q];
+    return r + t * p.tWT;
+  };
+  // tile id -> layer, 32-row block of k, 32-column block of o
+  auto tile_src = [&](int id) {
+    const int ll = 1 + id / 64, tk = (id & 63) >> 3, to = id & 7;
+    return wl(ll) + (int64_t)(32 * tk + tr_row) * MC_F + 32 * to + 4 * tr_q;
+  };
+  auto tile_dst = [&](int id) {
+    const int ll = 1 + id / 64, tk = (id & 63) >> 3, to = id & 7;
+    return wtl(ll) + (int64_t)(32 * to + tr_row) * MC_F + 32 * tk + 4 * tr_q;
+  };
+  floatx4 tv[WT_EARLY];
+  if (wt_early) {
+#pragma unroll
+    for (int i = 0; i < WT_EARLY; ++i)
+      if (i < wt_mine) tv[i] = *reinterpret_cast<const floatx4*>(tile_src(blockIdx.x + i * nwg));
+  }
+  // the transposed run of tile i this thread writes: o = row, k = 4 q .. 4 q + 3
+  auto tile_out = [&](int i) {
+    return floatx4{s_tile[i][4 * tr_q][tr_row], s_tile[i][4 * tr_q + 1][tr_row], s_tile[i][4 * tr_q + 2][tr_row],
+                   s_tile[i][4 * tr_q + 3][tr_row]};
+  };
+
   for (int l = 0; l < p.L; ++l) {
     const float* W = p.W[l] + t * p.tP;
     floatx4 acc[4];
@@ -229,6 +282,13 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p) {
         s_sq[wave][4 * kq + v] = pq[v];
       }
     }
+    if (l == 0 && wt_early) {
+#pragma unroll
+      for (int i = 0; i < WT_EARLY; ++i)
+        if (i < wt_mine)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s_tile[i][tr_row][4 * tr_q + e] = tv[i][e];
+    }
     const floatx4 gl = g4, bel = be4;
     if (l + 1 < p.L) {
       load_w<MC_F>(0, w0, p.W[l + 1] + t * p.tP, MC_F, MC_F, kq, c4);
@@ -236,6 +296,11 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p) {
     }
     // every wave is past its contraction (its reads of sX) once here
     __syncthreads();
+    if (l == 0 && wt_early) {
+#pragma unroll
+      for (int i = 0; i < WT_EARLY; ++i)
+        if (i < wt_mine) *reinterpret_cast<floatx4*>(tile_dst(blockIdx.x + i * nwg)) = tile_out(i);
+    }
     float* Zl = p.Z[l] + t * p.tR;
     float* Yl = p.Y[l] + t * p.tR;
 #pragma unroll
@@ -263,6 +328,17 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p) {
     }
     // the next layer's contraction reads the tile (and s_sum is rewritten)
     __syncthreads();
+  }
+  if (!wt_early) {
+    for (int i = 0; i < wt_mine; ++i) {
+      const int id = blockIdx.x + i * nwg;
+      const floatx4 v = *reinterpret_cast<const floatx4*>(tile_src(id));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s_tile[0][tr_row][4 * tr_q + e] = v[e];
+      __syncthreads();
+      *reinterpret_cast<floatx4*>(tile_dst(id)) = tile_out(0);
+      __syncthreads();
+    }
   }
 }
 
@@ -414,34 +490,6 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_bwd_kernel(BwdArgs p) {
   }
 }
 
-// dst[b][c][r] = src[b][r][c] for a batch of row-major matrices, through 32 x 32
-// LDS tiles (coalesced reads and writes).
-struct TransposeArgs {
-  const float* src[2 * MC_MAXL];
-  float* dst[2 * MC_MAXL];
-  int rows, cols;
-  int64_t lds, ldd;
-};
-
-__global__ void __launch_bounds__(256) transpose_kernel(TransposeArgs a) {
-  __shared__ float tile[32][33];
-  const float* src = a.src[blockIdx.z];
-  float* dst = a.dst[blockIdx.z];
-  const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
-#pragma unroll
-  for (int i = 0; i < 32; i += 8) {
-    const int r = r0 + ty + i, c = c0 + tx;
-    if (r < a.rows && c < a.cols) tile[ty + i][tx] = src[(int64_t)r * a.lds + c];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 32; i += 8) {
-    const int c = c0 + ty + i, r = r0 + tx;
-    if (r < a.rows && c < a.cols) dst[(int64_t)c * a.ldd + r] = tile[tx][ty + i];
-  }
-}
-
 bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
 
 }  // namespace
@@ -456,7 +504,8 @@ PPO_EXPORT int ppo_mlp_ln_fwd_f32(void* stream, int towers, int L, const float* 
                                  int64_t ldw, const float* const* bias, const float* const* gamma,
                                  const float* const* beta, float* const* Z, float* const* Y, int64_t ld,
                                  float* const* mean, float* const* rstd, float eps, int act, int64_t stride_x,
-                                 int64_t stride_params, int64_t stride_rows, int64_t stride_stats) {
+                                 int64_t stride_params, int64_t stride_rows, int64_t stride_stats,
+                                 float* const* WT, int64_t stride_wt) {
   if (towers < 1 || towers > 8 || L < 1 || L > MC_MAXL || M < 0 || K0 < 1 || act < 0 || act > 3 || ldx < K0 ||
       ldw0 < MC_F || ldw != MC_F || ld < MC_F || !W || !bias || !gamma || !beta || !Z || !Y || !mean || !rstd ||
       ldw0 % 4 || ldw % 4 || ld % 4 || (towers > 1 && (stride_x % 4 || stride_params % 4 || stride_rows % 4)))
@@ -466,8 +515,16 @@ PPO_EXPORT int ppo_mlp_ln_fwd_f32(void* stream, int towers, int L, const float* 
   FwdArgs a{};
   a.X = X; a.ldx = ldx; a.idx = rows_idx; a.M = M; a.K0 = K0; a.L = L; a.act = act; a.eps = eps;
   a.ldw0 = ldw0; a.ldw = ldw; a.ld = ld;
-  a.tX = stride_x; a.tP = stride_params; a.tR = stride_rows; a.tS = stride_stats;
+  a.tX = stride_x; a.tP = stride_params; a.tR = stride_rows; a.tS = stride_stats; a.tWT = stride_wt;
   if (!X) return ppo::set_error(PPO_ERR_ARG, "ppo_mlp_ln_fwd_f32: null input");
+  if (WT && L > 1) {
+    if (towers > 1 && stride_wt % 4) return ppo::set_error(PPO_ERR_ARG, "ppo_mlp_ln_fwd_f32: bad WT stride");
+    for (int l = 1; l < L; ++l) {
+      if (!WT[l] || !aligned16(WT[l]))
+        return ppo::set_error(PPO_ERR_ARG, "ppo_mlp_ln_fwd_f32: layer %d needs a 16-byte aligned WT", l);
+      a.WT[l] = WT[l];
+    }
+  }
   for (int l = 0; l < L; ++l) {
     if (!W[l] || !gamma[l] || !beta[l] || !Z[l] || !Y[l] || !mean[l] || !rstd[l] || !aligned16(W[l]) ||
         (bias[l] && !aligned16(bias[l])) || !aligned16(gamma[l]) || !aligned16(beta[l]) || !aligned16(Z[l]) ||
@@ -530,23 +587,4 @@ PPO_EXPORT int ppo_mlp_ln_bwd_f32(void* stream, int towers, int L, const float* 
     default: hipLaunchKernelGGL(mlp_ln_bwd_kernel<ACT_NONE>, grid, block, 0, ppo::as_stream(stream), a); break;
   }
   return ppo::check_launch("ppo_mlp_ln_bwd_f32");
-}
-
-// dst[b] = src[b]^T for n <= 16 row-major [rows][cols] matrices (pitches lds, ldd).
-PPO_EXPORT int ppo_transpose_f32_batched(void* stream, int n, const float* const* src, float* const* dst, int rows,
-                                        int cols, int64_t lds, int64_t ldd) {
-  if (n < 0 || n > 2 * MC_MAXL || rows < 0 || cols < 0 || lds < cols || ldd < rows || (n > 0 && (!src || !dst)))
-    return ppo::set_error(PPO_ERR_ARG, "ppo_transpose_f32_batched: bad argument (n=%d rows=%d cols=%d)", n, rows,
-                          cols);
-  if (n == 0 || rows == 0 || cols == 0) return PPO_OK;
-  TransposeArgs a{};
-  a.rows = rows; a.cols = cols; a.lds = lds; a.ldd = ldd;
-  for (int b = 0; b < n; ++b) {
-    if (!src[b] || !dst[b]) return ppo::set_error(PPO_ERR_ARG, "ppo_transpose_f32_batched: null matrix %d", b);
-    a.src[b] = src[b];
-    a.dst[b] = dst[b];
-  }
-  const dim3 grid(ppo::ceil_div(cols, 32), ppo::ceil_div(rows, 32), n);
-  hipLaunchKernelGGL(transpose_kernel, grid, dim3(256), 0, ppo::as_stream(stream), a);
-  return ppo::check_launch("ppo_transpose_f32_batched");
 }

@@ -714,14 +714,8 @@ class MLPExecutor(ForwardChain):
         T["rstd"] = arr([_p(lb.rstd) for lb in A])
         T["dZ"] = arr([_p(lb.dZ) for lb in A])
         T["part"] = arr([_p(lb.lnpart) for lb in A])
+        # the forward writes layer l >= 1's kernel transposed into WT[l - 1, tower]
         T["WT"] = arr([None] + [_p(self.WT[l - 1, 0]) for l in range(1, L)])
-        # the transposes: layer l >= 1 of each tower into WT[l - 1, tower]
-        src, dst = [], []
-        for l in range(1, L):
-            for t in range(2):
-                src.append(view(specs[l].dense.w) + 4 * t * self.pair)
-                dst.append(_p(self.WT[l - 1, t]))
-        T["tsrc"], T["tdst"], T["nT"] = arr(src), arr(dst), len(src)
         boot = self.boot_layers
         cspecs = [lb.spec for lb in boot]
         T["bW"] = arr([view(s.dense.w) for s in cspecs])
@@ -918,7 +912,7 @@ class MLPExecutor(ForwardChain):
         s0 = boot[0].spec
         self._call("ppo_mlp_ln_fwd_f32", st, 1, len(boot), x, ldx, None, nrows, s0.dense.fin, c["bW"],
                    s0.dense.w.ld, 256, c["bb"], c["bg"], c["bbe"], c["bZ"], c["bY"], s0.ld, c["bmean"], c["brstd"],
-                   self._chain_eps, self._chain_act, 0, 0, 0, 0)
+                   self._chain_eps, self._chain_act, 0, 0, 0, 0, None, 0)
         return _p(boot[-1].Y), boot[-1].spec.ld
 
     def _fwd_pair(self, st, x, ldx, rows_idx, nrows):
@@ -927,11 +921,11 @@ class MLPExecutor(ForwardChain):
         D, sx = self.pair, 0
         if self.chain_ln:
             c, s0 = self._chain, self.actor[0].spec
-            # the kernels' transposed images for this step's backward
-            self._call("ppo_transpose_f32_batched", st, c["nT"], c["tsrc"], c["tdst"], 256, 256, 256, 256)
+            # (it also writes the kernels' transposed images for this step's backward)
             self._call("ppo_mlp_ln_fwd_f32", st, 2, len(self.actor), x, ldx, rows_idx, nrows, s0.dense.fin, c["W"],
                        s0.dense.w.ld, 256, c["b"], c["g"], c["be"], c["Z"], c["Y"], s0.ld, c["mean"], c["rstd"],
-                       self._chain_eps, self._chain_act, 0, D, self._chain_rs, self._chain_ss)
+                       self._chain_eps, self._chain_act, 0, D, self._chain_rs, self._chain_ss, c["WT"],
+                       256 * 256)
             return
         for la, lc in zip(self.actor, self.critic):
             s = la.spec

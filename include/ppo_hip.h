@@ -210,19 +210,22 @@ int ppo_gemm_ln_act_fwd_f32_towers(void* stream, int towers, const float* X, int
  * non-NULL; K0 features, kernel [K0][ldw0]), layer l > 0 the previous
  * output (kernel [256][ldw], ldw == 256); each layer writes Z = x W + b, its row mean /
  * rstd (fast variance) and Y = act(LayerNorm(Z)).  Bit-identical to one
- * ppo_gemm_ln_act_fwd_f32 per layer. */
+ * ppo_gemm_ln_act_fwd_f32 per layer.  WT (may be NULL): for l >= 1, WT[l]
+ * receives layer l's kernel transposed ([256 out][256 in], pitch 256; tower
+ * t's at t * stride_wt), the operand ppo_mlp_ln_bwd_f32 reads. */
 int ppo_mlp_chain_max_layers(void);
 int ppo_mlp_ln_fwd_f32(void* stream, int towers, int L, const float* X, int64_t ldx, const int32_t* rows_idx, int M,
                        int K0, const float* const* W, int64_t ldw0, int64_t ldw, const float* const* bias,
                        const float* const* gamma, const float* const* beta, float* const* Z, float* const* Y,
                        int64_t ld, float* const* mean, float* const* rstd, float eps, int act, int64_t stride_x,
-                       int64_t stride_params, int64_t stride_rows, int64_t stride_stats);
+                       int64_t stride_params, int64_t stride_rows, int64_t stride_stats, float* const* WT,
+                       int64_t stride_wt);
 /* Backward: from dY, the cotangent of the last layer's output, each layer's
  * activation + LayerNorm backward (writes dZ and partial[blocks][2 * 256],
  * the scale | bias gradient sums of each 16-row block, blocks =
  * ppo_mlp_ln_bwd_blocks(M)) and for l > 0 the input cotangent dZ W_l^T read
- * through WT[l] = W_l transposed ([256 out][ldwt], ldwt == 256, e.g. from
- * ppo_transpose_f32_batched).  The values of ppo_layernorm_act_bwd_f32 and
+ * through WT[l] = W_l transposed ([256 out][ldwt], ldwt == 256, as
+ * ppo_mlp_ln_fwd_f32 writes it).  The values of ppo_layernorm_act_bwd_f32 and
  * ppo_gemm_f32 (dZ W^T) per layer, up to float32 summation order. */
 int ppo_mlp_ln_bwd_blocks(int rows);
 int ppo_mlp_ln_bwd_f32(void* stream, int towers, int L, const float* dY, int64_t lddy, int M, const float* const* Z,
@@ -230,10 +233,6 @@ int ppo_mlp_ln_bwd_f32(void* stream, int towers, int L, const float* dY, int64_t
                        const float* const* beta, const float* const* WT, int64_t ldwt, float* const* dZ, int64_t ld,
                        float* const* partial, int act, int64_t stride_rows, int64_t stride_stats,
                        int64_t stride_params, int64_t stride_wt, int64_t stride_part);
-/* dst[b] = src[b]^T for n <= 16 row-major [rows][cols] matrices (the
- * transposed kernel images the backward chain reads). */
-int ppo_transpose_f32_batched(void* stream, int n, const float* const* src, float* const* dst, int rows, int cols,
-                              int64_t lds, int64_t ldd);
 
 /* ------------------------------------------------------- linear scan
  * Replace boonta's linear-recurrence scan and its custom VJP

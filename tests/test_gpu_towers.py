@@ -254,8 +254,18 @@ def test_forward_chain_equals_one_fused_launch_per_layer(towers, L, M, K0, gathe
             ptrs([Y[l, 0].data_ptr() for l in range(L)]), ptrs([mean[l, 0].data_ptr() for l in range(L)]),
             ptrs([rstd[l, 0].data_ptr() for l in range(L)])]
     a = [k[1] for k in keep]
+    # the transposed kernels of layers 1.. (one pass of the threads covers a
+    # workgroup's share at 2048 and 4096 rows; the smaller grids take the loop
+    # at the end of the kernel)
+    WT = torch.full((max(L - 1, 1), towers, F, F), 3.0, device="cuda")
+    kwt = ptrs([0] + [WT[l - 1, 0].data_ptr() for l in range(1, L)])
     _lib.call("ppo_mlp_ln_fwd_f32", st(), towers, L, X.data_ptr(), K0, p(I), M, K0, a[0], F, F, a[1], a[2], a[3],
-              a[4], a[5], F, a[6], a[7], 1e-6, act, 0, block, M * F, M)
+              a[4], a[5], F, a[6], a[7], 1e-6, act, 0, block, M * F, M, kwt[1], F * F)
+    torch.cuda.synchronize()
+    for t in range(towers):
+        for l in range(1, L):
+            o = offs[l]["W"] + t * block
+            assert torch.equal(WT[l - 1, t], P.view(-1)[o:o + F * F].view(F, F).t()), (t, l)
     for t in range(towers):
         x, ldx, idx = X.data_ptr(), K0, p(I)
         for l, d in enumerate(offs):
@@ -308,14 +318,11 @@ def test_backward_chain_matches_float64_autograd(towers, L, M, act):
     lay = lambda T_: [T_[l, 0].data_ptr() for l in range(L)]
     keep = [ptrs(at(k)) for k in ("W", "b", "g", "be")] + [ptrs(lay(T_)) for T_ in (Z, Y, mean, rstd)]
     a = [k[1] for k in keep]
-    _lib.call("ppo_mlp_ln_fwd_f32", st(), towers, L, X.data_ptr(), K0, p(I), M, K0, a[0], F, F, a[1], a[2], a[3],
-              a[4], a[5], F, a[6], a[7], 1e-6, act, 0, block, M * F, M)
-    # transposed kernels of layers 1..L-1
+    # the forward also writes the transposed kernels of layers 1..L-1
     WT = torch.zeros(max(L - 1, 1), towers, F, F, device="cuda")
-    src = [base + 4 * (t * block + offs[l]["W"]) for l in range(1, L) for t in range(towers)]
-    dst = [WT[l - 1, t].data_ptr() for l in range(1, L) for t in range(towers)]
-    ks, kd = ptrs(src or [0]), ptrs(dst or [0])
-    _lib.call("ppo_transpose_f32_batched", st(), len(src), ks[1], kd[1], F, F, F, F)
+    kwt = ptrs([0] + [WT[l - 1, 0].data_ptr() for l in range(1, L)])
+    _lib.call("ppo_mlp_ln_fwd_f32", st(), towers, L, X.data_ptr(), K0, p(I), M, K0, a[0], F, F, a[1], a[2], a[3],
+              a[4], a[5], F, a[6], a[7], 1e-6, act, 0, block, M * F, M, kwt[1], F * F)
     dY = torch.from_numpy(g.standard_normal((towers, M, F)).astype(np.float32)).cuda()
     dZ = torch.full((L, towers, M, F), 5.0, device="cuda")
     blocks = lib.ppo_mlp_ln_bwd_blocks(M)
@@ -341,22 +348,6 @@ def test_backward_chain_matches_float64_autograd(towers, L, M, act):
             tot = part[l, t].double().sum(0)
             assert float((tot[:F] - gam.grad).norm() / gam.grad.norm()) < 1e-5, (t, l, "scale")
             assert float((tot[F:] - bet.grad).norm() / bet.grad.norm()) < 1e-5, (t, l, "bias")
-
-
-def test_batched_transpose_is_exact():
-    g = np.random.default_rng(3)
-    mats = [torch.from_numpy(g.standard_normal((r, c)).astype(np.float32)).cuda() for r, c in ((256, 256),) * 3]
-    outs = [torch.zeros(256, 256, device="cuda") for _ in mats]
-    ks, kd = ptrs([m.data_ptr() for m in mats]), ptrs([o.data_ptr() for o in outs])
-    _lib.call("ppo_transpose_f32_batched", st(), 3, ks[1], kd[1], 256, 256, 256, 256)
-    A = torch.from_numpy(g.standard_normal((70, 45)).astype(np.float32)).cuda()
-    B = torch.zeros(45, 72, device="cuda")
-    ka, kb = ptrs([A.data_ptr()]), ptrs([B.data_ptr()])
-    _lib.call("ppo_transpose_f32_batched", st(), 1, ka[1], kb[1], 70, 45, 45, 72)
-    torch.cuda.synchronize()
-    for m, o in zip(mats, outs):
-        assert torch.equal(o, m.t())
-    assert torch.equal(B[:, :70], A.t())
 
 
 @pytest.mark.parametrize("use_graph", [False, True])

@@ -179,12 +179,11 @@ def test_gaussian_update_runs_each_torso_chain_in_one_launch():
     assert ex.chain_ln
     names = [n for n, _ in ex.record()]
     steps = r.cfg.update_epochs * r.cfg.num_minibatches
-    # per minibatch step: the transposed kernel images, the forward chain of
-    # both towers, the fused heads + loss, the backward chain and the dW
+    # per minibatch step: the forward chain of both towers (which also writes
+    # the kernels' transposed images), the fused heads + loss, the backward chain and the dW
     # contractions (layer 0 of both towers, then layers 1-3 of both towers in
     # one launch); the critic's bootstrap chain once
     calls = ex.record(max_steps=1)
-    assert names.count("ppo_transpose_f32_batched") == steps
     assert names.count("ppo_mlp_ln_fwd_f32") == steps + 1
     assert names.count("ppo_mlp_ln_bwd_f32") == steps
     assert names.count("ppo_gemm_f32_towers") == 2 * steps
@@ -225,14 +224,12 @@ def test_gaussian_update_runs_each_torso_chain_in_one_launch():
             assert T[key][l] == getattr(a, attr).data_ptr(), key
             assert T[key][l] + 4 * stride == getattr(c, attr).data_ptr(), key
         assert a.lnpart.shape[0] == _lib.load().ppo_mlp_ln_bwd_blocks(ex.mb)
-    # the transposes read each tower's kernel of layers 1.. into WT[layer - 1, tower]
-    assert T["nT"] == 2 * (len(ex.actor) - 1)
-    k = 0
+    # the forward writes each tower's kernel of layers 1.. transposed into WT[layer - 1, tower]
     for l in range(1, len(ex.actor)):
-        for t, lb in enumerate((ex.actor[l], ex.critic[l])):
-            assert T["tsrc"][k] == flat.view(lb.spec.dense.w) and T["tdst"][k] == ex.WT[l - 1, t].data_ptr()
-            k += 1
         assert T["WT"][l] == ex.WT[l - 1, 0].data_ptr()
+    fwd = [a for n_, a in calls if n_ == "ppo_mlp_ln_fwd_f32"]
+    assert [a[-2] for a in fwd] == [None, ex._chain["WT"]]   # the bootstrap chain writes none
+    assert fwd[1][-1] == ex.WT[0, 1].data_ptr() - ex.WT[0, 0].data_ptr() >> 2
     # the bootstrap chain runs the critic's own layers
     for l, lb in enumerate(ex.boot_layers):
         assert T["bW"][l] == flat.view(ex.critic[l].spec.dense.w) and T["bY"][l] == lb.Y.data_ptr()
