@@ -295,7 +295,16 @@ __device__ __forceinline__ floatx4 mfma4(floatx4 a, const float (&b)[4], floatx4
   return acc;
 }
 
-template <bool SEP>
+// The torso activation's derivative with the activation a compile-time
+// constant where the launch knows it (ACT >= 0: both towers' activation), so
+// the per-element loops of phase C hold only its code; ACT < 0 switches on
+// the run-time value.
+template <int ACT>
+__device__ __forceinline__ bool has_act(int act) { return (ACT >= 0 ? ACT : act) != ACT_NONE; }
+template <int ACT>
+__device__ __forceinline__ float dact(int act, float x) { return ppo::act_grad(ACT >= 0 ? ACT : act, x); }
+
+template <bool SEP, int ACT>
 __global__ void __launch_bounds__(HL_THREADS) head_loss_kernel(HeadLossParams p) {
   __shared__ __attribute__((aligned(16))) float s_out[1][TR][LDO];
   __shared__ __attribute__((aligned(16))) float s_dout[TR][LDO];
@@ -409,13 +418,13 @@ __global__ void __launch_bounds__(HL_THREADS) head_loss_kernel(HeadLossParams p)
           const int row = r0 + rr;
           if (row >= p.rows) continue;
           float d = g[v];
-          if (p.act_a != ACT_NONE)
-            d *= ppo::act_grad(p.act_a, a_is_h ? av[cc][v] : p.aux_a[(int64_t)row * p.ldaux_a + f]);
+          if (has_act<ACT>(p.act_a))
+            d *= dact<ACT>(p.act_a, a_is_h ? av[cc][v] : p.aux_a[(int64_t)row * p.ldaux_a + f]);
           p.dha[(int64_t)row * p.lddha + f] = d;
           if (SEP) {
             float dc = s_dout[rr][16] * wcf;
-            if (p.act_c != ACT_NONE)
-              dc *= ppo::act_grad(p.act_c, c_is_h ? cv[cc][v] : p.aux_c[(int64_t)row * p.ldaux_c + f]);
+            if (has_act<ACT>(p.act_c))
+              dc *= dact<ACT>(p.act_c, c_is_h ? cv[cc][v] : p.aux_c[(int64_t)row * p.ldaux_c + f]);
             p.dhc[(int64_t)row * p.lddhc + f] = dc;
           }
         }
@@ -439,7 +448,7 @@ __global__ void __launch_bounds__(HL_THREADS) head_loss_kernel(HeadLossParams p)
 // Phase A's four per-wave partial head outputs are summed in wave order.
 constexpr int TS = 16;
 
-template <bool SEP, int NB>
+template <bool SEP, int NB, int ACT>
 __global__ void __launch_bounds__(HL_THREADS) head_loss_fs_kernel(HeadLossParams p) {
   __shared__ __attribute__((aligned(16))) float s_part[4][TS][LDO];
   __shared__ __attribute__((aligned(16))) float s_dout[TS][LDO];
@@ -547,11 +556,11 @@ __global__ void __launch_bounds__(HL_THREADS) head_loss_fs_kernel(HeadLossParams
       if (!liveq[v]) continue;
       const int64_t row = rowq[v];
       float d = g[v];
-      if (p.act_a != ACT_NONE) d *= ppo::act_grad(p.act_a, xa[i][v]);
+      if (has_act<ACT>(p.act_a)) d *= dact<ACT>(p.act_a, xa[i][v]);
       p.dha[row * p.lddha + f] = d;
       if (SEP) {
         float dc = dvq[v] * wcf[i];
-        if (p.act_c != ACT_NONE) dc *= ppo::act_grad(p.act_c, xc[i][v]);
+        if (has_act<ACT>(p.act_c)) dc *= dact<ACT>(p.act_c, xc[i][v]);
         p.dhc[row * p.lddhc + f] = dc;
       }
     }
@@ -629,22 +638,33 @@ static int head_loss_impl(
   p.ratio_out = ratio_out; p.ratio_envs = ratio_envs; p.ratio_steps = ratio_steps;
   const int blocks = ppo_head_loss_blocks(rows);
   hipStream_t st = ppo::as_stream(stream);
-  if (rows <= PPO_HL_SMALL_ROWS) {
-    const int nb = ppo::ceil_div(F, 64);  // 16-feature blocks per wave
-    auto fs = [&](auto sep_c) {
-      constexpr bool S = decltype(sep_c)::value;
-      if (nb <= 1) hipLaunchKernelGGL((head_loss_fs_kernel<S, 1>), dim3(blocks), dim3(HL_THREADS), 0, st, p);
-      else if (nb <= 2) hipLaunchKernelGGL((head_loss_fs_kernel<S, 2>), dim3(blocks), dim3(HL_THREADS), 0, st, p);
-      else if (nb <= 4) hipLaunchKernelGGL((head_loss_fs_kernel<S, 4>), dim3(blocks), dim3(HL_THREADS), 0, st, p);
-      else hipLaunchKernelGGL((head_loss_fs_kernel<S, 8>), dim3(blocks), dim3(HL_THREADS), 0, st, p);
-    };
-    if (sep) fs(std::true_type{});
-    else fs(std::false_type{});
-  } else if (sep) {
-    hipLaunchKernelGGL(head_loss_kernel<true>, dim3(blocks), dim3(HL_THREADS), 0, st, p);
-  } else {
-    hipLaunchKernelGGL(head_loss_kernel<false>, dim3(blocks), dim3(HL_THREADS), 0, st, p);
-  }
+  // the activation as a template constant when both towers use one of
+  // none / relu / silu (else the run-time switch, -1)
+  const int actc = (!sep || act_a == act_c) && (act_a == ACT_NONE || act_a == ACT_RELU || act_a == ACT_SILU) ? act_a
+                                                                                                              : -1;
+  auto launch = [&](auto sep_c, auto act_c_) {
+    constexpr bool S = decltype(sep_c)::value;
+    constexpr int AC = decltype(act_c_)::value;
+    if (rows <= PPO_HL_SMALL_ROWS) {
+      const int nb = ppo::ceil_div(F, 64);  // 16-feature blocks per wave
+      if (nb <= 1) hipLaunchKernelGGL((head_loss_fs_kernel<S, 1, AC>), dim3(blocks), dim3(HL_THREADS), 0, st, p);
+      else if (nb <= 2) hipLaunchKernelGGL((head_loss_fs_kernel<S, 2, AC>), dim3(blocks), dim3(HL_THREADS), 0, st, p);
+      else if (nb <= 4) hipLaunchKernelGGL((head_loss_fs_kernel<S, 4, AC>), dim3(blocks), dim3(HL_THREADS), 0, st, p);
+      else hipLaunchKernelGGL((head_loss_fs_kernel<S, 8, AC>), dim3(blocks), dim3(HL_THREADS), 0, st, p);
+    } else {
+      hipLaunchKernelGGL((head_loss_kernel<S, AC>), dim3(blocks), dim3(HL_THREADS), 0, st, p);
+    }
+  };
+  auto by_act = [&](auto sep_c) {
+    switch (actc) {
+      case ACT_NONE: launch(sep_c, std::integral_constant<int, ACT_NONE>{}); break;
+      case ACT_RELU: launch(sep_c, std::integral_constant<int, ACT_RELU>{}); break;
+      case ACT_SILU: launch(sep_c, std::integral_constant<int, ACT_SILU>{}); break;
+      default: launch(sep_c, std::integral_constant<int, -1>{}); break;
+    }
+  };
+  if (sep) by_act(std::true_type{});
+  else by_act(std::false_type{});
   return ppo::check_launch("ppo_head_loss_f32");
 }
 
