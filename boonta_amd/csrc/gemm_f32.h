@@ -50,10 +50,12 @@ __device__ __forceinline__ GemmParams tower_params(const GemmParams& p, int t) {
 
 // Stores a wave's MB x NB blocks of 32 x 32 (v_mfma_f32_32x32x*: lane l holds
 // rows 8 (r / 4) + 4 (l / 32) + r % 4 of column l % 32) from row wm0 and column
-// wn0 through the epilogue, and the bias-gradient column sums of B.
-template <int MB, int NB>
-__device__ __forceinline__ void epilogue_f32(const GemmParams& p, floatx16 (&acc)[MB][NB], const float (&bsum)[NB],
-                                             bool do_bsum, int wm0, int wn0, int split, int lane) {
+// wn0 through the epilogue EPI with activation ACT (compile-time, so the
+// unrolled element loop holds only their code), and the bias-gradient column
+// sums of B.
+template <int MB, int NB, int EPI, int ACT>
+__device__ __forceinline__ void epilogue_f32_t(const GemmParams& p, floatx16 (&acc)[MB][NB], const float (&bsum)[NB],
+                                               bool do_bsum, int wm0, int wn0, int split, int lane) {
   const int h = lane >> 5;
   const int l32 = lane & 31;
   float* C = p.C + (int64_t)split * p.c_split_stride;
@@ -64,19 +66,19 @@ __device__ __forceinline__ void epilogue_f32(const GemmParams& p, floatx16 (&acc
       const int gn = wn0 + bj * 32 + l32;
       const bool n_ok = gn < p.N;
       float bias = 0.f;
-      if (p.epi == EPI_BIAS_ACT && p.bias && n_ok) bias = p.bias[gn];
+      if (EPI == EPI_BIAS_ACT && p.bias && n_ok) bias = p.bias[gn];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int gm = wm0 + bi * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
         if (!n_ok || gm >= p.M) continue;
         float v = acc[bi][bj][r];
         const int64_t o = (int64_t)gm * p.ldc + gn;
-        if (p.epi == EPI_BIAS_ACT) {
+        if (EPI == EPI_BIAS_ACT) {
           v += bias;
           if (p.pre) p.pre[o] = v;
-          v = ppo::act_fwd(p.act, v);
-        } else if (p.epi == EPI_DACT) {
-          v *= ppo::act_grad(p.act, p.aux[(int64_t)gm * p.ldaux + gn]);
+          v = ppo::act_fwd(ACT, v);
+        } else if (EPI == EPI_DACT) {
+          v *= ppo::act_grad(ACT, p.aux[(int64_t)gm * p.ldaux + gn]);
         }
         C[o] = v;
       }
@@ -90,6 +92,27 @@ __device__ __forceinline__ void epilogue_f32(const GemmParams& p, floatx16 (&acc
       if (h == 0 && gn < p.N) p.bias_grad[(int64_t)split * p.N + gn] = t;
     }
   }
+}
+
+// The epilogue of the launch's kind and activation, chosen once.
+template <int MB, int NB>
+__device__ __forceinline__ void epilogue_f32(const GemmParams& p, floatx16 (&acc)[MB][NB], const float (&bsum)[NB],
+                                             bool do_bsum, int wm0, int wn0, int split, int lane) {
+#define PPO_EPI_ACTS(E)                                                                       \
+  switch (p.act) {                                                                            \
+    case ACT_RELU: epilogue_f32_t<MB, NB, E, ACT_RELU>(p, acc, bsum, do_bsum, wm0, wn0, split, lane); break; \
+    case ACT_TANH: epilogue_f32_t<MB, NB, E, ACT_TANH>(p, acc, bsum, do_bsum, wm0, wn0, split, lane); break; \
+    case ACT_SILU: epilogue_f32_t<MB, NB, E, ACT_SILU>(p, acc, bsum, do_bsum, wm0, wn0, split, lane); break; \
+    default: epilogue_f32_t<MB, NB, E, ACT_NONE>(p, acc, bsum, do_bsum, wm0, wn0, split, lane); break;       \
+  }
+  if (p.epi == EPI_BIAS_ACT) {
+    PPO_EPI_ACTS(EPI_BIAS_ACT)
+  } else if (p.epi == EPI_DACT) {
+    PPO_EPI_ACTS(EPI_DACT)
+  } else {
+    epilogue_f32_t<MB, NB, EPI_STORE, ACT_NONE>(p, acc, bsum, do_bsum, wm0, wn0, split, lane);
+  }
+#undef PPO_EPI_ACTS
 }
 
 // The copy-fed pipeline (gemm_f32d.hip): 16-byte rows along every operand's
