@@ -230,42 +230,48 @@ __device__ __forceinline__ bf16x8 operand(const uint16_t* lds, int r0, int kk, i
   }
 }
 
-// One 32 x 32 block (rows wm0b.., columns wn0b..) of the epilogue.
+// One 32 x 32 block (rows wm0b.., columns wn0b..) of the epilogue.  EPI_ /
+// ACT_: the epilogue kind and activation when the launch fixes them at
+// compile time (the unrolled element loop then holds only their code), -1
+// for the run-time values.
+template <int EPI_, int ACT_>
 __device__ __forceinline__ void epilogue_block(const Params& p, float* C, const floatx16& a, int wm0b, int wn0b,
                                                int h, int l32) {
+  const int epi = EPI_ >= 0 ? EPI_ : p.epi;
+  const int act = ACT_ >= 0 ? ACT_ : p.act;
   const bool rnd = p.round_out != 0;
   const int gn = wn0b + l32;
   const bool n_ok = gn < p.N;
   float bias = 0.f;
-  if (p.epi == EPI_BIAS_ACT && p.bias && n_ok) bias = rnd ? bf16_round(p.bias[gn]) : p.bias[gn];
+  if (epi == EPI_BIAS_ACT && p.bias && n_ok) bias = rnd ? bf16_round(p.bias[gn]) : p.bias[gn];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int gm = wm0b + 8 * (r >> 2) + 4 * h + (r & 3);
     if (!n_ok || gm >= p.M) continue;
     float v = a[r];
     if (rnd) v = bf16_round(v);
-    if (p.epi == EPI_BIAS_ACT) {
+    if (epi == EPI_BIAS_ACT) {
       if (p.bias) {
         v += bias;
         if (rnd) v = bf16_round(v);
       }
-      if (p.act != ACT_NONE) {
-        v = ppo::act_fwd(p.act, v);
+      if (act != ACT_NONE) {
+        v = ppo::act_fwd(act, v);
         if (rnd) v = bf16_round(v);
       }
-    } else if (p.epi == EPI_DACT) {
-      v *= ppo::act_grad(p.act, p.aux[(int64_t)gm * p.ldaux + gn]);
+    } else if (epi == EPI_DACT) {
+      v *= ppo::act_grad(act, p.aux[(int64_t)gm * p.ldaux + gn]);
       if (rnd) v = bf16_round(v);
     }
     C[(int64_t)gm * p.ldc + gn] = v;
   }
 }
 
-template <int BI, int BJ, int... I>
+template <int EPI_, int ACT_, int BI, int BJ, int... I>
 __device__ __forceinline__ void epilogue_blocks(const Params& p, float* C, floatx16 (&acc)[BI][BJ], int wm0, int wn0,
                                                 int h, int l32, std::integer_sequence<int, I...>) {
   // compile-time block indices: the accumulators stay in registers
-  (epilogue_block(p, C, acc[I / BJ][I % BJ], wm0 + (I / BJ) * 32, wn0 + (I % BJ) * 32, h, l32), ...);
+  (epilogue_block<EPI_, ACT_>(p, C, acc[I / BJ][I % BJ], wm0 + (I / BJ) * 32, wn0 + (I % BJ) * 32, h, l32), ...);
 }
 
 // The wave's BI x BJ accumulator blocks (rows from wm0, columns from wn0)
@@ -276,7 +282,16 @@ __device__ __forceinline__ void epilogue(const Params& p, floatx16 (&acc)[BI][BJ
   const int h = lane >> 5;
   const int l32 = lane & 31;
   float* C = p.C + (int64_t)split * p.c_split_stride;
-  epilogue_blocks<BI, BJ>(p, C, acc, wm0, wn0, h, l32, std::make_integer_sequence<int, BI * BJ>{});
+  // the workloads' epilogues as compile-time constants; others at run time
+  const auto seq = std::make_integer_sequence<int, BI * BJ>{};
+  if (p.epi == EPI_STORE)
+    epilogue_blocks<EPI_STORE, ACT_NONE, BI, BJ>(p, C, acc, wm0, wn0, h, l32, seq);
+  else if (p.epi == EPI_BIAS_ACT && p.act == ACT_RELU)
+    epilogue_blocks<EPI_BIAS_ACT, ACT_RELU, BI, BJ>(p, C, acc, wm0, wn0, h, l32, seq);
+  else if (p.epi == EPI_DACT && p.act == ACT_RELU)
+    epilogue_blocks<EPI_DACT, ACT_RELU, BI, BJ>(p, C, acc, wm0, wn0, h, l32, seq);
+  else
+    epilogue_blocks<-1, -1, BI, BJ>(p, C, acc, wm0, wn0, h, l32, seq);
   if (do_bsum) {
 #pragma unroll
     for (int bj = 0; bj < BJ; ++bj) {

@@ -22,7 +22,9 @@ constexpr int MAX_VPL = 16;  // features per lane: F <= 1024
 
 // ------------------------------------------------------------ LayerNorm fwd
 // z [rows, F] (ld ldz) -> y = act(LN(z)) [rows, F] (ld ldy); mean/rstd [rows].
-template <int VPL>
+// ACT: the activation (a compile-time constant: the element loops then hold
+// only its code; the act argument is the same value).
+template <int VPL, int ACT>
 __global__ void __launch_bounds__(ROW_THREADS)
 ln_act_fwd_kernel(const float* __restrict__ z, int64_t ldz, const float* __restrict__ gamma,
                   const float* __restrict__ beta, float* __restrict__ y, int64_t ldy, float* __restrict__ mean_out,
@@ -59,10 +61,10 @@ ln_act_fwd_kernel(const float* __restrict__ z, int64_t ldz, const float* __restr
         if (round) {
           // flax casts the fp32 LayerNorm result back to the bf16 compute dtype
           o = ppo::bf16_round(o);
-          o = ppo::act_fwd(act, o);
-          if (act != ACT_RELU && act != ACT_NONE) o = ppo::bf16_round(o);
+          o = ppo::act_fwd(ACT, o);
+          if (ACT != ACT_RELU && ACT != ACT_NONE) o = ppo::bf16_round(o);
         } else {
-          o = ppo::act_fwd(act, o);
+          o = ppo::act_fwd(ACT, o);
         }
         if (yr) yr[f] = o;
         if (y16) y16[r * ldy16 + f] = (uint16_t)ppo::bf16_bits(o);
@@ -81,7 +83,7 @@ struct LnTowers {
 // dy = dL/d(act output) [rows, F]; recomputes the LN output from z, mean,
 // rstd; writes dz [rows, F] and per-block partials [gridDim.x][2F] holding
 // (sum over the block's rows of dyl * xhat | sum of dyl) for scale and bias.
-template <int VPL>
+template <int VPL, int ACT>
 __global__ void __launch_bounds__(ROW_THREADS)
 ln_act_bwd_kernel(const float* __restrict__ dy, int64_t lddy, const float* __restrict__ z, int64_t ldz,
                   const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
@@ -146,8 +148,8 @@ ln_act_bwd_kernel(const float* __restrict__ dy, int64_t lddy, const float* __res
           xh[e] = (zv[j][e] - mean) * rstd;
           float yl = xh[e] * gam[e] + bet[e];
           if (round) yl = ppo::bf16_round(yl);
-          const float a = (act == ACT_RELU || act == ACT_TANH) ? ppo::act_fwd(act, yl) : yl;
-          const float dyl = dv[j][e] * ppo::act_grad(act, a);
+          const float a = (ACT == ACT_RELU || ACT == ACT_TANH) ? ppo::act_fwd(ACT, yl) : yl;
+          const float dyl = dv[j][e] * ppo::act_grad(ACT, a);
           acc_g[e] += dyl * xh[e];
           acc_b[e] += dyl;
           g[e] = dyl * gam[e];
@@ -523,8 +525,16 @@ template <int VPL>
 int launch_ln_fwd(hipStream_t st, int blocks, const float* z, int64_t ldz, const float* gamma, const float* beta,
                   float* y, int64_t ldy, float* mean, float* rstd, int rows, int F, float eps, int act, int round,
                   uint16_t* y16, int64_t ldy16) {
-  hipLaunchKernelGGL((ln_act_fwd_kernel<VPL>), dim3(blocks), dim3(ROW_THREADS), 0, st, z, ldz, gamma, beta, y, ldy,
-                     mean, rstd, rows, F, eps, act, round, y16, ldy16);
+#define PPO_LN_FWD(A)                                                                                   \
+  hipLaunchKernelGGL((ln_act_fwd_kernel<VPL, A>), dim3(blocks), dim3(ROW_THREADS), 0, st, z, ldz, gamma, beta, y, ldy, \
+                     mean, rstd, rows, F, eps, act, round, y16, ldy16)
+  switch (act) {
+    case ACT_RELU: PPO_LN_FWD(ACT_RELU); break;
+    case ACT_TANH: PPO_LN_FWD(ACT_TANH); break;
+    case ACT_SILU: PPO_LN_FWD(ACT_SILU); break;
+    default: PPO_LN_FWD(ACT_NONE); break;
+  }
+#undef PPO_LN_FWD
   return ppo::check_launch("ppo_layernorm_act_fwd_f32");
 }
 
@@ -533,8 +543,16 @@ int launch_ln_bwd(hipStream_t st, int blocks, const float* dy, int64_t lddy, con
                   const float* mean, const float* rstd, const float* gamma, const float* beta, void* dz,
                   int64_t lddz, float* partial, int rows, int F, int act, int round, int out16, int towers,
                   LnTowers tw) {
-  hipLaunchKernelGGL((ln_act_bwd_kernel<VPL>), dim3(blocks, towers), dim3(ROW_THREADS), 0, st, dy, lddy, z, ldz, mean,
-                     rstd, gamma, beta, dz, lddz, partial, rows, F, act, round, out16, tw);
+#define PPO_LN_BWD(A)                                                                                       \
+  hipLaunchKernelGGL((ln_act_bwd_kernel<VPL, A>), dim3(blocks, towers), dim3(ROW_THREADS), 0, st, dy, lddy, z, ldz, \
+                     mean, rstd, gamma, beta, dz, lddz, partial, rows, F, act, round, out16, tw)
+  switch (act) {
+    case ACT_RELU: PPO_LN_BWD(ACT_RELU); break;
+    case ACT_TANH: PPO_LN_BWD(ACT_TANH); break;
+    case ACT_SILU: PPO_LN_BWD(ACT_SILU); break;
+    default: PPO_LN_BWD(ACT_NONE); break;
+  }
+#undef PPO_LN_BWD
   return ppo::check_launch("ppo_layernorm_act_bwd_f32");
 }
 
