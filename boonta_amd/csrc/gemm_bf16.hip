@@ -175,6 +175,47 @@ __device__ __forceinline__ float act_apply(int act, float v, bool round) {
   return round ? bf16_round(y) : y;
 }
 
+// The wave's MB x NB blocks of 32 x 32 from row wm0, column wn0 through the
+// epilogue; EPI_ / ACT_: the epilogue kind and activation as compile-time
+// constants (the unrolled element loop then holds only their code), -1 for
+// the run-time values.
+template <int EPI_, int ACT_, int MB, int NB>
+__device__ __forceinline__ void epilogue_bf16(const GemmParams& p, float* C, floatx16 (&acc)[MB][NB], int wm0, int wn0,
+                                              int h, int l32) {
+  const int epi = EPI_ >= 0 ? EPI_ : p.epi;
+  const int act = ACT_ >= 0 ? ACT_ : p.act;
+  const bool rnd = p.round_out != 0;
+#pragma unroll
+  for (int bi = 0; bi < MB; ++bi) {
+#pragma unroll
+    for (int bj = 0; bj < NB; ++bj) {
+      const int gn = wn0 + bj * 32 + l32;
+      const bool n_ok = gn < p.N;
+      float bias = 0.f;
+      if (epi == EPI_BIAS_ACT && p.bias && n_ok) bias = rnd ? bf16_round(p.bias[gn]) : p.bias[gn];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int gm = wm0 + bi * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (!n_ok || gm >= p.M) continue;
+        float v = acc[bi][bj][r];
+        if (rnd) v = bf16_round(v);
+        const int64_t o = (int64_t)gm * p.ldc + gn;
+        if (epi == EPI_BIAS_ACT) {
+          if (p.bias) {
+            v += bias;
+            if (rnd) v = bf16_round(v);
+          }
+          v = act_apply(act, v, rnd);
+        } else if (epi == EPI_DACT) {
+          v *= ppo::act_grad(act, p.aux[(int64_t)gm * p.ldaux + gn]);
+          if (rnd) v = bf16_round(v);
+        }
+        C[o] = v;
+      }
+    }
+  }
+}
+
 template <int BM, int BN, bool A_K, bool B_K, bool VA, bool VB>
 __global__ void __launch_bounds__(256, 2) gemm_bf16_kernel(GemmParams p) {
   constexpr int MB = BM / 64;
@@ -261,37 +302,17 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_kernel(GemmParams p) {
   }
 
   // ---------------------------------------------------------------- epilogue
-  const bool rnd = p.round_out != 0;
+  // (the workloads' forms as compile-time constants; others at run time)
   float* C = p.C + (int64_t)split * p.c_split_stride;
-#pragma unroll
-  for (int bi = 0; bi < MB; ++bi) {
-#pragma unroll
-    for (int bj = 0; bj < NB; ++bj) {
-      const int gn = n0 + wn * (BN / 2) + bj * 32 + l32;
-      const bool n_ok = gn < p.N;
-      float bias = 0.f;
-      if (p.epi == EPI_BIAS_ACT && p.bias && n_ok) bias = rnd ? bf16_round(p.bias[gn]) : p.bias[gn];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int gm = m0 + wm * (BM / 2) + bi * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (!n_ok || gm >= p.M) continue;
-        float v = acc[bi][bj][r];
-        if (rnd) v = bf16_round(v);
-        const int64_t o = (int64_t)gm * p.ldc + gn;
-        if (p.epi == EPI_BIAS_ACT) {
-          if (p.bias) {
-            v += bias;
-            if (rnd) v = bf16_round(v);
-          }
-          v = act_apply(p.act, v, rnd);
-        } else if (p.epi == EPI_DACT) {
-          v *= ppo::act_grad(p.act, p.aux[(int64_t)gm * p.ldaux + gn]);
-          if (rnd) v = bf16_round(v);
-        }
-        C[o] = v;
-      }
-    }
-  }
+  const int wm0 = m0 + wm * (BM / 2), wn0 = n0 + wn * (BN / 2);
+  if (p.epi == EPI_STORE)
+    epilogue_bf16<EPI_STORE, ACT_NONE, MB, NB>(p, C, acc, wm0, wn0, h, l32);
+  else if (p.epi == EPI_BIAS_ACT && p.act == ACT_NONE)
+    epilogue_bf16<EPI_BIAS_ACT, ACT_NONE, MB, NB>(p, C, acc, wm0, wn0, h, l32);
+  else if (p.epi == EPI_DACT && p.act == ACT_RELU)
+    epilogue_bf16<EPI_DACT, ACT_RELU, MB, NB>(p, C, acc, wm0, wn0, h, l32);
+  else
+    epilogue_bf16<-1, -1, MB, NB>(p, C, acc, wm0, wn0, h, l32);
   if (do_bsum) {
 #pragma unroll
     for (int bj = 0; bj < NB; ++bj) {
