@@ -378,6 +378,21 @@ class ForwardChain:
         self.mb = -1
         self.inp: dict = {}
 
+    @staticmethod
+    def _f32_tile(a_layout: int, b_layout: int, M: int, K: int) -> int:
+        """fp32 tile for a whole-minibatch contraction, measured per update:
+        over 32768 rows or more (the Anakin minibatch) the 8-wave 256 x 128
+        tile for forwards and 128 x 128 for the weight gradient of a 256-row
+        kernel (11.43 -> 11.31 ms per update); at 16384 rows (the GRU
+        workload) both were slower (17.8 -> 28.2 us on 16384 x 256 x 128,
+        76 -> 90 us on its 256 x 768 dW), so below that the library's default
+        (64 x 64)."""
+        if a_layout == A_ROW and b_layout == B_KN and M >= 32768:
+            return 9
+        if a_layout == A_COL and M == 256 and K >= 32768:
+            return 0
+        return -1
+
     def _gemm(self, st, a_layout, b_layout, A, lda, rows, B, ldb, C, ldc, M, N, K, splits, stride, epi, bias, act,
               pre, aux, ldaux, bias_grad, tile):
         """One Dense contraction: fp32 MFMA, or for a bf16-compute network the
@@ -385,6 +400,8 @@ class ForwardChain:
         forward and input-cotangent results rounded to bf16; dW partials kept
         fp32 and rounded after their sum)."""
         if not self.bf16:
+            if tile == -1:
+                tile = self._f32_tile(a_layout, b_layout, M, K)
             self._call("ppo_gemm_f32", st, a_layout, b_layout, A, lda, rows, B, ldb, C, ldc, M, N, K, splits, stride,
                        epi, bias, act, pre, aux, ldaux, bias_grad, tile)
             return
