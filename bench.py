@@ -153,6 +153,14 @@ def _single_launch_work(name, args):
         towers, L, M = args[1], args[2], args[5]
         weights = 256 * 256 * (L - 1) + 2 * 256 * L
         return towers * 2.0 * M * 256 * 256 * (L - 1), towers * 4.0 * (M * 256 + weights + M * L * (2 * 256 + 2))
+    if name == "ppo_mlp16_ln_fwd":
+        # split partials in; per layer Z (fp32), Y16, mean, rstd out, the top layer's Y; bf16 kernels
+        L, nsplit, M = args[1], args[5], args[6]
+        return (2.0 * M * 512 * 512 * (L - 1),
+                4.0 * M * 512 * nsplit + 2.0 * 512 * 512 * (L - 1) + M * L * (6.0 * 512 + 8) + 4.0 * M * 512)
+    if name == "ppo_pack_bf16_operands":
+        L, K, N = args[1], args[4], args[5]
+        return 0.0, 4.0 * L * K * N
     if name == "ppo_gru_fwd_seq_f32":
         Bm, H, T = args[-6], args[-5], args[-4]
         return 2.0 * Bm * H * 3 * H * T, 4.0 * T * Bm * (3 * H + H + H + 4 * H) + 4.0 * H * 3 * H
@@ -204,6 +212,8 @@ def _single_launch_shape(name, args):
         return [args[5], 256, 256, args[2], args[1]]
     if name in ("ppo_gru_fwd_seq_f32", "ppo_gru_bwd_seq_f32"):
         return [args[-6], args[-5], args[-4]]
+    if name == "ppo_mlp16_ln_fwd":
+        return [args[6], 512, 512, args[1]]
     if name.startswith("ppo_gru"):
         return [args[-2], args[-1]]
     return None
@@ -229,6 +239,8 @@ def launch_key(name, args):
         return (name, args[-2], args[-1], bool(args[1]))
     if name in ("ppo_gru_fwd_seq_f32", "ppo_gru_bwd_seq_f32"):
         return (name, args[-6], args[-5], args[-4])
+    if name == "ppo_mlp16_ln_fwd":
+        return (name, args[1], args[5], args[6])
     return (name, id(args))
 
 

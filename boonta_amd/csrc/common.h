@@ -79,11 +79,14 @@ __device__ __forceinline__ float load_or_zero(const float* p, int64_t i, bool ok
 
 // Round to nearest even bf16 (NaN stays NaN), returned as the fp32 value
 // of that bf16 (bits() gives the 16-bit pattern).
+// Both results are computed and one is selected: as an if / else the compiler
+// makes a divergent branch (exec-mask save / restore) of every rounding in an
+// unrolled element loop.
 __device__ __forceinline__ uint32_t bf16_bits(float x) {
-  uint32_t u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t qnan = (u >> 16) | 0x40u;
+  return (u & 0x7fffffffu) > 0x7f800000u ? qnan : rne;
 }
 
 __device__ __forceinline__ float bf16_round(float x) { return __uint_as_float(bf16_bits(x) << 16); }
@@ -166,6 +169,81 @@ __device__ __forceinline__ float ln_apply(float z, float mean, float rstd, float
   return __fmaf_rn(z - mean, rstd * gamma, beta);
 }
 
+// LayerNorm of one row held by a wavefront, VPL features per lane (feature
+// lane + 64 e in v[e], zeros past the row's F features), with every rounding
+// step explicit so that the per-layer LayerNorm kernel and the bf16 chains
+// produce the same bits: per-lane sums in e order (z, then z * z by one fma),
+// wave sums, mean = s / F, variance max(E[z^2] - mean^2, 0) (flax's fast
+// variance), and the normalised, scaled value.
+template <int VPL>
+__device__ __forceinline__ void ln_row_stats(const float (&v)[VPL], float F, float eps, float& mean, float& rstd) {
+  float s = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int e = 0; e < VPL; ++e) {
+    s += v[e];
+    s2 = __fmaf_rn(v[e], v[e], s2);
+  }
+  s = wave_sum(s);
+  s2 = wave_sum(s2);
+  mean = s / F;
+  const float var = fmaxf(__fmaf_rn(-mean, mean, s2 / F), 0.f);
+  rstd = rsqrtf(var + eps);
+}
+// The statistics of R rows at once: per row exactly the operations of
+// ln_row_stats (the same sums in the same order, the same butterfly), with
+// the rows' reductions interleaved so that their shuffle latencies overlap.
+template <int R, int VPL>
+__device__ __forceinline__ void ln_rows_stats(const float (&v)[R][VPL], float F, float eps, float (&mean)[R],
+                                              float (&rstd)[R]) {
+  float s[R], s2[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    s[j] = 0.f;
+    s2[j] = 0.f;
+#pragma unroll
+    for (int e = 0; e < VPL; ++e) {
+      s[j] += v[j][e];
+      s2[j] = __fmaf_rn(v[j][e], v[j][e], s2[j]);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      s[j] += __shfl_xor(s[j], o, 64);
+      s2[j] += __shfl_xor(s2[j], o, 64);
+    }
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    mean[j] = s[j] / F;
+    const float var = fmaxf(__fmaf_rn(-mean[j], mean[j], s2[j] / F), 0.f);
+    rstd[j] = rsqrtf(var + eps);
+  }
+}
+__device__ __forceinline__ float ln_row_apply(float v, float mean, float rstd, float gamma, float beta) {
+  return __fmaf_rn(v - mean, rstd * gamma, beta);
+}
+
+// LayerNorm + activation backward of one element of a row, every rounding
+// explicit (the per-layer LayerNorm backward and the bf16 chain's give the
+// same bits): xh = (z - mean) rstd; the output recomputed as fma(xh, gamma,
+// beta), rounded to bf16 when `round` (the bf16 forward rounds it before the
+// activation); returns dyl = dy act'(.), the LayerNorm output's cotangent.
+// A row's input cotangent is then ln_bwd_dz of its element's g = dyl gamma
+// with the row means of g and g xh.
+// The kernels that use them compile their LayerNorm backward with
+// floating-point contraction off (#pragma clang fp contract(off)): otherwise
+// the compiler fuses a product into a later sum (dyl gamma into the row sum
+// of g, or into g - mean_g) where it finds it worth it, differently from one
+// kernel to another.
+template <int ACT>
+__device__ __forceinline__ float ln_bwd_dyl(float z, float dy, float mean, float rstd, float gamma, float beta,
+                                            bool round, float& xh);
+__device__ __forceinline__ float ln_bwd_dz(float g, float xh, float mean_g, float mean_gxh, float rstd) {
+#pragma clang fp contract(off)
+  return rstd * __fmaf_rn(-xh, mean_gxh, g - mean_g);
+}
+
 // x / d for d >= 1 (d may be +inf): the hardware reciprocal (1 ulp) and one
 // correction of the quotient from its exact fma residual (Markstein's
 // step), instead of the IEEE division sequence, whose scale / fmas / fixup
@@ -209,6 +287,17 @@ __device__ __forceinline__ float act_grad(int act, float x_or_y) {
     }
     default: return 1.f;
   }
+}
+
+template <int ACT>
+__device__ __forceinline__ float ln_bwd_dyl(float z, float dy, float mean, float rstd, float gamma, float beta,
+                                            bool round, float& xh) {
+#pragma clang fp contract(off)
+  xh = (z - mean) * rstd;
+  float yl = __fmaf_rn(xh, gamma, beta);
+  if (round) yl = bf16_round(yl);
+  const float a = (ACT == ACT_RELU || ACT == ACT_TANH) ? act_fwd(ACT, yl) : yl;
+  return dy * act_grad(ACT, a);
 }
 
 }  // namespace ppo

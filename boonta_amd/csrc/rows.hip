@@ -35,19 +35,13 @@ ln_act_fwd_kernel(const float* __restrict__ z, int64_t ldz, const float* __restr
   for (int64_t r = (int64_t)blockIdx.x * wpb + (threadIdx.x >> 6); r < rows; r += (int64_t)gridDim.x * wpb) {
     const float* zr = z + r * ldz;
     float v[VPL];
-    float s = 0.f, s2 = 0.f;
 #pragma unroll
     for (int e = 0; e < VPL; ++e) {
       const int f = lane + 64 * e;
       v[e] = f < F ? zr[f] : 0.f;
-      s += v[e];
-      s2 += v[e] * v[e];
     }
-    s = ppo::wave_sum(s);
-    s2 = ppo::wave_sum(s2);
-    const float mean = s / (float)F;
-    const float var = fmaxf(s2 / (float)F - mean * mean, 0.f);
-    const float rstd = rsqrtf(var + eps);
+    float mean, rstd;
+    ppo::ln_row_stats<VPL>(v, (float)F, eps, mean, rstd);
     if (lane == 0) {
       if (mean_out) mean_out[r] = mean;
       if (rstd_out) rstd_out[r] = rstd;
@@ -57,7 +51,7 @@ ln_act_fwd_kernel(const float* __restrict__ z, int64_t ldz, const float* __restr
     for (int e = 0; e < VPL; ++e) {
       const int f = lane + 64 * e;
       if (f < F) {
-        float o = (v[e] - mean) * (rstd * gamma[f]) + beta[f];
+        float o = ppo::ln_row_apply(v[e], mean, rstd, gamma[f], beta[f]);
         if (round) {
           // flax casts the fp32 LayerNorm result back to the bf16 compute dtype
           o = ppo::bf16_round(o);
@@ -90,6 +84,7 @@ ln_act_bwd_kernel(const float* __restrict__ dy, int64_t lddy, const float* __res
                   const float* __restrict__ gamma, const float* __restrict__ beta, void* __restrict__ dz,
                   int64_t lddz, float* __restrict__ partial, int rows, int F, int act, int round, int out16,
                   LnTowers tw) {
+#pragma clang fp contract(off)  // the roundings of ppo::ln_bwd_dyl / ln_bwd_dz's callers stay as written
   if (blockIdx.y) {  // tower t of a tower-batched launch
     const int64_t t = blockIdx.y;
     dy += t * tw.rows;
@@ -145,12 +140,8 @@ ln_act_bwd_kernel(const float* __restrict__ dy, int64_t lddy, const float* __res
       for (int e = 0; e < VPL; ++e) {
         const int f = lane + 64 * e;
         if (f < F) {
-          xh[e] = (zv[j][e] - mean) * rstd;
-          float yl = xh[e] * gam[e] + bet[e];
-          if (round) yl = ppo::bf16_round(yl);
-          const float a = (ACT == ACT_RELU || ACT == ACT_TANH) ? ppo::act_fwd(ACT, yl) : yl;
-          const float dyl = dv[j][e] * ppo::act_grad(ACT, a);
-          acc_g[e] += dyl * xh[e];
+          const float dyl = ppo::ln_bwd_dyl<ACT>(zv[j][e], dv[j][e], mean, rstd, gam[e], bet[e], round, xh[e]);
+          acc_g[e] = __fmaf_rn(dyl, xh[e], acc_g[e]);
           acc_b[e] += dyl;
           g[e] = dyl * gam[e];
         } else {
@@ -158,7 +149,7 @@ ln_act_bwd_kernel(const float* __restrict__ dy, int64_t lddy, const float* __res
           g[e] = 0.f;
         }
         sg += g[e];
-        sgx += g[e] * xh[e];
+        sgx = __fmaf_rn(g[e], xh[e], sgx);
       }
       sg = ppo::wave_sum(sg) / (float)F;
       sgx = ppo::wave_sum(sgx) / (float)F;
@@ -166,7 +157,7 @@ ln_act_bwd_kernel(const float* __restrict__ dy, int64_t lddy, const float* __res
       for (int e = 0; e < VPL; ++e) {
         const int f = lane + 64 * e;
         if (f < F) {
-          const float d = rstd * (g[e] - sg - xh[e] * sgx);
+          const float d = ppo::ln_bwd_dz(g[e], xh[e], sg, sgx, rstd);
           if (out16)
             static_cast<uint16_t*>(dz)[r * lddz + f] = (uint16_t)ppo::bf16_bits(d);
           else

@@ -236,6 +236,7 @@ class LayerBufs:
     y32_unused: bool = False  # only the bf16 copy Y16 of this layer's output is read
     X16: torch.Tensor | None = None  # bf16 copy of a split-K first layer's input rows
     W16: torch.Tensor | None = None  # and of its kernel
+    chain16: dict | None = None  # first layer of a bf16 chain group: the chain launch's pointer tables
 
 
 class FlatState:
@@ -433,6 +434,69 @@ class ForwardChain:
             self._call(self._ln_fwd, st, _p(lb.Z) + o, s.ld, scale, bias, _p(lb.Y) + o, s.ld, _p(lb.mean) + 4 * row0,
                        _p(lb.rstd) + 4 * row0, nrows, s.fout, s.ln["eps"], _act(s.act))
 
+    # The bf16 chain (ppo_mlp16_ln_fwd) runs a LayerNorm group's layers after
+    # the first contraction in one launch, and its backward (ppo_mlp16_ln_bwd)
+    # every LayerNorm backward and input cotangent of the group in another;
+    # off, each layer has its own launches.
+    CHAIN16 = True
+    CHAIN16_BWD = True
+
+    def _plan_chain16(self, group):
+        """Pointer tables of the bf16 chain over ``group`` when it fits the
+        chain: a first layer on the observation copy, then 512-wide Dense ->
+        LayerNorm -> activation layers with biases, one activation and one
+        epsilon; the later layers' kernels get packed operand images."""
+        lib = _lib.load()
+        if not (self.CHAIN16 and group and len(group) <= lib.ppo_mlp16_max_layers()
+                and group[0].fpart is not None):
+            return
+        s0 = group[0].spec
+        for i, lb in enumerate(group):
+            s = lb.spec
+            if (s.ln is None or s.fout != 512 or s.ld != 512 or s.dense.b is None or lb.Y16 is None
+                    or _act(s.act) != _act(s0.act) or s.ln["eps"] != s0.ln["eps"]
+                    or (i > 0 and (s.dense.fin != 512 or s.dense.w.ld != 512))):
+                return
+        view = self.flat.view
+        arr = lambda xs: (ctypes.c_void_p * len(xs))(*xs)
+        L = len(group)
+        bwd = self.CHAIN16_BWD
+        pk = torch.zeros(max(L - 1, 1), 2 if bwd else 1, 512 * 512, dtype=torch.int16, device=self.P16.device)
+        if bwd:
+            # the backward's LayerNorm gradient sums come in blocks of 32 rows
+            blocks = lib.ppo_mlp16_ln_bwd_blocks(self.mb)
+            for lb in group:
+                if lb.lnpart.shape[0] < blocks:
+                    lb.lnpart = torch.zeros(blocks, 2 * lb.spec.fout, dtype=torch.float32, device=self.P16.device)
+                lb.lnblocks = blocks
+        T = {"Wp": arr([None] + [_p(pk[l - 1, 0]) for l in range(1, L)]),
+             "Wb": arr([None] + [_p(pk[l - 1, 1]) if bwd else None for l in range(1, L)]),
+             "dZ16": arr([_p(lb.dZ16) for lb in group]),
+             "part": arr([_p(lb.lnpart) for lb in group]),
+             "b": arr([view(lb.spec.dense.b) for lb in group]),
+             "g": arr([view(lb.spec.ln["scale"]) for lb in group]),
+             "be": arr([view(lb.spec.ln["bias"]) for lb in group]),
+             "Z": arr([_p(lb.Z) for lb in group]),
+             "Y": arr([None if lb.y32_unused else _p(lb.Y) for lb in group]),
+             "Y16": arr([_p(lb.Y16) for lb in group]),
+             "mean": arr([_p(lb.mean) for lb in group]),
+             "rstd": arr([_p(lb.rstd) for lb in group])}
+        addr = lambda a: ctypes.cast(a, ctypes.c_void_p).value
+        c = {k: addr(v) for k, v in T.items()}
+        c.update(keep=T, packed=pk, L=L, act=_act(s0.act), eps=float(s0.ln["eps"]), bwd=bwd)
+        group[0].chain16 = c
+        if L > 1:
+            W = arr([self._view16(lb.spec.dense.w) for lb in group[1:]])
+            F = arr([_p(pk[l, 0]) for l in range(L - 1)])
+            B = arr([_p(pk[l, 1]) for l in range(L - 1)]) if bwd else None
+            self._pack16_tables.append((L - 1, addr(W), addr(F), addr(B) if bwd else None, (W, F, B)))
+
+    def _pack16(self, st):
+        """Packed operand images of the bf16 chains' kernels from the bf16
+        parameter image (after each write of the image)."""
+        for n, W, F, B, _ in self._pack16_tables:
+            self._call("ppo_pack_bf16_operands", st, n, W, 512, 512, 512, F, B)
+
     def _view16(self, region: Region) -> int:
         """Address of a parameter region in the bf16 parameter image."""
         return _p(self.P16) + 2 * region.offset
@@ -451,6 +515,14 @@ class ForwardChain:
                 self._call("ppo_gemm_bf16s", st, A_ROW, B_KN, 1, 1, _p(self.OBS16), self.ldo16, rows_idx,
                            self._view16(d.w), d.w.ld, _p(lb.fpart), s.ld, nrows, s.ld, d.fin, self.FWD16_SPLITS,
                            nrows * s.ld, EPI_STORE, None, 0, 0, None, 0, None, self.FWD16_TILE)
+                c = lb.chain16
+                if c is not None and nrows == self.mb and row0 == 0:
+                    # the rest of the group in one launch from the split partials
+                    self._call("ppo_mlp16_ln_fwd", st, c["L"], _p(lb.fpart), s.ld, nrows * s.ld,
+                               self.FWD16_SPLITS, nrows, c["Wp"], c["b"], c["g"], c["be"], c["Z"], c["Y"],
+                               c["Y16"], s.ld, c["mean"], c["rstd"], c["eps"], c["act"])
+                    top = layers[-1]
+                    return _p(top.Y), top.spec.ld, None
                 self._call("ppo_splits_bias_act_bf16", st, _p(lb.fpart), s.ld, nrows * s.ld, self.FWD16_SPLITS, Bb,
                            _act(s.act) if s.ln is None else 0, _p(dst), s.ld, nrows, s.ld)
                 if s.ln is not None:
@@ -595,6 +667,10 @@ class MLPExecutor(ForwardChain):
                         lb.splits = self.DW16_SPLITS_INNER
                         lb.wpart = torch.zeros(lb.splits, d.fin, lb.spec.ld, **f32)
                         lb.bpart = torch.zeros(lb.splits, lb.spec.ld, **f32)
+        self._pack16_tables = []
+        if self.obs16:
+            for group in (self.trunk, self.actor, self.critic):
+                self._plan_chain16(group)
         self.boot_layers = [layer_bufs(s, self._boot_rows(), False) for s in
                             (program.trunk if program.shared_head else program.critic_layers)]
         if self.boot_layers and program.gru is None:
@@ -881,6 +957,25 @@ class MLPExecutor(ForwardChain):
 
     def _bwd_layers(self, st, layers, x0, ldx0, idx0):
         """Back-propagates through layers whose last output cotangent is in place."""
+        c = layers[0].chain16 if layers else None
+        if c is not None and c["bwd"]:
+            # every LayerNorm backward and input cotangent in one launch; then
+            # the weight gradients from the bf16 cotangents it leaves
+            top = layers[-1]
+            self._call("ppo_mlp16_ln_bwd", st, c["L"], _p(top.dY), top.spec.ld, self.mb, c["Wb"], c["Z"],
+                       c["mean"], c["rstd"], c["g"], c["be"], c["dZ16"], top.spec.ld, c["part"], c["act"])
+            for i in range(len(layers) - 1, -1, -1):
+                lb = layers[i]
+                s, d = lb.spec, lb.spec.dense
+                if i == 0:
+                    self._call("ppo_gemm_bf16s", st, A_COL, B_KN, 1, 1, _p(self.OBS16), self.ldo16, idx0,
+                               _p(lb.dZ16), s.ld, _p(lb.wpart), s.ld, d.fin, s.ld, self.mb, lb.splits, d.fin * s.ld,
+                               EPI_STORE, None, 0, 0, None, 0, _p(lb.bpart), self.DW16_TILE)
+                else:
+                    self._call("ppo_gemm_bf16s", st, A_COL, B_KN, 1, 1, _p(layers[i - 1].Y16), layers[i - 1].spec.ld,
+                               None, _p(lb.dZ16), s.ld, _p(lb.wpart), s.ld, d.fin, s.ld, self.mb, lb.splits,
+                               d.fin * s.ld, EPI_STORE, None, 0, 0, None, 0, _p(lb.bpart), -1)
+            return
         for i in range(len(layers) - 1, -1, -1):
             lb = layers[i]
             s = lb.spec
@@ -1059,6 +1154,7 @@ class MLPExecutor(ForwardChain):
             # (once per update) and the parameters (Adam refreshes the image)
             self._call("ppo_cast_bf16_2d", st, obs, ldo, _p(self.OBS16), self.ldo16, B, ldo)
             self._call("ppo_cast_bf16", st, _p(self.flat.P), _p(self.P16), self.flat.P.numel())
+            self._pack16(st)
         # 1. bootstrap value of second.obs[-1] with the current parameters
         x, ldx, _ = inp["next_obs_last"], ldo, None
         if prog.shared_head:
@@ -1120,6 +1216,8 @@ class MLPExecutor(ForwardChain):
         self._call("ppo_adam_clip_f32", st, _p(self.flat.P), _p(self.flat.G), _p(self.flat.MU), _p(self.flat.NU),
                    _p(self.P16) if self.obs16 else None, self.flat.P.numel(), norm, nnorm, float(max_norm),
                    adam.learning_rate, adam.b1, adam.b2, adam.eps, _p(self.flat.count), step)
+        if self.obs16:
+            self._pack16(st)
 
     def _stats(self, step: int) -> int:
         """Loss-statistics partials of optimizer step ``step``."""

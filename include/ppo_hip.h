@@ -234,6 +234,50 @@ int ppo_mlp_ln_bwd_f32(void* stream, int towers, int L, const float* dY, int64_t
                        float* const* partial, int act, int64_t stride_rows, int64_t stride_stats,
                        int64_t stride_params, int64_t stride_wt, int64_t stride_part);
 
+/* ------------------------------------------------ bf16 torso chain
+ * The 512-wide Dense -> LayerNorm -> activation layers of a bf16 network
+ * (flax Dense / LayerNorm with a bf16 compute dtype, fp32 parameters:
+ * boonta/networks/network.py:38-49 as the large-observation workload
+ * composes it) after the first layer's split-K contraction, in one launch:
+ * layer 0's split sum (split order) + bias, LayerNorm + activation, then for
+ * l >= 1 the 512 x 512 contraction of the previous output (bf16 MFMA), bias,
+ * LayerNorm + activation.  Writes each layer's Z (the bf16-valued
+ * pre-activations), mean, rstd and bf16 output Y16 (row pitch ld), and Y
+ * (fp32) where Y != NULL and Y[l] != NULL.  Bit-identical to
+ * ppo_splits_bias_act_bf16 + ppo_layernorm_act_fwd_bf16_out16 for layer 0
+ * and ppo_gemm_bf16s (bias epilogue, rounded) +
+ * ppo_layernorm_act_fwd_bf16_out16 per later layer.  Wp[l] (l >= 1): the
+ * layer's kernel as the packed forward operand image that
+ * ppo_pack_bf16_operands writes. */
+int ppo_mlp16_max_layers(void);
+int ppo_mlp16_ln_fwd(void* stream, int L, const float* part, int64_t ldp, int64_t part_stride, int nsplit, int M,
+                     const void* const* Wp, const float* const* bias, const float* const* gamma,
+                     const float* const* beta, float* const* Z, float* const* Y, void* const* Y16, int64_t ld,
+                     float* const* mean, float* const* rstd, float eps, int act);
+/* Backward of the same chain from dY, the cotangent of the top layer's
+ * output (fp32, row pitch lddy): per layer from the top, the LayerNorm +
+ * activation backward (dZ16[l], bf16, row pitch ld, bit-identical to
+ * ppo_layernorm_act_bwd_bf16_out16; part[l] [ppo_mlp16_ln_bwd_blocks(M)][2 *
+ * 512], the scale | bias gradient sums of each 32-row block) and below the
+ * top the input cotangent dZ16[l] W_l^T rounded to bf16 (bit-identical to
+ * ppo_gemm_bf16s), read through Wb[l], the packed backward operand image of
+ * layer l's kernel.  Replaces, per layer, jax.value_and_grad's LayerNorm,
+ * activation and Dense input-cotangent rules (boonta/algorithms/ppo.py:155-157)
+ * as the per-layer launches do. */
+int ppo_mlp16_ln_bwd_blocks(int rows);
+int ppo_mlp16_ln_bwd(void* stream, int L, const float* dY, int64_t lddy, int M, const void* const* Wb,
+                     const float* const* Z, const float* const* mean, const float* const* rstd,
+                     const float* const* gamma, const float* const* beta, void* const* dZ16, int64_t ld,
+                     float* const* part, int act);
+/* Packs L bf16 kernels W[l] ([K][N], row pitch ldw; the bf16 parameter
+ * image) into the MFMA operand images of the bf16 chains: fwd[l] for the
+ * contraction over K, bwd[l] (W^T) for the input cotangent's contraction over
+ * N; K * N bf16 each, 16-byte aligned; NULL entries are skipped.  Layout:
+ * 1 KB chunk kb * (ND / 32) + nb holds, for lane l, element i, B[16 kb + 8
+ * (l >> 5) + i][32 nb + (l & 31)] of B = W [K][N] (fwd) or W^T [N][K] (bwd). */
+int ppo_pack_bf16_operands(void* stream, int L, const void* const* W, int64_t ldw, int K, int N,
+                           void* const* fwd, void* const* bwd);
+
 /* ------------------------------------------------------- linear scan
  * Replace boonta's linear-recurrence scan and its custom VJP
  * (boonta/networks/kernels/scan.py:13-88: scan / _scan_fwd / _scan_bwd),

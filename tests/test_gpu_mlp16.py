@@ -1,0 +1,306 @@
+"""The bf16 torso chain (ppo_mlp16_ln_fwd) and the packed operand images it
+reads (ppo_pack_bf16_operands), on the GPU through the C ABI:
+
+- a packed image holds, chunk by chunk, the MFMA operand layout the header
+  states (checked element by element against numpy on the host);
+- the chain is bit-identical to the per-layer launches it replaces
+  (ppo_splits_bias_act_bf16 + ppo_layernorm_act_fwd_bf16_out16 for the first
+  layer; ppo_gemm_bf16s with the rounded bias epilogue +
+  ppo_layernorm_act_fwd_bf16_out16 for each later one): the large-observation
+  trunk (8192 rows, 3 x 512, ReLU, two K splits), ragged row counts, one
+  split, a single layer, and the other activations;
+- the backward chain (ppo_mlp16_ln_bwd) gives the per-layer launches' dZ16
+  bit for bit and their LayerNorm gradient sums to fp32 summation order;
+- a whole bf16 PPO.update with the forward chain equals, bit for bit, the same
+  update with one launch per layer, and with both chains agrees with it to
+  fp32 summation order (the chains' parity with the oracle is that of the
+  per-layer path, which test_gpu_bf16 checks; it runs with both chains)."""
+import numpy as np
+import pytest
+import torch
+
+from boonta_amd import _lib
+from boonta_amd.algorithms.ppo import flat_state_of
+from boonta_amd.learner import ForwardChain
+from boonta_amd.random import key as make_key
+from ppo_cases import device_transition, gpu_algorithm, make_case
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+F = 512
+EPI_BIAS_ACT = 1
+
+
+def st():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def bits16(x):
+    return x.to(torch.bfloat16).view(torch.int16).contiguous()
+
+
+def ptrs(ts):
+    import ctypes
+    arr = (ctypes.c_void_p * len(ts))(*[None if t is None else t.data_ptr() for t in ts])
+    return arr, ctypes.cast(arr, ctypes.c_void_p).value
+
+
+def unpack_reference(W, K, N):
+    """The packed layouts restated on the host: fwd chunk kb * (N / 32) + nb
+    holds B[16 kb + 8 (l >> 5) + i][32 nb + (l & 31)] at 512 c + 8 l + i for
+    B = W; bwd the same for B = W^T."""
+    def pack(B):
+        KD, ND = B.shape
+        out = np.zeros(KD * ND, np.int16)
+        l = np.arange(64)
+        for kb in range(KD // 16):
+            for nb in range(ND // 32):
+                c = kb * (ND // 32) + nb
+                for i in range(8):
+                    out[512 * c + 8 * l + i] = B[16 * kb + 8 * (l >> 5) + i, 32 * nb + (l & 31)]
+        return out
+    return pack(W), pack(W.T.copy())
+
+
+@pytest.mark.parametrize("K,N,ldw", [(512, 512, 512), (64, 96, 104)])
+def test_pack_bf16_operands_layout(K, N, ldw):
+    torch.manual_seed(1)
+    Wf = torch.randn(K, ldw, device=DEV)
+    W = bits16(Wf)
+    fwd = torch.zeros(K * N, dtype=torch.int16, device=DEV)
+    bwd = torch.zeros(K * N, dtype=torch.int16, device=DEV)
+    wa, wp = ptrs([W])
+    fa, fp = ptrs([fwd])
+    ba, bp = ptrs([bwd])
+    _lib.call("ppo_pack_bf16_operands", st(), 1, wp, ldw, K, N, fp, bp)
+    torch.cuda.synchronize()
+    ef, eb = unpack_reference(W.cpu().numpy()[:, :N], K, N)
+    np.testing.assert_array_equal(fwd.cpu().numpy(), ef)
+    np.testing.assert_array_equal(bwd.cpu().numpy(), eb)
+
+
+def make_layers(L, seed):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=g).to(DEV)
+    lay = []
+    for l in range(L):
+        lay.append(dict(W16=bits16(r(F, F) * 0.05) if l > 0 else None, b=r(F) * 0.1, g=1 + 0.1 * r(F),
+                        be=0.1 * r(F)))
+    return lay
+
+
+def per_layer(part, S, M, lay, act, eps=1e-6):
+    """The per-layer launches: split sum + bias, then LayerNorm; per later
+    layer the bf16 GEMM with the rounded bias epilogue, then LayerNorm."""
+    out = []
+    for l, p in enumerate(lay):
+        Z = torch.zeros(M, F, device=DEV)
+        if l == 0:
+            _lib.call("ppo_splits_bias_act_bf16", st(), part.data_ptr(), F, M * F, S, p["b"].data_ptr(), 0,
+                      Z.data_ptr(), F, M, F)
+        else:
+            _lib.call("ppo_gemm_bf16s", st(), 0, 0, 1, 1, out[-1]["Y16"].data_ptr(), F, None, p["W16"].data_ptr(),
+                      F, Z.data_ptr(), F, M, F, F, 1, 0, EPI_BIAS_ACT, p["b"].data_ptr(), 0, 1, None, 0, None, -1)
+        Y = torch.zeros(M, F, device=DEV)
+        Y16 = torch.zeros(M, F, dtype=torch.int16, device=DEV)
+        mean = torch.zeros(M, device=DEV)
+        rstd = torch.zeros(M, device=DEV)
+        _lib.call("ppo_layernorm_act_fwd_bf16_out16", st(), Z.data_ptr(), F, p["g"].data_ptr(), p["be"].data_ptr(),
+                  Y.data_ptr(), F, Y16.data_ptr(), F, mean.data_ptr(), rstd.data_ptr(), M, F, eps, act)
+        out.append(dict(Z=Z, Y=Y, Y16=Y16, mean=mean, rstd=rstd))
+    return out
+
+
+def chain(part, S, M, lay, act, eps=1e-6, y32=None):
+    L = len(lay)
+    keep = []
+    pk = [None] + [torch.zeros(F * F, dtype=torch.int16, device=DEV) for _ in range(1, L)]
+    if L > 1:
+        wa, wp = ptrs([p["W16"] for p in lay[1:]])
+        fa, fp = ptrs(pk[1:])
+        keep += [wa, fa]
+        _lib.call("ppo_pack_bf16_operands", st(), L - 1, wp, F, F, F, fp, None)
+    out = [dict(Z=torch.full((M, F), 7.0, device=DEV), Y=torch.full((M, F), 7.0, device=DEV),
+                Y16=torch.full((M, F), 7, dtype=torch.int16, device=DEV), mean=torch.full((M,), 7.0, device=DEV),
+                rstd=torch.full((M,), 7.0, device=DEV)) for _ in range(L)]
+    y32 = [True] * L if y32 is None else y32
+    tabs = {}
+    for k, src in (("Wp", pk), ("b", [p["b"] for p in lay]), ("g", [p["g"] for p in lay]),
+                   ("be", [p["be"] for p in lay]), ("Z", [o["Z"] for o in out]),
+                   ("Y", [o["Y"] if y32[l] else None for l, o in enumerate(out)]), ("Y16", [o["Y16"] for o in out]),
+                   ("mean", [o["mean"] for o in out]), ("rstd", [o["rstd"] for o in out])):
+        a, p = ptrs(src)
+        keep.append(a)
+        tabs[k] = p
+    _lib.call("ppo_mlp16_ln_fwd", st(), L, part.data_ptr(), F, M * F, S, M, tabs["Wp"], tabs["b"], tabs["g"],
+              tabs["be"], tabs["Z"], tabs["Y"], tabs["Y16"], F, tabs["mean"], tabs["rstd"], eps, act)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("M,L,S,act", [(8192, 3, 2, 1), (96, 3, 2, 1), (50, 3, 2, 1), (70, 2, 1, 1), (64, 1, 2, 1),
+                                       (64, 2, 2, 3), (64, 2, 2, 2), (33, 2, 3, 0)])
+def test_chain_is_bit_identical_to_per_layer_launches(M, L, S, act):
+    torch.manual_seed(M + 7 * L + 3 * S + act)
+    print(f"chain case M={M} L={L} S={S} act={act}", flush=True)
+    part = torch.randn(S, M, F, device=DEV) * 1.5
+    lay = make_layers(L, seed=M + L)
+    ref = per_layer(part, S, M, lay, act)
+    got = chain(part, S, M, lay, act)
+    for l in range(L):
+        for k in ("Z", "Y", "Y16", "mean", "rstd"):
+            assert torch.equal(got[l][k], ref[l][k]), (l, k, (got[l][k] != ref[l][k]).sum().item())
+
+
+def test_chain_without_fp32_outputs_leaves_them_untouched():
+    M, L = 64, 3
+    part = torch.randn(2, M, F, device=DEV)
+    lay = make_layers(L, seed=11)
+    ref = per_layer(part, 2, M, lay, 1)
+    got = chain(part, 2, M, lay, 1, y32=[False, False, True])
+    for l in range(L):
+        assert torch.equal(got[l]["Y16"], ref[l]["Y16"]) and torch.equal(got[l]["Z"], ref[l]["Z"])
+    assert bool((got[0]["Y"] == 7.0).all()) and bool((got[1]["Y"] == 7.0).all())
+    assert torch.equal(got[2]["Y"], ref[2]["Y"])
+
+
+def test_chain_rejects_bad_arguments():
+    part = torch.zeros(2, 32, F, device=DEV)
+    a, p = ptrs([None, None])
+    # a later layer without its packed operand image
+    with pytest.raises(_lib.KernelError, match="ppo_mlp16_ln_fwd"):
+        _lib.call("ppo_mlp16_ln_fwd", st(), 2, part.data_ptr(), F, 32 * F, 2, 32, p, p, p, p, p, p, p, F, p, p,
+                  1e-6, 1)
+    # K not a multiple of 32
+    with pytest.raises(_lib.KernelError, match="ppo_pack_bf16_operands"):
+        _lib.call("ppo_pack_bf16_operands", st(), 1, p, F, 500, F, p, p)
+
+
+def bwd_inputs(M, L, act, seed):
+    """Forward state of an L-layer chain (Z, mean, rstd, Y16 from the forward
+    chain on random split partials), kernels and a top cotangent."""
+    torch.manual_seed(seed)
+    part = torch.randn(2, M, F, device=DEV) * 1.5
+    lay = make_layers(L, seed=seed)
+    fwd = chain(part, 2, M, lay, act)
+    dY = torch.randn(M, F, device=DEV)
+    return lay, fwd, dY
+
+
+def bwd_per_layer(lay, fwd, dY, M, act):
+    L = len(lay)
+    nb = _lib.load().ppo_layernorm_bwd_blocks(M)
+    out = [None] * L
+    dy = dY
+    for l in range(L - 1, -1, -1):
+        dz16 = torch.zeros(M, F, dtype=torch.int16, device=DEV)
+        part = torch.zeros(nb, 2 * F, device=DEV)
+        _lib.call("ppo_layernorm_act_bwd_bf16_out16", st(), dy.data_ptr(), F, fwd[l]["Z"].data_ptr(), F,
+                  fwd[l]["mean"].data_ptr(), fwd[l]["rstd"].data_ptr(), lay[l]["g"].data_ptr(), lay[l]["be"].data_ptr(),
+                  dz16.data_ptr(), F, part.data_ptr(), M, F, act)
+        out[l] = dict(dZ16=dz16, part=part)
+        if l > 0:
+            dy = torch.zeros(M, F, device=DEV)
+            _lib.call("ppo_gemm_bf16s", st(), 0, 1, 1, 1, dz16.data_ptr(), F, None, lay[l]["W16"].data_ptr(), F,
+                      dy.data_ptr(), F, M, F, F, 1, 0, 0, None, 0, 1, None, 0, None, -1)
+    torch.cuda.synchronize()
+    return out
+
+
+def bwd_chain(lay, fwd, dY, M, act):
+    L = len(lay)
+    nb = _lib.load().ppo_mlp16_ln_bwd_blocks(M)
+    keep = []
+    pb = [None] + [torch.zeros(F * F, dtype=torch.int16, device=DEV) for _ in range(1, L)]
+    if L > 1:
+        wa, wp = ptrs([p["W16"] for p in lay[1:]])
+        ba, bp = ptrs(pb[1:])
+        keep += [wa, ba]
+        _lib.call("ppo_pack_bf16_operands", st(), L - 1, wp, F, F, F, None, bp)
+    out = [dict(dZ16=torch.full((M, F), 7, dtype=torch.int16, device=DEV), part=torch.zeros(nb, 2 * F, device=DEV))
+           for _ in range(L)]
+    tabs = {}
+    for k, src in (("Wb", pb), ("Z", [f["Z"] for f in fwd]), ("mean", [f["mean"] for f in fwd]),
+                   ("rstd", [f["rstd"] for f in fwd]), ("g", [p["g"] for p in lay]), ("be", [p["be"] for p in lay]),
+                   ("dZ16", [o["dZ16"] for o in out]), ("part", [o["part"] for o in out])):
+        a, p = ptrs(src)
+        keep.append(a)
+        tabs[k] = p
+    _lib.call("ppo_mlp16_ln_bwd", st(), L, dY.data_ptr(), F, M, tabs["Wb"], tabs["Z"], tabs["mean"], tabs["rstd"],
+              tabs["g"], tabs["be"], tabs["dZ16"], F, tabs["part"], act)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("M,L,act", [(8192, 3, 1), (96, 3, 1), (50, 3, 1), (64, 1, 1), (64, 2, 3), (64, 2, 2),
+                                     (33, 2, 0)])
+def test_backward_chain_matches_per_layer_launches(M, L, act):
+    """dZ16 bit for bit (the input cotangents between layers are the bf16
+    GEMM's, bit for bit, or dZ16 below the top would differ); the LayerNorm
+    gradient sums over all rows to fp32 summation order (the chain sums its
+    own 32-row blocks)."""
+    print(f"backward chain case M={M} L={L} act={act}", flush=True)
+    lay, fwd, dY = bwd_inputs(M, L, act, seed=M + L + act)
+    ref = bwd_per_layer(lay, fwd, dY, M, act)
+    got = bwd_chain(lay, fwd, dY, M, act)
+    for l in range(L):
+        assert torch.equal(got[l]["dZ16"], ref[l]["dZ16"]), (l, (got[l]["dZ16"] != ref[l]["dZ16"]).sum().item())
+        g = got[l]["part"].double().sum(0).cpu().numpy()
+        r = ref[l]["part"].double().sum(0).cpu().numpy()
+        scale = ref[l]["part"].double().abs().sum(0).cpu().numpy() + 1e-30
+        assert np.all(np.abs(g - r) <= 1e-5 * scale), (l, np.max(np.abs(g - r) / scale))
+
+
+def run_update(monkeypatch, chain16, bwd=True):
+    monkeypatch.setattr(ForwardChain, "CHAIN16", chain16)
+    monkeypatch.setattr(ForwardChain, "CHAIN16_BWD", bwd)
+    r, plan, params, tr, roll = make_case(config=5, T=8, N=64, M=2, E=2)
+    alg = gpu_algorithm(r, use_graph=False)
+    state = alg.init_from_params({"params": params}, r.obs_dim)
+    trans = device_transition(tr, roll)
+    alg.update(state, make_key(3), trans)
+    torch.cuda.synchronize()
+    ex = alg.executor(state, r.T, r.N, r.obs_dim)
+    assert (ex.trunk[0].chain16 is not None) == chain16
+    flat = flat_state_of(state)
+    logs = alg.logs(state, r.T, r.N, r.obs_dim)
+    return flat.P.clone(), flat.MU.clone(), flat.NU.clone(), logs
+
+
+def test_update_with_forward_chain_equals_per_layer_update(monkeypatch):
+    P1, MU1, NU1, logs1 = run_update(monkeypatch, True, bwd=False)
+    P0, MU0, NU0, logs0 = run_update(monkeypatch, False)
+    assert torch.equal(P1, P0) and torch.equal(MU1, MU0) and torch.equal(NU1, NU0)
+    for k in logs0:
+        np.testing.assert_array_equal(logs1[k], logs0[k], err_msg=k)
+
+
+def first_step_gradient(monkeypatch, chain16, bwd):
+    monkeypatch.setattr(ForwardChain, "CHAIN16", chain16)
+    monkeypatch.setattr(ForwardChain, "CHAIN16_BWD", bwd)
+    r, plan, params, tr, roll = make_case(config=5, T=8, N=64, M=2, E=2)
+    alg = gpu_algorithm(r, use_graph=False)
+    state = alg.init_from_params({"params": params}, r.obs_dim)
+    trans = device_transition(tr, roll)
+    ex = alg.executor(state, r.T, r.N, r.obs_dim)
+    ex.KEY.copy_(torch.from_numpy(make_key(3).view(np.int32).copy()))
+    ex.bind(alg._inputs(trans, r.obs_dim)[0])
+    ex.issue(torch.cuda.current_stream().cuda_stream, max_steps=1)
+    torch.cuda.synchronize()
+    return flat_state_of(state).G.clone(), ex
+
+
+def test_gradient_with_both_chains_matches_per_layer_launches(monkeypatch):
+    """The first step's gradient: every Dense gradient bit for bit (their
+    operands dZ16 and Y16 are), the LayerNorm scale and bias gradients to
+    fp32 summation order (the backward chain sums 32-row blocks)."""
+    G1, ex = first_step_gradient(monkeypatch, True, True)
+    G0, _ = first_step_gradient(monkeypatch, False, False)
+    ln = torch.zeros_like(G0, dtype=torch.bool)
+    for lb in ex.trunk:
+        for k in ("scale", "bias"):
+            reg = lb.spec.ln[k]
+            ln[reg.offset:reg.offset + lb.spec.fout] = True
+    assert torch.equal(G1[~ln], G0[~ln])
+    a, b = G1[ln].double(), G0[ln].double()
+    assert ((a - b).abs() <= 1e-5 * b.abs().max() + 1e-5 * b.abs()).all(), (a - b).abs().max().item()
