@@ -28,14 +28,17 @@
 // each 1 KB chunk is one wave's MFMA B operand for one 32-column block and
 // one 16-deep k step, so every operand load is a coalesced 16 bytes per lane
 // straight into registers, several k steps ahead of the MFMAs.  The workgroup's
-// four waves own 128 output columns each; no kernel data goes through LDS.
+// eight waves own 64 output columns each; no kernel data goes through LDS.
 #include "common.h"
 
 namespace {
 
 constexpr int C16_F = 512;                 // features in and out of every chain layer
 constexpr int C16_ROWS = 32;               // rows per workgroup
-constexpr int C16_THREADS = 256;           // four waves of 128 output columns
+constexpr int C16_WAVES = 8;               // two per SIMD: one's LayerNorm latencies hide behind the other's work
+constexpr int C16_THREADS = 64 * C16_WAVES;
+constexpr int C16_CPW = C16_F / C16_WAVES;  // output columns per wave in a contraction
+constexpr int C16_BJ = C16_CPW / 32;        // its 32-column MFMA blocks
 constexpr int C16_MAXL = 8;
 constexpr int C16_KSTEPS = C16_F / 16;     // 16-deep k steps of one contraction
 constexpr int C16_NB = C16_F / 32;         // 32-column blocks of one layer
@@ -111,15 +114,15 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_fwd_kernel(Fwd16Args 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int m0 = blockIdx.x * C16_ROWS;
   const int h = lane >> 5, l32 = lane & 31;
-  constexpr int RPW = C16_ROWS / 4;  // rows of a wave's row stages
+  constexpr int RPW = C16_ROWS / C16_WAVES;  // rows of a wave's row stages
   const int r0 = RPW * wave;         // the wave's first row in the tile
 
-  // kernel operand ring: w[s % PF][j] holds k step s of column block 4 wave + j
-  bf16x8 w[PF][4];
-  auto load_w = [&](int l, int s, bf16x8 (&dst)[4]) {
-    const uint16_t* Ws = a.Wp[l] + ((int64_t)s * C16_NB + 4 * wave) * 512 + 8 * lane;
+  // kernel operand ring: w[s % PF][j] holds k step s of column block C16_BJ wave + j
+  bf16x8 w[PF][C16_BJ];
+  auto load_w = [&](int l, int s, bf16x8 (&dst)[C16_BJ]) {
+    const uint16_t* Ws = a.Wp[l] + ((int64_t)s * C16_NB + C16_BJ * wave) * 512 + 8 * lane;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dst[j] = *reinterpret_cast<const bf16x8*>(Ws + 512 * j);
+    for (int j = 0; j < C16_BJ; ++j) dst[j] = *reinterpret_cast<const bf16x8*>(Ws + 512 * j);
   };
   float g[VPL], be[VPL];
   auto load_ln = [&](int l) {
@@ -201,23 +204,24 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_fwd_kernel(Fwd16Args 
       for (int s = 0; s < PF; ++s) load_w(1, s, w[s]);
     }
     constexpr int NC = RPW * C16_F / 256;  // 16-byte chunks per lane
+    constexpr int NB = NC > 8 ? 2 : 1;     // batches of them
 #pragma unroll
-    for (int hb = 0; hb < 2; ++hb) {
-      floatx4 p[NC / 2];
-      const float* src[NC / 2];
+    for (int hb = 0; hb < NB; ++hb) {
+      floatx4 p[NC / NB];
+      const float* src[NC / NB];
 #pragma unroll
-      for (int ii = 0; ii < NC / 2; ++ii) {
-        const int c = 64 * (hb * (NC / 2) + ii) + lane, rr = c >> 7, c4 = c & 127;
+      for (int ii = 0; ii < NC / NB; ++ii) {
+        const int c = 64 * (hb * (NC / NB) + ii) + lane, rr = c >> 7, c4 = c & 127;
         const int grow = m0 + r0 + rr;
         src[ii] = a.part + (int64_t)(grow < a.M ? grow : a.M - 1) * a.ldp + 4 * c4;
         p[ii] = *reinterpret_cast<const floatx4*>(src[ii]);
       }
       for (int sp = 1; sp < a.nsplit; ++sp)
 #pragma unroll
-        for (int ii = 0; ii < NC / 2; ++ii) p[ii] += *reinterpret_cast<const floatx4*>(src[ii] + sp * a.pstride);
+        for (int ii = 0; ii < NC / NB; ++ii) p[ii] += *reinterpret_cast<const floatx4*>(src[ii] + sp * a.pstride);
 #pragma unroll
-      for (int ii = 0; ii < NC / 2; ++ii) {
-        const int i = hb * (NC / 2) + ii;
+      for (int ii = 0; ii < NC / NB; ++ii) {
+        const int i = hb * (NC / NB) + ii;
         const int c = 64 * i + lane, rr = c >> 7, c4 = c & 127;
         const floatx4 bq = b4[i & 1];
         floatx4 v;
@@ -238,14 +242,14 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_fwd_kernel(Fwd16Args 
     // the layer's parameters, ahead of the contraction (its loads are waited
     // for with the kernel operands', none after a store)
     const float* bias = a.bias[l];
-    float bc[4];
+    float bc[C16_BJ];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) bc[j] = bias ? bias[128 * wave + 32 * j + l32] : 0.f;
+    for (int j = 0; j < C16_BJ; ++j) bc[j] = bias ? bias[C16_CPW * wave + 32 * j + l32] : 0.f;
     load_ln(l);
     __syncthreads();  // the layer input is in sA
-    floatx16 acc[4];
+    floatx16 acc[C16_BJ];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < C16_BJ; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
     const uint16_t* arow = sA + l32 * A_PITCH + 8 * h;
@@ -255,7 +259,7 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_fwd_kernel(Fwd16Args 
     for (int s = 0; s < C16_KSTEPS; ++s) {
       if (s + 1 < C16_KSTEPS) x8[(s + 1) & 1] = *reinterpret_cast<const bf16x8*>(arow + 16 * (s + 1));
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < C16_BJ; ++j)
         acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x8[s & 1], w[s % PF][j], acc[j], 0, 0, 0);
       // refill the slot just consumed: step s + PF of this layer, or the
       // next layer's first steps (in flight across the epilogue)
@@ -269,8 +273,8 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_fwd_kernel(Fwd16Args 
     }
     // bias epilogue of the contraction into the pre-activation tile
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = 128 * wave + 32 * j + l32;
+    for (int j = 0; j < C16_BJ; ++j) {
+      const int n = C16_CPW * wave + 32 * j + l32;
       const float bb = ppo::bf16_round(bc[j]);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -322,18 +326,19 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_bwd_kernel(Bwd16Args 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int m0 = blockIdx.x * C16_ROWS;
   const int h = lane >> 5, l32 = lane & 31;
-  constexpr int RPW = C16_ROWS / 4;
-  constexpr int RB = 4;  // rows per LayerNorm batch
+  constexpr int RPW = C16_ROWS / C16_WAVES;
+  constexpr int RB = RPW;  // rows per LayerNorm batch
   const int r0 = RPW * wave;
   // the wave's gradient-sum slot (4 KB) lies in its own rows of sD, free once
   // the wave has read its cotangents
+  static_assert(RPW * Z_PITCH >= 2 * C16_F, "a wave's rows of sD hold its gradient sums");
   float* red = sD + r0 * Z_PITCH;
 
-  bf16x8 w[PF][4];
-  auto load_w = [&](int l, int s, bf16x8 (&dst)[4]) {
-    const uint16_t* Ws = a.Wb[l] + ((int64_t)s * C16_NB + 4 * wave) * 512 + 8 * lane;
+  bf16x8 w[PF][C16_BJ];
+  auto load_w = [&](int l, int s, bf16x8 (&dst)[C16_BJ]) {
+    const uint16_t* Ws = a.Wb[l] + ((int64_t)s * C16_NB + C16_BJ * wave) * 512 + 8 * lane;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dst[j] = *reinterpret_cast<const bf16x8*>(Ws + 512 * j);
+    for (int j = 0; j < C16_BJ; ++j) dst[j] = *reinterpret_cast<const bf16x8*>(Ws + 512 * j);
   };
   // layer l's pre-activations and statistics of the wave's rows (lane + 64 e)
   float zv[RPW][VPL], mu[RPW], rs[RPW];
@@ -434,15 +439,15 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_bwd_kernel(Bwd16Args 
         const int f = tid + C16_THREADS * k;
         float t = 0.f;
 #pragma unroll
-        for (int wv = 0; wv < 4; ++wv) t += sD[RPW * wv * Z_PITCH + f];
+        for (int wv = 0; wv < C16_WAVES; ++wv) t += sD[RPW * wv * Z_PITCH + f];
         part[f] = t;
       }
     }
     if (l == 0) break;
     __syncthreads();  // the sums are read before the contraction's epilogue overwrites sD
-    floatx16 acc[4];
+    floatx16 acc[C16_BJ];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < C16_BJ; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
     const uint16_t* arow = sA + l32 * A_PITCH + 8 * h;
@@ -452,7 +457,7 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_bwd_kernel(Bwd16Args 
     for (int s = 0; s < C16_KSTEPS; ++s) {
       if (s + 1 < C16_KSTEPS) x8[(s + 1) & 1] = *reinterpret_cast<const bf16x8*>(arow + 16 * (s + 1));
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < C16_BJ; ++j)
         acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x8[s & 1], w[s % PF][j], acc[j], 0, 0, 0);
       if (s + PF < C16_KSTEPS)
         load_w(l, s + PF, w[s % PF]);
@@ -463,8 +468,8 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_bwd_kernel(Bwd16Args 
     // the next layer's pre-activations, in flight across the epilogue
     load_z(l - 1);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = 128 * wave + 32 * j + l32;
+    for (int j = 0; j < C16_BJ; ++j) {
+      const int n = C16_CPW * wave + 32 * j + l32;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = 8 * (r >> 2) + 4 * h + (r & 3);
