@@ -158,6 +158,12 @@ def _single_launch_work(name, args):
         L, nsplit, M = args[1], args[5], args[6]
         return (2.0 * M * 512 * 512 * (L - 1),
                 4.0 * M * 512 * nsplit + 2.0 * 512 * 512 * (L - 1) + M * L * (6.0 * 512 + 8) + 4.0 * M * 512)
+    if name == "ppo_mlp16_ln_bwd":
+        # top cotangent and per layer Z, mean, rstd in; dZ16 and the 32-row gradient sums out; bf16 kernels
+        L, M = args[1], args[4]
+        return (2.0 * M * 512 * 512 * (L - 1),
+                4.0 * M * 512 + M * L * (4.0 * 512 + 8 + 2.0 * 512) + L * ((M + 31) // 32) * 4096.0
+                + 2.0 * 512 * 512 * (L - 1))
     if name == "ppo_pack_bf16_operands":
         L, K, N = args[1], args[4], args[5]
         return 0.0, 4.0 * L * K * N
@@ -214,6 +220,8 @@ def _single_launch_shape(name, args):
         return [args[-6], args[-5], args[-4]]
     if name == "ppo_mlp16_ln_fwd":
         return [args[6], 512, 512, args[1]]
+    if name == "ppo_mlp16_ln_bwd":
+        return [args[4], 512, 512, args[1]]
     if name.startswith("ppo_gru"):
         return [args[-2], args[-1]]
     return None
@@ -241,6 +249,8 @@ def launch_key(name, args):
         return (name, args[-6], args[-5], args[-4])
     if name == "ppo_mlp16_ln_fwd":
         return (name, args[1], args[5], args[6])
+    if name == "ppo_mlp16_ln_bwd":
+        return (name, args[1], args[4])
     return (name, id(args))
 
 
@@ -401,10 +411,14 @@ def _cpu_baseline_pupo(recipe, params, plan, cfg, opt, key, budget_s, tr):
                       f"{per:.2f} s per step), extrapolated to {E * M} steps"}
 
 
+BF16_KERNELS = ("ppo_gemm_bf16", "ppo_gemm_bf16s", "ppo_mlp16_ln_fwd", "ppo_mlp16_ln_bwd")
+
+
 def roofline_of(dom, total, workload):
-    if dom["flops"] > 0:
+    peak = PEAK["bf16_mfma"] if dom["name"] in BF16_KERNELS else PEAK["fp32_mfma"]
+    # the roof the kernel meets first: its MFMA time at peak against its HBM time at peak
+    if dom["flops"] > 0 and dom["flops"] / (peak * 1e12) >= dom["bytes"] / (PEAK["hbm"] * 1e9):
         achieved = dom["flops"] / (dom["ms"] * 1e-3) / 1e12
-        peak = PEAK["bf16_mfma"] if dom["name"] in ("ppo_gemm_bf16", "ppo_gemm_bf16s") else PEAK["fp32_mfma"]
         roof = {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
                 "frac": achieved / peak, "traffic": None}
     else:
@@ -426,8 +440,9 @@ def launch_rows(rows):
     for r in rows:
         e = {k: r[k] for k in ("name", "layout", "shape", "ms", "count")}
         sec = r["ms"] * 1e-3
-        if r["flops"] > 0:
-            peak = PEAK["bf16_mfma"] if r["name"] in ("ppo_gemm_bf16", "ppo_gemm_bf16s") else PEAK["fp32_mfma"]
+        peak = PEAK["bf16_mfma"] if r["name"] in BF16_KERNELS else PEAK["fp32_mfma"]
+        # the roof a launch meets first: its MFMA time at peak against its HBM time at peak
+        if r["flops"] > 0 and r["flops"] / (peak * 1e12) >= r["bytes"] / (PEAK["hbm"] * 1e9):
             e.update(bound="mfma", achieved=r["flops"] / sec / 1e12, frac=r["flops"] / sec / 1e12 / peak)
         elif r["bytes"] > 0:
             e.update(bound="hbm", achieved=r["bytes"] / sec / 1e9, frac=r["bytes"] / sec / 1e9 / PEAK["hbm"])
