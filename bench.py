@@ -154,10 +154,16 @@ def _single_launch_work(name, args):
         weights = 256 * 256 * (L - 1) + 2 * 256 * L
         return towers * 2.0 * M * 256 * 256 * (L - 1), towers * 4.0 * (M * 256 + weights + M * L * (2 * 256 + 2))
     if name == "ppo_mlp16_ln_fwd":
-        # split partials in; per layer Z (fp32), Y16, mean, rstd out, the top layer's Y; bf16 kernels
+        # split partials in; per layer Z (fp32), Y16, mean, rstd out, the top layer's Y; bf16 kernels;
+        # with the head, its outputs
         L, nsplit, M = args[1], args[5], args[6]
-        return (2.0 * M * 512 * 512 * (L - 1),
-                4.0 * M * 512 * nsplit + 2.0 * 512 * 512 * (L - 1) + M * L * (6.0 * 512 + 8) + 4.0 * M * 512)
+        nh = args[21] if len(args) > 21 and args[19] else 0
+        return (2.0 * M * 512 * (512 * (L - 1) + nh),
+                4.0 * M * 512 * nsplit + 2.0 * 512 * (512 * (L - 1) + nh) + M * L * (6.0 * 512 + 8) + 4.0 * M * 512
+                + 4.0 * M * nh)
+    if name == "ppo_pack_bf16_operand_padded":
+        K, n_pad = args[3], args[5]
+        return 0.0, 4.0 * K * n_pad
     if name == "ppo_mlp16_ln_bwd":
         # top cotangent and per layer Z, mean, rstd in; dZ16 and the 32-row gradient sums out; bf16 kernels
         L, M = args[1], args[4]

@@ -60,6 +60,7 @@ struct PackArgs {
   uint16_t* bwd[C16_MAXL];
   int64_t ldw;
   int K, N;
+  int nvalid;  // kernel columns present; forward columns nvalid .. N - 1 are packed as zeros
 };
 
 __global__ void __launch_bounds__(256) pack_operands_kernel(PackArgs a) {
@@ -82,7 +83,7 @@ __global__ void __launch_bounds__(256) pack_operands_kernel(PackArgs a) {
       *reinterpret_cast<uint4*>(v) = q;
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = W[(int64_t)(k0 + i) * a.ldw + n];
+      for (int i = 0; i < 8; ++i) v[i] = n < a.nvalid ? W[(int64_t)(k0 + i) * a.ldw + n] : (uint16_t)0;
     }
     *reinterpret_cast<uint4*>(dst + 8 * u) = *reinterpret_cast<const uint4*>(v);
   }
@@ -104,6 +105,14 @@ struct Fwd16Args {
   uint16_t* Y16[C16_MAXL];
   float* mean[C16_MAXL];
   float* rstd[C16_MAXL];
+  // optional: a Dense head on the last layer's output (nh <= 256 outputs):
+  // its packed forward operand image (512 x 32 ceil(nh / 32)), bias, and the
+  // rounded head outputs [M][ldh]
+  const uint16_t* Wh;
+  const float* bh;
+  float* head;
+  int64_t ldh;
+  int nh;
 };
 
 template <int ACT>
@@ -287,6 +296,45 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_fwd_kernel(Fwd16Args 
     __syncthreads();  // every wave's columns are in sZ; sA is free
     rows_out_f32(a.Z[l], sZ);
     ln_rows(l);
+  }
+
+  // the head: wave j < ceil(nh / 32) computes output columns 32 j .. 32 j + 31
+  // of the tile's 32 rows from the last layer's bf16 output, as the bf16
+  // GEMM's bias epilogue rounds them (the same MFMA sequence: k ascending in
+  // steps of 16, one accumulator)
+  if (a.Wh) {
+    __syncthreads();  // the last layer's output of every row is in sA
+    const int nhb = (a.nh + 31) / 32;
+    if (wave < nhb) {
+      constexpr int HPF = 8;
+      const uint16_t* Wj = a.Wh + (int64_t)wave * 512 + 8 * lane;
+      const int64_t step = (int64_t)nhb * 512;
+      bf16x8 hw[HPF];
+#pragma unroll
+      for (int s = 0; s < HPF; ++s) hw[s] = *reinterpret_cast<const bf16x8*>(Wj + s * step);
+      floatx16 acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+      const uint16_t* arow = sA + l32 * A_PITCH + 8 * h;
+#pragma unroll
+      for (int s = 0; s < C16_KSTEPS; ++s) {
+        const bf16x8 x8 = *reinterpret_cast<const bf16x8*>(arow + 16 * s);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x8, hw[s % HPF], acc, 0, 0, 0);
+        if (s + HPF < C16_KSTEPS) hw[s % HPF] = *reinterpret_cast<const bf16x8*>(Wj + (s + HPF) * step);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      const int n = 32 * wave + l32;
+      if (n < a.nh) {
+        const float bb = a.bh ? ppo::bf16_round(a.bh[n]) : 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int grow = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
+          float v = ppo::bf16_round(acc[r]);
+          if (a.bh) v = ppo::bf16_round(v + bb);
+          if (grow < a.M) a.head[(int64_t)grow * a.ldh + n] = v;
+        }
+      }
+    }
   }
 }
 
@@ -496,7 +544,7 @@ PPO_EXPORT int ppo_pack_bf16_operands(void* stream, int L, const void* const* W,
     return ppo::set_error(PPO_ERR_ARG, "ppo_pack_bf16_operands: bad argument (L=%d K=%d N=%d ldw=%lld)", L, K, N,
                           (long long)ldw);
   PackArgs a{};
-  a.ldw = ldw; a.K = K; a.N = N;
+  a.ldw = ldw; a.K = K; a.N = N; a.nvalid = N;
   for (int l = 0; l < L; ++l) {
     a.W[l] = static_cast<const uint16_t*>(W[l]);
     a.fwd[l] = fwd ? static_cast<uint16_t*>(fwd[l]) : nullptr;
@@ -510,16 +558,39 @@ PPO_EXPORT int ppo_pack_bf16_operands(void* stream, int L, const void* const* W,
   return ppo::check_launch("ppo_pack_bf16_operands");
 }
 
+// Packs one bf16 kernel W [K][N] (row pitch ldw) as the forward operand
+// image of a K x n_pad contraction, n_pad a multiple of 32 >= N, columns N ..
+// n_pad - 1 zero (a head narrower than a 32-column MFMA block).
+PPO_EXPORT int ppo_pack_bf16_operand_padded(void* stream, const void* W, int64_t ldw, int K, int N, int n_pad,
+                                            void* fwd) {
+  if (!W || !fwd || K < 16 || K % 32 || N < 1 || ldw < N || n_pad < N || n_pad % 32 || !aligned16(fwd))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_pack_bf16_operand_padded: bad argument (K=%d N=%d n_pad=%d)", K, N,
+                          n_pad);
+  PackArgs a{};
+  a.ldw = ldw; a.K = K; a.N = n_pad; a.nvalid = N;
+  a.W[0] = static_cast<const uint16_t*>(W);
+  a.fwd[0] = static_cast<uint16_t*>(fwd);
+  const int64_t units = (int64_t)K * n_pad / 8;
+  const dim3 grid((unsigned)std::min<int64_t>(ppo::ceil_div64(units, 256), 1024), 1, 1);
+  hipLaunchKernelGGL(pack_operands_kernel, grid, dim3(256), 0, ppo::as_stream(stream), a);
+  return ppo::check_launch("ppo_pack_bf16_operand_padded");
+}
+
 // Forward of the bf16 chain on M rows from the first Dense's split
 // partials: layer 0's split sum, bias, LayerNorm and activation, then layers
 // 1 .. L-1 (512 x 512 kernels, packed forward operands Wp[l]), each with its
 // bias, LayerNorm and activation.  Writes Z, Y16, mean, rstd of every layer
-// and Y where Y[l] is non-null.
+// and Y where Y[l] is non-null; with Wh non-null also the head on the last
+// layer's output (nh outputs, Wh its packed forward operand image of
+// 32 ceil(nh / 32) columns, bias bh) into head [M][ldh].
 PPO_EXPORT int ppo_mlp16_ln_fwd(void* stream, int L, const float* part, int64_t ldp, int64_t part_stride,
                                 int nsplit, int M, const void* const* Wp, const float* const* bias,
                                 const float* const* gamma, const float* const* beta, float* const* Z,
                                 float* const* Y, void* const* Y16, int64_t ld, float* const* mean,
-                                float* const* rstd, float eps, int act) {
+                                float* const* rstd, float eps, int act, const void* Wh, const float* bh, int nh,
+                                float* head, int64_t ldh) {
+  if (Wh && (nh < 1 || nh > 32 * C16_WAVES || !head || ldh < nh || !aligned16(Wh)))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_mlp16_ln_fwd: bad head (nh=%d ldh=%lld)", nh, (long long)ldh);
   if (L < 1 || L > C16_MAXL || M < 0 || nsplit < 1 || act < 0 || act > 3 || !part || !aligned16(part) ||
       ldp < C16_F || ldp % 4 || (nsplit > 1 && (part_stride < (int64_t)M * ldp || part_stride % 4)) ||
       ld < C16_F || ld % 8 || !gamma || !beta || !Z || !Y16 || !mean || !rstd || !bias || (L > 1 && !Wp))
@@ -528,6 +599,7 @@ PPO_EXPORT int ppo_mlp16_ln_fwd(void* stream, int L, const float* part, int64_t 
   Fwd16Args a{};
   a.part = part; a.ldp = ldp; a.pstride = part_stride; a.nsplit = nsplit; a.M = M; a.L = L; a.eps = eps;
   a.ld = ld;
+  a.Wh = static_cast<const uint16_t*>(Wh); a.bh = bh; a.head = head; a.ldh = ldh; a.nh = nh;
   for (int l = 0; l < L; ++l) {
     if (!gamma[l] || !beta[l] || !Z[l] || !Y16[l] || !mean[l] || !rstd[l] || !aligned16(Z[l]) ||
         !aligned16(Y16[l]) || (Y && Y[l] && !aligned16(Y[l])) || (bias[l] && !aligned16(bias[l])) ||

@@ -491,11 +491,31 @@ class ForwardChain:
             B = arr([_p(pk[l, 1]) for l in range(L - 1)]) if bwd else None
             self._pack16_tables.append((L - 1, addr(W), addr(F), addr(B) if bwd else None, (W, F, B)))
 
+    def _plan_chain16_head(self):
+        """The shared head (heads.py:9-45) rides on the trunk chain's forward
+        when it reads the trunk's 512-wide output: its packed operand image and
+        the head output table of the chain launch."""
+        prog = self.prog
+        c = self.trunk[0].chain16 if self.trunk else None
+        h = prog.head_a
+        if (c is None or not prog.shared_head or self.fused or h.fin != 512 or h.b is None
+                or h.w.ld > 256 or getattr(self, "HEAD", None) is None):
+            return
+        npad = (h.w.ld + 31) // 32 * 32
+        hpk = torch.zeros(512 * npad, dtype=torch.int16, device=self.P16.device)
+        c.update(Wh=_p(hpk), bh=self.flat.view(h.b), nh=h.w.ld, head=_p(self.HEAD), ldh=h.w.ld, head_pack=hpk,
+                 head_npad=npad)
+
     def _pack16(self, st):
         """Packed operand images of the bf16 chains' kernels from the bf16
         parameter image (after each write of the image)."""
         for n, W, F, B, _ in self._pack16_tables:
             self._call("ppo_pack_bf16_operands", st, n, W, 512, 512, 512, F, B)
+        c = self.trunk[0].chain16 if self.trunk else None
+        if c is not None and c.get("Wh"):
+            h = self.prog.head_a
+            self._call("ppo_pack_bf16_operand_padded", st, self._view16(h.w), h.w.ld, 512, h.w.ld, c["head_npad"],
+                       c["Wh"])
 
     def _view16(self, region: Region) -> int:
         """Address of a parameter region in the bf16 parameter image."""
@@ -520,7 +540,8 @@ class ForwardChain:
                     # the rest of the group in one launch from the split partials
                     self._call("ppo_mlp16_ln_fwd", st, c["L"], _p(lb.fpart), s.ld, nrows * s.ld,
                                self.FWD16_SPLITS, nrows, c["Wp"], c["b"], c["g"], c["be"], c["Z"], c["Y"],
-                               c["Y16"], s.ld, c["mean"], c["rstd"], c["eps"], c["act"])
+                               c["Y16"], s.ld, c["mean"], c["rstd"], c["eps"], c["act"], c.get("Wh"), c.get("bh"),
+                               c.get("nh", 0), c.get("head"), c.get("ldh", 0))
                     top = layers[-1]
                     return _p(top.Y), top.spec.ld, None
                 self._call("ppo_splits_bias_act_bf16", st, _p(lb.fpart), s.ld, nrows * s.ld, self.FWD16_SPLITS, Bb,
@@ -716,6 +737,7 @@ class MLPExecutor(ForwardChain):
             self.HCWPART = torch.zeros(self.hc_splits, hc.fin, hc.w.ld, **f32)
             self.HCBPART = torch.zeros(self.hc_splits, hc.w.ld, **f32)
             self.HEADB = torch.zeros(N, hc.w.ld, **f32)
+        self._plan_chain16_head()
         self.loss_blocks = self.head_blocks if self.fused else lib.ppo_loss_blocks(mb)
         self.nstat = lib.ppo_loss_stat_count()
         # loss statistics of every step, finalized into LOGS once per update
@@ -1306,9 +1328,11 @@ class MLPExecutor(ForwardChain):
         if prog.shared_head:
             hx, ldhx, hidx = self._fwd_layers(st, self.trunk, obs, ldo, idx, mb)
             h = prog.head_a
-            self._gemm(st, A_ROW, B_KN, hx, ldhx, hidx, self.flat.view(h.w), h.w.ld, _p(self.HEAD),
-                      h.w.ld, mb, h.w.ld, h.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(h.b), 0, None, None, 0, None,
-                      -1)
+            c = self.trunk[0].chain16 if self.trunk else None
+            if c is None or not c.get("Wh"):  # else the trunk chain wrote the head outputs
+                self._gemm(st, A_ROW, B_KN, hx, ldhx, hidx, self.flat.view(h.w), h.w.ld, _p(self.HEAD),
+                          h.w.ld, mb, h.w.ld, h.fin, 1, 0, EPI_BIAS_ACT, self.flat.view(h.b), 0, None, None, 0,
+                          None, -1)
             vcol = prog.head_out
             self._call("ppo_loss_f32", st, dist, mb, idx, _p(self.HEAD), h.w.ld, _p(self.HEAD) + 4 * vcol, h.w.ld,
                       A, scale_ptr, act_i, act_f, inp["log_prob"], inp["value"], _p(self.ADV), _p(self.RET),

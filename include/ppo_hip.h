@@ -248,12 +248,18 @@ int ppo_mlp_ln_bwd_f32(void* stream, int towers, int L, const float* dY, int64_t
  * and ppo_gemm_bf16s (bias epilogue, rounded) +
  * ppo_layernorm_act_fwd_bf16_out16 per later layer.  Wp[l] (l >= 1): the
  * layer's kernel as the packed forward operand image that
- * ppo_pack_bf16_operands writes. */
+ * ppo_pack_bf16_operands writes.  With Wh != NULL the launch also computes
+ * the Dense head that reads the last layer's output (heads.py:9-45 on a
+ * shared torso; nh <= 256 outputs, bias bh, written rounded into head
+ * [M][ldh]), bit-identical to ppo_gemm_bf16 with the bias epilogue; Wh is
+ * the head kernel's forward operand image from
+ * ppo_pack_bf16_operand_padded (n_pad = 32 ceil(nh / 32)). */
 int ppo_mlp16_max_layers(void);
 int ppo_mlp16_ln_fwd(void* stream, int L, const float* part, int64_t ldp, int64_t part_stride, int nsplit, int M,
                      const void* const* Wp, const float* const* bias, const float* const* gamma,
                      const float* const* beta, float* const* Z, float* const* Y, void* const* Y16, int64_t ld,
-                     float* const* mean, float* const* rstd, float eps, int act);
+                     float* const* mean, float* const* rstd, float eps, int act, const void* Wh, const float* bh,
+                     int nh, float* head, int64_t ldh);
 /* Backward of the same chain from dY, the cotangent of the top layer's
  * output (fp32, row pitch lddy): per layer from the top, the LayerNorm +
  * activation backward (dZ16[l], bf16, row pitch ld, bit-identical to
@@ -277,6 +283,10 @@ int ppo_mlp16_ln_bwd(void* stream, int L, const float* dY, int64_t lddy, int M, 
  * (l >> 5) + i][32 nb + (l & 31)] of B = W [K][N] (fwd) or W^T [N][K] (bwd). */
 int ppo_pack_bf16_operands(void* stream, int L, const void* const* W, int64_t ldw, int K, int N,
                            void* const* fwd, void* const* bwd);
+/* The forward operand image of one bf16 kernel [K][N] (row pitch ldw) padded
+ * with zero columns to n_pad (a multiple of 32 >= N): a head narrower than
+ * the 32-column MFMA blocks. */
+int ppo_pack_bf16_operand_padded(void* stream, const void* W, int64_t ldw, int K, int N, int n_pad, void* fwd);
 
 /* ------------------------------------------------------- linear scan
  * Replace boonta's linear-recurrence scan and its custom VJP

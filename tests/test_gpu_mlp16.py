@@ -6,9 +6,10 @@ reads (ppo_pack_bf16_operands), on the GPU through the C ABI:
 - the chain is bit-identical to the per-layer launches it replaces
   (ppo_splits_bias_act_bf16 + ppo_layernorm_act_fwd_bf16_out16 for the first
   layer; ppo_gemm_bf16s with the rounded bias epilogue +
-  ppo_layernorm_act_fwd_bf16_out16 for each later one): the large-observation
-  trunk (8192 rows, 3 x 512, ReLU, two K splits), ragged row counts, one
-  split, a single layer, and the other activations;
+  ppo_layernorm_act_fwd_bf16_out16 for each later one; ppo_gemm_bf16 for the
+  head it can carry): the large-observation trunk (8192 rows, 3 x 512, ReLU,
+  two K splits, 44 head outputs), ragged row counts, one split, a single
+  layer, heads of 8 to 100 outputs, and the other activations;
 - the backward chain (ppo_mlp16_ln_bwd) gives the per-layer launches' dZ16
   bit for bit and their LayerNorm gradient sums to fp32 summation order;
 - a whole bf16 PPO.update with the forward chain equals, bit for bit, the same
@@ -111,7 +112,9 @@ def per_layer(part, S, M, lay, act, eps=1e-6):
     return out
 
 
-def chain(part, S, M, lay, act, eps=1e-6, y32=None):
+def chain(part, S, M, lay, act, eps=1e-6, y32=None, head=None):
+    """The chain launch; head = (W16 [512][nh], bias [nh], nh) adds the head
+    stage, whose outputs come back as out[-1]["head"]."""
     L = len(lay)
     keep = []
     pk = [None] + [torch.zeros(F * F, dtype=torch.int16, device=DEV) for _ in range(1, L)]
@@ -132,8 +135,17 @@ def chain(part, S, M, lay, act, eps=1e-6, y32=None):
         a, p = ptrs(src)
         keep.append(a)
         tabs[k] = p
+    hargs = (None, None, 0, None, 0)
+    if head is not None:
+        W16h, bh, nh = head
+        npad = (nh + 31) // 32 * 32
+        hpk = torch.zeros(F * npad, dtype=torch.int16, device=DEV)
+        _lib.call("ppo_pack_bf16_operand_padded", st(), W16h.data_ptr(), nh, F, nh, npad, hpk.data_ptr())
+        out[-1]["head"] = torch.full((M, nh), 7.0, device=DEV)
+        keep.append(hpk)
+        hargs = (hpk.data_ptr(), bh.data_ptr(), nh, out[-1]["head"].data_ptr(), nh)
     _lib.call("ppo_mlp16_ln_fwd", st(), L, part.data_ptr(), F, M * F, S, M, tabs["Wp"], tabs["b"], tabs["g"],
-              tabs["be"], tabs["Z"], tabs["Y"], tabs["Y16"], F, tabs["mean"], tabs["rstd"], eps, act)
+              tabs["be"], tabs["Z"], tabs["Y"], tabs["Y16"], F, tabs["mean"], tabs["rstd"], eps, act, *hargs)
     torch.cuda.synchronize()
     return out
 
@@ -150,6 +162,28 @@ def test_chain_is_bit_identical_to_per_layer_launches(M, L, S, act):
     for l in range(L):
         for k in ("Z", "Y", "Y16", "mean", "rstd"):
             assert torch.equal(got[l][k], ref[l][k]), (l, k, (got[l][k] != ref[l][k]).sum().item())
+
+
+@pytest.mark.parametrize("M,L,nh", [(8192, 3, 44), (50, 2, 44), (64, 1, 8), (96, 3, 64), (33, 2, 100)])
+def test_chain_head_is_bit_identical_to_the_head_gemm(M, L, nh):
+    """The head stage against ppo_gemm_bf16 on the last layer's fp32 output
+    with the bias epilogue, rounded (the per-layer path's head launch)."""
+    print(f"chain head case M={M} L={L} nh={nh}", flush=True)
+    torch.manual_seed(M + nh)
+    part = torch.randn(2, M, F, device=DEV) * 1.5
+    lay = make_layers(L, seed=M + 3)
+    W16h = bits16(torch.randn(F, nh, device=DEV) * 0.05)
+    bh = torch.randn(nh, device=DEV) * 0.1
+    got = chain(part, 2, M, lay, 1, head=(W16h, bh, nh))
+    ref = per_layer(part, 2, M, lay, 1)
+    Wf = W16h.view(torch.bfloat16).float().contiguous()
+    H = torch.zeros(M, nh, device=DEV)
+    _lib.call("ppo_gemm_bf16", st(), 0, 0, ref[-1]["Y"].data_ptr(), F, None, Wf.data_ptr(), nh, H.data_ptr(), nh, M,
+              nh, F, 1, 0, EPI_BIAS_ACT, bh.data_ptr(), 0, 1, None, 0, None, -1)
+    torch.cuda.synchronize()
+    assert torch.equal(got[-1]["head"], H), (got[-1]["head"] != H).sum().item()
+    for k in ("Z", "Y16", "mean", "rstd"):
+        assert torch.equal(got[-1][k], ref[-1][k])
 
 
 def test_chain_without_fp32_outputs_leaves_them_untouched():
@@ -170,7 +204,12 @@ def test_chain_rejects_bad_arguments():
     # a later layer without its packed operand image
     with pytest.raises(_lib.KernelError, match="ppo_mlp16_ln_fwd"):
         _lib.call("ppo_mlp16_ln_fwd", st(), 2, part.data_ptr(), F, 32 * F, 2, 32, p, p, p, p, p, p, p, F, p, p,
-                  1e-6, 1)
+                  1e-6, 1, None, None, 0, None, 0)
+    # a head of more outputs than the eight waves' column blocks
+    hp = torch.zeros(F * 288, dtype=torch.int16, device=DEV)
+    with pytest.raises(_lib.KernelError, match="bad head"):
+        _lib.call("ppo_mlp16_ln_fwd", st(), 1, part.data_ptr(), F, 32 * F, 2, 32, p, p, p, p, p, p, p, F, p, p,
+                  1e-6, 1, hp.data_ptr(), None, 288, part.data_ptr(), 288)
     # K not a multiple of 32
     with pytest.raises(_lib.KernelError, match="ppo_pack_bf16_operands"):
         _lib.call("ppo_pack_bf16_operands", st(), 1, p, F, 500, F, p, p)
