@@ -60,7 +60,7 @@ struct PackArgs {
   uint16_t* bwd[C16_MAXL];
   int64_t ldw;
   int K, N;
-  int nvalid;  // kernel columns present; forward columns nvalid .. N - 1 are packed as zeros
+  int nvalid;  // kernel columns present: forward columns and backward k rows nvalid .. N - 1 pack as zeros
 };
 
 __global__ void __launch_bounds__(256) pack_operands_kernel(PackArgs a) {
@@ -77,10 +77,13 @@ __global__ void __launch_bounds__(256) pack_operands_kernel(PackArgs a) {
     const int nb = (int)(c % (ND / 32)), kb = (int)(c / (ND / 32));
     const int k0 = 16 * kb + 8 * (lane >> 5), n = 32 * nb + (lane & 31);
     uint16_t v[8];
-    if (bwd) {
+    if (bwd && a.nvalid == a.N && a.ldw % 8 == 0) {
       // B[k][n] = W[n][k]: eight consecutive k of kernel row n
       const uint4 q = *reinterpret_cast<const uint4*>(W + (int64_t)n * a.ldw + k0);
       *reinterpret_cast<uint4*>(v) = q;
+    } else if (bwd) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = k0 + i < a.nvalid ? W[(int64_t)n * a.ldw + k0 + i] : (uint16_t)0;
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = n < a.nvalid ? W[(int64_t)(k0 + i) * a.ldw + n] : (uint16_t)0;
@@ -352,6 +355,13 @@ struct Bwd16Args {
   const float* beta[C16_MAXL];
   uint16_t* dZ16[C16_MAXL];
   float* part[C16_MAXL];             // [blocks][2 * 512]: scale | bias gradient sums of each workgroup's rows
+  // optional: the top cotangent from a Dense head's output cotangents dhead
+  // [M][lddh] (nh columns) and the head kernel's packed backward operand
+  // image Whb (W^T over nhk 16-deep k steps); dY is then not read
+  const float* dhead;
+  int64_t lddh;
+  const uint16_t* Whb;
+  int nh, nhk;
 };
 
 // From the top layer down: the LayerNorm + activation backward of layer l
@@ -407,14 +417,49 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_bwd_kernel(Bwd16Args 
 #pragma unroll
     for (int s = 0; s < PF; ++s) load_w(a.L - 1, s, w[s]);
   }
-  // the top cotangent: the wave's rows into sD, 16 bytes per lane
+  if (a.Whb) {
+    // the top cotangent from the head: dY = dhead W^T, the head's output
+    // cotangents rounded to bf16 as the bf16 GEMM stages them (sA row r,
+    // columns k < 16 nhk, zero past nh), then its MFMA sequence (k ascending
+    // in steps of 16) and its rounding
+    for (int i = threadIdx.x; i < C16_ROWS * 16 * a.nhk; i += C16_THREADS) {
+      const int r = i / (16 * a.nhk), k = i % (16 * a.nhk);
+      const int grow = m0 + r;
+      const float v = (k < a.nh && grow < a.M) ? a.dhead[(int64_t)grow * a.lddh + k] : 0.f;
+      sA[r * A_PITCH + k] = (uint16_t)ppo::bf16_bits(v);
+    }
+    __syncthreads();
+    floatx16 acc[C16_BJ];
 #pragma unroll
-  for (int i = 0; i < RPW * C16_F / 256; ++i) {
-    const int c = 64 * i + lane, rr = c >> 7, c4 = c & 127;
-    const int grow = m0 + r0 + rr;
-    const floatx4 v =
-        *reinterpret_cast<const floatx4*>(a.dY + (int64_t)(grow < a.M ? grow : a.M - 1) * a.lddy + 4 * c4);
-    *reinterpret_cast<floatx4*>(sD + (r0 + rr) * Z_PITCH + 4 * c4) = v;
+    for (int j = 0; j < C16_BJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+    const uint16_t* arow = sA + l32 * A_PITCH + 8 * h;
+    for (int s = 0; s < a.nhk; ++s) {
+      const bf16x8 x8 = *reinterpret_cast<const bf16x8*>(arow + 16 * s);
+      const uint16_t* Ws = a.Whb + ((int64_t)s * C16_NB + C16_BJ * wave) * 512 + 8 * lane;
+#pragma unroll
+      for (int j = 0; j < C16_BJ; ++j)
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x8, *reinterpret_cast<const bf16x8*>(Ws + 512 * j), acc[j],
+                                                         0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < C16_BJ; ++j) {
+      const int n = C16_CPW * wave + 32 * j + l32;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sD[(8 * (r >> 2) + 4 * h + (r & 3)) * Z_PITCH + n] = ppo::bf16_round(acc[j][r]);
+    }
+    __syncthreads();  // every row's cotangent is in sD; sA is free
+  } else {
+    // the top cotangent: the wave's rows into sD, 16 bytes per lane
+#pragma unroll
+    for (int i = 0; i < RPW * C16_F / 256; ++i) {
+      const int c = 64 * i + lane, rr = c >> 7, c4 = c & 127;
+      const int grow = m0 + r0 + rr;
+      const floatx4 v =
+          *reinterpret_cast<const floatx4*>(a.dY + (int64_t)(grow < a.M ? grow : a.M - 1) * a.lddy + 4 * c4);
+      *reinterpret_cast<floatx4*>(sD + (r0 + rr) * Z_PITCH + 4 * c4) = v;
+    }
   }
 
   for (int l = a.L - 1; l >= 0; --l) {
@@ -558,20 +603,24 @@ PPO_EXPORT int ppo_pack_bf16_operands(void* stream, int L, const void* const* W,
   return ppo::check_launch("ppo_pack_bf16_operands");
 }
 
-// Packs one bf16 kernel W [K][N] (row pitch ldw) as the forward operand
-// image of a K x n_pad contraction, n_pad a multiple of 32 >= N, columns N ..
-// n_pad - 1 zero (a head narrower than a 32-column MFMA block).
+// Packs one bf16 kernel W [K][N] (row pitch ldw) as the operand images of a
+// head narrower than a 32-column MFMA block, padded with zeros to n_pad (a
+// multiple of 32 >= N): fwd, the forward operand of the K x n_pad
+// contraction; bwd (may be null), W^T as the operand of the input
+// cotangent's contraction over the n_pad outputs.
 PPO_EXPORT int ppo_pack_bf16_operand_padded(void* stream, const void* W, int64_t ldw, int K, int N, int n_pad,
-                                            void* fwd) {
-  if (!W || !fwd || K < 16 || K % 32 || N < 1 || ldw < N || n_pad < N || n_pad % 32 || !aligned16(fwd))
+                                            void* fwd, void* bwd) {
+  if (!W || !fwd || K < 16 || K % 32 || N < 1 || ldw < N || n_pad < N || n_pad % 32 || !aligned16(fwd) ||
+      (bwd && !aligned16(bwd)))
     return ppo::set_error(PPO_ERR_ARG, "ppo_pack_bf16_operand_padded: bad argument (K=%d N=%d n_pad=%d)", K, N,
                           n_pad);
   PackArgs a{};
   a.ldw = ldw; a.K = K; a.N = n_pad; a.nvalid = N;
   a.W[0] = static_cast<const uint16_t*>(W);
   a.fwd[0] = static_cast<uint16_t*>(fwd);
+  a.bwd[0] = static_cast<uint16_t*>(bwd);
   const int64_t units = (int64_t)K * n_pad / 8;
-  const dim3 grid((unsigned)std::min<int64_t>(ppo::ceil_div64(units, 256), 1024), 1, 1);
+  const dim3 grid((unsigned)std::min<int64_t>(ppo::ceil_div64(units, 256), 1024), 1, 2);
   hipLaunchKernelGGL(pack_operands_kernel, grid, dim3(256), 0, ppo::as_stream(stream), a);
   return ppo::check_launch("ppo_pack_bf16_operand_padded");
 }
@@ -628,17 +677,25 @@ PPO_EXPORT int ppo_mlp16_ln_bwd_blocks(int rows) { return rows > 0 ? ppo::ceil_d
 // (bf16, row pitch ld) and part[l] ([ppo_mlp16_ln_bwd_blocks(M)][2 * 512]:
 // the LayerNorm scale | bias gradient sums of each 32-row block), and below
 // the top the input cotangent through Wb[l], the packed backward operand
-// image of layer l's kernel.
+// image of layer l's kernel.  With Whb non-null the top cotangent is instead
+// dhead W_h^T from the head's output cotangents dhead [M][lddh] (nh columns)
+// and Whb, the head kernel's packed backward image over nh_pad (32 or 64)
+// outputs (ppo_pack_bf16_operand_padded), as the bf16 head GEMM rounds it.
 PPO_EXPORT int ppo_mlp16_ln_bwd(void* stream, int L, const float* dY, int64_t lddy, int M, const void* const* Wb,
                                 const float* const* Z, const float* const* mean, const float* const* rstd,
                                 const float* const* gamma, const float* const* beta, void* const* dZ16, int64_t ld,
-                                float* const* part, int act) {
-  if (L < 1 || L > C16_MAXL || M < 0 || act < 0 || act > 3 || !dY || !aligned16(dY) || lddy < C16_F || lddy % 4 ||
-      ld < C16_F || ld % 8 || !Z || !mean || !rstd || !gamma || !beta || !dZ16 || !part || (L > 1 && !Wb))
+                                float* const* part, int act, const float* dhead, int64_t lddh, const void* Whb,
+                                int nh, int nh_pad) {
+  if (Whb && (!dhead || nh < 1 || lddh < nh || nh_pad < nh || nh_pad % 32 || nh_pad > 64 || !aligned16(Whb)))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_mlp16_ln_bwd: bad head (nh=%d nh_pad=%d)", nh, nh_pad);
+  if (L < 1 || L > C16_MAXL || M < 0 || act < 0 || act > 3 || (!Whb && (!dY || !aligned16(dY) || lddy < C16_F ||
+      lddy % 4)) || ld < C16_F || ld % 8 || !Z || !mean || !rstd || !gamma || !beta || !dZ16 || !part ||
+      (L > 1 && !Wb))
     return ppo::set_error(PPO_ERR_ARG, "ppo_mlp16_ln_bwd: bad argument (L=%d M=%d)", L, M);
   if (M == 0) return PPO_OK;
   Bwd16Args a{};
   a.dY = dY; a.lddy = lddy; a.M = M; a.L = L; a.ld = ld;
+  a.dhead = dhead; a.lddh = lddh; a.Whb = static_cast<const uint16_t*>(Whb); a.nh = nh; a.nhk = nh_pad / 16;
   for (int l = 0; l < L; ++l) {
     if (!Z[l] || !mean[l] || !rstd[l] || !gamma[l] || !beta[l] || !dZ16[l] || !part[l] || !aligned16(dZ16[l]) ||
         (l > 0 && (!Wb[l] || !aligned16(Wb[l]))))

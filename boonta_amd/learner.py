@@ -502,9 +502,12 @@ class ForwardChain:
                 or h.w.ld > 256 or getattr(self, "HEAD", None) is None):
             return
         npad = (h.w.ld + 31) // 32 * 32
-        hpk = torch.zeros(512 * npad, dtype=torch.int16, device=self.P16.device)
-        c.update(Wh=_p(hpk), bh=self.flat.view(h.b), nh=h.w.ld, head=_p(self.HEAD), ldh=h.w.ld, head_pack=hpk,
+        hpk = torch.zeros(2, 512 * npad, dtype=torch.int16, device=self.P16.device)
+        c.update(Wh=_p(hpk[0]), bh=self.flat.view(h.b), nh=h.w.ld, head=_p(self.HEAD), ldh=h.w.ld, head_pack=hpk,
                  head_npad=npad)
+        if c["bwd"] and npad <= 64:
+            # the backward chain also takes the head's input cotangent over
+            c.update(Whb=_p(hpk[1]))
 
     def _pack16(self, st):
         """Packed operand images of the bf16 chains' kernels from the bf16
@@ -515,7 +518,7 @@ class ForwardChain:
         if c is not None and c.get("Wh"):
             h = self.prog.head_a
             self._call("ppo_pack_bf16_operand_padded", st, self._view16(h.w), h.w.ld, 512, h.w.ld, c["head_npad"],
-                       c["Wh"])
+                       c["Wh"], c.get("Whb"))
 
     def _view16(self, region: Region) -> int:
         """Address of a parameter region in the bf16 parameter image."""
@@ -984,8 +987,11 @@ class MLPExecutor(ForwardChain):
             # every LayerNorm backward and input cotangent in one launch; then
             # the weight gradients from the bf16 cotangents it leaves
             top = layers[-1]
+            h = self.prog.head_a
+            hd = ((_p(self.DHEAD), h.w.ld, c["Whb"], h.w.ld, c["head_npad"]) if c.get("Whb")
+                  else (None, 0, None, 0, 0))
             self._call("ppo_mlp16_ln_bwd", st, c["L"], _p(top.dY), top.spec.ld, self.mb, c["Wb"], c["Z"],
-                       c["mean"], c["rstd"], c["g"], c["be"], c["dZ16"], top.spec.ld, c["part"], c["act"])
+                       c["mean"], c["rstd"], c["g"], c["be"], c["dZ16"], top.spec.ld, c["part"], c["act"], *hd)
             for i in range(len(layers) - 1, -1, -1):
                 lb = layers[i]
                 s, d = lb.spec, lb.spec.dense
@@ -1129,7 +1135,8 @@ class MLPExecutor(ForwardChain):
         self._gemm(st, A_COL, B_KN, hx, ldhx, hidx, _p(dhead), head.w.ld, _p(wpart), head.w.ld,
                   head.fin, head.w.ld, self.mb, splits, head.fin * head.w.ld, EPI_STORE, None, 0, None, None, 0,
                   _p(bpart), -1)
-        if layers:
+        c = layers[0].chain16 if layers else None
+        if layers and not (c is not None and c.get("Whb")):  # else the backward chain takes it over
             dst, epi, act, aux, ldaux = self._dx_target(layers[-1])
             self._gemm(st, A_ROW, B_NK, _p(dhead), head.w.ld, None, self.flat.view(head.w),
                       head.w.ld, dst, layers[-1].spec.ld, self.mb, head.fin, head.w.ld, 1, 0, epi, None, act, None,

@@ -269,12 +269,17 @@ int ppo_mlp16_ln_fwd(void* stream, int L, const float* part, int64_t ldp, int64_
  * ppo_gemm_bf16s), read through Wb[l], the packed backward operand image of
  * layer l's kernel.  Replaces, per layer, jax.value_and_grad's LayerNorm,
  * activation and Dense input-cotangent rules (boonta/algorithms/ppo.py:155-157)
- * as the per-layer launches do. */
+ * as the per-layer launches do.  With Whb != NULL dY is not read: the top
+ * cotangent is the head's input cotangent dhead W_h^T (dhead [M][lddh], nh
+ * columns; Whb the head kernel's backward image from
+ * ppo_pack_bf16_operand_padded over nh_pad = 32 or 64 outputs), bit-identical
+ * to the bf16 head GEMM's. */
 int ppo_mlp16_ln_bwd_blocks(int rows);
 int ppo_mlp16_ln_bwd(void* stream, int L, const float* dY, int64_t lddy, int M, const void* const* Wb,
                      const float* const* Z, const float* const* mean, const float* const* rstd,
                      const float* const* gamma, const float* const* beta, void* const* dZ16, int64_t ld,
-                     float* const* part, int act);
+                     float* const* part, int act, const float* dhead, int64_t lddh, const void* Whb, int nh,
+                     int nh_pad);
 /* Packs L bf16 kernels W[l] ([K][N], row pitch ldw; the bf16 parameter
  * image) into the MFMA operand images of the bf16 chains: fwd[l] for the
  * contraction over K, bwd[l] (W^T) for the input cotangent's contraction over
@@ -283,10 +288,12 @@ int ppo_mlp16_ln_bwd(void* stream, int L, const float* dY, int64_t lddy, int M, 
  * (l >> 5) + i][32 nb + (l & 31)] of B = W [K][N] (fwd) or W^T [N][K] (bwd). */
 int ppo_pack_bf16_operands(void* stream, int L, const void* const* W, int64_t ldw, int K, int N,
                            void* const* fwd, void* const* bwd);
-/* The forward operand image of one bf16 kernel [K][N] (row pitch ldw) padded
- * with zero columns to n_pad (a multiple of 32 >= N): a head narrower than
- * the 32-column MFMA blocks. */
-int ppo_pack_bf16_operand_padded(void* stream, const void* W, int64_t ldw, int K, int N, int n_pad, void* fwd);
+/* The operand images of one bf16 kernel [K][N] (row pitch ldw) padded with
+ * zeros to n_pad (a multiple of 32 >= N) outputs: a head narrower than the
+ * 32-column MFMA blocks.  fwd: the forward operand; bwd (may be NULL): W^T,
+ * the operand of the input cotangent's contraction over the n_pad outputs. */
+int ppo_pack_bf16_operand_padded(void* stream, const void* W, int64_t ldw, int K, int N, int n_pad, void* fwd,
+                                 void* bwd);
 
 /* ------------------------------------------------------- linear scan
  * Replace boonta's linear-recurrence scan and its custom VJP

@@ -140,7 +140,7 @@ def chain(part, S, M, lay, act, eps=1e-6, y32=None, head=None):
         W16h, bh, nh = head
         npad = (nh + 31) // 32 * 32
         hpk = torch.zeros(F * npad, dtype=torch.int16, device=DEV)
-        _lib.call("ppo_pack_bf16_operand_padded", st(), W16h.data_ptr(), nh, F, nh, npad, hpk.data_ptr())
+        _lib.call("ppo_pack_bf16_operand_padded", st(), W16h.data_ptr(), nh, F, nh, npad, hpk.data_ptr(), None)
         out[-1]["head"] = torch.full((M, nh), 7.0, device=DEV)
         keep.append(hpk)
         hargs = (hpk.data_ptr(), bh.data_ptr(), nh, out[-1]["head"].data_ptr(), nh)
@@ -246,7 +246,9 @@ def bwd_per_layer(lay, fwd, dY, M, act):
     return out
 
 
-def bwd_chain(lay, fwd, dY, M, act):
+def bwd_chain(lay, fwd, dY, M, act, head=None):
+    """The backward chain launch; head = (dhead [M][nh], W16 [512][nh], nh)
+    replaces dY by the head's input cotangent."""
     L = len(lay)
     nb = _lib.load().ppo_mlp16_ln_bwd_blocks(M)
     keep = []
@@ -265,8 +267,19 @@ def bwd_chain(lay, fwd, dY, M, act):
         a, p = ptrs(src)
         keep.append(a)
         tabs[k] = p
-    _lib.call("ppo_mlp16_ln_bwd", st(), L, dY.data_ptr(), F, M, tabs["Wb"], tabs["Z"], tabs["mean"], tabs["rstd"],
-              tabs["g"], tabs["be"], tabs["dZ16"], F, tabs["part"], act)
+    hargs = (None, 0, None, 0, 0)
+    dy_ptr = dY.data_ptr() if dY is not None else None
+    if head is not None:
+        dhead, W16h, nh = head
+        npad = (nh + 31) // 32 * 32
+        hpk = torch.zeros(2, F * npad, dtype=torch.int16, device=DEV)
+        _lib.call("ppo_pack_bf16_operand_padded", st(), W16h.data_ptr(), nh, F, nh, npad, hpk[0].data_ptr(),
+                  hpk[1].data_ptr())
+        keep.append(hpk)
+        hargs = (dhead.data_ptr(), nh, hpk[1].data_ptr(), nh, npad)
+        dy_ptr = None
+    _lib.call("ppo_mlp16_ln_bwd", st(), L, dy_ptr, F, M, tabs["Wb"], tabs["Z"], tabs["mean"], tabs["rstd"],
+              tabs["g"], tabs["be"], tabs["dZ16"], F, tabs["part"], act, *hargs)
     torch.cuda.synchronize()
     return out
 
@@ -288,6 +301,26 @@ def test_backward_chain_matches_per_layer_launches(M, L, act):
         r = ref[l]["part"].double().sum(0).cpu().numpy()
         scale = ref[l]["part"].double().abs().sum(0).cpu().numpy() + 1e-30
         assert np.all(np.abs(g - r) <= 1e-5 * scale), (l, np.max(np.abs(g - r) / scale))
+
+
+@pytest.mark.parametrize("M,L,nh", [(8192, 3, 44), (50, 2, 44), (64, 1, 8), (96, 3, 64)])
+def test_backward_chain_head_cotangent_matches_the_head_gemm(M, L, nh):
+    """The top cotangent from the head (the bf16 head GEMM's dhead W^T,
+    rounded) then the chain: dZ16 of every layer bit for bit against the head
+    GEMM followed by the per-layer launches."""
+    print(f"backward chain head case M={M} L={L} nh={nh}", flush=True)
+    lay, fwd, _ = bwd_inputs(M, L, 1, seed=M + nh)
+    torch.manual_seed(nh)
+    dhead = torch.randn(M, nh, device=DEV) * 0.01
+    W16h = bits16(torch.randn(F, nh, device=DEV) * 0.05)
+    Wf = W16h.view(torch.bfloat16).float().contiguous()
+    dY = torch.zeros(M, F, device=DEV)
+    _lib.call("ppo_gemm_bf16", st(), 0, 1, dhead.data_ptr(), nh, None, Wf.data_ptr(), nh, dY.data_ptr(), F, M, F, nh,
+              1, 0, 0, None, 0, 1, None, 0, None, -1)
+    ref = bwd_per_layer(lay, fwd, dY, M, 1)
+    got = bwd_chain(lay, fwd, None, M, 1, head=(dhead, W16h, nh))
+    for l in range(L):
+        assert torch.equal(got[l]["dZ16"], ref[l]["dZ16"]), (l, (got[l]["dZ16"] != ref[l]["dZ16"]).sum().item())
 
 
 def run_update(monkeypatch, chain16, bwd=True):
