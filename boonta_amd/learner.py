@@ -440,6 +440,7 @@ class ForwardChain:
     # off, each layer has its own launches.
     CHAIN16 = True
     CHAIN16_BWD = True
+    DW16_SIDE = True  # the chain group's later weight gradients beside the first layer's, on the side stream
 
     def _plan_chain16(self, group):
         """Pointer tables of the bf16 chain over ``group`` when it fits the
@@ -992,6 +993,9 @@ class MLPExecutor(ForwardChain):
                   else (None, 0, None, 0, 0))
             self._call("ppo_mlp16_ln_bwd", st, c["L"], _p(top.dY), top.spec.ld, self.mb, c["Wb"], c["Z"],
                        c["mean"], c["rstd"], c["g"], c["be"], c["dZ16"], top.spec.ld, c["part"], c["act"], *hd)
+            # the first layer's dW fills 198 of the 256 CUs: the later layers'
+            # run beside it on the side stream
+            s2 = self._fork(st) if self.DW16_SIDE else st
             for i in range(len(layers) - 1, -1, -1):
                 lb = layers[i]
                 s, d = lb.spec, lb.spec.dense
@@ -1000,9 +1004,10 @@ class MLPExecutor(ForwardChain):
                                _p(lb.dZ16), s.ld, _p(lb.wpart), s.ld, d.fin, s.ld, self.mb, lb.splits, d.fin * s.ld,
                                EPI_STORE, None, 0, 0, None, 0, _p(lb.bpart), self.DW16_TILE)
                 else:
-                    self._call("ppo_gemm_bf16s", st, A_COL, B_KN, 1, 1, _p(layers[i - 1].Y16), layers[i - 1].spec.ld,
+                    self._call("ppo_gemm_bf16s", s2, A_COL, B_KN, 1, 1, _p(layers[i - 1].Y16), layers[i - 1].spec.ld,
                                None, _p(lb.dZ16), s.ld, _p(lb.wpart), s.ld, d.fin, s.ld, self.mb, lb.splits,
                                d.fin * s.ld, EPI_STORE, None, 0, 0, None, 0, _p(lb.bpart), -1)
+            self._join(st, s2)
             return
         for i in range(len(layers) - 1, -1, -1):
             lb = layers[i]
