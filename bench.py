@@ -154,21 +154,26 @@ def _single_launch_work(name, args):
         weights = 256 * 256 * (L - 1) + 2 * 256 * L
         return towers * 2.0 * M * 256 * 256 * (L - 1), towers * 4.0 * (M * 256 + weights + M * L * (2 * 256 + 2))
     if name == "ppo_mlp16_ln_fwd":
-        # split partials in; per layer Z (fp32), Y16, mean, rstd out, the top layer's Y; bf16 kernels;
-        # with the head, its outputs
+        # split partials in; per layer Z (fp32, or bf16 with z16), Y16, mean, rstd out, the top layer's Y;
+        # bf16 kernels; with the head, its outputs
         L, nsplit, M = args[1], args[5], args[6]
         nh = args[21] if len(args) > 21 and args[19] else 0
+        zb = 2.0 if len(args) > 24 and args[24] else 4.0
         return (2.0 * M * 512 * (512 * (L - 1) + nh),
-                4.0 * M * 512 * nsplit + 2.0 * 512 * (512 * (L - 1) + nh) + M * L * (6.0 * 512 + 8) + 4.0 * M * 512
-                + 4.0 * M * nh)
+                4.0 * M * 512 * nsplit + 2.0 * 512 * (512 * (L - 1) + nh) + M * L * ((zb + 2.0) * 512 + 8)
+                + 4.0 * M * 512 + 4.0 * M * nh)
     if name == "ppo_pack_bf16_operand_padded":
         K, n_pad = args[3], args[5]
         return 0.0, 4.0 * K * n_pad
     if name == "ppo_mlp16_ln_bwd":
-        # top cotangent and per layer Z, mean, rstd in; dZ16 and the 32-row gradient sums out; bf16 kernels
+        # top cotangent (or the head's output cotangents) and per layer Z (fp32, or bf16 with z16), mean,
+        # rstd in; dZ16 and the 32-row gradient sums out; bf16 kernels
         L, M = args[1], args[4]
-        return (2.0 * M * 512 * 512 * (L - 1),
-                4.0 * M * 512 + M * L * (4.0 * 512 + 8 + 2.0 * 512) + L * ((M + 31) // 32) * 4096.0
+        nh = args[18] if len(args) > 18 and args[17] else 0
+        zb = 2.0 if len(args) > 20 and args[20] else 4.0
+        top = 4.0 * M * nh + 2.0 * 512 * (nh + 31) // 32 * 32 if nh else 4.0 * M * 512
+        return (2.0 * M * 512 * (512 * (L - 1) + (nh + 31) // 32 * 32),
+                top + M * L * (zb * 512 + 8 + 2.0 * 512) + L * ((M + 31) // 32) * 4096.0
                 + 2.0 * 512 * 512 * (L - 1))
     if name == "ppo_pack_bf16_operands":
         L, K, N = args[1], args[4], args[5]

@@ -99,6 +99,7 @@ struct Fwd16Args {
   int nsplit, M, L;
   float eps;
   int64_t ld;                        // row pitch of Z, Y and Y16
+  int z16;                           // Z[l] holds bf16 (the pre-activations are bf16 numbers), else fp32
   const uint16_t* Wp[C16_MAXL];      // layer l >= 1: packed forward operand image of its kernel
   const float* bias[C16_MAXL];       // may be null
   const float* gamma[C16_MAXL];
@@ -153,6 +154,22 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_fwd_kernel(Fwd16Args 
       const int grow = m0 + r0 + rr;
       const floatx4 v = *reinterpret_cast<const floatx4*>(tile + (r0 + rr) * Z_PITCH + 4 * c4);
       if (grow < a.M) *reinterpret_cast<floatx4*>(dst + (int64_t)grow * a.ld + 4 * c4) = v;
+    }
+  };
+  // The same rows as bf16 (values that are bf16 numbers), 16 bytes per lane.
+  auto rows_out_bf16 = [&](uint16_t* dst, const float* tile) {
+#pragma unroll
+    for (int i = 0; i < RPW * C16_F / 512; ++i) {
+      const int c = 64 * i + lane, rr = c >> 6, c8 = c & 63;
+      const int grow = m0 + r0 + rr;
+      const floatx4 u = *reinterpret_cast<const floatx4*>(tile + (r0 + rr) * Z_PITCH + 8 * c8);
+      const floatx4 v = *reinterpret_cast<const floatx4*>(tile + (r0 + rr) * Z_PITCH + 8 * c8 + 4);
+      uint4 q;
+      q.x = ppo::bf16_bits(u[0]) | (ppo::bf16_bits(u[1]) << 16);
+      q.y = ppo::bf16_bits(u[2]) | (ppo::bf16_bits(u[3]) << 16);
+      q.z = ppo::bf16_bits(v[0]) | (ppo::bf16_bits(v[1]) << 16);
+      q.w = ppo::bf16_bits(v[2]) | (ppo::bf16_bits(v[3]) << 16);
+      if (grow < a.M) *reinterpret_cast<uint4*>(dst + (int64_t)grow * a.ld + 8 * c8) = q;
     }
   };
   // LayerNorm + activation of the wave's rows from their pre-activations in
@@ -244,7 +261,16 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_fwd_kernel(Fwd16Args 
         }
         const int grow = m0 + r0 + rr;
         *reinterpret_cast<floatx4*>(sZ + (r0 + rr) * Z_PITCH + 4 * c4) = v;
-        if (grow < a.M) *reinterpret_cast<floatx4*>(a.Z[0] + (int64_t)grow * a.ld + 4 * c4) = v;
+        if (grow < a.M) {
+          if (a.z16) {
+            uint2 q;
+            q.x = ppo::bf16_bits(v[0]) | (ppo::bf16_bits(v[1]) << 16);
+            q.y = ppo::bf16_bits(v[2]) | (ppo::bf16_bits(v[3]) << 16);
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.Z[0]) + (int64_t)grow * a.ld + 4 * c4) = q;
+          } else {
+            *reinterpret_cast<floatx4*>(a.Z[0] + (int64_t)grow * a.ld + 4 * c4) = v;
+          }
+        }
       }
     }
     ln_rows(0);
@@ -297,7 +323,10 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_fwd_kernel(Fwd16Args 
       }
     }
     __syncthreads();  // every wave's columns are in sZ; sA is free
-    rows_out_f32(a.Z[l], sZ);
+    if (a.z16)
+      rows_out_bf16(reinterpret_cast<uint16_t*>(a.Z[l]), sZ);
+    else
+      rows_out_f32(a.Z[l], sZ);
     ln_rows(l);
   }
 
@@ -347,6 +376,7 @@ struct Bwd16Args {
   int64_t lddy;
   int M, L;
   int64_t ld;                        // row pitch of Z and dZ16
+  int z16;                           // Z[l] holds bf16, else fp32
   const uint16_t* Wb[C16_MAXL];      // layer l >= 1: packed backward operand image of its kernel
   const float* Z[C16_MAXL];
   const float* mean[C16_MAXL];
@@ -407,8 +437,14 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_bwd_kernel(Bwd16Args 
       const int64_t gc = grow < a.M ? grow : a.M - 1;
       mu[j] = a.mean[l][gc];
       rs[j] = a.rstd[l][gc];
+      if (a.z16) {
+        const uint16_t* z = reinterpret_cast<const uint16_t*>(a.Z[l]) + gc * a.ld + lane;
 #pragma unroll
-      for (int e = 0; e < VPL; ++e) zv[j][e] = a.Z[l][gc * a.ld + lane + 64 * e];
+        for (int e = 0; e < VPL; ++e) zv[j][e] = __uint_as_float((uint32_t)z[64 * e] << 16);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VPL; ++e) zv[j][e] = a.Z[l][gc * a.ld + lane + 64 * e];
+      }
     }
   };
 
@@ -629,7 +665,8 @@ PPO_EXPORT int ppo_pack_bf16_operand_padded(void* stream, const void* W, int64_t
 // partials: layer 0's split sum, bias, LayerNorm and activation, then layers
 // 1 .. L-1 (512 x 512 kernels, packed forward operands Wp[l]), each with its
 // bias, LayerNorm and activation.  Writes Z, Y16, mean, rstd of every layer
-// and Y where Y[l] is non-null; with Wh non-null also the head on the last
+// and Y where Y[l] is non-null (Z as bf16 when z16: its values are bf16
+// numbers); with Wh non-null also the head on the last
 // layer's output (nh outputs, Wh its packed forward operand image of
 // 32 ceil(nh / 32) columns, bias bh) into head [M][ldh].
 PPO_EXPORT int ppo_mlp16_ln_fwd(void* stream, int L, const float* part, int64_t ldp, int64_t part_stride,
@@ -637,7 +674,7 @@ PPO_EXPORT int ppo_mlp16_ln_fwd(void* stream, int L, const float* part, int64_t 
                                 const float* const* gamma, const float* const* beta, float* const* Z,
                                 float* const* Y, void* const* Y16, int64_t ld, float* const* mean,
                                 float* const* rstd, float eps, int act, const void* Wh, const float* bh, int nh,
-                                float* head, int64_t ldh) {
+                                float* head, int64_t ldh, int z16) {
   if (Wh && (nh < 1 || nh > 32 * C16_WAVES || !head || ldh < nh || !aligned16(Wh)))
     return ppo::set_error(PPO_ERR_ARG, "ppo_mlp16_ln_fwd: bad head (nh=%d ldh=%lld)", nh, (long long)ldh);
   if (L < 1 || L > C16_MAXL || M < 0 || nsplit < 1 || act < 0 || act > 3 || !part || !aligned16(part) ||
@@ -647,7 +684,7 @@ PPO_EXPORT int ppo_mlp16_ln_fwd(void* stream, int L, const float* part, int64_t 
   if (M == 0) return PPO_OK;
   Fwd16Args a{};
   a.part = part; a.ldp = ldp; a.pstride = part_stride; a.nsplit = nsplit; a.M = M; a.L = L; a.eps = eps;
-  a.ld = ld;
+  a.ld = ld; a.z16 = z16 != 0;
   a.Wh = static_cast<const uint16_t*>(Wh); a.bh = bh; a.head = head; a.ldh = ldh; a.nh = nh;
   for (int l = 0; l < L; ++l) {
     if (!gamma[l] || !beta[l] || !Z[l] || !Y16[l] || !mean[l] || !rstd[l] || !aligned16(Z[l]) ||
@@ -681,11 +718,12 @@ PPO_EXPORT int ppo_mlp16_ln_bwd_blocks(int rows) { return rows > 0 ? ppo::ceil_d
 // dhead W_h^T from the head's output cotangents dhead [M][lddh] (nh columns)
 // and Whb, the head kernel's packed backward image over nh_pad (32 or 64)
 // outputs (ppo_pack_bf16_operand_padded), as the bf16 head GEMM rounds it.
+// z16: Z[l] holds the forward's bf16 Z.
 PPO_EXPORT int ppo_mlp16_ln_bwd(void* stream, int L, const float* dY, int64_t lddy, int M, const void* const* Wb,
                                 const float* const* Z, const float* const* mean, const float* const* rstd,
                                 const float* const* gamma, const float* const* beta, void* const* dZ16, int64_t ld,
                                 float* const* part, int act, const float* dhead, int64_t lddh, const void* Whb,
-                                int nh, int nh_pad) {
+                                int nh, int nh_pad, int z16) {
   if (Whb && (!dhead || nh < 1 || lddh < nh || nh_pad < nh || nh_pad % 32 || nh_pad > 64 || !aligned16(Whb)))
     return ppo::set_error(PPO_ERR_ARG, "ppo_mlp16_ln_bwd: bad head (nh=%d nh_pad=%d)", nh, nh_pad);
   if (L < 1 || L > C16_MAXL || M < 0 || act < 0 || act > 3 || (!Whb && (!dY || !aligned16(dY) || lddy < C16_F ||
@@ -694,7 +732,7 @@ PPO_EXPORT int ppo_mlp16_ln_bwd(void* stream, int L, const float* dY, int64_t ld
     return ppo::set_error(PPO_ERR_ARG, "ppo_mlp16_ln_bwd: bad argument (L=%d M=%d)", L, M);
   if (M == 0) return PPO_OK;
   Bwd16Args a{};
-  a.dY = dY; a.lddy = lddy; a.M = M; a.L = L; a.ld = ld;
+  a.dY = dY; a.lddy = lddy; a.M = M; a.L = L; a.ld = ld; a.z16 = z16 != 0;
   a.dhead = dhead; a.lddh = lddh; a.Whb = static_cast<const uint16_t*>(Whb); a.nh = nh; a.nhk = nh_pad / 16;
   for (int l = 0; l < L; ++l) {
     if (!Z[l] || !mean[l] || !rstd[l] || !gamma[l] || !beta[l] || !dZ16[l] || !part[l] || !aligned16(dZ16[l]) ||

@@ -470,6 +470,8 @@ class ForwardChain:
                 if lb.lnpart.shape[0] < blocks:
                     lb.lnpart = torch.zeros(blocks, 2 * lb.spec.fout, dtype=torch.float32, device=self.P16.device)
                 lb.lnblocks = blocks
+        # with both chains, Z goes between them as bf16 (its values are bf16 numbers)
+        z16 = [torch.zeros(self.mb, 512, dtype=torch.int16, device=self.P16.device) for _ in group] if bwd else None
         T = {"Wp": arr([None] + [_p(pk[l - 1, 0]) for l in range(1, L)]),
              "Wb": arr([None] + [_p(pk[l - 1, 1]) if bwd else None for l in range(1, L)]),
              "dZ16": arr([_p(lb.dZ16) for lb in group]),
@@ -477,14 +479,15 @@ class ForwardChain:
              "b": arr([view(lb.spec.dense.b) for lb in group]),
              "g": arr([view(lb.spec.ln["scale"]) for lb in group]),
              "be": arr([view(lb.spec.ln["bias"]) for lb in group]),
-             "Z": arr([_p(lb.Z) for lb in group]),
+             "Z": arr([_p(z) for z in z16] if bwd else [_p(lb.Z) for lb in group]),
              "Y": arr([None if lb.y32_unused else _p(lb.Y) for lb in group]),
              "Y16": arr([_p(lb.Y16) for lb in group]),
              "mean": arr([_p(lb.mean) for lb in group]),
              "rstd": arr([_p(lb.rstd) for lb in group])}
         addr = lambda a: ctypes.cast(a, ctypes.c_void_p).value
         c = {k: addr(v) for k, v in T.items()}
-        c.update(keep=T, packed=pk, L=L, act=_act(s0.act), eps=float(s0.ln["eps"]), bwd=bwd)
+        c.update(keep=T, packed=pk, L=L, act=_act(s0.act), eps=float(s0.ln["eps"]), bwd=bwd, z16=int(bwd),
+                 z16_bufs=z16)
         group[0].chain16 = c
         if L > 1:
             W = arr([self._view16(lb.spec.dense.w) for lb in group[1:]])
@@ -545,7 +548,7 @@ class ForwardChain:
                     self._call("ppo_mlp16_ln_fwd", st, c["L"], _p(lb.fpart), s.ld, nrows * s.ld,
                                self.FWD16_SPLITS, nrows, c["Wp"], c["b"], c["g"], c["be"], c["Z"], c["Y"],
                                c["Y16"], s.ld, c["mean"], c["rstd"], c["eps"], c["act"], c.get("Wh"), c.get("bh"),
-                               c.get("nh", 0), c.get("head"), c.get("ldh", 0))
+                               c.get("nh", 0), c.get("head"), c.get("ldh", 0), c["z16"])
                     top = layers[-1]
                     return _p(top.Y), top.spec.ld, None
                 self._call("ppo_splits_bias_act_bf16", st, _p(lb.fpart), s.ld, nrows * s.ld, self.FWD16_SPLITS, Bb,
@@ -992,7 +995,8 @@ class MLPExecutor(ForwardChain):
             hd = ((_p(self.DHEAD), h.w.ld, c["Whb"], h.w.ld, c["head_npad"]) if c.get("Whb")
                   else (None, 0, None, 0, 0))
             self._call("ppo_mlp16_ln_bwd", st, c["L"], _p(top.dY), top.spec.ld, self.mb, c["Wb"], c["Z"],
-                       c["mean"], c["rstd"], c["g"], c["be"], c["dZ16"], top.spec.ld, c["part"], c["act"], *hd)
+                       c["mean"], c["rstd"], c["g"], c["be"], c["dZ16"], top.spec.ld, c["part"], c["act"], *hd,
+                       c["z16"])
             # the first layer's dW fills 198 of the 256 CUs: the later layers'
             # run beside it on the side stream
             s2 = self._fork(st) if self.DW16_SIDE else st

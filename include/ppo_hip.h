@@ -253,13 +253,15 @@ int ppo_mlp_ln_bwd_f32(void* stream, int towers, int L, const float* dY, int64_t
  * shared torso; nh <= 256 outputs, bias bh, written rounded into head
  * [M][ldh]), bit-identical to ppo_gemm_bf16 with the bias epilogue; Wh is
  * the head kernel's forward operand image from
- * ppo_pack_bf16_operand_padded (n_pad = 32 ceil(nh / 32)). */
+ * ppo_pack_bf16_operand_padded (n_pad = 32 ceil(nh / 32)).  z16 != 0: Z[l]
+ * receives Z as bf16 (uint16 bit patterns; its values are bf16 numbers, so
+ * nothing is lost), the form ppo_mlp16_ln_bwd reads with its z16. */
 int ppo_mlp16_max_layers(void);
 int ppo_mlp16_ln_fwd(void* stream, int L, const float* part, int64_t ldp, int64_t part_stride, int nsplit, int M,
                      const void* const* Wp, const float* const* bias, const float* const* gamma,
                      const float* const* beta, float* const* Z, float* const* Y, void* const* Y16, int64_t ld,
                      float* const* mean, float* const* rstd, float eps, int act, const void* Wh, const float* bh,
-                     int nh, float* head, int64_t ldh);
+                     int nh, float* head, int64_t ldh, int z16);
 /* Backward of the same chain from dY, the cotangent of the top layer's
  * output (fp32, row pitch lddy): per layer from the top, the LayerNorm +
  * activation backward (dZ16[l], bf16, row pitch ld, bit-identical to
@@ -273,13 +275,14 @@ int ppo_mlp16_ln_fwd(void* stream, int L, const float* part, int64_t ldp, int64_
  * cotangent is the head's input cotangent dhead W_h^T (dhead [M][lddh], nh
  * columns; Whb the head kernel's backward image from
  * ppo_pack_bf16_operand_padded over nh_pad = 32 or 64 outputs), bit-identical
- * to the bf16 head GEMM's. */
+ * to the bf16 head GEMM's.  z16 != 0: Z[l] holds bf16 (ppo_mlp16_ln_fwd's z16
+ * output). */
 int ppo_mlp16_ln_bwd_blocks(int rows);
 int ppo_mlp16_ln_bwd(void* stream, int L, const float* dY, int64_t lddy, int M, const void* const* Wb,
                      const float* const* Z, const float* const* mean, const float* const* rstd,
                      const float* const* gamma, const float* const* beta, void* const* dZ16, int64_t ld,
                      float* const* part, int act, const float* dhead, int64_t lddh, const void* Whb, int nh,
-                     int nh_pad);
+                     int nh_pad, int z16);
 /* Packs L bf16 kernels W[l] ([K][N], row pitch ldw; the bf16 parameter
  * image) into the MFMA operand images of the bf16 chains: fwd[l] for the
  * contraction over K, bwd[l] (W^T) for the input cotangent's contraction over

@@ -112,7 +112,7 @@ def per_layer(part, S, M, lay, act, eps=1e-6):
     return out
 
 
-def chain(part, S, M, lay, act, eps=1e-6, y32=None, head=None):
+def chain(part, S, M, lay, act, eps=1e-6, y32=None, head=None, z16=False):
     """The chain launch; head = (W16 [512][nh], bias [nh], nh) adds the head
     stage, whose outputs come back as out[-1]["head"]."""
     L = len(lay)
@@ -123,7 +123,8 @@ def chain(part, S, M, lay, act, eps=1e-6, y32=None, head=None):
         fa, fp = ptrs(pk[1:])
         keep += [wa, fa]
         _lib.call("ppo_pack_bf16_operands", st(), L - 1, wp, F, F, F, fp, None)
-    out = [dict(Z=torch.full((M, F), 7.0, device=DEV), Y=torch.full((M, F), 7.0, device=DEV),
+    out = [dict(Z=(torch.full((M, F), 7, dtype=torch.int16, device=DEV) if z16 else torch.full((M, F), 7.0, device=DEV)),
+                Y=torch.full((M, F), 7.0, device=DEV),
                 Y16=torch.full((M, F), 7, dtype=torch.int16, device=DEV), mean=torch.full((M,), 7.0, device=DEV),
                 rstd=torch.full((M,), 7.0, device=DEV)) for _ in range(L)]
     y32 = [True] * L if y32 is None else y32
@@ -145,7 +146,8 @@ def chain(part, S, M, lay, act, eps=1e-6, y32=None, head=None):
         keep.append(hpk)
         hargs = (hpk.data_ptr(), bh.data_ptr(), nh, out[-1]["head"].data_ptr(), nh)
     _lib.call("ppo_mlp16_ln_fwd", st(), L, part.data_ptr(), F, M * F, S, M, tabs["Wp"], tabs["b"], tabs["g"],
-              tabs["be"], tabs["Z"], tabs["Y"], tabs["Y16"], F, tabs["mean"], tabs["rstd"], eps, act, *hargs)
+              tabs["be"], tabs["Z"], tabs["Y"], tabs["Y16"], F, tabs["mean"], tabs["rstd"], eps, act, *hargs,
+              int(z16))
     torch.cuda.synchronize()
     return out
 
@@ -186,6 +188,28 @@ def test_chain_head_is_bit_identical_to_the_head_gemm(M, L, nh):
         assert torch.equal(got[-1][k], ref[-1][k])
 
 
+@pytest.mark.parametrize("M,L", [(8192, 3), (50, 2)])
+def test_chain_bf16_z_is_the_fp32_z_rounded_and_feeds_the_backward_alike(M, L):
+    """Z as bf16 (z16): the bit patterns of the fp32 Z (bf16 numbers, so
+    exact), every other output unchanged; the backward chain reading it gives
+    the same dZ16 and gradient sums as from the fp32 Z."""
+    torch.manual_seed(M)
+    part = torch.randn(2, M, F, device=DEV) * 1.5
+    lay = make_layers(L, seed=M + 9)
+    f32 = chain(part, 2, M, lay, 1)
+    b16 = chain(part, 2, M, lay, 1, z16=True)
+    for l in range(L):
+        assert torch.equal(f32[l]["Z"], bits16(f32[l]["Z"]).view(torch.bfloat16).float())
+        assert torch.equal(b16[l]["Z"], bits16(f32[l]["Z"]))
+        for k in ("Y", "Y16", "mean", "rstd"):
+            assert torch.equal(b16[l][k], f32[l][k])
+    dY = torch.randn(M, F, device=DEV)
+    r32 = bwd_chain(lay, f32, dY, M, 1)
+    r16 = bwd_chain(lay, f32, dY, M, 1, z16=True)
+    for l in range(L):
+        assert torch.equal(r16[l]["dZ16"], r32[l]["dZ16"]) and torch.equal(r16[l]["part"], r32[l]["part"])
+
+
 def test_chain_without_fp32_outputs_leaves_them_untouched():
     M, L = 64, 3
     part = torch.randn(2, M, F, device=DEV)
@@ -204,12 +228,12 @@ def test_chain_rejects_bad_arguments():
     # a later layer without its packed operand image
     with pytest.raises(_lib.KernelError, match="ppo_mlp16_ln_fwd"):
         _lib.call("ppo_mlp16_ln_fwd", st(), 2, part.data_ptr(), F, 32 * F, 2, 32, p, p, p, p, p, p, p, F, p, p,
-                  1e-6, 1, None, None, 0, None, 0)
+                  1e-6, 1, None, None, 0, None, 0, 0)
     # a head of more outputs than the eight waves' column blocks
     hp = torch.zeros(F * 288, dtype=torch.int16, device=DEV)
     with pytest.raises(_lib.KernelError, match="bad head"):
         _lib.call("ppo_mlp16_ln_fwd", st(), 1, part.data_ptr(), F, 32 * F, 2, 32, p, p, p, p, p, p, p, F, p, p,
-                  1e-6, 1, hp.data_ptr(), None, 288, part.data_ptr(), 288)
+                  1e-6, 1, hp.data_ptr(), None, 288, part.data_ptr(), 288, 0)
     # K not a multiple of 32
     with pytest.raises(_lib.KernelError, match="ppo_pack_bf16_operands"):
         _lib.call("ppo_pack_bf16_operands", st(), 1, p, F, 500, F, p, p)
@@ -246,7 +270,7 @@ def bwd_per_layer(lay, fwd, dY, M, act):
     return out
 
 
-def bwd_chain(lay, fwd, dY, M, act, head=None):
+def bwd_chain(lay, fwd, dY, M, act, head=None, z16=False):
     """The backward chain launch; head = (dhead [M][nh], W16 [512][nh], nh)
     replaces dY by the head's input cotangent."""
     L = len(lay)
@@ -261,7 +285,9 @@ def bwd_chain(lay, fwd, dY, M, act, head=None):
     out = [dict(dZ16=torch.full((M, F), 7, dtype=torch.int16, device=DEV), part=torch.zeros(nb, 2 * F, device=DEV))
            for _ in range(L)]
     tabs = {}
-    for k, src in (("Wb", pb), ("Z", [f["Z"] for f in fwd]), ("mean", [f["mean"] for f in fwd]),
+    zs = [bits16(f["Z"]) for f in fwd] if z16 else [f["Z"] for f in fwd]
+    keep += zs
+    for k, src in (("Wb", pb), ("Z", zs), ("mean", [f["mean"] for f in fwd]),
                    ("rstd", [f["rstd"] for f in fwd]), ("g", [p["g"] for p in lay]), ("be", [p["be"] for p in lay]),
                    ("dZ16", [o["dZ16"] for o in out]), ("part", [o["part"] for o in out])):
         a, p = ptrs(src)
@@ -279,7 +305,7 @@ def bwd_chain(lay, fwd, dY, M, act, head=None):
         hargs = (dhead.data_ptr(), nh, hpk[1].data_ptr(), nh, npad)
         dy_ptr = None
     _lib.call("ppo_mlp16_ln_bwd", st(), L, dy_ptr, F, M, tabs["Wb"], tabs["Z"], tabs["mean"], tabs["rstd"],
-              tabs["g"], tabs["be"], tabs["dZ16"], F, tabs["part"], act, *hargs)
+              tabs["g"], tabs["be"], tabs["dZ16"], F, tabs["part"], act, *hargs, int(z16))
     torch.cuda.synchronize()
     return out
 
