@@ -170,9 +170,10 @@ def _single_launch_work(name, args):
         # rstd in; dZ16 and the 32-row gradient sums out; bf16 kernels
         L, M = args[1], args[4]
         nh = args[18] if len(args) > 18 and args[17] else 0
+        pad = (nh + 31) // 32 * 32
         zb = 2.0 if len(args) > 20 and args[20] else 4.0
-        top = 4.0 * M * nh + 2.0 * 512 * (nh + 31) // 32 * 32 if nh else 4.0 * M * 512
-        return (2.0 * M * 512 * (512 * (L - 1) + (nh + 31) // 32 * 32),
+        top = (4.0 * M * nh + 2.0 * 512 * pad) if nh else 4.0 * M * 512
+        return (2.0 * M * 512 * (512 * (L - 1) + pad),
                 top + M * L * (zb * 512 + 8 + 2.0 * 512) + L * ((M + 31) // 32) * 4096.0
                 + 2.0 * 512 * 512 * (L - 1))
     if name == "ppo_pack_bf16_operands":
