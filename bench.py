@@ -178,7 +178,8 @@ def _single_launch_work(name, args):
                 + 2.0 * 512 * 512 * (L - 1))
     if name == "ppo_pack_bf16_operands":
         L, K, N = args[1], args[4], args[5]
-        return 0.0, 4.0 * L * K * N
+        head = 8.0 * K * args[11] if len(args) > 11 and args[8] else 0.0
+        return 0.0, 4.0 * L * K * N + head
     if name == "ppo_gru_fwd_seq_f32":
         Bm, H, T = args[-6], args[-5], args[-4]
         return 2.0 * Bm * H * 3 * H * T, 4.0 * T * Bm * (3 * H + H + H + 4 * H) + 4.0 * H * 3 * H

@@ -59,7 +59,7 @@ SIGNATURES = {
                                            I64, I64, I64, I64]),
     "ppo_mlp16_max_layers": (I, []),
     "ppo_mlp16_ln_fwd": (I, [P, I, P, I64, I64, I, I, P, P, P, P, P, P, P, I64, P, P, F, I, P, P, I, P, I64, I]),
-    "ppo_pack_bf16_operands": (I, [P, I, P, I64, I, I, P, P]),
+    "ppo_pack_bf16_operands": (I, [P, I, P, I64, I, I, P, P, P, I64, I, I, P, P]),
     "ppo_pack_bf16_operand_padded": (I, [P, P, I64, I, I, I, P, P]),
     "ppo_mlp16_ln_bwd_blocks": (I, [I]),
     "ppo_mlp16_ln_bwd": (I, [P, I, P, I64, I, P, P, P, P, P, P, P, I64, P, I, P, I64, P, I, I, I]),

@@ -54,13 +54,13 @@ static_assert(C16_KSTEPS % PF == 0, "the operand ring must divide the k steps");
 // element i, B[16 kb + 8 (l >> 5) + i][32 nb + (l & 31)] at 512 c + 8 l + i.
 // fwd: B = W (a layer's kernel [K][N], row pitch ldw); bwd: B = W^T (the input
 // cotangent dZ W^T contracts over the output features).
-struct PackArgs {
-  const uint16_t* W[C16_MAXL];
-  uint16_t* fwd[C16_MAXL];
-  uint16_t* bwd[C16_MAXL];
-  int64_t ldw;
-  int K, N;
-  int nvalid;  // kernel columns present: forward columns and backward k rows nvalid .. N - 1 pack as zeros
+struct PackArgs {  // slot l: one kernel (the chain's layers, then a head)
+  const uint16_t* W[C16_MAXL + 1];
+  uint16_t* fwd[C16_MAXL + 1];
+  uint16_t* bwd[C16_MAXL + 1];
+  int64_t ldw[C16_MAXL + 1];
+  int K[C16_MAXL + 1], N[C16_MAXL + 1];
+  int nvalid[C16_MAXL + 1];  // kernel columns present: forward columns and backward k rows nvalid .. N - 1 pack as zeros
 };
 
 __global__ void __launch_bounds__(256) pack_operands_kernel(PackArgs a) {
@@ -69,7 +69,9 @@ __global__ void __launch_bounds__(256) pack_operands_kernel(PackArgs a) {
   uint16_t* dst = bwd ? a.bwd[l] : a.fwd[l];
   const uint16_t* W = a.W[l];
   if (!dst || !W) return;
-  const int KD = bwd ? a.N : a.K, ND = bwd ? a.K : a.N;
+  const int K = a.K[l], N = a.N[l], nvalid = a.nvalid[l];
+  const int64_t ldw = a.ldw[l];
+  const int KD = bwd ? N : K, ND = bwd ? K : N;
   const int64_t units = (int64_t)KD * ND / 8;
   for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < units; u += (int64_t)gridDim.x * blockDim.x) {
     const int lane = (int)(u & 63);
@@ -77,16 +79,16 @@ __global__ void __launch_bounds__(256) pack_operands_kernel(PackArgs a) {
     const int nb = (int)(c % (ND / 32)), kb = (int)(c / (ND / 32));
     const int k0 = 16 * kb + 8 * (lane >> 5), n = 32 * nb + (lane & 31);
     uint16_t v[8];
-    if (bwd && a.nvalid == a.N && a.ldw % 8 == 0) {
+    if (bwd && nvalid == N && ldw % 8 == 0) {
       // B[k][n] = W[n][k]: eight consecutive k of kernel row n
-      const uint4 q = *reinterpret_cast<const uint4*>(W + (int64_t)n * a.ldw + k0);
+      const uint4 q = *reinterpret_cast<const uint4*>(W + (int64_t)n * ldw + k0);
       *reinterpret_cast<uint4*>(v) = q;
     } else if (bwd) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = k0 + i < a.nvalid ? W[(int64_t)n * a.ldw + k0 + i] : (uint16_t)0;
+      for (int i = 0; i < 8; ++i) v[i] = k0 + i < nvalid ? W[(int64_t)n * ldw + k0 + i] : (uint16_t)0;
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = n < a.nvalid ? W[(int64_t)(k0 + i) * a.ldw + n] : (uint16_t)0;
+      for (int i = 0; i < 8; ++i) v[i] = n < nvalid ? W[(int64_t)(k0 + i) * ldw + n] : (uint16_t)0;
     }
     *reinterpret_cast<uint4*>(dst + 8 * u) = *reinterpret_cast<const uint4*>(v);
   }
@@ -618,23 +620,37 @@ PPO_EXPORT int ppo_mlp16_max_layers() { return C16_MAXL; }
 // Packs the bf16 kernels W[l] [K][N] (row pitch ldw) of L layers into the
 // MFMA operand images the bf16 chains read: fwd[l] for the forward's
 // contraction over K, bwd[l] for the input cotangent's contraction over N
-// (each K * N bf16; a null W[l], or a null output, is skipped).
+// (each K * N bf16; a null W[l], or a null output, is skipped).  With Wh
+// non-null the same launch also packs a head kernel Wh [K][nh] (row pitch
+// ldwh) as ppo_pack_bf16_operand_padded would, into fwdh and bwdh.
 PPO_EXPORT int ppo_pack_bf16_operands(void* stream, int L, const void* const* W, int64_t ldw, int K, int N,
-                                      void* const* fwd, void* const* bwd) {
+                                      void* const* fwd, void* const* bwd, const void* Wh, int64_t ldwh, int nh,
+                                      int nh_pad, void* fwdh, void* bwdh) {
   if (L < 1 || L > C16_MAXL || K < 16 || N < 32 || K % 32 || N % 32 || ldw < N || ldw % 8 || !W)
     return ppo::set_error(PPO_ERR_ARG, "ppo_pack_bf16_operands: bad argument (L=%d K=%d N=%d ldw=%lld)", L, K, N,
                           (long long)ldw);
+  if (Wh && (!fwdh || nh < 1 || ldwh < nh || nh_pad < nh || nh_pad % 32 || !aligned16(fwdh) ||
+             (bwdh && !aligned16(bwdh))))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_pack_bf16_operands: bad head (nh=%d nh_pad=%d)", nh, nh_pad);
   PackArgs a{};
-  a.ldw = ldw; a.K = K; a.N = N; a.nvalid = N;
   for (int l = 0; l < L; ++l) {
+    a.ldw[l] = ldw; a.K[l] = K; a.N[l] = N; a.nvalid[l] = N;
     a.W[l] = static_cast<const uint16_t*>(W[l]);
     a.fwd[l] = fwd ? static_cast<uint16_t*>(fwd[l]) : nullptr;
     a.bwd[l] = bwd ? static_cast<uint16_t*>(bwd[l]) : nullptr;
     if ((a.W[l] && !aligned16(a.W[l])) || (a.fwd[l] && !aligned16(a.fwd[l])) || (a.bwd[l] && !aligned16(a.bwd[l])))
       return ppo::set_error(PPO_ERR_ARG, "ppo_pack_bf16_operands: layer %d needs 16-byte aligned buffers", l);
   }
+  int slots = L;
+  if (Wh) {  // the head rides in one more slot of the same launch
+    a.ldw[L] = ldwh; a.K[L] = K; a.N[L] = nh_pad; a.nvalid[L] = nh;
+    a.W[L] = static_cast<const uint16_t*>(Wh);
+    a.fwd[L] = static_cast<uint16_t*>(fwdh);
+    a.bwd[L] = static_cast<uint16_t*>(bwdh);
+    slots = L + 1;
+  }
   const int64_t units = (int64_t)K * N / 8;
-  const dim3 grid((unsigned)std::min<int64_t>(ppo::ceil_div64(units, 256), 1024), L, 2);
+  const dim3 grid((unsigned)std::min<int64_t>(ppo::ceil_div64(units, 256), 1024), slots, 2);
   hipLaunchKernelGGL(pack_operands_kernel, grid, dim3(256), 0, ppo::as_stream(stream), a);
   return ppo::check_launch("ppo_pack_bf16_operands");
 }
@@ -651,7 +667,7 @@ PPO_EXPORT int ppo_pack_bf16_operand_padded(void* stream, const void* W, int64_t
     return ppo::set_error(PPO_ERR_ARG, "ppo_pack_bf16_operand_padded: bad argument (K=%d N=%d n_pad=%d)", K, N,
                           n_pad);
   PackArgs a{};
-  a.ldw = ldw; a.K = K; a.N = n_pad; a.nvalid = N;
+  a.ldw[0] = ldw; a.K[0] = K; a.N[0] = n_pad; a.nvalid[0] = N;
   a.W[0] = static_cast<const uint16_t*>(W);
   a.fwd[0] = static_cast<uint16_t*>(fwd);
   a.bwd[0] = static_cast<uint16_t*>(bwd);

@@ -494,6 +494,7 @@ class ForwardChain:
             F = arr([_p(pk[l, 0]) for l in range(L - 1)])
             B = arr([_p(pk[l, 1]) for l in range(L - 1)]) if bwd else None
             self._pack16_tables.append((L - 1, addr(W), addr(F), addr(B) if bwd else None, (W, F, B)))
+            c["pack_F"] = addr(F)
 
     def _plan_chain16_head(self):
         """The shared head (heads.py:9-45) rides on the trunk chain's forward
@@ -516,11 +517,18 @@ class ForwardChain:
     def _pack16(self, st):
         """Packed operand images of the bf16 chains' kernels from the bf16
         parameter image (after each write of the image)."""
-        for n, W, F, B, _ in self._pack16_tables:
-            self._call("ppo_pack_bf16_operands", st, n, W, 512, 512, 512, F, B)
         c = self.trunk[0].chain16 if self.trunk else None
-        if c is not None and c.get("Wh"):
-            h = self.prog.head_a
+        head = c is not None and c.get("Wh")
+        h = self.prog.head_a
+        packed_head = False
+        for n, W, F, B, _ in self._pack16_tables:
+            # the trunk's head rides in the same launch
+            hargs = (None, 0, 0, 0, None, None)
+            if head and F == c.get("pack_F"):
+                hargs = (self._view16(h.w), h.w.ld, h.w.ld, c["head_npad"], c["Wh"], c.get("Whb"))
+                packed_head = True
+            self._call("ppo_pack_bf16_operands", st, n, W, 512, 512, 512, F, B, *hargs)
+        if head and not packed_head:
             self._call("ppo_pack_bf16_operand_padded", st, self._view16(h.w), h.w.ld, 512, h.w.ld, c["head_npad"],
                        c["Wh"], c.get("Whb"))
 

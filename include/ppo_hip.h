@@ -288,9 +288,13 @@ int ppo_mlp16_ln_bwd(void* stream, int L, const float* dY, int64_t lddy, int M, 
  * contraction over K, bwd[l] (W^T) for the input cotangent's contraction over
  * N; K * N bf16 each, 16-byte aligned; NULL entries are skipped.  Layout:
  * 1 KB chunk kb * (ND / 32) + nb holds, for lane l, element i, B[16 kb + 8
- * (l >> 5) + i][32 nb + (l & 31)] of B = W [K][N] (fwd) or W^T [N][K] (bwd). */
+ * (l >> 5) + i][32 nb + (l & 31)] of B = W [K][N] (fwd) or W^T [N][K] (bwd).
+ * With Wh != NULL the same launch also packs a head kernel Wh [K][nh] (row
+ * pitch ldwh) as ppo_pack_bf16_operand_padded does (into fwdh, and bwdh when
+ * not NULL). */
 int ppo_pack_bf16_operands(void* stream, int L, const void* const* W, int64_t ldw, int K, int N,
-                           void* const* fwd, void* const* bwd);
+                           void* const* fwd, void* const* bwd, const void* Wh, int64_t ldwh, int nh, int nh_pad,
+                           void* fwdh, void* bwdh);
 /* The operand images of one bf16 kernel [K][N] (row pitch ldw) padded with
  * zeros to n_pad (a multiple of 32 >= N) outputs: a head narrower than the
  * 32-column MFMA blocks.  fwd: the forward operand; bwd (may be NULL): W^T,

@@ -73,11 +73,35 @@ def test_pack_bf16_operands_layout(K, N, ldw):
     wa, wp = ptrs([W])
     fa, fp = ptrs([fwd])
     ba, bp = ptrs([bwd])
-    _lib.call("ppo_pack_bf16_operands", st(), 1, wp, ldw, K, N, fp, bp)
+    _lib.call("ppo_pack_bf16_operands", st(), 1, wp, ldw, K, N, fp, bp, None, 0, 0, 0, None, None)
     torch.cuda.synchronize()
     ef, eb = unpack_reference(W.cpu().numpy()[:, :N], K, N)
     np.testing.assert_array_equal(fwd.cpu().numpy(), ef)
     np.testing.assert_array_equal(bwd.cpu().numpy(), eb)
+
+
+def test_pack_head_slot_equals_the_padded_pack():
+    """The layers' pack launch with the head in its extra slot gives the
+    images ppo_pack_bf16_operand_padded gives."""
+    torch.manual_seed(2)
+    W = bits16(torch.randn(F, F, device=DEV))
+    Wh = bits16(torch.randn(F, 44, device=DEV))
+    f1 = torch.zeros(F * F, dtype=torch.int16, device=DEV)
+    hf = torch.zeros(F * 64, dtype=torch.int16, device=DEV)
+    hb = torch.zeros(F * 64, dtype=torch.int16, device=DEV)
+    rf = torch.zeros(F * 64, dtype=torch.int16, device=DEV)
+    rb = torch.zeros(F * 64, dtype=torch.int16, device=DEV)
+    wa, wp = ptrs([W])
+    fa, fp = ptrs([f1])
+    _lib.call("ppo_pack_bf16_operands", st(), 1, wp, F, F, F, fp, None, Wh.data_ptr(), 44, 44, 64, hf.data_ptr(),
+              hb.data_ptr())
+    _lib.call("ppo_pack_bf16_operand_padded", st(), Wh.data_ptr(), 44, F, 44, 64, rf.data_ptr(), rb.data_ptr())
+    torch.cuda.synchronize()
+    assert torch.equal(hf, rf) and torch.equal(hb, rb)
+    ef, eb = unpack_reference(torch.cat([Wh, torch.zeros(F, 20, dtype=torch.int16, device=DEV)], 1).cpu().numpy(),
+                              F, 64)
+    np.testing.assert_array_equal(hf.cpu().numpy(), ef)
+    np.testing.assert_array_equal(hb.cpu().numpy(), eb)
 
 
 def make_layers(L, seed):
@@ -122,7 +146,7 @@ def chain(part, S, M, lay, act, eps=1e-6, y32=None, head=None, z16=False):
         wa, wp = ptrs([p["W16"] for p in lay[1:]])
         fa, fp = ptrs(pk[1:])
         keep += [wa, fa]
-        _lib.call("ppo_pack_bf16_operands", st(), L - 1, wp, F, F, F, fp, None)
+        _lib.call("ppo_pack_bf16_operands", st(), L - 1, wp, F, F, F, fp, None, None, 0, 0, 0, None, None)
     out = [dict(Z=(torch.full((M, F), 7, dtype=torch.int16, device=DEV) if z16 else torch.full((M, F), 7.0, device=DEV)),
                 Y=torch.full((M, F), 7.0, device=DEV),
                 Y16=torch.full((M, F), 7, dtype=torch.int16, device=DEV), mean=torch.full((M,), 7.0, device=DEV),
@@ -236,7 +260,7 @@ def test_chain_rejects_bad_arguments():
                   1e-6, 1, hp.data_ptr(), None, 288, part.data_ptr(), 288, 0)
     # K not a multiple of 32
     with pytest.raises(_lib.KernelError, match="ppo_pack_bf16_operands"):
-        _lib.call("ppo_pack_bf16_operands", st(), 1, p, F, 500, F, p, p)
+        _lib.call("ppo_pack_bf16_operands", st(), 1, p, F, 500, F, p, p, None, 0, 0, 0, None, None)
 
 
 def bwd_inputs(M, L, act, seed):
@@ -281,7 +305,7 @@ def bwd_chain(lay, fwd, dY, M, act, head=None, z16=False):
         wa, wp = ptrs([p["W16"] for p in lay[1:]])
         ba, bp = ptrs(pb[1:])
         keep += [wa, ba]
-        _lib.call("ppo_pack_bf16_operands", st(), L - 1, wp, F, F, F, None, bp)
+        _lib.call("ppo_pack_bf16_operands", st(), L - 1, wp, F, F, F, None, bp, None, 0, 0, 0, None, None)
     out = [dict(dZ16=torch.full((M, F), 7, dtype=torch.int16, device=DEV), part=torch.zeros(nb, 2 * F, device=DEV))
            for _ in range(L)]
     tabs = {}
