@@ -618,7 +618,12 @@ class MLPExecutor(ForwardChain):
     FWD16_TILE = 1    # 128 x 128 tiles (two resident per CU) for the bf16 first-layer forward
     DW16_SPLITS = 3   # row splits of the bf16 first-layer dW (with 256 x 256 tiles: 198 workgroups at 8268 x 512)
     DW16_TILE = 2     # 256 x 256 tiles for the bf16 first-layer dW
-    DW16_SPLITS_INNER = 16  # row splits of a bf16 dW between two LayerNorm layers
+    # row splits of a bf16 dW between two LayerNorm layers: with the chains these
+    # run beside the first layer's dW on the side stream, where 4 splits (64
+    # workgroups each) finish inside it and leave the gradient reduce a quarter
+    # of the partials of 16 (large-observation update 14.70 -> 14.2-14.3 ms;
+    # 2 splits 15.0, 1 split 18.5)
+    DW16_SPLITS_INNER = 4
 
     def __init__(self, program: Program, flat: FlatState, cfg, chain, T: int, N: int):
         if program.gru is not None and type(self) is MLPExecutor:
