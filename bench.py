@@ -156,12 +156,15 @@ def _single_launch_work(name, args):
     if name == "ppo_mlp16_ln_fwd":
         # split partials in; per layer Z (fp32, or bf16 with z16), Y16, mean, rstd out, the top layer's Y;
         # bf16 kernels; with the head, its outputs
+        import ctypes
         L, nsplit, M = args[1], args[5], args[6]
         nh = args[21] if len(args) > 21 and args[19] else 0
         zb = 2.0 if len(args) > 24 and args[24] else 4.0
+        ytab = ctypes.cast(args[12], ctypes.POINTER(ctypes.c_void_p)) if args[12] else None
+        ys = sum(1 for l in range(L) if ytab is not None and ytab[l])  # layers whose fp32 output is written
         return (2.0 * M * 512 * (512 * (L - 1) + nh),
                 4.0 * M * 512 * nsplit + 2.0 * 512 * (512 * (L - 1) + nh) + M * L * ((zb + 2.0) * 512 + 8)
-                + 4.0 * M * 512 + 4.0 * M * nh)
+                + 4.0 * M * 512 * ys + 4.0 * M * nh)
     if name == "ppo_pack_bf16_operand_padded":
         K, n_pad = args[3], args[5]
         return 0.0, 4.0 * K * n_pad

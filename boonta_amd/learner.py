@@ -511,8 +511,11 @@ class ForwardChain:
         c.update(Wh=_p(hpk[0]), bh=self.flat.view(h.b), nh=h.w.ld, head=_p(self.HEAD), ldh=h.w.ld, head_pack=hpk,
                  head_npad=npad)
         if c["bwd"] and npad <= 64:
-            # the backward chain also takes the head's input cotangent over
+            # the backward chain also takes the head's input cotangent over,
+            # and the head's dW reads the bf16 output: the chain's fp32 one is
+            # not needed
             c.update(Whb=_p(hpk[1]))
+            c["keep"]["Y"][c["L"] - 1] = None
 
     def _pack16(self, st):
         """Packed operand images of the bf16 chains' kernels from the bf16
@@ -1154,9 +1157,17 @@ class MLPExecutor(ForwardChain):
 
     def _head_back(self, st, layers, dhead, head: DenseSpec, wpart, bpart, splits, hx, ldhx, hidx):
         """Head dW and the cotangent of the head input."""
-        self._gemm(st, A_COL, B_KN, hx, ldhx, hidx, _p(dhead), head.w.ld, _p(wpart), head.w.ld,
-                  head.fin, head.w.ld, self.mb, splits, head.fin * head.w.ld, EPI_STORE, None, 0, None, None, 0,
-                  _p(bpart), -1)
+        top = layers[-1] if layers else None
+        if top is not None and top.Y16 is not None and hidx is None and head.w.ld % 4 == 0:
+            # from the bf16 copy of the head input (the same bf16 values the
+            # fp32 one rounds to, the same MFMA sequence and split boundaries)
+            self._call("ppo_gemm_bf16s", st, A_COL, B_KN, 1, 0, _p(top.Y16), top.spec.ld, None, _p(dhead),
+                       head.w.ld, _p(wpart), head.w.ld, head.fin, head.w.ld, self.mb, splits, head.fin * head.w.ld,
+                       EPI_STORE, None, 0, 0, None, 0, _p(bpart), -1)
+        else:
+            self._gemm(st, A_COL, B_KN, hx, ldhx, hidx, _p(dhead), head.w.ld, _p(wpart), head.w.ld,
+                      head.fin, head.w.ld, self.mb, splits, head.fin * head.w.ld, EPI_STORE, None, 0, None, None, 0,
+                      _p(bpart), -1)
         c = layers[0].chain16 if layers else None
         if layers and not (c is not None and c.get("Whb")):  # else the backward chain takes it over
             dst, epi, act, aux, ldaux = self._dx_target(layers[-1])
