@@ -36,7 +36,7 @@ constexpr int SEG_ROUND_BF16 = 1;
 
 struct Chunk {
   int seg;
-  int pad_;
+  int slot;  // its squared-norm partial's index in sumsq
   int64_t start;
 };
 
@@ -49,13 +49,53 @@ constexpr int CHUNK = 256;  // elements per block: one float4 per lane of a wave
 // step's missing partials read a clamped partial and count as zero), then
 // the quarters are added in wave order: a fixed association, so the result
 // never depends on scheduling.
+//
+// The first nfew chunks (of segments with at most FEW_PARTS partials) are
+// taken one per wave, four per block, with all of a lane's partial loads in
+// flight at once: the same sum (0 + p0 + p1 + ..., in partial order, which is
+// what the quarter split above gives for so few partials) with four times the
+// loads in flight per block and a quarter of the blocks.
+constexpr int FEW_PARTS = 4;
+
 __global__ void __launch_bounds__(REDUCE_THREADS)
-grad_reduce_kernel(const Segment* __restrict__ segs, const Chunk* __restrict__ chunks, double* __restrict__ sumsq) {
+grad_reduce_kernel(const Segment* __restrict__ segs, const Chunk* __restrict__ chunks, int nfew,
+                   double* __restrict__ sumsq) {
   __shared__ floatx4 part[REDUCE_THREADS / 64][64];
-  const Chunk ch = chunks[blockIdx.x];
-  const Segment sg = segs[ch.seg];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int few_blocks = (nfew + 3) / 4;
+  if ((int)blockIdx.x < few_blocks) {
+    const int ci = 4 * blockIdx.x + wave;
+    if (ci >= nfew) return;  // this path has no barrier
+    const Chunk ch = chunks[ci];
+    const Segment sg = segs[ch.seg];
+    const int64_t i = ch.start + 4 * lane;
+    const bool live = i < sg.count;
+    floatx4 v[FEW_PARTS];
+#pragma unroll
+    for (int q = 0; q < FEW_PARTS; ++q)
+      v[q] = (live && q < sg.nparts) ? *reinterpret_cast<const floatx4*>(sg.src + i + (int64_t)q * sg.part_stride)
+                                     : floatx4{0.f, 0.f, 0.f, 0.f};
+    double sq = 0.0;
+    if (live) {
+      floatx4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < FEW_PARTS; ++q)
+        if (q < sg.nparts) t += v[q];
+      if (sg.flags & SEG_ROUND_BF16) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] = ppo::bf16_round(t[e]);
+      }
+      *reinterpret_cast<floatx4*>(sg.dst + i) = t;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sq += (double)t[e] * (double)t[e];
+    }
+    sq = ppo::wave_sum_d(sq);
+    if (lane == 0) sumsq[ch.slot] = sq;
+    return;
+  }
+  const Chunk ch = chunks[nfew + ((int)blockIdx.x - few_blocks)];
+  const Segment sg = segs[ch.seg];
   const int64_t i = ch.start + 4 * lane;  // first element of this lane's float4
   const bool live = i < sg.count;
   const int q0 = (sg.nparts * wave) / 4, q1 = (sg.nparts * (wave + 1)) / 4;
@@ -93,7 +133,7 @@ grad_reduce_kernel(const Segment* __restrict__ segs, const Chunk* __restrict__ c
       for (int e = 0; e < 4; ++e) sq += (double)t[e] * (double)t[e];
     }
     sq = ppo::wave_sum_d(sq);
-    if (lane == 0) sumsq[blockIdx.x] = sq;
+    if (lane == 0) sumsq[ch.slot] = sq;
   }
 }
 
@@ -209,13 +249,18 @@ PPO_EXPORT int ppo_grad_reduce_chunk_elems(void) { return CHUNK; }
 // one block per chunk; sumsq receives nchunks doubles.
 // Every segment's count, part stride and pointers must be multiples of 4
 // floats (16 bytes): the learner's flat layout guarantees it.
-PPO_EXPORT int ppo_grad_reduce(void* stream, const void* segs, const void* chunks, int nchunks, double* sumsq) {
-  if (nchunks < 0 || !segs || !chunks || !sumsq) return ppo::set_error(PPO_ERR_ARG, "ppo_grad_reduce: bad argument");
+PPO_EXPORT int ppo_grad_reduce(void* stream, const void* segs, const void* chunks, int nchunks, int nfew,
+                               double* sumsq) {
+  if (nchunks < 0 || nfew < 0 || nfew > nchunks || !segs || !chunks || !sumsq)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_grad_reduce: bad argument (nchunks=%d nfew=%d)", nchunks, nfew);
   if (nchunks == 0) return PPO_OK;
-  hipLaunchKernelGGL(grad_reduce_kernel, dim3(nchunks), dim3(REDUCE_THREADS), 0, ppo::as_stream(stream),
-                     (const Segment*)segs, (const Chunk*)chunks, sumsq);
+  const int blocks = (nfew + 3) / 4 + (nchunks - nfew);
+  hipLaunchKernelGGL(grad_reduce_kernel, dim3(blocks), dim3(REDUCE_THREADS), 0, ppo::as_stream(stream),
+                     (const Segment*)segs, (const Chunk*)chunks, nfew, sumsq);
   return ppo::check_launch("ppo_grad_reduce");
 }
+
+PPO_EXPORT int ppo_grad_reduce_few_parts(void) { return FEW_PARTS; }
 
 // Hyper-parameters arrive as double, as optax receives Python floats: 1 - b is
 // formed in double and rounded once to fp32, like optax's (1 - decay) * g.

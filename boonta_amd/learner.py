@@ -963,14 +963,21 @@ class MLPExecutor(ForwardChain):
         assert lib.ppo_grad_reduce_segment_bytes() == 40 and lib.ppo_grad_reduce_chunk_bytes() == 16
         chunk = lib.ppo_grad_reduce_chunk_elems()
         seg_bytes = b"".join(struct.pack("<QQqqii", d, s, c, st, n, f) for d, s, c, st, n, f in segs)
-        chunks = []
-        for i, (_, _, c, _, _, _) in enumerate(segs):
+        # chunks of few-partial segments first (the kernel's wave-per-chunk
+        # path); each keeps its slot in segment order, so the norm's fold
+        # order does not depend on the split
+        few_parts = lib.ppo_grad_reduce_few_parts()
+        few, many = [], []
+        for i, (_, _, c, _, n, _) in enumerate(segs):
             for start in range(0, c, chunk):
-                chunks.append(struct.pack("<iiq", i, 0, start))
+                slot = len(few) + len(many)
+                (few if n <= few_parts else many).append(struct.pack("<iiq", i, slot, start))
+        chunks = few + many
         dev = flat.device
         self.SEGS = torch.tensor(list(seg_bytes), dtype=torch.uint8, device=dev)
         self.CHUNKS = torch.tensor(list(b"".join(chunks)), dtype=torch.uint8, device=dev)
         self.nchunks = len(chunks)
+        self.nfew = len(few)
         self.SUMSQ = torch.zeros(self.nchunks, dtype=torch.float64, device=dev)
         self.SUMSQ1 = torch.zeros(1, dtype=torch.float64, device=dev)
         self.segments = segs
@@ -1269,7 +1276,7 @@ class MLPExecutor(ForwardChain):
         chain = self.chain
         adam = chain.adam
         max_norm = chain.max_grad_norm if chain.max_grad_norm is not None else 0.0
-        self._call("ppo_grad_reduce", st, _p(self.SEGS), _p(self.CHUNKS), self.nchunks, _p(self.SUMSQ))
+        self._call("ppo_grad_reduce", st, _p(self.SEGS), _p(self.CHUNKS), self.nchunks, self.nfew, _p(self.SUMSQ))
         if self.nchunks <= self.FOLD_NORM_MAX:
             norm, nnorm = _p(self.SUMSQ), self.nchunks
         else:

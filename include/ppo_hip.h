@@ -577,13 +577,17 @@ int ppo_sequence_rows(void* stream, const int32_t* envs, int S, int T, int N, in
  * A segment is {float* dst; const float* src; int64 count; int64
  * part_stride; int32 nparts; int32 flags} (flags bit 0: round the summed
  * gradient to bf16, for parameters a bf16-compute layer casts); a chunk is
- * {int32 segment; int32 pad; int64 start} covering
- * ppo_grad_reduce_chunk_elems() elements.
+ * {int32 segment; int32 slot; int64 start} covering
+ * ppo_grad_reduce_chunk_elems() elements, whose sum of squares lands in
+ * sumsq[slot].  The first nfew chunks (0 <= nfew <= nchunks) must belong to
+ * segments with at most ppo_grad_reduce_few_parts() partials: they take a
+ * path with more loads in flight that gives the same bits.
  * The optax count is count_base[0] + step_offset + 1 (device int32). */
 int ppo_grad_reduce_segment_bytes(void);
 int ppo_grad_reduce_chunk_bytes(void);
 int ppo_grad_reduce_chunk_elems(void);
-int ppo_grad_reduce(void* stream, const void* segs, const void* chunks, int nchunks, double* sumsq);
+int ppo_grad_reduce_few_parts(void);
+int ppo_grad_reduce(void* stream, const void* segs, const void* chunks, int nchunks, int nfew, double* sumsq);
 /* params_bf16 (may be NULL): receives the bf16 image of the updated parameters. */
 int ppo_adam_clip_f32(void* stream, float* params, const float* grads, float* mu, float* nu, void* params_bf16,
                       int64_t n, const double* sumsq, int nsumsq, double max_norm, double lr, double b1,

@@ -410,14 +410,15 @@ def test_grad_reduce_partials(nparts):
         D = torch.full((n,), float("nan"), device=DEV)
         keep += [P, D]
         segs += struct.pack("<QQqqii", D.data_ptr(), P.data_ptr(), n, stride, nparts, 0)
-        chunks += b"".join(struct.pack("<iiq", k, 0, s) for s in range(0, n, chunk))
+        chunks += b"".join(struct.pack("<iiq", k, len(chunks) // 16 + j, s)
+                           for j, s in enumerate(range(0, n, chunk)))
         outs.append(D)
         refs.append(parts[:, :n].astype(np.float64).sum(0))
     nch = len(chunks) // 16
     SEGS = torch.tensor(list(segs), dtype=torch.uint8, device=DEV)
     CH = torch.tensor(list(chunks), dtype=torch.uint8, device=DEV)
     SQ = torch.zeros(nch, dtype=torch.float64, device=DEV)
-    _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), CH.data_ptr(), nch, SQ.data_ptr())
+    _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), CH.data_ptr(), nch, 0, SQ.data_ptr())
     torch.cuda.synchronize()
     tot = 0.0
     for D, ref in zip(outs, refs):
@@ -425,6 +426,58 @@ def test_grad_reduce_partials(nparts):
         np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6 * np.sqrt(nparts))
         tot += float((got * got).sum())
     np.testing.assert_allclose(host(SQ).sum(), tot, rtol=1e-12)
+
+
+def test_grad_reduce_few_part_path_is_bit_identical():
+    """Chunks of segments with at most ppo_grad_reduce_few_parts() partials,
+    put first and counted in nfew, take the wave-per-chunk path: the same
+    gradient bits and per-slot squared norms as the block-per-chunk path, for
+    1..4 partials, ragged counts, bf16 rounding, signed zeros and a chunk
+    count that leaves the last block's waves partly idle."""
+    import struct
+    lib = _lib.load()
+    few_parts = lib.ppo_grad_reduce_few_parts()
+    assert few_parts == 4
+    g = np.random.default_rng(11)
+    chunk = lib.ppo_grad_reduce_chunk_elems()
+    specs = [(1, 1000, 1008, 0), (2, 300, 304, 1), (3, 4096 + 256, 4096 + 256, 1), (4, 2060, 2064, 0),
+             (3, 36, 40, 0), (7, 520, 520, 0)]  # (nparts, count, part stride, bf16 flag)
+    segs, keep, outs, descr = b"", [], [], []
+    for k, (npart, n, stride, rb) in enumerate(specs):
+        parts = (g.standard_normal((npart, stride)) * 0.1).astype(np.float32)
+        parts[:, :8] = 0.0
+        parts[0, :4] = -0.0
+        P = dev(parts)
+        D = torch.full((n,), float("nan"), device=DEV)
+        keep += [P]
+        outs.append(D)
+        segs += struct.pack("<QQqqii", D.data_ptr(), P.data_ptr(), n, stride, npart, rb)
+        descr += [(k, s) for s in range(0, n, chunk)]
+    slots = {c: i for i, c in enumerate(descr)}
+    few = [c for c in descr if specs[c[0]][0] <= few_parts]
+    many = [c for c in descr if specs[c[0]][0] > few_parts]
+    nch = len(descr)
+    SEGS = torch.tensor(list(segs), dtype=torch.uint8, device=DEV)
+
+    def run(order, nfew):
+        CH = torch.tensor(list(b"".join(struct.pack("<iiq", k, slots[(k, s)], s) for k, s in order)),
+                          dtype=torch.uint8, device=DEV)
+        SQ = torch.full((nch,), float("nan"), dtype=torch.float64, device=DEV)
+        for D in outs:
+            D.fill_(float("nan"))
+        _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), CH.data_ptr(), nch, nfew, SQ.data_ptr())
+        torch.cuda.synchronize()
+        return [host(D).view(np.uint32).copy() for D in outs], host(SQ).view(np.uint64).copy()
+
+    ref_g, ref_sq = run(descr, 0)
+    got_g, got_sq = run(few + many, len(few))
+    assert (len(few) + 3) // 4 * 4 != len(few)  # a partly idle last block
+    for k, (a, b) in enumerate(zip(ref_g, got_g)):
+        np.testing.assert_array_equal(a, b, err_msg=f"segment {k}")
+    np.testing.assert_array_equal(ref_sq, got_sq)
+    # an nfew past nchunks is rejected before launch
+    with pytest.raises(RuntimeError):
+        _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), SEGS.data_ptr(), 2, 3, SEGS.data_ptr())
 
 
 @pytest.mark.parametrize("max_norm, scale", [(0.5, 1.0), (0.5, 1e-3), (0.0, 1.0)])
@@ -442,12 +495,12 @@ def test_grad_reduce_and_adam_match_optax_restatement(max_norm, scale):
     PARTS = dev(parts)
     segs = struct.pack("<QQqqii", Gt.data_ptr(), PARTS.data_ptr(), n, n, nparts, 0)
     chunk = _lib.load().ppo_grad_reduce_chunk_elems()
-    chunks = b"".join(struct.pack("<iiq", 0, 0, s) for s in range(0, n, chunk))
+    chunks = b"".join(struct.pack("<iiq", 0, j, s) for j, s in enumerate(range(0, n, chunk)))
     nch = len(range(0, n, chunk))
     SEGS = torch.tensor(list(segs), dtype=torch.uint8, device=DEV)
     CH = torch.tensor(list(chunks), dtype=torch.uint8, device=DEV)
     SQ = torch.zeros(nch, dtype=torch.float64, device=DEV)
-    _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), CH.data_ptr(), nch, SQ.data_ptr())
+    _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), CH.data_ptr(), nch, 0, SQ.data_ptr())
     count = torch.tensor([6], dtype=torch.int32, device=DEV)
     _lib.call("ppo_adam_clip_f32", st(), P.data_ptr(), Gt.data_ptr(), MU.data_ptr(), NU.data_ptr(), None, n,
               SQ.data_ptr(), nch, max_norm, 3e-4, 0.9, 0.999, 1e-8, count.data_ptr(), 2)
