@@ -144,8 +144,9 @@ __device__ __forceinline__ bf16x8 doperand(const uint16_t* lds, int r0, int kk, 
 
 using ppo::ring_barrier;
 
-template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF, int KIDX = KIDX_MAX>
-__global__ void __launch_bounds__(WM * WN * 64, 1) gemm_bf16d_kernel(Params p) {
+// One workgroup's output tile tc of the GEMM p.
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF, int KIDX>
+__device__ __forceinline__ void gemm_bf16d_tile(const Params& p, const ppo::TileCoord tc) {
   constexpr int NW = WM * WN;
   constexpr int BI = BM / WM / 32, BJ = BN / WN / 32;
   static_assert(BI * WM * 32 == BM && BJ * WN * 32 == BN, "tile must split into 32 x 32 blocks");
@@ -160,7 +161,6 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_bf16d_kernel(Params p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave % WM;
   const int wn = wave / WM;
-  const ppo::TileCoord tc = ppo::xcd_tile();
   const int m0 = tc.m * BM;
   const int n0 = tc.n * BN;
   const int split = tc.z;
@@ -253,6 +253,40 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_bf16d_kernel(Params p) {
   }
 
   epilogue<BI, BJ>(p, acc, bsum, do_bsum, m0 + wm * (BI * 32), n0 + wn * (BJ * 32), split, lane);
+}
+
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF, int KIDX = KIDX_MAX>
+__global__ void __launch_bounds__(WM * WN * 64, 1) gemm_bf16d_kernel(Params p) {
+  gemm_bf16d_tile<BM, BN, WM, WN, A_K, B_K, NBUF, KIDX>(p, ppo::xcd_tile());
+}
+
+// Several GEMMs of one tile shape in one launch: problem i owns the linear
+// tiles [start[i], start[i + 1]), each problem's tiles ordered n fastest, then
+// m, then split.  Linear tiles are dealt to the XCDs in contiguous ranges, as
+// xcd_tile does for one GEMM.
+constexpr int GROUP_MAX = 8;
+struct GroupParams {
+  Params p[GROUP_MAX];
+  int start[GROUP_MAX + 1];
+  int gx[GROUP_MAX], gy[GROUP_MAX];
+  int count;
+};
+
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF, int KIDX>
+__global__ void __launch_bounds__(WM * WN * 64, 1) gemm_bf16d_group_kernel(GroupParams g) {
+  const int total = gridDim.x;
+  const int w = blockIdx.x;
+  const int x = w & 7, j = w >> 3;
+  const int q = total >> 3, r = total & 7;
+  const int t = x * q + (x < r ? x : r) + j;
+  int i = 0;
+  while (i + 1 < g.count && t >= g.start[i + 1]) ++i;
+  const int local = t - g.start[i];
+  ppo::TileCoord tc;
+  tc.n = local % g.gx[i];
+  tc.m = (local / g.gx[i]) % g.gy[i];
+  tc.z = local / (g.gx[i] * g.gy[i]);
+  gemm_bf16d_tile<BM, BN, WM, WN, A_K, B_K, NBUF, KIDX>(g.p[i], tc);
 }
 
 template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF, int KIDX = KIDX_MAX>

@@ -441,6 +441,10 @@ class ForwardChain:
     CHAIN16 = True
     CHAIN16_BWD = True
     DW16_SIDE = True  # the chain group's later weight gradients beside the first layer's, on the side stream
+    # every weight gradient of the chain group in one launch (ppo_gemm_bf16s_dw_group):
+    # the later layers' few tiles run beside the first layer's 198, with no
+    # stream fork and join around them
+    DW16_GROUP = True
 
     def _plan_chain16(self, group):
         """Pointer tables of the bf16 chain over ``group`` when it fits the
@@ -622,11 +626,12 @@ class MLPExecutor(ForwardChain):
     DW16_SPLITS = 3   # row splits of the bf16 first-layer dW (with 256 x 256 tiles: 198 workgroups at 8268 x 512)
     DW16_TILE = 2     # 256 x 256 tiles for the bf16 first-layer dW
     # row splits of a bf16 dW between two LayerNorm layers: with the chains these
-    # run beside the first layer's dW on the side stream, where 4 splits (64
-    # workgroups each) finish inside it and leave the gradient reduce a quarter
-    # of the partials of 16 (large-observation update 14.70 -> 14.2-14.3 ms;
-    # 2 splits 15.0, 1 split 18.5)
-    DW16_SPLITS_INNER = 4
+    # run in the first layer's dW launch, where 3 splits (12 workgroups of
+    # 256 x 256 each) take as long as the first layer's workgroups; on the side
+    # stream 4 splits of 128 x 128 tiles finished inside the first layer's dW
+    # (large-observation update 14.70 -> 14.2-14.3 ms from 16 splits; 2 splits
+    # 15.0, 1 split 18.5)
+    DW16_SPLITS_INNER = 3
 
     def __init__(self, program: Program, flat: FlatState, cfg, chain, T: int, N: int):
         if program.gru is not None and type(self) is MLPExecutor:
@@ -1007,6 +1012,30 @@ class MLPExecutor(ForwardChain):
         aux = lb.PRE if s.act == "silu" else lb.Y
         return _p(lb.dZ), EPI_DACT, _act(s.act), _p(aux), s.ld
 
+    def _plan_dw_group(self, layers):
+        """Host argument arrays of ppo_gemm_bf16s_dw_group over a bf16 chain
+        group's weight gradients: the first layer's from the observation copy
+        (its gather indices set per call in ``rows[0]``), each later layer's
+        from the previous layer's bf16 output."""
+        L = len(layers)
+        vp = lambda xs: (ctypes.c_void_p * L)(*xs)
+        i64 = lambda xs: (ctypes.c_int64 * L)(*xs)
+        i32 = lambda xs: (ctypes.c_int * L)(*xs)
+        A = [_p(self.OBS16)] + [_p(layers[i - 1].Y16) for i in range(1, L)]
+        lda = [self.ldo16] + [layers[i - 1].spec.ld for i in range(1, L)]
+        g = {
+            "A": vp(A), "lda": i64(lda), "rows": vp([None] * L),
+            "B": vp([_p(lb.dZ16) for lb in layers]), "ldb": i64([lb.spec.ld for lb in layers]),
+            "C": vp([_p(lb.wpart) for lb in layers]), "ldc": i64([lb.spec.ld for lb in layers]),
+            "M": i32([lb.spec.dense.fin for lb in layers]), "N": i32([lb.spec.ld for lb in layers]),
+            "K": i32([self.mb] * L), "splits": i32([lb.splits for lb in layers]),
+            "stride": i64([lb.spec.dense.fin * lb.spec.ld for lb in layers]),
+            "bias_grad": vp([_p(lb.bpart) for lb in layers]),
+        }
+        order = ("A", "lda", "rows", "B", "ldb", "C", "ldc", "M", "N", "K", "splits", "stride", "bias_grad")
+        g["args"] = [ctypes.addressof(g[k]) for k in order]
+        return g
+
     def _bwd_layers(self, st, layers, x0, ldx0, idx0):
         """Back-propagates through layers whose last output cotangent is in place."""
         c = layers[0].chain16 if layers else None
@@ -1020,6 +1049,13 @@ class MLPExecutor(ForwardChain):
             self._call("ppo_mlp16_ln_bwd", st, c["L"], _p(top.dY), top.spec.ld, self.mb, c["Wb"], c["Z"],
                        c["mean"], c["rstd"], c["g"], c["be"], c["dZ16"], top.spec.ld, c["part"], c["act"], *hd,
                        c["z16"])
+            if self.DW16_GROUP and len(layers) <= 8:
+                g = c.get("dw_group")
+                if g is None:
+                    g = c["dw_group"] = self._plan_dw_group(layers)
+                g["rows"][0] = idx0
+                self._call("ppo_gemm_bf16s_dw_group", st, len(layers), *g["args"])
+                return
             # the first layer's dW fills 198 of the 256 CUs: the later layers'
             # run beside it on the side stream
             s2 = self._fork(st) if self.DW16_SIDE else st

@@ -416,6 +416,81 @@ def test_gemm_bf16s_gathered_reduction_beyond_index_cache():
                     bias_grad=True, seed=splits)
 
 
+def test_gemm_bf16s_dw_group_is_bit_identical_to_single_launches():
+    """ppo_gemm_bf16s_dw_group: a gathered first-layer-like dW (ragged M, a
+    split over 2752 gathered rows), two 512-wide ones over contiguous rows
+    (one without a bias gradient) and a ragged small one, in one launch: every
+    partial and bias-gradient partial equal bit for bit to the same problem's
+    ppo_gemm_bf16s launch at tile 2, and to the oracle's bf16 product."""
+    import ctypes
+    g = np.random.default_rng(41)
+    K = 8192 // 2
+    probs = [  # (M, N, splits, gathered, bias_grad)
+        (1300, 512, 3, True, True),
+        (512, 512, 3, False, True),
+        (512, 512, 2, False, False),
+        (200, 72, 1, False, True),
+    ]
+    src_rows = 6000
+    idx = g.permutation(src_rows)[:K].astype(np.int32)
+    IDX = dev(idx)
+    keep, single, grouped, refs = [], [], [], []
+    args = {k: [] for k in ("A", "lda", "rows", "B", "ldb", "C", "ldc", "M", "N", "K", "splits", "stride", "bg")}
+    for M, N, S, gathered, bg in probs:
+        rows_n = src_rows if gathered else K
+        lda = (M + 7) // 8 * 8 + 8
+        Abits = np.full((rows_n, lda), 0x7FC0, np.uint16)
+        Alog = (g.standard_normal((rows_n, M)) * 0.5).astype(np.float32)
+        Abits[:, :M] = to_bf16_bits(Alog)
+        ldb = (N + 7) // 8 * 8
+        Blog = g.standard_normal((K, N)).astype(np.float32)
+        Bbits = np.zeros((K, ldb), np.uint16)
+        Bbits[:, :N] = to_bf16_bits(Blog)
+        At, Bt = dev(Abits.view(np.int16)), dev(Bbits.view(np.int16))
+        C1 = torch.full((S, M, N), float("nan"), device=DEV)
+        C2 = torch.full((S, M, N), float("nan"), device=DEV)
+        G1 = torch.full((S, N), float("nan"), device=DEV) if bg else None
+        G2 = torch.full((S, N), float("nan"), device=DEV) if bg else None
+        keep += [At, Bt]
+        rp = IDX.data_ptr() if gathered else None
+        _lib.call("ppo_gemm_bf16s", st(), 1, 0, 1, 1, At.data_ptr(), lda, rp, Bt.data_ptr(), ldb, C1.data_ptr(), N,
+                  M, N, K, S, M * N, 0, None, 0, 0, None, 0, None if G1 is None else G1.data_ptr(), 2)
+        single.append((C1, G1))
+        grouped.append((C2, G2))
+        Aeff = Alog[idx] if gathered else Alog
+        refs.append((nets.bf16(Aeff).T @ nets.bf16(Blog), nets.bf16(Blog).sum(0)))
+        for k, v in (("A", At.data_ptr()), ("lda", lda), ("rows", rp), ("B", Bt.data_ptr()), ("ldb", ldb),
+                     ("C", C2.data_ptr()), ("ldc", N), ("M", M), ("N", N), ("K", K), ("splits", S),
+                     ("stride", M * N), ("bg", None if G2 is None else G2.data_ptr())):
+            args[k].append(v)
+    L = len(probs)
+    vp = lambda xs: (ctypes.c_void_p * L)(*xs)
+    i64 = lambda xs: (ctypes.c_int64 * L)(*xs)
+    i32 = lambda xs: (ctypes.c_int * L)(*xs)
+    arrs = [vp(args["A"]), i64(args["lda"]), vp(args["rows"]), vp(args["B"]), i64(args["ldb"]), vp(args["C"]),
+            i64(args["ldc"]), i32(args["M"]), i32(args["N"]), i32(args["K"]), i32(args["splits"]),
+            i64(args["stride"]), vp(args["bg"])]
+    _lib.call("ppo_gemm_bf16s_dw_group", st(), L, *[ctypes.addressof(a) for a in arrs])
+    torch.cuda.synchronize()
+    for i, ((C1, G1), (C2, G2), (ref, bref)) in enumerate(zip(single, grouped, refs)):
+        assert torch.equal(C1, C2), f"problem {i}: partials differ"
+        if G1 is not None:
+            assert torch.equal(G1, G2), f"problem {i}: bias-gradient partials differ"
+            np.testing.assert_allclose(G2.cpu().numpy().astype(np.float64).sum(0), bref, rtol=1e-5,
+                                       atol=1e-5 * np.sqrt(K))
+        np.testing.assert_allclose(C2.cpu().numpy().astype(np.float64).sum(0), ref, rtol=1e-5,
+                                   atol=1e-4 * np.sqrt(K))
+    # a gathered split beyond the 4096-row index cache, and too many problems, are refused
+    big = i32([8200] * L)
+    one = i32([1] * L)
+    bad = list(arrs)
+    bad[9], bad[10] = big, one
+    with pytest.raises(RuntimeError):
+        _lib.call("ppo_gemm_bf16s_dw_group", st(), L, *[ctypes.addressof(a) for a in bad])
+    with pytest.raises(RuntimeError):
+        _lib.call("ppo_gemm_bf16s_dw_group", st(), 9, *[ctypes.addressof(a) for a in arrs])
+
+
 def test_cast_bf16():
     x = np.random.default_rng(9).standard_normal(100005).astype(np.float32) * 10
     X = dev(x)
