@@ -189,6 +189,8 @@ def _single_launch_work(name, args):
         pad = (nh + 31) // 32 * 32
         zb = 2.0 if len(args) > 20 and args[20] else 4.0
         top = (4.0 * M * nh + 2.0 * 512 * pad) if nh else 4.0 * M * 512
+        if len(args) > 22 and args[21]:  # the bf16 copy of the head cotangents
+            top += 2.0 * M * args[22]
         return (2.0 * M * 512 * (512 * (L - 1) + pad),
                 top + M * L * (zb * 512 + 8 + 2.0 * 512) + L * ((M + 31) // 32) * 4096.0
                 + 2.0 * 512 * 512 * (L - 1))

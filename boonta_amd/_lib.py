@@ -62,7 +62,7 @@ SIGNATURES = {
     "ppo_pack_bf16_operands": (I, [P, I, P, I64, I, I, P, P, P, I64, I, I, P, P]),
     "ppo_pack_bf16_operand_padded": (I, [P, P, I64, I, I, I, P, P]),
     "ppo_mlp16_ln_bwd_blocks": (I, [I]),
-    "ppo_mlp16_ln_bwd": (I, [P, I, P, I64, I, P, P, P, P, P, P, P, I64, P, I, P, I64, P, I, I, I]),
+    "ppo_mlp16_ln_bwd": (I, [P, I, P, I64, I, P, P, P, P, P, P, P, I64, P, I, P, I64, P, I, I, I, P, I64]),
     "ppo_linear_scan_fwd": (I, [P, I, P, P, P, P, I, I, I]),
     "ppo_linear_scan_bwd": (I, [P, I, P, P, P, P, P, P, P, I, I, I]),
     "ppo_ssm_scan_fwd": (I, [P, I, P, P, P, P, P, P, I, I, I]),

@@ -394,6 +394,10 @@ struct Bwd16Args {
   int64_t lddh;
   const uint16_t* Whb;
   int nh, nhk;
+  // optional with the head: the rounded cotangents as bf16 [M][ld16] (zero
+  // past nh), the B operand of the head's weight gradient
+  uint16_t* dhead16;
+  int64_t ld16;
 };
 
 // From the top layer down: the LayerNorm + activation backward of layer l
@@ -464,7 +468,9 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_bwd_kernel(Bwd16Args 
       const int r = i / (16 * a.nhk), k = i % (16 * a.nhk);
       const int grow = m0 + r;
       const float v = (k < a.nh && grow < a.M) ? a.dhead[(int64_t)grow * a.lddh + k] : 0.f;
-      sA[r * A_PITCH + k] = (uint16_t)ppo::bf16_bits(v);
+      const uint16_t bits = (uint16_t)ppo::bf16_bits(v);
+      sA[r * A_PITCH + k] = bits;
+      if (a.dhead16 && grow < a.M && k < a.ld16) a.dhead16[(int64_t)grow * a.ld16 + k] = bits;
     }
     __syncthreads();
     floatx16 acc[C16_BJ];
@@ -734,14 +740,19 @@ PPO_EXPORT int ppo_mlp16_ln_bwd_blocks(int rows) { return rows > 0 ? ppo::ceil_d
 // dhead W_h^T from the head's output cotangents dhead [M][lddh] (nh columns)
 // and Whb, the head kernel's packed backward image over nh_pad (32 or 64)
 // outputs (ppo_pack_bf16_operand_padded), as the bf16 head GEMM rounds it.
-// z16: Z[l] holds the forward's bf16 Z.
+// z16: Z[l] holds the forward's bf16 Z.  dhead16 (with the head; may be
+// null): receives the rounded head cotangents as bf16 [M][lddh16], zero in
+// columns nh .. lddh16 - 1 (lddh16 a multiple of 8, nh <= lddh16 <= nh_pad).
 PPO_EXPORT int ppo_mlp16_ln_bwd(void* stream, int L, const float* dY, int64_t lddy, int M, const void* const* Wb,
                                 const float* const* Z, const float* const* mean, const float* const* rstd,
                                 const float* const* gamma, const float* const* beta, void* const* dZ16, int64_t ld,
                                 float* const* part, int act, const float* dhead, int64_t lddh, const void* Whb,
-                                int nh, int nh_pad, int z16) {
+                                int nh, int nh_pad, int z16, void* dhead16, int64_t lddh16) {
   if (Whb && (!dhead || nh < 1 || lddh < nh || nh_pad < nh || nh_pad % 32 || nh_pad > 64 || !aligned16(Whb)))
     return ppo::set_error(PPO_ERR_ARG, "ppo_mlp16_ln_bwd: bad head (nh=%d nh_pad=%d)", nh, nh_pad);
+  if (dhead16 && (!Whb || lddh16 < nh || lddh16 > nh_pad || lddh16 % 8 || !aligned16(dhead16)))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_mlp16_ln_bwd: bad bf16 head cotangent (lddh16=%lld nh=%d nh_pad=%d)",
+                          (long long)lddh16, nh, nh_pad);
   if (L < 1 || L > C16_MAXL || M < 0 || act < 0 || act > 3 || (!Whb && (!dY || !aligned16(dY) || lddy < C16_F ||
       lddy % 4)) || ld < C16_F || ld % 8 || !Z || !mean || !rstd || !gamma || !beta || !dZ16 || !part ||
       (L > 1 && !Wb))
@@ -750,6 +761,7 @@ PPO_EXPORT int ppo_mlp16_ln_bwd(void* stream, int L, const float* dY, int64_t ld
   Bwd16Args a{};
   a.dY = dY; a.lddy = lddy; a.M = M; a.L = L; a.ld = ld; a.z16 = z16 != 0;
   a.dhead = dhead; a.lddh = lddh; a.Whb = static_cast<const uint16_t*>(Whb); a.nh = nh; a.nhk = nh_pad / 16;
+  a.dhead16 = static_cast<uint16_t*>(dhead16); a.ld16 = lddh16;
   for (int l = 0; l < L; ++l) {
     if (!Z[l] || !mean[l] || !rstd[l] || !gamma[l] || !beta[l] || !dZ16[l] || !part[l] || !aligned16(dZ16[l]) ||
         (l > 0 && (!Wb[l] || !aligned16(Wb[l]))))

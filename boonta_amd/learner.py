@@ -520,6 +520,12 @@ class ForwardChain:
             # not needed
             c.update(Whb=_p(hpk[1]))
             c["keep"]["Y"][c["L"] - 1] = None
+            if self.DW16_GROUP and c["L"] < 8 and self.head_splits == self.HEAD16_SPLITS:
+                # the chain leaves the rounded head cotangents as bf16, and the
+                # head's dW joins the trunk's grouped dW launch
+                ld16 = (h.w.ld + 7) // 8 * 8
+                self.DHEAD16 = torch.zeros(self.mb, ld16, dtype=torch.int16, device=self.P16.device)
+                c.update(dhead16=(_p(self.DHEAD16), ld16))
 
     def _pack16(self, st):
         """Packed operand images of the bf16 chains' kernels from the bf16
@@ -632,6 +638,9 @@ class MLPExecutor(ForwardChain):
     # (large-observation update 14.70 -> 14.2-14.3 ms from 16 splits; 2 splits
     # 15.0, 1 split 18.5)
     DW16_SPLITS_INNER = 3
+    # row splits of the shared head's dW in a bf16 network: in the grouped dW
+    # launch its 2 x 4 workgroups of 2048 rows finish inside the first layer's
+    HEAD16_SPLITS = 4
 
     def __init__(self, program: Program, flat: FlatState, cfg, chain, T: int, N: int):
         if program.gru is not None and type(self) is MLPExecutor:
@@ -749,7 +758,9 @@ class MLPExecutor(ForwardChain):
         elif program.shared_head:
             self.HEAD = torch.zeros(mb, ha.w.ld, **f32)
             self.DHEAD = torch.zeros(mb, ha.w.ld, **f32)
-            self.head_splits = _splits(mb, ha.fin, ha.w.ld)
+            # bf16 networks: the head's dW may run in the trunk's grouped dW
+            # launch, and both backward paths keep the same split boundaries
+            self.head_splits = self.HEAD16_SPLITS if self.obs16 else _splits(mb, ha.fin, ha.w.ld)
             self.HWPART = torch.zeros(self.head_splits, ha.fin, ha.w.ld, **f32)
             self.HBPART = torch.zeros(self.head_splits, ha.w.ld, **f32)
             self.HEADB = torch.zeros(N, ha.w.ld, **f32)
@@ -1012,25 +1023,34 @@ class MLPExecutor(ForwardChain):
         aux = lb.PRE if s.act == "silu" else lb.Y
         return _p(lb.dZ), EPI_DACT, _act(s.act), _p(aux), s.ld
 
-    def _plan_dw_group(self, layers):
+    def _plan_dw_group(self, layers, c):
         """Host argument arrays of ppo_gemm_bf16s_dw_group over a bf16 chain
         group's weight gradients: the first layer's from the observation copy
         (its gather indices set per call in ``rows[0]``), each later layer's
-        from the previous layer's bf16 output."""
-        L = len(layers)
+        from the previous layer's bf16 output, and with ``dhead16`` the shared
+        head's from the top layer's bf16 output and the chain's bf16 head
+        cotangents."""
+        # (A, lda, B, ldb, C, ldc, M, N, splits, bias_grad) per problem
+        probs = []
+        for i, lb in enumerate(layers):
+            s = lb.spec
+            a, lda = (_p(self.OBS16), self.ldo16) if i == 0 else (_p(layers[i - 1].Y16), layers[i - 1].spec.ld)
+            probs.append((a, lda, _p(lb.dZ16), s.ld, _p(lb.wpart), s.ld, s.dense.fin, s.ld, lb.splits, _p(lb.bpart)))
+        if c.get("dhead16"):
+            h, top = self.prog.head_a, layers[-1]
+            d16, ld16 = c["dhead16"]
+            probs.append((_p(top.Y16), top.spec.ld, d16, ld16, _p(self.HWPART), h.w.ld, h.fin, h.w.ld,
+                          self.head_splits, _p(self.HBPART)))
+        L = len(probs)
         vp = lambda xs: (ctypes.c_void_p * L)(*xs)
         i64 = lambda xs: (ctypes.c_int64 * L)(*xs)
         i32 = lambda xs: (ctypes.c_int * L)(*xs)
-        A = [_p(self.OBS16)] + [_p(layers[i - 1].Y16) for i in range(1, L)]
-        lda = [self.ldo16] + [layers[i - 1].spec.ld for i in range(1, L)]
+        col = lambda j: [p[j] for p in probs]
         g = {
-            "A": vp(A), "lda": i64(lda), "rows": vp([None] * L),
-            "B": vp([_p(lb.dZ16) for lb in layers]), "ldb": i64([lb.spec.ld for lb in layers]),
-            "C": vp([_p(lb.wpart) for lb in layers]), "ldc": i64([lb.spec.ld for lb in layers]),
-            "M": i32([lb.spec.dense.fin for lb in layers]), "N": i32([lb.spec.ld for lb in layers]),
-            "K": i32([self.mb] * L), "splits": i32([lb.splits for lb in layers]),
-            "stride": i64([lb.spec.dense.fin * lb.spec.ld for lb in layers]),
-            "bias_grad": vp([_p(lb.bpart) for lb in layers]),
+            "A": vp(col(0)), "lda": i64(col(1)), "rows": vp([None] * L), "B": vp(col(2)), "ldb": i64(col(3)),
+            "C": vp(col(4)), "ldc": i64(col(5)), "M": i32(col(6)), "N": i32(col(7)), "K": i32([self.mb] * L),
+            "splits": i32(col(8)), "stride": i64([p[6] * p[5] for p in probs]), "bias_grad": vp(col(9)),
+            "count": L,
         }
         order = ("A", "lda", "rows", "B", "ldb", "C", "ldc", "M", "N", "K", "splits", "stride", "bias_grad")
         g["args"] = [ctypes.addressof(g[k]) for k in order]
@@ -1048,13 +1068,13 @@ class MLPExecutor(ForwardChain):
                   else (None, 0, None, 0, 0))
             self._call("ppo_mlp16_ln_bwd", st, c["L"], _p(top.dY), top.spec.ld, self.mb, c["Wb"], c["Z"],
                        c["mean"], c["rstd"], c["g"], c["be"], c["dZ16"], top.spec.ld, c["part"], c["act"], *hd,
-                       c["z16"])
+                       c["z16"], *c.get("dhead16", (None, 0)))
             if self.DW16_GROUP and len(layers) <= 8:
                 g = c.get("dw_group")
                 if g is None:
-                    g = c["dw_group"] = self._plan_dw_group(layers)
+                    g = c["dw_group"] = self._plan_dw_group(layers, c)
                 g["rows"][0] = idx0
-                self._call("ppo_gemm_bf16s_dw_group", st, len(layers), *g["args"])
+                self._call("ppo_gemm_bf16s_dw_group", st, g["count"], *g["args"])
                 return
             # the first layer's dW fills 198 of the 256 CUs: the later layers'
             # run beside it on the side stream
@@ -1201,7 +1221,10 @@ class MLPExecutor(ForwardChain):
     def _head_back(self, st, layers, dhead, head: DenseSpec, wpart, bpart, splits, hx, ldhx, hidx):
         """Head dW and the cotangent of the head input."""
         top = layers[-1] if layers else None
-        if top is not None and top.Y16 is not None and hidx is None and head.w.ld % 4 == 0:
+        c = layers[0].chain16 if layers else None
+        if c is not None and c.get("dhead16") and self.DW16_GROUP:
+            pass  # the head's dW runs in the trunk's grouped dW launch, after the backward chain
+        elif top is not None and top.Y16 is not None and hidx is None and head.w.ld % 4 == 0:
             # from the bf16 copy of the head input (the same bf16 values the
             # fp32 one rounds to, the same MFMA sequence and split boundaries)
             self._call("ppo_gemm_bf16s", st, A_COL, B_KN, 1, 0, _p(top.Y16), top.spec.ld, None, _p(dhead),
@@ -1211,7 +1234,6 @@ class MLPExecutor(ForwardChain):
             self._gemm(st, A_COL, B_KN, hx, ldhx, hidx, _p(dhead), head.w.ld, _p(wpart), head.w.ld,
                       head.fin, head.w.ld, self.mb, splits, head.fin * head.w.ld, EPI_STORE, None, 0, None, None, 0,
                       _p(bpart), -1)
-        c = layers[0].chain16 if layers else None
         if layers and not (c is not None and c.get("Whb")):  # else the backward chain takes it over
             dst, epi, act, aux, ldaux = self._dx_target(layers[-1])
             self._gemm(st, A_ROW, B_NK, _p(dhead), head.w.ld, None, self.flat.view(head.w),

@@ -276,13 +276,16 @@ int ppo_mlp16_ln_fwd(void* stream, int L, const float* part, int64_t ldp, int64_
  * columns; Whb the head kernel's backward image from
  * ppo_pack_bf16_operand_padded over nh_pad = 32 or 64 outputs), bit-identical
  * to the bf16 head GEMM's.  z16 != 0: Z[l] holds bf16 (ppo_mlp16_ln_fwd's z16
- * output). */
+ * output).  dhead16 (with the head, or NULL): receives the head cotangents
+ * rounded to bf16 [M][lddh16] (zero in columns nh .. lddh16 - 1; lddh16 a
+ * multiple of 8 between nh and nh_pad), the operand of the head's dW in
+ * ppo_gemm_bf16s_dw_group. */
 int ppo_mlp16_ln_bwd_blocks(int rows);
 int ppo_mlp16_ln_bwd(void* stream, int L, const float* dY, int64_t lddy, int M, const void* const* Wb,
                      const float* const* Z, const float* const* mean, const float* const* rstd,
                      const float* const* gamma, const float* const* beta, void* const* dZ16, int64_t ld,
                      float* const* part, int act, const float* dhead, int64_t lddh, const void* Whb, int nh,
-                     int nh_pad, int z16);
+                     int nh_pad, int z16, void* dhead16, int64_t lddh16);
 /* Packs L bf16 kernels W[l] ([K][N], row pitch ldw; the bf16 parameter
  * image) into the MFMA operand images of the bf16 chains: fwd[l] for the
  * contraction over K, bwd[l] (W^T) for the input cotangent's contraction over

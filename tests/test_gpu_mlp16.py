@@ -318,6 +318,7 @@ def bwd_chain(lay, fwd, dY, M, act, head=None, z16=False):
         keep.append(a)
         tabs[k] = p
     hargs = (None, 0, None, 0, 0)
+    d16 = (None, 0)
     dy_ptr = dY.data_ptr() if dY is not None else None
     if head is not None:
         dhead, W16h, nh = head
@@ -328,8 +329,11 @@ def bwd_chain(lay, fwd, dY, M, act, head=None, z16=False):
         keep.append(hpk)
         hargs = (dhead.data_ptr(), nh, hpk[1].data_ptr(), nh, npad)
         dy_ptr = None
+        ld16 = (nh + 7) // 8 * 8
+        out[0]["dhead16"] = torch.full((M, ld16), 7, dtype=torch.int16, device=DEV)
+        d16 = (out[0]["dhead16"].data_ptr(), ld16)
     _lib.call("ppo_mlp16_ln_bwd", st(), L, dy_ptr, F, M, tabs["Wb"], tabs["Z"], tabs["mean"], tabs["rstd"],
-              tabs["g"], tabs["be"], tabs["dZ16"], F, tabs["part"], act, *hargs, int(z16))
+              tabs["g"], tabs["be"], tabs["dZ16"], F, tabs["part"], act, *hargs, int(z16), *d16)
     torch.cuda.synchronize()
     return out
 
@@ -371,6 +375,11 @@ def test_backward_chain_head_cotangent_matches_the_head_gemm(M, L, nh):
     got = bwd_chain(lay, fwd, None, M, 1, head=(dhead, W16h, nh))
     for l in range(L):
         assert torch.equal(got[l]["dZ16"], ref[l]["dZ16"]), (l, (got[l]["dZ16"] != ref[l]["dZ16"]).sum().item())
+    # the bf16 copy of the head cotangents: dhead rounded to nearest even, zero past nh
+    d16 = got[0]["dhead16"]
+    exp = torch.zeros_like(d16)
+    exp[:, :nh] = bits16(dhead[:, :nh])
+    assert torch.equal(d16, exp)
 
 
 def run_update(monkeypatch, chain16, bwd=True):
