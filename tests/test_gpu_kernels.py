@@ -394,7 +394,7 @@ def test_fused_loss_matches_the_oracle(dist, A, spread):
 
 
 # ------------------------------------------------------------------- Adam
-@pytest.mark.parametrize("nparts", [1, 3, 37, 64])
+@pytest.mark.parametrize("nparts", [1, 3, 17, 37, 64, 512])
 def test_grad_reduce_partials(nparts):
     """Partial sums of two segments (ragged counts, padded part strides):
     the reduced gradient and its per-chunk squared norms."""
@@ -402,7 +402,7 @@ def test_grad_reduce_partials(nparts):
     g = np.random.default_rng(nparts)
     chunk = _lib.load().ppo_grad_reduce_chunk_elems()
     specs = [(1000, 1008), (300, 304)]  # (count, part stride)
-    segs, chunks, outs, refs = b"", b"", [], []
+    segs, chunks, outs, refs, parts32 = b"", b"", [], [], []
     keep = []
     for k, (n, stride) in enumerate(specs):
         parts = (g.standard_normal((nparts, stride)) * 0.1).astype(np.float32)
@@ -414,6 +414,7 @@ def test_grad_reduce_partials(nparts):
                            for j, s in enumerate(range(0, n, chunk)))
         outs.append(D)
         refs.append(parts[:, :n].astype(np.float64).sum(0))
+        parts32.append(np.ascontiguousarray(parts[:, :n]))
     nch = len(chunks) // 16
     SEGS = torch.tensor(list(segs), dtype=torch.uint8, device=DEV)
     CH = torch.tensor(list(chunks), dtype=torch.uint8, device=DEV)
@@ -421,11 +422,30 @@ def test_grad_reduce_partials(nparts):
     _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), CH.data_ptr(), nch, 0, SQ.data_ptr())
     torch.cuda.synchronize()
     tot = 0.0
-    for D, ref in zip(outs, refs):
+    for D, ref, p32 in zip(outs, refs, parts32):
         got = host(D).astype(np.float64)
         np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6 * np.sqrt(nparts))
+        # and bit for bit the documented order, in float32: each quarter of the
+        # partials in groups of eight added as a fixed tree, quarters in order
+        np.testing.assert_array_equal(host(D), reduce_order_f32(p32))
         tot += float((got * got).sum())
     np.testing.assert_allclose(host(SQ).sum(), tot, rtol=1e-12)
+
+
+def reduce_order_f32(parts):
+    """ppo_grad_reduce's sum of partials [nparts, n] in its fixed order, in
+    float32 (IEEE round to nearest even, as the kernel's adds)."""
+    P, n = parts.shape
+    z = np.zeros(n, np.float32)
+    t = None
+    for w in range(4):
+        q0, q1 = P * w // 4, P * (w + 1) // 4
+        acc = np.zeros(n, np.float32)
+        for q in range(q0, q1, 8):
+            v = [parts[q + u] if q + u < q1 else z for u in range(8)]
+            acc = acc + (((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7])))
+        t = acc if t is None else t + acc
+    return t
 
 
 def test_grad_reduce_few_part_path_is_bit_identical():
