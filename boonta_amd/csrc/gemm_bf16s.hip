@@ -25,15 +25,18 @@ __global__ void cast_bf16_kernel(const float* __restrict__ x, uint16_t* __restri
 }
 
 // Row-pitched cast: y[r][c] = bf16(x[r][c]) for c < cols, 0 for cols <= c < ldy.
-// One thread per 8 output elements; rows of x are 16-byte aligned.
+// One thread per 8 output elements; rows of x are 16-byte aligned.  IDX:
+// the unit index type (32-bit when rows * ldy / 8 fits, which keeps the
+// row division short), one unit per thread in that case.
+template <typename IDX>
 __global__ void cast_bf16_rows_kernel(const float* __restrict__ x, int64_t ldx, uint16_t* __restrict__ y, int64_t ldy,
                                       int rows, int cols) {
-  const int64_t per_row = ldy / 8;
-  const int64_t total = (int64_t)rows * per_row;
-  for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < total; u += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = u / per_row;
+  const IDX per_row = (IDX)(ldy / 8);
+  const IDX total = (IDX)rows * per_row;
+  for (IDX u = (IDX)blockIdx.x * blockDim.x + threadIdx.x; u < total; u += (IDX)gridDim.x * blockDim.x) {
+    const IDX r = u / per_row;
     const int c = (int)(u - r * per_row) * 8;
-    const float* xr = x + r * ldx;
+    const float* xr = x + (int64_t)r * ldx;
     float v[8];
     if (c + 8 <= cols) {
       const floatx4 a = *reinterpret_cast<const floatx4*>(xr + c);
@@ -52,7 +55,7 @@ __global__ void cast_bf16_rows_kernel(const float* __restrict__ x, int64_t ldx, 
     o.y = pack2(v[2], v[3]);
     o.z = pack2(v[4], v[5]);
     o.w = pack2(v[6], v[7]);
-    *reinterpret_cast<uint4*>(y + r * ldy + c) = o;
+    *reinterpret_cast<uint4*>(y + (int64_t)r * ldy + c) = o;
   }
 }
 
@@ -145,9 +148,15 @@ PPO_EXPORT int ppo_cast_bf16_2d(void* stream, const float* x, int64_t ldx, void*
   if (!x || !y || !aligned16(x) || !aligned16(y))
     return ppo::set_error(PPO_ERR_ARG, "ppo_cast_bf16_2d: buffers must be non-null and 16-byte aligned");
   const int64_t units = (int64_t)rows * (ldy / 8);
-  const int64_t blocks = std::min<int64_t>(ppo::ceil_div64(units, 256), 16384);
-  hipLaunchKernelGGL(cast_bf16_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, ppo::as_stream(stream), x, ldx,
-                     static_cast<uint16_t*>(y), ldy, rows, cols);
+  hipStream_t st = ppo::as_stream(stream);
+  if (units < ((int64_t)1 << 31) - 256) {
+    hipLaunchKernelGGL(cast_bf16_rows_kernel<uint32_t>, dim3((unsigned)ppo::ceil_div64(units, 256)), dim3(256), 0, st,
+                       x, ldx, static_cast<uint16_t*>(y), ldy, rows, cols);
+  } else {
+    const int64_t blocks = std::min<int64_t>(ppo::ceil_div64(units, 256), 16384);
+    hipLaunchKernelGGL(cast_bf16_rows_kernel<int64_t>, dim3((unsigned)blocks), dim3(256), 0, st, x, ldx,
+                       static_cast<uint16_t*>(y), ldy, rows, cols);
+  }
   return ppo::check_launch("ppo_cast_bf16_2d");
 }
 
