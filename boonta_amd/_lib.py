@@ -115,7 +115,9 @@ SIGNATURES = {
     "ppo_grad_reduce_chunk_bytes": (I, []),
     "ppo_grad_reduce_chunk_elems": (I, []),
     "ppo_grad_reduce_few_parts": (I, []),
-    "ppo_grad_reduce": (I, [P, P, P, I, I, P]),
+    "ppo_grad_reduce_wide_parts": (I, []),
+    "ppo_grad_reduce_wide_chunk_elems": (I, []),
+    "ppo_grad_reduce": (I, [P, P, P, I, I, I, P]),
     "ppo_sumsq_total": (I, [P, P, I, P]),
     "ppo_adam_clip_f32": (I, [P, P, P, P, P, P, I64, P, I, D, D, D, D, D, P, I]),
     "ppo_count_advance": (I, [P, P, I]),

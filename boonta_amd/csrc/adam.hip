@@ -56,14 +56,68 @@ constexpr int CHUNK = 256;  // elements per block: one float4 per lane of a wave
 // what the quarter split above gives for so few partials) with four times the
 // loads in flight per block and a quarter of the blocks.
 constexpr int FEW_PARTS = 4;
+//
+// The last nwide chunks (of segments with more than WIDE_PARTS partials, such
+// as a fused head's per-tile partials) cover WIDE_CHUNK elements each: lane l
+// of wave w sums partial range j = 4 w + l / 16 of sixteen equal ranges for
+// float4 l % 16, in groups of eight added as the same fixed tree, and the
+// sixteen range sums are then added in range order.  A long segment's
+// dependent load rounds per lane drop from nparts / 32 to nparts / 128.
+constexpr int WIDE_PARTS = 64;
+constexpr int WIDE_CHUNK = 64;
 
 __global__ void __launch_bounds__(REDUCE_THREADS)
-grad_reduce_kernel(const Segment* __restrict__ segs, const Chunk* __restrict__ chunks, int nfew,
-                   double* __restrict__ sumsq) {
+grad_reduce_kernel(const Segment* __restrict__ segs, const Chunk* __restrict__ chunks, int nchunks, int nfew,
+                   int nwide, double* __restrict__ sumsq) {
   __shared__ floatx4 part[REDUCE_THREADS / 64][64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int few_blocks = (nfew + 3) / 4;
+  const int wide_first = (int)gridDim.x - nwide;  // the wide chunks' blocks come last
+  if ((int)blockIdx.x >= wide_first) {
+    const Chunk ch = chunks[nchunks - nwide + ((int)blockIdx.x - wide_first)];
+    const Segment sg = segs[ch.seg];
+    const int c = lane & 15, j = 4 * wave + (lane >> 4);
+    const int64_t i = ch.start + 4 * c;
+    const bool live = i < sg.count;
+    const int q0 = (sg.nparts * j) / 16, q1 = (sg.nparts * (j + 1)) / 16;
+    constexpr int U = 8;
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (live && q1 > q0) {
+      const float* src = sg.src + i;
+      for (int q = q0; q < q1; q += U) {
+        floatx4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int qq = min(q + u, q1 - 1);
+          v[u] = *reinterpret_cast<const floatx4*>(src + (int64_t)qq * sg.part_stride);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = q + u < q1 ? v[u] : floatx4{0.f, 0.f, 0.f, 0.f};
+        acc += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+      }
+    }
+    part[j >> 2][16 * (j & 3) + c] = acc;  // range j of float4 c
+    __syncthreads();
+    if (wave == 0) {
+      double sq = 0.0;
+      if (lane < 16 && live) {
+        floatx4 t = part[0][lane];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) t += part[r >> 2][16 * (r & 3) + lane];
+        if (sg.flags & SEG_ROUND_BF16) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) t[e] = ppo::bf16_round(t[e]);
+        }
+        *reinterpret_cast<floatx4*>(sg.dst + i) = t;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sq += (double)t[e] * (double)t[e];
+      }
+      sq = ppo::wave_sum_d(sq);
+      if (lane == 0) sumsq[ch.slot] = sq;
+    }
+    return;
+  }
   if ((int)blockIdx.x < few_blocks) {
     const int ci = 4 * blockIdx.x + wave;
     if (ci >= nfew) return;  // this path has no barrier
@@ -250,17 +304,20 @@ PPO_EXPORT int ppo_grad_reduce_chunk_elems(void) { return CHUNK; }
 // Every segment's count, part stride and pointers must be multiples of 4
 // floats (16 bytes): the learner's flat layout guarantees it.
 PPO_EXPORT int ppo_grad_reduce(void* stream, const void* segs, const void* chunks, int nchunks, int nfew,
-                               double* sumsq) {
-  if (nchunks < 0 || nfew < 0 || nfew > nchunks || !segs || !chunks || !sumsq)
-    return ppo::set_error(PPO_ERR_ARG, "ppo_grad_reduce: bad argument (nchunks=%d nfew=%d)", nchunks, nfew);
+                               int nwide, double* sumsq) {
+  if (nchunks < 0 || nfew < 0 || nwide < 0 || nfew + nwide > nchunks || !segs || !chunks || !sumsq)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_grad_reduce: bad argument (nchunks=%d nfew=%d nwide=%d)", nchunks,
+                          nfew, nwide);
   if (nchunks == 0) return PPO_OK;
   const int blocks = (nfew + 3) / 4 + (nchunks - nfew);
   hipLaunchKernelGGL(grad_reduce_kernel, dim3(blocks), dim3(REDUCE_THREADS), 0, ppo::as_stream(stream),
-                     (const Segment*)segs, (const Chunk*)chunks, nfew, sumsq);
+                     (const Segment*)segs, (const Chunk*)chunks, nchunks, nfew, nwide, sumsq);
   return ppo::check_launch("ppo_grad_reduce");
 }
 
 PPO_EXPORT int ppo_grad_reduce_few_parts(void) { return FEW_PARTS; }
+PPO_EXPORT int ppo_grad_reduce_wide_parts(void) { return WIDE_PARTS; }
+PPO_EXPORT int ppo_grad_reduce_wide_chunk_elems(void) { return WIDE_CHUNK; }
 
 // Hyper-parameters arrive as double, as optax receives Python floats: 1 - b is
 // formed in double and rounded once to fp32, like optax's (1 - decay) * g.

@@ -982,18 +982,20 @@ class MLPExecutor(ForwardChain):
         # chunks of few-partial segments first (the kernel's wave-per-chunk
         # path); each keeps its slot in segment order, so the norm's fold
         # order does not depend on the split
-        few_parts = lib.ppo_grad_reduce_few_parts()
-        few, many = [], []
+        few_parts, wide_parts = lib.ppo_grad_reduce_few_parts(), lib.ppo_grad_reduce_wide_parts()
+        wide_chunk = lib.ppo_grad_reduce_wide_chunk_elems()
+        few, many, wide = [], [], []
         for i, (_, _, c, _, n, _) in enumerate(segs):
-            for start in range(0, c, chunk):
-                slot = len(few) + len(many)
-                (few if n <= few_parts else many).append(struct.pack("<iiq", i, slot, start))
-        chunks = few + many
+            dst = few if n <= few_parts else wide if n > wide_parts else many
+            for start in range(0, c, wide_chunk if dst is wide else chunk):
+                slot = len(few) + len(many) + len(wide)
+                dst.append(struct.pack("<iiq", i, slot, start))
+        chunks = few + many + wide
         dev = flat.device
         self.SEGS = torch.tensor(list(seg_bytes), dtype=torch.uint8, device=dev)
         self.CHUNKS = torch.tensor(list(b"".join(chunks)), dtype=torch.uint8, device=dev)
         self.nchunks = len(chunks)
-        self.nfew = len(few)
+        self.nfew, self.nwide = len(few), len(wide)
         self.SUMSQ = torch.zeros(self.nchunks, dtype=torch.float64, device=dev)
         self.SUMSQ1 = torch.zeros(1, dtype=torch.float64, device=dev)
         self.segments = segs
@@ -1334,7 +1336,8 @@ class MLPExecutor(ForwardChain):
         chain = self.chain
         adam = chain.adam
         max_norm = chain.max_grad_norm if chain.max_grad_norm is not None else 0.0
-        self._call("ppo_grad_reduce", st, _p(self.SEGS), _p(self.CHUNKS), self.nchunks, self.nfew, _p(self.SUMSQ))
+        self._call("ppo_grad_reduce", st, _p(self.SEGS), _p(self.CHUNKS), self.nchunks, self.nfew, self.nwide,
+                   _p(self.SUMSQ))
         if self.nchunks <= self.FOLD_NORM_MAX:
             norm, nnorm = _p(self.SUMSQ), self.nchunks
         else:

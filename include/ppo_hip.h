@@ -597,13 +597,20 @@ int ppo_sequence_rows(void* stream, const int32_t* envs, int S, int T, int N, in
  * ppo_grad_reduce_chunk_elems() elements, whose sum of squares lands in
  * sumsq[slot].  The first nfew chunks (0 <= nfew <= nchunks) must belong to
  * segments with at most ppo_grad_reduce_few_parts() partials: they take a
- * path with more loads in flight that gives the same bits.
+ * path with more loads in flight that gives the same bits.  The last nwide
+ * chunks (nfew + nwide <= nchunks) cover ppo_grad_reduce_wide_chunk_elems()
+ * elements each, of segments with more than ppo_grad_reduce_wide_parts()
+ * partials: sixteen partial ranges summed side by side, then added in range
+ * order (a fixed order of its own).
  * The optax count is count_base[0] + step_offset + 1 (device int32). */
 int ppo_grad_reduce_segment_bytes(void);
 int ppo_grad_reduce_chunk_bytes(void);
 int ppo_grad_reduce_chunk_elems(void);
 int ppo_grad_reduce_few_parts(void);
-int ppo_grad_reduce(void* stream, const void* segs, const void* chunks, int nchunks, int nfew, double* sumsq);
+int ppo_grad_reduce_wide_parts(void);
+int ppo_grad_reduce_wide_chunk_elems(void);
+int ppo_grad_reduce(void* stream, const void* segs, const void* chunks, int nchunks, int nfew, int nwide,
+                    double* sumsq);
 /* params_bf16 (may be NULL): receives the bf16 image of the updated parameters. */
 int ppo_adam_clip_f32(void* stream, float* params, const float* grads, float* mu, float* nu, void* params_bf16,
                       int64_t n, const double* sumsq, int nsumsq, double max_norm, double lr, double b1,

@@ -419,7 +419,7 @@ def test_grad_reduce_partials(nparts):
     SEGS = torch.tensor(list(segs), dtype=torch.uint8, device=DEV)
     CH = torch.tensor(list(chunks), dtype=torch.uint8, device=DEV)
     SQ = torch.zeros(nch, dtype=torch.float64, device=DEV)
-    _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), CH.data_ptr(), nch, 0, SQ.data_ptr())
+    _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), CH.data_ptr(), nch, 0, 0, SQ.data_ptr())
     torch.cuda.synchronize()
     tot = 0.0
     for D, ref, p32 in zip(outs, refs, parts32):
@@ -485,7 +485,7 @@ def test_grad_reduce_few_part_path_is_bit_identical():
         SQ = torch.full((nch,), float("nan"), dtype=torch.float64, device=DEV)
         for D in outs:
             D.fill_(float("nan"))
-        _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), CH.data_ptr(), nch, nfew, SQ.data_ptr())
+        _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), CH.data_ptr(), nch, nfew, 0, SQ.data_ptr())
         torch.cuda.synchronize()
         return [host(D).view(np.uint32).copy() for D in outs], host(SQ).view(np.uint64).copy()
 
@@ -497,7 +497,76 @@ def test_grad_reduce_few_part_path_is_bit_identical():
     np.testing.assert_array_equal(ref_sq, got_sq)
     # an nfew past nchunks is rejected before launch
     with pytest.raises(RuntimeError):
-        _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), SEGS.data_ptr(), 2, 3, SEGS.data_ptr())
+        _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), SEGS.data_ptr(), 2, 3, 0, SEGS.data_ptr())
+    with pytest.raises(RuntimeError):
+        _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), SEGS.data_ptr(), 2, 1, 2, SEGS.data_ptr())
+
+
+def reduce_wide_order_f32(parts):
+    """The wide path's order, in float32: sixteen equal partial ranges, each
+    in groups of eight added as the fixed tree, the range sums in order."""
+    P, n = parts.shape
+    z = np.zeros(n, np.float32)
+    t = None
+    for j in range(16):
+        q0, q1 = P * j // 16, P * (j + 1) // 16
+        acc = np.zeros(n, np.float32)
+        for q in range(q0, q1, 8):
+            v = [parts[q + u] if q + u < q1 else z for u in range(8)]
+            acc = acc + (((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7])))
+        t = acc if t is None else t + acc
+    return t
+
+
+def test_grad_reduce_wide_part_path():
+    """Segments with more than ppo_grad_reduce_wide_parts() partials, as the
+    last nwide chunks of ppo_grad_reduce_wide_chunk_elems() elements: the
+    documented sixteen-range order bit for bit in float32 (ragged counts, a
+    bf16-rounded segment), the per-slot squared norms to float64, and a
+    middle-path segment and a few-path segment in the same launch unchanged."""
+    import struct
+    lib = _lib.load()
+    wide_parts, wchunk = lib.ppo_grad_reduce_wide_parts(), lib.ppo_grad_reduce_wide_chunk_elems()
+    chunk, few_parts = lib.ppo_grad_reduce_chunk_elems(), lib.ppo_grad_reduce_few_parts()
+    assert wide_parts == 64 and wchunk == 64
+    g = np.random.default_rng(23)
+    specs = [(3, 520, 520, 0), (37, 1000, 1008, 0), (65, 300, 304, 0), (512, 2304, 2304, 1), (130, 36, 40, 0)]
+    segs, keep, outs, parts32 = b"", [], [], []
+    few, mid, wide = [], [], []
+    for k, (npart, n, stride, rb) in enumerate(specs):
+        parts = (g.standard_normal((npart, stride)) * 0.05).astype(np.float32)
+        P = dev(parts)
+        D = torch.full((n,), float("nan"), device=DEV)
+        keep.append(P)
+        outs.append(D)
+        parts32.append(np.ascontiguousarray(parts[:, :n]))
+        segs += struct.pack("<QQqqii", D.data_ptr(), P.data_ptr(), n, stride, npart, rb)
+        dst = few if npart <= few_parts else wide if npart > wide_parts else mid
+        dst += [(k, s) for s in range(0, n, wchunk if dst is wide else chunk)]
+    order = few + mid + wide
+    nch = len(order)
+    SEGS = torch.tensor(list(segs), dtype=torch.uint8, device=DEV)
+    CH = torch.tensor(list(b"".join(struct.pack("<iiq", k, i, s) for i, (k, s) in enumerate(order))),
+                      dtype=torch.uint8, device=DEV)
+    SQ = torch.full((nch,), float("nan"), dtype=torch.float64, device=DEV)
+    _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), CH.data_ptr(), nch, len(few), len(wide), SQ.data_ptr())
+    torch.cuda.synchronize()
+    sq = host(SQ)
+    for k, ((npart, n, _, rb), D, p32) in enumerate(zip(specs, outs, parts32)):
+        got = host(D)
+        if npart > wide_parts:
+            exp = reduce_wide_order_f32(p32)
+        else:
+            exp = reduce_order_f32(p32)
+        if rb:
+            exp = nets.bf16(exp).astype(np.float32)
+        np.testing.assert_array_equal(got, exp, err_msg=f"segment {k}")
+        for i, (kk, s0) in enumerate(order):
+            if kk != k:
+                continue
+            w = wchunk if npart > wide_parts else chunk
+            blk = got[s0:s0 + w].astype(np.float64)
+            np.testing.assert_allclose(sq[i], (blk * blk).sum(), rtol=1e-12, err_msg=f"segment {k} chunk {s0}")
 
 
 @pytest.mark.parametrize("max_norm, scale", [(0.5, 1.0), (0.5, 1e-3), (0.0, 1.0)])
@@ -520,7 +589,7 @@ def test_grad_reduce_and_adam_match_optax_restatement(max_norm, scale):
     SEGS = torch.tensor(list(segs), dtype=torch.uint8, device=DEV)
     CH = torch.tensor(list(chunks), dtype=torch.uint8, device=DEV)
     SQ = torch.zeros(nch, dtype=torch.float64, device=DEV)
-    _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), CH.data_ptr(), nch, 0, SQ.data_ptr())
+    _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), CH.data_ptr(), nch, 0, 0, SQ.data_ptr())
     count = torch.tensor([6], dtype=torch.int32, device=DEV)
     _lib.call("ppo_adam_clip_f32", st(), P.data_ptr(), Gt.data_ptr(), MU.data_ptr(), NU.data_ptr(), None, n,
               SQ.data_ptr(), nch, max_norm, 3e-4, 0.9, 0.999, 1e-8, count.data_ptr(), 2)
