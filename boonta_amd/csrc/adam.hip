@@ -58,7 +58,8 @@ constexpr int CHUNK = 256;  // elements per block: one float4 per lane of a wave
 constexpr int FEW_PARTS = 4;
 //
 // The last nwide chunks (of segments with more than WIDE_PARTS partials, such
-// as a fused head's per-tile partials) cover WIDE_CHUNK elements each: lane l
+// as a fused head's per-tile partials or LayerNorm row blocks) cover
+// WIDE_CHUNK elements each: lane l
 // of wave w sums partial range j = 4 w + l / 16 of sixteen equal ranges for
 // float4 l % 16, in groups of eight added as the same fixed tree, and the
 // sixteen range sums are then added in range order.  A long segment's
@@ -73,9 +74,11 @@ grad_reduce_kernel(const Segment* __restrict__ segs, const Chunk* __restrict__ c
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int few_blocks = (nfew + 3) / 4;
-  const int wide_first = (int)gridDim.x - nwide;  // the wide chunks' blocks come last
-  if ((int)blockIdx.x >= wide_first) {
-    const Chunk ch = chunks[nchunks - nwide + ((int)blockIdx.x - wide_first)];
+  // the wide chunks' blocks are dispatched first (their partial loops are the
+  // longest), then the few-part blocks, then the others
+  int b = (int)blockIdx.x;
+  if (b < nwide) {
+    const Chunk ch = chunks[nchunks - nwide + b];
     const Segment sg = segs[ch.seg];
     const int c = lane & 15, j = 4 * wave + (lane >> 4);
     const int64_t i = ch.start + 4 * c;
@@ -118,8 +121,9 @@ grad_reduce_kernel(const Segment* __restrict__ segs, const Chunk* __restrict__ c
     }
     return;
   }
-  if ((int)blockIdx.x < few_blocks) {
-    const int ci = 4 * blockIdx.x + wave;
+  b -= nwide;
+  if (b < few_blocks) {
+    const int ci = 4 * b + wave;
     if (ci >= nfew) return;  // this path has no barrier
     const Chunk ch = chunks[ci];
     const Segment sg = segs[ch.seg];
@@ -148,7 +152,7 @@ grad_reduce_kernel(const Segment* __restrict__ segs, const Chunk* __restrict__ c
     if (lane == 0) sumsq[ch.slot] = sq;
     return;
   }
-  const Chunk ch = chunks[nfew + ((int)blockIdx.x - few_blocks)];
+  const Chunk ch = chunks[nfew + (b - few_blocks)];
   const Segment sg = segs[ch.seg];
   const int64_t i = ch.start + 4 * lane;  // first element of this lane's float4
   const bool live = i < sg.count;

@@ -530,7 +530,8 @@ def test_grad_reduce_wide_part_path():
     chunk, few_parts = lib.ppo_grad_reduce_chunk_elems(), lib.ppo_grad_reduce_few_parts()
     assert wide_parts == 64 and wchunk == 64
     g = np.random.default_rng(23)
-    specs = [(3, 520, 520, 0), (37, 1000, 1008, 0), (65, 300, 304, 0), (512, 2304, 2304, 1), (130, 36, 40, 0)]
+    specs = [(3, 520, 520, 0), (12, 1000, 1008, 0), (64, 1000, 1008, 1), (65, 300, 304, 0), (512, 2304, 2304, 1),
+             (130, 36, 40, 0)]
     segs, keep, outs, parts32 = b"", [], [], []
     few, mid, wide = [], [], []
     for k, (npart, n, stride, rb) in enumerate(specs):
