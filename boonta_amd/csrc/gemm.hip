@@ -227,7 +227,8 @@ __global__ void __launch_bounds__(256, 2) gemm_f32_kernel(GemmParams p0) {
     __syncthreads();
   }
 
-  epilogue_f32<MB, NB>(p, acc, bsum, do_bsum, m0 + wm * (BM / 2), n0 + wn * (BN / 2), split, lane);
+  float no_aux[MB * NB * 16];
+  epilogue_f32<MB, NB>(p, acc, bsum, do_bsum, m0 + wm * (BM / 2), n0 + wn * (BN / 2), split, lane, no_aux);
 }
 
 template <int BM, int BN, int BK, bool A_K, bool B_K>

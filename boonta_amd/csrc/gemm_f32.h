@@ -53,9 +53,12 @@ __device__ __forceinline__ GemmParams tower_params(const GemmParams& p, int t) {
 // wn0 through the epilogue EPI with activation ACT (compile-time, so the
 // unrolled element loop holds only their code), and the bias-gradient column
 // sums of B.
-template <int MB, int NB, int EPI, int ACT>
+// PRE: EPI_DACT's aux values of this lane's outputs were loaded earlier by
+// the caller into auxv (block bi, bj at [16 (bi NB + bj) + r]).
+template <int MB, int NB, int EPI, int ACT, bool PRE>
 __device__ __forceinline__ void epilogue_f32_t(const GemmParams& p, floatx16 (&acc)[MB][NB], const float (&bsum)[NB],
-                                               bool do_bsum, int wm0, int wn0, int split, int lane) {
+                                               bool do_bsum, int wm0, int wn0, int split, int lane,
+                                               const float (&auxv)[MB * NB * 16]) {
   const int h = lane >> 5;
   const int l32 = lane & 31;
   float* C = p.C + (int64_t)split * p.c_split_stride;
@@ -78,7 +81,7 @@ __device__ __forceinline__ void epilogue_f32_t(const GemmParams& p, floatx16 (&a
           if (p.pre) p.pre[o] = v;
           v = ppo::act_fwd(ACT, v);
         } else if (EPI == EPI_DACT) {
-          v *= ppo::act_grad(ACT, p.aux[(int64_t)gm * p.ldaux + gn]);
+          v *= ppo::act_grad(ACT, PRE ? auxv[16 * (bi * NB + bj) + r] : p.aux[(int64_t)gm * p.ldaux + gn]);
         }
         C[o] = v;
       }
@@ -95,22 +98,26 @@ __device__ __forceinline__ void epilogue_f32_t(const GemmParams& p, floatx16 (&a
 }
 
 // The epilogue of the launch's kind and activation, chosen once.
-template <int MB, int NB>
+// PRE: EPI_DACT reads auxv (loaded by the caller) instead of p.aux.
+template <int MB, int NB, bool PRE = false>
 __device__ __forceinline__ void epilogue_f32(const GemmParams& p, floatx16 (&acc)[MB][NB], const float (&bsum)[NB],
-                                             bool do_bsum, int wm0, int wn0, int split, int lane) {
-#define PPO_EPI_ACTS(E)                                                                       \
-  switch (p.act) {                                                                            \
-    case ACT_RELU: epilogue_f32_t<MB, NB, E, ACT_RELU>(p, acc, bsum, do_bsum, wm0, wn0, split, lane); break; \
-    case ACT_TANH: epilogue_f32_t<MB, NB, E, ACT_TANH>(p, acc, bsum, do_bsum, wm0, wn0, split, lane); break; \
-    case ACT_SILU: epilogue_f32_t<MB, NB, E, ACT_SILU>(p, acc, bsum, do_bsum, wm0, wn0, split, lane); break; \
-    default: epilogue_f32_t<MB, NB, E, ACT_NONE>(p, acc, bsum, do_bsum, wm0, wn0, split, lane); break;       \
+                                             bool do_bsum, int wm0, int wn0, int split, int lane,
+                                             const float (&auxv)[MB * NB * 16]) {
+#define PPO_EPI_ACTS(E, P)                                                                                  \
+  switch (p.act) {                                                                                          \
+    case ACT_RELU: epilogue_f32_t<MB, NB, E, ACT_RELU, P>(p, acc, bsum, do_bsum, wm0, wn0, split, lane, auxv); break; \
+    case ACT_TANH: epilogue_f32_t<MB, NB, E, ACT_TANH, P>(p, acc, bsum, do_bsum, wm0, wn0, split, lane, auxv); break; \
+    case ACT_SILU: epilogue_f32_t<MB, NB, E, ACT_SILU, P>(p, acc, bsum, do_bsum, wm0, wn0, split, lane, auxv); break; \
+    default: epilogue_f32_t<MB, NB, E, ACT_NONE, P>(p, acc, bsum, do_bsum, wm0, wn0, split, lane, auxv); break;       \
   }
-  if (p.epi == EPI_BIAS_ACT) {
-    PPO_EPI_ACTS(EPI_BIAS_ACT)
+  if (PRE) {
+    PPO_EPI_ACTS(EPI_DACT, true)
+  } else if (p.epi == EPI_BIAS_ACT) {
+    PPO_EPI_ACTS(EPI_BIAS_ACT, false)
   } else if (p.epi == EPI_DACT) {
-    PPO_EPI_ACTS(EPI_DACT)
+    PPO_EPI_ACTS(EPI_DACT, false)
   } else {
-    epilogue_f32_t<MB, NB, EPI_STORE, ACT_NONE>(p, acc, bsum, do_bsum, wm0, wn0, split, lane);
+    epilogue_f32_t<MB, NB, EPI_STORE, ACT_NONE, false>(p, acc, bsum, do_bsum, wm0, wn0, split, lane, auxv);
   }
 #undef PPO_EPI_ACTS
 }

@@ -172,6 +172,21 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_kernel(GemmParams p0) 
   for (int j = 0; j < NB; ++j) bsum[j] = 0.f;
   const bool do_bsum = (p.bias_grad != nullptr) && (tc.m == 0) && (wm == 0);
 
+  // EPI_DACT on one 32 x 32 block per wave: the lane's 16 aux values are
+  // loaded before the main loop (clamped rows / columns read in-range data
+  // for outputs that are not stored), so the epilogue does not wait on them
+  float auxv[MB * NB * 16];
+  const bool pre_aux = MB * NB == 1 && p.epi == EPI_DACT && p.aux != nullptr;
+  if (pre_aux) {
+    const int h = lane >> 5;
+    const int gn = min(n0 + wn * (BN / WN) + (lane & 31), p.N - 1);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int gm = min(m0 + wm * (BM / WM) + 8 * (r >> 2) + 4 * h + (r & 3), p.M - 1);
+      auxv[r] = p.aux[(int64_t)gm * p.ldaux + gn];
+    }
+  }
+
   OpA oa;
   OpB ob;
   oa.init(p.A, p.lda, m0, p.M, A_K ? p.rows : nullptr, wave, lane);
@@ -239,7 +254,10 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_kernel(GemmParams p0) 
     }
   }
 
-  epilogue_f32<MB, NB>(p, acc, bsum, do_bsum, m0 + wm * (BM / WM), n0 + wn * (BN / WN), split, lane);
+  if (pre_aux)
+    epilogue_f32<MB, NB, true>(p, acc, bsum, do_bsum, m0 + wm * (BM / WM), n0 + wn * (BN / WN), split, lane, auxv);
+  else
+    epilogue_f32<MB, NB>(p, acc, bsum, do_bsum, m0 + wm * (BM / WM), n0 + wn * (BN / WN), split, lane, auxv);
 }
 
 template <int BM, int BN, int WM, int WN, bool A_K, bool B_K>

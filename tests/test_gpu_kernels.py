@@ -166,6 +166,7 @@ def gemm_case(a_layout, b_layout, M, N, K, rows_src=None, gather=False, epi=0, a
     assert np.all(np.abs(got - ref) <= 1e-5 * scale), np.abs(got - ref).max()
     if bias_grad:
         np.testing.assert_allclose(host(BG).sum(0), Blog.astype(np.float64).sum(0), rtol=1e-4, atol=1e-3)
+    return C
 
 
 @pytest.mark.parametrize("a_layout, b_layout", [(0, 0), (0, 1), (1, 0), (1, 1)])
@@ -194,6 +195,16 @@ def test_gemm_bias_activation_epilogue(act):
 @pytest.mark.parametrize("act", ["relu", "tanh", "silu"])
 def test_gemm_activation_derivative_epilogue(act):
     gemm_case(0, 1, 300, 256, 136, epi=2, act=act)
+
+
+@pytest.mark.parametrize("act", ["relu", "silu"])
+def test_gemm_activation_derivative_prefetched_aux_is_bit_identical(act):
+    """The 64 x 64 tile loads the activation values of its outputs before its
+    main loop; ragged M and N (clamped rows and columns) and the same bits as
+    the 128 x 128 tile, which reads them in its epilogue."""
+    c64 = gemm_case(0, 1, 300, 200, 136, epi=2, act=act, seed=5, tile=3)
+    c128 = gemm_case(0, 1, 300, 200, 136, epi=2, act=act, seed=5, tile=0)
+    assert torch.equal(c64, c128)
 
 
 def test_silu_and_its_derivative_on_special_and_extreme_arguments():
