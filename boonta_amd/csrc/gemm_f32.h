@@ -53,8 +53,9 @@ __device__ __forceinline__ GemmParams tower_params(const GemmParams& p, int t) {
 // wn0 through the epilogue EPI with activation ACT (compile-time, so the
 // unrolled element loop holds only their code), and the bias-gradient column
 // sums of B.
-// PRE: EPI_DACT's aux values of this lane's outputs were loaded earlier by
-// the caller into auxv (block bi, bj at [16 (bi NB + bj) + r]).
+// PRE: the epilogue's per-lane inputs were loaded earlier by the caller into
+// auxv: EPI_DACT's aux values of this lane's outputs (block bi, bj at
+// [16 (bi NB + bj) + r]), EPI_BIAS_ACT's bias of block column bj at [bj].
 template <int MB, int NB, int EPI, int ACT, bool PRE>
 __device__ __forceinline__ void epilogue_f32_t(const GemmParams& p, floatx16 (&acc)[MB][NB], const float (&bsum)[NB],
                                                bool do_bsum, int wm0, int wn0, int split, int lane,
@@ -69,7 +70,7 @@ __device__ __forceinline__ void epilogue_f32_t(const GemmParams& p, floatx16 (&a
       const int gn = wn0 + bj * 32 + l32;
       const bool n_ok = gn < p.N;
       float bias = 0.f;
-      if (EPI == EPI_BIAS_ACT && p.bias && n_ok) bias = p.bias[gn];
+      if (EPI == EPI_BIAS_ACT && p.bias && n_ok) bias = PRE ? auxv[bj] : p.bias[gn];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int gm = wm0 + bi * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -98,7 +99,7 @@ __device__ __forceinline__ void epilogue_f32_t(const GemmParams& p, floatx16 (&a
 }
 
 // The epilogue of the launch's kind and activation, chosen once.
-// PRE: EPI_DACT reads auxv (loaded by the caller) instead of p.aux.
+// PRE: the bias or the aux values come from auxv (loaded by the caller).
 template <int MB, int NB, bool PRE = false>
 __device__ __forceinline__ void epilogue_f32(const GemmParams& p, floatx16 (&acc)[MB][NB], const float (&bsum)[NB],
                                              bool do_bsum, int wm0, int wn0, int split, int lane,
@@ -110,12 +111,10 @@ __device__ __forceinline__ void epilogue_f32(const GemmParams& p, floatx16 (&acc
     case ACT_SILU: epilogue_f32_t<MB, NB, E, ACT_SILU, P>(p, acc, bsum, do_bsum, wm0, wn0, split, lane, auxv); break; \
     default: epilogue_f32_t<MB, NB, E, ACT_NONE, P>(p, acc, bsum, do_bsum, wm0, wn0, split, lane, auxv); break;       \
   }
-  if (PRE) {
-    PPO_EPI_ACTS(EPI_DACT, true)
-  } else if (p.epi == EPI_BIAS_ACT) {
-    PPO_EPI_ACTS(EPI_BIAS_ACT, false)
+  if (p.epi == EPI_BIAS_ACT) {
+    PPO_EPI_ACTS(EPI_BIAS_ACT, PRE)
   } else if (p.epi == EPI_DACT) {
-    PPO_EPI_ACTS(EPI_DACT, false)
+    PPO_EPI_ACTS(EPI_DACT, PRE)
   } else {
     epilogue_f32_t<MB, NB, EPI_STORE, ACT_NONE, false>(p, acc, bsum, do_bsum, wm0, wn0, split, lane, auxv);
   }

@@ -172,19 +172,32 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_kernel(GemmParams p0) 
   for (int j = 0; j < NB; ++j) bsum[j] = 0.f;
   const bool do_bsum = (p.bias_grad != nullptr) && (tc.m == 0) && (wm == 0);
 
-  // EPI_DACT on one 32 x 32 block per wave: the lane's 16 aux values are
-  // loaded before the main loop (clamped rows / columns read in-range data
-  // for outputs that are not stored), so the epilogue does not wait on them
+  // One 32 x 32 block per wave: the epilogue's inputs are loaded before the
+  // main loop (clamped rows / columns read in-range data for outputs that
+  // are not stored), so the epilogue does not wait on them.  Only in the
+  // layouts of the input-cotangent GEMM (A k-contiguous, B = W read as
+  // [N][K]: EPI_DACT's 16 aux values per lane) and of the forward (A
+  // k-contiguous, B k-outer: EPI_BIAS_ACT's bias), so no other instance
+  // holds registers for them.
+  constexpr bool PRE_DACT = MB * NB == 1 && A_K && B_K;
+  constexpr bool PRE_BIAS = MB * NB == 1 && A_K && !B_K;
   float auxv[MB * NB * 16];
-  const bool pre_aux = MB * NB == 1 && p.epi == EPI_DACT && p.aux != nullptr;
-  if (pre_aux) {
-    const int h = lane >> 5;
-    const int gn = min(n0 + wn * (BN / WN) + (lane & 31), p.N - 1);
+  bool pre_aux = false;
+  const int gn_pre = min(n0 + wn * (BN / WN) + (lane & 31), p.N - 1);
+  if constexpr (PRE_DACT) {
+    pre_aux = p.epi == EPI_DACT && p.aux != nullptr;
+    if (pre_aux) {
+      const int h = lane >> 5;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int gm = min(m0 + wm * (BM / WM) + 8 * (r >> 2) + 4 * h + (r & 3), p.M - 1);
-      auxv[r] = p.aux[(int64_t)gm * p.ldaux + gn];
+      for (int r = 0; r < 16; ++r) {
+        const int gm = min(m0 + wm * (BM / WM) + 8 * (r >> 2) + 4 * h + (r & 3), p.M - 1);
+        auxv[r] = p.aux[(int64_t)gm * p.ldaux + gn_pre];
+      }
     }
+  }
+  if constexpr (PRE_BIAS) {
+    pre_aux = p.epi == EPI_BIAS_ACT && p.bias != nullptr;
+    if (pre_aux) auxv[0] = p.bias[gn_pre];
   }
 
   OpA oa;
