@@ -217,6 +217,18 @@ __global__ void __launch_bounds__(256) adam_kernel(AdamParams a) {
   __shared__ float s_scale_norm[2];
   __shared__ float s_bc[2];
   __shared__ double s_w[4];
+  const int64_t n4 = a.n / 4;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  // the first group's loads go out with the norm partials' loads below, so
+  // the two round trips overlap
+  floatx4 g, m, v, p;
+  if (i < n4) {
+    g = reinterpret_cast<const floatx4*>(a.g)[i];
+    m = reinterpret_cast<floatx4*>(a.mu)[i];
+    v = reinterpret_cast<floatx4*>(a.nu)[i];
+    p = reinterpret_cast<floatx4*>(a.p)[i];
+  }
   // the squared norm from its partials, in a fixed order every block repeats:
   // thread t adds partials t, t + 256, ..., then wave sums, then the four
   // wave totals in wave order
@@ -244,12 +256,13 @@ __global__ void __launch_bounds__(256) adam_kernel(AdamParams a) {
   const float bc1 = s_bc[0], bc2 = s_bc[1];
   const float omb1 = a.omb1, omb2 = a.omb2;
   const float neg_lr = a.neg_lr;
-  const int64_t n4 = a.n / 4;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
-    floatx4 g = reinterpret_cast<const floatx4*>(a.g)[i];
-    floatx4 m = reinterpret_cast<floatx4*>(a.mu)[i];
-    floatx4 v = reinterpret_cast<floatx4*>(a.nu)[i];
-    floatx4 p = reinterpret_cast<floatx4*>(a.p)[i];
+  for (bool first = true; i < n4; i += stride, first = false) {
+    if (!first) {
+      g = reinterpret_cast<const floatx4*>(a.g)[i];
+      m = reinterpret_cast<floatx4*>(a.mu)[i];
+      v = reinterpret_cast<floatx4*>(a.nu)[i];
+      p = reinterpret_cast<floatx4*>(a.p)[i];
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float ge = g[e];
