@@ -233,8 +233,7 @@ __global__ void __launch_bounds__(256) adam_kernel(AdamParams a) {
   // thread t adds partials t, t + 256, ..., then wave sums, then the four
   // wave totals in wave order
   {
-    double t = 0.0;
-    for (int i = threadIdx.x; i < a.nsumsq; i += 256) t += a.sumsq[i];
+    double t = ppo::strided_sum_d<256, 4>(a.sumsq, a.nsumsq, threadIdx.x);
     t = ppo::wave_sum_d(t);
     if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = t;
   }
@@ -294,8 +293,7 @@ constexpr int NORM_THREADS = 1024;
 __global__ void __launch_bounds__(NORM_THREADS) sumsq_total_kernel(const double* __restrict__ sumsq, int n,
                                                                    double* __restrict__ total) {
   __shared__ double w[NORM_THREADS / 64];
-  double t = 0.0;
-  for (int i = threadIdx.x; i < n; i += NORM_THREADS) t += sumsq[i];
+  double t = ppo::strided_sum_d<NORM_THREADS, 8>(sumsq, n, threadIdx.x);
   t = ppo::wave_sum_d(t);
   if ((threadIdx.x & 63) == 0) w[threadIdx.x >> 6] = t;
   __syncthreads();

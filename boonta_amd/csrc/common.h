@@ -139,6 +139,26 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// 0 + x[t] + x[t + S] + x[t + 2 S] + ... (i < n) added in that order, with
+// the loads of U terms in flight at a time (the order, and so the result,
+// of the one-load-per-step loop).
+template <int S, int U>
+__device__ __forceinline__ double strided_sum_d(const double* __restrict__ x, int n, int t) {
+  double acc = 0.0;
+  for (int i = t; i < n; i += S * U) {
+    double v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = i + S * u;
+      v[u] = x[j < n ? j : t];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i + S * u < n) acc += v[u];
+  }
+  return acc;
+}
+
 __device__ __forceinline__ double wave_sum_d(double v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
