@@ -172,15 +172,15 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_kernel(GemmParams p0) 
   for (int j = 0; j < NB; ++j) bsum[j] = 0.f;
   const bool do_bsum = (p.bias_grad != nullptr) && (tc.m == 0) && (wm == 0);
 
-  // One 32 x 32 block per wave: the epilogue's inputs are loaded before the
-  // main loop (clamped rows / columns read in-range data for outputs that
-  // are not stored), so the epilogue does not wait on them.  Only in the
-  // layouts of the input-cotangent GEMM (A k-contiguous, B = W read as
-  // [N][K]: EPI_DACT's 16 aux values per lane) and of the forward (A
-  // k-contiguous, B k-outer: EPI_BIAS_ACT's bias), so no other instance
-  // holds registers for them.
+  // The epilogue's inputs are loaded before the main loop (clamped rows /
+  // columns read in-range data for outputs that are not stored), so the
+  // epilogue does not wait on them.  Only in the layouts of the
+  // input-cotangent GEMM (A k-contiguous, B = W read as [N][K]; one 32 x 32
+  // block per wave: EPI_DACT's 16 aux values per lane) and of the forward
+  // (A k-contiguous, B k-outer: EPI_BIAS_ACT's bias of each block column; the
+  // 64 x 64 and 8-wave tiles), so no other instance holds registers for them.
   constexpr bool PRE_DACT = MB * NB == 1 && A_K && B_K;
-  constexpr bool PRE_BIAS = MB * NB == 1 && A_K && !B_K;
+  constexpr bool PRE_BIAS = A_K && !B_K && (MB * NB == 1 || NW == 8);  // the others would lose occupancy
   float auxv[MB * NB * 16];
   bool pre_aux = false;
   const int gn_pre = min(n0 + wn * (BN / WN) + (lane & 31), p.N - 1);
@@ -197,7 +197,10 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_kernel(GemmParams p0) 
   }
   if constexpr (PRE_BIAS) {
     pre_aux = p.epi == EPI_BIAS_ACT && p.bias != nullptr;
-    if (pre_aux) auxv[0] = p.bias[gn_pre];
+    if (pre_aux) {
+#pragma unroll
+      for (int bj = 0; bj < NB; ++bj) auxv[bj] = p.bias[min(n0 + wn * (BN / WN) + bj * 32 + (lane & 31), p.N - 1)];
+    }
   }
 
   OpA oa;
