@@ -346,6 +346,9 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_fwd_kernel(Fwd16Args 
       bf16x8 hw[HPF];
 #pragma unroll
       for (int s = 0; s < HPF; ++s) hw[s] = *reinterpret_cast<const bf16x8*>(Wj + s * step);
+      const int n = 32 * wave + l32;
+      // the bias goes out with the first kernel chunks, not after the last MFMA
+      const float bh = a.bh ? a.bh[n < a.nh ? n : a.nh - 1] : 0.f;
       floatx16 acc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[r] = 0.f;
@@ -357,9 +360,8 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_fwd_kernel(Fwd16Args 
         if (s + HPF < C16_KSTEPS) hw[s % HPF] = *reinterpret_cast<const bf16x8*>(Wj + (s + HPF) * step);
         __builtin_amdgcn_sched_barrier(0);
       }
-      const int n = 32 * wave + l32;
       if (n < a.nh) {
-        const float bb = a.bh ? ppo::bf16_round(a.bh[n]) : 0.f;
+        const float bb = ppo::bf16_round(bh);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int grow = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
