@@ -49,6 +49,8 @@ def parse():
                     help="other workloads measured in the same run, into the line's 'configs' list: "
                          "'auto' (3,4,5,6 beside the default headline 2), 'none', or a comma list")
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--detail", default=None, metavar="PATH",
+                    help="also write the per-launch tables of every workload (JSON) to PATH")
     ap.add_argument("--profile-only", action="store_true", help="warmup + timed updates only")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (calibrates rocprofv3 FETCH/WRITE_SIZE)")
@@ -293,10 +295,15 @@ def launch_key(name, args):
 
 
 def time_launches(ex, reps, per_update_steps):
-    """Times the launches of (bootstrap + GAE + permutations + one minibatch
-    step) with HIP events on the launching stream: each distinct launch shape
-    once, `reps` back-to-back repetitions, counted as many times as it occurs
-    per update."""
+    """Per-launch durations of one update, each distinct launch of (bootstrap
+    + GAE + permutations + one minibatch step) counted as many times as it
+    occurs per update.
+
+    ``ms``: the launch inside a whole update issued eagerly on one stream,
+    HIP events recorded between consecutive launches (so each launch runs
+    with the caches its predecessors left), averaged over its occurrences.
+    ``ms_alone``: ``reps`` back-to-back repetitions of the launch on the same
+    inputs (its inputs stay in the caches: an optimistic figure)."""
     import torch
     from boonta_amd import _lib
 
@@ -306,13 +313,30 @@ def time_launches(ex, reps, per_update_steps):
     # launches before the first minibatch step: those of an update stopped
     # before it, less its log finalize
     first_mb = len(ex.record(max_steps=0)) - 1
-    rows, seen = [], {}
+    per_step = len(calls) - 1 - first_mb
+    full = ex.record()
+    S = per_update_steps
+    if len(full) != first_mb + S * per_step + 2:
+        raise RuntimeError(f"unexpected launch count per update ({len(full)})")
+    # position of each launch of the whole update in the one-step record
+    pos = list(range(first_mb)) + [first_mb + k % per_step for k in range(S * per_step)] + [len(calls) - 1, None]
+    if any(p is not None and full[k][0] != calls[p][0] for k, p in enumerate(pos)):
+        raise RuntimeError("the minibatch steps of one update do not repeat one launch sequence")
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(full) + 1)]
+    ev[0].record(stream)
+    for k, (name, args) in enumerate(full):
+        _lib.call(name, st, *args[1:])
+        ev[k + 1].record(stream)
+    ev[-1].synchronize()
+    ctx_ms = [ev[k].elapsed_time(ev[k + 1]) for k in range(len(full))]
+    rows, seen, by_pos = [], {}, {}
     for i, (name, args) in enumerate(calls):
         # the logs of every step are finalized once, after the last step
         count = per_update_steps if i >= first_mb and name != "ppo_loss_finalize_steps" else 1
         key = launch_key(name, args)
         if key in seen:
             seen[key]["count"] += count
+            by_pos[i] = seen[key]
             continue
         args = (st,) + tuple(args[1:])
         _lib.call(name, *args)  # warm
@@ -322,12 +346,18 @@ def time_launches(ex, reps, per_update_steps):
             _lib.call(name, *args)
         e1.record(stream)
         e1.synchronize()
-        ms = e0.elapsed_time(e1) / reps
         flops, nbytes = launch_work(name, args)
-        row = {"i": i, "name": name, "ms": ms, "count": count, "flops": flops, "bytes": nbytes,
-               "shape": launch_shape(name, args), "layout": launch_layout(name, args)}
+        row = {"i": i, "name": name, "ms_alone": e0.elapsed_time(e1) / reps, "count": count, "flops": flops,
+               "bytes": nbytes, "shape": launch_shape(name, args), "layout": launch_layout(name, args),
+               "ctx": []}
         rows.append(row)
         seen[key] = row
+        by_pos[i] = row
+    for k, p in enumerate(pos):
+        if p is not None:
+            by_pos[p]["ctx"].append(ctx_ms[k])
+    for r in rows:
+        r["ms"] = sum(r.pop("ctx")) / r["count"]
     return rows
 
 
@@ -402,10 +432,8 @@ def cpu_baseline(recipe, params, tr_dev, budget_s):
     t_update = t_pre + E * M * spent / steps
     unit = f"{N // M} envs x {T} steps" if recipe.recurrent else f"{mb} rows"
     return {"value": B / t_update, "unit": "samples/s", "cores": _cores(), "kind": "port",
-            "sample": f"oracle restatement in float32 numpy: bootstrap forward, GAE over the full [{T},{N}] "
-                      f"rollout and the {E} epoch permutations ({t_pre:.2f} s), plus {steps} of the {E * M} "
-                      f"minibatch steps of {unit} (gather, forward, backward, clip, Adam; {spent:.1f} s), "
-                      f"extrapolated to one update"}
+            "sample": f"float32 numpy oracle: bootstrap, GAE, {E} permutations ({t_pre:.2f} s) + {steps} of "
+                      f"{E * M} minibatch steps of {unit} ({spent:.1f} s), extrapolated to one update"}
 
 
 def _cores() -> int:
@@ -443,10 +471,8 @@ def _cpu_baseline_pupo(recipe, params, plan, cfg, opt, key, budget_s, tr):
         per = (run(k) - t1) / (k - 1) if k > 1 else t1
     t_update = t1 + (E * M - 1) * per
     return {"value": recipe.batch / t_update, "unit": "samples/s", "cores": _cores(), "kind": "port",
-            "sample": f"oracle restatement of RecurrentPuPO.update in float32 numpy: bootstrap and the first "
-                      f"minibatch step ({t1:.2f} s), then {k} steps (each a V-trace over the full "
-                      f"[{recipe.T},{recipe.N}] rollout, the env draw, gather, forward, backward, clip, Adam; "
-                      f"{per:.2f} s per step), extrapolated to {E * M} steps"}
+            "sample": f"float32 numpy oracle of RecurrentPuPO.update: bootstrap + first step ({t1:.2f} s), "
+                      f"{k} steps at {per:.2f} s each, extrapolated to {E * M} steps"}
 
 
 BF16_KERNELS = ("ppo_gemm_bf16", "ppo_gemm_bf16s", "ppo_gemm_bf16s_dw_group", "ppo_mlp16_ln_fwd", "ppo_mlp16_ln_bwd")
@@ -466,6 +492,8 @@ def roofline_of(dom, total, workload):
     roof["kernel"] = f"{dom['name']} layout={dom['layout']} MNK={dom['shape']}"
     roof["traffic"] = measured_traffic(workload, roof["kernel"])
     roof["avg_ms"] = dom["ms"]
+    if "ms_alone" in dom:
+        roof["avg_ms_alone"] = dom["ms_alone"]
     roof["share_of_update"] = dom["ms"] * dom["count"] / total
     return roof
 
@@ -476,7 +504,7 @@ def launch_rows(rows):
     HBM for the rest (frac is null where no algorithmic work is modelled)."""
     out = []
     for r in rows:
-        e = {k: r[k] for k in ("name", "layout", "shape", "ms", "count")}
+        e = {k: r[k] for k in ("name", "layout", "shape", "ms", "ms_alone", "count") if k in r}
         sec = r["ms"] * 1e-3
         peak = PEAK["bf16_mfma"] if r["name"] in BF16_KERNELS else PEAK["fp32_mfma"]
         # the roof a launch meets first: its MFMA time at peak against its HBM time at peak
@@ -488,6 +516,58 @@ def launch_rows(rows):
             e.update(bound=None, achieved=None, frac=None)
         out.append(e)
     return out
+
+
+def _r(x, digits=4):
+    """A float rounded to ``digits`` significant digits (None passes)."""
+    return None if x is None else float(f"{x:.{digits}g}")
+
+
+def short_kernel(label: str) -> str:
+    """'name layout=[1, 0] MNK=[400, 256, 32768]' as 'name [1,0] [400,256,32768]'."""
+    return label.replace("layout=", "").replace("MNK=", "").replace(", ", ",")
+
+
+def compact_roofline(roof: dict) -> dict:
+    """The headline's roofline object without the launch table's detail."""
+    keep = {k: roof[k] for k in ("bound", "unit") if k in roof}
+    keep["kernel"] = short_kernel(roof["kernel"])
+    keep.update({k: _r(roof.get(k)) for k in ("achieved", "peak", "frac", "traffic", "avg_ms", "share_of_update")})
+    return keep
+
+
+def compact_config(m: dict) -> dict:
+    """One extra workload as the headline line carries it."""
+    out = {"workload": m["config"]["workload"], "value": _r(m["value"]), "ms_per_step": _r(m["ms_per_step"])}
+    if "roofline" in m:
+        out["frac"] = _r(m["roofline"]["frac"], 3)
+        out["bound"] = m["roofline"]["bound"]
+        out["kernel"] = short_kernel(m["roofline"]["kernel"])
+    if "cpu_baseline" in m:
+        out["cpu"] = _r(m["cpu_baseline"]["value"])
+    return out
+
+
+def emit(out: dict, args) -> None:
+    """Prints the one-line JSON result on stdout (kept short: the per-launch
+    tables go to stderr, and to --detail when given)."""
+    detail = {"headline": out, "configs": out.pop("_configs_full", [])}
+    line = dict(out)
+    if "launches" in line:
+        line.pop("launches")
+        line.pop("launch_sum_ms", None)
+    if "roofline" in line:
+        line["roofline"] = compact_roofline(line["roofline"])
+    for k in ("value", "ms_per_step"):
+        line[k] = _r(line[k], 6)
+    if "cpu_baseline" in line:
+        line["cpu_baseline"] = dict(line["cpu_baseline"], value=_r(line["cpu_baseline"]["value"]))
+    text = json.dumps(detail)
+    log("detail " + text)
+    if args.detail:
+        with open(args.detail, "w") as f:
+            f.write(text + "\n")
+    print(json.dumps(line, separators=(",", ":")), flush=True)
 
 
 def time_calls(calls, reps, count):
@@ -639,7 +719,7 @@ def step_main(args, recipe, alg, state, params, dev):
                                    "kind": "port",
                                    "sample": f"oracle float64 numpy: {steps} steps of forward + sampling over "
                                              f"{N} envs ({spent:.1f} s)"}
-    print(json.dumps(out), flush=True)
+    emit(out, args)
 
 
 def scan_main(args):
@@ -712,7 +792,7 @@ def scan_main(args):
         out["cpu_baseline"] = {"value": k * t * f / spent, "unit": "elements/s", "cores": 1, "kind": "port",
                                "sample": f"oracle float64 numpy forward + VJP on {k} of the {n} sequences "
                                          f"({spent:.2f} s)"}
-    print(json.dumps(out), flush=True)
+    emit(out, args)
 
 
 def main():
@@ -745,10 +825,10 @@ def main():
            **measure_update(args, args.config, dev, headline=True)}
     extra = also_configs(args)
     if extra:
-        out["configs"] = []
-        for c in extra:
-            out["configs"].append(measure_update(args, c, dev, headline=False))
-    print(json.dumps(out), flush=True)
+        full = [measure_update(args, c, dev, headline=False) for c in extra]
+        out["configs"] = [compact_config(m) for m in full]
+        out["_configs_full"] = full
+    emit(out, args)
 
 
 def algorithm_of(recipe, use_graph: bool):
@@ -810,11 +890,11 @@ def measure_update(args, config: int, dev, headline: bool) -> dict:
         "warmup": args.warmup, "ms_per_step": 1000.0 * elapsed / args.steps, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16" if recipe.network.plan(recipe.obs_dim)["compute_dtype"] == "bfloat16" else "f32",
-        "data": "synthetic (seeded rollout of the workload's distributions, random-init network)",
+        "data": "synthetic seeded rollout, random-init network",
         "config": {"workload": f"config {config}: {recipe.name}", "T": recipe.T, "N": recipe.N,
                    "obs": recipe.obs_dim, "epochs": recipe.cfg.update_epochs,
                    "minibatches": recipe.cfg.num_minibatches, "minibatch": recipe.minibatch,
-                   "global_batch": recipe.batch, "graph": not args.no_graph},
+                   "global_batch": recipe.batch},
     }
     if not args.profile_only:
         ex = alg.executor(state, recipe.T, recipe.N, recipe.obs_dim)

@@ -37,6 +37,8 @@ SIGNATURES = {
     "ppo_fill_f32": (I, [P, P, I64, F]),
     "ppo_threefry_split": (I, [P, P, P, I64]),
     "ppo_permutation_workspace": (SZ, [I64]),
+    "ppo_permutation_bucket_bits": (I, [I64]),
+    "ppo_permutation_bucket_cap": (I, [I64]),
     "ppo_permutation": (I, [P, P, P, I64, P, SZ]),
     "ppo_epoch_permutations_workspace": (SZ, [I, I64]),
     "ppo_epoch_permutations": (I, [P, P, I, I64, P, P, SZ]),
@@ -119,8 +121,8 @@ SIGNATURES = {
     "ppo_grad_reduce_wide_chunk_elems": (I, []),
     "ppo_grad_reduce": (I, [P, P, P, I, I, I, P]),
     "ppo_sumsq_total": (I, [P, P, I, P]),
-    "ppo_adam_clip_f32": (I, [P, P, P, P, P, P, I64, P, I, D, D, D, D, D, P, I]),
-    "ppo_count_advance": (I, [P, P, I]),
+    "ppo_adam_clip_f32": (I, [P, P, P, P, P, P, I64, P, I, D, D, D, D, D, P, I, P]),
+    "ppo_count_advance": (I, [P, P, I, P]),
 }
 
 ACT = {"none": 0, None: 0, "relu": 1, "tanh": 2, "silu": 3}

@@ -31,6 +31,13 @@ class RecurrentPPOConfig(PPOConfig):
     pass
 
 
+class RecurrenceError(RuntimeError):
+    """A one-launch GRU recurrence of an update gave up waiting (its bounded
+    step wait ran out, e.g. because other work held the GPU's compute units).
+    The update's optimizer steps from that point on wrote nothing, so the
+    parameters are those of the last optimizer step before it."""
+
+
 RecurrentPPOState = PPOState
 
 
@@ -78,6 +85,46 @@ class RecurrentPPO(PPO):
                  flags[1], float(temperature), new_carry.data_ptr(), action.data_ptr(), log_prob.data_ptr(),
                  value.data_ptr())
         return state, new_carry, action, {"log_prob": log_prob, "value": value}
+
+    def update(self, state, key, transitions):
+        """RecurrentPPO.update (recurrent_ppo.py:98-281).  Raises
+        RecurrenceError when an earlier update's recurrence is known to have
+        given up (checked without waiting; ``logs`` waits and checks)."""
+        T, N = transitions.second.reward.shape[:2]
+        ex = self.executor(state, T, N, int(transitions.first.obs.shape[-1]))
+        self._check_recurrence(ex, wait=False)
+        state = super().update(state, key, transitions)
+        if ex.seq:
+            # a copy of the error word that a later call reads once it has landed
+            if getattr(ex, "err_host", None) is None:
+                ex.err_host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+                ex.err_event = torch.cuda.Event()
+            ex.err_host.copy_(ex.SEQERR, non_blocking=True)
+            ex.err_event.record()
+            ex.err_pending = True
+        return state
+
+    @staticmethod
+    def _check_recurrence(ex, wait: bool):
+        if not getattr(ex, "err_pending", False):
+            return
+        if not wait and not ex.err_event.query():
+            return
+        ex.err_event.synchronize()
+        ex.err_pending = False
+        if int(ex.err_host[0]) != 0:
+            raise RecurrenceError("a GRU sequence launch gave up waiting for a step of its recurrence: the "
+                                  "update stopped applying optimizer steps at that point")
+
+    def logs(self, state, T: int, N: int, obs_dim: int) -> dict:
+        """The logged scalars of the last update; raises RecurrenceError when
+        its recurrence gave up (its logs then describe no valid update)."""
+        ex = self.executor(state, T, N, obs_dim)
+        self._check_recurrence(ex, wait=True)
+        if ex.recurrence_error():
+            raise RecurrenceError("a GRU sequence launch of the last update gave up waiting for a step of its "
+                                  "recurrence: the update stopped applying optimizer steps at that point")
+        return super().logs(state, T, N, obs_dim)
 
     def _stage(self, transitions, own: dict) -> list:
         f, carry = transitions.first, transitions.carry

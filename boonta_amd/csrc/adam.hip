@@ -211,11 +211,13 @@ struct AdamParams {
   float eps;
   const int* count_base;
   int step_offset;
+  const int* abort_word;  // may be null; nonzero: the step is skipped (nothing written)
 };
 
 __global__ void __launch_bounds__(256) adam_kernel(AdamParams a) {
   __shared__ float s_scale_norm[2];
   __shared__ float s_bc[2];
+  __shared__ int s_abort;
   __shared__ double s_w[4];
   const int64_t n4 = a.n / 4;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -247,9 +249,13 @@ __global__ void __launch_bounds__(256) adam_kernel(AdamParams a) {
       const int count = *a.count_base + a.step_offset + 1;
       s_bc[0] = 1.f - powf(a.b1, (float)count);
       s_bc[1] = 1.f - powf(a.b2, (float)count);
+      s_abort = a.abort_word ? *a.abort_word : 0;
     }
   }
   __syncthreads();
+  // an earlier launch of this update flagged its results unusable: leave the
+  // parameters and moments as they are
+  if (s_abort != 0) return;
   const float norm = s_scale_norm[0];
   const bool clip = s_scale_norm[1] != 0.f;
   const float bc1 = s_bc[0], bc2 = s_bc[1];
@@ -304,8 +310,8 @@ __global__ void __launch_bounds__(NORM_THREADS) sumsq_total_kernel(const double*
   }
 }
 
-__global__ void count_advance_kernel(int* count_base, int steps) {
-  if (threadIdx.x == 0 && blockIdx.x == 0) *count_base += steps;
+__global__ void count_advance_kernel(int* count_base, int steps, const int* abort_word) {
+  if (threadIdx.x == 0 && blockIdx.x == 0 && !(abort_word && *abort_word != 0)) *count_base += steps;
 }
 
 }  // namespace
@@ -339,7 +345,7 @@ PPO_EXPORT int ppo_grad_reduce_wide_chunk_elems(void) { return WIDE_CHUNK; }
 PPO_EXPORT int ppo_adam_clip_f32(void* stream, float* params, const float* grads, float* mu, float* nu,
                                  void* params_bf16, int64_t n, const double* sumsq, int nsumsq, double max_norm,
                                  double lr, double b1, double b2, double eps, const int* count_base,
-                                 int step_offset) {
+                                 int step_offset, const int* abort_word) {
   if (n < 0 || (n % 4) != 0 || !params || !grads || !mu || !nu || !count_base || (nsumsq > 0 && !sumsq) ||
       nsumsq < 0)
     return ppo::set_error(PPO_ERR_ARG, "ppo_adam_clip_f32: bad argument (n=%lld must be a multiple of 4)",
@@ -348,7 +354,8 @@ PPO_EXPORT int ppo_adam_clip_f32(void* stream, float* params, const float* grads
     return ppo::set_error(PPO_ERR_ARG, "ppo_adam_clip_f32: buffers must be 16-byte aligned");
   if (n == 0) return PPO_OK;
   AdamParams a{params, grads, mu, nu, params_bf16, n, sumsq, nsumsq, (float)max_norm, (float)(-lr),
-               (float)b1, (float)b2, (float)(1.0 - b1), (float)(1.0 - b2), (float)eps, count_base, step_offset};
+               (float)b1, (float)b2, (float)(1.0 - b1), (float)(1.0 - b2), (float)eps, count_base, step_offset,
+               abort_word};
   const int blocks = (int)std::min<int64_t>(ppo::ceil_div64(n / 4, 256), 2048);
   hipLaunchKernelGGL(adam_kernel, dim3(blocks), dim3(256), 0, ppo::as_stream(stream), a);
   return ppo::check_launch("ppo_adam_clip_f32");
@@ -362,8 +369,9 @@ PPO_EXPORT int ppo_sumsq_total(void* stream, const double* sumsq, int n, double*
   return ppo::check_launch("ppo_sumsq_total");
 }
 
-PPO_EXPORT int ppo_count_advance(void* stream, int* count_base, int steps) {
+PPO_EXPORT int ppo_count_advance(void* stream, int* count_base, int steps, const int* abort_word) {
   if (!count_base) return ppo::set_error(PPO_ERR_ARG, "ppo_count_advance: null counter");
-  hipLaunchKernelGGL(count_advance_kernel, dim3(1), dim3(64), 0, ppo::as_stream(stream), count_base, steps);
+  hipLaunchKernelGGL(count_advance_kernel, dim3(1), dim3(64), 0, ppo::as_stream(stream), count_base, steps,
+                     abort_word);
   return ppo::check_launch("ppo_count_advance");
 }

@@ -270,9 +270,14 @@ __device__ __forceinline__ float ln_bwd_dz(float g, float xh, float mean_g, floa
 // steps serialise on VCC and cost about four times as much.  An exact
 // product (zero residual) is kept as it is, which keeps the sign of a zero;
 // where the residual is not finite (d or x infinite) the product x * (1 / d)
-// is the quotient (0, +-inf or NaN as the division gives).  Against IEEE
-// x / d on 2M random SiLU arguments, with the reciprocal exact or 1 ulp off
-// either way, it gave the same float every time.
+// is the quotient (0, +-inf or NaN as the division gives).  Error bound: with
+// a reciprocal within 1 ulp of 1 / d, the quotient q is within about 2 ulp
+// and the corrected q1 = q + r (x - d q) within 1 ulp of x / d (faithful);
+// Markstein's correct-rounding result needs a correctly rounded reciprocal,
+// so correct rounding is not proven here.  Observed: on 6M random SiLU
+// arguments it gave the IEEE quotient every time.  Kernels agree with each
+// other bit for bit because all of them divide through this function; the
+// oracle comparison is to a tolerance.
 __device__ __forceinline__ float div_ge1(float x, float d) {
   const float r = __builtin_amdgcn_rcpf(d);
   const float q = x * r;

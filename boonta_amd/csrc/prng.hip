@@ -39,6 +39,12 @@ constexpr int TILE_THREADS = 1024;
 constexpr int SORT_CAP = 2048;      // elements a bucket sorts in LDS
 constexpr int SORT_THREADS = 512;
 constexpr int MAX_BUCKET_BITS = 12;
+// Buckets larger than SORT_CAP go to a second sort launch with room for
+// SORT_CAP2 elements (run only when the expected bucket passes 512 elements,
+// i.e. from 2^21 items per epoch, where the bucket count stops growing);
+// larger ones still are ranked from global memory, exactly but slowly.
+constexpr int SORT_CAP2 = 8192;
+constexpr int SORT_THREADS2 = 1024;
 
 // keys[2*i..2*i+1] = split(key, num)[i]
 __global__ void split_kernel(const uint32_t* __restrict__ key, uint32_t* __restrict__ out, int64_t num) {
@@ -81,6 +87,7 @@ struct ShuffleArgs {
   int bbits;            // bucket bits (0: one bucket)
   int nb;               // 1 << bbits
   int round;
+  int big_pass;         // buckets over SORT_CAP go to a second sort launch
   int32_t* out;         // [E][n]: values in, values out
   uint32_t* keys;       // [E][n]
   uint32_t* hist;       // [E][tiles][nb]
@@ -232,14 +239,18 @@ __global__ void __launch_bounds__(TILE_THREADS) shuffle_scatter_kernel(ShuffleAr
 // scatter into per-sub-bucket ranges whose order inside a range is
 // arbitrary); the pairs are unique, so each one's slot is its sub-bucket's
 // start plus the number of smaller pairs in that sub-bucket (about
-// m / 256 compares, not m).
+// m / 256 compares, not m).  The first launch (CAP = SORT_CAP) takes the
+// buckets that fit it; the second (CAP = SORT_CAP2, only when a.big_pass)
+// the ones from SORT_CAP + 1 to SORT_CAP2 elements; whichever launch is last
+// ranks larger buckets from global memory.
 constexpr int SUB_BITS = 8;
 constexpr int SUB = 1 << SUB_BITS;
-constexpr int SORT_PER = SORT_CAP / SORT_THREADS;
 
-__global__ void __launch_bounds__(SORT_THREADS) shuffle_sort_kernel(ShuffleArgs a) {
-  __shared__ uint64_t sk[SORT_CAP];
-  __shared__ int32_t sv[SORT_CAP];
+template <int CAP, int THREADS, int MIN_M>
+__global__ void __launch_bounds__(THREADS) shuffle_sort_kernel(ShuffleArgs a) {
+  constexpr int PER = CAP / THREADS;
+  __shared__ uint64_t sk[CAP];
+  __shared__ int32_t sv[CAP];
   __shared__ uint32_t cnt[SUB];
   __shared__ uint32_t start[SUB + 1];
   const int tid = threadIdx.x;
@@ -250,24 +261,24 @@ __global__ void __launch_bounds__(SORT_THREADS) shuffle_sort_kernel(ShuffleArgs 
   const int m = (int)(t - s);
   const int64_t eo = (int64_t)e * a.n;
   int32_t* out = a.out + eo;
-  if (m <= 0) return;
-  if (m <= SORT_CAP) {
+  if (m <= MIN_M) return;  // empty, or sorted by the first launch
+  if (m <= CAP) {
     const int shift = 32 - a.bbits - SUB_BITS;
-    for (int d = tid; d < SUB; d += SORT_THREADS) cnt[d] = 0;
+    for (int d = tid; d < SUB; d += THREADS) cnt[d] = 0;
     __syncthreads();
-    uint64_t kk[SORT_PER];
-    int32_t vv[SORT_PER];
+    uint64_t kk[PER];
+    int32_t vv[PER];
 #pragma unroll
-    for (int q = 0; q < SORT_PER; ++q) {
-      const int i = tid + q * SORT_THREADS;
+    for (int q = 0; q < PER; ++q) {
+      const int i = tid + q * THREADS;
       const int ic = i < m ? i : m - 1;
       const uint4 rec = a.trec[eo + s + ic];
       kk[q] = ((uint64_t)rec.x << 32) | (uint64_t)rec.y;
       vv[q] = (int32_t)rec.z;
     }
 #pragma unroll
-    for (int q = 0; q < SORT_PER; ++q)
-      if (tid + q * SORT_THREADS < m) atomicAdd(&cnt[(uint32_t)(kk[q] >> (32 + shift)) & (SUB - 1)], 1u);
+    for (int q = 0; q < PER; ++q)
+      if (tid + q * THREADS < m) atomicAdd(&cnt[(uint32_t)(kk[q] >> (32 + shift)) & (SUB - 1)], 1u);
     __syncthreads();
     // exclusive scan of the SUB counts by the first wave (SUB / 64 per lane)
     if (tid < 64) {
@@ -293,18 +304,18 @@ __global__ void __launch_bounds__(SORT_THREADS) shuffle_sort_kernel(ShuffleArgs 
       if (tid == 63) start[SUB] = inc;
     }
     __syncthreads();
-    for (int d = tid; d < SUB; d += SORT_THREADS) cnt[d] = start[d];  // cursors
+    for (int d = tid; d < SUB; d += THREADS) cnt[d] = start[d];  // cursors
     __syncthreads();
 #pragma unroll
-    for (int q = 0; q < SORT_PER; ++q) {
-      if (tid + q * SORT_THREADS < m) {
+    for (int q = 0; q < PER; ++q) {
+      if (tid + q * THREADS < m) {
         const uint32_t p = atomicAdd(&cnt[(uint32_t)(kk[q] >> (32 + shift)) & (SUB - 1)], 1u);
         sk[p] = kk[q];
         sv[p] = vv[q];
       }
     }
     __syncthreads();
-    for (int i = tid; i < m; i += SORT_THREADS) {
+    for (int i = tid; i < m; i += THREADS) {
       const uint64_t ki = sk[i];
       const uint32_t d = (uint32_t)(ki >> (32 + shift)) & (SUB - 1);
       const int j1 = (int)start[d + 1];
@@ -312,9 +323,9 @@ __global__ void __launch_bounds__(SORT_THREADS) shuffle_sort_kernel(ShuffleArgs 
       for (int j = (int)start[d]; j < j1; ++j) rank += sk[j] < ki;
       out[s + rank] = sv[i];
     }
-  } else {
+  } else if (MIN_M > 0 || !a.big_pass) {
     // rank by counting from global memory: exact for any size
-    for (int i = tid; i < m; i += SORT_THREADS) {
+    for (int i = tid; i < m; i += THREADS) {
       const uint4 ri = a.trec[eo + s + i];
       const uint64_t ki = ((uint64_t)ri.x << 32) | (uint64_t)ri.y;
       int rank = 0;
@@ -339,6 +350,10 @@ int bucket_bits(int64_t n) {
   while (b < MAX_BUCKET_BITS && (n >> b) > 512) ++b;
   return b;
 }
+
+// Whether the second sort launch runs: the expected bucket holds more than
+// 512 elements (the bucket count has stopped growing).
+bool big_pass(int64_t n) { return (n >> bucket_bits(n)) > 512; }
 
 size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
 
@@ -393,6 +408,7 @@ int shuffle_impl(hipStream_t st, const uint32_t* key, int split_epochs, int epoc
   a.tiles = (int)ppo::ceil_div64(n, TILE);
   a.bbits = bucket_bits(n);
   a.nb = 1 << a.bbits;
+  a.big_pass = big_pass(n) ? 1 : 0;
   a.out = out; a.keys = sp.keys; a.hist = sp.hist; a.bstart = sp.bstart;
   a.trec = sp.trec;
   const size_t shm = sizeof(uint32_t) * a.nb;
@@ -401,7 +417,11 @@ int shuffle_impl(hipStream_t st, const uint32_t* key, int split_epochs, int epoc
     hipLaunchKernelGGL(shuffle_bits_kernel, dim3(a.tiles, epochs), dim3(TILE_THREADS), shm, st, a);
     hipLaunchKernelGGL(shuffle_scan_kernel, dim3(epochs), dim3(SCAN_THREADS), shm, st, a);
     hipLaunchKernelGGL(shuffle_scatter_kernel, dim3(a.tiles, epochs), dim3(TILE_THREADS), shm, st, a);
-    hipLaunchKernelGGL(shuffle_sort_kernel, dim3(a.nb, epochs), dim3(SORT_THREADS), 0, st, a);
+    hipLaunchKernelGGL((shuffle_sort_kernel<SORT_CAP, SORT_THREADS, 0>), dim3(a.nb, epochs), dim3(SORT_THREADS), 0,
+                       st, a);
+    if (a.big_pass)
+      hipLaunchKernelGGL((shuffle_sort_kernel<SORT_CAP2, SORT_THREADS2, SORT_CAP>), dim3(a.nb, epochs),
+                         dim3(SORT_THREADS2), 0, st, a);
   }
   return ppo::check_launch("ppo_permutation");
 }
@@ -443,6 +463,11 @@ static int scratch_address(void** out) {
 }
 
 PPO_EXPORT size_t ppo_permutation_workspace(int64_t n) { return space_bytes(1, n); }
+
+// The bucket sort's plan for n items (host only): bucket count bits, and the
+// largest bucket sorted in LDS (larger ones are ranked from global memory).
+PPO_EXPORT int ppo_permutation_bucket_bits(int64_t n) { return n > 0 ? bucket_bits(n) : 0; }
+PPO_EXPORT int ppo_permutation_bucket_cap(int64_t n) { return n > 0 && big_pass(n) ? SORT_CAP2 : SORT_CAP; }
 
 PPO_EXPORT int ppo_threefry_split(void* stream, const uint32_t* key, uint32_t* out, int64_t num) {
   if (num < 0 || !key || !out) return ppo::set_error(PPO_ERR_ARG, "ppo_threefry_split: bad argument");

@@ -1323,7 +1323,12 @@ class MLPExecutor(ForwardChain):
                 self._minibatch(st, idx, step, obs, ldo, dist, A)
                 self._optimizer_step(st, step)
         self._finish_logs(st, self.E * self.M)
-        self._call("ppo_count_advance", st, _p(self.flat.count), self.E * self.M)
+        self._call("ppo_count_advance", st, _p(self.flat.count), self.E * self.M, self._abort_word())
+
+    def _abort_word(self):
+        """Device int32 that, when nonzero, makes the optimizer steps and the
+        count advance of this update write nothing (None: no such word)."""
+        return None
 
     # Up to this many norm partials every Adam block folds itself (all 256
     # threads, about 16 loads each at most); above it one block folds them
@@ -1345,7 +1350,7 @@ class MLPExecutor(ForwardChain):
             norm, nnorm = _p(self.SUMSQ1), 1
         self._call("ppo_adam_clip_f32", st, _p(self.flat.P), _p(self.flat.G), _p(self.flat.MU), _p(self.flat.NU),
                    _p(self.P16) if self.obs16 else None, self.flat.P.numel(), norm, nnorm, float(max_norm),
-                   adam.learning_rate, adam.b1, adam.b2, adam.eps, _p(self.flat.count), step)
+                   adam.learning_rate, adam.b1, adam.b2, adam.eps, _p(self.flat.count), step, self._abort_word())
         if self.obs16:
             self._pack16(st)
 

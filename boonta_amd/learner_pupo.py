@@ -61,6 +61,7 @@ class PuPOExecutor(RecurrentExecutor):
         S = self.E * self.M
         if not self.trunk:
             raise NotImplementedError("the recurrent learner needs an MLP feature extractor before the GRU")
+        self._clear_recurrence_error(st)
         self._bootstrap(st)
         self._call("ppo_fill_f32", st, _p(self.RATIO), N * T, 1.0)
         self._call("ppo_threefry_split", st, _p(self.KEY), _p(self.KEYS), S)
@@ -82,4 +83,4 @@ class PuPOExecutor(RecurrentExecutor):
             self._sequence_minibatch(st, rows, envs, step)
             self._optimizer_step(st, step)
         self._finish_logs(st, S)
-        self._call("ppo_count_advance", st, _p(self.flat.count), S)
+        self._call("ppo_count_advance", st, _p(self.flat.count), S, self._abort_word())

@@ -96,9 +96,21 @@ class RecurrentExecutor(MLPExecutor):
         return (Bm + 15) // 16 * (H // 16) <= _lib.load().ppo_gru_seq_max_workgroups()
 
     def recurrence_error(self) -> bool:
-        """True when a wait of a one-launch recurrence gave up (the update's
-        results are then not to be used); reading it synchronizes."""
+        """True when a wait of a one-launch recurrence of the last update gave
+        up; reading it synchronizes.  From that launch on, the update's
+        optimizer steps and its count advance wrote nothing (their abort word
+        is this error word), so the parameters are those of the last step
+        before it."""
         return bool(self.seq and int(self.SEQERR.item()) != 0)
+
+    def _abort_word(self):
+        return _p(self.SEQERR) if self.seq else None
+
+    def _clear_recurrence_error(self, st):
+        """Zeroes the error word at the start of an update, with a kernel (a
+        memset node in a replayed graph is avoided on purpose)."""
+        if self.seq:
+            self._call("ppo_fill_f32", st, _p(self.SEQERR), 1, 0.0)
 
     def _extra_input_buffers(self) -> dict:
         """first.terminated / first.truncated [T, N] and the carry sequence
@@ -143,6 +155,7 @@ class RecurrentExecutor(MLPExecutor):
         T, N, mb, Bm = self.T, self.N, self.mb, self.Bm
         if not self.trunk:
             raise NotImplementedError("the recurrent learner needs an MLP feature extractor before the GRU")
+        self._clear_recurrence_error(st)
         # 1. bootstrap: the two-step tail sequence from carry[-1]
         self._bootstrap(st)
         # 2. GAE
@@ -166,7 +179,7 @@ class RecurrentExecutor(MLPExecutor):
                 self._sequence_minibatch(st, rows, envs, step)
                 self._optimizer_step(st, step)
         self._finish_logs(st, self.E * self.M)
-        self._call("ppo_count_advance", st, _p(self.flat.count), self.E * self.M)
+        self._call("ppo_count_advance", st, _p(self.flat.count), self.E * self.M, self._abort_word())
 
     def _bootstrap(self, st):
         """Value of second.obs[-1]: the two-step tail sequence (first[-1],

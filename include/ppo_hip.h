@@ -96,6 +96,12 @@ int ppo_fill_f32(void* stream, float* a, int64_t n, float value);
  * threefry2x32, partitionable).  key: device uint32[2] key data. */
 int ppo_threefry_split(void* stream, const uint32_t* key, uint32_t* out, int64_t num);
 size_t ppo_permutation_workspace(int64_t n);
+/* The bucket sort's plan for n items (host only, no launch): the bucket count
+ * is 2^ppo_permutation_bucket_bits(n); buckets of up to
+ * ppo_permutation_bucket_cap(n) items are sorted in LDS, larger ones (not
+ * expected below 2^24 items) are ranked from global memory. */
+int ppo_permutation_bucket_bits(int64_t n);
+int ppo_permutation_bucket_cap(int64_t n);
 int ppo_permutation(void* stream, const uint32_t* key, int32_t* out, int64_t n, void* workspace,
                     size_t workspace_bytes);
 size_t ppo_epoch_permutations_workspace(int epochs, int64_t n);
@@ -611,14 +617,19 @@ int ppo_grad_reduce_wide_parts(void);
 int ppo_grad_reduce_wide_chunk_elems(void);
 int ppo_grad_reduce(void* stream, const void* segs, const void* chunks, int nchunks, int nfew, int nwide,
                     double* sumsq);
-/* params_bf16 (may be NULL): receives the bf16 image of the updated parameters. */
+/* params_bf16 (may be NULL): receives the bf16 image of the updated parameters.
+ * abort_word (may be NULL): a device int32; when it is nonzero at the time the
+ * launch runs (e.g. the error word of a GRU sequence launch of this update
+ * whose bounded wait gave up), the step writes nothing, so parameters and
+ * moments keep their values. */
 int ppo_adam_clip_f32(void* stream, float* params, const float* grads, float* mu, float* nu, void* params_bf16,
                       int64_t n, const double* sumsq, int nsumsq, double max_norm, double lr, double b1,
-                      double b2, double eps, const int* count_base, int step_offset);
+                      double b2, double eps, const int* count_base, int step_offset, const int* abort_word);
 /* total[0] = sum of sumsq[0..n) in a fixed order (one block of 1024 threads):
  * the squared global norm, handed to ppo_adam_clip_f32 as one partial. */
 int ppo_sumsq_total(void* stream, const double* sumsq, int n, double* total);
-int ppo_count_advance(void* stream, int* count_base, int steps);
+/* count_base[0] += steps, unless abort_word (may be NULL) is nonzero. */
+int ppo_count_advance(void* stream, int* count_base, int steps, const int* abort_word);
 
 #ifdef __cplusplus
 }

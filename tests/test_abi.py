@@ -43,7 +43,7 @@ def test_argument_errors_are_reported_not_launched():
                           0, None, -1)
     assert rc == -1
     assert lib.ppo_adam_clip_f32(None, None, None, None, None, None, 6, None, 0, 0.5, 1e-3, 0.9, 0.999, 1e-8,
-                                 None, 0) == -1
+                                 None, 0, None) == -1
 
 
 def test_sampling_rejects_unsupported_sizes_without_launching():
@@ -96,3 +96,15 @@ def test_vtrace_rejects_a_short_ratio_pitch_without_launching():
     lib = _lib.load()
     assert lib.ppo_vtrace_f32(None, 1, 1, 1, 1, 1, 1, 3, 1.0, 1.0, 1, 1, 4, 8, 0.99, 0.95, 0) == -1
     assert b"ppo_vtrace_f32" in lib.ppo_last_error()
+
+
+def test_permutation_buckets_fit_the_lds_sort_at_large_sizes():
+    """Up to 2^24 items per epoch the expected bucket (n / 2^bits) plus six
+    standard deviations of its Poisson count stays within the LDS sort's
+    capacity, so the global-memory ranking is not expected to run."""
+    lib = _lib.load()
+    for e in range(1, 25):
+        for n in ((1 << e) - 1, 1 << e, 3 << (e - 1)):
+            bits, cap = lib.ppo_permutation_bucket_bits(n), lib.ppo_permutation_bucket_cap(n)
+            mean = n / (1 << bits)
+            assert mean + 6 * mean ** 0.5 <= cap or n <= cap, (n, bits, cap)

@@ -165,3 +165,55 @@ def test_recurrent_update_with_sequence_launches_equals_the_step_launches(use_gr
         results.append((flat_state_of(state).P.cpu().clone(), ex.LOGS.cpu().clone()))
     assert torch.equal(results[0][0], results[1][0])
     assert torch.equal(results[0][1], results[1][1])
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_an_update_whose_recurrence_gave_up_keeps_its_parameters_and_raises(use_graph):
+    """A recurrence forced to give up (spin limit 0, set from the host): the
+    update's optimizer steps and count advance write nothing, logs() raises,
+    and so does the next update once the error word's copy has landed; the
+    update after that runs again."""
+    from boonta_amd.algorithms import RecurrenceError
+    from boonta_amd.algorithms.ppo import flat_state_of
+    from boonta_amd.algorithms.recurrent_ppo import RecurrentPPO
+    from boonta_amd.learner_rnn import RecurrentExecutor
+    from boonta_amd.random import key as make_key
+    from ppo_cases import device_recurrent_transition, make_recurrent_case
+
+    class GivesUp(RecurrentExecutor):
+        SEQ_SPIN = 0
+
+    class GivesUpPPO(RecurrentPPO):
+        executor_class = GivesUp
+
+    r, plan, params, tr, roll, extra = make_recurrent_case(4, T=16, N=256, M=4, E=2, seed=3)
+    alg = GivesUpPPO(cfg=r.cfg, network=r.network, optimizer=r.optimizer, use_graph=use_graph)
+    state = alg.init_from_params({"params": params}, r.obs_dim)
+    ex = alg.executor(state, r.T, r.N, r.obs_dim)
+    assert ex.seq
+    flat = flat_state_of(state)
+    p0, count0 = flat.P.clone(), int(flat.count.item())
+    trans = device_recurrent_transition(tr, roll, extra)
+    alg.update(state, make_key(1), trans)
+    torch.cuda.synchronize()
+    assert ex.recurrence_error()
+    assert torch.equal(flat.P, p0)
+    assert int(flat.count.item()) == count0
+    with pytest.raises(RecurrenceError):
+        alg.logs(state, r.T, r.N, r.obs_dim)
+    # the next update learns of it from the error word's copy without waiting
+    alg.update(state, make_key(2), trans)
+    torch.cuda.synchronize()
+    with pytest.raises(RecurrenceError):
+        alg.update(state, make_key(3), trans)
+    # a healthy spin limit: the error word is cleared at the start of the update
+    ex.SEQ_SPIN = RecurrentExecutor.SEQ_SPIN
+    if use_graph:
+        ex.graphs.clear()   # the captured update holds the spin limit it was captured with
+    alg.update(state, make_key(4), trans)
+    torch.cuda.synchronize()
+    assert not ex.recurrence_error()
+    assert not torch.equal(flat.P, p0)
+    assert int(flat.count.item()) == count0 + r.cfg.update_epochs * r.cfg.num_minibatches
+    logs = alg.logs(state, r.T, r.N, r.obs_dim)
+    assert all(np.isfinite(v).all() for v in logs.values())

@@ -102,7 +102,8 @@ def test_permutation_is_bit_exact(n):
     np.testing.assert_array_equal(got, prng.permutation(k, n))
 
 
-@pytest.mark.parametrize("E, n", [(4, 512), (4, 65536), (4, 262144), (4, 1024), (3, 1), (2, 5000), (1, 2000000)])
+@pytest.mark.parametrize("E, n", [(4, 512), (4, 65536), (4, 262144), (4, 1024), (3, 1), (2, 5000), (1, 2000000),
+                                  (1, 1 << 23)])
 def test_epoch_permutations_are_bit_exact(E, n):
     k = prng.key(7 * n + E)
     K = dev(k.view(np.int32))
@@ -604,7 +605,7 @@ def test_grad_reduce_and_adam_match_optax_restatement(max_norm, scale):
     _lib.call("ppo_grad_reduce", st(), SEGS.data_ptr(), CH.data_ptr(), nch, 0, 0, SQ.data_ptr())
     count = torch.tensor([6], dtype=torch.int32, device=DEV)
     _lib.call("ppo_adam_clip_f32", st(), P.data_ptr(), Gt.data_ptr(), MU.data_ptr(), NU.data_ptr(), None, n,
-              SQ.data_ptr(), nch, max_norm, 3e-4, 0.9, 0.999, 1e-8, count.data_ptr(), 2)
+              SQ.data_ptr(), nch, max_norm, 3e-4, 0.9, 0.999, 1e-8, count.data_ptr(), 2, None)
     grad = parts.astype(np.float64).sum(0)
     # absolute floors: fp32 rounding of the operands (|parts| <= ~0.05, |b1 mu| ~ 1e-3,
     # |b2 nu| ~ 1e-5), which exceed the result where terms cancel
@@ -621,9 +622,26 @@ def test_grad_reduce_and_adam_match_optax_restatement(max_norm, scale):
     _lib.call("ppo_sumsq_total", st(), SQ.data_ptr(), nch, SQ1.data_ptr())
     P2, MU2, NU2 = dev(p0), dev(mu0), dev(nu0)
     _lib.call("ppo_adam_clip_f32", st(), P2.data_ptr(), Gt.data_ptr(), MU2.data_ptr(), NU2.data_ptr(), None, n,
-              SQ1.data_ptr(), 1, max_norm, 3e-4, 0.9, 0.999, 1e-8, count.data_ptr(), 2)
+              SQ1.data_ptr(), 1, max_norm, 3e-4, 0.9, 0.999, 1e-8, count.data_ptr(), 2, None)
     np.testing.assert_allclose(host(SQ1)[0], host(SQ).sum(), rtol=1e-14)
     np.testing.assert_allclose(host(P2), new["w"], rtol=1e-6, atol=1e-7)
+    # an abort word of zero changes nothing; a nonzero one leaves p, mu, nu (and
+    # the bf16 image) as they were, and holds the count
+    for word in (0, 3):
+        W = torch.tensor([word], dtype=torch.int32, device=DEV)
+        P3, MU3, NU3 = dev(p0), dev(mu0), dev(nu0)
+        IMG = torch.full((n,), 7, dtype=torch.int16, device=DEV)
+        _lib.call("ppo_adam_clip_f32", st(), P3.data_ptr(), Gt.data_ptr(), MU3.data_ptr(), NU3.data_ptr(),
+                  IMG.data_ptr(), n, SQ1.data_ptr(), 1, max_norm, 3e-4, 0.9, 0.999, 1e-8, count.data_ptr(), 2,
+                  W.data_ptr())
+        C = torch.tensor([6], dtype=torch.int32, device=DEV)
+        _lib.call("ppo_count_advance", st(), C.data_ptr(), 32, W.data_ptr())
+        torch.cuda.synchronize()
+        if word == 0:
+            assert torch.equal(P3, P2) and int(C.item()) == 38
+        else:
+            assert np.array_equal(host(P3), p0) and np.array_equal(host(MU3), mu0)
+            assert np.array_equal(host(NU3), nu0) and bool((IMG == 7).all()) and int(C.item()) == 6
 
 
 @pytest.mark.parametrize("n", [0, 1, 1023, 1024, 18700])
