@@ -299,11 +299,13 @@ def time_launches(ex, reps, per_update_steps):
     + GAE + permutations + one minibatch step) counted as many times as it
     occurs per update.
 
-    ``ms``: the launch inside a whole update issued eagerly on one stream,
-    HIP events recorded between consecutive launches (so each launch runs
-    with the caches its predecessors left), averaged over its occurrences.
-    ``ms_alone``: ``reps`` back-to-back repetitions of the launch on the same
-    inputs (its inputs stay in the caches: an optimistic figure)."""
+    ``ms_bracketed``: the launch inside a whole update issued eagerly on one
+    stream, HIP events recorded between consecutive launches (so each launch
+    runs with the caches its predecessors left), averaged over its
+    occurrences; each interval also holds the launch's share of the gaps
+    between eager launches.  ``ms_alone``: ``reps`` back-to-back repetitions
+    of the launch on the same inputs (its inputs stay in the caches: an
+    optimistic figure).  Returns (rows, launches per update)."""
     import torch
     from boonta_amd import _lib
 
@@ -357,8 +359,20 @@ def time_launches(ex, reps, per_update_steps):
         if p is not None:
             by_pos[p]["ctx"].append(ctx_ms[k])
     for r in rows:
-        r["ms"] = sum(r.pop("ctx")) / r["count"]
-    return rows
+        r["ms_bracketed"] = sum(r.pop("ctx")) / r["count"]
+    return rows, len(full)
+
+
+def in_update_durations(rows, launches: int, ms_per_update: float) -> float:
+    """Sets each row's ``ms``: its bracketed interval less the mean per-launch
+    excess of the bracketed eager update over the replayed graph's update,
+    (sum of the intervals - ms_per_update) / launches, i.e. the time the
+    launch takes inside the replayed update.  Returns that excess (ms)."""
+    total = sum(r["ms_bracketed"] * r["count"] for r in rows)
+    excess = max(0.0, (total - ms_per_update) / launches)
+    for r in rows:
+        r["ms"] = max(r["ms_bracketed"] - excess, 1e-6)
+    return excess
 
 
 def cpu_baseline(recipe, params, tr_dev, budget_s):
@@ -492,8 +506,9 @@ def roofline_of(dom, total, workload):
     roof["kernel"] = f"{dom['name']} layout={dom['layout']} MNK={dom['shape']}"
     roof["traffic"] = measured_traffic(workload, roof["kernel"])
     roof["avg_ms"] = dom["ms"]
-    if "ms_alone" in dom:
-        roof["avg_ms_alone"] = dom["ms_alone"]
+    for k in ("ms_bracketed", "ms_alone"):
+        if k in dom:
+            roof["avg_" + k] = dom[k]
     roof["share_of_update"] = dom["ms"] * dom["count"] / total
     return roof
 
@@ -504,7 +519,7 @@ def launch_rows(rows):
     HBM for the rest (frac is null where no algorithmic work is modelled)."""
     out = []
     for r in rows:
-        e = {k: r[k] for k in ("name", "layout", "shape", "ms", "ms_alone", "count") if k in r}
+        e = {k: r[k] for k in ("name", "layout", "shape", "ms", "ms_bracketed", "ms_alone", "count") if k in r}
         sec = r["ms"] * 1e-3
         peak = PEAK["bf16_mfma"] if r["name"] in BF16_KERNELS else PEAK["fp32_mfma"]
         # the roof a launch meets first: its MFMA time at peak against its HBM time at peak
@@ -556,6 +571,7 @@ def emit(out: dict, args) -> None:
     if "launches" in line:
         line.pop("launches")
         line.pop("launch_sum_ms", None)
+        line.pop("launch_excess_ms", None)
     if "roofline" in line:
         line["roofline"] = compact_roofline(line["roofline"])
     for k in ("value", "ms_per_step"):
@@ -898,7 +914,8 @@ def measure_update(args, config: int, dev, headline: bool) -> dict:
     }
     if not args.profile_only:
         ex = alg.executor(state, recipe.T, recipe.N, recipe.obs_dim)
-        rows = time_launches(ex, args.launch_reps, recipe.cfg.update_epochs * recipe.cfg.num_minibatches)
+        rows, launches = time_launches(ex, args.launch_reps, recipe.cfg.update_epochs * recipe.cfg.num_minibatches)
+        out["launch_excess_ms"] = in_update_durations(rows, launches, out["ms_per_step"])
         total = sum(r["ms"] * r["count"] for r in rows)
         dom = max(rows, key=lambda r: r["ms"] * r["count"])
         out["roofline"] = roofline_of(dom, total, out["config"]["workload"])
