@@ -139,6 +139,44 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// The value of lane (l xor M) within each row of 16 lanes (M = 1, 2, 4, 8),
+// moved by DPP on the vector ALU instead of an LDS-unit permute
+// (__shfl_xor with width 16 compiles to ds_bpermute, a round trip that the
+// compiler waits for one at a time).  xor 1 and xor 2 are quad permutes,
+// xor 8 is a rotation of the row by 8, xor 4 is the half-row mirror
+// (l xor 7) followed by the quad reversal (l xor 3).  Every lane of the row
+// must be active.
+template <int M>
+__device__ __forceinline__ float xor16(float v) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8, "xor16: M in {1, 2, 4, 8}");
+  const int x = __float_as_int(v);
+  int r;
+  if constexpr (M == 1) r = __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, true);         // quad_perm [1,0,3,2]
+  else if constexpr (M == 2) r = __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, true);    // quad_perm [2,3,0,1]
+  else if constexpr (M == 4)
+    r = __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, true),   // row_half_mirror
+                                 0x1B, 0xF, 0xF, true);                                  // quad_perm [3,2,1,0]
+  else r = __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, true);                           // row_ror:8
+  return __int_as_float(r);
+}
+
+// Sum / max over each row of 16 lanes as the xor butterfly 8, 4, 2, 1 (the
+// order of the __shfl_xor loop, so the same bits); every lane gets the result.
+__device__ __forceinline__ float sum16(float v) {
+  v += xor16<8>(v);
+  v += xor16<4>(v);
+  v += xor16<2>(v);
+  v += xor16<1>(v);
+  return v;
+}
+__device__ __forceinline__ float max16(float v) {
+  v = fmaxf(v, xor16<8>(v));
+  v = fmaxf(v, xor16<4>(v));
+  v = fmaxf(v, xor16<2>(v));
+  v = fmaxf(v, xor16<1>(v));
+  return v;
+}
+
 // 0 + x[t] + x[t + S] + x[t + 2 S] + ... (i < n) added in that order, with
 // the loads of U terms in flight at a time (the order, and so the result,
 // of the one-load-per-step loop).

@@ -60,8 +60,11 @@ struct HeadLossParams {
   float* ratio_out; int ratio_envs, ratio_steps;
 };
 
+// jax's tie rule: x's share of the cotangent of ans = min / max (x, y) is 1
+// when x alone is ans, 1/2 when both are (the division by 2 or 1 written as
+// the exact product by 1/2 or 1).
 __device__ __forceinline__ float tie_first(float x, float y, float ans) {
-  return (x == ans ? 1.f : 0.f) / (y == ans ? 2.f : 1.f);
+  return (x == ans ? 1.f : 0.f) * (y == ans ? 0.5f : 1.f);
 }
 __device__ __forceinline__ void clip_grad(float x, float lo, float hi, float& out, float& dx) {
   const float m = fmaxf(lo, x);
@@ -94,21 +97,34 @@ struct LaneIn {
   int64_t s;   // its sample index
 };
 
-__device__ __forceinline__ LaneIn load_lane(const HeadLossParams& p, int r, int j) {
-  LaneIn in;
-  in.live = r < p.rows;
-  const int rc = in.live ? r : p.rows - 1;
-  const int64_t s = p.idx ? (int64_t)p.idx[rc] : (int64_t)rc;
-  in.s = s;
-  in.olp = p.old_logp[s];
-  in.adv = p.adv[s];
-  in.ret = p.ret[s];
-  in.vold = p.old_value[s];
-  in.a = 0;
-  in.actf = 0.f;
-  if (p.dist == DIST_CATEGORICAL) in.a = p.action_i[s];
-  else in.actf = p.action_f[s * p.A + min(j, p.A - 1)];
-  return in;
+// The rows' sample indices first (one load each), then the gathers that
+// depend on them: every index load of the group is in flight before the
+// first gather waits, so the chain costs two round trips, not two per row.
+template <int G, int RW = 16>
+__device__ __forceinline__ void lane_samples(const HeadLossParams& p, int r0, int t, LaneIn (&in)[G]) {
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int r = r0 + t / RW + (HL_THREADS / RW) * g;
+    in[g].live = r < p.rows;
+    const int rc = in[g].live ? r : p.rows - 1;
+    in[g].s = p.idx ? (int64_t)p.idx[rc] : (int64_t)rc;
+  }
+}
+
+template <int G>
+__device__ __forceinline__ void lane_gathers(const HeadLossParams& p, int j, LaneIn (&in)[G]) {
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int64_t s = in[g].s;
+    in[g].olp = p.old_logp[s];
+    in[g].adv = p.adv[s];
+    in[g].ret = p.ret[s];
+    in[g].vold = p.old_value[s];
+    in[g].a = 0;
+    in[g].actf = 0.f;
+    if (p.dist == DIST_CATEGORICAL) in[g].a = p.action_i[s];
+    else in[g].actf = p.action_f[s * p.A + min(j, p.A - 1)];
+  }
 }
 
 // Per-thread constants of phase B (column j): the head bias and, for a
@@ -134,15 +150,20 @@ __device__ __forceinline__ ColConst load_cols(const HeadLossParams& p, bool sep,
   return c;
 }
 
-__device__ __forceinline__ float row16_sum(float v) {
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 16);
-  return v;
+// Sum / max over a row of RW = 16 or 8 lanes (xor butterfly, every lane gets it).
+template <int RW>
+__device__ __forceinline__ float row_sum(float v) {
+  if constexpr (RW == 16) return ppo::sum16(v);
+  v += ppo::xor16<4>(v);
+  v += ppo::xor16<2>(v);
+  return v + ppo::xor16<1>(v);
 }
-__device__ __forceinline__ float row16_max(float v) {
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 16));
-  return v;
+template <int RW>
+__device__ __forceinline__ float row_max(float v) {
+  if constexpr (RW == 16) return ppo::max16(v);
+  v = fmaxf(v, ppo::xor16<4>(v));
+  v = fmaxf(v, ppo::xor16<2>(v));
+  return fmaxf(v, ppo::xor16<1>(v));
 }
 
 // Phase B over ROWS rows whose head outputs (no bias) are the sum of NPART
@@ -150,12 +171,17 @@ __device__ __forceinline__ float row16_max(float v) {
 // Writes dout[row][0..16] (rows past the minibatch: zeros), the statistics
 // and Gaussian-scale terms of each row to st / dsc, then (after a barrier)
 // the block partials.  Ends with a barrier, so dout is ready for phase C.
-template <int ROWS, int NPART, bool SEP>
+// A row is RW = 16 lanes, or 8 for heads of at most 8 outputs (half the
+// instructions: twice the rows per wave instruction; dout columns 8 .. 15
+// are then written as zeros).
+template <int ROWS, int NPART, bool SEP, int RW = 16>
 __device__ __forceinline__ void phase_b(const HeadLossParams& p, int64_t blk, const float (*src)[ROWS][LDO],
                                         float (*dout)[LDO], double (*st)[NSTAT], float (*dsc)[16],
-                                        const LaneIn (&in)[ROWS / 16], const ColConst& cc) {
+                                        const LaneIn (&in)[ROWS * RW / HL_THREADS], const ColConst& cc) {
+  static_assert(RW == 16 || RW == 8, "rows of 16 or 8 lanes");
+  constexpr int RPG = HL_THREADS / RW;  // rows per group
   const int t = threadIdx.x;
-  const int j = t & 15;
+  const int j = t % RW;
   const int A = p.A;
   const float inv_t = 1.f / p.temperature;
   const float eps = p.clip_eps;
@@ -163,8 +189,8 @@ __device__ __forceinline__ void phase_b(const HeadLossParams& p, int64_t blk, co
   const bool gauss = p.dist != DIST_CATEGORICAL;
   const bool spread = p.scale_param != nullptr;
 #pragma unroll
-  for (int g = 0; g < ROWS / 16; ++g) {
-    const int rr = (t >> 4) + 16 * g;
+  for (int g = 0; g < ROWS / RPG; ++g) {
+    const int rr = t / RW + RPG * g;
     const LaneIn& x = in[g];
     float o = src[0][rr][j];
 #pragma unroll
@@ -177,19 +203,19 @@ __device__ __forceinline__ void phase_b(const HeadLossParams& p, int64_t blk, co
       for (int w = 1; w < NPART; ++w) c += src[w][rr][16];
       v = c + cc.bias_c;
     } else {
-      v = __shfl(o, p.na - 1, 16);
+      v = __shfl(o, p.na - 1, RW);
     }
     float lp, ent, val, draw = 0.f, pmin_r, clip_r, ratio_r;
     if (!gauss) {
       const float z = o * inv_t;
-      const float mx = row16_max(jin ? z : -INFINITY);
-      const float se = row16_sum(jin ? __expf(z - mx) : 0.f);
+      const float mx = row_max<RW>(jin ? z : -INFINITY);
+      const float se = row_sum<RW>(jin ? __expf(z - mx) : 0.f);
       const float lse = mx + __logf(se);
-      const float za = row16_sum(j == x.a ? z : 0.f);
+      const float za = row_sum<RW>(j == x.a ? z : 0.f);
       lp = (x.a >= 0 && x.a < A) ? za - lse : -INFINITY;
       const float lq = z - lse;
       const float q = __expf(lq);
-      ent = -row16_sum(jin ? q * lq : 0.f);
+      ent = -row_sum<RW>(jin ? q * lq : 0.f);
       // per-row terms below need lp and ent; the cotangent follows them
       val = 0.f;
       const float ratio = __expf(lp - x.olp);
@@ -205,13 +231,13 @@ __device__ __forceinline__ void phase_b(const HeadLossParams& p, int64_t blk, co
       clip_r = (fabsf(ratio - 1.f) > eps) ? 1.f : 0.f;
       ratio_r = ratio;
     } else {
-      const float raw = spread ? 0.f : __shfl(o, min(A + j, 15), 16);
+      const float raw = spread ? 0.f : __shfl(o, min(A + j, RW - 1), RW);
       const float sig = spread ? cc.sig : p.temperature * (softplusf(raw) + 1e-3f);
       const float ls = spread ? cc.lsig : __logf(sig);
       const float d = x.actf - o;
       const float zz = d / sig;
-      lp = row16_sum(jin ? -0.5f * zz * zz - ls - 0.5f * LOG_2PI : 0.f);
-      ent = row16_sum(jin ? 0.5f + 0.5f * LOG_2PI + ls : 0.f);
+      lp = row_sum<RW>(jin ? -0.5f * zz * zz - ls - 0.5f * LOG_2PI : 0.f);
+      ent = row_sum<RW>(jin ? 0.5f + 0.5f * LOG_2PI + ls : 0.f);
       const float ratio = __expf(lp - x.olp);
       float cr, dcr;
       clip_grad(ratio, 1.f - eps, 1.f + eps, cr, dcr);
@@ -224,7 +250,7 @@ __device__ __forceinline__ void phase_b(const HeadLossParams& p, int64_t blk, co
       const float dsig = g_lp * (d * d / (sig * sig * sig) - 1.f / sig) + g_ent / sig;
       draw = dsig * (spread ? cc.dsp : p.temperature / (1.f + __expf(-raw)));
       if (!spread) {
-        const float dr = __shfl(draw, max(j - A, 0), 16);
+        const float dr = __shfl(draw, max(j - A, 0), RW);
         if (j >= A && j < 2 * A) val = dr;
       }
       pmin_r = pmin;
@@ -248,6 +274,7 @@ __device__ __forceinline__ void phase_b(const HeadLossParams& p, int64_t blk, co
     const float dvalue = p.vf_coef * gv * p.inv_n;
     if (!SEP && j == p.na - 1) val = dvalue;
     dout[rr][j] = x.live ? val : 0.f;
+    if (RW == 8) dout[rr][j + 8] = 0.f;
     if (spread) dsc[rr][j] = (x.live && jin) ? draw : 0.f;
     if (j == 0) {
       dout[rr][16] = x.live ? dvalue : 0.f;
@@ -320,8 +347,8 @@ __global__ void __launch_bounds__(HL_THREADS) head_loss_kernel(HeadLossParams p)
 
   // phase B's inputs, loaded first
   LaneIn lin[TR / 16];
-#pragma unroll
-  for (int g = 0; g < TR / 16; ++g) lin[g] = load_lane(p, r0 + (threadIdx.x >> 4) + 16 * g, threadIdx.x & 15);
+  lane_samples(p, r0, threadIdx.x, lin);
+  lane_gathers(p, threadIdx.x & 15, lin);
   const ColConst cc = load_cols(p, SEP, threadIdx.x & 15);
 
   // ---------------- A. head outputs of the wave's 16 rows
@@ -463,9 +490,10 @@ __global__ void __launch_bounds__(HL_THREADS) head_loss_fs_kernel(HeadLossParams
   const int64_t blk = blockIdx.x;
   const int last = p.rows - 1;
 
-  // phase B's inputs (thread: row threadIdx.x / 16, column threadIdx.x % 16)
+  // phase B's sample indices (thread: row threadIdx.x / 16, column
+  // threadIdx.x % 16); their gathers follow the operand loads below
   LaneIn lin[1];
-  lin[0] = load_lane(p, r0 + (threadIdx.x >> 4), threadIdx.x & 15);
+  lane_samples(p, r0, threadIdx.x, lin);
   const ColConst cc = load_cols(p, SEP, threadIdx.x & 15);
 
   // ---- loads of phases A, C1, C2 (clamped in-range addresses, zeroed after)
@@ -501,6 +529,7 @@ __global__ void __launch_bounds__(HL_THREADS) head_loss_fs_kernel(HeadLossParams
       if (SEP) c2[i][q] = p.hc[rowq[q] * p.ldhc + f];
     }
   }
+  lane_gathers(p, threadIdx.x & 15, lin);
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
     const bool fin = 16 * (wave + 4 * i) < F;
@@ -579,6 +608,217 @@ __global__ void __launch_bounds__(HL_THREADS) head_loss_fs_kernel(HeadLossParams
   }
 }
 
+// Shared heads (one Dense over the torso output feeding every head output),
+// large minibatches: the head input tile is read from HBM once and kept in
+// registers for all three phases.  A workgroup owns 64 rows; wave w owns the
+// 64 features [64 w, 64 w + 64) of all of them, lane (li, kq) holding
+// H[16 cc + 4 kq + s][64 w + 4 li + m] (cc, s, m < 4) as sixteen float4.
+// That layout serves C1 and C2 on MFMA directly (their 16-feature MFMA
+// columns are the features 64 w + 4 li + m of one m, their row index is
+// 4 kq + s); phase A, which contracts over the features, forms each lane's
+// partial products over its four features and sums the sixteen lanes of a
+// row group by a reduce-scatter of xor shuffles (each level keeps half of
+// the values), then the four waves' partials meet in LDS and phase B sums
+// them in wave order.  F <= 256, a multiple of 16.
+constexpr int RT_F = 256;
+
+// One level of the reduce-scatter over a row of 16 lanes: a lane keeps the
+// half of its first n values selected by its lane bit M and adds the other
+// half of lane (l xor M).  The halves are chosen with bit masks, not a
+// select, which the compiler would turn into a lane-dependent index into
+// the register array.
+template <int M, int n, int N>
+__device__ __forceinline__ void rs_level(float (&v)[N], int li) {
+  const uint32_t hi = (li & M) ? 0xffffffffu : 0u;
+#pragma unroll
+  for (int k = 0; k < n / 2; ++k) {
+    const uint32_t lo_b = __float_as_uint(v[k]), hi_b = __float_as_uint(v[n / 2 + k]);
+    const float keep = __uint_as_float((hi_b & hi) | (lo_b & ~hi));
+    const float send = __uint_as_float((lo_b & hi) | (hi_b & ~hi));
+    v[k] = keep + ppo::xor16<M>(send);
+  }
+}
+
+// Sums each of the 4 JP values over the 16 lanes of a row, scattered: lane
+// li ends with the sums of values [li * JP / 4, (li + 1) * JP / 4) in
+// v[0 .. JP / 4).
+template <int JP>
+__device__ __forceinline__ void reduce_scatter16(float (&v)[4 * JP], int li) {
+  constexpr int N = 4 * JP;
+  rs_level<8, N>(v, li);
+  rs_level<4, N / 2>(v, li);
+  rs_level<2, N / 4>(v, li);
+  rs_level<1, N / 8>(v, li);
+}
+
+template <int JP, bool AUX, int ACT>
+__global__ void __launch_bounds__(HL_THREADS) head_loss_rt_kernel(HeadLossParams p) {
+  __shared__ __attribute__((aligned(16))) float s_part[4][TR][LDO];
+  __shared__ __attribute__((aligned(16))) float s_dout[TR][LDO];
+  __shared__ double s_st[TR][NSTAT];
+  __shared__ float s_dsc[TR][16];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 15;
+  const int kq = lane >> 4;
+  const int F = p.F;
+  const int r0 = blockIdx.x * TR;
+  const int64_t blk = blockIdx.x;
+  const int last = p.rows - 1;
+  const int f0 = 64 * wave + 4 * li;  // this lane's four features f0 + m
+  const bool fin = f0 < F;             // F % 16 == 0: all four or none
+
+  // ---- every load first: phase B's sample indices, the head input (and
+  // activation input) tile, the lane's head kernel rows, then the rollout
+  // gathers that need the indices
+  constexpr int RW = JP <= 8 ? 8 : 16;   // phase B's lanes per row
+  LaneIn lin[TR * RW / HL_THREADS];
+  lane_samples<TR * RW / HL_THREADS, RW>(p, r0, threadIdx.x, lin);
+  floatx4 h[4][4], xa[AUX ? 4 : 1][4];
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = r0 + 16 * cc + 4 * kq + q;
+      const int64_t rc = min(r, last);
+      const int fc = fin ? f0 : 0;
+      h[cc][q] = *reinterpret_cast<const floatx4*>(p.ha + rc * p.ldha + fc);
+      if (AUX) xa[cc][q] = *reinterpret_cast<const floatx4*>(p.aux_a + rc * p.ldaux_a + fc);
+    }
+  }
+  // wA[m][j] = W[f0 + m][j] (phase A), 16-byte loads (ldwa is a multiple of
+  // 4, <= JP)
+  float wA[4][JP];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const float* wrow = p.wa + (int64_t)(fin ? f0 + m : 0) * p.ldwa;
+#pragma unroll
+    for (int j4 = 0; j4 < JP / 4; ++j4) {
+      const floatx4 w4 = *reinterpret_cast<const floatx4*>(wrow + min(4 * j4, (int)p.ldwa - 4));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wA[m][4 * j4 + e] = w4[e];
+    }
+  }
+  lane_gathers(p, threadIdx.x % RW, lin);
+  const ColConst cc0 = load_cols(p, false, threadIdx.x % RW);
+  // zero what lies outside the rows, the features or the head outputs
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bool ok = fin && r0 + 16 * cc + 4 * kq + q < p.rows;
+      h[cc][q] = ok ? h[cc][q] : floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+#pragma unroll
+    for (int j = 0; j < JP; ++j) wA[m][j] = (fin && j < p.na) ? wA[m][j] : 0.f;
+  }
+  // C1's B operand for k step s: wb[m][s] = W[f0 + m][kq + 4 s], taken from
+  // wA by bit masks on kq (a select would become a lane-dependent index)
+  constexpr int SJ = JP / 4;
+  float wb[4][SJ];
+  {
+    uint32_t sel[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) sel[c] = kq == c ? 0xffffffffu : 0u;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+#pragma unroll
+      for (int s2 = 0; s2 < SJ; ++s2) {
+        uint32_t b = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) b |= __float_as_uint(wA[m][4 * s2 + c]) & sel[c];
+        wb[m][s2] = __uint_as_float(b);
+      }
+    }
+  }
+
+  // ---------------- A. head outputs: per-lane products over the lane's four
+  // features, summed over the sixteen lanes of each row group, per wave
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc) {
+    float v[4 * JP];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int j = 0; j < JP; ++j) {
+        float a = h[cc][q][0] * wA[0][j];
+        a = __fmaf_rn(h[cc][q][1], wA[1][j], a);
+        a = __fmaf_rn(h[cc][q][2], wA[2][j], a);
+        v[q * JP + j] = __fmaf_rn(h[cc][q][3], wA[3][j], a);
+      }
+    }
+    reduce_scatter16<JP>(v, li);
+    // lane li now holds row 4 kq + (li >> 2) of this group, outputs
+    // (li & 3) * JP / 4 + c
+    const int rr = 16 * cc + 4 * kq + (li >> 2);
+#pragma unroll
+    for (int c = 0; c < JP / 4; ++c) s_part[wave][rr][(li & 3) * (JP / 4) + c] = v[c];
+  }
+  __syncthreads();
+
+  // ---------------- B. loss and output cotangents (element-parallel)
+  phase_b<TR, 4, false, RW>(p, blk, s_part, s_dout, s_st, s_dsc, lin, cc0);
+
+  // ---------------- C1. input cotangent dH = dOUT W^T (times the activation's
+  // derivative) of every row group, from the same registers
+  // (k step s contracts head outputs kq + 4 s: SJ = JP / 4 steps cover them)
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc) {
+    const bool liveA = r0 + 16 * cc + li < p.rows;
+    float a_in[SJ];
+#pragma unroll
+    for (int s2 = 0; s2 < SJ; ++s2) a_in[s2] = liveA ? s_dout[16 * cc + li][kq + 4 * s2] : 0.f;
+    floatx4 g[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      g[m] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s2 = 0; s2 < SJ; ++s2) g[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(a_in[s2], wb[m][s2], g[m], 0, 0, 0);
+    }
+    // g[m][v]: row 16 cc + 4 kq + v, feature f0 + m
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int r = r0 + 16 * cc + 4 * kq + v;
+      if (!fin || r >= p.rows) continue;
+      floatx4 d = {g[0][v], g[1][v], g[2][v], g[3][v]};
+      if (has_act<ACT>(p.act_a)) {
+        const floatx4 x = AUX ? xa[cc][v] : h[cc][v];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) d[m] *= dact<ACT>(p.act_a, x[m]);
+      }
+      *reinterpret_cast<floatx4*>(p.dha + (int64_t)r * p.lddha + f0) = d;
+    }
+  }
+
+  // ---------------- C2. head weight gradient partial H^T dOUT over the 64 rows
+  float dq[4][4];
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dq[cc][q] = s_dout[16 * cc + 4 * kq + q][li];
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const floatx4 a = {h[cc][0][m], h[cc][1][m], h[cc][2][m], h[cc][3][m]};
+      acc = mfma4(a, dq[cc], acc);
+    }
+    // acc[v]: feature 64 w + 4 (4 kq + v) + m, output li
+    if (li < (int)p.ldwa) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int f = 64 * wave + 4 * (4 * kq + v) + m;
+        if (f < F) p.wpart_a[(blk * F + f) * p.ldwa + li] = acc[v];
+      }
+    }
+  }
+}
+
 }  // namespace
 
 #ifndef PPO_HL_SMALL_ROWS
@@ -651,6 +891,21 @@ static int head_loss_impl(
       else if (nb <= 2) hipLaunchKernelGGL((head_loss_fs_kernel<S, 2, AC>), dim3(blocks), dim3(HL_THREADS), 0, st, p);
       else if (nb <= 4) hipLaunchKernelGGL((head_loss_fs_kernel<S, 4, AC>), dim3(blocks), dim3(HL_THREADS), 0, st, p);
       else hipLaunchKernelGGL((head_loss_fs_kernel<S, 8, AC>), dim3(blocks), dim3(HL_THREADS), 0, st, p);
+    } else if (!S && F <= RT_F && ldwa % 4 == 0 && (reinterpret_cast<uintptr_t>(wa) & 15) == 0) {
+      // the shared head's input read once, kept in registers
+      const bool aux = act_a != ACT_NONE && !(aux_a == ha && ldaux_a == ldha);
+      const int jp = ldwa <= 4 ? 4 : ldwa <= 8 ? 8 : 16;
+      auto rt = [&](auto jp_c, auto aux_c) {
+        hipLaunchKernelGGL((head_loss_rt_kernel<decltype(jp_c)::value, decltype(aux_c)::value, AC>), dim3(blocks),
+                           dim3(HL_THREADS), 0, st, p);
+      };
+      auto by_jp = [&](auto aux_c) {
+        if (jp == 4) rt(std::integral_constant<int, 4>{}, aux_c);
+        else if (jp == 8) rt(std::integral_constant<int, 8>{}, aux_c);
+        else rt(std::integral_constant<int, 16>{}, aux_c);
+      };
+      if (aux) by_jp(std::true_type{});
+      else by_jp(std::false_type{});
     } else {
       hipLaunchKernelGGL((head_loss_kernel<S, AC>), dim3(blocks), dim3(HL_THREADS), 0, st, p);
     }
