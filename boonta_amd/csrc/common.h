@@ -160,6 +160,32 @@ __device__ __forceinline__ float xor16(float v) {
   return __int_as_float(r);
 }
 
+// x + x[l xor 16] and x + x[l xor 32] for every lane l, from the gfx950
+// lane swaps of two copies of x: permlane16_swap exchanges the odd 16-lane
+// rows of its first operand with the even rows of its second, permlane32_swap
+// the upper half of the first with the lower half of the second, so the two
+// results hold x and its partner in every lane (the same sum as
+// x + __shfl_xor(x, 16 or 32): the addition is commutative).
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// x + x[l xor M] over the whole wave for M = 32, 16, 8, 4, 2, 1 in turn
+// (the order of the __shfl_xor loop, so the same bits); every lane active.
+__device__ __forceinline__ float wave_sum_lanes(float v) {
+  v = add_xor32(v);
+  v = add_xor16(v);
+  v += xor16<8>(v);
+  v += xor16<4>(v);
+  v += xor16<2>(v);
+  return v + xor16<1>(v);
+}
+
 // Sum / max over each row of 16 lanes as the xor butterfly 8, 4, 2, 1 (the
 // order of the __shfl_xor loop, so the same bits); every lane gets the result.
 __device__ __forceinline__ float sum16(float v) {

@@ -316,7 +316,7 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_kernel(GemmParams p) {
   if (do_bsum) {
 #pragma unroll
     for (int bj = 0; bj < NB; ++bj) {
-      const float t = bsum[bj] + __shfl_xor(bsum[bj], 32, 64);
+      const float t = ppo::add_xor32(bsum[bj]);
       const int gn = n0 + wn * (BN / 2) + bj * 32 + l32;
       if (h == 0 && gn < p.N) p.bias_grad[(int64_t)split * p.N + gn] = t;
     }

@@ -91,7 +91,7 @@ __device__ __forceinline__ void epilogue_f32_t(const GemmParams& p, floatx16 (&a
   if (do_bsum) {
 #pragma unroll
     for (int bj = 0; bj < NB; ++bj) {
-      const float t = bsum[bj] + __shfl_xor(bsum[bj], 32, 64);
+      const float t = ppo::add_xor32(bsum[bj]);
       const int gn = wn0 + bj * 32 + l32;
       if (h == 0 && gn < p.N) p.bias_grad[(int64_t)split * p.N + gn] = t;
     }

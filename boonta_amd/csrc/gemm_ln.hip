@@ -150,11 +150,8 @@ __global__ void __launch_bounds__(GL_THREADS) gemm_ln_fwd_kernel(GemmLnArgs p0) 
       z[v][j] = acc[j][v] + bias4[j];
       ppo::ln_accum(z[v][j], ps[v], pq[v]);
     }
-#pragma unroll
-    for (int o = 8; o; o >>= 1) {
-      ps[v] += __shfl_xor(ps[v], o, 16);
-      pq[v] += __shfl_xor(pq[v], o, 16);
-    }
+    ps[v] = ppo::sum16(ps[v]);
+    pq[v] = ppo::sum16(pq[v]);
   }
   if (li == 0) {
 #pragma unroll

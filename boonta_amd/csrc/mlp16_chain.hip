@@ -540,12 +540,10 @@ __global__ void __launch_bounds__(C16_THREADS, 1) mlp16_ln_bwd_kernel(Bwd16Args 
         }
       }
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1)
-#pragma unroll
-        for (int j = 0; j < RB; ++j) {
-          sg[j] += __shfl_xor(sg[j], o, 64);
-          sgx[j] += __shfl_xor(sgx[j], o, 64);
-        }
+      for (int j = 0; j < RB; ++j) {
+        sg[j] = ppo::wave_sum_lanes(sg[j]);
+        sgx[j] = ppo::wave_sum_lanes(sgx[j]);
+      }
 #pragma unroll
       for (int j = 0; j < RB; ++j) {
         const int jj = hb * RB + j;

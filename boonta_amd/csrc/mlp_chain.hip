@@ -269,11 +269,8 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p) {
         z[v][j] = acc[j][v] + bias4[j];
         ppo::ln_accum(z[v][j], ps[v], pq[v]);
       }
-#pragma unroll
-      for (int o = 8; o; o >>= 1) {
-        ps[v] += __shfl_xor(ps[v], o, 16);
-        pq[v] += __shfl_xor(pq[v], o, 16);
-      }
+      ps[v] = ppo::sum16(ps[v]);
+      pq[v] = ppo::sum16(pq[v]);
     }
     if (li == 0) {
 #pragma unroll
@@ -432,11 +429,8 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_bwd_kernel(BwdArgs p) {
         sg[v] += g[v][j];
         sgx[v] += g[v][j] * xh[v][j];
       }
-#pragma unroll
-      for (int o = 8; o; o >>= 1) {
-        sg[v] += __shfl_xor(sg[v], o, 16);
-        sgx[v] += __shfl_xor(sgx[v], o, 16);
-      }
+      sg[v] = ppo::sum16(sg[v]);
+      sgx[v] = ppo::sum16(sgx[v]);
     }
     if (li == 0) {
 #pragma unroll
@@ -449,10 +443,10 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_bwd_kernel(BwdArgs p) {
     // order (the lane's four rows, then the four row groups)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      pg[j] += __shfl_xor(pg[j], 16);
-      pb[j] += __shfl_xor(pb[j], 16);
-      pg[j] += __shfl_xor(pg[j], 32);
-      pb[j] += __shfl_xor(pb[j], 32);
+      pg[j] = ppo::add_xor16(pg[j]);
+      pb[j] = ppo::add_xor16(pb[j]);
+      pg[j] = ppo::add_xor32(pg[j]);
+      pb[j] = ppo::add_xor32(pb[j]);
     }
     if (l > 0) load_w<MC_F>(0, w0, p.WT[l] + t * p.tWT, MC_F, MC_F, kq, c4);
     if (kq == 0) {

@@ -284,16 +284,9 @@ constexpr int LOSS_GROUP = 16;
 constexpr int LOSS_ROWS = LOSS_THREADS / LOSS_GROUP;
 constexpr int LOSS_K = 4;  // head outputs per lane
 
-__device__ __forceinline__ float group16_sum(float v) {
-#pragma unroll
-  for (int o = LOSS_GROUP / 2; o; o >>= 1) v += __shfl_xor(v, o, LOSS_GROUP);
-  return v;
-}
-__device__ __forceinline__ float group16_max(float v) {
-#pragma unroll
-  for (int o = LOSS_GROUP / 2; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, LOSS_GROUP));
-  return v;
-}
+static_assert(LOSS_GROUP == 16, "the group reductions are 16-lane DPP butterflies");
+__device__ __forceinline__ float group16_sum(float v) { return ppo::sum16(v); }
+__device__ __forceinline__ float group16_max(float v) { return ppo::max16(v); }
 
 __global__ void __launch_bounds__(LOSS_THREADS) ppo_loss_kernel(LossParams p) {
   __shared__ double sred[LOSS_THREADS / 64][NSTAT];
@@ -456,8 +449,8 @@ __global__ void __launch_bounds__(LOSS_THREADS) ppo_loss_kernel(LossParams p) {
   if (p.scale_param) {
     // the wave's four groups hold the same outputs: fold them, lanes 0-15 keep the sums
     float v = dscale_acc;
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
+    v = ppo::add_xor16(v);
+    v = ppo::add_xor32(v);
     if (lane < LOSS_GROUP) sscale[wave][lane] = v;
   }
   __syncthreads();
