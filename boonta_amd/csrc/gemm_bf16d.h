@@ -42,9 +42,11 @@ using ppo::stage_barrier;
 // unit's k offset in the stage; k-outer: col is the unit's first element
 // (clamped to the row's extent), rows come from the stage's k rows (through
 // the block's LDS copy of the gather indices when the reduction is gathered).
-template <int ROWS, bool KC, int NW>
+template <int ROWS, bool KC, int NW, int SBK = BK>
 struct DOperand {
-  static constexpr int ELEMS = ROWS * BK;
+  static_assert(SBK == BK || (!KC && (SBK == 32 || SBK == 16)),
+                "a k-contiguous operand keeps 64-deep stages (its swizzle spans 8 chunks per row)");
+  static constexpr int ELEMS = ROWS * SBK;
   static constexpr int COPIES = ELEMS / 512;
   static constexpr int PERW = COPIES / NW;
   static_assert(PERW >= 1 && COPIES % NW == 0, "tile too small for the wave count");
@@ -60,13 +62,13 @@ struct DOperand {
     for (int i = 0; i < PERW; ++i) {
       const int u = 64 * (wave * PERW + i) + lane;
       if (KC) {
-        const int r = u / (BK / 8);
+        const int r = u / (SBK / 8);
         const int g = r0 + r;
         ok[i] = g < lim;
         const int gc = ok[i] ? g : 0;
         const int64_t row = rows_idx ? (int64_t)rows_idx[gc] : (int64_t)gc;
         src[i] = base + row * ld;
-        col[i] = 8 * ((u % (BK / 8)) ^ kc_swizzle(r));
+        col[i] = 8 * ((u % (SBK / 8)) ^ kc_swizzle(r));
         krow[i] = 0;
       } else {
         const int k = u / (ROWS / 8);
@@ -122,12 +124,12 @@ struct DOperand {
 };
 
 // MFMA operand (v_mfma_f32_32x32x16_bf16) for rows r0 .. r0 + 31, k kk .. kk + 15.
-template <int ROWS, bool KC>
+template <int ROWS, bool KC, int SBK = BK>
 __device__ __forceinline__ bf16x8 doperand(const uint16_t* lds, int r0, int kk, int lane) {
   if (KC) {
     const int r = r0 + (lane & 31);
     const int c = (kk >> 3) + (lane >> 5);
-    return *reinterpret_cast<const bf16x8*>(lds + r * BK + ((c ^ kc_swizzle(r)) << 3));
+    return *reinterpret_cast<const bf16x8*>(lds + r * SBK + ((c ^ kc_swizzle(r)) << 3));
   } else {
     const int g = lane >> 4, j = lane & 15;
     const int k = kk + 8 * (g >> 1) + (j >> 2);
@@ -144,14 +146,17 @@ __device__ __forceinline__ bf16x8 doperand(const uint16_t* lds, int r0, int kk, 
 
 using ppo::ring_barrier;
 
-// One workgroup's output tile tc of the GEMM p.
-template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF, int KIDX>
+// One workgroup's output tile tc of the GEMM p, SBK reduction elements per
+// stage (64; 32 or 16 when both operands are k-outer, for a deeper ring in
+// the same LDS).
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF, int KIDX, int SBK = BK>
 __device__ __forceinline__ void gemm_bf16d_tile(const Params& p, const ppo::TileCoord tc) {
   constexpr int NW = WM * WN;
   constexpr int BI = BM / WM / 32, BJ = BN / WN / 32;
   static_assert(BI * WM * 32 == BM && BJ * WN * 32 == BN, "tile must split into 32 x 32 blocks");
-  using OpA = DOperand<BM, A_K, NW>;
-  using OpB = DOperand<BN, B_K, NW>;
+  static_assert(BK % SBK == 0, "split boundaries (multiples of BK) must fall on stage boundaries");
+  using OpA = DOperand<BM, A_K, NW, SBK>;
+  using OpB = DOperand<BN, B_K, NW, SBK>;
   __shared__ __attribute__((aligned(1024))) uint16_t sA[NBUF][OpA::ELEMS];
   __shared__ __attribute__((aligned(1024))) uint16_t sB[NBUF][OpB::ELEMS];
   // gather indices of the split's reduction rows (A k-outer and gathered)
@@ -193,14 +198,14 @@ __device__ __forceinline__ void gemm_bf16d_tile(const Params& p, const ppo::Tile
     __syncthreads();
   }
 
-  const int nk = (ke > kb) ? (ke - kb + BK - 1) / BK : 0;
-  const int nfull = (ke - kb) / BK;  // stages entirely inside [kb, ke)
+  const int nk = (ke > kb) ? (ke - kb + SBK - 1) / SBK : 0;
+  const int nfull = (ke - kb) / SBK;  // stages entirely inside [kb, ke)
   constexpr int PER_STAGE = OpA::PERW + OpB::PERW;  // copies a wave issues per stage
 
   auto issue = [&](int s) {  // stage s into ring slot s % NBUF
     uint16_t* la = sA[s % NBUF];
     uint16_t* lb = sB[s % NBUF];
-    const int k0 = kb + s * BK;
+    const int k0 = kb + s * SBK;
     if (s < nfull) {
       oa.copy(la, p.lda, k0, kb, kidx, wave);
       ob.copy(lb, p.ldb, k0, kb, nullptr, wave);
@@ -218,15 +223,17 @@ __device__ __forceinline__ void gemm_bf16d_tile(const Params& p, const ppo::Tile
     bf16x8 a8[2][BI], b8[2][BJ];
     auto read_ops = [&](int set, int kk) {
 #pragma unroll
-      for (int bi = 0; bi < BI; ++bi) a8[set][bi] = doperand<BM, A_K>(la, wm * (BI * 32) + bi * 32, kk, lane);
+      for (int bi = 0; bi < BI; ++bi)
+        a8[set][bi] = doperand<BM, A_K, SBK>(la, wm * (BI * 32) + bi * 32, kk, lane);
 #pragma unroll
-      for (int bj = 0; bj < BJ; ++bj) b8[set][bj] = doperand<BN, B_K>(lb, wn * (BJ * 32) + bj * 32, kk, lane);
+      for (int bj = 0; bj < BJ; ++bj)
+        b8[set][bj] = doperand<BN, B_K, SBK>(lb, wn * (BJ * 32) + bj * 32, kk, lane);
     };
     read_ops(0, 0);
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
+    for (int ks = 0; ks < SBK / 16; ++ks) {
       const int cur = ks & 1;
-      if (ks + 1 < BK / 16) read_ops(cur ^ 1, (ks + 1) * 16);
+      if (ks + 1 < SBK / 16) read_ops(cur ^ 1, (ks + 1) * 16);
 #pragma unroll
       for (int bi = 0; bi < BI; ++bi)
 #pragma unroll
@@ -255,9 +262,9 @@ __device__ __forceinline__ void gemm_bf16d_tile(const Params& p, const ppo::Tile
   epilogue<BI, BJ>(p, acc, bsum, do_bsum, m0 + wm * (BI * 32), n0 + wn * (BJ * 32), split, lane);
 }
 
-template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF, int KIDX = KIDX_MAX>
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF, int KIDX = KIDX_MAX, int SBK = BK>
 __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_bf16d_kernel(Params p) {
-  gemm_bf16d_tile<BM, BN, WM, WN, A_K, B_K, NBUF, KIDX>(p, ppo::xcd_tile());
+  gemm_bf16d_tile<BM, BN, WM, WN, A_K, B_K, NBUF, KIDX, SBK>(p, ppo::xcd_tile());
 }
 
 // Several GEMMs of one tile shape in one launch: problem i owns the linear
@@ -272,7 +279,7 @@ struct GroupParams {
   int count;
 };
 
-template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF, int KIDX>
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF, int KIDX, int SBK = BK>
 __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_bf16d_group_kernel(GroupParams g) {
   const int total = gridDim.x;
   const int w = blockIdx.x;
@@ -286,14 +293,14 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_bf16d_group_kernel(Group
   tc.n = local % g.gx[i];
   tc.m = (local / g.gx[i]) % g.gy[i];
   tc.z = local / (g.gx[i] * g.gy[i]);
-  gemm_bf16d_tile<BM, BN, WM, WN, A_K, B_K, NBUF, KIDX>(g.p[i], tc);
+  gemm_bf16d_tile<BM, BN, WM, WN, A_K, B_K, NBUF, KIDX, SBK>(g.p[i], tc);
 }
 
-template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF, int KIDX = KIDX_MAX>
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF, int KIDX = KIDX_MAX, int SBK = BK>
 int launch_d(hipStream_t st, const Params& p, int splits) {
   dim3 grid(ppo::ceil_div(p.N, BN), ppo::ceil_div(p.M, BM), splits);
-  hipLaunchKernelGGL((gemm_bf16d_kernel<BM, BN, WM, WN, A_K, B_K, NBUF, KIDX>), grid, dim3(WM * WN * 64), 0, st,
-                     p);
+  hipLaunchKernelGGL((gemm_bf16d_kernel<BM, BN, WM, WN, A_K, B_K, NBUF, KIDX, SBK>), grid, dim3(WM * WN * 64), 0,
+                     st, p);
   return ppo::check_launch("ppo_gemm_bf16s");
 }
 
