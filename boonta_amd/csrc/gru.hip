@@ -317,24 +317,34 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 // ------------------------------------------------- persistent recurrence
 // The whole sequence in one launch per direction.  Workgroup (x, y) owns
-// sequences 16 x .. 16 x + 15 and units 16 y .. 16 y + 15 for every step, with
-// its slice of the recurrent kernel in LDS for the whole launch.  Step t of a
-// sequence block needs only the previous step of the same block, produced by
-// the gridDim.y workgroups that share x.  They hand it over through an
-// exchange ring of two slots, each [Bm][K] 64-bit pairs {value bits, tag}
-// (K = H forward, 3H backward), zeroed at launch: a producer stores each value
-// with the tag of its step (device-coherent 64-bit stores, which land whole),
-// and a consumer loads the K columns of its 16 rows (coalesced,
-// device-coherent 64-bit loads), reloading the pairs whose tag is not yet the
-// step's, then stages the values in LDS for the contraction.  No counter, no
-// fence: a value is read only once its own tag says it is there.  A slot is
-// written again two steps later, only after its producer has consumed the
-// step in between, which every consumer of the slot produced after reading
-// it.  A wait polls at most spin_limit times (0: not at all, which tests the
-// error path from the host): when one gives up it sets *error and the
-// workgroup returns, so every workgroup ends.  The contraction and epilogue
-// of a step are those of the one-step kernels, so the results are the same
-// bits.
+// sequences 16 x .. 16 x + 15 and units 16 y .. 16 y + 15 for every step; each
+// lane holds its slice of the recurrent kernel in registers for the whole
+// launch.  Step t of a sequence block needs only the previous step of the
+// same block, produced by the gridDim.y workgroups that share x.  They hand it
+// over through an exchange ring of two slots, each [Bm][K] 64-bit pairs
+// {value bits, tag} (K = H forward, 3H backward), zeroed at launch: a
+// producer stores each value with the tag of its step (device-coherent 64-bit
+// stores, which land whole), and each consumer wave loads the pairs of its
+// own quarter of K for the block's 16 rows (device-coherent 64-bit loads,
+// each load of the wave 64 consecutive pairs), reloading those whose tag is
+// not yet the step's, and stages them in an LDS tile of its own for the
+// contraction.  No counter, no fence: a value is read only once its own tag
+// says it is there.  The contraction and epilogue of a step are those of the
+// one-step kernels, so the results are the same bits.
+//
+// Waves of one workgroup meet once per step, where the four partial tiles are
+// summed; a wave may run one step ahead of another, so the partial tiles
+// alternate between two LDS buffers.  A wave writes a buffer again two steps
+// later only after it has read, from some producer, values that producer
+// wrote after its own waves had read all 16 rows of this workgroup's previous
+// step (each producer's waves together read every column), and this
+// workgroup's waves put those rows out only after summing the buffer.  The
+// same chain keeps the ring: a slot is written again two steps later only
+// after its producer has consumed the step in between, which every consumer
+// of the slot produced after reading it.  A wait polls at most spin_limit
+// times (0: not at all, which tests the error path from the host): when one
+// gives up it sets *error and records its step in LDS, and after that step's
+// meeting every wave of the workgroup returns, so every workgroup ends.
 
 typedef unsigned long long u64;
 
@@ -348,31 +358,38 @@ __device__ __forceinline__ void put_pair(u64* p, float v, unsigned tag) {
   __hip_atomic_store(p, ((u64)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Stages rows b0 .. b0 + 15 of a ring slot ([Bm][K] pairs) into sA[16][K + 4]
-// once each of their pairs carries `tag`; rows from Bm on (never written) are
-// zeros.  Returns, in every thread, false when a wait gave up.
-template <int K>
-__device__ bool stage_exchange(const u64* slot, int Bm, int b0, unsigned tag, float* sA, const SeqSync& s) {
-  constexpr int NL = TILE * K / 256;
-  static_assert(TILE * K % 256 == 0, "rows of K pairs over 256 threads");
-  const int tid = threadIdx.x;
+__device__ __forceinline__ unsigned tag_of(u64 p) { return (unsigned)(p >> 32); }
+
+// Waits until the wave's quarter of a ring slot's columns, kw .. kw + KW - 1
+// of rows b0 .. b0 + 15 ([Bm][K] pairs), carries `tag`, and stages it in the
+// wave's own LDS tile sA[16][KW + 4] (rows from Bm on, never written, are
+// zeros).  Each load of the wave reads 64 consecutive pairs of the tile's
+// rows.  Only this wave writes and reads sA, and a wave's LDS accesses
+// complete in order, so no barrier follows.  Returns false, alike in every
+// lane, when spin_limit polls went by without all of them there.
+template <int K, int KW>
+__device__ __forceinline__ bool stage_wave(const u64* slot, int Bm, int b0, int kw, unsigned tag, float* sA,
+                                           int spin_limit) {
+  constexpr int NL = TILE * KW / 64;
+  static_assert(TILE * KW % 64 == 0, "rows of KW pairs over a wave");
+  const int lane = threadIdx.x & 63;
   u64 v[NL];
 #pragma unroll
-  for (int q = 0; q < NL; ++q) v[q] = b0 + (tid + 256 * q) / K < Bm ? 0ull : (u64)tag << 32;
+  for (int q = 0; q < NL; ++q) v[q] = b0 + (lane + 64 * q) / KW < Bm ? 0ull : (u64)tag << 32;
   bool ok = false;
-  for (int it = 0; it < s.spin_limit; ++it) {
+  for (int it = 0; it < spin_limit; ++it) {
+    bool mine = true;
 #pragma unroll
     for (int q = 0; q < NL; ++q) {
-      if ((unsigned)(v[q] >> 32) != tag) {
-        const int e = tid + 256 * q, r = e / K;
-        v[q] = __hip_atomic_load(slot + (int64_t)(b0 + r) * K + (e - r * K), __ATOMIC_RELAXED,
+      if (tag_of(v[q]) != tag) {
+        const int e = lane + 64 * q, r = e / KW;
+        v[q] = __hip_atomic_load(slot + (int64_t)(b0 + r) * K + kw + (e - r * KW), __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    bool all = true;
 #pragma unroll
-    for (int q = 0; q < NL; ++q) all = all && (unsigned)(v[q] >> 32) == tag;
-    if (all) {
+    for (int q = 0; q < NL; ++q) mine = mine && tag_of(v[q]) == tag;
+    if (__builtin_amdgcn_ballot_w64(!mine) == 0) {
       ok = true;
       break;
     }
@@ -380,11 +397,11 @@ __device__ bool stage_exchange(const u64* slot, int Bm, int b0, unsigned tag, fl
   }
 #pragma unroll
   for (int q = 0; q < NL; ++q) {
-    const int e = tid + 256 * q, r = e / K;
-    sA[r * (K + 4) + (e - r * K)] = __uint_as_float((uint32_t)v[q]);
+    const int e = lane + 64 * q, r = e / KW;
+    sA[r * (KW + 4) + (e - r * KW)] = __uint_as_float((uint32_t)v[q]);
   }
-  if (!ok) __hip_atomic_fetch_or(s.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return __syncthreads_or(!ok) == 0;
+  __builtin_amdgcn_wave_barrier();
+  return ok;
 }
 
 // The reset flags of the block's 16 rows for FLAG_CHUNK steps, read once per
@@ -426,111 +443,117 @@ struct FwdSeqArgs {
   SeqSync sync;
 };
 
-// dynamic LDS: [3 gates][16 units][H + 4] (the B operand rows, k contiguous),
-// then [16 sequences][H + 4] (the previous step's h of the block's rows)
 template <int NIT>
 __global__ void __launch_bounds__(256) gru_fwd_seq_kernel(FwdSeqArgs a) {
   constexpr int H = 64 * NIT;
-  constexpr int P = H + 4;
-  extern __shared__ float sW[];
-  float* sA = sW + 3 * TILE * P;
-  __shared__ float red[WAVES][3][TILE][TILE + 1];
+  __shared__ float red[2][WAVES][3][TILE][TILE + 1];
+  __shared__ float sA[WAVES][TILE * (H / WAVES + 4)];  // each wave's staged quarter of the previous h
   __shared__ uint8_t done[FLAG_CHUNK][TILE];
+  __shared__ int gave_up;  // the step at which a wait gave up, -1 while none has
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int b0 = blockIdx.x * TILE;
   const int u0 = blockIdx.y * TILE;
-  for (int e = tid; e < 3 * H * TILE; e += 256) {
-    const int i = e % TILE, k = (e / TILE) % H, g = e / (TILE * H);
-    sW[(g * TILE + i) * P + k] = a.wh[(int64_t)k * a.ldwh + g * H + u0 + i];
-  }
-
   const int i = lane & 15;
   const int kq = lane >> 4;
-  const int kbeg = wave * (H / WAVES);
+  // this lane's columns: k0 + 16 c + q, c < NIT, q < 4 (the wave's quarter of H)
+  const int k0 = wave * (H / WAVES) + 4 * kq;
+  float* sAw = sA[wave];
+  float bv[NIT][3][4];
+#pragma unroll
+  for (int c = 0; c < NIT; ++c)
+#pragma unroll
+    for (int g = 0; g < 3; ++g)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) bv[c][g][q] = a.wh[(int64_t)(k0 + 16 * c + q) * a.ldwh + g * H + u0 + i];
+
   const int ti = tid >> 4;
   const int tj = tid & 15;
   const int bb = b0 + ti;
   const int u = u0 + tj;
   const bool bb_ok = bb < a.Bm;
   const int bbc = bb_ok ? bb : b0;
+  const bool row_in = b0 + i < a.Bm;  // the lane's A row
+  const int rowc = row_in ? b0 + i : b0;
   const float bhn = a.bhn[u];
   const int64_t slot_size = (int64_t)a.Bm * H;
-  // this thread's input projections, loaded a step ahead (no other
-  // workgroup writes them)
+  // this thread's input projections, loaded a step ahead, and its own
+  // previous h (no other workgroup writes them)
   const float* x = a.xi + (int64_t)bbc * a.ldxi;
   float xn = x[u], xr = x[H + u], xz = x[2 * H + u];
+  float hp_raw = a.h0[(a.h0_rows ? (int64_t)a.h0_rows[bbc] : (int64_t)bbc) * a.ldh0 + u];
+  if (tid == 0) gave_up = -1;  // (published by the first flag chunk's barriers)
 
   for (int t = 0; t < a.T; ++t) {
     const int j = t % FLAG_CHUNK;
     if (j == 0) load_flag_chunk(done, a.term, a.trunc, a.flag_rows, a.flag_step, a.Bm, a.T, b0, t, 1);
     const bool reset_e = done[j][ti] != 0;
-    const bool live = done[j][i] == 0;
-    if (t == 0) {
-      // the carries entering the sequence, gathered through h0_rows
-      for (int e = tid; e < TILE * H; e += 256) {
-        const int r = e / H, c = e - r * H;
-        const int b = b0 + r;
-        float v = 0.f;
-        if (b < a.Bm) v = a.h0[(a.h0_rows ? (int64_t)a.h0_rows[b] : (int64_t)b) * a.ldh0 + c];
-        sA[r * P + c] = v;
-      }
-      __syncthreads();
-    } else if (!stage_exchange<H>(a.sync.ring + ((t - 1) & 1) * slot_size, a.Bm, b0, (unsigned)t, sA, a.sync)) {
-      return;
-    }
-    floatx4 av[NIT];
-    float bv[NIT][3][4];
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      const int k = kbeg + 16 * it + 4 * kq;
-      av[it] = *reinterpret_cast<const floatx4*>(&sA[i * P + k]);
-#pragma unroll
-      for (int g = 0; g < 3; ++g) {
-        const floatx4 w = *reinterpret_cast<const floatx4*>(&sW[(g * TILE + i) * P + k]);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) bv[it][g][q] = w[q];
-      }
-    }
-    const float hp_raw = sA[ti * P + u];
-    float xn_next = 0.f, xr_next = 0.f, xz_next = 0.f;
-    if (t + 1 < a.T) {
-      const float* xt = x + (t + 1) * a.xi_step;
-      xn_next = xt[u];
-      xr_next = xt[H + u];
-      xz_next = xt[2 * H + u];
-    }
-
+    const bool live = done[j][i] == 0;  // a reset sequence starts from h = 0
     floatx4 acc[3];
 #pragma unroll
     for (int g = 0; g < 3; ++g) acc[g] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      floatx4 avv = av[it];
-      if (!live) avv = floatx4{0.f, 0.f, 0.f, 0.f};  // a reset sequence starts from h = 0
+    auto mfma_chunk = [&](int c, const float (&av)[4]) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
 #pragma unroll
         for (int g = 0; g < 3; ++g)
-          acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(avv[q], bv[it][g][q], acc[g], 0, 0, 0);
+          acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[q], bv[c][g][q], acc[g], 0, 0, 0);
+      }
+    };
+    float xn_next = 0.f, xr_next = 0.f, xz_next = 0.f;
+    auto load_next = [&]() {
+      if (t + 1 < a.T) {
+        const float* xt = x + (t + 1) * a.xi_step;
+        xn_next = xt[u];
+        xr_next = xt[H + u];
+        xz_next = xt[2 * H + u];
+      }
+    };
+    bool ok = true;
+    if (t == 0) {
+      // the carries entering the sequence, gathered through h0_rows
+      const float* h0r = a.h0 + (a.h0_rows ? (int64_t)a.h0_rows[rowc] : (int64_t)rowc) * a.ldh0 + k0;
+      load_next();
+#pragma unroll
+      for (int c = 0; c < NIT; ++c) {
+        float av[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) av[q] = live ? h0r[16 * c + q] : 0.f;
+        mfma_chunk(c, av);
+      }
+    } else {
+      ok = stage_wave<H, H / WAVES>(a.sync.ring + ((t - 1) & 1) * slot_size, a.Bm, b0, wave * (H / WAVES),
+                                    (unsigned)t, sAw, a.sync.spin_limit);
+      load_next();  // (issued after the wait, so that they do not hold it up)
+#pragma unroll
+      for (int c = 0; c < NIT; ++c) {
+        const floatx4 w = *reinterpret_cast<const floatx4*>(&sAw[i * (H / WAVES + 4) + 16 * c + 4 * kq]);
+        float av[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) av[q] = live ? w[q] : 0.f;
+        mfma_chunk(c, av);
       }
     }
+    if (!ok && lane == 0) {
+      __hip_atomic_fetch_or(a.sync.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      gave_up = t;
+    }
+    float (*rt)[3][TILE][TILE + 1] = red[t & 1];
 #pragma unroll
     for (int g = 0; g < 3; ++g)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) red[wave][g][4 * kq + v][i] = acc[g][v];
-    // (after this barrier no thread reads sA or red of this step until the
-    // next step's staging barrier, so the next staging may overwrite sA)
+      for (int v = 0; v < 4; ++v) rt[wave][g][4 * kq + v][i] = acc[g][v];
     __syncthreads();
+    if (gave_up == t) return;
 
     if (bb_ok) {
       float ar = 0.f, az = 0.f, an = 0.f;
 #pragma unroll
       for (int w = 0; w < WAVES; ++w) {
-        ar += red[w][0][ti][tj];
-        az += red[w][1][ti][tj];
-        an += red[w][2][ti][tj];
+        ar += rt[w][0][ti][tj];
+        az += rt[w][1][ti][tj];
+        an += rt[w][2][ti][tj];
       }
       const float hp = reset_e ? 0.f : hp_raw;
       float r, z, hn, n;
@@ -545,6 +568,7 @@ __global__ void __launch_bounds__(256) gru_fwd_seq_kernel(FwdSeqArgs a) {
         g[2 * H + u] = z;
         g[3 * H + u] = hn;
       }
+      hp_raw = h;
     }
     xn = xn_next;
     xr = xr_next;
@@ -564,27 +588,29 @@ struct BwdSeqArgs {
   SeqSync sync;
 };
 
-// dynamic LDS: [16 units][3H + 4] (rows u0 .. u0 + 15 of the recurrent kernel),
-// then [16 sequences][3H + 4] (the block's dgate_{s+1}[:, H:4H])
 template <int NIT>
 __global__ void __launch_bounds__(256) gru_bwd_seq_kernel(BwdSeqArgs a) {
   constexpr int H3 = 64 * NIT;
   constexpr int H = H3 / 3;
-  constexpr int P = H3 + 4;
-  extern __shared__ float sW[];
-  float* sA = sW + TILE * P;
-  __shared__ float red[WAVES][TILE][TILE + 1];
+  __shared__ float red[2][WAVES][TILE][TILE + 1];
+  __shared__ float sA[WAVES][TILE * (H3 / WAVES + 4)];  // each wave's staged quarter of dgate_{s+1}[:, H:4H]
   __shared__ uint8_t done[FLAG_CHUNK][TILE];
+  __shared__ int gave_up;  // the step at which a wait gave up, -1 while none has
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int b0 = blockIdx.x * TILE;
   const int u0 = blockIdx.y * TILE;
-  for (int e = tid; e < TILE * H3; e += 256) {
-    const int i = e / H3, c = e - i * H3;
-    sW[i * P + c] = a.wh[(int64_t)(u0 + i) * a.ldwh + c];
-  }
-  __syncthreads();
+  const int i = lane & 15;
+  const int kq = lane >> 4;
+  // this lane's columns: k0 + 16 c + q, c < NIT, q < 4 (the wave's quarter of 3H)
+  const int k0 = wave * (H3 / WAVES) + 4 * kq;
+  float* sAw = sA[wave];
+  float bv[NIT][4];
+#pragma unroll
+  for (int c = 0; c < NIT; ++c)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bv[c][q] = a.wh[(int64_t)(u0 + i) * a.ldwh + k0 + 16 * c + q];
 
   const int ti = tid >> 4;
   const int tj = tid & 15;
@@ -592,10 +618,7 @@ __global__ void __launch_bounds__(256) gru_bwd_seq_kernel(BwdSeqArgs a) {
   const int u = u0 + tj;
   const bool bb_ok = bb < a.Bm;
   const int bbc = bb_ok ? bb : b0;
-  const int i = lane & 15;
-  const int kq = lane >> 4;
-  const bool live = b0 + i < a.Bm;
-  const int kbeg = wave * (H3 / WAVES);
+  const bool live = b0 + i < a.Bm;  // the lane's A row
   const int64_t slot_size = (int64_t)a.Bm * H3;
   // step s's own operands, loaded a step ahead (no other workgroup writes
   // them); dh and z of step s + 1 stay in registers from that step
@@ -611,6 +634,7 @@ __global__ void __launch_bounds__(256) gru_bwd_seq_kernel(BwdSeqArgs a) {
   float dout, n, r, z, hn, hp;
   own(a.T - 1, dout, n, r, z, hn, hp);
   float dh_t = 0.f, z_t = 0.f;
+  if (tid == 0) gave_up = -1;  // (published by the first flag chunk's barriers)
 
   for (int s = a.T - 1; s >= 0; --s) {
     const int t = s + 1;
@@ -622,33 +646,32 @@ __global__ void __launch_bounds__(256) gru_bwd_seq_kernel(BwdSeqArgs a) {
       // this thread's own dh_t and step t's update gate and resets
       const float direct = __fmul_rn(dh_t, z_t);
       const bool reset_t = done[j][ti] != 0;
-      if (!stage_exchange<H3>(a.sync.ring + (t & 1) * slot_size, a.Bm, b0, (unsigned)(a.T - t), sA, a.sync))
-        return;
+      // dhp[b][u] = sum_c dgate_t[b][H + c] Wh[u][c], c < 3H
+      const bool ok = stage_wave<H3, H3 / WAVES>(a.sync.ring + (t & 1) * slot_size, a.Bm, b0, wave * (H3 / WAVES),
+                                                 (unsigned)(a.T - t), sAw, a.sync.spin_limit);
       // (issued after the wait, so that they do not hold it up)
       if (s > 0) own(s - 1, dout_n, n_n, r_n, z_n, hn_n, hp_n);
-      // dhp[b][u] = sum_c dgate_t[b][H + c] Wh[u][c], c < 3H
-      floatx4 av[NIT], bv[NIT];
-#pragma unroll
-      for (int it = 0; it < NIT; ++it) {
-        const int k = kbeg + 16 * it + 4 * kq;
-        av[it] = *reinterpret_cast<const floatx4*>(&sA[i * P + k]);
-        bv[it] = *reinterpret_cast<const floatx4*>(&sW[i * P + k]);
-      }
       floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int it = 0; it < NIT; ++it) {
-        floatx4 x = av[it];
-        if (!live) x = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < NIT; ++c) {
+        const floatx4 w = *reinterpret_cast<const floatx4*>(&sAw[i * (H3 / WAVES + 4) + 16 * c + 4 * kq]);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[q], bv[it][q], acc, 0, 0, 0);
+        for (int q = 0; q < 4; ++q) {
+          const float x = live ? w[q] : 0.f;
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x, bv[c][q], acc, 0, 0, 0);
+        }
       }
+      if (!ok && lane == 0) {
+        __hip_atomic_fetch_or(a.sync.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        gave_up = s;
+      }
+      float (*rs)[TILE][TILE + 1] = red[s & 1];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) red[wave][4 * kq + v][i] = acc[v];
-      // (after this barrier no thread reads sA or red of this step until the
-      // next step's staging barrier)
+      for (int v = 0; v < 4; ++v) rs[wave][4 * kq + v][i] = acc[v];
       __syncthreads();
+      if (gave_up == s) return;
       if (bb_ok) {
-        const float dhp = red[0][ti][tj] + red[1][ti][tj] + red[2][ti][tj] + red[3][ti][tj] + direct;
+        const float dhp = rs[0][ti][tj] + rs[1][ti][tj] + rs[2][ti][tj] + rs[3][ti][tj] + direct;
         if (!reset_t) dh += dhp;
       }
     } else if (s > 0) {
@@ -779,12 +802,11 @@ PPO_EXPORT int64_t ppo_gru_seq_exchange_bytes(int Bm, int H) {
   return Bm > 0 && H > 0 ? 2 * (int64_t)Bm * 3 * H * (int64_t)sizeof(u64) : 0;
 }
 
-// Launches a persistent kernel with `lds` bytes of dynamic LDS (beyond the
-// 64 KiB a launch gets without asking).
+// Launches a persistent kernel (one workgroup of 256 threads per 16 x 16
+// tile, all resident at once).
 template <typename Kernel, typename Args>
-static void launch_seq(Kernel k, dim3 grid, size_t lds, hipStream_t st, const Args& a) {
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  hipLaunchKernelGGL(k, grid, dim3(256), lds, st, a);
+static void launch_seq(Kernel k, dim3 grid, hipStream_t st, const Args& a) {
+  hipLaunchKernelGGL(k, grid, dim3(256), 0, st, a);
 }
 
 static void zero_ring(hipStream_t st, void* ring, int64_t n) {
@@ -834,12 +856,11 @@ PPO_EXPORT int ppo_gru_fwd_seq_f32(void* stream, const float* xi, int64_t ldxi, 
   hipStream_t st = ppo::as_stream(stream);
   if (T > 1) zero_ring(st, exchange, 2 * (int64_t)Bm * H);
   const dim3 grid(ppo::ceil_div(Bm, TILE), H / TILE);
-  const size_t lds = sizeof(float) * 4 * TILE * (H + 4);
   switch (H / 64) {
-    case 1: launch_seq(gru_fwd_seq_kernel<1>, grid, lds, st, a); break;
-    case 2: launch_seq(gru_fwd_seq_kernel<2>, grid, lds, st, a); break;
-    case 3: launch_seq(gru_fwd_seq_kernel<3>, grid, lds, st, a); break;
-    default: launch_seq(gru_fwd_seq_kernel<4>, grid, lds, st, a); break;
+    case 1: launch_seq(gru_fwd_seq_kernel<1>, grid, st, a); break;
+    case 2: launch_seq(gru_fwd_seq_kernel<2>, grid, st, a); break;
+    case 3: launch_seq(gru_fwd_seq_kernel<3>, grid, st, a); break;
+    default: launch_seq(gru_fwd_seq_kernel<4>, grid, st, a); break;
   }
   return ppo::check_launch("ppo_gru_fwd_seq_f32");
 }
@@ -871,12 +892,11 @@ PPO_EXPORT int ppo_gru_bwd_seq_f32(void* stream, const float* wh, int64_t ldwh, 
   hipStream_t st = ppo::as_stream(stream);
   if (T > 1) zero_ring(st, exchange, 2 * (int64_t)Bm * 3 * H);
   const dim3 grid(ppo::ceil_div(Bm, TILE), H / TILE);
-  const size_t lds = sizeof(float) * 2 * TILE * (3 * H + 4);
   switch (3 * H / 64) {
-    case 3: launch_seq(gru_bwd_seq_kernel<3>, grid, lds, st, a); break;
-    case 6: launch_seq(gru_bwd_seq_kernel<6>, grid, lds, st, a); break;
-    case 9: launch_seq(gru_bwd_seq_kernel<9>, grid, lds, st, a); break;
-    default: launch_seq(gru_bwd_seq_kernel<12>, grid, lds, st, a); break;
+    case 3: launch_seq(gru_bwd_seq_kernel<3>, grid, st, a); break;
+    case 6: launch_seq(gru_bwd_seq_kernel<6>, grid, st, a); break;
+    case 9: launch_seq(gru_bwd_seq_kernel<9>, grid, st, a); break;
+    default: launch_seq(gru_bwd_seq_kernel<12>, grid, st, a); break;
   }
   return ppo::check_launch("ppo_gru_bwd_seq_f32");
 }
