@@ -78,6 +78,7 @@ SIGNATURES = {
     "ppo_gemm_bf16s_dw_group": (I, [P, I, P, P, P, P, P, P, P, P, P, P, P, P, P]),
     "ppo_cast_bf16": (I, [P, P, P, I64]),
     "ppo_cast_bf16_2d": (I, [P, P, I64, P, I64, I, I]),
+    "ppo_pad_rows_f32": (I, [P, P, I64, P, I64, I, I]),
     "ppo_splits_bias_act_bf16": (I, [P, P, I64, I64, I, P, I, P, I64, I, I]),
     "ppo_layernorm_act_fwd_f32": (I, [P, P, I64, P, P, P, I64, P, P, I, I, F, I]),
     "ppo_layernorm_act_fwd_bf16": (I, [P, P, I64, P, P, P, I64, P, P, I, I, F, I]),

@@ -259,6 +259,24 @@ int launch_layout(hipStream_t st, const GemmParams& p, int splits, bool va, bool
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
+// y[r][4 u .. 4 u + 3] = x[r][c] for c < cols, 0 up to ldy: one thread per
+// four output columns, one 16-byte store.
+__global__ void pad_rows_kernel(const float* __restrict__ x, int64_t ldx, float* __restrict__ y, int64_t ldy,
+                                int rows, int cols) {
+  const int64_t units = ldy / 4;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)rows * units) return;
+  const int64_t r = i / units;
+  const int c0 = (int)(i - r * units) * 4;
+  const float* xr = x + r * ldx;
+  float4 v;
+  v.x = c0 < cols ? xr[c0] : 0.f;
+  v.y = c0 + 1 < cols ? xr[c0 + 1] : 0.f;
+  v.z = c0 + 2 < cols ? xr[c0 + 2] : 0.f;
+  v.w = c0 + 3 < cols ? xr[c0 + 3] : 0.f;
+  *reinterpret_cast<float4*>(y + r * ldy + c0) = v;
+}
+
 }  // namespace
 
 // Generic entry: C[m][n] (+ split * c_split_stride) = epilogue(sum_k A(m,k) B(k,n)).
@@ -348,4 +366,23 @@ PPO_EXPORT int ppo_gemm_f32_towers(void* stream, int towers, int a_layout, int b
   const int64_t t[7] = {stride_a, stride_b, stride_c, stride_bias, stride_pre, stride_aux, stride_bias_grad};
   return gemm_f32_impl(stream, a_layout, b_layout, A, lda, rows, B, ldb, C, ldc, M, N, K, splits, c_split_stride,
                        epi, bias, act, pre, aux, ldaux, bias_grad, tile, towers, t);
+}
+
+// Row-pitched copy that pads each row with zeros: y[r][c] = x[r][c] for
+// c < cols, 0 for cols <= c < ldy (ldy a multiple of 4, y 16-byte aligned; x
+// any pitch).  The per-update copy of observation rows whose width is not a
+// multiple of four, so that the first layer's weight gradient runs on the
+// copy-fed GEMM over the padded width.
+PPO_EXPORT int ppo_pad_rows_f32(void* stream, const float* x, int64_t ldx, float* y, int64_t ldy, int rows,
+                                int cols) {
+  if (rows < 0 || cols < 0 || ldx < cols || ldy < cols || ldy % 4 != 0)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_pad_rows_f32: bad shape (rows=%d cols=%d ldx=%lld ldy=%lld)", rows,
+                          cols, (long long)ldx, (long long)ldy);
+  if (rows == 0 || ldy == 0) return PPO_OK;
+  if (!x || !y || !aligned16(y))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_pad_rows_f32: buffers must be non-null and y 16-byte aligned");
+  const int64_t n = (int64_t)rows * (ldy / 4);
+  hipLaunchKernelGGL(pad_rows_kernel, dim3((unsigned)ppo::ceil_div64(n, 256)), dim3(256), 0, ppo::as_stream(stream),
+                     x, ldx, y, ldy, rows, cols);
+  return ppo::check_launch("ppo_pad_rows_f32");
 }

@@ -300,7 +300,7 @@ def split_forward_bufs(lb: LayerBufs, rows: int, device, bf16: bool) -> None:
 
 
 def paired_tower_bufs(specs_a, specs_c, rows: int, device, ln_blocks: int | None = None,
-                      grouped_dw: bool = False) -> tuple:
+                      grouped_dw: bool = False, fin0_pad: int = 0) -> tuple:
     """Training buffers of two towers of one shape (actor and critic, layer by
     layer): each kind of buffer of consecutive layers of one shape is one
     [layers, 2, ...] tensor, so the critic's buffer sits one fixed stride
@@ -309,7 +309,10 @@ def paired_tower_bufs(specs_a, specs_c, rows: int, device, ln_blocks: int | None
     batched over depth addresses).  ``ln_blocks``: LayerNorm partial blocks
     of the backward that writes them (default: the row kernel's);
     ``grouped_dw``: the weight gradients past the first layer run as one
-    launch batched over depth and towers."""
+    launch batched over depth and towers.  ``fin0_pad``: the first layer's
+    weight-gradient partials hold this many input rows (the width of a
+    zero-padded copy of its input; the rows past the layer's own are never
+    read)."""
     f32 = dict(dtype=torch.float32, device=device)
     L = len(specs_a)
     A = [LayerBufs(sa, Y=None) for sa in specs_a]
@@ -350,7 +353,8 @@ def paired_tower_bufs(specs_a, specs_c, rows: int, device, ln_blocks: int | None
         A[i].splits = C[i].splits = max(1, _splits(rows, s.dense.fin, s.ld) // (2 if half else 1))
         if ln[i]:
             A[i].lnblocks = C[i].lnblocks = blocks
-    alloc("wpart", [(a.splits, s.dense.fin, s.ld) for a, s in zip(A, specs_a)])
+    alloc("wpart", [(a.splits, max(s.dense.fin, fin0_pad) if i == 0 else s.dense.fin, s.ld)
+                    for i, (a, s) in enumerate(zip(A, specs_a))])
     alloc("bpart", [(a.splits, s.ld) for a, s in zip(A, specs_a)])
     return A, C
 
@@ -684,10 +688,16 @@ class MLPExecutor(ForwardChain):
         # towers of 256-wide LayerNorm layers (one activation, one epsilon)
         # run each direction of the whole torso chain in one launch
         self.chain_ln = bool(self.pair) and self.CHAIN and self._chainable(program.actor_layers)
+        # observation rows whose width is not a multiple of four: a zero-padded
+        # copy per update lets the first layer's weight gradient run on the
+        # copy-fed GEMM over the padded width (the Gaussian workload's 87
+        # features: 10.2 us per step on the register-staged kernel)
+        fin0 = program.actor_layers[0].dense.fin if program.actor_layers else 0
+        self.obs_pad = (fin0 + 3) // 4 * 4 if self.chain_ln and fin0 % 4 != 0 and fin0 == self.obs_dim else 0
         if self.pair:
             lnb = _lib.load().ppo_mlp_ln_bwd_blocks(mb) if self.chain_ln else None
             self.actor, self.critic = paired_tower_bufs(program.actor_layers, program.critic_layers, mb, dev, lnb,
-                                                        grouped_dw=self.chain_ln)
+                                                        grouped_dw=self.chain_ln, fin0_pad=self.obs_pad)
         else:
             self.actor = [layer_bufs(s, mb, True) for s in program.actor_layers]
             self.critic = [layer_bufs(s, mb, True) for s in program.critic_layers]
@@ -697,6 +707,8 @@ class MLPExecutor(ForwardChain):
         firsts = [g[0] for g in (self.trunk, self.actor, self.critic) if g]
         self.obs16 = (self.bf16 and program.gru is None and self.obs_dim % 4 == 0 and bool(firsts)
                       and all(lb.spec.ld % 8 == 0 and lb.spec.dense.w.ld % 8 == 0 for lb in firsts))
+        if self.obs_pad:
+            self.OBSP = torch.zeros(self.B, self.obs_pad, dtype=torch.float32, device=dev)
         if self.obs16:
             i16 = dict(dtype=torch.int16, device=dev)
             self.ldo16 = (self.obs_dim + 7) // 8 * 8
@@ -954,8 +966,10 @@ class MLPExecutor(ForwardChain):
         rb = 1 if self.bf16 else 0   # a bf16 Dense's kernel and bias gradients are bf16 values
 
         def dense_segs(spec: DenseSpec, wpart, bpart, splits):
+            # (a split's partial may hold more input rows than the layer's:
+            # a zero-padded input's gradient rows, which the sum skips)
             n = spec.fin * spec.w.ld
-            segs.append((G + 4 * spec.w.offset, wpart.data_ptr(), n, n, splits, rb))
+            segs.append((G + 4 * spec.w.offset, wpart.data_ptr(), n, wpart.stride(0), splits, rb))
             if spec.b is not None:
                 segs.append((G + 4 * spec.b.offset, bpart.data_ptr(), spec.w.ld, spec.w.ld, splits, rb))
 
@@ -1189,9 +1203,13 @@ class MLPExecutor(ForwardChain):
                 s = la.spec
                 d = s.dense
                 x, ldx, ridx = (x0, ldx0, idx0) if i == 0 else (_p(A[i - 1].Y), A[i - 1].spec.ld, None)
+                fin = d.fin
+                if i == 0 and self.obs_pad:
+                    # the zero-padded observation copy, over its padded width
+                    x, ldx, fin = _p(self.OBSP), self.obs_pad, self.obs_pad
                 # problem k + 1 sits one (actor -> critic, or critic -> next actor) step after problem k
                 self._call("ppo_gemm_f32_towers", st, n, A_COL, B_KN, x, ldx, ridx, _p(la.dZ), s.ld, _p(la.wpart),
-                           s.ld, d.fin, s.ld, self.mb, la.splits, d.fin * s.ld, EPI_STORE, None, 0, None, None, 0,
+                           s.ld, fin, s.ld, self.mb, la.splits, fin * s.ld, EPI_STORE, None, 0, None, None, 0,
                            _p(la.bpart), -1, sx, _tstride(la.dZ, lc.dZ), _tstride(la.wpart, lc.wpart), 0, 0, 0,
                            _tstride(la.bpart, lc.bpart))
             return
@@ -1279,6 +1297,8 @@ class MLPExecutor(ForwardChain):
         inp, prog, cfg, chain = self.inp, self.prog, self.cfg, self.chain
         T, N, B, mb = self.T, self.N, self.B, self.mb
         obs, ldo = inp["obs"], self.obs_dim
+        if self.obs_pad:
+            self._call("ppo_pad_rows_f32", st, obs, ldo, _p(self.OBSP), self.obs_pad, B, ldo)
         if self.obs16:
             # bf16 copies the first-layer GEMMs read: the rollout's observations
             # (once per update) and the parameters (Adam refreshes the image)

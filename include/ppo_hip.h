@@ -412,6 +412,14 @@ int ppo_gemm_bf16s_dw_group(void* stream, int count, const void* const* A, const
                             const int32_t* const* rows, const void* const* B, const int64_t* ldb, float* const* C,
                             const int64_t* ldc, const int* M, const int* N, const int* K, const int* splits,
                             const int64_t* c_split_stride, float* const* bias_grad);
+/* Row-pitched float32 copy padded with zeros: y[r][c] = x[r][c] for c < cols,
+ * 0 for cols <= c < ldy (ldy a multiple of 4, y 16-byte aligned).  The
+ * per-update copy of observation rows whose width is not a multiple of four
+ * (obs [16, 4096, 87] of the Gaussian workload), which lets the first layer's
+ * weight gradient (ppo.py:148-151 gather, then the Dense of
+ * networks/network.py:18-49 under jax.grad) run on the copy-fed GEMM over the
+ * padded width; the pad columns' gradient rows are never read. */
+int ppo_pad_rows_f32(void* stream, const float* x, int64_t ldx, float* y, int64_t ldy, int rows, int cols);
 /* y[i] = bf16(x[i]) as 16-bit patterns (the bf16 parameter image); 16-byte aligned. */
 int ppo_cast_bf16(void* stream, const float* x, void* y, int64_t n);
 /* Row-pitched bf16 copy (the per-update observation copy): y[r][c] = bf16(x[r][c])

@@ -242,6 +242,42 @@ def test_silu_and_its_derivative_on_special_and_extreme_arguments():
     assert np.isfinite(dx[fin]).all()
 
 
+@pytest.mark.parametrize("rows, cols, ldx, ldy", [(65536, 87, 87, 88), (5, 3, 7, 8), (1, 4, 4, 12), (300, 1, 1, 4)])
+def test_pad_rows_copies_and_zero_fills(rows, cols, ldx, ldy):
+    rng = np.random.default_rng(rows + cols)
+    X = rng.normal(size=(rows, ldx)).astype(np.float32)
+    Y = torch.full((rows, ldy), float("nan"), device=DEV)
+    _lib.call("ppo_pad_rows_f32", st(), dev(X).data_ptr(), ldx, Y.data_ptr(), ldy, rows, cols)
+    want = np.zeros((rows, ldy), np.float32)
+    want[:, :cols] = X[:, :cols]
+    assert np.array_equal(host(Y), want)
+
+
+def test_weight_gradient_over_a_zero_padded_input_matches_the_unpadded_one():
+    # the first layer's dW of the paired towers over the padded observation
+    # copy (87 -> 88 columns, the copy-fed kernel) against the same contraction
+    # on the unpadded rows (the register-staged kernel): the 87 real rows agree
+    # to fp32 rounding, the pad row is zero
+    rng = np.random.default_rng(7)
+    R, F, N, mb, splits = 4096, 87, 256, 2048, 8
+    obs = dev(rng.normal(size=(R, F)).astype(np.float32))
+    idx = dev(rng.permutation(R)[:mb].astype(np.int32))
+    dZ = dev(rng.normal(size=(mb, N)).astype(np.float32))
+    pad = torch.zeros(R, 88, device=DEV)
+    _lib.call("ppo_pad_rows_f32", st(), obs.data_ptr(), F, pad.data_ptr(), 88, R, F)
+    out = {}
+    for name, x, ld, M in (("plain", obs, F, F), ("padded", pad, 88, 88)):
+        part = torch.zeros(splits, M, N, device=DEV)
+        bpart = torch.zeros(splits, N, device=DEV)
+        _lib.call("ppo_gemm_f32", st(), 1, 0, x.data_ptr(), ld, idx.data_ptr(), dZ.data_ptr(), N, part.data_ptr(), N,
+                  M, N, mb, splits, M * N, 0, None, 0, None, None, 0, bpart.data_ptr(), -1)
+        out[name] = host(part).astype(np.float64).sum(0)
+    want = host(obs).astype(np.float64)[host(idx)].T @ host(dZ).astype(np.float64)
+    np.testing.assert_allclose(out["plain"], want, rtol=2e-5, atol=2e-4)
+    np.testing.assert_allclose(out["padded"][:F], want, rtol=2e-5, atol=2e-4)
+    assert np.array_equal(out["padded"][F], np.zeros(N))
+
+
 @pytest.mark.parametrize("splits", [1, 4, 64])
 def test_gemm_split_rows_with_bias_gradient(splits):
     gemm_case(1, 0, 400, 256, 4096, rows_src=8192, gather=True, splits=splits, bias_grad=True)

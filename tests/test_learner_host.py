@@ -196,14 +196,21 @@ def test_gaussian_update_runs_each_torso_chain_in_one_launch():
         for k in range(n):
             i, t = first + k // 2, k % 2
             lb = (ex.actor, ex.critic)[t][i]
+            fin = lb.spec.dense.fin
             if i > 0:
                 assert A_ + 4 * k * sa == (ex.actor, ex.critic)[t][i - 1].Y.data_ptr()
             else:
-                assert sa == 0 and A_ == 4096   # both towers read the observation rows
+                # both towers read the observation rows: 87 features, so the
+                # zero-padded copy over 88 columns (partials of 88 rows)
+                assert sa == 0 and ex.obs_pad == 88 and A_ == ex.OBSP.data_ptr() and a[5] == 88
+                fin = 88
+                assert lb.wpart.shape[1] == 88
             assert B_ + 4 * k * sb == lb.dZ.data_ptr()
             assert C_ + 4 * k * sc == lb.wpart.data_ptr()
             assert bg + 4 * k * sbg == lb.bpart.data_ptr()
-            assert a[11] == lb.spec.dense.fin and a[13] == ex.mb and a[14] == lb.splits
+            assert a[11] == fin and a[13] == ex.mb and a[14] == lb.splits
+            assert a[15] == fin * lb.spec.ld    # the partials' split stride
+    assert names.count("ppo_pad_rows_f32") == 1   # the padded observation copy, once per update
     assert names.count("ppo_gemm_f32") == 1   # the bootstrap value head
     for gone in ("ppo_gemm_ln_act_fwd_f32", "ppo_gemm_ln_act_fwd_f32_towers", "ppo_layernorm_act_fwd_f32",
                  "ppo_layernorm_act_bwd_f32", "ppo_layernorm_act_bwd_f32_towers", "ppo_stream_wait"):
