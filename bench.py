@@ -108,9 +108,12 @@ def launch_work(name, args):
     return towers * flops, towers * nbytes
 
 
+DW_GROUPS = ("ppo_gemm_bf16s_dw_group", "ppo_gemm_f32_dw_group")
+
+
 def dw_group_problems(args):
-    """[(M, N, K, splits)] of a ppo_gemm_bf16s_dw_group call, read from its
-    host argument arrays."""
+    """[(M, N, K, splits)] of a ppo_gemm_bf16s_dw_group or ppo_gemm_f32_dw_group
+    call, read from its host argument arrays."""
     import ctypes
     L = int(args[1])
     ints = [list((ctypes.c_int * L).from_address(args[i])) for i in (9, 10, 11, 12)]
@@ -118,10 +121,11 @@ def dw_group_problems(args):
 
 
 def _single_launch_work(name, args):
-    if name == "ppo_gemm_bf16s_dw_group":
+    if name in DW_GROUPS:
         probs = dw_group_problems(args)
+        e = 2.0 if name == "ppo_gemm_bf16s_dw_group" else 4.0   # operand element bytes
         return (sum(2.0 * M * N * K for M, N, K, _ in probs),
-                sum(2.0 * M * K + 2.0 * K * N + 4.0 * M * N * S for M, N, K, S in probs))
+                sum(e * M * K + e * K * N + 4.0 * M * N * S for M, N, K, S in probs))
     if name in ("ppo_gemm_f32", "ppo_gemm_bf16"):
         M, N, K = args[10], args[11], args[12]
         return 2.0 * M * N * K, 4.0 * (M * K + K * N + M * N)
@@ -237,7 +241,7 @@ def launch_shape(name, args):
 
 
 def _single_launch_shape(name, args):
-    if name == "ppo_gemm_bf16s_dw_group":  # the first problem's [M, N, K] and the problem count
+    if name in DW_GROUPS:  # the first problem's [M, N, K] and the problem count
         M, N, K, _ = dw_group_problems(args)[0]
         return [M, N, K, int(args[1])]
     if name in ("ppo_gemm_f32", "ppo_gemm_bf16"):
@@ -267,7 +271,7 @@ def launch_layout(name, args):
     name, args, _ = untower(name, args)
     if name in ("ppo_gemm_f32", "ppo_gemm_bf16", "ppo_gemm_bf16s"):
         return [args[1], args[2]]
-    if name == "ppo_gemm_bf16s_dw_group":
+    if name in DW_GROUPS:
         return [1, 0]
     return None
 
@@ -281,7 +285,7 @@ def launch_key(name, args):
         return (name, args[1], args[2]) + tuple(args[10:16])
     if name == "ppo_gemm_bf16s":
         return (name,) + tuple(args[1:5]) + tuple(args[12:16])
-    if name == "ppo_gemm_bf16s_dw_group":
+    if name in DW_GROUPS:
         return (name,) + tuple(dw_group_problems(args))
     if name in ("ppo_gru_fwd_step_f32", "ppo_gru_bwd_step_f32"):
         return (name, args[-2], args[-1], bool(args[1]))

@@ -386,3 +386,55 @@ PPO_EXPORT int ppo_pad_rows_f32(void* stream, const float* x, int64_t ldx, float
                      x, ldx, y, ldy, rows, cols);
   return ppo::check_launch("ppo_pad_rows_f32");
 }
+
+// Weight gradients of several fp32 Dense layers in one launch (64 x 64
+// copy-fed tiles): problem i is what ppo_gemm_f32(a_layout = 1, b_layout = 0,
+// epi = store, tile = 3) computes from the same arguments, with the same bits.
+// Every operand row 16-byte vectorisable (lda, ldb and M[i], N[i] multiples
+// of 4, 16-byte aligned pointers); a gathered problem's split holds at most
+// F32D_KIDX_MAX rows.
+PPO_EXPORT int ppo_gemm_f32_dw_group(void* stream, int count, const float* const* A, const int64_t* lda,
+                                     const int32_t* const* rows, const float* const* B, const int64_t* ldb,
+                                     float* const* C, const int64_t* ldc, const int* M, const int* N, const int* K,
+                                     const int* splits, const int64_t* c_split_stride, float* const* bias_grad) {
+  using namespace ppo_f32;
+  if (count < 0 || count > F32_GROUP_MAX || (count > 0 && (!A || !lda || !B || !ldb || !C || !ldc || !M || !N ||
+                                                           !K || !splits || !c_split_stride)))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32_dw_group: bad argument (count=%d, at most %d)", count,
+                          F32_GROUP_MAX);
+  F32Group g = {};
+  int64_t total = 0;
+  for (int i = 0; i < count; ++i) {
+    if (M[i] < 0 || N[i] < 0 || K[i] < 0 || splits[i] < 1 || splits[i] > 65535)
+      return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32_dw_group: problem %d: bad shape (M=%d N=%d K=%d splits=%d)", i,
+                            M[i], N[i], K[i], splits[i]);
+    if (M[i] == 0 || N[i] == 0) continue;
+    if (!A[i] || !B[i] || !C[i]) return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32_dw_group: problem %d: null operand", i);
+    if (splits[i] > 1 && c_split_stride[i] < (int64_t)M[i] * ldc[i])
+      return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32_dw_group: problem %d: split stride too small", i);
+    if (lda[i] % 4 || M[i] % 4 || lda[i] < M[i] || !aligned16(A[i]) || ldb[i] % 4 || N[i] % 4 || ldb[i] < N[i] ||
+        !aligned16(B[i]) || ldc[i] < N[i])
+      return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32_dw_group: problem %d: operand rows must be 16-byte aligned "
+                            "with 16-byte vector extents (M=%d N=%d lda=%lld ldb=%lld ldc=%lld)", i, M[i], N[i],
+                            (long long)lda[i], (long long)ldb[i], (long long)ldc[i]);
+    GemmParams& p = g.p[g.count];
+    p = GemmParams{};
+    p.A = A[i]; p.lda = lda[i]; p.rows = rows ? rows[i] : nullptr; p.B = B[i]; p.ldb = ldb[i];
+    p.C = C[i]; p.ldc = ldc[i]; p.c_split_stride = c_split_stride[i]; p.M = M[i]; p.N = N[i]; p.K = K[i];
+    p.k_per_split = ((ppo::ceil_div(K[i] > 0 ? K[i] : 1, splits[i]) + F32D_BK - 1) / F32D_BK) * F32D_BK;
+    p.epi = EPI_STORE; p.act = 0; p.bias_grad = bias_grad ? bias_grad[i] : nullptr;
+    p.splits = splits[i]; p.towers = 1;
+    if (p.rows && p.k_per_split > F32D_KIDX_MAX)
+      return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32_dw_group: problem %d: a gathered split holds %d rows "
+                            "(at most %d)", i, p.k_per_split, F32D_KIDX_MAX);
+    g.gx[g.count] = ppo::ceil_div(N[i], 64);
+    g.gy[g.count] = ppo::ceil_div(M[i], 64);
+    g.start[g.count] = (int)total;
+    total += (int64_t)g.gx[g.count] * g.gy[g.count] * splits[i];
+    if (total > (1 << 30)) return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32_dw_group: too many tiles");
+    ++g.count;
+  }
+  g.start[g.count] = (int)total;
+  if (total == 0) return PPO_OK;
+  return launch_dw_group(ppo::as_stream(stream), g);
+}

@@ -33,6 +33,17 @@ struct GemmParams {
   int64_t tA, tB, tC, tBias, tPre, tAux, tBiasGrad;
 };
 
+// Up to F32_GROUP_MAX GEMMs of one launch (ppo_gemm_f32_dw_group): problem i
+// owns linear tiles [start[i], start[i + 1]) of a gx[i] x gy[i] tile grid per
+// split.
+constexpr int F32_GROUP_MAX = 8;
+struct F32Group {
+  GemmParams p[F32_GROUP_MAX];
+  int start[F32_GROUP_MAX + 1];
+  int gx[F32_GROUP_MAX], gy[F32_GROUP_MAX];
+  int count;
+};
+
 // The operands of tower t of a tower-batched launch.
 __device__ __forceinline__ GemmParams tower_params(const GemmParams& p, int t) {
   GemmParams q = p;
@@ -128,5 +139,7 @@ __device__ __forceinline__ void epilogue_f32(const GemmParams& p, floatx16 (&acc
 constexpr int F32D_BK = 32;
 constexpr int F32D_KIDX_MAX = 2048;
 int launch_dma(hipStream_t st, const GemmParams& p, int splits, int tile, int a_layout, int b_layout);
+// A weight-gradient group (A and B k-outer, 64 x 64 copy-fed tiles).
+int launch_dw_group(hipStream_t st, const F32Group& g);
 
 }  // namespace ppo_f32

@@ -136,8 +136,10 @@ __device__ __forceinline__ floatx4 operand(const float* lds, int rbase, int g, i
   }
 }
 
+// One BM x BN output tile (tile row tm, column tn) of split `split` of the
+// GEMM p.
 template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF>
-__global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_kernel(GemmParams p0) {
+__device__ __forceinline__ void gemm_f32d_tile(const GemmParams& p, int tm, int tn, int split) {
   constexpr int NW = WM * WN;
   constexpr int MB = BM / WM / 32, NB = BN / WN / 32;  // 32 x 32 blocks per wave
   static_assert(MB * WM * 32 == BM && NB * WN * 32 == BN, "tile must split into 32 x 32 blocks");
@@ -151,12 +153,8 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_kernel(GemmParams p0) 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave % WM;
   const int wn = wave / WM;
-  const ppo::TileCoord tc = ppo::xcd_tile();
-  const int tower = tc.z / p0.splits;
-  const int split = tc.z - tower * p0.splits;
-  const GemmParams p = tower_params(p0, tower);
-  const int m0 = tc.m * BM;
-  const int n0 = tc.n * BN;
+  const int m0 = tm * BM;
+  const int n0 = tn * BN;
   const int kb = split * p.k_per_split;
   const int ke = min(p.K, kb + p.k_per_split);
 
@@ -170,7 +168,7 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_kernel(GemmParams p0) 
   float bsum[NB];
 #pragma unroll
   for (int j = 0; j < NB; ++j) bsum[j] = 0.f;
-  const bool do_bsum = (p.bias_grad != nullptr) && (tc.m == 0) && (wm == 0);
+  const bool do_bsum = (p.bias_grad != nullptr) && (tm == 0) && (wm == 0);
 
   // The epilogue's inputs are loaded before the main loop (clamped rows /
   // columns read in-range data for outputs that are not stored), so the
@@ -276,6 +274,32 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_kernel(GemmParams p0) 
     epilogue_f32<MB, NB>(p, acc, bsum, do_bsum, m0 + wm * (BM / WM), n0 + wn * (BN / WN), split, lane, auxv);
 }
 
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF>
+__global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_kernel(GemmParams p0) {
+  const ppo::TileCoord tc = ppo::xcd_tile();
+  const int tower = tc.z / p0.splits;
+  const int split = tc.z - tower * p0.splits;
+  gemm_f32d_tile<BM, BN, WM, WN, A_K, B_K, NBUF>(tower_params(p0, tower), tc.m, tc.n, split);
+}
+
+// Several GEMMs of one tile shape in one launch: problem i owns the linear
+// tiles [start[i], start[i + 1]), ordered n fastest, then m, then split;
+// linear tiles are dealt to the XCDs in contiguous ranges, as xcd_tile does
+// for one GEMM.
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF>
+__global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_group_kernel(F32Group g) {
+  const int total = gridDim.x;
+  const int w = blockIdx.x;
+  const int x = w & 7, j = w >> 3;
+  const int q = total >> 3, r = total & 7;
+  const int t = x * q + (x < r ? x : r) + j;
+  int i = 0;
+  while (i + 1 < g.count && t >= g.start[i + 1]) ++i;
+  const int local = t - g.start[i];
+  gemm_f32d_tile<BM, BN, WM, WN, A_K, B_K, NBUF>(g.p[i], (local / g.gx[i]) % g.gy[i], local % g.gx[i],
+                                                 local / (g.gx[i] * g.gy[i]));
+}
+
 template <int BM, int BN, int WM, int WN, bool A_K, bool B_K>
 int launch(hipStream_t st, const GemmParams& p, int splits) {
   constexpr int NBUF = WM * WN == 4 ? 2 : 3;
@@ -297,6 +321,13 @@ int launch_tile(hipStream_t st, const GemmParams& p, int splits, int tile) {
 }
 
 }  // namespace
+
+// The weight-gradient group (A k-outer, B k-outer) on 64 x 64 tiles.
+int launch_dw_group(hipStream_t st, const F32Group& g) {
+  const int total = g.start[g.count];
+  hipLaunchKernelGGL((gemm_f32d_group_kernel<64, 64, 2, 2, false, false, 2>), dim3(total), dim3(256), 0, st, g);
+  return ppo::check_launch("ppo_gemm_f32_dw_group");
+}
 
 int launch_dma(hipStream_t st, const GemmParams& p, int splits, int tile, int a_layout, int b_layout) {
   if (a_layout == 0 && b_layout == 0) return launch_tile<true, false>(st, p, splits, tile);

@@ -906,6 +906,51 @@ class MLPExecutor(ForwardChain):
                    and _tstride(a.mean, c.mean) == self._chain_ss == _tstride(a.rstd, c.rstd)
                    and _tstride(a.lnpart, c.lnpart) == self._chain_ps for a, c in zip(A, C))
 
+    # the paired towers' weight gradients in one ppo_gemm_f32_dw_group launch
+    # (off: one launch for the first layers, one for the rest)
+    PAIR_DW_GROUP = True
+
+    def _pair_dw_group(self, x0, ldx0):
+        """Host argument arrays of ppo_gemm_f32_dw_group over every weight
+        gradient of the paired towers (layer-major, actor then critic; the
+        first layers read the observation rows, or their zero-padded copy,
+        through the minibatch's gather indices, set per call in rows[0] and
+        rows[1]), or None when a problem does not fit the copy-fed kernel."""
+        A, C = self.actor, self.critic
+        if not self.PAIR_DW_GROUP or 2 * len(A) > 8:
+            return None
+        g = getattr(self, "_dwg", None)
+        if g is not None and g["x0"] == (x0, ldx0):
+            return g if g["args"] else None
+        x, ldx, fin0 = (_p(self.OBSP), self.obs_pad, self.obs_pad) if self.obs_pad else (x0, ldx0, A[0].spec.dense.fin)
+        probs = []  # (A, lda, B, ldb, C, ldc, M, N, splits, bias_grad)
+        for i in range(len(A)):
+            for lb, prev in ((A[i], A[i - 1] if i else None), (C[i], C[i - 1] if i else None)):
+                s = lb.spec
+                a, lda, M = (x, ldx, fin0) if i == 0 else (_p(prev.Y), prev.spec.ld, s.dense.fin)
+                probs.append((a, lda, _p(lb.dZ), s.ld, _p(lb.wpart), s.ld, M, s.ld, lb.splits, _p(lb.bpart)))
+        fits = all(a % 16 == 0 and lda % 4 == 0 and M % 4 == 0 and N % 4 == 0 and b % 16 == 0 and ldb % 4 == 0
+                   and (i >= 2 or -(-self.mb // sp) <= 2048)
+                   for i, (a, lda, b, ldb, _, _, M, N, sp, _) in enumerate(probs))
+        g = {"x0": (x0, ldx0), "args": None}
+        self._dwg = g
+        if not fits:
+            return None
+        L = len(probs)
+        vp = lambda xs: (ctypes.c_void_p * L)(*xs)
+        i64 = lambda xs: (ctypes.c_int64 * L)(*xs)
+        i32 = lambda xs: (ctypes.c_int * L)(*xs)
+        col = lambda j: [p[j] for p in probs]
+        g.update({
+            "A": vp(col(0)), "lda": i64(col(1)), "rows": vp([None] * L), "B": vp(col(2)), "ldb": i64(col(3)),
+            "C": vp(col(4)), "ldc": i64(col(5)), "M": i32(col(6)), "N": i32(col(7)), "K": i32([self.mb] * L),
+            "splits": i32(col(8)), "stride": i64([p[6] * p[5] for p in probs]), "bias_grad": vp(col(9)),
+            "count": L,
+        })
+        order = ("A", "lda", "rows", "B", "ldb", "C", "ldc", "M", "N", "K", "splits", "stride", "bias_grad")
+        g["args"] = [ctypes.addressof(g[k]) for k in order]
+        return g
+
     def _plan_dw_groups(self) -> list:
         """The weight-gradient contractions of the paired towers as batched
         launches: layer 0 of both towers (the gathered observation rows
@@ -1198,6 +1243,12 @@ class MLPExecutor(ForwardChain):
             self._call("ppo_mlp_ln_bwd_f32", st, 2, len(A), _p(A[-1].dY), A[-1].spec.ld, self.mb, c["Z"], c["mean"],
                        c["rstd"], c["g"], c["be"], c["WT"], 256, c["dZ"], A[0].spec.ld, c["part"], self._chain_act,
                        self._chain_rs, self._chain_ss, D, 256 * 256, self._chain_ps)
+            g = self._pair_dw_group(x0, ldx0)
+            if g is not None:
+                # every weight gradient of both towers in one launch
+                g["rows"][0] = g["rows"][1] = idx0
+                self._call("ppo_gemm_f32_dw_group", st, g["count"], *g["args"])
+                return
             for i, n, sx in self._dw_groups:
                 la, lc = A[i], C[i]
                 s = la.spec

@@ -399,6 +399,21 @@ int ppo_gemm_bf16s(void* stream, int a_layout, int b_layout, int a_bf16, int b_b
                    const int32_t* rows, const void* B, int64_t ldb, float* C, int64_t ldc, int M, int N, int K,
                    int splits, int64_t c_split_stride, int epi, const float* bias, int act, int round_out,
                    const float* aux, int64_t ldaux, float* bias_grad, int tile);
+/* The weight gradients of up to 8 fp32 Dense layers in one launch (a
+ * backward pass's dW GEMMs, so that a layer with few tiles runs beside one
+ * with many instead of after it): problem i (host arrays, one entry per
+ * problem; rows and bias_grad may be NULL, or hold NULL entries) is exactly
+ * ppo_gemm_f32(stream, 1, 0, A[i], lda[i], rows[i], B[i], ldb[i], C[i], ldc[i],
+ * M[i], N[i], K[i], splits[i], c_split_stride[i], 0, NULL, 0, NULL, NULL, 0,
+ * bias_grad[i], 3), same bits, when every operand row is 16-byte vectorisable
+ * (lda, ldb, M[i], N[i] multiples of 4; 16-byte aligned A, B).  A gathered
+ * problem's split holds at most 2048 rows.  Part of the backward pass of
+ * jax.value_and_grad at boonta/algorithms/ppo.py:155-157 (the Dense kernel and
+ * bias cotangents). */
+int ppo_gemm_f32_dw_group(void* stream, int count, const float* const* A, const int64_t* lda,
+                          const int32_t* const* rows, const float* const* B, const int64_t* ldb, float* const* C,
+                          const int64_t* ldc, const int* M, const int* N, const int* K, const int* splits,
+                          const int64_t* c_split_stride, float* const* bias_grad);
 /* The weight gradients of up to 8 bf16 Dense layers in one launch (one
  * backward pass's dW GEMMs, so that a layer with few tiles runs beside one with
  * many instead of after it): problem i (host arrays, one entry per problem;

@@ -44,6 +44,8 @@ def test_argument_errors_are_reported_not_launched():
     assert rc == -1
     assert lib.ppo_adam_clip_f32(None, None, None, None, None, None, 6, None, 0, 0.5, 1e-3, 0.9, 0.999, 1e-8,
                                  None, 0, None) == -1
+    assert lib.ppo_gemm_f32_dw_group(None, 9, None, None, None, None, None, None, None, None, None, None, None, None,
+                                     None) == -1   # more problems than a launch takes
     assert lib.ppo_pad_rows_f32(None, None, 87, None, 90, 4, 87) == -1  # a pitch that is not a multiple of 4
     assert b"bad shape" in lib.ppo_last_error()
 

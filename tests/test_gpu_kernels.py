@@ -278,6 +278,48 @@ def test_weight_gradient_over_a_zero_padded_input_matches_the_unpadded_one():
     assert np.array_equal(out["padded"][F], np.zeros(N))
 
 
+def test_f32_dw_group_is_bit_identical_to_single_launches():
+    import ctypes
+    rng = np.random.default_rng(11)
+    # (rows of A, M, N, K, splits, gathered): the first layers of the paired
+    # towers over the padded observation copy, the later 256-wide layers, and
+    # a ragged problem (K not a multiple of the stage depth, M and N not of
+    # the tile)
+    shapes = [(4096, 88, 256, 2048, 8, True), (4096, 88, 256, 2048, 8, True), (2048, 256, 256, 2048, 4, False),
+              (2048, 256, 256, 2048, 4, False), (1000, 68, 132, 1000, 3, False)]
+    probs = []
+    for R, M, N, K, sp, gathered in shapes:
+        A = dev(rng.normal(size=(R, M)).astype(np.float32))
+        idx = dev(rng.permutation(R)[:K].astype(np.int32)) if gathered else None
+        B = dev(rng.normal(size=(K, N)).astype(np.float32))
+        probs.append((A, idx, B, M, N, K, sp))
+    single, group = [], []
+    for A, idx, B, M, N, K, sp in probs:
+        C = torch.full((sp, M, N), float("nan"), device=DEV)
+        bg = torch.full((sp, N), float("nan"), device=DEV)
+        _lib.call("ppo_gemm_f32", st(), 1, 0, A.data_ptr(), M, None if idx is None else idx.data_ptr(), B.data_ptr(),
+                  N, C.data_ptr(), N, M, N, K, sp, M * N, 0, None, 0, None, None, 0, bg.data_ptr(), 3)
+        single.append((host(C), host(bg)))
+        group.append((torch.full((sp, M, N), float("nan"), device=DEV), torch.full((sp, N), float("nan"), device=DEV)))
+    L = len(probs)
+    vp = lambda xs: (ctypes.c_void_p * L)(*xs)
+    i64 = lambda xs: (ctypes.c_int64 * L)(*xs)
+    i32 = lambda xs: (ctypes.c_int * L)(*xs)
+    args = [vp([p[0].data_ptr() for p in probs]), i64([p[3] for p in probs]),
+            vp([None if p[1] is None else p[1].data_ptr() for p in probs]), vp([p[2].data_ptr() for p in probs]),
+            i64([p[4] for p in probs]), vp([c.data_ptr() for c, _ in group]), i64([p[4] for p in probs]),
+            i32([p[3] for p in probs]), i32([p[4] for p in probs]), i32([p[5] for p in probs]),
+            i32([p[6] for p in probs]), i64([p[3] * p[4] for p in probs]), vp([b.data_ptr() for _, b in group])]
+    _lib.call("ppo_gemm_f32_dw_group", st(), L, *[ctypes.addressof(a) for a in args])
+    for k, ((c1, b1), (c2, b2)) in enumerate(zip(single, group)):
+        assert np.array_equal(c1, host(c2)), f"problem {k}: partials differ"
+        assert np.array_equal(b1, host(b2)), f"problem {k}: bias-gradient partials differ"
+    # against float64 for the gathered problem
+    A, idx, B, M, N, K, sp = probs[0]
+    want = host(A).astype(np.float64)[host(idx)].T @ host(B).astype(np.float64)
+    np.testing.assert_allclose(single[0][0].astype(np.float64).sum(0), want, rtol=2e-5, atol=2e-4)
+
+
 @pytest.mark.parametrize("splits", [1, 4, 64])
 def test_gemm_split_rows_with_bias_gradient(splits):
     gemm_case(1, 0, 400, 256, 4096, rows_src=8192, gather=True, splits=splits, bias_grad=True)

@@ -29,8 +29,9 @@ def small(config):
     return r
 
 
-def executor(r, prog, flat):
-    cls = RecurrentExecutor if prog.gru is not None else MLPExecutor
+def executor(r, prog, flat, cls=None):
+    if cls is None:
+        cls = RecurrentExecutor if prog.gru is not None else MLPExecutor
     return cls(prog, flat, r.cfg, r.optimizer, r.T, r.N)
 
 
@@ -170,26 +171,21 @@ class PerLayerExecutor(MLPExecutor):
     CHAIN = False
 
 
-def test_gaussian_update_runs_each_torso_chain_in_one_launch():
-    r = small(3)
-    prog = Program(r.network.plan(r.obs_dim))
-    flat = FlatState(prog, torch.device("cpu"))
-    ex = executor(r, prog, flat)
+class TowerDwExecutor(MLPExecutor):
+    """Paired towers with the weight gradients as two tower-batched launches."""
+    PAIR_DW_GROUP = False
+
+
+def check_tower_dw_launches(r, prog, flat, steps):
+    """The weight gradients as two ppo_gemm_f32_towers launches per step:
+    layer 0 of both towers, then layers 1-3 of both towers."""
+    ex = executor(r, prog, flat, cls=TowerDwExecutor)
     ex.bind(fake_inputs(ex))
-    assert ex.chain_ln
     names = [n for n, _ in ex.record()]
-    steps = r.cfg.update_epochs * r.cfg.num_minibatches
-    # per minibatch step: the forward chain of both towers (which also writes
-    # the kernels' transposed images), the fused heads + loss, the backward chain and the dW
-    # contractions (layer 0 of both towers, then layers 1-3 of both towers in
-    # one launch); the critic's bootstrap chain once
+    assert names.count("ppo_gemm_f32_towers") == 2 * steps and "ppo_gemm_f32_dw_group" not in names
     calls = ex.record(max_steps=1)
-    assert names.count("ppo_mlp_ln_fwd_f32") == steps + 1
-    assert names.count("ppo_mlp_ln_bwd_f32") == steps
-    assert names.count("ppo_gemm_f32_towers") == 2 * steps
     dw = [a for n, a in calls if n == "ppo_gemm_f32_towers"]
     assert [a[1] for a in dw] == [2, 6]
-    L = len(ex.actor)
     for a, first in zip(dw, (0, 1)):
         n, A_, B_, C_, bg = a[1], a[4], a[7], a[9], a[22]
         sa, sb, sc, sbg = a[24], a[25], a[26], a[30]
@@ -210,7 +206,45 @@ def test_gaussian_update_runs_each_torso_chain_in_one_launch():
             assert bg + 4 * k * sbg == lb.bpart.data_ptr()
             assert a[11] == fin and a[13] == ex.mb and a[14] == lb.splits
             assert a[15] == fin * lb.spec.ld    # the partials' split stride
+
+
+def test_gaussian_update_runs_each_torso_chain_in_one_launch():
+    r = small(3)
+    prog = Program(r.network.plan(r.obs_dim))
+    flat = FlatState(prog, torch.device("cpu"))
+    ex = executor(r, prog, flat)
+    ex.bind(fake_inputs(ex))
+    assert ex.chain_ln
+    names = [n for n, _ in ex.record()]
+    steps = r.cfg.update_epochs * r.cfg.num_minibatches
+    # per minibatch step: the forward chain of both towers (which also writes
+    # the kernels' transposed images), the fused heads + loss, the backward
+    # chain and every weight gradient of both towers in one launch; the
+    # critic's bootstrap chain once
+    calls = ex.record(max_steps=1)
+    assert names.count("ppo_mlp_ln_fwd_f32") == steps + 1
+    assert names.count("ppo_mlp_ln_bwd_f32") == steps
+    assert names.count("ppo_gemm_f32_dw_group") == steps and "ppo_gemm_f32_towers" not in names
     assert names.count("ppo_pad_rows_f32") == 1   # the padded observation copy, once per update
+    dwg = [a for n, a in calls if n == "ppo_gemm_f32_dw_group"]
+    assert len(dwg) == 1 and dwg[0][1] == 2 * len(ex.actor)
+    g = ex._dwg
+    idx = [a for n, a in calls if n == "ppo_mlp_ln_fwd_f32"][-1][5]   # the step's gather indices
+    for k in range(g["count"]):
+        i, t = k // 2, k % 2
+        lb = (ex.actor, ex.critic)[t][i]
+        if i > 0:
+            prev = (ex.actor, ex.critic)[t][i - 1]
+            assert g["A"][k] == prev.Y.data_ptr() and g["lda"][k] == prev.spec.ld and g["rows"][k] is None
+            assert g["M"][k] == lb.spec.dense.fin
+        else:
+            # the zero-padded observation copy (87 -> 88 columns), gathered
+            assert g["A"][k] == ex.OBSP.data_ptr() and g["lda"][k] == 88 and g["M"][k] == 88
+            assert g["rows"][k] == idx and lb.wpart.shape[1] == 88
+        assert g["B"][k] == lb.dZ.data_ptr() and g["C"][k] == lb.wpart.data_ptr()
+        assert g["bias_grad"][k] == lb.bpart.data_ptr() and g["splits"][k] == lb.splits
+        assert g["K"][k] == ex.mb and g["N"][k] == lb.spec.ld and g["stride"][k] == g["M"][k] * lb.spec.ld
+    check_tower_dw_launches(r, prog, flat, steps)
     assert names.count("ppo_gemm_f32") == 1   # the bootstrap value head
     for gone in ("ppo_gemm_ln_act_fwd_f32", "ppo_gemm_ln_act_fwd_f32_towers", "ppo_layernorm_act_fwd_f32",
                  "ppo_layernorm_act_bwd_f32", "ppo_layernorm_act_bwd_f32_towers", "ppo_stream_wait"):
