@@ -102,6 +102,10 @@ SIGNATURES = {
     "ppo_head_loss_max_features": (I, []),
     "ppo_head_loss_f32": (I, [P, I, I, P, P, I64, P, I64, P, I, P, I64, P, I64, P, I, I, P, P, P, P, P, P, P,
                               I, P, I64, P, I64, I, P, I64, P, I64, P, P, P, P, P, P, F, I, F, F, F]),
+    "ppo_mlp_ln_fwd_head_loss_f32": (I, [P, I, I, P, I64, P, I, I, P, I64, I64, P, P, P, P, P, I64, P, P, F, I, I64,
+                                         I64, I64, I64, P, I64,
+                                         I, I, P, P, I64, P, I64, P, I, P, I64, P, I64, P, I, I, P, P, P, P, P, P,
+                                         P, I, P, I64, P, I64, I, P, I64, P, I64, P, P, P, P, P, P, F, I, F, F, F]),
     "ppo_head_loss_ratio_f32": (I, [P, I, I, P, P, I64, P, I64, P, I, P, I64, P, I64, P, I, I, P, P, P, P, P, P, P,
                                     I, P, I64, P, I64, I, P, I64, P, I64, P, P, P, P, P, P, F, I, F, F, F, P, I,
                                     I]),

@@ -23,7 +23,9 @@
 // reads the layer's kernel transposed (an image the forward writes from the
 // parameters it is given, each workgroup a share of its rows), which gives
 // its B operand the forward's coalesced row reads.
-#include "common.h"
+#include "headloss.h"
+
+using namespace ppo_hl;
 
 namespace {
 
@@ -162,13 +164,168 @@ __device__ __forceinline__ void contract(floatx4 (&acc)[4], const float* xrow, b
   }
 }
 
+// The fused heads + PPO loss of a pair of separate towers, run by the
+// forward chain on its last layer's output: workgroup (x, tower) holds rows
+// 16 x .. 16 x + 15 of its tower's last Y in the LDS tile and computes, for
+// its tower alone, the head outputs (phase A), the loss terms and the head
+// outputs' cotangents (phase B), the head input's cotangent dY — the
+// backward chain's input — and the head weight partials (C1, C2).  Every
+// operand and operation is that of head_loss_fs_kernel<true, 4, ACT_NONE>
+// over the same rows (the head input read from LDS instead of HBM), so the
+// results are the same bits; the two towers write disjoint entries of each
+// 16-row block's partials.
+constexpr int HEAD_NB = MC_F / 64;  // 16-feature blocks per wave in the head phases
+
+// A lane's head parameters for the phases below: the B operands of phase A
+// and C1 (actor) or of phase A and the value weights of C1 (critic), read
+// from the tower's head kernel [256][ld] that the workgroup copied to LDS
+// (hk) at its start.
+struct HeadW {
+  float wA[HEAD_NB][4], bT[HEAD_NB][4], wcf[HEAD_NB];
+};
+
+// Copies the tower's head kernel ([256][ld] floats, 256-byte aligned: ld KB)
+// straight into LDS, 1 KB per wave copy; the copies complete in order with
+// the chain's own loads.
+__device__ __forceinline__ void copy_head_w(const HeadLossParams& hp, bool actor, float* hk) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const char* src = reinterpret_cast<const char*>(actor ? hp.wa : hp.wc);
+  const int ld = actor ? (int)hp.ldwa : (int)hp.ldwc;
+  for (int c = wave; c < ld; c += MC_THREADS / 64)
+    ppo::lds_copy16(src + 1024 * c + 16 * lane, reinterpret_cast<char*>(hk) + 1024 * c);
+}
+
+__device__ __forceinline__ void load_head_w(const HeadLossParams& hp, bool actor, const float* hk, HeadW& w) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 15;
+  const int kq = lane >> 4;
+  const int ja = min(li, (int)hp.ldwa - 1);
+#pragma unroll
+  for (int i = 0; i < HEAD_NB; ++i) {
+    const int fb = 16 * (wave + 4 * i);
+    const int f = fb + li;
+    w.wcf[i] = actor ? 0.f : hk[f * hp.ldwc];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (actor) {
+        w.wA[i][q] = li < hp.na ? hk[(fb + 4 * kq + q) * hp.ldwa + ja] : 0.f;
+        w.bT[i][q] = 4 * kq + q < hp.na ? hk[f * hp.ldwa + min(4 * kq + q, (int)hp.ldwa - 1)] : 0.f;
+      } else {
+        w.wA[i][q] = li == 0 ? hk[(fb + 4 * kq + q) * hp.ldwc] : 0.f;
+        w.bT[i][q] = 0.f;
+      }
+    }
+  }
+}
+
+template <int PART>
+__device__ __forceinline__ void chain_head(const HeadLossParams& hp, const float (*sX)[SX_PITCH],
+                                           const LaneIn (&lin)[1], const HeadW& w, float (*s_part)[MC_ROWS][LDO],
+                                           float (*s_dout)[LDO], double (*s_st)[NSTAT], float (*s_dsc)[16]) {
+  constexpr bool ACTOR = PART == PART_ACTOR;
+  constexpr int NB = HEAD_NB;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 15;
+  const int kq = lane >> 4;
+  const int r0 = blockIdx.x * MC_ROWS;
+  const int64_t blk = blockIdx.x;
+  const int last = hp.rows - 1;
+  const ColConst cc = load_cols(hp, true, threadIdx.x & 15);
+  const bool liveA = r0 + li < hp.rows;
+  int64_t rowq[4];
+  bool liveq[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    liveq[q] = r0 + 4 * kq + q < hp.rows;
+    rowq[q] = min(r0 + 4 * kq + q, last);
+  }
+  const floatx4 z4 = {0.f, 0.f, 0.f, 0.f};
+  floatx4 hA[NB];
+  float h2[NB][4];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int fb = 16 * (wave + 4 * i);
+    const int f = fb + li;
+    hA[i] = liveA ? *reinterpret_cast<const floatx4*>(&sX[li][fb + 4 * kq]) : z4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) h2[i][q] = liveq[q] ? sX[4 * kq + q][f] : 0.f;
+  }
+
+  // A. per-wave partial head outputs of the 16 rows
+  {
+    floatx4 acc = z4;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) acc = ppo_hl::mfma4(hA[i], w.wA[i], acc);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      if (ACTOR) s_part[wave][4 * kq + v][li] = acc[v];
+      else if (li == 0) s_part[wave][4 * kq + v][16] = acc[v];
+    }
+  }
+  __syncthreads();
+
+  // B. this tower's loss terms and head-output cotangents
+  phase_b<MC_ROWS, 4, true, 16, PART>(hp, blk, s_part, s_dout, s_st, s_dsc, lin, cc);
+
+  // C1. the head input's cotangent; C2. the head weight gradient partial
+  if (ACTOR) {
+    const floatx4 dv4 = *reinterpret_cast<const floatx4*>(&s_dout[li][4 * kq]);
+    const floatx4 a_in = liveA ? dv4 : z4;
+    float dq[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dq[q] = s_dout[4 * kq + q][li];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int fb = 16 * (wave + 4 * i);
+      const int f = fb + li;
+      const floatx4 g = ppo_hl::mfma4(a_in, w.bT[i], z4);
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (liveq[v]) hp.dha[rowq[v] * hp.lddha + f] = g[v];
+      const floatx4 gw = ppo_hl::mfma4(floatx4{h2[i][0], h2[i][1], h2[i][2], h2[i][3]}, dq, z4);
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (li < (int)hp.ldwa) hp.wpart_a[(blk * MC_F + fb + 4 * kq + v) * hp.ldwa + li] = gw[v];
+    }
+  } else {
+    float dvq[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dvq[q] = s_dout[4 * kq + q][16];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int fb = 16 * (wave + 4 * i);
+      const int f = fb + li;
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (liveq[v]) hp.dhc[rowq[v] * hp.lddhc + f] = dvq[v] * w.wcf[i];
+      float wv[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) wv[q] = li == 0 ? dvq[q] : 0.f;
+      const floatx4 gc = ppo_hl::mfma4(floatx4{h2[i][0], h2[i][1], h2[i][2], h2[i][3]}, wv, z4);
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (li < (int)hp.ldwc) hp.wpart_c[(blk * MC_F + fb + 4 * kq + v) * hp.ldwc + li] = li == 0 ? gc[v] : 0.f;
+    }
+  }
+}
+
 // ACT: the activation as a compile-time constant, so that the epilogue holds
 // only its code (a run-time switch per element interleaves every case's code,
 // tanhf's included, through the loop and the taken path thrashes the
 // instruction cache)
-template <bool VA, int ACT>
-__global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p) {
-  __shared__ float sX[MC_ROWS][SX_PITCH];
+// HEAD: the fused heads + loss of a pair of towers on the last layer's output
+// (chain_head; hp is unused otherwise).
+template <bool VA, int ACT, bool HEAD>
+__global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p, HeadLossParams hp) {
+  __shared__ __attribute__((aligned(16))) float sX[MC_ROWS][SX_PITCH];
+  __shared__ __attribute__((aligned(16))) float s_part[HEAD ? 4 : 1][MC_ROWS][LDO];
+  __shared__ __attribute__((aligned(16))) float s_dout[HEAD ? MC_ROWS : 1][LDO];
+  __shared__ double s_st[HEAD ? MC_ROWS : 1][NSTAT];
+  __shared__ float s_dsc[HEAD ? MC_ROWS : 1][16];
+  __shared__ __attribute__((aligned(1024))) float s_hk[HEAD ? MC_F * 16 : 1];  // the tower's head kernel
   __shared__ float s_sum[4][MC_ROWS];
   __shared__ float s_sq[4][MC_ROWS];
   const int64_t t = blockIdx.y;
@@ -182,6 +339,13 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p) {
   const float* X = p.X + t * p.tX;
   const float* xrow = X + (a_live ? (int64_t)(p.idx ? p.idx[ra] : ra) * p.ldx : 0);
   const int c4 = 64 * wave + 4 * li;
+  // the head loss's sample indices (thread: row threadIdx.x / 16, column
+  // threadIdx.x % 16); their gathers are issued with the last layer
+  LaneIn lin[1];
+  if constexpr (HEAD) {
+    lane_samples(hp, r0, threadIdx.x, lin);
+    copy_head_w(hp, t == 0, s_hk);
+  }
 
   // layer l's bias, scale and offset for this lane's features, and (l >= 1)
   // the first chunk of its kernel: issued during layer l - 1, ahead of its
@@ -250,6 +414,9 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p) {
 
   for (int l = 0; l < p.L; ++l) {
     const float* W = p.W[l] + t * p.tP;
+    if constexpr (HEAD) {
+      if (l == p.L - 1) lane_gathers(hp, threadIdx.x & 15, lin);
+    }
     floatx4 acc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -314,7 +481,7 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p) {
         zo[j] = z[v][j];
         yo[j] = ppo::act_fwd(ACT, ppo::ln_apply(z[v][j], mean, rstd, gl[j], bel[j]));
       }
-      if (l + 1 < p.L) *reinterpret_cast<floatx4*>(&sX[rr][c4]) = yo;
+      if (HEAD || l + 1 < p.L) *reinterpret_cast<floatx4*>(&sX[rr][c4]) = yo;
       if (row >= p.M) continue;
       if (wave == 0 && li == 0) {
         p.mean[l][t * p.tS + row] = mean;
@@ -325,6 +492,16 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p) {
     }
     // the next layer's contraction reads the tile (and s_sum is rewritten)
     __syncthreads();
+  }
+  if constexpr (HEAD) {
+    // the head kernel's copies, issued first, are long complete: wait for
+    // them explicitly (the compiler does not track them), then meet
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    HeadW hw;
+    load_head_w(hp, t == 0, s_hk, hw);
+    if (t == 0) chain_head<PART_ACTOR>(hp, sX, lin, hw, s_part, s_dout, s_st, s_dsc);
+    else chain_head<PART_CRITIC>(hp, sX, lin, hw, s_part, s_dout, s_st, s_dsc);
   }
   if (!wt_early) {
     for (int i = 0; i < wt_mine; ++i) {
@@ -493,29 +670,27 @@ PPO_EXPORT int ppo_mlp_chain_max_layers() { return MC_MAXL; }
 // Forward of L Dense(256) -> LayerNorm -> activation layers for `towers`
 // towers in one launch (see the top of this file); arrays hold tower 0's
 // per-layer pointers.
-PPO_EXPORT int ppo_mlp_ln_fwd_f32(void* stream, int towers, int L, const float* X, int64_t ldx,
-                                 const int32_t* rows_idx, int M, int K0, const float* const* W, int64_t ldw0,
-                                 int64_t ldw, const float* const* bias, const float* const* gamma,
-                                 const float* const* beta, float* const* Z, float* const* Y, int64_t ld,
-                                 float* const* mean, float* const* rstd, float eps, int act, int64_t stride_x,
-                                 int64_t stride_params, int64_t stride_rows, int64_t stride_stats,
-                                 float* const* WT, int64_t stride_wt) {
+// Checks the chain forward's arguments (messages under `name`) and fills a.
+static int chain_fwd_setup(FwdArgs& a, bool& va, const char* name, int towers, int L, const float* X, int64_t ldx,
+                           const int32_t* rows_idx, int M, int K0, const float* const* W, int64_t ldw0, int64_t ldw,
+                           const float* const* bias, const float* const* gamma, const float* const* beta,
+                           float* const* Z, float* const* Y, int64_t ld, float* const* mean, float* const* rstd,
+                           float eps, int act, int64_t stride_x, int64_t stride_params, int64_t stride_rows,
+                           int64_t stride_stats, float* const* WT, int64_t stride_wt) {
   if (towers < 1 || towers > 8 || L < 1 || L > MC_MAXL || M < 0 || K0 < 1 || act < 0 || act > 3 || ldx < K0 ||
       ldw0 < MC_F || ldw != MC_F || ld < MC_F || !W || !bias || !gamma || !beta || !Z || !Y || !mean || !rstd ||
       ldw0 % 4 || ldw % 4 || ld % 4 || (towers > 1 && (stride_x % 4 || stride_params % 4 || stride_rows % 4)))
-    return ppo::set_error(PPO_ERR_ARG, "ppo_mlp_ln_fwd_f32: bad argument (towers=%d L=%d M=%d K0=%d)", towers, L,
-                          M, K0);
-  if (M == 0) return PPO_OK;
-  FwdArgs a{};
+    return ppo::set_error(PPO_ERR_ARG, "%s: bad argument (towers=%d L=%d M=%d K0=%d)", name, towers, L, M, K0);
+  a = FwdArgs{};
   a.X = X; a.ldx = ldx; a.idx = rows_idx; a.M = M; a.K0 = K0; a.L = L; a.act = act; a.eps = eps;
   a.ldw0 = ldw0; a.ldw = ldw; a.ld = ld;
   a.tX = stride_x; a.tP = stride_params; a.tR = stride_rows; a.tS = stride_stats; a.tWT = stride_wt;
-  if (!X) return ppo::set_error(PPO_ERR_ARG, "ppo_mlp_ln_fwd_f32: null input");
+  if (!X) return ppo::set_error(PPO_ERR_ARG, "%s: null input", name);
   if (WT && L > 1) {
-    if (towers > 1 && stride_wt % 4) return ppo::set_error(PPO_ERR_ARG, "ppo_mlp_ln_fwd_f32: bad WT stride");
+    if (towers > 1 && stride_wt % 4) return ppo::set_error(PPO_ERR_ARG, "%s: bad WT stride", name);
     for (int l = 1; l < L; ++l) {
       if (!WT[l] || !aligned16(WT[l]))
-        return ppo::set_error(PPO_ERR_ARG, "ppo_mlp_ln_fwd_f32: layer %d needs a 16-byte aligned WT", l);
+        return ppo::set_error(PPO_ERR_ARG, "%s: layer %d needs a 16-byte aligned WT", name, l);
       a.WT[l] = WT[l];
     }
   }
@@ -523,24 +698,92 @@ PPO_EXPORT int ppo_mlp_ln_fwd_f32(void* stream, int towers, int L, const float* 
     if (!W[l] || !gamma[l] || !beta[l] || !Z[l] || !Y[l] || !mean[l] || !rstd[l] || !aligned16(W[l]) ||
         (bias[l] && !aligned16(bias[l])) || !aligned16(gamma[l]) || !aligned16(beta[l]) || !aligned16(Z[l]) ||
         !aligned16(Y[l]))
-      return ppo::set_error(PPO_ERR_ARG, "ppo_mlp_ln_fwd_f32: layer %d needs 16-byte aligned buffers", l);
+      return ppo::set_error(PPO_ERR_ARG, "%s: layer %d needs 16-byte aligned buffers", name, l);
     a.W[l] = W[l]; a.bias[l] = bias[l]; a.gamma[l] = gamma[l]; a.beta[l] = beta[l];
     a.Z[l] = Z[l]; a.Y[l] = Y[l]; a.mean[l] = mean[l]; a.rstd[l] = rstd[l];
   }
-  const bool va = aligned16(X) && ldx % 4 == 0 && K0 % 4 == 0 && (towers == 1 || stride_x % 4 == 0);
-  const dim3 grid(ppo::ceil_div(M, MC_ROWS), towers), block(MC_THREADS);
-  hipStream_t st = ppo::as_stream(stream);
-#define PPO_CHAIN_FWD(ACTV)                                                   \
-  if (va) hipLaunchKernelGGL((mlp_ln_fwd_kernel<true, ACTV>), grid, block, 0, st, a); \
-  else hipLaunchKernelGGL((mlp_ln_fwd_kernel<false, ACTV>), grid, block, 0, st, a);
-  switch (act) {
+  va = aligned16(X) && ldx % 4 == 0 && K0 % 4 == 0 && (towers == 1 || stride_x % 4 == 0);
+  return PPO_OK;
+}
+
+template <bool HEAD>
+static void chain_fwd_launch(hipStream_t st, const FwdArgs& a, const HeadLossParams& hp, bool va, int towers) {
+  const dim3 grid(ppo::ceil_div(a.M, MC_ROWS), towers), block(MC_THREADS);
+#define PPO_CHAIN_FWD(ACTV)                                                                          \
+  if (va) hipLaunchKernelGGL((mlp_ln_fwd_kernel<true, ACTV, HEAD>), grid, block, 0, st, a, hp);     \
+  else hipLaunchKernelGGL((mlp_ln_fwd_kernel<false, ACTV, HEAD>), grid, block, 0, st, a, hp);
+  switch (a.act) {
     case ACT_RELU: PPO_CHAIN_FWD(ACT_RELU) break;
     case ACT_TANH: PPO_CHAIN_FWD(ACT_TANH) break;
     case ACT_SILU: PPO_CHAIN_FWD(ACT_SILU) break;
     default: PPO_CHAIN_FWD(ACT_NONE) break;
   }
 #undef PPO_CHAIN_FWD
+}
+
+PPO_EXPORT int ppo_mlp_ln_fwd_f32(void* stream, int towers, int L, const float* X, int64_t ldx,
+                                 const int32_t* rows_idx, int M, int K0, const float* const* W, int64_t ldw0,
+                                 int64_t ldw, const float* const* bias, const float* const* gamma,
+                                 const float* const* beta, float* const* Z, float* const* Y, int64_t ld,
+                                 float* const* mean, float* const* rstd, float eps, int act, int64_t stride_x,
+                                 int64_t stride_params, int64_t stride_rows, int64_t stride_stats,
+                                 float* const* WT, int64_t stride_wt) {
+  FwdArgs a;
+  bool va = false;
+  const int rc = chain_fwd_setup(a, va, "ppo_mlp_ln_fwd_f32", towers, L, X, ldx, rows_idx, M, K0, W, ldw0, ldw, bias,
+                                 gamma, beta, Z, Y, ld, mean, rstd, eps, act, stride_x, stride_params, stride_rows,
+                                 stride_stats, WT, stride_wt);
+  if (rc != PPO_OK) return rc;
+  if (M == 0) return PPO_OK;
+  chain_fwd_launch<false>(ppo::as_stream(stream), a, HeadLossParams{}, va, towers);
   return ppo::check_launch("ppo_mlp_ln_fwd_f32");
+}
+
+extern "C" int ppo_head_loss_blocks(int rows);
+
+// The forward chain of an actor / critic pair (towers = 2) followed by their
+// fused heads + PPO loss in the same launch: the results of
+// ppo_mlp_ln_fwd_f32(<chain arguments>) then ppo_head_loss_f32(<head
+// arguments>), bit for bit, where the head inputs are the chain's last
+// outputs (ha = Y[L - 1], hc = ha + stride_rows, ldha = ldhc = ld), the
+// heads are separate (hc non-null) over F = 256 features with no activation
+// derivative (act_a = act_c = 0), rows = M, and M is small enough that the
+// head loss's partials are kept per 16-row block.
+PPO_EXPORT int ppo_mlp_ln_fwd_head_loss_f32(
+    void* stream, int towers, int L, const float* X, int64_t ldx, const int32_t* rows_idx, int M, int K0,
+    const float* const* W, int64_t ldw0, int64_t ldw, const float* const* bias, const float* const* gamma,
+    const float* const* beta, float* const* Z, float* const* Y, int64_t ld, float* const* mean, float* const* rstd,
+    float eps, int act, int64_t stride_x, int64_t stride_params, int64_t stride_rows, int64_t stride_stats,
+    float* const* WT, int64_t stride_wt, int dist, int rows, const int32_t* idx, const float* ha, int64_t ldha,
+    const float* wa, int64_t ldwa, const float* ba, int na, const float* hc, int64_t ldhc, const float* wc,
+    int64_t ldwc, const float* bc, int F, int A, const float* scale_param, const int32_t* action_i,
+    const float* action_f, const float* old_logp, const float* old_value, const float* adv, const float* ret,
+    int act_a, const float* aux_a, int64_t ldaux_a, float* dha, int64_t lddha, int act_c, const float* aux_c,
+    int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a, float* wpart_c, float* bpart_c,
+    float* dscale_partial, double* stats_partial, float clip_eps, int clip_value_loss, float ent_coef,
+    float vf_coef, float temperature) {
+  const char* name = "ppo_mlp_ln_fwd_head_loss_f32";
+  FwdArgs a;
+  bool va = false;
+  int rc = chain_fwd_setup(a, va, name, towers, L, X, ldx, rows_idx, M, K0, W, ldw0, ldw, bias, gamma, beta, Z, Y,
+                           ld, mean, rstd, eps, act, stride_x, stride_params, stride_rows, stride_stats, WT,
+                           stride_wt);
+  if (rc != PPO_OK) return rc;
+  HeadLossParams hp;
+  rc = head_loss_setup(hp, name, dist, rows, idx, ha, ldha, wa, ldwa, ba, na, hc, ldhc, wc, ldwc, bc, F, A,
+                       scale_param, action_i, action_f, old_logp, old_value, adv, ret, act_a, aux_a, ldaux_a, dha,
+                       lddha, act_c, aux_c, ldaux_c, dhc, lddhc, wpart_a, bpart_a, wpart_c, bpart_c, dscale_partial,
+                       stats_partial, clip_eps, clip_value_loss, ent_coef, vf_coef, temperature, nullptr, 1, 1);
+  if (rc != PPO_OK) return rc;
+  if (towers != 2 || !hc || F != MC_F || act_a != ACT_NONE || act_c != ACT_NONE || rows != M || ha != Y[L - 1] ||
+      hc != Y[L - 1] + stride_rows || ldha != ld || ldhc != ld || (reinterpret_cast<uintptr_t>(wa) & 255) ||
+      (reinterpret_cast<uintptr_t>(wc) & 255) ||
+      (M > 0 && ppo_head_loss_blocks(M) != ppo::ceil_div(M, MC_ROWS)))
+    return ppo::set_error(PPO_ERR_ARG, "%s: the heads must read the last layer of both towers (towers=%d F=%d "
+                          "rows=%d M=%d)", name, towers, F, rows, M);
+  if (M == 0) return PPO_OK;
+  chain_fwd_launch<true>(ppo::as_stream(stream), a, hp, va, towers);
+  return ppo::check_launch(name);
 }
 
 PPO_EXPORT int ppo_mlp_ln_bwd_blocks(int rows) { return rows > 0 ? ppo::ceil_div(rows, MC_ROWS) : 0; }

@@ -1205,17 +1205,21 @@ class MLPExecutor(ForwardChain):
                    self._chain_eps, self._chain_act, 0, 0, 0, 0, None, 0)
         return _p(boot[-1].Y), boot[-1].spec.ld
 
+    def _chain_fwd_args(self, x, ldx, rows_idx, nrows) -> tuple:
+        """Arguments of ppo_mlp_ln_fwd_f32 after the stream for both towers'
+        chains (which also write the kernels' transposed images for this
+        step's backward)."""
+        c, s0 = self._chain, self.actor[0].spec
+        return (2, len(self.actor), x, ldx, rows_idx, nrows, s0.dense.fin, c["W"], s0.dense.w.ld, 256, c["b"], c["g"],
+                c["be"], c["Z"], c["Y"], s0.ld, c["mean"], c["rstd"], self._chain_eps, self._chain_act, 0, self.pair,
+                self._chain_rs, self._chain_ss, c["WT"], 256 * 256)
+
     def _fwd_pair(self, st, x, ldx, rows_idx, nrows):
         """Forward of the actor (tower 0) and critic (tower 1) towers, one
         launch per depth; both first layers read the same input rows."""
         D, sx = self.pair, 0
         if self.chain_ln:
-            c, s0 = self._chain, self.actor[0].spec
-            # (it also writes the kernels' transposed images for this step's backward)
-            self._call("ppo_mlp_ln_fwd_f32", st, 2, len(self.actor), x, ldx, rows_idx, nrows, s0.dense.fin, c["W"],
-                       s0.dense.w.ld, 256, c["b"], c["g"], c["be"], c["Z"], c["Y"], s0.ld, c["mean"], c["rstd"],
-                       self._chain_eps, self._chain_act, 0, D, self._chain_rs, self._chain_ss, c["WT"],
-                       256 * 256)
+            self._call("ppo_mlp_ln_fwd_f32", st, *self._chain_fwd_args(x, ldx, rows_idx, nrows))
             return
         for la, lc in zip(self.actor, self.critic):
             s = la.spec
@@ -1451,7 +1455,46 @@ class MLPExecutor(ForwardChain):
         da, epa, acta, auxa, ldauxa = self._dx_target(la)
         return _p(la.Y), la.spec.ld, da, (acta if epa == EPI_DACT else 0), auxa, ldauxa
 
+    # the paired chains' forward and the fused heads + loss in one launch
+    # (off: the chain launch, then the head loss launch)
+    CHAIN_HEAD = True
+
+    @property
+    def _chain_head(self) -> bool:
+        v = self.__dict__.get("_chain_head_v")
+        if v is None:
+            v = self.__dict__["_chain_head_v"] = self._chain_head_fits()
+        return v
+
+    def _chain_head_fits(self) -> bool:
+        """True when the paired towers' chain forward can run the fused heads
+        + loss itself (ppo_mlp_ln_fwd_head_loss_f32): 256-wide chains feeding
+        separate heads with no activation derivative, a minibatch whose head
+        partials are kept per 16-row block, no per-row ratio output."""
+        if not (self.CHAIN_HEAD and self.chain_ln and self.pair and not self.prog.shared_head):
+            return False
+        if self._ratio_out() is not None or self.actor[-1].spec.ld != 256 or self.prog.head_a.fin != 256:
+            return False
+        # the launch copies each head kernel into LDS from its 256-byte aligned
+        # start (every leaf of the flat buffer is; a host-memory buffer, used
+        # only to record launches, is checked by its leaf offsets)
+        base = self.flat.P.data_ptr() if self.flat.P.is_cuda else 0
+        if any((base + 4 * h.w.offset) % 256 for h in (self.prog.head_a, self.prog.head_c)):
+            return False
+        _, _, _, acta, _, _ = self._head_a_io(self.actor[-1])
+        _, epc, _, _, _ = self._dx_target(self.critic[-1])
+        return acta == 0 and epc != EPI_DACT and _lib.load().ppo_head_loss_blocks(self.mb) == -(-self.mb // 16)
+
     def _fused_head_loss(self, st, idx, step, dist, A, scale_ptr, act_i, act_f):
+        args = self._head_loss_args(idx, step, dist, A, scale_ptr, act_i, act_f)
+        ratio = self._ratio_out()
+        if ratio is None:
+            self._call("ppo_head_loss_f32", st, *args)
+        else:
+            self._call("ppo_head_loss_ratio_f32", st, *args, *ratio)
+
+    def _head_loss_args(self, idx, step, dist, A, scale_ptr, act_i, act_f) -> tuple:
+        """Arguments of ppo_head_loss_f32 after the stream."""
         prog, cfg, inp, mb = self.prog, self.cfg, self.inp, self.mb
         if prog.shared_head:
             la, lc = (self.trunk[-1] if self.trunk else None), None
@@ -1473,16 +1516,11 @@ class MLPExecutor(ForwardChain):
         else:
             c_args = (None, 0, None, 0, None)
             cd_args = (0, None, 0, None, 0)
-        args = (dist, mb, idx, ya, ldya, self.flat.view(h.w), h.w.ld, self.flat.view(h.b), na, *c_args, h.fin, A,
+        return (dist, mb, idx, ya, ldya, self.flat.view(h.w), h.w.ld, self.flat.view(h.b), na, *c_args, h.fin, A,
                 scale_ptr, act_i, act_f, inp["log_prob"], inp["value"], self._loss_adv(), _p(self.RET), acta, auxa,
                 ldauxa, da, ldya, *cd_args, _p(wpa), _p(bpa), _p(wpc), _p(bpc), _p(self.DSCALE), self._stats(step),
                 float(cfg.clip_coefficient), int(cfg.clip_value_loss), float(cfg.entropy_coefficient),
                 float(cfg.value_coefficient), 1.0)
-        ratio = self._ratio_out()
-        if ratio is None:
-            self._call("ppo_head_loss_f32", st, *args)
-        else:
-            self._call("ppo_head_loss_ratio_f32", st, *args, *ratio)
 
     def _minibatch(self, st, idx, step, obs, ldo, dist, A):
         prog, cfg, inp, mb = self.prog, self.cfg, self.inp, self.mb
@@ -1496,8 +1534,12 @@ class MLPExecutor(ForwardChain):
                 self._fused_head_loss(st, idx, step, dist, A, scale_ptr, act_i, act_f)
                 self._bwd_layers(st, self.trunk, obs, ldo, idx)
             elif self.pair:
-                self._fwd_pair(st, obs, ldo, idx, mb)
-                self._fused_head_loss(st, idx, step, dist, A, scale_ptr, act_i, act_f)
+                if self._chain_head:
+                    self._call("ppo_mlp_ln_fwd_head_loss_f32", st, *self._chain_fwd_args(obs, ldo, idx, mb),
+                               *self._head_loss_args(idx, step, dist, A, scale_ptr, act_i, act_f))
+                else:
+                    self._fwd_pair(st, obs, ldo, idx, mb)
+                    self._fused_head_loss(st, idx, step, dist, A, scale_ptr, act_i, act_f)
                 self._bwd_pair(st, obs, ldo, idx)
             else:
                 s2 = self._fork(st)

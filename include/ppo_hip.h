@@ -539,6 +539,31 @@ int ppo_head_loss_f32(void* stream, int dist, int rows, const int32_t* idx, cons
                       int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a,
                       float* wpart_c, float* bpart_c, float* dscale_partial, double* stats_partial,
                       float clip_eps, int clip_value_loss, float ent_coef, float vf_coef, float temperature);
+/* The forward chain of an actor / critic pair of towers followed, in the same
+ * launch, by their fused heads + PPO loss on the chains' last outputs: what
+ * ppo_mlp_ln_fwd_f32(stream, <its arguments>) then ppo_head_loss_f32(stream,
+ * <the remaining arguments>) compute, bit for bit (each tower's workgroups
+ * run that tower's half of the loss on the tile they hold in LDS).  Requires
+ * towers = 2, separate heads (hc non-NULL) over F = 256 features with no
+ * activation derivative (act_a = act_c = 0), ha = Y[L - 1], hc = ha +
+ * stride_rows, ldha = ldhc = ld, rows = M, and M within the head loss's
+ * 16-row-block range (ppo_head_loss_blocks(M) = ceil(M / 16)).  Replaces the
+ * torso forward of boonta/networks/network.py:38-49 and loss_fn of
+ * boonta/algorithms/ppo.py:77-146 with its head backward, for flax's
+ * ActorCritic with separate LayerNorm torsos. */
+int ppo_mlp_ln_fwd_head_loss_f32(
+    void* stream, int towers, int L, const float* X, int64_t ldx, const int32_t* rows_idx, int M, int K0,
+    const float* const* W, int64_t ldw0, int64_t ldw, const float* const* bias, const float* const* gamma,
+    const float* const* beta, float* const* Z, float* const* Y, int64_t ld, float* const* mean, float* const* rstd,
+    float eps, int act, int64_t stride_x, int64_t stride_params, int64_t stride_rows, int64_t stride_stats,
+    float* const* WT, int64_t stride_wt, int dist, int rows, const int32_t* idx, const float* ha, int64_t ldha,
+    const float* wa, int64_t ldwa, const float* ba, int na, const float* hc, int64_t ldhc, const float* wc,
+    int64_t ldwc, const float* bc, int F, int A, const float* scale_param, const int32_t* action_i,
+    const float* action_f, const float* old_logp, const float* old_value, const float* adv, const float* ret,
+    int act_a, const float* aux_a, int64_t ldaux_a, float* dha, int64_t lddha, int act_c, const float* aux_c,
+    int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a, float* wpart_c, float* bpart_c,
+    float* dscale_partial, double* stats_partial, float clip_eps, int clip_value_loss, float ent_coef,
+    float vf_coef, float temperature);
 /* ppo_head_loss_f32 that also keeps each row's ratio exp(logp - old_logp),
  * env-major: ratio_out[(s % envs) * steps + s / envs] for the row's sample
  * s = idx[row] = t * envs + env (the new ratio RecurrentPuPO scatters back

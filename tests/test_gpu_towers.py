@@ -370,3 +370,36 @@ def test_chain_update_matches_the_per_layer_update(use_graph):
     (pa, la), (pb, lb) = results
     assert float((pa - pb).norm() / pb.norm()) < 1e-5
     np.testing.assert_allclose(la.numpy(), lb.numpy(), rtol=1e-4, atol=1e-6)
+
+
+class _SeparateHead(MLPExecutor):
+    """The paired chains with the heads + loss as a launch of their own."""
+    CHAIN_HEAD = False
+
+
+class _SeparateHeadPPO(PPO):
+    executor_class = _SeparateHead
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_chain_with_fused_heads_is_bit_identical_to_separate_launches(use_graph):
+    """The forward chain that runs both towers' heads + loss on its last
+    layer's output (ppo_mlp_ln_fwd_head_loss_f32) against the chain launch
+    followed by ppo_head_loss_f32: the same operations on the same values, so
+    the parameters and every logged value after two updates are the same
+    bits.  Ragged last tile: 500-row minibatches."""
+    r, plan, params, tr, roll = make_case(config=3, T=8, N=250, M=4, E=2)
+    results = []
+    for cls in (PPO, _SeparateHeadPPO):
+        alg = cls(cfg=r.cfg, network=r.network, optimizer=r.optimizer, use_graph=use_graph)
+        state = alg.init_from_params({"params": params}, r.obs_dim)
+        ex = alg.executor(state, r.T, r.N, r.obs_dim)
+        assert ex.chain_ln and ex._chain_head == (cls is PPO) and ex.mb % 16 != 0
+        trans = device_transition(tr, roll)
+        for k in (1, 2):
+            alg.update(state, make_key(k), trans)
+        torch.cuda.synchronize()
+        results.append((flat_state_of(state).P.cpu().numpy().copy(), ex.LOGS.cpu().numpy().copy(),
+                        ex.STATS.cpu().numpy().copy()))
+    for a, b in zip(*results):
+        np.testing.assert_array_equal(a, b)

@@ -64,8 +64,11 @@ def test_recorded_launches_match_the_c_signatures(config):
         assert names.count("ppo_loss_f32") == steps and "ppo_gemm_f32" not in names
         assert all(n != "ppo_layernorm_act_fwd_f32" for n in names)
     else:
-        # every fp32 workload has torso features in front of its heads: the fused kernel runs
-        assert names.count("ppo_head_loss_f32") == steps and "ppo_loss_f32" not in names
+        # every fp32 workload has torso features in front of its heads: the fused kernel runs (for
+        # the Gaussian towers' chains, inside the forward chain's launch)
+        fused = names.count("ppo_head_loss_f32") + names.count("ppo_mlp_ln_fwd_head_loss_f32")
+        assert fused == steps and "ppo_loss_f32" not in names
+        assert (names.count("ppo_mlp_ln_fwd_head_loss_f32") == steps) == (config == 3)
     assert names[-1] == "ppo_count_advance"
     for name, args in calls:
         _, argtypes = _lib.SIGNATURES[name]
@@ -218,18 +221,25 @@ def test_gaussian_update_runs_each_torso_chain_in_one_launch():
     names = [n for n, _ in ex.record()]
     steps = r.cfg.update_epochs * r.cfg.num_minibatches
     # per minibatch step: the forward chain of both towers (which also writes
-    # the kernels' transposed images), the fused heads + loss, the backward
-    # chain and every weight gradient of both towers in one launch; the
-    # critic's bootstrap chain once
+    # the kernels' transposed images) with the fused heads + loss in the same
+    # launch, the backward chain and every weight gradient of both towers in
+    # one launch; the critic's bootstrap chain once
     calls = ex.record(max_steps=1)
-    assert names.count("ppo_mlp_ln_fwd_f32") == steps + 1
+    assert names.count("ppo_mlp_ln_fwd_head_loss_f32") == steps and "ppo_head_loss_f32" not in names
+    assert names.count("ppo_mlp_ln_fwd_f32") == 1
     assert names.count("ppo_mlp_ln_bwd_f32") == steps
     assert names.count("ppo_gemm_f32_dw_group") == steps and "ppo_gemm_f32_towers" not in names
     assert names.count("ppo_pad_rows_f32") == 1   # the padded observation copy, once per update
     dwg = [a for n, a in calls if n == "ppo_gemm_f32_dw_group"]
     assert len(dwg) == 1 and dwg[0][1] == 2 * len(ex.actor)
     g = ex._dwg
-    idx = [a for n, a in calls if n == "ppo_mlp_ln_fwd_f32"][-1][5]   # the step's gather indices
+    fwd = [a for n, a in calls if n == "ppo_mlp_ln_fwd_head_loss_f32"][0]
+    idx = fwd[5]   # the step's gather indices
+    # the heads read the last layer of both towers; their input cotangents are the backward chain's dY
+    c0 = 27   # first head-loss argument
+    la, lc = ex.actor[-1], ex.critic[-1]
+    assert fwd[c0 + 2] == idx and fwd[c0 + 3] == la.Y.data_ptr() and fwd[c0 + 9] == lc.Y.data_ptr()
+    assert fwd[c0 + 26] == la.dY.data_ptr() and fwd[c0 + 31] == lc.dY.data_ptr()
     for k in range(g["count"]):
         i, t = k // 2, k % 2
         lb = (ex.actor, ex.critic)[t][i]
@@ -268,7 +278,7 @@ def test_gaussian_update_runs_each_torso_chain_in_one_launch():
     # the forward writes each tower's kernel of layers 1.. transposed into WT[layer - 1, tower]
     for l in range(1, len(ex.actor)):
         assert T["WT"][l] == ex.WT[l - 1, 0].data_ptr()
-    fwd = [a for n_, a in calls if n_ == "ppo_mlp_ln_fwd_f32"]
+    fwd = [a[:27] for n_, a in calls if n_ in ("ppo_mlp_ln_fwd_f32", "ppo_mlp_ln_fwd_head_loss_f32")]
     assert [a[-2] for a in fwd] == [None, ex._chain["WT"]]   # the bootstrap chain writes none
     assert fwd[1][-1] == ex.WT[0, 1].data_ptr() - ex.WT[0, 0].data_ptr() >> 2
     # the bootstrap chain runs the critic's own layers
