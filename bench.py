@@ -120,6 +120,12 @@ def dw_group_problems(args):
     return list(zip(*ints))
 
 
+def gru_seq_shape(name, args):
+    """(sequences, units, steps) of a GRU sequence launch."""
+    i = 23 if name == "ppo_gru_fwd_seq_f32" else 22   # after the stream: Bm, H, T
+    return args[i], args[i + 1], args[i + 2]
+
+
 def _single_launch_work(name, args):
     if name in DW_GROUPS:
         probs = dw_group_problems(args)
@@ -207,9 +213,16 @@ def _single_launch_work(name, args):
     if name == "ppo_gru_fwd_seq_f32":
         Bm, H, T = args[-6], args[-5], args[-4]
         return 2.0 * Bm * H * 3 * H * T, 4.0 * T * Bm * (3 * H + H + H + 4 * H) + 4.0 * H * 3 * H
-    if name == "ppo_gru_bwd_seq_f32":
-        Bm, H, T = args[-6], args[-5], args[-4]
-        return 2.0 * Bm * 3 * H * H * max(T - 1, 0), 4.0 * T * Bm * (H + 4 * H + H + H + 4 * H) + 4.0 * H * 3 * H
+    if name in ("ppo_gru_bwd_seq_f32", "ppo_gru_bwd_seq_dw_f32"):
+        Bm, H, T = gru_seq_shape(name, args)
+        flops = 2.0 * Bm * 3 * H * H * max(T - 1, 0)
+        nbytes = 4.0 * T * Bm * (H + 4 * H + H + H + 4 * H) + 4.0 * H * 3 * H
+        if name == "ppo_gru_bwd_seq_dw_f32":
+            # the weight gradients: hp and e rows read, one partial per block of 16 sequences written
+            I, parts = args[31], (Bm + 15) // 16
+            flops += 2.0 * T * Bm * (H + I) * 3 * H
+            nbytes += 4.0 * T * Bm * I + 4.0 * parts * (H + I + 2) * 3 * H
+        return flops, nbytes
     if name in ("ppo_gru_fwd_step_f32",):
         Bm, H = args[-2], args[-1]
         return 2.0 * Bm * H * 3 * H, 4.0 * Bm * (3 * H + 2 * H + 6 * H) + 4.0 * H * 3 * H
@@ -256,8 +269,8 @@ def _single_launch_shape(name, args):
         return [args[6], 256, args[7], args[2], args[1]]
     if name == "ppo_mlp_ln_bwd_f32":
         return [args[5], 256, 256, args[2], args[1]]
-    if name in ("ppo_gru_fwd_seq_f32", "ppo_gru_bwd_seq_f32"):
-        return [args[-6], args[-5], args[-4]]
+    if name in ("ppo_gru_fwd_seq_f32", "ppo_gru_bwd_seq_f32", "ppo_gru_bwd_seq_dw_f32"):
+        return list(gru_seq_shape(name, args))
     if name == "ppo_mlp16_ln_fwd":
         return [args[6], 512, 512, args[1]]
     if name == "ppo_mlp16_ln_bwd":
@@ -289,8 +302,8 @@ def launch_key(name, args):
         return (name,) + tuple(dw_group_problems(args))
     if name in ("ppo_gru_fwd_step_f32", "ppo_gru_bwd_step_f32"):
         return (name, args[-2], args[-1], bool(args[1]))
-    if name in ("ppo_gru_fwd_seq_f32", "ppo_gru_bwd_seq_f32"):
-        return (name, args[-6], args[-5], args[-4])
+    if name in ("ppo_gru_fwd_seq_f32", "ppo_gru_bwd_seq_f32", "ppo_gru_bwd_seq_dw_f32"):
+        return (name,) + gru_seq_shape(name, args)
     if name == "ppo_mlp16_ln_fwd":
         return (name, args[1], args[5], args[6])
     if name == "ppo_mlp16_ln_bwd":

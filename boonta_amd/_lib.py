@@ -118,6 +118,9 @@ SIGNATURES = {
                                 I64, I64, I, I, I, P, P, I]),
     "ppo_gru_bwd_seq_f32": (I, [P, P, I64, P, P, P, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P,
                                 I64, I64, I, I, I, P, P, I]),
+    "ppo_gru_seq_dw_parts": (I, [I]),
+    "ppo_gru_bwd_seq_dw_f32": (I, [P, P, I64, P, P, P, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P,
+                                   I64, I64, I, I, I, P, P, I, P, I64, I64, I, P, P, P, P]),
     "ppo_sequence_rows": (I, [P, P, I, I, I, I, P]),
     "ppo_grad_reduce_segment_bytes": (I, []),
     "ppo_grad_reduce_chunk_bytes": (I, []),

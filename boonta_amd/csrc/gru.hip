@@ -362,43 +362,74 @@ __device__ __forceinline__ unsigned tag_of(u64 p) { return (unsigned)(p >> 32); 
 
 // Waits until the wave's quarter of a ring slot's columns, kw .. kw + KW - 1
 // of rows b0 .. b0 + 15 ([Bm][K] pairs), carries `tag`, and stages it in the
-// wave's own LDS tile sA[16][KW + 4] (rows from Bm on, never written, are
-// zeros).  Each load of the wave reads 64 consecutive pairs of the tile's
-// rows.  Only this wave writes and reads sA, and a wave's LDS accesses
-// complete in order, so no barrier follows.  Returns false, alike in every
-// lane, when spin_limit polls went by without all of them there.
-template <int K, int KW>
+// wave's own LDS tile sA[16][KW + 4] (rows from Bm on are staged as zeros).
+// Each load of the wave reads 64 consecutive pairs of the tile's rows.  Only
+// this wave writes and reads sA, and a wave's LDS accesses complete in
+// order, so no barrier follows.  Returns false, alike in every lane, when
+// spin_limit polls went by without all of them there.
+// EAGER: the first round loads every pair unconditionally (rows from Bm on
+// read row b0's) before the first check, which the forward's 16 loads per
+// lane run faster (212 -> 193 us per 64-step launch at 256 x 256); the
+// backward's 48 loads per lane run faster issued inside the polling loop,
+// each only while its pair is missing (310 against 414 us).
+template <int K, int KW, bool EAGER>
 __device__ __forceinline__ bool stage_wave(const u64* slot, int Bm, int b0, int kw, unsigned tag, float* sA,
                                            int spin_limit) {
   constexpr int NL = TILE * KW / 64;
   static_assert(TILE * KW % 64 == 0, "rows of KW pairs over a wave");
   const int lane = threadIdx.x & 63;
+  auto at = [&](int q) {
+    const int e = lane + 64 * q, r = e / KW;
+    return slot + (int64_t)(b0 + r < Bm ? b0 + r : b0) * K + kw + (e - r * KW);
+  };
+  auto in_rows = [&](int q) { return b0 + (lane + 64 * q) / KW < Bm; };
   u64 v[NL];
-#pragma unroll
-  for (int q = 0; q < NL; ++q) v[q] = b0 + (lane + 64 * q) / KW < Bm ? 0ull : (u64)tag << 32;
   bool ok = false;
-  for (int it = 0; it < spin_limit; ++it) {
-    bool mine = true;
+  if constexpr (EAGER) {
 #pragma unroll
-    for (int q = 0; q < NL; ++q) {
-      if (tag_of(v[q]) != tag) {
-        const int e = lane + 64 * q, r = e / KW;
-        v[q] = __hip_atomic_load(slot + (int64_t)(b0 + r) * K + kw + (e - r * KW), __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
+    for (int q = 0; q < NL; ++q) v[q] = __hip_atomic_load(at(q), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int polls = 1;; ++polls) {
+      bool mine = true;
+#pragma unroll
+      for (int q = 0; q < NL; ++q) mine = mine && (!in_rows(q) || tag_of(v[q]) == tag);
+      if (spin_limit > 0 && __builtin_amdgcn_ballot_w64(!mine) == 0) {
+        ok = true;
+        break;
       }
-    }
+      if (polls >= spin_limit) break;
+      __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-    for (int q = 0; q < NL; ++q) mine = mine && tag_of(v[q]) == tag;
-    if (__builtin_amdgcn_ballot_w64(!mine) == 0) {
-      ok = true;
-      break;
+      for (int q = 0; q < NL; ++q)
+        if (in_rows(q) && tag_of(v[q]) != tag)
+          v[q] = __hip_atomic_load(at(q), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    __builtin_amdgcn_s_sleep(1);
+  } else {
+#pragma unroll
+    for (int q = 0; q < NL; ++q) v[q] = in_rows(q) ? 0ull : (u64)tag << 32;
+    for (int it = 0; it < spin_limit; ++it) {
+      bool mine = true;
+#pragma unroll
+      for (int q = 0; q < NL; ++q) {
+        if (tag_of(v[q]) != tag) {
+          const int e = lane + 64 * q, r = e / KW;
+          v[q] = __hip_atomic_load(slot + (int64_t)(b0 + r) * K + kw + (e - r * KW), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < NL; ++q) mine = mine && tag_of(v[q]) == tag;
+      if (__builtin_amdgcn_ballot_w64(!mine) == 0) {
+        ok = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
   }
 #pragma unroll
   for (int q = 0; q < NL; ++q) {
     const int e = lane + 64 * q, r = e / KW;
-    sA[r * (KW + 4) + (e - r * KW)] = __uint_as_float((uint32_t)v[q]);
+    // (not EAGER: a row from Bm on holds the tag and zero value bits)
+    sA[r * (KW + 4) + (e - r * KW)] = !EAGER || in_rows(q) ? __uint_as_float((uint32_t)v[q]) : 0.f;
   }
   __builtin_amdgcn_wave_barrier();
   return ok;
@@ -523,8 +554,8 @@ __global__ void __launch_bounds__(256) gru_fwd_seq_kernel(FwdSeqArgs a) {
         mfma_chunk(c, av);
       }
     } else {
-      ok = stage_wave<H, H / WAVES>(a.sync.ring + ((t - 1) & 1) * slot_size, a.Bm, b0, wave * (H / WAVES),
-                                    (unsigned)t, sAw, a.sync.spin_limit);
+      ok = stage_wave<H, H / WAVES, true>(a.sync.ring + ((t - 1) & 1) * slot_size, a.Bm, b0, wave * (H / WAVES),
+                                          (unsigned)t, sAw, a.sync.spin_limit);
       load_next();  // (issued after the wait, so that they do not hold it up)
 #pragma unroll
       for (int c = 0; c < NIT; ++c) {
@@ -586,15 +617,38 @@ struct BwdSeqArgs {
   float* dgate; int64_t lddg, dg_step;
   int Bm, H, T;
   SeqSync sync;
+  // DW kernels: the weight gradients of both GRU kernels, one partial per
+  // sequence block x (rows 16 x .. 16 x + 15, every step):
+  //   whpart[x][k][c] = sum hp[k] dgate[H + c]   (k < H, c < 3H: [dar|daz|dhn])
+  //   wipart[x][k][c] = sum e[k] dgate[c]        (k < H, c < 3H: [dan|dar|daz])
+  //   whbpart[x][c], wibpart[x][c]: the column sums of dgate[H + c], dgate[c]
+  // where e is the GRU input of row t Bm + b at e + t e_step + b lde.
+  const float* e; int64_t lde, e_step;
+  float* whpart; float* whbpart; float* wipart; float* wibpart;
 };
 
-template <int NIT>
-__global__ void __launch_bounds__(256) gru_bwd_seq_kernel(BwdSeqArgs a) {
+// Weight gradients inside the backward (DW): the workgroup has four more
+// waves (two per SIMD), which multiply while the recurrence's waves wait for
+// their exchange loads.  The recurrence's epilogue of step s leaves the
+// step's dgate tile (16 rows x the workgroup's 16 units x 4 gates) in an LDS
+// pair of buffers; after the waves' meeting of step s - 1 (its partial
+// tiles), the weight-gradient waves add the tile's products into their 64 of
+// the K rows of both partials: k = 64 w + 16 (lane / 16) + 4 v + mt for
+// accumulator [mt][gate] element v (the MFMA's M index read as k = 64 w +
+// 4 m + mt, so that a lane's A operand is one 16-byte load of 4 consecutive
+// k), the block's rows as the MFMA's K (row 4 (lane / 16) + j at k-step j).
+// Every wave passes every barrier (the flag chunks' too), so a buffer is
+// read between the meetings of steps s - 1 and s - 2 and written again only
+// after the latter.
+template <int NIT, bool DW>
+__global__ void __launch_bounds__(DW ? 512 : 256) gru_bwd_seq_kernel(BwdSeqArgs a) {
   constexpr int H3 = 64 * NIT;
   constexpr int H = H3 / 3;
+  static_assert(!DW || H == 256, "the fused weight gradients take H = 256 (and a 256-wide input)");
   __shared__ float red[2][WAVES][TILE][TILE + 1];
   __shared__ float sA[WAVES][TILE * (H3 / WAVES + 4)];  // each wave's staged quarter of dgate_{s+1}[:, H:4H]
   __shared__ uint8_t done[FLAG_CHUNK][TILE];
+  __shared__ float sdg[DW ? 2 : 1][4][TILE][TILE + 4];   // [step % 2][dan|dar|daz|dhn][unit][row]
   __shared__ int gave_up;  // the step at which a wait gave up, -1 while none has
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -603,6 +657,70 @@ __global__ void __launch_bounds__(256) gru_bwd_seq_kernel(BwdSeqArgs a) {
   const int u0 = blockIdx.y * TILE;
   const int i = lane & 15;
   const int kq = lane >> 4;
+  if constexpr (DW) {
+    if (wave >= WAVES) {
+      const int g4 = 4 * kq;                        // this lane's rows g4 + j of the block
+      const int kd = 64 * (wave - WAVES) + 4 * i;   // its 4 consecutive k
+      floatx4 acc_h[4][3], acc_i[4][3];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 3; ++nt) acc_h[mt][nt] = acc_i[mt][nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      floatx4 ha[4], ea[4];  // step sd's hp and e rows, loaded a step ahead
+      auto dw_load = [&](int sd) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int row = b0 + g4 + j < a.Bm ? b0 + g4 + j : b0;  // (a row from Bm on has a zero dgate)
+          ha[j] = *reinterpret_cast<const floatx4*>(a.hp + sd * a.hp_step + (int64_t)row * a.ldhp + kd);
+          ea[j] = *reinterpret_cast<const floatx4*>(a.e + sd * a.e_step + (int64_t)row * a.lde + kd);
+        }
+      };
+      auto dw_step = [&](int sd) {
+        floatx4 bg[4];
+#pragma unroll
+        for (int gate = 0; gate < 4; ++gate)
+          bg[gate] = *reinterpret_cast<const floatx4*>(&sdg[sd & 1][gate][i][g4]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < 3; ++nt) {
+              acc_h[mt][nt] =
+                  __builtin_amdgcn_mfma_f32_16x16x4f32(ha[j][mt], bg[nt + 1][j], acc_h[mt][nt], 0, 0, 0);
+              acc_i[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(ea[j][mt], bg[nt][j], acc_i[mt][nt], 0, 0, 0);
+            }
+      };
+      dw_load(a.T - 1);
+      for (int s = a.T - 1; s >= 0; --s) {
+        const int t = s + 1;
+        const int j = (a.T - 1 - s) % FLAG_CHUNK;
+        if (j == 0) load_flag_chunk(done, a.term, a.trunc, a.flag_rows, a.flag_step, a.Bm, a.T, b0, t, -1);
+        if (t < a.T) {
+          __syncthreads();  // the meeting of step s: step s + 1's tile is in sdg
+          if (gave_up == s) return;
+          dw_step(s + 1);
+          dw_load(s);
+        }
+      }
+      __syncthreads();  // step 0's tile
+      dw_step(0);
+      __syncthreads();  // (the recurrence waves' column sums)
+      const int64_t xk = (int64_t)blockIdx.x * H;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 3; ++nt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int k = 64 * (wave - WAVES) + 16 * kq + 4 * v + mt;
+            const int64_t c = nt * H + u0 + i;
+            a.whpart[(xk + k) * 3 * H + c] = acc_h[mt][nt][v];
+            a.wipart[(xk + k) * 3 * H + c] = acc_i[mt][nt][v];
+          }
+      return;
+    }
+  }
   // this lane's columns: k0 + 16 c + q, c < NIT, q < 4 (the wave's quarter of 3H)
   const int k0 = wave * (H3 / WAVES) + 4 * kq;
   float* sAw = sA[wave];
@@ -636,6 +754,8 @@ __global__ void __launch_bounds__(256) gru_bwd_seq_kernel(BwdSeqArgs a) {
   float dh_t = 0.f, z_t = 0.f;
   if (tid == 0) gave_up = -1;  // (published by the first flag chunk's barriers)
 
+  float bsum[4] = {0.f, 0.f, 0.f, 0.f};  // DW: this thread's column sums of dan, dar, daz, dhn
+
   for (int s = a.T - 1; s >= 0; --s) {
     const int t = s + 1;
     float dh = dout;
@@ -647,8 +767,9 @@ __global__ void __launch_bounds__(256) gru_bwd_seq_kernel(BwdSeqArgs a) {
       const float direct = __fmul_rn(dh_t, z_t);
       const bool reset_t = done[j][ti] != 0;
       // dhp[b][u] = sum_c dgate_t[b][H + c] Wh[u][c], c < 3H
-      const bool ok = stage_wave<H3, H3 / WAVES>(a.sync.ring + (t & 1) * slot_size, a.Bm, b0, wave * (H3 / WAVES),
-                                                 (unsigned)(a.T - t), sAw, a.sync.spin_limit);
+      const bool ok = stage_wave<H3, H3 / WAVES, false>(a.sync.ring + (t & 1) * slot_size, a.Bm, b0,
+                                                        wave * (H3 / WAVES), (unsigned)(a.T - t), sAw,
+                                                        a.sync.spin_limit);
       // (issued after the wait, so that they do not hold it up)
       if (s > 0) own(s - 1, dout_n, n_n, r_n, z_n, hn_n, hp_n);
       floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -677,8 +798,8 @@ __global__ void __launch_bounds__(256) gru_bwd_seq_kernel(BwdSeqArgs a) {
     } else if (s > 0) {
       own(s - 1, dout_n, n_n, r_n, z_n, hn_n, hp_n);
     }
+    float dan = 0.f, dar = 0.f, daz = 0.f, dhn = 0.f;
     if (bb_ok) {
-      float dan, dar, daz, dhn;
       gru_cell_bwd(dh, n, r, z, hn, hp, dan, dar, daz, dhn);
       a.dh[s * a.dh_step + (int64_t)bb * a.lddh + u] = dh;
       if (s > 0) {
@@ -694,6 +815,17 @@ __global__ void __launch_bounds__(256) gru_bwd_seq_kernel(BwdSeqArgs a) {
       o[2 * H + u] = daz;
       o[3 * H + u] = dhn;
     }
+    if constexpr (DW) {
+      // (zeros for rows from Bm on)
+      sdg[s & 1][0][tj][ti] = dan;
+      sdg[s & 1][1][tj][ti] = dar;
+      sdg[s & 1][2][tj][ti] = daz;
+      sdg[s & 1][3][tj][ti] = dhn;
+      bsum[0] += dan;
+      bsum[1] += dar;
+      bsum[2] += daz;
+      bsum[3] += dhn;
+    }
     dh_t = dh;
     z_t = z;
     dout = dout_n;
@@ -702,6 +834,23 @@ __global__ void __launch_bounds__(256) gru_bwd_seq_kernel(BwdSeqArgs a) {
     z = z_n;
     hn = hn_n;
     hp = hp_n;
+  }
+  if constexpr (DW) {
+    __syncthreads();  // step 0's tile is in sdg for the weight-gradient waves
+    // the column sums of the block's rows, added in row order
+    float* bs = &red[0][0][0][0];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) bs[(ti * 4 + g) * TILE + tj] = bsum[g];
+    __syncthreads();
+    const int64_t x3 = (int64_t)blockIdx.x * 3 * H;
+    if (tid < 4 * TILE) {
+      const int g = tid / TILE, j = tid % TILE;
+      float sum = 0.f;
+      for (int row = 0; row < TILE; ++row) sum += bs[(row * 4 + g) * TILE + j];
+      const int c = u0 + j;
+      if (g < 3) a.wibpart[x3 + g * H + c] = sum;          // [dan|dar|daz]
+      if (g > 0) a.whbpart[x3 + (g - 1) * H + c] = sum;    // [dar|daz|dhn]
+    }
   }
 }
 
@@ -802,11 +951,11 @@ PPO_EXPORT int64_t ppo_gru_seq_exchange_bytes(int Bm, int H) {
   return Bm > 0 && H > 0 ? 2 * (int64_t)Bm * 3 * H * (int64_t)sizeof(u64) : 0;
 }
 
-// Launches a persistent kernel (one workgroup of 256 threads per 16 x 16
-// tile, all resident at once).
+// Launches a persistent kernel (one workgroup of 256 threads, 512 with the
+// weight-gradient waves, per 16 x 16 tile, all resident at once).
 template <typename Kernel, typename Args>
-static void launch_seq(Kernel k, dim3 grid, hipStream_t st, const Args& a) {
-  hipLaunchKernelGGL(k, grid, dim3(256), 0, st, a);
+static void launch_seq(Kernel k, dim3 grid, hipStream_t st, const Args& a, int threads = 256) {
+  hipLaunchKernelGGL(k, grid, dim3(threads), 0, st, a);
 }
 
 static void zero_ring(hipStream_t st, void* ring, int64_t n) {
@@ -888,15 +1037,60 @@ PPO_EXPORT int ppo_gru_bwd_seq_f32(void* stream, const float* wh, int64_t ldwh, 
     return ppo::set_error(PPO_ERR_ARG, "ppo_gru_bwd_seq_f32: dgate rows must be 16-byte aligned");
   BwdSeqArgs a{wh, ldwh, terminated, truncated, flag_rows, flag_step, dout, lddo, dout_step, gates, ldg, g_step,
                hp, ldhp, hp_step, dh, lddh, dh_step, dgate, lddg, dg_step, Bm, H, T,
-               SeqSync{static_cast<u64*>(exchange), error, spin_limit}};
+               SeqSync{static_cast<u64*>(exchange), error, spin_limit}, nullptr, 0, 0, nullptr, nullptr, nullptr,
+               nullptr};
   hipStream_t st = ppo::as_stream(stream);
   if (T > 1) zero_ring(st, exchange, 2 * (int64_t)Bm * 3 * H);
   const dim3 grid(ppo::ceil_div(Bm, TILE), H / TILE);
   switch (3 * H / 64) {
-    case 3: launch_seq(gru_bwd_seq_kernel<3>, grid, st, a); break;
-    case 6: launch_seq(gru_bwd_seq_kernel<6>, grid, st, a); break;
-    case 9: launch_seq(gru_bwd_seq_kernel<9>, grid, st, a); break;
-    default: launch_seq(gru_bwd_seq_kernel<12>, grid, st, a); break;
+    case 3: launch_seq(gru_bwd_seq_kernel<3, false>, grid, st, a); break;
+    case 6: launch_seq(gru_bwd_seq_kernel<6, false>, grid, st, a); break;
+    case 9: launch_seq(gru_bwd_seq_kernel<9, false>, grid, st, a); break;
+    default: launch_seq(gru_bwd_seq_kernel<12, false>, grid, st, a); break;
   }
   return ppo::check_launch("ppo_gru_bwd_seq_f32");
+}
+
+// Parts of the fused weight gradients of ppo_gru_bwd_seq_dw_f32: one per
+// block of 16 sequences.
+PPO_EXPORT int ppo_gru_seq_dw_parts(int Bm) { return Bm > 0 ? ppo::ceil_div(Bm, TILE) : 0; }
+
+// ppo_gru_bwd_seq_f32 that also leaves the weight gradients of both GRU
+// kernels and their biases as P = ppo_gru_seq_dw_parts(Bm) partials, each
+// over the rows of one block of 16 sequences and every step:
+//   whpart [P][H][3H]: hp^T dgate[:, H:4H]     whbpart [P][3H]: its column sums
+//   wipart [P][I][3H]: e^T dgate[:, 0:3H]      wibpart [P][3H]: its column sums
+// with e the GRU input of row t Bm + b at e + t e_step + b lde (the flax
+// GRUCell's input and recurrent Dense kernels, boonta/networks/blocks/rnn.py:
+// 34-54, differentiated by jax.value_and_grad at
+// boonta/algorithms/recurrent_ppo.py:213-215).  H = I = 256; hp and e rows
+// 16-byte aligned.
+PPO_EXPORT int ppo_gru_bwd_seq_dw_f32(void* stream, const float* wh, int64_t ldwh, const uint8_t* terminated,
+                                      const uint8_t* truncated, const int32_t* flag_rows, int64_t flag_step,
+                                      const float* dout, int64_t lddo, int64_t dout_step, const float* gates,
+                                      int64_t ldg, int64_t g_step, const float* hp, int64_t ldhp, int64_t hp_step,
+                                      float* dh, int64_t lddh, int64_t dh_step, float* dgate, int64_t lddg,
+                                      int64_t dg_step, int Bm, int H, int T, void* exchange, int* error,
+                                      int spin_limit, const float* e, int64_t lde, int64_t e_step, int I,
+                                      float* whpart, float* whbpart, float* wipart, float* wibpart) {
+  const int rc = seq_check("ppo_gru_bwd_seq_dw_f32", Bm, H, T, exchange, error);
+  if (rc != PPO_OK) return rc;
+  if (H != 256 || I != 256)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gru_bwd_seq_dw_f32: needs H = I = 256 (H=%d I=%d)", H, I);
+  if (Bm == 0 || T == 0) return PPO_OK;
+  if (!wh || !dout || !gates || !hp || !dh || !dgate || !e || !whpart || !whbpart || !wipart || !wibpart)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gru_bwd_seq_dw_f32: null buffer");
+  if (ldwh < 3 * H || lddo < H || ldg < 4 * H || ldhp < H || lddh < H || lddg < 4 * H || lde < I)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gru_bwd_seq_dw_f32: leading dimension too small");
+  if (!aligned16(dgate) || lddg % 4 || dg_step % 4 || !aligned16(hp) || ldhp % 4 || hp_step % 4 ||
+      !aligned16(e) || lde % 4 || e_step % 4)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gru_bwd_seq_dw_f32: dgate, hp and e rows must be 16-byte aligned");
+  BwdSeqArgs a{wh, ldwh, terminated, truncated, flag_rows, flag_step, dout, lddo, dout_step, gates, ldg, g_step,
+               hp, ldhp, hp_step, dh, lddh, dh_step, dgate, lddg, dg_step, Bm, H, T,
+               SeqSync{static_cast<u64*>(exchange), error, spin_limit}, e, lde, e_step, whpart, whbpart, wipart,
+               wibpart};
+  hipStream_t st = ppo::as_stream(stream);
+  if (T > 1) zero_ring(st, exchange, 2 * (int64_t)Bm * 3 * H);
+  launch_seq(gru_bwd_seq_kernel<12, true>, dim3(ppo::ceil_div(Bm, TILE), H / TILE), st, a, 512);
+  return ppo::check_launch("ppo_gru_bwd_seq_dw_f32");
 }

@@ -66,8 +66,18 @@ class RecurrentExecutor(MLPExecutor):
         self.DHOUT = torch.zeros(rows, H, **f32)
         self.DHS = torch.zeros(rows, H, **f32)
         self.DGATE = torch.zeros(rows, 4 * H, **f32)
-        self.wh_splits = _splits(rows, H, 3 * H)
-        self.wi_splits = _splits(rows, I, 3 * H)
+        # the recurrence of a minibatch in one launch per direction when all
+        # its workgroups fit the device at once (else one launch per step);
+        # the backward launch then also multiplies the GRU's weight
+        # gradients, one partial per block of 16 sequences, where it takes
+        # the shape (else two GEMMs after it)
+        self.seq = self.SEQ and self._seq_fits(self.Bm, H)
+        self.seq_dw = self.seq and self.SEQ_DW and H == 256 and I == 256
+        if self.seq_dw:
+            self.wh_splits = self.wi_splits = _lib.load().ppo_gru_seq_dw_parts(self.Bm)
+        else:
+            self.wh_splits = _splits(rows, H, 3 * H)
+            self.wi_splits = _splits(rows, I, 3 * H)
         self.WHPART = torch.zeros(self.wh_splits, H, 3 * H, **f32)
         self.WHBPART = torch.zeros(self.wh_splits, 3 * H, **f32)
         self.WIPART = torch.zeros(self.wi_splits, I, 3 * H, **f32)
@@ -75,9 +85,6 @@ class RecurrentExecutor(MLPExecutor):
         n2 = 2 * self.N
         self.XIB = torch.zeros(n2, 3 * H, **f32)
         self.HB = torch.zeros(n2, H, **f32)
-        # the recurrence of a minibatch in one launch per direction when all
-        # its workgroups fit the device at once (else one launch per step)
-        self.seq = self.SEQ and self._seq_fits(self.Bm, H)
         if self.seq:
             lib = _lib.load()
             self.SEQX = torch.zeros(max(1, lib.ppo_gru_seq_exchange_bytes(self.Bm, H) // 8), dtype=torch.int64,
@@ -85,6 +92,7 @@ class RecurrentExecutor(MLPExecutor):
             self.SEQERR = torch.zeros(1, dtype=torch.int32, device=dev)
 
     SEQ = True               # sequence launches where they fit
+    SEQ_DW = True            # the weight gradients inside the backward sequence launch where it takes them
     SEQ_SPIN = 1 << 18       # polls of a step wait before it gives up (about a second)
 
     @staticmethod
@@ -240,7 +248,12 @@ class RecurrentExecutor(MLPExecutor):
         # backward through time
         wh = self.flat.view(g.wh)
         G4 = 4 * H
-        if self.seq:
+        if self.seq_dw:
+            self._call("ppo_gru_bwd_seq_dw_f32", st, wh, 3 * H, fterm, ftrunc, rows, Bm, _p(self.DHOUT), H, blk,
+                       _p(self.GATES), G4, Bm * G4, _p(self.HP), H, blk, _p(self.DHS), H, blk, _p(self.DGATE), G4,
+                       Bm * G4, Bm, H, T, _p(self.SEQX), _p(self.SEQERR), self.SEQ_SPIN, e_ptr, lde, Bm * lde, I,
+                       _p(self.WHPART), _p(self.WHBPART), _p(self.WIPART), _p(self.WIBPART))
+        elif self.seq:
             self._call("ppo_gru_bwd_seq_f32", st, wh, 3 * H, fterm, ftrunc, rows, Bm, _p(self.DHOUT), H, blk,
                        _p(self.GATES), G4, Bm * G4, _p(self.HP), H, blk, _p(self.DHS), H, blk, _p(self.DGATE), G4,
                        Bm * G4, Bm, H, T, _p(self.SEQX), _p(self.SEQERR), self.SEQ_SPIN)
@@ -258,11 +271,13 @@ class RecurrentExecutor(MLPExecutor):
                        _p(self.HP) + 4 * s * blk, H, _p(self.DHS) + 4 * s * blk, H,
                        _p(self.DGATE) + 4 * s * Bm * G4, G4, Bm, H)
         # recurrent and input kernels: dWh = HP^T [dar|daz|dhn], dWi = E^T [dan|dar|daz]
-        self._gemm(st, A_COL, B_KN, _p(self.HP), H, None, _p(self.DGATE) + 4 * H, G4,
-                   _p(self.WHPART), 3 * H, H, 3 * H, mb, self.wh_splits, H * 3 * H, EPI_STORE, None, 0, None, None, 0,
-                   _p(self.WHBPART), -1)
-        self._gemm(st, A_COL, B_KN, e_ptr, lde, None, _p(self.DGATE), G4, _p(self.WIPART), 3 * H,
-                   I, 3 * H, mb, self.wi_splits, I * 3 * H, EPI_STORE, None, 0, None, None, 0, _p(self.WIBPART), -1)
+        if not self.seq_dw:
+            self._gemm(st, A_COL, B_KN, _p(self.HP), H, None, _p(self.DGATE) + 4 * H, G4,
+                       _p(self.WHPART), 3 * H, H, 3 * H, mb, self.wh_splits, H * 3 * H, EPI_STORE, None, 0, None, None,
+                       0, _p(self.WHBPART), -1)
+            self._gemm(st, A_COL, B_KN, e_ptr, lde, None, _p(self.DGATE), G4, _p(self.WIPART), 3 * H,
+                       I, 3 * H, mb, self.wi_splits, I * 3 * H, EPI_STORE, None, 0, None, None, 0, _p(self.WIBPART),
+                       -1)
         # cotangent of the trunk output: [dan|dar|daz] Wi^T, times the trunk's activation derivative
         dst, epi, act, aux, ldaux = self._dx_target(self.trunk[-1])
         self._gemm(st, A_ROW, B_NK, _p(self.DGATE), G4, None, self.flat.view(g.wi), 3 * H, dst,

@@ -633,6 +633,25 @@ int ppo_gru_bwd_seq_f32(void* stream, const float* wh, int64_t ldwh, const uint8
                         const float* hp, int64_t ldhp, int64_t hp_step, float* dh, int64_t lddh, int64_t dh_step,
                         float* dgate, int64_t lddg, int64_t dg_step, int Bm, int H, int T, void* exchange,
                         int* error, int spin_limit);
+/* ppo_gru_bwd_seq_f32 that also leaves the weight gradients of the GRU's
+ * input and recurrent Dense kernels and their biases (the flax GRUCell of
+ * boonta/networks/blocks/rnn.py:34-54 under jax.value_and_grad,
+ * recurrent_ppo.py:213-215), multiplied while the launch waits for its
+ * exchange loads, as P = ppo_gru_seq_dw_parts(Bm) partials (one per block of
+ * 16 sequences, over its rows and every step; the gradient reduce sums them):
+ *   whpart [P][H][3H] = hp^T dgate[:, H:4H]     whbpart [P][3H]: column sums of dgate[:, H:4H]
+ *   wipart [P][I][3H] = e^T dgate[:, 0:3H]      wibpart [P][3H]: column sums of dgate[:, 0:3H]
+ * where e is the GRU input of row t Bm + b at e + t e_step + b lde.  dh and
+ * dgate are those of ppo_gru_bwd_seq_f32, bit for bit.  H = I = 256; hp and
+ * e rows 16-byte aligned. */
+int ppo_gru_seq_dw_parts(int Bm);
+int ppo_gru_bwd_seq_dw_f32(void* stream, const float* wh, int64_t ldwh, const uint8_t* terminated,
+                           const uint8_t* truncated, const int32_t* flag_rows, int64_t flag_step, const float* dout,
+                           int64_t lddo, int64_t dout_step, const float* gates, int64_t ldg, int64_t g_step,
+                           const float* hp, int64_t ldhp, int64_t hp_step, float* dh, int64_t lddh, int64_t dh_step,
+                           float* dgate, int64_t lddg, int64_t dg_step, int Bm, int H, int T, void* exchange,
+                           int* error, int spin_limit, const float* e, int64_t lde, int64_t e_step, int I,
+                           float* whpart, float* whbpart, float* wipart, float* wibpart);
 /* Sample rows of S env-major sequence minibatches (recurrent_ppo.py:217-223):
  * out[s * T * Bm + t * Bm + b] = t * N + envs[s * Bm + b]. */
 int ppo_sequence_rows(void* stream, const int32_t* envs, int S, int T, int N, int Bm, int32_t* out);

@@ -32,6 +32,7 @@ def test_host_only_entry_points_answer_without_a_device():
     assert lib.ppo_grad_reduce_segment_bytes() == 40
     assert lib.ppo_grad_reduce_chunk_bytes() == 16
     assert lib.ppo_permutation_workspace(1 << 20) > 3 * 4 * (1 << 20)
+    assert lib.ppo_gru_seq_dw_parts(256) == 16 and lib.ppo_gru_seq_dw_parts(17) == 2
 
 
 def test_argument_errors_are_reported_not_launched():
@@ -48,6 +49,9 @@ def test_argument_errors_are_reported_not_launched():
                                      None) == -1   # more problems than a launch takes
     assert lib.ppo_pad_rows_f32(None, None, 87, None, 90, 4, 87) == -1  # a pitch that is not a multiple of 4
     assert b"bad shape" in lib.ppo_last_error()
+    assert lib.ppo_gru_bwd_seq_dw_f32(None, None, 768, None, None, None, 0, None, 256, 0, None, 1024, 0, None, 256,
+                                      0, None, 256, 0, None, 1024, 0, 16, 256, 4, None, None, 1, None, 256, 0, 256,
+                                      None, None, None, None) == -1   # no exchange ring
 
 
 def test_sampling_rejects_unsupported_sizes_without_launching():

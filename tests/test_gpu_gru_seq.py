@@ -1,5 +1,5 @@
 """The GRU recurrence of a sequence minibatch in one launch per direction
-(ppo_gru_fwd_seq_f32 / ppo_gru_bwd_seq_f32; the loop of
+(ppo_gru_fwd_seq_f32 / ppo_gru_bwd_seq_f32 / ppo_gru_bwd_seq_dw_f32; the loop of
 boonta/networks/blocks/rnn.py:34-54 and its backward through time) against
 the per-step launches it replaces, whose parity with the oracle is
 test_gpu_rnn.py's: bit-identical h, carries, gates, dh and gate cotangents,
@@ -67,7 +67,9 @@ def run_steps(c, o):
                   Q("HP") + 4 * s * blk, H, Q("DHS") + 4 * s * blk, H, Q("DG") + 4 * s * B * g4, g4, B, H)
 
 
-def run_seq(c, o, sync, err, spin=SPIN, backward=True):
+def run_seq(c, o, sync, err, spin=SPIN, backward=True, dw=None):
+    """Both sequence launches; dw: the backward with the weight gradients,
+    its GRU input rows dw["E"] and partials dw["WHP"], ["WHB"], ["WIP"], ["WIB"]."""
     B, H, T = c["B"], c["H"], c["T"]
     blk, g4 = B * H, 4 * H
     P = lambda k: c[k].data_ptr()
@@ -75,10 +77,16 @@ def run_seq(c, o, sync, err, spin=SPIN, backward=True):
     _lib.call("ppo_gru_fwd_seq_f32", st(), P("XI"), 3 * H, B * 3 * H, P("POOL"), H, P("ENVS"), P("TERM"), P("TRUNC"),
               P("ROWS"), B, P("WH"), 3 * H, P("BHN"), Q("HOUT"), H, blk, Q("HP"), H, blk, Q("GATES"), g4, B * g4,
               B, H, T, sync.data_ptr(), err.data_ptr(), spin)
-    if backward:
+    if backward and dw is None:
         _lib.call("ppo_gru_bwd_seq_f32", st(), P("WH"), 3 * H, P("TERM"), P("TRUNC"), P("ROWS"), B, P("DOUT"), H, blk,
                   Q("GATES"), g4, B * g4, Q("HP"), H, blk, Q("DHS"), H, blk, Q("DG"), g4, B * g4, B, H, T,
                   sync.data_ptr(), err.data_ptr(), spin)
+    elif backward:
+        I = dw["E"].shape[1]
+        _lib.call("ppo_gru_bwd_seq_dw_f32", st(), P("WH"), 3 * H, P("TERM"), P("TRUNC"), P("ROWS"), B, P("DOUT"), H,
+                  blk, Q("GATES"), g4, B * g4, Q("HP"), H, blk, Q("DHS"), H, blk, Q("DG"), g4, B * g4, B, H, T,
+                  sync.data_ptr(), err.data_ptr(), spin, dw["E"].data_ptr(), I, B * I, I, dw["WHP"].data_ptr(),
+                  dw["WHB"].data_ptr(), dw["WIP"].data_ptr(), dw["WIB"].data_ptr())
 
 
 def sync_bufs(B, H):
@@ -101,6 +109,41 @@ def test_sequence_launches_equal_the_step_launches(B, H, T):
         assert int(err.item()) == 0
         for k in ("HOUT", "HP", "GATES", "DHS", "DG"):
             assert torch.equal(got[k], ref[k]), (rep, k)
+
+
+@pytest.mark.parametrize("B,T", [(256, 64), (37, 9), (16, 3), (1, 2), (256, 1)])
+def test_backward_with_weight_gradients(B, T):
+    """ppo_gru_bwd_seq_dw_f32: dh and the gate cotangents bit-identical to the
+    step launches, and its partials summed over the sequence blocks equal to
+    the weight and bias gradients of both GRU kernels, dWh = sum_t hp_t^T
+    dgate_t[:, H:4H] and dWi = sum_t e_t^T dgate_t[:, 0:3H] (float64 products
+    of the same dgate and hp; 16384 rows at the largest case), to rel-L2
+    1e-5.  Ragged last block (37 rows), one step, one sequence."""
+    H = I = 256
+    c = case(B, H, T, seed=B * 7 + T)
+    ref, got = out_bufs(B, H, T), out_bufs(B, H, T)
+    run_steps(c, ref)
+    rng = np.random.default_rng(B + T)
+    parts = _lib.load().ppo_gru_seq_dw_parts(B)
+    assert parts == (B + 15) // 16
+    dw = dict(E=dev(rng.standard_normal((T * B, I)).astype(np.float32)),
+              WHP=torch.full((parts, H, 3 * H), 7.0, device=DEV), WHB=torch.full((parts, 3 * H), 7.0, device=DEV),
+              WIP=torch.full((parts, I, 3 * H), 7.0, device=DEV), WIB=torch.full((parts, 3 * H), 7.0, device=DEV))
+    sync, err = sync_bufs(B, H)
+    print(f"bwd seq dw B={B} T={T}", flush=True)
+    run_seq(c, got, sync, err, dw=dw)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    for k in ("HOUT", "HP", "GATES", "DHS", "DG"):
+        assert torch.equal(got[k], ref[k]), k
+    hp = ref["HP"].double().cpu().numpy()
+    dg = ref["DG"].double().cpu().numpy()
+    e = dw["E"].double().cpu().numpy()
+    want = {"WHP": hp.T @ dg[:, H:], "WIP": e.T @ dg[:, :3 * H], "WHB": dg[:, H:].sum(0), "WIB": dg[:, :3 * H].sum(0)}
+    for k, w in want.items():
+        g = dw[k].double().sum(0).cpu().numpy()
+        rel = np.linalg.norm(g - w) / np.linalg.norm(w)
+        assert rel < 1e-5, (k, rel)
 
 
 def test_a_wait_that_gives_up_sets_the_error_word_and_the_launch_ends():
@@ -136,8 +179,12 @@ def test_grids_larger_than_the_resident_workgroups_are_rejected():
 @pytest.mark.parametrize("use_graph", [False, True])
 def test_recurrent_update_with_sequence_launches_equals_the_step_launches(use_graph):
     """RecurrentPPO.update with each direction of the recurrence in one launch
-    against the same update issued step by step: parameters and logs bit for
-    bit after two updates, and no wait gave up."""
+    (the weight gradients as GEMMs after it) against the same update issued
+    step by step: parameters and logs bit for bit after two updates, and no
+    wait gave up.  The default update, whose backward launch also multiplies
+    the GRU's weight gradients (summed in another order), against the first:
+    the parameter change of the two updates within rel-L2 1e-3 of its norm,
+    the logs within 1e-3 (a clip fraction may move by a sample)."""
     from boonta_amd.algorithms.ppo import flat_state_of
     from boonta_amd.algorithms.recurrent_ppo import RecurrentPPO
     from boonta_amd.learner_rnn import RecurrentExecutor
@@ -150,21 +197,33 @@ def test_recurrent_update_with_sequence_launches_equals_the_step_launches(use_gr
     class StepPPO(RecurrentPPO):
         executor_class = StepExecutor
 
+    class GemmDwExecutor(RecurrentExecutor):
+        SEQ_DW = False
+
+    class GemmDwPPO(RecurrentPPO):
+        executor_class = GemmDwExecutor
+
     r, plan, params, tr, roll, extra = make_recurrent_case(4, T=16, N=256, M=4, E=2, seed=3)
-    results = []
-    for cls in (RecurrentPPO, StepPPO):
+    results = {}
+    for cls in (GemmDwPPO, StepPPO, RecurrentPPO):
         alg = cls(cfg=r.cfg, network=r.network, optimizer=r.optimizer, use_graph=use_graph)
         state = alg.init_from_params({"params": params}, r.obs_dim)
         ex = alg.executor(state, r.T, r.N, r.obs_dim)
-        assert ex.seq == (cls is RecurrentPPO)
+        assert ex.seq == (cls is not StepPPO) and ex.seq_dw == (cls is RecurrentPPO)
+        p0 = flat_state_of(state).P.cpu().clone()
         trans = device_recurrent_transition(tr, roll, extra)
         for k in (1, 2):
             alg.update(state, make_key(k), trans)
         torch.cuda.synchronize()
         assert not ex.recurrence_error()
-        results.append((flat_state_of(state).P.cpu().clone(), ex.LOGS.cpu().clone()))
-    assert torch.equal(results[0][0], results[1][0])
-    assert torch.equal(results[0][1], results[1][1])
+        results[cls] = (flat_state_of(state).P.cpu().clone(), ex.LOGS.cpu().clone())
+    assert torch.equal(results[GemmDwPPO][0], results[StepPPO][0])
+    assert torch.equal(results[GemmDwPPO][1], results[StepPPO][1])
+    d_gemm = (results[GemmDwPPO][0] - p0).double()
+    d_fused = (results[RecurrentPPO][0] - p0).double()
+    rel = float((d_fused - d_gemm).norm() / d_gemm.norm())
+    assert rel < 1e-3, rel
+    np.testing.assert_allclose(results[RecurrentPPO][1].numpy(), results[GemmDwPPO][1].numpy(), rtol=1e-3, atol=1e-3)
 
 
 @pytest.mark.parametrize("use_graph", [False, True])

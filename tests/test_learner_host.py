@@ -367,25 +367,43 @@ class SeqRecurrentExecutor(RecurrentExecutor):
         return True
 
 
-def test_recurrent_update_runs_each_direction_of_the_recurrence_in_one_launch():
+class SeqRecurrentGemmDwExecutor(SeqRecurrentExecutor):
+    """... with the GRU's weight gradients as two GEMMs after the backward."""
+    SEQ_DW = False
+
+
+@pytest.mark.parametrize("fused_dw", [True, False])
+def test_recurrent_update_runs_each_direction_of_the_recurrence_in_one_launch(fused_dw):
     r = small(4)
     prog = Program(r.network.plan(r.obs_dim))
     flat = FlatState(prog, torch.device("cpu"))
-    ex = SeqRecurrentExecutor(prog, flat, r.cfg, r.optimizer, r.T, r.N)
+    cls = SeqRecurrentExecutor if fused_dw else SeqRecurrentGemmDwExecutor
+    ex = cls(prog, flat, r.cfg, r.optimizer, r.T, r.N)
     ex.bind(fake_inputs(ex))
-    assert ex.seq
+    H, I, Bm, T = prog.gru.H, prog.gru.fin, ex.Bm, r.T
+    assert ex.seq and ex.seq_dw == (fused_dw and H == 256 and I == 256)
     calls = ex.record()
     names = [n for n, _ in calls]
     steps = r.cfg.update_epochs * r.cfg.num_minibatches
-    assert names.count("ppo_gru_fwd_seq_f32") == steps and names.count("ppo_gru_bwd_seq_f32") == steps
+    bwd = "ppo_gru_bwd_seq_dw_f32" if ex.seq_dw else "ppo_gru_bwd_seq_f32"
+    assert names.count("ppo_gru_fwd_seq_f32") == steps and names.count(bwd) == steps
     assert names.count("ppo_gru_fwd_step_f32") == 2          # the bootstrap's two-step tail
     assert "ppo_gru_bwd_step_f32" not in names
-    H, Bm, T = prog.gru.H, ex.Bm, r.T
+    # every GEMM whose output is a GRU kernel's gradient partial
+    dw_out = {ex.WHPART.data_ptr(), ex.WIPART.data_ptr()}
+    dw_gemms = sum(1 for n, a in calls if n == "ppo_gemm_f32" and a[8] in dw_out)
+    assert dw_gemms == (0 if ex.seq_dw else 2 * steps)
+    e_ptr, lde = ex._trunk_out()
     for name, args in calls:
         _, argtypes = _lib.SIGNATURES[name]
         assert len(args) == len(argtypes), name
         if name == "ppo_gru_fwd_seq_f32":
             assert args[3] == Bm * 3 * H and args[10] == Bm and args[-6:-3] == (Bm, H, T)
             assert args[-3] == ex.SEQX.data_ptr() and args[-2] == ex.SEQERR.data_ptr()
-        if name == "ppo_gru_bwd_seq_f32":
-            assert args[6] == Bm and args[9] == Bm * H and args[-6:-3] == (Bm, H, T)
+        if name in ("ppo_gru_bwd_seq_f32", "ppo_gru_bwd_seq_dw_f32"):
+            assert args[6] == Bm and args[9] == Bm * H and args[22:25] == (Bm, H, T)
+        if name == "ppo_gru_bwd_seq_dw_f32":
+            assert args[28:32] == (e_ptr, lde, Bm * lde, I)
+            assert args[32:] == (ex.WHPART.data_ptr(), ex.WHBPART.data_ptr(), ex.WIPART.data_ptr(),
+                                 ex.WIBPART.data_ptr())
+            assert ex.wh_splits == ex.wi_splits == (Bm + 15) // 16 == ex.WHPART.shape[0] == ex.WIPART.shape[0]
