@@ -372,9 +372,17 @@ __device__ __forceinline__ unsigned tag_of(u64 p) { return (unsigned)(p >> 32); 
 // lane run faster (212 -> 193 us per 64-step launch at 256 x 256); the
 // backward's 48 loads per lane run faster issued inside the polling loop,
 // each only while its pair is missing (310 against 414 us).
+// signal (may be null): set to sig once the first round of loads is issued
+// (a hint for the waves that share this wave's SIMD; see the backward).
 template <int K, int KW, bool EAGER>
 __device__ __forceinline__ bool stage_wave(const u64* slot, int Bm, int b0, int kw, unsigned tag, float* sA,
-                                           int spin_limit) {
+                                           int spin_limit, int* signal = nullptr, int sig = 0) {
+  auto raise = [&]() {
+    if (signal) {
+      __builtin_amdgcn_sched_barrier(0);
+      __hip_atomic_store(signal, sig, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  };
   constexpr int NL = TILE * KW / 64;
   static_assert(TILE * KW % 64 == 0, "rows of KW pairs over a wave");
   const int lane = threadIdx.x & 63;
@@ -388,6 +396,7 @@ __device__ __forceinline__ bool stage_wave(const u64* slot, int Bm, int b0, int 
   if constexpr (EAGER) {
 #pragma unroll
     for (int q = 0; q < NL; ++q) v[q] = __hip_atomic_load(at(q), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    raise();
     for (int polls = 1;; ++polls) {
       bool mine = true;
 #pragma unroll
@@ -416,6 +425,7 @@ __device__ __forceinline__ bool stage_wave(const u64* slot, int Bm, int b0, int 
                                    __HIP_MEMORY_SCOPE_AGENT);
         }
       }
+      if (it == 0) raise();
 #pragma unroll
       for (int q = 0; q < NL; ++q) mine = mine && tag_of(v[q]) == tag;
       if (__builtin_amdgcn_ballot_w64(!mine) == 0) {
@@ -424,6 +434,7 @@ __device__ __forceinline__ bool stage_wave(const u64* slot, int Bm, int b0, int 
       }
       __builtin_amdgcn_s_sleep(1);
     }
+    if (spin_limit <= 0) raise();
   }
 #pragma unroll
   for (int q = 0; q < NL; ++q) {
@@ -631,15 +642,20 @@ struct BwdSeqArgs {
 // waves (two per SIMD), which multiply while the recurrence's waves wait for
 // their exchange loads.  The recurrence's epilogue of step s leaves the
 // step's dgate tile (16 rows x the workgroup's 16 units x 4 gates) in an LDS
-// pair of buffers; after the waves' meeting of step s - 1 (its partial
-// tiles), the weight-gradient waves add the tile's products into their 64 of
-// the K rows of both partials: k = 64 w + 16 (lane / 16) + 4 v + mt for
-// accumulator [mt][gate] element v (the MFMA's M index read as k = 64 w +
-// 4 m + mt, so that a lane's A operand is one 16-byte load of 4 consecutive
-// k), the block's rows as the MFMA's K (row 4 (lane / 16) + j at k-step j).
-// Every wave passes every barrier (the flag chunks' too), so a buffer is
-// read between the meetings of steps s - 1 and s - 2 and written again only
-// after the latter.
+// pair of buffers; while the recurrence stages step s - 2, the
+// weight-gradient waves add the tile's products into their 64 of the K rows
+// of both partials: k = 64 w + 16 (lane / 16) + 4 v + mt for accumulator
+// [mt][gate] element v (the MFMA's M index read as k = 64 w + 4 m + mt, so
+// that a lane's A operand is one 16-byte load of 4 consecutive k), the
+// block's rows as the MFMA's K (row 4 (lane / 16) + j at k-step j).  Every
+// wave passes every barrier (the flag chunks' too): a buffer is written
+// after the meeting of step s, read before the meeting of step s - 2 and
+// written again after it.  MFMAs of one wave hold up the VALU work of the
+// other wave on its SIMD (measured: the recurrence's epilogue took 4 700
+// instead of 1 950 cycles with them beside it), so a weight-gradient wave
+// starts its products only once the recurrence wave of its SIMD has issued
+// the step's exchange loads (stage flag in LDS; a hint for the schedule
+// only, the barriers order the data), and they run under the loads' latency.
 template <int NIT, bool DW>
 __global__ void __launch_bounds__(DW ? 512 : 256) gru_bwd_seq_kernel(BwdSeqArgs a) {
   constexpr int H3 = 64 * NIT;
@@ -650,6 +666,7 @@ __global__ void __launch_bounds__(DW ? 512 : 256) gru_bwd_seq_kernel(BwdSeqArgs 
   __shared__ uint8_t done[FLAG_CHUNK][TILE];
   __shared__ float sdg[DW ? 2 : 1][4][TILE][TILE + 4];   // [step % 2][dan|dar|daz|dhn][unit][row]
   __shared__ int gave_up;  // the step at which a wait gave up, -1 while none has
+  __shared__ int staging[WAVES];  // DW: the step whose exchange loads recurrence wave w has issued
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -697,13 +714,25 @@ __global__ void __launch_bounds__(DW ? 512 : 256) gru_bwd_seq_kernel(BwdSeqArgs 
         const int j = (a.T - 1 - s) % FLAG_CHUNK;
         if (j == 0) load_flag_chunk(done, a.term, a.trunc, a.flag_rows, a.flag_step, a.Bm, a.T, b0, t, -1);
         if (t < a.T) {
-          __syncthreads();  // the meeting of step s: step s + 1's tile is in sdg
+          if (s + 2 < a.T) {
+            // step s + 2's tile (written before the meeting of step s + 1),
+            // once the recurrence wave of this SIMD has issued step s's loads
+            for (int p = 0; p < (1 << 14) &&
+                            __hip_atomic_load(&staging[wave - WAVES], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) > s;
+                 ++p)
+              __builtin_amdgcn_s_sleep(1);
+            dw_step(s + 2);
+            dw_load(s + 1);
+          }
+          __syncthreads();  // the meeting of step s
           if (gave_up == s) return;
-          dw_step(s + 1);
-          dw_load(s);
         }
       }
       __syncthreads();  // step 0's tile
+      if (a.T >= 2) {
+        dw_step(1);
+        dw_load(0);
+      }
       dw_step(0);
       __syncthreads();  // (the recurrence waves' column sums)
       const int64_t xk = (int64_t)blockIdx.x * H;
@@ -753,6 +782,7 @@ __global__ void __launch_bounds__(DW ? 512 : 256) gru_bwd_seq_kernel(BwdSeqArgs 
   own(a.T - 1, dout, n, r, z, hn, hp);
   float dh_t = 0.f, z_t = 0.f;
   if (tid == 0) gave_up = -1;  // (published by the first flag chunk's barriers)
+  if (DW && tid < WAVES) staging[tid] = a.T;  // (no step issued yet; published likewise)
 
   float bsum[4] = {0.f, 0.f, 0.f, 0.f};  // DW: this thread's column sums of dan, dar, daz, dhn
 
@@ -769,7 +799,7 @@ __global__ void __launch_bounds__(DW ? 512 : 256) gru_bwd_seq_kernel(BwdSeqArgs 
       // dhp[b][u] = sum_c dgate_t[b][H + c] Wh[u][c], c < 3H
       const bool ok = stage_wave<H3, H3 / WAVES, false>(a.sync.ring + (t & 1) * slot_size, a.Bm, b0,
                                                         wave * (H3 / WAVES), (unsigned)(a.T - t), sAw,
-                                                        a.sync.spin_limit);
+                                                        a.sync.spin_limit, DW ? &staging[wave] : nullptr, s);
       // (issued after the wait, so that they do not hold it up)
       if (s > 0) own(s - 1, dout_n, n_n, r_n, z_n, hn_n, hp_n);
       floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
