@@ -101,14 +101,16 @@ SIGNATURES = {
     "ppo_head_loss_max_outputs": (I, []),
     "ppo_head_loss_max_features": (I, []),
     "ppo_head_loss_f32": (I, [P, I, I, P, P, I64, P, I64, P, I, P, I64, P, I64, P, I, I, P, P, P, P, P, P, P,
-                              I, P, I64, P, I64, I, P, I64, P, I64, P, P, P, P, P, P, F, I, F, F, F]),
+                              I, P, I64, P, I64, I, P, I64, P, I64, P, P, P, P, P, P, F, I, F, F, F, I64]),
+    "ppo_pack_samples": (I, [P, I64, P, P, P, P, P, P]),
     "ppo_mlp_ln_fwd_head_loss_f32": (I, [P, I, I, P, I64, P, I, I, P, I64, I64, P, P, P, P, P, I64, P, P, F, I, I64,
                                          I64, I64, I64, P, I64,
                                          I, I, P, P, I64, P, I64, P, I, P, I64, P, I64, P, I, I, P, P, P, P, P, P,
-                                         P, I, P, I64, P, I64, I, P, I64, P, I64, P, P, P, P, P, P, F, I, F, F, F]),
+                                         P, I, P, I64, P, I64, I, P, I64, P, I64, P, P, P, P, P, P, F, I, F, F, F,
+                                         I64]),
     "ppo_head_loss_ratio_f32": (I, [P, I, I, P, P, I64, P, I64, P, I, P, I64, P, I64, P, I, I, P, P, P, P, P, P, P,
                                     I, P, I64, P, I64, I, P, I64, P, I64, P, P, P, P, P, P, F, I, F, F, F, P, I,
-                                    I]),
+                                    I, I64]),
     "ppo_gru_fwd_step_f32": (I, [P, P, I64, P, I64, P, P, P, P, P, I64, P, P, I64, P, I64, P, I64, I, I]),
     "ppo_gru_bwd_step_f32": (I, [P, P, I64, P, I64, P, I64, P, I64, P, P, P, P, I64, P, I64, P, I64, P, I64, P,
                                  I64, I, I]),

@@ -39,6 +39,11 @@ struct HeadLossParams {
   // optional: each row's ratio exp(logp - old_logp) written env-major,
   // ratio_out[(s % ratio_envs) * ratio_steps + s / ratio_envs] for sample s = t * N + env
   float* ratio_out; int ratio_envs, ratio_steps;
+  // elements between consecutive samples of old_logp, old_value, adv, ret
+  // and action_i (1: separate columns); rec4: those four are one 16-byte
+  // aligned float4 per sample (ppo_pack_samples records), read as one load
+  int64_t sample_stride;
+  bool rec4;
 };
 
 // jax's tie rule: x's share of the cotangent of ans = min / max (x, y) is 1
@@ -97,13 +102,22 @@ __device__ __forceinline__ void lane_gathers(const HeadLossParams& p, int j, Lan
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int64_t s = in[g].s;
-    in[g].olp = p.old_logp[s];
-    in[g].adv = p.adv[s];
-    in[g].ret = p.ret[s];
-    in[g].vold = p.old_value[s];
+    const int64_t o = s * p.sample_stride;
+    if (p.rec4) {
+      const floatx4 r = *reinterpret_cast<const floatx4*>(p.old_logp + o);
+      in[g].olp = r[0];
+      in[g].vold = r[1];
+      in[g].adv = r[2];
+      in[g].ret = r[3];
+    } else {
+      in[g].olp = p.old_logp[o];
+      in[g].adv = p.adv[o];
+      in[g].ret = p.ret[o];
+      in[g].vold = p.old_value[o];
+    }
     in[g].a = 0;
     in[g].actf = 0.f;
-    if (p.dist == DIST_CATEGORICAL) in[g].a = p.action_i[s];
+    if (p.dist == DIST_CATEGORICAL) in[g].a = p.action_i[o];
     else in[g].actf = p.action_f[s * p.A + min(j, p.A - 1)];
   }
 }
@@ -357,6 +371,6 @@ int head_loss_setup(HeadLossParams& p, const char* name, int dist, int rows, con
                     float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a, float* wpart_c, float* bpart_c,
                     float* dscale_partial, double* stats_partial, float clip_eps, int clip_value_loss,
                     float ent_coef, float vf_coef, float temperature, float* ratio_out, int ratio_envs,
-                    int ratio_steps);
+                    int ratio_steps, int64_t sample_stride);
 
 }  // namespace ppo_hl

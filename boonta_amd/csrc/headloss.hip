@@ -546,8 +546,9 @@ int ppo_hl::head_loss_setup(
     int act_a, const float* aux_a, int64_t ldaux_a, float* dha, int64_t lddha, int act_c, const float* aux_c,
     int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a, float* wpart_c, float* bpart_c,
     float* dscale_partial, double* stats_partial, float clip_eps, int clip_value_loss, float ent_coef,
-    float vf_coef, float temperature, float* ratio_out, int ratio_envs, int ratio_steps) {
+    float vf_coef, float temperature, float* ratio_out, int ratio_envs, int ratio_steps, int64_t sample_stride) {
   const bool sep = hc != nullptr;
+  if (sample_stride < 1) return ppo::set_error(PPO_ERR_ARG, "%s: sample_stride must be at least 1", name);
   if (rows < 0 || F <= 0 || F > 512 || F % 16 != 0 || na <= 0 || na > 16 || ldwa < na || ldwa > 16 || A <= 0 ||
       A > 16 ||
       (dist != DIST_CATEGORICAL && dist != DIST_GAUSSIAN) || !ha || !wa || !ba || !old_logp || !old_value ||
@@ -576,6 +577,9 @@ int ppo_hl::head_loss_setup(
   p.clip_eps = clip_eps; p.clip_value_loss = clip_value_loss; p.ent_coef = ent_coef; p.vf_coef = vf_coef;
   p.inv_n = rows > 0 ? 1.f / (float)rows : 0.f; p.temperature = temperature;
   p.ratio_out = ratio_out; p.ratio_envs = ratio_envs; p.ratio_steps = ratio_steps;
+  p.sample_stride = sample_stride;
+  p.rec4 = sample_stride % 4 == 0 && !(reinterpret_cast<uintptr_t>(old_logp) & 15) && old_value == old_logp + 1 &&
+           adv == old_logp + 2 && ret == old_logp + 3;
   return PPO_OK;
 }
 
@@ -587,14 +591,14 @@ static int head_loss_impl(
     const float* aux_a, int64_t ldaux_a, float* dha, int64_t lddha, int act_c, const float* aux_c,
     int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a, float* wpart_c, float* bpart_c,
     float* dscale_partial, double* stats_partial, float clip_eps, int clip_value_loss, float ent_coef,
-    float vf_coef, float temperature, float* ratio_out, int ratio_envs, int ratio_steps) {
+    float vf_coef, float temperature, float* ratio_out, int ratio_envs, int ratio_steps, int64_t sample_stride) {
   const bool sep = hc != nullptr;
   HeadLossParams p;
   const int rc = head_loss_setup(p, "ppo_head_loss_f32", dist, rows, idx, ha, ldha, wa, ldwa, ba, na, hc, ldhc, wc,
                                  ldwc, bc, F, A, scale_param, action_i, action_f, old_logp, old_value, adv, ret,
                                  act_a, aux_a, ldaux_a, dha, lddha, act_c, aux_c, ldaux_c, dhc, lddhc, wpart_a,
                                  bpart_a, wpart_c, bpart_c, dscale_partial, stats_partial, clip_eps, clip_value_loss,
-                                 ent_coef, vf_coef, temperature, ratio_out, ratio_envs, ratio_steps);
+                                 ent_coef, vf_coef, temperature, ratio_out, ratio_envs, ratio_steps, sample_stride);
   if (rc != PPO_OK) return rc;
   if (rows == 0) return PPO_OK;
   const int blocks = ppo_head_loss_blocks(rows);
@@ -652,11 +656,12 @@ PPO_EXPORT int ppo_head_loss_f32(
     const float* aux_a, int64_t ldaux_a, float* dha, int64_t lddha, int act_c, const float* aux_c,
     int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a, float* wpart_c, float* bpart_c,
     float* dscale_partial, double* stats_partial, float clip_eps, int clip_value_loss, float ent_coef,
-    float vf_coef, float temperature) {
+    float vf_coef, float temperature, int64_t sample_stride) {
   return head_loss_impl(stream, dist, rows, idx, ha, ldha, wa, ldwa, ba, na, hc, ldhc, wc, ldwc, bc, F, A,
                         scale_param, action_i, action_f, old_logp, old_value, adv, ret, act_a, aux_a, ldaux_a, dha,
                         lddha, act_c, aux_c, ldaux_c, dhc, lddhc, wpart_a, bpart_a, wpart_c, bpart_c, dscale_partial,
-                        stats_partial, clip_eps, clip_value_loss, ent_coef, vf_coef, temperature, nullptr, 1, 1);
+                        stats_partial, clip_eps, clip_value_loss, ent_coef, vf_coef, temperature, nullptr, 1, 1,
+                        sample_stride);
 }
 
 // ppo_head_loss_f32 that also writes each row's ratio exp(logp - old_logp)
@@ -671,12 +676,40 @@ PPO_EXPORT int ppo_head_loss_ratio_f32(
     const float* aux_a, int64_t ldaux_a, float* dha, int64_t lddha, int act_c, const float* aux_c,
     int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a, float* wpart_c, float* bpart_c,
     float* dscale_partial, double* stats_partial, float clip_eps, int clip_value_loss, float ent_coef,
-    float vf_coef, float temperature, float* ratio_out, int envs, int steps) {
+    float vf_coef, float temperature, float* ratio_out, int envs, int steps, int64_t sample_stride) {
   if (!ratio_out || envs < 1 || steps < 1 || (int64_t)envs * steps > INT32_MAX)
     return ppo::set_error(PPO_ERR_ARG, "ppo_head_loss_ratio_f32: bad ratio buffer (envs %d, steps %d)", envs, steps);
   return head_loss_impl(stream, dist, rows, idx, ha, ldha, wa, ldwa, ba, na, hc, ldhc, wc, ldwc, bc, F, A,
                         scale_param, action_i, action_f, old_logp, old_value, adv, ret, act_a, aux_a, ldaux_a, dha,
                         lddha, act_c, aux_c, ldaux_c, dhc, lddhc, wpart_a, bpart_a, wpart_c, bpart_c, dscale_partial,
                         stats_partial, clip_eps, clip_value_loss, ent_coef, vf_coef, temperature, ratio_out, envs,
-                        steps);
+                        steps, sample_stride);
+}
+
+// One 32-byte record per sample for the fused loss's gathers, sample_stride
+// 8: {old log-prob, old value, advantage, return, action (int32 bits, 0
+// without), 0, 0, 0}, so that a row's four rollout scalars arrive in one
+// 16-byte load and its action from the same 64-byte sector, instead of five
+// scattered 4-byte reads.
+__global__ void pack_samples_kernel(int64_t n, const float* __restrict__ old_logp, const float* __restrict__ old_value,
+                                    const float* __restrict__ adv, const float* __restrict__ ret,
+                                    const int32_t* __restrict__ action_i, float* __restrict__ rec) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const floatx4 a = {old_logp[i], old_value[i], adv[i], ret[i]};
+  const floatx4 b = {action_i ? __int_as_float(action_i[i]) : 0.f, 0.f, 0.f, 0.f};
+  reinterpret_cast<floatx4*>(rec)[2 * i] = a;
+  reinterpret_cast<floatx4*>(rec)[2 * i + 1] = b;
+}
+
+PPO_EXPORT int ppo_pack_samples(void* stream, int64_t n, const float* old_logp, const float* old_value,
+                                const float* adv, const float* ret, const int32_t* action_i, float* rec) {
+  if (n < 0 || (n > 0 && (!old_logp || !old_value || !adv || !ret || !rec)))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_pack_samples: bad argument (n=%lld)", (long long)n);
+  if (reinterpret_cast<uintptr_t>(rec) & 15)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_pack_samples: records must be 16-byte aligned");
+  if (n == 0) return PPO_OK;
+  hipLaunchKernelGGL(pack_samples_kernel, dim3((unsigned)ppo::ceil_div64(n, 256)), dim3(256), 0,
+                     ppo::as_stream(stream), n, old_logp, old_value, adv, ret, action_i, rec);
+  return ppo::check_launch("ppo_pack_samples");
 }

@@ -761,7 +761,7 @@ PPO_EXPORT int ppo_mlp_ln_fwd_head_loss_f32(
     int act_a, const float* aux_a, int64_t ldaux_a, float* dha, int64_t lddha, int act_c, const float* aux_c,
     int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a, float* wpart_c, float* bpart_c,
     float* dscale_partial, double* stats_partial, float clip_eps, int clip_value_loss, float ent_coef,
-    float vf_coef, float temperature) {
+    float vf_coef, float temperature, int64_t sample_stride) {
   const char* name = "ppo_mlp_ln_fwd_head_loss_f32";
   FwdArgs a;
   bool va = false;
@@ -773,7 +773,8 @@ PPO_EXPORT int ppo_mlp_ln_fwd_head_loss_f32(
   rc = head_loss_setup(hp, name, dist, rows, idx, ha, ldha, wa, ldwa, ba, na, hc, ldhc, wc, ldwc, bc, F, A,
                        scale_param, action_i, action_f, old_logp, old_value, adv, ret, act_a, aux_a, ldaux_a, dha,
                        lddha, act_c, aux_c, ldaux_c, dhc, lddhc, wpart_a, bpart_a, wpart_c, bpart_c, dscale_partial,
-                       stats_partial, clip_eps, clip_value_loss, ent_coef, vf_coef, temperature, nullptr, 1, 1);
+                       stats_partial, clip_eps, clip_value_loss, ent_coef, vf_coef, temperature, nullptr, 1, 1,
+                       sample_stride);
   if (rc != PPO_OK) return rc;
   if (towers != 2 || !hc || F != MC_F || act_a != ACT_NONE || act_c != ACT_NONE || rows != M || ha != Y[L - 1] ||
       hc != Y[L - 1] + stride_rows || ldha != ld || ldhc != ld || (reinterpret_cast<uintptr_t>(wa) & 255) ||

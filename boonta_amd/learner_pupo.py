@@ -36,6 +36,8 @@ class PuPOExecutor(RecurrentExecutor):
     """One compiled RecurrentPuPO.update for fixed (T, N, obs, minibatches, epochs)."""
 
     beta = 0.2  # importance_exponent(state.step), set by the algorithm before each issue
+    # the loss reads each step's own weighted advantages (no per-update records)
+    RECORDS = False
 
     def _alloc_extra(self):
         super()._alloc_extra()

@@ -171,6 +171,7 @@ class RecurrentExecutor(MLPExecutor):
                    _p(self.BOOT), None, None, _p(self.ADV), _p(self.RET), T, N, float(cfg.gamma),
                    float(cfg.gae_lambda), 0)
         self._normalize(st)
+        self._pack_samples(st)
         # 3. env permutations, and the sample rows of every minibatch
         self._call("ppo_epoch_permutations", st, _p(self.KEY), self.E, N, _p(self.PERM), _p(self.PERM_WS),
                    self.PERM_WS.numel())

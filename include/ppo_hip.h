@@ -526,7 +526,11 @@ int ppo_loss_finalize_steps(void* stream, const double* stats_partial, int nbloc
  * (times act'(aux) when act != NONE), per-block head weight / bias gradient
  * partials [blocks][F][ld] / [blocks][ld] (blocks = ppo_head_loss_blocks(rows)),
  * statistics and Gaussian scale partials as ppo_loss_f32 does.  F <= 512,
- * na <= 16. */
+ * na <= 16.  sample_stride: elements between consecutive samples of
+ * old_logp, old_value, adv, ret and action_i (1: separate columns; 8: the
+ * records of ppo_pack_samples, old_logp = rec, old_value = rec + 1, adv =
+ * rec + 2, ret = rec + 3, action_i = rec + 4, whose four scalars a row then
+ * reads in one 16-byte load). */
 int ppo_head_loss_blocks(int rows);
 int ppo_head_loss_max_outputs(void);
 int ppo_head_loss_max_features(void);
@@ -538,7 +542,16 @@ int ppo_head_loss_f32(void* stream, int dist, int rows, const int32_t* idx, cons
                       int64_t ldaux_a, float* dha, int64_t lddha, int act_c, const float* aux_c,
                       int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a,
                       float* wpart_c, float* bpart_c, float* dscale_partial, double* stats_partial,
-                      float clip_eps, int clip_value_loss, float ent_coef, float vf_coef, float temperature);
+                      float clip_eps, int clip_value_loss, float ent_coef, float vf_coef, float temperature,
+                      int64_t sample_stride);
+/* The per-sample rollout inputs of the fused loss (the gathers of
+ * boonta/algorithms/ppo.py:148-151 for log_prob, value, advantages, returns
+ * and categorical actions) as one 32-byte record per sample, written once per
+ * update after the advantages are final: rec[8 s .. 8 s + 7] = {old_logp,
+ * old_value, adv, ret, action_i bits (0 when action_i is NULL), 0, 0, 0}.
+ * rec 16-byte aligned. */
+int ppo_pack_samples(void* stream, int64_t n, const float* old_logp, const float* old_value, const float* adv,
+                     const float* ret, const int32_t* action_i, float* rec);
 /* The forward chain of an actor / critic pair of towers followed, in the same
  * launch, by their fused heads + PPO loss on the chains' last outputs: what
  * ppo_mlp_ln_fwd_f32(stream, <its arguments>) then ppo_head_loss_f32(stream,
@@ -563,7 +576,7 @@ int ppo_mlp_ln_fwd_head_loss_f32(
     int act_a, const float* aux_a, int64_t ldaux_a, float* dha, int64_t lddha, int act_c, const float* aux_c,
     int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a, float* wpart_c, float* bpart_c,
     float* dscale_partial, double* stats_partial, float clip_eps, int clip_value_loss, float ent_coef,
-    float vf_coef, float temperature);
+    float vf_coef, float temperature, int64_t sample_stride);
 /* ppo_head_loss_f32 that also keeps each row's ratio exp(logp - old_logp),
  * env-major: ratio_out[(s % envs) * steps + s / envs] for the row's sample
  * s = idx[row] = t * envs + env (the new ratio RecurrentPuPO scatters back
@@ -577,7 +590,8 @@ int ppo_head_loss_ratio_f32(void* stream, int dist, int rows, const int32_t* idx
                             const float* aux_c, int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a,
                             float* bpart_a, float* wpart_c, float* bpart_c, float* dscale_partial,
                             double* stats_partial, float clip_eps, int clip_value_loss, float ent_coef,
-                            float vf_coef, float temperature, float* ratio_out, int envs, int steps);
+                            float vf_coef, float temperature, float* ratio_out, int envs, int steps,
+                            int64_t sample_stride);
 
 /* ------------------------------------------------------------------- GRU
  * One time step of flax.linen.GRUCell inside boonta's RNN block

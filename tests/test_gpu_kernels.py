@@ -816,25 +816,52 @@ def test_fused_heads_loss_and_head_backward(sep, dist, A, F, rows, act):
     XA = dev(aux_a)
     XC = dev(aux_c) if sep else None
     blocks = _lib.load().ppo_head_loss_blocks(rows)
-    DHA = torch.zeros(rows, F, device=DEV)
-    DHC = torch.zeros(rows, F, device=DEV) if sep else None
-    WPA = torch.full((blocks, F, ldw), float("nan"), device=DEV)
-    BPA = torch.full((blocks, ldw), float("nan"), device=DEV)
-    WPC = torch.full((blocks, F, 4), float("nan"), device=DEV) if sep else None
-    BPC = torch.full((blocks, 4), float("nan"), device=DEV) if sep else None
-    DS = torch.zeros(blocks, A, device=DEV) if spread else None
-    STATS = torch.zeros(blocks, 11, dtype=torch.float64, device=DEV)
     IDX, ACT = dev(idx), dev(action)
     OLP, OV, ADV, RET = dev(old_logp), dev(old_value), dev(adv), dev(ret)
     SC = dev(scale) if spread else None
     a_code = _lib.ACT[act]
     p = lambda t: None if t is None else t.data_ptr()
-    _lib.call("ppo_head_loss_f32", st(), _lib.DIST[dist], rows, IDX.data_ptr(), HA.data_ptr(), F, WA.data_ptr(), ldw,
-              BA.data_ptr(), na, p(HC), F, p(WC) if sep else None, 4, p(BC) if sep else None, F, A, p(SC),
-              ACT.data_ptr() if dist == "categorical" else None, ACT.data_ptr() if dist == "gaussian" else None,
-              OLP.data_ptr(), OV.data_ptr(), ADV.data_ptr(), RET.data_ptr(), a_code, XA.data_ptr(), F,
-              DHA.data_ptr(), F, a_code if sep else 0, p(XC), F, p(DHC), F, WPA.data_ptr(),
-              BPA.data_ptr(), p(WPC), p(BPC), p(DS), STATS.data_ptr(), 0.2, 1, 0.01, 0.5, 1.0)
+    cat = dist == "categorical"
+
+    def launch(records):
+        """The kernel's outputs, its per-sample inputs read from separate
+        columns or from the 32-byte records of ppo_pack_samples."""
+        o = dict(DHA=torch.zeros(rows, F, device=DEV), DHC=torch.zeros(rows, F, device=DEV) if sep else None,
+                 WPA=torch.full((blocks, F, ldw), float("nan"), device=DEV),
+                 BPA=torch.full((blocks, ldw), float("nan"), device=DEV),
+                 WPC=torch.full((blocks, F, 4), float("nan"), device=DEV) if sep else None,
+                 BPC=torch.full((blocks, 4), float("nan"), device=DEV) if sep else None,
+                 DS=torch.zeros(blocks, A, device=DEV) if spread else None,
+                 STATS=torch.zeros(blocks, 11, dtype=torch.float64, device=DEV))
+        cols = (OLP.data_ptr(), OV.data_ptr(), ADV.data_ptr(), RET.data_ptr())
+        act_i, stride = (ACT.data_ptr() if cat else None), 1
+        if records:
+            REC = torch.full((B, 8), float("nan"), device=DEV)
+            _lib.call("ppo_pack_samples", st(), B, *cols, act_i, REC.data_ptr())
+            r = REC.data_ptr()
+            cols, act_i, stride = (r, r + 4, r + 8, r + 12), (r + 16 if cat else None), 8
+            o["REC"] = REC
+        _lib.call("ppo_head_loss_f32", st(), _lib.DIST[dist], rows, IDX.data_ptr(), HA.data_ptr(), F, WA.data_ptr(),
+                  ldw, BA.data_ptr(), na, p(HC), F, p(WC) if sep else None, 4, p(BC) if sep else None, F, A, p(SC),
+                  act_i, None if cat else ACT.data_ptr(), *cols, a_code, XA.data_ptr(), F,
+                  o["DHA"].data_ptr(), F, a_code if sep else 0, p(XC), F, p(o["DHC"]), F, o["WPA"].data_ptr(),
+                  o["BPA"].data_ptr(), p(o["WPC"]), p(o["BPC"]), p(o["DS"]), o["STATS"].data_ptr(), 0.2, 1, 0.01, 0.5,
+                  1.0, stride)
+        return o
+
+    o = launch(False)
+    DHA, DHC, WPA, BPA, WPC, BPC, DS, STATS = (o[k] for k in ("DHA", "DHC", "WPA", "BPA", "WPC", "BPC", "DS", "STATS"))
+    # the records path: the same values, so the same bits
+    r = launch(True)
+    torch.cuda.synchronize()
+    rec = host(r["REC"])
+    np.testing.assert_array_equal(rec[:, :4], np.stack([old_logp, old_value, adv, ret], 1))
+    np.testing.assert_array_equal(rec[:, 4].view(np.int32), action if cat else 0)
+    np.testing.assert_array_equal(rec[:, 5:], 0.0)
+    bits = lambda t: t.view(torch.int64 if t.dtype == torch.float64 else torch.int32)
+    for k, t in o.items():
+        if t is not None:
+            assert torch.equal(bits(t), bits(r[k])), k
     outv = torch.zeros(9, device=DEV)
     _lib.call("ppo_loss_finalize", st(), STATS.data_ptr(), blocks, rows, 0.01, 0.5, outv.data_ptr())
     np.testing.assert_allclose(host(DHA), dha_ref, rtol=1e-4, atol=1e-7)
