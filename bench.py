@@ -122,7 +122,7 @@ def dw_group_problems(args):
 
 def gru_seq_shape(name, args):
     """(sequences, units, steps) of a GRU sequence launch."""
-    i = 23 if name == "ppo_gru_fwd_seq_f32" else 22   # after the stream: Bm, H, T
+    i = {"ppo_gru_fwd_seq_f32": 23, "ppo_gru_fwd_seq_xw_f32": 20}.get(name, 22)   # after the stream: Bm, H, T
     return args[i], args[i + 1], args[i + 2]
 
 
@@ -170,6 +170,16 @@ def _single_launch_work(name, args):
         acts = (1 if args[26] else 0) + (1 if args[31] else 0)
         per_row = 4.0 * F * (2 * groups + acts) + 4.0 * 6 + (4.0 * A if args[1] == 1 else 0.0)
         return 0.0, rows * per_row
+    if name == "ppo_mlp_ln_fwd_head_loss_f32":
+        # the chain's work, then the fused heads + loss on its last outputs
+        # (the entry point's arguments after the chain's are the head loss's)
+        # (the heads read their inputs from the chain's last tiles in LDS: the
+        # head loss's own reads of them are not counted)
+        head = (args[0],) + tuple(args[27:])
+        cf, cb = _single_launch_work("ppo_mlp_ln_fwd_f32", args[:27])
+        hf, hb = _single_launch_work("ppo_head_loss_f32", head)
+        rows, F, groups = head[2], head[15], (2 if head[10] else 1)
+        return cf + hf, cb + hb - 4.0 * rows * F * groups
     if name == "ppo_mlp_ln_fwd_f32":
         towers, L, M, K0 = args[1], args[2], args[6], args[7]
         weights = 256 * (K0 + 256 * (L - 1)) + 3 * 256 * L
@@ -211,8 +221,15 @@ def _single_launch_work(name, args):
         head = 8.0 * K * args[11] if len(args) > 11 and args[8] else 0.0
         return 0.0, 4.0 * L * K * N + head
     if name == "ppo_gru_fwd_seq_f32":
-        Bm, H, T = args[-6], args[-5], args[-4]
+        Bm, H, T = gru_seq_shape(name, args)
         return 2.0 * Bm * H * 3 * H * T, 4.0 * T * Bm * (3 * H + H + H + 4 * H) + 4.0 * H * 3 * H
+    if name == "ppo_gru_fwd_seq_xw_f32":
+        # the input projections made in the launch: the GRU input rows read
+        # instead of the projections, and their products
+        Bm, H, T = gru_seq_shape(name, args)
+        I = args[29]
+        return (2.0 * Bm * H * 3 * H * T + 2.0 * T * Bm * I * 3 * H,
+                4.0 * T * Bm * (I + H + H + 4 * H) + 4.0 * (H + I) * 3 * H)
     if name in ("ppo_gru_bwd_seq_f32", "ppo_gru_bwd_seq_dw_f32"):
         Bm, H, T = gru_seq_shape(name, args)
         flops = 2.0 * Bm * 3 * H * H * max(T - 1, 0)
@@ -265,11 +282,11 @@ def _single_launch_shape(name, args):
         return [args[15], args[17], args[16]]
     if name == "ppo_step_mlp_categorical_f32":
         return [args[3], 256, args[4], args[5]]
-    if name == "ppo_mlp_ln_fwd_f32":
+    if name in ("ppo_mlp_ln_fwd_f32", "ppo_mlp_ln_fwd_head_loss_f32"):
         return [args[6], 256, args[7], args[2], args[1]]
     if name == "ppo_mlp_ln_bwd_f32":
         return [args[5], 256, 256, args[2], args[1]]
-    if name in ("ppo_gru_fwd_seq_f32", "ppo_gru_bwd_seq_f32", "ppo_gru_bwd_seq_dw_f32"):
+    if name in ("ppo_gru_fwd_seq_f32", "ppo_gru_fwd_seq_xw_f32", "ppo_gru_bwd_seq_f32", "ppo_gru_bwd_seq_dw_f32"):
         return list(gru_seq_shape(name, args))
     if name == "ppo_mlp16_ln_fwd":
         return [args[6], 512, 512, args[1]]
@@ -302,7 +319,7 @@ def launch_key(name, args):
         return (name,) + tuple(dw_group_problems(args))
     if name in ("ppo_gru_fwd_step_f32", "ppo_gru_bwd_step_f32"):
         return (name, args[-2], args[-1], bool(args[1]))
-    if name in ("ppo_gru_fwd_seq_f32", "ppo_gru_bwd_seq_f32", "ppo_gru_bwd_seq_dw_f32"):
+    if name in ("ppo_gru_fwd_seq_f32", "ppo_gru_fwd_seq_xw_f32", "ppo_gru_bwd_seq_f32", "ppo_gru_bwd_seq_dw_f32"):
         return (name,) + gru_seq_shape(name, args)
     if name == "ppo_mlp16_ln_fwd":
         return (name, args[1], args[5], args[6])

@@ -483,14 +483,30 @@ struct FwdSeqArgs {
   float* gates; int64_t ldg, g_step;
   int Bm, H, T;
   SeqSync sync;
+  // XW kernels: the input projections xi = e Wi + bi made in the launch from
+  // the GRU input e of row t Bm + b at e + t e_step + b lde (xi unused)
+  const float* e; int64_t lde, e_step;
+  const float* wi; int64_t ldwi;
+  const float* bi;
 };
 
-template <int NIT>
-__global__ void __launch_bounds__(256) gru_fwd_seq_kernel(FwdSeqArgs a) {
+// Input projections inside the forward (XW): four more waves (two per SIMD)
+// multiply step t's input rows of the workgroup's 16 sequences with its 48
+// columns of Wi ([n|r|z] of its 16 units), each wave a quarter of the 256
+// inputs with its slice of Wi in registers, between the waves' meetings of
+// steps t - 1 and t; the four partial tiles go to an LDS pair of buffers and
+// the recurrence's epilogue of step t adds them in wave order, then the bias.
+// Each MFMA group is followed by idle cycles so that the recurrence wave of
+// its SIMD keeps issuing (the backward's weight-gradient waves measured the
+// same).  Every wave passes every barrier (the flag chunks' too).
+template <int NIT, bool XW>
+__global__ void __launch_bounds__(XW ? 512 : 256) gru_fwd_seq_kernel(FwdSeqArgs a) {
   constexpr int H = 64 * NIT;
+  static_assert(!XW || H == 256, "the input projections in the launch take H = 256 (and a 256-wide input)");
   __shared__ float red[2][WAVES][3][TILE][TILE + 1];
   __shared__ float sA[WAVES][TILE * (H / WAVES + 4)];  // each wave's staged quarter of the previous h
   __shared__ uint8_t done[FLAG_CHUNK][TILE];
+  __shared__ float sxi[XW ? 2 : 1][WAVES][3][TILE][TILE + 1];  // XW: [step % 2][wave][n|r|z][row][unit]
   __shared__ int gave_up;  // the step at which a wait gave up, -1 while none has
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -499,6 +515,56 @@ __global__ void __launch_bounds__(256) gru_fwd_seq_kernel(FwdSeqArgs a) {
   const int u0 = blockIdx.y * TILE;
   const int i = lane & 15;
   const int kq = lane >> 4;
+  if constexpr (XW) {
+    if (wave >= WAVES) {
+      // this lane's inputs k = kx + 16 c + q (c, q < 4) of the wave's quarter
+      const int kx = 64 * (wave - WAVES) + 4 * kq;
+      float bw[4][3][4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int g = 0; g < 3; ++g)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) bw[c][g][q] = a.wi[(int64_t)(kx + 16 * c + q) * a.ldwi + g * H + u0 + i];
+      // (a row from Bm on reads row b0: its projections are never used)
+      const int row = b0 + i < a.Bm ? b0 + i : b0;
+      floatx4 ea[4];
+      auto load_e = [&](int t) {
+        const float* er = a.e + t * a.e_step + (int64_t)row * a.lde + kx;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ea[c] = *reinterpret_cast<const floatx4*>(er + 16 * c);
+      };
+      load_e(0);
+      for (int t = 0; t < a.T; ++t) {
+        const int j = t % FLAG_CHUNK;
+        if (j == 0) load_flag_chunk(done, a.term, a.trunc, a.flag_rows, a.flag_step, a.Bm, a.T, b0, t, 1);
+        floatx4 acc[3];
+#pragma unroll
+        for (int g = 0; g < 3; ++g) acc[g] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+#pragma unroll
+            for (int g = 0; g < 3; ++g)
+              acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(ea[c][q], bw[c][g][q], acc[g], 0, 0, 0);
+            // (the idle gap)
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        float (*xt)[3][TILE][TILE + 1] = sxi[t & 1];
+#pragma unroll
+        for (int g = 0; g < 3; ++g)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) xt[wave - WAVES][g][4 * kq + v][i] = acc[g][v];
+        if (t + 1 < a.T) load_e(t + 1);
+        __syncthreads();  // the meeting of step t: its projections are in sxi
+        if (gave_up == t) return;
+      }
+      return;
+    }
+  }
   // this lane's columns: k0 + 16 c + q, c < NIT, q < 4 (the wave's quarter of H)
   const int k0 = wave * (H / WAVES) + 4 * kq;
   float* sAw = sA[wave];
@@ -520,10 +586,19 @@ __global__ void __launch_bounds__(256) gru_fwd_seq_kernel(FwdSeqArgs a) {
   const int rowc = row_in ? b0 + i : b0;
   const float bhn = a.bhn[u];
   const int64_t slot_size = (int64_t)a.Bm * H;
-  // this thread's input projections, loaded a step ahead, and its own
-  // previous h (no other workgroup writes them)
-  const float* x = a.xi + (int64_t)bbc * a.ldxi;
-  float xn = x[u], xr = x[H + u], xz = x[2 * H + u];
+  // this thread's input projections, loaded a step ahead (XW: made by the
+  // projection waves), and its own previous h (no other workgroup writes them)
+  const float* x = XW ? nullptr : a.xi + (int64_t)bbc * a.ldxi;
+  float xn = 0.f, xr = 0.f, xz = 0.f, bin = 0.f, bir = 0.f, biz = 0.f;
+  if constexpr (XW) {
+    bin = a.bi[u];
+    bir = a.bi[H + u];
+    biz = a.bi[2 * H + u];
+  } else {
+    xn = x[u];
+    xr = x[H + u];
+    xz = x[2 * H + u];
+  }
   float hp_raw = a.h0[(a.h0_rows ? (int64_t)a.h0_rows[bbc] : (int64_t)bbc) * a.ldh0 + u];
   if (tid == 0) gave_up = -1;  // (published by the first flag chunk's barriers)
 
@@ -545,7 +620,7 @@ __global__ void __launch_bounds__(256) gru_fwd_seq_kernel(FwdSeqArgs a) {
     };
     float xn_next = 0.f, xr_next = 0.f, xz_next = 0.f;
     auto load_next = [&]() {
-      if (t + 1 < a.T) {
+      if (!XW && t + 1 < a.T) {
         const float* xt = x + (t + 1) * a.xi_step;
         xn_next = xt[u];
         xr_next = xt[H + u];
@@ -589,6 +664,12 @@ __global__ void __launch_bounds__(256) gru_fwd_seq_kernel(FwdSeqArgs a) {
     __syncthreads();
     if (gave_up == t) return;
 
+    if constexpr (XW) {
+      const float (*xt)[3][TILE][TILE + 1] = sxi[t & 1];
+      xn = (((xt[0][0][ti][tj] + xt[1][0][ti][tj]) + xt[2][0][ti][tj]) + xt[3][0][ti][tj]) + bin;
+      xr = (((xt[0][1][ti][tj] + xt[1][1][ti][tj]) + xt[2][1][ti][tj]) + xt[3][1][ti][tj]) + bir;
+      xz = (((xt[0][2][ti][tj] + xt[1][2][ti][tj]) + xt[2][2][ti][tj]) + xt[3][2][ti][tj]) + biz;
+    }
     if (bb_ok) {
       float ar = 0.f, az = 0.f, an = 0.f;
 #pragma unroll
@@ -612,9 +693,11 @@ __global__ void __launch_bounds__(256) gru_fwd_seq_kernel(FwdSeqArgs a) {
       }
       hp_raw = h;
     }
-    xn = xn_next;
-    xr = xr_next;
-    xz = xz_next;
+    if constexpr (!XW) {
+      xn = xn_next;
+      xr = xr_next;
+      xz = xz_next;
+    }
   }
 }
 
@@ -1031,17 +1114,52 @@ PPO_EXPORT int ppo_gru_fwd_seq_f32(void* stream, const float* xi, int64_t ldxi, 
     return ppo::set_error(PPO_ERR_ARG, "ppo_gru_fwd_seq_f32: h0 and h_out rows must be 16-byte aligned");
   FwdSeqArgs a{xi, ldxi, xi_step, h0, ldh0, h0_rows, terminated, truncated, flag_rows, flag_step, wh, ldwh, bhn,
                h_out, ldo, h_step, hp_out, ldhp, hp_step, gates, ldg, g_step, Bm, H, T,
-               SeqSync{static_cast<u64*>(exchange), error, spin_limit}};
+               SeqSync{static_cast<u64*>(exchange), error, spin_limit}, nullptr, 0, 0, nullptr, 0, nullptr};
   hipStream_t st = ppo::as_stream(stream);
   if (T > 1) zero_ring(st, exchange, 2 * (int64_t)Bm * H);
   const dim3 grid(ppo::ceil_div(Bm, TILE), H / TILE);
   switch (H / 64) {
-    case 1: launch_seq(gru_fwd_seq_kernel<1>, grid, st, a); break;
-    case 2: launch_seq(gru_fwd_seq_kernel<2>, grid, st, a); break;
-    case 3: launch_seq(gru_fwd_seq_kernel<3>, grid, st, a); break;
-    default: launch_seq(gru_fwd_seq_kernel<4>, grid, st, a); break;
+    case 1: launch_seq(gru_fwd_seq_kernel<1, false>, grid, st, a); break;
+    case 2: launch_seq(gru_fwd_seq_kernel<2, false>, grid, st, a); break;
+    case 3: launch_seq(gru_fwd_seq_kernel<3, false>, grid, st, a); break;
+    default: launch_seq(gru_fwd_seq_kernel<4, false>, grid, st, a); break;
   }
   return ppo::check_launch("ppo_gru_fwd_seq_f32");
+}
+
+// ppo_gru_fwd_seq_f32 with the input projections made in the launch: xi =
+// e Wi + bi for the GRU input e of row t Bm + b at e + t e_step + b lde
+// (wi [I][3H] with row pitch ldwi, bi [3H], columns [n|r|z]: the flax
+// GRUCell's input Dense kernels, boonta/networks/blocks/rnn.py:34-54),
+// each step's products summed in a fixed order (not the order of a separate
+// GEMM launch: equal to it to rounding).  H = I = 256; e rows 16-byte aligned.
+PPO_EXPORT int ppo_gru_fwd_seq_xw_f32(void* stream, const float* h0, int64_t ldh0, const int32_t* h0_rows,
+                                      const uint8_t* terminated, const uint8_t* truncated, const int32_t* flag_rows,
+                                      int64_t flag_step, const float* wh, int64_t ldwh, const float* bhn,
+                                      float* h_out, int64_t ldo, int64_t h_step, float* hp_out, int64_t ldhp,
+                                      int64_t hp_step, float* gates, int64_t ldg, int64_t g_step, int Bm, int H, int T,
+                                      void* exchange, int* error, int spin_limit, const float* e, int64_t lde,
+                                      int64_t e_step, int I, const float* wi, int64_t ldwi, const float* bi) {
+  const int rc = seq_check("ppo_gru_fwd_seq_xw_f32", Bm, H, T, exchange, error);
+  if (rc != PPO_OK) return rc;
+  if (H != 256 || I != 256)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gru_fwd_seq_xw_f32: needs H = I = 256 (H=%d I=%d)", H, I);
+  if (Bm == 0 || T == 0) return PPO_OK;
+  if (!h0 || !wh || !bhn || !h_out || !e || !wi || !bi)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gru_fwd_seq_xw_f32: null buffer");
+  if (ldh0 < H || ldwh < 3 * H || ldo < H || (hp_out && ldhp < H) || (gates && ldg < 4 * H) || lde < I ||
+      ldwi < 3 * H)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gru_fwd_seq_xw_f32: leading dimension too small");
+  if (!aligned16(h0) || ldh0 % 4 || !aligned16(h_out) || ldo % 4 || h_step % 4 || !aligned16(e) || lde % 4 ||
+      e_step % 4)
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gru_fwd_seq_xw_f32: h0, h_out and e rows must be 16-byte aligned");
+  FwdSeqArgs a{nullptr, 0, 0, h0, ldh0, h0_rows, terminated, truncated, flag_rows, flag_step, wh, ldwh, bhn,
+               h_out, ldo, h_step, hp_out, ldhp, hp_step, gates, ldg, g_step, Bm, H, T,
+               SeqSync{static_cast<u64*>(exchange), error, spin_limit}, e, lde, e_step, wi, ldwi, bi};
+  hipStream_t st = ppo::as_stream(stream);
+  if (T > 1) zero_ring(st, exchange, 2 * (int64_t)Bm * H);
+  launch_seq(gru_fwd_seq_kernel<4, true>, dim3(ppo::ceil_div(Bm, TILE), H / TILE), st, a, 512);
+  return ppo::check_launch("ppo_gru_fwd_seq_xw_f32");
 }
 
 // Backward through time over T steps in one launch: step s (T - 1 down to 0)

@@ -68,11 +68,13 @@ class RecurrentExecutor(MLPExecutor):
         self.DGATE = torch.zeros(rows, 4 * H, **f32)
         # the recurrence of a minibatch in one launch per direction when all
         # its workgroups fit the device at once (else one launch per step);
-        # the backward launch then also multiplies the GRU's weight
-        # gradients, one partial per block of 16 sequences, where it takes
-        # the shape (else two GEMMs after it)
+        # where they take the shape, the forward launch also makes the input
+        # projections (else one GEMM before it) and the backward launch the
+        # GRU's weight gradients, one partial per block of 16 sequences (else
+        # two GEMMs after it)
         self.seq = self.SEQ and self._seq_fits(self.Bm, H)
         self.seq_dw = self.seq and self.SEQ_DW and H == 256 and I == 256
+        self.seq_xw = self.seq and self.SEQ_XW and H == 256 and I == 256
         if self.seq_dw:
             self.wh_splits = self.wi_splits = _lib.load().ppo_gru_seq_dw_parts(self.Bm)
         else:
@@ -93,6 +95,7 @@ class RecurrentExecutor(MLPExecutor):
 
     SEQ = True               # sequence launches where they fit
     SEQ_DW = True            # the weight gradients inside the backward sequence launch where it takes them
+    SEQ_XW = True            # the input projections inside the forward sequence launch where it takes them
     SEQ_SPIN = 1 << 18       # polls of a step wait before it gives up (about a second)
 
     @staticmethod
@@ -227,10 +230,16 @@ class RecurrentExecutor(MLPExecutor):
         # forward: trunk on the gathered rows, input projections of every step
         self._fwd_layers(st, self.trunk, inp["obs"], ldo, rows, mb)
         e_ptr, lde = self._trunk_out()
-        self._gemm(st, A_ROW, B_KN, e_ptr, lde, None, self.flat.view(g.wi), 3 * H, _p(self.XI),
-                   3 * H, mb, 3 * H, I, 1, 0, EPI_BIAS_ACT, self.flat.view(g.bi), 0, None, None, 0, None, -1)
+        if not self.seq_xw:
+            self._gemm(st, A_ROW, B_KN, e_ptr, lde, None, self.flat.view(g.wi), 3 * H, _p(self.XI),
+                       3 * H, mb, 3 * H, I, 1, 0, EPI_BIAS_ACT, self.flat.view(g.bi), 0, None, None, 0, None, -1)
         blk = Bm * H
-        if self.seq:
+        if self.seq_xw:
+            self._call("ppo_gru_fwd_seq_xw_f32", st, inp["carry0"], H, envs, fterm, ftrunc, rows, Bm,
+                       self.flat.view(g.wh), 3 * H, self.flat.view(g.bhn), _p(self.HOUT), H, blk, _p(self.HP), H,
+                       blk, _p(self.GATES), 4 * H, Bm * 4 * H, Bm, H, T, _p(self.SEQX), _p(self.SEQERR),
+                       self.SEQ_SPIN, e_ptr, lde, Bm * lde, I, self.flat.view(g.wi), 3 * H, self.flat.view(g.bi))
+        elif self.seq:
             self._call("ppo_gru_fwd_seq_f32", st, _p(self.XI), 3 * H, Bm * 3 * H, inp["carry0"], H, envs, fterm,
                        ftrunc, rows, Bm, self.flat.view(g.wh), 3 * H, self.flat.view(g.bhn), _p(self.HOUT), H, blk,
                        _p(self.HP), H, blk, _p(self.GATES), 4 * H, Bm * 4 * H, Bm, H, T, _p(self.SEQX),

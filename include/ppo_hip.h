@@ -647,6 +647,21 @@ int ppo_gru_bwd_seq_f32(void* stream, const float* wh, int64_t ldwh, const uint8
                         const float* hp, int64_t ldhp, int64_t hp_step, float* dh, int64_t lddh, int64_t dh_step,
                         float* dgate, int64_t lddg, int64_t dg_step, int Bm, int H, int T, void* exchange,
                         int* error, int spin_limit);
+/* ppo_gru_fwd_seq_f32 with the input projections made in the same launch
+ * (the x Wi + bi of the flax GRUCell, boonta/networks/blocks/rnn.py:34-54,
+ * for every step instead of one GEMM launch before the recurrence): xi = e
+ * Wi + bi for the GRU input e of row t Bm + b at e + t e_step + b lde, wi
+ * [I][3H] with row pitch ldwi and bi [3H] in columns [n|r|z].  Each step's
+ * products are summed in a fixed order of their own, so the results equal
+ * ppo_gru_fwd_seq_f32 on a GEMM's xi to rounding, not bit for bit.  H = I =
+ * 256; e rows 16-byte aligned. */
+int ppo_gru_fwd_seq_xw_f32(void* stream, const float* h0, int64_t ldh0, const int32_t* h0_rows,
+                           const uint8_t* terminated, const uint8_t* truncated, const int32_t* flag_rows,
+                           int64_t flag_step, const float* wh, int64_t ldwh, const float* bhn, float* h_out,
+                           int64_t ldo, int64_t h_step, float* hp_out, int64_t ldhp, int64_t hp_step, float* gates,
+                           int64_t ldg, int64_t g_step, int Bm, int H, int T, void* exchange, int* error,
+                           int spin_limit, const float* e, int64_t lde, int64_t e_step, int I, const float* wi,
+                           int64_t ldwi, const float* bi);
 /* ppo_gru_bwd_seq_f32 that also leaves the weight gradients of the GRU's
  * input and recurrent Dense kernels and their biases (the flax GRUCell of
  * boonta/networks/blocks/rnn.py:34-54 under jax.value_and_grad,

@@ -1,5 +1,5 @@
 """The GRU recurrence of a sequence minibatch in one launch per direction
-(ppo_gru_fwd_seq_f32 / ppo_gru_bwd_seq_f32 / ppo_gru_bwd_seq_dw_f32; the loop of
+(ppo_gru_fwd_seq_f32 / _xw_f32, ppo_gru_bwd_seq_f32 / _dw_f32; the loop of
 boonta/networks/blocks/rnn.py:34-54 and its backward through time) against
 the per-step launches it replaces, whose parity with the oracle is
 test_gpu_rnn.py's: bit-identical h, carries, gates, dh and gate cotangents,
@@ -146,6 +146,39 @@ def test_backward_with_weight_gradients(B, T):
         assert rel < 1e-5, (k, rel)
 
 
+@pytest.mark.parametrize("B,T", [(256, 64), (37, 9), (16, 3), (1, 2), (256, 1)])
+def test_forward_with_input_projections(B, T):
+    """ppo_gru_fwd_seq_xw_f32 against ppo_gru_fwd_seq_f32 on the projections
+    xi = e Wi + bi made in float64 and rounded once: the launch sums each
+    step's products in an order of its own, so h, the carries and the gates
+    agree to 2e-5 (absolute; |h| <= 1) rather than bit for bit, through 64
+    steps of the recurrence with resets.  Ragged last block, one step, one
+    sequence."""
+    H = I = 256
+    c = case(B, H, T, seed=B * 5 + T)
+    rng = np.random.default_rng(B + 3 * T)
+    e = rng.standard_normal((T * B, I)).astype(np.float32)
+    wi = (rng.standard_normal((I, 3 * H)) / np.sqrt(I)).astype(np.float32)
+    bi = (0.1 * rng.standard_normal(3 * H)).astype(np.float32)
+    c["XI"] = dev((e.astype(np.float64) @ wi.astype(np.float64) + bi).astype(np.float32))
+    E, WI, BI = dev(e), dev(wi), dev(bi)
+    ref, got = out_bufs(B, H, T), out_bufs(B, H, T)
+    sync, err = sync_bufs(B, H)
+    run_seq(c, ref, sync, err, backward=False)
+    blk, g4 = B * H, 4 * H
+    P = lambda k: c[k].data_ptr()
+    Q = lambda k: got[k].data_ptr()
+    print(f"fwd seq xw B={B} T={T}", flush=True)
+    _lib.call("ppo_gru_fwd_seq_xw_f32", st(), P("POOL"), H, P("ENVS"), P("TERM"), P("TRUNC"), P("ROWS"), B, P("WH"),
+              3 * H, P("BHN"), Q("HOUT"), H, blk, Q("HP"), H, blk, Q("GATES"), g4, B * g4, B, H, T, sync.data_ptr(),
+              err.data_ptr(), SPIN, E.data_ptr(), I, B * I, I, WI.data_ptr(), 3 * H, BI.data_ptr())
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    for k in ("HOUT", "HP", "GATES"):
+        diff = float((got[k] - ref[k]).abs().max())
+        assert diff < 2e-5, (k, diff)
+
+
 def test_a_wait_that_gives_up_sets_the_error_word_and_the_launch_ends():
     """Spin limit 0: every wait past the first step gives up at once.  The
     launch completes; the error word is set; step 0 (no wait) is done."""
@@ -179,10 +212,12 @@ def test_grids_larger_than_the_resident_workgroups_are_rejected():
 @pytest.mark.parametrize("use_graph", [False, True])
 def test_recurrent_update_with_sequence_launches_equals_the_step_launches(use_graph):
     """RecurrentPPO.update with each direction of the recurrence in one launch
-    (the weight gradients as GEMMs after it) against the same update issued
-    step by step: parameters and logs bit for bit after two updates, and no
-    wait gave up.  The default update, whose backward launch also multiplies
-    the GRU's weight gradients (summed in another order), against the first:
+    (the input projections and weight gradients as GEMMs before and after
+    it) against the same update issued step by step: parameters and logs bit
+    for bit after two updates, and no wait gave up.  The default update,
+    whose forward launch also makes the input projections and whose backward
+    launch also multiplies the GRU's weight gradients (summed in other
+    orders), against the first:
     the parameter change of the two updates within rel-L2 1e-3 of its norm,
     the logs within 1e-3 (a clip fraction may move by a sample)."""
     from boonta_amd.algorithms.ppo import flat_state_of
@@ -199,6 +234,7 @@ def test_recurrent_update_with_sequence_launches_equals_the_step_launches(use_gr
 
     class GemmDwExecutor(RecurrentExecutor):
         SEQ_DW = False
+        SEQ_XW = False
 
     class GemmDwPPO(RecurrentPPO):
         executor_class = GemmDwExecutor
@@ -209,7 +245,7 @@ def test_recurrent_update_with_sequence_launches_equals_the_step_launches(use_gr
         alg = cls(cfg=r.cfg, network=r.network, optimizer=r.optimizer, use_graph=use_graph)
         state = alg.init_from_params({"params": params}, r.obs_dim)
         ex = alg.executor(state, r.T, r.N, r.obs_dim)
-        assert ex.seq == (cls is not StepPPO) and ex.seq_dw == (cls is RecurrentPPO)
+        assert ex.seq == (cls is not StepPPO) and ex.seq_dw == ex.seq_xw == (cls is RecurrentPPO)
         p0 = flat_state_of(state).P.cpu().clone()
         trans = device_recurrent_transition(tr, roll, extra)
         for k in (1, 2):

@@ -368,8 +368,10 @@ class SeqRecurrentExecutor(RecurrentExecutor):
 
 
 class SeqRecurrentGemmDwExecutor(SeqRecurrentExecutor):
-    """... with the GRU's weight gradients as two GEMMs after the backward."""
+    """... with the GRU's input projections and weight gradients as GEMMs
+    before the forward and after the backward."""
     SEQ_DW = False
+    SEQ_XW = False
 
 
 @pytest.mark.parametrize("fused_dw", [True, False])
@@ -381,12 +383,16 @@ def test_recurrent_update_runs_each_direction_of_the_recurrence_in_one_launch(fu
     ex = cls(prog, flat, r.cfg, r.optimizer, r.T, r.N)
     ex.bind(fake_inputs(ex))
     H, I, Bm, T = prog.gru.H, prog.gru.fin, ex.Bm, r.T
-    assert ex.seq and ex.seq_dw == (fused_dw and H == 256 and I == 256)
+    assert ex.seq and ex.seq_dw == ex.seq_xw == (fused_dw and H == 256 and I == 256)
     calls = ex.record()
     names = [n for n, _ in calls]
     steps = r.cfg.update_epochs * r.cfg.num_minibatches
     bwd = "ppo_gru_bwd_seq_dw_f32" if ex.seq_dw else "ppo_gru_bwd_seq_f32"
-    assert names.count("ppo_gru_fwd_seq_f32") == steps and names.count(bwd) == steps
+    fwd = "ppo_gru_fwd_seq_xw_f32" if ex.seq_xw else "ppo_gru_fwd_seq_f32"
+    assert names.count(fwd) == steps and names.count(bwd) == steps
+    # the input projections' GEMM (into XI) only without the in-launch projections
+    xi_gemms = sum(1 for n, a in calls if n == "ppo_gemm_f32" and a[8] == ex.XI.data_ptr())
+    assert xi_gemms == (0 if ex.seq_xw else steps)
     assert names.count("ppo_gru_fwd_step_f32") == 2          # the bootstrap's two-step tail
     assert "ppo_gru_bwd_step_f32" not in names
     # every GEMM whose output is a GRU kernel's gradient partial
@@ -400,6 +406,11 @@ def test_recurrent_update_runs_each_direction_of_the_recurrence_in_one_launch(fu
         if name == "ppo_gru_fwd_seq_f32":
             assert args[3] == Bm * 3 * H and args[10] == Bm and args[-6:-3] == (Bm, H, T)
             assert args[-3] == ex.SEQX.data_ptr() and args[-2] == ex.SEQERR.data_ptr()
+        if name == "ppo_gru_fwd_seq_xw_f32":
+            assert args[7] == Bm and args[20:23] == (Bm, H, T)
+            assert args[23] == ex.SEQX.data_ptr() and args[24] == ex.SEQERR.data_ptr()
+            assert args[26:30] == (e_ptr, lde, Bm * lde, I)
+            assert args[30] == ex.flat.view(prog.gru.wi) and args[31] == 3 * H and args[32] == ex.flat.view(prog.gru.bi)
         if name in ("ppo_gru_bwd_seq_f32", "ppo_gru_bwd_seq_dw_f32"):
             assert args[6] == Bm and args[9] == Bm * H and args[22:25] == (Bm, H, T)
         if name == "ppo_gru_bwd_seq_dw_f32":
