@@ -77,10 +77,13 @@ PPO_EXPORT int ppo_gemm_bf16s_dw_group(void* stream, int count, const void* cons
   }
   g.start[g.count] = total;
   if (total == 0) return PPO_OK;
-  // 32-deep stages in a three-stage ring (two in flight behind the MFMAs,
-  // 96 KB of LDS); the MFMA sequence along k is that of the 64-deep
-  // stages, so the partials are the same bits as tile 2's
-  hipLaunchKernelGGL((gemm_bf16d_group_kernel<256, 256, 2, 4, false, false, 3, KIDX_256, 32>), dim3(total), dim3(512),
+  // 32-deep stages in a four-stage ring (three in flight behind the MFMAs,
+  // 128 KB of LDS with the 16 KB gather cache 144 KB: the large-observation
+  // update's grouped dW 116 -> 108 us, three stages in flight covering more
+  // of the scattered rows' latency; eight 16-deep stages took 119 us); the
+  // MFMA sequence along k is that of the 64-deep stages, so the partials are
+  // the same bits as tile 2's
+  hipLaunchKernelGGL((gemm_bf16d_group_kernel<256, 256, 2, 4, false, false, 4, KIDX_256, 32>), dim3(total), dim3(512),
                      0, ppo::as_stream(stream), g);
   return ppo::check_launch("ppo_gemm_bf16s_dw_group");
 }
