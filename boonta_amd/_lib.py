@@ -77,6 +77,9 @@ SIGNATURES = {
     "ppo_gemm_bf16s": (I, [P, I, I, I, I, P, I64, P, P, I64, P, I64, I, I, I, I, I64, I, P, I, I, P, I64, P, I]),
     "ppo_gemm_bf16s_dw_group": (I, [P, I, P, P, P, P, P, P, P, P, P, P, P, P, P]),
     "ppo_gemm_f32_dw_group": (I, [P, I, P, P, P, P, P, P, P, P, P, P, P, P, P]),
+    "ppo_gemm_f32_dw_final_slots": (I, [I, P, P]),
+    "ppo_gemm_f32_dw_group_final": (I, [P, I, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I,
+                                        I]),
     "ppo_cast_bf16": (I, [P, P, P, I64]),
     "ppo_cast_bf16_2d": (I, [P, P, I64, P, I64, I, I]),
     "ppo_pad_rows_f32": (I, [P, P, I64, P, I64, I, I]),

@@ -17,182 +17,28 @@
 //      block, so no extra launch or grid barrier is needed, and the optax
 //      step counter lives in device memory (count_base + step_offset + 1), so
 //      a captured graph replays with the right bias corrections.
-#include "common.h"
+#include "grad_reduce.h"
 
 #include <algorithm>
 
 namespace {
 
-struct Segment {
-  float* dst;
-  const float* src;
-  int64_t count;
-  int64_t part_stride;
-  int nparts;
-  int flags;  // SEG_ROUND_BF16: the summed gradient is rounded to bf16
-};
+using ppo_gr::Chunk;
+using ppo_gr::Segment;
+using ppo_gr::CHUNK;
+using ppo_gr::FEW_PARTS;
+using ppo_gr::REDUCE_THREADS;
+using ppo_gr::WIDE_CHUNK;
+using ppo_gr::WIDE_PARTS;
 
-constexpr int SEG_ROUND_BF16 = 1;
-
-struct Chunk {
-  int seg;
-  int slot;  // its squared-norm partial's index in sumsq
-  int64_t start;
-};
-
-constexpr int REDUCE_THREADS = 256;
-constexpr int CHUNK = 256;  // elements per block: one float4 per lane of a wave
-
-// One block per chunk of 256 gradient elements.  Each of the 4 waves sums a
-// contiguous quarter of the partials for the same 64 float4, eight partials
-// per step (eight loads in flight per lane, added as a fixed tree; the last
-// step's missing partials read a clamped partial and count as zero), then
-// the quarters are added in wave order: a fixed association, so the result
-// never depends on scheduling.
-//
-// The first nfew chunks (of segments with at most FEW_PARTS partials) are
-// taken one per wave, four per block, with all of a lane's partial loads in
-// flight at once: the same sum (0 + p0 + p1 + ..., in partial order, which is
-// what the quarter split above gives for so few partials) with four times the
-// loads in flight per block and a quarter of the blocks.
-constexpr int FEW_PARTS = 4;
-//
-// The last nwide chunks (of segments with more than WIDE_PARTS partials, such
-// as a fused head's per-tile partials or LayerNorm row blocks) cover
-// WIDE_CHUNK elements each: lane l
-// of wave w sums partial range j = 4 w + l / 16 of sixteen equal ranges for
-// float4 l % 16, in groups of eight added as the same fixed tree, and the
-// sixteen range sums are then added in range order.  A long segment's
-// dependent load rounds per lane drop from nparts / 32 to nparts / 128.
-constexpr int WIDE_PARTS = 64;
-constexpr int WIDE_CHUNK = 64;
-
+// One block per chunk (ppo_gr::reduce_block: the fixed-order sum, the
+// summed values written to the flat gradient, one squared-norm partial per
+// chunk).
 __global__ void __launch_bounds__(REDUCE_THREADS)
 grad_reduce_kernel(const Segment* __restrict__ segs, const Chunk* __restrict__ chunks, int nchunks, int nfew,
                    int nwide, double* __restrict__ sumsq) {
   __shared__ floatx4 part[REDUCE_THREADS / 64][64];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int few_blocks = (nfew + 3) / 4;
-  // the wide chunks' blocks are dispatched first (their partial loops are the
-  // longest), then the few-part blocks, then the others
-  int b = (int)blockIdx.x;
-  if (b < nwide) {
-    const Chunk ch = chunks[nchunks - nwide + b];
-    const Segment sg = segs[ch.seg];
-    const int c = lane & 15, j = 4 * wave + (lane >> 4);
-    const int64_t i = ch.start + 4 * c;
-    const bool live = i < sg.count;
-    const int q0 = (sg.nparts * j) / 16, q1 = (sg.nparts * (j + 1)) / 16;
-    constexpr int U = 8;
-    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (live && q1 > q0) {
-      const float* src = sg.src + i;
-      for (int q = q0; q < q1; q += U) {
-        floatx4 v[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int qq = min(q + u, q1 - 1);
-          v[u] = *reinterpret_cast<const floatx4*>(src + (int64_t)qq * sg.part_stride);
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = q + u < q1 ? v[u] : floatx4{0.f, 0.f, 0.f, 0.f};
-        acc += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-      }
-    }
-    part[j >> 2][16 * (j & 3) + c] = acc;  // range j of float4 c
-    __syncthreads();
-    if (wave == 0) {
-      double sq = 0.0;
-      if (lane < 16 && live) {
-        floatx4 t = part[0][lane];
-#pragma unroll
-        for (int r = 1; r < 16; ++r) t += part[r >> 2][16 * (r & 3) + lane];
-        if (sg.flags & SEG_ROUND_BF16) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) t[e] = ppo::bf16_round(t[e]);
-        }
-        *reinterpret_cast<floatx4*>(sg.dst + i) = t;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sq += (double)t[e] * (double)t[e];
-      }
-      sq = ppo::wave_sum_d(sq);
-      if (lane == 0) sumsq[ch.slot] = sq;
-    }
-    return;
-  }
-  b -= nwide;
-  if (b < few_blocks) {
-    const int ci = 4 * b + wave;
-    if (ci >= nfew) return;  // this path has no barrier
-    const Chunk ch = chunks[ci];
-    const Segment sg = segs[ch.seg];
-    const int64_t i = ch.start + 4 * lane;
-    const bool live = i < sg.count;
-    floatx4 v[FEW_PARTS];
-#pragma unroll
-    for (int q = 0; q < FEW_PARTS; ++q)
-      v[q] = (live && q < sg.nparts) ? *reinterpret_cast<const floatx4*>(sg.src + i + (int64_t)q * sg.part_stride)
-                                     : floatx4{0.f, 0.f, 0.f, 0.f};
-    double sq = 0.0;
-    if (live) {
-      floatx4 t = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int q = 0; q < FEW_PARTS; ++q)
-        if (q < sg.nparts) t += v[q];
-      if (sg.flags & SEG_ROUND_BF16) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) t[e] = ppo::bf16_round(t[e]);
-      }
-      *reinterpret_cast<floatx4*>(sg.dst + i) = t;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sq += (double)t[e] * (double)t[e];
-    }
-    sq = ppo::wave_sum_d(sq);
-    if (lane == 0) sumsq[ch.slot] = sq;
-    return;
-  }
-  const Chunk ch = chunks[nfew + (b - few_blocks)];
-  const Segment sg = segs[ch.seg];
-  const int64_t i = ch.start + 4 * lane;  // first element of this lane's float4
-  const bool live = i < sg.count;
-  const int q0 = (sg.nparts * wave) / 4, q1 = (sg.nparts * (wave + 1)) / 4;
-  constexpr int U = 8;
-  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-  if (live && q1 > q0) {
-    const float* s = sg.src + i;
-    for (int q = q0; q < q1; q += U) {
-      floatx4 v[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int qq = min(q + u, q1 - 1);
-        v[u] = *reinterpret_cast<const floatx4*>(s + (int64_t)qq * sg.part_stride);
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) v[u] = q + u < q1 ? v[u] : floatx4{0.f, 0.f, 0.f, 0.f};
-      acc += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-    }
-  }
-  part[wave][lane] = acc;
-  __syncthreads();
-  if (wave == 0) {
-    double sq = 0.0;
-    if (live) {
-      floatx4 t = part[0][lane];
-#pragma unroll
-      for (int w = 1; w < REDUCE_THREADS / 64; ++w) t += part[w][lane];
-      if (sg.flags & SEG_ROUND_BF16) {
-        // the gradient of a parameter cast to bf16 arrives as a bf16 cotangent
-#pragma unroll
-        for (int e = 0; e < 4; ++e) t[e] = ppo::bf16_round(t[e]);
-      }
-      *reinterpret_cast<floatx4*>(sg.dst + i) = t;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sq += (double)t[e] * (double)t[e];
-    }
-    sq = ppo::wave_sum_d(sq);
-    if (lane == 0) sumsq[ch.slot] = sq;
-  }
+  ppo_gr::reduce_block((int)blockIdx.x, segs, chunks, nchunks, nfew, nwide, sumsq, part);
 }
 
 struct AdamParams {

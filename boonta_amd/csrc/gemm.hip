@@ -387,6 +387,60 @@ PPO_EXPORT int ppo_pad_rows_f32(void* stream, const float* x, int64_t ldx, float
   return ppo::check_launch("ppo_pad_rows_f32");
 }
 
+namespace {
+
+// The checked problems of a weight-gradient group (64 x 64 tiles); on error
+// the library's error is set and the status returned.  kidx: the largest
+// gathered split; all_live: problems with M or N zero are an error instead
+// of skipped.
+int build_dw_group(const char* name, int count, const float* const* A, const int64_t* lda,
+                   const int32_t* const* rows, const float* const* B, const int64_t* ldb, float* const* C,
+                   const int64_t* ldc, const int* M, const int* N, const int* K, const int* splits,
+                   const int64_t* c_split_stride, float* const* bias_grad, int kidx, bool all_live,
+                   ppo_f32::F32Group& g) {
+  using namespace ppo_f32;
+  if (count < 0 || count > F32_GROUP_MAX || (count > 0 && (!A || !lda || !B || !ldb || !C || !ldc || !M || !N ||
+                                                           !K || !splits || !c_split_stride)))
+    return ppo::set_error(PPO_ERR_ARG, "%s: bad argument (count=%d, at most %d)", name, count, F32_GROUP_MAX);
+  g = F32Group{};
+  int64_t total = 0;
+  for (int i = 0; i < count; ++i) {
+    if (M[i] < 0 || N[i] < 0 || K[i] < 0 || splits[i] < 1 || splits[i] > 65535 ||
+        (all_live && (M[i] == 0 || N[i] == 0)))
+      return ppo::set_error(PPO_ERR_ARG, "%s: problem %d: bad shape (M=%d N=%d K=%d splits=%d)", name, i, M[i],
+                            N[i], K[i], splits[i]);
+    if (M[i] == 0 || N[i] == 0) continue;
+    if (!A[i] || !B[i] || !C[i]) return ppo::set_error(PPO_ERR_ARG, "%s: problem %d: null operand", name, i);
+    if (splits[i] > 1 && c_split_stride[i] < (int64_t)M[i] * ldc[i])
+      return ppo::set_error(PPO_ERR_ARG, "%s: problem %d: split stride too small", name, i);
+    if (lda[i] % 4 || M[i] % 4 || lda[i] < M[i] || !aligned16(A[i]) || ldb[i] % 4 || N[i] % 4 || ldb[i] < N[i] ||
+        !aligned16(B[i]) || ldc[i] < N[i])
+      return ppo::set_error(PPO_ERR_ARG, "%s: problem %d: operand rows must be 16-byte aligned "
+                            "with 16-byte vector extents (M=%d N=%d lda=%lld ldb=%lld ldc=%lld)", name, i, M[i], N[i],
+                            (long long)lda[i], (long long)ldb[i], (long long)ldc[i]);
+    GemmParams& p = g.p[g.count];
+    p = GemmParams{};
+    p.A = A[i]; p.lda = lda[i]; p.rows = rows ? rows[i] : nullptr; p.B = B[i]; p.ldb = ldb[i];
+    p.C = C[i]; p.ldc = ldc[i]; p.c_split_stride = c_split_stride[i]; p.M = M[i]; p.N = N[i]; p.K = K[i];
+    p.k_per_split = ((ppo::ceil_div(K[i] > 0 ? K[i] : 1, splits[i]) + F32D_BK - 1) / F32D_BK) * F32D_BK;
+    p.epi = EPI_STORE; p.act = 0; p.bias_grad = bias_grad ? bias_grad[i] : nullptr;
+    p.splits = splits[i]; p.towers = 1;
+    if (p.rows && p.k_per_split > kidx)
+      return ppo::set_error(PPO_ERR_ARG, "%s: problem %d: a gathered split holds %d rows (at most %d)", name, i,
+                            p.k_per_split, kidx);
+    g.gx[g.count] = ppo::ceil_div(N[i], 64);
+    g.gy[g.count] = ppo::ceil_div(M[i], 64);
+    g.start[g.count] = (int)total;
+    total += (int64_t)g.gx[g.count] * g.gy[g.count] * splits[i];
+    if (total > (1 << 30)) return ppo::set_error(PPO_ERR_ARG, "%s: too many tiles", name);
+    ++g.count;
+  }
+  g.start[g.count] = (int)total;
+  return PPO_OK;
+}
+
+}  // namespace
+
 // Weight gradients of several fp32 Dense layers in one launch (64 x 64
 // copy-fed tiles): problem i is what ppo_gemm_f32(a_layout = 1, b_layout = 0,
 // epi = store, tile = 3) computes from the same arguments, with the same bits.
@@ -398,43 +452,90 @@ PPO_EXPORT int ppo_gemm_f32_dw_group(void* stream, int count, const float* const
                                      float* const* C, const int64_t* ldc, const int* M, const int* N, const int* K,
                                      const int* splits, const int64_t* c_split_stride, float* const* bias_grad) {
   using namespace ppo_f32;
-  if (count < 0 || count > F32_GROUP_MAX || (count > 0 && (!A || !lda || !B || !ldb || !C || !ldc || !M || !N ||
-                                                           !K || !splits || !c_split_stride)))
-    return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32_dw_group: bad argument (count=%d, at most %d)", count,
-                          F32_GROUP_MAX);
-  F32Group g = {};
-  int64_t total = 0;
-  for (int i = 0; i < count; ++i) {
-    if (M[i] < 0 || N[i] < 0 || K[i] < 0 || splits[i] < 1 || splits[i] > 65535)
-      return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32_dw_group: problem %d: bad shape (M=%d N=%d K=%d splits=%d)", i,
-                            M[i], N[i], K[i], splits[i]);
-    if (M[i] == 0 || N[i] == 0) continue;
-    if (!A[i] || !B[i] || !C[i]) return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32_dw_group: problem %d: null operand", i);
-    if (splits[i] > 1 && c_split_stride[i] < (int64_t)M[i] * ldc[i])
-      return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32_dw_group: problem %d: split stride too small", i);
-    if (lda[i] % 4 || M[i] % 4 || lda[i] < M[i] || !aligned16(A[i]) || ldb[i] % 4 || N[i] % 4 || ldb[i] < N[i] ||
-        !aligned16(B[i]) || ldc[i] < N[i])
-      return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32_dw_group: problem %d: operand rows must be 16-byte aligned "
-                            "with 16-byte vector extents (M=%d N=%d lda=%lld ldb=%lld ldc=%lld)", i, M[i], N[i],
-                            (long long)lda[i], (long long)ldb[i], (long long)ldc[i]);
-    GemmParams& p = g.p[g.count];
-    p = GemmParams{};
-    p.A = A[i]; p.lda = lda[i]; p.rows = rows ? rows[i] : nullptr; p.B = B[i]; p.ldb = ldb[i];
-    p.C = C[i]; p.ldc = ldc[i]; p.c_split_stride = c_split_stride[i]; p.M = M[i]; p.N = N[i]; p.K = K[i];
-    p.k_per_split = ((ppo::ceil_div(K[i] > 0 ? K[i] : 1, splits[i]) + F32D_BK - 1) / F32D_BK) * F32D_BK;
-    p.epi = EPI_STORE; p.act = 0; p.bias_grad = bias_grad ? bias_grad[i] : nullptr;
-    p.splits = splits[i]; p.towers = 1;
-    if (p.rows && p.k_per_split > F32D_KIDX_MAX)
-      return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32_dw_group: problem %d: a gathered split holds %d rows "
-                            "(at most %d)", i, p.k_per_split, F32D_KIDX_MAX);
-    g.gx[g.count] = ppo::ceil_div(N[i], 64);
-    g.gy[g.count] = ppo::ceil_div(M[i], 64);
-    g.start[g.count] = (int)total;
-    total += (int64_t)g.gx[g.count] * g.gy[g.count] * splits[i];
-    if (total > (1 << 30)) return ppo::set_error(PPO_ERR_ARG, "ppo_gemm_f32_dw_group: too many tiles");
-    ++g.count;
-  }
-  g.start[g.count] = (int)total;
-  if (total == 0) return PPO_OK;
+  F32Group g;
+  const int rc = build_dw_group("ppo_gemm_f32_dw_group", count, A, lda, rows, B, ldb, C, ldc, M, N, K, splits,
+                                c_split_stride, bias_grad, F32D_KIDX_MAX, false, g);
+  if (rc != PPO_OK) return rc;
+  if (g.start[g.count] == 0) return PPO_OK;
   return launch_dw_group(ppo::as_stream(stream), g);
+}
+
+// Output tiles (64 x 64) of a weight-gradient group: the arrival counters and
+// squared-norm slots ppo_gemm_f32_dw_group_final uses, problem after problem
+// (-1 on a bad shape).
+PPO_EXPORT int ppo_gemm_f32_dw_final_slots(int count, const int* M, const int* N) {
+  if (count < 0 || count > ppo_f32::F32_GROUP_MAX || (count > 0 && (!M || !N))) return -1;
+  int64_t n = 0;
+  for (int i = 0; i < count; ++i) {
+    if (M[i] <= 0 || N[i] <= 0) return -1;
+    n += (int64_t)ppo::ceil_div(M[i], 64) * ppo::ceil_div(N[i], 64);
+  }
+  return n > (1 << 30) ? -1 : (int)n;
+}
+
+// ppo_gemm_f32_dw_group with the gradient assembly of its problems done in
+// the same launch: problem i's split partials (C[i], bias_grad[i]) are still
+// written, and the last split of each 64 x 64 tile to finish sums them in
+// ppo_grad_reduce's fixed order into G[i] (rows < g_rows[i], pitch ldg[i])
+// and its bias gradient Gb[i] (or nothing when null), leaving the tile's
+// squared-norm partial at sumsq[slot] (slots and counters numbered as
+// ppo_gemm_f32_dw_final_slots counts them).  The segments in segs / chunks
+// (ppo_grad_reduce's tables, their chunk slots after the tiles') are reduced
+// by workgroups of the same launch.  counters: one zeroed unsigned per tile,
+// left zeroed.  The gradients are the same bits as ppo_gemm_f32_dw_group +
+// ppo_grad_reduce over the same segments (the norm partials are grouped by
+// tile instead of by chunk).  Splits per problem: 1, 2, 3,
+// 4, 6, 8, 12 or 16; gathered splits of at most F32D_FINAL_KIDX rows.
+PPO_EXPORT int ppo_gemm_f32_dw_group_final(void* stream, int count, const float* const* A, const int64_t* lda,
+                                           const int32_t* const* rows, const float* const* B, const int64_t* ldb,
+                                           float* const* C, const int64_t* ldc, const int* M, const int* N,
+                                           const int* K, const int* splits, const int64_t* c_split_stride,
+                                           float* const* bias_grad, float* const* G, const int64_t* ldg,
+                                           const int* g_rows, float* const* Gb, unsigned* counters, double* sumsq,
+                                           const void* segs, const void* chunks, int nchunks, int nfew, int nwide) {
+  using namespace ppo_f32;
+  const char* name = "ppo_gemm_f32_dw_group_final";
+  F32Group g;
+  const int rc = build_dw_group(name, count, A, lda, rows, B, ldb, C, ldc, M, N, K, splits, c_split_stride,
+                                bias_grad, F32D_FINAL_KIDX, true, g);
+  if (rc != PPO_OK) return rc;
+  if (count > 0 && (!G || !ldg || !g_rows || !counters || !sumsq))
+    return ppo::set_error(PPO_ERR_ARG, "%s: null gradient, counter or norm buffer", name);
+  if (nchunks < 0 || nfew < 0 || nwide < 0 || nfew + nwide > nchunks || (nchunks > 0 && (!segs || !chunks)))
+    return ppo::set_error(PPO_ERR_ARG, "%s: bad segment tables (nchunks=%d nfew=%d nwide=%d)", name, nchunks, nfew,
+                          nwide);
+  F32Final f = {};
+  int slot = 0;
+  for (int i = 0; i < count; ++i) {
+    const GemmParams& p = g.p[i];
+    if (!final_parts_supported(p.splits))
+      return ppo::set_error(PPO_ERR_ARG, "%s: problem %d: %d splits (supported: 1, 2, 3, 4, 6, 8, 12, 16)", name, i,
+                            p.splits);
+    if (!G[i] || !aligned16(G[i]) || ldg[i] % 4 || ldg[i] < p.N || g_rows[i] < 1 || g_rows[i] > p.M)
+      return ppo::set_error(PPO_ERR_ARG, "%s: problem %d: bad gradient (g_rows=%d of M=%d, ldg=%lld)", name, i,
+                            g_rows[i], p.M, (long long)ldg[i]);
+    if (!aligned16(p.C) || p.ldc % 4 || p.c_split_stride % 4 ||
+        4 * ((int64_t)p.splits * p.c_split_stride + (int64_t)p.M * p.ldc) > INT32_MAX)
+      return ppo::set_error(PPO_ERR_ARG, "%s: problem %d: partials must be 16-byte aligned and under 2 GB", name, i);
+    const bool with_bias = Gb && Gb[i] && p.bias_grad;
+    if (with_bias && (!aligned16(Gb[i]) || !aligned16(p.bias_grad)))
+      return ppo::set_error(PPO_ERR_ARG, "%s: problem %d: bias gradients must be 16-byte aligned", name, i);
+    f.G[i] = G[i];
+    f.ldg[i] = ldg[i];
+    f.g_rows[i] = g_rows[i];
+    f.Gb[i] = with_bias ? Gb[i] : nullptr;
+    f.slot0[i] = slot;
+    slot += g.gx[i] * g.gy[i];
+  }
+  f.counters = counters;
+  f.sumsq = sumsq;
+  f.segs = segs;
+  f.chunks = chunks;
+  f.nchunks = nchunks;
+  f.nfew = nfew;
+  f.nwide = nwide;
+  f.rblocks = nchunks > 0 ? (nfew + 3) / 4 + (nchunks - nfew) : 0;
+  f.rpad = (f.rblocks + 7) / 8 * 8;
+  if (g.start[g.count] + f.rpad == 0) return PPO_OK;
+  return launch_dw_group_final(ppo::as_stream(stream), g, f);
 }

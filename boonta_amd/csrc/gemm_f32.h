@@ -67,7 +67,18 @@ __device__ __forceinline__ GemmParams tower_params(const GemmParams& p, int t) {
 // PRE: the epilogue's per-lane inputs were loaded earlier by the caller into
 // auxv: EPI_DACT's aux values of this lane's outputs (block bi, bj at
 // [16 (bi NB + bj) + r]), EPI_BIAS_ACT's bias of block column bj at [bj].
-template <int MB, int NB, int EPI, int ACT, bool PRE>
+// WT: the outputs are stored device-coherent (write-through past this XCD's
+// L2), for a reader in another workgroup of the same launch.
+template <bool WT>
+__device__ __forceinline__ void store_out(float* q, float v) {
+  if constexpr (WT)
+    __hip_atomic_store(reinterpret_cast<uint32_t*>(q), __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *q = v;
+}
+
+template <int MB, int NB, int EPI, int ACT, bool PRE, bool WT = false>
 __device__ __forceinline__ void epilogue_f32_t(const GemmParams& p, floatx16 (&acc)[MB][NB], const float (&bsum)[NB],
                                                bool do_bsum, int wm0, int wn0, int split, int lane,
                                                const float (&auxv)[MB * NB * 16]) {
@@ -95,7 +106,7 @@ __device__ __forceinline__ void epilogue_f32_t(const GemmParams& p, floatx16 (&a
         } else if (EPI == EPI_DACT) {
           v *= ppo::act_grad(ACT, PRE ? auxv[16 * (bi * NB + bj) + r] : p.aux[(int64_t)gm * p.ldaux + gn]);
         }
-        C[o] = v;
+        store_out<WT>(C + o, v);
       }
     }
   }
@@ -104,7 +115,7 @@ __device__ __forceinline__ void epilogue_f32_t(const GemmParams& p, floatx16 (&a
     for (int bj = 0; bj < NB; ++bj) {
       const float t = ppo::add_xor32(bsum[bj]);
       const int gn = wn0 + bj * 32 + l32;
-      if (h == 0 && gn < p.N) p.bias_grad[(int64_t)split * p.N + gn] = t;
+      if (h == 0 && gn < p.N) store_out<WT>(p.bias_grad + (int64_t)split * p.N + gn, t);
     }
   }
 }
@@ -132,6 +143,25 @@ __device__ __forceinline__ void epilogue_f32(const GemmParams& p, floatx16 (&acc
 #undef PPO_EPI_ACTS
 }
 
+// A weight-gradient group that finishes its own split-K sums
+// (ppo_gemm_f32_dw_group_final): the last split of each output tile to
+// arrive (a per-tile arrival counter) sums the tile's partials in the
+// gradient-assembly launch's fixed order (ppo_gr::fixed_sum) into the final
+// gradient and writes the tile's squared-norm partial; workgroups placed
+// before the tiles run the gradient-assembly blocks of the other segments.
+struct F32Final {
+  float* G[F32_GROUP_MAX];    // problem i's final gradient, [g_rows][ldg]
+  int64_t ldg[F32_GROUP_MAX];
+  int g_rows[F32_GROUP_MAX];  // rows of the gradient (<= M: a zero-padded input's extra rows are dropped)
+  float* Gb[F32_GROUP_MAX];   // final bias gradient [N] (problems with bias partials)
+  int slot0[F32_GROUP_MAX];   // problem i's first tile: its counter and sumsq index
+  unsigned* counters;         // one per tile, zero between launches
+  double* sumsq;
+  const void* segs;           // the other segments (ppo_gr tables), reduced by rblocks workgroups
+  const void* chunks;
+  int nchunks, nfew, nwide, rblocks, rpad;  // rpad: rblocks rounded up to a multiple of 8
+};
+
 // The copy-fed pipeline (gemm_f32d.hip): 16-byte rows along every operand's
 // contiguous axis, stage depth F32D_BK; false when the shape needs the
 // register-staged one (a gathered k-outer A with more reduction rows per
@@ -141,5 +171,12 @@ constexpr int F32D_KIDX_MAX = 2048;
 int launch_dma(hipStream_t st, const GemmParams& p, int splits, int tile, int a_layout, int b_layout);
 // A weight-gradient group (A and B k-outer, 64 x 64 copy-fed tiles).
 int launch_dw_group(hipStream_t st, const F32Group& g);
+// The same with the split-K sums finished in the launch (64 x 64 tiles,
+// gathered splits of at most F32D_FINAL_KIDX rows, at most F32D_FINAL_PARTS
+// splits of one of the supported counts).
+constexpr int F32D_FINAL_KIDX = 512;
+constexpr int F32D_FINAL_PARTS = 16;
+bool final_parts_supported(int splits);
+int launch_dw_group_final(hipStream_t st, const F32Group& g, const F32Final& f);
 
 }  // namespace ppo_f32

@@ -25,6 +25,7 @@
 // column (only outputs that are not stored see them); a final stage cut short
 // by K goes through registers with the elements past K zeroed.
 #include "gemm_f32.h"
+#include "grad_reduce.h"
 
 namespace ppo_f32 {
 namespace {
@@ -138,7 +139,10 @@ __device__ __forceinline__ floatx4 operand(const float* lds, int rbase, int g, i
 
 // One BM x BN output tile (tile row tm, column tn) of split `split` of the
 // GEMM p.
-template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF>
+// KIDX: the LDS capacity for a gathered k-outer A's split indices.
+// WT: a weight-gradient store whose partials another workgroup of the launch
+// sums (EPI_STORE only; device-coherent stores).
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NBUF, int KIDX = F32D_KIDX_MAX, bool WT = false>
 __device__ __forceinline__ void gemm_f32d_tile(const GemmParams& p, int tm, int tn, int split) {
   constexpr int NW = WM * WN;
   constexpr int MB = BM / WM / 32, NB = BN / WN / 32;  // 32 x 32 blocks per wave
@@ -147,7 +151,7 @@ __device__ __forceinline__ void gemm_f32d_tile(const GemmParams& p, int tm, int 
   using OpB = Operand<BN, B_K, NW>;
   __shared__ __attribute__((aligned(1024))) float sA[NBUF][OpA::ELEMS];
   __shared__ __attribute__((aligned(1024))) float sB[NBUF][OpB::ELEMS];
-  __shared__ int32_t sIdx[A_K ? 1 : F32D_KIDX_MAX];  // gather indices of the split (k-outer A)
+  __shared__ int32_t sIdx[A_K ? 1 : KIDX];  // gather indices of the split (k-outer A)
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -268,7 +272,10 @@ __device__ __forceinline__ void gemm_f32d_tile(const GemmParams& p, int tm, int 
     }
   }
 
-  if (pre_aux)
+  if constexpr (WT)
+    epilogue_f32_t<MB, NB, EPI_STORE, ACT_NONE, false, true>(p, acc, bsum, do_bsum, m0 + wm * (BM / WM),
+                                                             n0 + wn * (BN / WN), split, lane, auxv);
+  else if (pre_aux)
     epilogue_f32<MB, NB, true>(p, acc, bsum, do_bsum, m0 + wm * (BM / WM), n0 + wn * (BN / WN), split, lane, auxv);
   else
     epilogue_f32<MB, NB>(p, acc, bsum, do_bsum, m0 + wm * (BM / WM), n0 + wn * (BN / WN), split, lane, auxv);
@@ -300,6 +307,124 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_group_kernel(F32Group 
                                                  local / (g.gx[i] * g.gy[i]));
 }
 
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+constexpr int SC1 = 16;  // cache policy of a device-coherent buffer access
+
+// The tile's split-K sum, finished by the last of its splits to arrive.
+// Thread t owns float4 t + 256 i (i < 4) of the 64 x 64 tile (row (t + 256 i)
+// / 16, columns 4 ((t + 256 i) % 16) ...): P of them at a time with all S
+// partial loads in flight (device-coherent loads: the partials of other
+// XCDs' workgroups), summed by ppo_gr::fixed_sum.
+template <int S>
+__device__ __forceinline__ void finish_tile(const GemmParams& p, const F32Final& f, int prob, int tm, int tn,
+                                            int slot, double* s_w) {
+  constexpr int BM = 64, BN = 64, POS = BM * BN / 4 / 256;
+  constexpr int P = S <= 4 ? 4 : S <= 8 ? 2 : 1;
+  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(p.C, (short)0, 0x7fffffff, 0x00020000);
+  const int t = threadIdx.x;
+  const int rows = f.g_rows[prob];
+  double sq = 0.0;
+#pragma unroll
+  for (int i0 = 0; i0 < POS; i0 += P) {
+    floatx4 v[P][S];
+    bool live[P];
+    int64_t dst[P];
+#pragma unroll
+    for (int u = 0; u < P; ++u) {
+      const int e = t + 256 * (i0 + u);
+      const int gm = tm * BM + e / (BN / 4), gn = tn * BN + 4 * (e % (BN / 4));
+      live[u] = gm < rows && gn < p.N;
+      dst[u] = (int64_t)gm * f.ldg[prob] + gn;
+      const int off = live[u] ? (int)(4 * ((int64_t)gm * p.ldc + gn)) : 0;
+#pragma unroll
+      for (int q = 0; q < S; ++q)
+        v[u][q] = __builtin_bit_cast(
+            floatx4, __builtin_amdgcn_raw_buffer_load_b128(rc, off + (int)(4 * q * p.c_split_stride), 0, SC1));
+    }
+#pragma unroll
+    for (int u = 0; u < P; ++u) {
+      if (!live[u]) continue;
+      const floatx4 g = ppo_gr::fixed_sum<S>(v[u]);
+      *reinterpret_cast<floatx4*>(f.G[prob] + dst[u]) = g;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sq += (double)g[e] * (double)g[e];
+    }
+  }
+  // the bias gradient's 64 columns with the first tile row
+  if (tm == 0 && p.bias_grad && f.Gb[prob] && t < BN / 4) {
+    const int gn = tn * BN + 4 * t;
+    if (gn < p.N) {
+      const __amdgpu_buffer_rsrc_t rb =
+          __builtin_amdgcn_make_buffer_rsrc(p.bias_grad, (short)0, 0x7fffffff, 0x00020000);
+      floatx4 v[S];
+#pragma unroll
+      for (int q = 0; q < S; ++q)
+        v[q] = __builtin_bit_cast(floatx4,
+                                  __builtin_amdgcn_raw_buffer_load_b128(rb, (int)(4 * ((int64_t)q * p.N + gn)), 0, SC1));
+      const floatx4 g = ppo_gr::fixed_sum<S>(v);
+      *reinterpret_cast<floatx4*>(f.Gb[prob] + gn) = g;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sq += (double)g[e] * (double)g[e];
+    }
+  }
+  // the tile's squared-norm partial: wave sums, then the waves in order
+  sq = ppo::wave_sum_d(sq);
+  if ((t & 63) == 0) s_w[t >> 6] = sq;
+  __syncthreads();
+  if (t == 0) f.sumsq[slot] = (s_w[0] + s_w[1]) + (s_w[2] + s_w[3]);
+}
+
+// The split-K counts the finishing sum is compiled for.
+#define PPO_F32_FINAL_PARTS(X) X(1) X(2) X(3) X(4) X(6) X(8) X(12) X(16)
+
+template <int BM, int BN, int WM, int WN, int NBUF, int KIDX>
+__global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_group_final_kernel(F32Group g, F32Final f) {
+  static_assert(BM == 64 && BN == 64 && WM * WN == 4, "the finishing sum assumes 64 x 64 tiles of 4 waves");
+  __shared__ floatx4 s_part[4][64];
+  __shared__ double s_w[4];
+  __shared__ int s_last;
+  if ((int)blockIdx.x < f.rpad) {
+    // the other segments, whose partials are complete before this launch
+    if ((int)blockIdx.x < f.rblocks)
+      ppo_gr::reduce_block((int)blockIdx.x, static_cast<const ppo_gr::Segment*>(f.segs),
+                           static_cast<const ppo_gr::Chunk*>(f.chunks), f.nchunks, f.nfew, f.nwide, f.sumsq, s_part);
+    return;
+  }
+  // tiles as in gemm_f32d_group_kernel (rpad is a multiple of 8, so w & 7
+  // is still the XCD the workgroup runs on)
+  const int total = gridDim.x - f.rpad;
+  const int w = blockIdx.x - f.rpad;
+  const int x = w & 7, j = w >> 3;
+  const int q = total >> 3, r = total & 7;
+  const int t = x * q + (x < r ? x : r) + j;
+  int i = 0;
+  while (i + 1 < g.count && t >= g.start[i + 1]) ++i;
+  const GemmParams& p = g.p[i];
+  const int local = t - g.start[i];
+  const int tm = (local / g.gx[i]) % g.gy[i], tn = local % g.gx[i];
+  gemm_f32d_tile<BM, BN, WM, WN, false, false, NBUF, KIDX, true>(p, tm, tn, local / (g.gx[i] * g.gy[i]));
+  // every wave's partial stores complete, then one arrival for the tile
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  const int tile = tm * g.gx[i] + tn;
+  const int slot = f.slot0[i] + tile;
+  if (threadIdx.x == 0) {
+    const unsigned seen = __hip_atomic_fetch_add(f.counters + slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = seen + 1 == (unsigned)p.splits;
+    if (last) __hip_atomic_store(f.counters + slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  switch (p.splits) {
+#define PPO_F32_FINAL_CASE(S) \
+  case S: finish_tile<S>(p, f, i, tm, tn, slot, s_w); break;
+    PPO_F32_FINAL_PARTS(PPO_F32_FINAL_CASE)
+#undef PPO_F32_FINAL_CASE
+    default: break;  // rejected by the host
+  }
+}
+
 template <int BM, int BN, int WM, int WN, bool A_K, bool B_K>
 int launch(hipStream_t st, const GemmParams& p, int splits) {
   constexpr int NBUF = WM * WN == 4 ? 2 : 3;
@@ -327,6 +452,24 @@ int launch_dw_group(hipStream_t st, const F32Group& g) {
   const int total = g.start[g.count];
   hipLaunchKernelGGL((gemm_f32d_group_kernel<64, 64, 2, 2, false, false, 2>), dim3(total), dim3(256), 0, st, g);
   return ppo::check_launch("ppo_gemm_f32_dw_group");
+}
+
+bool final_parts_supported(int splits) {
+  switch (splits) {
+#define PPO_F32_FINAL_CASE(S) \
+  case S:
+    PPO_F32_FINAL_PARTS(PPO_F32_FINAL_CASE)
+#undef PPO_F32_FINAL_CASE
+    return true;
+    default: return false;
+  }
+}
+
+int launch_dw_group_final(hipStream_t st, const F32Group& g, const F32Final& f) {
+  const int total = g.start[g.count] + f.rpad;
+  hipLaunchKernelGGL((gemm_f32d_group_final_kernel<64, 64, 2, 2, 2, F32D_FINAL_KIDX>), dim3(total), dim3(256), 0, st,
+                     g, f);
+  return ppo::check_launch("ppo_gemm_f32_dw_group_final");
 }
 
 int launch_dma(hipStream_t st, const GemmParams& p, int splits, int tile, int a_layout, int b_layout) {

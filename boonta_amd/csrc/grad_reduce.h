@@ -1,0 +1,217 @@
+// The fixed-order sum of gradient partials shared by the gradient-assembly
+// launch (adam.hip: ppo_grad_reduce) and the weight-gradient launch that
+// finishes its own split-K sums (gemm_f32d.hip: ppo_gemm_f32_dw_group_final).
+//
+// A gradient leaf arrives as `nparts` partial buffers (split-K GEMM slices,
+// per-block LayerNorm / head partials).  Its sum is always formed in the
+// same association, whichever launch forms it:
+//   nparts <= FEW_PARTS:       ((0 + p0) + p1) + ...          (partial order)
+//   FEW_PARTS < nparts <= WIDE_PARTS: four quarters [n w / 4, n (w + 1) / 4),
+//     each 0 + tree8(p_q0..q0+7) + tree8(next 8) + ... (tree8 =
+//     ((a + b) + (c + d)) + ((e + f) + (g + h)), missing entries 0), then
+//     ((quarter0 + quarter1) + quarter2) + quarter3
+//   nparts > WIDE_PARTS:       sixteen ranges [n j / 16, n (j + 1) / 16) the
+//     same way, then added in range order
+// so a gradient is the same bits from either launch.
+#pragma once
+#include "common.h"
+
+namespace ppo_gr {
+
+struct Segment {
+  float* dst;
+  const float* src;
+  int64_t count;
+  int64_t part_stride;
+  int nparts;
+  int flags;  // SEG_ROUND_BF16: the summed gradient is rounded to bf16
+};
+
+constexpr int SEG_ROUND_BF16 = 1;
+
+struct Chunk {
+  int seg;
+  int slot;  // its squared-norm partial's index in sumsq
+  int64_t start;
+};
+
+constexpr int REDUCE_THREADS = 256;
+constexpr int CHUNK = 256;  // elements per block: one float4 per lane of a wave
+constexpr int FEW_PARTS = 4;
+constexpr int WIDE_PARTS = 64;
+constexpr int WIDE_CHUNK = 64;
+
+__device__ __forceinline__ floatx4 tree8(const floatx4 (&v)[8]) {
+  return ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+}
+
+// One block of the gradient-assembly launch (block b of its dispatch order:
+// the wide chunks' blocks first, then the few-part blocks, four chunks per
+// block, then the others).  part: 4 x 64 float4 of LDS.
+//
+// Each of the 4 waves sums a contiguous quarter of the partials for the same
+// 64 float4, eight partials per step (eight loads in flight per lane; the
+// last step's missing partials read a clamped partial and count as zero),
+// then the quarters are added in wave order.  Few-part chunks are taken one
+// per wave with all of a lane's partial loads in flight at once.  Wide
+// chunks cover WIDE_CHUNK elements: lane l of wave w sums range
+// j = 4 w + l / 16 for float4 l % 16, and the sixteen range sums are added
+// in range order.
+__device__ __forceinline__ void reduce_block(int b, const Segment* __restrict__ segs,
+                                             const Chunk* __restrict__ chunks, int nchunks, int nfew, int nwide,
+                                             double* __restrict__ sumsq, floatx4 (*part)[64]) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int few_blocks = (nfew + 3) / 4;
+  if (b < nwide) {
+    const Chunk ch = chunks[nchunks - nwide + b];
+    const Segment sg = segs[ch.seg];
+    const int c = lane & 15, j = 4 * wave + (lane >> 4);
+    const int64_t i = ch.start + 4 * c;
+    const bool live = i < sg.count;
+    const int q0 = (sg.nparts * j) / 16, q1 = (sg.nparts * (j + 1)) / 16;
+    constexpr int U = 8;
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (live && q1 > q0) {
+      const float* src = sg.src + i;
+      for (int q = q0; q < q1; q += U) {
+        floatx4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int qq = min(q + u, q1 - 1);
+          v[u] = *reinterpret_cast<const floatx4*>(src + (int64_t)qq * sg.part_stride);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = q + u < q1 ? v[u] : floatx4{0.f, 0.f, 0.f, 0.f};
+        acc += tree8(v);
+      }
+    }
+    part[j >> 2][16 * (j & 3) + c] = acc;  // range j of float4 c
+    __syncthreads();
+    if (wave == 0) {
+      double sq = 0.0;
+      if (lane < 16 && live) {
+        floatx4 t = part[0][lane];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) t += part[r >> 2][16 * (r & 3) + lane];
+        if (sg.flags & SEG_ROUND_BF16) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) t[e] = ppo::bf16_round(t[e]);
+        }
+        *reinterpret_cast<floatx4*>(sg.dst + i) = t;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sq += (double)t[e] * (double)t[e];
+      }
+      sq = ppo::wave_sum_d(sq);
+      if (lane == 0) sumsq[ch.slot] = sq;
+    }
+    return;
+  }
+  b -= nwide;
+  if (b < few_blocks) {
+    const int ci = 4 * b + wave;
+    if (ci >= nfew) return;  // this path has no barrier
+    const Chunk ch = chunks[ci];
+    const Segment sg = segs[ch.seg];
+    const int64_t i = ch.start + 4 * lane;
+    const bool live = i < sg.count;
+    floatx4 v[FEW_PARTS];
+#pragma unroll
+    for (int q = 0; q < FEW_PARTS; ++q)
+      v[q] = (live && q < sg.nparts) ? *reinterpret_cast<const floatx4*>(sg.src + i + (int64_t)q * sg.part_stride)
+                                     : floatx4{0.f, 0.f, 0.f, 0.f};
+    double sq = 0.0;
+    if (live) {
+      floatx4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < FEW_PARTS; ++q)
+        if (q < sg.nparts) t += v[q];
+      if (sg.flags & SEG_ROUND_BF16) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] = ppo::bf16_round(t[e]);
+      }
+      *reinterpret_cast<floatx4*>(sg.dst + i) = t;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sq += (double)t[e] * (double)t[e];
+    }
+    sq = ppo::wave_sum_d(sq);
+    if (lane == 0) sumsq[ch.slot] = sq;
+    return;
+  }
+  const Chunk ch = chunks[nfew + (b - few_blocks)];
+  const Segment sg = segs[ch.seg];
+  const int64_t i = ch.start + 4 * lane;  // first element of this lane's float4
+  const bool live = i < sg.count;
+  const int q0 = (sg.nparts * wave) / 4, q1 = (sg.nparts * (wave + 1)) / 4;
+  constexpr int U = 8;
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (live && q1 > q0) {
+    const float* s = sg.src + i;
+    for (int q = q0; q < q1; q += U) {
+      floatx4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int qq = min(q + u, q1 - 1);
+        v[u] = *reinterpret_cast<const floatx4*>(s + (int64_t)qq * sg.part_stride);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = q + u < q1 ? v[u] : floatx4{0.f, 0.f, 0.f, 0.f};
+      acc += tree8(v);
+    }
+  }
+  part[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    double sq = 0.0;
+    if (live) {
+      floatx4 t = part[0][lane];
+#pragma unroll
+      for (int w = 1; w < REDUCE_THREADS / 64; ++w) t += part[w][lane];
+      if (sg.flags & SEG_ROUND_BF16) {
+        // the gradient of a parameter cast to bf16 arrives as a bf16 cotangent
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] = ppo::bf16_round(t[e]);
+      }
+      *reinterpret_cast<floatx4*>(sg.dst + i) = t;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sq += (double)t[e] * (double)t[e];
+    }
+    sq = ppo::wave_sum_d(sq);
+    if (lane == 0) sumsq[ch.slot] = sq;
+  }
+}
+
+// The sum of S partials v[0..S) (compile-time S, at most WIDE_PARTS) in the
+// association above; the reduce forms the same value for an S-part segment.
+template <int S>
+__device__ __forceinline__ floatx4 fixed_sum(const floatx4 (&v)[S]) {
+  static_assert(S >= 1 && S <= WIDE_PARTS, "partial count out of range");
+  const floatx4 z = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (S <= FEW_PARTS) {
+    floatx4 t = z;
+#pragma unroll
+    for (int q = 0; q < S; ++q) t += v[q];
+    return t;
+  } else {
+    floatx4 quarter[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int q0 = (S * w) / 4, q1 = (S * (w + 1)) / 4;
+      floatx4 acc = z;
+#pragma unroll
+      for (int q = q0; q < q1; q += 8) {
+        floatx4 g[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) g[u] = q + u < q1 ? v[q + u] : z;
+        acc += tree8(g);
+      }
+      quarter[w] = acc;
+    }
+    floatx4 t = quarter[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) t += quarter[w];
+    return t;
+  }
+}
+
+}  // namespace ppo_gr

@@ -912,6 +912,23 @@ class MLPExecutor(ForwardChain):
     # (off: one launch for the first layers, one for the rest)
     PAIR_DW_GROUP = True
 
+    # the paired towers' weight gradients finish their split-K sums in their
+    # grouped launch (no gradient-reduce launch for them); the split counts
+    # that launch supports
+    DW_FINAL = True
+    FINAL_SPLITS = (1, 2, 3, 4, 6, 8, 12, 16)
+
+    def _pair_dw_shapes(self):
+        """(M, N, splits) of every problem of the paired towers' grouped
+        weight-gradient launch, in its order (layer-major, actor then
+        critic), or None when the towers do not take that launch."""
+        A, C = self.actor, self.critic
+        if not self.PAIR_DW_GROUP or not self.chain_ln or 2 * len(A) > 8:
+            return None
+        fin0 = self.obs_pad if self.obs_pad else A[0].spec.dense.fin
+        return [(fin0 if i == 0 else lb.spec.dense.fin, lb.spec.ld, lb.splits)
+                for i in range(len(A)) for lb in (A[i], C[i])]
+
     def _pair_dw_group(self, x0, ldx0):
         """Host argument arrays of ppo_gemm_f32_dw_group over every weight
         gradient of the paired towers (layer-major, actor then critic; the
@@ -951,6 +968,20 @@ class MLPExecutor(ForwardChain):
         })
         order = ("A", "lda", "rows", "B", "ldb", "C", "ldc", "M", "N", "K", "splits", "stride", "bias_grad")
         g["args"] = [ctypes.addressof(g[k]) for k in order]
+        fin = self.dw_final
+        if fin is not None:
+            # the final gradients: problem order as above
+            G = self.flat.G.data_ptr()
+            lbs = [lb for i in range(len(A)) for lb in (A[i], C[i])]
+            g.update({
+                "G": vp([G + 4 * lb.spec.dense.w.offset for lb in lbs]),
+                "ldg": i64([lb.spec.dense.w.ld for lb in lbs]),
+                "g_rows": i32([lb.spec.dense.fin for lb in lbs]),
+                "Gb": vp([G + 4 * lb.spec.dense.b.offset if lb.spec.dense.b is not None else None for lb in lbs]),
+            })
+            g["final_args"] = g["args"] + [ctypes.addressof(g[k]) for k in ("G", "ldg", "g_rows", "Gb")] + [
+                _p(fin["CNT"]), _p(fin["SUMSQ"]), _p(fin["SEGS"]), _p(fin["CHUNKS"]), fin["nchunks"], fin["nfew"],
+                fin["nwide"]]
         return g
 
     def _plan_dw_groups(self) -> list:
@@ -1020,8 +1051,12 @@ class MLPExecutor(ForwardChain):
             if spec.b is not None:
                 segs.append((G + 4 * spec.b.offset, bpart.data_ptr(), spec.w.ld, spec.w.ld, splits, rb))
 
-        for lb in self.trunk + self.actor + self.critic:
+        paired = set()   # the paired towers' Dense segments (their group launch can finish them)
+        for k, lb in enumerate(self.trunk + self.actor + self.critic):
+            n0 = len(segs)
             dense_segs(lb.spec.dense, lb.wpart, lb.bpart, lb.splits)
+            if self.chain_ln and k >= len(self.trunk):
+                paired.update(range(n0, len(segs)))
             if lb.spec.ln is not None:
                 F = lb.spec.fout
                 segs.append((G + 4 * lb.spec.ln["scale"].offset, lb.lnpart.data_ptr(), F, 2 * F, lb.lnblocks, 0))
@@ -1040,27 +1075,50 @@ class MLPExecutor(ForwardChain):
         lib = _lib.load()
         assert lib.ppo_grad_reduce_segment_bytes() == 40 and lib.ppo_grad_reduce_chunk_bytes() == 16
         chunk = lib.ppo_grad_reduce_chunk_elems()
-        seg_bytes = b"".join(struct.pack("<QQqqii", d, s, c, st, n, f) for d, s, c, st, n, f in segs)
-        # chunks of few-partial segments first (the kernel's wave-per-chunk
-        # path); each keeps its slot in segment order, so the norm's fold
-        # order does not depend on the split
         few_parts, wide_parts = lib.ppo_grad_reduce_few_parts(), lib.ppo_grad_reduce_wide_parts()
         wide_chunk = lib.ppo_grad_reduce_wide_chunk_elems()
-        few, many, wide = [], [], []
-        for i, (_, _, c, _, n, _) in enumerate(segs):
-            dst = few if n <= few_parts else wide if n > wide_parts else many
-            for start in range(0, c, wide_chunk if dst is wide else chunk):
-                slot = len(few) + len(many) + len(wide)
-                dst.append(struct.pack("<iiq", i, slot, start))
-        chunks = few + many + wide
         dev = flat.device
-        self.SEGS = torch.tensor(list(seg_bytes), dtype=torch.uint8, device=dev)
-        self.CHUNKS = torch.tensor(list(b"".join(chunks)), dtype=torch.uint8, device=dev)
-        self.nchunks = len(chunks)
-        self.nfew, self.nwide = len(few), len(wide)
+
+        def pack(sel, slot0):
+            """Device tables of the segments sel, their norm slots from slot0:
+            (SEGS, CHUNKS, nchunks, nfew, nwide)."""
+            sub = [segs[i] for i in sel]
+            seg_bytes = b"".join(struct.pack("<QQqqii", d, s, c, st, n, f) for d, s, c, st, n, f in sub)
+            # chunks of few-partial segments first (the kernel's wave-per-chunk
+            # path); each keeps its slot in segment order, so the norm's fold
+            # order does not depend on the split
+            few, many, wide = [], [], []
+            for i, (_, _, c, _, n, _) in enumerate(sub):
+                dst = few if n <= few_parts else wide if n > wide_parts else many
+                for start in range(0, c, wide_chunk if dst is wide else chunk):
+                    slot = slot0 + len(few) + len(many) + len(wide)
+                    dst.append(struct.pack("<iiq", i, slot, start))
+            chunks = few + many + wide
+            return (torch.tensor(list(seg_bytes) or [0], dtype=torch.uint8, device=dev),
+                    torch.tensor(list(b"".join(chunks)) or [0], dtype=torch.uint8, device=dev),
+                    len(chunks), len(few), len(wide))
+
+        self.SEGS, self.CHUNKS, self.nchunks, self.nfew, self.nwide = pack(range(len(segs)), 0)
         self.SUMSQ = torch.zeros(self.nchunks, dtype=torch.float64, device=dev)
         self.SUMSQ1 = torch.zeros(1, dtype=torch.float64, device=dev)
         self.segments = segs
+        # the paired towers' grouped weight-gradient launch finishing their
+        # split-K sums itself (ppo_gemm_f32_dw_group_final): its tiles' norm
+        # slots, then the other segments' chunks, reduced in the same launch
+        self.dw_final = None
+        shapes = self._pair_dw_shapes() if self.DW_FINAL and paired else None
+        if shapes and all(sp in self.FINAL_SPLITS and (i >= 2 or -(-self.mb // sp) <= 512)
+                          for i, (_, _, sp) in enumerate(shapes)):
+            L = len(shapes)
+            T = lib.ppo_gemm_f32_dw_final_slots(L, (ctypes.c_int * L)(*[m for m, _, _ in shapes]),
+                                                (ctypes.c_int * L)(*[n for _, n, _ in shapes]))
+            assert T > 0
+            rest = [i for i in range(len(segs)) if i not in paired]
+            SEGS, CHUNKS, nch, nfew, nwide = pack(rest, T)
+            self.dw_final = {"T": T, "SEGS": SEGS, "CHUNKS": CHUNKS, "nchunks": nch, "nfew": nfew, "nwide": nwide,
+                             "SUMSQ": torch.zeros(T + nch, dtype=torch.float64, device=dev),
+                             "CNT": torch.zeros(T, dtype=torch.int32, device=dev)}
+        self._dw_finished = False
 
     # ------------------------------------------------------------- pieces
     def _normalize(self, st):
@@ -1118,6 +1176,20 @@ class MLPExecutor(ForwardChain):
         }
         order = ("A", "lda", "rows", "B", "ldb", "C", "ldc", "M", "N", "K", "splits", "stride", "bias_grad")
         g["args"] = [ctypes.addressof(g[k]) for k in order]
+        fin = self.dw_final
+        if fin is not None:
+            # the final gradients: problem order as above
+            G = self.flat.G.data_ptr()
+            lbs = [lb for i in range(len(A)) for lb in (A[i], C[i])]
+            g.update({
+                "G": vp([G + 4 * lb.spec.dense.w.offset for lb in lbs]),
+                "ldg": i64([lb.spec.dense.w.ld for lb in lbs]),
+                "g_rows": i32([lb.spec.dense.fin for lb in lbs]),
+                "Gb": vp([G + 4 * lb.spec.dense.b.offset if lb.spec.dense.b is not None else None for lb in lbs]),
+            })
+            g["final_args"] = g["args"] + [ctypes.addressof(g[k]) for k in ("G", "ldg", "g_rows", "Gb")] + [
+                _p(fin["CNT"]), _p(fin["SUMSQ"]), _p(fin["SEGS"]), _p(fin["CHUNKS"]), fin["nchunks"], fin["nfew"],
+                fin["nwide"]]
         return g
 
     def _bwd_layers(self, st, layers, x0, ldx0, idx0):
@@ -1253,7 +1325,12 @@ class MLPExecutor(ForwardChain):
             if g is not None:
                 # every weight gradient of both towers in one launch
                 g["rows"][0] = g["rows"][1] = idx0
-                self._call("ppo_gemm_f32_dw_group", st, g["count"], *g["args"])
+                if "final_args" in g:
+                    # ... with their gradient assembly: the optimizer step reads them directly
+                    self._call("ppo_gemm_f32_dw_group_final", st, g["count"], *g["final_args"])
+                    self._dw_finished = True
+                else:
+                    self._call("ppo_gemm_f32_dw_group", st, g["count"], *g["args"])
                 return
             for i, n, sx in self._dw_groups:
                 la, lc = A[i], C[i]
@@ -1420,12 +1497,19 @@ class MLPExecutor(ForwardChain):
         chain = self.chain
         adam = chain.adam
         max_norm = chain.max_grad_norm if chain.max_grad_norm is not None else 0.0
-        self._call("ppo_grad_reduce", st, _p(self.SEGS), _p(self.CHUNKS), self.nchunks, self.nfew, self.nwide,
-                   _p(self.SUMSQ))
-        if self.nchunks <= self.FOLD_NORM_MAX:
-            norm, nnorm = _p(self.SUMSQ), self.nchunks
+        if self._dw_finished:
+            # the weight-gradient launch assembled every gradient (tiles' norm slots, then the others')
+            self._dw_finished = False
+            fin = self.dw_final
+            sumsq, nsq = fin["SUMSQ"], fin["T"] + fin["nchunks"]
         else:
-            self._call("ppo_sumsq_total", st, _p(self.SUMSQ), self.nchunks, _p(self.SUMSQ1))
+            self._call("ppo_grad_reduce", st, _p(self.SEGS), _p(self.CHUNKS), self.nchunks, self.nfew, self.nwide,
+                       _p(self.SUMSQ))
+            sumsq, nsq = self.SUMSQ, self.nchunks
+        if nsq <= self.FOLD_NORM_MAX:
+            norm, nnorm = _p(sumsq), nsq
+        else:
+            self._call("ppo_sumsq_total", st, _p(sumsq), nsq, _p(self.SUMSQ1))
             norm, nnorm = _p(self.SUMSQ1), 1
         self._call("ppo_adam_clip_f32", st, _p(self.flat.P), _p(self.flat.G), _p(self.flat.MU), _p(self.flat.NU),
                    _p(self.P16) if self.obs16 else None, self.flat.P.numel(), norm, nnorm, float(max_norm),

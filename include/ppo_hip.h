@@ -414,6 +414,36 @@ int ppo_gemm_f32_dw_group(void* stream, int count, const float* const* A, const 
                           const int32_t* const* rows, const float* const* B, const int64_t* ldb, float* const* C,
                           const int64_t* ldc, const int* M, const int* N, const int* K, const int* splits,
                           const int64_t* c_split_stride, float* const* bias_grad);
+/* Output tiles (64 x 64) of a weight-gradient group of count problems of
+ * M[i] x N[i] (all positive): the arrival counters and squared-norm slots of
+ * ppo_gemm_f32_dw_group_final, problem after problem; -1 on a bad shape. */
+int ppo_gemm_f32_dw_final_slots(int count, const int* M, const int* N);
+/* ppo_gemm_f32_dw_group with the gradient assembly of its problems in the
+ * same launch (the ppo_grad_reduce launch that would follow it is not
+ * needed): the split partials C[i] / bias_grad[i] are written as before, and
+ * the last split of each 64 x 64 output tile to finish sums them in
+ * ppo_grad_reduce's fixed order into the final gradient G[i] (rows below
+ * g_rows[i] <= M[i], row pitch ldg[i]; a zero-padded input's extra rows are
+ * dropped) and the bias gradient Gb[i] (skipped when Gb or Gb[i] is NULL),
+ * and writes the tile's squared-norm partial to sumsq[slot] (slots and
+ * counters numbered tile by tile, problem after problem, as
+ * ppo_gemm_f32_dw_final_slots counts them).  The gradient segments of the
+ * ppo_grad_reduce tables segs / chunks (their chunk slots numbered after the
+ * tiles') are reduced by workgroups of the same launch.  counters: one
+ * zeroed unsigned per tile, left zeroed; calls sharing counters must not
+ * overlap.  The gradients are the same bits as ppo_gemm_f32_dw_group followed
+ * by ppo_grad_reduce (the norm partials are grouped by tile instead of by
+ * chunk).  splits[i] in
+ * {1, 2, 3, 4, 6, 8, 12, 16}; a gathered split holds at most 512 rows; all
+ * problems non-empty.  Replaces the weight-gradient GEMMs and gradient
+ * assembly of jax.value_and_grad at boonta/algorithms/ppo.py:155-157. */
+int ppo_gemm_f32_dw_group_final(void* stream, int count, const float* const* A, const int64_t* lda,
+                                const int32_t* const* rows, const float* const* B, const int64_t* ldb,
+                                float* const* C, const int64_t* ldc, const int* M, const int* N, const int* K,
+                                const int* splits, const int64_t* c_split_stride, float* const* bias_grad,
+                                float* const* G, const int64_t* ldg, const int* g_rows, float* const* Gb,
+                                unsigned* counters, double* sumsq, const void* segs, const void* chunks, int nchunks,
+                                int nfew, int nwide);
 /* The weight gradients of up to 8 bf16 Dense layers in one launch (one
  * backward pass's dW GEMMs, so that a layer with few tiles runs beside one with
  * many instead of after it): problem i (host arrays, one entry per problem;

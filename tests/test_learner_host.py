@@ -3,6 +3,9 @@ full launch sequence, recorded instead of launched and checked against the C
 signatures (arity, required pointers, buffer extents)."""
 import numpy as np
 import pytest
+import ctypes
+import struct
+
 import torch
 
 from boonta_amd import _lib, recipes
@@ -211,6 +214,66 @@ def check_tower_dw_launches(r, prog, flat, steps):
             assert a[15] == fin * lb.spec.ld    # the partials' split stride
 
 
+class NoFinalExecutor(MLPExecutor):
+    """Paired towers whose grouped weight-gradient launch leaves the
+    gradient assembly to the reduce launch."""
+    DW_FINAL = False
+
+
+def _segment_table(seg_tensor, n):
+    """(dst, src, count, part_stride, nparts, flags) rows of a device segment table."""
+    raw = bytes(seg_tensor.cpu().numpy().tobytes())
+    return [struct.unpack_from("<QQqqii", raw, 40 * i) for i in range(n)]
+
+
+def check_final_gradient_tables(ex, flat, args, adam_calls):
+    """The finishing weight-gradient launch writes each paired Dense gradient
+    (and bias) to its place in the flat gradient, reduces every other segment
+    of the full table in the same launch, and the optimizer step folds its
+    tile slots and chunk slots."""
+    fin, g = ex.dw_final, ex._dwg
+    G = flat.G.data_ptr()
+    lbs = [lb for i in range(len(ex.actor)) for lb in (ex.actor[i], ex.critic[i])]
+    assert list(args[15:19]) == [ctypes.addressof(g[k]) for k in ("G", "ldg", "g_rows", "Gb")]
+    for k, lb in enumerate(lbs):
+        d = lb.spec.dense
+        assert g["G"][k] == G + 4 * d.w.offset and g["ldg"][k] == d.w.ld and g["g_rows"][k] == d.fin
+        assert g["Gb"][k] == G + 4 * d.b.offset
+    assert g["g_rows"][0] == 87 and g["M"][0] == 88     # the padded input's extra gradient row is dropped
+    assert args[19] == fin["CNT"].data_ptr() and args[20] == fin["SUMSQ"].data_ptr()
+    assert list(args[21:26]) == [fin["SEGS"].data_ptr(), fin["CHUNKS"].data_ptr(), fin["nchunks"], fin["nfew"],
+                           fin["nwide"]]
+    tiles = sum(-(-g["M"][k] // 64) * -(-g["N"][k] // 64) for k in range(g["count"]))
+    assert fin["T"] == tiles and fin["CNT"].numel() == tiles and fin["SUMSQ"].numel() == tiles + fin["nchunks"]
+    # the full table's segments = the finished Dense gradients + the rest table's
+    full = _segment_table(ex.SEGS, len(ex.segments))
+    nrest = len(ex.segments) - 2 * len(lbs)
+    rest = _segment_table(fin["SEGS"], nrest)
+    done = {g["G"][k] for k in range(len(lbs))} | {g["Gb"][k] for k in range(len(lbs))}
+    assert sorted(rest + [r for r in full if r[0] in done]) == sorted(full)
+    assert not any(r[0] in done for r in rest)
+    # chunk slots of the rest start after the tiles'
+    raw = bytes(fin["CHUNKS"].cpu().numpy().tobytes())
+    slots = sorted(struct.unpack_from("<iiq", raw, 16 * i)[1] for i in range(fin["nchunks"]))
+    assert slots == list(range(tiles, tiles + fin["nchunks"]))
+    for a in adam_calls:
+        assert a[7] == fin["SUMSQ"].data_ptr() and a[8] == tiles + fin["nchunks"]
+
+
+def test_gaussian_update_without_the_finishing_launch_reduces_its_gradients():
+    r = small(3)
+    prog = Program(r.network.plan(r.obs_dim))
+    flat = FlatState(prog, torch.device("cpu"))
+    ex = executor(r, prog, flat, cls=NoFinalExecutor)
+    ex.bind(fake_inputs(ex))
+    names = [n for n, _ in ex.record()]
+    steps = r.cfg.update_epochs * r.cfg.num_minibatches
+    assert ex.dw_final is None and "ppo_gemm_f32_dw_group_final" not in names
+    assert names.count("ppo_gemm_f32_dw_group") == steps and names.count("ppo_grad_reduce") == steps
+    adam = [a for n, a in ex.record(max_steps=1) if n == "ppo_adam_clip_f32"]
+    assert adam[0][7] == ex.SUMSQ.data_ptr() and adam[0][8] == ex.nchunks
+
+
 def test_gaussian_update_runs_each_torso_chain_in_one_launch():
     r = small(3)
     prog = Program(r.network.plan(r.obs_dim))
@@ -228,10 +291,13 @@ def test_gaussian_update_runs_each_torso_chain_in_one_launch():
     assert names.count("ppo_mlp_ln_fwd_head_loss_f32") == steps and "ppo_head_loss_f32" not in names
     assert names.count("ppo_mlp_ln_fwd_f32") == 1
     assert names.count("ppo_mlp_ln_bwd_f32") == steps
-    assert names.count("ppo_gemm_f32_dw_group") == steps and "ppo_gemm_f32_towers" not in names
+    # ... which also assembles the gradients: no reduce launch per step
+    assert names.count("ppo_gemm_f32_dw_group_final") == steps and "ppo_gemm_f32_towers" not in names
+    assert "ppo_gemm_f32_dw_group" not in names and "ppo_grad_reduce" not in names
     assert names.count("ppo_pad_rows_f32") == 1   # the padded observation copy, once per update
-    dwg = [a for n, a in calls if n == "ppo_gemm_f32_dw_group"]
+    dwg = [a for n, a in calls if n == "ppo_gemm_f32_dw_group_final"]
     assert len(dwg) == 1 and dwg[0][1] == 2 * len(ex.actor)
+    check_final_gradient_tables(ex, flat, dwg[0], [a for n, a in calls if n == "ppo_adam_clip_f32"])
     g = ex._dwg
     fwd = [a for n, a in calls if n == "ppo_mlp_ln_fwd_head_loss_f32"][0]
     idx = fwd[5]   # the step's gather indices
