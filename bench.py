@@ -108,7 +108,7 @@ def launch_work(name, args):
     return towers * flops, towers * nbytes
 
 
-DW_GROUPS = ("ppo_gemm_bf16s_dw_group", "ppo_gemm_f32_dw_group")
+DW_GROUPS = ("ppo_gemm_bf16s_dw_group", "ppo_gemm_f32_dw_group", "ppo_gemm_f32_dw_group_final")
 
 
 def dw_group_problems(args):
@@ -130,6 +130,11 @@ def _single_launch_work(name, args):
     if name in DW_GROUPS:
         probs = dw_group_problems(args)
         e = 2.0 if name == "ppo_gemm_bf16s_dw_group" else 4.0   # operand element bytes
+        if name == "ppo_gemm_f32_dw_group_final":
+            # the operands and the finished gradient (its split partials are
+            # the implementation's, not the algorithm's bytes)
+            return (sum(2.0 * M * N * K for M, N, K, _ in probs),
+                    sum(e * M * K + e * K * N + 4.0 * M * N for M, N, K, _ in probs))
         return (sum(2.0 * M * N * K for M, N, K, _ in probs),
                 sum(e * M * K + e * K * N + 4.0 * M * N * S for M, N, K, S in probs))
     if name in ("ppo_gemm_f32", "ppo_gemm_bf16"):
@@ -164,6 +169,9 @@ def _single_launch_work(name, args):
     if name == "ppo_adam_clip_f32":
         n = args[6]
         return 0.0, 28.0 * n
+    if name == "ppo_adam_clip_wt_f32":
+        n, ntr = args[6], args[17]
+        return 0.0, 28.0 * n + 4.0 * 256 * 256 * ntr
     if name == "ppo_head_loss_f32":
         rows, F, A = args[2], args[15], args[16]
         groups = 2 if args[10] else 1
@@ -180,6 +188,12 @@ def _single_launch_work(name, args):
         hf, hb = _single_launch_work("ppo_head_loss_f32", head)
         rows, F, groups = head[2], head[15], (2 if head[10] else 1)
         return cf + hf, cb + hb - 4.0 * rows * F * groups
+    if name == "ppo_mlp_ln_fwd_head_loss_bwd_f32":
+        # the forward chain with the heads + loss, then the backward chain
+        ff, fb = _single_launch_work("ppo_mlp_ln_fwd_head_loss_f32", args[:-3])
+        towers, L, M = args[1], args[2], args[6]
+        bf, bb = _single_launch_work("ppo_mlp_ln_bwd_f32", (args[0], towers, L, None, None, M))
+        return ff + bf, fb + bb
     if name == "ppo_mlp_ln_fwd_f32":
         towers, L, M, K0 = args[1], args[2], args[6], args[7]
         weights = 256 * (K0 + 256 * (L - 1)) + 3 * 256 * L
@@ -282,7 +296,7 @@ def _single_launch_shape(name, args):
         return [args[15], args[17], args[16]]
     if name == "ppo_step_mlp_categorical_f32":
         return [args[3], 256, args[4], args[5]]
-    if name in ("ppo_mlp_ln_fwd_f32", "ppo_mlp_ln_fwd_head_loss_f32"):
+    if name in ("ppo_mlp_ln_fwd_f32", "ppo_mlp_ln_fwd_head_loss_f32", "ppo_mlp_ln_fwd_head_loss_bwd_f32"):
         return [args[6], 256, args[7], args[2], args[1]]
     if name == "ppo_mlp_ln_bwd_f32":
         return [args[5], 256, 256, args[2], args[1]]
@@ -343,19 +357,29 @@ def time_launches(ex, reps, per_update_steps):
     import torch
     from boonta_amd import _lib
 
-    calls = ex.record(max_steps=1)
+    calls1 = ex.record(max_steps=1)
     stream = torch.cuda.current_stream()
     st = stream.cuda_stream
     # launches before the first minibatch step: those of an update stopped
     # before it, less its log finalize
     first_mb = len(ex.record(max_steps=0)) - 1
-    per_step = len(calls) - 1 - first_mb
     full = ex.record()
     S = per_update_steps
-    if len(full) != first_mb + S * per_step + 2:
+    # the first step's launches, and those every later step repeats (the
+    # first may differ: the Gaussian towers' first step writes the transposed
+    # kernels its backward reads, later steps have them from Adam)
+    step0 = calls1[first_mb:-1]
+    step1 = ex.record(max_steps=2)[len(calls1) - 1:-1] if S > 1 else step0
+    same = [n for n, _ in step0] == [n for n, _ in step1]
+    later = [] if same else step1
+    calls = calls1[:first_mb] + step0 + later + [calls1[-1]]
+    counts = [1] * first_mb + [S if same else 1] * len(step0) + [S - 1] * len(later) + [1]
+    if len(full) != first_mb + len(step0) + (S - 1) * len(step1) + 2:
         raise RuntimeError(f"unexpected launch count per update ({len(full)})")
-    # position of each launch of the whole update in the one-step record
-    pos = list(range(first_mb)) + [first_mb + k % per_step for k in range(S * per_step)] + [len(calls) - 1, None]
+    # position of each launch of the whole update in that template
+    a0, a1 = first_mb, first_mb + (0 if same else len(step0))
+    pos = (list(range(first_mb)) + [a0 + k for k in range(len(step0))]
+           + [a1 + k % len(step1) for k in range((S - 1) * len(step1))] + [len(calls) - 1, None])
     if any(p is not None and full[k][0] != calls[p][0] for k, p in enumerate(pos)):
         raise RuntimeError("the minibatch steps of one update do not repeat one launch sequence")
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(full) + 1)]
@@ -367,8 +391,7 @@ def time_launches(ex, reps, per_update_steps):
     ctx_ms = [ev[k].elapsed_time(ev[k + 1]) for k in range(len(full))]
     rows, seen, by_pos = [], {}, {}
     for i, (name, args) in enumerate(calls):
-        # the logs of every step are finalized once, after the last step
-        count = per_update_steps if i >= first_mb and name != "ppo_loss_finalize_steps" else 1
+        count = counts[i]
         key = launch_key(name, args)
         if key in seen:
             seen[key]["count"] += count

@@ -111,6 +111,11 @@ SIGNATURES = {
                                          I, I, P, P, I64, P, I64, P, I, P, I64, P, I64, P, I, I, P, P, P, P, P, P,
                                          P, I, P, I64, P, I64, I, P, I64, P, I64, P, P, P, P, P, P, F, I, F, F, F,
                                          I64]),
+    "ppo_mlp_ln_fwd_head_loss_bwd_f32": (I, [P, I, I, P, I64, P, I, I, P, I64, I64, P, P, P, P, P, I64, P, P, F, I,
+                                             I64, I64, I64, I64, P, I64,
+                                             I, I, P, P, I64, P, I64, P, I, P, I64, P, I64, P, I, I, P, P, P, P, P,
+                                             P, P, I, P, I64, P, I64, I, P, I64, P, I64, P, P, P, P, P, P, F, I, F,
+                                             F, F, I64, P, P, I64]),
     "ppo_head_loss_ratio_f32": (I, [P, I, I, P, P, I64, P, I64, P, I, P, I64, P, I64, P, I, I, P, P, P, P, P, P, P,
                                     I, P, I64, P, I64, I, P, I64, P, I64, P, P, P, P, P, P, F, I, F, F, F, P, I,
                                     I, I64]),
@@ -138,6 +143,7 @@ SIGNATURES = {
     "ppo_grad_reduce": (I, [P, P, P, I, I, I, P]),
     "ppo_sumsq_total": (I, [P, P, I, P]),
     "ppo_adam_clip_f32": (I, [P, P, P, P, P, P, I64, P, I, D, D, D, D, D, P, I, P]),
+    "ppo_adam_clip_wt_f32": (I, [P, P, P, P, P, P, I64, P, I, D, D, D, D, D, P, I, P, I, P, P]),
     "ppo_count_advance": (I, [P, P, I, P]),
 }
 

@@ -319,7 +319,7 @@ __device__ __forceinline__ void chain_head(const HeadLossParams& hp, const float
 // HEAD: the fused heads + loss of a pair of towers on the last layer's output
 // (chain_head; hp is unused otherwise).
 template <bool VA, int ACT, bool HEAD>
-__global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p, HeadLossParams hp) {
+__device__ __forceinline__ void mlp_ln_fwd_body(const FwdArgs& p, const HeadLossParams& hp) {
   __shared__ __attribute__((aligned(16))) float sX[MC_ROWS][SX_PITCH];
   __shared__ __attribute__((aligned(16))) float s_part[HEAD ? 4 : 1][MC_ROWS][LDO];
   __shared__ __attribute__((aligned(16))) float s_dout[HEAD ? MC_ROWS : 1][LDO];
@@ -516,6 +516,11 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p, HeadL
   }
 }
 
+template <bool VA, int ACT, bool HEAD>
+__global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_kernel(FwdArgs p, HeadLossParams hp) {
+  mlp_ln_fwd_body<VA, ACT, HEAD>(p, hp);
+}
+
 struct BwdArgs {
   const float* dY;  // cotangent of the last layer's output
   int64_t lddy;
@@ -534,7 +539,7 @@ struct BwdArgs {
 };
 
 template <int ACT>
-__global__ void __launch_bounds__(MC_THREADS) mlp_ln_bwd_kernel(BwdArgs p) {
+__device__ __forceinline__ void mlp_ln_bwd_body(const BwdArgs& p) {
   __shared__ float sX[MC_ROWS][SX_PITCH];
   __shared__ float s_sum[4][MC_ROWS];
   __shared__ float s_sq[4][MC_ROWS];
@@ -659,6 +664,26 @@ __global__ void __launch_bounds__(MC_THREADS) mlp_ln_bwd_kernel(BwdArgs p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) dy[v][j] = acc[j][v];
   }
+}
+
+template <int ACT>
+__global__ void __launch_bounds__(MC_THREADS) mlp_ln_bwd_kernel(BwdArgs p) {
+  mlp_ln_bwd_body<ACT>(p);
+}
+
+// The forward chain with the fused heads + loss, then the backward chain, in
+// one launch: every row's loss cotangent depends only on that row, so the
+// workgroup that owns 16 rows of a tower runs their backward right after
+// their forward.  The backward's input cotangents, Z and statistics are this
+// workgroup's own stores (complete and visible to its waves after the wait
+// and barrier below); the transposed kernels it reads were written before
+// the launch (the forward part writes none).
+template <bool VA, int ACT>
+__global__ void __launch_bounds__(MC_THREADS) mlp_ln_fwd_bwd_kernel(FwdArgs p, HeadLossParams hp, BwdArgs b) {
+  mlp_ln_fwd_body<VA, ACT, true>(p, hp);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  mlp_ln_bwd_body<ACT>(b);
 }
 
 bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
@@ -825,4 +850,76 @@ PPO_EXPORT int ppo_mlp_ln_bwd_f32(void* stream, int towers, int L, const float* 
     default: hipLaunchKernelGGL(mlp_ln_bwd_kernel<ACT_NONE>, grid, block, 0, ppo::as_stream(stream), a); break;
   }
   return ppo::check_launch("ppo_mlp_ln_bwd_f32");
+}
+
+// ppo_mlp_ln_fwd_head_loss_f32 followed by ppo_mlp_ln_bwd_f32 from the heads'
+// input cotangents, in one launch, bit for bit: the chain and head arguments
+// are those of ppo_mlp_ln_fwd_head_loss_f32, except that WT / stride_wt are
+// the transposed kernels the backward reads (layers 1..L-1, [256][256], made
+// before this launch, e.g. by ppo_adam_clip_wt_f32; none are written here);
+// the backward's dY is dha (tower 1: dhc = dha + stride_rows, lddhc = lddha),
+// and it writes dZ (pitch ld) and the LayerNorm parameter partials
+// (partial[l], tower stride stride_part) as ppo_mlp_ln_bwd_f32 does.
+PPO_EXPORT int ppo_mlp_ln_fwd_head_loss_bwd_f32(
+    void* stream, int towers, int L, const float* X, int64_t ldx, const int32_t* rows_idx, int M, int K0,
+    const float* const* W, int64_t ldw0, int64_t ldw, const float* const* bias, const float* const* gamma,
+    const float* const* beta, float* const* Z, float* const* Y, int64_t ld, float* const* mean, float* const* rstd,
+    float eps, int act, int64_t stride_x, int64_t stride_params, int64_t stride_rows, int64_t stride_stats,
+    float* const* WT, int64_t stride_wt, int dist, int rows, const int32_t* idx, const float* ha, int64_t ldha,
+    const float* wa, int64_t ldwa, const float* ba, int na, const float* hc, int64_t ldhc, const float* wc,
+    int64_t ldwc, const float* bc, int F, int A, const float* scale_param, const int32_t* action_i,
+    const float* action_f, const float* old_logp, const float* old_value, const float* adv, const float* ret,
+    int act_a, const float* aux_a, int64_t ldaux_a, float* dha, int64_t lddha, int act_c, const float* aux_c,
+    int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a, float* wpart_c, float* bpart_c,
+    float* dscale_partial, double* stats_partial, float clip_eps, int clip_value_loss, float ent_coef,
+    float vf_coef, float temperature, int64_t sample_stride, float* const* dZ, float* const* partial,
+    int64_t stride_part) {
+  const char* name = "ppo_mlp_ln_fwd_head_loss_bwd_f32";
+  FwdArgs a;
+  bool va = false;
+  // the forward part writes no transposed kernels
+  int rc = chain_fwd_setup(a, va, name, towers, L, X, ldx, rows_idx, M, K0, W, ldw0, ldw, bias, gamma, beta, Z, Y,
+                           ld, mean, rstd, eps, act, stride_x, stride_params, stride_rows, stride_stats, nullptr, 0);
+  if (rc != PPO_OK) return rc;
+  HeadLossParams hp;
+  rc = head_loss_setup(hp, name, dist, rows, idx, ha, ldha, wa, ldwa, ba, na, hc, ldhc, wc, ldwc, bc, F, A,
+                       scale_param, action_i, action_f, old_logp, old_value, adv, ret, act_a, aux_a, ldaux_a, dha,
+                       lddha, act_c, aux_c, ldaux_c, dhc, lddhc, wpart_a, bpart_a, wpart_c, bpart_c, dscale_partial,
+                       stats_partial, clip_eps, clip_value_loss, ent_coef, vf_coef, temperature, nullptr, 1, 1,
+                       sample_stride);
+  if (rc != PPO_OK) return rc;
+  if (towers != 2 || !hc || F != MC_F || act_a != ACT_NONE || act_c != ACT_NONE || rows != M || ha != Y[L - 1] ||
+      hc != Y[L - 1] + stride_rows || ldha != ld || ldhc != ld || (reinterpret_cast<uintptr_t>(wa) & 255) ||
+      (reinterpret_cast<uintptr_t>(wc) & 255) ||
+      (M > 0 && ppo_head_loss_blocks(M) != ppo::ceil_div(M, MC_ROWS)))
+    return ppo::set_error(PPO_ERR_ARG, "%s: the heads must read the last layer of both towers (towers=%d F=%d "
+                          "rows=%d M=%d)", name, towers, F, rows, M);
+  if (!dha || dhc != dha + stride_rows || lddhc != lddha || lddha < MC_F || lddha % 4 || !aligned16(dha) || !dZ ||
+      !partial || stride_part % 4 || (L > 1 && (!WT || stride_wt % 4)))
+    return ppo::set_error(PPO_ERR_ARG, "%s: the backward reads dha and dhc = dha + stride_rows; it needs dZ, "
+                          "partial and (L > 1) WT tables", name);
+  BwdArgs b{};
+  b.dY = dha; b.lddy = lddha; b.M = M; b.L = L; b.act = act; b.ld = ld; b.ldwt = MC_F;
+  b.tR = stride_rows; b.tS = stride_stats; b.tP = stride_params; b.tWT = stride_wt; b.tPart = stride_part;
+  for (int l = 0; l < L; ++l) {
+    if (!dZ[l] || !partial[l] || (l > 0 && (!WT[l] || !aligned16(WT[l]))) || !aligned16(dZ[l]) ||
+        !aligned16(partial[l]))
+      return ppo::set_error(PPO_ERR_ARG, "%s: layer %d needs 16-byte aligned backward buffers", name, l);
+    b.Z[l] = Z[l]; b.mean[l] = mean[l]; b.rstd[l] = rstd[l]; b.gamma[l] = gamma[l]; b.beta[l] = beta[l];
+    b.WT[l] = l > 0 ? WT[l] : nullptr; b.dZ[l] = dZ[l]; b.part[l] = partial[l];
+  }
+  if (M == 0) return PPO_OK;
+  const dim3 grid(ppo::ceil_div(M, MC_ROWS), towers), block(MC_THREADS);
+  hipStream_t st = ppo::as_stream(stream);
+#define PPO_CHAIN_FB(ACTV)                                                                              \
+  if (va) hipLaunchKernelGGL((mlp_ln_fwd_bwd_kernel<true, ACTV>), grid, block, 0, st, a, hp, b);       \
+  else hipLaunchKernelGGL((mlp_ln_fwd_bwd_kernel<false, ACTV>), grid, block, 0, st, a, hp, b);
+  switch (act) {
+    case ACT_RELU: PPO_CHAIN_FB(ACT_RELU) break;
+    case ACT_TANH: PPO_CHAIN_FB(ACT_TANH) break;
+    case ACT_SILU: PPO_CHAIN_FB(ACT_SILU) break;
+    default: PPO_CHAIN_FB(ACT_NONE) break;
+  }
+#undef PPO_CHAIN_FB
+  return ppo::check_launch(name);
 }

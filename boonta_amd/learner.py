@@ -346,11 +346,15 @@ def paired_tower_bufs(specs_a, specs_c, rows: int, device, ln_blocks: int | None
     alloc("lnpart", [(blocks, 2 * s.fout) if ln[i] else None for i, s in enumerate(specs_a)])
     alloc("PRE", [(rows, s.ld) if not ln[i] and s.act == "silu" else None for i, s in enumerate(specs_a)])
     for i, s in enumerate(specs_a):
-        # batched over depth and towers, the weight gradients past the first
-        # layer fill the chip with half the row splits (2048-row Gaussian
-        # minibatches: 8 splits 20.02 ms per update, 16: 20.45, 4: 20.44)
-        half = grouped_dw and i > 0
-        A[i].splits = C[i].splits = max(1, _splits(rows, s.dense.fin, s.ld) // (2 if half else 1))
+        # batched over depth and towers in one launch that also finishes the
+        # split-K sums (the last split of each tile reads the others'
+        # partials back), fewer splits: half for the first layer, 3/8 for the
+        # later ones (2048-row Gaussian minibatches: 8 and 6 splits, 5.08 M
+        # samples/s, against 5.05 M with 16 and 8)
+        sp = _splits(rows, s.dense.fin, s.ld)
+        if grouped_dw:
+            sp = sp // 2 if i == 0 else 3 * sp // 8
+        A[i].splits = C[i].splits = max(1, sp)
         if ln[i]:
             A[i].lnblocks = C[i].lnblocks = blocks
     alloc("wpart", [(a.splits, max(s.dense.fin, fin0_pad) if i == 0 else s.dense.fin, s.ld)
@@ -1312,15 +1316,18 @@ class MLPExecutor(ForwardChain):
                            _tstride(la.Y, lc.Y), D, _tstride(la.PRE, lc.PRE) if pre else 0, 0, 0)
             x, ldx, rows_idx, sx = _p(la.Y), s.ld, None, _tstride(la.Y, lc.Y)
 
-    def _bwd_pair(self, st, x0, ldx0, idx0):
+    def _bwd_pair(self, st, x0, ldx0, idx0, chain_done=False):
         """Backward of the actor and critic towers, one launch per depth and
-        contraction, once both last-layer output cotangents are in place."""
+        contraction, once both last-layer output cotangents are in place
+        (chain_done: the torso chains' backward already ran, in the forward's
+        launch; only the weight gradients remain)."""
         D, A, C = self.pair, self.actor, self.critic
         if self.chain_ln:
             c = self._chain
-            self._call("ppo_mlp_ln_bwd_f32", st, 2, len(A), _p(A[-1].dY), A[-1].spec.ld, self.mb, c["Z"], c["mean"],
-                       c["rstd"], c["g"], c["be"], c["WT"], 256, c["dZ"], A[0].spec.ld, c["part"], self._chain_act,
-                       self._chain_rs, self._chain_ss, D, 256 * 256, self._chain_ps)
+            if not chain_done:
+                self._call("ppo_mlp_ln_bwd_f32", st, 2, len(A), _p(A[-1].dY), A[-1].spec.ld, self.mb, c["Z"],
+                           c["mean"], c["rstd"], c["g"], c["be"], c["WT"], 256, c["dZ"], A[0].spec.ld, c["part"],
+                           self._chain_act, self._chain_rs, self._chain_ss, D, 256 * 256, self._chain_ps)
             g = self._pair_dw_group(x0, ldx0)
             if g is not None:
                 # every weight gradient of both towers in one launch
@@ -1511,9 +1518,18 @@ class MLPExecutor(ForwardChain):
         else:
             self._call("ppo_sumsq_total", st, _p(sumsq), nsq, _p(self.SUMSQ1))
             norm, nnorm = _p(self.SUMSQ1), 1
-        self._call("ppo_adam_clip_f32", st, _p(self.flat.P), _p(self.flat.G), _p(self.flat.MU), _p(self.flat.NU),
-                   _p(self.P16) if self.obs16 else None, self.flat.P.numel(), norm, nnorm, float(max_norm),
-                   adam.learning_rate, adam.b1, adam.b2, adam.eps, _p(self.flat.count), step, self._abort_word())
+        args = (_p(self.flat.P), _p(self.flat.G), _p(self.flat.MU), _p(self.flat.NU),
+                _p(self.P16) if self.obs16 else None, self.flat.P.numel(), norm, nnorm, float(max_norm),
+                adam.learning_rate, adam.b1, adam.b2, adam.eps, _p(self.flat.count), step, self._abort_word())
+        if self.pair and self.fused and self._fwd_bwd_fused():
+            tr = self.__dict__.get("_tr_args")
+            if tr is None:
+                offs, dsts = self._transposed_kernels()
+                n = len(offs)
+                tr = self._tr_args = (n, (ctypes.c_int64 * n)(*offs), (ctypes.c_void_p * n)(*dsts))
+            self._call("ppo_adam_clip_wt_f32", st, *args, tr[0], ctypes.addressof(tr[1]), ctypes.addressof(tr[2]))
+        else:
+            self._call("ppo_adam_clip_f32", st, *args)
         if self.obs16:
             self._pack16(st)
 
@@ -1545,6 +1561,27 @@ class MLPExecutor(ForwardChain):
     # the paired chains' forward and the fused heads + loss in one launch
     # (off: the chain launch, then the head loss launch)
     CHAIN_HEAD = True
+
+    # after the first optimizer step of an update, the paired towers' forward
+    # chain, heads + loss and backward chain run as one launch; each Adam step
+    # writes the transposed kernels that launch's backward reads
+    # (ppo_adam_clip_wt_f32), the first step's forward writes them itself
+    FWD_BWD_FUSED = True
+
+    def _fwd_bwd_fused(self) -> bool:
+        return self.FWD_BWD_FUSED and self._chain_head and len(self.actor) > 1
+
+    def _transposed_kernels(self):
+        """(offsets in the flat parameters, transposed image pointers) of the
+        paired towers' 256 x 256 kernels of layers 1.., actor then critic per
+        layer: what ppo_adam_clip_wt_f32 keeps transposed for the fused
+        forward + backward launch."""
+        offs, dsts = [], []
+        for l in range(1, len(self.actor)):
+            for t, lb in enumerate((self.actor[l], self.critic[l])):
+                offs.append(lb.spec.dense.w.offset)
+                dsts.append(self.WT[l - 1, t].data_ptr())
+        return offs, dsts
 
     @property
     def _chain_head(self) -> bool:
@@ -1642,6 +1679,15 @@ class MLPExecutor(ForwardChain):
                 self._fused_head_loss(st, idx, step, dist, A, scale_ptr, act_i, act_f)
                 self._bwd_layers(st, self.trunk, obs, ldo, idx)
             elif self.pair:
+                if self._chain_head and self._fwd_bwd_fused() and step > 0:
+                    # forward, heads + loss and the torso backward in one launch: the
+                    # previous optimizer step wrote the transposed kernels it reads
+                    c = self._chain
+                    self._call("ppo_mlp_ln_fwd_head_loss_bwd_f32", st, *self._chain_fwd_args(obs, ldo, idx, mb),
+                               *self._head_loss_args(idx, step, dist, A, scale_ptr, act_i, act_f),
+                               self._sample_stride(), c["dZ"], c["part"], self._chain_ps)
+                    self._bwd_pair(st, obs, ldo, idx, chain_done=True)
+                    return
                 if self._chain_head:
                     self._call("ppo_mlp_ln_fwd_head_loss_f32", st, *self._chain_fwd_args(obs, ldo, idx, mb),
                                *self._head_loss_args(idx, step, dist, A, scale_ptr, act_i, act_f),

@@ -607,6 +607,33 @@ int ppo_mlp_ln_fwd_head_loss_f32(
     int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a, float* wpart_c, float* bpart_c,
     float* dscale_partial, double* stats_partial, float clip_eps, int clip_value_loss, float ent_coef,
     float vf_coef, float temperature, int64_t sample_stride);
+/* ppo_mlp_ln_fwd_head_loss_f32 followed by ppo_mlp_ln_bwd_f32 from the heads'
+ * input cotangents, in one launch, bit for bit (each workgroup runs the
+ * backward of its own 16 rows after their forward and loss: every row's loss
+ * cotangent depends only on that row).  The chain and head arguments are
+ * those of ppo_mlp_ln_fwd_head_loss_f32 except WT / stride_wt: the transposed
+ * kernels of layers 1..L-1 that the backward reads, written before this
+ * launch (e.g. by ppo_adam_clip_wt_f32); this launch writes none.  The
+ * backward reads dY = dha (tower 1: dhc = dha + stride_rows, lddhc = lddha)
+ * and writes dZ[l] (row pitch ld) and the LayerNorm parameter partials
+ * partial[l] (tower stride stride_part) as ppo_mlp_ln_bwd_f32 does.  Replaces
+ * the same reference code as those two entry points (the torso forward of
+ * boonta/networks/network.py:38-49, loss_fn of boonta/algorithms/ppo.py:77-146
+ * and its backward under jax.value_and_grad, ppo.py:155-157). */
+int ppo_mlp_ln_fwd_head_loss_bwd_f32(
+    void* stream, int towers, int L, const float* X, int64_t ldx, const int32_t* rows_idx, int M, int K0,
+    const float* const* W, int64_t ldw0, int64_t ldw, const float* const* bias, const float* const* gamma,
+    const float* const* beta, float* const* Z, float* const* Y, int64_t ld, float* const* mean, float* const* rstd,
+    float eps, int act, int64_t stride_x, int64_t stride_params, int64_t stride_rows, int64_t stride_stats,
+    float* const* WT, int64_t stride_wt, int dist, int rows, const int32_t* idx, const float* ha, int64_t ldha,
+    const float* wa, int64_t ldwa, const float* ba, int na, const float* hc, int64_t ldhc, const float* wc,
+    int64_t ldwc, const float* bc, int F, int A, const float* scale_param, const int32_t* action_i,
+    const float* action_f, const float* old_logp, const float* old_value, const float* adv, const float* ret,
+    int act_a, const float* aux_a, int64_t ldaux_a, float* dha, int64_t lddha, int act_c, const float* aux_c,
+    int64_t ldaux_c, float* dhc, int64_t lddhc, float* wpart_a, float* bpart_a, float* wpart_c, float* bpart_c,
+    float* dscale_partial, double* stats_partial, float clip_eps, int clip_value_loss, float ent_coef,
+    float vf_coef, float temperature, int64_t sample_stride, float* const* dZ, float* const* partial,
+    int64_t stride_part);
 /* ppo_head_loss_f32 that also keeps each row's ratio exp(logp - old_logp),
  * env-major: ratio_out[(s % envs) * steps + s / envs] for the row's sample
  * s = idx[row] = t * envs + env (the new ratio RecurrentPuPO scatters back
@@ -751,6 +778,18 @@ int ppo_grad_reduce(void* stream, const void* segs, const void* chunks, int nchu
 int ppo_adam_clip_f32(void* stream, float* params, const float* grads, float* mu, float* nu, void* params_bf16,
                       int64_t n, const double* sumsq, int nsumsq, double max_norm, double lr, double b1,
                       double b2, double eps, const int* count_base, int step_offset, const int* abort_word);
+/* ppo_adam_clip_f32 that also writes the transposed image of ntr (at most 8)
+ * 256 x 256 row-major kernels inside the parameters: kernel r starts at
+ * element tr_off[r] (a multiple of 4; kernels disjoint) and its updated
+ * values go to tr_dst[r] as [256 out][256 in] (16-byte aligned), the operand
+ * ppo_mlp_ln_fwd_head_loss_bwd_f32's backward reads.  Parameters, moments and
+ * bf16 image are the same bits as ppo_adam_clip_f32's; with an abort word set
+ * nothing is written.  Replaces the same optax update as ppo_adam_clip_f32
+ * (boonta/algorithms/ppo.py:182-191). */
+int ppo_adam_clip_wt_f32(void* stream, float* params, const float* grads, float* mu, float* nu, void* params_bf16,
+                         int64_t n, const double* sumsq, int nsumsq, double max_norm, double lr, double b1,
+                         double b2, double eps, const int* count_base, int step_offset, const int* abort_word,
+                         int ntr, const int64_t* tr_off, float* const* tr_dst);
 /* total[0] = sum of sumsq[0..n) in a fixed order (one block of 1024 threads):
  * the squared global norm, handed to ppo_adam_clip_f32 as one partial. */
 int ppo_sumsq_total(void* stream, const double* sumsq, int n, double* total);

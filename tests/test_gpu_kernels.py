@@ -882,3 +882,52 @@ def test_fused_heads_loss_and_head_backward(sep, dist, A, F, rows, act):
     o = host(outv)
     np.testing.assert_allclose(o[8], loss, rtol=1e-5, atol=1e-6)
     np.testing.assert_allclose(o[1], logs["actor/entropy"], rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("bf16_image", [False, True])
+def test_adam_with_transposed_kernels_is_bit_identical_and_writes_the_transpose(bf16_image):
+    """ppo_adam_clip_wt_f32: the same parameters, moments and bf16 image as
+    ppo_adam_clip_f32, bit for bit, with each listed 256 x 256 kernel's
+    updated values also written transposed (kernels at offsets that are not
+    multiples of the block size, with plain elements before, between and after
+    them)."""
+    import ctypes
+    g = np.random.default_rng(21 + bf16_image)
+    offs = [260, 260 + 65536 + 1028]
+    n = offs[-1] + 65536 + 516
+    p0 = g.standard_normal(n).astype(np.float32)
+    mu0 = (g.standard_normal(n) * 1e-3).astype(np.float32)
+    nu0 = (g.random(n) * 1e-5).astype(np.float32)
+    grad = (g.standard_normal(n) * 0.01).astype(np.float32)
+    Gt = dev(grad)
+    SQ = torch.tensor([float((grad.astype(np.float64) ** 2).sum())], dtype=torch.float64, device=DEV)
+    count = torch.tensor([3], dtype=torch.int32, device=DEV)
+    outs = []
+    for wt in (False, True):
+        P, MU, NU = dev(p0), dev(mu0), dev(nu0)
+        P16 = torch.zeros(n // 2, dtype=torch.int32, device=DEV) if bf16_image else None
+        args = (P.data_ptr(), Gt.data_ptr(), MU.data_ptr(), NU.data_ptr(), P16.data_ptr() if bf16_image else None,
+                n, SQ.data_ptr(), 1, 0.5, 3e-4, 0.9, 0.999, 1e-8, count.data_ptr(), 1, None)
+        WT = torch.full((len(offs), 256, 256), float("nan"), device=DEV)
+        if wt:
+            o = (ctypes.c_int64 * 2)(*offs)
+            d = (ctypes.c_void_p * 2)(*[WT[r].data_ptr() for r in range(2)])
+            _lib.call("ppo_adam_clip_wt_f32", st(), *args, 2, ctypes.addressof(o), ctypes.addressof(d))
+        else:
+            _lib.call("ppo_adam_clip_f32", st(), *args)
+        outs.append((host(P), host(MU), host(NU), host(P16) if bf16_image else None, host(WT)))
+    (p1, m1, v1, b1, _), (p2, m2, v2, b2, wt2) = outs
+    for a, b in ((p1, p2), (m1, m2), (v1, v2)):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    if bf16_image:
+        assert np.array_equal(b1, b2)
+    assert not np.array_equal(p1, p0)   # the step moved the parameters
+    for r, o in enumerate(offs):
+        assert np.array_equal(wt2[r].view(np.uint32), p2[o:o + 65536].reshape(256, 256).T.view(np.uint32))
+    bad = (ctypes.c_int64 * 2)(offs[0], offs[0] + 256)   # overlapping kernels
+    d = (ctypes.c_void_p * 2)(*[WT[r].data_ptr() for r in range(2)])
+    P = dev(p0)
+    with pytest.raises(_lib.KernelError):
+        _lib.call("ppo_adam_clip_wt_f32", st(), P.data_ptr(), Gt.data_ptr(), P.data_ptr(), P.data_ptr(), None, n,
+                  SQ.data_ptr(), 1, 0.5, 3e-4, 0.9, 0.999, 1e-8, count.data_ptr(), 1, None, 2,
+                  ctypes.addressof(bad), ctypes.addressof(d))

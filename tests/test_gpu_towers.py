@@ -403,3 +403,38 @@ def test_chain_with_fused_heads_is_bit_identical_to_separate_launches(use_graph)
                         ex.STATS.cpu().numpy().copy()))
     for a, b in zip(*results):
         np.testing.assert_array_equal(a, b)
+
+
+class _UnfusedChains(MLPExecutor):
+    """The paired chains' forward (with the heads + loss) and backward as
+    separate launches at every step."""
+    FWD_BWD_FUSED = False
+
+
+class _UnfusedChainsPPO(PPO):
+    executor_class = _UnfusedChains
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_fused_forward_backward_chain_is_bit_identical_to_separate_launches(use_graph):
+    """From the second optimizer step of an update on, the forward chain with
+    the heads + loss and the backward chain run in one launch
+    (ppo_mlp_ln_fwd_head_loss_bwd_f32) on the transposed kernels each Adam
+    step writes (ppo_adam_clip_wt_f32): the parameters and every logged value
+    after two updates are the same bits as with the two launches per step.
+    Ragged last tile: 500-row minibatches."""
+    r, plan, params, tr, roll = make_case(config=3, T=8, N=250, M=4, E=2)
+    results = []
+    for cls in (PPO, _UnfusedChainsPPO):
+        alg = cls(cfg=r.cfg, network=r.network, optimizer=r.optimizer, use_graph=use_graph)
+        state = alg.init_from_params({"params": params}, r.obs_dim)
+        ex = alg.executor(state, r.T, r.N, r.obs_dim)
+        assert ex._fwd_bwd_fused() == (cls is PPO) and ex.mb % 16 != 0
+        trans = device_transition(tr, roll)
+        for k in (1, 2):
+            alg.update(state, make_key(k), trans)
+        torch.cuda.synchronize()
+        results.append((flat_state_of(state).P.cpu().numpy().copy(), ex.LOGS.cpu().numpy().copy(),
+                        ex.STATS.cpu().numpy().copy()))
+    for a, b in zip(*results):
+        np.testing.assert_array_equal(a, b)

@@ -59,7 +59,9 @@ def test_recorded_launches_match_the_c_signatures(config):
         assert names.count("ppo_gru_fwd_step_f32") == 2 + steps * r.T
         assert names.count("ppo_gru_bwd_step_f32") == steps * r.T
         assert names.count("ppo_sequence_rows") == 1
-    assert names.count("ppo_adam_clip_f32") == steps
+    # (the paired 256-wide towers' steps also keep their kernels transposed)
+    adam = "ppo_adam_clip_wt_f32" if ex.pair and ex._fwd_bwd_fused() else "ppo_adam_clip_f32"
+    assert names.count(adam) == steps and names.count("ppo_adam_clip_f32") + names.count("ppo_adam_clip_wt_f32") == steps
     assert names.count("ppo_loss_finalize_steps") == 1 and "ppo_loss_finalize" not in names
     assert names.count("ppo_sumsq_total") == (0 if ex.nchunks <= ex.FOLD_NORM_MAX else steps)
     if prog.bf16:
@@ -69,9 +71,12 @@ def test_recorded_launches_match_the_c_signatures(config):
     else:
         # every fp32 workload has torso features in front of its heads: the fused kernel runs (for
         # the Gaussian towers' chains, inside the forward chain's launch)
-        fused = names.count("ppo_head_loss_f32") + names.count("ppo_mlp_ln_fwd_head_loss_f32")
+        # the Gaussian towers' chains, inside the forward chain's launch; after the first step
+        # with the backward chain too)
+        chained = names.count("ppo_mlp_ln_fwd_head_loss_f32") + names.count("ppo_mlp_ln_fwd_head_loss_bwd_f32")
+        fused = names.count("ppo_head_loss_f32") + chained
         assert fused == steps and "ppo_loss_f32" not in names
-        assert (names.count("ppo_mlp_ln_fwd_head_loss_f32") == steps) == (config == 3)
+        assert (chained == steps) == (config == 3)
     assert names[-1] == "ppo_count_advance"
     for name, args in calls:
         _, argtypes = _lib.SIGNATURES[name]
@@ -260,6 +265,58 @@ def check_final_gradient_tables(ex, flat, args, adam_calls):
         assert a[7] == fin["SUMSQ"].data_ptr() and a[8] == tiles + fin["nchunks"]
 
 
+class UnfusedChainExecutor(MLPExecutor):
+    """Paired towers whose forward (with the heads + loss) and backward chains
+    are separate launches at every step."""
+    FWD_BWD_FUSED = False
+
+
+def check_fused_forward_backward(ex, flat, calls):
+    """The second step's fused launch: the first step's forward + head-loss
+    arguments, with the transposed kernels as the backward's operand and the
+    backward chain's own outputs; each Adam step keeps those kernels
+    transposed (actor then critic per layer from layer 1)."""
+    names = [n for n, _ in calls]
+    first = [a for n, a in calls if n == "ppo_mlp_ln_fwd_head_loss_f32"]
+    fused = [a for n, a in calls if n == "ppo_mlp_ln_fwd_head_loss_bwd_f32"]
+    bwd = [a for n, a in calls if n == "ppo_mlp_ln_bwd_f32"]
+    assert len(first) == len(fused) == len(bwd) == 1
+    assert names.index("ppo_mlp_ln_fwd_head_loss_bwd_f32") > names.index("ppo_adam_clip_wt_f32")
+    c = ex._chain
+    f, u = fused[0], first[0]
+    assert len(f) == len(u) + 3
+    # same chain and head arguments except the step's gather indices and statistics
+    same = [k for k in range(len(u)) if k not in (5, 29, 65)]
+    assert [f[k] for k in same] == [u[k] for k in same]
+    assert f[25] == c["WT"] and f[26] == 256 * 256
+    assert list(f[-3:]) == [c["dZ"], c["part"], ex._chain_ps]
+    # the backward reads the heads' input cotangents: dha and dhc = dha + stride_rows
+    b = bwd[0]
+    assert f[53] == b[3] and f[58] - f[53] == 4 * ex._chain_rs and f[54] == f[59] == b[4]
+    for a in [a for n, a in calls if n == "ppo_adam_clip_wt_f32"]:
+        n, offs, dsts = a[17], a[18], a[19]
+        L = len(ex.actor)
+        assert n == 2 * (L - 1)
+        got_o = list((ctypes.c_int64 * n).from_address(offs))
+        got_d = list((ctypes.c_void_p * n).from_address(dsts))
+        want = [(lb.spec.dense.w.offset, ex.WT[l - 1, t].data_ptr())
+                for l in range(1, L) for t, lb in enumerate((ex.actor[l], ex.critic[l]))]
+        assert list(zip(got_o, got_d)) == want
+
+
+def test_gaussian_update_without_the_fused_chains_runs_them_per_step():
+    r = small(3)
+    prog = Program(r.network.plan(r.obs_dim))
+    flat = FlatState(prog, torch.device("cpu"))
+    ex = executor(r, prog, flat, cls=UnfusedChainExecutor)
+    ex.bind(fake_inputs(ex))
+    names = [n for n, _ in ex.record()]
+    steps = r.cfg.update_epochs * r.cfg.num_minibatches
+    assert names.count("ppo_mlp_ln_fwd_head_loss_f32") == steps and names.count("ppo_mlp_ln_bwd_f32") == steps
+    assert "ppo_mlp_ln_fwd_head_loss_bwd_f32" not in names and "ppo_adam_clip_wt_f32" not in names
+    assert names.count("ppo_adam_clip_f32") == steps
+
+
 def test_gaussian_update_without_the_finishing_launch_reduces_its_gradients():
     r = small(3)
     prog = Program(r.network.plan(r.obs_dim))
@@ -270,7 +327,7 @@ def test_gaussian_update_without_the_finishing_launch_reduces_its_gradients():
     steps = r.cfg.update_epochs * r.cfg.num_minibatches
     assert ex.dw_final is None and "ppo_gemm_f32_dw_group_final" not in names
     assert names.count("ppo_gemm_f32_dw_group") == steps and names.count("ppo_grad_reduce") == steps
-    adam = [a for n, a in ex.record(max_steps=1) if n == "ppo_adam_clip_f32"]
+    adam = [a for n, a in ex.record(max_steps=1) if n in ("ppo_adam_clip_f32", "ppo_adam_clip_wt_f32")]
     assert adam[0][7] == ex.SUMSQ.data_ptr() and adam[0][8] == ex.nchunks
 
 
@@ -288,16 +345,20 @@ def test_gaussian_update_runs_each_torso_chain_in_one_launch():
     # launch, the backward chain and every weight gradient of both towers in
     # one launch; the critic's bootstrap chain once
     calls = ex.record(max_steps=1)
-    assert names.count("ppo_mlp_ln_fwd_head_loss_f32") == steps and "ppo_head_loss_f32" not in names
+    # (from the second step on, the backward chain runs in the forward's launch)
+    assert names.count("ppo_mlp_ln_fwd_head_loss_f32") == 1 and "ppo_head_loss_f32" not in names
+    assert names.count("ppo_mlp_ln_fwd_head_loss_bwd_f32") == steps - 1
     assert names.count("ppo_mlp_ln_fwd_f32") == 1
-    assert names.count("ppo_mlp_ln_bwd_f32") == steps
+    assert names.count("ppo_mlp_ln_bwd_f32") == 1
     # ... which also assembles the gradients: no reduce launch per step
     assert names.count("ppo_gemm_f32_dw_group_final") == steps and "ppo_gemm_f32_towers" not in names
     assert "ppo_gemm_f32_dw_group" not in names and "ppo_grad_reduce" not in names
     assert names.count("ppo_pad_rows_f32") == 1   # the padded observation copy, once per update
     dwg = [a for n, a in calls if n == "ppo_gemm_f32_dw_group_final"]
     assert len(dwg) == 1 and dwg[0][1] == 2 * len(ex.actor)
-    check_final_gradient_tables(ex, flat, dwg[0], [a for n, a in calls if n == "ppo_adam_clip_f32"])
+    adam = [a for n, a in calls if n == "ppo_adam_clip_wt_f32"]
+    assert len(adam) == 1
+    check_final_gradient_tables(ex, flat, dwg[0], adam)
     g = ex._dwg
     fwd = [a for n, a in calls if n == "ppo_mlp_ln_fwd_head_loss_f32"][0]
     idx = fwd[5]   # the step's gather indices
@@ -350,6 +411,7 @@ def test_gaussian_update_runs_each_torso_chain_in_one_launch():
     # the bootstrap chain runs the critic's own layers
     for l, lb in enumerate(ex.boot_layers):
         assert T["bW"][l] == flat.view(ex.critic[l].spec.dense.w) and T["bY"][l] == lb.Y.data_ptr()
+    check_fused_forward_backward(ex, flat, ex.record(max_steps=2))
 
 
 def test_gaussian_update_pairs_its_towers_layer_by_layer():
