@@ -504,7 +504,7 @@ PPO_EXPORT int ppo_gemm_f32_dw_group_final(void* stream, int count, const float*
   if (nchunks < 0 || nfew < 0 || nwide < 0 || nfew + nwide > nchunks || (nchunks > 0 && (!segs || !chunks)))
     return ppo::set_error(PPO_ERR_ARG, "%s: bad segment tables (nchunks=%d nfew=%d nwide=%d)", name, nchunks, nfew,
                           nwide);
-  F32Final f = {};
+  ppo_gr::DwFinal f = {};
   int slot = 0;
   for (int i = 0; i < count; ++i) {
     const GemmParams& p = g.p[i];
@@ -525,6 +525,7 @@ PPO_EXPORT int ppo_gemm_f32_dw_group_final(void* stream, int count, const float*
     f.g_rows[i] = g_rows[i];
     f.Gb[i] = with_bias ? Gb[i] : nullptr;
     f.slot0[i] = slot;
+    f.splits[i] = p.splits;
     slot += g.gx[i] * g.gy[i];
   }
   f.counters = counters;

@@ -2,7 +2,7 @@
 // gemm_f32d.hip: pipeline fed by direct global -> LDS copies): parameters
 // and the epilogue.
 #pragma once
-#include "common.h"
+#include "grad_reduce.h"
 
 namespace ppo_f32 {
 
@@ -143,25 +143,6 @@ __device__ __forceinline__ void epilogue_f32(const GemmParams& p, floatx16 (&acc
 #undef PPO_EPI_ACTS
 }
 
-// A weight-gradient group that finishes its own split-K sums
-// (ppo_gemm_f32_dw_group_final): the last split of each output tile to
-// arrive (a per-tile arrival counter) sums the tile's partials in the
-// gradient-assembly launch's fixed order (ppo_gr::fixed_sum) into the final
-// gradient and writes the tile's squared-norm partial; workgroups placed
-// before the tiles run the gradient-assembly blocks of the other segments.
-struct F32Final {
-  float* G[F32_GROUP_MAX];    // problem i's final gradient, [g_rows][ldg]
-  int64_t ldg[F32_GROUP_MAX];
-  int g_rows[F32_GROUP_MAX];  // rows of the gradient (<= M: a zero-padded input's extra rows are dropped)
-  float* Gb[F32_GROUP_MAX];   // final bias gradient [N] (problems with bias partials)
-  int slot0[F32_GROUP_MAX];   // problem i's first tile: its counter and sumsq index
-  unsigned* counters;         // one per tile, zero between launches
-  double* sumsq;
-  const void* segs;           // the other segments (ppo_gr tables), reduced by rblocks workgroups
-  const void* chunks;
-  int nchunks, nfew, nwide, rblocks, rpad;  // rpad: rblocks rounded up to a multiple of 8
-};
-
 // The copy-fed pipeline (gemm_f32d.hip): 16-byte rows along every operand's
 // contiguous axis, stage depth F32D_BK; false when the shape needs the
 // register-staged one (a gathered k-outer A with more reduction rows per
@@ -177,6 +158,6 @@ int launch_dw_group(hipStream_t st, const F32Group& g);
 constexpr int F32D_FINAL_KIDX = 512;
 constexpr int F32D_FINAL_PARTS = 16;
 bool final_parts_supported(int splits);
-int launch_dw_group_final(hipStream_t st, const F32Group& g, const F32Final& f);
+int launch_dw_group_final(hipStream_t st, const F32Group& g, const ppo_gr::DwFinal& f);
 
 }  // namespace ppo_f32

@@ -307,78 +307,11 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_group_kernel(F32Group 
                                                  local / (g.gx[i] * g.gy[i]));
 }
 
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-constexpr int SC1 = 16;  // cache policy of a device-coherent buffer access
-
-// The tile's split-K sum, finished by the last of its splits to arrive.
-// Thread t owns float4 t + 256 i (i < 4) of the 64 x 64 tile (row (t + 256 i)
-// / 16, columns 4 ((t + 256 i) % 16) ...): P of them at a time with all S
-// partial loads in flight (device-coherent loads: the partials of other
-// XCDs' workgroups), summed by ppo_gr::fixed_sum.
-template <int S>
-__device__ __forceinline__ void finish_tile(const GemmParams& p, const F32Final& f, int prob, int tm, int tn,
-                                            int slot, double* s_w) {
-  constexpr int BM = 64, BN = 64, POS = BM * BN / 4 / 256;
-  constexpr int P = S <= 4 ? 4 : S <= 8 ? 2 : 1;
-  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(p.C, (short)0, 0x7fffffff, 0x00020000);
-  const int t = threadIdx.x;
-  const int rows = f.g_rows[prob];
-  double sq = 0.0;
-#pragma unroll
-  for (int i0 = 0; i0 < POS; i0 += P) {
-    floatx4 v[P][S];
-    bool live[P];
-    int64_t dst[P];
-#pragma unroll
-    for (int u = 0; u < P; ++u) {
-      const int e = t + 256 * (i0 + u);
-      const int gm = tm * BM + e / (BN / 4), gn = tn * BN + 4 * (e % (BN / 4));
-      live[u] = gm < rows && gn < p.N;
-      dst[u] = (int64_t)gm * f.ldg[prob] + gn;
-      const int off = live[u] ? (int)(4 * ((int64_t)gm * p.ldc + gn)) : 0;
-#pragma unroll
-      for (int q = 0; q < S; ++q)
-        v[u][q] = __builtin_bit_cast(
-            floatx4, __builtin_amdgcn_raw_buffer_load_b128(rc, off + (int)(4 * q * p.c_split_stride), 0, SC1));
-    }
-#pragma unroll
-    for (int u = 0; u < P; ++u) {
-      if (!live[u]) continue;
-      const floatx4 g = ppo_gr::fixed_sum<S>(v[u]);
-      *reinterpret_cast<floatx4*>(f.G[prob] + dst[u]) = g;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sq += (double)g[e] * (double)g[e];
-    }
-  }
-  // the bias gradient's 64 columns with the first tile row
-  if (tm == 0 && p.bias_grad && f.Gb[prob] && t < BN / 4) {
-    const int gn = tn * BN + 4 * t;
-    if (gn < p.N) {
-      const __amdgpu_buffer_rsrc_t rb =
-          __builtin_amdgcn_make_buffer_rsrc(p.bias_grad, (short)0, 0x7fffffff, 0x00020000);
-      floatx4 v[S];
-#pragma unroll
-      for (int q = 0; q < S; ++q)
-        v[q] = __builtin_bit_cast(floatx4,
-                                  __builtin_amdgcn_raw_buffer_load_b128(rb, (int)(4 * ((int64_t)q * p.N + gn)), 0, SC1));
-      const floatx4 g = ppo_gr::fixed_sum<S>(v);
-      *reinterpret_cast<floatx4*>(f.Gb[prob] + gn) = g;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sq += (double)g[e] * (double)g[e];
-    }
-  }
-  // the tile's squared-norm partial: wave sums, then the waves in order
-  sq = ppo::wave_sum_d(sq);
-  if ((t & 63) == 0) s_w[t >> 6] = sq;
-  __syncthreads();
-  if (t == 0) f.sumsq[slot] = (s_w[0] + s_w[1]) + (s_w[2] + s_w[3]);
-}
-
 // The split-K counts the finishing sum is compiled for.
 #define PPO_F32_FINAL_PARTS(X) X(1) X(2) X(3) X(4) X(6) X(8) X(12) X(16)
 
 template <int BM, int BN, int WM, int WN, int NBUF, int KIDX>
-__global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_group_final_kernel(F32Group g, F32Final f) {
+__global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_group_final_kernel(F32Group g, ppo_gr::DwFinal f) {
   static_assert(BM == 64 && BN == 64 && WM * WN == 4, "the finishing sum assumes 64 x 64 tiles of 4 waves");
   __shared__ floatx4 s_part[4][64];
   __shared__ double s_w[4];
@@ -404,25 +337,21 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_group_final_kernel(F32
   const int tm = (local / g.gx[i]) % g.gy[i], tn = local % g.gx[i];
   gemm_f32d_tile<BM, BN, WM, WN, false, false, NBUF, KIDX, true>(p, tm, tn, local / (g.gx[i] * g.gy[i]));
   // every wave's partial stores complete, then one arrival for the tile
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  const int tile = tm * g.gx[i] + tn;
-  const int slot = f.slot0[i] + tile;
-  if (threadIdx.x == 0) {
-    const unsigned seen = __hip_atomic_fetch_add(f.counters + slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = seen + 1 == (unsigned)p.splits;
-    if (last) __hip_atomic_store(f.counters + slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = last;
-  }
-  __syncthreads();
-  if (!s_last) return;
+  const int slot = f.slot0[i] + tm * g.gx[i] + tn;
+  if (!ppo_gr::arrive_last(f.counters + slot, p.splits, &s_last)) return;
+  double sq = 0.0;
   switch (p.splits) {
-#define PPO_F32_FINAL_CASE(S) \
-  case S: finish_tile<S>(p, f, i, tm, tn, slot, s_w); break;
+#define PPO_F32_FINAL_CASE(S)                                                                                     \
+  case S:                                                                                                         \
+    sq = ppo_gr::finish_tile_sum<BM, BN, WM * WN * 64, S, 16>(p.C, p.ldc, p.c_split_stride, f.g_rows[i], p.N, tm, \
+                                                              tn, f.G[i] + 0, f.ldg[i], false, p.bias_grad,      \
+                                                              f.Gb[i]);                                           \
+    break;
     PPO_F32_FINAL_PARTS(PPO_F32_FINAL_CASE)
 #undef PPO_F32_FINAL_CASE
     default: break;  // rejected by the host
   }
+  ppo_gr::block_sumsq<WM * WN * 64>(sq, s_w, f.sumsq + slot);
 }
 
 template <int BM, int BN, int WM, int WN, bool A_K, bool B_K>
@@ -465,7 +394,7 @@ bool final_parts_supported(int splits) {
   }
 }
 
-int launch_dw_group_final(hipStream_t st, const F32Group& g, const F32Final& f) {
+int launch_dw_group_final(hipStream_t st, const F32Group& g, const ppo_gr::DwFinal& f) {
   const int total = g.start[g.count] + f.rpad;
   hipLaunchKernelGGL((gemm_f32d_group_final_kernel<64, 64, 2, 2, 2, F32D_FINAL_KIDX>), dim3(total), dim3(256), 0, st,
                      g, f);

@@ -214,4 +214,128 @@ __device__ __forceinline__ floatx4 fixed_sum(const floatx4 (&v)[S]) {
   }
 }
 
+// A weight-gradient launch that finishes its own split-K sums: the last
+// split of each output tile to arrive (a per-tile arrival counter) sums the
+// tile's partials in the fixed order above into the final gradient and
+// writes the tile's squared-norm partial; workgroups placed before the tiles
+// reduce the table's other segments.
+constexpr int DW_FINAL_MAX = 8;
+struct DwFinal {
+  float* G[DW_FINAL_MAX];    // problem i's final gradient, [g_rows][ldg]
+  int64_t ldg[DW_FINAL_MAX];
+  int g_rows[DW_FINAL_MAX];  // rows of the gradient (<= M: a zero-padded input's extra rows are dropped)
+  float* Gb[DW_FINAL_MAX];   // final bias gradient [N] (problems with bias partials)
+  int slot0[DW_FINAL_MAX];   // problem i's first tile: its counter and sumsq index
+  int splits[DW_FINAL_MAX];  // problem i's split count
+  unsigned* counters;        // one per tile, zero between launches
+  double* sumsq;
+  const void* segs;          // the other segments, reduced by rblocks workgroups
+  const void* chunks;
+  int nchunks, nfew, nwide, rblocks, rpad;  // rpad: rblocks rounded up to a multiple of 8
+  int round_bf16;            // the gradients are rounded to bf16 (bf16 layers' parameters)
+};
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+constexpr int SC1 = 16;  // cache policy of a device-coherent buffer access
+
+// Largest power of two <= x (x >= 1).
+constexpr int pow2_floor(int x) { return x >= 2 ? 2 * pow2_floor(x / 2) : 1; }
+
+// The finishing sum of one BM x BN output tile (tile row tm, column tn) of
+// S split partials (fp32, row pitch ldc, split stride split_stride, written
+// device-coherent by other workgroups) into G (rows below rows_out, pitch
+// ldg; rounded to bf16 when round_bf16), and for the first tile row the bias
+// partials [S][N] (bias_part, or null) into Gb.  Thread t of NT owns float4
+// t + NT i of the tile; LOADS bounds a thread's partial loads in flight.
+// Returns the thread's sum of squares of the values it wrote.
+template <int BM, int BN, int NT, int S, int LOADS>
+__device__ __forceinline__ double finish_tile_sum(const float* C, int64_t ldc, int64_t split_stride, int rows_out,
+                                                  int N, int tm, int tn, float* G, int64_t ldg, bool round_bf16,
+                                                  const float* bias_part, float* Gb) {
+  constexpr int POS = BM * BN / 4 / NT;
+  constexpr int P0 = pow2_floor(LOADS / S > 0 ? LOADS / S : 1);
+  constexpr int P = P0 < POS ? P0 : POS;
+  static_assert(POS % P == 0, "positions per round must divide the tile's");
+  const __amdgpu_buffer_rsrc_t rc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(C), (short)0, 0x7fffffff, 0x00020000);
+  const int t = threadIdx.x;
+  double sq = 0.0;
+  auto store = [&](float* dst, floatx4 g) {
+    if (round_bf16) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) g[e] = ppo::bf16_round(g[e]);
+    }
+    *reinterpret_cast<floatx4*>(dst) = g;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sq += (double)g[e] * (double)g[e];
+  };
+#pragma unroll
+  for (int i0 = 0; i0 < POS; i0 += P) {
+    floatx4 v[P][S];
+    bool live[P];
+    int64_t dst[P];
+#pragma unroll
+    for (int u = 0; u < P; ++u) {
+      const int e = t + NT * (i0 + u);
+      const int gm = tm * BM + e / (BN / 4), gn = tn * BN + 4 * (e % (BN / 4));
+      live[u] = gm < rows_out && gn < N;
+      dst[u] = (int64_t)gm * ldg + gn;
+      const int off = live[u] ? (int)(4 * ((int64_t)gm * ldc + gn)) : 0;
+#pragma unroll
+      for (int q = 0; q < S; ++q)
+        v[u][q] = __builtin_bit_cast(
+            floatx4, __builtin_amdgcn_raw_buffer_load_b128(rc, off + (int)(4 * q * split_stride), 0, SC1));
+    }
+#pragma unroll
+    for (int u = 0; u < P; ++u)
+      if (live[u]) store(G + dst[u], fixed_sum<S>(v[u]));
+  }
+  if (tm == 0 && bias_part && Gb && t < BN / 4) {
+    const int gn = tn * BN + 4 * t;
+    if (gn < N) {
+      const __amdgpu_buffer_rsrc_t rb =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(bias_part), (short)0, 0x7fffffff, 0x00020000);
+      floatx4 v[S];
+#pragma unroll
+      for (int q = 0; q < S; ++q)
+        v[q] = __builtin_bit_cast(floatx4,
+                                  __builtin_amdgcn_raw_buffer_load_b128(rb, (int)(4 * ((int64_t)q * N + gn)), 0, SC1));
+      store(Gb + gn, fixed_sum<S>(v));
+    }
+  }
+  return sq;
+}
+
+// A workgroup's arrival at its tile once its partial stores (device-coherent)
+// are complete: true for the last of the tile's splits, which then resets the
+// counter.  s_last: one int of LDS.
+__device__ __forceinline__ bool arrive_last(unsigned* counter, int splits, int* s_last) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned seen = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = seen + 1 == (unsigned)splits;
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_last = last;
+  }
+  __syncthreads();
+  return *s_last != 0;
+}
+
+// The squared-norm partial of a workgroup of NT threads (each thread's sq):
+// wave sums, then the waves in order, written by thread 0.  s_w: NT / 64
+// doubles of LDS.
+template <int NT>
+__device__ __forceinline__ void block_sumsq(double sq, double* s_w, double* out) {
+  sq = ppo::wave_sum_d(sq);
+  if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = sq;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double tot = s_w[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; ++w) tot += s_w[w];
+    *out = tot;
+  }
+}
+
 }  // namespace ppo_gr

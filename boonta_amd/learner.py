@@ -1180,20 +1180,6 @@ class MLPExecutor(ForwardChain):
         }
         order = ("A", "lda", "rows", "B", "ldb", "C", "ldc", "M", "N", "K", "splits", "stride", "bias_grad")
         g["args"] = [ctypes.addressof(g[k]) for k in order]
-        fin = self.dw_final
-        if fin is not None:
-            # the final gradients: problem order as above
-            G = self.flat.G.data_ptr()
-            lbs = [lb for i in range(len(A)) for lb in (A[i], C[i])]
-            g.update({
-                "G": vp([G + 4 * lb.spec.dense.w.offset for lb in lbs]),
-                "ldg": i64([lb.spec.dense.w.ld for lb in lbs]),
-                "g_rows": i32([lb.spec.dense.fin for lb in lbs]),
-                "Gb": vp([G + 4 * lb.spec.dense.b.offset if lb.spec.dense.b is not None else None for lb in lbs]),
-            })
-            g["final_args"] = g["args"] + [ctypes.addressof(g[k]) for k in ("G", "ldg", "g_rows", "Gb")] + [
-                _p(fin["CNT"]), _p(fin["SUMSQ"]), _p(fin["SEGS"]), _p(fin["CHUNKS"]), fin["nchunks"], fin["nfew"],
-                fin["nwide"]]
         return g
 
     def _bwd_layers(self, st, layers, x0, ldx0, idx0):

@@ -30,9 +30,10 @@ def host(t):
     return t.detach().cpu().numpy()
 
 
-def tables(segs, slot0):
+def tables(segs, slot0, flags=0):
     """Device segment / chunk tables in the reduce's layout (the learner's
-    packing): (SEGS, CHUNKS, nchunks, nfew, nwide)."""
+    packing): (SEGS, CHUNKS, nchunks, nfew, nwide); flags 1 rounds the sums
+    to bf16."""
     lib = _lib.load()
     chunk, wide_chunk = lib.ppo_grad_reduce_chunk_elems(), lib.ppo_grad_reduce_wide_chunk_elems()
     few_parts, wide_parts = lib.ppo_grad_reduce_few_parts(), lib.ppo_grad_reduce_wide_parts()
@@ -41,7 +42,7 @@ def tables(segs, slot0):
         dst = few if n <= few_parts else wide if n > wide_parts else many
         for start in range(0, c, wide_chunk if dst is wide else chunk):
             dst.append(struct.pack("<iiq", i, slot0 + len(few) + len(many) + len(wide), start))
-    seg_bytes = b"".join(struct.pack("<QQqqii", d, s, c, ps, n, 0) for d, s, c, ps, n in segs)
+    seg_bytes = b"".join(struct.pack("<QQqqii", d, s, c, ps, n, flags) for d, s, c, ps, n in segs)
     chunks = few + many + wide
     t = lambda b: torch.tensor(list(b) or [0], dtype=torch.uint8, device=DEV)
     return t(seg_bytes), t(b"".join(chunks)), len(chunks), len(few), len(wide)
@@ -195,3 +196,4 @@ def test_final_group_rejects_unsupported_shapes():
     gidx = dev(np.arange(p[5], dtype=np.int32))
     assert call(splits=2, idx=gidx) != 0   # a gathered split of 1024 rows (at most 512)
     torch.cuda.synchronize()
+

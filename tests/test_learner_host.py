@@ -63,7 +63,12 @@ def test_recorded_launches_match_the_c_signatures(config):
     adam = "ppo_adam_clip_wt_f32" if ex.pair and ex._fwd_bwd_fused() else "ppo_adam_clip_f32"
     assert names.count(adam) == steps and names.count("ppo_adam_clip_f32") + names.count("ppo_adam_clip_wt_f32") == steps
     assert names.count("ppo_loss_finalize_steps") == 1 and "ppo_loss_finalize" not in names
-    assert names.count("ppo_sumsq_total") == (0 if ex.nchunks <= ex.FOLD_NORM_MAX else steps)
+    # the norm's partials: the reduce's chunks, or, where the weight-gradient launch assembles the
+    # gradients (the Gaussian towers' and the bf16 trunk's grouped launches), its tiles' and the rest's
+    fin = ex.dw_final
+    nsq = fin["T"] + fin["nchunks"] if fin is not None else ex.nchunks
+    assert names.count("ppo_sumsq_total") == (0 if nsq <= ex.FOLD_NORM_MAX else steps)
+    assert names.count("ppo_grad_reduce") == (0 if fin is not None else steps)
     if prog.bf16:
         # 43 actions: the unfused head GEMM + loss + head backward, every GEMM on bf16 MFMA
         assert names.count("ppo_loss_f32") == steps and "ppo_gemm_f32" not in names
