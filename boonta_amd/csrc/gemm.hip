@@ -481,11 +481,14 @@ PPO_EXPORT int ppo_gemm_f32_dw_final_slots(int count, const int* M, const int* N
 // squared-norm partial at sumsq[slot] (slots and counters numbered as
 // ppo_gemm_f32_dw_final_slots counts them).  The segments in segs / chunks
 // (ppo_grad_reduce's tables, their chunk slots after the tiles') are reduced
-// by workgroups of the same launch.  counters: one zeroed unsigned per tile,
-// left zeroed.  The gradients are the same bits as ppo_gemm_f32_dw_group +
+// by workgroups of the same launch.  counters: nine zeroed unsigneds per
+// tile (one per tile, then eight per tile for the two-level sums of 32 or 64
+// splits), left zeroed.  The gradients are the same bits as ppo_gemm_f32_dw_group +
 // ppo_grad_reduce over the same segments (the norm partials are grouped by
 // tile instead of by chunk).  Splits per problem: 1, 2, 3,
-// 4, 6, 8, 12 or 16; gathered splits of at most F32D_FINAL_KIDX rows.
+// 4, 6, 8, 12, 16 (one level), 32 or 64 (the last of each group of eight
+// splits sums it, the last group the group sums); gathered splits of at most
+// F32D_FINAL_KIDX rows.
 PPO_EXPORT int ppo_gemm_f32_dw_group_final(void* stream, int count, const float* const* A, const int64_t* lda,
                                            const int32_t* const* rows, const float* const* B, const int64_t* ldb,
                                            float* const* C, const int64_t* ldc, const int* M, const int* N,
@@ -509,8 +512,8 @@ PPO_EXPORT int ppo_gemm_f32_dw_group_final(void* stream, int count, const float*
   for (int i = 0; i < count; ++i) {
     const GemmParams& p = g.p[i];
     if (!final_parts_supported(p.splits))
-      return ppo::set_error(PPO_ERR_ARG, "%s: problem %d: %d splits (supported: 1, 2, 3, 4, 6, 8, 12, 16)", name, i,
-                            p.splits);
+      return ppo::set_error(PPO_ERR_ARG, "%s: problem %d: %d splits (supported: 1, 2, 3, 4, 6, 8, 12, 16, 32, 64)",
+                            name, i, p.splits);
     if (!G[i] || !aligned16(G[i]) || ldg[i] % 4 || ldg[i] < p.N || g_rows[i] < 1 || g_rows[i] > p.M)
       return ppo::set_error(PPO_ERR_ARG, "%s: problem %d: bad gradient (g_rows=%d of M=%d, ldg=%lld)", name, i,
                             g_rows[i], p.M, (long long)ldg[i]);
@@ -529,6 +532,7 @@ PPO_EXPORT int ppo_gemm_f32_dw_group_final(void* stream, int count, const float*
     slot += g.gx[i] * g.gy[i];
   }
   f.counters = counters;
+  f.ntiles = slot;
   f.sumsq = sumsq;
   f.segs = segs;
   f.chunks = chunks;

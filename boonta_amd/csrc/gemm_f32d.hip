@@ -316,17 +316,19 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_group_final_kernel(F32
   __shared__ floatx4 s_part[4][64];
   __shared__ double s_w[4];
   __shared__ int s_last;
-  if ((int)blockIdx.x < f.rpad) {
-    // the other segments, whose partials are complete before this launch
-    if ((int)blockIdx.x < f.rblocks)
-      ppo_gr::reduce_block((int)blockIdx.x, static_cast<const ppo_gr::Segment*>(f.segs),
+  // the tiles first, then the workgroups of the other segments (whose
+  // partials are complete before this launch): dispatched behind the tiles,
+  // they do not hold back the tiles' start
+  const int total = gridDim.x - f.rpad;
+  if ((int)blockIdx.x >= total) {
+    const int b = (int)blockIdx.x - total;
+    if (b < f.rblocks)
+      ppo_gr::reduce_block(b, static_cast<const ppo_gr::Segment*>(f.segs),
                            static_cast<const ppo_gr::Chunk*>(f.chunks), f.nchunks, f.nfew, f.nwide, f.sumsq, s_part);
     return;
   }
-  // tiles as in gemm_f32d_group_kernel (rpad is a multiple of 8, so w & 7
-  // is still the XCD the workgroup runs on)
-  const int total = gridDim.x - f.rpad;
-  const int w = blockIdx.x - f.rpad;
+  // tiles as in gemm_f32d_group_kernel
+  const int w = blockIdx.x;
   const int x = w & 7, j = w >> 3;
   const int q = total >> 3, r = total & 7;
   const int t = x * q + (x < r ? x : r) + j;
@@ -338,8 +340,25 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32d_group_final_kernel(F32
   gemm_f32d_tile<BM, BN, WM, WN, false, false, NBUF, KIDX, true>(p, tm, tn, local / (g.gx[i] * g.gy[i]));
   // every wave's partial stores complete, then one arrival for the tile
   const int slot = f.slot0[i] + tm * g.gx[i] + tn;
-  if (!ppo_gr::arrive_last(f.counters + slot, p.splits, &s_last)) return;
   double sq = 0.0;
+  if (p.splits == 32 || p.splits == 64) {
+    // two levels: the last of each group of eight splits sums the group,
+    // the last group the group sums
+    const int grp = (local / (g.gx[i] * g.gy[i])) >> 3;
+    if (!ppo_gr::arrive_last(f.counters + f.ntiles + 8 * slot + grp, 8, &s_last)) return;
+    ppo_gr::finish_group8<BM, BN, WM * WN * 64>(p.C, p.ldc, p.c_split_stride, f.g_rows[i], p.N, tm, tn, grp,
+                                                p.bias_grad);
+    if (!ppo_gr::arrive_last(f.counters + slot, p.splits / 8, &s_last)) return;
+    if (p.splits == 32)
+      sq = ppo_gr::finish_level2<BM, BN, WM * WN * 64, 4>(p.C, p.ldc, p.c_split_stride, f.g_rows[i], p.N, tm, tn,
+                                                          f.G[i], f.ldg[i], p.bias_grad, f.Gb[i]);
+    else
+      sq = ppo_gr::finish_level2<BM, BN, WM * WN * 64, 8>(p.C, p.ldc, p.c_split_stride, f.g_rows[i], p.N, tm, tn,
+                                                          f.G[i], f.ldg[i], p.bias_grad, f.Gb[i]);
+    ppo_gr::block_sumsq<WM * WN * 64>(sq, s_w, f.sumsq + slot);
+    return;
+  }
+  if (!ppo_gr::arrive_last(f.counters + slot, p.splits, &s_last)) return;
   switch (p.splits) {
 #define PPO_F32_FINAL_CASE(S)                                                                                     \
   case S:                                                                                                         \
@@ -384,6 +403,7 @@ int launch_dw_group(hipStream_t st, const F32Group& g) {
 }
 
 bool final_parts_supported(int splits) {
+  if (splits == 32 || splits == 64) return true;   // two-level sums
   switch (splits) {
 #define PPO_F32_FINAL_CASE(S) \
   case S:

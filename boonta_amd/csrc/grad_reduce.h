@@ -227,7 +227,8 @@ struct DwFinal {
   float* Gb[DW_FINAL_MAX];   // final bias gradient [N] (problems with bias partials)
   int slot0[DW_FINAL_MAX];   // problem i's first tile: its counter and sumsq index
   int splits[DW_FINAL_MAX];  // problem i's split count
-  unsigned* counters;        // one per tile, zero between launches
+  unsigned* counters;        // one per tile, then (two-level sums) eight per tile; zero between launches
+  int ntiles;                // tiles of the launch (the second block of counters starts there)
   double* sumsq;
   const void* segs;          // the other segments, reduced by rblocks workgroups
   const void* chunks;
@@ -301,6 +302,109 @@ __device__ __forceinline__ double finish_tile_sum(const float* C, int64_t ldc, i
         v[q] = __builtin_bit_cast(floatx4,
                                   __builtin_amdgcn_raw_buffer_load_b128(rb, (int)(4 * ((int64_t)q * N + gn)), 0, SC1));
       store(Gb + gn, fixed_sum<S>(v));
+    }
+  }
+  return sq;
+}
+
+// The first level of a two-level finishing sum (32 or 64 splits): the sum
+// of splits 8 grp .. 8 grp + 7 of the tile (and of their bias partials for the
+// first tile row) as tree8 — the reduce's sum of those eight partials — stored
+// device-coherent over split 8 grp's partial (which no one reads after this).
+template <int BM, int BN, int NT>
+__device__ __forceinline__ void finish_group8(float* C, int64_t ldc, int64_t split_stride, int rows_out, int N,
+                                              int tm, int tn, int grp, float* bias_part) {
+  constexpr int POS = BM * BN / 4 / NT;
+  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(C, (short)0, 0x7fffffff, 0x00020000);
+  const int t = threadIdx.x;
+  const int q0 = 8 * grp;
+#pragma unroll
+  for (int i = 0; i < POS; ++i) {
+    const int e = t + NT * i;
+    const int gm = tm * BM + e / (BN / 4), gn = tn * BN + 4 * (e % (BN / 4));
+    if (gm >= rows_out || gn >= N) continue;
+    const int off = (int)(4 * ((int64_t)gm * ldc + gn));
+    floatx4 v[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      v[q] = __builtin_bit_cast(
+          floatx4, __builtin_amdgcn_raw_buffer_load_b128(rc, off + (int)(4 * (q0 + q) * split_stride), 0, SC1));
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, tree8(v)), rc,
+                                           off + (int)(4 * q0 * split_stride), 0, SC1);
+  }
+  if (tm == 0 && bias_part && t < BN / 4) {
+    const int gn = tn * BN + 4 * t;
+    if (gn < N) {
+      const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(bias_part, (short)0, 0x7fffffff, 0x00020000);
+      floatx4 v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        v[q] = __builtin_bit_cast(
+            floatx4, __builtin_amdgcn_raw_buffer_load_b128(rb, (int)(4 * ((int64_t)(q0 + q) * N + gn)), 0, SC1));
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, tree8(v)), rb,
+                                             (int)(4 * ((int64_t)q0 * N + gn)), 0, SC1);
+    }
+  }
+}
+
+// The second level for S = 8 GR splits: the GR group sums g_k (at split
+// 8 k's partial) added as the reduce adds an S-part segment — quarter w is
+// 0 + the tree8 sums of its eight-partial groups in order, then the quarters
+// in order — into G / Gb as finish_tile_sum does.
+template <int BM, int BN, int NT, int GR>
+__device__ __forceinline__ double finish_level2(const float* C, int64_t ldc, int64_t split_stride, int rows_out,
+                                                int N, int tm, int tn, float* G, int64_t ldg,
+                                                const float* bias_part, float* Gb) {
+  static_assert(GR == 4 || GR == 8, "two-level sums of 32 or 64 splits");
+  constexpr int POS = BM * BN / 4 / NT;
+  const __amdgpu_buffer_rsrc_t rc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(C), (short)0, 0x7fffffff, 0x00020000);
+  const int t = threadIdx.x;
+  const floatx4 z = {0.f, 0.f, 0.f, 0.f};
+  double sq = 0.0;
+  auto combine = [&](const floatx4 (&g)[GR]) {
+    floatx4 quarter[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      floatx4 acc = z;
+#pragma unroll
+      for (int k = GR * w / 4; k < GR * (w + 1) / 4; ++k) acc += g[k];
+      quarter[w] = acc;
+    }
+    floatx4 r = quarter[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) r += quarter[w];
+    return r;
+  };
+  auto store = [&](float* dst, floatx4 v) {
+    *reinterpret_cast<floatx4*>(dst) = v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sq += (double)v[e] * (double)v[e];
+  };
+#pragma unroll
+  for (int i = 0; i < POS; ++i) {
+    const int e = t + NT * i;
+    const int gm = tm * BM + e / (BN / 4), gn = tn * BN + 4 * (e % (BN / 4));
+    if (gm >= rows_out || gn >= N) continue;
+    const int off = (int)(4 * ((int64_t)gm * ldc + gn));
+    floatx4 g[GR];
+#pragma unroll
+    for (int k = 0; k < GR; ++k)
+      g[k] = __builtin_bit_cast(floatx4,
+                                __builtin_amdgcn_raw_buffer_load_b128(rc, off + (int)(4 * 8 * k * split_stride), 0, SC1));
+    store(G + (int64_t)gm * ldg + gn, combine(g));
+  }
+  if (tm == 0 && bias_part && Gb && t < BN / 4) {
+    const int gn = tn * BN + 4 * t;
+    if (gn < N) {
+      const __amdgpu_buffer_rsrc_t rb =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(bias_part), (short)0, 0x7fffffff, 0x00020000);
+      floatx4 g[GR];
+#pragma unroll
+      for (int k = 0; k < GR; ++k)
+        g[k] = __builtin_bit_cast(
+            floatx4, __builtin_amdgcn_raw_buffer_load_b128(rb, (int)(4 * ((int64_t)8 * k * N + gn)), 0, SC1));
+      store(Gb + gn, combine(g));
     }
   }
   return sq;

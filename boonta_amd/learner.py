@@ -920,7 +920,36 @@ class MLPExecutor(ForwardChain):
     # grouped launch (no gradient-reduce launch for them); the split counts
     # that launch supports
     DW_FINAL = True
-    FINAL_SPLITS = (1, 2, 3, 4, 6, 8, 12, 16)
+    FINAL_SPLITS = (1, 2, 3, 4, 6, 8, 12, 16, 32, 64)
+
+    def _first_dw_final(self, st, layers, x, ldx, ridx) -> bool:
+        """The shared trunk's first-layer weight gradient as a one-problem
+        ppo_gemm_f32_dw_group_final launch that also assembles every other
+        leaf's gradient (the optimizer step then skips the reduce); False when
+        the trunk does not take it (the caller runs the plain GEMM)."""
+        fin = self.dw_final
+        if fin is None or not fin.get("first") or layers is not self.trunk or x % 16 or ldx % 4:
+            return False
+        g = self.__dict__.get("_ffa")
+        if g is None or g["x"] != (x, ldx):
+            # host argument arrays, kept (a recorded launch is replayed from them); the
+            # gather indices are set per call in rows[0]
+            lb = layers[0]
+            s, d = lb.spec, lb.spec.dense
+            G = self.flat.G.data_ptr()
+            vp = lambda v: (ctypes.c_void_p * 1)(v)
+            arrs = [vp(x), (ctypes.c_int64 * 1)(ldx), vp(None), vp(_p(lb.dZ)), (ctypes.c_int64 * 1)(s.ld),
+                    vp(_p(lb.wpart)), (ctypes.c_int64 * 1)(s.ld), (ctypes.c_int * 1)(d.fin), (ctypes.c_int * 1)(s.ld),
+                    (ctypes.c_int * 1)(self.mb), (ctypes.c_int * 1)(lb.splits), (ctypes.c_int64 * 1)(d.fin * s.ld),
+                    vp(_p(lb.bpart)), vp(G + 4 * d.w.offset), (ctypes.c_int64 * 1)(d.w.ld), (ctypes.c_int * 1)(d.fin),
+                    vp(G + 4 * d.b.offset if d.b is not None else None)]
+            g = self._ffa = {"x": (x, ldx), "arrs": arrs, "rows": arrs[2],
+                             "args": [ctypes.addressof(a) for a in arrs]}
+        g["rows"][0] = ridx
+        self._call("ppo_gemm_f32_dw_group_final", st, 1, *g["args"], _p(fin["CNT"]), _p(fin["SUMSQ"]),
+                   _p(fin["SEGS"]), _p(fin["CHUNKS"]), fin["nchunks"], fin["nfew"], fin["nwide"])
+        self._dw_finished = True
+        return True
 
     def _pair_dw_shapes(self):
         """(M, N, splits) of every problem of the paired towers' grouped
@@ -1056,11 +1085,14 @@ class MLPExecutor(ForwardChain):
                 segs.append((G + 4 * spec.b.offset, bpart.data_ptr(), spec.w.ld, spec.w.ld, splits, rb))
 
         paired = set()   # the paired towers' Dense segments (their group launch can finish them)
+        first = set()    # the shared fp32 trunk's first Dense (its weight-gradient launch can finish it)
         for k, lb in enumerate(self.trunk + self.actor + self.critic):
             n0 = len(segs)
             dense_segs(lb.spec.dense, lb.wpart, lb.bpart, lb.splits)
             if self.chain_ln and k >= len(self.trunk):
                 paired.update(range(n0, len(segs)))
+            elif k == 0 and self.trunk:
+                first.update(range(n0, len(segs)))
             if lb.spec.ln is not None:
                 F = lb.spec.fout
                 segs.append((G + 4 * lb.spec.ln["scale"].offset, lb.lnpart.data_ptr(), F, 2 * F, lb.lnblocks, 0))
@@ -1121,7 +1153,22 @@ class MLPExecutor(ForwardChain):
             SEGS, CHUNKS, nch, nfew, nwide = pack(rest, T)
             self.dw_final = {"T": T, "SEGS": SEGS, "CHUNKS": CHUNKS, "nchunks": nch, "nfew": nfew, "nwide": nwide,
                              "SUMSQ": torch.zeros(T + nch, dtype=torch.float64, device=dev),
-                             "CNT": torch.zeros(T, dtype=torch.int32, device=dev)}
+                             "CNT": torch.zeros(9 * T, dtype=torch.int32, device=dev)}
+        # the shared fp32 trunk's first layer: its weight gradient (the last
+        # launch of a step, over the gathered observation rows) with the
+        # gradient assembly of every leaf (ppo_gemm_f32_dw_group_final, one
+        # problem; its own split-K sums in two levels at 32 or 64 splits)
+        lb0 = self.trunk[0] if self.trunk else None
+        if (self.DW_FINAL and self.dw_final is None and lb0 is not None and not self.bf16 and self.fused
+                and self.prog.shared_head and lb0.spec.ln is None and lb0.splits in self.FINAL_SPLITS
+                and -(-self.mb // lb0.splits) <= 512 and lb0.spec.dense.fin % 4 == 0 and lb0.spec.ld % 4 == 0):
+            d = lb0.spec.dense
+            T = lib.ppo_gemm_f32_dw_final_slots(1, (ctypes.c_int * 1)(d.fin), (ctypes.c_int * 1)(lb0.spec.ld))
+            assert T > 0
+            SEGS, CHUNKS, nch, nfew, nwide = pack([i for i in range(len(segs)) if i not in first], T)
+            self.dw_final = {"T": T, "SEGS": SEGS, "CHUNKS": CHUNKS, "nchunks": nch, "nfew": nfew, "nwide": nwide,
+                             "SUMSQ": torch.zeros(T + nch, dtype=torch.float64, device=dev),
+                             "CNT": torch.zeros(9 * T, dtype=torch.int32, device=dev), "first": True}
         self._dw_finished = False
 
     # ------------------------------------------------------------- pieces
@@ -1245,6 +1292,8 @@ class MLPExecutor(ForwardChain):
                 self._call("ppo_gemm_bf16s", st, A_COL, B_KN, int(y16), int(dz16), a, ldx, None, dz, s.ld,
                            _p(lb.wpart), s.ld, d.fin, s.ld, self.mb, lb.splits, d.fin * s.ld, EPI_STORE, None, 0, 0,
                            None, 0, _p(lb.bpart), -1)
+            elif i == 0 and self._first_dw_final(st, layers, x, ldx, ridx):
+                pass   # the first layer's weight gradient with every leaf's gradient assembly
             else:
                 self._gemm(st, A_COL, B_KN, x, ldx, ridx, _p(lb.dZ), s.ld, _p(lb.wpart), s.ld, d.fin,
                           s.ld, self.mb, lb.splits, d.fin * s.ld, EPI_STORE, None, 0, None, None, 0, _p(lb.bpart),

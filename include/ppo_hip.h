@@ -429,13 +429,14 @@ int ppo_gemm_f32_dw_final_slots(int count, const int* M, const int* N);
  * counters numbered tile by tile, problem after problem, as
  * ppo_gemm_f32_dw_final_slots counts them).  The gradient segments of the
  * ppo_grad_reduce tables segs / chunks (their chunk slots numbered after the
- * tiles') are reduced by workgroups of the same launch.  counters: one
- * zeroed unsigned per tile, left zeroed; calls sharing counters must not
- * overlap.  The gradients are the same bits as ppo_gemm_f32_dw_group followed
- * by ppo_grad_reduce (the norm partials are grouped by tile instead of by
- * chunk).  splits[i] in
- * {1, 2, 3, 4, 6, 8, 12, 16}; a gathered split holds at most 512 rows; all
- * problems non-empty.  Replaces the weight-gradient GEMMs and gradient
+ * tiles') are reduced by workgroups of the same launch.  counters: nine
+ * zeroed unsigneds per tile (the last eight per tile for the two-level sums),
+ * left zeroed; calls sharing counters must not overlap.  The gradients are
+ * the same bits as ppo_gemm_f32_dw_group followed by ppo_grad_reduce (the
+ * norm partials are grouped by tile instead of by chunk).  splits[i] in
+ * {1, 2, 3, 4, 6, 8, 12, 16} (one level) or {32, 64} (the last of each group
+ * of eight splits sums it, the last group the group sums); a gathered split
+ * holds at most 512 rows; all problems non-empty.  Replaces the weight-gradient GEMMs and gradient
  * assembly of jax.value_and_grad at boonta/algorithms/ppo.py:155-157. */
 int ppo_gemm_f32_dw_group_final(void* stream, int count, const float* const* A, const int64_t* lda,
                                 const int32_t* const* rows, const float* const* B, const int64_t* ldb,

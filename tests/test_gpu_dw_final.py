@@ -60,9 +60,9 @@ SHAPES = [(4096, 88, 256, 2048, 16, True, 87, True), (4096, 88, 256, 2048, 16, T
 OTHER = [(512, 128), (256, 3), (1000, 20), (4, 200)]
 
 
-def make_case(rng):
+def make_case(rng, shapes=SHAPES):
     probs = []
-    for R, M, N, K, sp, gathered, grows, bias in SHAPES:
+    for R, M, N, K, sp, gathered, grows, bias in shapes:
         A = dev(rng.normal(size=(R, M)).astype(np.float32))
         idx = dev(rng.permutation(R)[:K].astype(np.int32)) if gathered else None
         B = dev(rng.normal(size=(K, N)).astype(np.float32))
@@ -112,6 +112,7 @@ def finished(probs, other, counters=None):
     T = lib.ppo_gemm_f32_dw_final_slots(L, (ctypes.c_int * L)(*[p[3] for p in probs]),
                                         (ctypes.c_int * L)(*[p[4] for p in probs]))
     assert T == sum(-(-p[3] // 64) * -(-p[4] // 64) for p in probs)
+    # one counter per tile, then eight per tile for the two-level sums
     C = [torch.full((p[6], p[3], p[4]), float("nan"), device=DEV) for p in probs]
     bg = [torch.full((p[6], p[4]), float("nan"), device=DEV) for p in probs]
     # one guard row after each gradient: the rows past g_rows stay untouched
@@ -122,7 +123,7 @@ def finished(probs, other, counters=None):
     SEGS, CH, nch, nfew, nwide = tables(segs, T)
     SQ = torch.full((T + nch,), float("nan"), dtype=torch.float64, device=DEV)
     if counters is None:
-        counters = torch.zeros(T, dtype=torch.int32, device=DEV)
+        counters = torch.zeros(9 * T, dtype=torch.int32, device=DEV)
     args = group_args(probs, C, bg)
     vp = lambda xs: (ctypes.c_void_p * L)(*xs)
     fin = [vp([g.data_ptr() for g in G]), (ctypes.c_int64 * L)(*[p[4] for p in probs]),
@@ -170,6 +171,20 @@ def test_final_group_matches_the_group_and_reduce_launches():
     np.testing.assert_allclose(G[0][:grows], want, rtol=2e-5, atol=2e-4)
 
 
+# two-level sums: 64 splits (the discrete Anakin workload's first layer: 400 x 256 over gathered rows)
+# and 32 splits (a ragged problem)
+SHAPES2 = [(8192, 400, 256, 4096, 64, True, 400, True), (3000, 128, 136, 2048, 32, False, 120, True),
+           (2048, 256, 256, 2048, 8, False, 256, True)]
+
+
+def test_final_group_two_level_sums_match_the_group_and_reduce_launches():
+    rng = np.random.default_rng(9)
+    counters = None
+    for _ in range(2):
+        probs, other = make_case(rng, SHAPES2)
+        counters = check(probs, other, counters)
+
+
 def test_final_group_rejects_unsupported_shapes():
     rng = np.random.default_rng(4)
     probs, other = make_case(rng)
@@ -178,7 +193,7 @@ def test_final_group_rejects_unsupported_shapes():
     C = torch.zeros((p[6], p[3], p[4]), device=DEV)
     bg = torch.zeros((p[6], p[4]), device=DEV)
     G = torch.zeros((p[3], p[4]), device=DEV)
-    cnt = torch.zeros(16, dtype=torch.int32, device=DEV)
+    cnt = torch.zeros(9 * 16, dtype=torch.int32, device=DEV)
     SQ = torch.zeros(16, dtype=torch.float64, device=DEV)
 
     def call(splits=p[6], grows=p[7], K=p[5], idx=None):

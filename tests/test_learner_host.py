@@ -254,7 +254,7 @@ def check_final_gradient_tables(ex, flat, args, adam_calls):
     assert list(args[21:26]) == [fin["SEGS"].data_ptr(), fin["CHUNKS"].data_ptr(), fin["nchunks"], fin["nfew"],
                            fin["nwide"]]
     tiles = sum(-(-g["M"][k] // 64) * -(-g["N"][k] // 64) for k in range(g["count"]))
-    assert fin["T"] == tiles and fin["CNT"].numel() == tiles and fin["SUMSQ"].numel() == tiles + fin["nchunks"]
+    assert fin["T"] == tiles and fin["CNT"].numel() == 9 * tiles and fin["SUMSQ"].numel() == tiles + fin["nchunks"]
     # the full table's segments = the finished Dense gradients + the rest table's
     full = _segment_table(ex.SEGS, len(ex.segments))
     nrest = len(ex.segments) - 2 * len(lbs)
