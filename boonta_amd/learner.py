@@ -940,7 +940,7 @@ class MLPExecutor(ForwardChain):
             vp = lambda v: (ctypes.c_void_p * 1)(v)
             arrs = [vp(x), (ctypes.c_int64 * 1)(ldx), vp(None), vp(_p(lb.dZ)), (ctypes.c_int64 * 1)(s.ld),
                     vp(_p(lb.wpart)), (ctypes.c_int64 * 1)(s.ld), (ctypes.c_int * 1)(d.fin), (ctypes.c_int * 1)(s.ld),
-                    (ctypes.c_int * 1)(self.mb), (ctypes.c_int * 1)(lb.splits), (ctypes.c_int64 * 1)(d.fin * s.ld),
+                    (ctypes.c_int * 1)(self.mb), (ctypes.c_int * 1)(fin["first"]), (ctypes.c_int64 * 1)(d.fin * s.ld),
                     vp(_p(lb.bpart)), vp(G + 4 * d.w.offset), (ctypes.c_int64 * 1)(d.w.ld), (ctypes.c_int * 1)(d.fin),
                     vp(G + 4 * d.b.offset if d.b is not None else None)]
             g = self._ffa = {"x": (x, ldx), "arrs": arrs, "rows": arrs[2],
@@ -1158,17 +1158,20 @@ class MLPExecutor(ForwardChain):
         # launch of a step, over the gathered observation rows) with the
         # gradient assembly of every leaf (ppo_gemm_f32_dw_group_final, one
         # problem; its own split-K sums in two levels at 32 or 64 splits)
+        # (at the largest split count the launch sums that does not exceed the
+        # layer's own: the GRU workload's 128 splits of 128 rows become 64)
         lb0 = self.trunk[0] if self.trunk else None
-        if (self.DW_FINAL and self.dw_final is None and lb0 is not None and not self.bf16 and self.fused
-                and self.prog.shared_head and lb0.spec.ln is None and lb0.splits in self.FINAL_SPLITS
-                and -(-self.mb // lb0.splits) <= 512 and lb0.spec.dense.fin % 4 == 0 and lb0.spec.ld % 4 == 0):
+        sp0 = max([sp for sp in self.FINAL_SPLITS if lb0 is not None and sp <= lb0.splits] or [0])
+        if (self.DW_FINAL and self.dw_final is None and sp0 > 0 and not self.bf16 and self.fused
+                and self.prog.shared_head and lb0.spec.ln is None and -(-self.mb // sp0) <= 512
+                and lb0.spec.dense.fin % 4 == 0 and lb0.spec.ld % 4 == 0):
             d = lb0.spec.dense
             T = lib.ppo_gemm_f32_dw_final_slots(1, (ctypes.c_int * 1)(d.fin), (ctypes.c_int * 1)(lb0.spec.ld))
             assert T > 0
             SEGS, CHUNKS, nch, nfew, nwide = pack([i for i in range(len(segs)) if i not in first], T)
             self.dw_final = {"T": T, "SEGS": SEGS, "CHUNKS": CHUNKS, "nchunks": nch, "nfew": nfew, "nwide": nwide,
                              "SUMSQ": torch.zeros(T + nch, dtype=torch.float64, device=dev),
-                             "CNT": torch.zeros(9 * T, dtype=torch.int32, device=dev), "first": True}
+                             "CNT": torch.zeros(9 * T, dtype=torch.int32, device=dev), "first": sp0}
         self._dw_finished = False
 
     # ------------------------------------------------------------- pieces
