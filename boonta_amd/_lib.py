@@ -129,10 +129,10 @@ SIGNATURES = {
     "ppo_gru_bwd_seq_f32": (I, [P, P, I64, P, P, P, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P,
                                 I64, I64, I, I, I, P, P, I]),
     "ppo_gru_fwd_seq_xw_f32": (I, [P, P, I64, P, P, P, P, I64, P, I64, P, P, I64, I64, P, I64, I64, P, I64, I64,
-                                   I, I, I, P, P, I, P, I64, I64, I, P, I64, P]),
+                                   I, I, I, P, P, I, P, I64, I64, I, P, I64, P, I, P, I64]),
     "ppo_gru_seq_dw_parts": (I, [I]),
     "ppo_gru_bwd_seq_dw_f32": (I, [P, P, I64, P, P, P, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P,
-                                   I64, I64, I, I, I, P, P, I, P, I64, I64, I, P, P, P, P]),
+                                   I64, I64, I, I, I, P, P, I, P, I64, I64, I, P, P, P, P, I, P, I64]),
     "ppo_sequence_rows": (I, [P, P, I, I, I, I, P]),
     "ppo_grad_reduce_segment_bytes": (I, []),
     "ppo_grad_reduce_chunk_bytes": (I, []),

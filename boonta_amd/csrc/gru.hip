@@ -352,7 +352,20 @@ struct SeqSync {
   u64* ring;     // [2][Bm][K] pairs, zero at launch
   int* error;    // set to 1 when a wait gave up
   int spin_limit;
+  u64* clear;    // or null: the other direction's ring, which the launch leaves zero
+  int64_t clear_n;  // its pairs
 };
+
+// This workgroup's share of the other direction's ring, zeroed by its
+// recurrence waves (threads 0 .. 255) as they finish, so that the next
+// launch, which exchanges through it, needs no zeroing launch before it.
+__device__ __forceinline__ void clear_share(const SeqSync& s, int tid) {
+  if (!s.clear) return;
+  const int64_t nwg = (int64_t)gridDim.x * gridDim.y, wg = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+  const int64_t per = (s.clear_n + nwg - 1) / nwg;
+  const int64_t b = wg * per, e = min(s.clear_n, b + per);
+  for (int64_t i = b + tid; i < e; i += 256) s.clear[i] = 0ull;
+}
 
 __device__ __forceinline__ void put_pair(u64* p, float v, unsigned tag) {
   __hip_atomic_store(p, ((u64)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -699,6 +712,7 @@ __global__ void __launch_bounds__(XW ? 512 : 256) gru_fwd_seq_kernel(FwdSeqArgs 
       xz = xz_next;
     }
   }
+  clear_share(a.sync, threadIdx.x);
 }
 
 struct BwdSeqArgs {
@@ -965,6 +979,7 @@ __global__ void __launch_bounds__(DW ? 512 : 256) gru_bwd_seq_kernel(BwdSeqArgs 
       if (g > 0) a.whbpart[x3 + (g - 1) * H + c] = sum;    // [dar|daz|dhn]
     }
   }
+  clear_share(a.sync, tid);
 }
 
 int cu_count() {
@@ -1133,15 +1148,22 @@ PPO_EXPORT int ppo_gru_fwd_seq_f32(void* stream, const float* xi, int64_t ldxi, 
 // GRUCell's input Dense kernels, boonta/networks/blocks/rnn.py:34-54),
 // each step's products summed in a fixed order (not the order of a separate
 // GEMM launch: equal to it to rounding).  H = I = 256; e rows 16-byte aligned.
+// ring_is_zero: the exchange ring is already zero (no zeroing launch first);
+// clear_ring (clear_bytes, or null / 0): a ring the launch zeroes as its
+// workgroups finish — the backward's, so that it needs no zeroing launch
+// either (a launch that sets the error word may leave it unzeroed).
 PPO_EXPORT int ppo_gru_fwd_seq_xw_f32(void* stream, const float* h0, int64_t ldh0, const int32_t* h0_rows,
                                       const uint8_t* terminated, const uint8_t* truncated, const int32_t* flag_rows,
                                       int64_t flag_step, const float* wh, int64_t ldwh, const float* bhn,
                                       float* h_out, int64_t ldo, int64_t h_step, float* hp_out, int64_t ldhp,
                                       int64_t hp_step, float* gates, int64_t ldg, int64_t g_step, int Bm, int H, int T,
                                       void* exchange, int* error, int spin_limit, const float* e, int64_t lde,
-                                      int64_t e_step, int I, const float* wi, int64_t ldwi, const float* bi) {
+                                      int64_t e_step, int I, const float* wi, int64_t ldwi, const float* bi,
+                                      int ring_is_zero, void* clear_ring, int64_t clear_bytes) {
   const int rc = seq_check("ppo_gru_fwd_seq_xw_f32", Bm, H, T, exchange, error);
   if (rc != PPO_OK) return rc;
+  if (clear_bytes < 0 || clear_bytes % 8 || (clear_bytes > 0 && (!clear_ring || !aligned16(clear_ring))))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gru_fwd_seq_xw_f32: bad ring to clear (%lld bytes)", (long long)clear_bytes);
   if (H != 256 || I != 256)
     return ppo::set_error(PPO_ERR_ARG, "ppo_gru_fwd_seq_xw_f32: needs H = I = 256 (H=%d I=%d)", H, I);
   if (Bm == 0 || T == 0) return PPO_OK;
@@ -1155,9 +1177,11 @@ PPO_EXPORT int ppo_gru_fwd_seq_xw_f32(void* stream, const float* h0, int64_t ldh
     return ppo::set_error(PPO_ERR_ARG, "ppo_gru_fwd_seq_xw_f32: h0, h_out and e rows must be 16-byte aligned");
   FwdSeqArgs a{nullptr, 0, 0, h0, ldh0, h0_rows, terminated, truncated, flag_rows, flag_step, wh, ldwh, bhn,
                h_out, ldo, h_step, hp_out, ldhp, hp_step, gates, ldg, g_step, Bm, H, T,
-               SeqSync{static_cast<u64*>(exchange), error, spin_limit}, e, lde, e_step, wi, ldwi, bi};
+               SeqSync{static_cast<u64*>(exchange), error, spin_limit,
+                       clear_bytes > 0 ? static_cast<u64*>(clear_ring) : nullptr, clear_bytes / 8},
+               e, lde, e_step, wi, ldwi, bi};
   hipStream_t st = ppo::as_stream(stream);
-  if (T > 1) zero_ring(st, exchange, 2 * (int64_t)Bm * H);
+  if (T > 1 && !ring_is_zero) zero_ring(st, exchange, 2 * (int64_t)Bm * H);
   launch_seq(gru_fwd_seq_kernel<4, true>, dim3(ppo::ceil_div(Bm, TILE), H / TILE), st, a, 512);
   return ppo::check_launch("ppo_gru_fwd_seq_xw_f32");
 }
@@ -1212,7 +1236,8 @@ PPO_EXPORT int ppo_gru_seq_dw_parts(int Bm) { return Bm > 0 ? ppo::ceil_div(Bm, 
 // GRUCell's input and recurrent Dense kernels, boonta/networks/blocks/rnn.py:
 // 34-54, differentiated by jax.value_and_grad at
 // boonta/algorithms/recurrent_ppo.py:213-215).  H = I = 256; hp and e rows
-// 16-byte aligned.
+// 16-byte aligned.  ring_is_zero, clear_ring, clear_bytes: as for
+// ppo_gru_fwd_seq_xw_f32 (here clear_ring is the forward's ring).
 PPO_EXPORT int ppo_gru_bwd_seq_dw_f32(void* stream, const float* wh, int64_t ldwh, const uint8_t* terminated,
                                       const uint8_t* truncated, const int32_t* flag_rows, int64_t flag_step,
                                       const float* dout, int64_t lddo, int64_t dout_step, const float* gates,
@@ -1220,9 +1245,12 @@ PPO_EXPORT int ppo_gru_bwd_seq_dw_f32(void* stream, const float* wh, int64_t ldw
                                       float* dh, int64_t lddh, int64_t dh_step, float* dgate, int64_t lddg,
                                       int64_t dg_step, int Bm, int H, int T, void* exchange, int* error,
                                       int spin_limit, const float* e, int64_t lde, int64_t e_step, int I,
-                                      float* whpart, float* whbpart, float* wipart, float* wibpart) {
+                                      float* whpart, float* whbpart, float* wipart, float* wibpart,
+                                      int ring_is_zero, void* clear_ring, int64_t clear_bytes) {
   const int rc = seq_check("ppo_gru_bwd_seq_dw_f32", Bm, H, T, exchange, error);
   if (rc != PPO_OK) return rc;
+  if (clear_bytes < 0 || clear_bytes % 8 || (clear_bytes > 0 && (!clear_ring || !aligned16(clear_ring))))
+    return ppo::set_error(PPO_ERR_ARG, "ppo_gru_bwd_seq_dw_f32: bad ring to clear (%lld bytes)", (long long)clear_bytes);
   if (H != 256 || I != 256)
     return ppo::set_error(PPO_ERR_ARG, "ppo_gru_bwd_seq_dw_f32: needs H = I = 256 (H=%d I=%d)", H, I);
   if (Bm == 0 || T == 0) return PPO_OK;
@@ -1235,10 +1263,11 @@ PPO_EXPORT int ppo_gru_bwd_seq_dw_f32(void* stream, const float* wh, int64_t ldw
     return ppo::set_error(PPO_ERR_ARG, "ppo_gru_bwd_seq_dw_f32: dgate, hp and e rows must be 16-byte aligned");
   BwdSeqArgs a{wh, ldwh, terminated, truncated, flag_rows, flag_step, dout, lddo, dout_step, gates, ldg, g_step,
                hp, ldhp, hp_step, dh, lddh, dh_step, dgate, lddg, dg_step, Bm, H, T,
-               SeqSync{static_cast<u64*>(exchange), error, spin_limit}, e, lde, e_step, whpart, whbpart, wipart,
-               wibpart};
+               SeqSync{static_cast<u64*>(exchange), error, spin_limit,
+                       clear_bytes > 0 ? static_cast<u64*>(clear_ring) : nullptr, clear_bytes / 8},
+               e, lde, e_step, whpart, whbpart, wipart, wibpart};
   hipStream_t st = ppo::as_stream(stream);
-  if (T > 1) zero_ring(st, exchange, 2 * (int64_t)Bm * 3 * H);
+  if (T > 1 && !ring_is_zero) zero_ring(st, exchange, 2 * (int64_t)Bm * 3 * H);
   launch_seq(gru_bwd_seq_kernel<12, true>, dim3(ppo::ceil_div(Bm, TILE), H / TILE), st, a, 512);
   return ppo::check_launch("ppo_gru_bwd_seq_dw_f32");
 }

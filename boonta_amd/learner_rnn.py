@@ -92,11 +92,17 @@ class RecurrentExecutor(MLPExecutor):
             self.SEQX = torch.zeros(max(1, lib.ppo_gru_seq_exchange_bytes(self.Bm, H) // 8), dtype=torch.int64,
                                     device=dev)
             self.SEQERR = torch.zeros(1, dtype=torch.int32, device=dev)
+            # with both fused sequence launches, one ring per direction: each
+            # launch leaves the other's ring zero as it finishes, so no zeroing
+            # launch runs before either (both zeroed at the start of an update)
+            self.SEQX_F = (torch.zeros(max(1, 2 * self.Bm * H), dtype=torch.int64, device=dev)
+                           if self.RING_PAIR and self.seq_xw and self.seq_dw else None)
 
     SEQ = True               # sequence launches where they fit
     SEQ_DW = True            # the weight gradients inside the backward sequence launch where it takes them
     SEQ_XW = True            # the input projections inside the forward sequence launch where it takes them
     SEQ_SPIN = 1 << 18       # polls of a step wait before it gives up (about a second)
+    RING_PAIR = True         # one exchange ring per direction, each left zero by the other's launch
 
     @staticmethod
     def _seq_fits(Bm: int, H: int) -> bool:
@@ -117,11 +123,29 @@ class RecurrentExecutor(MLPExecutor):
     def _abort_word(self):
         return _p(self.SEQERR) if self.seq else None
 
+    def _ring(self, fwd: bool):
+        """(exchange ring) of a fused sequence launch: the forward's own ring
+        when the directions have one each, else the shared one."""
+        return (_p(self.SEQX_F) if fwd and self.SEQX_F is not None else _p(self.SEQX),)
+
+    def _ring_clear(self, fwd: bool):
+        """(ring_is_zero, ring to clear, its bytes) of a fused sequence
+        launch: with a ring per direction, its own ring is zero on entry and it
+        zeroes the other direction's as it finishes."""
+        if self.SEQX_F is None:
+            return (0, None, 0)
+        other = self.SEQX if fwd else self.SEQX_F
+        return (1, _p(other), 8 * other.numel())
+
     def _clear_recurrence_error(self, st):
         """Zeroes the error word at the start of an update, with a kernel (a
         memset node in a replayed graph is avoided on purpose)."""
         if self.seq:
             self._call("ppo_fill_f32", st, _p(self.SEQERR), 1, 0.0)
+            if self.SEQX_F is not None:
+                # (also after an update whose recurrence gave up, which may leave a ring unzeroed)
+                self._call("ppo_fill_f32", st, _p(self.SEQX), 2 * self.SEQX.numel(), 0.0)
+                self._call("ppo_fill_f32", st, _p(self.SEQX_F), 2 * self.SEQX_F.numel(), 0.0)
 
     def _extra_input_buffers(self) -> dict:
         """first.terminated / first.truncated [T, N] and the carry sequence
@@ -237,8 +261,9 @@ class RecurrentExecutor(MLPExecutor):
         if self.seq_xw:
             self._call("ppo_gru_fwd_seq_xw_f32", st, inp["carry0"], H, envs, fterm, ftrunc, rows, Bm,
                        self.flat.view(g.wh), 3 * H, self.flat.view(g.bhn), _p(self.HOUT), H, blk, _p(self.HP), H,
-                       blk, _p(self.GATES), 4 * H, Bm * 4 * H, Bm, H, T, _p(self.SEQX), _p(self.SEQERR),
-                       self.SEQ_SPIN, e_ptr, lde, Bm * lde, I, self.flat.view(g.wi), 3 * H, self.flat.view(g.bi))
+                       blk, _p(self.GATES), 4 * H, Bm * 4 * H, Bm, H, T, *self._ring(fwd=True), _p(self.SEQERR),
+                       self.SEQ_SPIN, e_ptr, lde, Bm * lde, I, self.flat.view(g.wi), 3 * H, self.flat.view(g.bi),
+                       *self._ring_clear(fwd=True))
         elif self.seq:
             self._call("ppo_gru_fwd_seq_f32", st, _p(self.XI), 3 * H, Bm * 3 * H, inp["carry0"], H, envs, fterm,
                        ftrunc, rows, Bm, self.flat.view(g.wh), 3 * H, self.flat.view(g.bhn), _p(self.HOUT), H, blk,
@@ -261,8 +286,9 @@ class RecurrentExecutor(MLPExecutor):
         if self.seq_dw:
             self._call("ppo_gru_bwd_seq_dw_f32", st, wh, 3 * H, fterm, ftrunc, rows, Bm, _p(self.DHOUT), H, blk,
                        _p(self.GATES), G4, Bm * G4, _p(self.HP), H, blk, _p(self.DHS), H, blk, _p(self.DGATE), G4,
-                       Bm * G4, Bm, H, T, _p(self.SEQX), _p(self.SEQERR), self.SEQ_SPIN, e_ptr, lde, Bm * lde, I,
-                       _p(self.WHPART), _p(self.WHBPART), _p(self.WIPART), _p(self.WIBPART))
+                       Bm * G4, Bm, H, T, *self._ring(fwd=False), _p(self.SEQERR), self.SEQ_SPIN, e_ptr, lde,
+                       Bm * lde, I, _p(self.WHPART), _p(self.WHBPART), _p(self.WIPART), _p(self.WIBPART),
+                       *self._ring_clear(fwd=False))
         elif self.seq:
             self._call("ppo_gru_bwd_seq_f32", st, wh, 3 * H, fterm, ftrunc, rows, Bm, _p(self.DHOUT), H, blk,
                        _p(self.GATES), G4, Bm * G4, _p(self.HP), H, blk, _p(self.DHS), H, blk, _p(self.DGATE), G4,

@@ -712,14 +712,19 @@ int ppo_gru_bwd_seq_f32(void* stream, const float* wh, int64_t ldwh, const uint8
  * [I][3H] with row pitch ldwi and bi [3H] in columns [n|r|z].  Each step's
  * products are summed in a fixed order of their own, so the results equal
  * ppo_gru_fwd_seq_f32 on a GEMM's xi to rounding, not bit for bit.  H = I =
- * 256; e rows 16-byte aligned. */
+ * 256; e rows 16-byte aligned.  ring_is_zero: the exchange ring is already
+ * zero, so the launch does not zero it first; clear_ring / clear_bytes (or
+ * NULL / 0): a second ring (the backward's) that the launch leaves zero as
+ * its workgroups finish — with one ring per direction, each sequence launch
+ * leaves the other's ring ready and neither needs a zeroing launch (zero
+ * both once, and again after a launch that set the error word). */
 int ppo_gru_fwd_seq_xw_f32(void* stream, const float* h0, int64_t ldh0, const int32_t* h0_rows,
                            const uint8_t* terminated, const uint8_t* truncated, const int32_t* flag_rows,
                            int64_t flag_step, const float* wh, int64_t ldwh, const float* bhn, float* h_out,
                            int64_t ldo, int64_t h_step, float* hp_out, int64_t ldhp, int64_t hp_step, float* gates,
                            int64_t ldg, int64_t g_step, int Bm, int H, int T, void* exchange, int* error,
                            int spin_limit, const float* e, int64_t lde, int64_t e_step, int I, const float* wi,
-                           int64_t ldwi, const float* bi);
+                           int64_t ldwi, const float* bi, int ring_is_zero, void* clear_ring, int64_t clear_bytes);
 /* ppo_gru_bwd_seq_f32 that also leaves the weight gradients of the GRU's
  * input and recurrent Dense kernels and their biases (the flax GRUCell of
  * boonta/networks/blocks/rnn.py:34-54 under jax.value_and_grad,
@@ -730,7 +735,8 @@ int ppo_gru_fwd_seq_xw_f32(void* stream, const float* h0, int64_t ldh0, const in
  *   wipart [P][I][3H] = e^T dgate[:, 0:3H]      wibpart [P][3H]: column sums of dgate[:, 0:3H]
  * where e is the GRU input of row t Bm + b at e + t e_step + b lde.  dh and
  * dgate are those of ppo_gru_bwd_seq_f32, bit for bit.  H = I = 256; hp and
- * e rows 16-byte aligned. */
+ * e rows 16-byte aligned.  ring_is_zero, clear_ring, clear_bytes: as for
+ * ppo_gru_fwd_seq_xw_f32 (here clear_ring is the forward's ring). */
 int ppo_gru_seq_dw_parts(int Bm);
 int ppo_gru_bwd_seq_dw_f32(void* stream, const float* wh, int64_t ldwh, const uint8_t* terminated,
                            const uint8_t* truncated, const int32_t* flag_rows, int64_t flag_step, const float* dout,
@@ -738,7 +744,8 @@ int ppo_gru_bwd_seq_dw_f32(void* stream, const float* wh, int64_t ldwh, const ui
                            const float* hp, int64_t ldhp, int64_t hp_step, float* dh, int64_t lddh, int64_t dh_step,
                            float* dgate, int64_t lddg, int64_t dg_step, int Bm, int H, int T, void* exchange,
                            int* error, int spin_limit, const float* e, int64_t lde, int64_t e_step, int I,
-                           float* whpart, float* whbpart, float* wipart, float* wibpart);
+                           float* whpart, float* whbpart, float* wipart, float* wibpart, int ring_is_zero,
+                           void* clear_ring, int64_t clear_bytes);
 /* Sample rows of S env-major sequence minibatches (recurrent_ppo.py:217-223):
  * out[s * T * Bm + t * Bm + b] = t * N + envs[s * Bm + b]. */
 int ppo_sequence_rows(void* stream, const int32_t* envs, int S, int T, int N, int Bm, int32_t* out);

@@ -51,7 +51,7 @@ def test_argument_errors_are_reported_not_launched():
     assert b"bad shape" in lib.ppo_last_error()
     assert lib.ppo_gru_bwd_seq_dw_f32(None, None, 768, None, None, None, 0, None, 256, 0, None, 1024, 0, None, 256,
                                       0, None, 256, 0, None, 1024, 0, 16, 256, 4, None, None, 1, None, 256, 0, 256,
-                                      None, None, None, None) == -1   # no exchange ring
+                                      None, None, None, None, 0, None, 0) == -1   # no exchange ring
 
 
 def test_sampling_rejects_unsupported_sizes_without_launching():

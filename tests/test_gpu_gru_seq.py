@@ -86,7 +86,7 @@ def run_seq(c, o, sync, err, spin=SPIN, backward=True, dw=None):
         _lib.call("ppo_gru_bwd_seq_dw_f32", st(), P("WH"), 3 * H, P("TERM"), P("TRUNC"), P("ROWS"), B, P("DOUT"), H,
                   blk, Q("GATES"), g4, B * g4, Q("HP"), H, blk, Q("DHS"), H, blk, Q("DG"), g4, B * g4, B, H, T,
                   sync.data_ptr(), err.data_ptr(), spin, dw["E"].data_ptr(), I, B * I, I, dw["WHP"].data_ptr(),
-                  dw["WHB"].data_ptr(), dw["WIP"].data_ptr(), dw["WIB"].data_ptr())
+                  dw["WHB"].data_ptr(), dw["WIP"].data_ptr(), dw["WIB"].data_ptr(), 0, None, 0)
 
 
 def sync_bufs(B, H):
@@ -171,7 +171,7 @@ def test_forward_with_input_projections(B, T):
     print(f"fwd seq xw B={B} T={T}", flush=True)
     _lib.call("ppo_gru_fwd_seq_xw_f32", st(), P("POOL"), H, P("ENVS"), P("TERM"), P("TRUNC"), P("ROWS"), B, P("WH"),
               3 * H, P("BHN"), Q("HOUT"), H, blk, Q("HP"), H, blk, Q("GATES"), g4, B * g4, B, H, T, sync.data_ptr(),
-              err.data_ptr(), SPIN, E.data_ptr(), I, B * I, I, WI.data_ptr(), 3 * H, BI.data_ptr())
+              err.data_ptr(), SPIN, E.data_ptr(), I, B * I, I, WI.data_ptr(), 3 * H, BI.data_ptr(), 0, None, 0)
     torch.cuda.synchronize()
     assert int(err.item()) == 0
     for k in ("HOUT", "HP", "GATES"):
@@ -312,3 +312,60 @@ def test_an_update_whose_recurrence_gave_up_keeps_its_parameters_and_raises(use_
     assert int(flat.count.item()) == count0 + r.cfg.update_epochs * r.cfg.num_minibatches
     logs = alg.logs(state, r.T, r.N, r.obs_dim)
     assert all(np.isfinite(v).all() for v in logs.values())
+
+
+@pytest.mark.parametrize("B,T", [(256, 64), (37, 9)])
+def test_ring_per_direction_needs_no_zeroing_launch(B, T):
+    """The learner's fused sequence launches with one exchange ring per
+    direction (ring_is_zero: no zeroing launch; each launch zeroes the other
+    direction's ring as its workgroups finish): the same bits as the launches
+    that zero a shared ring first (itself left full of this launch's tags), the
+    other ring all zero after each launch, over two forward / backward rounds
+    through the same rings."""
+    H = I = 256
+    c = case(B, H, T, seed=B * 3 + T)
+    rng = np.random.default_rng(B + 5 * T)
+    E = dev(rng.standard_normal((T * B, I)).astype(np.float32))
+    WI = dev((rng.standard_normal((I, 3 * H)) / np.sqrt(I)).astype(np.float32))
+    BI = dev((0.1 * rng.standard_normal(3 * H)).astype(np.float32))
+    parts = _lib.load().ppo_gru_seq_dw_parts(B)
+    blk, g4 = B * H, 4 * H
+
+    def run(o, dw, fwd_ring, bwd_ring, pair, err):
+        P = lambda k: c[k].data_ptr()
+        Q = lambda k: o[k].data_ptr()
+        fclear = (1, bwd_ring.data_ptr(), 8 * bwd_ring.numel()) if pair else (0, None, 0)
+        bclear = (1, fwd_ring.data_ptr(), 8 * fwd_ring.numel()) if pair else (0, None, 0)
+        _lib.call("ppo_gru_fwd_seq_xw_f32", st(), P("POOL"), H, P("ENVS"), P("TERM"), P("TRUNC"), P("ROWS"), B,
+                  P("WH"), 3 * H, P("BHN"), Q("HOUT"), H, blk, Q("HP"), H, blk, Q("GATES"), g4, B * g4, B, H, T,
+                  fwd_ring.data_ptr(), err.data_ptr(), SPIN, E.data_ptr(), I, B * I, I, WI.data_ptr(), 3 * H,
+                  BI.data_ptr(), *fclear)
+        if pair:
+            torch.cuda.synchronize()
+            assert not bwd_ring.any(), "the forward left the backward's ring unzeroed"
+        _lib.call("ppo_gru_bwd_seq_dw_f32", st(), P("WH"), 3 * H, P("TERM"), P("TRUNC"), P("ROWS"), B, P("DOUT"), H,
+                  blk, Q("GATES"), g4, B * g4, Q("HP"), H, blk, Q("DHS"), H, blk, Q("DG"), g4, B * g4, B, H, T,
+                  bwd_ring.data_ptr(), err.data_ptr(), SPIN, E.data_ptr(), I, B * I, I, dw["WHP"].data_ptr(),
+                  dw["WHB"].data_ptr(), dw["WIP"].data_ptr(), dw["WIB"].data_ptr(), *bclear)
+        if pair:
+            torch.cuda.synchronize()
+            assert not fwd_ring.any(), "the backward left the forward's ring unzeroed"
+
+    def bufs():
+        return dict(WHP=torch.full((parts, H, 3 * H), 7.0, device=DEV), WHB=torch.full((parts, 3 * H), 7.0, device=DEV),
+                    WIP=torch.full((parts, I, 3 * H), 7.0, device=DEV), WIB=torch.full((parts, 3 * H), 7.0, device=DEV))
+
+    ref, dref = out_bufs(B, H, T), bufs()
+    sync, err = sync_bufs(B, H)
+    run(ref, dref, sync, sync, False, err)
+    ring_f = torch.zeros(2 * B * H, dtype=torch.int64, device=DEV)
+    ring_b = torch.zeros(_lib.load().ppo_gru_seq_exchange_bytes(B, H) // 8, dtype=torch.int64, device=DEV)
+    for rnd in range(2):
+        got, dgot = out_bufs(B, H, T), bufs()
+        run(got, dgot, ring_f, ring_b, True, err)
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0
+        for k in ("HOUT", "HP", "GATES", "DHS", "DG"):
+            assert torch.equal(got[k], ref[k]), (rnd, k)
+        for k in ("WHP", "WHB", "WIP", "WIB"):
+            assert torch.equal(dgot[k], dref[k]), (rnd, k)

@@ -539,15 +539,25 @@ def test_recurrent_update_runs_each_direction_of_the_recurrence_in_one_launch(fu
         if name == "ppo_gru_fwd_seq_f32":
             assert args[3] == Bm * 3 * H and args[10] == Bm and args[-6:-3] == (Bm, H, T)
             assert args[-3] == ex.SEQX.data_ptr() and args[-2] == ex.SEQERR.data_ptr()
+        # with both fused launches, one ring per direction: each is zero on entry (no zeroing
+        # launch) and its launch zeroes the other direction's ring as it finishes
+        pair = ex.SEQX_F is not None
+        assert pair == (ex.seq_xw and ex.seq_dw)
         if name == "ppo_gru_fwd_seq_xw_f32":
             assert args[7] == Bm and args[20:23] == (Bm, H, T)
-            assert args[23] == ex.SEQX.data_ptr() and args[24] == ex.SEQERR.data_ptr()
+            ring = ex.SEQX_F if pair else ex.SEQX
+            assert args[23] == ring.data_ptr() and args[24] == ex.SEQERR.data_ptr()
             assert args[26:30] == (e_ptr, lde, Bm * lde, I)
             assert args[30] == ex.flat.view(prog.gru.wi) and args[31] == 3 * H and args[32] == ex.flat.view(prog.gru.bi)
+            assert args[33:] == ((1, ex.SEQX.data_ptr(), 8 * ex.SEQX.numel()) if pair else (0, None, 0))
+            if pair:
+                assert ex.SEQX_F.numel() == 2 * Bm * H
         if name in ("ppo_gru_bwd_seq_f32", "ppo_gru_bwd_seq_dw_f32"):
             assert args[6] == Bm and args[9] == Bm * H and args[22:25] == (Bm, H, T)
         if name == "ppo_gru_bwd_seq_dw_f32":
             assert args[28:32] == (e_ptr, lde, Bm * lde, I)
-            assert args[32:] == (ex.WHPART.data_ptr(), ex.WHBPART.data_ptr(), ex.WIPART.data_ptr(),
-                                 ex.WIBPART.data_ptr())
+            assert args[32:36] == (ex.WHPART.data_ptr(), ex.WHBPART.data_ptr(), ex.WIPART.data_ptr(),
+                                   ex.WIBPART.data_ptr())
+            assert args[25] == ex.SEQX.data_ptr()
+            assert args[36:] == ((1, ex.SEQX_F.data_ptr(), 8 * ex.SEQX_F.numel()) if pair else (0, None, 0))
             assert ex.wh_splits == ex.wi_splits == (Bm + 15) // 16 == ex.WHPART.shape[0] == ex.WIPART.shape[0]
