@@ -395,7 +395,9 @@ class ForwardChain:
         kernel (11.43 -> 11.31 ms per update); at 16384 rows (the GRU
         workload) both were slower (17.8 -> 28.2 us on 16384 x 256 x 128,
         76 -> 90 us on its 256 x 768 dW), so below that the library's default
-        (64 x 64)."""
+        (64 x 64).  The input cotangent (B = W^T) of a 32768-row minibatch
+        also stays on 64 x 64: 10.18 ms per Anakin update against 10.54
+        (256 x 128), 10.47 (128 x 128) and 10.51 (128 x 256)."""
         if a_layout == A_ROW and b_layout == B_KN and M >= 32768:
             return 9
         if a_layout == A_COL and M == 256 and K >= 32768:

@@ -181,6 +181,8 @@ def test_gemm_layouts_match_float64(a_layout, b_layout, M, N, K):
 def test_gemm_every_tile(tile):
     gemm_case(0, 0, 200, 190, 48, tile=tile, seed=tile)
     gemm_case(1, 0, 130, 70, 500, tile=tile, splits=3, bias_grad=True, seed=tile + 10)
+    # the input cotangent's layout (B = W^T) with the activation derivative, ragged M and N
+    gemm_case(0, 1, 300, 200, 136, epi=2, act="relu", seed=tile + 20, tile=tile)
 
 
 def test_gemm_forward_gathers_rows():
