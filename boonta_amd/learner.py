@@ -210,9 +210,13 @@ def _splits(rows: int, m: int, n: int) -> int:
     """Row splits of a dW contraction over ``rows`` rows: at least 128 rows
     (four 32-deep stages) per split, and about 512 workgroups counted in
     128 x 128 tiles (2048-row minibatches: 16 splits, 31.4 -> 30.0 ms on the
-    Gaussian update; 8 and 32 splits were both slower)."""
+    Gaussian update; 8 and 32 splits were both slower).  The 128 x 128-tile
+    weight gradient of a 256 x 256 kernel over 32768 rows or more aims for
+    256 workgroups instead (the Anakin minibatch's later layer: 64 splits,
+    10.18 -> 10.12 ms per update; 128 splits 10.18, 32 splits 11.22)."""
     tiles = max(1, math.ceil(m / 128) * math.ceil(n / 128))
-    return max(1, min(max(1, rows // 128), math.ceil(512 / tiles)))
+    target = 256 if m == 256 and n == 256 and rows >= 32768 else 512
+    return max(1, min(max(1, rows // 128), math.ceil(target / tiles)))
 
 
 @dataclass
