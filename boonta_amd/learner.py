@@ -455,6 +455,7 @@ class ForwardChain:
     CHAIN16 = True
     CHAIN16_BWD = True
     DW16_SIDE = True  # the chain group's later weight gradients beside the first layer's, on the side stream
+    DW_SIDE = True    # fp32: a later layer's weight gradient beside its input cotangent, on the side stream
     # every weight gradient of the chain group in one launch (ppo_gemm_bf16s_dw_group):
     # the later layers' few tiles run beside the first layer's 198, with no
     # stream fork and join around them
@@ -1238,8 +1239,10 @@ class MLPExecutor(ForwardChain):
         g["args"] = [ctypes.addressof(g[k]) for k in order]
         return g
 
-    def _bwd_layers(self, st, layers, x0, ldx0, idx0):
-        """Back-propagates through layers whose last output cotangent is in place."""
+    def _bwd_layers(self, st, layers, x0, ldx0, idx0, side_dw=False):
+        """Back-propagates through layers whose last output cotangent is in
+        place; with side_dw (st the main stream) each later layer's fp32
+        weight gradient runs on the side stream beside its input cotangent."""
         c = layers[0].chain16 if layers else None
         if c is not None and c["bwd"]:
             # every LayerNorm backward and input cotangent in one launch; then
@@ -1284,6 +1287,7 @@ class MLPExecutor(ForwardChain):
                 x, ldx, ridx = x0, ldx0, idx0
             obs16 = i == 0 and self._reads_obs16(x, ridx, 0)
             y16 = i > 0 and layers[i - 1].Y16 is not None
+            side_dw = st
             # bf16 cotangent of a LayerNorm layer: read by its dW and dX contractions
             dz16 = s.ln is not None and lb.dZ16 is not None and (obs16 or i > 0)
             if s.ln is not None:
@@ -1304,9 +1308,13 @@ class MLPExecutor(ForwardChain):
             elif i == 0 and self._first_dw_final(st, layers, x, ldx, ridx):
                 pass   # the first layer's weight gradient with every leaf's gradient assembly
             else:
-                self._gemm(st, A_COL, B_KN, x, ldx, ridx, _p(lb.dZ), s.ld, _p(lb.wpart), s.ld, d.fin,
+                # a later layer's weight gradient runs on the side stream beside
+                # its input cotangent (neither writes what the other reads)
+                sd = self._fork(st) if i > 0 and side_dw and self.DW_SIDE else st
+                self._gemm(sd, A_COL, B_KN, x, ldx, ridx, _p(lb.dZ), s.ld, _p(lb.wpart), s.ld, d.fin,
                           s.ld, self.mb, lb.splits, d.fin * s.ld, EPI_STORE, None, 0, None, None, 0, _p(lb.bpart),
                           -1)
+                side_dw = sd
             if i > 0:
                 dst, epi, act, aux, ldaux = self._dx_target(layers[i - 1])
                 if dz16:
@@ -1317,6 +1325,8 @@ class MLPExecutor(ForwardChain):
                     self._gemm(st, A_ROW, B_NK, _p(lb.dZ), s.ld, None, self.flat.view(d.w), d.w.ld,
                               dst, layers[i - 1].spec.ld, self.mb, d.fin, s.ld, 1, 0, epi, None, act, None, aux,
                               ldaux, None, -1)
+            if side_dw != st:
+                self._join(st, side_dw)
 
     def _fwd_boot_chain(self, st, x, ldx, nrows):
         """The critic tower's forward for the bootstrap rows in one launch."""
@@ -1721,7 +1731,7 @@ class MLPExecutor(ForwardChain):
             if prog.shared_head:
                 self._fwd_layers(st, self.trunk, obs, ldo, idx, mb)
                 self._fused_head_loss(st, idx, step, dist, A, scale_ptr, act_i, act_f)
-                self._bwd_layers(st, self.trunk, obs, ldo, idx)
+                self._bwd_layers(st, self.trunk, obs, ldo, idx, side_dw=True)
             elif self.pair:
                 if self._chain_head and self._fwd_bwd_fused() and step > 0:
                     # forward, heads + loss and the torso backward in one launch: the
@@ -1766,7 +1776,7 @@ class MLPExecutor(ForwardChain):
                       int(cfg.clip_value_loss), float(cfg.entropy_coefficient), float(cfg.value_coefficient), 1.0)
             self._head_back(st, self.trunk, self.DHEAD, h, self.HWPART, self.HBPART, self.head_splits, hx, ldhx,
                             hidx)
-            self._bwd_layers(st, self.trunk, obs, ldo, idx)
+            self._bwd_layers(st, self.trunk, obs, ldo, idx, side_dw=True)
         else:
             ha, hc = prog.head_a, prog.head_c
             s2 = self._fork(st)
@@ -1813,6 +1823,8 @@ class MLPExecutor(ForwardChain):
         if self._recording or self.side is None:
             return st
         side = self.side.cuda_stream
+        if st == side:
+            return st   # never a stream waiting on its own event
         self._call("ppo_stream_wait", side, st, self._ev_fork)
         return side
 

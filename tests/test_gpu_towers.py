@@ -208,6 +208,36 @@ def test_paired_towers_update_equals_two_stream_update(use_graph):
     np.testing.assert_array_equal(results[0][1], results[1][1])
 
 
+class _OneStreamDW(MLPExecutor):
+    """The shared trunk's later weight gradients on the main stream."""
+    DW_SIDE = False
+
+
+class _OneStreamDWPPO(PPO):
+    executor_class = _OneStreamDW
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_side_stream_weight_gradients_are_bit_identical(use_graph):
+    """The discrete shared-trunk update (two 256-wide layers) with the later
+    layer's weight gradient beside its input cotangent on the side stream,
+    against the same launches on one stream: parameters and logs bit for bit."""
+    r, plan, params, tr, roll = make_case(config=2, T=8, N=512, M=2, E=2)
+    results = []
+    for cls in (PPO, _OneStreamDWPPO):
+        alg = cls(cfg=r.cfg, network=r.network, optimizer=r.optimizer, use_graph=use_graph)
+        state = alg.init_from_params({"params": params}, r.obs_dim)
+        ex = alg.executor(state, r.T, r.N, r.obs_dim)
+        assert ex.fused and ex.prog.shared_head and len(ex.trunk) == 2 and ex.DW_SIDE == (cls is PPO)
+        trans = device_transition(tr, roll)
+        for k in (1, 2):
+            alg.update(state, make_key(k), trans)
+        torch.cuda.synchronize()
+        results.append((flat_state_of(state).P.cpu().numpy().copy(), ex.LOGS.cpu().numpy().copy()))
+    np.testing.assert_array_equal(results[0][0], results[1][0])
+    np.testing.assert_array_equal(results[0][1], results[1][1])
+
+
 # ------------------------------------------------------ whole torso chains
 def chain_case(g, towers, L, M, K0, gather):
     """Random parameters of `towers` towers of L Dense(256) + LayerNorm layers,
