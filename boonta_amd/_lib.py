@@ -157,10 +157,12 @@ class KernelError(RuntimeError):
     pass
 
 
-def build(verbose: bool = False) -> str:
-    """Compiles the HIP sources for gfx950 into boonta_amd/libppo_hip.so."""
+def build(verbose: bool = False, force: bool = False) -> str:
+    """Compiles the HIP sources for gfx950 into boonta_amd/libppo_hip.so
+    (force: every source again, also where the built files are current)."""
     jobs = str(min(16, os.cpu_count() or 4))
-    out = subprocess.run(["make", "-C", CSRC, "-j", jobs], capture_output=not verbose, text=True)
+    out = subprocess.run(["make", "-C", CSRC, "-j", jobs] + (["-B"] if force else []), capture_output=not verbose,
+                         text=True)
     if out.returncode != 0:
         raise KernelError(f"building libppo_hip.so failed:\n{out.stdout}\n{out.stderr}")
     return LIB_PATH

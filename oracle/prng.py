@@ -17,8 +17,8 @@ _LIB = os.path.join(_HERE, "liboracle.so")
 _lib = None
 
 
-def build() -> str:
-    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+def build(force: bool = False) -> str:
+    subprocess.run(["make", "-s", "-C", _HERE] + (["-B"] if force else []), check=True)
     return _LIB
 
 
